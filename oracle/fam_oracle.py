@@ -1,0 +1,498 @@
+"""CPU oracle for the FastWAM / DiT4DiT action-DiT denoising hot path.
+
+TEST INFRASTRUCTURE ONLY.  This module restates, in plain PyTorch running on the
+CPU, the arithmetic of the reference's eager path so that the HIP kernels can be
+checked against it.  Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker or as
+the timed CPU baseline -- never as a substitute for the HIP library.
+
+Every function names the reference file:line whose behaviour it restates.  Paths
+are relative to the reference checkout:
+
+    FB  = src/fastwam-baseline/fastwam/models/wan22
+    FG  = src/fastwam-geak/fastwam/models/wan22
+    CA  = src/cae-fastwam/fastwam/models/wan22
+    SCH = FB/schedulers/scheduler_continuous.py
+
+Functions operate in the dtype of their inputs, exactly like the reference's eager
+modules: passing bfloat16 tensors reproduces the rounding points of the reference's
+bf16 inference path (every torch op rounds its result to bf16), passing float32
+gives the fp32 oracle the kernels are held to.  Attention and the RoPE rotation
+compute internally in fp32 / fp64 as the reference does.
+
+Pinning (what checks each function, see ``tests/test_oracle.py``):
+  sinusoidal_embedding_1d   closed forms (pos 0, first/last frequency, unit pairs) + goldens
+  precompute_freqs_cis(_3d) closed-form angles, |z| = 1, 3-D split sizes, goldens
+  rope_apply                identity at pos 0, norm preservation, inverse rotation,
+                            2x2 rotation-matrix brute force, goldens
+  rms_norm / layer_norm     unit RMS / zero-mean-unit-var, scale invariance,
+                            torch.nn.functional.layer_norm, goldens
+  attention                 brute-force fp64 loops, F.scaled_dot_product_attention,
+                            Sk=1 => v, key permutation invariance, masked keys
+  build_inference_schedule  known answers (shift 5, N=10 / N=4; shift 1), sum(delta) = -1
+  dit_block / action_dit_forward / denoise_loop
+                            golden vectors written by tests/golden/make_golden.py from
+                            the reference modules themselves (tiny seeded configs)
+  mot_action_forward        golden vectors from the reference MoT (tiny seeded config)
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, asdict
+from typing import Dict, Optional, Sequence, Tuple
+
+import torch
+import torch.nn.functional as F
+
+Params = Dict[str, torch.Tensor]
+
+
+# ---------------------------------------------------------------------------
+# Configurations
+# ---------------------------------------------------------------------------
+@dataclass(frozen=True)
+class ActionDiTConfig:
+    """Hyper-parameters of the action expert (FB/action_dit.py:47-103)."""
+
+    hidden_dim: int = 1024
+    action_dim: int = 7
+    ffn_dim: int = 4096
+    text_dim: int = 1024
+    freq_dim: int = 256
+    eps: float = 1e-6
+    num_heads: int = 16
+    attn_head_dim: int = 64
+    num_layers: int = 12
+
+    @property
+    def attn_dim(self) -> int:
+        return self.num_heads * self.attn_head_dim
+
+    def to_dict(self) -> dict:
+        return asdict(self)
+
+
+# ---------------------------------------------------------------------------
+# Elementary functions
+# ---------------------------------------------------------------------------
+def sinusoidal_embedding_1d(dim: int, position: torch.Tensor) -> torch.Tensor:
+    """cat(cos(p*f), sin(p*f)) with f_i = 10000^(-i/(dim/2)), fp64, cast to position's dtype.
+
+    Restates FB/wan_video_dit.py:34-38 (FG/wan_video_dit.py:110-122).
+    """
+    half = dim // 2
+    expo = torch.arange(half, dtype=torch.float64) / half
+    freq = torch.pow(torch.tensor(10000.0, dtype=torch.float64), -expo)
+    ang = position.to(torch.float64).reshape(-1, 1) * freq.reshape(1, -1)
+    out = torch.cat([torch.cos(ang), torch.sin(ang)], dim=1)
+    return out.to(position.dtype)
+
+
+def precompute_freqs_cis(dim: int, end: int = 1024, theta: float = 10000.0) -> torch.Tensor:
+    """complex128 table [end, dim/2]: exp(i * pos * theta^(-2j/dim)).
+
+    Restates FB/wan_video_dit.py:49-55 (built through torch.polar, as the reference does,
+    because cos/sin and polar differ in the last bits; CA/wan_video_dit.py:747-750).
+    """
+    j = torch.arange(0, dim, 2)[: dim // 2].to(torch.float64)
+    inv = 1.0 / (theta ** (j / dim))
+    ang = torch.arange(end).to(torch.float64).reshape(-1, 1) * inv.reshape(1, -1)
+    return torch.polar(torch.ones_like(ang), ang)
+
+
+def precompute_freqs_cis_3d(dim: int, end: int = 1024, theta: float = 10000.0):
+    """Per-axis tables (frame, height, width) with dims (dim-2*(dim//3), dim//3, dim//3).
+
+    Restates FB/wan_video_dit.py:41-46.
+    """
+    return (
+        precompute_freqs_cis(dim - 2 * (dim // 3), end, theta),
+        precompute_freqs_cis(dim // 3, end, theta),
+        precompute_freqs_cis(dim // 3, end, theta),
+    )
+
+
+def video_freqs(freqs3d, f: int, h: int, w: int) -> torch.Tensor:
+    """3-D RoPE table for an (f,h,w) token grid, [f*h*w, 1, Dh/2] complex.
+
+    Restates the concatenation in FB/wan_video_dit.py:620-624 (token order f-major, then h, w).
+    """
+    ff, fh, fw = freqs3d
+    a = ff[:f].reshape(f, 1, 1, -1).expand(f, h, w, -1)
+    b = fh[:h].reshape(1, h, 1, -1).expand(f, h, w, -1)
+    c = fw[:w].reshape(1, 1, w, -1).expand(f, h, w, -1)
+    return torch.cat([a, b, c], dim=-1).reshape(f * h * w, 1, -1)
+
+
+def action_freqs(attn_head_dim: int, seq_len: int, end: int = 1024) -> torch.Tensor:
+    """1-D RoPE table for action tokens 0..S-1, [S, 1, Dh/2] complex (FB/action_dit.py:101, :291-295)."""
+    if seq_len > end:
+        raise ValueError(f"Action token length {seq_len} exceeds RoPE cache {end}.")
+    return precompute_freqs_cis(attn_head_dim, end)[:seq_len].reshape(seq_len, 1, -1)
+
+
+def rope_apply(x: torch.Tensor, freqs: torch.Tensor, num_heads: int) -> torch.Tensor:
+    """Rotate interleaved pairs (x[2i], x[2i+1]) by the complex table, computed in fp64.
+
+    x [B, S, H*Dh], freqs complex [S, 1, Dh/2].  Restates FB/wan_video_dit.py:58-70.
+    """
+    b, s, nd = x.shape
+    xc = torch.view_as_complex(x.to(torch.float64).reshape(b, s, num_heads, nd // num_heads // 2, 2).contiguous())
+    out = torch.view_as_real(xc * freqs.to(torch.complex128)).reshape(b, s, nd)
+    return out.to(x.dtype)
+
+
+def rope_tables_real(freqs: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(cos, sin) fp32 [S, Dh/2] from a complex [S, 1, Dh/2] table (FG/wan_video_dit.py:173-177)."""
+    f = freqs.reshape(freqs.shape[0], -1)
+    return f.real.to(torch.float32).contiguous(), f.imag.to(torch.float32).contiguous()
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """x*rsqrt(mean(x^2)+eps) in fp32, rounded to x.dtype, then times weight.
+
+    Restates FB/wan_video_dit.py:156-167 (note the rounding before the weight multiply).
+    """
+    xf = x.float()
+    y = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return y.to(x.dtype) * weight
+
+
+def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor], eps: float) -> torch.Tensor:
+    """nn.LayerNorm over the last dim (biased variance), optional affine (FB/wan_video_dit.py:258-261)."""
+    xf = x.float()
+    mu = xf.mean(dim=-1, keepdim=True)
+    var = (xf - mu).pow(2).mean(dim=-1, keepdim=True)
+    y = ((xf - mu) * torch.rsqrt(var + eps)).to(x.dtype)
+    if weight is not None:
+        y = y * weight
+    if bias is not None:
+        y = y + bias
+    return y
+
+
+def modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """x*(1+scale)+shift (FB/wan_video_dit.py:30-31)."""
+    return x * (1 + scale) + shift
+
+
+def adaln(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, eps: float) -> torch.Tensor:
+    """AdaLN-Zero: LayerNorm(x, affine=False)*(1+scale)+shift (FB/fused_adaln.py:522-523, eager branch)."""
+    return layer_norm(x, None, None, eps) * (1 + scale) + shift
+
+
+def gelu_tanh(x: torch.Tensor) -> torch.Tensor:
+    """0.5x(1+tanh(sqrt(2/pi)(x+0.044715x^3))) (nn.GELU(approximate='tanh'), FB/wan_video_dit.py:262)."""
+    xf = x.float()
+    y = 0.5 * xf * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (xf + 0.044715 * xf * xf * xf)))
+    return y.to(x.dtype)
+
+
+def silu(x: torch.Tensor) -> torch.Tensor:
+    xf = x.float()
+    return (xf / (1.0 + torch.exp(-xf))).to(x.dtype)
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, b: Optional[torch.Tensor]) -> torch.Tensor:
+    """y = x W^T + b (nn.Linear)."""
+    return F.linear(x, w, b)
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor] = None,
+              scale: Optional[float] = None) -> torch.Tensor:
+    """softmax(q k^T * scale + mask) v over [B, H, S, Dh], fp32 inside, output in q.dtype.
+
+    Semantics of F.scaled_dot_product_attention as called at FB/wan_video_dit.py:22: bool
+    masks keep True entries, float masks are added; a query row with every key masked
+    yields zeros (what torch's SDPA returns for such rows).
+    """
+    dh = q.shape[-1]
+    sc = (1.0 / math.sqrt(dh)) if scale is None else scale
+    s = torch.matmul(q.float(), k.float().transpose(-1, -2)) * sc
+    if mask is not None:
+        if mask.dtype == torch.bool:
+            s = s.masked_fill(~mask, float("-inf"))
+        else:
+            s = s + mask.float()
+    mx = s.amax(dim=-1, keepdim=True)
+    dead = torch.isinf(mx) & (mx < 0)
+    mx = torch.where(dead, torch.zeros_like(mx), mx)
+    p = torch.exp(s - mx)
+    l = p.sum(dim=-1, keepdim=True)
+    p = p / torch.where(l > 0, l, torch.ones_like(l))
+    out = torch.matmul(p, v.float())
+    return out.to(q.dtype)
+
+
+def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
+                    ctx_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """[B,S,H*Dh] -> heads -> attention -> [B,Sq,H*Dh] (FB/wan_video_dit.py:17-26)."""
+    def heads(t):
+        b, s, nd = t.shape
+        return t.reshape(b, s, num_heads, nd // num_heads).transpose(1, 2)
+
+    o = attention(heads(q), heads(k), heads(v), ctx_mask)
+    b, h, s, d = o.shape
+    return o.transpose(1, 2).reshape(b, s, h * d)
+
+
+# ---------------------------------------------------------------------------
+# Flow-matching scheduler (SCH)
+# ---------------------------------------------------------------------------
+def build_inference_schedule(num_steps: int, shift: float, dtype=torch.float32,
+                             num_train_timesteps: int = 1000) -> Tuple[torch.Tensor, torch.Tensor]:
+    """sigma = s*u/(1+(s-1)u), u = linspace(1,0,N+1) in fp32; t = 1000*sigma[:-1]; delta = diff(sigma).
+
+    Restates SCH:17-19 and SCH:63-80 (both results cast to `dtype`, as the reference casts to
+    the latents' dtype).
+    """
+    if num_steps <= 0:
+        raise ValueError(f"`num_inference_steps` must be positive, got {num_steps}")
+    if shift <= 0:
+        raise ValueError(f"`shift` must be positive, got {shift}")
+    u = torch.linspace(1.0, 0.0, num_steps + 1, dtype=torch.float32)
+    sigma = shift * u / (1.0 + (shift - 1.0) * u)
+    t = sigma[:-1] * float(num_train_timesteps)
+    d = sigma[1:] - sigma[:-1]
+    return t.to(dtype), d.to(dtype)
+
+
+def scheduler_step(model_output: torch.Tensor, delta: torch.Tensor, sample: torch.Tensor) -> torch.Tensor:
+    """sample + model_output * delta, in sample's dtype (SCH:82-88)."""
+    delta = delta.to(sample.dtype)
+    if delta.ndim != 0:
+        delta = delta.reshape(-1, *([1] * (sample.ndim - 1)))
+    return sample + model_output * delta
+
+
+# ---------------------------------------------------------------------------
+# Parameters (state-dict key layout of FB/action_dit.py ActionDiT)
+# ---------------------------------------------------------------------------
+def action_dit_param_shapes(cfg: ActionDiTConfig) -> Dict[str, Tuple[int, ...]]:
+    """Parameter names and shapes of ActionDiT (FB/action_dit.py:76-97, FB/wan_video_dit.py:180-265)."""
+    H, A, Fd, T, Q = cfg.hidden_dim, cfg.attn_dim, cfg.ffn_dim, cfg.text_dim, cfg.freq_dim
+    shapes: Dict[str, Tuple[int, ...]] = {
+        "action_encoder.weight": (H, cfg.action_dim), "action_encoder.bias": (H,),
+        "text_embedding.0.weight": (H, T), "text_embedding.0.bias": (H,),
+        "text_embedding.2.weight": (H, H), "text_embedding.2.bias": (H,),
+        "time_embedding.0.weight": (H, Q), "time_embedding.0.bias": (H,),
+        "time_embedding.2.weight": (H, H), "time_embedding.2.bias": (H,),
+        "time_projection.1.weight": (6 * H, H), "time_projection.1.bias": (6 * H,),
+        "head.weight": (cfg.action_dim, H), "head.bias": (cfg.action_dim,),
+    }
+    for i in range(cfg.num_layers):
+        p = f"blocks.{i}."
+        for att in ("self_attn", "cross_attn"):
+            for n in ("q", "k", "v"):
+                shapes[p + f"{att}.{n}.weight"] = (A, H)
+                shapes[p + f"{att}.{n}.bias"] = (A,)
+            shapes[p + f"{att}.o.weight"] = (H, A)
+            shapes[p + f"{att}.o.bias"] = (H,)
+            shapes[p + f"{att}.norm_q.weight"] = (A,)
+            shapes[p + f"{att}.norm_k.weight"] = (A,)
+        shapes[p + "norm3.weight"] = (H,)
+        shapes[p + "norm3.bias"] = (H,)
+        shapes[p + "ffn.0.weight"] = (Fd, H)
+        shapes[p + "ffn.0.bias"] = (Fd,)
+        shapes[p + "ffn.2.weight"] = (H, Fd)
+        shapes[p + "ffn.2.bias"] = (H,)
+        shapes[p + "modulation"] = (1, 6, H)
+    return shapes
+
+
+def init_action_dit_params(cfg: ActionDiTConfig, seed: int, std: float = 0.02) -> Params:
+    """Seeded synthetic weights: N(0,std) weights and biases, modulation randn/sqrt(H)
+    (FB/wan_video_dit.py:264), norm weights 1 and norm biases 0.  Drawn in sorted-name order
+    from one CPU generator, fp32."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    out: Params = {}
+    for name, shape in sorted(action_dit_param_shapes(cfg).items()):
+        if name.endswith("modulation"):
+            out[name] = torch.randn(shape, generator=g) / math.sqrt(cfg.hidden_dim)
+        elif ".norm_q." in name or ".norm_k." in name or name.endswith("norm3.weight"):
+            out[name] = torch.ones(shape)
+        elif name.endswith("norm3.bias"):
+            out[name] = torch.zeros(shape)
+        else:
+            out[name] = torch.randn(shape, generator=g) * std
+    return out
+
+
+def cast_params(p: Params, dtype) -> Params:
+    return {k: v.to(dtype) for k, v in p.items()}
+
+
+# ---------------------------------------------------------------------------
+# Composite modules
+# ---------------------------------------------------------------------------
+def split_modulation(modulation: torch.Tensor, t_mod: torch.Tensor):
+    """(modulation + t_mod).chunk(6) -> shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp.
+
+    t_mod [B,6,D] gives [B,1,D] pieces; per-token t_mod [B,S,6,D] gives [B,S,D] pieces.
+    Restates FB/wan_video_dit.py:271-280 and FB/mot.py:63-80.
+    """
+    has_seq = t_mod.dim() == 4
+    m = modulation.to(t_mod.dtype) + t_mod
+    parts = m.chunk(6, dim=2 if has_seq else 1)
+    if has_seq:
+        parts = tuple(x.squeeze(2) for x in parts)
+    return parts
+
+
+def self_attention(p: Params, pre: str, x: torch.Tensor, freqs: torch.Tensor, num_heads: int, eps: float,
+                   mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """SelfAttention.forward (FB/wan_video_dit.py:197-204)."""
+    q = rms_norm(linear(x, p[pre + "q.weight"], p[pre + "q.bias"]), p[pre + "norm_q.weight"], eps)
+    k = rms_norm(linear(x, p[pre + "k.weight"], p[pre + "k.bias"]), p[pre + "norm_k.weight"], eps)
+    v = linear(x, p[pre + "v.weight"], p[pre + "v.bias"])
+    q = rope_apply(q, freqs, num_heads)
+    k = rope_apply(k, freqs, num_heads)
+    o = flash_attention(q, k, v, num_heads, mask)
+    return linear(o, p[pre + "o.weight"], p[pre + "o.bias"])
+
+
+def cross_kv(p: Params, pre: str, context: torch.Tensor, eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Context keys/values of CrossAttention: norm_k(k(ctx)), v(ctx) (FB/wan_video_dit.py:226-227)."""
+    k = rms_norm(linear(context, p[pre + "k.weight"], p[pre + "k.bias"]), p[pre + "norm_k.weight"], eps)
+    v = linear(context, p[pre + "v.weight"], p[pre + "v.bias"])
+    return k, v
+
+
+def cross_attention(p: Params, pre: str, x: torch.Tensor, context: torch.Tensor, num_heads: int, eps: float,
+                    mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """CrossAttention.forward (FB/wan_video_dit.py:224-229)."""
+    q = rms_norm(linear(x, p[pre + "q.weight"], p[pre + "q.bias"]), p[pre + "norm_q.weight"], eps)
+    k, v = cross_kv(p, pre, context, eps)
+    o = flash_attention(q, k, v, num_heads, mask)
+    return linear(o, p[pre + "o.weight"], p[pre + "o.bias"])
+
+
+def ffn(p: Params, pre: str, x: torch.Tensor) -> torch.Tensor:
+    """Linear -> GELU(tanh) -> Linear (FB/wan_video_dit.py:262-263)."""
+    h = gelu_tanh(linear(x, p[pre + "ffn.0.weight"], p[pre + "ffn.0.bias"]))
+    return linear(h, p[pre + "ffn.2.weight"], p[pre + "ffn.2.bias"])
+
+
+def dit_block(p: Params, idx: int, x: torch.Tensor, context: torch.Tensor, t_mod: torch.Tensor,
+              freqs: torch.Tensor, num_heads: int, eps: float,
+              context_mask: Optional[torch.Tensor] = None,
+              self_attn_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """DiTBlock.forward (FB/wan_video_dit.py:267-286).
+
+    context_mask: None, bool [B,Sq,L] (unsqueezed to [B,1,Sq,L] as at :268-269) or [B,1,Sq,L].
+    """
+    pre = f"blocks.{idx}."
+    if context_mask is not None and context_mask.dim() == 3:
+        context_mask = context_mask.unsqueeze(1)
+    sh_a, sc_a, g_a, sh_m, sc_m, g_m = split_modulation(p[pre + "modulation"], t_mod)
+    h = adaln(x, sh_a, sc_a, eps)
+    x = x + g_a * self_attention(p, pre + "self_attn.", h, freqs, num_heads, eps, self_attn_mask)
+    x = x + cross_attention(p, pre + "cross_attn.",
+                            layer_norm(x, p[pre + "norm3.weight"], p[pre + "norm3.bias"], eps),
+                            context, num_heads, eps, context_mask)
+    h = adaln(x, sh_m, sc_m, eps)
+    x = x + g_m * ffn(p, pre, h)
+    return x
+
+
+def time_mlp(p: Params, cfg: ActionDiTConfig, timestep: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """t = time_embedding(sinusoid(t)); t_mod = time_projection(t) viewed [B,6,H] (FB/action_dit.py:282-283)."""
+    e = sinusoidal_embedding_1d(cfg.freq_dim, timestep)
+    t = linear(silu(linear(e, p["time_embedding.0.weight"], p["time_embedding.0.bias"])),
+               p["time_embedding.2.weight"], p["time_embedding.2.bias"])
+    t_mod = linear(silu(t), p["time_projection.1.weight"], p["time_projection.1.bias"])
+    return t, t_mod.unflatten(1, (6, cfg.hidden_dim))
+
+
+def text_embedding(p: Params, context: torch.Tensor) -> torch.Tensor:
+    """Linear -> GELU(tanh) -> Linear over the context (FB/action_dit.py:77-81, :286)."""
+    h = gelu_tanh(linear(context, p["text_embedding.0.weight"], p["text_embedding.0.bias"]))
+    return linear(h, p["text_embedding.2.weight"], p["text_embedding.2.bias"])
+
+
+def action_dit_forward(p: Params, cfg: ActionDiTConfig, action_tokens: torch.Tensor, timestep: torch.Tensor,
+                       context: torch.Tensor, context_mask: Optional[torch.Tensor] = None,
+                       context_emb: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """ActionDiT.forward = pre_dit -> blocks -> head (FB/action_dit.py:228-353).
+
+    context_emb, when given, is text_embedding(context) computed earlier (the same value
+    pre_dit recomputes every call)."""
+    b, s, _ = action_tokens.shape
+    if timestep.shape[0] == 1 and b > 1:
+        timestep = timestep.expand(b)
+    _, t_mod = time_mlp(p, cfg, timestep)
+    x = linear(action_tokens, p["action_encoder.weight"], p["action_encoder.bias"])
+    ctx = text_embedding(p, context) if context_emb is None else context_emb
+    cmask = None
+    if context_mask is not None:
+        cmask = context_mask.unsqueeze(1).expand(-1, s, -1)
+    freqs = action_freqs(cfg.attn_head_dim, s)
+    for i in range(cfg.num_layers):
+        x = dit_block(p, i, x, ctx, t_mod, freqs, cfg.num_heads, cfg.eps, cmask)
+    return linear(x, p["head.weight"], p["head.bias"])
+
+
+def denoise_loop(p: Params, cfg: ActionDiTConfig, noise: torch.Tensor, context: torch.Tensor,
+                 num_steps: int, shift: float, context_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Flow-matching Euler loop of the policy call (FB/fastwam.py:1040-1069) over the action expert.
+
+    The latents, schedule and every op run in the dtype of `noise` (the reference casts the
+    seeded CPU noise to the model dtype, FB/fastwam.py:971-977)."""
+    dtype = noise.dtype
+    ts, ds = build_inference_schedule(num_steps, shift, dtype)
+    ctx_emb = text_embedding(p, context)
+    x = noise
+    for t, d in zip(ts, ds):
+        v = action_dit_forward(p, cfg, x, t.reshape(1), context, context_mask, context_emb=ctx_emb)
+        x = scheduler_step(v, d, x)
+    return x
+
+
+def mot_action_forward(p: Params, cfg: ActionDiTConfig, x: torch.Tensor, freqs: torch.Tensor,
+                       t_mod: torch.Tensor, context: torch.Tensor, video_kv: Sequence[Tuple[torch.Tensor, torch.Tensor]],
+                       joint_mask: torch.Tensor, video_seq_len: int,
+                       context_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """MoT action branch over a cached video K/V prefix (FB/mot.py:378-478 and :104-189).
+
+    Per layer: AdaLN -> q,k,v (RMSNorm + RoPE) -> attention of the action rows over
+    cat(video K/V, action K/V) with the action rows of the joint mask -> o-proj + gate ->
+    cross-attention -> AdaLN -> FFN + gate."""
+    sa = x.shape[1]
+    amask = joint_mask[video_seq_len:video_seq_len + sa, :video_seq_len + sa]
+    cmask = context_mask
+    if cmask is not None and cmask.dim() == 3:
+        cmask = cmask.unsqueeze(1)
+    for i in range(cfg.num_layers):
+        pre = f"blocks.{i}."
+        sh_a, sc_a, g_a, sh_m, sc_m, g_m = split_modulation(p[pre + "modulation"], t_mod)
+        h = adaln(x, sh_a, sc_a, cfg.eps)
+        sp = pre + "self_attn."
+        q = rms_norm(linear(h, p[sp + "q.weight"], p[sp + "q.bias"]), p[sp + "norm_q.weight"], cfg.eps)
+        k = rms_norm(linear(h, p[sp + "k.weight"], p[sp + "k.bias"]), p[sp + "norm_k.weight"], cfg.eps)
+        v = linear(h, p[sp + "v.weight"], p[sp + "v.bias"])
+        q = rope_apply(q, freqs, cfg.num_heads)
+        k = rope_apply(k, freqs, cfg.num_heads)
+        kv, vv = video_kv[i]
+        mixed = flash_attention(q, torch.cat([kv, k], dim=1), torch.cat([vv, v], dim=1), cfg.num_heads, amask)
+        x = x + g_a * linear(mixed, p[sp + "o.weight"], p[sp + "o.bias"])
+        x = x + cross_attention(p, pre + "cross_attn.",
+                                layer_norm(x, p[pre + "norm3.weight"], p[pre + "norm3.bias"], cfg.eps),
+                                context, cfg.num_heads, cfg.eps, cmask)
+        h = adaln(x, sh_m, sc_m, cfg.eps)
+        x = x + g_m * ffn(p, pre, h)
+    return x
+
+
+def mot_joint_mask(video_seq_len: int, action_seq_len: int, video_tokens_per_frame: int) -> torch.Tensor:
+    """Joint [video+action] bool mask for first_frame_causal video (FB/fastwam.py:389-410,
+    FB/wan_video_dit.py:493-498): video->video first-frame causal, action->action all,
+    action->first video frame only."""
+    n = video_seq_len + action_seq_len
+    m = torch.zeros((n, n), dtype=torch.bool)
+    vv = torch.ones((video_seq_len, video_seq_len), dtype=torch.bool)
+    ff = min(video_tokens_per_frame, video_seq_len)
+    vv[:ff, ff:] = False
+    m[:video_seq_len, :video_seq_len] = vv
+    m[video_seq_len:, video_seq_len:] = True
+    m[video_seq_len:, :ff] = True
+    return m

@@ -1,0 +1,257 @@
+"""Pins of the CPU oracle: closed forms, library routines, brute force and the golden
+vectors written from the reference modules (tests/golden/make_golden.py)."""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+from safetensors.torch import load_file
+
+from oracle import fam_oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "action_dit_tiny.safetensors")
+TINY = O.ActionDiTConfig(hidden_dim=32, action_dim=7, ffn_dim=64, text_dim=24, freq_dim=16,
+                         eps=1e-6, num_heads=2, attn_head_dim=16, num_layers=2)
+
+
+# --------------------------------------------------------------------------- sinusoid
+def test_sinusoid_closed_forms():
+    pos = torch.tensor([0.0, 1.0, 250.0, 999.5], dtype=torch.float64)
+    e = O.sinusoidal_embedding_1d(256, pos)
+    assert e.shape == (4, 256) and e.dtype == torch.float64
+    # position 0: cos = 1, sin = 0
+    assert torch.all(e[0, :128] == 1) and torch.all(e[0, 128:] == 0)
+    # first frequency is 1: column 0 is cos(p), column 128 is sin(p)
+    assert torch.allclose(e[:, 0], torch.cos(pos)) and torch.allclose(e[:, 128], torch.sin(pos))
+    # last frequency is 10000^(-127/128)
+    f_last = 10000.0 ** (-127.0 / 128.0)
+    assert torch.allclose(e[:, 127], torch.cos(pos * f_last)) and torch.allclose(e[:, 255], torch.sin(pos * f_last))
+    # every (cos, sin) pair is a unit vector
+    assert torch.allclose(e[:, :128] ** 2 + e[:, 128:] ** 2, torch.ones(4, 128, dtype=torch.float64))
+    # cast to the dtype of the positions (bf16 timesteps -> bf16 embedding)
+    assert O.sinusoidal_embedding_1d(16, pos.to(torch.bfloat16)).dtype == torch.bfloat16
+
+
+# --------------------------------------------------------------------------- rope
+def test_rope_tables():
+    f = O.precompute_freqs_cis(64, 1024)
+    assert f.shape == (1024, 32) and f.dtype == torch.complex128
+    assert torch.allclose(f.abs(), torch.ones_like(f.abs()))
+    # angle(pos, j) = pos * 10000^(-2j/64); checked where the angle is below pi
+    pos, j = 3, 5
+    assert math.isclose(torch.angle(f[pos, j]).item(), pos * 10000.0 ** (-2 * j / 64), rel_tol=1e-12)
+    ff, fh, fw = O.precompute_freqs_cis_3d(128)
+    assert (ff.shape[1], fh.shape[1], fw.shape[1]) == (22, 21, 21)  # 44/42/42 dims
+    vf = O.video_freqs((ff, fh, fw), 2, 3, 4)
+    assert vf.shape == (24, 1, 64)
+    # token (f=1, h=2, w=3) -> row 1*12 + 2*4 + 3
+    r = vf[1 * 12 + 2 * 4 + 3, 0]
+    assert torch.equal(r[:22], ff[1]) and torch.equal(r[22:43], fh[2]) and torch.equal(r[43:], fw[3])
+
+
+def test_rope_apply_invariants():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2, 6, 4 * 16, generator=g, dtype=torch.float64)
+    fr = O.action_freqs(16, 6)
+    y = O.rope_apply(x, fr, 4)
+    # position 0 is the identity
+    assert torch.allclose(y[:, 0], x[:, 0])
+    # pairwise norms preserved
+    xp = x.reshape(2, 6, 4, 8, 2)
+    yp = y.reshape(2, 6, 4, 8, 2)
+    assert torch.allclose(xp.norm(dim=-1), yp.norm(dim=-1))
+    # rotating back by the conjugate recovers x
+    assert torch.allclose(O.rope_apply(y, fr.conj(), 4), x)
+    # brute force: a 2x2 rotation matrix per pair
+    c, s = fr.real[:, 0, :], fr.imag[:, 0, :]
+    for t in range(6):
+        for i in range(8):
+            a, b = x[1, t, 2 * 16 + 2 * i], x[1, t, 2 * 16 + 2 * i + 1]
+            exp0 = a * c[t, i] - b * s[t, i]
+            exp1 = a * s[t, i] + b * c[t, i]
+            assert math.isclose(y[1, t, 32 + 2 * i].item(), exp0.item(), abs_tol=1e-12)
+            assert math.isclose(y[1, t, 32 + 2 * i + 1].item(), exp1.item(), abs_tol=1e-12)
+
+
+# --------------------------------------------------------------------------- norms
+def test_norms():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(3, 5, 48, generator=g) * 3 + 0.5
+    ones = torch.ones(48)
+    r = O.rms_norm(x, ones, 1e-6)
+    assert torch.allclose(r.pow(2).mean(-1), torch.ones(3, 5), atol=1e-5)
+    assert torch.allclose(O.rms_norm(7.0 * x, ones, 1e-6), r, atol=1e-5)   # scale invariant
+    ln = O.layer_norm(x, None, None, 1e-6)
+    assert torch.allclose(ln.mean(-1), torch.zeros(3, 5), atol=1e-5)
+    assert torch.allclose(ln.var(-1, unbiased=False), torch.ones(3, 5), atol=1e-4)
+    w, b = torch.randn(48, generator=g), torch.randn(48, generator=g)
+    assert torch.allclose(O.layer_norm(x, w, b, 1e-6), F.layer_norm(x, (48,), w, b, 1e-6), atol=1e-5)
+    z = torch.zeros(3, 1, 48)
+    assert torch.allclose(O.adaln(x, z, z, 1e-6), F.layer_norm(x, (48,), eps=1e-6), atol=1e-5)
+    # bf16: the rounding point before the weight multiply (FB/wan_video_dit.py:166-167)
+    xb = x.to(torch.bfloat16)
+    wb = torch.full((48,), 1.5, dtype=torch.bfloat16)
+    exp = (xb.float() * torch.rsqrt(xb.float().pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16) * wb
+    assert torch.equal(O.rms_norm(xb, wb, 1e-6), exp)
+
+
+def test_gelu_silu_library():
+    x = torch.linspace(-6, 6, 1001)
+    assert torch.allclose(O.gelu_tanh(x), F.gelu(x, approximate="tanh"), atol=1e-6)
+    assert torch.allclose(O.silu(x), F.silu(x), atol=1e-6)
+
+
+# --------------------------------------------------------------------------- attention
+def _brute_attention(q, k, v, mask):
+    B, H, Sq, D = q.shape
+    Sk = k.shape[2]
+    out = np.zeros((B, H, Sq, D))
+    qn, kn, vn = q.double().numpy(), k.double().numpy(), v.double().numpy()
+    for b in range(B):
+        for h in range(H):
+            for i in range(Sq):
+                sc = []
+                for j in range(Sk):
+                    if mask is not None and not bool(mask[i, j]):
+                        continue
+                    sc.append((j, float(np.dot(qn[b, h, i], kn[b, h, j]) / math.sqrt(D))))
+                if not sc:
+                    continue
+                m = max(s for _, s in sc)
+                den = sum(math.exp(s - m) for _, s in sc)
+                for j, s in sc:
+                    out[b, h, i] += math.exp(s - m) / den * vn[b, h, j]
+    return torch.from_numpy(out)
+
+
+@pytest.mark.parametrize("sq,sk", [(3, 5), (4, 1), (6, 9)])
+def test_attention_bruteforce_and_sdpa(sq, sk):
+    g = torch.Generator().manual_seed(sq * 10 + sk)
+    q = torch.randn(2, 2, sq, 8, generator=g)
+    k = torch.randn(2, 2, sk, 8, generator=g)
+    v = torch.randn(2, 2, sk, 8, generator=g)
+    mask = torch.rand(sq, sk, generator=g) > 0.3
+    mask[0] = False                     # a fully masked row -> zeros
+    if sk > 1:
+        mask[1, :] = True
+    o = O.attention(q, k, v, mask)
+    assert torch.allclose(o.double(), _brute_attention(q, k, v, mask), atol=1e-5)
+    assert torch.allclose(o, F.scaled_dot_product_attention(q, k, v, attn_mask=mask), atol=1e-5)
+    assert torch.allclose(O.attention(q, k, v), F.scaled_dot_product_attention(q, k, v), atol=1e-5)
+    # additive masks are added to the scores
+    add = torch.where(mask, 0.0, float("-inf"))
+    assert torch.allclose(O.attention(q, k, v, add)[:, :, 1:], o[:, :, 1:], atol=1e-6)
+
+
+def test_attention_invariants():
+    g = torch.Generator().manual_seed(7)
+    q = torch.randn(1, 3, 5, 16, generator=g)
+    k = torch.randn(1, 3, 7, 16, generator=g)
+    v = torch.randn(1, 3, 7, 16, generator=g)
+    perm = torch.randperm(7, generator=g)
+    assert torch.allclose(O.attention(q, k, v), O.attention(q, k[:, :, perm], v[:, :, perm]), atol=1e-6)
+    assert torch.allclose(O.attention(q, k[:, :, :1], v[:, :, :1]), v[:, :, :1].expand(1, 3, 5, 16), atol=1e-6)
+    o = O.attention(q, k, v)
+    assert torch.all(o.amax(2) <= v.amax(2) + 1e-5) and torch.all(o.amin(2) >= v.amin(2) - 1e-5)
+
+
+# --------------------------------------------------------------------------- scheduler
+def test_schedule_known_answers():
+    t, d = O.build_inference_schedule(10, 5.0)
+    exp_t = [1000, 978.261, 952.381, 921.053, 882.353, 833.333, 769.231, 681.818, 555.556, 357.143]
+    exp_d = [-0.021739, -0.025880, -0.031328, -0.038700, -0.049020, -0.064103, -0.087413,
+             -0.126263, -0.198413, -0.357143]
+    assert np.allclose(t.numpy(), exp_t, atol=2e-3)
+    assert np.allclose(d.numpy(), exp_d, atol=2e-6)
+    assert math.isclose(d.sum().item(), -1.0, abs_tol=1e-6)
+    tb, _ = O.build_inference_schedule(10, 5.0, torch.bfloat16)
+    assert tb.float().tolist() == [1000, 980, 952, 920, 884, 832, 768, 680, 556, 358]
+    t4, d4 = O.build_inference_schedule(4, 5.0)
+    assert np.allclose(t4.numpy(), [1000, 937.5, 833.333, 625], atol=2e-3)
+    assert np.allclose(d4.numpy(), [-0.0625, -0.104167, -0.208333, -0.625], atol=2e-6)
+    _, d1 = O.build_inference_schedule(8, 1.0)
+    assert np.allclose(d1.numpy(), -1.0 / 8, atol=1e-7)
+    with pytest.raises(ValueError):
+        O.build_inference_schedule(0, 5.0)
+    x = torch.ones(2, 3)
+    assert torch.equal(O.scheduler_step(torch.full((2, 3), 2.0), torch.tensor(-0.25), x), torch.full((2, 3), 0.5))
+
+
+# --------------------------------------------------------------------------- goldens
+@pytest.fixture(scope="module")
+def golden():
+    return load_file(GOLDEN)
+
+
+@pytest.fixture(scope="module")
+def tiny_params(golden):
+    p = O.init_action_dit_params(TINY, int(golden["meta.seed"][0]))
+    acc = torch.zeros((), dtype=torch.float64)
+    for i, k in enumerate(sorted(p)):
+        acc = acc + (i + 1) * p[k].double().sum()
+    assert math.isclose(float(acc), float(golden["meta.param_checksum"][0]), rel_tol=0, abs_tol=1e-9)
+    return p
+
+
+def _tol(name):
+    return (2e-5, 2e-5) if name == "fp32" else (3e-2, 3e-2)
+
+
+@pytest.mark.parametrize("name,dt", [("fp32", torch.float32), ("bf16", torch.bfloat16)])
+def test_golden_block(golden, tiny_params, name, dt):
+    p = O.cast_params(tiny_params, dt)
+    S = golden["block.in.x"].shape[1]
+    cm = golden["in.context_mask"].bool().unsqueeze(1).expand(-1, S, -1)
+    y = O.dit_block(p, 0, golden["block.in.x"].to(dt), golden["block.in.context"].to(dt),
+                    golden["block.in.t_mod"].to(dt), O.action_freqs(TINY.attn_head_dim, S),
+                    TINY.num_heads, TINY.eps, cm)
+    rt, at = _tol(name)
+    assert torch.allclose(y.float(), golden[f"block.out.{name}"], rtol=rt, atol=at)
+
+
+@pytest.mark.parametrize("name,dt", [("fp32", torch.float32), ("bf16", torch.bfloat16)])
+def test_golden_action_dit(golden, tiny_params, name, dt):
+    p = O.cast_params(tiny_params, dt)
+    y = O.action_dit_forward(p, TINY, golden["in.actions"].to(dt), golden["in.timestep"].to(dt),
+                             golden["in.context"].to(dt), golden["in.context_mask"].bool())
+    rt, at = _tol(name)
+    assert torch.allclose(y.float(), golden[f"action_dit.out.{name}"], rtol=rt, atol=at)
+
+
+@pytest.mark.parametrize("name,dt", [("fp32", torch.float32), ("bf16", torch.bfloat16)])
+def test_golden_loop(golden, tiny_params, name, dt):
+    p = O.cast_params(tiny_params, dt)
+    ts, ds = O.build_inference_schedule(3, 5.0, dt)
+    assert torch.equal(ts.float(), golden[f"loop.timesteps.{name}"])
+    assert torch.equal(ds.float(), golden[f"loop.deltas.{name}"])
+    y = O.denoise_loop(p, TINY, golden["loop.in.noise"].to(dt), golden["in.context"][:1].to(dt), 3, 5.0)
+    rt, at = _tol(name)
+    assert torch.allclose(y.float(), golden[f"loop.out.{name}"], rtol=rt, atol=at)
+
+
+@pytest.mark.parametrize("name,dt", [("fp32", torch.float32), ("bf16", torch.bfloat16)])
+def test_golden_mot(golden, tiny_params, name, dt):
+    p = O.cast_params(tiny_params, dt)
+    S = golden["mot.in.x"].shape[1]
+    kv = [(golden[f"mot.in.k{i}"].to(dt), golden[f"mot.in.v{i}"].to(dt)) for i in range(TINY.num_layers)]
+    Sv = kv[0][0].shape[1]
+    y = O.mot_action_forward(p, TINY, golden["mot.in.x"].to(dt), O.action_freqs(TINY.attn_head_dim, S),
+                             golden["mot.in.t_mod"].to(dt), golden["mot.in.context"].to(dt), kv,
+                             golden["mot.in.joint_mask"].bool(), Sv)
+    rt, at = _tol(name)
+    assert torch.allclose(y.float(), golden[f"mot.out.{name}"], rtol=rt, atol=at)
+
+
+def test_golden_detects_planted_mistake(golden, tiny_params):
+    """A dropped term in the block (no cross-attention) must fail the golden comparison."""
+    p = O.cast_params(tiny_params, torch.float32)
+    for k in list(p):
+        if ".cross_attn.o." in k:
+            p[k] = torch.zeros_like(p[k])
+    S = golden["block.in.x"].shape[1]
+    cm = golden["in.context_mask"].bool().unsqueeze(1).expand(-1, S, -1)
+    y = O.dit_block(p, 0, golden["block.in.x"], golden["block.in.context"], golden["block.in.t_mod"],
+                    O.action_freqs(TINY.attn_head_dim, S), TINY.num_heads, TINY.eps, cm)
+    assert not torch.allclose(y, golden["block.out.fp32"], rtol=2e-5, atol=2e-5)
