@@ -1,0 +1,347 @@
+#!/usr/bin/env python3
+"""Benchmark: p50 ms per policy call of the action-DiT denoise loop on one MI355X.
+
+Workload (the BASELINE configuration the metric is quoted on, "config 1"): the FastWAM-style
+action expert with 12 blocks (hidden 1024, 16 heads x 64, FFN 4096), 32 action tokens from a
+32x7 chunk, cross-attention to a fixed 1560x1024 context, 10 flow-matching Euler steps with
+shift 5, bf16, batch 1 (use --batch 32 for the throughput point).  Synthetic seeded inputs
+and weights (no checkpoints offline).
+
+A "step" of this benchmark is one policy call: the whole denoise loop for one batch of
+noise, with the inputs already resident in device memory, replayed from one captured HIP
+graph.  Timing mirrors the reference latency workers: W warmups, then K calls each fenced
+by a device synchronize; the value is the p50 (min and p90 also reported).
+
+Extra legs (one JSON line in total):
+  roofline      per kernel class, the launches of one policy call replayed back-to-back from
+                a captured graph between two HIP events on the launching stream; achieved =
+                algorithmic bytes (or flops) per launch / average launch duration, for the
+                class with the largest time per call ("dominant").
+  cpu_baseline  the CPU oracle (fp32 PyTorch restatement of the reference modules) timed on
+                the host cores on a bounded sample of full policy calls.
+  eager_gpu     the reference's eager module sequence (ops as FB/action_dit.py,
+                FB/wan_video_dit.py issue them, bf16) on the same GPU, for comparison.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "faster-action-models_amd"))
+sys.path.insert(0, REPO)
+
+METRIC = "p50 ms per policy call (full denoise loop, bs=1); kernel HBM GB/s / MFMA util"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=40, help="timed policy calls")
+    ap.add_argument("--warmup", type=int, default=25)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-eager", action="store_true")
+    ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--cpu-sample-s", type=float, default=20.0, help="CPU baseline time budget")
+    return ap.parse_args()
+
+
+# --------------------------------------------------------------------------- workload
+def workload(batch: int):
+    from fam.action_dit import ActionDiTConfig
+    cfg = ActionDiTConfig(hidden_dim=1024, action_dim=7, ffn_dim=4096, text_dim=1024, freq_dim=256, eps=1e-6,
+                          num_heads=16, attn_head_dim=64, num_layers=12)
+    return cfg, dict(batch=batch, seq_len=32, ctx_len=1560, num_steps=10, shift=5.0)
+
+
+def inputs(batch: int, seed: int = 1234):
+    import torch
+    g = torch.Generator("cpu").manual_seed(seed)
+    noise = torch.randn(batch, 32, 7, generator=g)
+    ctx = torch.randn(1, 1560, 1024, generator=g)
+    return noise, ctx
+
+
+def pct(xs, q):
+    s = sorted(xs)
+    return s[min(len(s) - 1, max(0, int(math.ceil(q * len(s))) - 1))]
+
+
+# --------------------------------------------------------------------------- roofline
+def kernel_breakdown(model, reps_target: int = 2000):
+    """Per kernel class: launches/call, avg launch duration (HIP events around a captured graph
+    of that class's launches replayed back-to-back), algorithmic bytes and flops per launch."""
+    import torch
+    plan = model.plan
+    classes = sorted({m["kernel"] for m in plan.meta if m["kernel"] not in ("copy",)})
+    stream = torch.cuda.current_stream()
+    out = {}
+    for cls in classes:
+        idx = [i for i, m in enumerate(plan.meta) if m["kernel"] == cls]
+        reps = max(1, reps_target // len(idx))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            s = torch.cuda.current_stream().cuda_stream
+            for _ in range(reps):
+                for i in idx:
+                    plan.steps[i](s)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        avg_us = e0.elapsed_time(e1) * 1e3 / (reps * len(idx))
+        nbytes = sum(plan.meta[i]["bytes"] for i in idx) / len(idx)
+        flops = sum(plan.meta[i]["flops"] for i in idx) / len(idx)
+        out[cls] = {
+            "launches_per_call": len(idx),
+            "avg_launch_us": round(avg_us, 3),
+            "us_per_call": round(avg_us * len(idx), 1),
+            "alg_bytes_per_launch": int(nbytes),
+            "alg_flops_per_launch": int(flops),
+            "achieved_GBs": round(nbytes / (avg_us * 1e-6) / 1e9, 1),
+            "achieved_TFLOPs": round(flops / (avg_us * 1e-6) / 1e12, 2),
+        }
+        del g
+    # graphs replayed kernels in isolation: restore a consistent state with one real call
+    model.run()
+    torch.cuda.synchronize()
+    return out
+
+
+# --------------------------------------------------------------------------- CPU baseline (oracle)
+def cpu_baseline(batch: int, budget_s: float):
+    import torch
+    from oracle import fam_oracle as O
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cfg = O.ActionDiTConfig(hidden_dim=1024, action_dim=7, ffn_dim=4096, text_dim=1024, freq_dim=256, eps=1e-6,
+                            num_heads=16, attn_head_dim=64, num_layers=12)
+    p = {k: v.to(torch.bfloat16).float() for k, v in O.init_action_dit_params(cfg, 4321).items()}
+    noise, ctx = inputs(batch)
+    noise = noise.to(torch.bfloat16).float()
+    ctx = ctx.to(torch.bfloat16).float()
+    ts, ds = O.build_inference_schedule(10, 5.0, torch.bfloat16)
+
+    def call(nsteps=10):
+        emb = O.text_embedding(p, ctx)
+        x = noise
+        for t, d in list(zip(ts.float(), ds.float()))[:nsteps]:
+            x = x + O.action_dit_forward(p, cfg, x, t.reshape(1), ctx.expand(batch, -1, -1), context_emb=emb) * d
+        return x
+
+    call(1)  # warmup: one step
+    times = []
+    t_begin = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        call()
+        times.append((time.perf_counter() - t0) * 1e3)
+        if time.perf_counter() - t_begin + times[-1] / 1e3 > budget_s or len(times) >= 20:
+            break
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(statistics.median(times), 1), "unit": "ms per policy call", "cores": cores,
+            "kind": "port", "cpu_model": model, "min_ms": round(min(times), 1),
+            "sample": f"{len(times)} full policy calls (config 1, B={batch}, fp32 oracle, 12 blocks x 10 steps, "
+                      f"context K/V recomputed per block and step as the reference does) after a 1-step warmup"}
+
+
+# --------------------------------------------------------------------------- eager GPU reference
+class EagerReference:
+    """The reference's eager bf16 op sequence on the GPU (ActionDiT.pre_dit + DiTBlock.forward +
+    head + scheduler step, FB/action_dit.py:228-353, FB/wan_video_dit.py:17-286, SCH:82-88):
+    text embedding and context K/V recomputed every step and block, complex fp64 RoPE, SDPA."""
+
+    def __init__(self, cfg, params, dev):
+        import torch
+        self.cfg, self.dev = cfg, dev
+        self.p = {k: v.to(device=dev, dtype=torch.bfloat16) for k, v in params.items()}
+        d = cfg.attn_head_dim
+        j = torch.arange(0, d, 2)[: d // 2].double()
+        ang = torch.arange(1024).double()[:, None] * (1.0 / (10000.0 ** (j / d)))[None]
+        self.freqs = torch.polar(torch.ones_like(ang), ang)[:32].view(32, 1, -1).to(dev)
+
+    def rope(self, x):
+        import torch
+        b, s, nd = x.shape
+        h = self.cfg.num_heads
+        xc = torch.view_as_complex(x.to(torch.float64).reshape(b, s, h, -1, 2))
+        return torch.view_as_real(xc * self.freqs).flatten(2).to(x.dtype)
+
+    @staticmethod
+    def rms(x, w, eps):
+        import torch
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * w
+
+    def attn(self, q, k, v):
+        import torch.nn.functional as F
+        h = self.cfg.num_heads
+        sh = lambda t: t.unflatten(2, (h, -1)).transpose(1, 2)  # noqa: E731
+        return F.scaled_dot_product_attention(sh(q), sh(k), sh(v)).transpose(1, 2).flatten(2)
+
+    def forward(self, x, t, ctx):
+        import torch
+        import torch.nn.functional as F
+        p, cfg = self.p, self.cfg
+        H, eps = cfg.hidden_dim, cfg.eps
+        half = cfg.freq_dim // 2
+        sinus = torch.outer(t.double(), torch.pow(10000, -torch.arange(half, dtype=torch.float64, device=t.device).div(half)))
+        e = torch.cat([torch.cos(sinus), torch.sin(sinus)], 1).to(t.dtype)
+        te = F.linear(F.silu(F.linear(e, p["time_embedding.0.weight"], p["time_embedding.0.bias"])),
+                      p["time_embedding.2.weight"], p["time_embedding.2.bias"])
+        tmod = F.linear(F.silu(te), p["time_projection.1.weight"], p["time_projection.1.bias"]).unflatten(1, (6, H))
+        x = F.linear(x, p["action_encoder.weight"], p["action_encoder.bias"])
+        c = F.linear(F.gelu(F.linear(ctx, p["text_embedding.0.weight"], p["text_embedding.0.bias"]), approximate="tanh"),
+                     p["text_embedding.2.weight"], p["text_embedding.2.bias"])
+        for i in range(cfg.num_layers):
+            b = f"blocks.{i}."
+            sa, ca = b + "self_attn.", b + "cross_attn."
+            sh_a, sc_a, g_a, sh_m, sc_m, g_m = (p[b + "modulation"] + tmod).chunk(6, dim=1)
+            hx = F.layer_norm(x, (H,), eps=eps) * (1 + sc_a) + sh_a
+            q = self.rope(self.rms(F.linear(hx, p[sa + "q.weight"], p[sa + "q.bias"]), p[sa + "norm_q.weight"], eps))
+            k = self.rope(self.rms(F.linear(hx, p[sa + "k.weight"], p[sa + "k.bias"]), p[sa + "norm_k.weight"], eps))
+            v = F.linear(hx, p[sa + "v.weight"], p[sa + "v.bias"])
+            x = x + g_a * F.linear(self.attn(q, k, v), p[sa + "o.weight"], p[sa + "o.bias"])
+            n3 = F.layer_norm(x, (H,), p[b + "norm3.weight"], p[b + "norm3.bias"], eps)
+            q = self.rms(F.linear(n3, p[ca + "q.weight"], p[ca + "q.bias"]), p[ca + "norm_q.weight"], eps)
+            k = self.rms(F.linear(c, p[ca + "k.weight"], p[ca + "k.bias"]), p[ca + "norm_k.weight"], eps)
+            v = F.linear(c, p[ca + "v.weight"], p[ca + "v.bias"])
+            x = x + F.linear(self.attn(q, k.expand(x.shape[0], -1, -1), v.expand(x.shape[0], -1, -1)),
+                             p[ca + "o.weight"], p[ca + "o.bias"])
+            hx = F.layer_norm(x, (H,), eps=eps) * (1 + sc_m) + sh_m
+            f = F.linear(F.gelu(F.linear(hx, p[b + "ffn.0.weight"], p[b + "ffn.0.bias"]), approximate="tanh"),
+                         p[b + "ffn.2.weight"], p[b + "ffn.2.bias"])
+            x = x + g_m * f
+        return F.linear(x, p["head.weight"], p["head.bias"])
+
+    def call(self, noise, ctx, ts, ds):
+        x = noise
+        for t, d in zip(ts, ds):
+            x = x + self.forward(x, t.reshape(1), ctx) * d
+        return x
+
+
+def eager_gpu_baseline(cfg, params, noise, ctx, warmup=3, iters=10):
+    import torch
+    dev = torch.device("cuda")
+    ref = EagerReference(cfg, params, dev)
+    from fam.action_dit import schedule
+    ts, ds = schedule(10, 5.0)
+    ts, ds = ts.to(dev), ds.to(dev)
+    n = noise.to(dev, torch.bfloat16)
+    c = ctx.to(dev, torch.bfloat16)
+    with torch.no_grad():
+        for _ in range(warmup):
+            ref.call(n, c, ts, ds)
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(iters):
+            t0 = time.perf_counter()
+            ref.call(n, c, ts, ds)
+            torch.cuda.synchronize()
+            times.append((time.perf_counter() - t0) * 1e3)
+    return {"p50_ms": round(statistics.median(times), 3), "min_ms": round(min(times), 3), "iters": iters,
+            "what": "reference eager op sequence restated in bench.py (bf16, torch ops, SDPA), same GPU"}
+
+
+# --------------------------------------------------------------------------- main
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures the denoise loop on ONE GPU: the B=1 loop is a sequential chain of "
+              "launches and this build ships no multi-GPU path (see the sharding notes in DESIGN.md). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from fam.action_dit import FusedActionDiT, synthetic_params
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg, shape = workload(args.batch)
+    params = synthetic_params(cfg, 4321)
+    noise, ctx = inputs(args.batch)
+    log(f"building fused model: B={args.batch}")
+    model = FusedActionDiT(cfg, params, device=dev, **shape)
+    model.set_inputs(noise.to(dev, torch.bfloat16), ctx.to(dev, torch.bfloat16))
+    model.run()
+    torch.cuda.synchronize()
+    model.capture()
+    log(f"captured {model.num_launches} launches per policy call")
+
+    for _ in range(args.warmup):
+        model.run()
+        torch.cuda.synchronize()
+    times = []
+    torch.cuda.synchronize()
+    t_begin = time.perf_counter()
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        model.run()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    total_ms = (time.perf_counter() - t_begin) * 1e3
+    p50 = statistics.median(times)
+    log(f"policy call p50 {p50:.3f} ms (min {min(times):.3f}, p90 {pct(times, 0.9):.3f})")
+
+    out = {
+        "metric": METRIC, "value": round(p50, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(total_ms / max(args.steps, 1), 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) noise and context, N(0,0.02) weights",
+        "config": {"workload": "config1 action-DiT denoise loop: 12 blocks (hidden 1024, 16x64 heads, FFN 4096), "
+                               "32 action tokens (32x7 chunk), ctx 1560x1024, 10 Euler steps shift 5",
+                   "batch": args.batch, "action_tokens": 32, "context_tokens": 1560, "denoise_steps": 10,
+                   "blocks": 12, "hidden": 1024, "parallelism": "single GPU"},
+        "p50_ms": round(p50, 4), "min_ms": round(min(times), 4), "p90_ms": round(pct(times, 0.9), 4),
+        "policy_calls_per_s": round(1e3 / p50, 2), "action_chunks_per_s": round(args.batch * 1e3 / p50, 1),
+        "launches_per_call": model.num_launches,
+    }
+
+    if not args.no_roofline:
+        log("kernel breakdown (graph replays per kernel class)")
+        kb = kernel_breakdown(model)
+        dom = max(kb, key=lambda k: kb[k]["us_per_call"])
+        d = kb[dom]
+        bound = "hbm"
+        out["roofline"] = {"kernel": dom, "bound": bound, "achieved": d["achieved_GBs"], "peak": HBM_PEAK_GBS,
+                           "unit": "GB/s", "frac": round(d["achieved_GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                           "alg_bytes_per_launch": d["alg_bytes_per_launch"], "avg_launch_us": d["avg_launch_us"]}
+        out["kernels"] = kb
+
+    if not args.no_eager:
+        log("eager GPU reference sequence")
+        out["eager_gpu_baseline"] = eager_gpu_baseline(cfg, params, noise, ctx)
+        out["speedup_vs_eager_gpu"] = round(out["eager_gpu_baseline"]["p50_ms"] / p50, 2)
+
+    if not args.no_cpu_baseline:
+        log("CPU baseline (oracle) on host cores")
+        out["cpu_baseline"] = cpu_baseline(args.batch, args.cpu_sample_s)
+
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,93 @@
+// Shared device helpers for the gfx950 kernels of the action-DiT hot path.
+//
+// Conventions used by every kernel in this library:
+//   * storage is bf16 (`__bf16`), arithmetic is fp32; `(__bf16)f` lowers to the
+//     hardware round-to-nearest-even convert (v_cvt_pk_bf16_f32) on gfx950;
+//   * a wavefront is 64 lanes; reductions use cross-lane shuffles, never atomics;
+//   * 16-byte vector loads (8 x bf16) need 16-byte aligned rows, which the host
+//     validation layer checks before any launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/fam_hip.h"
+
+namespace fam {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float to_f(bf16 v) { return (float)v; }
+__device__ __forceinline__ bf16 to_bf(float v) { return (bf16)v; }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Sum over the four lane groups {l, l^16, l^32, l^48} (MFMA 16x16 column reductions).
+__device__ __forceinline__ float group4_sum(float v) {
+  v += __shfl_xor(v, 16, kWave);
+  v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+__device__ __forceinline__ float group4_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  v = fmaxf(v, __shfl_xor(v, 32, kWave));
+  return v;
+}
+
+__device__ __forceinline__ bf16x8 load8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+__device__ __forceinline__ void store8(bf16* p, bf16x8 v) { *reinterpret_cast<bf16x8*>(p) = v; }
+
+__device__ __forceinline__ bf16x8 zero8() {
+  bf16x8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (bf16)0.0f;
+  return z;
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+  const float k0 = 0.7978845608028654f;
+  const float u = k0 * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(u));
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+
+// MFMA 16x16x32 bf16 -> fp32 (gfx950).  Lane l holds A[row=l%16][k=8*(l/16)..+7],
+// B[k=8*(l/16)..+7][col=l%16]; D[row=4*(l/16)+i][col=l%16], i = 0..3.
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace fam
+
+// Host-side helpers shared by the C-ABI wrappers.
+namespace fam_host {
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+}  // namespace fam_host
+
+#define FAM_REQUIRE(cond, code, ...)            \
+  do {                                          \
+    if (!(cond)) {                              \
+      fam_host::set_error(__VA_ARGS__);         \
+      return (code);                            \
+    }                                           \
+  } while (0)

@@ -1,0 +1,284 @@
+// Row-normalisation kernels: AdaLN-Zero / LayerNorm and RMSNorm + rotary embedding.
+//
+// One 64-lane wavefront owns one row; a 256-thread workgroup handles four rows.  Each
+// lane reads 16-byte vectors (8 x bf16) at column (v*64 + lane)*8, so a wavefront's
+// load instruction covers 1 KB of contiguous row.  Rows up to 4096 wide stay in
+// registers between the statistics and the output pass (NV = 8-element vectors per
+// lane); wider rows are re-read (the second read hits L2).
+//
+// Bytes per row (the roofline numerator):  AdaLN  2*D (x) + 2*D (y) + modulation;
+// RMSNorm+RoPE  2*D + 2*D + tables.  Both are HBM-bound streaming kernels.
+#include "fam_common.h"
+
+namespace fam {
+
+struct AdalnArgs {
+  const bf16* x; int64_t xrs;
+  const bf16* shift; const bf16* scale; int64_t mbs, mrs;
+  const bf16* w; const bf16* b;
+  bf16* y; int64_t yrs;
+  int64_t rows, rpb, dim;
+  float eps;
+};
+
+template <int NV>
+__global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.rows) return;  // wave-uniform
+  const bf16* xr = a.x + r * a.xrs;
+  const int64_t D = a.dim;
+  const float invD = 1.0f / (float)D;
+
+  float v[NV > 0 ? NV : 1][8];
+  float s = 0.f;
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = ((int64_t)i * 64 + lane) * 8;
+      if (c < D) {
+        bf16x8 t = load8(xr + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { v[i][e] = to_f(t[e]); s += v[i][e]; }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
+      }
+    }
+  } else {
+    for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
+      bf16x8 t = load8(xr + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += to_f(t[e]);
+    }
+  }
+  const float mean = wave_sum(s) * invD;
+  float q = 0.f;
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = ((int64_t)i * 64 + lane) * 8;
+      if (c < D) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { const float d = v[i][e] - mean; q += d * d; }
+      }
+    }
+  } else {
+    for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
+      bf16x8 t = load8(xr + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { const float d = to_f(t[e]) - mean; q += d * d; }
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(q) * invD + a.eps);
+
+  const int64_t bidx = r / a.rpb, sidx = r - bidx * a.rpb;
+  const int64_t moff = bidx * a.mbs + sidx * a.mrs;
+  bf16* yr = a.y + r * a.yrs;
+
+  auto emit = [&](int64_t c, const float* xv) {
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (xv[e] - mean) * rstd;
+    if (a.w) {
+      bf16x8 wv = load8(a.w + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] *= to_f(wv[e]);
+    }
+    if (a.b) {
+      bf16x8 bv = load8(a.b + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += to_f(bv[e]);
+    }
+    if (a.shift) {
+      bf16x8 sh = load8(a.shift + moff + c);
+      bf16x8 sc = load8(a.scale + moff + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = o[e] * (1.0f + to_f(sc[e])) + to_f(sh[e]);
+    }
+    bf16x8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = to_bf(o[e]);
+    store8(yr + c, out);
+  };
+
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = ((int64_t)i * 64 + lane) * 8;
+      if (c < D) emit(c, v[i]);
+    }
+  } else {
+    for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
+      bf16x8 t = load8(xr + c);
+      float xv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[e] = to_f(t[e]);
+      emit(c, xv);
+    }
+  }
+}
+
+struct RmsRopeArgs {
+  const bf16* x; int64_t xrs;
+  bf16* y; int64_t yrs;
+  int64_t rows, seq, dim;
+  const bf16* w; float eps;
+  const float* cs; const float* sn; int64_t trs, tes, hd;
+};
+
+template <int NV>
+__global__ __launch_bounds__(256) void rmsnorm_rope_kernel(RmsRopeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.rows) return;  // wave-uniform
+  const bf16* xr = a.x + r * a.xrs;
+  const int64_t D = a.dim;
+
+  // All loads of the row happen before any store, so y == x (in place) is safe: each
+  // lane rewrites exactly the 8 elements it read.
+  bf16x8 in[NV > 0 ? NV : 1];
+  float q = 0.f;
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = ((int64_t)i * 64 + lane) * 8;
+      in[i] = (c < D) ? load8(xr + c) : zero8();
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { const float f = to_f(in[i][e]); q += f * f; }
+    }
+  } else {
+    for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
+      bf16x8 t = load8(xr + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { const float f = to_f(t[e]); q += f * f; }
+    }
+  }
+  const float rs = a.w ? rsqrtf(wave_sum(q) / (float)D + a.eps) : 1.0f;
+  const int64_t pos = r % a.seq;
+  bf16* yr = a.y + r * a.yrs;
+  auto emit = [&](int64_t c, bf16x8 t) {
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = to_f(t[e]);
+    if (a.w) {
+      // RMSNorm rounds to the storage dtype before the weight multiply (FB/wan_video_dit.py:166-167).
+      bf16x8 wv = load8(a.w + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = to_f(to_bf(to_f(to_bf(o[e] * rs)) * to_f(wv[e])));
+    }
+    if (a.cs) {
+      const int64_t j0 = (c % a.hd) >> 1;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int64_t t = pos * a.trs + (j0 + p) * a.tes;
+        const float cc = a.cs[t], ss = a.sn[t];
+        const float x0 = o[2 * p], x1 = o[2 * p + 1];
+        o[2 * p] = x0 * cc - x1 * ss;
+        o[2 * p + 1] = x0 * ss + x1 * cc;
+      }
+    }
+    bf16x8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = to_bf(o[e]);
+    store8(yr + c, out);
+  };
+  if constexpr (NV > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int64_t c = ((int64_t)i * 64 + lane) * 8;
+      if (c < D) emit(c, in[i]);
+    }
+  } else {
+    // Wide rows: not in registers; out-of-place only (checked on the host).
+    for (int64_t c = (int64_t)lane * 8; c < D; c += 512) emit(c, load8(xr + c));
+  }
+}
+
+}  // namespace fam
+
+using namespace fam;
+
+static int nv_for(int64_t dim) {
+  const int64_t nv = (dim + 511) / 512;
+  if (nv <= 1) return 1;
+  if (nv <= 2) return 2;
+  if (nv <= 4) return 4;
+  if (nv <= 6) return 6;
+  if (nv <= 8) return 8;
+  return 0;
+}
+
+extern "C" int fam_adaln(const void* x, int64_t x_row_stride, const void* shift, const void* scale,
+                         int64_t mod_batch_stride, int64_t mod_row_stride, const void* ln_weight,
+                         const void* ln_bias, void* y, int64_t y_row_stride, int64_t rows,
+                         int64_t rows_per_batch, int64_t dim, float eps, void* stream) {
+  FAM_REQUIRE(x && y, FAM_ERR_INVALID_ARG, "fam_adaln: x and y must be non-null");
+  FAM_REQUIRE(rows >= 0 && dim >= 8 && dim <= 16384 && dim % 8 == 0, FAM_ERR_INVALID_ARG,
+              "fam_adaln: need dim %% 8 == 0 and 8 <= dim <= 16384 (dim=%lld)", (long long)dim);
+  FAM_REQUIRE((shift == nullptr) == (scale == nullptr), FAM_ERR_INVALID_ARG,
+              "fam_adaln: shift and scale must both be given or both be null");
+  FAM_REQUIRE(rows_per_batch >= 1, FAM_ERR_INVALID_ARG, "fam_adaln: rows_per_batch must be >= 1");
+  FAM_REQUIRE(x_row_stride >= dim && y_row_stride >= dim && x_row_stride % 8 == 0 && y_row_stride % 8 == 0,
+              FAM_ERR_INVALID_ARG, "fam_adaln: row strides must be >= dim and multiples of 8");
+  FAM_REQUIRE(fam_host::aligned16(x) && fam_host::aligned16(y), FAM_ERR_INVALID_ARG,
+              "fam_adaln: x and y must be 16-byte aligned");
+  FAM_REQUIRE(!shift || (fam_host::aligned16(shift) && fam_host::aligned16(scale) &&
+                         mod_batch_stride % 8 == 0 && mod_row_stride % 8 == 0),
+              FAM_ERR_INVALID_ARG, "fam_adaln: shift/scale must be 16-byte aligned with strides %% 8 == 0");
+  FAM_REQUIRE((!ln_weight || fam_host::aligned16(ln_weight)) && (!ln_bias || fam_host::aligned16(ln_bias)),
+              FAM_ERR_INVALID_ARG, "fam_adaln: ln_weight/ln_bias must be 16-byte aligned");
+  if (rows == 0) return FAM_OK;
+  AdalnArgs a{(const bf16*)x, x_row_stride, (const bf16*)shift, (const bf16*)scale, mod_batch_stride,
+              mod_row_stride, (const bf16*)ln_weight, (const bf16*)ln_bias, (bf16*)y, y_row_stride,
+              rows, rows_per_batch, dim, eps};
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  switch (nv_for(dim)) {
+    case 1: hipLaunchKernelGGL(adaln_kernel<1>, grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL(adaln_kernel<2>, grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL(adaln_kernel<4>, grid, block, 0, s, a); break;
+    case 6: hipLaunchKernelGGL(adaln_kernel<6>, grid, block, 0, s, a); break;
+    case 8: hipLaunchKernelGGL(adaln_kernel<8>, grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL(adaln_kernel<0>, grid, block, 0, s, a); break;
+  }
+  return fam_host::check_launch("fam_adaln");
+}
+
+extern "C" int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride,
+                                int64_t rows, int64_t seq_len, int64_t dim, const void* weight, float eps,
+                                const float* cos_tab, const float* sin_tab, int64_t tab_row_stride,
+                                int64_t tab_elem_stride, int64_t head_dim, void* stream) {
+  FAM_REQUIRE(x && y, FAM_ERR_INVALID_ARG, "fam_rmsnorm_rope: x and y must be non-null");
+  FAM_REQUIRE(rows >= 0 && dim >= 8 && dim <= 16384 && dim % 8 == 0, FAM_ERR_INVALID_ARG,
+              "fam_rmsnorm_rope: need dim %% 8 == 0 and 8 <= dim <= 16384 (dim=%lld)", (long long)dim);
+  FAM_REQUIRE(x_row_stride >= dim && y_row_stride >= dim && x_row_stride % 8 == 0 && y_row_stride % 8 == 0,
+              FAM_ERR_INVALID_ARG, "fam_rmsnorm_rope: row strides must be >= dim and multiples of 8");
+  FAM_REQUIRE(fam_host::aligned16(x) && fam_host::aligned16(y) && (!weight || fam_host::aligned16(weight)),
+              FAM_ERR_INVALID_ARG, "fam_rmsnorm_rope: x, y, weight must be 16-byte aligned");
+  FAM_REQUIRE((cos_tab == nullptr) == (sin_tab == nullptr), FAM_ERR_INVALID_ARG,
+              "fam_rmsnorm_rope: cos_tab and sin_tab must both be given or both be null");
+  if (cos_tab) {
+    FAM_REQUIRE(head_dim >= 8 && head_dim % 8 == 0 && dim % head_dim == 0, FAM_ERR_INVALID_ARG,
+                "fam_rmsnorm_rope: head_dim must be a multiple of 8 dividing dim (head_dim=%lld)",
+                (long long)head_dim);
+    FAM_REQUIRE(seq_len >= 1, FAM_ERR_INVALID_ARG, "fam_rmsnorm_rope: seq_len must be >= 1");
+  }
+  const int nv = nv_for(dim);
+  FAM_REQUIRE(nv != 0 || x != y, FAM_ERR_UNSUPPORTED, "fam_rmsnorm_rope: in-place needs dim <= 4096");
+  if (rows == 0) return FAM_OK;
+  RmsRopeArgs a{(const bf16*)x, x_row_stride, (bf16*)y, y_row_stride, rows, seq_len > 0 ? seq_len : 1, dim,
+                (const bf16*)weight, eps, cos_tab, sin_tab, tab_row_stride, tab_elem_stride,
+                head_dim > 0 ? head_dim : 8};
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  switch (nv) {
+    case 1: hipLaunchKernelGGL(rmsnorm_rope_kernel<1>, grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL(rmsnorm_rope_kernel<2>, grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL(rmsnorm_rope_kernel<4>, grid, block, 0, s, a); break;
+    case 6: hipLaunchKernelGGL(rmsnorm_rope_kernel<6>, grid, block, 0, s, a); break;
+    case 8: hipLaunchKernelGGL(rmsnorm_rope_kernel<8>, grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL(rmsnorm_rope_kernel<0>, grid, block, 0, s, a); break;
+  }
+  return fam_host::check_launch("fam_rmsnorm_rope");
+}

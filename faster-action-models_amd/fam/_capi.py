@@ -1,0 +1,127 @@
+"""ctypes binding of libfam_hip.so, the C ABI declared in include/fam_hip.h.
+
+This module is the only place that touches the shared library.  Loading fails loudly
+when the library has not been built: there is no other implementation to fall back to.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+LIB_NAME = "libfam_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+FAM_OK = 0
+FAM_ERR_INVALID_ARG = 1
+FAM_ERR_UNSUPPORTED = 2
+FAM_ERR_LAUNCH = 3
+FAM_ERR_WORKSPACE = 4
+FAM_ABI_VERSION = 1
+
+FAM_MASK_NONE, FAM_MASK_BOOL, FAM_MASK_ADD_F32, FAM_MASK_ADD_BF16 = 0, 1, 2, 3
+FAM_PRO_NONE, FAM_PRO_LAYERNORM, FAM_PRO_ADALN = 0, 1, 2
+FAM_ACT_NONE, FAM_ACT_GELU_TANH, FAM_ACT_SILU = 0, 1, 2
+
+_i64 = C.c_int64
+_vp = C.c_void_p
+
+
+class FamError(RuntimeError):
+    """Raised when an entry point of libfam_hip.so returns an error code."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed (code {code}): {msg}")
+        self.code = code
+
+
+class AttnDesc(C.Structure):
+    """fam_attn_desc (include/fam_hip.h)."""
+    _fields_ = [
+        ("q", _vp), ("q_bs", _i64), ("q_rs", _i64), ("q_hs", _i64),
+        ("k0", _vp), ("k0_bs", _i64), ("k0_rs", _i64), ("k0_hs", _i64),
+        ("v0", _vp), ("v0_bs", _i64), ("v0_rs", _i64), ("v0_hs", _i64),
+        ("k1", _vp), ("k1_bs", _i64), ("k1_rs", _i64), ("k1_hs", _i64),
+        ("v1", _vp), ("v1_bs", _i64), ("v1_rs", _i64), ("v1_hs", _i64),
+        ("o", _vp), ("o_bs", _i64), ("o_rs", _i64), ("o_hs", _i64),
+        ("batch", _i64), ("heads", _i64), ("sq", _i64), ("sk0", _i64), ("sk1", _i64), ("head_dim", _i64),
+        ("scale", C.c_float),
+        ("mask", _vp), ("mask_kind", C.c_int), ("mask_bs", _i64), ("mask_hs", _i64), ("mask_qs", _i64),
+        ("num_splits", C.c_int),
+        ("workspace", _vp), ("workspace_bytes", _i64),
+    ]
+
+
+class GemmDesc(C.Structure):
+    """fam_gemm_desc (include/fam_hip.h)."""
+    _fields_ = [
+        ("a", _vp), ("lda", _i64),
+        ("w", _vp), ("ldw", _i64),
+        ("bias", _vp),
+        ("out", _vp), ("ldo", _i64),
+        ("M", _i64), ("N", _i64), ("K", _i64),
+        ("prologue", C.c_int),
+        ("pro_w", _vp), ("pro_b", _vp),
+        ("pro_shift", _vp), ("pro_scale", _vp),
+        ("pro_mod_bs", _i64), ("pro_mod_rs", _i64),
+        ("pro_eps", C.c_float),
+        ("act", C.c_int),
+        ("res", _vp), ("ldr", _i64),
+        ("gate", _vp), ("gate_bs", _i64), ("gate_rs", _i64), ("gate_ns", _i64),
+        ("rows_per_batch", _i64),
+        ("split_k", C.c_int),
+        ("workspace", _vp), ("workspace_bytes", _i64),
+    ]
+
+
+# name -> (restype, argtypes); every symbol declared in include/fam_hip.h
+SIGNATURES = {
+    "fam_version": (C.c_int, []),
+    "fam_last_error": (C.c_char_p, []),
+    "fam_adaln": (C.c_int, [_vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, C.c_float, _vp]),
+    "fam_rmsnorm_rope": (C.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, C.c_float, _vp, _vp, _i64, _i64,
+                                   _i64, _vp]),
+    "fam_attention": (C.c_int, [C.POINTER(AttnDesc), _vp]),
+    "fam_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, C.c_int]),
+    "fam_gemm": (C.c_int, [C.POINTER(GemmDesc), _vp]),
+    "fam_gemm_workspace_bytes": (_i64, [_i64, _i64, _i64, C.c_int]),
+    "fam_linear_smallk": (C.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "fam_euler_step": (C.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "fam_sinusoid": (C.c_int, [_vp, _vp, _i64, _i64, _vp]),
+    "fam_add_modulation": (C.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+}
+
+_lib = None
+
+
+def load(path: str = LIB_PATH) -> C.CDLL:
+    """Load the library once; raise with build instructions if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(
+            f"{path} not found: build the HIP library first "
+            "(python faster-action-models_amd/build_hip.py, or __graft_entry__.build())")
+    lib = C.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    v = lib.fam_version()
+    if v != FAM_ABI_VERSION:
+        raise ImportError(f"{path}: ABI version {v}, expected {FAM_ABI_VERSION}; rebuild it")
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    """Call an int-returning entry point and raise FamError on a non-zero code."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != FAM_OK:
+        msg = lib.fam_last_error().decode(errors="replace")
+        raise FamError(name, rc, msg)
+
+
+def lib() -> C.CDLL:
+    return load()

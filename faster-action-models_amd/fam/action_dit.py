@@ -1,0 +1,460 @@
+"""The action expert of FastWAM on the fused HIP kernels, and its flow-matching denoise loop.
+
+Semantics follow the reference's eager modules (paths under src/fastwam-baseline/fastwam/
+models/wan22, "FB"):
+
+    ActionDiT.pre_dit / forward / post_dit    FB/action_dit.py:228-353
+    DiTBlock.forward                           FB/wan_video_dit.py:267-286
+    SelfAttention / CrossAttention             FB/wan_video_dit.py:180-229
+    FastWAM.infer_action denoise loop          FB/fastwam.py:1040-1069
+    WanContinuousFlowMatchScheduler            FB/schedulers/scheduler_continuous.py:63-88
+
+The model is organised for one GPU and a fixed call shape (batch, action tokens, context
+length, number of steps), so that every buffer is allocated once and one policy call is a
+fixed sequence of launches -- a "plan" -- that replays eagerly or from a captured HIP graph.
+Per policy call the plan runs:
+
+  prologue (once per call, work that is identical for every denoise step):
+    sinusoid(t_0..t_{T-1}) -> time MLP for all T steps (three GEMMs with SiLU epilogues)
+    -> t_mod + modulation of every block; context embedding (GEMM+GELU, GEMM); the context
+    K/V of every block from one GEMM over the concatenated weights; RMSNorm of each K.
+  per step:
+    action encoder (7 -> H) -> 12 x block -> head GEMM whose epilogue is the Euler update.
+  per block (11 launches):
+    [AdaLN1 + QKV GEMM] -> RMSNorm+RoPE(q) -> RMSNorm+RoPE(k) -> self-attention ->
+    [o GEMM + gate_msa + residual] -> [LayerNorm3 + cross-q GEMM] -> RMSNorm(q) ->
+    cross-attention (keys split over workgroups) -> [cross-o GEMM + residual] ->
+    [AdaLN2 + FFN-up GEMM + GELU] -> [FFN-down GEMM + gate_mlp + residual].
+
+The per-call prologue replaces work the reference repeats inside every step (time MLP,
+text embedding, context K/V projection): the values are identical at every step of one
+call, so computing them once per call is the same arithmetic (the GEAK tree hoists the
+same work, FG/action_dit.py:419-447, FG/mot.py:2580-2593).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from dataclasses import dataclass, asdict
+from typing import Callable, Dict, List, Optional
+
+import torch
+
+from . import _capi
+from ._capi import FamError
+
+_BF16 = torch.bfloat16
+
+
+@dataclass(frozen=True)
+class ActionDiTConfig:
+    """Hyper-parameters of the action expert (FB/action_dit.py:47-103)."""
+
+    hidden_dim: int = 1024
+    action_dim: int = 7
+    ffn_dim: int = 4096
+    text_dim: int = 1024
+    freq_dim: int = 256
+    eps: float = 1e-6
+    num_heads: int = 16
+    attn_head_dim: int = 64
+    num_layers: int = 12
+
+    @property
+    def attn_dim(self) -> int:
+        return self.num_heads * self.attn_head_dim
+
+    def to_dict(self) -> dict:
+        return asdict(self)
+
+
+def param_shapes(cfg: ActionDiTConfig) -> Dict[str, tuple]:
+    """Parameter names (the reference's state-dict keys) and shapes of ActionDiT
+    (FB/action_dit.py:76-97, FB/wan_video_dit.py:180-265)."""
+    H, A, Fd = cfg.hidden_dim, cfg.attn_dim, cfg.ffn_dim
+    shapes = {
+        "action_encoder.weight": (H, cfg.action_dim), "action_encoder.bias": (H,),
+        "text_embedding.0.weight": (H, cfg.text_dim), "text_embedding.0.bias": (H,),
+        "text_embedding.2.weight": (H, H), "text_embedding.2.bias": (H,),
+        "time_embedding.0.weight": (H, cfg.freq_dim), "time_embedding.0.bias": (H,),
+        "time_embedding.2.weight": (H, H), "time_embedding.2.bias": (H,),
+        "time_projection.1.weight": (6 * H, H), "time_projection.1.bias": (6 * H,),
+        "head.weight": (cfg.action_dim, H), "head.bias": (cfg.action_dim,),
+    }
+    for i in range(cfg.num_layers):
+        p = f"blocks.{i}."
+        for att in ("self_attn", "cross_attn"):
+            for n in "qkv":
+                shapes[p + f"{att}.{n}.weight"], shapes[p + f"{att}.{n}.bias"] = (A, H), (A,)
+            shapes[p + f"{att}.o.weight"], shapes[p + f"{att}.o.bias"] = (H, A), (H,)
+            shapes[p + f"{att}.norm_q.weight"] = shapes[p + f"{att}.norm_k.weight"] = (A,)
+        shapes[p + "norm3.weight"] = shapes[p + "norm3.bias"] = (H,)
+        shapes[p + "ffn.0.weight"], shapes[p + "ffn.0.bias"] = (Fd, H), (Fd,)
+        shapes[p + "ffn.2.weight"], shapes[p + "ffn.2.bias"] = (H, Fd), (H,)
+        shapes[p + "modulation"] = (1, 6, H)
+    return shapes
+
+
+def synthetic_params(cfg: ActionDiTConfig, seed: int, std: float = 0.02) -> Dict[str, torch.Tensor]:
+    """Seeded random weights for benchmarking (no checkpoints are available offline):
+    N(0, std) weights and biases, modulation randn/sqrt(H) as the reference initialises it
+    (FB/wan_video_dit.py:264), RMSNorm/LayerNorm weights 1 and LayerNorm biases 0; drawn in
+    sorted-name order from one CPU generator, fp32."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    out = {}
+    for name, shape in sorted(param_shapes(cfg).items()):
+        if name.endswith("modulation"):
+            out[name] = torch.randn(shape, generator=g) / math.sqrt(cfg.hidden_dim)
+        elif ".norm_q." in name or ".norm_k." in name or name.endswith("norm3.weight"):
+            out[name] = torch.ones(shape)
+        elif name.endswith("norm3.bias"):
+            out[name] = torch.zeros(shape)
+        else:
+            out[name] = torch.randn(shape, generator=g) * std
+    return out
+
+
+def rope_1d_tables(head_dim: int, seq_len: int, theta: float = 10000.0, end: int = 1024):
+    """cos/sin [S, Dh/2] fp32 of the 1-D action RoPE: angles pos * theta^(-2j/Dh) built in fp64
+    through torch.polar like precompute_freqs_cis (FB/wan_video_dit.py:49-55, FB/action_dit.py:101)."""
+    if seq_len > end:
+        raise ValueError(f"Action token length {seq_len} exceeds RoPE cache {end}.")
+    j = torch.arange(0, head_dim, 2)[: head_dim // 2].to(torch.float64)
+    inv = 1.0 / (theta ** (j / head_dim))
+    ang = torch.arange(seq_len).to(torch.float64).reshape(-1, 1) * inv.reshape(1, -1)
+    z = torch.polar(torch.ones_like(ang), ang)
+    return z.real.to(torch.float32).contiguous(), z.imag.to(torch.float32).contiguous()
+
+
+def schedule(num_steps: int, shift: float, num_train_timesteps: int = 1000):
+    """bf16 timesteps and deltas of the shifted flow-matching schedule (SCH:63-80)."""
+    u = torch.linspace(1.0, 0.0, num_steps + 1, dtype=torch.float32)
+    sigma = shift * u / (1.0 + (shift - 1.0) * u)
+    return (sigma[:-1] * float(num_train_timesteps)).to(_BF16), (sigma[1:] - sigma[:-1]).to(_BF16)
+
+
+class _Plan:
+    """An ordered list of launches on prebuilt descriptors, each with its kernel class and
+    algorithmic work (HBM bytes and flops that the operation must move/do at minimum)."""
+
+    def __init__(self):
+        self.steps: List[Callable[[int], None]] = []
+        self.names: List[str] = []
+        self.meta: List[dict] = []
+
+    def add(self, name: str, fn: Callable[[int], None], kernel: str = "other", nbytes: int = 0,
+            flops: int = 0) -> None:
+        self.names.append(name)
+        self.steps.append(fn)
+        self.meta.append({"kernel": kernel, "bytes": int(nbytes), "flops": int(flops)})
+
+    def run(self, stream: int) -> None:
+        for fn in self.steps:
+            fn(stream)
+
+
+def _checked(lib, name: str, *args):
+    f = getattr(lib, name)
+
+    def run(stream: int):
+        rc = f(*args, stream)
+        if rc != 0:
+            raise FamError(name, rc, lib.fam_last_error().decode(errors="replace"))
+    return run
+
+
+class FusedActionDiT:
+    """ActionDiT + flow-matching loop on the gfx950 kernels, for a fixed call shape.
+
+    Args:
+        cfg: architecture.
+        params: state dict in the reference's key layout (FB/action_dit.py ActionDiT), any
+            float dtype; converted to bf16 on `device`.
+        batch: B, action chunks denoised together (the context is shared by the batch).
+        seq_len: action tokens per chunk (S).
+        ctx_len: context tokens (L).
+        num_steps / shift: the flow-matching schedule (SCH:63-80).
+    """
+
+    def __init__(self, cfg: ActionDiTConfig, params: Dict[str, torch.Tensor], *, batch: int, seq_len: int,
+                 ctx_len: int, num_steps: int, shift: float = 5.0, device="cuda", mode: str = "denoise"):
+        if mode not in ("denoise", "forward"):
+            raise ValueError(f"mode must be 'denoise' or 'forward', got {mode!r}")
+        if mode == "forward" and num_steps != 1:
+            raise ValueError("forward mode runs one ActionDiT.forward: num_steps must be 1")
+        self.mode = mode
+        self.cfg = cfg
+        self.B, self.S, self.Lc, self.T = batch, seq_len, ctx_len, num_steps
+        self.shift = shift
+        self.device = torch.device(device)
+        self.lib = _capi.load()
+        H, A, Fd, L = cfg.hidden_dim, cfg.attn_dim, cfg.ffn_dim, cfg.num_layers
+        dev = self.device
+
+        def P(name):
+            if name not in params:
+                raise KeyError(f"missing parameter {name}")
+            return params[name].to(device=dev, dtype=_BF16).contiguous()
+
+        def cat(names):
+            return torch.cat([params[n].to(dtype=torch.float32) for n in names], 0).to(device=dev, dtype=_BF16).contiguous()
+
+        # ---- weights
+        self.w = w = {}
+        w["enc_w"], w["enc_b"] = P("action_encoder.weight"), P("action_encoder.bias")
+        w["txt0_w"], w["txt0_b"] = P("text_embedding.0.weight"), P("text_embedding.0.bias")
+        w["txt2_w"], w["txt2_b"] = P("text_embedding.2.weight"), P("text_embedding.2.bias")
+        w["te0_w"], w["te0_b"] = P("time_embedding.0.weight"), P("time_embedding.0.bias")
+        w["te2_w"], w["te2_b"] = P("time_embedding.2.weight"), P("time_embedding.2.bias")
+        w["tp_w"], w["tp_b"] = P("time_projection.1.weight"), P("time_projection.1.bias")
+        w["head_w"], w["head_b"] = P("head.weight"), P("head.bias")
+        w["mod"] = torch.stack([P(f"blocks.{i}.modulation").reshape(6 * H) for i in range(L)]).contiguous()
+        kv_w, kv_b = [], []
+        for i in range(L):
+            p = f"blocks.{i}."
+            w[f"qkv_w{i}"] = cat([p + f"self_attn.{n}.weight" for n in "qkv"])
+            w[f"qkv_b{i}"] = cat([p + f"self_attn.{n}.bias" for n in "qkv"])
+            for n in ("o", "norm_q", "norm_k"):
+                w[f"sa_{n}_w{i}"] = P(p + f"self_attn.{n}.weight")
+            w[f"sa_o_b{i}"] = P(p + "self_attn.o.bias")
+            w[f"ca_q_w{i}"], w[f"ca_q_b{i}"] = P(p + "cross_attn.q.weight"), P(p + "cross_attn.q.bias")
+            w[f"ca_o_w{i}"], w[f"ca_o_b{i}"] = P(p + "cross_attn.o.weight"), P(p + "cross_attn.o.bias")
+            w[f"ca_nq_w{i}"], w[f"ca_nk_w{i}"] = P(p + "cross_attn.norm_q.weight"), P(p + "cross_attn.norm_k.weight")
+            w[f"n3_w{i}"], w[f"n3_b{i}"] = P(p + "norm3.weight"), P(p + "norm3.bias")
+            w[f"ff0_w{i}"], w[f"ff0_b{i}"] = P(p + "ffn.0.weight"), P(p + "ffn.0.bias")
+            w[f"ff2_w{i}"], w[f"ff2_b{i}"] = P(p + "ffn.2.weight"), P(p + "ffn.2.bias")
+            kv_w += [p + "cross_attn.k.weight", p + "cross_attn.v.weight"]
+            kv_b += [p + "cross_attn.k.bias", p + "cross_attn.v.bias"]
+        w["ctxkv_w"], w["ctxkv_b"] = cat(kv_w), cat(kv_b)   # [L*2A, H]: layer-major (K_l, V_l)
+
+        # ---- schedule and RoPE tables
+        ts, ds = schedule(num_steps, shift)
+        self.timesteps = ts.to(dev)
+        self.deltas = ds.to(dev)
+        cos, sin = rope_1d_tables(cfg.attn_head_dim, seq_len)
+        self.rope_cos, self.rope_sin = cos.to(dev), sin.to(dev)
+
+        # ---- activations (static, so a captured graph can replay them)
+        M = batch * seq_len
+        z = lambda *s: torch.zeros(*s, dtype=_BF16, device=dev)  # noqa: E731
+        self.noise_in = z(batch, seq_len, cfg.action_dim)
+        self.context_in = z(ctx_len, cfg.text_dim)
+        self.latents = z(batch, seq_len, cfg.action_dim)
+        self.x = z(M, H)
+        self.qkv = z(M, 3 * A)
+        self.attn = z(M, A)
+        self.qc = z(M, A)
+        self.hid = z(M, Fd)
+        self.head_out = z(M, cfg.action_dim)
+        self.t_emb = z(num_steps, cfg.freq_dim)
+        self.t1 = z(num_steps, H)
+        self.t2 = z(num_steps, H)
+        self.tmod = z(num_steps, 6 * H)
+        self.mods = z(num_steps, L, 6 * H)
+        self.ctx_h = z(ctx_len, H)
+        self.ctx_emb = z(ctx_len, H)
+        self.ctxkv = z(ctx_len, L * 2 * A)
+
+        self._descs: list = []   # keeps ctypes descriptors alive
+        self._ws_need = 0
+        self.plan = self._build_plan()
+        self.workspace = torch.zeros(max(self._ws_need, 256), dtype=torch.uint8, device=dev)
+        for d in self._descs:
+            if isinstance(d, (_capi.GemmDesc, _capi.AttnDesc)):
+                d.workspace, d.workspace_bytes = self.workspace.data_ptr(), self.workspace.numel()
+        self.graph: Optional[torch.cuda.CUDAGraph] = None
+
+    # ------------------------------------------------------------------ plan building
+    def _gemm(self, name, a, w, bias, out, *, prologue=_capi.FAM_PRO_NONE, pro_w=None, pro_b=None,
+              shift=None, scale=None, act=_capi.FAM_ACT_NONE, res=None, gate=None, gate_strides=(0, 0, 1),
+              rows_per_batch=None, M=None, K=None, lda=None, ldo=None, ldr=None):
+        d = _capi.GemmDesc()
+        Mv = a.shape[0] if M is None else M
+        Kv = w.shape[1] if K is None else K
+        d.a, d.lda = a.data_ptr(), (a.stride(0) if lda is None else lda)
+        d.w, d.ldw = w.data_ptr(), w.stride(0)
+        d.bias = bias.data_ptr() if bias is not None else None
+        d.out, d.ldo = out.data_ptr(), (out.stride(0) if ldo is None else ldo)
+        d.M, d.N, d.K = Mv, w.shape[0], Kv
+        d.prologue = prologue
+        d.pro_w = pro_w.data_ptr() if pro_w is not None else None
+        d.pro_b = pro_b.data_ptr() if pro_b is not None else None
+        d.pro_shift = shift.data_ptr() if shift is not None else None
+        d.pro_scale = scale.data_ptr() if scale is not None else None
+        d.pro_mod_bs = d.pro_mod_rs = 0   # one modulation vector for every row (per-sample t)
+        d.pro_eps = float(self.cfg.eps)
+        d.act = act
+        if res is not None:
+            d.res, d.ldr = res.data_ptr(), (res.stride(0) if ldr is None else ldr)
+        d.gate = gate.data_ptr() if gate is not None else None
+        d.gate_bs, d.gate_rs, d.gate_ns = gate_strides
+        d.rows_per_batch = rows_per_batch or max(Mv, 1)
+        d.split_k = 0
+        self._ws_need = max(self._ws_need, self.lib.fam_gemm_workspace_bytes(Mv, d.N, Kv, 0))
+        self._descs.append(d)
+        f = self.lib.fam_gemm
+        lib = self.lib
+        ref = C.byref(d)
+
+        def run(stream):
+            rc = f(ref, stream)
+            if rc != 0:
+                raise FamError(f"fam_gemm[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
+        N = d.N
+        nbytes = 2 * (Mv * Kv + N * Kv + Mv * N) + (2 * N if bias is not None else 0)
+        nbytes += 2 * Mv * N if res is not None else 0
+        nbytes += 2 * N if gate is not None else 0
+        nbytes += 4 * Kv if prologue != _capi.FAM_PRO_NONE else 0
+        self.plan.add(name, run, "gemm", nbytes, 2 * Mv * N * Kv)
+
+    def _attn(self, name, q, q_bs, q_rs, k, k_bs, k_rs, v, v_bs, v_rs, out, sq, sk):
+        cfg = self.cfg
+        Dh = cfg.attn_head_dim
+        d = _capi.AttnDesc()
+        d.q, d.q_bs, d.q_rs, d.q_hs = q, q_bs, q_rs, Dh
+        d.k0, d.k0_bs, d.k0_rs, d.k0_hs = k, k_bs, k_rs, Dh
+        d.v0, d.v0_bs, d.v0_rs, d.v0_hs = v, v_bs, v_rs, Dh
+        d.o, d.o_bs, d.o_rs, d.o_hs = out.data_ptr(), sq * cfg.attn_dim, cfg.attn_dim, Dh
+        d.batch, d.heads, d.sq, d.sk0, d.sk1, d.head_dim = self.B, cfg.num_heads, sq, sk, 0, Dh
+        d.scale = 1.0 / math.sqrt(Dh)
+        d.mask_kind = _capi.FAM_MASK_NONE
+        d.num_splits = 0
+        self._ws_need = max(self._ws_need,
+                            self.lib.fam_attention_workspace_bytes(self.B, cfg.num_heads, sq, sk, Dh, 0))
+        self._descs.append(d)
+        f, lib, ref = self.lib.fam_attention, self.lib, C.byref(d)
+
+        def run(stream):
+            rc = f(ref, stream)
+            if rc != 0:
+                raise FamError(f"fam_attention[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
+        A = cfg.attn_dim
+        kv_batches = self.B if k_bs else 1   # a batch-broadcast context is read once
+        nbytes = 2 * (2 * self.B * sq * A + 2 * kv_batches * sk * A)
+        self.plan.add(name, run, "attention", nbytes, 4 * self.B * cfg.num_heads * sq * sk * Dh)
+
+    def _build_plan(self) -> _Plan:
+        cfg, lib = self.cfg, self.lib
+        H, A, L, Dh = cfg.hidden_dim, cfg.attn_dim, cfg.num_layers, cfg.attn_head_dim
+        B, S, Lc, T = self.B, self.S, self.Lc, self.T
+        M = B * S
+        self.plan = plan = _Plan()
+        w = self.w
+        eps = float(cfg.eps)
+
+        # -- input copy and per-call prologue
+        plan.add("latents<-noise", lambda s: self.latents.copy_(self.noise_in), "copy", 4 * self.latents.numel())
+        plan.add("sinusoid", _checked(lib, "fam_sinusoid", self.timesteps.data_ptr(), self.t_emb.data_ptr(), T,
+                                      cfg.freq_dim), "sinusoid", 2 * T * (1 + cfg.freq_dim))
+        self._gemm("time_emb0", self.t_emb, w["te0_w"], w["te0_b"], self.t1, act=_capi.FAM_ACT_SILU)
+        self._gemm("time_emb2", self.t1, w["te2_w"], w["te2_b"], self.t2, act=_capi.FAM_ACT_SILU)
+        self._gemm("time_proj", self.t2, w["tp_w"], w["tp_b"], self.tmod)
+        plan.add("modulation", _checked(lib, "fam_add_modulation", self.tmod.data_ptr(), w["mod"].data_ptr(),
+                                        self.mods.data_ptr(), T, L, 6 * H), "modulation",
+                 2 * 6 * H * (T + L + T * L))
+        self._gemm("ctx_emb0", self.context_in, w["txt0_w"], w["txt0_b"], self.ctx_h, act=_capi.FAM_ACT_GELU_TANH)
+        self._gemm("ctx_emb2", self.ctx_h, w["txt2_w"], w["txt2_b"], self.ctx_emb)
+        self._gemm("ctx_kv", self.ctx_emb, w["ctxkv_w"], w["ctxkv_b"], self.ctxkv)
+        kvp = self.ctxkv.data_ptr()
+        for l in range(L):
+            plan.add(f"ctx_knorm{l}", _checked(lib, "fam_rmsnorm_rope", kvp + 2 * (l * 2 * A), L * 2 * A,
+                                               kvp + 2 * (l * 2 * A), L * 2 * A, Lc, 1, A,
+                                               w[f"ca_nk_w{l}"].data_ptr(), eps, None, None, 0, 0, 0),
+                     "rmsnorm_rope", 2 * (2 * Lc * A + A))
+
+        lat = self.latents.view(M, cfg.action_dim)
+        x, qkv, attn, qc, hid = self.x, self.qkv, self.attn, self.qc, self.hid
+        qkvp = qkv.data_ptr()
+        for t in range(T):
+            plan.add(f"s{t}.encoder", _checked(lib, "fam_linear_smallk", lat.data_ptr(), cfg.action_dim,
+                                               w["enc_w"].data_ptr(), w["enc_b"].data_ptr(), x.data_ptr(), H,
+                                               M, H, cfg.action_dim), "linear_smallk",
+                     2 * (M * cfg.action_dim + H * cfg.action_dim + H + M * H))
+            for l in range(L):
+                mod = self.mods[t, l]
+                sh_a, sc_a, g_a = mod[0:H], mod[H:2 * H], mod[2 * H:3 * H]
+                sh_m, sc_m, g_m = mod[3 * H:4 * H], mod[4 * H:5 * H], mod[5 * H:6 * H]
+                tag = f"s{t}.b{l}"
+                self._gemm(tag + ".qkv", x, w[f"qkv_w{l}"], w[f"qkv_b{l}"], qkv, prologue=_capi.FAM_PRO_ADALN,
+                           shift=sh_a, scale=sc_a)
+                for nm, off, wn in (("q", 0, "norm_q"), ("k", A, "norm_k")):
+                    plan.add(tag + f".{nm}_norm_rope",
+                             _checked(lib, "fam_rmsnorm_rope", qkvp + 2 * off, 3 * A, qkvp + 2 * off, 3 * A, M, S, A,
+                                      w[f"sa_{wn}_w{l}"].data_ptr(), eps, self.rope_cos.data_ptr(),
+                                      self.rope_sin.data_ptr(), Dh // 2, 1, Dh),
+                             "rmsnorm_rope", 2 * (2 * M * A + A) + 8 * S * (Dh // 2))
+                self._attn(tag + ".self_attn", qkvp, S * 3 * A, 3 * A, qkvp + 2 * A, S * 3 * A, 3 * A,
+                           qkvp + 4 * A, S * 3 * A, 3 * A, attn, S, S)
+                self._gemm(tag + ".o", attn, w[f"sa_o_w{l}"], w[f"sa_o_b{l}"], x, res=x, gate=g_a)
+                self._gemm(tag + ".cross_q", x, w[f"ca_q_w{l}"], w[f"ca_q_b{l}"], qc, prologue=_capi.FAM_PRO_LAYERNORM,
+                           pro_w=w[f"n3_w{l}"], pro_b=w[f"n3_b{l}"])
+                plan.add(tag + ".cross_q_norm",
+                         _checked(lib, "fam_rmsnorm_rope", qc.data_ptr(), A, qc.data_ptr(), A, M, 1, A,
+                                  w[f"ca_nq_w{l}"].data_ptr(), eps, None, None, 0, 0, 0),
+                         "rmsnorm_rope", 2 * (2 * M * A + A))
+                kb = kvp + 2 * (l * 2 * A)
+                self._attn(tag + ".cross_attn", qc.data_ptr(), S * A, A, kb, 0, L * 2 * A, kb + 2 * A, 0, L * 2 * A,
+                           attn, S, Lc)
+                self._gemm(tag + ".cross_o", attn, w[f"ca_o_w{l}"], w[f"ca_o_b{l}"], x, res=x)
+                self._gemm(tag + ".ffn_up", x, w[f"ff0_w{l}"], w[f"ff0_b{l}"], hid, prologue=_capi.FAM_PRO_ADALN,
+                           shift=sh_m, scale=sc_m, act=_capi.FAM_ACT_GELU_TANH)
+                self._gemm(tag + ".ffn_down", hid, w[f"ff2_w{l}"], w[f"ff2_b{l}"], x, res=x, gate=g_m)
+            if self.mode == "forward":
+                # ActionDiT.post_dit: the head alone (FB/action_dit.py:317-318)
+                self._gemm(f"s{t}.head", x, w["head_w"], w["head_b"], self.head_out)
+            else:
+                # head GEMM with the Euler update as its epilogue: latents += delta_t * (x W^T + b)
+                self._gemm(f"s{t}.head_euler", x, w["head_w"], w["head_b"], lat, res=lat,
+                           gate=self.deltas[t:t + 1], gate_strides=(0, 0, 0))
+        return plan
+
+    # ------------------------------------------------------------------ execution
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def set_inputs(self, noise: torch.Tensor, context: torch.Tensor) -> None:
+        """Copy one call's inputs into the static input buffers (noise [B,S,action_dim],
+        context [L, text_dim] or [1, L, text_dim])."""
+        self.noise_in.copy_(noise.reshape(self.noise_in.shape))
+        self.context_in.copy_(context.reshape(self.context_in.shape))
+
+    def run(self) -> None:
+        """Enqueue one policy call on the current stream (graph replay if captured)."""
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self.plan.run(self._stream())
+
+    def capture(self, warmup: int = 1) -> None:
+        """Capture the whole policy call into one HIP graph (kernel and copy nodes only)."""
+        s = torch.cuda.Stream(self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            for _ in range(warmup):
+                self.plan.run(s.cuda_stream)
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.plan.run(self._stream())
+        self.graph = g
+
+    def forward(self, action_tokens: torch.Tensor, timestep: float, context: torch.Tensor) -> torch.Tensor:
+        """One ActionDiT.forward (mode='forward'): head output [B, S, action_dim] for the given
+        noisy action tokens, timestep (rounded to bf16 as the reference's bf16 timestep) and context."""
+        if self.mode != "forward":
+            raise RuntimeError("forward() needs mode='forward'")
+        self.timesteps.fill_(float(timestep))
+        self.set_inputs(action_tokens, context)
+        self.run()
+        return self.head_out.view(self.B, self.S, self.cfg.action_dim).clone()
+
+    def infer(self, noise: torch.Tensor, context: torch.Tensor) -> torch.Tensor:
+        """One policy call: returns the denoised chunk [B, S, action_dim] (bf16, a copy)."""
+        self.set_inputs(noise, context)
+        self.run()
+        return self.latents.clone()
+
+    @property
+    def num_launches(self) -> int:
+        return len(self.plan.steps)

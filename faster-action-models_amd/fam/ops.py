@@ -1,0 +1,463 @@
+"""Drop-in operators for the reference's call sites, each backed by one C-ABI entry point.
+
+The functions keep the reference signatures so that they replace the originals inside the
+existing PyTorch modules:
+
+    adaln_forward(x, norm, shift, scale)           FB/fused_adaln.py:513-523
+    layer_norm(x, weight, bias, eps)               nn.LayerNorm (norm3, FB/wan_video_dit.py:261)
+    rms_norm(x, weight, eps) / RMSNorm             FB/wan_video_dit.py:156-167
+    rope_apply(x, freqs, num_heads)                FB/wan_video_dit.py:58-70, FG/wan_video_dit.py:193-215
+    rope_apply_cae(x, freqs, num_heads, force_complex=False)
+                                                   CA/wan_video_dit.py:769-799
+    flash_attention(q, k, v, num_heads, ctx_mask=None, compatibility_mode=True)
+                                                   FB/wan_video_dit.py:17-26, FG:18-39, CA:569-587
+    linear(x, weight, bias)                        nn.Linear on the hot path
+    euler_step(model_output, delta, sample)        WanContinuousFlowMatchScheduler.step, SCH:82-88
+
+(FB = src/fastwam-baseline/fastwam/models/wan22, FG = src/fastwam-geak/..., CA =
+src/cae-fastwam/..., SCH = FB/schedulers/scheduler_continuous.py.)
+
+Tensors must be bf16 CUDA (HIP) tensors with a contiguous last dimension; anything else
+raises -- there is no fallback implementation.  Outputs are new tensors allocated on the
+input's device, launches go to torch's current stream.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from . import _capi
+from ._capi import call
+
+_BF16 = torch.bfloat16
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _check(t: torch.Tensor, name: str, dtype=_BF16) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on a HIP device (got {t.device})")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+    if t.dim() > 0 and t.stride(-1) != 1 and t.shape[-1] != 1:
+        raise ValueError(f"{name} must have a contiguous last dimension")
+
+
+def _rows(x: torch.Tensor) -> Tuple[torch.Tensor, int, int, int]:
+    """View x as [B*S, D]; returns (2-D view, rows, rows_per_batch, D)."""
+    D = x.shape[-1]
+    if x.dim() == 3:
+        B, S = x.shape[0], x.shape[1]
+    elif x.dim() == 2:
+        B, S = 1, x.shape[0]
+    else:
+        raise ValueError(f"expected a 2-D or 3-D tensor, got shape {tuple(x.shape)}")
+    x2 = x.reshape(B * S, D)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    return x2, B * S, S, D
+
+
+# --------------------------------------------------------------------------- workspaces
+class Workspace:
+    """Per-(device, stream) scratch for split-K / split-KV partials and tile counters.
+
+    The counter area must be zero before first use; kernels leave it zero, so the buffer is
+    zero-filled once when it is allocated (a fill kernel, never a memset node)."""
+
+    _pool: Dict[Tuple[int, int], torch.Tensor] = {}
+
+    @classmethod
+    def get(cls, device: torch.device, nbytes: int) -> torch.Tensor:
+        if nbytes <= 0:
+            return None
+        key = (device.index if device.index is not None else torch.cuda.current_device(),
+               torch.cuda.current_stream(device).cuda_stream)
+        buf = cls._pool.get(key)
+        if buf is None or buf.numel() < nbytes:
+            size = max(nbytes, 1 << 20)
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
+            buf.zero_()
+            cls._pool[key] = buf
+        return buf
+
+
+# --------------------------------------------------------------------------- norms
+def _broadcast_mod(t: torch.Tensor, x: torch.Tensor, name: str) -> Tuple[torch.Tensor, int, int]:
+    """Broadcast shift/scale to x's shape; returns (tensor, batch stride, row stride)."""
+    _check(t, name)
+    tb = torch.broadcast_to(t, x.shape)
+    if tb.stride(-1) != 1:
+        tb = tb.contiguous()
+    if x.dim() == 3:
+        bs, rs = tb.stride(0), tb.stride(1)
+    else:
+        bs, rs = 0, tb.stride(0)
+    if bs % 8 or rs % 8 or tb.data_ptr() % 16:
+        tb = tb.contiguous()
+        bs, rs = (tb.stride(0), tb.stride(1)) if x.dim() == 3 else (0, tb.stride(0))
+    return tb, bs, rs
+
+
+def _adaln_launch(x: torch.Tensor, shift, scale, weight, bias, eps: float) -> torch.Tensor:
+    _check(x, "x")
+    x2, rows, rpb, D = _rows(x)
+    y = torch.empty((rows, D), dtype=_BF16, device=x.device)
+    sh_p = sc_p = None
+    bs = rs = 0
+    if shift is not None:
+        sh, bs, rs = _broadcast_mod(shift, x, "shift")
+        sc, bs2, rs2 = _broadcast_mod(scale, x, "scale")
+        if (bs, rs) != (bs2, rs2):
+            sc = torch.broadcast_to(scale, x.shape).contiguous()
+            sh = torch.broadcast_to(shift, x.shape).contiguous()
+            bs, rs = (sh.stride(0), sh.stride(1)) if x.dim() == 3 else (0, sh.stride(0))
+        sh_p, sc_p = sh.data_ptr(), sc.data_ptr()
+        keep = (sh, sc)  # noqa: F841  (kept alive across the launch)
+    w_p = b_p = None
+    if weight is not None:
+        _check(weight, "ln weight")
+        w_p = weight.contiguous().data_ptr()
+    if bias is not None:
+        _check(bias, "ln bias")
+        b_p = bias.contiguous().data_ptr()
+    call("fam_adaln", x2.data_ptr(), x2.stride(0), sh_p, sc_p, bs, rs, w_p, b_p,
+         y.data_ptr(), D, rows, rpb, D, float(eps), _stream(x))
+    return y.reshape(x.shape)
+
+
+def adaln_forward(x: torch.Tensor, norm: torch.nn.LayerNorm, shift: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """norm(x) * (1 + scale) + shift in one kernel (FB/fused_adaln.py:513-523).
+
+    `norm` is the block's nn.LayerNorm (its eps and, if elementwise_affine, weight/bias are
+    used); shift/scale broadcast as [B,1,D] (per sample) or [B,S,D] (per token)."""
+    w = norm.weight if getattr(norm, "elementwise_affine", False) else None
+    b = norm.bias if getattr(norm, "elementwise_affine", False) else None
+    return _adaln_launch(x, shift, scale, w, b, norm.eps)
+
+
+def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor], eps: float) -> torch.Tensor:
+    """nn.LayerNorm forward over the last dim (FB/wan_video_dit.py:258-261)."""
+    return _adaln_launch(x, None, None, weight, bias, eps)
+
+
+def modulate_layer_norm(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """modulate(LayerNorm(x, affine=False), shift, scale) -- the CAE form (CA/wan_video_dit.py:590-591)."""
+    return _adaln_launch(x, shift, scale, None, None, eps)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm.forward: bf16(x*rsqrt(mean(x^2)+eps)) * weight (FB/wan_video_dit.py:156-167)."""
+    _check(x, "x")
+    _check(weight, "weight")
+    x2, rows, _, D = _rows(x)
+    y = torch.empty((rows, D), dtype=_BF16, device=x.device)
+    call("fam_rmsnorm_rope", x2.data_ptr(), x2.stride(0), y.data_ptr(), D, rows, 1, D,
+         weight.contiguous().data_ptr(), float(eps), None, None, 0, 0, 0, _stream(x))
+    return y.reshape(x.shape)
+
+
+class RMSNorm(torch.nn.Module):
+    """Module form with the reference's parameter layout (`weight` [dim], eps)."""
+
+    def __init__(self, dim: int, eps: float = 1e-5):
+        super().__init__()
+        self.eps = eps
+        self.weight = torch.nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return rms_norm(x, self.weight, self.eps)
+
+
+# --------------------------------------------------------------------------- rope
+_TABLES: Dict[tuple, Tuple[torch.Tensor, torch.Tensor, int, int]] = {}
+
+
+def rope_tables(freqs: torch.Tensor, layout: str, device: torch.device):
+    """(cos, sin, row stride, element stride) fp32 device tables for a RoPE `freqs` tensor.
+
+    layout 'complex'     complex [S, 1, Dh/2] (FB/wan_video_dit.py:49-55)
+           'cat'         real [S, 1, Dh] = cat(cos, sin) (FG/wan_video_dit.py:173-177)
+           'interleaved' real [S, 1, Dh] = (cos0, sin0, cos1, sin1, ...) (CA/wan_video_dit.py:736-766)
+    Conversions (complex -> fp32, fp64 -> fp32, host -> device) are cached per source tensor."""
+    key = (freqs.data_ptr(), tuple(freqs.shape), freqs.dtype, str(freqs.device), freqs._version, layout, str(device))
+    hit = _TABLES.get(key)
+    if hit is not None:
+        return hit
+    S = freqs.shape[0]
+    if layout == "complex":
+        f = freqs.reshape(S, -1)
+        cos = f.real.to(device=device, dtype=torch.float32).contiguous()
+        sin = f.imag.to(device=device, dtype=torch.float32).contiguous()
+        res = (cos, sin, cos.shape[1], 1)
+    else:
+        f = freqs.reshape(S, -1).to(device=device, dtype=torch.float32).contiguous()
+        half = f.shape[1] // 2
+        if layout == "cat":
+            res = (f, f[:, half:], f.shape[1], 1)
+        elif layout == "interleaved":
+            res = (f, f[:, 1:], f.shape[1], 2)
+        else:
+            raise ValueError(f"unknown RoPE layout {layout!r}")
+    if len(_TABLES) > 64:
+        _TABLES.clear()
+    _TABLES[key] = res
+    return res
+
+
+def _rope_launch(x: torch.Tensor, freqs: torch.Tensor, num_heads: int, layout: str,
+                 weight: Optional[torch.Tensor] = None, eps: float = 0.0) -> torch.Tensor:
+    _check(x, "x")
+    if x.dim() != 3:
+        raise ValueError(f"x must be [B, S, H*Dh], got {tuple(x.shape)}")
+    B, S, ND = x.shape
+    if ND % num_heads:
+        raise ValueError(f"last dim {ND} not divisible by num_heads {num_heads}")
+    Dh = ND // num_heads
+    if freqs.shape[0] < S:
+        raise ValueError(f"freqs has {freqs.shape[0]} positions, need {S}")
+    cos, sin, trs, tes = rope_tables(freqs, layout, x.device)
+    x2, rows, _, D = _rows(x)
+    y = torch.empty((rows, D), dtype=_BF16, device=x.device)
+    w_p = weight.contiguous().data_ptr() if weight is not None else None
+    call("fam_rmsnorm_rope", x2.data_ptr(), x2.stride(0), y.data_ptr(), D, rows, S, D, w_p, float(eps),
+         cos.data_ptr(), sin.data_ptr(), trs, tes, Dh, _stream(x))
+    return y.reshape(x.shape)
+
+
+def rope_apply(x: torch.Tensor, freqs: torch.Tensor, num_heads: int) -> torch.Tensor:
+    """Rotary embedding with the FB/FG call signature: freqs complex [S,1,Dh/2] or packed
+    real cat(cos, sin) [S,1,Dh] (FB/wan_video_dit.py:58-70, FG/wan_video_dit.py:193-215)."""
+    return _rope_launch(x, freqs, num_heads, "complex" if freqs.is_complex() else "cat")
+
+
+def rope_apply_cae(x: torch.Tensor, freqs: torch.Tensor, num_heads: int, force_complex: bool = False) -> torch.Tensor:
+    """Rotary embedding with the CAE call signature: freqs complex or interleaved real
+    (cos, sin) pairs [S,1,Dh] (CA/wan_video_dit.py:769-799).  force_complex only selects the
+    reference's arithmetic route; the rotation is the same."""
+    del force_complex
+    return _rope_launch(x, freqs, num_heads, "complex" if freqs.is_complex() else "interleaved")
+
+
+def rms_norm_rope(x: torch.Tensor, weight: torch.Tensor, eps: float, freqs: torch.Tensor, num_heads: int,
+                  layout: str = "complex") -> torch.Tensor:
+    """rope_apply(RMSNorm(x), freqs) in one kernel (the q/k post-processing, FG/mot.py:786-816)."""
+    return _rope_launch(x, freqs, num_heads, layout, weight, eps)
+
+
+# --------------------------------------------------------------------------- attention
+def _mask_args(mask: Optional[torch.Tensor], B: int, H: int, Sq: int, Sk: int):
+    if mask is None:
+        return None, _capi.FAM_MASK_NONE, 0, 0, 0, None
+    if mask.device.type != "cuda":
+        raise ValueError("ctx_mask must be on the device of q")
+    if mask.dtype == torch.bool:
+        kind = _capi.FAM_MASK_BOOL
+        m = mask
+    elif mask.dtype == torch.float32:
+        kind, m = _capi.FAM_MASK_ADD_F32, mask
+    elif mask.dtype == torch.bfloat16:
+        kind, m = _capi.FAM_MASK_ADD_BF16, mask
+    else:
+        kind, m = _capi.FAM_MASK_ADD_F32, mask.float()
+    m4 = torch.broadcast_to(m, (B, H, Sq, Sk))
+    if m4.stride(-1) != 1:
+        m4 = m4.contiguous()
+    return m4.data_ptr(), kind, m4.stride(0), m4.stride(1), m4.stride(2), m4
+
+
+def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
+                   mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+                   k_prefix: Optional[torch.Tensor] = None, v_prefix: Optional[torch.Tensor] = None,
+                   num_splits: int = 0, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Attention on [B, S, H*Dh] tensors; keys/values are cat(k_prefix, k) when a prefix is
+    given (the MoT joint attention over a cached video K/V, FB/mot.py:446-478) without
+    materialising the concatenation."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _check(t, n)
+        if t.dim() != 3:
+            raise ValueError(f"{n} must be [B, S, H*Dh], got {tuple(t.shape)}")
+    B, Sq, ND = q.shape
+    Dh = ND // num_heads
+    if ND % num_heads or k.shape[-1] != ND or v.shape[-1] != ND:
+        raise ValueError("q/k/v last dims must equal num_heads * head_dim")
+    if k.shape[:2] != v.shape[:2]:
+        raise ValueError("k and v must have the same [B, S]")
+    if k.shape[0] != B and k.shape[0] != 1:
+        raise ValueError("k batch must equal q batch (or 1 to broadcast)")
+    segs = []
+    if k_prefix is not None:
+        _check(k_prefix, "k_prefix")
+        _check(v_prefix, "v_prefix")
+        segs.append((k_prefix, v_prefix))
+    segs.append((k, v))
+    Sk = sum(s[0].shape[1] for s in segs)
+    if out is None:
+        out = torch.empty((B, Sq, ND), dtype=_BF16, device=q.device)
+    d = _capi.AttnDesc()
+    d.q, d.q_bs, d.q_rs, d.q_hs = q.data_ptr(), q.stride(0), q.stride(1), Dh
+    (k0, v0) = segs[0]
+    d.k0, d.k0_bs, d.k0_rs, d.k0_hs = k0.data_ptr(), (k0.stride(0) if k0.shape[0] == B else 0), k0.stride(1), Dh
+    d.v0, d.v0_bs, d.v0_rs, d.v0_hs = v0.data_ptr(), (v0.stride(0) if v0.shape[0] == B else 0), v0.stride(1), Dh
+    d.sk0 = k0.shape[1]
+    if len(segs) > 1:
+        (k1, v1) = segs[1]
+        d.k1, d.k1_bs, d.k1_rs, d.k1_hs = k1.data_ptr(), (k1.stride(0) if k1.shape[0] == B else 0), k1.stride(1), Dh
+        d.v1, d.v1_bs, d.v1_rs, d.v1_hs = v1.data_ptr(), (v1.stride(0) if v1.shape[0] == B else 0), v1.stride(1), Dh
+        d.sk1 = k1.shape[1]
+    d.o, d.o_bs, d.o_rs, d.o_hs = out.data_ptr(), out.stride(0), out.stride(1), Dh
+    d.batch, d.heads, d.sq, d.head_dim = B, num_heads, Sq, Dh
+    d.scale = (1.0 / math.sqrt(Dh)) if scale is None else float(scale)
+    mp, kind, mbs, mhs, mqs, keep = _mask_args(mask, B, num_heads, Sq, Sk)
+    d.mask, d.mask_kind, d.mask_bs, d.mask_hs, d.mask_qs = mp, kind, mbs, mhs, mqs
+    d.num_splits = num_splits
+    nbytes = _capi.lib().fam_attention_workspace_bytes(B, num_heads, Sq, Sk, Dh, num_splits)
+    ws = Workspace.get(q.device, nbytes)
+    if ws is not None:
+        d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
+    call("fam_attention", C.byref(d), _stream(q))
+    return out
+
+
+def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
+                    ctx_mask: Optional[torch.Tensor] = None, compatibility_mode: bool = True) -> torch.Tensor:
+    """softmax(q k^T / sqrt(Dh) + mask) v over [B, S, H*Dh] tensors -> [B, Sq, H*Dh]
+    (FB/wan_video_dit.py:17-26).  Bool masks keep True entries; float masks are added."""
+    if not compatibility_mode:
+        raise NotImplementedError("Only compatibility mode is implemented for flash attention. "
+                                  "Please set compatibility_mode=True.")
+    return attention_bshd(q, k, v, num_heads, ctx_mask)
+
+
+# --------------------------------------------------------------------------- linear
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = x W^T + b for bf16 x [..., K], W [N, K] (nn.Linear)."""
+    _check(x, "x")
+    _check(weight, "weight")
+    K = x.shape[-1]
+    N = weight.shape[0]
+    if weight.shape[1] != K:
+        raise ValueError(f"weight {tuple(weight.shape)} does not match input features {K}")
+    x2 = x.reshape(-1, K)
+    if x2.stride(-1) != 1:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    b = None
+    if bias is not None:
+        _check(bias, "bias")
+        b = bias.contiguous()
+    y = torch.empty((M, N), dtype=_BF16, device=x.device)
+    aligned = (K % 8 == 0 and x2.stride(0) % 8 == 0 and x2.data_ptr() % 16 == 0 and w.data_ptr() % 16 == 0)
+    if not aligned:
+        if K > 64:
+            x2 = x2.contiguous()
+            if x2.data_ptr() % 16 or K % 8:
+                raise ValueError(f"linear: unsupported K={K} (needs K % 8 == 0 or K <= 64)")
+        else:
+            call("fam_linear_smallk", x2.data_ptr(), x2.stride(0), w.data_ptr(),
+                 b.data_ptr() if b is not None else None, y.data_ptr(), N, M, N, K, _stream(x))
+            return y.reshape(*x.shape[:-1], N)
+    gemm(x2, w, b, y)
+    return y.reshape(*x.shape[:-1], N)
+
+
+def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: torch.Tensor, *,
+         prologue: int = _capi.FAM_PRO_NONE, pro_w=None, pro_b=None, pro_shift=None, pro_scale=None,
+         pro_mod_bs: int = 0, pro_mod_rs: int = 0, pro_eps: float = 1e-6, act: int = _capi.FAM_ACT_NONE,
+         res: Optional[torch.Tensor] = None, gate: Optional[torch.Tensor] = None, gate_bs: int = 0,
+         gate_rs: int = 0, gate_ns: int = 1, rows_per_batch: Optional[int] = None, split_k: int = 0) -> None:
+    """Fused GEMM on 2-D views (see fam_gemm in include/fam_hip.h): a [M, K], w [N, K], out [M, N]."""
+    M, K = a.shape
+    N = w.shape[0]
+    d = _capi.GemmDesc()
+    d.a, d.lda = a.data_ptr(), a.stride(0)
+    d.w, d.ldw = w.data_ptr(), w.stride(0)
+    d.bias = bias.data_ptr() if bias is not None else None
+    d.out, d.ldo = out.data_ptr(), out.stride(0)
+    d.M, d.N, d.K = M, N, K
+    d.prologue = prologue
+    d.pro_w = pro_w.data_ptr() if pro_w is not None else None
+    d.pro_b = pro_b.data_ptr() if pro_b is not None else None
+    d.pro_shift = pro_shift.data_ptr() if pro_shift is not None else None
+    d.pro_scale = pro_scale.data_ptr() if pro_scale is not None else None
+    d.pro_mod_bs, d.pro_mod_rs, d.pro_eps = pro_mod_bs, pro_mod_rs, float(pro_eps)
+    d.act = act
+    d.res, d.ldr = (res.data_ptr(), res.stride(0)) if res is not None else (None, 0)
+    d.gate = gate.data_ptr() if gate is not None else None
+    d.gate_bs, d.gate_rs, d.gate_ns = gate_bs, gate_rs, gate_ns
+    d.rows_per_batch = rows_per_batch if rows_per_batch is not None else max(M, 1)
+    d.split_k = split_k
+    nbytes = _capi.lib().fam_gemm_workspace_bytes(M, N, K, split_k)
+    ws = Workspace.get(a.device, nbytes)
+    if ws is not None:
+        d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
+    call("fam_gemm", C.byref(d), _stream(a))
+
+
+# --------------------------------------------------------------------------- sampler
+def euler_step(model_output: torch.Tensor, delta: torch.Tensor, sample: torch.Tensor,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """sample + model_output * delta in bf16 (SCH:82-88); delta a scalar or per-batch [B]."""
+    _check(sample, "sample")
+    _check(model_output, "model_output")
+    if model_output.shape != sample.shape:
+        raise ValueError("model_output and sample must have the same shape")
+    if not isinstance(delta, torch.Tensor):
+        delta = torch.tensor(float(delta))
+    delta = delta.to(device=sample.device, dtype=_BF16).contiguous()
+    n = sample.numel()
+    if delta.numel() == 1:
+        inner = max(n, 1)
+    else:
+        if delta.numel() != sample.shape[0]:
+            raise ValueError("delta must be a scalar or have one value per batch row")
+        inner = max(n // sample.shape[0], 1)
+    s = sample.contiguous()
+    v = model_output.contiguous()
+    if out is None:
+        out = torch.empty_like(s)
+    call("fam_euler_step", s.data_ptr(), v.data_ptr(), delta.data_ptr(), out.data_ptr(), n, inner, _stream(s))
+    return out
+
+
+class WanContinuousFlowMatchScheduler:
+    """Inference half of the reference scheduler (SCH:4-88): the shifted schedule and the
+    Euler `step`, the latter on the device through fam_euler_step."""
+
+    def __init__(self, num_train_timesteps: int = 1000, shift: float = 5.0, eps: float = 1e-10):
+        if num_train_timesteps <= 0:
+            raise ValueError(f"`num_train_timesteps` must be positive, got {num_train_timesteps}")
+        if shift <= 0:
+            raise ValueError(f"`shift` must be positive, got {shift}")
+        self.num_train_timesteps = int(num_train_timesteps)
+        self.shift = float(shift)
+        self.eps = float(eps)
+
+    @staticmethod
+    def _phi(u: torch.Tensor, shift: float) -> torch.Tensor:
+        return shift * u / (1.0 + (shift - 1.0) * u)
+
+    def build_inference_schedule(self, num_inference_steps: int, device, dtype, shift_override=None):
+        """(timesteps, deltas) in `dtype` on `device`; fp32 arithmetic on the host (SCH:63-80)."""
+        if num_inference_steps <= 0:
+            raise ValueError(f"`num_inference_steps` must be positive, got {num_inference_steps}")
+        shift = self.shift if shift_override is None else float(shift_override)
+        if shift <= 0:
+            raise ValueError(f"`shift` must be positive, got {shift}")
+        u = torch.linspace(1.0, 0.0, num_inference_steps + 1, dtype=torch.float32)
+        sigma = self._phi(u, shift)
+        t = sigma[:-1] * float(self.num_train_timesteps)
+        d = sigma[1:] - sigma[:-1]
+        return t.to(device=device, dtype=dtype), d.to(device=device, dtype=dtype)
+
+    @staticmethod
+    def step(model_output: torch.Tensor, delta: torch.Tensor, sample: torch.Tensor) -> torch.Tensor:
+        return euler_step(model_output, delta, sample)

@@ -1,0 +1,228 @@
+/*
+ * fam_hip.h -- C ABI of the MI355X (gfx950) kernels for the FastWAM / DiT4DiT
+ * action-DiT denoising hot path.
+ *
+ * Every entry point takes plain device pointers, element counts and strides, and
+ * the HIP stream to launch on (a hipStream_t passed as void*; NULL = the null
+ * stream).  The library never allocates: the caller owns every buffer, including
+ * the optional workspace, so every entry point can be recorded into a HIP graph.
+ * Tensors are bf16 unless a parameter says fp32.  Strides are in elements.
+ *
+ * Return value: FAM_OK, or an error code with a message readable through
+ * fam_last_error() (thread-local).  Argument validation happens before any launch,
+ * so an error return means nothing was enqueued.
+ *
+ * Reference paths below are relative to the reference checkout:
+ *   FB  = src/fastwam-baseline/fastwam/models/wan22
+ *   FG  = src/fastwam-geak/fastwam/models/wan22
+ *   CA  = src/cae-fastwam/fastwam/models/wan22
+ *   SCH = FB/schedulers/scheduler_continuous.py
+ */
+#ifndef FAM_HIP_H
+#define FAM_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FAM_OK 0
+#define FAM_ERR_INVALID_ARG 1
+#define FAM_ERR_UNSUPPORTED 2
+#define FAM_ERR_LAUNCH 3
+#define FAM_ERR_WORKSPACE 4
+
+#define FAM_ABI_VERSION 1
+
+/*
+ * Workspaces.  The split-K GEMM and the split-key attention exchange fp32 partials through
+ * a caller-owned workspace.  Its first FAM_WS_COUNTER_BYTES bytes are per-tile arrival
+ * counters: they must be zero before the first use, every kernel leaves them zero again,
+ * and the partials live after them, so one workspace can serve launches of any shape and
+ * of both kernels, one after another on a stream.  Launches that share a workspace must not
+ * run concurrently.  A split launch may use at most FAM_WS_COUNTER_BYTES / 4 tiles.
+ */
+#define FAM_WS_COUNTER_BYTES 65536
+
+/* Library ABI version (FAM_ABI_VERSION). */
+int fam_version(void);
+
+/* Message of the last error returned on this thread ("" if none). */
+const char* fam_last_error(void);
+
+/*
+ * fam_adaln -- LayerNorm over the last dim with AdaLN-Zero modulation:
+ *   y[r,:] = (LN(x[r,:]) [* ln_weight + ln_bias]) * (1 + scale[r,:]) + shift[r,:]
+ * LN is biased-variance, eps inside the rsqrt, fp32 statistics.
+ * shift/scale (both or neither) are indexed as
+ *   base + (r / rows_per_batch) * mod_batch_stride + (r % rows_per_batch) * mod_row_stride
+ * so mod_row_stride = 0 broadcasts one vector over a batch's tokens ([B,1,D]) and
+ * mod_row_stride = D gives per-token modulation ([B,S,D]).  ln_weight / ln_bias may be
+ * NULL (elementwise_affine=False).
+ * Replaces: adaln_forward(x, norm, shift, scale)   FB/fused_adaln.py:513-523
+ *           (eager branch :522-523; used FB/wan_video_dit.py:281,284, FB/mot.py:125,169),
+ *           DiTBlock.norm3                          FB/wan_video_dit.py:261,283,
+ *           modulate(norm(x), shift, scale)         CA/wan_video_dit.py:590-591.
+ * Limits: dim % 8 == 0, 8 <= dim <= 16384; x/y rows 16-byte aligned.
+ */
+int fam_adaln(const void* x, int64_t x_row_stride,
+              const void* shift, const void* scale,
+              int64_t mod_batch_stride, int64_t mod_row_stride,
+              const void* ln_weight, const void* ln_bias,
+              void* y, int64_t y_row_stride,
+              int64_t rows, int64_t rows_per_batch, int64_t dim, float eps, void* stream);
+
+/*
+ * fam_rmsnorm_rope -- RMSNorm then rotary embedding, per row:
+ *   n = bf16(x * rsqrt(mean(x^2) + eps)) * weight          (skipped if weight == NULL)
+ *   y[2i], y[2i+1] = n[2i] c - n[2i+1] s,  n[2i] s + n[2i+1] c   (skipped if cos_tab == NULL)
+ * with (c, s) = (cos_tab, sin_tab)[pos * tab_row_stride + j * tab_elem_stride], pos = row % seq_len,
+ * j = pair index within the head (0 .. head_dim/2-1).  Tables are fp32.  The RMS is over the
+ * full row (all heads), as RMSNorm(H*Dh) in the reference.  y may equal x (in place).
+ * Replaces: RMSNorm.forward                 FB/wan_video_dit.py:156-167,
+ *           rope_apply(x, freqs, num_heads) FB/wan_video_dit.py:58-70, FG/wan_video_dit.py:193-215,
+ *                                           CA/wan_video_dit.py:769-799,
+ *           fused q/k post-processing       FG/mot.py:786-816 (qkv_post without the K/V cache write).
+ * Limits: dim % 8 == 0, dim <= 16384, head_dim even and dim % head_dim == 0 (rope);
+ * 16-byte aligned rows.
+ */
+int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride,
+                     int64_t rows, int64_t seq_len, int64_t dim,
+                     const void* weight, float eps,
+                     const float* cos_tab, const float* sin_tab,
+                     int64_t tab_row_stride, int64_t tab_elem_stride, int64_t head_dim,
+                     void* stream);
+
+/* Attention mask kinds for fam_attn_desc.mask_kind. */
+#define FAM_MASK_NONE 0
+#define FAM_MASK_BOOL 1      /* uint8, nonzero = attend (torch bool)      */
+#define FAM_MASK_ADD_F32 2   /* fp32 added to the scaled scores           */
+#define FAM_MASK_ADD_BF16 3  /* bf16 added to the scaled scores           */
+
+/*
+ * Attention over [B, H] heads: o = softmax(q k^T * scale + mask) v, fp32 softmax.
+ * Element (b, s, h, d) of tensor t lives at t + b*t_bs + s*t_rs + h*t_hs + d, which covers
+ * both [B,S,H*Dh] (t_hs = Dh) and [B,H,S,Dh] (t_rs = Dh, t_hs = S*Dh) layouts.  The keys and
+ * values are the concatenation of two segments: keys 0..sk0-1 from (k0, v0) and
+ * sk0..sk0+sk1-1 from (k1, v1) (sk1 = 0: one segment), e.g. a cached video prefix followed
+ * by the action tokens.  The mask element for (b, h, q, key) is
+ * mask[b*mask_bs + h*mask_hs + q*mask_qs + key].  A query row with every key masked gives 0.
+ * num_splits > 1 splits the keys over that many workgroups per (b, h, q-tile) (0: chosen
+ * by the library) and combines the partial results in a fixed order (deterministic).  A
+ * split launch needs a workspace (see FAM_WS_COUNTER_BYTES) of
+ * fam_attention_workspace_bytes() bytes (0 when no split is used).
+ * Replaces: flash_attention(q, k, v, num_heads, ctx_mask)  FB/wan_video_dit.py:17-26,
+ *           FG/wan_video_dit.py:18-39, CA/wan_video_dit.py:569-587;
+ *           fastwam::short_attn / short_attn_bsd          FG/wan_video_dit.py:1680-1721, FG/mot.py:682-722;
+ *           joint [video cache; action] attention          FB/mot.py:446-478.
+ * Limits: head_dim in {8, 16, 32, 64, 128}; all strides multiples of 8; 16-byte aligned
+ * bases; batch*heads <= 65535.
+ */
+typedef struct fam_attn_desc {
+  const void* q;  int64_t q_bs, q_rs, q_hs;
+  const void* k0; int64_t k0_bs, k0_rs, k0_hs;
+  const void* v0; int64_t v0_bs, v0_rs, v0_hs;
+  const void* k1; int64_t k1_bs, k1_rs, k1_hs;
+  const void* v1; int64_t v1_bs, v1_rs, v1_hs;
+  void* o;        int64_t o_bs, o_rs, o_hs;
+  int64_t batch, heads, sq, sk0, sk1, head_dim;
+  float scale;
+  const void* mask; int mask_kind; int64_t mask_bs, mask_hs, mask_qs;
+  int num_splits;
+  void* workspace; int64_t workspace_bytes;
+} fam_attn_desc;
+
+int fam_attention(const fam_attn_desc* d, void* stream);
+int64_t fam_attention_workspace_bytes(int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t head_dim,
+                                      int num_splits);
+
+/* GEMM prologues (applied to each row of A before the product) and activations. */
+#define FAM_PRO_NONE 0
+#define FAM_PRO_LAYERNORM 1  /* LN(a) [* pro_w + pro_b]                        */
+#define FAM_PRO_ADALN 2      /* LN(a) * (1 + pro_scale) + pro_shift            */
+#define FAM_ACT_NONE 0
+#define FAM_ACT_GELU_TANH 1
+#define FAM_ACT_SILU 2
+
+/*
+ * fam_gemm -- out[m, n] = epilogue( sum_k pro(a)[m, k] * w[n, k] + bias[n] ),
+ * w in nn.Linear layout [N, K].  Epilogue, in order: activation; then, if res != NULL,
+ * out = res[m, n] + g(m, n) * value with g = 1 when gate == NULL, else
+ * g = gate[(m / rows_per_batch) * gate_bs + (m % rows_per_batch) * gate_rs + n * gate_ns]
+ * (gate_ns = 0 with gate_bs = gate_rs = 0 makes it one scalar, e.g. the Euler delta).
+ * res may equal out (in-place residual update).  AdaLN shift/scale use the same
+ * (rows_per_batch, pro_mod_bs, pro_mod_rs) indexing with a unit column stride.
+ * split_k > 1 splits the K range over that many workgroups (split_k = 0: chosen by the
+ * library from M, N, K); the last workgroup to finish a tile reduces the fp32 partials in
+ * split order (deterministic) and runs the epilogue.  A split launch needs a workspace (see
+ * FAM_WS_COUNTER_BYTES) of fam_gemm_workspace_bytes(M, N, K, split_k) bytes (0 when no split
+ * is used).
+ * Replaces: nn.Linear / F.linear on the hot path (FB/wan_video_dit.py:188-191,215-218,262-263,
+ *           FB/action_dit.py:76-97,317-318), fastwam::skmm + skpost (split-K GEMM with
+ *           bias/gate/residual/norm epilogue, FG/mot.py:1080-1348), geak_head::mmx with the
+ *           fused Euler epilogue (DG/modules/action_model/ActionDiT.py:1260-1272).
+ * Limits: K % 8 == 0; a, w rows 16-byte aligned (lda, ldw multiples of 8); 1 <= split_k <= 64.
+ */
+typedef struct fam_gemm_desc {
+  const void* a; int64_t lda;
+  const void* w; int64_t ldw;
+  const void* bias;
+  void* out; int64_t ldo;
+  int64_t M, N, K;
+  int prologue;
+  const void* pro_w; const void* pro_b;
+  const void* pro_shift; const void* pro_scale;
+  int64_t pro_mod_bs, pro_mod_rs;
+  float pro_eps;
+  int act;
+  const void* res; int64_t ldr;
+  const void* gate; int64_t gate_bs, gate_rs, gate_ns;
+  int64_t rows_per_batch;
+  int split_k;
+  void* workspace; int64_t workspace_bytes;
+} fam_gemm_desc;
+
+int fam_gemm(const fam_gemm_desc* d, void* stream);
+int64_t fam_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int split_k);
+
+/*
+ * fam_linear_smallk -- y[m, n] = sum_k x[m, k] w[n, k] + b[n] for small, unaligned K
+ * (the 7-wide action encoder, FB/action_dit.py:76, :285).  fp32 accumulation.
+ * Limits: K <= 64.
+ */
+int fam_linear_smallk(const void* x, int64_t ldx, const void* w, const void* b,
+                      void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);
+
+/*
+ * fam_euler_step -- out[i] = bf16(sample[i] + bf16(model_output[i] * delta[i / inner])), the
+ * flow-matching update in the rounding order of the eager bf16 expression
+ * `sample + model_output * delta` (SCH:82-88).  delta holds bf16 values in device memory:
+ * one scalar (inner = n) or one per batch row ([B] deltas viewed [B,1,...], inner = n / B).
+ * n elements, contiguous; out may equal sample (in place).
+ * Replaces: WanContinuousFlowMatchScheduler.step  SCH:82-88;
+ *           actions - dt * v                       DB/modules/action_model/ActionDiT.py:368.
+ */
+int fam_euler_step(const void* sample, const void* model_output, const void* delta, void* out,
+                   int64_t n, int64_t inner, void* stream);
+
+/*
+ * fam_sinusoid -- out[t, :] = bf16(cat(cos(p_t f), sin(p_t f))), f_i = 10000^(-i/(dim/2)),
+ * computed in fp64 from the bf16 positions p (FB/wan_video_dit.py:34-38).  out [T, dim].
+ */
+int fam_sinusoid(const void* positions, void* out, int64_t T, int64_t dim, void* stream);
+
+/*
+ * fam_add_modulation -- out[t, l, :] = bf16(modulation[l, :] + t_mod[t, :]) for every
+ * denoise step t < T and block l < L, vectors of length n (= 6 * hidden): the
+ * `modulation + t_mod` of every block (FB/wan_video_dit.py:273-274, FB/mot.py:63-80).
+ * Limits: n % 8 == 0.
+ */
+int fam_add_modulation(const void* t_mod, const void* modulation, void* out,
+                       int64_t T, int64_t L, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FAM_HIP_H */

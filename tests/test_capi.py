@@ -1,0 +1,137 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol include/fam_hip.h
+declares, the ctypes descriptor layouts match the C header, and argument validation
+rejects bad calls before anything is launched (no GPU needed for any of this)."""
+import ctypes as C
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from fam import _capi
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "fam_hip.h")
+
+
+def _header_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(fam_\w+)\s*\(", src, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_capi.LIB_PATH):
+        pytest.fail(f"{_capi.LIB_PATH} missing: run __graft_entry__.build() first")
+    return _capi.load()
+
+
+def test_exports_every_header_symbol(lib):
+    names = _header_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in fam_hip.h but not exported"
+    assert sorted(_capi.SIGNATURES) == names, "ctypes signatures must cover exactly the header's functions"
+    out = subprocess.run(["nm", "-D", "--defined-only", _capi.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\sT\s(fam_\w+)", out))
+    assert set(names) <= exported
+
+
+def test_version(lib):
+    assert lib.fam_version() == _capi.FAM_ABI_VERSION
+
+
+def _c_offsets(struct: str, fields):
+    prog = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
+    prog.append(f'printf("%zu\\n", sizeof({struct}));')
+    for f in fields:
+        prog.append(f'printf("%zu\\n", offsetof({struct}, {f}));')
+    prog.append("return 0;}")
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "t.c")
+        exe = os.path.join(d, "t")
+        open(c, "w").write("\n".join(prog))
+        subprocess.run(["gcc", "-std=c11", c, "-o", exe], check=True)
+        vals = [int(v) for v in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
+    return vals[0], vals[1:]
+
+
+@pytest.mark.parametrize("cls,cname", [(_capi.AttnDesc, "fam_attn_desc"), (_capi.GemmDesc, "fam_gemm_desc")])
+def test_struct_layout_matches_header(cls, cname):
+    fields = [f for f, _ in cls._fields_]
+    size, offs = _c_offsets(cname, fields)
+    assert C.sizeof(cls) == size
+    for f, o in zip(fields, offs):
+        assert getattr(cls, f).offset == o, f"{cname}.{f}"
+
+
+def _err(lib):
+    return lib.fam_last_error().decode()
+
+
+def test_validation_rejects_before_launch(lib):
+    # bad dims / alignment -> error codes, nothing launched (this host has no GPU)
+    assert lib.fam_adaln(16, 1024, None, None, 0, 0, None, None, 32, 1024, 4, 4, 1020, 1e-6, None) == _capi.FAM_ERR_INVALID_ARG
+    assert "dim" in _err(lib)
+    assert lib.fam_adaln(16, 1024, 16, None, 0, 0, None, None, 32, 1024, 4, 4, 1024, 1e-6, None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_adaln(18, 1024, None, None, 0, 0, None, None, 32, 1024, 4, 4, 1024, 1e-6, None) == _capi.FAM_ERR_INVALID_ARG
+    assert "aligned" in _err(lib)
+    assert lib.fam_rmsnorm_rope(16, 64, 32, 64, 4, 4, 64, None, 1e-6, 64, 64, 32, 1, 12, None) == _capi.FAM_ERR_INVALID_ARG
+
+    d = _capi.GemmDesc()
+    d.a, d.w, d.out = 16, 32, 48
+    d.M, d.N, d.K, d.lda, d.ldw, d.ldo, d.rows_per_batch = 32, 64, 7, 8, 8, 64, 32
+    assert lib.fam_gemm(C.byref(d), None) == _capi.FAM_ERR_INVALID_ARG
+    d.K, d.lda, d.ldw = 64, 64, 64
+    d.prologue = 2  # AdaLN without shift/scale
+    assert lib.fam_gemm(C.byref(d), None) == _capi.FAM_ERR_INVALID_ARG
+    d.prologue = 0
+    d.split_k, d.K, d.lda, d.ldw = 4, 1024, 1024, 1024  # split without workspace
+    assert lib.fam_gemm(C.byref(d), None) == _capi.FAM_ERR_WORKSPACE
+    assert "workspace" in _err(lib)
+    d.split_k = 65
+    assert lib.fam_gemm(C.byref(d), None) == _capi.FAM_ERR_INVALID_ARG
+
+    a = _capi.AttnDesc()
+    a.q, a.k0, a.v0, a.o = 16, 32, 48, 64
+    a.batch, a.heads, a.sq, a.sk0, a.head_dim = 1, 2, 4, 4, 48
+    assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_UNSUPPORTED
+    a.head_dim, a.q_rs = 64, 12
+    assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_INVALID_ARG
+    a.q_rs, a.sk0, a.num_splits = 128, 1560, 8
+    assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_WORKSPACE
+    a.num_splits, a.mask_kind = 0, 1
+    assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_INVALID_ARG
+
+    assert lib.fam_linear_smallk(16, 7, 32, None, 48, 64, 4, 64, 65, None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_euler_step(16, 32, None, 48, 10, 10, None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_sinusoid(16, 32, 4, 7, None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_add_modulation(16, 32, 48, 2, 3, 12, None) == _capi.FAM_ERR_INVALID_ARG
+
+
+def test_workspace_sizes(lib):
+    # no split -> no workspace; split sizes grow with the split count
+    assert lib.fam_gemm_workspace_bytes(2048, 4096, 1024, 1) == 0
+    w8 = lib.fam_gemm_workspace_bytes(32, 1024, 4096, 8)
+    w16 = lib.fam_gemm_workspace_bytes(32, 1024, 4096, 16)
+    assert 0 < w8 < w16
+    assert lib.fam_gemm_workspace_bytes(32, 3072, 1024, 0) > 0          # auto split at M=32
+    assert lib.fam_attention_workspace_bytes(1, 16, 32, 32, 64, 0) == 0  # short keys: no split
+    assert lib.fam_attention_workspace_bytes(1, 16, 32, 1560, 64, 0) > 0
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(ImportError, match="build the HIP library"):
+        _capi.load.__wrapped__(str(tmp_path / "nope.so")) if hasattr(_capi.load, "__wrapped__") else \
+            _load_fresh(str(tmp_path / "nope.so"))
+
+
+def _load_fresh(path):
+    saved = _capi._lib
+    _capi._lib = None
+    try:
+        return _capi.load(path)
+    finally:
+        _capi._lib = saved

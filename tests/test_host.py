@@ -1,0 +1,33 @@
+"""CPU checks of the host-side logic of the package against the oracle."""
+import torch
+
+from oracle import fam_oracle as O
+from fam import action_dit as AD
+
+
+def test_synthetic_params_match_oracle_init():
+    cfg = AD.ActionDiTConfig(num_layers=2, hidden_dim=64, ffn_dim=128, text_dim=48, freq_dim=32, num_heads=4,
+                             attn_head_dim=16)
+    a = AD.synthetic_params(cfg, 77)
+    b = O.init_action_dit_params(O.ActionDiTConfig(**cfg.to_dict()), 77)
+    assert sorted(a) == sorted(b)
+    for k in a:
+        assert torch.equal(a[k], b[k]), k
+
+
+def test_param_shapes_match_oracle():
+    cfg = AD.ActionDiTConfig()
+    assert AD.param_shapes(cfg) == O.action_dit_param_shapes(O.ActionDiTConfig(**cfg.to_dict()))
+
+
+def test_schedule_matches_oracle():
+    for n, s in ((10, 5.0), (4, 5.0), (2, 1.0)):
+        ts, ds = AD.schedule(n, s)
+        ots, ods = O.build_inference_schedule(n, s, torch.bfloat16)
+        assert torch.equal(ts, ots) and torch.equal(ds, ods)
+
+
+def test_rope_tables_match_oracle():
+    cos, sin = AD.rope_1d_tables(64, 32)
+    oc, os_ = O.rope_tables_real(O.action_freqs(64, 32))
+    assert torch.equal(cos, oc) and torch.equal(sin, os_)
