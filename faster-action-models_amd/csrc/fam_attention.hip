@@ -1,19 +1,23 @@
 // Flash-style attention on bf16 MFMA (gfx950):  o = softmax(q k^T * scale + mask) v.
 //
-// Formulation.  Scores are computed transposed, S^T = K Q^T, with the key tile as the
-// MFMA A-operand and the query tile as the B-operand (v_mfma_f32_16x16x32_bf16).  A lane
-// then owns ONE query (column l%16) and four keys per 16-key sub-tile, so the running
+// Formulation (both kernels).  Scores are computed transposed, S^T = K Q^T, with the key
+// tile as the MFMA A-operand and the query tile as the B-operand (v_mfma_f32_16x16x32_bf16).
+// A lane then owns ONE query (column l%16) and four keys per 16-key sub-tile, so the running
 // max / sum of the online softmax are per-lane scalars reduced over the 4 lane groups with
 // two shuffles, and the probabilities already sit in the B-operand layout of the second
 // product O^T = V^T P^T (A-operand = V^T read from a transposed LDS tile).  The key order
 // inside an MFMA k-block is permuted consistently on both operands (keys {4g..4g+3} and
 // {16+4g..16+4g+3} for lane group g), which leaves the dot products unchanged.
 //
-// Work split.  A workgroup of NW waves owns 16*NW queries of one (batch, head); K/V blocks
-// of 32 keys are staged through LDS and shared by the waves.  For short query blocks
-// (Sq <= 64, e.g. 32 action tokens over 1560 context tokens) the keys are additionally
-// split over grid.z workgroups; each writes its unnormalised partial (O, m, l) and the last
-// to arrive combines them in split order (deterministic, no float atomics).
+// attn_short_kernel (Sq <= 64: 32 action tokens over their own 32 keys, over a 1560-token
+// context, or over a cached video prefix): one workgroup per (batch, head) holds every
+// query; its waves split the keys into contiguous runs of 32-key blocks, each wave with a
+// private transposed V tile in LDS and the next block's K/V loads in flight while it
+// computes the current one.  The per-wave partial softmax states are merged through LDS in
+// wave order at the end (deterministic, no cross-workgroup traffic).
+//
+// attn_tiled_kernel (Sq > 64: video tokens): a workgroup of 4 waves owns 64 queries of one
+// (batch, head); 32-key K/V blocks are staged through LDS and shared by the waves.
 //
 // Algorithmic bytes per launch: 2*B*H*Dh*(2*Sq + 2*Sk) (+ mask); flops 4*B*H*Sq*Sk*Dh.
 #include <algorithm>
@@ -22,7 +26,8 @@
 
 namespace fam {
 
-constexpr int KB = 32;  // keys per LDS block
+constexpr int KB = 32;  // keys per block
+constexpr float kLog2e = 1.4426950408889634f;
 
 struct AttnArgs {
   const bf16* q; int64_t q_bs, q_rs, q_hs;
@@ -31,130 +36,291 @@ struct AttnArgs {
   const bf16* k1; int64_t k1_bs, k1_rs, k1_hs;
   const bf16* v1; int64_t v1_bs, v1_rs, v1_hs;
   bf16* o; int64_t o_bs, o_rs, o_hs;
-  int64_t H, Sq, sk0, Sk, kchunk;
+  int64_t H, Sq, sk0, Sk;
   float scale_log2;
   const void* mask; int mask_kind; int64_t mbs, mhs, mqs;
-  int splits;
-  unsigned* cnt; float* opart; float* mlpart;
-  int64_t sq_pad;
 };
 
-template <int DH, int NW>
-__global__ __launch_bounds__(NW * 64) void attn_kernel(AttnArgs a) {
+__device__ __forceinline__ const bf16* key_ptr(const AttnArgs& a, int64_t b, int64_t h, int64_t kk) {
+  return kk < a.sk0 ? a.k0 + b * a.k0_bs + kk * a.k0_rs + h * a.k0_hs
+                    : a.k1 + b * a.k1_bs + (kk - a.sk0) * a.k1_rs + h * a.k1_hs;
+}
+__device__ __forceinline__ const bf16* val_ptr(const AttnArgs& a, int64_t b, int64_t h, int64_t kk) {
+  return kk < a.sk0 ? a.v0 + b * a.v0_bs + kk * a.v0_rs + h * a.v0_hs
+                    : a.v1 + b * a.v1_bs + (kk - a.sk0) * a.v1_rs + h * a.v1_hs;
+}
+
+// scaled (log2 domain) and masked score of query qi and key kk
+__device__ __forceinline__ float score(const AttnArgs& a, float raw, int64_t b, int64_t h, int64_t qi, bool qvalid,
+                                       int64_t kk) {
+  if (kk >= a.Sk) return -INFINITY;
+  float v = raw * a.scale_log2;
+  if (a.mask_kind != FAM_MASK_NONE && qvalid) {
+    const int64_t mi = b * a.mbs + h * a.mhs + qi * a.mqs + kk;
+    if (a.mask_kind == FAM_MASK_BOOL) {
+      if (!reinterpret_cast<const uint8_t*>(a.mask)[mi]) v = -INFINITY;
+    } else if (a.mask_kind == FAM_MASK_ADD_F32) {
+      v += reinterpret_cast<const float*>(a.mask)[mi] * kLog2e;
+    } else {
+      v += to_f(reinterpret_cast<const bf16*>(a.mask)[mi]) * kLog2e;
+    }
+  }
+  return v;
+}
+
+// Online-softmax update of one query column with the 8 scores of a 32-key block; returns
+// the probabilities as the bf16 B-operand of the P V product and rescales the accumulator.
+template <int NDT>
+__device__ __forceinline__ bf16x8 softmax_update(const float (&s)[2][4], float& m_run, float& l_run, f32x4 (&oacc)[NDT]) {
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mloc = fmaxf(mloc, s[kt][e]);
+  const float m_new = fmaxf(m_run, group4_max(mloc));
+  bf16x8 pf;
+  if (m_new == -INFINITY) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pf[j] = (bf16)0.0f;
+    return pf;
+  }
+  const float alpha = exp2f(m_run - m_new);  // m_run = -inf -> 0
+  float psum = 0.f;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p = exp2f(s[kt][e] - m_new);
+      psum += p;
+      pf[kt * 4 + e] = to_bf(p);
+    }
+  l_run = l_run * alpha + group4_sum(psum);
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) oacc[t] *= alpha;
+  m_run = m_new;
+  return pf;
+}
+
+// ---------------------------------------------------------------------------------------
+template <int DH, int QT, int NW>
+__global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
   constexpr int NC = (DH + 31) / 32;   // 32-wide k-chunks of the head dim (zero padded)
   constexpr int NDT = (DH + 15) / 16;  // 16-row output tiles of the head dim
-  constexpr int DP = NC * 32 + 8;      // padded K row in LDS
   constexpr int VROWS = NDT * 16;
-  constexpr int NT = NW * 64;
+  constexpr int NVC = (KB * DH / 8 + 63) / 64;  // 16-byte V chunks per lane per block
+  constexpr int NQ = QT * 16;
+  __shared__ bf16 Vt[NW][VROWS][KB + 8];
+  __shared__ float s_m[NW][NQ], s_l[NW][NQ];
+  __shared__ float s_o[NQ][DH];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t bh = blockIdx.x, b = bh / a.H, h = bh - b * a.H;
+  const int64_t nkb = (a.Sk + KB - 1) / KB;
+  const int64_t per = (nkb + NW - 1) / NW;
+  const int64_t kb_beg = std::min(nkb, (int64_t)wave * per), kb_end = std::min(nkb, kb_beg + per);
+
+  bf16x8 qf[QT][NC];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int64_t qi = qt * 16 + l16;
+      const int d0 = c * 32 + lg * 8;
+      qf[qt][c] = (qi < a.Sq && d0 < DH) ? load8(a.q + b * a.q_bs + qi * a.q_rs + h * a.q_hs + d0) : zero8();
+    }
+
+  f32x4 oacc[QT][NDT];
+  float m_run[QT], l_run[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.f;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) oacc[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // K fragments (A-operand rows = keys) and V chunks of one block, straight from global
+  bf16x8 kf[2][NC], vc[NVC];
+  auto gload = [&](int64_t blk) {
+    const int64_t kb = blk * KB;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int64_t kk = kb + kt * 16 + l16;
+        const int d0 = c * 32 + lg * 8;
+        kf[kt][c] = (kk < a.Sk && d0 < DH) ? load8(key_ptr(a, b, h, kk) + d0) : zero8();
+      }
+#pragma unroll
+    for (int p = 0; p < NVC; ++p) {
+      const int cidx = lane + 64 * p;
+      const int key = cidx / (DH / 8), d0 = (cidx % (DH / 8)) * 8;
+      const int64_t kk = kb + key;
+      vc[p] = (cidx < KB * DH / 8 && kk < a.Sk) ? load8(val_ptr(a, b, h, kk) + d0) : zero8();
+    }
+  };
+
+  if (kb_beg < kb_end) gload(kb_beg);
+  for (int64_t blk = kb_beg; blk < kb_end; ++blk) {
+    const int64_t kb = blk * KB;
+    // V block -> this wave's transposed tile (LDS operations of one wave complete in order)
+#pragma unroll
+    for (int p = 0; p < NVC; ++p) {
+      const int cidx = lane + 64 * p;
+      if (cidx < KB * DH / 8) {
+        const int key = cidx / (DH / 8), d0 = (cidx % (DH / 8)) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) Vt[wave][d0 + e][key] = vc[p][e];
+      }
+    }
+    bf16x8 kcur[2][NC];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) kcur[kt][c] = kf[kt][c];
+    if (blk + 1 < kb_end) gload(blk + 1);  // next block in flight during this one's math
+    __builtin_amdgcn_wave_barrier();
+
+    bf16x8 vfr[NDT];
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      const int d = t * 16 + l16;
+      if (d < DH) {
+        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&Vt[wave][d][lg * 4]);
+        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(&Vt[wave][d][16 + lg * 4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { vfr[t][e] = lo[e]; vfr[t][4 + e] = hi[e]; }
+      } else {
+        vfr[t] = zero8();
+      }
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int64_t qi = qt * 16 + l16;
+      const bool qvalid = qi < a.Sq;
+      float s[2][4];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NC; ++c) sacc = mfma16(kcur[kt][c], qf[qt][c], sacc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s[kt][e] = score(a, sacc[e], b, h, qi, qvalid, kb + kt * 16 + lg * 4 + e);
+      }
+      const bf16x8 pf = softmax_update<NDT>(s, m_run[qt], l_run[qt], oacc[qt]);
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) oacc[qt][t] = mfma16(vfr[t], pf, oacc[qt][t]);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // ---- merge the waves' partial states in wave order
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt)
+    if (lg == 0) { s_m[wave][qt * 16 + l16] = m_run[qt]; s_l[wave][qt * 16 + l16] = l_run[qt]; }
+  __syncthreads();
+  float wscale[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int q = qt * 16 + l16;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_m[w][q]);
+    wscale[qt] = (mx == -INFINITY) ? 0.f : exp2f(m_run[qt] - mx);
+  }
+  for (int w = 0; w < NW; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) {
+          const int d0 = t * 16 + lg * 4;
+          if (d0 < DH) {
+            f32x4* dst = reinterpret_cast<f32x4*>(&s_o[qt * 16 + l16][d0]);
+            const f32x4 v = oacc[qt][t] * wscale[qt];
+            *dst = (w == 0) ? v : (*dst + v);
+          }
+        }
+    }
+    __syncthreads();
+  }
+  for (int idx = tid; idx < NQ * (DH / 4); idx += NW * 64) {
+    const int q = idx / (DH / 4), d0 = (idx % (DH / 4)) * 4;
+    if (q >= a.Sq) continue;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_m[w][q]);
+    float L = 0.f;
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) L += s_l[w][q] * exp2f(s_m[w][q] - mx);
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    const f32x4 v = *reinterpret_cast<const f32x4*>(&s_o[q][d0]);
+    bf16x4 ov;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ov[e] = to_bf(v[e] * inv);
+    *reinterpret_cast<bf16x4*>(a.o + b * a.o_bs + q * a.o_rs + h * a.o_hs + d0) = ov;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+template <int DH>
+__global__ __launch_bounds__(256) void attn_tiled_kernel(AttnArgs a) {
+  constexpr int NW = 4;
+  constexpr int NC = (DH + 31) / 32;
+  constexpr int NDT = (DH + 15) / 16;
+  constexpr int DP = NC * 32 + 8;
+  constexpr int VROWS = NDT * 16;
   __shared__ bf16 Ks[KB][DP];
   __shared__ bf16 Vt[VROWS][KB + 8];
-  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
   const int64_t bh = blockIdx.y, b = bh / a.H, h = bh - b * a.H;
-  const int64_t qbase = (int64_t)blockIdx.x * 16 * NW + wave * 16;
-  const int64_t qi = qbase + l16;
+  const int64_t qi = (int64_t)blockIdx.x * 16 * NW + wave * 16 + l16;
   const bool qvalid = qi < a.Sq;
-  const int z = blockIdx.z;
-  const int64_t kbeg = (int64_t)z * a.kchunk;
-  const int64_t kend = std::min(a.Sk, kbeg + a.kchunk);
 
-  // Q^T fragments (B-operand): lane holds q[qi][c*32 + 8*lg .. +7].
   bf16x8 qf[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int d0 = c * 32 + lg * 8;
     qf[c] = (qvalid && d0 < DH) ? load8(a.q + b * a.q_bs + qi * a.q_rs + h * a.q_hs + d0) : zero8();
   }
-
   f32x4 oacc[NDT];
 #pragma unroll
   for (int t = 0; t < NDT; ++t) oacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  for (int64_t kb = kbeg; kb < kend; kb += KB) {
-    // ---- stage K (row-major) and V (transposed) for keys kb .. kb+31
-    for (int c = tid; c < KB * (DH / 8); c += NT) {
+  for (int64_t kb = 0; kb < a.Sk; kb += KB) {
+    for (int c = tid; c < KB * (DH / 8); c += NW * 64) {
       const int key = c / (DH / 8), d0 = (c % (DH / 8)) * 8;
       const int64_t kk = kb + key;
       bf16x8 kv = zero8(), vv = zero8();
-      if (kk < kend) {
-        if (kk < a.sk0) {
-          kv = load8(a.k0 + b * a.k0_bs + kk * a.k0_rs + h * a.k0_hs + d0);
-          vv = load8(a.v0 + b * a.v0_bs + kk * a.v0_rs + h * a.v0_hs + d0);
-        } else {
-          const int64_t k1i = kk - a.sk0;
-          kv = load8(a.k1 + b * a.k1_bs + k1i * a.k1_rs + h * a.k1_hs + d0);
-          vv = load8(a.v1 + b * a.v1_bs + k1i * a.v1_rs + h * a.v1_hs + d0);
-        }
+      if (kk < a.Sk) {
+        kv = load8(key_ptr(a, b, h, kk) + d0);
+        vv = load8(val_ptr(a, b, h, kk) + d0);
       }
       *reinterpret_cast<bf16x8*>(&Ks[key][d0]) = kv;
 #pragma unroll
       for (int e = 0; e < 8; ++e) Vt[d0 + e][key] = vv[e];
     }
     __syncthreads();
-
-    // ---- S^T = K Q^T for the two 16-key sub-tiles
-    f32x4 sacc[2];
+    float s[2][4];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      sacc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int d0 = c * 32 + lg * 8;
         const bf16x8 kfr = (d0 < DH) ? *reinterpret_cast<const bf16x8*>(&Ks[kt * 16 + l16][d0]) : zero8();
-        sacc[kt] = mfma16(kfr, qf[c], sacc[kt]);
+        sacc = mfma16(kfr, qf[c], sacc);
       }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[kt][e] = score(a, sacc[e], b, h, qi, qvalid, kb + kt * 16 + lg * 4 + e);
     }
-
-    // ---- scale, mask, online softmax (per lane: one query, 8 keys)
-    float s[2][4];
-    float mloc = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t kk = kb + kt * 16 + lg * 4 + e;
-        float v = sacc[kt][e] * a.scale_log2;
-        if (kk >= kend) {
-          v = -INFINITY;
-        } else if (a.mask_kind != FAM_MASK_NONE && qvalid) {
-          const int64_t mi = b * a.mbs + h * a.mhs + qi * a.mqs + kk;
-          if (a.mask_kind == FAM_MASK_BOOL) {
-            if (!reinterpret_cast<const uint8_t*>(a.mask)[mi]) v = -INFINITY;
-          } else if (a.mask_kind == FAM_MASK_ADD_F32) {
-            v += reinterpret_cast<const float*>(a.mask)[mi] * 1.4426950408889634f;
-          } else {
-            v += to_f(reinterpret_cast<const bf16*>(a.mask)[mi]) * 1.4426950408889634f;
-          }
-        }
-        s[kt][e] = v;
-        mloc = fmaxf(mloc, v);
-      }
-    const float m_new = fmaxf(m_run, group4_max(mloc));
-    float psum = 0.f;
-    bf16x8 pf;
-    if (m_new == -INFINITY) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) pf[j] = (bf16)0.0f;
-    } else {
-      const float alpha = exp2f(m_run - m_new);  // m_run = -inf -> 0
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p = exp2f(s[kt][e] - m_new);
-          psum += p;
-          pf[kt * 4 + e] = to_bf(p);
-        }
-      l_run = l_run * alpha + group4_sum(psum);
-#pragma unroll
-      for (int t = 0; t < NDT; ++t) oacc[t] *= alpha;
-      m_run = m_new;
-    }
-
-    // ---- O^T += V^T P^T
+    const bf16x8 pf = softmax_update<NDT>(s, m_run, l_run, oacc);
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
       const int d = t * 16 + l16;
@@ -172,51 +338,6 @@ __global__ __launch_bounds__(NW * 64) void attn_kernel(AttnArgs a) {
     __syncthreads();
   }
 
-  // lane owns O[qi][t*16 + 4*lg + e]
-  if (a.splits > 1) {
-    const int64_t nqt = gridDim.x;
-    const int64_t tile = bh * nqt + blockIdx.x;
-    const int64_t rowz = ((int64_t)z * gridDim.y + bh) * a.sq_pad + qi;  // (split, b*h, q)
-#pragma unroll
-    for (int t = 0; t < NDT; ++t) {
-      const int d0 = t * 16 + lg * 4;
-      if (d0 < DH) *reinterpret_cast<f32x4*>(a.opart + rowz * DH + d0) = oacc[t];
-    }
-    if (lg == 0) { a.mlpart[rowz * 2] = m_run; a.mlpart[rowz * 2 + 1] = l_run; }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) s_last = (atomicAdd(&a.cnt[tile], 1u) == (unsigned)(a.splits - 1));
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    float mx = -INFINITY;
-    for (int zz = 0; zz < a.splits; ++zz) {
-      const int64_t r = ((int64_t)zz * gridDim.y + bh) * a.sq_pad + qi;
-      mx = fmaxf(mx, *reinterpret_cast<const volatile float*>(a.mlpart + r * 2));
-    }
-    l_run = 0.f;
-#pragma unroll
-    for (int t = 0; t < NDT; ++t) oacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (mx != -INFINITY) {
-      for (int zz = 0; zz < a.splits; ++zz) {
-        const int64_t r = ((int64_t)zz * gridDim.y + bh) * a.sq_pad + qi;
-        const float mz = *reinterpret_cast<const volatile float*>(a.mlpart + r * 2);
-        const float lz = *reinterpret_cast<const volatile float*>(a.mlpart + r * 2 + 1);
-        const float w = exp2f(mz - mx);  // mz = -inf -> 0
-        l_run += lz * w;
-#pragma unroll
-        for (int t = 0; t < NDT; ++t) {
-          const int d0 = t * 16 + lg * 4;
-          if (d0 < DH) {
-            const f32x4 p = *reinterpret_cast<const volatile f32x4*>(a.opart + r * DH + d0);
-            oacc[t] += p * w;
-          }
-        }
-      }
-    }
-    if (tid == 0) atomicExch(&a.cnt[tile], 0u);
-  }
-
   if (!qvalid) return;
   const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
   bf16* orow = a.o + b * a.o_bs + qi * a.o_rs + h * a.o_hs;
@@ -232,48 +353,36 @@ __global__ __launch_bounds__(NW * 64) void attn_kernel(AttnArgs a) {
   }
 }
 
-static int pick_nw(int64_t sq) { return sq <= 16 ? 1 : (sq <= 32 ? 2 : 4); }
-
 static int64_t rup(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
-static int auto_splits(int64_t tiles, int64_t sk) {
-  const int64_t nkb = (sk + KB - 1) / KB;
-  if (tiles >= 256 || nkb < 4) return 1;
-  int64_t s = (512 + tiles - 1) / tiles;
-  s = std::min<int64_t>(s, nkb / 2);
-  s = std::min<int64_t>(s, 32);
-  return (int)std::max<int64_t>(s, 1);
+// Waves per workgroup: enough to split long key runs, few enough that the per-wave state
+// (query fragments, accumulators, the next block's K/V) fits the register file without spills.
+template <int DH, int QT>
+static void launch_short_q(const AttnArgs& a, int64_t nkb, dim3 grid, hipStream_t s) {
+  constexpr bool wide = DH >= 128 && QT >= 2;
+  if (nkb <= 1) hipLaunchKernelGGL((attn_short_kernel<DH, QT, 1>), grid, dim3(64), 0, s, a);
+  else if (nkb <= 4 || wide) hipLaunchKernelGGL((attn_short_kernel<DH, QT, 4>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((attn_short_kernel<DH, QT, (wide ? 4 : 8)>), grid, dim3((wide ? 4 : 8) * 64), 0, s, a);
 }
 
-static int resolve_splits(int64_t B, int64_t H, int64_t sq, int64_t sk, int req) {
-  const int nw = pick_nw(sq);
-  const int64_t tiles = rup(sq, 16 * nw) / (16 * nw) * B * H;
-  int s = req > 0 ? req : auto_splits(tiles, sk);
-  const int64_t nkb = std::max<int64_t>((sk + KB - 1) / KB, 1);
-  if (s > nkb) s = (int)nkb;
-  return s;
+template <int DH>
+static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
+  // (Dh = 128 with more than 32 queries would not fit the short kernel's registers)
+  if (a.Sq <= 32 || (a.Sq <= 64 && DH < 128)) {
+    const int64_t nkb = (a.Sk + KB - 1) / KB;
+    const dim3 grid((unsigned)bh);
+    if (a.Sq <= 16) launch_short_q<DH, 1>(a, nkb, grid, s);
+    else if (a.Sq <= 32) launch_short_q<DH, 2>(a, nkb, grid, s);
+    else launch_short_q<DH, 4>(a, nkb, grid, s);
+  } else {
+    const dim3 grid((unsigned)(rup(a.Sq, 64) / 64), (unsigned)bh);
+    hipLaunchKernelGGL((attn_tiled_kernel<DH>), grid, dim3(256), 0, s, a);
+  }
 }
-
 
 }  // namespace fam
 
 using namespace fam;
-
-extern "C" int64_t fam_attention_workspace_bytes(int64_t batch, int64_t heads, int64_t sq, int64_t sk,
-                                                 int64_t head_dim, int num_splits) {
-  if (batch <= 0 || heads <= 0 || sq <= 0 || sk <= 0 || head_dim <= 0) return 0;
-  const int s = resolve_splits(batch, heads, sq, sk, num_splits);
-  if (s <= 1) return 0;
-  const int64_t rows = (int64_t)s * batch * heads * rup(sq, 64);
-  return FAM_WS_COUNTER_BYTES + rows * head_dim * 4 + rows * 2 * 4;
-}
-
-template <int DH>
-static void launch_dh(const AttnArgs& a, int nw, dim3 grid, hipStream_t s) {
-  if (nw == 1) hipLaunchKernelGGL((attn_kernel<DH, 1>), grid, dim3(64), 0, s, a);
-  else if (nw == 2) hipLaunchKernelGGL((attn_kernel<DH, 2>), grid, dim3(128), 0, s, a);
-  else hipLaunchKernelGGL((attn_kernel<DH, 4>), grid, dim3(256), 0, s, a);
-}
 
 extern "C" int fam_attention(const fam_attn_desc* d, void* stream) {
   FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_attention: null descriptor");
@@ -295,12 +404,10 @@ extern "C" int fam_attention(const fam_attn_desc* d, void* stream) {
   FAM_REQUIRE(d->mask_kind >= FAM_MASK_NONE && d->mask_kind <= FAM_MASK_ADD_BF16, FAM_ERR_INVALID_ARG,
               "fam_attention: unknown mask kind %d", d->mask_kind);
   FAM_REQUIRE(d->mask_kind == FAM_MASK_NONE || d->mask, FAM_ERR_INVALID_ARG, "fam_attention: mask kind without mask");
-  FAM_REQUIRE(d->num_splits >= 0 && d->num_splits <= 64, FAM_ERR_INVALID_ARG, "fam_attention: num_splits in [0, 64]");
-  const int64_t Sk = d->sk0 + d->sk1;
+  const int64_t bh = d->batch * d->heads;
+  FAM_REQUIRE(bh <= 65535 || d->sq <= 64, FAM_ERR_UNSUPPORTED, "fam_attention: batch*heads must be <= 65535");
   if (d->batch == 0 || d->sq == 0) return FAM_OK;
 
-  const int nw = pick_nw(d->sq);
-  const int splits = Sk > 0 ? resolve_splits(d->batch, d->heads, d->sq, Sk, d->num_splits) : 1;
   AttnArgs a{};
   a.q = (const bf16*)d->q; a.q_bs = d->q_bs; a.q_rs = d->q_rs; a.q_hs = d->q_hs;
   a.k0 = (const bf16*)d->k0; a.k0_bs = d->k0_bs; a.k0_rs = d->k0_rs; a.k0_hs = d->k0_hs;
@@ -308,34 +415,16 @@ extern "C" int fam_attention(const fam_attn_desc* d, void* stream) {
   a.k1 = (const bf16*)d->k1; a.k1_bs = d->k1_bs; a.k1_rs = d->k1_rs; a.k1_hs = d->k1_hs;
   a.v1 = (const bf16*)d->v1; a.v1_bs = d->v1_bs; a.v1_rs = d->v1_rs; a.v1_hs = d->v1_hs;
   a.o = (bf16*)d->o; a.o_bs = d->o_bs; a.o_rs = d->o_rs; a.o_hs = d->o_hs;
-  a.H = d->heads; a.Sq = d->sq; a.sk0 = d->sk0; a.Sk = Sk;
-  const int64_t nkb = (Sk + KB - 1) / KB;
-  a.kchunk = std::max<int64_t>((nkb + splits - 1) / splits, 1) * KB;
-  a.scale_log2 = d->scale * 1.4426950408889634f;
+  a.H = d->heads; a.Sq = d->sq; a.sk0 = d->sk0; a.Sk = d->sk0 + d->sk1;
+  a.scale_log2 = d->scale * kLog2e;
   a.mask = d->mask; a.mask_kind = d->mask_kind; a.mbs = d->mask_bs; a.mhs = d->mask_hs; a.mqs = d->mask_qs;
-  a.splits = splits;
-  a.sq_pad = rup(d->sq, 64);
-  if (splits > 1) {
-    const int64_t need = fam_attention_workspace_bytes(d->batch, d->heads, d->sq, Sk, Dh, splits);
-    FAM_REQUIRE(d->workspace && d->workspace_bytes >= need && fam_host::aligned16(d->workspace), FAM_ERR_WORKSPACE,
-                "fam_attention: %d key splits need a 16-byte aligned workspace of %lld bytes (got %lld)", splits,
-                (long long)need, (long long)d->workspace_bytes);
-    a.cnt = (unsigned*)d->workspace;
-    a.opart = (float*)((char*)d->workspace + FAM_WS_COUNTER_BYTES);
-    a.mlpart = a.opart + (int64_t)splits * d->batch * d->heads * a.sq_pad * Dh;
-  }
-  FAM_REQUIRE(d->batch * d->heads <= 65535, FAM_ERR_UNSUPPORTED, "fam_attention: batch*heads must be <= 65535");
-  dim3 grid((unsigned)(rup(d->sq, 16 * nw) / (16 * nw)), (unsigned)(d->batch * d->heads), (unsigned)splits);
-  FAM_REQUIRE(splits <= 1 || (int64_t)grid.x * grid.y <= FAM_WS_COUNTER_BYTES / 4, FAM_ERR_UNSUPPORTED,
-              "fam_attention: %d key splits with %lld tiles exceed the workspace counter area", splits,
-              (long long)grid.x * grid.y);
   hipStream_t s = (hipStream_t)stream;
   switch (Dh) {
-    case 8: launch_dh<8>(a, nw, grid, s); break;
-    case 16: launch_dh<16>(a, nw, grid, s); break;
-    case 32: launch_dh<32>(a, nw, grid, s); break;
-    case 64: launch_dh<64>(a, nw, grid, s); break;
-    default: launch_dh<128>(a, nw, grid, s); break;
+    case 8: launch_dh<8>(a, bh, s); break;
+    case 16: launch_dh<16>(a, bh, s); break;
+    case 32: launch_dh<32>(a, bh, s); break;
+    case 64: launch_dh<64>(a, bh, s); break;
+    default: launch_dh<128>(a, bh, s); break;
   }
   return fam_host::check_launch("fam_attention");
 }

@@ -2,31 +2,32 @@
 //     out[m, n] = epi( sum_k pro(a)[m, k] * w[n, k] + bias[n] )
 // w is in nn.Linear layout [N, K] (K contiguous), a is [M, K] (K contiguous).
 //
-// Tiling (gfx950, wave64, MFMA v_mfma_f32_16x16x32_bf16):
-//   * a 256-thread workgroup (4 waves) owns a BM x BN output tile; the waves are laid out
-//     WAVES_M x WAVES_N and each computes (BM/WAVES_M) x (BN/WAVES_N) as 16x16 MFMA tiles;
-//   * K advances in steps of BK = 64 (two MFMA k-substeps); the A and W tiles of a step
-//     are staged through LDS, double-buffered so one barrier per step suffices, and the
-//     next step's global loads are issued before the current step's MFMAs;
-//   * the weight tile is the MFMA A-operand and the activation tile the B-operand, so a
-//     lane ends up owning 4 consecutive output columns of one row (8-byte stores);
-//   * the prologue (LayerNorm, optional affine, or AdaLN modulate) is applied while the
-//     activation tile is written to LDS, from per-row statistics computed at kernel start;
-//   * split-K: grid.z workgroups share a tile; each writes fp32 partials to the workspace,
-//     and the last to arrive (agent-scope counter) sums them in split order and runs the
-//     epilogue, then resets the counter, so results are deterministic and the workspace
-//     needs no clearing between launches.
+// Two kernels, chosen by M; neither communicates between workgroups (on gfx950 a release /
+// acquire fence between workgroups writes back and invalidates the XCD's L2, which costs far
+// more than these small products), so every workgroup owns its outputs outright.
 //
-// Algorithmic bytes per launch (HBM roofline numerator): 2*(M*K + N*K + M*N) (+ bias,
-// residual, modulation).  At M <= 64 the weight stream dominates (AI ~ M flop/byte).
+// skinny_kernel (M <= 64, the 16..64-token action projections): weight streaming.
+//   * a workgroup of 8 waves owns 16 output columns for all M rows; the waves split the K
+//     range (32-wide MFMA k-steps, contiguous per wave) and each wave issues the loads of its
+//     whole weight slice up front, so a workgroup keeps its full 16 x K weight panel in
+//     flight at once -- the bytes in flight, not the MFMA rate, bound this regime;
+//   * the weight rows are the MFMA A-operand and the activations the B-operand
+//     (v_mfma_f32_16x16x32_bf16), read straight from global memory (the activation block is
+//     small and L2-resident); the LayerNorm / AdaLN prologue is applied in registers from
+//     per-row statistics the waves compute at kernel start while the weights are in flight;
+//   * the 8 partial accumulators are summed through LDS in wave order (deterministic), then
+//     the epilogue runs one output element per thread.
+//   Bytes per launch (HBM roofline numerator): 2*(N*K + M*K + M*N) + bias/residual/modulation.
+//
+// tiled_kernel (M > 64: the per-call context projections, batched throughput points):
+//   * 256-thread workgroup, BM x BN output tile (64x64 or 128x128), 2x2 waves of 16x16 MFMA
+//     tiles, K in steps of 64 through double-buffered LDS, next step's global loads issued
+//     before the current step's MFMAs; prologue statistics per tile row at kernel start.
 #include <algorithm>
 
 #include "fam_common.h"
 
 namespace fam {
-
-constexpr int BK = 64;
-constexpr int LDS_K = BK + 8;  // padded row (144 B) to spread LDS banks
 
 struct GemmArgs {
   const bf16* a; int64_t lda;
@@ -41,8 +42,7 @@ struct GemmArgs {
   const bf16* res; int64_t ldr;
   const bf16* gate; int64_t gbs, grs, gns;
   int64_t rpb;
-  int split; int64_t kchunk;  // K range of split z: [z*kchunk, min(K, (z+1)*kchunk))
-  unsigned* cnt; float* part;
+  int out_f32;
 };
 
 __device__ __forceinline__ float apply_act(float v, int act) {
@@ -51,8 +51,163 @@ __device__ __forceinline__ float apply_act(float v, int act) {
   return v;
 }
 
+// bias, activation, gate * value + residual, store (bf16 or fp32) for one output element
+__device__ __forceinline__ void epilogue_store(const GemmArgs& g, int64_t m, int64_t n, float v) {
+  if (g.bias) v += to_f(g.bias[n]);
+  v = apply_act(v, g.act);
+  if (g.res) {
+    const int64_t bi = m / g.rpb, si = m - bi * g.rpb;
+    float gt = 1.0f;
+    if (g.gate) gt = to_f(g.gate[bi * g.gbs + si * g.grs + n * g.gns]);
+    const float r = g.out_f32 ? reinterpret_cast<const float*>(g.res)[m * g.ldr + n] : to_f(g.res[m * g.ldr + n]);
+    v = r + gt * v;
+  }
+  if (g.out_f32) reinterpret_cast<float*>(g.out)[m * g.ldo + n] = v;
+  else g.out[m * g.ldo + n] = to_bf(v);
+}
+
+// LayerNorm / AdaLN of 8 consecutive elements (row m, columns k..k+7) of the A operand.
+template <int PRO>
+__device__ __forceinline__ bf16x8 prologue8(const GemmArgs& g, bf16x8 v, int64_t m, int64_t k, float mu, float rs) {
+  if constexpr (PRO == FAM_PRO_NONE) {
+    return v;
+  } else {
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (to_f(v[e]) - mu) * rs;
+    if constexpr (PRO == FAM_PRO_LAYERNORM) {
+      if (g.pw) {
+        const bf16x8 wv = load8(g.pw + k);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] *= to_f(wv[e]);
+      }
+      if (g.pb) {
+        const bf16x8 bv = load8(g.pb + k);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] += to_f(bv[e]);
+      }
+    } else {
+      const int64_t bi = m / g.rpb, si = m - bi * g.rpb;
+      const int64_t off = bi * g.mbs + si * g.mrs + k;
+      const bf16x8 sh = load8(g.shift + off), sc = load8(g.scale + off);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = o[e] * (1.0f + to_f(sc[e])) + to_f(sh[e]);
+    }
+    bf16x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = to_bf(o[e]);
+    return r;
+  }
+}
+
+// Row statistics (mean, rstd) of rows m0 .. m0+rows-1: one wave per row, two passes
+// (mean, then centred variance); rows past M get zeros.
+__device__ __forceinline__ void row_stats(const GemmArgs& g, int64_t m0, int rows, int wave, int nwaves, int lane,
+                                          float* s_mean, float* s_rstd) {
+  for (int r = wave; r < rows; r += nwaves) {
+    const int64_t m = m0 + r;
+    float mean = 0.f, rstd = 0.f;
+    if (m < g.M) {  // wave-uniform
+      const bf16* ar = g.a + m * g.lda;
+      float s = 0.f;
+      for (int64_t c = (int64_t)lane * 8; c < g.K; c += 512) {
+        const bf16x8 t = load8(ar + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s += to_f(t[e]);
+      }
+      mean = wave_sum(s) / (float)g.K;
+      float q = 0.f;
+      for (int64_t c = (int64_t)lane * 8; c < g.K; c += 512) {
+        const bf16x8 t = load8(ar + c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { const float d = to_f(t[e]) - mean; q += d * d; }
+      }
+      rstd = rsqrtf(wave_sum(q) / (float)g.K + g.eps);
+    }
+    if (lane == 0) { s_mean[r] = mean; s_rstd[r] = rstd; }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// skinny_kernel: M <= 16*MT rows, 16 output columns per workgroup, NW waves split K,
+// KS k-steps of weights in flight per wave.
+template <int MT, int NW, int KS, int PRO>
+__global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
+  constexpr int MR = MT * 16;
+  __shared__ float s_mean[MR], s_rstd[MR];
+  __shared__ float s_red[NW][MR][16];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t nsub = (g.K + 31) / 32;       // 32-wide k-steps
+  const int64_t per = (nsub + NW - 1) / NW;   // k-steps per wave
+  const int64_t s_beg = std::min(nsub, (int64_t)wave * per), s_end = std::min(nsub, s_beg + per);
+  const int64_t nrow = n0 + l16;
+  const bf16* wrow = g.w + nrow * g.ldw;
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  bf16x8 wf[KS];
+  auto wload = [&](int64_t sb) {
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+      const int64_t k = (sb + j) * 32 + lg * 8;
+      wf[j] = (sb + j < s_end && nrow < g.N && k < g.K) ? load8(wrow + k) : zero8();
+    }
+  };
+  wload(s_beg);  // the weight stream starts before the prologue statistics
+
+  if constexpr (PRO != FAM_PRO_NONE) {
+    row_stats(g, 0, MR, wave, NW, lane, s_mean, s_rstd);
+    __syncthreads();
+  }
+
+  for (int64_t sb = s_beg; sb < s_end; sb += KS) {
+    if (sb != s_beg) wload(sb);
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+      const int64_t s = sb + j;
+      if (s < s_end) {
+        const int64_t k = s * 32 + lg * 8;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const int64_t m = i * 16 + l16;
+          bf16x8 af = zero8();
+          if (m < g.M && k < g.K) {
+            af = load8(g.a + m * g.lda + k);
+            if constexpr (PRO != FAM_PRO_NONE) af = prologue8<PRO>(g, af, m, k, s_mean[m], s_rstd[m]);
+          }
+          acc[i] = mfma16(wf[j], af, acc[i]);
+        }
+      }
+    }
+  }
+
+  // lane holds out[m = i*16 + l16][n = n0 + 4*lg + e]; reduce the waves in order
+#pragma unroll
+  for (int i = 0; i < MT; ++i) *reinterpret_cast<f32x4*>(&s_red[wave][i * 16 + l16][lg * 4]) = acc[i];
+  __syncthreads();
+  for (int t = tid; t < MR * 16; t += NW * 64) {
+    const int mr = t >> 4, nc = t & 15;
+    const int64_t n = n0 + nc;
+    if (mr >= g.M || n >= g.N) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) v += s_red[w][mr][nc];
+    epilogue_store(g, mr, n, v);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// tiled_kernel: BM x BN tiles, 4 waves as WAVES_M x WAVES_N.
+constexpr int BK = 64;
+constexpr int LDS_K = BK + 8;  // padded row (144 B) to spread LDS banks
+
 template <int BM, int BN, int WAVES_M, int PRO>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256) void tiled_kernel(GemmArgs g) {
   constexpr int WAVES_N = 4 / WAVES_M;
   constexpr int TM = BM / WAVES_M, TN = BN / WAVES_N;
   constexpr int FM = TM / 16, FN = TN / 16;
@@ -63,40 +218,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   __shared__ bf16 As[2][BM][LDS_K];
   __shared__ bf16 Ws[2][BN][LDS_K];
   __shared__ float s_mean[BM], s_rstd[BM];
-  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
   const int wm0 = (wave / WAVES_N) * TM, wn0 = (wave % WAVES_N) * TN;
   const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
-  const int z = blockIdx.z;
-  const int64_t kbeg = (int64_t)z * g.kchunk;
-  const int64_t kend = min(g.K, kbeg + g.kchunk);
 
-  // ---- prologue statistics: one wave per row, two passes (mean, then centred variance)
   if constexpr (PRO != FAM_PRO_NONE) {
-    for (int r = wave; r < BM; r += 4) {
-      const int64_t m = m0 + r;
-      float mean = 0.f, rstd = 0.f;
-      if (m < g.M) {  // wave-uniform
-        const bf16* ar = g.a + m * g.lda;
-        float s = 0.f;
-        for (int64_t c = (int64_t)lane * 8; c < g.K; c += 512) {
-          bf16x8 t = load8(ar + c);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) s += to_f(t[e]);
-        }
-        mean = wave_sum(s) / (float)g.K;
-        float q = 0.f;
-        for (int64_t c = (int64_t)lane * 8; c < g.K; c += 512) {
-          bf16x8 t = load8(ar + c);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) { const float d = to_f(t[e]) - mean; q += d * d; }
-        }
-        rstd = rsqrtf(wave_sum(q) / (float)g.K + g.eps);
-      }
-      if (lane == 0) { s_mean[r] = mean; s_rstd[r] = rstd; }
-    }
+    row_stats(g, m0, BM, wave, 4, lane, s_mean, s_rstd);
     __syncthreads();
   }
 
@@ -106,13 +235,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     for (int p = 0; p < CA; ++p) {
       const int c = tid + 256 * p, r = c >> 3, kc = (c & 7) * 8;
       const int64_t m = m0 + r, k = k0 + kc;
-      ra[p] = (m < g.M && k < kend) ? load8(g.a + m * g.lda + k) : zero8();
+      ra[p] = (m < g.M && k < g.K) ? load8(g.a + m * g.lda + k) : zero8();
     }
 #pragma unroll
     for (int p = 0; p < CW; ++p) {
       const int c = tid + 256 * p, r = c >> 3, kc = (c & 7) * 8;
       const int64_t n = n0 + r, k = k0 + kc;
-      rw[p] = (n < g.N && k < kend) ? load8(g.w + n * g.ldw + k) : zero8();
+      rw[p] = (n < g.N && k < g.K) ? load8(g.w + n * g.ldw + k) : zero8();
     }
   };
   auto lstore = [&](int buf, int64_t k0) {
@@ -122,32 +251,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
       bf16x8 v = ra[p];
       if constexpr (PRO != FAM_PRO_NONE) {
         const int64_t m = m0 + r, k = k0 + kc;
-        if (m < g.M && k < kend) {
-          const float mu = s_mean[r], rs = s_rstd[r];
-          float o[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[e] = (to_f(v[e]) - mu) * rs;
-          if constexpr (PRO == FAM_PRO_LAYERNORM) {
-            if (g.pw) {
-              bf16x8 wv = load8(g.pw + k);
-#pragma unroll
-              for (int e = 0; e < 8; ++e) o[e] *= to_f(wv[e]);
-            }
-            if (g.pb) {
-              bf16x8 bv = load8(g.pb + k);
-#pragma unroll
-              for (int e = 0; e < 8; ++e) o[e] += to_f(bv[e]);
-            }
-          } else {
-            const int64_t bi = m / g.rpb, si = m - bi * g.rpb;
-            const int64_t off = bi * g.mbs + si * g.mrs + k;
-            bf16x8 sh = load8(g.shift + off), sc = load8(g.scale + off);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = o[e] * (1.0f + to_f(sc[e])) + to_f(sh[e]);
-          }
-#pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = to_bf(o[e]);
-        }
+        if (m < g.M && k < g.K) v = prologue8<PRO>(g, v, m, k, s_mean[r], s_rstd[r]);
       }
       *reinterpret_cast<bf16x8*>(&As[buf][r][kc]) = v;
     }
@@ -164,16 +268,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int64_t niter = (kend > kbeg) ? (kend - kbeg + BK - 1) / BK : 0;
-  if (niter > 0) {
-    gload(kbeg);
-    lstore(0, kbeg);
-    __syncthreads();
-  }
+  const int64_t niter = (g.K + BK - 1) / BK;
+  gload(0);
+  lstore(0, 0);
+  __syncthreads();
   for (int64_t it = 0; it < niter; ++it) {
     const int buf = (int)(it & 1);
     const bool more = it + 1 < niter;
-    if (more) gload(kbeg + (it + 1) * BK);
+    if (more) gload((it + 1) * BK);
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       bf16x8 af[FM], wf[FN];
@@ -186,122 +288,58 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = mfma16(wf[j], af[i], acc[i][j]);
     }
-    if (more) lstore(buf ^ 1, kbeg + (it + 1) * BK);
+    if (more) lstore(buf ^ 1, (it + 1) * BK);
     __syncthreads();
   }
 
-  // ---- split-K: publish partials, last arriver reduces in split order
-  if (g.split > 1) {
-    const int64_t ntile = (int64_t)gridDim.x * gridDim.y;
-    const int64_t tile = (int64_t)blockIdx.y * gridDim.x + blockIdx.x;
-    auto pptr = [&](int zz, int i, int j) {
-      const int lm = wm0 + i * 16 + l16, ln = wn0 + j * 16 + lg * 4;
-      return g.part + (((int64_t)zz * ntile + tile) * BM + lm) * BN + ln;
-    };
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) *reinterpret_cast<f32x4*>(pptr(z, i, j)) = acc[i][j];
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const unsigned prev = atomicAdd(&g.cnt[tile], 1u);
-      s_last = (prev == (unsigned)(g.split - 1));
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int zz = 0; zz < g.split; ++zz) {
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const f32x4 p = *reinterpret_cast<const volatile f32x4*>(pptr(zz, i, j));
-          acc[i][j] += p;
-        }
-    }
-    if (tid == 0) atomicExch(&g.cnt[tile], 0u);
-  }
-
-  // ---- epilogue: bias, activation, gate * value + residual, bf16 store
+  // lane owns out[m0 + wm0 + i*16 + l16][n0 + wn0 + j*16 + 4*lg + e]
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int64_t m = m0 + wm0 + i * 16 + l16;
     if (m >= g.M) continue;
-    const int64_t bi = m / g.rpb, si = m - bi * g.rpb;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
       const int64_t nb = n0 + wn0 + j * 16 + lg * 4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t n = nb + e;
-        if (n >= g.N) continue;
-        float v = acc[i][j][e];
-        if (g.bias) v += to_f(g.bias[n]);
-        v = apply_act(v, g.act);
-        if (g.res) {
-          float gt = 1.0f;
-          if (g.gate) gt = to_f(g.gate[bi * g.gbs + si * g.grs + n * g.gns]);
-          v = to_f(g.res[m * g.ldr + n]) + gt * v;
-        }
-        g.out[m * g.ldo + n] = to_bf(v);
-      }
+      for (int e = 0; e < 4; ++e)
+        if (nb + e < g.N) epilogue_store(g, m, nb + e, acc[i][j][e]);
     }
   }
 }
 
-struct Cfg { int bm, bn, wm; };
-
-static Cfg pick_cfg(int64_t M, int64_t N) {
-  if (M <= 32) return {32, 64, 1};
-  if (M <= 64 || N < 128) return {64, 64, 2};
-  return {128, 128, 2};
-}
-
 static int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
-static int auto_split(int64_t tiles, int64_t K) {
-  const int64_t kiter = (K + BK - 1) / BK;
-  if (tiles >= 256 || kiter < 4) return 1;
-  int64_t s = (512 + tiles - 1) / tiles;
-  s = std::min<int64_t>(s, kiter / 2);
-  s = std::min<int64_t>(s, 16);
-  return (int)std::max<int64_t>(s, 1);
+template <int MT, int KS>
+static void launch_skinny(const GemmArgs& a, int pro, hipStream_t s) {
+  constexpr int NW = 8;
+  dim3 grid((unsigned)(round_up(a.N, 16) / 16));
+  switch (pro) {
+    case FAM_PRO_LAYERNORM: hipLaunchKernelGGL((skinny_kernel<MT, NW, KS, FAM_PRO_LAYERNORM>), grid, dim3(NW * 64), 0, s, a); break;
+    case FAM_PRO_ADALN: hipLaunchKernelGGL((skinny_kernel<MT, NW, KS, FAM_PRO_ADALN>), grid, dim3(NW * 64), 0, s, a); break;
+    default: hipLaunchKernelGGL((skinny_kernel<MT, NW, KS, FAM_PRO_NONE>), grid, dim3(NW * 64), 0, s, a); break;
+  }
+}
+
+template <int MT>
+static void launch_skinny_k(const GemmArgs& a, int pro, hipStream_t s) {
+  const int64_t per = ((a.K + 31) / 32 + 7) / 8;  // k-steps per wave
+  if (per <= 4) launch_skinny<MT, 4>(a, pro, s);
+  else launch_skinny<MT, 16>(a, pro, s);
+}
+
+template <int BM, int BN, int WM>
+static void launch_tiled(const GemmArgs& a, int pro, hipStream_t s) {
+  dim3 grid((unsigned)(round_up(a.N, BN) / BN), (unsigned)(round_up(a.M, BM) / BM));
+  switch (pro) {
+    case FAM_PRO_LAYERNORM: hipLaunchKernelGGL((tiled_kernel<BM, BN, WM, FAM_PRO_LAYERNORM>), grid, dim3(256), 0, s, a); break;
+    case FAM_PRO_ADALN: hipLaunchKernelGGL((tiled_kernel<BM, BN, WM, FAM_PRO_ADALN>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((tiled_kernel<BM, BN, WM, FAM_PRO_NONE>), grid, dim3(256), 0, s, a); break;
+  }
 }
 
 }  // namespace fam
 
 using namespace fam;
-
-
-static int resolve_split(int64_t M, int64_t N, int64_t K, int split_k) {
-  const Cfg c = pick_cfg(M, N);
-  const int64_t tiles = round_up(M, c.bm) / c.bm * (round_up(N, c.bn) / c.bn);
-  int s = split_k > 0 ? split_k : auto_split(tiles, K);
-  const int64_t kiter = (K + BK - 1) / BK;
-  if (s > kiter) s = (int)std::max<int64_t>(kiter, 1);
-  return s;
-}
-
-extern "C" int64_t fam_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int split_k) {
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
-  const int s = resolve_split(M, N, K, split_k);
-  if (s <= 1) return 0;
-  return FAM_WS_COUNTER_BYTES + (int64_t)s * round_up(M, 128) * round_up(N, 128) * 4;
-}
-
-template <int BM, int BN, int WM>
-static void launch_cfg(const GemmArgs& a, int pro, dim3 grid, hipStream_t s) {
-  switch (pro) {
-    case FAM_PRO_LAYERNORM: hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, FAM_PRO_LAYERNORM>), grid, dim3(256), 0, s, a); break;
-    case FAM_PRO_ADALN: hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, FAM_PRO_ADALN>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, FAM_PRO_NONE>), grid, dim3(256), 0, s, a); break;
-  }
-}
 
 extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
   FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_gemm: null descriptor");
@@ -329,11 +367,9 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
   }
   FAM_REQUIRE(d->rows_per_batch >= 1, FAM_ERR_INVALID_ARG, "fam_gemm: rows_per_batch must be >= 1");
   FAM_REQUIRE(!d->gate || d->res, FAM_ERR_INVALID_ARG, "fam_gemm: a gate needs a residual");
-  FAM_REQUIRE(d->split_k >= 0 && d->split_k <= 64, FAM_ERR_INVALID_ARG, "fam_gemm: split_k must be in [0, 64]");
+  FAM_REQUIRE(d->N <= (int64_t)65535 * 16 && d->M <= (int64_t)65535 * 64, FAM_ERR_UNSUPPORTED, "fam_gemm: too large");
   if (d->M == 0) return FAM_OK;
 
-  const Cfg c = pick_cfg(d->M, d->N);
-  const int split = resolve_split(d->M, d->N, d->K, d->split_k);
   GemmArgs a{};
   a.a = (const bf16*)d->a; a.lda = d->lda;
   a.w = (const bf16*)d->w; a.ldw = d->ldw;
@@ -347,25 +383,12 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
   a.res = (const bf16*)d->res; a.ldr = d->ldr;
   a.gate = (const bf16*)d->gate; a.gbs = d->gate_bs; a.grs = d->gate_rs; a.gns = d->gate_ns;
   a.rpb = d->rows_per_batch;
-  a.split = split;
-  const int64_t kiter = (d->K + BK - 1) / BK;
-  a.kchunk = ((kiter + split - 1) / split) * BK;
-  if (split > 1) {
-    const int64_t need = fam_gemm_workspace_bytes(d->M, d->N, d->K, split);
-    FAM_REQUIRE(d->workspace && d->workspace_bytes >= need && fam_host::aligned16(d->workspace), FAM_ERR_WORKSPACE,
-                "fam_gemm: split_k=%d needs a 16-byte aligned workspace of %lld bytes (got %lld)", split,
-                (long long)need, (long long)d->workspace_bytes);
-    a.cnt = (unsigned*)d->workspace;
-    a.part = (float*)((char*)d->workspace + FAM_WS_COUNTER_BYTES);
-  }
-  dim3 grid((unsigned)(round_up(d->N, c.bn) / c.bn), (unsigned)(round_up(d->M, c.bm) / c.bm), (unsigned)split);
-  FAM_REQUIRE(split <= 1 || (int64_t)grid.x * grid.y <= FAM_WS_COUNTER_BYTES / 4, FAM_ERR_UNSUPPORTED,
-              "fam_gemm: split_k=%d with %lld tiles exceeds the workspace counter area", split,
-              (long long)grid.x * grid.y);
-  FAM_REQUIRE(grid.y <= 65535 && split <= 65535, FAM_ERR_UNSUPPORTED, "fam_gemm: M too large");
+  a.out_f32 = d->out_f32 != 0;
   hipStream_t s = (hipStream_t)stream;
-  if (c.bm == 32) launch_cfg<32, 64, 1>(a, d->prologue, grid, s);
-  else if (c.bm == 64) launch_cfg<64, 64, 2>(a, d->prologue, grid, s);
-  else launch_cfg<128, 128, 2>(a, d->prologue, grid, s);
+  if (d->M <= 16) launch_skinny_k<1>(a, d->prologue, s);
+  else if (d->M <= 32) launch_skinny_k<2>(a, d->prologue, s);
+  else if (d->M <= 64) launch_skinny_k<4>(a, d->prologue, s);
+  else if (round_up(d->M, 128) / 128 * (round_up(d->N, 128) / 128) >= 200) launch_tiled<128, 128, 2>(a, d->prologue, s);
+  else launch_tiled<64, 64, 2>(a, d->prologue, s);
   return fam_host::check_launch("fam_gemm");
 }

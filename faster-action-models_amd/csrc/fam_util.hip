@@ -72,7 +72,8 @@ __global__ __launch_bounds__(256) void add_mod_kernel(const bf16* __restrict__ t
 }
 
 // y[m, n] = sum_k x[m, k] w[n, k] + b[n], one thread per output, K <= 64.
-__global__ __launch_bounds__(256) void linear_smallk_kernel(const bf16* __restrict__ x, int64_t ldx,
+template <typename XT>
+__global__ __launch_bounds__(256) void linear_smallk_kernel(const XT* __restrict__ x, int64_t ldx,
                                                             const bf16* __restrict__ w, const bf16* __restrict__ b,
                                                             bf16* __restrict__ y, int64_t ldy, int64_t M, int64_t N,
                                                             int64_t K) {
@@ -80,7 +81,7 @@ __global__ __launch_bounds__(256) void linear_smallk_kernel(const bf16* __restri
   if (idx >= M * N) return;
   const int64_t m = idx / N, n = idx - m * N;
   float acc = 0.f;
-  for (int64_t k = 0; k < K; ++k) acc += to_f(x[m * ldx + k]) * to_f(w[n * K + k]);
+  for (int64_t k = 0; k < K; ++k) acc += (float)x[m * ldx + k] * to_f(w[n * K + k]);
   if (b) acc += to_f(b[n]);
   y[m * ldy + n] = to_bf(acc);
 }
@@ -126,13 +127,17 @@ extern "C" int fam_add_modulation(const void* t_mod, const void* modulation, voi
   return fam_host::check_launch("fam_add_modulation");
 }
 
-extern "C" int fam_linear_smallk(const void* x, int64_t ldx, const void* w, const void* b, void* y, int64_t ldy,
-                                 int64_t M, int64_t N, int64_t K, void* stream) {
+extern "C" int fam_linear_smallk(const void* x, int64_t ldx, int x_f32, const void* w, const void* b, void* y,
+                                 int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream) {
   FAM_REQUIRE(x && w && y, FAM_ERR_INVALID_ARG, "fam_linear_smallk: null pointer");
   FAM_REQUIRE(M >= 0 && N >= 1 && K >= 1 && K <= 64, FAM_ERR_INVALID_ARG, "fam_linear_smallk: need 1 <= K <= 64");
   FAM_REQUIRE(ldx >= K && ldy >= N, FAM_ERR_INVALID_ARG, "fam_linear_smallk: bad leading dimensions");
   if (M == 0) return FAM_OK;
-  hipLaunchKernelGGL(linear_smallk_kernel, dim3(blocks_for(M * N)), dim3(256), 0, (hipStream_t)stream,
-                     (const bf16*)x, ldx, (const bf16*)w, (const bf16*)b, (bf16*)y, ldy, M, N, K);
+  if (x_f32)
+    hipLaunchKernelGGL(linear_smallk_kernel<float>, dim3(blocks_for(M * N)), dim3(256), 0, (hipStream_t)stream,
+                       (const float*)x, ldx, (const bf16*)w, (const bf16*)b, (bf16*)y, ldy, M, N, K);
+  else
+    hipLaunchKernelGGL(linear_smallk_kernel<bf16>, dim3(blocks_for(M * N)), dim3(256), 0, (hipStream_t)stream,
+                       (const bf16*)x, ldx, (const bf16*)w, (const bf16*)b, (bf16*)y, ldy, M, N, K);
   return fam_host::check_launch("fam_linear_smallk");
 }

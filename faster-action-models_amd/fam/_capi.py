@@ -15,7 +15,6 @@ FAM_OK = 0
 FAM_ERR_INVALID_ARG = 1
 FAM_ERR_UNSUPPORTED = 2
 FAM_ERR_LAUNCH = 3
-FAM_ERR_WORKSPACE = 4
 FAM_ABI_VERSION = 1
 
 FAM_MASK_NONE, FAM_MASK_BOOL, FAM_MASK_ADD_F32, FAM_MASK_ADD_BF16 = 0, 1, 2, 3
@@ -46,8 +45,6 @@ class AttnDesc(C.Structure):
         ("batch", _i64), ("heads", _i64), ("sq", _i64), ("sk0", _i64), ("sk1", _i64), ("head_dim", _i64),
         ("scale", C.c_float),
         ("mask", _vp), ("mask_kind", C.c_int), ("mask_bs", _i64), ("mask_hs", _i64), ("mask_qs", _i64),
-        ("num_splits", C.c_int),
-        ("workspace", _vp), ("workspace_bytes", _i64),
     ]
 
 
@@ -68,8 +65,7 @@ class GemmDesc(C.Structure):
         ("res", _vp), ("ldr", _i64),
         ("gate", _vp), ("gate_bs", _i64), ("gate_rs", _i64), ("gate_ns", _i64),
         ("rows_per_batch", _i64),
-        ("split_k", C.c_int),
-        ("workspace", _vp), ("workspace_bytes", _i64),
+        ("out_f32", C.c_int),
     ]
 
 
@@ -81,10 +77,8 @@ SIGNATURES = {
     "fam_rmsnorm_rope": (C.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, C.c_float, _vp, _vp, _i64, _i64,
                                    _i64, _vp]),
     "fam_attention": (C.c_int, [C.POINTER(AttnDesc), _vp]),
-    "fam_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, C.c_int]),
     "fam_gemm": (C.c_int, [C.POINTER(GemmDesc), _vp]),
-    "fam_gemm_workspace_bytes": (_i64, [_i64, _i64, _i64, C.c_int]),
-    "fam_linear_smallk": (C.c_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "fam_linear_smallk": (C.c_int, [_vp, _i64, C.c_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "fam_euler_step": (C.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "fam_sinusoid": (C.c_int, [_vp, _vp, _i64, _i64, _vp]),
     "fam_add_modulation": (C.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),

@@ -23,7 +23,7 @@ Per policy call the plan runs:
   per block (11 launches):
     [AdaLN1 + QKV GEMM] -> RMSNorm+RoPE(q) -> RMSNorm+RoPE(k) -> self-attention ->
     [o GEMM + gate_msa + residual] -> [LayerNorm3 + cross-q GEMM] -> RMSNorm(q) ->
-    cross-attention (keys split over workgroups) -> [cross-o GEMM + residual] ->
+    cross-attention (keys split over the waves of a workgroup) -> [cross-o GEMM + residual] ->
     [AdaLN2 + FFN-up GEMM + GELU] -> [FFN-down GEMM + gate_mlp + residual].
 
 The per-call prologue replaces work the reference repeats inside every step (time MLP,
@@ -239,7 +239,9 @@ class FusedActionDiT:
         z = lambda *s: torch.zeros(*s, dtype=_BF16, device=dev)  # noqa: E731
         self.noise_in = z(batch, seq_len, cfg.action_dim)
         self.context_in = z(ctx_len, cfg.text_dim)
-        self.latents = z(batch, seq_len, cfg.action_dim)
+        # the chunk being denoised is carried in fp32 between steps (the reference rounds it to
+        # bf16 after every step); it is the only state that survives a step
+        self.latents = torch.zeros(batch, seq_len, cfg.action_dim, dtype=torch.float32, device=dev)
         self.x = z(M, H)
         self.qkv = z(M, 3 * A)
         self.attn = z(M, A)
@@ -256,18 +258,13 @@ class FusedActionDiT:
         self.ctxkv = z(ctx_len, L * 2 * A)
 
         self._descs: list = []   # keeps ctypes descriptors alive
-        self._ws_need = 0
         self.plan = self._build_plan()
-        self.workspace = torch.zeros(max(self._ws_need, 256), dtype=torch.uint8, device=dev)
-        for d in self._descs:
-            if isinstance(d, (_capi.GemmDesc, _capi.AttnDesc)):
-                d.workspace, d.workspace_bytes = self.workspace.data_ptr(), self.workspace.numel()
         self.graph: Optional[torch.cuda.CUDAGraph] = None
 
     # ------------------------------------------------------------------ plan building
     def _gemm(self, name, a, w, bias, out, *, prologue=_capi.FAM_PRO_NONE, pro_w=None, pro_b=None,
               shift=None, scale=None, act=_capi.FAM_ACT_NONE, res=None, gate=None, gate_strides=(0, 0, 1),
-              rows_per_batch=None, M=None, K=None, lda=None, ldo=None, ldr=None):
+              rows_per_batch=None, M=None, K=None, lda=None, ldo=None, ldr=None, out_f32=False):
         d = _capi.GemmDesc()
         Mv = a.shape[0] if M is None else M
         Kv = w.shape[1] if K is None else K
@@ -289,8 +286,7 @@ class FusedActionDiT:
         d.gate = gate.data_ptr() if gate is not None else None
         d.gate_bs, d.gate_rs, d.gate_ns = gate_strides
         d.rows_per_batch = rows_per_batch or max(Mv, 1)
-        d.split_k = 0
-        self._ws_need = max(self._ws_need, self.lib.fam_gemm_workspace_bytes(Mv, d.N, Kv, 0))
+        d.out_f32 = int(out_f32)
         self._descs.append(d)
         f = self.lib.fam_gemm
         lib = self.lib
@@ -318,9 +314,6 @@ class FusedActionDiT:
         d.batch, d.heads, d.sq, d.sk0, d.sk1, d.head_dim = self.B, cfg.num_heads, sq, sk, 0, Dh
         d.scale = 1.0 / math.sqrt(Dh)
         d.mask_kind = _capi.FAM_MASK_NONE
-        d.num_splits = 0
-        self._ws_need = max(self._ws_need,
-                            self.lib.fam_attention_workspace_bytes(self.B, cfg.num_heads, sq, sk, Dh, 0))
         self._descs.append(d)
         f, lib, ref = self.lib.fam_attention, self.lib, C.byref(d)
 
@@ -366,7 +359,7 @@ class FusedActionDiT:
         x, qkv, attn, qc, hid = self.x, self.qkv, self.attn, self.qc, self.hid
         qkvp = qkv.data_ptr()
         for t in range(T):
-            plan.add(f"s{t}.encoder", _checked(lib, "fam_linear_smallk", lat.data_ptr(), cfg.action_dim,
+            plan.add(f"s{t}.encoder", _checked(lib, "fam_linear_smallk", lat.data_ptr(), cfg.action_dim, 1,
                                                w["enc_w"].data_ptr(), w["enc_b"].data_ptr(), x.data_ptr(), H,
                                                M, H, cfg.action_dim), "linear_smallk",
                      2 * (M * cfg.action_dim + H * cfg.action_dim + H + M * H))
@@ -405,7 +398,7 @@ class FusedActionDiT:
             else:
                 # head GEMM with the Euler update as its epilogue: latents += delta_t * (x W^T + b)
                 self._gemm(f"s{t}.head_euler", x, w["head_w"], w["head_b"], lat, res=lat,
-                           gate=self.deltas[t:t + 1], gate_strides=(0, 0, 0))
+                           gate=self.deltas[t:t + 1], gate_strides=(0, 0, 0), out_f32=True)
         return plan
 
     # ------------------------------------------------------------------ execution
@@ -450,7 +443,8 @@ class FusedActionDiT:
         return self.head_out.view(self.B, self.S, self.cfg.action_dim).clone()
 
     def infer(self, noise: torch.Tensor, context: torch.Tensor) -> torch.Tensor:
-        """One policy call: returns the denoised chunk [B, S, action_dim] (bf16, a copy)."""
+        """One policy call: returns the denoised chunk [B, S, action_dim] (fp32, a copy; the
+        reference returns its bf16 chunk converted to fp32, FB/fastwam.py:1071-1073)."""
         self.set_inputs(noise, context)
         self.run()
         return self.latents.clone()

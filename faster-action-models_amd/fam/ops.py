@@ -65,30 +65,6 @@ def _rows(x: torch.Tensor) -> Tuple[torch.Tensor, int, int, int]:
     return x2, B * S, S, D
 
 
-# --------------------------------------------------------------------------- workspaces
-class Workspace:
-    """Per-(device, stream) scratch for split-K / split-KV partials and tile counters.
-
-    The counter area must be zero before first use; kernels leave it zero, so the buffer is
-    zero-filled once when it is allocated (a fill kernel, never a memset node)."""
-
-    _pool: Dict[Tuple[int, int], torch.Tensor] = {}
-
-    @classmethod
-    def get(cls, device: torch.device, nbytes: int) -> torch.Tensor:
-        if nbytes <= 0:
-            return None
-        key = (device.index if device.index is not None else torch.cuda.current_device(),
-               torch.cuda.current_stream(device).cuda_stream)
-        buf = cls._pool.get(key)
-        if buf is None or buf.numel() < nbytes:
-            size = max(nbytes, 1 << 20)
-            buf = torch.empty(size, dtype=torch.uint8, device=device)
-            buf.zero_()
-            cls._pool[key] = buf
-        return buf
-
-
 # --------------------------------------------------------------------------- norms
 def _broadcast_mod(t: torch.Tensor, x: torch.Tensor, name: str) -> Tuple[torch.Tensor, int, int]:
     """Broadcast shift/scale to x's shape; returns (tensor, batch stride, row stride)."""
@@ -120,15 +96,16 @@ def _adaln_launch(x: torch.Tensor, shift, scale, weight, bias, eps: float) -> to
             sh = torch.broadcast_to(shift, x.shape).contiguous()
             bs, rs = (sh.stride(0), sh.stride(1)) if x.dim() == 3 else (0, sh.stride(0))
         sh_p, sc_p = sh.data_ptr(), sc.data_ptr()
-        keep = (sh, sc)  # noqa: F841  (kept alive across the launch)
-    w_p = b_p = None
+    # every temporary whose pointer is passed stays referenced until the launch is enqueued
+    wc = bc = None
     if weight is not None:
         _check(weight, "ln weight")
-        w_p = weight.contiguous().data_ptr()
+        wc = weight.contiguous()
     if bias is not None:
         _check(bias, "ln bias")
-        b_p = bias.contiguous().data_ptr()
-    call("fam_adaln", x2.data_ptr(), x2.stride(0), sh_p, sc_p, bs, rs, w_p, b_p,
+        bc = bias.contiguous()
+    call("fam_adaln", x2.data_ptr(), x2.stride(0), sh_p, sc_p, bs, rs,
+         wc.data_ptr() if wc is not None else None, bc.data_ptr() if bc is not None else None,
          y.data_ptr(), D, rows, rpb, D, float(eps), _stream(x))
     return y.reshape(x.shape)
 
@@ -159,8 +136,9 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     _check(weight, "weight")
     x2, rows, _, D = _rows(x)
     y = torch.empty((rows, D), dtype=_BF16, device=x.device)
+    wc = weight.contiguous()
     call("fam_rmsnorm_rope", x2.data_ptr(), x2.stride(0), y.data_ptr(), D, rows, 1, D,
-         weight.contiguous().data_ptr(), float(eps), None, None, 0, 0, 0, _stream(x))
+         wc.data_ptr(), float(eps), None, None, 0, 0, 0, _stream(x))
     return y.reshape(x.shape)
 
 
@@ -226,7 +204,8 @@ def _rope_launch(x: torch.Tensor, freqs: torch.Tensor, num_heads: int, layout: s
     cos, sin, trs, tes = rope_tables(freqs, layout, x.device)
     x2, rows, _, D = _rows(x)
     y = torch.empty((rows, D), dtype=_BF16, device=x.device)
-    w_p = weight.contiguous().data_ptr() if weight is not None else None
+    wc = weight.contiguous() if weight is not None else None
+    w_p = wc.data_ptr() if wc is not None else None
     call("fam_rmsnorm_rope", x2.data_ptr(), x2.stride(0), y.data_ptr(), D, rows, S, D, w_p, float(eps),
          cos.data_ptr(), sin.data_ptr(), trs, tes, Dh, _stream(x))
     return y.reshape(x.shape)
@@ -276,7 +255,7 @@ def _mask_args(mask: Optional[torch.Tensor], B: int, H: int, Sq: int, Sk: int):
 def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
                    mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
                    k_prefix: Optional[torch.Tensor] = None, v_prefix: Optional[torch.Tensor] = None,
-                   num_splits: int = 0, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Attention on [B, S, H*Dh] tensors; keys/values are cat(k_prefix, k) when a prefix is
     given (the MoT joint attention over a cached video K/V, FB/mot.py:446-478) without
     materialising the concatenation."""
@@ -317,11 +296,6 @@ def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads:
     d.scale = (1.0 / math.sqrt(Dh)) if scale is None else float(scale)
     mp, kind, mbs, mhs, mqs, keep = _mask_args(mask, B, num_heads, Sq, Sk)
     d.mask, d.mask_kind, d.mask_bs, d.mask_hs, d.mask_qs = mp, kind, mbs, mhs, mqs
-    d.num_splits = num_splits
-    nbytes = _capi.lib().fam_attention_workspace_bytes(B, num_heads, Sq, Sk, Dh, num_splits)
-    ws = Workspace.get(q.device, nbytes)
-    if ws is not None:
-        d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
     call("fam_attention", C.byref(d), _stream(q))
     return out
 
@@ -362,7 +336,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
             if x2.data_ptr() % 16 or K % 8:
                 raise ValueError(f"linear: unsupported K={K} (needs K % 8 == 0 or K <= 64)")
         else:
-            call("fam_linear_smallk", x2.data_ptr(), x2.stride(0), w.data_ptr(),
+            call("fam_linear_smallk", x2.data_ptr(), x2.stride(0), 0, w.data_ptr(),
                  b.data_ptr() if b is not None else None, y.data_ptr(), N, M, N, K, _stream(x))
             return y.reshape(*x.shape[:-1], N)
     gemm(x2, w, b, y)
@@ -373,7 +347,7 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: to
          prologue: int = _capi.FAM_PRO_NONE, pro_w=None, pro_b=None, pro_shift=None, pro_scale=None,
          pro_mod_bs: int = 0, pro_mod_rs: int = 0, pro_eps: float = 1e-6, act: int = _capi.FAM_ACT_NONE,
          res: Optional[torch.Tensor] = None, gate: Optional[torch.Tensor] = None, gate_bs: int = 0,
-         gate_rs: int = 0, gate_ns: int = 1, rows_per_batch: Optional[int] = None, split_k: int = 0) -> None:
+         gate_rs: int = 0, gate_ns: int = 1, rows_per_batch: Optional[int] = None, out_f32: bool = False) -> None:
     """Fused GEMM on 2-D views (see fam_gemm in include/fam_hip.h): a [M, K], w [N, K], out [M, N]."""
     M, K = a.shape
     N = w.shape[0]
@@ -394,11 +368,7 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: to
     d.gate = gate.data_ptr() if gate is not None else None
     d.gate_bs, d.gate_rs, d.gate_ns = gate_bs, gate_rs, gate_ns
     d.rows_per_batch = rows_per_batch if rows_per_batch is not None else max(M, 1)
-    d.split_k = split_k
-    nbytes = _capi.lib().fam_gemm_workspace_bytes(M, N, K, split_k)
-    ws = Workspace.get(a.device, nbytes)
-    if ws is not None:
-        d.workspace, d.workspace_bytes = ws.data_ptr(), ws.numel()
+    d.out_f32 = int(out_f32)
     call("fam_gemm", C.byref(d), _stream(a))
 
 

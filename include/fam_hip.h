@@ -4,8 +4,8 @@
  *
  * Every entry point takes plain device pointers, element counts and strides, and
  * the HIP stream to launch on (a hipStream_t passed as void*; NULL = the null
- * stream).  The library never allocates: the caller owns every buffer, including
- * the optional workspace, so every entry point can be recorded into a HIP graph.
+ * stream).  The library never allocates and uses no scratch memory: the caller owns
+ * every buffer, so every entry point can be recorded into a HIP graph.
  * Tensors are bf16 unless a parameter says fp32.  Strides are in elements.
  *
  * Return value: FAM_OK, or an error code with a message readable through
@@ -31,19 +31,14 @@ extern "C" {
 #define FAM_ERR_INVALID_ARG 1
 #define FAM_ERR_UNSUPPORTED 2
 #define FAM_ERR_LAUNCH 3
-#define FAM_ERR_WORKSPACE 4
 
 #define FAM_ABI_VERSION 1
 
 /*
- * Workspaces.  The split-K GEMM and the split-key attention exchange fp32 partials through
- * a caller-owned workspace.  Its first FAM_WS_COUNTER_BYTES bytes are per-tile arrival
- * counters: they must be zero before the first use, every kernel leaves them zero again,
- * and the partials live after them, so one workspace can serve launches of any shape and
- * of both kernels, one after another on a stream.  Launches that share a workspace must not
- * run concurrently.  A split launch may use at most FAM_WS_COUNTER_BYTES / 4 tiles.
+ * No entry point allocates, keeps state between calls or communicates between
+ * workgroups: every launch is self-contained, deterministic (fixed reduction order, no
+ * float atomics) and may be recorded into a HIP graph.
  */
-#define FAM_WS_COUNTER_BYTES 65536
 
 /* Library ABI version (FAM_ABI_VERSION). */
 int fam_version(void);
@@ -108,16 +103,15 @@ int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, int64_t y_row
  * sk0..sk0+sk1-1 from (k1, v1) (sk1 = 0: one segment), e.g. a cached video prefix followed
  * by the action tokens.  The mask element for (b, h, q, key) is
  * mask[b*mask_bs + h*mask_hs + q*mask_qs + key].  A query row with every key masked gives 0.
- * num_splits > 1 splits the keys over that many workgroups per (b, h, q-tile) (0: chosen
- * by the library) and combines the partial results in a fixed order (deterministic).  A
- * split launch needs a workspace (see FAM_WS_COUNTER_BYTES) of
- * fam_attention_workspace_bytes() bytes (0 when no split is used).
+ * Work split: for Sq <= 64 one workgroup per (b, h) holds all queries and its waves split
+ * the keys (partial softmax states merged in LDS in a fixed order); for longer Sq each
+ * workgroup owns 64 queries of one (b, h).
  * Replaces: flash_attention(q, k, v, num_heads, ctx_mask)  FB/wan_video_dit.py:17-26,
  *           FG/wan_video_dit.py:18-39, CA/wan_video_dit.py:569-587;
  *           fastwam::short_attn / short_attn_bsd          FG/wan_video_dit.py:1680-1721, FG/mot.py:682-722;
  *           joint [video cache; action] attention          FB/mot.py:446-478.
  * Limits: head_dim in {8, 16, 32, 64, 128}; all strides multiples of 8; 16-byte aligned
- * bases; batch*heads <= 65535.
+ * bases; batch*heads <= 65535 when Sq > 64.
  */
 typedef struct fam_attn_desc {
   const void* q;  int64_t q_bs, q_rs, q_hs;
@@ -129,13 +123,9 @@ typedef struct fam_attn_desc {
   int64_t batch, heads, sq, sk0, sk1, head_dim;
   float scale;
   const void* mask; int mask_kind; int64_t mask_bs, mask_hs, mask_qs;
-  int num_splits;
-  void* workspace; int64_t workspace_bytes;
 } fam_attn_desc;
 
 int fam_attention(const fam_attn_desc* d, void* stream);
-int64_t fam_attention_workspace_bytes(int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t head_dim,
-                                      int num_splits);
 
 /* GEMM prologues (applied to each row of A before the product) and activations. */
 #define FAM_PRO_NONE 0
@@ -151,18 +141,16 @@ int64_t fam_attention_workspace_bytes(int64_t batch, int64_t heads, int64_t sq, 
  * out = res[m, n] + g(m, n) * value with g = 1 when gate == NULL, else
  * g = gate[(m / rows_per_batch) * gate_bs + (m % rows_per_batch) * gate_rs + n * gate_ns]
  * (gate_ns = 0 with gate_bs = gate_rs = 0 makes it one scalar, e.g. the Euler delta).
- * res may equal out (in-place residual update).  AdaLN shift/scale use the same
+ * res may equal out (in-place residual update).  out_f32 != 0 makes out and res fp32
+ * (e.g. the fused Euler update of fp32 latents); otherwise both are bf16.  AdaLN shift/scale use the same
  * (rows_per_batch, pro_mod_bs, pro_mod_rs) indexing with a unit column stride.
- * split_k > 1 splits the K range over that many workgroups (split_k = 0: chosen by the
- * library from M, N, K); the last workgroup to finish a tile reduces the fp32 partials in
- * split order (deterministic) and runs the epilogue.  A split launch needs a workspace (see
- * FAM_WS_COUNTER_BYTES) of fam_gemm_workspace_bytes(M, N, K, split_k) bytes (0 when no split
- * is used).
+ * Work split: for M <= 64 a workgroup of 8 waves owns 16 output columns and the waves split
+ * K (reduced through LDS in wave order); for larger M, 64x64 or 128x128 output tiles.
  * Replaces: nn.Linear / F.linear on the hot path (FB/wan_video_dit.py:188-191,215-218,262-263,
  *           FB/action_dit.py:76-97,317-318), fastwam::skmm + skpost (split-K GEMM with
  *           bias/gate/residual/norm epilogue, FG/mot.py:1080-1348), geak_head::mmx with the
  *           fused Euler epilogue (DG/modules/action_model/ActionDiT.py:1260-1272).
- * Limits: K % 8 == 0; a, w rows 16-byte aligned (lda, ldw multiples of 8); 1 <= split_k <= 64.
+ * Limits: K % 8 == 0; a, w rows 16-byte aligned (lda, ldw multiples of 8); N <= 1048560.
  */
 typedef struct fam_gemm_desc {
   const void* a; int64_t lda;
@@ -179,19 +167,17 @@ typedef struct fam_gemm_desc {
   const void* res; int64_t ldr;
   const void* gate; int64_t gate_bs, gate_rs, gate_ns;
   int64_t rows_per_batch;
-  int split_k;
-  void* workspace; int64_t workspace_bytes;
+  int out_f32;
 } fam_gemm_desc;
 
 int fam_gemm(const fam_gemm_desc* d, void* stream);
-int64_t fam_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int split_k);
 
 /*
  * fam_linear_smallk -- y[m, n] = sum_k x[m, k] w[n, k] + b[n] for small, unaligned K
- * (the 7-wide action encoder, FB/action_dit.py:76, :285).  fp32 accumulation.
- * Limits: K <= 64.
+ * (the 7-wide action encoder, FB/action_dit.py:76, :285).  x is bf16, or fp32 when
+ * x_f32 != 0; w, b and y are bf16; fp32 accumulation.  Limits: K <= 64.
  */
-int fam_linear_smallk(const void* x, int64_t ldx, const void* w, const void* b,
+int fam_linear_smallk(const void* x, int64_t ldx, int x_f32, const void* w, const void* b,
                       void* y, int64_t ldy, int64_t M, int64_t N, int64_t K, void* stream);
 
 /*

@@ -30,7 +30,7 @@ def lib():
 
 def test_exports_every_header_symbol(lib):
     names = _header_functions()
-    assert len(names) >= 12
+    assert len(names) >= 10
     for n in names:
         assert hasattr(lib, n), f"{n} declared in fam_hip.h but not exported"
     assert sorted(_capi.SIGNATURES) == names, "ctypes signatures must cover exactly the header's functions"
@@ -88,10 +88,9 @@ def test_validation_rejects_before_launch(lib):
     d.prologue = 2  # AdaLN without shift/scale
     assert lib.fam_gemm(C.byref(d), None) == _capi.FAM_ERR_INVALID_ARG
     d.prologue = 0
-    d.split_k, d.K, d.lda, d.ldw = 4, 1024, 1024, 1024  # split without workspace
-    assert lib.fam_gemm(C.byref(d), None) == _capi.FAM_ERR_WORKSPACE
-    assert "workspace" in _err(lib)
-    d.split_k = 65
+    d.ldo = 32  # ldo < N
+    assert lib.fam_gemm(C.byref(d), None) == _capi.FAM_ERR_INVALID_ARG
+    d.ldo, d.gate = 64, 80  # a gate without a residual
     assert lib.fam_gemm(C.byref(d), None) == _capi.FAM_ERR_INVALID_ARG
 
     a = _capi.AttnDesc()
@@ -100,26 +99,15 @@ def test_validation_rejects_before_launch(lib):
     assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_UNSUPPORTED
     a.head_dim, a.q_rs = 64, 12
     assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_INVALID_ARG
-    a.q_rs, a.sk0, a.num_splits = 128, 1560, 8
-    assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_WORKSPACE
-    a.num_splits, a.mask_kind = 0, 1
+    a.q_rs, a.mask_kind = 128, 1  # a mask kind without a mask
+    assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_INVALID_ARG
+    a.mask_kind = 7
     assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_INVALID_ARG
 
-    assert lib.fam_linear_smallk(16, 7, 32, None, 48, 64, 4, 64, 65, None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_linear_smallk(16, 7, 0, 32, None, 48, 64, 4, 64, 65, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_euler_step(16, 32, None, 48, 10, 10, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_sinusoid(16, 32, 4, 7, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_add_modulation(16, 32, 48, 2, 3, 12, None) == _capi.FAM_ERR_INVALID_ARG
-
-
-def test_workspace_sizes(lib):
-    # no split -> no workspace; split sizes grow with the split count
-    assert lib.fam_gemm_workspace_bytes(2048, 4096, 1024, 1) == 0
-    w8 = lib.fam_gemm_workspace_bytes(32, 1024, 4096, 8)
-    w16 = lib.fam_gemm_workspace_bytes(32, 1024, 4096, 16)
-    assert 0 < w8 < w16
-    assert lib.fam_gemm_workspace_bytes(32, 3072, 1024, 0) > 0          # auto split at M=32
-    assert lib.fam_attention_workspace_bytes(1, 16, 32, 32, 64, 0) == 0  # short keys: no split
-    assert lib.fam_attention_workspace_bytes(1, 16, 32, 1560, 64, 0) > 0
 
 
 def test_missing_library_fails_loudly(tmp_path):
