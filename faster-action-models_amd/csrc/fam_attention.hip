@@ -39,33 +39,59 @@ struct AttnArgs {
   int64_t H, Sq, sk0, Sk;
   float scale_log2;
   const void* mask; int mask_kind; int64_t mbs, mhs, mqs;
+  int splits; float* part_o; float* part_ml;   // key splits over workgroups (grid.y)
 };
 
-__device__ __forceinline__ const bf16* key_ptr(const AttnArgs& a, int64_t b, int64_t h, int64_t kk) {
-  return kk < a.sk0 ? a.k0 + b * a.k0_bs + kk * a.k0_rs + h * a.k0_hs
-                    : a.k1 + b * a.k1_bs + (kk - a.sk0) * a.k1_rs + h * a.k1_hs;
+// Row addressing of the two key/value segments of one (batch, head), held in registers:
+// key kk < sk0 lives in segment 0, the others in segment 1.  Computing both candidate
+// addresses and selecting per lane keeps the loads branch-free.
+struct SegRows {
+  const bf16* base0; int64_t rs0;
+  const bf16* base1; int64_t rs1;
+  int64_t sk0;
+  __device__ __forceinline__ const bf16* row(int64_t kk) const {
+    const bf16* p0 = base0 + kk * rs0;
+    const bf16* p1 = base1 + (kk - sk0) * rs1;
+    return kk < sk0 ? p0 : p1;
+  }
+};
+
+__device__ __forceinline__ SegRows key_rows(const AttnArgs& a, int64_t b, int64_t h) {
+  SegRows r;
+  r.base0 = a.k0 + b * a.k0_bs + h * a.k0_hs; r.rs0 = a.k0_rs;
+  r.base1 = a.k1 + b * a.k1_bs + h * a.k1_hs; r.rs1 = a.k1_rs;
+  r.sk0 = a.sk0;
+  if (a.sk0 == 0) { r.base0 = r.base1; r.rs0 = r.rs1; }   // segment 0 empty: keep both valid
+  if (a.Sk == a.sk0) { r.base1 = r.base0; r.rs1 = r.rs0; } // segment 1 empty
+  return r;
 }
-__device__ __forceinline__ const bf16* val_ptr(const AttnArgs& a, int64_t b, int64_t h, int64_t kk) {
-  return kk < a.sk0 ? a.v0 + b * a.v0_bs + kk * a.v0_rs + h * a.v0_hs
-                    : a.v1 + b * a.v1_bs + (kk - a.sk0) * a.v1_rs + h * a.v1_hs;
+__device__ __forceinline__ SegRows val_rows(const AttnArgs& a, int64_t b, int64_t h) {
+  SegRows r;
+  r.base0 = a.v0 + b * a.v0_bs + h * a.v0_hs; r.rs0 = a.v0_rs;
+  r.base1 = a.v1 + b * a.v1_bs + h * a.v1_hs; r.rs1 = a.v1_rs;
+  r.sk0 = a.sk0;
+  if (a.sk0 == 0) { r.base0 = r.base1; r.rs0 = r.rs1; }
+  if (a.Sk == a.sk0) { r.base1 = r.base0; r.rs1 = r.rs0; }
+  return r;
 }
 
-// scaled (log2 domain) and masked score of query qi and key kk
+// scaled (log2 domain) and masked score of query qi and key kk; branch-free per lane (the
+// mask kind is uniform): out-of-range queries/keys read a clamped mask element
 __device__ __forceinline__ float score(const AttnArgs& a, float raw, int64_t b, int64_t h, int64_t qi, bool qvalid,
                                        int64_t kk) {
-  if (kk >= a.Sk) return -INFINITY;
+  const bool kvalid = kk < a.Sk;
   float v = raw * a.scale_log2;
-  if (a.mask_kind != FAM_MASK_NONE && qvalid) {
-    const int64_t mi = b * a.mbs + h * a.mhs + qi * a.mqs + kk;
+  if (a.mask_kind != FAM_MASK_NONE) {
+    const int64_t mi = b * a.mbs + h * a.mhs + (qvalid ? qi : 0) * a.mqs + (kvalid ? kk : 0);
     if (a.mask_kind == FAM_MASK_BOOL) {
-      if (!reinterpret_cast<const uint8_t*>(a.mask)[mi]) v = -INFINITY;
+      v = reinterpret_cast<const uint8_t*>(a.mask)[mi] ? v : -INFINITY;
     } else if (a.mask_kind == FAM_MASK_ADD_F32) {
       v += reinterpret_cast<const float*>(a.mask)[mi] * kLog2e;
     } else {
       v += to_f(reinterpret_cast<const bf16*>(a.mask)[mi]) * kLog2e;
     }
   }
-  return v;
+  return kvalid ? v : -INFINITY;
 }
 
 // Online-softmax update of one query column with the 8 scores of a 32-key block; returns
@@ -116,18 +142,23 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
   const int64_t bh = blockIdx.x, b = bh / a.H, h = bh - b * a.H;
-  const int64_t nkb = (a.Sk + KB - 1) / KB;
-  const int64_t per = (nkb + NW - 1) / NW;
-  const int64_t kb_beg = std::min(nkb, (int64_t)wave * per), kb_end = std::min(nkb, kb_beg + per);
+  // this workgroup's key blocks (split blockIdx.y of a.splits), divided among its waves
+  const int64_t nkb_all = (a.Sk + KB - 1) / KB;
+  const int64_t per_split = (nkb_all + a.splits - 1) / a.splits;
+  const int64_t wg_beg = std::min(nkb_all, (int64_t)blockIdx.y * per_split);
+  const int64_t wg_end = std::min(nkb_all, wg_beg + per_split);
+  const int64_t per = (wg_end - wg_beg + NW - 1) / NW;
+  const int64_t kb_beg = std::min(wg_end, wg_beg + (int64_t)wave * per), kb_end = std::min(wg_end, kb_beg + per);
 
   bf16x8 qf[QT][NC];
+  const bf16* qbase = a.q + b * a.q_bs + h * a.q_hs;
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
       const int64_t qi = qt * 16 + l16;
       const int d0 = c * 32 + lg * 8;
-      qf[qt][c] = (qi < a.Sq && d0 < DH) ? load8(a.q + b * a.q_bs + qi * a.q_rs + h * a.q_hs + d0) : zero8();
+      qf[qt][c] = load8_if(qi < a.Sq && d0 < DH, qbase + qi * a.q_rs + d0, qbase);
     }
 
   f32x4 oacc[QT][NDT];
@@ -142,6 +173,10 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
 
   // K fragments (A-operand rows = keys) and V chunks of one block, straight from global
   bf16x8 kf[2][NC], vc[NVC];
+  const SegRows krows = key_rows(a, b, h), vrows = val_rows(a, b, h);
+  const int64_t Sk = a.Sk;
+  const bf16* ksafe = krows.row(0);
+  const bf16* vsafe = vrows.row(0);
   auto gload = [&](int64_t blk) {
     const int64_t kb = blk * KB;
 #pragma unroll
@@ -150,18 +185,21 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
       for (int c = 0; c < NC; ++c) {
         const int64_t kk = kb + kt * 16 + l16;
         const int d0 = c * 32 + lg * 8;
-        kf[kt][c] = (kk < a.Sk && d0 < DH) ? load8(key_ptr(a, b, h, kk) + d0) : zero8();
+        const bool ok = kk < Sk && d0 < DH;
+        kf[kt][c] = load8_if(ok, krows.row(ok ? kk : 0) + (ok ? d0 : 0), ksafe);
       }
 #pragma unroll
     for (int p = 0; p < NVC; ++p) {
       const int cidx = lane + 64 * p;
       const int key = cidx / (DH / 8), d0 = (cidx % (DH / 8)) * 8;
       const int64_t kk = kb + key;
-      vc[p] = (cidx < KB * DH / 8 && kk < a.Sk) ? load8(val_ptr(a, b, h, kk) + d0) : zero8();
+      const bool ok = cidx < KB * DH / 8 && kk < Sk;
+      vc[p] = load8_if(ok, vrows.row(ok ? kk : 0) + (ok ? d0 : 0), vsafe);
     }
   };
 
   if (kb_beg < kb_end) gload(kb_beg);
+  __builtin_amdgcn_sched_barrier(0);
   for (int64_t blk = kb_beg; blk < kb_end; ++blk) {
     const int64_t kb = blk * KB;
     // V block -> this wave's transposed tile (LDS operations of one wave complete in order)
@@ -180,7 +218,7 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
 #pragma unroll
       for (int c = 0; c < NC; ++c) kcur[kt][c] = kf[kt][c];
     if (blk + 1 < kb_end) gload(blk + 1);  // next block in flight during this one's math
-    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_sched_barrier(0);     // ... issued here, not sunk to its first use
 
     bf16x8 vfr[NDT];
 #pragma unroll
@@ -256,13 +294,46 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
 #pragma unroll
       for (int w = 0; w < NW; ++w) L += s_l[w][q] * exp2f(s_m[w][q] - mx);
     }
-    const float inv = L > 0.f ? 1.0f / L : 0.f;
     const f32x4 v = *reinterpret_cast<const f32x4*>(&s_o[q][d0]);
+    if (a.splits > 1) {
+      // unnormalised partial of this split, merged by fam_attention_combine
+      const int64_t row = ((int64_t)blockIdx.y * gridDim.x + bh) * a.Sq + q;
+      *reinterpret_cast<f32x4*>(a.part_o + row * DH + d0) = v;
+      if (d0 == 0) { a.part_ml[row * 2] = mx; a.part_ml[row * 2 + 1] = L; }
+      continue;
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
     bf16x4 ov;
 #pragma unroll
     for (int e = 0; e < 4; ++e) ov[e] = to_bf(v[e] * inv);
     *reinterpret_cast<bf16x4*>(a.o + b * a.o_bs + q * a.o_rs + h * a.o_hs + d0) = ov;
   }
+}
+
+// Merge of the key-split partials: one thread per (b*h, q, 4 channels), splits in order.
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int64_t DH, int64_t BH) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t nd4 = DH / 4;
+  if (idx >= BH * a.Sq * nd4) return;
+  const int64_t d0 = (idx % nd4) * 4, rq = idx / nd4;   // rq = bh * Sq + q
+  const int64_t q = rq % a.Sq, bh = rq / a.Sq, b = bh / a.H, h = bh - b * a.H;
+  float mx = -INFINITY;
+  for (int z = 0; z < a.splits; ++z) mx = fmaxf(mx, a.part_ml[((int64_t)z * BH * a.Sq + rq) * 2]);
+  f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+  float L = 0.f;
+  if (mx != -INFINITY) {
+    for (int z = 0; z < a.splits; ++z) {
+      const int64_t row = (int64_t)z * BH * a.Sq + rq;
+      const float w = exp2f(a.part_ml[row * 2] - mx);  // an empty split has m = -inf -> 0
+      L += a.part_ml[row * 2 + 1] * w;
+      o += *reinterpret_cast<const f32x4*>(a.part_o + row * DH + d0) * w;
+    }
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  bf16x4 ov;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) ov[e] = to_bf(o[e] * inv);
+  *reinterpret_cast<bf16x4*>(a.o + b * a.o_bs + q * a.o_rs + h * a.o_hs + d0) = ov;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -283,11 +354,15 @@ __global__ __launch_bounds__(256) void attn_tiled_kernel(AttnArgs a) {
   const bool qvalid = qi < a.Sq;
 
   bf16x8 qf[NC];
+  const bf16* qbase = a.q + b * a.q_bs + h * a.q_hs;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int d0 = c * 32 + lg * 8;
-    qf[c] = (qvalid && d0 < DH) ? load8(a.q + b * a.q_bs + qi * a.q_rs + h * a.q_hs + d0) : zero8();
+    qf[c] = load8_if(qvalid && d0 < DH, qbase + qi * a.q_rs + d0, qbase);
   }
+  const SegRows krows = key_rows(a, b, h), vrows = val_rows(a, b, h);
+  const bf16* ksafe = krows.row(0);
+  const bf16* vsafe = vrows.row(0);
   f32x4 oacc[NDT];
 #pragma unroll
   for (int t = 0; t < NDT; ++t) oacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -297,11 +372,9 @@ __global__ __launch_bounds__(256) void attn_tiled_kernel(AttnArgs a) {
     for (int c = tid; c < KB * (DH / 8); c += NW * 64) {
       const int key = c / (DH / 8), d0 = (c % (DH / 8)) * 8;
       const int64_t kk = kb + key;
-      bf16x8 kv = zero8(), vv = zero8();
-      if (kk < a.Sk) {
-        kv = load8(key_ptr(a, b, h, kk) + d0);
-        vv = load8(val_ptr(a, b, h, kk) + d0);
-      }
+      const bool ok = kk < a.Sk;
+      const bf16x8 kv = load8_if(ok, krows.row(ok ? kk : 0) + d0, ksafe);
+      const bf16x8 vv = load8_if(ok, vrows.row(ok ? kk : 0) + d0, vsafe);
       *reinterpret_cast<bf16x8*>(&Ks[key][d0]) = kv;
 #pragma unroll
       for (int e = 0; e < 8; ++e) Vt[d0 + e][key] = vv[e];
@@ -369,8 +442,8 @@ template <int DH>
 static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
   // (Dh = 128 with more than 32 queries would not fit the short kernel's registers)
   if (a.Sq <= 32 || (a.Sq <= 64 && DH < 128)) {
-    const int64_t nkb = (a.Sk + KB - 1) / KB;
-    const dim3 grid((unsigned)bh);
+    const int64_t nkb = ((a.Sk + KB - 1) / KB + a.splits - 1) / a.splits;  // key blocks per workgroup
+    const dim3 grid((unsigned)bh, (unsigned)a.splits);
     if (a.Sq <= 16) launch_short_q<DH, 1>(a, nkb, grid, s);
     else if (a.Sq <= 32) launch_short_q<DH, 2>(a, nkb, grid, s);
     else launch_short_q<DH, 4>(a, nkb, grid, s);
@@ -406,6 +479,10 @@ extern "C" int fam_attention(const fam_attn_desc* d, void* stream) {
   FAM_REQUIRE(d->mask_kind == FAM_MASK_NONE || d->mask, FAM_ERR_INVALID_ARG, "fam_attention: mask kind without mask");
   const int64_t bh = d->batch * d->heads;
   FAM_REQUIRE(bh <= 65535 || d->sq <= 64, FAM_ERR_UNSUPPORTED, "fam_attention: batch*heads must be <= 65535");
+  FAM_REQUIRE(d->num_splits >= 0 && d->num_splits <= 64, FAM_ERR_INVALID_ARG, "fam_attention: num_splits in [0, 64]");
+  const bool short_q = d->sq <= 32 || (d->sq <= 64 && Dh < 128);
+  FAM_REQUIRE(d->num_splits <= 1 || (short_q && d->part_o && d->part_ml && fam_host::aligned16(d->part_o)),
+              FAM_ERR_INVALID_ARG, "fam_attention: key splits need Sq <= 32 (<= 64 for Dh < 128) and 16-byte aligned partial buffers");
   if (d->batch == 0 || d->sq == 0) return FAM_OK;
 
   AttnArgs a{};
@@ -418,6 +495,8 @@ extern "C" int fam_attention(const fam_attn_desc* d, void* stream) {
   a.H = d->heads; a.Sq = d->sq; a.sk0 = d->sk0; a.Sk = d->sk0 + d->sk1;
   a.scale_log2 = d->scale * kLog2e;
   a.mask = d->mask; a.mask_kind = d->mask_kind; a.mbs = d->mask_bs; a.mhs = d->mask_hs; a.mqs = d->mask_qs;
+  a.splits = d->num_splits > 1 ? d->num_splits : 1;
+  a.part_o = d->part_o; a.part_ml = d->part_ml;
   hipStream_t s = (hipStream_t)stream;
   switch (Dh) {
     case 8: launch_dh<8>(a, bh, s); break;
@@ -427,4 +506,23 @@ extern "C" int fam_attention(const fam_attn_desc* d, void* stream) {
     default: launch_dh<128>(a, bh, s); break;
   }
   return fam_host::check_launch("fam_attention");
+}
+
+extern "C" int fam_attention_combine(const fam_attn_desc* d, void* stream) {
+  FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_attention_combine: null descriptor");
+  FAM_REQUIRE(d->num_splits >= 2 && d->part_o && d->part_ml && d->o, FAM_ERR_INVALID_ARG,
+              "fam_attention_combine: needs num_splits >= 2, the partial buffers and o");
+  FAM_REQUIRE(d->head_dim % 4 == 0 && d->head_dim >= 8 && d->o_bs % 8 == 0 && d->o_rs % 8 == 0 && d->o_hs % 8 == 0 &&
+                  fam_host::aligned16(d->o) && fam_host::aligned16(d->part_o),
+              FAM_ERR_INVALID_ARG, "fam_attention_combine: bad head_dim, strides or alignment");
+  const int64_t bh = d->batch * d->heads;
+  if (bh == 0 || d->sq == 0) return FAM_OK;
+  AttnArgs a{};
+  a.o = (bf16*)d->o; a.o_bs = d->o_bs; a.o_rs = d->o_rs; a.o_hs = d->o_hs;
+  a.H = d->heads; a.Sq = d->sq;
+  a.splits = d->num_splits; a.part_o = d->part_o; a.part_ml = d->part_ml;
+  const int64_t n = bh * d->sq * (d->head_dim / 4);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a,
+                     d->head_dim, bh);
+  return fam_host::check_launch("fam_attention_combine");
 }

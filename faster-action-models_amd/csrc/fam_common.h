@@ -60,6 +60,15 @@ __device__ __forceinline__ bf16x8 zero8() {
   return z;
 }
 
+// Branch-free guarded 16-byte load: a lane whose element is out of range reads `safe` (any
+// valid address of the same tensor) and gets zeros.  Keeping the load unconditional lets
+// the compiler batch it with its neighbours instead of wrapping each one in an exec-masked
+// branch.
+__device__ __forceinline__ bf16x8 load8_if(bool ok, const bf16* p, const bf16* safe) {
+  const bf16x8 v = load8(ok ? p : safe);
+  return ok ? v : zero8();
+}
+
 __device__ __forceinline__ float gelu_tanh(float x) {
   // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
   const float k0 = 0.7978845608028654f;

@@ -19,6 +19,15 @@
 //     the epilogue runs one output element per thread.
 //   Bytes per launch (HBM roofline numerator): 2*(N*K + M*K + M*N) + bias/residual/modulation.
 //
+// partial_kernel (M <= 64, used by the fused action expert): split-K without any
+// cross-workgroup traffic.  A workgroup of 4 waves owns 64 output columns (16 per wave) over
+// one K slice; the activation slice [M x Kc] is staged once in LDS and shared by the 4
+// waves, so each workgroup reads 64*Kc weights and only M*Kc activations.  K is split so
+// that ~256-384 workgroups stream the weights (on gfx950 the per-CU memory parallelism, not
+// HBM, limits a skinny product spread over few CUs).  The fp32 partials partial[z][m][n]
+// are summed, in split order, by the row kernel that follows (fam_rowop), which also runs
+// the epilogue and the next normalisation on whole rows.
+//
 // tiled_kernel (M > 64: the per-call context projections, batched throughput points):
 //   * 256-thread workgroup, BM x BN output tile (64x64 or 128x128), 2x2 waves of 16x16 MFMA
 //     tiles, K in steps of 64 through double-buffered LDS, next step's global loads issued
@@ -129,11 +138,14 @@ __device__ __forceinline__ void row_stats(const GemmArgs& g, int64_t m0, int row
 }
 
 // ---------------------------------------------------------------------------------------
-// skinny_kernel: M <= 16*MT rows, 16 output columns per workgroup, NW waves split K,
-// KS k-steps of weights in flight per wave.
+// skinny_kernel: M <= 16*MT rows, 16 output columns per workgroup, NW waves split K into
+// contiguous runs of 32-wide k-steps; each wave holds KS k-steps of weights and activations
+// in registers at once.  Every load is branch-free (out-of-range lanes load a valid address
+// and are zeroed), so the loads of a chunk are issued back to back.
 template <int MT, int NW, int KS, int PRO>
 __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
   constexpr int MR = MT * 16;
+  constexpr int TPR = NW * 64 / MR;  // threads per row in the statistics pass
   __shared__ float s_mean[MR], s_rstd[MR];
   __shared__ float s_red[NW][MR][16];
 
@@ -143,45 +155,79 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
   const int64_t nsub = (g.K + 31) / 32;       // 32-wide k-steps
   const int64_t per = (nsub + NW - 1) / NW;   // k-steps per wave
   const int64_t s_beg = std::min(nsub, (int64_t)wave * per), s_end = std::min(nsub, s_beg + per);
-  const int64_t nrow = n0 + l16;
-  const bf16* wrow = g.w + nrow * g.ldw;
+  const bool nok = n0 + l16 < g.N;
+  const bf16* wrow = g.w + (nok ? n0 + l16 : 0) * g.ldw;
 
   f32x4 acc[MT];
 #pragma unroll
   for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  bf16x8 wf[KS];
-  auto wload = [&](int64_t sb) {
+  bf16x8 wf[KS], af[KS][MT];
+  auto chunk_load = [&](int64_t sb) {
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
       const int64_t k = (sb + j) * 32 + lg * 8;
-      wf[j] = (sb + j < s_end && nrow < g.N && k < g.K) ? load8(wrow + k) : zero8();
+      const bool kok = (sb + j < s_end) && k < g.K;
+      wf[j] = load8_if(kok && nok, wrow + k, g.w);
+#pragma unroll
+      for (int i = 0; i < MT; ++i) {
+        const int64_t m = i * 16 + l16;
+        af[j][i] = load8_if(kok && m < g.M, g.a + m * g.lda + k, g.a);
+      }
     }
   };
-  wload(s_beg);  // the weight stream starts before the prologue statistics
+  chunk_load(s_beg);  // weights and activations of the first chunk in flight at once
+  // keep the scheduler from sinking those loads next to their first use (it would, to save
+  // registers, and each k-step would then pay a full memory round trip)
+  __builtin_amdgcn_sched_barrier(0);
 
   if constexpr (PRO != FAM_PRO_NONE) {
-    row_stats(g, 0, MR, wave, NW, lane, s_mean, s_rstd);
+    // one pass over each row: sums about the row's first element (a shared pivot keeps the
+    // difference of large sums well conditioned), reduced over the TPR lanes of the row
+    const int r = tid / TPR, t = tid % TPR;
+    const bool rok = r < g.M;
+    const bf16* ar = g.a + (rok ? r : 0) * g.lda;
+    const float pivot = to_f(ar[0]);
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll 8
+    for (int64_t c = (int64_t)t * 8; c < g.K; c += TPR * 8) {
+      const bf16x8 v = load8(ar + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { const float d = to_f(v[e]) - pivot; s1 += d; s2 += d * d; }
+    }
+#pragma unroll
+    for (int o = TPR / 2; o >= 1; o >>= 1) {
+      s1 += __shfl_xor(s1, o, kWave);
+      s2 += __shfl_xor(s2, o, kWave);
+    }
+    if (t == 0) {
+      const float invk = 1.0f / (float)g.K;
+      const float dm = s1 * invk;
+      const float var = fmaxf(s2 * invk - dm * dm, 0.f);
+      s_mean[r] = rok ? pivot + dm : 0.f;
+      s_rstd[r] = rok ? rsqrtf(var + g.eps) : 0.f;
+    }
     __syncthreads();
   }
 
   for (int64_t sb = s_beg; sb < s_end; sb += KS) {
-    if (sb != s_beg) wload(sb);
+    if (sb != s_beg) {
+      chunk_load(sb);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
-      const int64_t s = sb + j;
-      if (s < s_end) {
-        const int64_t k = s * 32 + lg * 8;
 #pragma unroll
-        for (int i = 0; i < MT; ++i) {
+      for (int i = 0; i < MT; ++i) {
+        bf16x8 a = af[j][i];
+        if constexpr (PRO != FAM_PRO_NONE) {
+          // rows past M normalise to finite values that only reach their own (unstored)
+          // outputs; k past K meets zero weights
           const int64_t m = i * 16 + l16;
-          bf16x8 af = zero8();
-          if (m < g.M && k < g.K) {
-            af = load8(g.a + m * g.lda + k);
-            if constexpr (PRO != FAM_PRO_NONE) af = prologue8<PRO>(g, af, m, k, s_mean[m], s_rstd[m]);
-          }
-          acc[i] = mfma16(wf[j], af, acc[i]);
+          const int64_t k = std::min((sb + j) * 32 + lg * 8, g.K - 8);
+          a = prologue8<PRO>(g, a, std::min(m, g.M - 1), k, s_mean[m], s_rstd[m]);
         }
+        acc[i] = mfma16(wf[j], a, acc[i]);
       }
     }
   }
@@ -198,6 +244,79 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
 #pragma unroll
     for (int w = 0; w < NW; ++w) v += s_red[w][mr][nc];
     epilogue_store(g, mr, n, v);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// partial_kernel: MT m-tiles (M <= 16*MT), STEPS 32-wide k-steps per split (Kc = 32*STEPS).
+struct PartArgs {
+  const bf16* a; int64_t lda;
+  const bf16* w; int64_t ldw;
+  float* part;               // [splits][M][N]
+  int64_t M, N, K;
+};
+
+template <int MT, int STEPS>
+__global__ __launch_bounds__(256) void partial_kernel(PartArgs g) {
+  constexpr int MR = MT * 16;
+  constexpr int KC = 32 * STEPS;
+  constexpr int CH = MR * KC / 8;              // 16-byte activation chunks per workgroup
+  constexpr int CPT = (CH + 255) / 256;        // chunks per thread
+  __shared__ bf16 As[MR][KC + 8];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t n = (int64_t)blockIdx.x * 64 + wave * 16 + l16;   // this lane's weight row
+  const int64_t z = blockIdx.y, kbase = z * KC;
+  const bool nok = n < g.N;
+  const bf16* wrow = g.w + (nok ? n : 0) * g.ldw;
+
+  bf16x8 wf[STEPS], ac[CPT];
+#pragma unroll
+  for (int j = 0; j < STEPS; ++j) {
+    const int64_t k = kbase + j * 32 + lg * 8;
+    wf[j] = load8_if(nok && k < g.K, wrow + k, g.w);
+  }
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    const int c = tid + 256 * p, r = c / (KC / 8), kc = (c % (KC / 8)) * 8;
+    const int64_t k = kbase + kc;
+    ac[p] = load8_if(c < CH && r < g.M && k < g.K, g.a + r * g.lda + k, g.a);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every load of the workgroup is in flight here
+#pragma unroll
+  for (int p = 0; p < CPT; ++p) {
+    const int c = tid + 256 * p;
+    if (c < CH) *reinterpret_cast<bf16x8*>(&As[c / (KC / 8)][(c % (KC / 8)) * 8]) = ac[p];
+  }
+  __syncthreads();
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < STEPS; ++j)
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const bf16x8 af = *reinterpret_cast<const bf16x8*>(&As[i * 16 + l16][j * 32 + lg * 8]);
+      acc[i] = mfma16(wf[j], af, acc[i]);
+    }
+
+  // lane holds rows m = i*16 + l16, columns nb .. nb+3 of this split's partial
+  const int64_t nb = (int64_t)blockIdx.x * 64 + wave * 16 + lg * 4;
+  float* pz = g.part + z * g.M * g.N;
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    const int64_t m = i * 16 + l16;
+    if (m >= g.M) continue;
+    float* dst = pz + m * g.N + nb;
+    if (nb + 3 < g.N && (g.N & 3) == 0) {
+      *reinterpret_cast<f32x4*>(dst) = acc[i];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (nb + e < g.N) dst[e] = acc[i][e];
+    }
   }
 }
 
@@ -309,10 +428,13 @@ __global__ __launch_bounds__(256) void tiled_kernel(GemmArgs g) {
 
 static int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
-template <int MT, int KS>
+template <int MT, int NW, int KS>
 static void launch_skinny(const GemmArgs& a, int pro, hipStream_t s) {
-  constexpr int NW = 8;
   dim3 grid((unsigned)(round_up(a.N, 16) / 16));
+  if constexpr (NW > 8) {
+    hipLaunchKernelGGL((skinny_kernel<MT, NW, KS, FAM_PRO_NONE>), grid, dim3(NW * 64), 0, s, a);
+    return;
+  }
   switch (pro) {
     case FAM_PRO_LAYERNORM: hipLaunchKernelGGL((skinny_kernel<MT, NW, KS, FAM_PRO_LAYERNORM>), grid, dim3(NW * 64), 0, s, a); break;
     case FAM_PRO_ADALN: hipLaunchKernelGGL((skinny_kernel<MT, NW, KS, FAM_PRO_ADALN>), grid, dim3(NW * 64), 0, s, a); break;
@@ -320,11 +442,12 @@ static void launch_skinny(const GemmArgs& a, int pro, hipStream_t s) {
   }
 }
 
+// 8 waves with 4 k-steps each cover K <= 1024 in one chunk; longer K takes 16 waves with
+// 8 k-steps each (K <= 4096 in one chunk), more chunks beyond that.
 template <int MT>
 static void launch_skinny_k(const GemmArgs& a, int pro, hipStream_t s) {
-  const int64_t per = ((a.K + 31) / 32 + 7) / 8;  // k-steps per wave
-  if (per <= 4) launch_skinny<MT, 4>(a, pro, s);
-  else launch_skinny<MT, 16>(a, pro, s);
+  if (a.K <= 1024) launch_skinny<MT, 8, 4>(a, pro, s);
+  else launch_skinny<MT, 16, 8>(a, pro, s);
 }
 
 template <int BM, int BN, int WM>
@@ -385,10 +508,64 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
   a.rpb = d->rows_per_batch;
   a.out_f32 = d->out_f32 != 0;
   hipStream_t s = (hipStream_t)stream;
-  if (d->M <= 16) launch_skinny_k<1>(a, d->prologue, s);
-  else if (d->M <= 32) launch_skinny_k<2>(a, d->prologue, s);
-  else if (d->M <= 64) launch_skinny_k<4>(a, d->prologue, s);
+  // (a prologue over K > 1024 would not fit the 16-wave skinny variant's registers)
+  const bool skinny = d->M <= 64 && (d->prologue == FAM_PRO_NONE || d->K <= 1024);
+  if (skinny && d->M <= 16) launch_skinny_k<1>(a, d->prologue, s);
+  else if (skinny && d->M <= 32) launch_skinny_k<2>(a, d->prologue, s);
+  else if (skinny) launch_skinny_k<4>(a, d->prologue, s);
   else if (round_up(d->M, 128) / 128 * (round_up(d->N, 128) / 128) >= 200) launch_tiled<128, 128, 2>(a, d->prologue, s);
   else launch_tiled<64, 64, 2>(a, d->prologue, s);
   return fam_host::check_launch("fam_gemm");
+}
+
+// Split plan of fam_gemm_partial: k-steps per split and number of splits.
+static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* splits) {
+  const int64_t groups = (N + 63) / 64;
+  const int64_t ksteps = (K + 31) / 32;
+  // Longest split (8, 4, 2 or 1 k-steps of 32) that still gives one workgroup per CU.
+  int p2 = 8;
+  while (p2 > 1 && ((ksteps + p2 - 1) / p2) * groups < 256) p2 >>= 1;
+  *steps = p2;
+  *splits = (int)((ksteps + p2 - 1) / p2);
+  (void)M;
+}
+
+extern "C" int fam_gemm_partial_splits(int64_t M, int64_t N, int64_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  int st, sp;
+  partial_plan(M, N, K, &st, &sp);
+  return sp;
+}
+
+template <int MT>
+static void launch_partial(const PartArgs& a, int steps, int splits, hipStream_t s) {
+  const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)splits);
+  switch (steps) {
+    case 1: hipLaunchKernelGGL((partial_kernel<MT, 1>), grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((partial_kernel<MT, 2>), grid, dim3(256), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((partial_kernel<MT, 4>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((partial_kernel<MT, 8>), grid, dim3(256), 0, s, a); break;
+  }
+}
+
+extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64_t ldw, float* partials,
+                                int64_t M, int64_t N, int64_t K, void* stream) {
+  FAM_REQUIRE(a && w && partials, FAM_ERR_INVALID_ARG, "fam_gemm_partial: null pointer");
+  FAM_REQUIRE(M >= 0 && M <= 64 && N >= 1 && K >= 8 && K % 8 == 0, FAM_ERR_INVALID_ARG,
+              "fam_gemm_partial: need 0 <= M <= 64, N >= 1, K a positive multiple of 8 (M=%lld N=%lld K=%lld)",
+              (long long)M, (long long)N, (long long)K);
+  FAM_REQUIRE(lda >= K && ldw >= K && lda % 8 == 0 && ldw % 8 == 0, FAM_ERR_INVALID_ARG,
+              "fam_gemm_partial: lda/ldw must be >= K and multiples of 8");
+  FAM_REQUIRE(fam_host::aligned16(a) && fam_host::aligned16(w) && fam_host::aligned16(partials), FAM_ERR_INVALID_ARG,
+              "fam_gemm_partial: a, w and partials must be 16-byte aligned");
+  FAM_REQUIRE((N + 63) / 64 <= 65535, FAM_ERR_UNSUPPORTED, "fam_gemm_partial: N too large");
+  if (M == 0) return FAM_OK;
+  int steps, splits;
+  partial_plan(M, N, K, &steps, &splits);
+  PartArgs pa{(const bf16*)a, lda, (const bf16*)w, ldw, partials, M, N, K};
+  hipStream_t s = (hipStream_t)stream;
+  if (M <= 16) launch_partial<1>(pa, steps, splits, s);
+  else if (M <= 32) launch_partial<2>(pa, steps, splits, s);
+  else launch_partial<4>(pa, steps, splits, s);
+  return fam_host::check_launch("fam_gemm_partial");
 }

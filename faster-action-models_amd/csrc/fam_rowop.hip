@@ -1,0 +1,267 @@
+// Row kernel of the fused action expert: one workgroup per output row.
+//
+//   v[n] = source(m, n) + bias[n]            source: the split-K partials of fam_gemm_partial
+//                                            summed in split order, or a small-K linear
+//   v    = act(v)                            (GELU-tanh / SiLU)
+//   v    = res[m, n] + gate(m, n) * v        (optional residual update)
+//   out[m, n] = v                            (bf16, or fp32 for the fp32 latents)
+//   then, on the stored row, the normalisation the NEXT operation needs:
+//     LayerNorm (optional affine) or AdaLN modulate over the whole row, or RMSNorm (+ RoPE)
+//     over up to two column segments (the q and k parts of a fused QKV row)  -> nout
+//
+// Because a workgroup holds the whole row, the row statistics need no second kernel and no
+// cross-workgroup traffic; the block reductions run through LDS in a fixed order.
+// Bytes per row: 4*splits*N (partials) + 2*N (out) [+ 2*N residual] [+ 2*N nout].
+#include "fam_common.h"
+
+namespace fam {
+
+struct RowArgs {
+  int src;
+  const float* part; int64_t splits, split_stride;
+  const float* xin; int64_t ldx, kin; const bf16* win;
+  int64_t M, N;
+  const bf16* bias; int act;
+  const void* res; int64_t ldr;
+  const bf16* gate; int64_t gbs, grs, gns; int64_t rpb;
+  void* out; int64_t ldo; int out_f32;
+  int norm; float eps;
+  const bf16* nw; const bf16* nb;
+  const bf16* shift; const bf16* scale; int64_t mbs, mrs;
+  int nseg; int64_t seg0[2]; int64_t segw; const bf16* segwt[2];
+  const float* cs; const float* sn; int64_t trs, tes, hd, seq;
+  bf16* nout; int64_t ldn;
+};
+
+constexpr int RT = 256;  // threads per row
+
+__device__ __forceinline__ float act_fn(float v, int act) {
+  if (act == FAM_ACT_GELU_TANH) return gelu_tanh(v);
+  if (act == FAM_ACT_SILU) return silu(v);
+  return v;
+}
+
+// Sum over the 256 threads of the workgroup; every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();  // red may still be read by a previous reduction
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+// NV groups of 4 columns per thread: N <= 4 * RT * NV.
+template <int NV>
+__global__ __launch_bounds__(RT) void rowop_kernel(RowArgs a) {
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int64_t m = blockIdx.x;
+  const int64_t bi = m / a.rpb, si = m - bi * a.rpb;
+  float v[NV][4];
+  bool ok[NV][4];
+
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t c = ((int64_t)tid + RT * j) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[j][e] = 0.f; ok[j][e] = c + e < a.N; }
+    if (a.src == 0) {
+      if ((a.N & 3) == 0) {
+        if (c < a.N) {
+          const float* p = a.part + m * a.N + c;
+#pragma unroll 8
+          for (int64_t z = 0; z < a.splits; ++z) {
+            const f32x4 t = *reinterpret_cast<const f32x4*>(p + z * a.split_stride);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[j][e] += t[e];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (ok[j][e])
+            for (int64_t z = 0; z < a.splits; ++z) v[j][e] += a.part[z * a.split_stride + m * a.N + c + e];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (ok[j][e])
+          for (int64_t k = 0; k < a.kin; ++k) v[j][e] += a.xin[m * a.ldx + k] * to_f(a.win[(c + e) * a.kin + k]);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (!ok[j][e]) continue;
+      const int64_t n = c + e;
+      float x = v[j][e];
+      if (a.bias) x += to_f(a.bias[n]);
+      x = act_fn(x, a.act);
+      if (a.res) {
+        float g = 1.0f;
+        if (a.gate) g = to_f(a.gate[bi * a.gbs + si * a.grs + n * a.gns]);
+        const float r = a.out_f32 ? reinterpret_cast<const float*>(a.res)[m * a.ldr + n]
+                                  : to_f(reinterpret_cast<const bf16*>(a.res)[m * a.ldr + n]);
+        x = r + g * x;
+      }
+      if (a.out_f32) {
+        reinterpret_cast<float*>(a.out)[m * a.ldo + n] = x;
+      } else {
+        const bf16 xb = to_bf(x);
+        reinterpret_cast<bf16*>(a.out)[m * a.ldo + n] = xb;
+        x = to_f(xb);  // the stored (rounded) value feeds the normalisation
+      }
+      v[j][e] = x;
+    }
+  }
+  if (a.norm == FAM_ROWNORM_NONE) return;
+
+  if (a.norm == FAM_ROWNORM_LAYERNORM || a.norm == FAM_ROWNORM_ADALN) {
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s += ok[j][e] ? v[j][e] : 0.f;
+    const float mean = block_sum(s, red) / (float)a.N;
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = ok[j][e] ? v[j][e] - mean : 0.f;
+        q += d * d;
+      }
+    const float rstd = rsqrtf(block_sum(q, red) / (float)a.N + a.eps);
+    const int64_t moff = bi * a.mbs + si * a.mrs;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (!ok[j][e]) continue;
+        const int64_t n = ((int64_t)tid + RT * j) * 4 + e;
+        float o = (v[j][e] - mean) * rstd;
+        if (a.norm == FAM_ROWNORM_LAYERNORM) {
+          if (a.nw) o *= to_f(a.nw[n]);
+          if (a.nb) o += to_f(a.nb[n]);
+        } else {
+          o = o * (1.0f + to_f(a.scale[moff + n])) + to_f(a.shift[moff + n]);
+        }
+        a.nout[m * a.ldn + n] = to_bf(o);
+      }
+    return;
+  }
+
+  // RMSNorm (+ RoPE) over column segments [seg0[g], seg0[g] + segw)
+  const int64_t pos = m % a.seq;
+  for (int sg = 0; sg < a.nseg; ++sg) {
+    const int64_t c0 = a.seg0[sg];
+    float q = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t n = ((int64_t)tid + RT * j) * 4 + e;
+        if (ok[j][e] && n >= c0 && n < c0 + a.segw) q += v[j][e] * v[j][e];
+      }
+    const float rs = rsqrtf(block_sum(q, red) / (float)a.segw + a.eps);
+    const bf16* wt = a.segwt[sg];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t cb = ((int64_t)tid + RT * j) * 4;
+      if (cb < c0 || cb >= c0 + a.segw || cb >= a.N) continue;  // segments are 4-aligned
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)  // bf16 before the weight multiply, as RMSNorm.forward
+        o[e] = to_f(to_bf(to_f(to_bf(v[j][e] * rs)) * to_f(wt[cb - c0 + e])));
+      if (a.cs) {
+        const int64_t j0 = ((cb - c0) % a.hd) >> 1;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int64_t t = pos * a.trs + (j0 + p) * a.tes;
+          const float cc = a.cs[t], ss = a.sn[t];
+          const float x0 = o[2 * p], x1 = o[2 * p + 1];
+          o[2 * p] = x0 * cc - x1 * ss;
+          o[2 * p + 1] = x0 * ss + x1 * cc;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a.nout[m * a.ldn + cb + e] = to_bf(o[e]);
+    }
+  }
+}
+
+}  // namespace fam
+
+using namespace fam;
+
+extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
+  FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_rowop: null descriptor");
+  FAM_REQUIRE(d->M >= 0 && d->N >= 1 && d->N <= 4 * RT * 4, FAM_ERR_INVALID_ARG,
+              "fam_rowop: need 1 <= N <= 4096 (N=%lld)", (long long)d->N);
+  FAM_REQUIRE(d->out, FAM_ERR_INVALID_ARG, "fam_rowop: out must be non-null");
+  FAM_REQUIRE(d->ldo >= d->N, FAM_ERR_INVALID_ARG, "fam_rowop: ldo must be >= N");
+  if (d->src == FAM_ROWSRC_PARTIALS) {
+    FAM_REQUIRE(d->partials && d->splits >= 1 && d->split_stride >= d->M * d->N, FAM_ERR_INVALID_ARG,
+                "fam_rowop: partials need splits >= 1 and split_stride >= M*N");
+    FAM_REQUIRE(d->N % 4 != 0 || fam_host::aligned16(d->partials), FAM_ERR_INVALID_ARG,
+                "fam_rowop: partials must be 16-byte aligned");
+    FAM_REQUIRE(d->N % 4 != 0 || d->split_stride % 4 == 0, FAM_ERR_INVALID_ARG,
+                "fam_rowop: split_stride must be a multiple of 4");
+  } else if (d->src == FAM_ROWSRC_SMALLK) {
+    FAM_REQUIRE(d->x_in && d->w_in && d->k_in >= 1 && d->k_in <= 64 && d->ldx >= d->k_in, FAM_ERR_INVALID_ARG,
+                "fam_rowop: small-K source needs x_in, w_in and 1 <= k_in <= 64");
+  } else {
+    FAM_REQUIRE(false, FAM_ERR_INVALID_ARG, "fam_rowop: unknown source %d", d->src);
+  }
+  FAM_REQUIRE(d->act >= FAM_ACT_NONE && d->act <= FAM_ACT_SILU, FAM_ERR_INVALID_ARG, "fam_rowop: unknown act");
+  FAM_REQUIRE(!d->gate || d->res, FAM_ERR_INVALID_ARG, "fam_rowop: a gate needs a residual");
+  FAM_REQUIRE(d->rows_per_batch >= 1, FAM_ERR_INVALID_ARG, "fam_rowop: rows_per_batch must be >= 1");
+  FAM_REQUIRE(d->norm >= FAM_ROWNORM_NONE && d->norm <= FAM_ROWNORM_RMS, FAM_ERR_INVALID_ARG, "fam_rowop: unknown norm");
+  if (d->norm != FAM_ROWNORM_NONE) {
+    FAM_REQUIRE(!d->out_f32, FAM_ERR_UNSUPPORTED, "fam_rowop: normalisation needs a bf16 row");
+    FAM_REQUIRE(d->nout && d->ldn >= d->N, FAM_ERR_INVALID_ARG, "fam_rowop: norm output missing or ldn < N");
+  }
+  if (d->norm == FAM_ROWNORM_ADALN) {
+    FAM_REQUIRE(d->shift && d->scale, FAM_ERR_INVALID_ARG, "fam_rowop: AdaLN needs shift and scale");
+  }
+  if (d->norm == FAM_ROWNORM_RMS) {
+    FAM_REQUIRE(d->nseg >= 1 && d->nseg <= 2 && d->seg_width >= 4 && d->seg_width % 4 == 0, FAM_ERR_INVALID_ARG,
+                "fam_rowop: RMS needs 1 or 2 segments of a width that is a multiple of 4");
+    for (int g = 0; g < d->nseg; ++g) {
+      FAM_REQUIRE(d->seg_weight[g] && d->seg_col0[g] >= 0 && d->seg_col0[g] % 4 == 0 &&
+                      d->seg_col0[g] + d->seg_width <= d->N,
+                  FAM_ERR_INVALID_ARG, "fam_rowop: bad RMS segment %d", g);
+    }
+    FAM_REQUIRE((d->rope_cos == nullptr) == (d->rope_sin == nullptr), FAM_ERR_INVALID_ARG,
+                "fam_rowop: rope_cos and rope_sin must both be given or both be null");
+    if (d->rope_cos) {
+      FAM_REQUIRE(d->head_dim >= 4 && d->head_dim % 4 == 0 && d->seg_width % d->head_dim == 0 && d->seq_len >= 1,
+                  FAM_ERR_INVALID_ARG, "fam_rowop: RoPE needs head_dim %% 4 == 0 dividing the segment, seq_len >= 1");
+    }
+  }
+  if (d->M == 0) return FAM_OK;
+
+  RowArgs a{};
+  a.src = d->src;
+  a.part = d->partials; a.splits = d->splits; a.split_stride = d->split_stride;
+  a.xin = d->x_in; a.ldx = d->ldx; a.kin = d->k_in; a.win = (const bf16*)d->w_in;
+  a.M = d->M; a.N = d->N;
+  a.bias = (const bf16*)d->bias; a.act = d->act;
+  a.res = d->res; a.ldr = d->ldr;
+  a.gate = (const bf16*)d->gate; a.gbs = d->gate_bs; a.grs = d->gate_rs; a.gns = d->gate_ns;
+  a.rpb = d->rows_per_batch;
+  a.out = d->out; a.ldo = d->ldo; a.out_f32 = d->out_f32 != 0;
+  a.norm = d->norm; a.eps = d->eps;
+  a.nw = (const bf16*)d->ln_weight; a.nb = (const bf16*)d->ln_bias;
+  a.shift = (const bf16*)d->shift; a.scale = (const bf16*)d->scale; a.mbs = d->mod_bs; a.mrs = d->mod_rs;
+  a.nseg = d->nseg; a.seg0[0] = d->seg_col0[0]; a.seg0[1] = d->seg_col0[1]; a.segw = d->seg_width;
+  a.segwt[0] = (const bf16*)d->seg_weight[0]; a.segwt[1] = (const bf16*)d->seg_weight[1];
+  a.cs = d->rope_cos; a.sn = d->rope_sin; a.trs = d->rope_row_stride; a.tes = d->rope_elem_stride;
+  a.hd = d->head_dim > 0 ? d->head_dim : 4; a.seq = d->seq_len > 0 ? d->seq_len : 1;
+  a.nout = (bf16*)d->nout; a.ldn = d->ldn;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)d->M);
+  if (d->N <= 4 * RT) hipLaunchKernelGGL(rowop_kernel<1>, grid, dim3(RT), 0, s, a);
+  else if (d->N <= 8 * RT) hipLaunchKernelGGL(rowop_kernel<2>, grid, dim3(RT), 0, s, a);
+  else hipLaunchKernelGGL(rowop_kernel<4>, grid, dim3(RT), 0, s, a);
+  return fam_host::check_launch("fam_rowop");
+}

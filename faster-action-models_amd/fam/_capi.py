@@ -20,6 +20,8 @@ FAM_ABI_VERSION = 1
 FAM_MASK_NONE, FAM_MASK_BOOL, FAM_MASK_ADD_F32, FAM_MASK_ADD_BF16 = 0, 1, 2, 3
 FAM_PRO_NONE, FAM_PRO_LAYERNORM, FAM_PRO_ADALN = 0, 1, 2
 FAM_ACT_NONE, FAM_ACT_GELU_TANH, FAM_ACT_SILU = 0, 1, 2
+FAM_ROWSRC_PARTIALS, FAM_ROWSRC_SMALLK = 0, 1
+FAM_ROWNORM_NONE, FAM_ROWNORM_LAYERNORM, FAM_ROWNORM_ADALN, FAM_ROWNORM_RMS = 0, 1, 2, 3
 
 _i64 = C.c_int64
 _vp = C.c_void_p
@@ -45,6 +47,7 @@ class AttnDesc(C.Structure):
         ("batch", _i64), ("heads", _i64), ("sq", _i64), ("sk0", _i64), ("sk1", _i64), ("head_dim", _i64),
         ("scale", C.c_float),
         ("mask", _vp), ("mask_kind", C.c_int), ("mask_bs", _i64), ("mask_hs", _i64), ("mask_qs", _i64),
+        ("num_splits", C.c_int), ("part_o", _vp), ("part_ml", _vp),
     ]
 
 
@@ -69,6 +72,27 @@ class GemmDesc(C.Structure):
     ]
 
 
+class RowopDesc(C.Structure):
+    """fam_rowop_desc (include/fam_hip.h)."""
+    _fields_ = [
+        ("src", C.c_int),
+        ("partials", _vp), ("splits", _i64), ("split_stride", _i64),
+        ("x_in", _vp), ("ldx", _i64), ("k_in", _i64), ("w_in", _vp),
+        ("M", _i64), ("N", _i64),
+        ("bias", _vp), ("act", C.c_int),
+        ("res", _vp), ("ldr", _i64),
+        ("gate", _vp), ("gate_bs", _i64), ("gate_rs", _i64), ("gate_ns", _i64), ("rows_per_batch", _i64),
+        ("out", _vp), ("ldo", _i64), ("out_f32", C.c_int),
+        ("norm", C.c_int), ("eps", C.c_float),
+        ("ln_weight", _vp), ("ln_bias", _vp),
+        ("shift", _vp), ("scale", _vp), ("mod_bs", _i64), ("mod_rs", _i64),
+        ("nseg", C.c_int), ("seg_col0", _i64 * 2), ("seg_width", _i64), ("seg_weight", _vp * 2),
+        ("rope_cos", _vp), ("rope_sin", _vp), ("rope_row_stride", _i64), ("rope_elem_stride", _i64),
+        ("head_dim", _i64), ("seq_len", _i64),
+        ("nout", _vp), ("ldn", _i64),
+    ]
+
+
 # name -> (restype, argtypes); every symbol declared in include/fam_hip.h
 SIGNATURES = {
     "fam_version": (C.c_int, []),
@@ -77,6 +101,10 @@ SIGNATURES = {
     "fam_rmsnorm_rope": (C.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, C.c_float, _vp, _vp, _i64, _i64,
                                    _i64, _vp]),
     "fam_attention": (C.c_int, [C.POINTER(AttnDesc), _vp]),
+    "fam_attention_combine": (C.c_int, [C.POINTER(AttnDesc), _vp]),
+    "fam_gemm_partial": (C.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
+    "fam_gemm_partial_splits": (C.c_int, [_i64, _i64, _i64]),
+    "fam_rowop": (C.c_int, [C.POINTER(RowopDesc), _vp]),
     "fam_gemm": (C.c_int, [C.POINTER(GemmDesc), _vp]),
     "fam_linear_smallk": (C.c_int, [_vp, _i64, C.c_int, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "fam_euler_step": (C.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),

@@ -19,12 +19,14 @@ Per policy call the plan runs:
     -> t_mod + modulation of every block; context embedding (GEMM+GELU, GEMM); the context
     K/V of every block from one GEMM over the concatenated weights; RMSNorm of each K.
   per step:
-    action encoder (7 -> H) -> 12 x block -> head GEMM whose epilogue is the Euler update.
-  per block (11 launches):
-    [AdaLN1 + QKV GEMM] -> RMSNorm+RoPE(q) -> RMSNorm+RoPE(k) -> self-attention ->
-    [o GEMM + gate_msa + residual] -> [LayerNorm3 + cross-q GEMM] -> RMSNorm(q) ->
-    cross-attention (keys split over the waves of a workgroup) -> [cross-o GEMM + residual] ->
-    [AdaLN2 + FFN-up GEMM + GELU] -> [FFN-down GEMM + gate_mlp + residual].
+    [action encoder (7 -> H) + AdaLN1] -> 12 x block -> [head GEMM] -> [Euler update].
+  per block (15 launches): every projection is a split-K GEMM writing fp32 partials, and the
+  row kernel after it sums them and runs the epilogue plus the next normalisation:
+    qkv GEMM -> [bias, RMSNorm+RoPE of q and k] -> self-attention ->
+    o GEMM -> [bias, x += gate_msa*o, LayerNorm3] -> cross-q GEMM -> [bias, RMSNorm(q)] ->
+    cross-attention (keys split over workgroups) -> combine ->
+    cross-o GEMM -> [bias, x += o, AdaLN2] -> FFN-up GEMM -> [bias, GELU] ->
+    FFN-down GEMM -> [bias, x += gate_mlp*ffn, AdaLN1 of the next block].
 
 The per-call prologue replaces work the reference repeats inside every step (time MLP,
 text embedding, context K/V projection): the values are identical at every step of one
@@ -256,6 +258,18 @@ class FusedActionDiT:
         self.ctx_h = z(ctx_len, H)
         self.ctx_emb = z(ctx_len, H)
         self.ctxkv = z(ctx_len, L * 2 * A)
+        self.h = z(M, H)   # normalised input of the next projection
+
+        # split-K partials of the action projections (one buffer, reused launch after launch)
+        part_need = 0
+        for (n_, k_) in ((3 * A, H), (H, A), (A, H), (Fd, H), (H, Fd), (cfg.action_dim, H)):
+            part_need = max(part_need, self.lib.fam_gemm_partial_splits(M, n_, k_) * M * n_)
+        self.part = torch.zeros(part_need, dtype=torch.float32, device=dev)
+        # key-split partials of the cross-attention: ~4 blocks of 32 keys per workgroup
+        self.kv_splits = max(1, min(64, -(-ctx_len // 128)))
+        nq = batch * cfg.num_heads * seq_len
+        self.apart_o = torch.zeros(self.kv_splits * nq * cfg.attn_head_dim, dtype=torch.float32, device=dev)
+        self.apart_ml = torch.zeros(self.kv_splits * nq * 2, dtype=torch.float32, device=dev)
 
         self._descs: list = []   # keeps ctypes descriptors alive
         self.plan = self._build_plan()
@@ -303,7 +317,68 @@ class FusedActionDiT:
         nbytes += 4 * Kv if prologue != _capi.FAM_PRO_NONE else 0
         self.plan.add(name, run, "gemm", nbytes, 2 * Mv * N * Kv)
 
-    def _attn(self, name, q, q_bs, q_rs, k, k_bs, k_rs, v, v_bs, v_rs, out, sq, sk):
+    def _launch(self, name, fname, ref, kernel, nbytes, flops=0):
+        f, lib = getattr(self.lib, fname), self.lib
+
+        def run(stream):
+            rc = f(ref, stream)
+            if rc != 0:
+                raise FamError(f"{fname}[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
+        self.plan.add(name, run, kernel, nbytes, flops)
+
+    def _gemm_partial(self, name, a, w):
+        """Split-K partials of a [M, K] x w[N, K]^T into self.part; returns the split count."""
+        M, K = a.shape[0], w.shape[1]
+        N = w.shape[0]
+        splits = self.lib.fam_gemm_partial_splits(M, N, K)
+        args = (a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), self.part.data_ptr(), M, N, K)
+        self.plan.add(name, _checked(self.lib, "fam_gemm_partial", *args), "gemm_partial",
+                      2 * (M * K + N * K) + 4 * splits * M * N, 2 * M * N * K)
+        return splits
+
+    def _rowop(self, name, *, N, splits=1, src=_capi.FAM_ROWSRC_PARTIALS, x_in=None, w_in=None, bias=None,
+               act=_capi.FAM_ACT_NONE, res=None, gate=None, gate_strides=(0, 0, 1), out=None, out_f32=False,
+               norm=_capi.FAM_ROWNORM_NONE, ln_w=None, ln_b=None, shift=None, scale=None, segs=(), rope=False,
+               nout=None):
+        cfg = self.cfg
+        M = self.B * self.S
+        d = _capi.RowopDesc()
+        d.src = src
+        if src == _capi.FAM_ROWSRC_PARTIALS:
+            d.partials, d.splits, d.split_stride = self.part.data_ptr(), splits, M * N
+        else:
+            d.x_in, d.ldx, d.k_in, d.w_in = x_in.data_ptr(), x_in.stride(0), w_in.shape[1], w_in.data_ptr()
+        d.M, d.N = M, N
+        d.bias = bias.data_ptr() if bias is not None else None
+        d.act = act
+        if res is not None:
+            d.res, d.ldr = res.data_ptr(), res.stride(0)
+        d.gate = gate.data_ptr() if gate is not None else None
+        d.gate_bs, d.gate_rs, d.gate_ns = gate_strides
+        d.rows_per_batch = self.S
+        d.out, d.ldo, d.out_f32 = out.data_ptr(), out.stride(0), int(out_f32)
+        d.norm, d.eps = norm, float(cfg.eps)
+        d.ln_weight = ln_w.data_ptr() if ln_w is not None else None
+        d.ln_bias = ln_b.data_ptr() if ln_b is not None else None
+        d.shift = shift.data_ptr() if shift is not None else None
+        d.scale = scale.data_ptr() if scale is not None else None
+        d.mod_bs = d.mod_rs = 0   # one modulation vector for every row (the timestep is shared)
+        d.nseg = len(segs)
+        for g_, (c0, wt) in enumerate(segs):
+            d.seg_col0[g_], d.seg_weight[g_] = c0, wt.data_ptr()
+        d.seg_width = cfg.attn_dim
+        if rope:
+            d.rope_cos, d.rope_sin = self.rope_cos.data_ptr(), self.rope_sin.data_ptr()
+            d.rope_row_stride, d.rope_elem_stride = cfg.attn_head_dim // 2, 1
+            d.head_dim, d.seq_len = cfg.attn_head_dim, self.S
+        if nout is not None:
+            d.nout, d.ldn = nout.data_ptr(), nout.stride(0)
+        self._descs.append(d)
+        nbytes = (4 * splits * M * N if src == _capi.FAM_ROWSRC_PARTIALS else 4 * M * d.k_in) + 2 * M * N
+        nbytes += (2 * M * N if res is not None else 0) + (2 * M * N if nout is not None else 0)
+        self._launch(name, "fam_rowop", C.byref(d), "rowop", nbytes)
+
+    def _attn(self, name, q, q_bs, q_rs, k, k_bs, k_rs, v, v_bs, v_rs, out, sq, sk, splits=1):
         cfg = self.cfg
         Dh = cfg.attn_head_dim
         d = _capi.AttnDesc()
@@ -314,17 +389,19 @@ class FusedActionDiT:
         d.batch, d.heads, d.sq, d.sk0, d.sk1, d.head_dim = self.B, cfg.num_heads, sq, sk, 0, Dh
         d.scale = 1.0 / math.sqrt(Dh)
         d.mask_kind = _capi.FAM_MASK_NONE
+        d.num_splits = splits
+        if splits > 1:
+            d.part_o, d.part_ml = self.apart_o.data_ptr(), self.apart_ml.data_ptr()
         self._descs.append(d)
-        f, lib, ref = self.lib.fam_attention, self.lib, C.byref(d)
-
-        def run(stream):
-            rc = f(ref, stream)
-            if rc != 0:
-                raise FamError(f"fam_attention[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
         A = cfg.attn_dim
         kv_batches = self.B if k_bs else 1   # a batch-broadcast context is read once
         nbytes = 2 * (2 * self.B * sq * A + 2 * kv_batches * sk * A)
-        self.plan.add(name, run, "attention", nbytes, 4 * self.B * cfg.num_heads * sq * sk * Dh)
+        self._launch(name, "fam_attention", C.byref(d), "attention", nbytes,
+                     4 * self.B * cfg.num_heads * sq * sk * Dh)
+        if splits > 1:
+            nq = self.B * cfg.num_heads * sq
+            self._launch(name + "_combine", "fam_attention_combine", C.byref(d), "attn_combine",
+                         splits * nq * (4 * Dh + 8) + 2 * nq * Dh)
 
     def _build_plan(self) -> _Plan:
         cfg, lib = self.cfg, self.lib
@@ -356,49 +433,59 @@ class FusedActionDiT:
                      "rmsnorm_rope", 2 * (2 * Lc * A + A))
 
         lat = self.latents.view(M, cfg.action_dim)
-        x, qkv, attn, qc, hid = self.x, self.qkv, self.attn, self.qc, self.hid
+        x, qkv, attn, qc, hid, h = self.x, self.qkv, self.attn, self.qc, self.hid, self.h
         qkvp = qkv.data_ptr()
+        kvp = self.ctxkv.data_ptr()
+        RMS, LN, ADALN = _capi.FAM_ROWNORM_RMS, _capi.FAM_ROWNORM_LAYERNORM, _capi.FAM_ROWNORM_ADALN
+
+        def mod(t, l, i):   # chunk i of (modulation + t_mod) of block l at step t: [H]
+            return self.mods[t, l, i * H:(i + 1) * H]
+
         for t in range(T):
-            plan.add(f"s{t}.encoder", _checked(lib, "fam_linear_smallk", lat.data_ptr(), cfg.action_dim, 1,
-                                               w["enc_w"].data_ptr(), w["enc_b"].data_ptr(), x.data_ptr(), H,
-                                               M, H, cfg.action_dim), "linear_smallk",
-                     2 * (M * cfg.action_dim + H * cfg.action_dim + H + M * H))
+            # action encoder (7 -> H) + AdaLN1 of block 0, one row per workgroup
+            self._rowop(f"s{t}.encoder", N=H, src=_capi.FAM_ROWSRC_SMALLK, x_in=lat, w_in=w["enc_w"],
+                        bias=w["enc_b"], out=x, norm=ADALN, shift=mod(t, 0, 0), scale=mod(t, 0, 1), nout=h)
             for l in range(L):
-                mod = self.mods[t, l]
-                sh_a, sc_a, g_a = mod[0:H], mod[H:2 * H], mod[2 * H:3 * H]
-                sh_m, sc_m, g_m = mod[3 * H:4 * H], mod[4 * H:5 * H], mod[5 * H:6 * H]
                 tag = f"s{t}.b{l}"
-                self._gemm(tag + ".qkv", x, w[f"qkv_w{l}"], w[f"qkv_b{l}"], qkv, prologue=_capi.FAM_PRO_ADALN,
-                           shift=sh_a, scale=sc_a)
-                for nm, off, wn in (("q", 0, "norm_q"), ("k", A, "norm_k")):
-                    plan.add(tag + f".{nm}_norm_rope",
-                             _checked(lib, "fam_rmsnorm_rope", qkvp + 2 * off, 3 * A, qkvp + 2 * off, 3 * A, M, S, A,
-                                      w[f"sa_{wn}_w{l}"].data_ptr(), eps, self.rope_cos.data_ptr(),
-                                      self.rope_sin.data_ptr(), Dh // 2, 1, Dh),
-                             "rmsnorm_rope", 2 * (2 * M * A + A) + 8 * S * (Dh // 2))
+                # q, k, v projection; RMSNorm + RoPE of q and k in the row kernel
+                sp = self._gemm_partial(tag + ".qkv", h, w[f"qkv_w{l}"])
+                self._rowop(tag + ".qkv_row", N=3 * A, splits=sp, bias=w[f"qkv_b{l}"], out=qkv, norm=RMS,
+                            segs=((0, w[f"sa_norm_q_w{l}"]), (A, w[f"sa_norm_k_w{l}"])), rope=True, nout=qkv)
                 self._attn(tag + ".self_attn", qkvp, S * 3 * A, 3 * A, qkvp + 2 * A, S * 3 * A, 3 * A,
                            qkvp + 4 * A, S * 3 * A, 3 * A, attn, S, S)
-                self._gemm(tag + ".o", attn, w[f"sa_o_w{l}"], w[f"sa_o_b{l}"], x, res=x, gate=g_a)
-                self._gemm(tag + ".cross_q", x, w[f"ca_q_w{l}"], w[f"ca_q_b{l}"], qc, prologue=_capi.FAM_PRO_LAYERNORM,
-                           pro_w=w[f"n3_w{l}"], pro_b=w[f"n3_b{l}"])
-                plan.add(tag + ".cross_q_norm",
-                         _checked(lib, "fam_rmsnorm_rope", qc.data_ptr(), A, qc.data_ptr(), A, M, 1, A,
-                                  w[f"ca_nq_w{l}"].data_ptr(), eps, None, None, 0, 0, 0),
-                         "rmsnorm_rope", 2 * (2 * M * A + A))
+                # o projection; x += gate_msa * o; LayerNorm3 (affine) for the cross-attention query
+                sp = self._gemm_partial(tag + ".o", attn, w[f"sa_o_w{l}"])
+                self._rowop(tag + ".o_row", N=H, splits=sp, bias=w[f"sa_o_b{l}"], res=x, gate=mod(t, l, 2), out=x,
+                            norm=LN, ln_w=w[f"n3_w{l}"], ln_b=w[f"n3_b{l}"], nout=h)
+                # cross-attention query + its RMSNorm
+                sp = self._gemm_partial(tag + ".cross_q", h, w[f"ca_q_w{l}"])
+                self._rowop(tag + ".cross_q_row", N=A, splits=sp, bias=w[f"ca_q_b{l}"], out=qc, norm=RMS,
+                            segs=((0, w[f"ca_nq_w{l}"]),), nout=qc)
                 kb = kvp + 2 * (l * 2 * A)
                 self._attn(tag + ".cross_attn", qc.data_ptr(), S * A, A, kb, 0, L * 2 * A, kb + 2 * A, 0, L * 2 * A,
-                           attn, S, Lc)
-                self._gemm(tag + ".cross_o", attn, w[f"ca_o_w{l}"], w[f"ca_o_b{l}"], x, res=x)
-                self._gemm(tag + ".ffn_up", x, w[f"ff0_w{l}"], w[f"ff0_b{l}"], hid, prologue=_capi.FAM_PRO_ADALN,
-                           shift=sh_m, scale=sc_m, act=_capi.FAM_ACT_GELU_TANH)
-                self._gemm(tag + ".ffn_down", hid, w[f"ff2_w{l}"], w[f"ff2_b{l}"], x, res=x, gate=g_m)
+                           attn, S, Lc, splits=self.kv_splits)
+                # cross o projection; x += o; AdaLN2 for the FFN
+                sp = self._gemm_partial(tag + ".cross_o", attn, w[f"ca_o_w{l}"])
+                self._rowop(tag + ".cross_o_row", N=H, splits=sp, bias=w[f"ca_o_b{l}"], res=x, out=x, norm=ADALN,
+                            shift=mod(t, l, 3), scale=mod(t, l, 4), nout=h)
+                # FFN: up + GELU, down; x += gate_mlp * ffn; AdaLN1 of the next block
+                sp = self._gemm_partial(tag + ".ffn_up", h, w[f"ff0_w{l}"])
+                self._rowop(tag + ".ffn_up_row", N=Fd, splits=sp, bias=w[f"ff0_b{l}"], act=_capi.FAM_ACT_GELU_TANH,
+                            out=hid)
+                sp = self._gemm_partial(tag + ".ffn_down", hid, w[f"ff2_w{l}"])
+                if l + 1 < L:
+                    self._rowop(tag + ".ffn_down_row", N=H, splits=sp, bias=w[f"ff2_b{l}"], res=x, gate=mod(t, l, 5),
+                                out=x, norm=ADALN, shift=mod(t, l + 1, 0), scale=mod(t, l + 1, 1), nout=h)
+                else:
+                    self._rowop(tag + ".ffn_down_row", N=H, splits=sp, bias=w[f"ff2_b{l}"], res=x, gate=mod(t, l, 5),
+                                out=x)
+            # head; the row kernel's epilogue is the Euler update of the fp32 latents
+            sp = self._gemm_partial(f"s{t}.head", x, w["head_w"])
             if self.mode == "forward":
-                # ActionDiT.post_dit: the head alone (FB/action_dit.py:317-318)
-                self._gemm(f"s{t}.head", x, w["head_w"], w["head_b"], self.head_out)
+                self._rowop(f"s{t}.head_row", N=cfg.action_dim, splits=sp, bias=w["head_b"], out=self.head_out)
             else:
-                # head GEMM with the Euler update as its epilogue: latents += delta_t * (x W^T + b)
-                self._gemm(f"s{t}.head_euler", x, w["head_w"], w["head_b"], lat, res=lat,
-                           gate=self.deltas[t:t + 1], gate_strides=(0, 0, 0), out_f32=True)
+                self._rowop(f"s{t}.head_euler", N=cfg.action_dim, splits=sp, bias=w["head_b"], res=lat,
+                            gate=self.deltas[t:t + 1], gate_strides=(0, 0, 0), out=lat, out_f32=True)
         return plan
 
     # ------------------------------------------------------------------ execution

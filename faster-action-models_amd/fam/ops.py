@@ -255,7 +255,7 @@ def _mask_args(mask: Optional[torch.Tensor], B: int, H: int, Sq: int, Sk: int):
 def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
                    mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
                    k_prefix: Optional[torch.Tensor] = None, v_prefix: Optional[torch.Tensor] = None,
-                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                   out: Optional[torch.Tensor] = None, num_splits: int = 1) -> torch.Tensor:
     """Attention on [B, S, H*Dh] tensors; keys/values are cat(k_prefix, k) when a prefix is
     given (the MoT joint attention over a cached video K/V, FB/mot.py:446-478) without
     materialising the concatenation."""
@@ -296,7 +296,16 @@ def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads:
     d.scale = (1.0 / math.sqrt(Dh)) if scale is None else float(scale)
     mp, kind, mbs, mhs, mqs, keep = _mask_args(mask, B, num_heads, Sq, Sk)
     d.mask, d.mask_kind, d.mask_bs, d.mask_hs, d.mask_qs = mp, kind, mbs, mhs, mqs
+    part_o = part_ml = None
+    if num_splits > 1:
+        # key splits over workgroups: per-split partials, then an ordered merge
+        nq = B * num_heads * Sq
+        part_o = torch.empty(num_splits * nq * Dh, dtype=torch.float32, device=q.device)
+        part_ml = torch.empty(num_splits * nq * 2, dtype=torch.float32, device=q.device)
+        d.num_splits, d.part_o, d.part_ml = num_splits, part_o.data_ptr(), part_ml.data_ptr()
     call("fam_attention", C.byref(d), _stream(q))
+    if num_splits > 1:
+        call("fam_attention_combine", C.byref(d), _stream(q))
     return out
 
 
@@ -370,6 +379,64 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: to
     d.rows_per_batch = rows_per_batch if rows_per_batch is not None else max(M, 1)
     d.out_f32 = int(out_f32)
     call("fam_gemm", C.byref(d), _stream(a))
+
+
+def gemm_partial(a: torch.Tensor, w: torch.Tensor):
+    """Split-K partials of a [M, K] x w [N, K]^T (M <= 64): returns ([S, M, N] fp32, S)."""
+    _check(a, "a")
+    _check(w, "w")
+    M, K = a.shape
+    N = w.shape[0]
+    S = _capi.lib().fam_gemm_partial_splits(M, N, K)
+    part = torch.empty((S, M, N), dtype=torch.float32, device=a.device)
+    call("fam_gemm_partial", a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), part.data_ptr(), M, N, K,
+         _stream(a))
+    return part, S
+
+
+def rowop(out: torch.Tensor, *, partials: Optional[torch.Tensor] = None, x_in: Optional[torch.Tensor] = None,
+          w_in: Optional[torch.Tensor] = None, bias=None, act: int = _capi.FAM_ACT_NONE, res=None, gate=None,
+          gate_strides=(0, 0, 1), rows_per_batch: Optional[int] = None, norm: int = _capi.FAM_ROWNORM_NONE,
+          eps: float = 1e-6, ln_w=None, ln_b=None, shift=None, scale=None, mod_strides=(0, 0), segs=(),
+          seg_width: int = 0, rope=None, nout: Optional[torch.Tensor] = None) -> None:
+    """Row kernel (fam_rowop in include/fam_hip.h) on 2-D row-major tensors.  `partials` is the
+    [S, M, N] output of gemm_partial; `rope` is (cos, sin, row_stride, elem_stride, head_dim,
+    seq_len) with fp32 tables."""
+    M, N = out.shape
+    d = _capi.RowopDesc()
+    keep = []
+    if partials is not None:
+        d.src, d.partials, d.splits, d.split_stride = _capi.FAM_ROWSRC_PARTIALS, partials.data_ptr(), partials.shape[0], M * N
+    else:
+        d.src = _capi.FAM_ROWSRC_SMALLK
+        d.x_in, d.ldx, d.k_in, d.w_in = x_in.data_ptr(), x_in.stride(0), w_in.shape[1], w_in.data_ptr()
+    d.M, d.N = M, N
+    d.bias = bias.data_ptr() if bias is not None else None
+    d.act = act
+    if res is not None:
+        d.res, d.ldr = res.data_ptr(), res.stride(0)
+    d.gate = gate.data_ptr() if gate is not None else None
+    d.gate_bs, d.gate_rs, d.gate_ns = gate_strides
+    d.rows_per_batch = rows_per_batch or M
+    d.out, d.ldo, d.out_f32 = out.data_ptr(), out.stride(0), int(out.dtype == torch.float32)
+    d.norm, d.eps = norm, float(eps)
+    d.ln_weight = ln_w.data_ptr() if ln_w is not None else None
+    d.ln_bias = ln_b.data_ptr() if ln_b is not None else None
+    d.shift = shift.data_ptr() if shift is not None else None
+    d.scale = scale.data_ptr() if scale is not None else None
+    d.mod_bs, d.mod_rs = mod_strides
+    d.nseg = len(segs)
+    for i, (c0, wt) in enumerate(segs):
+        d.seg_col0[i], d.seg_weight[i] = c0, wt.data_ptr()
+    d.seg_width = seg_width
+    if rope is not None:
+        cs, sn, trs, tes, hd, seq = rope
+        d.rope_cos, d.rope_sin, d.rope_row_stride, d.rope_elem_stride = cs.data_ptr(), sn.data_ptr(), trs, tes
+        d.head_dim, d.seq_len = hd, seq
+    if nout is not None:
+        d.nout, d.ldn = nout.data_ptr(), nout.stride(0)
+    call("fam_rowop", C.byref(d), _stream(out))
+    del keep
 
 
 # --------------------------------------------------------------------------- sampler

@@ -123,9 +123,19 @@ typedef struct fam_attn_desc {
   int64_t batch, heads, sq, sk0, sk1, head_dim;
   float scale;
   const void* mask; int mask_kind; int64_t mask_bs, mask_hs, mask_qs;
+  int num_splits; float* part_o; float* part_ml;
 } fam_attn_desc;
 
 int fam_attention(const fam_attn_desc* d, void* stream);
+
+/*
+ * Key split over workgroups (Sq <= 32, or <= 64 for head_dim < 128): with num_splits = S > 1,
+ * fam_attention writes, instead of o, the unnormalised partial output of each split to
+ * part_o [S][B*H][Sq][head_dim] (fp32) and its (running max in log2 units, sum) to
+ * part_ml [S][B*H][Sq][2]; fam_attention_combine then merges the splits in order into o.
+ * The caller allocates both buffers.  Two launches, no cross-workgroup synchronisation.
+ */
+int fam_attention_combine(const fam_attn_desc* d, void* stream);
 
 /* GEMM prologues (applied to each row of A before the product) and activations. */
 #define FAM_PRO_NONE 0
@@ -171,6 +181,70 @@ typedef struct fam_gemm_desc {
 } fam_gemm_desc;
 
 int fam_gemm(const fam_gemm_desc* d, void* stream);
+
+/*
+ * fam_gemm_partial -- split-K product for 1 <= M <= 64 rows without any cross-workgroup
+ * traffic: partials[z][m][n] = sum over k in split z of a[m, k] * w[n, k], fp32,
+ * z < fam_gemm_partial_splits(M, N, K) (a deterministic function of the shape).  The caller
+ * allocates splits*M*N floats and sums them with fam_rowop, which also applies the
+ * epilogue.  a [M, K] and w [N, K] bf16 (nn.Linear layout).
+ * Replaces: the projections of the action tokens (q/k/v/o, cross q/o, FFN up/down, head;
+ *           FB/wan_video_dit.py:188-191,215-218,262-263, FB/action_dit.py:317-318) and the
+ *           reference's split-K kernel fastwam::skmm (FG/mot.py:1080-1243).
+ * Limits: M <= 64; K % 8 == 0; lda, ldw multiples of 8; 16-byte aligned a, w, partials.
+ */
+int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64_t ldw, float* partials,
+                     int64_t M, int64_t N, int64_t K, void* stream);
+int fam_gemm_partial_splits(int64_t M, int64_t N, int64_t K);
+
+/* Row sources and row normalisations for fam_rowop. */
+#define FAM_ROWSRC_PARTIALS 0   /* sum of fam_gemm_partial splits                 */
+#define FAM_ROWSRC_SMALLK 1     /* x_in [M, k_in] fp32 times w_in [N, k_in] bf16  */
+#define FAM_ROWNORM_NONE 0
+#define FAM_ROWNORM_LAYERNORM 1 /* LN(row) [* ln_weight + ln_bias]                */
+#define FAM_ROWNORM_ADALN 2     /* LN(row) * (1 + scale) + shift                  */
+#define FAM_ROWNORM_RMS 3       /* RMSNorm (+ RoPE) of 1 or 2 column segments     */
+
+/*
+ * fam_rowop -- one workgroup per row m < M of width N:
+ *   v = source(m, n) + bias[n];  v = act(v);
+ *   if res: v = res[m, n] + g(m, n) * v  (g as in fam_gemm: gate[(m/rpb)*gate_bs +
+ *           (m%rpb)*gate_rs + n*gate_ns], 1 without a gate);
+ *   out[m, n] = v  (bf16, or fp32 with res when out_f32);
+ *   then, on the stored row:
+ *     LAYERNORM  nout = LN(v) [* ln_weight + ln_bias]
+ *     ADALN      nout = LN(v) * (1 + scale) + shift, modulation indexed like fam_adaln
+ *     RMS        for each segment g < nseg: columns [seg_col0[g], seg_col0[g] + seg_width):
+ *                nout = rope(bf16(bf16(v * rsqrt(mean(v^2) + eps)) * seg_weight[g][col])),
+ *                rope as in fam_rmsnorm_rope (skipped when rope_cos == NULL; position =
+ *                m % seq_len); other columns of nout are not written (nout may equal out).
+ * LN statistics are biased-variance, eps inside the rsqrt, fp32, reduced in a fixed order.
+ * Replaces the epilogues and the norms between the reference's projections:
+ *   gate/residual  FB/wan_video_dit.py:232-237,282-285;  adaln_forward FB/fused_adaln.py:513-523;
+ *   norm3          FB/wan_video_dit.py:261,283;  RMSNorm + rope_apply FB/wan_video_dit.py:156-167,58-70;
+ *   GELU           FB/wan_video_dit.py:262;  the reference's fused epilogue kernels fastwam::skpost,
+ *   qkv_post, res_ln* (FG/mot.py:1280-1348, 786-816, 1771-1941); the Euler update of
+ *   geak_head::mmx (DG/modules/action_model/ActionDiT.py:1260-1272) with out_f32.
+ * Limits: 1 <= N <= 4096; a normalised row must be bf16 (out_f32 == 0).
+ */
+typedef struct fam_rowop_desc {
+  int src;
+  const float* partials; int64_t splits, split_stride;
+  const float* x_in; int64_t ldx, k_in; const void* w_in;
+  int64_t M, N;
+  const void* bias; int act;
+  const void* res; int64_t ldr;
+  const void* gate; int64_t gate_bs, gate_rs, gate_ns; int64_t rows_per_batch;
+  void* out; int64_t ldo; int out_f32;
+  int norm; float eps;
+  const void* ln_weight; const void* ln_bias;
+  const void* shift; const void* scale; int64_t mod_bs, mod_rs;
+  int nseg; int64_t seg_col0[2]; int64_t seg_width; const void* seg_weight[2];
+  const float* rope_cos; const float* rope_sin; int64_t rope_row_stride, rope_elem_stride, head_dim, seq_len;
+  void* nout; int64_t ldn;
+} fam_rowop_desc;
+
+int fam_rowop(const fam_rowop_desc* d, void* stream);
 
 /*
  * fam_linear_smallk -- y[m, n] = sum_k x[m, k] w[n, k] + b[n] for small, unaligned K

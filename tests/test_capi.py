@@ -58,7 +58,8 @@ def _c_offsets(struct: str, fields):
     return vals[0], vals[1:]
 
 
-@pytest.mark.parametrize("cls,cname", [(_capi.AttnDesc, "fam_attn_desc"), (_capi.GemmDesc, "fam_gemm_desc")])
+@pytest.mark.parametrize("cls,cname", [(_capi.AttnDesc, "fam_attn_desc"), (_capi.GemmDesc, "fam_gemm_desc"),
+                                       (_capi.RowopDesc, "fam_rowop_desc")])
 def test_struct_layout_matches_header(cls, cname):
     fields = [f for f, _ in cls._fields_]
     size, offs = _c_offsets(cname, fields)
@@ -103,6 +104,36 @@ def test_validation_rejects_before_launch(lib):
     assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_INVALID_ARG
     a.mask_kind = 7
     assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_INVALID_ARG
+
+    a.mask_kind, a.num_splits = 0, 4  # key splits without partial buffers
+    assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_attention_combine(C.byref(a), None) == _capi.FAM_ERR_INVALID_ARG
+    a.num_splits = 65
+    assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_INVALID_ARG
+
+    # split-K partials: M above 64, unaligned K, misaligned partial buffer
+    assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 65, 64, 64, None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 4, 64, 60, None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_gemm_partial(16, 64, 32, 64, 52, 4, 64, 64, None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_gemm_partial_splits(32, 3072, 1024) * 8 >= 32  # every k-step covered
+    assert lib.fam_gemm_partial_splits(0, 64, 64) == 0
+
+    r = _capi.RowopDesc()
+    r.src, r.partials, r.splits, r.split_stride = _capi.FAM_ROWSRC_PARTIALS, 16, 2, 4 * 64
+    r.M, r.N, r.out, r.ldo, r.rows_per_batch = 4, 64, 32, 64, 4
+    r.norm = _capi.FAM_ROWNORM_ADALN  # AdaLN without a norm output / modulation
+    assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG
+    r.nout, r.ldn = 48, 64
+    assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG
+    assert "shift" in _err(lib)
+    r.norm, r.nseg, r.seg_width = _capi.FAM_ROWNORM_RMS, 1, 6  # segment width not a multiple of 4
+    assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG
+    r.norm, r.nseg, r.N, r.ldo = _capi.FAM_ROWNORM_NONE, 0, 20000, 20000  # N beyond one workgroup row
+    assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG
+    r.N, r.ldo, r.split_stride = 64, 64, 10  # partial planes overlap
+    assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG
+    r.split_stride, r.src = 256, 9
+    assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG
 
     assert lib.fam_linear_smallk(16, 7, 0, 32, None, 48, 64, 4, 64, 65, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_euler_step(16, 32, None, 48, 10, 10, None) == _capi.FAM_ERR_INVALID_ARG

@@ -298,3 +298,147 @@ def test_sinusoid_and_modulation():
     _capi.call("fam_add_modulation", tm_d.data_ptr(), mod_d.data_ptr(), o.data_ptr(), 3, 5, 48,
                torch.cuda.current_stream().cuda_stream)
     assert torch.equal(o.cpu(), mod[None] + tm[:, None])
+
+
+# --------------------------------------------------------------------------- split-K partials + row kernel
+@pytest.mark.parametrize("M,N,K", [(32, 3072, 1024), (32, 1024, 4096), (32, 7, 1024), (1, 64, 8), (7, 1000, 256),
+                                    (64, 4096, 1024), (17, 2048, 1000), (33, 96, 64)])
+def test_gemm_partial_rowop(M, N, K):
+    """Split-K partials summed in split order by the row kernel = linear; bit-identical reruns."""
+    x, w, b = rnd(M, K, seed=70), rnd(N, K, seed=71, scale=0.02), rnd(N, seed=72, scale=0.02)
+    ref = O.linear(x.float(), w.float(), b.float())
+    xd, wd, bd = dev(x), dev(w), dev(b)
+    outs = []
+    for _ in range(2):
+        part, S = ops().gemm_partial(xd, wd)
+        assert S >= 1 and part.shape == (S, M, N)
+        y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+        ops().rowop(y, partials=part, bias=bd)
+        outs.append(y)
+    assert relerr(outs[0], ref) <= TOL
+    assert torch.equal(outs[0], outs[1])
+    # the partials alone add up to the product (fp32 sum of the split planes)
+    assert relerr(part.sum(0), O.linear(x.float(), w.float(), None)) <= 1e-3
+
+
+@pytest.mark.parametrize("M,rpb", [(32, 32), (96, 32)])
+def test_rowop_gelu_gate_residual_adaln(M, rpb):
+    """out = res + gate[b] * gelu(a w^T + b), then AdaLN(out) for the next block (FB/wan_video_dit.py:281-288)."""
+    from fam import _capi
+    K, N = 4096, 1024
+    B = M // rpb
+    a, w, b = rnd(M, K, seed=73), rnd(N, K, seed=74, scale=0.02), rnd(N, seed=75, scale=0.02)
+    res, gate = rnd(M, N, seed=76), rnd(B, N, seed=77, scale=0.2)
+    sh, sc = rnd(B, N, seed=78, scale=0.1), rnd(B, N, seed=79, scale=0.1)
+    ref = res.float() + gate.float().repeat_interleave(rpb, 0) * O.gelu_tanh(O.linear(a.float(), w.float(), b.float()))
+    ad, wd = dev(a), dev(w)
+    out, h = dev(res.clone()), torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    bd, gd, shd, scd = dev(b), dev(gate), dev(sh), dev(sc)
+    for m0 in range(0, M, 64):  # partials cover <= 64 rows per call
+        m1 = min(M, m0 + 64)
+        part, _ = ops().gemm_partial(ad[m0:m1], wd)
+        ops().rowop(out[m0:m1], partials=part, bias=bd, act=_capi.FAM_ACT_GELU_TANH, res=out[m0:m1],
+                    gate=gd[m0 // rpb:], gate_strides=(N, 0, 1), rows_per_batch=rpb,
+                    norm=_capi.FAM_ROWNORM_ADALN, eps=1e-6, shift=shd[m0 // rpb:], scale=scd[m0 // rpb:],
+                    mod_strides=(N, 0), nout=h[m0:m1])
+    assert relerr(out, ref) <= TOL
+    ob = out.float().cpu().reshape(B, rpb, N)  # the norm reads the stored bf16 row
+    href = O.adaln(ob, sh.float()[:, None], sc.float()[:, None], 1e-6).reshape(M, N)
+    assert relerr(h, href) <= TOL
+
+
+def test_rowop_layernorm_affine():
+    from fam import _capi
+    M, K, N = 32, 1024, 1024
+    a, w, b = rnd(M, K, seed=80), rnd(N, K, seed=81, scale=0.02), rnd(N, seed=82, scale=0.02)
+    lw, lb = rnd(N, seed=83, scale=0.3) + 1, rnd(N, seed=84, scale=0.3)
+    part, _ = ops().gemm_partial(dev(a), dev(w))
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    h = torch.empty_like(out)
+    lwd, lbd, bd = dev(lw), dev(lb), dev(b)
+    ops().rowop(out, partials=part, bias=bd, norm=_capi.FAM_ROWNORM_LAYERNORM, eps=1e-6, ln_w=lwd, ln_b=lbd, nout=h)
+    assert relerr(out, O.linear(a.float(), w.float(), b.float())) <= TOL
+    assert relerr(h, O.layer_norm(out.float().cpu(), lw.float(), lb.float(), 1e-6)) <= TOL
+
+
+def test_rowop_rms_segments_rope():
+    """Fused QKV row: q and k segments RMS-normalised and rotated, v passed through
+    (FB/wan_video_dit.py:116-131 with rope_apply :49-55)."""
+    from fam import _capi
+    S, H, Dh, K = 32, 16, 64, 1024
+    A = H * Dh
+    a, w, b = rnd(S, K, seed=85), rnd(3 * A, K, seed=86, scale=0.02), rnd(3 * A, seed=87, scale=0.02)
+    wq, wk = rnd(A, seed=88, scale=0.2) + 1, rnd(A, seed=89, scale=0.2) + 1
+    fr = O.action_freqs(Dh, S)
+    cs, sn, trs, tes = ops().rope_tables(fr, "complex", torch.device("cuda"))
+    part, _ = ops().gemm_partial(dev(a), dev(w))
+    qkv = torch.empty(S, 3 * A, dtype=torch.bfloat16, device="cuda")
+    wqd, wkd, bd = dev(wq), dev(wk), dev(b)
+    ops().rowop(qkv, partials=part, bias=bd, norm=_capi.FAM_ROWNORM_RMS, eps=1e-6, segs=[(0, wqd), (A, wkd)],
+                seg_width=A, rope=(cs, sn, trs, tes, Dh, S), nout=qkv)
+    lin = O.linear(a.float(), w.float(), b.float()).to(torch.bfloat16).float()
+    qr = O.rope_apply(O.rms_norm(lin[None, :, :A], wq.float(), 1e-6), fr, H)[0]
+    kr = O.rope_apply(O.rms_norm(lin[None, :, A:2 * A], wk.float(), 1e-6), fr, H)[0]
+    y = qkv.cpu()
+    assert relerr(y[:, :A], qr) <= TOL
+    assert relerr(y[:, A:2 * A], kr) <= TOL
+    assert relerr(y[:, 2 * A:], lin[:, 2 * A:]) <= TOL
+
+
+def test_rowop_smallk_source_fp32_input():
+    """Small-K source (the 7-wide action encoder on fp32 latents) + AdaLN of the result."""
+    from fam import _capi
+    M, K, N = 32, 7, 1024
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(90))
+    w, b = rnd(N, K, seed=91, scale=0.3), rnd(N, seed=92, scale=0.02)
+    sh, sc = rnd(1, N, seed=93, scale=0.1), rnd(1, N, seed=94, scale=0.1)
+    xd, wd, bd, shd, scd = dev(x), dev(w), dev(b), dev(sh), dev(sc)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    h = torch.empty_like(out)
+    ops().rowop(out, x_in=xd, w_in=wd, bias=bd, norm=_capi.FAM_ROWNORM_ADALN, eps=1e-6, shift=shd, scale=scd,
+                mod_strides=(N, 0), nout=h)
+    assert relerr(out, O.linear(x, w.float(), b.float())) <= TOL
+    assert relerr(h, O.adaln(out.float().cpu(), sh.float(), sc.float(), 1e-6)) <= TOL
+
+
+def test_rowop_fp32_euler_update():
+    """Head projection + Euler step on fp32 latents: lat += delta * (a w^T + b)."""
+    M, N, K = 32, 7, 1024
+    a, w, b = rnd(M, K, seed=95), rnd(N, K, seed=96, scale=0.02), rnd(N, seed=97, scale=0.02)
+    lat = torch.randn(M, N, generator=torch.Generator().manual_seed(98))
+    delta = torch.tensor([-0.0217], dtype=torch.bfloat16)
+    ref = lat + delta.float() * O.linear(a.float(), w.float(), b.float())
+    part, _ = ops().gemm_partial(dev(a), dev(w))
+    out, dd, bd = dev(lat.clone()), dev(delta), dev(b)
+    ops().rowop(out, partials=part, bias=bd, res=out, gate=dd, gate_strides=(0, 0, 0))
+    assert (out.cpu() - ref).abs().max().item() <= 1e-4
+
+
+# --------------------------------------------------------------------------- attention key splits
+@pytest.mark.parametrize("Sq,Sk,splits", [(32, 1560, 13), (32, 1560, 4), (16, 129, 2), (32, 100, 8), (1, 77, 3)])
+def test_attention_key_splits(Sq, Sk, splits):
+    """Keys divided among workgroups, partials merged by the combine kernel in split order:
+    matches the oracle, the unsplit kernel and itself bit for bit."""
+    B, H, Dh = 1, 16, 64
+    q, k, v = rnd(B, Sq, H * Dh, seed=99), rnd(B, Sk, H * Dh, seed=100), rnd(B, Sk, H * Dh, seed=101)
+    ref = O.flash_attention(q.float(), k.float(), v.float(), H)
+    qd, kd, vd = dev(q), dev(k), dev(v)
+    y1 = ops().attention_bshd(qd, kd, vd, H, num_splits=splits)
+    y2 = ops().attention_bshd(qd, kd, vd, H, num_splits=splits)
+    y0 = ops().attention_bshd(qd, kd, vd, H)
+    assert relerr(y1, ref) <= TOL
+    assert torch.equal(y1, y2)
+    assert relerr(y1, y0.float().cpu()) <= TOL
+
+
+def test_attention_key_splits_masked_rows():
+    """A split whose keys are all masked contributes nothing; a fully masked row stays 0."""
+    B, H, Sq, Sk, Dh = 2, 4, 8, 300, 128
+    q, k, v = rnd(B, Sq, H * Dh, seed=102), rnd(B, Sk, H * Dh, seed=103), rnd(B, Sk, H * Dh, seed=104)
+    m = torch.ones(B, 1, Sq, Sk, dtype=torch.bool)
+    m[:, :, :, 100:] = False      # splits past key 100 are fully masked
+    m[:, :, 2] = False            # fully masked row
+    ref = O.flash_attention(q.float(), k.float(), v.float(), H, m)
+    y = ops().attention_bshd(dev(q), dev(k), dev(v), H, mask=dev(m), num_splits=3)
+    assert relerr(y, ref) <= TOL
+    assert torch.all(y[:, 2] == 0)
