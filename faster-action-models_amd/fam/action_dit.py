@@ -263,7 +263,7 @@ class FusedActionDiT:
         # split-K partials of the action projections (one buffer, reused launch after launch)
         part_need = 0
         for (n_, k_) in ((3 * A, H), (H, A), (A, H), (Fd, H), (H, Fd), (cfg.action_dim, H)):
-            part_need = max(part_need, self.lib.fam_gemm_partial_splits(M, n_, k_) * M * n_)
+            part_need = max(part_need, self._part_splits(M, n_, k_) * M * n_)
         self.part = torch.zeros(part_need, dtype=torch.float32, device=dev)
         # key-split partials of the cross-attention: ~4 blocks of 32 keys per workgroup
         self.kv_splits = max(1, min(64, -(-ctx_len // 128)))
@@ -326,11 +326,18 @@ class FusedActionDiT:
                 raise FamError(f"{fname}[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
         self.plan.add(name, run, kernel, nbytes, flops)
 
+    def _part_splits(self, M, N, K):
+        # above 64 rows the tiled GEMM writes a single fp32 plane
+        return 1 if M > 64 else self.lib.fam_gemm_partial_splits(M, N, K)
+
     def _gemm_partial(self, name, a, w):
         """Split-K partials of a [M, K] x w[N, K]^T into self.part; returns the split count."""
         M, K = a.shape[0], w.shape[1]
         N = w.shape[0]
-        splits = self.lib.fam_gemm_partial_splits(M, N, K)
+        if M > 64:
+            self._gemm(name, a, w, None, self.part, ldo=N, out_f32=True)
+            return 1
+        splits = self._part_splits(M, N, K)
         args = (a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), self.part.data_ptr(), M, N, K)
         self.plan.add(name, _checked(self.lib, "fam_gemm_partial", *args), "gemm_partial",
                       2 * (M * K + N * K) + 4 * splits * M * N, 2 * M * N * K)
@@ -405,7 +412,7 @@ class FusedActionDiT:
 
     def _build_plan(self) -> _Plan:
         cfg, lib = self.cfg, self.lib
-        H, A, L, Dh = cfg.hidden_dim, cfg.attn_dim, cfg.num_layers, cfg.attn_head_dim
+        H, A, L, Dh, Fd = cfg.hidden_dim, cfg.attn_dim, cfg.num_layers, cfg.attn_head_dim, cfg.ffn_dim
         B, S, Lc, T = self.B, self.S, self.Lc, self.T
         M = B * S
         self.plan = plan = _Plan()

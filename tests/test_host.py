@@ -31,3 +31,26 @@ def test_rope_tables_match_oracle():
     cos, sin = AD.rope_1d_tables(64, 32)
     oc, os_ = O.rope_tables_real(O.action_freqs(64, 32))
     assert torch.equal(cos, oc) and torch.equal(sin, os_)
+
+
+def test_fused_plan_builds_on_host():
+    """The launch plan of the fused loop is assembled (descriptors validated by shape only,
+    nothing launched) for B=1 and for B*S above the 64-row partial limit."""
+    cfg = AD.ActionDiTConfig(num_layers=2, hidden_dim=64, ffn_dim=128, text_dim=48, freq_dim=32, num_heads=4,
+                             attn_head_dim=16)
+    params = AD.synthetic_params(cfg, 3)
+    for batch in (1, 4):
+        m = AD.FusedActionDiT(cfg, params, batch=batch, seq_len=32, ctx_len=200, num_steps=3, device="cpu")
+        kinds = [d["kernel"] for d in m.plan.meta]
+        # prologue: copy, sinusoid, 3 time GEMMs, modulation, 3 context GEMMs, one K-norm per layer
+        pro = 9 + cfg.num_layers
+        # per step: encoder row + per block (6 projections x 2 + self-attn + cross-attn + combine) + head x 2
+        per_block = 15 if m.kv_splits > 1 else 14
+        assert m.num_launches == pro + 3 * (1 + cfg.num_layers * per_block + 2)
+        assert kinds.count("attention") == 3 * 2 * cfg.num_layers
+        if batch * 32 > 64:
+            assert "gemm_partial" not in kinds
+        else:
+            assert kinds.count("gemm_partial") == 3 * (6 * cfg.num_layers + 1)
+    fwd = AD.FusedActionDiT(cfg, params, batch=1, seq_len=32, ctx_len=200, num_steps=1, device="cpu", mode="forward")
+    assert fwd.plan.meta[-1]["kernel"] == "rowop"
