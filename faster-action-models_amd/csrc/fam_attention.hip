@@ -311,22 +311,51 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
 }
 
 // Merge of the key-split partials: one thread per (b*h, q, 4 channels), splits in order.
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a, int64_t DH, int64_t BH) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+// Up to MAXS splits are loaded before the first use (one memory round trip); more splits
+// (MAXS = 0) take the looped form.
+template <int MAXS>
+__global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, int64_t DH, int64_t BH) {
+  const int64_t idx = (int64_t)blockIdx.x * 64 + threadIdx.x;
   const int64_t nd4 = DH / 4;
   if (idx >= BH * a.Sq * nd4) return;
   const int64_t d0 = (idx % nd4) * 4, rq = idx / nd4;   // rq = bh * Sq + q
   const int64_t q = rq % a.Sq, bh = rq / a.Sq, b = bh / a.H, h = bh - b * a.H;
-  float mx = -INFINITY;
-  for (int z = 0; z < a.splits; ++z) mx = fmaxf(mx, a.part_ml[((int64_t)z * BH * a.Sq + rq) * 2]);
+  const int64_t plane = BH * a.Sq;
   f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
   float L = 0.f;
-  if (mx != -INFINITY) {
-    for (int z = 0; z < a.splits; ++z) {
-      const int64_t row = (int64_t)z * BH * a.Sq + rq;
-      const float w = exp2f(a.part_ml[row * 2] - mx);  // an empty split has m = -inf -> 0
-      L += a.part_ml[row * 2 + 1] * w;
-      o += *reinterpret_cast<const f32x4*>(a.part_o + row * DH + d0) * w;
+  if constexpr (MAXS > 0) {
+    float2 ml[MAXS];
+    f32x4 po[MAXS];
+#pragma unroll
+    for (int z = 0; z < MAXS; ++z) {
+      const int64_t row = (int64_t)(z < a.splits ? z : a.splits - 1) * plane + rq;
+      ml[z] = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
+      po[z] = *reinterpret_cast<const f32x4*>(a.part_o + row * DH + d0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int z = 0; z < MAXS; ++z)
+      if (z < a.splits) mx = fmaxf(mx, ml[z].x);
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int z = 0; z < MAXS; ++z)
+        if (z < a.splits) {
+          const float w = exp2f(ml[z].x - mx);  // an empty split has m = -inf -> 0
+          L += ml[z].y * w;
+          o += po[z] * w;
+        }
+    }
+  } else {
+    float mx = -INFINITY;
+    for (int z = 0; z < a.splits; ++z) mx = fmaxf(mx, a.part_ml[((int64_t)z * plane + rq) * 2]);
+    if (mx != -INFINITY) {
+      for (int z = 0; z < a.splits; ++z) {
+        const int64_t row = (int64_t)z * plane + rq;
+        const float w = exp2f(a.part_ml[row * 2] - mx);
+        L += a.part_ml[row * 2 + 1] * w;
+        o += *reinterpret_cast<const f32x4*>(a.part_o + row * DH + d0) * w;
+      }
     }
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;
@@ -481,7 +510,8 @@ extern "C" int fam_attention(const fam_attn_desc* d, void* stream) {
   FAM_REQUIRE(bh <= 65535 || d->sq <= 64, FAM_ERR_UNSUPPORTED, "fam_attention: batch*heads must be <= 65535");
   FAM_REQUIRE(d->num_splits >= 0 && d->num_splits <= 64, FAM_ERR_INVALID_ARG, "fam_attention: num_splits in [0, 64]");
   const bool short_q = d->sq <= 32 || (d->sq <= 64 && Dh < 128);
-  FAM_REQUIRE(d->num_splits <= 1 || (short_q && d->part_o && d->part_ml && fam_host::aligned16(d->part_o)),
+  FAM_REQUIRE(d->num_splits <= 1 || (short_q && d->part_o && d->part_ml && fam_host::aligned16(d->part_o) &&
+                                     (reinterpret_cast<uintptr_t>(d->part_ml) & 7u) == 0),
               FAM_ERR_INVALID_ARG, "fam_attention: key splits need Sq <= 32 (<= 64 for Dh < 128) and 16-byte aligned partial buffers");
   if (d->batch == 0 || d->sq == 0) return FAM_OK;
 
@@ -513,7 +543,8 @@ extern "C" int fam_attention_combine(const fam_attn_desc* d, void* stream) {
   FAM_REQUIRE(d->num_splits >= 2 && d->part_o && d->part_ml && d->o, FAM_ERR_INVALID_ARG,
               "fam_attention_combine: needs num_splits >= 2, the partial buffers and o");
   FAM_REQUIRE(d->head_dim % 4 == 0 && d->head_dim >= 8 && d->o_bs % 8 == 0 && d->o_rs % 8 == 0 && d->o_hs % 8 == 0 &&
-                  fam_host::aligned16(d->o) && fam_host::aligned16(d->part_o),
+                  fam_host::aligned16(d->o) && fam_host::aligned16(d->part_o) &&
+                  (reinterpret_cast<uintptr_t>(d->part_ml) & 7u) == 0,
               FAM_ERR_INVALID_ARG, "fam_attention_combine: bad head_dim, strides or alignment");
   const int64_t bh = d->batch * d->heads;
   if (bh == 0 || d->sq == 0) return FAM_OK;
@@ -522,7 +553,11 @@ extern "C" int fam_attention_combine(const fam_attn_desc* d, void* stream) {
   a.H = d->heads; a.Sq = d->sq;
   a.splits = d->num_splits; a.part_o = d->part_o; a.part_ml = d->part_ml;
   const int64_t n = bh * d->sq * (d->head_dim / 4);
-  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a,
-                     d->head_dim, bh);
+  const dim3 grid((unsigned)((n + 63) / 64));
+  hipStream_t s = (hipStream_t)stream;
+  if (a.splits <= 4) hipLaunchKernelGGL((attn_combine_kernel<4>), grid, dim3(64), 0, s, a, d->head_dim, bh);
+  else if (a.splits <= 8) hipLaunchKernelGGL((attn_combine_kernel<8>), grid, dim3(64), 0, s, a, d->head_dim, bh);
+  else if (a.splits <= 16) hipLaunchKernelGGL((attn_combine_kernel<16>), grid, dim3(64), 0, s, a, d->head_dim, bh);
+  else hipLaunchKernelGGL((attn_combine_kernel<0>), grid, dim3(64), 0, s, a, d->head_dim, bh);
   return fam_host::check_launch("fam_attention_combine");
 }

@@ -189,9 +189,218 @@ __global__ __launch_bounds__(RT) void rowop_kernel(RowArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------------------
+// rowop_vec_kernel: the split-K source with every operand 4-column aligned.  NW waves hold
+// 4 consecutive columns per thread (N <= 256 * NW); all global loads of the row (up to
+// MAXS partial planes, bias, residual, gate, modulation, norm weights, RoPE tables) are
+// issued before the first use, so a row costs one memory round trip instead of one per
+// operand.
+__device__ __forceinline__ void ld4(const bf16* p, float o[4]) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = to_f(v[e]);
+}
+
+template <int NW>
+__device__ __forceinline__ float block_sum_nw(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) t += red[w];
+  return t;
+}
+
+template <int NW>
+__device__ __forceinline__ void block_sum2_nw(float& a, float& b, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  a = wave_sum(a);
+  b = wave_sum(b);
+  __syncthreads();
+  if (lane == 0) { red[wave] = a; red[NW + wave] = b; }
+  __syncthreads();
+  float ta = 0.f, tb = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) { ta += red[w]; tb += red[NW + w]; }
+  a = ta;
+  b = tb;
+}
+
+template <int NW, int MAXS>
+__global__ __launch_bounds__(NW * 64) void rowop_vec_kernel(RowArgs a) {
+  __shared__ float red[2 * NW];
+  const int tid = threadIdx.x;
+  const int64_t m = blockIdx.x;
+  const int64_t bi = m / a.rpb, si = m - bi * a.rpb;
+  const int64_t c = (int64_t)tid * 4;
+  const bool act = c < a.N;
+  const int64_t cs = act ? c : 0;  // a valid column for inactive threads' loads
+
+  // ---- phase 1: every load of the row
+  f32x4 pz[MAXS];
+  const int64_t ns = a.splits;
+#pragma unroll
+  for (int z = 0; z < MAXS; ++z) {
+    const int64_t zz = z < ns ? z : ns - 1;
+    pz[z] = *reinterpret_cast<const f32x4*>(a.part + zz * a.split_stride + m * a.N + cs);
+  }
+  float bias[4] = {0.f, 0.f, 0.f, 0.f}, res[4] = {0.f, 0.f, 0.f, 0.f}, gate[4] = {1.f, 1.f, 1.f, 1.f};
+  if (a.bias) ld4(a.bias + cs, bias);
+  if (a.res) {
+    if (a.out_f32) {
+      const f32x4 r = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.res) + m * a.ldr + cs);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) res[e] = r[e];
+    } else {
+      ld4(reinterpret_cast<const bf16*>(a.res) + m * a.ldr + cs, res);
+    }
+  }
+  if (a.gate) {
+    const bf16* gp = a.gate + bi * a.gbs + si * a.grs;
+    if (a.gns == 0) {
+      const float g = to_f(gp[0]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) gate[e] = g;
+    } else {
+      ld4(gp + cs, gate);
+    }
+  }
+  float na[4] = {0.f, 0.f, 0.f, 0.f}, nb[4] = {0.f, 0.f, 0.f, 0.f};  // norm operands
+  float rc[2] = {1.f, 1.f}, rsn[2] = {0.f, 0.f};                       // RoPE of the 2 pairs
+  int seg = -1;
+  if (a.norm == FAM_ROWNORM_ADALN) {
+    const int64_t mo = bi * a.mbs + si * a.mrs;
+    ld4(a.scale + mo + cs, na);
+    ld4(a.shift + mo + cs, nb);
+  } else if (a.norm == FAM_ROWNORM_LAYERNORM) {
+    if (a.nw) ld4(a.nw + cs, na); else { na[0] = na[1] = na[2] = na[3] = 1.f; }
+    if (a.nb) ld4(a.nb + cs, nb);
+  } else if (a.norm == FAM_ROWNORM_RMS) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+      if (g < a.nseg && c >= a.seg0[g] && c < a.seg0[g] + a.segw) seg = g;
+    if (act && seg >= 0) {
+      const int64_t cl = c - a.seg0[seg];
+      ld4(a.segwt[seg] + cl, na);
+      if (a.cs) {
+        const int64_t pos = m % a.seq;
+        const int64_t j0 = (cl % a.hd) >> 1;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int64_t t = pos * a.trs + (j0 + p) * a.tes;
+          rc[p] = a.cs[t];
+          rsn[p] = a.sn[t];
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- phase 2: sum the planes in split order, epilogue, store
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int z = 0; z < MAXS; ++z)
+    if (z < ns) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += pz[z][e];
+    }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float x = act_fn(v[e] + bias[e], a.act);
+    if (a.res) x = res[e] + gate[e] * x;
+    v[e] = x;
+  }
+  if (a.out_f32) {
+    if (act) {
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = v[e];
+      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(a.out) + m * a.ldo + c) = o;
+    }
+  } else {
+    bf16x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = to_bf(v[e]);
+      v[e] = to_f(o[e]);  // the stored (rounded) value feeds the normalisation
+    }
+    if (act) *reinterpret_cast<bf16x4*>(reinterpret_cast<bf16*>(a.out) + m * a.ldo + c) = o;
+  }
+  if (a.norm == FAM_ROWNORM_NONE) return;
+
+  bf16x4 o;
+  if (a.norm == FAM_ROWNORM_LAYERNORM || a.norm == FAM_ROWNORM_ADALN) {
+    const float s = act ? (v[0] + v[1]) + (v[2] + v[3]) : 0.f;
+    const float mean = block_sum_nw<NW>(s, red) / (float)a.N;
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d = act ? v[e] - mean : 0.f;
+      q += d * d;
+    }
+    const float rstd = rsqrtf(block_sum_nw<NW>(q, red) / (float)a.N + a.eps);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float y = (v[e] - mean) * rstd;
+      o[e] = to_bf(a.norm == FAM_ROWNORM_LAYERNORM ? y * na[e] + nb[e] : y * (1.0f + na[e]) + nb[e]);
+    }
+    if (act) *reinterpret_cast<bf16x4*>(a.nout + m * a.ldn + c) = o;
+    return;
+  }
+
+  // RMSNorm over each segment (one combined reduction for both), then RoPE on the pairs
+  float q0 = 0.f, q1 = 0.f;
+  if (act && seg >= 0) {
+    const float q = (v[0] * v[0] + v[1] * v[1]) + (v[2] * v[2] + v[3] * v[3]);
+    if (seg == 0) q0 = q; else q1 = q;
+  }
+  block_sum2_nw<NW>(q0, q1, red);
+  if (!act || seg < 0) return;
+  const float rs = rsqrtf((seg == 0 ? q0 : q1) / (float)a.segw + a.eps);
+  float y[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)  // bf16 before the weight multiply, as RMSNorm.forward
+    y[e] = to_f(to_bf(to_f(to_bf(v[e] * rs)) * na[e]));
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const float x0 = y[2 * p], x1 = y[2 * p + 1];
+    y[2 * p] = x0 * rc[p] - x1 * rsn[p];
+    y[2 * p + 1] = x0 * rsn[p] + x1 * rc[p];
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = to_bf(y[e]);
+  *reinterpret_cast<bf16x4*>(a.nout + m * a.ldn + c) = o;
+}
+
 }  // namespace fam
 
 using namespace fam;
+
+// The vectorised kernel takes the split-K source with <= 16 planes when every operand row
+// starts on a 4-column boundary; anything else runs the generic per-element kernel.
+static bool vec_eligible(const fam_rowop_desc* d) {
+  auto al = [](const void* p, unsigned b) { return (reinterpret_cast<uintptr_t>(p) & (b - 1)) == 0; };
+  if (d->src != FAM_ROWSRC_PARTIALS || d->N % 4 != 0 || d->splits > 16 || d->ldo % 4 != 0) return false;
+  if (!al(d->out, d->out_f32 ? 16 : 8) || (d->bias && !al(d->bias, 8))) return false;
+  if (d->res && (d->ldr % 4 != 0 || !al(d->res, d->out_f32 ? 16 : 8))) return false;
+  if (d->gate && !(d->gate_ns == 0 || (d->gate_ns == 1 && d->gate_bs % 4 == 0 && d->gate_rs % 4 == 0 &&
+                                       al(d->gate, 8))))
+    return false;
+  if (d->norm != FAM_ROWNORM_NONE && (d->ldn % 4 != 0 || !al(d->nout, 8))) return false;
+  if (d->norm == FAM_ROWNORM_ADALN &&
+      (d->mod_bs % 4 != 0 || d->mod_rs % 4 != 0 || !al(d->shift, 8) || !al(d->scale, 8)))
+    return false;
+  if (d->norm == FAM_ROWNORM_LAYERNORM && ((d->ln_weight && !al(d->ln_weight, 8)) || (d->ln_bias && !al(d->ln_bias, 8))))
+    return false;
+  if (d->norm == FAM_ROWNORM_RMS)
+    for (int g = 0; g < d->nseg; ++g)
+      if (!al(d->seg_weight[g], 8)) return false;
+  return true;
+}
 
 extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
   FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_rowop: null descriptor");
@@ -260,6 +469,17 @@ extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
   a.nout = (bf16*)d->nout; a.ldn = d->ldn;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)d->M);
+  if (vec_eligible(d)) {
+    const int nw = d->N <= 1024 ? 4 : (d->N <= 2048 ? 8 : 16);
+    const int ms = d->splits <= 4 ? 4 : (d->splits <= 8 ? 8 : 16);
+#define FAM_ROWVEC(NW_, MS_) \
+  if (nw == NW_ && ms == MS_) hipLaunchKernelGGL((rowop_vec_kernel<NW_, MS_>), grid, dim3(NW_ * 64), 0, s, a)
+    FAM_ROWVEC(4, 4); FAM_ROWVEC(4, 8); FAM_ROWVEC(4, 16);
+    FAM_ROWVEC(8, 4); FAM_ROWVEC(8, 8); FAM_ROWVEC(8, 16);
+    FAM_ROWVEC(16, 4); FAM_ROWVEC(16, 8); FAM_ROWVEC(16, 16);
+#undef FAM_ROWVEC
+    return fam_host::check_launch("fam_rowop");
+  }
   if (d->N <= 4 * RT) hipLaunchKernelGGL(rowop_kernel<1>, grid, dim3(RT), 0, s, a);
   else if (d->N <= 8 * RT) hipLaunchKernelGGL(rowop_kernel<2>, grid, dim3(RT), 0, s, a);
   else hipLaunchKernelGGL(rowop_kernel<4>, grid, dim3(RT), 0, s, a);

@@ -442,3 +442,26 @@ def test_attention_key_splits_masked_rows():
     y = ops().attention_bshd(dev(q), dev(k), dev(v), H, mask=dev(m), num_splits=3)
     assert relerr(y, ref) <= TOL
     assert torch.all(y[:, 2] == 0)
+
+
+def test_rowop_generic_path_matches_vector_path():
+    """Rows that do not start on a 4-column boundary take the per-element kernel: same
+    stored row (same split order), same normalised row within rounding."""
+    from fam import _capi
+    M, K, N = 32, 1024, 1024
+    a, w, b = rnd(M, K, seed=105), rnd(N, K, seed=106, scale=0.02), rnd(N, seed=107, scale=0.02)
+    res = rnd(M, N, seed=108)
+    sh, sc = rnd(1, N, seed=109, scale=0.1), rnd(1, N, seed=110, scale=0.1)
+    part, _ = ops().gemm_partial(dev(a), dev(w))
+    bd, shd, scd = dev(b), dev(sh), dev(sc)
+    outs = []
+    for pad in (0, 2):   # pad 2: row pitch N + 2 is not a multiple of 4 columns
+        buf = torch.zeros(M, N + pad, dtype=torch.bfloat16, device="cuda")
+        out = buf[:, :N]
+        out.copy_(dev(res))
+        h = torch.zeros(M, N + pad, dtype=torch.bfloat16, device="cuda")[:, :N]
+        ops().rowop(out, partials=part, bias=bd, res=out, norm=_capi.FAM_ROWNORM_ADALN, eps=1e-6,
+                    shift=shd, scale=scd, mod_strides=(N, 0), nout=h)
+        outs.append((out.cpu(), h.cpu()))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert relerr(outs[1][1], outs[0][1].float()) <= 1e-2
