@@ -20,13 +20,13 @@
 //   Bytes per launch (HBM roofline numerator): 2*(N*K + M*K + M*N) + bias/residual/modulation.
 //
 // partial_kernel (M <= 64, used by the fused action expert): split-K without any
-// cross-workgroup traffic.  A workgroup of 4 waves owns 64 output columns (16 per wave) over
-// one K slice; the activation slice [M x Kc] is staged once in LDS and shared by the 4
-// waves, so each workgroup reads 64*Kc weights and only M*Kc activations.  K is split so
-// that ~256-384 workgroups stream the weights (on gfx950 the per-CU memory parallelism, not
-// HBM, limits a skinny product spread over few CUs).  The fp32 partials partial[z][m][n]
-// are summed, in split order, by the row kernel that follows (fam_rowop), which also runs
-// the epilogue and the next normalisation on whole rows.
+// cross-workgroup traffic.  A workgroup of 4 waves owns 16 output columns over one K slice
+// and its waves split the slice again (summed through LDS); every weight and activation
+// fragment of a wave is loaded before the first MFMA.  The slice length is chosen so that
+// >= 256 workgroups stream the weights (on gfx950 the per-CU memory parallelism, not HBM,
+// limits a skinny product spread over few CUs) with as few partial planes as possible.  The
+// fp32 partials partial[z][m][n] are summed, in split order, by the row kernel that follows
+// (fam_rowop), which also runs the epilogue and the next normalisation on whole rows.
 //
 // tiled_kernel (M > 64: the per-call context projections, batched throughput points):
 //   * 256-thread workgroup, BM x BN output tile (64x64 or 128x128), 2x2 waves of 16x16 MFMA
@@ -248,7 +248,12 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------------------
-// partial_kernel: MT m-tiles (M <= 16*MT), STEPS 32-wide k-steps per split (Kc = 32*STEPS).
+// partial_kernel: MT m-tiles (M <= 16*MT).  A workgroup owns 16 output columns over one K
+// slice of 4*32*STEPS; each of its 4 waves takes a quarter of the slice with every load
+// (STEPS weight fragments, MT*STEPS activation fragments) issued before the first MFMA, and
+// the 4 wave accumulators are summed through LDS in wave order.  The product is computed
+// transposed, D = W A^T, so a lane ends with 4 consecutive columns of one row: one 16-byte
+// store per m-tile.
 struct PartArgs {
   const bf16* a; int64_t lda;
   const bf16* w; int64_t ldw;
@@ -258,64 +263,58 @@ struct PartArgs {
 
 template <int MT, int STEPS>
 __global__ __launch_bounds__(256) void partial_kernel(PartArgs g) {
-  constexpr int MR = MT * 16;
-  constexpr int KC = 32 * STEPS;
-  constexpr int CH = MR * KC / 8;              // 16-byte activation chunks per workgroup
-  constexpr int CPT = (CH + 255) / 256;        // chunks per thread
-  __shared__ bf16 As[MR][KC + 8];
-
+  __shared__ f32x4 red[4][MT][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
-  const int64_t n = (int64_t)blockIdx.x * 64 + wave * 16 + l16;   // this lane's weight row
-  const int64_t z = blockIdx.y, kbase = z * KC;
-  const bool nok = n < g.N;
-  const bf16* wrow = g.w + (nok ? n : 0) * g.ldw;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t z = blockIdx.y;
+  const int64_t kw = z * (4 * 32 * STEPS) + (int64_t)wave * (32 * STEPS) + lg * 8;  // this lane's first k
 
-  bf16x8 wf[STEPS], ac[CPT];
+  const int64_t wn = n0 + l16;
+  const bool wrow = wn < g.N;
+  const bf16* wp = g.w + (wrow ? wn : 0) * g.ldw;
+  bf16x8 wf[STEPS], af[MT][STEPS];
 #pragma unroll
-  for (int j = 0; j < STEPS; ++j) {
-    const int64_t k = kbase + j * 32 + lg * 8;
-    wf[j] = load8_if(nok && k < g.K, wrow + k, g.w);
+  for (int s = 0; s < STEPS; ++s) {
+    const int64_t k = kw + s * 32;
+    wf[s] = load8_if(wrow && k < g.K, wp + k, g.w);
   }
 #pragma unroll
-  for (int p = 0; p < CPT; ++p) {
-    const int c = tid + 256 * p, r = c / (KC / 8), kc = (c % (KC / 8)) * 8;
-    const int64_t k = kbase + kc;
-    ac[p] = load8_if(c < CH && r < g.M && k < g.K, g.a + r * g.lda + k, g.a);
-  }
-  __builtin_amdgcn_sched_barrier(0);  // every load of the workgroup is in flight here
+  for (int t = 0; t < MT; ++t) {
+    const int64_t m = t * 16 + l16;
+    const bool arow = m < g.M;
+    const bf16* ap = g.a + (arow ? m : 0) * g.lda;
 #pragma unroll
-  for (int p = 0; p < CPT; ++p) {
-    const int c = tid + 256 * p;
-    if (c < CH) *reinterpret_cast<bf16x8*>(&As[c / (KC / 8)][(c % (KC / 8)) * 8]) = ac[p];
+    for (int s = 0; s < STEPS; ++s) {
+      const int64_t k = kw + s * 32;
+      af[t][s] = load8_if(arow && k < g.K, ap + k, g.a);
+    }
   }
-  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);
 
   f32x4 acc[MT];
 #pragma unroll
-  for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < MT; ++t) {
+    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < STEPS; ++j)
+    for (int s = 0; s < STEPS; ++s) acc[t] = mfma16(wf[s], af[t][s], acc[t]);
+  }
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const bf16x8 af = *reinterpret_cast<const bf16x8*>(&As[i * 16 + l16][j * 32 + lg * 8]);
-      acc[i] = mfma16(wf[j], af, acc[i]);
-    }
-
-  // lane holds rows m = i*16 + l16, columns nb .. nb+3 of this split's partial
-  const int64_t nb = (int64_t)blockIdx.x * 64 + wave * 16 + lg * 4;
-  float* pz = g.part + z * g.M * g.N;
-#pragma unroll
-  for (int i = 0; i < MT; ++i) {
-    const int64_t m = i * 16 + l16;
+  for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
+  __syncthreads();
+  // wave t sums m-tile t over the 4 waves in order and stores it
+  for (int t = wave; t < MT; t += 4) {
+    const f32x4 v = ((red[0][t][lane] + red[1][t][lane]) + red[2][t][lane]) + red[3][t][lane];
+    const int64_t m = t * 16 + l16;            // D[col = 4*lg + e][row = l16]
+    const int64_t n = n0 + lg * 4;
     if (m >= g.M) continue;
-    float* dst = pz + m * g.N + nb;
-    if (nb + 3 < g.N && (g.N & 3) == 0) {
-      *reinterpret_cast<f32x4*>(dst) = acc[i];
+    float* dst = g.part + (z * g.M + m) * g.N + n;
+    if ((g.N & 3) == 0) {
+      if (n < g.N) *reinterpret_cast<f32x4*>(dst) = v;
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (nb + e < g.N) dst[e] = acc[i][e];
+        if (n + e < g.N) dst[e] = v[e];
     }
   }
 }
@@ -518,15 +517,16 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
   return fam_host::check_launch("fam_gemm");
 }
 
-// Split plan of fam_gemm_partial: k-steps per split and number of splits.
+// Split plan of fam_gemm_partial: STEPS (32-wide k-steps per wave; a workgroup covers
+// 4*32*STEPS of K) is the longest of 8, 4, 2, 1 that still gives >= 256 workgroups (one per
+// CU), so the partial planes are as few as the machine's width allows.
 static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* splits) {
-  const int64_t groups = (N + 63) / 64;
+  const int64_t groups = (N + 15) / 16;
   const int64_t ksteps = (K + 31) / 32;
-  // Longest split (8, 4, 2 or 1 k-steps of 32) that still gives one workgroup per CU.
-  int p2 = 8;
-  while (p2 > 1 && ((ksteps + p2 - 1) / p2) * groups < 256) p2 >>= 1;
-  *steps = p2;
-  *splits = (int)((ksteps + p2 - 1) / p2);
+  int st = 8;
+  while (st > 1 && ((ksteps + 4 * st - 1) / (4 * st)) * groups < 256) st >>= 1;
+  *steps = st;
+  *splits = (int)((ksteps + 4 * st - 1) / (4 * st));
   (void)M;
 }
 
@@ -539,7 +539,7 @@ extern "C" int fam_gemm_partial_splits(int64_t M, int64_t N, int64_t K) {
 
 template <int MT>
 static void launch_partial(const PartArgs& a, int steps, int splits, hipStream_t s) {
-  const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)splits);
+  const dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)splits);
   switch (steps) {
     case 1: hipLaunchKernelGGL((partial_kernel<MT, 1>), grid, dim3(256), 0, s, a); break;
     case 2: hipLaunchKernelGGL((partial_kernel<MT, 2>), grid, dim3(256), 0, s, a); break;
@@ -558,7 +558,7 @@ extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64
               "fam_gemm_partial: lda/ldw must be >= K and multiples of 8");
   FAM_REQUIRE(fam_host::aligned16(a) && fam_host::aligned16(w) && fam_host::aligned16(partials), FAM_ERR_INVALID_ARG,
               "fam_gemm_partial: a, w and partials must be 16-byte aligned");
-  FAM_REQUIRE((N + 63) / 64 <= 65535, FAM_ERR_UNSUPPORTED, "fam_gemm_partial: N too large");
+  FAM_REQUIRE((N + 15) / 16 <= 2147483647LL, FAM_ERR_UNSUPPORTED, "fam_gemm_partial: N too large");
   if (M == 0) return FAM_OK;
   int steps, splits;
   partial_plan(M, N, K, &steps, &splits);

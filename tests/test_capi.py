@@ -115,7 +115,9 @@ def test_validation_rejects_before_launch(lib):
     assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 65, 64, 64, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 4, 64, 60, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_gemm_partial(16, 64, 32, 64, 52, 4, 64, 64, None) == _capi.FAM_ERR_INVALID_ARG
-    assert lib.fam_gemm_partial_splits(32, 3072, 1024) * 8 >= 32  # every k-step covered
+    # the split plan of the action projections: >= 256 workgroups of 16 columns, fewest planes
+    assert [lib.fam_gemm_partial_splits(32, n, k) for n, k in ((3072, 1024), (1024, 1024), (4096, 1024),
+                                                              (1024, 4096), (7, 1024))] == [2, 4, 1, 4, 8]
     assert lib.fam_gemm_partial_splits(0, 64, 64) == 0
 
     r = _capi.RowopDesc()
