@@ -141,7 +141,8 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
-  const int64_t bh = blockIdx.x, b = bh / a.H, h = bh - b * a.H;
+  const uint32_t bh32 = blockIdx.x, H32 = (uint32_t)a.H;
+  const int64_t bh = bh32, b = bh32 / H32, h = bh32 - (uint32_t)b * H32;
   // this workgroup's key blocks (split blockIdx.y of a.splits), divided among its waves
   const int64_t nkb_all = (a.Sk + KB - 1) / KB;
   const int64_t per_split = (nkb_all + a.splits - 1) / a.splits;
@@ -149,6 +150,33 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
   const int64_t wg_end = std::min(nkb_all, wg_beg + per_split);
   const int64_t per = (wg_end - wg_beg + NW - 1) / NW;
   const int64_t kb_beg = std::min(wg_end, wg_beg + (int64_t)wave * per), kb_end = std::min(wg_end, kb_beg + per);
+
+  const SegRows krows = key_rows(a, b, h), vrows = val_rows(a, b, h);
+  const int64_t Sk = a.Sk;
+  const bf16* ksafe = krows.row(0);
+  const bf16* vsafe = vrows.row(0);
+  // Raw loads of one key block from clamped addresses (no selects between the loads).  A key
+  // past Sk reads row 0: its score is masked to -inf below and its V row is weighted by 0.
+  auto gload = [&](int64_t blk, bf16x8 (&kf)[2][NC], bf16x8 (&vc)[NVC]) {
+    const int64_t kb = blk * KB;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int64_t kk = kb + kt * 16 + l16;
+        const int d0 = c * 32 + lg * 8;
+        const bool ok = kk < Sk && d0 < DH;
+        kf[kt][c] = load8(ok ? krows.row(kk) + d0 : ksafe);
+      }
+#pragma unroll
+    for (int p = 0; p < NVC; ++p) {
+      const int cidx = lane + 64 * p;
+      const int key = cidx / (DH / 8), d0 = (cidx % (DH / 8)) * 8;
+      const int64_t kk = kb + key;
+      const bool ok = cidx < KB * DH / 8 && kk < Sk;
+      vc[p] = load8(ok ? vrows.row(kk) + d0 : vsafe);
+    }
+  };
 
   bf16x8 qf[QT][NC];
   const bf16* qbase = a.q + b * a.q_bs + h * a.q_hs;
@@ -158,8 +186,19 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
     for (int c = 0; c < NC; ++c) {
       const int64_t qi = qt * 16 + l16;
       const int d0 = c * 32 + lg * 8;
-      qf[qt][c] = load8_if(qi < a.Sq && d0 < DH, qbase + qi * a.q_rs + d0, qbase);
+      qf[qt][c] = load8(qi < a.Sq && d0 < DH ? qbase + qi * a.q_rs + d0 : qbase);
     }
+  bf16x8 kA[2][NC], vA[NVC], kB[2][NC], vB[NVC];
+  if (kb_beg < kb_end) gload(kb_beg, kA, vA);
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (DH < 32) {
+    // zero-padded head dim: the padding lanes of the q fragments must be exactly 0
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        if (c * 32 + lg * 8 >= DH) qf[qt][c] = zero8();
+  }
 
   f32x4 oacc[QT][NDT];
   float m_run[QT], l_run[QT];
@@ -171,38 +210,16 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
     for (int t = 0; t < NDT; ++t) oacc[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // K fragments (A-operand rows = keys) and V chunks of one block, straight from global
-  bf16x8 kf[2][NC], vc[NVC];
-  const SegRows krows = key_rows(a, b, h), vrows = val_rows(a, b, h);
-  const int64_t Sk = a.Sk;
-  const bf16* ksafe = krows.row(0);
-  const bf16* vsafe = vrows.row(0);
-  auto gload = [&](int64_t blk) {
+  // one 32-key block: V -> this wave's transposed LDS tile, S^T = K Q^T, online softmax, O^T += V^T P^T
+  auto process = [&](int64_t blk, bf16x8 (&kf)[2][NC], const bf16x8 (&vc)[NVC]) {
     const int64_t kb = blk * KB;
+    if constexpr (DH < 32) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int64_t kk = kb + kt * 16 + l16;
-        const int d0 = c * 32 + lg * 8;
-        const bool ok = kk < Sk && d0 < DH;
-        kf[kt][c] = load8_if(ok, krows.row(ok ? kk : 0) + (ok ? d0 : 0), ksafe);
-      }
-#pragma unroll
-    for (int p = 0; p < NVC; ++p) {
-      const int cidx = lane + 64 * p;
-      const int key = cidx / (DH / 8), d0 = (cidx % (DH / 8)) * 8;
-      const int64_t kk = kb + key;
-      const bool ok = cidx < KB * DH / 8 && kk < Sk;
-      vc[p] = load8_if(ok, vrows.row(ok ? kk : 0) + (ok ? d0 : 0), vsafe);
+        for (int c = 0; c < NC; ++c)
+          if (c * 32 + lg * 8 >= DH) kf[kt][c] = zero8();
     }
-  };
-
-  if (kb_beg < kb_end) gload(kb_beg);
-  __builtin_amdgcn_sched_barrier(0);
-  for (int64_t blk = kb_beg; blk < kb_end; ++blk) {
-    const int64_t kb = blk * KB;
-    // V block -> this wave's transposed tile (LDS operations of one wave complete in order)
 #pragma unroll
     for (int p = 0; p < NVC; ++p) {
       const int cidx = lane + 64 * p;
@@ -212,14 +229,7 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
         for (int e = 0; e < 8; ++e) Vt[wave][d0 + e][key] = vc[p][e];
       }
     }
-    bf16x8 kcur[2][NC];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int c = 0; c < NC; ++c) kcur[kt][c] = kf[kt][c];
-    if (blk + 1 < kb_end) gload(blk + 1);  // next block in flight during this one's math
-    __builtin_amdgcn_sched_barrier(0);     // ... issued here, not sunk to its first use
-
+    __builtin_amdgcn_wave_barrier();
     bf16x8 vfr[NDT];
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
@@ -237,23 +247,62 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
     for (int qt = 0; qt < QT; ++qt) {
       const int64_t qi = qt * 16 + l16;
       const bool qvalid = qi < a.Sq;
-      float s[2][4];
+      float sc[2][4];
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
         f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < NC; ++c) sacc = mfma16(kcur[kt][c], qf[qt][c], sacc);
+        for (int c = 0; c < NC; ++c) sacc = mfma16(kf[kt][c], qf[qt][c], sacc);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) s[kt][e] = score(a, sacc[e], b, h, qi, qvalid, kb + kt * 16 + lg * 4 + e);
+        for (int e = 0; e < 4; ++e) sc[kt][e] = score(a, sacc[e], b, h, qi, qvalid, kb + kt * 16 + lg * 4 + e);
       }
-      const bf16x8 pf = softmax_update<NDT>(s, m_run[qt], l_run[qt], oacc[qt]);
+      const bf16x8 pf = softmax_update<NDT>(sc, m_run[qt], l_run[qt], oacc[qt]);
 #pragma unroll
       for (int t = 0; t < NDT; ++t) oacc[qt][t] = mfma16(vfr[t], pf, oacc[qt][t]);
     }
-    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_wave_barrier();  // the next block may overwrite this wave's V tile
+  };
+
+  // two register sets: the next block's loads are in flight while the current one computes
+  for (int64_t blk = kb_beg; blk < kb_end; blk += 2) {
+    if (blk + 1 < kb_end) gload(blk + 1, kB, vB);
+    __builtin_amdgcn_sched_barrier(0);
+    process(blk, kA, vA);
+    if (blk + 1 >= kb_end) break;
+    if (blk + 2 < kb_end) gload(blk + 2, kA, vA);
+    __builtin_amdgcn_sched_barrier(0);
+    process(blk + 1, kB, vB);
   }
 
   // ---- merge the waves' partial states in wave order
+  if constexpr (NW == 1) {
+    // one wave: its accumulator is the result; lanes with lg == 0 hold (m, l) of query l16
+    (void)s_m; (void)s_l;
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int64_t q = qt * 16 + l16;
+      if (q >= a.Sq) continue;
+      const float L = l_run[qt];
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) {
+        const int d0 = t * 16 + lg * 4;
+        if (d0 >= DH) continue;
+        const f32x4 v = oacc[qt][t];
+        if (a.splits > 1) {
+          const int64_t row = ((int64_t)blockIdx.y * gridDim.x + bh) * a.Sq + q;
+          *reinterpret_cast<f32x4*>(a.part_o + row * DH + d0) = v;
+          if (d0 == 0) *reinterpret_cast<float2*>(a.part_ml + row * 2) = make_float2(m_run[qt], L);
+        } else {
+          const float inv = L > 0.f ? 1.0f / L : 0.f;
+          bf16x4 ov;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ov[e] = to_bf(v[e] * inv);
+          *reinterpret_cast<bf16x4*>(a.o + b * a.o_bs + q * a.o_rs + h * a.o_hs + d0) = ov;
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt)
     if (lg == 0) { s_m[wave][qt * 16 + l16] = m_run[qt]; s_l[wave][qt * 16 + l16] = l_run[qt]; }
@@ -299,7 +348,7 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
       // unnormalised partial of this split, merged by fam_attention_combine
       const int64_t row = ((int64_t)blockIdx.y * gridDim.x + bh) * a.Sq + q;
       *reinterpret_cast<f32x4*>(a.part_o + row * DH + d0) = v;
-      if (d0 == 0) { a.part_ml[row * 2] = mx; a.part_ml[row * 2 + 1] = L; }
+      if (d0 == 0) *reinterpret_cast<float2*>(a.part_ml + row * 2) = make_float2(mx, L);
       continue;
     }
     const float inv = L > 0.f ? 1.0f / L : 0.f;

@@ -270,27 +270,32 @@ __global__ __launch_bounds__(256) void partial_kernel(PartArgs g) {
   const int64_t z = blockIdx.y;
   const int64_t kw = z * (4 * 32 * STEPS) + (int64_t)wave * (32 * STEPS) + lg * 8;  // this lane's first k
 
+  // Phase 1: raw loads from clamped (always valid) addresses, nothing else, so the compiler
+  // cannot put a wait between them.  Rows past N or M only produce outputs that are never
+  // stored; k past K is zeroed on the activation side after the loads.
   const int64_t wn = n0 + l16;
-  const bool wrow = wn < g.N;
-  const bf16* wp = g.w + (wrow ? wn : 0) * g.ldw;
+  const bf16* wp = g.w + (wn < g.N ? wn : 0) * g.ldw;
   bf16x8 wf[STEPS], af[MT][STEPS];
+  bool kok[STEPS];
 #pragma unroll
   for (int s = 0; s < STEPS; ++s) {
     const int64_t k = kw + s * 32;
-    wf[s] = load8_if(wrow && k < g.K, wp + k, g.w);
+    kok[s] = k < g.K;
+    wf[s] = load8(kok[s] ? wp + k : g.w);
   }
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
     const int64_t m = t * 16 + l16;
-    const bool arow = m < g.M;
-    const bf16* ap = g.a + (arow ? m : 0) * g.lda;
+    const bf16* ap = g.a + (m < g.M ? m : 0) * g.lda;
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      const int64_t k = kw + s * 32;
-      af[t][s] = load8_if(arow && k < g.K, ap + k, g.a);
-    }
+    for (int s = 0; s < STEPS; ++s) af[t][s] = load8(kok[s] ? ap + kw + s * 32 : g.a);
   }
   __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s)
+      if (!kok[s]) af[t][s] = zero8();
 
   f32x4 acc[MT];
 #pragma unroll

@@ -234,13 +234,18 @@ template <int NW, int MAXS>
 __global__ __launch_bounds__(NW * 64) void rowop_vec_kernel(RowArgs a) {
   __shared__ float red[2 * NW];
   const int tid = threadIdx.x;
-  const int64_t m = blockIdx.x;
-  const int64_t bi = m / a.rpb, si = m - bi * a.rpb;
+  // 32-bit index arithmetic (M, rows_per_batch, seq_len and head_dim are < 2^31, checked on
+  // the host): a 64-bit division is a ~100-instruction sequence on the critical path
+  const uint32_t m32 = blockIdx.x, rpb32 = (uint32_t)a.rpb;
+  const int64_t m = m32;
+  const int64_t bi = m32 / rpb32, si = m32 - (uint32_t)bi * rpb32;
   const int64_t c = (int64_t)tid * 4;
   const bool act = c < a.N;
   const int64_t cs = act ? c : 0;  // a valid column for inactive threads' loads
 
-  // ---- phase 1: every load of the row
+  // ---- phase 1: every load of the row, raw, from always-valid addresses (an absent operand
+  // reads the partials instead), so that no wait can be scheduled between the loads
+  const float* safe = a.part;
   f32x4 pz[MAXS];
   const int64_t ns = a.splits;
 #pragma unroll
@@ -248,57 +253,77 @@ __global__ __launch_bounds__(NW * 64) void rowop_vec_kernel(RowArgs a) {
     const int64_t zz = z < ns ? z : ns - 1;
     pz[z] = *reinterpret_cast<const f32x4*>(a.part + zz * a.split_stride + m * a.N + cs);
   }
-  float bias[4] = {0.f, 0.f, 0.f, 0.f}, res[4] = {0.f, 0.f, 0.f, 0.f}, gate[4] = {1.f, 1.f, 1.f, 1.f};
-  if (a.bias) ld4(a.bias + cs, bias);
-  if (a.res) {
-    if (a.out_f32) {
-      const f32x4 r = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(a.res) + m * a.ldr + cs);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) res[e] = r[e];
-    } else {
-      ld4(reinterpret_cast<const bf16*>(a.res) + m * a.ldr + cs, res);
-    }
-  }
-  if (a.gate) {
-    const bf16* gp = a.gate + bi * a.gbs + si * a.grs;
-    if (a.gns == 0) {
-      const float g = to_f(gp[0]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) gate[e] = g;
-    } else {
-      ld4(gp + cs, gate);
-    }
-  }
-  float na[4] = {0.f, 0.f, 0.f, 0.f}, nb[4] = {0.f, 0.f, 0.f, 0.f};  // norm operands
-  float rc[2] = {1.f, 1.f}, rsn[2] = {0.f, 0.f};                       // RoPE of the 2 pairs
+  auto raw4 = [&](const bf16* p) { return *reinterpret_cast<const uint2*>(p ? (const void*)p : (const void*)safe); };
+  const uint2 r_bias = raw4(a.bias ? a.bias + cs : nullptr);
+  const bool res_f32 = a.res && a.out_f32, res_bf = a.res && !a.out_f32;
+  const f32x4 r_resf = *reinterpret_cast<const f32x4*>(res_f32 ? reinterpret_cast<const float*>(a.res) + m * a.ldr + cs : safe);
+  const uint2 r_resb = raw4(res_bf ? reinterpret_cast<const bf16*>(a.res) + m * a.ldr + cs : nullptr);
+  const bf16* gp = a.gate ? a.gate + bi * a.gbs + si * a.grs : nullptr;
+  const uint2 r_gate4 = raw4(gp && a.gns ? gp + cs : nullptr);
+  const bf16 r_gate1 = *(gp && !a.gns ? gp : reinterpret_cast<const bf16*>(safe));
+  // norm operands: (scale, shift) for AdaLN, (weight, bias) for LayerNorm, weight for RMS
+  const int64_t mo = bi * a.mbs + si * a.mrs;
+  const bf16* p_na = nullptr;
+  const bf16* p_nb = nullptr;
   int seg = -1;
+  const bf16* sw0 = a.segwt[0];
+  const bf16* sw1 = a.segwt[1];
+  const int64_t s0 = a.seg0[0], s1 = a.seg0[1], sgw = a.segw;
+  int64_t cl = 0;
   if (a.norm == FAM_ROWNORM_ADALN) {
-    const int64_t mo = bi * a.mbs + si * a.mrs;
-    ld4(a.scale + mo + cs, na);
-    ld4(a.shift + mo + cs, nb);
+    p_na = a.scale + mo + cs;
+    p_nb = a.shift + mo + cs;
   } else if (a.norm == FAM_ROWNORM_LAYERNORM) {
-    if (a.nw) ld4(a.nw + cs, na); else { na[0] = na[1] = na[2] = na[3] = 1.f; }
-    if (a.nb) ld4(a.nb + cs, nb);
+    p_na = a.nw ? a.nw + cs : nullptr;
+    p_nb = a.nb ? a.nb + cs : nullptr;
   } else if (a.norm == FAM_ROWNORM_RMS) {
+    if (a.nseg > 0 && c >= s0 && c < s0 + sgw) seg = 0;
+    if (a.nseg > 1 && c >= s1 && c < s1 + sgw) seg = 1;
+    if (!act) seg = -1;
+    cl = c - (seg == 1 ? s1 : s0);
+    p_na = seg == 0 ? sw0 + cl : (seg == 1 ? sw1 + cl : nullptr);
+  }
+  const uint2 r_na = raw4(p_na), r_nb = raw4(p_nb);
+  // RoPE table entries of the thread's two pairs
+  const bool rope = a.cs != nullptr && seg >= 0;
+  int64_t t0 = 0, t1 = 0;
+  if (rope) {
+    const int64_t pos = m32 % (uint32_t)a.seq, j0 = ((uint32_t)cl % (uint32_t)a.hd) >> 1;
+    t0 = pos * a.trs + j0 * a.tes;
+    t1 = t0 + a.tes;
+  }
+  const float* tc = rope ? a.cs : safe;
+  const float* tsn = rope ? a.sn : safe;
+  const float rc0 = tc[t0], rc1 = tc[t1], rs0 = tsn[t0], rs1 = tsn[t1];
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- unpack
+  auto unpack = [](uint2 r, float o[4]) {
+    bf16x4 v;
+    __builtin_memcpy(&v, &r, 8);
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
-      if (g < a.nseg && c >= a.seg0[g] && c < a.seg0[g] + a.segw) seg = g;
-    if (act && seg >= 0) {
-      const int64_t cl = c - a.seg0[seg];
-      ld4(a.segwt[seg] + cl, na);
-      if (a.cs) {
-        const int64_t pos = m % a.seq;
-        const int64_t j0 = (cl % a.hd) >> 1;
+    for (int e = 0; e < 4; ++e) o[e] = to_f(v[e]);
+  };
+  float bias[4] = {0.f, 0.f, 0.f, 0.f}, res[4] = {0.f, 0.f, 0.f, 0.f}, gate[4] = {1.f, 1.f, 1.f, 1.f};
+  if (a.bias) unpack(r_bias, bias);
+  if (res_f32) {
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-          const int64_t t = pos * a.trs + (j0 + p) * a.tes;
-          rc[p] = a.cs[t];
-          rsn[p] = a.sn[t];
-        }
-      }
+    for (int e = 0; e < 4; ++e) res[e] = r_resf[e];
+  } else if (res_bf) {
+    unpack(r_resb, res);
+  }
+  if (gp) {
+    if (a.gns) {
+      unpack(r_gate4, gate);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) gate[e] = to_f(r_gate1);
     }
   }
-  __builtin_amdgcn_sched_barrier(0);
+  float na[4] = {1.f, 1.f, 1.f, 1.f}, nb[4] = {0.f, 0.f, 0.f, 0.f};
+  if (p_na) unpack(r_na, na);
+  if (p_nb) unpack(r_nb, nb);
+  const float rc[2] = {rope ? rc0 : 1.f, rope ? rc1 : 1.f}, rsn[2] = {rope ? rs0 : 0.f, rope ? rs1 : 0.f};
 
   // ---- phase 2: sum the planes in split order, epilogue, store
   float v[4] = {0.f, 0.f, 0.f, 0.f};
@@ -447,6 +472,9 @@ extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
                   FAM_ERR_INVALID_ARG, "fam_rowop: RoPE needs head_dim %% 4 == 0 dividing the segment, seq_len >= 1");
     }
   }
+  FAM_REQUIRE(d->M < (1LL << 31) && d->rows_per_batch < (1LL << 31) && d->seq_len < (1LL << 31) &&
+                  d->head_dim < (1LL << 31),
+              FAM_ERR_UNSUPPORTED, "fam_rowop: M, rows_per_batch, seq_len and head_dim must be < 2^31");
   if (d->M == 0) return FAM_OK;
 
   RowArgs a{};
