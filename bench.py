@@ -55,6 +55,8 @@ def parse():
     ap.add_argument("--no-eager", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--cpu-sample-s", type=float, default=20.0, help="CPU baseline time budget")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
 
 
@@ -80,6 +82,35 @@ def pct(xs, q):
 
 
 # --------------------------------------------------------------------------- roofline
+# HBM traffic per launch of a kernel class, from two rocprofv3 --pmc runs of this script
+# (FETCH_SIZE, then WRITE_SIZE), each scaled by what the counter reads for the --copy-probe
+# copy of known size.  Written by hand from those runs into this text file (one line per
+# class: "<class> <bytes per launch>"); absent file or class -> traffic null.
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_per_launch.txt")
+
+
+def measured_traffic(cls: str):
+    try:
+        for line in open(TRAFFIC_FILE):
+            f = line.split()
+            if len(f) >= 2 and not line.startswith("#") and f[0] == cls:
+                return int(float(f[1]))
+    except OSError:
+        pass
+    return None
+
+
+def copy_probe():
+    import torch
+    n = 256 << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "launches": 5}), flush=True)
+
+
 def kernel_breakdown(model, reps_target: int = 2000):
     """Per kernel class: launches/call, avg launch duration (HIP events around a captured graph
     of that class's launches replayed back-to-back), algorithmic bytes and flops per launch."""
@@ -278,6 +309,9 @@ def main():
     from fam.action_dit import FusedActionDiT, synthetic_params
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_probe:
+        copy_probe()
+        return
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     cfg, shape = workload(args.batch)
@@ -327,7 +361,8 @@ def main():
         d = kb[dom]
         bound = "hbm"
         out["roofline"] = {"kernel": dom, "bound": bound, "achieved": d["achieved_GBs"], "peak": HBM_PEAK_GBS,
-                           "unit": "GB/s", "frac": round(d["achieved_GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                           "unit": "GB/s", "frac": round(d["achieved_GBs"] / HBM_PEAK_GBS, 4),
+                           "traffic": measured_traffic(dom),
                            "alg_bytes_per_launch": d["alg_bytes_per_launch"], "avg_launch_us": d["avg_launch_us"]}
         out["kernels"] = kb
 

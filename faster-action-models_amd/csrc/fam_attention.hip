@@ -512,6 +512,7 @@ template <int DH, int QT>
 static void launch_short_q(const AttnArgs& a, int64_t nkb, dim3 grid, hipStream_t s) {
   constexpr bool wide = DH >= 128 && QT >= 2;
   if (nkb <= 1) hipLaunchKernelGGL((attn_short_kernel<DH, QT, 1>), grid, dim3(64), 0, s, a);
+  else if (nkb <= 2) hipLaunchKernelGGL((attn_short_kernel<DH, QT, 2>), grid, dim3(128), 0, s, a);
   else if (nkb <= 4 || wide) hipLaunchKernelGGL((attn_short_kernel<DH, QT, 4>), grid, dim3(256), 0, s, a);
   else hipLaunchKernelGGL((attn_short_kernel<DH, QT, (wide ? 4 : 8)>), grid, dim3((wide ? 4 : 8) * 64), 0, s, a);
 }
