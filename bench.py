@@ -13,10 +13,11 @@ graph.  Timing mirrors the reference latency workers: W warmups, then K calls ea
 by a device synchronize; the value is the p50 (min and p90 also reported).
 
 Extra legs (one JSON line in total):
-  roofline      per kernel class, the launches of one policy call replayed back-to-back from
-                a captured graph between two HIP events on the launching stream; achieved =
-                algorithmic bytes (or flops) per launch / average launch duration, for the
-                class with the largest time per call ("dominant").
+  roofline      per kernel class, each launch's own duration from a start/stop HIP event pair
+                that the library records at the kernel's begin and end (hipExtLaunchKernelGGL),
+                over 3 eager policy calls on the launching stream; achieved = algorithmic bytes
+                (or flops) per launch / average duration, for the class with the largest time
+                per call ("dominant").  traffic = HBM bytes per launch from rocprofv3 counters.
   cpu_baseline  the CPU oracle (fp32 PyTorch restatement of the reference modules) timed on
                 the host cores on a bounded sample of full policy calls.
   eager_gpu     the reference's eager module sequence (ops as FB/action_dit.py,
@@ -111,31 +112,42 @@ def copy_probe():
     print(json.dumps({"copy_probe_bytes_read": n, "copy_probe_bytes_written": n, "launches": 5}), flush=True)
 
 
-def kernel_breakdown(model, reps_target: int = 2000):
-    """Per kernel class: launches/call, avg launch duration (HIP events around a captured graph
-    of that class's launches replayed back-to-back), algorithmic bytes and flops per launch."""
+def kernel_breakdown(model, calls: int = 3):
+    """Per kernel class: launches per call and the average duration of one launch, measured over
+    `calls` eager policy calls on the launching stream.  Each library launch is armed with a
+    start/stop HIP event pair (fam_set_launch_events -> hipExtLaunchKernelGGL), so an elapsed
+    time is that kernel's own begin-to-end duration on the GPU, the quantity rocprofv3's kernel
+    trace reports.  Achieved = algorithmic bytes (flops) per launch / that duration."""
     import torch
-    plan = model.plan
-    classes = sorted({m["kernel"] for m in plan.meta if m["kernel"] not in ("copy",)})
+    plan, lib = model.plan, model.lib
     stream = torch.cuda.current_stream()
-    out = {}
-    for cls in classes:
-        idx = [i for i, m in enumerate(plan.meta) if m["kernel"] == cls]
-        reps = max(1, reps_target // len(idx))
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            s = torch.cuda.current_stream().cuda_stream
-            for _ in range(reps):
-                for i in idx:
-                    plan.steps[i](s)
-        g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s = stream.cuda_stream
+    n = len(plan.steps)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for e0, e1 in ev:  # create the underlying HIP events
         e0.record(stream)
-        g.replay()
         e1.record(stream)
+    torch.cuda.synchronize()
+    dur = {}
+    for _ in range(calls):
+        for i, fn in enumerate(plan.steps):
+            if plan.meta[i]["kernel"] == "copy":
+                fn(s)
+                continue
+            lib.fam_set_launch_events(ev[i][0].cuda_event, ev[i][1].cuda_event)
+            try:
+                fn(s)
+            finally:
+                lib.fam_set_launch_events(None, None)
         torch.cuda.synchronize()
-        avg_us = e0.elapsed_time(e1) * 1e3 / (reps * len(idx))
+        for i in range(n):
+            if plan.meta[i]["kernel"] != "copy":
+                dur.setdefault(i, []).append(ev[i][0].elapsed_time(ev[i][1]) * 1e3)
+    out = {}
+    for cls in sorted({m["kernel"] for m in plan.meta if m["kernel"] != "copy"}):
+        idx = [i for i, m in enumerate(plan.meta) if m["kernel"] == cls]
+        us = [d for i in idx for d in dur[i]]
+        avg_us = sum(us) / len(us)
         nbytes = sum(plan.meta[i]["bytes"] for i in idx) / len(idx)
         flops = sum(plan.meta[i]["flops"] for i in idx) / len(idx)
         out[cls] = {
@@ -147,10 +159,6 @@ def kernel_breakdown(model, reps_target: int = 2000):
             "achieved_GBs": round(nbytes / (avg_us * 1e-6) / 1e9, 1),
             "achieved_TFLOPs": round(flops / (avg_us * 1e-6) / 1e12, 2),
         }
-        del g
-    # graphs replayed kernels in isolation: restore a consistent state with one real call
-    model.run()
-    torch.cuda.synchronize()
     return out
 
 
@@ -355,7 +363,7 @@ def main():
     }
 
     if not args.no_roofline:
-        log("kernel breakdown (graph replays per kernel class)")
+        log("kernel breakdown (per-launch HIP events over eager policy calls)")
         kb = kernel_breakdown(model)
         dom = max(kb, key=lambda k: kb[k]["us_per_call"])
         d = kb[dom]

@@ -511,10 +511,10 @@ static int64_t rup(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 template <int DH, int QT>
 static void launch_short_q(const AttnArgs& a, int64_t nkb, dim3 grid, hipStream_t s) {
   constexpr bool wide = DH >= 128 && QT >= 2;
-  if (nkb <= 1) hipLaunchKernelGGL((attn_short_kernel<DH, QT, 1>), grid, dim3(64), 0, s, a);
-  else if (nkb <= 2) hipLaunchKernelGGL((attn_short_kernel<DH, QT, 2>), grid, dim3(128), 0, s, a);
-  else if (nkb <= 4 || wide) hipLaunchKernelGGL((attn_short_kernel<DH, QT, 4>), grid, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL((attn_short_kernel<DH, QT, (wide ? 4 : 8)>), grid, dim3((wide ? 4 : 8) * 64), 0, s, a);
+  if (nkb <= 1) FAM_LAUNCH((attn_short_kernel<DH, QT, 1>), grid, dim3(64), 0, s, a);
+  else if (nkb <= 2) FAM_LAUNCH((attn_short_kernel<DH, QT, 2>), grid, dim3(128), 0, s, a);
+  else if (nkb <= 4 || wide) FAM_LAUNCH((attn_short_kernel<DH, QT, 4>), grid, dim3(256), 0, s, a);
+  else FAM_LAUNCH((attn_short_kernel<DH, QT, (wide ? 4 : 8)>), grid, dim3((wide ? 4 : 8) * 64), 0, s, a);
 }
 
 template <int DH>
@@ -528,7 +528,7 @@ static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
     else launch_short_q<DH, 4>(a, nkb, grid, s);
   } else {
     const dim3 grid((unsigned)(rup(a.Sq, 64) / 64), (unsigned)bh);
-    hipLaunchKernelGGL((attn_tiled_kernel<DH>), grid, dim3(256), 0, s, a);
+    FAM_LAUNCH((attn_tiled_kernel<DH>), grid, dim3(256), 0, s, a);
   }
 }
 
@@ -605,9 +605,9 @@ extern "C" int fam_attention_combine(const fam_attn_desc* d, void* stream) {
   const int64_t n = bh * d->sq * (d->head_dim / 4);
   const dim3 grid((unsigned)((n + 63) / 64));
   hipStream_t s = (hipStream_t)stream;
-  if (a.splits <= 4) hipLaunchKernelGGL((attn_combine_kernel<4>), grid, dim3(64), 0, s, a, d->head_dim, bh);
-  else if (a.splits <= 8) hipLaunchKernelGGL((attn_combine_kernel<8>), grid, dim3(64), 0, s, a, d->head_dim, bh);
-  else if (a.splits <= 16) hipLaunchKernelGGL((attn_combine_kernel<16>), grid, dim3(64), 0, s, a, d->head_dim, bh);
-  else hipLaunchKernelGGL((attn_combine_kernel<0>), grid, dim3(64), 0, s, a, d->head_dim, bh);
+  if (a.splits <= 4) FAM_LAUNCH((attn_combine_kernel<4>), grid, dim3(64), 0, s, a, d->head_dim, bh);
+  else if (a.splits <= 8) FAM_LAUNCH((attn_combine_kernel<8>), grid, dim3(64), 0, s, a, d->head_dim, bh);
+  else if (a.splits <= 16) FAM_LAUNCH((attn_combine_kernel<16>), grid, dim3(64), 0, s, a, d->head_dim, bh);
+  else FAM_LAUNCH((attn_combine_kernel<0>), grid, dim3(64), 0, s, a, d->head_dim, bh);
   return fam_host::check_launch("fam_attention_combine");
 }

@@ -8,6 +8,7 @@
 //     validation layer checks before any launch.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -91,7 +92,21 @@ namespace fam_host {
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// Launch-timing events armed by fam_set_launch_events (null: plain launches).
+extern thread_local hipEvent_t t_evt_start, t_evt_stop;
 }  // namespace fam_host
+
+// Every kernel launch of the library goes through this macro: when the calling thread has
+// armed a start/stop event pair, the launch records them at the kernel's own begin and end
+// (hipExtLaunchKernelGGL), which is how bench.py measures per-kernel durations.
+#define FAM_LAUNCH(kernel, grid, block, shmem, stream, ...)                                              \
+  do {                                                                                                   \
+    if (fam_host::t_evt_start != nullptr)                                                                \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, fam_host::t_evt_start, fam_host::t_evt_stop, \
+                            0, __VA_ARGS__);                                                             \
+    else                                                                                                 \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                               \
+  } while (0)
 
 #define FAM_REQUIRE(cond, code, ...)            \
   do {                                          \

@@ -436,13 +436,13 @@ template <int MT, int NW, int KS>
 static void launch_skinny(const GemmArgs& a, int pro, hipStream_t s) {
   dim3 grid((unsigned)(round_up(a.N, 16) / 16));
   if constexpr (NW > 8) {
-    hipLaunchKernelGGL((skinny_kernel<MT, NW, KS, FAM_PRO_NONE>), grid, dim3(NW * 64), 0, s, a);
+    FAM_LAUNCH((skinny_kernel<MT, NW, KS, FAM_PRO_NONE>), grid, dim3(NW * 64), 0, s, a);
     return;
   }
   switch (pro) {
-    case FAM_PRO_LAYERNORM: hipLaunchKernelGGL((skinny_kernel<MT, NW, KS, FAM_PRO_LAYERNORM>), grid, dim3(NW * 64), 0, s, a); break;
-    case FAM_PRO_ADALN: hipLaunchKernelGGL((skinny_kernel<MT, NW, KS, FAM_PRO_ADALN>), grid, dim3(NW * 64), 0, s, a); break;
-    default: hipLaunchKernelGGL((skinny_kernel<MT, NW, KS, FAM_PRO_NONE>), grid, dim3(NW * 64), 0, s, a); break;
+    case FAM_PRO_LAYERNORM: FAM_LAUNCH((skinny_kernel<MT, NW, KS, FAM_PRO_LAYERNORM>), grid, dim3(NW * 64), 0, s, a); break;
+    case FAM_PRO_ADALN: FAM_LAUNCH((skinny_kernel<MT, NW, KS, FAM_PRO_ADALN>), grid, dim3(NW * 64), 0, s, a); break;
+    default: FAM_LAUNCH((skinny_kernel<MT, NW, KS, FAM_PRO_NONE>), grid, dim3(NW * 64), 0, s, a); break;
   }
 }
 
@@ -458,9 +458,9 @@ template <int BM, int BN, int WM>
 static void launch_tiled(const GemmArgs& a, int pro, hipStream_t s) {
   dim3 grid((unsigned)(round_up(a.N, BN) / BN), (unsigned)(round_up(a.M, BM) / BM));
   switch (pro) {
-    case FAM_PRO_LAYERNORM: hipLaunchKernelGGL((tiled_kernel<BM, BN, WM, FAM_PRO_LAYERNORM>), grid, dim3(256), 0, s, a); break;
-    case FAM_PRO_ADALN: hipLaunchKernelGGL((tiled_kernel<BM, BN, WM, FAM_PRO_ADALN>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((tiled_kernel<BM, BN, WM, FAM_PRO_NONE>), grid, dim3(256), 0, s, a); break;
+    case FAM_PRO_LAYERNORM: FAM_LAUNCH((tiled_kernel<BM, BN, WM, FAM_PRO_LAYERNORM>), grid, dim3(256), 0, s, a); break;
+    case FAM_PRO_ADALN: FAM_LAUNCH((tiled_kernel<BM, BN, WM, FAM_PRO_ADALN>), grid, dim3(256), 0, s, a); break;
+    default: FAM_LAUNCH((tiled_kernel<BM, BN, WM, FAM_PRO_NONE>), grid, dim3(256), 0, s, a); break;
   }
 }
 
@@ -546,10 +546,10 @@ template <int MT>
 static void launch_partial(const PartArgs& a, int steps, int splits, hipStream_t s) {
   const dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)splits);
   switch (steps) {
-    case 1: hipLaunchKernelGGL((partial_kernel<MT, 1>), grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((partial_kernel<MT, 2>), grid, dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((partial_kernel<MT, 4>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((partial_kernel<MT, 8>), grid, dim3(256), 0, s, a); break;
+    case 1: FAM_LAUNCH((partial_kernel<MT, 1>), grid, dim3(256), 0, s, a); break;
+    case 2: FAM_LAUNCH((partial_kernel<MT, 2>), grid, dim3(256), 0, s, a); break;
+    case 4: FAM_LAUNCH((partial_kernel<MT, 4>), grid, dim3(256), 0, s, a); break;
+    default: FAM_LAUNCH((partial_kernel<MT, 8>), grid, dim3(256), 0, s, a); break;
   }
 }
 

@@ -235,12 +235,12 @@ extern "C" int fam_adaln(const void* x, int64_t x_row_stride, const void* shift,
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
   hipStream_t s = (hipStream_t)stream;
   switch (nv_for(dim)) {
-    case 1: hipLaunchKernelGGL(adaln_kernel<1>, grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL(adaln_kernel<2>, grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL(adaln_kernel<4>, grid, block, 0, s, a); break;
-    case 6: hipLaunchKernelGGL(adaln_kernel<6>, grid, block, 0, s, a); break;
-    case 8: hipLaunchKernelGGL(adaln_kernel<8>, grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL(adaln_kernel<0>, grid, block, 0, s, a); break;
+    case 1: FAM_LAUNCH(adaln_kernel<1>, grid, block, 0, s, a); break;
+    case 2: FAM_LAUNCH(adaln_kernel<2>, grid, block, 0, s, a); break;
+    case 4: FAM_LAUNCH(adaln_kernel<4>, grid, block, 0, s, a); break;
+    case 6: FAM_LAUNCH(adaln_kernel<6>, grid, block, 0, s, a); break;
+    case 8: FAM_LAUNCH(adaln_kernel<8>, grid, block, 0, s, a); break;
+    default: FAM_LAUNCH(adaln_kernel<0>, grid, block, 0, s, a); break;
   }
   return fam_host::check_launch("fam_adaln");
 }
@@ -273,12 +273,12 @@ extern "C" int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, in
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
   hipStream_t s = (hipStream_t)stream;
   switch (nv) {
-    case 1: hipLaunchKernelGGL(rmsnorm_rope_kernel<1>, grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL(rmsnorm_rope_kernel<2>, grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL(rmsnorm_rope_kernel<4>, grid, block, 0, s, a); break;
-    case 6: hipLaunchKernelGGL(rmsnorm_rope_kernel<6>, grid, block, 0, s, a); break;
-    case 8: hipLaunchKernelGGL(rmsnorm_rope_kernel<8>, grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL(rmsnorm_rope_kernel<0>, grid, block, 0, s, a); break;
+    case 1: FAM_LAUNCH(rmsnorm_rope_kernel<1>, grid, block, 0, s, a); break;
+    case 2: FAM_LAUNCH(rmsnorm_rope_kernel<2>, grid, block, 0, s, a); break;
+    case 4: FAM_LAUNCH(rmsnorm_rope_kernel<4>, grid, block, 0, s, a); break;
+    case 6: FAM_LAUNCH(rmsnorm_rope_kernel<6>, grid, block, 0, s, a); break;
+    case 8: FAM_LAUNCH(rmsnorm_rope_kernel<8>, grid, block, 0, s, a); break;
+    default: FAM_LAUNCH(rmsnorm_rope_kernel<0>, grid, block, 0, s, a); break;
   }
   return fam_host::check_launch("fam_rmsnorm_rope");
 }

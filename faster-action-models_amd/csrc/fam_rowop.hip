@@ -501,15 +501,15 @@ extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
     const int nw = d->N <= 1024 ? 4 : (d->N <= 2048 ? 8 : 16);
     const int ms = d->splits <= 4 ? 4 : (d->splits <= 8 ? 8 : 16);
 #define FAM_ROWVEC(NW_, MS_) \
-  if (nw == NW_ && ms == MS_) hipLaunchKernelGGL((rowop_vec_kernel<NW_, MS_>), grid, dim3(NW_ * 64), 0, s, a)
+  if (nw == NW_ && ms == MS_) FAM_LAUNCH((rowop_vec_kernel<NW_, MS_>), grid, dim3(NW_ * 64), 0, s, a)
     FAM_ROWVEC(4, 4); FAM_ROWVEC(4, 8); FAM_ROWVEC(4, 16);
     FAM_ROWVEC(8, 4); FAM_ROWVEC(8, 8); FAM_ROWVEC(8, 16);
     FAM_ROWVEC(16, 4); FAM_ROWVEC(16, 8); FAM_ROWVEC(16, 16);
 #undef FAM_ROWVEC
     return fam_host::check_launch("fam_rowop");
   }
-  if (d->N <= 4 * RT) hipLaunchKernelGGL(rowop_kernel<1>, grid, dim3(RT), 0, s, a);
-  else if (d->N <= 8 * RT) hipLaunchKernelGGL(rowop_kernel<2>, grid, dim3(RT), 0, s, a);
-  else hipLaunchKernelGGL(rowop_kernel<4>, grid, dim3(RT), 0, s, a);
+  if (d->N <= 4 * RT) FAM_LAUNCH(rowop_kernel<1>, grid, dim3(RT), 0, s, a);
+  else if (d->N <= 8 * RT) FAM_LAUNCH(rowop_kernel<2>, grid, dim3(RT), 0, s, a);
+  else FAM_LAUNCH(rowop_kernel<4>, grid, dim3(RT), 0, s, a);
   return fam_host::check_launch("fam_rowop");
 }

@@ -18,6 +18,8 @@ void set_error(const char* fmt, ...) {
   va_end(ap);
 }
 
+thread_local hipEvent_t t_evt_start = nullptr, t_evt_stop = nullptr;
+
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
@@ -28,6 +30,14 @@ int check_launch(const char* what) {
 }
 
 }  // namespace fam_host
+
+extern "C" int fam_set_launch_events(void* start_event, void* stop_event) {
+  FAM_REQUIRE((start_event == nullptr) == (stop_event == nullptr), FAM_ERR_INVALID_ARG,
+              "fam_set_launch_events: give both events or neither");
+  fam_host::t_evt_start = (hipEvent_t)start_event;
+  fam_host::t_evt_stop = (hipEvent_t)stop_event;
+  return FAM_OK;
+}
 
 namespace fam {
 
@@ -101,7 +111,7 @@ extern "C" int fam_euler_step(const void* sample, const void* model_output, cons
   FAM_REQUIRE(sample && model_output && delta && out, FAM_ERR_INVALID_ARG, "fam_euler_step: null pointer");
   FAM_REQUIRE(n >= 0 && inner >= 1, FAM_ERR_INVALID_ARG, "fam_euler_step: need n >= 0 and inner >= 1");
   if (n == 0) return FAM_OK;
-  hipLaunchKernelGGL(euler_kernel, dim3(blocks_for(n)), dim3(256), 0, (hipStream_t)stream, (const bf16*)sample,
+  FAM_LAUNCH(euler_kernel, dim3(blocks_for(n)), dim3(256), 0, (hipStream_t)stream, (const bf16*)sample,
                      (const bf16*)model_output, (const bf16*)delta, (bf16*)out, n, inner);
   return fam_host::check_launch("fam_euler_step");
 }
@@ -110,7 +120,7 @@ extern "C" int fam_sinusoid(const void* positions, void* out, int64_t T, int64_t
   FAM_REQUIRE(positions && out, FAM_ERR_INVALID_ARG, "fam_sinusoid: null pointer");
   FAM_REQUIRE(T >= 0 && dim >= 2 && dim % 2 == 0, FAM_ERR_INVALID_ARG, "fam_sinusoid: dim must be even and >= 2");
   if (T == 0) return FAM_OK;
-  hipLaunchKernelGGL(sinusoid_kernel, dim3(blocks_for(T * (dim / 2))), dim3(256), 0, (hipStream_t)stream,
+  FAM_LAUNCH(sinusoid_kernel, dim3(blocks_for(T * (dim / 2))), dim3(256), 0, (hipStream_t)stream,
                      (const bf16*)positions, (bf16*)out, T, dim);
   return fam_host::check_launch("fam_sinusoid");
 }
@@ -122,7 +132,7 @@ extern "C" int fam_add_modulation(const void* t_mod, const void* modulation, voi
   FAM_REQUIRE(fam_host::aligned16(t_mod) && fam_host::aligned16(modulation) && fam_host::aligned16(out),
               FAM_ERR_INVALID_ARG, "fam_add_modulation: pointers must be 16-byte aligned");
   if (T == 0 || L == 0) return FAM_OK;
-  hipLaunchKernelGGL(add_mod_kernel, dim3(blocks_for(T * L * (n / 8))), dim3(256), 0, (hipStream_t)stream,
+  FAM_LAUNCH(add_mod_kernel, dim3(blocks_for(T * L * (n / 8))), dim3(256), 0, (hipStream_t)stream,
                      (const bf16*)t_mod, (const bf16*)modulation, (bf16*)out, T, L, n);
   return fam_host::check_launch("fam_add_modulation");
 }
@@ -134,10 +144,10 @@ extern "C" int fam_linear_smallk(const void* x, int64_t ldx, int x_f32, const vo
   FAM_REQUIRE(ldx >= K && ldy >= N, FAM_ERR_INVALID_ARG, "fam_linear_smallk: bad leading dimensions");
   if (M == 0) return FAM_OK;
   if (x_f32)
-    hipLaunchKernelGGL(linear_smallk_kernel<float>, dim3(blocks_for(M * N)), dim3(256), 0, (hipStream_t)stream,
+    FAM_LAUNCH(linear_smallk_kernel<float>, dim3(blocks_for(M * N)), dim3(256), 0, (hipStream_t)stream,
                        (const float*)x, ldx, (const bf16*)w, (const bf16*)b, (bf16*)y, ldy, M, N, K);
   else
-    hipLaunchKernelGGL(linear_smallk_kernel<bf16>, dim3(blocks_for(M * N)), dim3(256), 0, (hipStream_t)stream,
+    FAM_LAUNCH(linear_smallk_kernel<bf16>, dim3(blocks_for(M * N)), dim3(256), 0, (hipStream_t)stream,
                        (const bf16*)x, ldx, (const bf16*)w, (const bf16*)b, (bf16*)y, ldy, M, N, K);
   return fam_host::check_launch("fam_linear_smallk");
 }

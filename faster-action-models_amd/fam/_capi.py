@@ -97,6 +97,7 @@ class RowopDesc(C.Structure):
 SIGNATURES = {
     "fam_version": (C.c_int, []),
     "fam_last_error": (C.c_char_p, []),
+    "fam_set_launch_events": (C.c_int, [_vp, _vp]),
     "fam_adaln": (C.c_int, [_vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, C.c_float, _vp]),
     "fam_rmsnorm_rope": (C.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, C.c_float, _vp, _vp, _i64, _i64,
                                    _i64, _vp]),

@@ -47,6 +47,15 @@ int fam_version(void);
 const char* fam_last_error(void);
 
 /*
+ * fam_set_launch_events -- profiling aid with no counterpart in the reference: while a pair
+ * of hipEvent_t (created with timing enabled) is armed on the calling thread, every kernel
+ * the library launches records start_event at its begin and stop_event at its end
+ * (hipExtLaunchKernelGGL), so hipEventElapsedTime gives that kernel's own duration.  Pass
+ * two nulls to disarm.  Not for use under stream capture.
+ */
+int fam_set_launch_events(void* start_event, void* stop_event);
+
+/*
  * fam_adaln -- LayerNorm over the last dim with AdaLN-Zero modulation:
  *   y[r,:] = (LN(x[r,:]) [* ln_weight + ln_bias]) * (1 + scale[r,:]) + shift[r,:]
  * LN is biased-variance, eps inside the rsqrt, fp32 statistics.

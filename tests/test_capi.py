@@ -137,6 +137,8 @@ def test_validation_rejects_before_launch(lib):
     r.split_stride, r.src = 256, 9
     assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG
 
+    assert lib.fam_set_launch_events(16, None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_set_launch_events(None, None) == _capi.FAM_OK
     assert lib.fam_linear_smallk(16, 7, 0, 32, None, 48, 64, 4, 64, 65, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_euler_step(16, 32, None, 48, 10, 10, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_sinusoid(16, 32, 4, 7, None) == _capi.FAM_ERR_INVALID_ARG

@@ -465,3 +465,24 @@ def test_rowop_generic_path_matches_vector_path():
         outs.append((out.cpu(), h.cpu()))
     assert torch.equal(outs[0][0], outs[1][0])
     assert relerr(outs[1][1], outs[0][1].float()) <= 1e-2
+
+
+def test_launch_events_time_the_kernel():
+    """fam_set_launch_events arms a start/stop pair recorded at a kernel's own begin and end."""
+    from fam import _capi
+    lib = _capi.lib()
+    x, w = dev(rnd(32, 1024, seed=111)), dev(rnd(1024, 1024, seed=112))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st = torch.cuda.current_stream()
+    e0.record(st)
+    e1.record(st)
+    torch.cuda.synchronize()
+    assert lib.fam_set_launch_events(e0.cuda_event, e1.cuda_event) == 0
+    try:
+        part, _ = ops().gemm_partial(x, w)
+    finally:
+        lib.fam_set_launch_events(None, None)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3
+    assert 0.0 < us < 1e4
+    assert relerr(part.sum(0), O.linear(x.float().cpu(), w.float().cpu(), None)) <= 1e-3
