@@ -325,6 +325,102 @@ __global__ __launch_bounds__(256) void partial_kernel(PartArgs g) {
 }
 
 // ---------------------------------------------------------------------------------------
+// final_kernel (fam_gemm_final, M <= 64): the whole K of 16 output columns in one workgroup
+// of NW waves, each wave a contiguous quarter/eighth/sixteenth of K with every fragment
+// loaded before the first MFMA; the wave accumulators are summed through LDS in wave order
+// and the epilogue (bias, activation, bf16 store) runs in the same kernel.  Optionally it
+// also writes, per row and per 16-column group, the sum of squares of the stored values:
+// the statistics a consumer needs for an RMSNorm over any union of column groups.
+struct FinalArgs {
+  const bf16* a; int64_t lda;
+  const bf16* w; int64_t ldw;
+  const bf16* bias; int act;
+  bf16* out; int64_t ldo;
+  float* sumsq;              // [ceil(N/16)][M] or null
+  int64_t M, N, K;
+};
+
+template <int MT, int NW, int STEPS>
+__global__ __launch_bounds__(NW * 64) void final_kernel(FinalArgs g) {
+  __shared__ f32x4 red[NW][MT][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const int64_t kw = (int64_t)wave * (32 * STEPS) + lg * 8;
+
+  const int64_t wn = n0 + l16;
+  const bf16* wp = g.w + (wn < g.N ? wn : 0) * g.ldw;
+  bf16x8 wf[STEPS], af[MT][STEPS];
+  bool kok[STEPS];
+#pragma unroll
+  for (int s = 0; s < STEPS; ++s) {
+    const int64_t k = kw + s * 32;
+    kok[s] = k < g.K;
+    wf[s] = load8(kok[s] ? wp + k : g.w);
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int64_t m = t * 16 + l16;
+    const bf16* ap = g.a + (m < g.M ? m : 0) * g.lda;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) af[t][s] = load8(kok[s] ? ap + kw + s * 32 : g.a);
+  }
+  // the epilogue's bias (4 consecutive columns per lane), loaded with the operands
+  const int64_t nc = n0 + lg * 4;
+  float bias[4] = {0.f, 0.f, 0.f, 0.f};
+  bf16 braw[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) braw[e] = g.bias ? g.bias[nc + e < g.N ? nc + e : 0] : (bf16)0.0f;
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) bias[e] = to_f(braw[e]);
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s)
+      if (!kok[s]) af[t][s] = zero8();
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) acc[t] = mfma16(wf[s], af[t][s], acc[t]);
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
+  __syncthreads();
+  for (int t = wave; t < MT; t += NW) {
+    f32x4 v = red[0][t][lane];
+#pragma unroll
+    for (int q = 1; q < NW; ++q) v += red[q][t][lane];
+    const int64_t m = t * 16 + l16;            // D[col = 4*lg + e][row = l16]
+    bf16x4 o;
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = v[e] + bias[e];
+      if (g.act == FAM_ACT_GELU_TANH) x = gelu_tanh(x);
+      else if (g.act == FAM_ACT_SILU) x = silu(x);
+      o[e] = to_bf(x);
+      const float r = to_f(o[e]);
+      ss += (nc + e < g.N) ? r * r : 0.f;
+    }
+    ss = group4_sum(ss);  // the 16 columns of this group, fixed order
+    if (m >= g.M) continue;
+    bf16* dst = g.out + m * g.ldo + nc;
+    if ((g.N & 3) == 0 && (g.ldo & 3) == 0) {
+      if (nc < g.N) *reinterpret_cast<bf16x4*>(dst) = o;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (nc + e < g.N) dst[e] = o[e];
+    }
+    if (g.sumsq && lg == 0) g.sumsq[(int64_t)blockIdx.x * g.M + m] = ss;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // tiled_kernel: BM x BN tiles, 4 waves as WAVES_M x WAVES_N.
 constexpr int BK = 64;
 constexpr int LDS_K = BK + 8;  // padded row (144 B) to spread LDS banks
@@ -573,4 +669,48 @@ extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64
   else if (M <= 32) launch_partial<2>(pa, steps, splits, s);
   else launch_partial<4>(pa, steps, splits, s);
   return fam_host::check_launch("fam_gemm_partial");
+}
+
+template <int MT, int NW>
+static void launch_final_steps(const FinalArgs& a, int steps, hipStream_t s) {
+  const dim3 grid((unsigned)((a.N + 15) / 16));
+  switch (steps) {
+    case 1: FAM_LAUNCH((final_kernel<MT, NW, 1>), grid, dim3(NW * 64), 0, s, a); break;
+    case 2: FAM_LAUNCH((final_kernel<MT, NW, 2>), grid, dim3(NW * 64), 0, s, a); break;
+    case 4: FAM_LAUNCH((final_kernel<MT, NW, 4>), grid, dim3(NW * 64), 0, s, a); break;
+    default: FAM_LAUNCH((final_kernel<MT, NW, 8>), grid, dim3(NW * 64), 0, s, a); break;
+  }
+}
+
+template <int MT>
+static void launch_final(const FinalArgs& a, hipStream_t s) {
+  // K <= 1024: 4 waves; <= 2048: 8 waves; <= 4096: 16 waves; k-steps per wave 1, 2, 4 or 8
+  const int64_t ksteps = (a.K + 31) / 32;
+  const int nw = ksteps <= 32 ? 4 : (ksteps <= 64 ? 8 : 16);
+  int steps = 1;
+  while (steps * nw < ksteps) steps <<= 1;
+  if (nw == 4) launch_final_steps<MT, 4>(a, steps, s);
+  else if (nw == 8) launch_final_steps<MT, 8>(a, steps, s);
+  else launch_final_steps<MT, 16>(a, steps, s);
+}
+
+extern "C" int fam_gemm_final(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, int act,
+                              void* out, int64_t ldo, float* sumsq, int64_t M, int64_t N, int64_t K, void* stream) {
+  FAM_REQUIRE(a && w && out, FAM_ERR_INVALID_ARG, "fam_gemm_final: a, w and out must be non-null");
+  FAM_REQUIRE(M >= 0 && M <= 64 && N >= 1 && K >= 8 && K % 8 == 0 && K <= 4096, FAM_ERR_INVALID_ARG,
+              "fam_gemm_final: need 0 <= M <= 64, N >= 1, K a multiple of 8 in [8, 4096] (M=%lld N=%lld K=%lld)",
+              (long long)M, (long long)N, (long long)K);
+  FAM_REQUIRE(lda >= K && ldw >= K && lda % 8 == 0 && ldw % 8 == 0 && ldo >= N, FAM_ERR_INVALID_ARG,
+              "fam_gemm_final: lda/ldw must be >= K and multiples of 8, ldo >= N");
+  FAM_REQUIRE(fam_host::aligned16(a) && fam_host::aligned16(w) && (reinterpret_cast<uintptr_t>(out) & 7u) == 0,
+              FAM_ERR_INVALID_ARG, "fam_gemm_final: a, w 16-byte and out 8-byte aligned");
+  FAM_REQUIRE(act >= FAM_ACT_NONE && act <= FAM_ACT_SILU, FAM_ERR_INVALID_ARG, "fam_gemm_final: unknown act %d", act);
+  FAM_REQUIRE((N + 15) / 16 <= 2147483647LL, FAM_ERR_UNSUPPORTED, "fam_gemm_final: N too large");
+  if (M == 0) return FAM_OK;
+  FinalArgs fa{(const bf16*)a, lda, (const bf16*)w, ldw, (const bf16*)bias, act, (bf16*)out, ldo, sumsq, M, N, K};
+  hipStream_t s = (hipStream_t)stream;
+  if (M <= 16) launch_final<1>(fa, s);
+  else if (M <= 32) launch_final<2>(fa, s);
+  else launch_final<4>(fa, s);
+  return fam_host::check_launch("fam_gemm_final");
 }

@@ -104,6 +104,7 @@ SIGNATURES = {
     "fam_attention": (C.c_int, [C.POINTER(AttnDesc), _vp]),
     "fam_attention_combine": (C.c_int, [C.POINTER(AttnDesc), _vp]),
     "fam_gemm_partial": (C.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
+    "fam_gemm_final": (C.c_int, [_vp, _i64, _vp, _i64, _vp, C.c_int, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "fam_gemm_partial_splits": (C.c_int, [_i64, _i64, _i64]),
     "fam_rowop": (C.c_int, [C.POINTER(RowopDesc), _vp]),
     "fam_gemm": (C.c_int, [C.POINTER(GemmDesc), _vp]),

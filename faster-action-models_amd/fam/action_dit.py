@@ -343,6 +343,15 @@ class FusedActionDiT:
                       2 * (M * K + N * K) + 4 * splits * M * N, 2 * M * N * K)
         return splits
 
+    def _gemm_final(self, name, a, w, bias, out, act=_capi.FAM_ACT_NONE, sumsq=None):
+        """Whole-K projection with its bias/activation epilogue (M <= 64), no partials."""
+        M, K = a.shape[0], w.shape[1]
+        N = w.shape[0]
+        args = (a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), bias.data_ptr() if bias is not None else None,
+                act, out.data_ptr(), out.stride(0), sumsq.data_ptr() if sumsq is not None else None, M, N, K)
+        self.plan.add(name, _checked(self.lib, "fam_gemm_final", *args), "gemm_final",
+                      2 * (M * K + N * K + M * N), 2 * M * N * K)
+
     def _rowop(self, name, *, N, splits=1, src=_capi.FAM_ROWSRC_PARTIALS, x_in=None, w_in=None, bias=None,
                act=_capi.FAM_ACT_NONE, res=None, gate=None, gate_strides=(0, 0, 1), out=None, out_f32=False,
                norm=_capi.FAM_ROWNORM_NONE, ln_w=None, ln_b=None, shift=None, scale=None, segs=(), rope=False,
@@ -476,9 +485,13 @@ class FusedActionDiT:
                 self._rowop(tag + ".cross_o_row", N=H, splits=sp, bias=w[f"ca_o_b{l}"], res=x, out=x, norm=ADALN,
                             shift=mod(t, l, 3), scale=mod(t, l, 4), nout=h)
                 # FFN: up + GELU, down; x += gate_mlp * ffn; AdaLN1 of the next block
-                sp = self._gemm_partial(tag + ".ffn_up", h, w[f"ff0_w{l}"])
-                self._rowop(tag + ".ffn_up_row", N=Fd, splits=sp, bias=w[f"ff0_b{l}"], act=_capi.FAM_ACT_GELU_TANH,
-                            out=hid)
+                if M <= 64:
+                    self._gemm_final(tag + ".ffn_up", h, w[f"ff0_w{l}"], w[f"ff0_b{l}"], hid,
+                                     act=_capi.FAM_ACT_GELU_TANH)
+                else:
+                    sp = self._gemm_partial(tag + ".ffn_up", h, w[f"ff0_w{l}"])
+                    self._rowop(tag + ".ffn_up_row", N=Fd, splits=sp, bias=w[f"ff0_b{l}"],
+                                act=_capi.FAM_ACT_GELU_TANH, out=hid)
                 sp = self._gemm_partial(tag + ".ffn_down", hid, w[f"ff2_w{l}"])
                 if l + 1 < L:
                     self._rowop(tag + ".ffn_down_row", N=H, splits=sp, bias=w[f"ff2_b{l}"], res=x, gate=mod(t, l, 5),

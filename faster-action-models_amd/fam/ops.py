@@ -394,6 +394,23 @@ def gemm_partial(a: torch.Tensor, w: torch.Tensor):
     return part, S
 
 
+def gemm_final(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None, act: int = _capi.FAM_ACT_NONE,
+               out: Optional[torch.Tensor] = None, want_sumsq: bool = False):
+    """act(a w^T + bias) for M <= 64 in one kernel; with want_sumsq also the per-row sum of
+    squares of each 16-column group of the (bf16) output, [ceil(N/16), M] fp32."""
+    _check(a, "a")
+    _check(w, "w")
+    M, K = a.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=_BF16, device=a.device)
+    ss = torch.empty(((N + 15) // 16, M), dtype=torch.float32, device=a.device) if want_sumsq else None
+    call("fam_gemm_final", a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0),
+         bias.data_ptr() if bias is not None else None, act, out.data_ptr(), out.stride(0),
+         ss.data_ptr() if ss is not None else None, M, N, K, _stream(a))
+    return (out, ss) if want_sumsq else out
+
+
 def rowop(out: torch.Tensor, *, partials: Optional[torch.Tensor] = None, x_in: Optional[torch.Tensor] = None,
           w_in: Optional[torch.Tensor] = None, bias=None, act: int = _capi.FAM_ACT_NONE, res=None, gate=None,
           gate_strides=(0, 0, 1), rows_per_batch: Optional[int] = None, norm: int = _capi.FAM_ROWNORM_NONE,

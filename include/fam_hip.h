@@ -206,6 +206,21 @@ int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64_t ldw, flo
                      int64_t M, int64_t N, int64_t K, void* stream);
 int fam_gemm_partial_splits(int64_t M, int64_t N, int64_t K);
 
+/*
+ * fam_gemm_final -- out[m, n] = bf16(act(sum_k a[m, k] * w[n, k] + bias[n])) for 1 <= M <= 64
+ * with the whole K of 16 output columns in one workgroup (no partials, no second kernel).
+ * If sumsq is non-null it also receives, for every 16-column group g and row m,
+ *   sumsq[g * M + m] = sum over the group's columns of out[m, n]^2   (of the stored bf16 values),
+ * the statistics a later RMSNorm over any union of whole groups needs (fam_attention's q/k
+ * normalisation).  a [M, K], w [N, K] bf16; bias bf16 [N] or null; act FAM_ACT_*.
+ * Replaces: the q/k/v, cross-q and FFN-up projections of the action tokens
+ *           (FB/wan_video_dit.py:188-191, 215, 262) with their bias/GELU epilogues.
+ * Limits: M <= 64; K % 8 == 0, K <= 4096; lda, ldw multiples of 8; a, w 16-byte and out
+ *         8-byte aligned; sumsq holds ceil(N/16)*M floats.
+ */
+int fam_gemm_final(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, int act,
+                   void* out, int64_t ldo, float* sumsq, int64_t M, int64_t N, int64_t K, void* stream);
+
 /* Row sources and row normalisations for fam_rowop. */
 #define FAM_ROWSRC_PARTIALS 0   /* sum of fam_gemm_partial splits                 */
 #define FAM_ROWSRC_SMALLK 1     /* x_in [M, k_in] fp32 times w_in [N, k_in] bf16  */

@@ -486,3 +486,23 @@ def test_launch_events_time_the_kernel():
     us = e0.elapsed_time(e1) * 1e3
     assert 0.0 < us < 1e4
     assert relerr(part.sum(0), O.linear(x.float().cpu(), w.float().cpu(), None)) <= 1e-3
+
+
+@pytest.mark.parametrize("M,N,K,act", [(32, 4096, 1024, 1), (32, 3072, 1024, 0), (32, 1024, 4096, 0), (7, 1000, 256, 2),
+                                        (64, 96, 2048, 1), (1, 16, 8, 0), (17, 30, 4000, 0), (33, 1024, 3000, 1)])
+def test_gemm_final(M, N, K, act):
+    """Whole-K projection with bias/activation epilogue and per-16-column sums of squares."""
+    x, w, b = rnd(M, K, seed=113), rnd(N, K, seed=114, scale=0.02), rnd(N, seed=115, scale=0.02)
+    ref = O.linear(x.float(), w.float(), b.float())
+    ref = O.gelu_tanh(ref) if act == 1 else (O.silu(ref) if act == 2 else ref)
+    xd, wd, bd = dev(x), dev(w), dev(b)
+    y, ss = ops().gemm_final(xd, wd, bd, act, want_sumsq=True)
+    y2, ss2 = ops().gemm_final(xd, wd, bd, act, want_sumsq=True)
+    assert relerr(y, ref) <= TOL
+    assert torch.equal(y, y2) and torch.equal(ss, ss2)
+    yf = y.float().cpu()
+    G = (N + 15) // 16
+    pad = torch.zeros(M, G * 16)
+    pad[:, :N] = yf
+    ss_ref = (pad * pad).reshape(M, G, 16).sum(-1).t()
+    assert torch.allclose(ss.cpu(), ss_ref, rtol=1e-5, atol=1e-6)
