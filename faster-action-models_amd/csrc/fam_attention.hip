@@ -40,7 +40,58 @@ struct AttnArgs {
   float scale_log2;
   const void* mask; int mask_kind; int64_t mbs, mhs, mqs;
   int splits; float* part_o; float* part_ml;   // key splits over workgroups (grid.y)
+  // on-load RMSNorm (+ RoPE) of q / k from the producer's per-16-column sums of squares
+  const float* qss; const float* kss; int64_t ssrs, ssbr, qg0, kg0, nwidth;
+  const bf16* qnw; const bf16* knw; float neps;
+  const float* rcs; const float* rsn; int64_t rrs;
 };
+
+// Reciprocal RMS of producer row `row` over the groups [g0, g0 + nwidth/16): the four lane
+// groups of a row each sum a quarter (16 groups per chunk of four 16-byte loads) and
+// group4_sum adds the quarters in a fixed order.  `first` holds the first chunk, loaded with
+// the kernel's other operands.
+__device__ __forceinline__ void ss_load(const AttnArgs& a, const float* ss, int64_t row, int64_t g0, int lg,
+                                        f32x4 (&r)[4]) {
+  const float* p = ss + row * a.ssrs + g0 + lg * (a.nwidth / 64);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r[j] = *reinterpret_cast<const f32x4*>(p + 4 * j);
+}
+__device__ __forceinline__ float ss_rstd(const AttnArgs& a, const float* ss, int64_t row, int64_t g0, int lg,
+                                         const f32x4 (&first)[4]) {
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s += (first[j][0] + first[j][1]) + (first[j][2] + first[j][3]);
+  const int64_t per = a.nwidth / 64;  // groups per lane group
+  for (int64_t c = 16; c < per; c += 16) {
+    const float* p = ss + row * a.ssrs + g0 + lg * per + c;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(p + 4 * j);
+      s += (v[0] + v[1]) + (v[2] + v[3]);
+    }
+  }
+  s = group4_sum(s);
+  return rsqrtf(s / (float)a.nwidth + a.neps);
+}
+// RMSNorm rounding of the reference (bf16 before the weight) and the RoPE rotation of the
+// fragment's four (d, d+1) pairs, in fp32; cs / sn hold the pairs' table entries.
+__device__ __forceinline__ bf16x8 norm_rope8(bf16x8 x, float rstd, bf16x8 w, f32x4 cs, f32x4 sn, bool rope) {
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = to_f(to_bf(to_f(to_bf(to_f(x[e]) * rstd)) * to_f(w[e])));
+  if (rope) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const float x0 = y[2 * p], x1 = y[2 * p + 1];
+      y[2 * p] = x0 * cs[p] - x1 * sn[p];
+      y[2 * p + 1] = x0 * sn[p] + x1 * cs[p];
+    }
+  }
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = to_bf(y[e]);
+  return o;
+}
 
 // Row addressing of the two key/value segments of one (batch, head), held in registers:
 // key kk < sk0 lives in segment 0, the others in segment 1.  Computing both candidate
@@ -128,7 +179,7 @@ __device__ __forceinline__ bf16x8 softmax_update(const float (&s)[2][4], float& 
 }
 
 // ---------------------------------------------------------------------------------------
-template <int DH, int QT, int NW>
+template <int DH, int QT, int NW, bool QN = false, bool KN = false>
 __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
   constexpr int NC = (DH + 31) / 32;   // 32-wide k-chunks of the head dim (zero padded)
   constexpr int NDT = (DH + 15) / 16;  // 16-row output tiles of the head dim
@@ -157,6 +208,35 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
   const bf16* vsafe = vrows.row(0);
   // Raw loads of one key block from clamped addresses (no selects between the loads).  A key
   // past Sk reads row 0: its score is masked to -inf below and its V row is weighted by 0.
+  // k normalisation operands of one block (KN): sums-of-squares chunk and RoPE entries per key row
+  struct KNorm {
+    f32x4 ss[2][4];
+    f32x4 cs[2][NC], sn[2][NC];
+  };
+  const bool rope = a.rcs != nullptr;
+  const float* rsafe = rope ? a.rcs : a.kss ? a.kss : a.qss;
+  auto kn_load = [&](int64_t blk, KNorm& n) {
+    if constexpr (KN) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const int64_t kk = blk * KB + kt * 16 + l16;
+        const int64_t kc = kk < a.Sk ? kk : 0;
+        ss_load(a, a.kss, b * a.ssbr + kc, a.kg0, lg, n.ss[kt]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int64_t t = kc * a.rrs + (c * 32 + lg * 8) / 2;
+          n.cs[kt][c] = *reinterpret_cast<const f32x4*>(rope ? a.rcs + t : rsafe);
+          n.sn[kt][c] = *reinterpret_cast<const f32x4*>(rope ? a.rsn + t : rsafe);
+        }
+      }
+    }
+  };
+  bf16x8 knw[NC];
+  if constexpr (KN) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) knw[c] = load8(a.knw + h * DH + c * 32 + lg * 8);
+  }
+
   auto gload = [&](int64_t blk, bf16x8 (&kf)[2][NC], bf16x8 (&vc)[NVC]) {
     const int64_t kb = blk * KB;
 #pragma unroll
@@ -188,9 +268,41 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
       const int d0 = c * 32 + lg * 8;
       qf[qt][c] = load8(qi < a.Sq && d0 < DH ? qbase + qi * a.q_rs + d0 : qbase);
     }
+  // q normalisation operands (QN): sums of squares, weights, RoPE entries of the lane's rows
+  f32x4 qss[QT][4], qcs[QT][NC], qsn[QT][NC];
+  bf16x8 qnw[NC];
+  if constexpr (QN) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int64_t qi = qt * 16 + l16;
+      const int64_t qc = qi < a.Sq ? qi : 0;
+      ss_load(a, a.qss, b * a.ssbr + qc, a.qg0, lg, qss[qt]);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const int64_t t = qc * a.rrs + (c * 32 + lg * 8) / 2;
+        qcs[qt][c] = *reinterpret_cast<const f32x4*>(rope ? a.rcs + t : rsafe);
+        qsn[qt][c] = *reinterpret_cast<const f32x4*>(rope ? a.rsn + t : rsafe);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qnw[c] = load8(a.qnw + h * DH + c * 32 + lg * 8);
+  }
   bf16x8 kA[2][NC], vA[NVC], kB[2][NC], vB[NVC];
-  if (kb_beg < kb_end) gload(kb_beg, kA, vA);
+  KNorm nA, nB;
+  if (kb_beg < kb_end) {
+    gload(kb_beg, kA, vA);
+    kn_load(kb_beg, nA);
+  }
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (QN) {
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int64_t qi = qt * 16 + l16;
+      const float r = ss_rstd(a, a.qss, b * a.ssbr + (qi < a.Sq ? qi : 0), a.qg0, lg, qss[qt]);
+#pragma unroll
+      for (int c = 0; c < NC; ++c) qf[qt][c] = norm_rope8(qf[qt][c], r, qnw[c], qcs[qt][c], qsn[qt][c], rope);
+    }
+  }
   if constexpr (DH < 32) {
     // zero-padded head dim: the padding lanes of the q fragments must be exactly 0
 #pragma unroll
@@ -211,8 +323,17 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
   }
 
   // one 32-key block: V -> this wave's transposed LDS tile, S^T = K Q^T, online softmax, O^T += V^T P^T
-  auto process = [&](int64_t blk, bf16x8 (&kf)[2][NC], const bf16x8 (&vc)[NVC]) {
+  auto process = [&](int64_t blk, bf16x8 (&kf)[2][NC], const bf16x8 (&vc)[NVC], const KNorm& kn) {
     const int64_t kb = blk * KB;
+    if constexpr (KN) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const int64_t kk = kb + kt * 16 + l16;
+        const float r = ss_rstd(a, a.kss, b * a.ssbr + (kk < a.Sk ? kk : 0), a.kg0, lg, kn.ss[kt]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) kf[kt][c] = norm_rope8(kf[kt][c], r, knw[c], kn.cs[kt][c], kn.sn[kt][c], rope);
+      }
+    }
     if constexpr (DH < 32) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
@@ -265,13 +386,19 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
 
   // two register sets: the next block's loads are in flight while the current one computes
   for (int64_t blk = kb_beg; blk < kb_end; blk += 2) {
-    if (blk + 1 < kb_end) gload(blk + 1, kB, vB);
+    if (blk + 1 < kb_end) {
+      gload(blk + 1, kB, vB);
+      kn_load(blk + 1, nB);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    process(blk, kA, vA);
+    process(blk, kA, vA, nA);
     if (blk + 1 >= kb_end) break;
-    if (blk + 2 < kb_end) gload(blk + 2, kA, vA);
+    if (blk + 2 < kb_end) {
+      gload(blk + 2, kA, vA);
+      kn_load(blk + 2, nA);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    process(blk + 1, kB, vB);
+    process(blk + 1, kB, vB, nB);
   }
 
   // ---- merge the waves' partial states in wave order
@@ -508,8 +635,25 @@ static int64_t rup(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 // Waves per workgroup: enough to split long key runs, few enough that the per-wave state
 // (query fragments, accumulators, the next block's K/V) fits the register file without spills.
+template <int DH, int QT, bool QN, bool KN>
+static void launch_short_qk(const AttnArgs& a, int64_t nkb, dim3 grid, hipStream_t s) {
+  constexpr bool wide = DH >= 128 && QT >= 2;
+  if (nkb <= 1) FAM_LAUNCH((attn_short_kernel<DH, QT, 1, QN, KN>), grid, dim3(64), 0, s, a);
+  else if (nkb <= 2) FAM_LAUNCH((attn_short_kernel<DH, QT, 2, QN, KN>), grid, dim3(128), 0, s, a);
+  else if (nkb <= 4 || wide) FAM_LAUNCH((attn_short_kernel<DH, QT, 4, QN, KN>), grid, dim3(256), 0, s, a);
+  else FAM_LAUNCH((attn_short_kernel<DH, QT, (wide ? 4 : 8), QN, KN>), grid, dim3((wide ? 4 : 8) * 64), 0, s, a);
+}
+
 template <int DH, int QT>
 static void launch_short_q(const AttnArgs& a, int64_t nkb, dim3 grid, hipStream_t s) {
+  if constexpr (DH >= 64 && QT <= 2) {
+    if (a.qss != nullptr || a.kss != nullptr) {
+      if (a.kss == nullptr) launch_short_qk<DH, QT, true, false>(a, nkb, grid, s);
+      else if (a.qss == nullptr) launch_short_qk<DH, QT, false, true>(a, nkb, grid, s);
+      else launch_short_qk<DH, QT, true, true>(a, nkb, grid, s);
+      return;
+    }
+  }
   constexpr bool wide = DH >= 128 && QT >= 2;
   if (nkb <= 1) FAM_LAUNCH((attn_short_kernel<DH, QT, 1>), grid, dim3(64), 0, s, a);
   else if (nkb <= 2) FAM_LAUNCH((attn_short_kernel<DH, QT, 2>), grid, dim3(128), 0, s, a);
@@ -563,6 +707,28 @@ extern "C" int fam_attention(const fam_attn_desc* d, void* stream) {
   FAM_REQUIRE(d->num_splits <= 1 || (short_q && d->part_o && d->part_ml && fam_host::aligned16(d->part_o) &&
                                      (reinterpret_cast<uintptr_t>(d->part_ml) & 7u) == 0),
               FAM_ERR_INVALID_ARG, "fam_attention: key splits need Sq <= 32 (<= 64 for Dh < 128) and 16-byte aligned partial buffers");
+  if (d->qk_norm) {
+    FAM_REQUIRE(short_q && (Dh == 64 || Dh == 128) && d->sq <= 32, FAM_ERR_UNSUPPORTED,
+                "fam_attention: q/k normalisation needs the short-query path (Sq <= 32) and head_dim 64 or 128");
+    FAM_REQUIRE(d->q_sumsq || d->k_sumsq, FAM_ERR_INVALID_ARG, "fam_attention: qk_norm without sums of squares");
+    FAM_REQUIRE(d->norm_width >= 1024 && d->norm_width % 1024 == 0 && d->ss_row_stride % 4 == 0 &&
+                    d->q_group0 % 4 == 0 && d->k_group0 % 4 == 0 && d->ss_row_stride >= d->norm_width / 16 &&
+                    d->ss_batch_rows >= 0,
+                FAM_ERR_INVALID_ARG, "fam_attention: norm_width must be a multiple of 1024, strides/groups multiples of 4");
+    FAM_REQUIRE(d->heads * Dh <= d->norm_width, FAM_ERR_INVALID_ARG, "fam_attention: heads*head_dim exceeds norm_width");
+    FAM_REQUIRE(d->q_group0 >= 0 && d->k_group0 >= 0 && d->q_group0 + d->norm_width / 16 <= d->ss_row_stride &&
+                    d->k_group0 + d->norm_width / 16 <= d->ss_row_stride,
+                FAM_ERR_INVALID_ARG, "fam_attention: the q/k column groups must lie inside a sums-of-squares row");
+    FAM_REQUIRE((!d->q_sumsq || (d->q_norm_w && fam_host::aligned16(d->q_norm_w) && fam_host::aligned16(d->q_sumsq))) &&
+                    (!d->k_sumsq || (d->k_norm_w && fam_host::aligned16(d->k_norm_w) && fam_host::aligned16(d->k_sumsq))),
+                FAM_ERR_INVALID_ARG, "fam_attention: normalised side needs its 16-byte aligned weight and sums");
+    FAM_REQUIRE(!d->k_sumsq || d->sk1 == 0, FAM_ERR_UNSUPPORTED, "fam_attention: k normalisation needs one key segment");
+    FAM_REQUIRE((d->rope_cos == nullptr) == (d->rope_sin == nullptr), FAM_ERR_INVALID_ARG,
+                "fam_attention: rope_cos and rope_sin must both be given or both be null");
+    FAM_REQUIRE(!d->rope_cos || (fam_host::aligned16(d->rope_cos) && fam_host::aligned16(d->rope_sin) &&
+                                 d->rope_row_stride % 4 == 0 && d->rope_row_stride >= Dh / 2),
+                FAM_ERR_INVALID_ARG, "fam_attention: RoPE tables need 16-byte alignment and a row stride multiple of 4");
+  }
   if (d->batch == 0 || d->sq == 0) return FAM_OK;
 
   AttnArgs a{};
@@ -577,6 +743,12 @@ extern "C" int fam_attention(const fam_attn_desc* d, void* stream) {
   a.mask = d->mask; a.mask_kind = d->mask_kind; a.mbs = d->mask_bs; a.mhs = d->mask_hs; a.mqs = d->mask_qs;
   a.splits = d->num_splits > 1 ? d->num_splits : 1;
   a.part_o = d->part_o; a.part_ml = d->part_ml;
+  if (d->qk_norm) {
+    a.qss = d->q_sumsq; a.kss = d->k_sumsq; a.ssrs = d->ss_row_stride; a.ssbr = d->ss_batch_rows;
+    a.qg0 = d->q_group0; a.kg0 = d->k_group0; a.nwidth = d->norm_width;
+    a.qnw = (const bf16*)d->q_norm_w; a.knw = (const bf16*)d->k_norm_w; a.neps = d->norm_eps;
+    a.rcs = d->rope_cos; a.rsn = d->rope_sin; a.rrs = d->rope_row_stride;
+  }
   hipStream_t s = (hipStream_t)stream;
   switch (Dh) {
     case 8: launch_dh<8>(a, bh, s); break;

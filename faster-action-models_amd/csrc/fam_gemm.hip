@@ -336,7 +336,7 @@ struct FinalArgs {
   const bf16* w; int64_t ldw;
   const bf16* bias; int act;
   bf16* out; int64_t ldo;
-  float* sumsq;              // [ceil(N/16)][M] or null
+  float* sumsq;              // [M][ceil(N/16)] or null
   int64_t M, N, K;
 };
 
@@ -416,7 +416,7 @@ __global__ __launch_bounds__(NW * 64) void final_kernel(FinalArgs g) {
       for (int e = 0; e < 4; ++e)
         if (nc + e < g.N) dst[e] = o[e];
     }
-    if (g.sumsq && lg == 0) g.sumsq[(int64_t)blockIdx.x * g.M + m] = ss;
+    if (g.sumsq && lg == 0) g.sumsq[m * (int64_t)gridDim.x + blockIdx.x] = ss;
   }
 }
 

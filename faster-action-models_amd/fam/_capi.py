@@ -15,7 +15,7 @@ FAM_OK = 0
 FAM_ERR_INVALID_ARG = 1
 FAM_ERR_UNSUPPORTED = 2
 FAM_ERR_LAUNCH = 3
-FAM_ABI_VERSION = 1
+FAM_ABI_VERSION = 2
 
 FAM_MASK_NONE, FAM_MASK_BOOL, FAM_MASK_ADD_F32, FAM_MASK_ADD_BF16 = 0, 1, 2, 3
 FAM_PRO_NONE, FAM_PRO_LAYERNORM, FAM_PRO_ADALN = 0, 1, 2
@@ -48,6 +48,10 @@ class AttnDesc(C.Structure):
         ("scale", C.c_float),
         ("mask", _vp), ("mask_kind", C.c_int), ("mask_bs", _i64), ("mask_hs", _i64), ("mask_qs", _i64),
         ("num_splits", C.c_int), ("part_o", _vp), ("part_ml", _vp),
+        ("qk_norm", C.c_int), ("q_sumsq", _vp), ("k_sumsq", _vp),
+        ("ss_row_stride", _i64), ("ss_batch_rows", _i64), ("q_group0", _i64), ("k_group0", _i64), ("norm_width", _i64),
+        ("q_norm_w", _vp), ("k_norm_w", _vp), ("norm_eps", C.c_float),
+        ("rope_cos", _vp), ("rope_sin", _vp), ("rope_row_stride", _i64),
     ]
 
 

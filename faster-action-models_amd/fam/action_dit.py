@@ -259,6 +259,9 @@ class FusedActionDiT:
         self.ctx_emb = z(ctx_len, H)
         self.ctxkv = z(ctx_len, L * 2 * A)
         self.h = z(M, H)   # normalised input of the next projection
+        # per-row, per-16-column sums of squares of the raw q/k projections (fam_gemm_final)
+        self.ss_qkv = torch.zeros(M, 3 * A // 16, dtype=torch.float32, device=dev)
+        self.ss_q = torch.zeros(M, A // 16, dtype=torch.float32, device=dev)
 
         # split-K partials of the action projections (one buffer, reused launch after launch)
         part_need = 0
@@ -394,7 +397,7 @@ class FusedActionDiT:
         nbytes += (2 * M * N if res is not None else 0) + (2 * M * N if nout is not None else 0)
         self._launch(name, "fam_rowop", C.byref(d), "rowop", nbytes)
 
-    def _attn(self, name, q, q_bs, q_rs, k, k_bs, k_rs, v, v_bs, v_rs, out, sq, sk, splits=1):
+    def _attn(self, name, q, q_bs, q_rs, k, k_bs, k_rs, v, v_bs, v_rs, out, sq, sk, splits=1, qk_norm=None):
         cfg = self.cfg
         Dh = cfg.attn_head_dim
         d = _capi.AttnDesc()
@@ -408,6 +411,19 @@ class FusedActionDiT:
         d.num_splits = splits
         if splits > 1:
             d.part_o, d.part_ml = self.apart_o.data_ptr(), self.apart_ml.data_ptr()
+        if qk_norm is not None:
+            # q (and k) arrive raw from fam_gemm_final; RMSNorm (+ RoPE) happens on load
+            n = qk_norm
+            d.qk_norm = 1
+            d.q_sumsq = n["ss"].data_ptr()
+            d.k_sumsq = n["ss"].data_ptr() if n.get("k_w") is not None else None
+            d.ss_row_stride, d.ss_batch_rows = n["ss"].stride(0), sq
+            d.q_group0, d.k_group0, d.norm_width = 0, n.get("k_group0", 0), cfg.attn_dim
+            d.q_norm_w = n["q_w"].data_ptr()
+            d.k_norm_w = n["k_w"].data_ptr() if n.get("k_w") is not None else None
+            d.norm_eps = float(cfg.eps)
+            if n.get("rope"):
+                d.rope_cos, d.rope_sin, d.rope_row_stride = self.rope_cos.data_ptr(), self.rope_sin.data_ptr(), Dh // 2
         self._descs.append(d)
         A = cfg.attn_dim
         kv_batches = self.B if k_bs else 1   # a batch-broadcast context is read once
@@ -454,6 +470,10 @@ class FusedActionDiT:
         kvp = self.ctxkv.data_ptr()
         RMS, LN, ADALN = _capi.FAM_ROWNORM_RMS, _capi.FAM_ROWNORM_LAYERNORM, _capi.FAM_ROWNORM_ADALN
 
+        # M <= 64 rows, Sq <= 32 and an RMS width the on-load normaliser supports: q/k projections
+        # are single kernels and their norms run inside the attention kernels
+        fused_qk = M <= 64 and S <= 32 and A % 1024 == 0 and Dh in (64, 128)
+
         def mod(t, l, i):   # chunk i of (modulation + t_mod) of block l at step t: [H]
             return self.mods[t, l, i * H:(i + 1) * H]
 
@@ -463,23 +483,39 @@ class FusedActionDiT:
                         bias=w["enc_b"], out=x, norm=ADALN, shift=mod(t, 0, 0), scale=mod(t, 0, 1), nout=h)
             for l in range(L):
                 tag = f"s{t}.b{l}"
-                # q, k, v projection; RMSNorm + RoPE of q and k in the row kernel
-                sp = self._gemm_partial(tag + ".qkv", h, w[f"qkv_w{l}"])
-                self._rowop(tag + ".qkv_row", N=3 * A, splits=sp, bias=w[f"qkv_b{l}"], out=qkv, norm=RMS,
-                            segs=((0, w[f"sa_norm_q_w{l}"]), (A, w[f"sa_norm_k_w{l}"])), rope=True, nout=qkv)
-                self._attn(tag + ".self_attn", qkvp, S * 3 * A, 3 * A, qkvp + 2 * A, S * 3 * A, 3 * A,
-                           qkvp + 4 * A, S * 3 * A, 3 * A, attn, S, S)
+                if fused_qk:
+                    # raw q, k, v in one kernel (+ per-row sums of squares); the attention
+                    # kernel applies RMSNorm + RoPE to q and k as it loads them
+                    self._gemm_final(tag + ".qkv", h, w[f"qkv_w{l}"], w[f"qkv_b{l}"], qkv, sumsq=self.ss_qkv)
+                    self._attn(tag + ".self_attn", qkvp, S * 3 * A, 3 * A, qkvp + 2 * A, S * 3 * A, 3 * A,
+                               qkvp + 4 * A, S * 3 * A, 3 * A, attn, S, S,
+                               qk_norm=dict(ss=self.ss_qkv, q_w=w[f"sa_norm_q_w{l}"], k_w=w[f"sa_norm_k_w{l}"],
+                                            k_group0=A // 16, rope=True))
+                else:
+                    # q, k, v projection; RMSNorm + RoPE of q and k in the row kernel
+                    sp = self._gemm_partial(tag + ".qkv", h, w[f"qkv_w{l}"])
+                    self._rowop(tag + ".qkv_row", N=3 * A, splits=sp, bias=w[f"qkv_b{l}"], out=qkv, norm=RMS,
+                                segs=((0, w[f"sa_norm_q_w{l}"]), (A, w[f"sa_norm_k_w{l}"])), rope=True, nout=qkv)
+                    self._attn(tag + ".self_attn", qkvp, S * 3 * A, 3 * A, qkvp + 2 * A, S * 3 * A, 3 * A,
+                               qkvp + 4 * A, S * 3 * A, 3 * A, attn, S, S)
                 # o projection; x += gate_msa * o; LayerNorm3 (affine) for the cross-attention query
                 sp = self._gemm_partial(tag + ".o", attn, w[f"sa_o_w{l}"])
                 self._rowop(tag + ".o_row", N=H, splits=sp, bias=w[f"sa_o_b{l}"], res=x, gate=mod(t, l, 2), out=x,
                             norm=LN, ln_w=w[f"n3_w{l}"], ln_b=w[f"n3_b{l}"], nout=h)
-                # cross-attention query + its RMSNorm
-                sp = self._gemm_partial(tag + ".cross_q", h, w[f"ca_q_w{l}"])
-                self._rowop(tag + ".cross_q_row", N=A, splits=sp, bias=w[f"ca_q_b{l}"], out=qc, norm=RMS,
-                            segs=((0, w[f"ca_nq_w{l}"]),), nout=qc)
                 kb = kvp + 2 * (l * 2 * A)
-                self._attn(tag + ".cross_attn", qc.data_ptr(), S * A, A, kb, 0, L * 2 * A, kb + 2 * A, 0, L * 2 * A,
-                           attn, S, Lc, splits=self.kv_splits)
+                if fused_qk:
+                    # raw cross-attention query; its RMSNorm happens as the attention loads it
+                    self._gemm_final(tag + ".cross_q", h, w[f"ca_q_w{l}"], w[f"ca_q_b{l}"], qc, sumsq=self.ss_q)
+                    self._attn(tag + ".cross_attn", qc.data_ptr(), S * A, A, kb, 0, L * 2 * A, kb + 2 * A, 0,
+                               L * 2 * A, attn, S, Lc, splits=self.kv_splits,
+                               qk_norm=dict(ss=self.ss_q, q_w=w[f"ca_nq_w{l}"]))
+                else:
+                    # cross-attention query + its RMSNorm
+                    sp = self._gemm_partial(tag + ".cross_q", h, w[f"ca_q_w{l}"])
+                    self._rowop(tag + ".cross_q_row", N=A, splits=sp, bias=w[f"ca_q_b{l}"], out=qc, norm=RMS,
+                                segs=((0, w[f"ca_nq_w{l}"]),), nout=qc)
+                    self._attn(tag + ".cross_attn", qc.data_ptr(), S * A, A, kb, 0, L * 2 * A, kb + 2 * A, 0,
+                               L * 2 * A, attn, S, Lc, splits=self.kv_splits)
                 # cross o projection; x += o; AdaLN2 for the FFN
                 sp = self._gemm_partial(tag + ".cross_o", attn, w[f"ca_o_w{l}"])
                 self._rowop(tag + ".cross_o_row", N=H, splits=sp, bias=w[f"ca_o_b{l}"], res=x, out=x, norm=ADALN,

@@ -255,7 +255,8 @@ def _mask_args(mask: Optional[torch.Tensor], B: int, H: int, Sq: int, Sk: int):
 def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
                    mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
                    k_prefix: Optional[torch.Tensor] = None, v_prefix: Optional[torch.Tensor] = None,
-                   out: Optional[torch.Tensor] = None, num_splits: int = 1) -> torch.Tensor:
+                   out: Optional[torch.Tensor] = None, num_splits: int = 1,
+                   qk_norm: Optional[dict] = None) -> torch.Tensor:
     """Attention on [B, S, H*Dh] tensors; keys/values are cat(k_prefix, k) when a prefix is
     given (the MoT joint attention over a cached video K/V, FB/mot.py:446-478) without
     materialising the concatenation."""
@@ -296,6 +297,22 @@ def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads:
     d.scale = (1.0 / math.sqrt(Dh)) if scale is None else float(scale)
     mp, kind, mbs, mhs, mqs, keep = _mask_args(mask, B, num_heads, Sq, Sk)
     d.mask, d.mask_kind, d.mask_bs, d.mask_hs, d.mask_qs = mp, kind, mbs, mhs, mqs
+    if qk_norm is not None:
+        # on-load RMSNorm (+ RoPE) of q / k from fam_gemm_final sums of squares (include/fam_hip.h)
+        n = qk_norm
+        d.qk_norm = 1
+        qs, ks = n.get("q_sumsq"), n.get("k_sumsq")
+        ss = qs if qs is not None else ks
+        d.q_sumsq = qs.data_ptr() if qs is not None else None
+        d.k_sumsq = ks.data_ptr() if ks is not None else None
+        d.ss_row_stride, d.ss_batch_rows = ss.stride(0), n["ss_batch_rows"]
+        d.q_group0, d.k_group0, d.norm_width = n.get("q_group0", 0), n.get("k_group0", 0), n["norm_width"]
+        d.q_norm_w = n["q_norm_w"].data_ptr() if qs is not None else None
+        d.k_norm_w = n["k_norm_w"].data_ptr() if ks is not None else None
+        d.norm_eps = float(n.get("eps", 1e-6))
+        if n.get("rope") is not None:
+            cs, sn, trs = n["rope"]
+            d.rope_cos, d.rope_sin, d.rope_row_stride = cs.data_ptr(), sn.data_ptr(), trs
     part_o = part_ml = None
     if num_splits > 1:
         # key splits over workgroups: per-split partials, then an ordered merge
@@ -397,14 +414,14 @@ def gemm_partial(a: torch.Tensor, w: torch.Tensor):
 def gemm_final(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None, act: int = _capi.FAM_ACT_NONE,
                out: Optional[torch.Tensor] = None, want_sumsq: bool = False):
     """act(a w^T + bias) for M <= 64 in one kernel; with want_sumsq also the per-row sum of
-    squares of each 16-column group of the (bf16) output, [ceil(N/16), M] fp32."""
+    squares of each 16-column group of the (bf16) output, [M, ceil(N/16)] fp32."""
     _check(a, "a")
     _check(w, "w")
     M, K = a.shape
     N = w.shape[0]
     if out is None:
         out = torch.empty((M, N), dtype=_BF16, device=a.device)
-    ss = torch.empty(((N + 15) // 16, M), dtype=torch.float32, device=a.device) if want_sumsq else None
+    ss = torch.empty((M, (N + 15) // 16), dtype=torch.float32, device=a.device) if want_sumsq else None
     call("fam_gemm_final", a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0),
          bias.data_ptr() if bias is not None else None, act, out.data_ptr(), out.stride(0),
          ss.data_ptr() if ss is not None else None, M, N, K, _stream(a))

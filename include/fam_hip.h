@@ -32,7 +32,7 @@ extern "C" {
 #define FAM_ERR_UNSUPPORTED 2
 #define FAM_ERR_LAUNCH 3
 
-#define FAM_ABI_VERSION 1
+#define FAM_ABI_VERSION 2
 
 /*
  * No entry point allocates, keeps state between calls or communicates between
@@ -133,9 +133,33 @@ typedef struct fam_attn_desc {
   float scale;
   const void* mask; int mask_kind; int64_t mask_bs, mask_hs, mask_qs;
   int num_splits; float* part_o; float* part_ml;
+  /* RMSNorm (+ RoPE) of q and/or k applied as they are loaded (qk_norm = 1); see below. */
+  int qk_norm;
+  const float* q_sumsq; const float* k_sumsq;
+  int64_t ss_row_stride, ss_batch_rows, q_group0, k_group0, norm_width;
+  const void* q_norm_w; const void* k_norm_w;
+  float norm_eps;
+  const float* rope_cos; const float* rope_sin; int64_t rope_row_stride;
 } fam_attn_desc;
 
 int fam_attention(const fam_attn_desc* d, void* stream);
+
+/*
+ * On-load q/k normalisation (qk_norm = 1, short-query path only): q and k arrive as the raw
+ * projections (fam_gemm_final output, bias added) and are normalised the way the reference's
+ * q/k post-processing does, RMSNorm over the full H*Dh row with a bf16 rounding before the
+ * weight, then the RoPE rotation of (d, d+1) pairs (FB/wan_video_dit.py:156-167, 58-70,
+ * 193-196, 215-216):
+ *   rstd(b, s) = rsqrt(sum_{g < norm_width/16} ss[row*ss_row_stride + group0 + g] / norm_width + eps),
+ *   row = b*ss_batch_rows + s, ss = q_sumsq / k_sumsq (fam_gemm_final's sums of squares);
+ *   y[d] = bf16(bf16(x[d] * rstd) * w[h*head_dim + d]);
+ *   with rope_cos/sin (complex layout [pos][head_dim/2], row stride rope_row_stride, pos = s):
+ *   (y[2j], y[2j+1]) rotated by (cos, sin)[s][ (d of y[2j]) / 2 ].
+ * A null q_sumsq / k_sumsq leaves that side as loaded.
+ * Limits: head_dim 64 or 128; norm_width a multiple of 256; ss_row_stride, q_group0, k_group0
+ * and rope_row_stride multiples of 4; one key segment when k is normalised; 16-byte aligned
+ * weights and tables.
+ */
 
 /*
  * Key split over workgroups (Sq <= 32, or <= 64 for head_dim < 128): with num_splits = S > 1,
@@ -209,14 +233,14 @@ int fam_gemm_partial_splits(int64_t M, int64_t N, int64_t K);
 /*
  * fam_gemm_final -- out[m, n] = bf16(act(sum_k a[m, k] * w[n, k] + bias[n])) for 1 <= M <= 64
  * with the whole K of 16 output columns in one workgroup (no partials, no second kernel).
- * If sumsq is non-null it also receives, for every 16-column group g and row m,
- *   sumsq[g * M + m] = sum over the group's columns of out[m, n]^2   (of the stored bf16 values),
+ * If sumsq is non-null it also receives, for every row m and 16-column group g < G = ceil(N/16),
+ *   sumsq[m * G + g] = sum over the group's columns of out[m, n]^2   (of the stored bf16 values),
  * the statistics a later RMSNorm over any union of whole groups needs (fam_attention's q/k
  * normalisation).  a [M, K], w [N, K] bf16; bias bf16 [N] or null; act FAM_ACT_*.
  * Replaces: the q/k/v, cross-q and FFN-up projections of the action tokens
  *           (FB/wan_video_dit.py:188-191, 215, 262) with their bias/GELU epilogues.
  * Limits: M <= 64; K % 8 == 0, K <= 4096; lda, ldw multiples of 8; a, w 16-byte and out
- *         8-byte aligned; sumsq holds ceil(N/16)*M floats.
+ *         8-byte aligned; sumsq holds M*ceil(N/16) floats.
  */
 int fam_gemm_final(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias, int act,
                    void* out, int64_t ldo, float* sumsq, int64_t M, int64_t N, int64_t K, void* stream);

@@ -45,8 +45,11 @@ def test_fused_plan_builds_on_host():
         # prologue: copy, sinusoid, 3 time GEMMs, modulation, 3 context GEMMs, one K-norm per layer
         pro = 9 + cfg.num_layers
         # per step: encoder row + per block (6 projections x 2 + self-attn + cross-attn + combine) + head x 2;
-        # at M <= 64 the FFN-up projection is one whole-K kernel with its epilogue
-        per_block = 15 - (0 if m.kv_splits > 1 else 1) - (1 if batch * 32 <= 64 else 0)
+        # at M <= 64 the FFN-up projection is one whole-K kernel with its epilogue (and, when the
+        # attention width allows the on-load q/k norm, so are the q/k/v and cross-q projections)
+        small = batch * 32 <= 64
+        fused_qk = small and cfg.attn_dim % 1024 == 0
+        per_block = 15 - (0 if m.kv_splits > 1 else 1) - (1 if small else 0) - (2 if fused_qk else 0)
         assert m.num_launches == pro + 3 * (1 + cfg.num_layers * per_block + 2)
         assert kinds.count("attention") == 3 * 2 * cfg.num_layers
         if batch * 32 > 64:
@@ -54,5 +57,12 @@ def test_fused_plan_builds_on_host():
         else:
             assert kinds.count("gemm_partial") == 3 * (5 * cfg.num_layers + 1)
             assert kinds.count("gemm_final") == 3 * cfg.num_layers
+    # attention width 1024: q/k norms move into the attention kernels
+    cfg2 = AD.ActionDiTConfig(num_layers=1, hidden_dim=64, ffn_dim=128, text_dim=48, freq_dim=32, num_heads=16,
+                              attn_head_dim=64)
+    m2 = AD.FusedActionDiT(cfg2, AD.synthetic_params(cfg2, 3), batch=1, seq_len=32, ctx_len=200, num_steps=2,
+                           device="cpu")
+    kinds2 = [d["kernel"] for d in m2.plan.meta]
+    assert kinds2.count("gemm_final") == 2 * 3 and kinds2.count("gemm_partial") == 2 * (3 + 1)
     fwd = AD.FusedActionDiT(cfg, params, batch=1, seq_len=32, ctx_len=200, num_steps=1, device="cpu", mode="forward")
     assert fwd.plan.meta[-1]["kernel"] == "rowop"

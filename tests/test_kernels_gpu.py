@@ -504,5 +504,44 @@ def test_gemm_final(M, N, K, act):
     G = (N + 15) // 16
     pad = torch.zeros(M, G * 16)
     pad[:, :N] = yf
-    ss_ref = (pad * pad).reshape(M, G, 16).sum(-1).t()
+    ss_ref = (pad * pad).reshape(M, G, 16).sum(-1)
     assert torch.allclose(ss.cpu(), ss_ref, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("B", [1, 2])
+def test_attention_qk_norm_on_load(B):
+    """Raw q/k from fam_gemm_final + its sums of squares; attention applies RMSNorm (bf16
+    before the weight) and RoPE to q and k as it loads them (FB/wan_video_dit.py:193-196)."""
+    S, H, Dh, Kd = 32, 16, 64, 1024
+    A = H * Dh
+    x, w, bb = rnd(B * S, Kd, seed=116), rnd(3 * A, Kd, seed=117, scale=0.02), rnd(3 * A, seed=118, scale=0.02)
+    wq, wk = rnd(A, seed=119, scale=0.2) + 1, rnd(A, seed=120, scale=0.2) + 1
+    fr = O.action_freqs(Dh, S)
+    qkv, ss = ops().gemm_final(dev(x), dev(w), dev(bb), want_sumsq=True)
+    cs, sn, trs, _ = ops().rope_tables(fr, "complex", torch.device("cuda"))
+    wqd, wkd = dev(wq), dev(wk)
+    q3 = qkv.view(B, S, 3 * A)
+    y = ops().attention_bshd(q3[:, :, :A], q3[:, :, A:2 * A], q3[:, :, 2 * A:], H,
+                             qk_norm=dict(q_sumsq=ss, k_sumsq=ss, ss_batch_rows=S, q_group0=0, k_group0=A // 16,
+                                          norm_width=A, q_norm_w=wqd, k_norm_w=wkd, eps=1e-6, rope=(cs, sn, trs)))
+    raw = qkv.float().cpu().view(B, S, 3 * A)
+    q = O.rope_apply(O.rms_norm(raw[..., :A].to(torch.bfloat16), wq, 1e-6).float(), fr, H)
+    k = O.rope_apply(O.rms_norm(raw[..., A:2 * A].to(torch.bfloat16), wk, 1e-6).float(), fr, H)
+    ref = O.flash_attention(q, k, raw[..., 2 * A:], H)
+    assert relerr(y, ref) <= TOL
+
+
+def test_attention_q_norm_cross_with_splits():
+    """Cross attention with the query normalised on load (no RoPE) and 13 key splits."""
+    S, H, Dh, Lc, Kd = 32, 16, 64, 1560, 1024
+    A = H * Dh
+    x, w, bb = rnd(S, Kd, seed=121), rnd(A, Kd, seed=122, scale=0.02), rnd(A, seed=123, scale=0.02)
+    wq = rnd(A, seed=124, scale=0.2) + 1
+    k, v = rnd(1, Lc, A, seed=125), rnd(1, Lc, A, seed=126)
+    q_raw, ss = ops().gemm_final(dev(x), dev(w), dev(bb), want_sumsq=True)
+    wqd, kd, vd = dev(wq), dev(k), dev(v)
+    y = ops().attention_bshd(q_raw.view(1, S, A), kd, vd, H, num_splits=13,
+                             qk_norm=dict(q_sumsq=ss, ss_batch_rows=S, norm_width=A, q_norm_w=wqd, eps=1e-6))
+    q = O.rms_norm(q_raw.cpu().view(1, S, A), wq, 1e-6).float()
+    ref = O.flash_attention(q, k.float(), v.float(), H)
+    assert relerr(y, ref) <= TOL
