@@ -486,6 +486,161 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// attn_self_kernel: the action tokens' own attention (Sq <= 32, Sk <= 32, one key segment, no
+// mask), one workgroup of 4 waves per (batch, head).  All 256 threads stage the head's q and k
+// (normalised and rotated on the way when QKN) and the transposed V in LDS, one 16-byte chunk
+// of each per thread (two for Dh = 128); then waves 0 and 1 each finish 16 queries over the
+// (single) key block with exact softmax, no running rescale and no merge.
+template <int DH, bool QKN>
+__global__ __launch_bounds__(256) void attn_self_kernel(AttnArgs a) {
+  constexpr int NC = DH / 32;             // 32-wide k-chunks of the head dim
+  constexpr int NDT = DH / 16;            // 16-row output tiles of the head dim
+  constexpr int CPR = DH / 8;             // 16-byte chunks per row
+  constexpr int CH = 32 * CPR / 256;      // chunks per thread per tensor (1 or 2)
+  constexpr int LD = DH + 8;              // padded LDS rows (bf16)
+  __shared__ bf16 Qs[32][LD];
+  __shared__ bf16 Ks[32][LD];
+  __shared__ bf16 Vt[DH][32 + 8];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const uint32_t bh = blockIdx.x, H32 = (uint32_t)a.H;
+  const uint32_t b = bh / H32, h = bh - b * H32;
+  const int Sq = (int)a.Sq, Sk = (int)a.Sk;
+  const bf16* qb = a.q + b * a.q_bs + h * a.q_hs;
+  const bf16* kb = a.k0 + b * a.k0_bs + h * a.k0_hs;
+  const bf16* vb = a.v0 + b * a.v0_bs + h * a.v0_hs;
+
+  // ---- phase 1: raw loads of this thread's chunks (row r, dims d0..d0+7)
+  bf16x8 qr[CH], kr[CH], vr[CH];
+  f32x4 qss[CH][2], kss[CH][2], qcs[CH], qsn[CH], kcs[CH], ksn[CH];
+  bf16x8 qw[CH], kw[CH];
+  const bool rope = QKN && a.rcs != nullptr;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int idx = tid + 256 * c, r = idx / CPR, d0 = (idx % CPR) * 8;
+    const int rq = r < Sq ? r : 0, rk = r < Sk ? r : 0;
+    qr[c] = load8(qb + rq * a.q_rs + d0);
+    kr[c] = load8(kb + rk * a.k0_rs + d0);
+    vr[c] = load8(vb + rk * a.v0_rs + d0);
+    if constexpr (QKN) {
+      // the row's sums of squares: CPR threads share a row, each sums nwidth/16/CPR groups
+      const int64_t per = a.nwidth / 16 / CPR;
+      const float* qsp = a.qss + (b * a.ssbr + rq) * a.ssrs + a.qg0 + (idx % CPR) * per;
+      const float* ksp = a.kss + (b * a.ssbr + rk) * a.ssrs + a.kg0 + (idx % CPR) * per;
+      // (a share of 4 groups reads its first 16 bytes twice and counts them once, below)
+      qss[c][0] = *reinterpret_cast<const f32x4*>(qsp);
+      qss[c][1] = *reinterpret_cast<const f32x4*>(per >= 8 ? qsp + 4 : qsp);
+      kss[c][0] = *reinterpret_cast<const f32x4*>(ksp);
+      kss[c][1] = *reinterpret_cast<const f32x4*>(per >= 8 ? ksp + 4 : ksp);
+      qw[c] = load8(a.qnw + h * DH + d0);
+      kw[c] = load8(a.knw + h * DH + d0);
+      const float* cb = rope ? a.rcs : a.qss;
+      const float* sb = rope ? a.rsn : a.qss;
+      qcs[c] = *reinterpret_cast<const f32x4*>(cb + (rope ? rq * a.rrs + d0 / 2 : 0));
+      qsn[c] = *reinterpret_cast<const f32x4*>(sb + (rope ? rq * a.rrs + d0 / 2 : 0));
+      kcs[c] = *reinterpret_cast<const f32x4*>(cb + (rope ? rk * a.rrs + d0 / 2 : 0));
+      ksn[c] = *reinterpret_cast<const f32x4*>(sb + (rope ? rk * a.rrs + d0 / 2 : 0));
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- phase 2: normalise, stage in LDS
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int idx = tid + 256 * c, r = idx / CPR, d0 = (idx % CPR) * 8;
+    bf16x8 qn = qr[c], kn = kr[c];
+    if constexpr (QKN) {
+      const int64_t per = a.nwidth / 16 / CPR;
+      float sq = 0.f, sk = 0.f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (j == 1 && per < 8) break;
+        sq += (qss[c][j][0] + qss[c][j][1]) + (qss[c][j][2] + qss[c][j][3]);
+        sk += (kss[c][j][0] + kss[c][j][1]) + (kss[c][j][2] + kss[c][j][3]);
+      }
+      // groups beyond the first 8 of this thread's share (wider rows), in order
+      for (int64_t g = 8; g < per; g += 4) {
+        const int rq = r < Sq ? r : 0, rk = r < Sk ? r : 0;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(a.qss + (b * a.ssbr + rq) * a.ssrs + a.qg0 + (idx % CPR) * per + g);
+        const f32x4 y = *reinterpret_cast<const f32x4*>(a.kss + (b * a.ssbr + rk) * a.ssrs + a.kg0 + (idx % CPR) * per + g);
+        sq += (x[0] + x[1]) + (x[2] + x[3]);
+        sk += (y[0] + y[1]) + (y[2] + y[3]);
+      }
+      // sum over the CPR threads of the row (consecutive lanes), fixed butterfly order
+#pragma unroll
+      for (int o = 1; o < CPR; o <<= 1) {
+        sq += __shfl_xor(sq, o, kWave);
+        sk += __shfl_xor(sk, o, kWave);
+      }
+      const float rq = rsqrtf(sq / (float)a.nwidth + a.neps), rk = rsqrtf(sk / (float)a.nwidth + a.neps);
+      qn = norm_rope8(qr[c], rq, qw[c], qcs[c], qsn[c], rope);
+      kn = norm_rope8(kr[c], rk, kw[c], kcs[c], ksn[c], rope);
+    }
+    *reinterpret_cast<bf16x8*>(&Qs[r][d0]) = qn;
+    *reinterpret_cast<bf16x8*>(&Ks[r][d0]) = kn;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) Vt[d0 + e][r] = vr[c][e];
+  }
+  __syncthreads();
+  if (wave >= 2 || wave * 16 >= Sq) return;
+
+  // ---- phase 3: wave w finishes queries 16w..16w+15 (S^T = K Q^T, lane = one query)
+  const int qt = wave;
+  bf16x8 qf[NC], kf[2][NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    qf[c] = *reinterpret_cast<const bf16x8*>(&Qs[qt * 16 + l16][c * 32 + lg * 8]);
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) kf[kt][c] = *reinterpret_cast<const bf16x8*>(&Ks[kt * 16 + l16][c * 32 + lg * 8]);
+  }
+  float sc[2][4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc = mfma16(kf[kt][c], qf[c], acc);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int kk = kt * 16 + lg * 4 + e;   // keys {4g..4g+3} and {16+4g..16+4g+3} of lane group g
+      const float v = kk < Sk ? acc[e] * a.scale_log2 : -INFINITY;
+      sc[kt][e] = v;
+      mx = fmaxf(mx, v);
+    }
+  }
+  mx = group4_max(mx);
+  float psum = 0.f;
+  bf16x8 pf;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float pv = exp2f(sc[kt][e] - mx);
+      psum += pv;
+      pf[kt * 4 + e] = to_bf(pv);
+    }
+  const float inv = 1.0f / group4_sum(psum);
+  const int q = qt * 16 + l16;
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) {
+    const int d = t * 16 + l16;
+    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&Vt[d][lg * 4]);
+    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(&Vt[d][16 + lg * 4]);
+    bf16x8 vf;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { vf[e] = lo[e]; vf[4 + e] = hi[e]; }
+    const f32x4 o = mfma16(vf, pf, f32x4{0.f, 0.f, 0.f, 0.f});   // O^T[d = 16t + 4lg + i][q]
+    if (q < Sq) {
+      bf16x4 ov;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ov[e] = to_bf(o[e] * inv);
+      *reinterpret_cast<bf16x4*>(a.o + b * a.o_bs + q * a.o_rs + h * a.o_hs + t * 16 + lg * 4) = ov;
+    }
+  }
+}
+
 // Merge of the key-split partials: one thread per (b*h, q, 4 channels), splits in order.
 // Up to MAXS splits are loaded before the first use (one memory round trip); more splits
 // (MAXS = 0) take the looped form.
@@ -663,6 +818,15 @@ static void launch_short_q(const AttnArgs& a, int64_t nkb, dim3 grid, hipStream_
 
 template <int DH>
 static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
+  if constexpr (DH == 64 || DH == 128) {
+    // the action tokens over their own keys: one workgroup per head, LDS-staged q/k/v
+    if (a.Sq <= 32 && a.Sk >= 1 && a.Sk <= 32 && a.sk0 == a.Sk && a.mask_kind == FAM_MASK_NONE && a.splits == 1 &&
+        (a.qss == nullptr) == (a.kss == nullptr)) {
+      if (a.qss) FAM_LAUNCH((attn_self_kernel<DH, true>), dim3((unsigned)bh), dim3(256), 0, s, a);
+      else FAM_LAUNCH((attn_self_kernel<DH, false>), dim3((unsigned)bh), dim3(256), 0, s, a);
+      return;
+    }
+  }
   // (Dh = 128 with more than 32 queries would not fit the short kernel's registers)
   if (a.Sq <= 32 || (a.Sq <= 64 && DH < 128)) {
     const int64_t nkb = ((a.Sk + KB - 1) / KB + a.splits - 1) / a.splits;  // key blocks per workgroup

@@ -545,3 +545,33 @@ def test_attention_q_norm_cross_with_splits():
     q = O.rms_norm(q_raw.cpu().view(1, S, A), wq, 1e-6).float()
     ref = O.flash_attention(q, k.float(), v.float(), H)
     assert relerr(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("B,Sq,Sk,H,Dh", [(1, 32, 32, 16, 64), (2, 20, 27, 4, 64), (1, 32, 32, 24, 128), (3, 7, 1, 2, 128)])
+def test_attention_self_small(B, Sq, Sk, H, Dh):
+    """The action tokens' own attention (Sq, Sk <= 32, no mask): the LDS-staged kernel."""
+    q, k, v = rnd(B, Sq, H * Dh, seed=127), rnd(B, Sk, H * Dh, seed=128), rnd(B, Sk, H * Dh, seed=129)
+    ref = O.flash_attention(q.float(), k.float(), v.float(), H)
+    y = ops().attention_bshd(dev(q), dev(k), dev(v), H)
+    assert relerr(y, ref) <= TOL
+
+
+def test_attention_qk_norm_on_load_wide_heads():
+    """Real FastWAM action-expert attention width (24 x 128 = 3072) with q/k norm + RoPE on load."""
+    S, H, Dh, Kd = 32, 24, 128, 1024
+    A = H * Dh
+    x, w, bb = rnd(S, Kd, seed=130), rnd(3 * A, Kd, seed=131, scale=0.02), rnd(3 * A, seed=132, scale=0.02)
+    wq, wk = rnd(A, seed=133, scale=0.2) + 1, rnd(A, seed=134, scale=0.2) + 1
+    fr = O.action_freqs(Dh, S)
+    qkv, ss = ops().gemm_final(dev(x), dev(w), dev(bb), want_sumsq=True)
+    cs, sn, trs, _ = ops().rope_tables(fr, "complex", torch.device("cuda"))
+    wqd, wkd = dev(wq), dev(wk)
+    q3 = qkv.view(1, S, 3 * A)
+    y = ops().attention_bshd(q3[:, :, :A], q3[:, :, A:2 * A], q3[:, :, 2 * A:], H,
+                             qk_norm=dict(q_sumsq=ss, k_sumsq=ss, ss_batch_rows=S, q_group0=0, k_group0=A // 16,
+                                          norm_width=A, q_norm_w=wqd, k_norm_w=wkd, eps=1e-6, rope=(cs, sn, trs)))
+    raw = qkv.float().cpu().view(1, S, 3 * A)
+    q = O.rope_apply(O.rms_norm(raw[..., :A].to(torch.bfloat16), wq, 1e-6).float(), fr, H)
+    k = O.rope_apply(O.rms_norm(raw[..., A:2 * A].to(torch.bfloat16), wk, 1e-6).float(), fr, H)
+    ref = O.flash_attention(q, k, raw[..., 2 * A:], H)
+    assert relerr(y, ref) <= TOL
