@@ -641,6 +641,224 @@ __global__ __launch_bounds__(256) void attn_self_kernel(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// attn_cross_kernel: 32 or fewer queries over a long key sequence in one segment, no mask (the
+// action tokens over the context).  Grid (batch*head, key split), 4 waves.  The workgroup's
+// threads normalise the head's queries once into LDS (QN: RMSNorm from the producer's sums of
+// squares); each wave then streams its own run of 32-key blocks with the next block's loads
+// in flight, and the four partial softmax states are merged through LDS with two barriers.
+// Output: o, or with splits the unnormalised partial (o, m, l) merged by attn_combine_kernel.
+template <int DH, bool QN>
+__global__ __launch_bounds__(256) void attn_cross_kernel(AttnArgs a) {
+  constexpr int NW = 4;
+  constexpr int NC = DH / 32, NDT = DH / 16, CPR = DH / 8, CH = 32 * CPR / 256;
+  constexpr int NVC = KB * DH / 8 / 64;    // 16-byte V chunks per lane per block
+  constexpr int LD = DH + 8;
+  __shared__ bf16 Qs[32][LD];
+  __shared__ bf16 Vt[NW][DH][KB + 8];
+  __shared__ float s_m[NW][32], s_l[NW][32];
+  __shared__ float s_o[NW][32][DH + 4];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const uint32_t bh = blockIdx.x, H32 = (uint32_t)a.H;
+  const uint32_t b = bh / H32, h = bh - b * H32;
+  const int Sq = (int)a.Sq, Sk = (int)a.Sk;
+  const int nkb_all = (Sk + KB - 1) / KB;
+  const int per_split = (nkb_all + a.splits - 1) / a.splits;
+  const int wg_beg = min(nkb_all, (int)blockIdx.y * per_split);
+  const int wg_end = min(nkb_all, wg_beg + per_split);
+  const int per = (wg_end - wg_beg + NW - 1) / NW;
+  const int kb_beg = min(wg_end, wg_beg + wave * per), kb_end = min(wg_end, kb_beg + per);
+
+  const bf16* qb = a.q + b * a.q_bs + h * a.q_hs;
+  const bf16* kbase = a.k0 + b * a.k0_bs + h * a.k0_hs;
+  const bf16* vbase = a.v0 + b * a.v0_bs + h * a.v0_hs;
+  auto gload = [&](int blk, bf16x8 (&kf)[2][NC], bf16x8 (&vc)[NVC]) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      const int kk = blk * KB + kt * 16 + l16;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) kf[kt][c] = load8(kbase + (int64_t)(kk < Sk ? kk : 0) * a.k0_rs + c * 32 + lg * 8);
+    }
+#pragma unroll
+    for (int p = 0; p < NVC; ++p) {
+      const int cidx = lane + 64 * p, key = cidx / CPR, d0 = (cidx % CPR) * 8;
+      const int kk = blk * KB + key;
+      vc[p] = load8(vbase + (int64_t)(kk < Sk ? kk : 0) * a.v0_rs + d0);
+    }
+  };
+
+  // ---- phase 1: raw loads (this thread's query chunks and their norm operands; the wave's first block)
+  bf16x8 qr[CH], qw[CH];
+  f32x4 qss[CH][2];
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int idx = tid + 256 * c, r = idx / CPR, d0 = (idx % CPR) * 8;
+    const int rq = r < Sq ? r : 0;
+    qr[c] = load8(qb + rq * a.q_rs + d0);
+    if constexpr (QN) {
+      const int64_t sper = a.nwidth / 16 / CPR;
+      const float* qsp = a.qss + (b * a.ssbr + rq) * a.ssrs + a.qg0 + (idx % CPR) * sper;
+      qss[c][0] = *reinterpret_cast<const f32x4*>(qsp);
+      qss[c][1] = *reinterpret_cast<const f32x4*>(sper >= 8 ? qsp + 4 : qsp);
+      qw[c] = load8(a.qnw + h * DH + d0);
+    }
+  }
+  bf16x8 kA[2][NC], vA[NVC], kB[2][NC], vB[NVC];
+  if (kb_beg < kb_end) gload(kb_beg, kA, vA);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- phase 2: normalised queries -> LDS
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int idx = tid + 256 * c, r = idx / CPR, d0 = (idx % CPR) * 8;
+    bf16x8 qn = qr[c];
+    if constexpr (QN) {
+      const int64_t sper = a.nwidth / 16 / CPR;
+      float sq = 0.f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (j == 1 && sper < 8) break;
+        sq += (qss[c][j][0] + qss[c][j][1]) + (qss[c][j][2] + qss[c][j][3]);
+      }
+      for (int64_t g = 8; g < sper; g += 4) {
+        const int rq = r < Sq ? r : 0;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(a.qss + (b * a.ssbr + rq) * a.ssrs + a.qg0 + (idx % CPR) * sper + g);
+        sq += (x[0] + x[1]) + (x[2] + x[3]);
+      }
+#pragma unroll
+      for (int o = 1; o < CPR; o <<= 1) sq += __shfl_xor(sq, o, kWave);
+      const float rq = rsqrtf(sq / (float)a.nwidth + a.neps);
+      qn = norm_rope8(qr[c], rq, qw[c], f32x4{1.f, 1.f, 1.f, 1.f}, f32x4{0.f, 0.f, 0.f, 0.f}, false);
+    }
+    *reinterpret_cast<bf16x8*>(&Qs[r][d0]) = qn;
+  }
+  __syncthreads();
+  bf16x8 qf[2][NC];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qf[qt][c] = *reinterpret_cast<const bf16x8*>(&Qs[qt * 16 + l16][c * 32 + lg * 8]);
+
+  f32x4 oacc[2][NDT];
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) oacc[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto process = [&](int blk, const bf16x8 (&kf)[2][NC], const bf16x8 (&vc)[NVC]) {
+#pragma unroll
+    for (int p = 0; p < NVC; ++p) {
+      const int cidx = lane + 64 * p, key = cidx / CPR, d0 = (cidx % CPR) * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Vt[wave][d0 + e][key] = vc[p][e];
+    }
+    __builtin_amdgcn_wave_barrier();
+    bf16x8 vfr[NDT];
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      const int d = t * 16 + l16;
+      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&Vt[wave][d][lg * 4]);
+      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(&Vt[wave][d][16 + lg * 4]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { vfr[t][e] = lo[e]; vfr[t][4 + e] = hi[e]; }
+    }
+    const bool full = (blk + 1) * KB <= Sk;
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      float sc[2][4];
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc = mfma16(kf[kt][c], qf[qt][c], acc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float v = acc[e] * a.scale_log2;
+          if (!full) v = (blk * KB + kt * 16 + lg * 4 + e < Sk) ? v : -INFINITY;
+          sc[kt][e] = v;
+          mloc = fmaxf(mloc, v);
+        }
+      }
+      const float m_new = fmaxf(m_run[qt], group4_max(mloc));   // finite: the block has a valid key
+      const float alpha = exp2f(m_run[qt] - m_new);
+      float psum = 0.f;
+      bf16x8 pf;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float pv = exp2f(sc[kt][e] - m_new);
+          psum += pv;
+          pf[kt * 4 + e] = to_bf(pv);
+        }
+      l_run[qt] = l_run[qt] * alpha + group4_sum(psum);
+      m_run[qt] = m_new;
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) oacc[qt][t] = mfma16(vfr[t], pf, oacc[qt][t] * alpha);
+    }
+    __builtin_amdgcn_wave_barrier();  // the next block may overwrite this wave's V tile
+  };
+
+  for (int blk = kb_beg; blk < kb_end; blk += 2) {
+    if (blk + 1 < kb_end) gload(blk + 1, kB, vB);
+    __builtin_amdgcn_sched_barrier(0);
+    process(blk, kA, vA);
+    if (blk + 1 >= kb_end) break;
+    if (blk + 2 < kb_end) gload(blk + 2, kA, vA);
+    __builtin_amdgcn_sched_barrier(0);
+    process(blk + 1, kB, vB);
+  }
+
+  // ---- merge the four waves' states: (m, l) first, then each wave's rescaled o, summed in wave order
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+    if (lg == 0) { s_m[wave][qt * 16 + l16] = m_run[qt]; s_l[wave][qt * 16 + l16] = l_run[qt]; }
+  __syncthreads();
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int q = qt * 16 + l16;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_m[w][q]);
+    const float sc = (mx == -INFINITY) ? 0.f : exp2f(m_run[qt] - mx);  // a wave without keys has m = -inf
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+      *reinterpret_cast<f32x4*>(&s_o[wave][q][t * 16 + lg * 4]) = oacc[qt][t] * sc;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < 32 * (DH / 4); idx += 256) {
+    const int q = idx / (DH / 4), d0 = (idx % (DH / 4)) * 4;
+    if (q >= Sq) continue;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_m[w][q]);
+    float L = 0.f;
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        L += s_l[w][q] * exp2f(s_m[w][q] - mx);
+        v += *reinterpret_cast<const f32x4*>(&s_o[w][q][d0]);
+      }
+    }
+    if (a.splits > 1) {
+      const int64_t row = ((int64_t)blockIdx.y * gridDim.x + bh) * a.Sq + q;
+      *reinterpret_cast<f32x4*>(a.part_o + row * DH + d0) = v;
+      if (d0 == 0) *reinterpret_cast<float2*>(a.part_ml + row * 2) = make_float2(mx, L);
+    } else {
+      const float inv = L > 0.f ? 1.0f / L : 0.f;
+      bf16x4 ov;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ov[e] = to_bf(v[e] * inv);
+      *reinterpret_cast<bf16x4*>(a.o + b * a.o_bs + q * a.o_rs + h * a.o_hs + d0) = ov;
+    }
+  }
+}
+
 // Merge of the key-split partials: one thread per (b*h, q, 4 channels), splits in order.
 // Up to MAXS splits are loaded before the first use (one memory round trip); more splits
 // (MAXS = 0) take the looped form.
@@ -824,6 +1042,15 @@ static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
         (a.qss == nullptr) == (a.kss == nullptr)) {
       if (a.qss) FAM_LAUNCH((attn_self_kernel<DH, true>), dim3((unsigned)bh), dim3(256), 0, s, a);
       else FAM_LAUNCH((attn_self_kernel<DH, false>), dim3((unsigned)bh), dim3(256), 0, s, a);
+      return;
+    }
+  }
+  if constexpr (DH == 64 || DH == 128) {
+    // up to 32 queries over one long unmasked key segment (the context)
+    if (a.Sq <= 32 && a.sk0 == a.Sk && a.mask_kind == FAM_MASK_NONE && a.kss == nullptr) {
+      const dim3 grid((unsigned)bh, (unsigned)a.splits);
+      if (a.qss) FAM_LAUNCH((attn_cross_kernel<DH, true>), grid, dim3(256), 0, s, a);
+      else FAM_LAUNCH((attn_cross_kernel<DH, false>), grid, dim3(256), 0, s, a);
       return;
     }
   }
