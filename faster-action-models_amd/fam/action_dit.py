@@ -176,10 +176,16 @@ class FusedActionDiT:
         seq_len: action tokens per chunk (S).
         ctx_len: context tokens (L).
         num_steps / shift: the flow-matching schedule (SCH:63-80).
+        video_len: Sv > 0 selects the MoT action step (FB/mot.py:378-478): the action tokens'
+            self-attention runs over [cached video K/V of the layer ; action K/V]; the caches
+            are given per call through `set_video_kv`.
+        video_mask: optional bool [S, Sv + S], the action rows of the joint mask
+            (FB/fastwam.py:388-410; True = attend); None = every key.
     """
 
     def __init__(self, cfg: ActionDiTConfig, params: Dict[str, torch.Tensor], *, batch: int, seq_len: int,
-                 ctx_len: int, num_steps: int, shift: float = 5.0, device="cuda", mode: str = "denoise"):
+                 ctx_len: int, num_steps: int, shift: float = 5.0, device="cuda", mode: str = "denoise",
+                 video_len: int = 0, video_mask: Optional[torch.Tensor] = None):
         if mode not in ("denoise", "forward"):
             raise ValueError(f"mode must be 'denoise' or 'forward', got {mode!r}")
         if mode == "forward" and num_steps != 1:
@@ -259,6 +265,17 @@ class FusedActionDiT:
         self.ctx_emb = z(ctx_len, H)
         self.ctxkv = z(ctx_len, L * 2 * A)
         self.h = z(M, H)   # normalised input of the next projection
+        # MoT: per-layer cached video K/V [L, B, Sv, A] and the action rows of the joint mask
+        self.Sv = int(video_len)
+        if self.Sv > 0:
+            self.video_k = z(L, batch, self.Sv, A)
+            self.video_v = z(L, batch, self.Sv, A)
+            self.video_mask = None
+            if video_mask is not None:
+                vm = video_mask.to(device=dev, dtype=torch.bool).contiguous()
+                if tuple(vm.shape) != (seq_len, self.Sv + seq_len):
+                    raise ValueError(f"video_mask must be [S, Sv + S] = [{seq_len}, {self.Sv + seq_len}]")
+                self.video_mask = vm
         # per-row, per-16-column sums of squares of the raw q/k projections (fam_gemm_final)
         self.ss_qkv = torch.zeros(M, 3 * A // 16, dtype=torch.float32, device=dev)
         self.ss_q = torch.zeros(M, A // 16, dtype=torch.float32, device=dev)
@@ -435,6 +452,41 @@ class FusedActionDiT:
             self._launch(name + "_combine", "fam_attention_combine", C.byref(d), "attn_combine",
                          splits * nq * (4 * Dh + 8) + 2 * nq * Dh)
 
+    def _attn_joint(self, name, l, out):
+        """MoT self-attention of the action rows over [video K/V cache of layer l ; action K/V]
+        with the action rows of the joint mask (FB/mot.py:446-478): two key segments read in
+        place, no concat."""
+        cfg = self.cfg
+        A, Dh, S, Sv = cfg.attn_dim, cfg.attn_head_dim, self.S, self.Sv
+        qkvp = self.qkv.data_ptr()
+        d = _capi.AttnDesc()
+        d.q, d.q_bs, d.q_rs, d.q_hs = qkvp, S * 3 * A, 3 * A, Dh
+        vk, vv = self.video_k[l], self.video_v[l]
+        d.k0, d.k0_bs, d.k0_rs, d.k0_hs = vk.data_ptr(), Sv * A, A, Dh
+        d.v0, d.v0_bs, d.v0_rs, d.v0_hs = vv.data_ptr(), Sv * A, A, Dh
+        d.k1, d.k1_bs, d.k1_rs, d.k1_hs = qkvp + 2 * A, S * 3 * A, 3 * A, Dh
+        d.v1, d.v1_bs, d.v1_rs, d.v1_hs = qkvp + 4 * A, S * 3 * A, 3 * A, Dh
+        d.o, d.o_bs, d.o_rs, d.o_hs = out.data_ptr(), S * A, A, Dh
+        d.batch, d.heads, d.sq, d.sk0, d.sk1, d.head_dim = self.B, cfg.num_heads, S, Sv, S, Dh
+        d.scale = 1.0 / math.sqrt(Dh)
+        if self.video_mask is not None:
+            d.mask, d.mask_kind = self.video_mask.data_ptr(), _capi.FAM_MASK_BOOL
+            d.mask_bs, d.mask_hs, d.mask_qs = 0, 0, Sv + S
+        d.num_splits = 1
+        self._descs.append(d)
+        nbytes = 2 * (2 * self.B * S * A + 2 * self.B * (Sv + S) * A)
+        self._launch(name, "fam_attention", C.byref(d), "attention", nbytes,
+                     4 * self.B * cfg.num_heads * S * (Sv + S) * Dh)
+
+    def set_video_kv(self, keys, values) -> None:
+        """Copy the per-layer cached video K/V (each [B, Sv, A] or [Sv, A], already normalised
+        and rotated as the video expert's prefill leaves them) into the static buffers."""
+        if self.Sv == 0:
+            raise ValueError("this model was built without a video prefix (video_len=0)")
+        for l, (k, v) in enumerate(zip(keys, values)):
+            self.video_k[l].copy_(k.reshape(self.video_k[l].shape) if k.dim() == 3 else k.expand_as(self.video_k[l]))
+            self.video_v[l].copy_(v.reshape(self.video_v[l].shape) if v.dim() == 3 else v.expand_as(self.video_v[l]))
+
     def _build_plan(self) -> _Plan:
         cfg, lib = self.cfg, self.lib
         H, A, L, Dh, Fd = cfg.hidden_dim, cfg.attn_dim, cfg.num_layers, cfg.attn_head_dim, cfg.ffn_dim
@@ -472,7 +524,7 @@ class FusedActionDiT:
 
         # M <= 64 rows, Sq <= 32 and an RMS width the on-load normaliser supports: q/k projections
         # are single kernels and their norms run inside the attention kernels
-        fused_qk = M <= 64 and S <= 32 and A % 1024 == 0 and Dh in (64, 128)
+        fused_qk = M <= 64 and S <= 32 and A % 1024 == 0 and Dh in (64, 128) and self.Sv == 0
 
         def mod(t, l, i):   # chunk i of (modulation + t_mod) of block l at step t: [H]
             return self.mods[t, l, i * H:(i + 1) * H]
@@ -496,8 +548,11 @@ class FusedActionDiT:
                     sp = self._gemm_partial(tag + ".qkv", h, w[f"qkv_w{l}"])
                     self._rowop(tag + ".qkv_row", N=3 * A, splits=sp, bias=w[f"qkv_b{l}"], out=qkv, norm=RMS,
                                 segs=((0, w[f"sa_norm_q_w{l}"]), (A, w[f"sa_norm_k_w{l}"])), rope=True, nout=qkv)
-                    self._attn(tag + ".self_attn", qkvp, S * 3 * A, 3 * A, qkvp + 2 * A, S * 3 * A, 3 * A,
-                               qkvp + 4 * A, S * 3 * A, 3 * A, attn, S, S)
+                    if self.Sv > 0:
+                        self._attn_joint(tag + ".joint_attn", l, attn)
+                    else:
+                        self._attn(tag + ".self_attn", qkvp, S * 3 * A, 3 * A, qkvp + 2 * A, S * 3 * A, 3 * A,
+                                   qkvp + 4 * A, S * 3 * A, 3 * A, attn, S, S)
                 # o projection; x += gate_msa * o; LayerNorm3 (affine) for the cross-attention query
                 sp = self._gemm_partial(tag + ".o", attn, w[f"sa_o_w{l}"])
                 self._rowop(tag + ".o_row", N=H, splits=sp, bias=w[f"sa_o_b{l}"], res=x, gate=mod(t, l, 2), out=x,

@@ -66,3 +66,18 @@ def test_fused_plan_builds_on_host():
     assert kinds2.count("gemm_final") == 2 * 3 and kinds2.count("gemm_partial") == 2 * (3 + 1)
     fwd = AD.FusedActionDiT(cfg, params, batch=1, seq_len=32, ctx_len=200, num_steps=1, device="cpu", mode="forward")
     assert fwd.plan.meta[-1]["kernel"] == "rowop"
+
+
+def test_fused_plan_mot_mode_on_host():
+    """MoT mode: the self-attention of every block becomes a two-segment joint attention over
+    the cached video K/V; the caches copy into static buffers."""
+    cfg = AD.ActionDiTConfig(num_layers=2, hidden_dim=64, ffn_dim=128, text_dim=48, freq_dim=32, num_heads=4,
+                             attn_head_dim=16)
+    params = AD.synthetic_params(cfg, 3)
+    m = AD.FusedActionDiT(cfg, params, batch=1, seq_len=32, ctx_len=129, num_steps=2, device="cpu", video_len=98)
+    names = m.plan.names
+    assert sum(n.endswith(".joint_attn") for n in names) == 2 * cfg.num_layers
+    assert not any(n.endswith(".self_attn") for n in names)
+    k = [torch.full((98, cfg.attn_dim), float(i + 1)) for i in range(cfg.num_layers)]
+    m.set_video_kv(k, k)
+    assert float(m.video_k[1].float().mean()) == 2.0

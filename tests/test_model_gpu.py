@@ -123,3 +123,43 @@ def test_tiny_golden_config_through_fused_model():
     ref = gold["loop.out.fp32"]
     print(f"tiny golden loop max|d| {(y - ref).abs().max().item():.3e}")
     assert (y - ref).abs().max().item() <= 3e-2
+
+
+@pytest.mark.parametrize("tokens_per_frame", [98, 49])
+def test_mot_loop_over_video_prefix(tokens_per_frame):
+    """MoT action step (FB/mot.py:378-478) in the fused loop: the action tokens' self-attention
+    runs over [cached video K/V ; action K/V] with the action rows of the joint mask; attention
+    width (12 x 64) differs from the hidden size (512); 3 Euler steps."""
+    Cfg, Model = _model_cls()
+    cfg = Cfg(hidden_dim=512, action_dim=7, ffn_dim=1024, text_dim=256, freq_dim=256, num_heads=12,
+              attn_head_dim=64, num_layers=2)
+    S, Sv, Lc, steps = 32, 98, 129, 3
+    A = cfg.num_heads * cfg.attn_head_dim
+    p = _params(cfg, 21)
+    g = torch.Generator().manual_seed(22)
+    noise = torch.randn(1, S, 7, generator=g).to(torch.bfloat16)
+    ctx = torch.randn(1, Lc, 256, generator=g).to(torch.bfloat16)
+    vks = [torch.randn(1, Sv, A, generator=g).to(torch.bfloat16) for _ in range(cfg.num_layers)]
+    vvs = [torch.randn(1, Sv, A, generator=g).to(torch.bfloat16) for _ in range(cfg.num_layers)]
+    joint = O.mot_joint_mask(Sv, S, tokens_per_frame)
+    amask = joint[Sv:, :]
+    m = Model(cfg, p, batch=1, seq_len=S, ctx_len=Lc, num_steps=steps, shift=5.0, video_len=Sv,
+              video_mask=None if bool(amask.all()) else amask)
+    m.set_video_kv([k.cuda() for k in vks], [v.cuda() for v in vvs])
+    y = m.infer(noise.cuda(), ctx.cuda()).float().cpu()
+
+    p32 = {k: v.float() for k, v in p.items()}
+    ocfg = O.ActionDiTConfig(**cfg.to_dict())
+    ts, ds = O.build_inference_schedule(steps, 5.0, torch.bfloat16)
+    ctx_emb = O.text_embedding(p32, ctx.float())
+    freqs = O.action_freqs(cfg.attn_head_dim, S)
+    vkv = [(k.float(), v.float()) for k, v in zip(vks, vvs)]
+    x_lat = noise.float()
+    for t, d in zip(ts.float(), ds.float()):
+        _, t_mod = O.time_mlp(p32, ocfg, t.reshape(1))
+        x = O.linear(x_lat, p32["action_encoder.weight"], p32["action_encoder.bias"])
+        x = O.mot_action_forward(p32, ocfg, x, freqs, t_mod, ctx_emb, vkv, joint, Sv)
+        x_lat = x_lat + O.linear(x, p32["head.weight"], p32["head.bias"]) * d
+    dd = (y - x_lat).abs()
+    print(f"MoT loop: max|d| {dd.max().item():.3e} mean|d| {dd.mean().item():.3e}")
+    assert dd.max().item() <= 1e-2
