@@ -56,6 +56,9 @@ def parse():
     ap.add_argument("--no-eager", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--cpu-sample-s", type=float, default=20.0, help="CPU baseline time budget")
+    ap.add_argument("--workload", choices=["c1", "c2"], default="c1",
+                    help="c1: the action-DiT denoise loop (the metric); c2: one long-sequence video DiT block "
+                         "(config 2 shape), reported as ms per 30-block forward with MFMA utilisation")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -305,6 +308,85 @@ def eager_gpu_baseline(cfg, params, noise, ctx, warmup=3, iters=10):
             "what": "reference eager op sequence restated in bench.py (bf16, torch ops, SDPA), same GPU"}
 
 
+# --------------------------------------------------------------------------- config 2: video DiT block
+def bench_c2(args):
+    """Config 2 (Wan2.2-5B-style video DiT, bf16): one block at the full shape (1560 tokens =
+    2 x 30 x 26 with 3-D RoPE, hidden 3072, 24 x 128 heads, FFN 14336, 512 text tokens, per-token
+    AdaLN), replayed from a captured graph; the forward is 30 such blocks."""
+    import torch
+    from fam.action_dit import ActionDiTConfig, synthetic_params
+    from fam.video_dit import FusedVideoDiTBlock, video_freqs_3d
+    f, hh, ww, H, nh, Dh, F, Lc, L = 2, 30, 26, 3072, 24, 128, 14336, 512, 30
+    S = f * hh * ww
+    cfg = ActionDiTConfig(hidden_dim=H, action_dim=7, ffn_dim=F, text_dim=H, freq_dim=256, num_heads=nh,
+                          attn_head_dim=Dh, num_layers=1)
+    params = {k: v for k, v in synthetic_params(cfg, 4321).items() if k.startswith("blocks.0.")}
+    freqs = video_freqs_3d(Dh, f, hh, ww)
+    dev = torch.device("cuda:0")
+    blk = FusedVideoDiTBlock(params, 0, hidden=H, num_heads=nh, head_dim=Dh, ffn_dim=F, batch=1, seq_len=S,
+                             ctx_len=Lc, freqs=freqs, per_token_mod=True, device=dev)
+    g = torch.Generator("cpu").manual_seed(1234)
+    blk.set_inputs(torch.randn(1, S, H, generator=g).to(dev, torch.bfloat16),
+                   (torch.randn(1, S, 6, H, generator=g) * 0.1).to(dev, torch.bfloat16),
+                   torch.randn(1, Lc, H, generator=g).to(dev, torch.bfloat16))
+    blk.run()
+    torch.cuda.synchronize()
+    blk.capture()
+    for _ in range(args.warmup):
+        blk.run()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        blk.run()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    p50 = statistics.median(times)
+    # per-launch durations (eager, HIP events recorded at each kernel's begin and end)
+    lib, st = blk.lib, torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in blk.steps]
+    for e0, e1 in ev:
+        e0.record(st)
+        e1.record(st)
+    torch.cuda.synchronize()
+    for i, fn in enumerate(blk.steps):
+        lib.fam_set_launch_events(ev[i][0].cuda_event, ev[i][1].cuda_event)
+        try:
+            fn(st.cuda_stream)
+        finally:
+            lib.fam_set_launch_events(None, None)
+    torch.cuda.synchronize()
+    kernels = {}
+    for (e0, e1), m in zip(ev, blk.meta):
+        us = e0.elapsed_time(e1) * 1e3
+        kernels[m["name"]] = {"us": round(us, 2), "TFLOPs": round(m["flops"] / (us * 1e-6) / 1e12, 1) if m["flops"] else None}
+    flops = sum(m["flops"] for m in blk.meta)
+    att = [k for k in kernels if k.endswith("attn")]
+    att_us = sum(kernels[k]["us"] for k in att)
+    att_fl = sum(m["flops"] for m in blk.meta if m["name"] in att)
+    gem = [m["name"] for m in blk.meta if m["kernel"] == "gemm"]
+    gem_us = sum(kernels[k]["us"] for k in gem)
+    gem_fl = sum(m["flops"] for m in blk.meta if m["kernel"] == "gemm")
+    att_tf = att_fl / (att_us * 1e-6) / 1e12
+    out = {
+        "metric": "ms per video-DiT forward (30 blocks, config 2)", "value": round(p50 * L, 3), "unit": "ms",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(p50, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) tokens, text and per-token t_mod x0.1, N(0,0.02) weights",
+        "config": {"workload": "config2 video DiT block x30: 1560 tokens (2x30x26, 3-D RoPE), hidden 3072, "
+                               "24x128 heads, FFN 14336, 512 text tokens, per-token AdaLN",
+                   "blocks": L, "tokens": S, "text_tokens": Lc},
+        "block_ms": round(p50, 4), "block_gflop": round(flops / 1e9, 1),
+        "block_TFLOPs": round(flops / (p50 * 1e-3) / 1e12, 1),
+        "roofline": {"kernel": "attention", "bound": "mfma", "achieved": round(att_tf, 1),
+                     "peak": BF16_DENSE_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(att_tf / BF16_DENSE_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "gemm_TFLOPs": round(gem_fl / (gem_us * 1e-6) / 1e12, 1),
+        "kernels": kernels,
+    }
+    print(json.dumps(out), flush=True)
+
+
 # --------------------------------------------------------------------------- main
 def main():
     args = parse()
@@ -319,6 +401,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.copy_probe:
         copy_probe()
+        return
+    if args.workload == "c2":
+        bench_c2(args)
         return
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

@@ -1,0 +1,238 @@
+"""DiT block of the video backbone at long sequence length on the gfx950 kernels.
+
+One `DiTBlock.forward` (FB/wan_video_dit.py:267-286) for the video tokens of the backbone
+(Wan2.2-5B-style config: 1560 tokens = 2 latent frames x 30 x 26 patches with 3-D RoPE,
+hidden 3072, 24 x 128 heads, FFN 14336, 512 text tokens, per-token AdaLN modulation,
+FB/wan_video_dit.py:555-568), built from the library's kernels:
+
+    mods   = modulation + t_mod                           fam_add_modulation
+    h      = AdaLN1(x)   (per-token shift/scale)          fam_adaln
+    qkv    = h Wqkv^T + b                                 fam_gemm (tiled, MFMA)
+    q, k   = RoPE3D(RMSNorm(q)), RoPE3D(RMSNorm(k))       fam_rmsnorm_rope (in place)
+    a      = softmax(q k^T / sqrt(Dh)) v                  fam_attention (64-query tiles)
+    x      = x + g_msa * (a Wo^T + bo)                    fam_gemm epilogue (per-token gate)
+    h      = LayerNorm3(x)                                fam_adaln (affine)
+    qc     = RMSNorm(h Wq^T + bq)                         fam_gemm + fam_rmsnorm_rope
+    kc, vc = RMSNorm(ctx Wk^T + bk), ctx Wv^T + bv        fam_gemm (fused k|v) + fam_rmsnorm_rope
+    x      = x + (attn(qc, kc, vc) Wo^T + bo)             fam_attention + fam_gemm epilogue
+    h      = AdaLN2(x)                                    fam_adaln
+    x      = x + g_mlp * (GELU(h W1^T + b1) W2^T + b2)    fam_gemm (GELU epilogue), fam_gemm (gate)
+
+Every launch is prebuilt once per shape; `run()` enqueues them on the current stream and
+`capture()` records them in one HIP graph.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from typing import Dict, List, Optional
+
+import torch
+
+from . import _capi
+from .ops import rope_tables
+
+_BF16 = torch.bfloat16
+
+
+def video_freqs_3d(head_dim: int, f: int, h: int, w: int):
+    """3-D RoPE table of an (f, h, w) grid, complex [f*h*w, 1, head_dim/2]: the head dim splits
+    into f/h/w parts of head_dim - 4*(head_dim//6), 2*(head_dim//6), 2*(head_dim//6) dims
+    (FB/wan_video_dit.py:41-46, 620-624), angles pos * 10000^(-2j/d) in fp64."""
+    import torch
+    d3 = head_dim // 6
+    dims = (head_dim - 4 * d3, 2 * d3, 2 * d3)
+
+    def table(d, n):
+        j = torch.arange(0, d, 2, dtype=torch.float64)[: d // 2]
+        ang = torch.outer(torch.arange(n, dtype=torch.float64), 1.0 / (10000.0 ** (j / d)))
+        return torch.polar(torch.ones_like(ang), ang)
+
+    tf, th, tw = table(dims[0], f), table(dims[1], h), table(dims[2], w)
+    grid = torch.cat([tf[:, None, None, :].expand(f, h, w, -1), th[None, :, None, :].expand(f, h, w, -1),
+                      tw[None, None, :, :].expand(f, h, w, -1)], dim=-1)
+    return grid.reshape(f * h * w, 1, -1)
+
+
+class FusedVideoDiTBlock:
+    """One DiT block (the reference's `blocks.{idx}.` parameters) for fixed (B, S, Lc)."""
+
+    def __init__(self, params: Dict[str, torch.Tensor], idx: int, *, hidden: int, num_heads: int, head_dim: int,
+                 ffn_dim: int, batch: int, seq_len: int, ctx_len: int, freqs: torch.Tensor, eps: float = 1e-6,
+                 per_token_mod: bool = True, device="cuda"):
+        dev = torch.device(device)
+        self.lib = _capi.load()
+        self.B, self.S, self.Lc = batch, seq_len, ctx_len
+        self.H, self.nh, self.Dh, self.F = hidden, num_heads, head_dim, ffn_dim
+        self.A = A = num_heads * head_dim
+        self.eps = float(eps)
+        self.per_token = per_token_mod
+        H, F = hidden, ffn_dim
+        M = batch * seq_len
+        pre = f"blocks.{idx}."
+
+        def P(n):
+            return params[pre + n].to(device=dev, dtype=_BF16).contiguous()
+
+        def cat(ns):
+            return torch.cat([params[pre + n].float() for n in ns], 0).to(device=dev, dtype=_BF16).contiguous()
+
+        self.w = w = {
+            "qkv_w": cat([f"self_attn.{n}.weight" for n in "qkv"]), "qkv_b": cat([f"self_attn.{n}.bias" for n in "qkv"]),
+            "o_w": P("self_attn.o.weight"), "o_b": P("self_attn.o.bias"),
+            "nq": P("self_attn.norm_q.weight"), "nk": P("self_attn.norm_k.weight"),
+            "cq_w": P("cross_attn.q.weight"), "cq_b": P("cross_attn.q.bias"),
+            "ckv_w": cat(["cross_attn.k.weight", "cross_attn.v.weight"]),
+            "ckv_b": cat(["cross_attn.k.bias", "cross_attn.v.bias"]),
+            "co_w": P("cross_attn.o.weight"), "co_b": P("cross_attn.o.bias"),
+            "cnq": P("cross_attn.norm_q.weight"), "cnk": P("cross_attn.norm_k.weight"),
+            "n3_w": P("norm3.weight"), "n3_b": P("norm3.bias"),
+            "f0_w": P("ffn.0.weight"), "f0_b": P("ffn.0.bias"), "f2_w": P("ffn.2.weight"), "f2_b": P("ffn.2.bias"),
+            "mod": P("modulation").reshape(6 * H).contiguous(),
+        }
+        cos, sin, trs, tes = rope_tables(freqs, "complex", dev)
+        self.rope = (cos, sin, trs, tes)
+
+        z = lambda *s: torch.zeros(*s, dtype=_BF16, device=dev)  # noqa: E731
+        self.x = z(M, H)
+        self.tmod_in = z(M if per_token_mod else batch, 6 * H)
+        self.ctx = z(batch * ctx_len, H)
+        self.mods = z(M if per_token_mod else batch, 6 * H)
+        self.h = z(M, H)
+        self.qkv = z(M, 3 * A)
+        self.attn = z(M, A)
+        self.qc = z(M, A)
+        self.ckv = z(batch * ctx_len, 2 * A)
+        self.hid = z(M, F)
+        self._descs: List = []
+        self.steps: List = []
+        self.meta: List[dict] = []
+        self._build()
+        self.graph: Optional[torch.cuda.CUDAGraph] = None
+
+    # ------------------------------------------------------------------ launches
+    def _add(self, name, fname, args, kind, flops=0):
+        f, lib = getattr(self.lib, fname), self.lib
+
+        def run(stream):
+            rc = f(*args, stream)
+            if rc != 0:
+                raise _capi.FamError(f"{fname}[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
+        self.steps.append(run)
+        self.meta.append({"name": name, "kernel": kind, "flops": int(flops)})
+
+    def _gemm(self, name, a, w, bias, out, act=_capi.FAM_ACT_NONE, res=None, gate=None, gate_strides=(0, 0, 1)):
+        d = _capi.GemmDesc()
+        M, K = a.shape
+        N = w.shape[0]
+        d.a, d.lda, d.w, d.ldw = a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0)
+        d.bias = bias.data_ptr() if bias is not None else None
+        d.out, d.ldo = out.data_ptr(), out.stride(0)
+        d.M, d.N, d.K = M, N, K
+        d.act = act
+        if res is not None:
+            d.res, d.ldr = res.data_ptr(), res.stride(0)
+        if gate is not None:
+            d.gate = gate.data_ptr()
+            d.gate_bs, d.gate_rs, d.gate_ns = gate_strides
+        d.rows_per_batch = self.S if M == self.B * self.S else M
+        self._descs.append(d)
+        self._add(name, "fam_gemm", (C.byref(d),), "gemm", 2 * M * N * K)
+
+    def _adaln(self, name, x, y, shift=None, scale=None, lw=None, lb=None):
+        M, H = x.shape
+        mbs, mrs = (self.S * 6 * H, 6 * H) if self.per_token else (6 * H, 0)
+        args = (x.data_ptr(), x.stride(0), shift.data_ptr() if shift is not None else None,
+                scale.data_ptr() if scale is not None else None, mbs, mrs,
+                lw.data_ptr() if lw is not None else None, lb.data_ptr() if lb is not None else None,
+                y.data_ptr(), y.stride(0), M, self.S, H, self.eps)
+        self._add(name, "fam_adaln", args, "adaln")
+
+    def _rms(self, name, x_ptr, ld, rows, seq, weight, rope):
+        A, Dh = self.A, self.Dh
+        cs, sn, trs, tes = self.rope if rope else (None, None, 0, 0)
+        args = (x_ptr, ld, x_ptr, ld, rows, seq, A, weight.data_ptr(), self.eps,
+                cs.data_ptr() if cs is not None else None, sn.data_ptr() if sn is not None else None, trs, tes, Dh)
+        self._add(name, "fam_rmsnorm_rope", args, "rmsnorm_rope")
+
+    def _attention(self, name, q, q_rs, k, k_rs, v, v_rs, sq, sk, kv_batch_rows):
+        d = _capi.AttnDesc()
+        A, Dh = self.A, self.Dh
+        d.q, d.q_bs, d.q_rs, d.q_hs = q, sq * q_rs, q_rs, Dh
+        d.k0, d.k0_bs, d.k0_rs, d.k0_hs = k, kv_batch_rows * k_rs, k_rs, Dh
+        d.v0, d.v0_bs, d.v0_rs, d.v0_hs = v, kv_batch_rows * v_rs, v_rs, Dh
+        d.o, d.o_bs, d.o_rs, d.o_hs = self.attn.data_ptr(), sq * A, A, Dh
+        d.batch, d.heads, d.sq, d.sk0, d.sk1, d.head_dim = self.B, self.nh, sq, sk, 0, Dh
+        d.scale = 1.0 / math.sqrt(Dh)
+        d.num_splits = 1
+        self._descs.append(d)
+        self._add(name, "fam_attention", (C.byref(d),), "attention", 4 * self.B * self.nh * sq * sk * Dh)
+
+    def _build(self):
+        w, H, A, S, Lc = self.w, self.H, self.A, self.S, self.Lc
+        M = self.B * S
+        rows = self.mods.shape[0]
+        self._add("modulation", "fam_add_modulation",
+                  (self.tmod_in.data_ptr(), w["mod"].data_ptr(), self.mods.data_ptr(), rows, 1, 6 * H), "modulation")
+
+        def mod(i):  # chunk i of (modulation + t_mod), [rows, H] view with row stride 6H
+            return self.mods[:, i * H:(i + 1) * H]
+
+        gstr = (S * 6 * H, 6 * H, 1) if self.per_token else (6 * H, 0, 1)
+        # self-attention
+        self._adaln("adaln1", self.x, self.h, shift=mod(0), scale=mod(1))
+        self._gemm("qkv", self.h, w["qkv_w"], w["qkv_b"], self.qkv)
+        qp = self.qkv.data_ptr()
+        self._rms("q_norm_rope", qp, 3 * A, M, S, w["nq"], True)
+        self._rms("k_norm_rope", qp + 2 * A, 3 * A, M, S, w["nk"], True)
+        self._attention("self_attn", qp, 3 * A, qp + 2 * A, 3 * A, qp + 4 * A, 3 * A, S, S, S)
+        self._gemm("o", self.attn, w["o_w"], w["o_b"], self.x, res=self.x, gate=mod(2), gate_strides=gstr)
+        # cross-attention
+        self._adaln("norm3", self.x, self.h, lw=w["n3_w"], lb=w["n3_b"])
+        self._gemm("cross_q", self.h, w["cq_w"], w["cq_b"], self.qc)
+        self._rms("cross_q_norm", self.qc.data_ptr(), A, M, S, w["cnq"], False)
+        self._gemm("cross_kv", self.ctx, w["ckv_w"], w["ckv_b"], self.ckv)
+        kp = self.ckv.data_ptr()
+        self._rms("cross_k_norm", kp, 2 * A, self.B * Lc, Lc, w["cnk"], False)
+        self._attention("cross_attn", self.qc.data_ptr(), A, kp, 2 * A, kp + 2 * A, 2 * A, S, Lc, Lc)
+        self._gemm("cross_o", self.attn, w["co_w"], w["co_b"], self.x, res=self.x)
+        # FFN
+        self._adaln("adaln2", self.x, self.h, shift=mod(3), scale=mod(4))
+        self._gemm("ffn_up", self.h, w["f0_w"], w["f0_b"], self.hid, act=_capi.FAM_ACT_GELU_TANH)
+        self._gemm("ffn_down", self.hid, w["f2_w"], w["f2_b"], self.x, res=self.x, gate=mod(5), gate_strides=gstr)
+
+    # ------------------------------------------------------------------ execution
+    def set_inputs(self, x: torch.Tensor, t_mod: torch.Tensor, context: torch.Tensor) -> None:
+        """x [B, S, H]; t_mod [B, S, 6, H] (per token) or [B, 6, H]; context [B, Lc, H] (bf16)."""
+        self.x.copy_(x.reshape(self.x.shape))
+        self.tmod_in.copy_(t_mod.reshape(self.tmod_in.shape))
+        self.ctx.copy_(context.reshape(self.ctx.shape))
+
+    def run(self) -> None:
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            s = torch.cuda.current_stream().cuda_stream
+            for f in self.steps:
+                f(s)
+
+    def capture(self) -> None:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for f in self.steps:
+                f(s.cuda_stream)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            st = torch.cuda.current_stream().cuda_stream
+            for f in self.steps:
+                f(st)
+        self.graph = g
+
+    def forward(self, x: torch.Tensor, t_mod: torch.Tensor, context: torch.Tensor) -> torch.Tensor:
+        """One block forward; returns a copy of the new x, [B, S, H]."""
+        self.set_inputs(x, t_mod, context)
+        self.run()
+        return self.x.clone().view(self.B, self.S, self.H)

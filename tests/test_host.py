@@ -81,3 +81,9 @@ def test_fused_plan_mot_mode_on_host():
     k = [torch.full((98, cfg.attn_dim), float(i + 1)) for i in range(cfg.num_layers)]
     m.set_video_kv(k, k)
     assert float(m.video_k[1].float().mean()) == 2.0
+
+
+def test_video_rope_table_matches_oracle():
+    from fam.video_dit import video_freqs_3d
+    for dh, (f, h, w) in ((128, (2, 30, 26)), (64, (1, 4, 5))):
+        assert torch.equal(video_freqs_3d(dh, f, h, w), O.video_freqs(O.precompute_freqs_cis_3d(dh), f, h, w))
