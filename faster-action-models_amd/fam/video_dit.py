@@ -36,12 +36,12 @@ _BF16 = torch.bfloat16
 
 
 def video_freqs_3d(head_dim: int, f: int, h: int, w: int):
-    """3-D RoPE table of an (f, h, w) grid, complex [f*h*w, 1, head_dim/2]: the head dim splits
-    into f/h/w parts of head_dim - 4*(head_dim//6), 2*(head_dim//6), 2*(head_dim//6) dims
-    (FB/wan_video_dit.py:41-46, 620-624), angles pos * 10000^(-2j/d) in fp64."""
+    """3-D RoPE table of an (f, h, w) grid, complex [f*h*w, 1, .]: per-axis tables over
+    head_dim - 2*(head_dim//3), head_dim//3 and head_dim//3 dims (44/42/42 for head_dim 128),
+    angles pos * 10000^(-2j/d) in fp64 through torch.polar, concatenated per token in f-major
+    order (FB/wan_video_dit.py:41-55, 620-624)."""
     import torch
-    d3 = head_dim // 6
-    dims = (head_dim - 4 * d3, 2 * d3, 2 * d3)
+    dims = (head_dim - 2 * (head_dim // 3), head_dim // 3, head_dim // 3)
 
     def table(d, n):
         j = torch.arange(0, d, 2, dtype=torch.float64)[: d // 2]
