@@ -1,0 +1,229 @@
+// Action-VAE decoder of CAE-FastWAM (fp32): latent tokens -> action chunk.
+//
+//   x = input_proj(z) (+ suite embedding)                     [B, T0, C] -> channels-first [B, C, T0]
+//   per stage (stride s): ConvTranspose1d(C, C, 2s, s, s/2) -> GroupNorm(G) -> SiLU
+//                         -> x + GN(Conv1d(SiLU(GN(Conv1d(x)))))  (ResidualConv1dBlock, k = 3)
+//   crop / zero-pad the time axis to the horizon, output_proj per position -> [B, horizon, A]
+//
+// One workgroup per (batch row, GroupNorm group): the group's channels over all time steps
+// are exactly one GroupNorm reduction, so normalisation needs no cross-workgroup traffic;
+// the convolutions read every input channel of the previous stage from the global work
+// buffers, so each stage boundary is a kernel boundary.  Fixed-order reductions throughout.
+#include "fam_common.h"
+
+namespace fam {
+
+constexpr int CT = 256;  // threads per workgroup
+
+struct CaeArgs {
+  int64_t B, T0, L, C, G, T_in, T_out, stride, horizon, A;
+  const float* z; const float* suite; const float* in_w; const float* in_b;
+  const float* x;   // stage input [B, C, T_in] (stages after the first)
+  const float* w; const float* b; const float* gw; const float* gb;
+  const float* res; // residual [B, C, T] added after the GroupNorm (or null)
+  int silu;
+  float* y;         // [B, C, T_out]
+  float eps;
+  const float* ow; const float* ob; float* out;
+};
+
+// Sum of v over the workgroup (fixed order: wave sums, then waves in order).
+__device__ __forceinline__ float cae_block_sum(float v, float* red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// GroupNorm over this workgroup's CG channels x T values held as vals[j] (j-th element of
+// this thread, index e = tid + CT*j < n), affine, optional SiLU / residual, store.
+template <int NJ>
+__device__ __forceinline__ void cae_gn_store(const CaeArgs& a, float (&vals)[NJ], int n, int64_t c0, int64_t T,
+                                             float* red) {
+  const int tid = threadIdx.x;
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) s += (tid + CT * j < n) ? vals[j] : 0.f;
+  const float mean = cae_block_sum(s, red) / (float)n;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const float d = (tid + CT * j < n) ? vals[j] - mean : 0.f;
+    q += d * d;
+  }
+  const float rstd = rsqrtf(cae_block_sum(q, red) / (float)n + a.eps);
+  const int64_t bi = blockIdx.x;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int e = tid + CT * j;
+    if (e >= n) continue;
+    const int64_t c = c0 + e / T, t = e % T;
+    float v = (vals[j] - mean) * rstd * a.gw[c] + a.gb[c];
+    if (a.silu) v = v / (1.0f + expf(-v));
+    const int64_t o = (bi * a.C + c) * T + t;
+    if (a.res) v += a.res[o];
+    a.y[o] = v;
+  }
+}
+
+// Stage head: input projection (first stage) or the previous stage's output, then the
+// transposed convolution of this group's channels, GroupNorm, SiLU.
+template <int NJ>
+__global__ __launch_bounds__(CT) void cae_up_kernel(CaeArgs a) {
+  extern __shared__ float xs[];  // [C][T_in]
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int64_t bi = blockIdx.x, g = blockIdx.y;
+  const int64_t C = a.C, Ti = a.T_in, To = a.T_out, s = a.stride, K = 2 * s, P = s / 2;
+  for (int64_t e = tid; e < C * Ti; e += CT) {
+    const int64_t c = e / Ti, i = e % Ti;
+    float v;
+    if (a.z) {  // x[c][i] = in_b[c] + sum_l in_w[c][l] z[i][l] (+ suite[c])
+      v = a.in_b[c];
+      const float* zr = a.z + (bi * a.T0 + i) * a.L;
+      for (int64_t l = 0; l < a.L; ++l) v += a.in_w[c * a.L + l] * zr[l];
+      if (a.suite) v += a.suite[bi * C + c];
+    } else {
+      v = a.x[(bi * C + c) * Ti + i];
+    }
+    xs[e] = v;
+  }
+  __syncthreads();
+  const int64_t CG = C / a.G, c0 = g * CG;
+  const int n = (int)(CG * To);
+  float vals[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int e = tid + CT * j;
+    vals[j] = 0.f;
+    if (e >= n) continue;
+    const int64_t co = c0 + e / To, t = e % To;
+    float acc = a.b[co];
+    // taps: input step i contributes at t = i*s - P + kk, kk in [0, 2s)
+    const int64_t ihi = (t + P) / s, ilo = ihi - 1;
+    for (int64_t ci = 0; ci < C; ++ci) {
+      const float* wr = a.w + (ci * C + co) * K;
+      if (ihi < Ti) acc += xs[ci * Ti + ihi] * wr[t + P - ihi * s];
+      if (ilo >= 0 && ilo < Ti) acc += xs[ci * Ti + ilo] * wr[t + P - ilo * s];
+    }
+    vals[j] = acc;
+  }
+  cae_gn_store<NJ>(a, vals, n, c0, To, red);
+}
+
+// Conv1d (k = 3, padding 1) of this group's channels over every input channel, GroupNorm,
+// then SiLU or the residual add.
+template <int NJ>
+__global__ __launch_bounds__(CT) void cae_conv_kernel(CaeArgs a) {
+  extern __shared__ float xs[];  // [C][T]
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int64_t bi = blockIdx.x, g = blockIdx.y;
+  const int64_t C = a.C, T = a.T_out;
+  for (int64_t e = tid; e < C * T; e += CT) xs[e] = a.x[bi * C * T + e];
+  __syncthreads();
+  const int64_t CG = C / a.G, c0 = g * CG;
+  const int n = (int)(CG * T);
+  float vals[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int e = tid + CT * j;
+    vals[j] = 0.f;
+    if (e >= n) continue;
+    const int64_t co = c0 + e / T, t = e % T;
+    float acc = a.b[co];
+    for (int64_t ci = 0; ci < C; ++ci) {
+      const float* wr = a.w + (co * C + ci) * 3;
+      const float* xr = xs + ci * T;
+      if (t >= 1) acc += wr[0] * xr[t - 1];
+      acc += wr[1] * xr[t];
+      if (t + 1 < T) acc += wr[2] * xr[t + 1];
+    }
+    vals[j] = acc;
+  }
+  cae_gn_store<NJ>(a, vals, n, c0, T, red);
+}
+
+// output_proj over the horizon (time steps past the decoded length read zeros).
+__global__ __launch_bounds__(CT) void cae_out_kernel(CaeArgs a) {
+  const int64_t bi = blockIdx.x;
+  for (int64_t e = threadIdx.x; e < a.horizon * a.A; e += CT) {
+    const int64_t t = e / a.A, k = e % a.A;
+    float acc = a.ob[k];
+    if (t < a.T_in)
+      for (int64_t c = 0; c < a.C; ++c) acc += a.ow[k * a.C + c] * a.x[(bi * a.C + c) * a.T_in + t];
+    a.out[(bi * a.horizon + t) * a.A + k] = acc;
+  }
+}
+
+}  // namespace fam
+
+using namespace fam;
+
+static int launch_nj(int n, bool up, const CaeArgs& a, size_t lds, hipStream_t s) {
+  const dim3 grid((unsigned)a.B, (unsigned)a.G);
+  const int nj = (n + CT - 1) / CT;
+  if (nj > 16) return FAM_ERR_UNSUPPORTED;
+#define FAM_CAE(NJ)                                                                   \
+  if (nj <= NJ) {                                                                     \
+    if (up) FAM_LAUNCH((cae_up_kernel<NJ>), grid, dim3(CT), lds, s, a);               \
+    else FAM_LAUNCH((cae_conv_kernel<NJ>), grid, dim3(CT), lds, s, a);                \
+    return FAM_OK;                                                                    \
+  }
+  FAM_CAE(2) FAM_CAE(4) FAM_CAE(8) FAM_CAE(16)
+#undef FAM_CAE
+  return FAM_ERR_UNSUPPORTED;
+}
+
+extern "C" int fam_cae_decode(const fam_cae_desc* d, void* stream) {
+  FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_cae_decode: null descriptor");
+  FAM_REQUIRE(d->z && d->in_w && d->in_b && d->out_w && d->out_b && d->work && d->out, FAM_ERR_INVALID_ARG,
+              "fam_cae_decode: missing tensor pointer");
+  FAM_REQUIRE(d->batch >= 0 && d->tokens >= 1 && d->latent_dim >= 1 && d->hidden >= 1 && d->horizon >= 1 &&
+                  d->action_dim >= 1 && d->nstages >= 1 && d->nstages <= 3,
+              FAM_ERR_INVALID_ARG, "fam_cae_decode: bad sizes");
+  const int64_t C = d->hidden, G = C < 8 ? C : 8;
+  FAM_REQUIRE(C % G == 0 && C <= 512, FAM_ERR_UNSUPPORTED, "fam_cae_decode: hidden must be <= 512 and divisible by min(8, hidden)");
+  int64_t T = d->tokens;
+  for (int i = 0; i < d->nstages; ++i) {
+    FAM_REQUIRE(d->strides[i] >= 1 && d->up_w[i] && d->up_b[i] && d->gn_w[i] && d->gn_b[i] && d->r1_w[i] &&
+                    d->r1_b[i] && d->rg1_w[i] && d->rg1_b[i] && d->r2_w[i] && d->r2_b[i] && d->rg2_w[i] && d->rg2_b[i],
+                FAM_ERR_INVALID_ARG, "fam_cae_decode: stage %d incomplete", i);
+    // ConvTranspose1d(k = 2s, stride s, padding s/2): T -> (T-1)s - 2(s/2) + 2s
+    T = (T - 1) * d->strides[i] - 2 * (d->strides[i] / 2) + 2 * d->strides[i];
+  }
+  FAM_REQUIRE(T <= 1024 && (C / G) * T <= (int64_t)CT * 16 && C * T * 4 <= 64 * 1024, FAM_ERR_UNSUPPORTED,
+              "fam_cae_decode: decoded length %lld too long for one workgroup per group", (long long)T);
+  if (d->batch == 0) return FAM_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t Tmax = T;
+  float* wa = d->work;                       // stage head output
+  float* wb = d->work + d->batch * C * Tmax;  // residual branch
+  float* wr = d->work + 2 * d->batch * C * Tmax;  // stage output
+  CaeArgs a{};
+  a.B = d->batch; a.T0 = d->tokens; a.L = d->latent_dim; a.C = C; a.G = G; a.horizon = d->horizon; a.A = d->action_dim;
+  a.eps = d->gn_eps;
+  int64_t Tin = d->tokens;
+  for (int i = 0; i < d->nstages; ++i) {
+    const int64_t st = d->strides[i];
+    const int64_t Tout = (Tin - 1) * st - 2 * (st / 2) + 2 * st;
+    // head: (input projection |) transposed conv, GN, SiLU -> wa
+    a.z = i == 0 ? d->z : nullptr; a.suite = i == 0 ? d->suite : nullptr; a.in_w = d->in_w; a.in_b = d->in_b;
+    a.x = wr; a.T_in = Tin; a.T_out = Tout; a.stride = st;
+    a.w = d->up_w[i]; a.b = d->up_b[i]; a.gw = d->gn_w[i]; a.gb = d->gn_b[i]; a.res = nullptr; a.silu = 1; a.y = wa;
+    int rc = launch_nj((int)((C / G) * Tout), true, a, (size_t)(C * Tin * 4), s);
+    if (rc) { fam_host::set_error("fam_cae_decode: unsupported stage shape"); return rc; }
+    // residual block: conv, GN, SiLU -> wb; conv, GN, + wa -> wr
+    a.z = nullptr; a.x = wa; a.T_in = Tout; a.T_out = Tout;
+    a.w = d->r1_w[i]; a.b = d->r1_b[i]; a.gw = d->rg1_w[i]; a.gb = d->rg1_b[i]; a.res = nullptr; a.silu = 1; a.y = wb;
+    launch_nj((int)((C / G) * Tout), false, a, (size_t)(C * Tout * 4), s);
+    a.x = wb; a.w = d->r2_w[i]; a.b = d->r2_b[i]; a.gw = d->rg2_w[i]; a.gb = d->rg2_b[i]; a.res = wa; a.silu = 0; a.y = wr;
+    launch_nj((int)((C / G) * Tout), false, a, (size_t)(C * Tout * 4), s);
+    Tin = Tout;
+  }
+  a.x = wr; a.T_in = Tin; a.ow = d->out_w; a.ob = d->out_b; a.out = d->out;
+  FAM_LAUNCH(cae_out_kernel, dim3((unsigned)a.B), dim3(CT), 0, s, a);
+  return fam_host::check_launch("fam_cae_decode");
+}

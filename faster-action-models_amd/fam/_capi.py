@@ -98,6 +98,22 @@ class RowopDesc(C.Structure):
 
 
 # name -> (restype, argtypes); every symbol declared in include/fam_hip.h
+class CaeDesc(C.Structure):
+    """fam_cae_desc (include/fam_hip.h)."""
+    _fields_ = [
+        ("z", _vp), ("batch", _i64), ("tokens", _i64), ("latent_dim", _i64),
+        ("suite", _vp),
+        ("hidden", _i64), ("horizon", _i64), ("action_dim", _i64), ("nstages", _i64), ("strides", _i64 * 3),
+        ("in_w", _vp), ("in_b", _vp),
+        ("up_w", _vp * 3), ("up_b", _vp * 3), ("gn_w", _vp * 3), ("gn_b", _vp * 3),
+        ("r1_w", _vp * 3), ("r1_b", _vp * 3), ("rg1_w", _vp * 3), ("rg1_b", _vp * 3),
+        ("r2_w", _vp * 3), ("r2_b", _vp * 3), ("rg2_w", _vp * 3), ("rg2_b", _vp * 3),
+        ("out_w", _vp), ("out_b", _vp),
+        ("work", _vp), ("out", _vp),
+        ("gn_eps", C.c_float),
+    ]
+
+
 SIGNATURES = {
     "fam_version": (C.c_int, []),
     "fam_last_error": (C.c_char_p, []),
@@ -108,6 +124,7 @@ SIGNATURES = {
     "fam_attention": (C.c_int, [C.POINTER(AttnDesc), _vp]),
     "fam_attention_combine": (C.c_int, [C.POINTER(AttnDesc), _vp]),
     "fam_gemm_partial": (C.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
+    "fam_cae_decode": (C.c_int, [C.POINTER(CaeDesc), _vp]),
     "fam_gemm_final": (C.c_int, [_vp, _i64, _vp, _i64, _vp, C.c_int, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "fam_gemm_partial_splits": (C.c_int, [_i64, _i64, _i64]),
     "fam_rowop": (C.c_int, [C.POINTER(RowopDesc), _vp]),

@@ -329,6 +329,32 @@ int fam_sinusoid(const void* positions, void* out, int64_t T, int64_t dim, void*
 int fam_add_modulation(const void* t_mod, const void* modulation, void* out,
                        int64_t T, int64_t L, int64_t n, void* stream);
 
+/*
+ * fam_cae_decode -- the CAE-FastWAM action-VAE decoder, fp32 (CAm/action_ae.py:123-166, run in
+ * fp32 by CA/fastwam.py:855-863): z [B, tokens, latent_dim] -> out [B, horizon, action_dim].
+ *   x = in_w z + in_b (+ suite[b], the caller's suite embedding row, optional)
+ *   for each of nstages strides s: ConvTranspose1d(C, C, 2s, stride s, padding s/2) ->
+ *     GroupNorm(min(8, C)) -> SiLU -> x + GN(Conv1d_3(SiLU(GN(Conv1d_3(x)))))  (CAm/action_ae.py:32-48)
+ *   time axis cropped / zero-padded to horizon, then out_w x + out_b per position.
+ * Weights in PyTorch layouts: ConvTranspose1d [in, out, k], Conv1d [out, in, 3], Linear [out, in].
+ * work: 3 * B * C * T floats of scratch (T = decoded length).  Limits: C <= 512 and divisible by
+ * min(8, C); C * T * 4 bytes <= 64 KiB; (C / G) * T <= 4096; nstages <= 3.
+ */
+typedef struct fam_cae_desc {
+  const float* z; int64_t batch, tokens, latent_dim;
+  const float* suite;
+  int64_t hidden, horizon, action_dim, nstages; int64_t strides[3];
+  const float* in_w; const float* in_b;
+  const float* up_w[3]; const float* up_b[3]; const float* gn_w[3]; const float* gn_b[3];
+  const float* r1_w[3]; const float* r1_b[3]; const float* rg1_w[3]; const float* rg1_b[3];
+  const float* r2_w[3]; const float* r2_b[3]; const float* rg2_w[3]; const float* rg2_b[3];
+  const float* out_w; const float* out_b;
+  float* work; float* out;
+  float gn_eps;
+} fam_cae_desc;
+
+int fam_cae_decode(const fam_cae_desc* d, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,7 +39,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass, asdict
-from typing import Dict, Optional, Sequence, Tuple
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
 import torch.nn.functional as F
@@ -496,3 +496,99 @@ def mot_joint_mask(video_seq_len: int, action_seq_len: int, video_tokens_per_fra
     m[video_seq_len:, video_seq_len:] = True
     m[video_seq_len:, :ff] = True
     return m
+
+
+# ---------------------------------------------------------------------------
+# CAE-FastWAM action-VAE decoder (fp32)
+# ---------------------------------------------------------------------------
+@dataclass
+class CaeDecoderConfig:
+    """The decoder's shape (CAm/action_ae.py:15-29): latent tokens x latent_dim -> horizon x action_dim."""
+    latent_dim: int = 16
+    num_tokens: int = 8
+    action_horizon: int = 32
+    action_dim: int = 7
+    decoder_hidden: int = 128
+
+
+def cae_strides(ratio: int) -> List[int]:
+    """ActionEncoder._factorise_ratio (CAm/action_ae.py:90-101): factors 4, then 2, then 3, then
+    the remainder."""
+    if ratio == 1:
+        return [1]
+    out = []
+    for f in (4, 2, 3):
+        while ratio % f == 0:
+            out.append(f)
+            ratio //= f
+    if ratio > 1:
+        out.append(ratio)
+    return out
+
+
+def cae_decoder_param_shapes(cfg: CaeDecoderConfig) -> Dict[str, tuple]:
+    """State-dict keys of ActionAE.decoder (CAm/action_ae.py:123-150): nn.Sequential `up` holds
+    per stride [ConvTranspose1d, GroupNorm, SiLU, ResidualConv1dBlock(net: Conv1d, GN, SiLU,
+    Conv1d, GN)]."""
+    C = cfg.decoder_hidden
+    s = {"decoder.input_proj.weight": (C, cfg.latent_dim), "decoder.input_proj.bias": (C,),
+         "decoder.output_proj.weight": (cfg.action_dim, C), "decoder.output_proj.bias": (cfg.action_dim,)}
+    for j, st in enumerate(cae_strides(cfg.action_horizon // cfg.num_tokens)):
+        u = f"decoder.up.{4 * j}"
+        s[u + ".weight"], s[u + ".bias"] = (C, C, 2 * st), (C,)
+        s[f"decoder.up.{4 * j + 1}.weight"] = s[f"decoder.up.{4 * j + 1}.bias"] = (C,)
+        r = f"decoder.up.{4 * j + 3}.net."
+        for k in ("0", "3"):
+            s[r + k + ".weight"], s[r + k + ".bias"] = (C, C, 3), (C,)
+        for k in ("1", "4"):
+            s[r + k + ".weight"] = s[r + k + ".bias"] = (C,)
+    return s
+
+
+def init_cae_decoder_params(cfg: CaeDecoderConfig, seed: int) -> Params:
+    """Seeded synthetic decoder weights (fp32), drawn in sorted-name order: weights with two or
+    more dims N(0, 1/fan_in) with fan_in = prod(shape[1:]); GroupNorm weights 1 + N(0, 0.1) and
+    biases N(0, 0.1); other biases N(0, 0.02)."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    out: Params = {}
+    for name, shape in sorted(cae_decoder_param_shapes(cfg).items()):
+        parts = name.split(".")
+        is_gn = (len(parts) == 4 and parts[1] == "up" and int(parts[2]) % 4 == 1) or \
+            ".net.1." in name or ".net.4." in name
+        if len(shape) >= 2:
+            out[name] = torch.randn(shape, generator=g) / math.sqrt(math.prod(shape[1:]))
+        elif is_gn and name.endswith(".weight"):
+            out[name] = 1.0 + torch.randn(shape, generator=g) * 0.1
+        elif is_gn:
+            out[name] = torch.randn(shape, generator=g) * 0.1
+        else:
+            out[name] = torch.randn(shape, generator=g) * 0.02
+    return out
+
+
+def cae_decode(p: Params, cfg: CaeDecoderConfig, z: torch.Tensor, suite: Optional[torch.Tensor] = None,
+               gn_eps: float = 1e-5) -> torch.Tensor:
+    """ActionDecoder.forward (CAm/action_ae.py:152-166, ResidualConv1dBlock :32-48), fp32:
+    z [B, num_tokens, latent_dim] -> [B, action_horizon, action_dim]; suite: optional [B, C]
+    suite-embedding rows added after the input projection."""
+    x = F.linear(z, p["decoder.input_proj.weight"], p["decoder.input_proj.bias"])
+    if suite is not None:
+        x = x + suite.unsqueeze(1)
+    x = x.transpose(1, 2)
+    C = x.shape[1]
+    G = min(8, C)
+    for j, st in enumerate(cae_strides(cfg.action_horizon // cfg.num_tokens)):
+        u = f"decoder.up.{4 * j}"
+        x = F.conv_transpose1d(x, p[u + ".weight"], p[u + ".bias"], stride=st, padding=st // 2)
+        x = F.silu(F.group_norm(x, G, p[f"decoder.up.{4 * j + 1}.weight"], p[f"decoder.up.{4 * j + 1}.bias"], gn_eps))
+        r = f"decoder.up.{4 * j + 3}.net."
+        h = F.conv1d(x, p[r + "0.weight"], p[r + "0.bias"], padding=1)
+        h = F.silu(F.group_norm(h, G, p[r + "1.weight"], p[r + "1.bias"], gn_eps))
+        h = F.conv1d(h, p[r + "3.weight"], p[r + "3.bias"], padding=1)
+        x = x + F.group_norm(h, G, p[r + "4.weight"], p[r + "4.bias"], gn_eps)
+    T = x.shape[2]
+    if T > cfg.action_horizon:
+        x = x[:, :, :cfg.action_horizon]
+    elif T < cfg.action_horizon:
+        x = F.pad(x, (0, cfg.action_horizon - T))
+    return F.linear(x.transpose(1, 2), p["decoder.output_proj.weight"], p["decoder.output_proj.bias"])

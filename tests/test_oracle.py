@@ -255,3 +255,46 @@ def test_golden_detects_planted_mistake(golden, tiny_params):
     y = O.dit_block(p, 0, golden["block.in.x"], golden["block.in.context"], golden["block.in.t_mod"],
                     O.action_freqs(TINY.attn_head_dim, S), TINY.num_heads, TINY.eps, cm)
     assert not torch.allclose(y, golden["block.out.fp32"], rtol=2e-5, atol=2e-5)
+
+
+# --------------------------------------------------------------------------- CAE action decoder
+CAE_CASES = {"base": (16, 8, 32, 7, 128, 0, 41), "two_stage_suite": (8, 4, 32, 7, 64, 3, 42),
+             "stride3_pad": (6, 3, 10, 5, 32, 0, 43)}
+
+
+def _checksum(p) -> float:
+    acc = torch.zeros((), dtype=torch.float64)
+    for i, k in enumerate(sorted(p)):
+        acc = acc + (i + 1) * p[k].double().sum()
+    return float(acc)
+
+
+@pytest.fixture(scope="module")
+def cae_golden():
+    from safetensors.torch import load_file
+    return load_file(os.path.join(os.path.dirname(__file__), "golden", "cae_decoder.safetensors"))
+
+
+def _cae(name):
+    L, T0, hz, A, C, ns, seed = CAE_CASES[name]
+    cfg = O.CaeDecoderConfig(latent_dim=L, num_tokens=T0, action_horizon=hz, action_dim=A, decoder_hidden=C)
+    return cfg, O.init_cae_decoder_params(cfg, seed)
+
+
+@pytest.mark.parametrize("name", sorted(CAE_CASES))
+def test_cae_decoder_golden(cae_golden, name):
+    """The oracle's ActionDecoder restatement against the reference module's own outputs."""
+    cfg, p = _cae(name)
+    assert abs(cae_golden[f"{name}.checksum"].item() - _checksum(p)) < 1e-9
+    suite = cae_golden.get(f"{name}.suite_rows")
+    y = O.cae_decode(p, cfg, cae_golden[f"{name}.z"], suite)
+    torch.testing.assert_close(y, cae_golden[f"{name}.out"], rtol=1e-5, atol=1e-5)
+
+
+def test_cae_decoder_detects_planted_mistake(cae_golden):
+    cfg, p = _cae("base")
+    q = dict(p)
+    q["decoder.up.3.net.4.weight"] = -q["decoder.up.3.net.4.weight"]   # residual branch sign
+    y = O.cae_decode(q, cfg, cae_golden["base.z"])
+    assert (y - cae_golden["base.out"]).abs().max() > 1e-2
+    assert O.cae_strides(4) == [4] and O.cae_strides(8) == [4, 2] and O.cae_strides(12) == [4, 3]
