@@ -56,9 +56,10 @@ def parse():
     ap.add_argument("--no-eager", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--cpu-sample-s", type=float, default=20.0, help="CPU baseline time budget")
-    ap.add_argument("--workload", choices=["c1", "c2"], default="c1",
+    ap.add_argument("--workload", choices=["c1", "c2", "c3"], default="c1",
                     help="c1: the action-DiT denoise loop (the metric); c2: one long-sequence video DiT block "
-                         "(config 2 shape), reported as ms per 30-block forward with MFMA utilisation")
+                         "(config 2 shape), reported as ms per 30-block forward with MFMA utilisation; c3: the "
+                         "compact expert loop + action-VAE decoder at B=1 and B=256")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -387,6 +388,72 @@ def bench_c2(args):
     print(json.dumps(out), flush=True)
 
 
+# --------------------------------------------------------------------------- config 3: compact expert + decoder
+def bench_c3(args):
+    """Config 3: the compact action expert (hidden 32, 4 x 8 heads, 8 blocks) denoising an 8 x 16
+    latent over 4 Euler steps against a 1560 x 1024 context, then the action-VAE decoder to a
+    32 x 7 chunk, as one captured graph per policy call; B = 1 (launch-bound) and B = 256."""
+    import torch
+    from fam.action_dit import ActionDiTConfig, FusedActionDiT, synthetic_params
+    from fam.cae import CaeDecoder
+    cfg = ActionDiTConfig(hidden_dim=32, action_dim=16, ffn_dim=256, text_dim=1024, freq_dim=256, num_heads=4,
+                          attn_head_dim=8, num_layers=8)
+    params = synthetic_params(cfg, 4321)
+    g = torch.Generator("cpu").manual_seed(99)
+    dec_params = {}
+    for name, shape in sorted({"decoder.input_proj.weight": (128, 16), "decoder.input_proj.bias": (128,),
+                               "decoder.output_proj.weight": (7, 128), "decoder.output_proj.bias": (7,),
+                               "decoder.up.0.weight": (128, 128, 8), "decoder.up.0.bias": (128,),
+                               "decoder.up.1.weight": (128,), "decoder.up.1.bias": (128,),
+                               "decoder.up.3.net.0.weight": (128, 128, 3), "decoder.up.3.net.0.bias": (128,),
+                               "decoder.up.3.net.1.weight": (128,), "decoder.up.3.net.1.bias": (128,),
+                               "decoder.up.3.net.3.weight": (128, 128, 3), "decoder.up.3.net.3.bias": (128,),
+                               "decoder.up.3.net.4.weight": (128,), "decoder.up.3.net.4.bias": (128,)}.items()):
+        dec_params[name] = torch.randn(shape, generator=g) * (0.05 if len(shape) > 1 else 0.02)
+    dev = torch.device("cuda:0")
+    ctx = torch.randn(1, 1560, 1024, generator=g).to(dev, torch.bfloat16)
+    res = {}
+    for B in (1, 256):
+        m = FusedActionDiT(cfg, params, batch=B, seq_len=8, ctx_len=1560, num_steps=4, shift=5.0, device=dev)
+        dec = CaeDecoder(dec_params, latent_dim=16, num_tokens=8, action_horizon=32, action_dim=7, decoder_hidden=128,
+                         batch=B, device=dev)
+        dec.d.z = m.latents.data_ptr()  # the decoder reads the loop's fp32 latents in place
+        m.set_inputs(torch.randn(B, 8, 16, generator=g).to(dev, torch.bfloat16), ctx)
+        st = torch.cuda.Stream(dev)
+        st.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(st):
+            m.plan.run(st.cuda_stream)
+            dec.launch(st.cuda_stream)
+        torch.cuda.current_stream(dev).wait_stream(st)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            cs = torch.cuda.current_stream().cuda_stream
+            m.plan.run(cs)
+            dec.launch(cs)
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(args.steps):
+            t0 = time.perf_counter()
+            graph.replay()
+            torch.cuda.synchronize()
+            times.append((time.perf_counter() - t0) * 1e3)
+        p50 = statistics.median(times)
+        res[B] = {"p50_ms": round(p50, 4), "min_ms": round(min(times), 4), "chunks_per_s": round(B * 1e3 / p50, 1),
+                  "launches": m.num_launches + 4}
+        log(f"config 3 B={B}: p50 {p50:.3f} ms")
+    out = {"metric": "p50 ms per policy call (compact expert loop + action-VAE decode, config 3)",
+           "value": res[1]["p50_ms"], "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": res[1]["p50_ms"], "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+           "dtype": "bf16 (decoder fp32)", "data": "synthetic: seeded noise, context and weights",
+           "config": {"workload": "config3 compact expert: hidden 32, 4x8 heads, 8 blocks, 8x16 latent, 4 Euler "
+                                  "steps, ctx 1560x1024, conv action-VAE decoder to 32x7", "batch": [1, 256]},
+           "by_batch": res}
+    print(json.dumps(out), flush=True)
+
+
 # --------------------------------------------------------------------------- main
 def main():
     args = parse()
@@ -404,6 +471,9 @@ def main():
         return
     if args.workload == "c2":
         bench_c2(args)
+        return
+    if args.workload == "c3":
+        bench_c3(args)
         return
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

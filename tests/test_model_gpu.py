@@ -163,3 +163,31 @@ def test_mot_loop_over_video_prefix(tokens_per_frame):
     dd = (y - x_lat).abs()
     print(f"MoT loop: max|d| {dd.max().item():.3e} mean|d| {dd.mean().item():.3e}")
     assert dd.max().item() <= 1e-2
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+def test_compact_expert_loop_with_cae_decoder(batch):
+    """Config 3 (compact action expert): hidden 32, 4 x 8 heads, 8 blocks, an 8 x 16 latent,
+    4 Euler steps over a 1560 x 1024 context, then the action-VAE decoder to 32 x 7."""
+    from fam.cae import CaeDecoder
+    Cfg, Model = _model_cls()
+    cfg = Cfg(hidden_dim=32, action_dim=16, ffn_dim=256, text_dim=1024, freq_dim=256, num_heads=4, attn_head_dim=8,
+              num_layers=8)
+    p = _params(cfg, 51)
+    g = torch.Generator().manual_seed(52)
+    noise = torch.randn(batch, 8, 16, generator=g).to(torch.bfloat16)
+    ctx = torch.randn(1, 1560, 1024, generator=g).to(torch.bfloat16)
+    m = Model(cfg, p, batch=batch, seq_len=8, ctx_len=1560, num_steps=4, shift=5.0)
+    lat = m.infer(noise.cuda(), ctx.cuda())
+    dcfg = O.CaeDecoderConfig()
+    dp = O.init_cae_decoder_params(dcfg, 53)
+    dec = CaeDecoder(dp, latent_dim=16, num_tokens=8, action_horizon=32, action_dim=7, decoder_hidden=128, batch=batch)
+    y = dec.decode(lat).cpu()
+    p32 = {k: v.float() for k, v in p.items()}
+    ref_lat = _oracle_loop(p32, O.ActionDiTConfig(**cfg.to_dict()), noise.float(), ctx.float(), 4, 5.0)
+    dl = (lat.float().cpu() - ref_lat).abs().max().item()
+    ref = O.cae_decode(dp, dcfg, ref_lat)
+    d = (y - ref).abs()
+    print(f"compact expert B={batch}: latent max|d| {dl:.3e}, decoded max|d| {d.max().item():.3e}")
+    assert dl <= 1e-2
+    assert d.max().item() <= 2e-2 * max(1.0, ref.abs().max().item())
