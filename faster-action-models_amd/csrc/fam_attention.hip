@@ -859,6 +859,166 @@ __global__ __launch_bounds__(256) void attn_cross_kernel(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// attn_long_kernel: long query sequences (video tokens), no mask, one key segment.
+// A workgroup of 4 waves owns 128 queries of one (batch, head), 32 per wave; keys stream in
+// 64-key tiles through double-buffered LDS (K row-major, V transposed), one barrier per tile,
+// the next tile's global loads in flight during the current tile's math.  Per wave and tile:
+//   S^T [64 keys x 32 queries] = K Q^T      2 x DH/16 MFMA 32x32x16 (A = K rows from LDS,
+//                                           B = the wave's queries, held in registers)
+//   online softmax per query (a lane owns one query: 32 of its scores plus 32 in lane l^32)
+//   O^T [DH x 32 queries] += V^T P^T        2 x 2 x DH/32 MFMA (P stays in registers as the
+//                                           B operand; the key order inside a 16-key step is
+//                                           permuted identically on both operands)
+// Work-groups are mapped so that all query blocks of one head run on the same XCD (its
+// 4 MB L2 then holds that head's K/V once).
+template <int DH>
+__global__ __launch_bounds__(256) void attn_long_kernel(AttnArgs a, int nqb) {
+  constexpr int BN = 64;                 // keys per tile
+  constexpr int KS = DH / 16;            // 16-wide k-steps of S^T = K Q^T
+  constexpr int DT = DH / 32;            // 32-row dim tiles of O^T
+  constexpr int CPR = DH / 8;            // 16-byte chunks per K/V row
+  constexpr int NCH = BN * CPR / 256;    // chunks of K (and of V) per thread per tile
+  constexpr int KLD = DH + 8, VLD = BN + 8;
+  __shared__ bf16 Ks[2][BN][KLD];
+  __shared__ bf16 Vt[2][DH][VLD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hh = lane >> 5;
+  // XCD-aware task order: workgroup i runs on XCD i % 8; give each XCD a contiguous range of
+  // (head, query block) tasks so that a head's query blocks share that XCD's L2
+  const int nwg = gridDim.x;
+  int task = blockIdx.x;
+  if ((nwg & 7) == 0) task = (blockIdx.x & 7) * (nwg >> 3) + (blockIdx.x >> 3);
+  const int bh = task / nqb, qb = task - bh * nqb;
+  const uint32_t H32 = (uint32_t)a.H;
+  const uint32_t b = (uint32_t)bh / H32, h = (uint32_t)bh - b * H32;
+  const int Sq = (int)a.Sq, Sk = (int)a.Sk;
+  const bf16* qbase = a.q + b * a.q_bs + h * a.q_hs;
+  const bf16* kbase = a.k0 + b * a.k0_bs + h * a.k0_hs;
+  const bf16* vbase = a.v0 + b * a.v0_bs + h * a.v0_hs;
+
+  // the wave's 32 queries as B operands: lane -> query l32, dims 16s + 8hh .. +7
+  const int q = qb * 128 + wave * 32 + l32;
+  const int qc = q < Sq ? q : 0;
+  bf16x8 qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) qf[ks] = load8(qbase + (int64_t)qc * a.q_rs + ks * 16 + hh * 8);
+
+  bf16x8 kr[NCH], vr[NCH];
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = tid + 256 * j, key = c / CPR, d0 = (c % CPR) * 8;
+      const int kk = t * BN + key, kc = kk < Sk ? kk : 0;
+      kr[j] = load8(kbase + (int64_t)kc * a.k0_rs + d0);
+      vr[j] = load8(vbase + (int64_t)kc * a.v0_rs + d0);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = tid + 256 * j, key = c / CPR, d0 = (c % CPR) * 8;
+      *reinterpret_cast<bf16x8*>(&Ks[buf][key][d0]) = kr[j];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) Vt[buf][d0 + e][key] = vr[j][e];
+    }
+  };
+
+  const int ntiles = (Sk + BN - 1) / BN;
+  gload(0);
+  __builtin_amdgcn_sched_barrier(0);
+  lstore(0);
+  __syncthreads();
+
+  f32x16 acc[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) acc[d] = f32x16{};
+  float m_run = -INFINITY, l_run = 0.f;
+  const float sl2 = a.scale_log2;
+
+  for (int t = 0; t < ntiles; ++t) {
+    const int buf = t & 1;
+    if (t + 1 < ntiles) gload(t + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    // S^T for the tile's two 32-key halves
+    f32x16 st[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      st[kt] = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Ks[buf][kt * 32 + l32][ks * 16 + hh * 8]);
+        st[kt] = mfma32(kf, qf[ks], st[kt]);
+      }
+    }
+    // online softmax (log2 domain); register r of half kt holds key kt*32 + 8*(r/4) + 4*hh + r%4
+    float mloc = -INFINITY;
+    const bool tail = (t + 1) * BN > Sk;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float v = st[kt][r] * sl2;
+        if (tail) {
+          const int key = t * BN + kt * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
+          v = key < Sk ? v : -INFINITY;
+        }
+        st[kt][r] = v;
+        mloc = fmaxf(mloc, v);
+      }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
+    const float m_new = fmaxf(m_run, mloc);
+    const float alpha = exp2f(m_run - m_new);
+    float psum = 0.f;
+    bf16x8 pf[2][2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float pv = exp2f(st[kt][r] - m_new);
+        psum += pv;
+        pf[kt][r / 8][r % 8] = to_bf(pv);
+      }
+    psum += __shfl_xor(psum, 32, kWave);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) acc[d] *= alpha;
+    // O^T += V^T P^T: k-step c of half kt covers keys kt*32 + 16c + {4hh..4hh+3, 8+4hh..8+4hh+3}
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int k0 = kt * 32 + 16 * c + 4 * hh;
+#pragma unroll
+        for (int d = 0; d < DT; ++d) {
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&Vt[buf][d * 32 + l32][k0]);
+          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(&Vt[buf][d * 32 + l32][k0 + 8]);
+          bf16x8 vf;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { vf[e] = lo[e]; vf[4 + e] = hi[e]; }
+          acc[d] = mfma32(vf, pf[kt][c], acc[d]);
+        }
+      }
+    if (t + 1 < ntiles) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (q >= Sq) return;
+  const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+  bf16* op = a.o + b * a.o_bs + (int64_t)q * a.o_rs + h * a.o_hs;
+#pragma unroll
+  for (int d = 0; d < DT; ++d)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {   // registers 4g..4g+3: dims d*32 + 8g + 4hh .. +3
+      bf16x4 ov;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ov[e] = to_bf(acc[d][4 * g + e] * inv);
+      *reinterpret_cast<bf16x4*>(op + d * 32 + 8 * g + 4 * hh) = ov;
+    }
+}
+
 // Merge of the key-split partials: one thread per (b*h, q, 4 channels), splits in order.
 // Up to MAXS splits are loaded before the first use (one memory round trip); more splits
 // (MAXS = 0) take the looped form.
@@ -1062,6 +1222,13 @@ static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
     else if (a.Sq <= 32) launch_short_q<DH, 2>(a, nkb, grid, s);
     else launch_short_q<DH, 4>(a, nkb, grid, s);
   } else {
+    if constexpr (DH == 64 || DH == 128) {
+      if (a.sk0 == a.Sk && a.mask_kind == FAM_MASK_NONE && a.Sk >= 1) {
+        const int nqb = (int)((a.Sq + 127) / 128);
+        FAM_LAUNCH((attn_long_kernel<DH>), dim3((unsigned)(nqb * bh)), dim3(256), 0, s, a, nqb);
+        return;
+      }
+    }
     const dim3 grid((unsigned)(rup(a.Sq, 64) / 64), (unsigned)bh);
     FAM_LAUNCH((attn_tiled_kernel<DH>), grid, dim3(256), 0, s, a);
   }

@@ -85,6 +85,12 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// MFMA 32x32x16 bf16 -> fp32 (gfx950).  Lane l holds A[row=l%32][k=8*(l/32)..+7],
+// B[k=8*(l/32)..+7][col=l%32]; D register r of lane l is D[8*(r/4) + 4*(l/32) + r%4][l%32].
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
 }  // namespace fam
 
 // Host-side helpers shared by the C-ABI wrappers.

@@ -575,3 +575,13 @@ def test_attention_qk_norm_on_load_wide_heads():
     k = O.rope_apply(O.rms_norm(raw[..., A:2 * A].to(torch.bfloat16), wk, 1e-6).float(), fr, H)
     ref = O.flash_attention(q, k, raw[..., 2 * A:], H)
     assert relerr(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,Dh", [(1, 8, 1560, 1560, 128), (2, 4, 200, 333, 64), (1, 2, 129, 512, 128),
+                                           (1, 3, 65, 1, 128)])
+def test_attention_long_sequences(B, H, Sq, Sk, Dh):
+    """Video-token attention (Sq > 64, no mask): 128-query workgroups, 64-key LDS tiles, 32x32 MFMA."""
+    q, k, v = rnd(B, Sq, H * Dh, seed=135), rnd(B, Sk, H * Dh, seed=136), rnd(B, Sk, H * Dh, seed=137)
+    ref = O.flash_attention(q.float(), k.float(), v.float(), H)
+    y = ops().flash_attention(dev(q), dev(k), dev(v), H)
+    assert relerr(y, ref) <= TOL
