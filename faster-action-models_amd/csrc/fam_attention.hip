@@ -915,13 +915,18 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnArgs a, int nqb) {
       vr[j] = load8(vbase + (int64_t)kc * a.v0_rs + d0);
     }
   };
+  // V^T tile element (d, key) lives at Vt[d][key ^ vsw(d)]: the XOR (a multiple of 4, so runs
+  // of 4 keys stay contiguous) spreads the 16 lanes that write one key's 8-dim chunks, and the
+  // 32 lanes that read 32 consecutive dims, over the LDS banks
+  auto vsw = [](int d) { return ((d >> 3) & 7) << 2; };
   auto lstore = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = tid + 256 * j, key = c / CPR, d0 = (c % CPR) * 8;
       *reinterpret_cast<bf16x8*>(&Ks[buf][key][d0]) = kr[j];
+      const int ks = key ^ vsw(d0);   // d0 .. d0 + 7 share (d >> 3)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[buf][d0 + e][key] = vr[j][e];
+      for (int e = 0; e < 8; ++e) Vt[buf][d0 + e][ks] = vr[j][e];
     }
   };
 
@@ -952,39 +957,46 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnArgs a, int nqb) {
         st[kt] = mfma32(kf, qf[ks], st[kt]);
       }
     }
-    // online softmax (log2 domain); register r of half kt holds key kt*32 + 8*(r/4) + 4*hh + r%4
-    float mloc = -INFINITY;
-    const bool tail = (t + 1) * BN > Sk;
+    // online softmax (log2 domain); register r of half kt holds key kt*32 + 8*(r/4) + 4*hh + r%4.
+    // The running max only moves when a score exceeds it by more than 2^8 (or on the first
+    // tile), so the accumulator rescale is skipped on most tiles; p <= 2^8 in between is exact
+    // in fp32 and bf16 keeps its relative precision.
+    if ((t + 1) * BN > Sk) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = t * BN + kt * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
+          st[kt][r] = key < Sk ? st[kt][r] : -INFINITY;
+        }
+    }
+    float mraw = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float v = st[kt][r] * sl2;
-        if (tail) {
-          const int key = t * BN + kt * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
-          v = key < Sk ? v : -INFINITY;
-        }
-        st[kt][r] = v;
-        mloc = fmaxf(mloc, v);
-      }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
-    const float m_new = fmaxf(m_run, mloc);
-    const float alpha = exp2f(m_run - m_new);
+      for (int r = 0; r < 16; ++r) mraw = fmaxf(mraw, st[kt][r]);
+    mraw = fmaxf(mraw, __shfl_xor(mraw, 32, kWave));
+    const float mloc = mraw * sl2;   // sl2 > 0
+    if (__any(mloc > m_run + 8.0f)) {
+      const float m_new = fmaxf(m_run, mloc);
+      const float alpha = exp2f(m_run - m_new);   // lanes whose max did not move: 1
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DT; ++d) acc[d] *= alpha;
+      m_run = m_new;
+    }
     float psum = 0.f;
     bf16x8 pf[2][2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pv = exp2f(st[kt][r] - m_new);
+        const float pv = exp2f(__builtin_fmaf(st[kt][r], sl2, -m_run));
         psum += pv;
         pf[kt][r / 8][r % 8] = to_bf(pv);
       }
     psum += __shfl_xor(psum, 32, kWave);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int d = 0; d < DT; ++d) acc[d] *= alpha;
+    l_run += psum;
     // O^T += V^T P^T: k-step c of half kt covers keys kt*32 + 16c + {4hh..4hh+3, 8+4hh..8+4hh+3}
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
@@ -993,8 +1005,9 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnArgs a, int nqb) {
         const int k0 = kt * 32 + 16 * c + 4 * hh;
 #pragma unroll
         for (int d = 0; d < DT; ++d) {
-          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&Vt[buf][d * 32 + l32][k0]);
-          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(&Vt[buf][d * 32 + l32][k0 + 8]);
+          const int dr = d * 32 + l32, sw = vsw(dr);
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&Vt[buf][dr][k0 ^ sw]);
+          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(&Vt[buf][dr][(k0 + 8) ^ sw]);
           bf16x8 vf;
 #pragma unroll
           for (int e = 0; e < 4; ++e) { vf[e] = lo[e]; vf[4 + e] = hi[e]; }
