@@ -862,26 +862,31 @@ __global__ __launch_bounds__(256) void attn_cross_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------------------
 // attn_long_kernel: long query sequences (video tokens), no mask, one key segment.
 // A workgroup of 4 waves owns 128 queries of one (batch, head), 32 per wave; keys stream in
-// 64-key tiles through double-buffered LDS (K row-major, V transposed), one barrier per tile,
-// the next tile's global loads in flight during the current tile's math.  Per wave and tile:
+// 64-key tiles through double-buffered LDS (K and V row-major), one barrier per tile, the
+// next tile's buffer loads in flight during the current tile's math.  Per wave and tile:
 //   S^T [64 keys x 32 queries] = K Q^T      2 x DH/16 MFMA 32x32x16 (A = K rows from LDS,
 //                                           B = the wave's queries, held in registers)
 //   online softmax per query (a lane owns one query: 32 of its scores plus 32 in lane l^32)
-//   O^T [DH x 32 queries] += V^T P^T        2 x 2 x DH/32 MFMA (P stays in registers as the
-//                                           B operand; the key order inside a 16-key step is
-//                                           permuted identically on both operands)
-// Work-groups are mapped so that all query blocks of one head run on the same XCD (its
-// 4 MB L2 then holds that head's K/V once).
+//   O^T [DH x 32 queries] += V^T P^T        2 x 2 x DH/32 MFMA (A = V^T through transposing
+//                                           LDS reads, B = P kept in registers; the key order
+//                                           inside a 16-key step is permuted identically on
+//                                           both operands)
+// At most 256 registers per lane, so two workgroups share a CU and one's vector work fills
+// the other's matrix-core gaps.  Work-groups are mapped so that all query blocks of one head
+// run on the same XCD (its 4 MB L2 then holds that head's K/V once).
 template <int DH>
-__global__ __launch_bounds__(256) void attn_long_kernel(AttnArgs a, int nqb) {
+__global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) {
   constexpr int BN = 64;                 // keys per tile
   constexpr int KS = DH / 16;            // 16-wide k-steps of S^T = K Q^T
   constexpr int DT = DH / 32;            // 32-row dim tiles of O^T
   constexpr int CPR = DH / 8;            // 16-byte chunks per K/V row
   constexpr int NCH = BN * CPR / 256;    // chunks of K (and of V) per thread per tile
-  constexpr int KLD = DH + 8, VLD = BN + 8;
+  // K and V tiles row-major ([key][dim]).  Row pitches: K 272 bytes (16-byte reads of 32 rows
+  // hit distinct LDS banks); V a multiple of 64 bytes that is 64 mod 256 (DH 128) or 192 mod
+  // 256 (DH 64), so the transposing reads of 8 rows x 64 bytes fill the banks twice exactly
+  constexpr int KLD = DH + 8, VLD = DH == 128 ? 160 : 96;
   __shared__ bf16 Ks[2][BN][KLD];
-  __shared__ bf16 Vt[2][DH][VLD];
+  __shared__ bf16 Vs[2][BN][VLD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
@@ -905,62 +910,88 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnArgs a, int nqb) {
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) qf[ks] = load8(qbase + (int64_t)qc * a.q_rs + ks * 16 + hh * 8);
 
+  // K/V tiles come in through raw buffer loads: the descriptor (scalar registers) is rebuilt
+  // per tile over the rows from the tile's first key to Sk, so rows past the end (and whole
+  // tiles past the end) read as zero and each thread keeps only 32-bit row offsets
+  const uint32_t krs = (uint32_t)a.k0_rs * 2u, vrs = (uint32_t)a.v0_rs * 2u;   // bytes per row
+  // chunk j of a thread is key tid / CPR + j * (256 / CPR), dims (tid % CPR) * 8 .. + 7: one
+  // per-lane offset, the j steps go to the scalar offset
+  const uint32_t koff = (uint32_t)(tid / CPR) * krs + (uint32_t)(tid % CPR) * 16u;
+  const uint32_t voff = (uint32_t)(tid / CPR) * vrs + (uint32_t)(tid % CPR) * 16u;
   bf16x8 kr[NCH], vr[NCH];
-  auto gload = [&](int t) {
+  auto gload_k = [&](int t) {
+    const int k0 = t * BN, left = Sk - k0 > 0 ? Sk - k0 : 0;
+    const auto rsrc = buffer_rsrc(kbase + (int64_t)k0 * a.k0_rs, (uint32_t)left * krs);
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = tid + 256 * j, key = c / CPR, d0 = (c % CPR) * 8;
-      const int kk = t * BN + key, kc = kk < Sk ? kk : 0;
-      kr[j] = load8(kbase + (int64_t)kc * a.k0_rs + d0);
-      vr[j] = load8(vbase + (int64_t)kc * a.v0_rs + d0);
-    }
+    for (int j = 0; j < NCH; ++j) kr[j] = buffer_load8(rsrc, koff, (uint32_t)j * (256 / CPR) * krs);
   };
-  // V^T tile element (d, key) lives at Vt[d][key ^ vsw(d)]: the XOR (a multiple of 4, so runs
-  // of 4 keys stay contiguous) spreads the 16 lanes that write one key's 8-dim chunks, and the
-  // 32 lanes that read 32 consecutive dims, over the LDS banks
-  auto vsw = [](int d) { return ((d >> 3) & 7) << 2; };
-  auto lstore = [&](int buf) {
+  auto gload_v = [&](int t) {
+    const int k0 = t * BN, left = Sk - k0 > 0 ? Sk - k0 : 0;
+    const auto rsrc = buffer_rsrc(vbase + (int64_t)k0 * a.v0_rs, (uint32_t)left * vrs);
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) vr[j] = buffer_load8(rsrc, voff, (uint32_t)j * (256 / CPR) * vrs);
+  };
+  auto lstore_k = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int c = tid + 256 * j, key = c / CPR, d0 = (c % CPR) * 8;
       *reinterpret_cast<bf16x8*>(&Ks[buf][key][d0]) = kr[j];
-      const int ks = key ^ vsw(d0);   // d0 .. d0 + 7 share (d >> 3)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[buf][d0 + e][ks] = vr[j][e];
     }
   };
-
-  const int ntiles = (Sk + BN - 1) / BN;
-  gload(0);
-  __builtin_amdgcn_sched_barrier(0);
-  lstore(0);
-  __syncthreads();
-
+  auto lstore_v = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int c = tid + 256 * j, key = c / CPR, d0 = (c % CPR) * 8;
+      *reinterpret_cast<bf16x8*>(&Vs[buf][key][d0]) = vr[j];
+    }
+  };
+  // A operand of the PV product (V^T: row = dim, k = key) straight from the row-major tile
+  // with two transposing LDS reads (ds_read_b64_tr_b16).  Within each 16-lane group, lane i
+  // receives element i % 4 of the 8-byte loads of lanes i / 4 + 4e (e = 0..3); so lane s of a
+  // group loads key k0 + s / 4, dims dbase + 4 (s % 4) .. + 3, and lane i ends up with keys
+  // k0 .. k0 + 3 of dim dbase + i.  Lanes 0-15 / 16-31 take dims 0-15 / 16-31 of the 32-dim
+  // tile, lanes 32-63 the same dims for keys 4 further (their k-half of the MFMA).
+  auto vfrag = [&](int buf, int k0, int d) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const int s = lane & 15, key = k0 + 4 * hh + (s >> 2);
+    const int dim = d * 32 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
+    lds_s16x4* p0 = (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&Vs[buf][key][dim];
+    lds_s16x4* p1 = (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&Vs[buf][key + 8][dim];
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p0);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p1);
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8, v);
+  };
+  // S^T of a tile: register r of half kt holds key kt*32 + 8*(r/4) + 4*hh + r%4 of the lane's
+  // query; the two halves are independent MFMA chains, interleaved
+  auto kfrag = [&](int buf, int kt, int ks) {
+    return *reinterpret_cast<const bf16x8*>(&Ks[buf][kt * 32 + l32][ks * 16 + hh * 8]);
+  };
   f32x16 acc[DT];
 #pragma unroll
   for (int d = 0; d < DT; ++d) acc[d] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = a.scale_log2;
 
+  const int ntiles = (Sk + BN - 1) / BN;
+  gload_k(0);
+  gload_v(0);
+  __builtin_amdgcn_sched_barrier(0);
+  lstore_k(0);
+  lstore_v(0);
+  __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
-    if (t + 1 < ntiles) gload(t + 1);
+    gload_k(t + 1);   // zeros past Sk
+    gload_v(t + 1);
     __builtin_amdgcn_sched_barrier(0);
-    // S^T for the tile's two 32-key halves
-    f32x16 st[2];
+    f32x16 st[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      st[kt] = f32x16{};
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&Ks[buf][kt * 32 + l32][ks * 16 + hh * 8]);
-        st[kt] = mfma32(kf, qf[ks], st[kt]);
-      }
-    }
-    // online softmax (log2 domain); register r of half kt holds key kt*32 + 8*(r/4) + 4*hh + r%4.
-    // The running max only moves when a score exceeds it by more than 2^8 (or on the first
-    // tile), so the accumulator rescale is skipped on most tiles; p <= 2^8 in between is exact
-    // in fp32 and bf16 keeps its relative precision.
+      for (int kt = 0; kt < 2; ++kt) st[kt] = mfma32(kfrag(buf, kt, ks), qf[ks], st[kt]);
     if ((t + 1) * BN > Sk) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
@@ -970,6 +1001,9 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnArgs a, int nqb) {
           st[kt][r] = key < Sk ? st[kt][r] : -INFINITY;
         }
     }
+    // online softmax (log2 domain).  The running max only moves when a score exceeds it by
+    // more than 2^8 (or on the first tile), so the accumulator rescale is skipped on most
+    // tiles; p <= 2^8 in between is exact in fp32 and bf16 keeps its relative precision.
     float mraw = -INFINITY;
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
@@ -979,7 +1013,7 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnArgs a, int nqb) {
     const float mloc = mraw * sl2;   // sl2 > 0
     if (__any(mloc > m_run + 8.0f)) {
       const float m_new = fmaxf(m_run, mloc);
-      const float alpha = exp2f(m_run - m_new);   // lanes whose max did not move: 1
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);   // max unchanged: 1; -inf: 0
       l_run *= alpha;
 #pragma unroll
       for (int d = 0; d < DT; ++d) acc[d] *= alpha;
@@ -991,7 +1025,7 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnArgs a, int nqb) {
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pv = exp2f(__builtin_fmaf(st[kt][r], sl2, -m_run));
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kt][r], sl2, -m_run));
         psum += pv;
         pf[kt][r / 8][r % 8] = to_bf(pv);
       }
@@ -1001,20 +1035,11 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnArgs a, int nqb) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int k0 = kt * 32 + 16 * c + 4 * hh;
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int d = 0; d < DT; ++d) {
-          const int dr = d * 32 + l32, sw = vsw(dr);
-          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&Vt[buf][dr][k0 ^ sw]);
-          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(&Vt[buf][dr][(k0 + 8) ^ sw]);
-          bf16x8 vf;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) { vf[e] = lo[e]; vf[4 + e] = hi[e]; }
-          acc[d] = mfma32(vf, pf[kt][c], acc[d]);
-        }
-      }
-    if (t + 1 < ntiles) lstore(buf ^ 1);
+        for (int d = 0; d < DT; ++d) acc[d] = mfma32(vfrag(buf, kt * 32 + 16 * c, d), pf[kt][c], acc[d]);
+    lstore_k(buf ^ 1);
+    lstore_v(buf ^ 1);
     __syncthreads();
   }
 
@@ -1236,7 +1261,10 @@ static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
     else launch_short_q<DH, 4>(a, nkb, grid, s);
   } else {
     if constexpr (DH == 64 || DH == 128) {
-      if (a.sk0 == a.Sk && a.mask_kind == FAM_MASK_NONE && a.Sk >= 1) {
+      // (buffer loads address a head's K and V rows with 32-bit byte offsets)
+      const bool fits32 = a.Sk * a.k0_rs * 2 < ((int64_t)1 << 31) && a.Sk * a.v0_rs * 2 < ((int64_t)1 << 31);
+      if (a.sk0 == a.Sk && a.mask_kind == FAM_MASK_NONE && a.Sk >= 1 && fits32 && a.k0_rs >= DH &&
+          a.v0_rs >= DH) {
         const int nqb = (int)((a.Sq + 127) / 128);
         FAM_LAUNCH((attn_long_kernel<DH>), dim3((unsigned)(nqb * bh)), dim3(256), 0, s, a, nqb);
         return;

@@ -91,6 +91,18 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Raw buffer resource over [base, base + bytes): loads at byte offsets >= bytes return 0.
+// The descriptor lives in SGPRs, so `base` and `bytes` must be wave-uniform.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+// 16 bytes at byte offset voff (per lane) + soff (wave-uniform)
+__device__ __forceinline__ bf16x8 buffer_load8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
 }  // namespace fam
 
 // Host-side helpers shared by the C-ABI wrappers.
