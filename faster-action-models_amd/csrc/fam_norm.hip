@@ -29,92 +29,102 @@ __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
   const bf16* xr = a.x + r * a.xrs;
   const int64_t D = a.dim;
   const float invD = 1.0f / (float)D;
-
-  float v[NV > 0 ? NV : 1][8];
-  float s = 0.f;
-  if constexpr (NV > 0) {
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int64_t c = ((int64_t)i * 64 + lane) * 8;
-      if (c < D) {
-        bf16x8 t = load8(xr + c);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) { v[i][e] = to_f(t[e]); s += v[i][e]; }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
-      }
-    }
-  } else {
-    for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
-      bf16x8 t = load8(xr + c);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s += to_f(t[e]);
-    }
-  }
-  const float mean = wave_sum(s) * invD;
-  float q = 0.f;
-  if constexpr (NV > 0) {
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int64_t c = ((int64_t)i * 64 + lane) * 8;
-      if (c < D) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) { const float d = v[i][e] - mean; q += d * d; }
-      }
-    }
-  } else {
-    for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
-      bf16x8 t = load8(xr + c);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) { const float d = to_f(t[e]) - mean; q += d * d; }
-    }
-  }
-  const float rstd = rsqrtf(wave_sum(q) * invD + a.eps);
-
   const int64_t bidx = r / a.rpb, sidx = r - bidx * a.rpb;
   const int64_t moff = bidx * a.mbs + sidx * a.mrs;
   bf16* yr = a.y + r * a.yrs;
 
-  auto emit = [&](int64_t c, const float* xv) {
+  // LayerNorm of 8 elements (two-pass statistics given), then affine and modulation
+  auto finish = [&](const float* xv, float mean, float rstd, bf16x8 wv, bf16x8 bv, bf16x8 sh, bf16x8 sc) {
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = (xv[e] - mean) * rstd;
     if (a.w) {
-      bf16x8 wv = load8(a.w + c);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] *= to_f(wv[e]);
     }
     if (a.b) {
-      bf16x8 bv = load8(a.b + c);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] += to_f(bv[e]);
     }
     if (a.shift) {
-      bf16x8 sh = load8(a.shift + moff + c);
-      bf16x8 sc = load8(a.scale + moff + c);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = o[e] * (1.0f + to_f(sc[e])) + to_f(sh[e]);
     }
     bf16x8 out;
 #pragma unroll
     for (int e = 0; e < 8; ++e) out[e] = to_bf(o[e]);
-    store8(yr + c, out);
+    return out;
   };
 
   if constexpr (NV > 0) {
+    // Every load of the row (x, LayerNorm affine, shift / scale) is issued before the
+    // statistics, so a wave waits for memory once (the branches are wave-uniform).
+    bf16x8 xv8[NV], wv[NV], bv[NV], sh[NV], sc[NV];
+    auto col = [&](int i) { const int64_t c = ((int64_t)i * 64 + lane) * 8; return c < D ? c : 0; };
+#pragma unroll
+    for (int i = 0; i < NV; ++i) xv8[i] = load8(xr + col(i));
+    if (a.w) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) wv[i] = load8(a.w + col(i));
+    }
+    if (a.b) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) bv[i] = load8(a.b + col(i));
+    }
+    if (a.shift) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        sh[i] = load8(a.shift + moff + col(i));
+        sc[i] = load8(a.scale + moff + col(i));
+      }
+    }
+    float v[NV][8];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const bool ok = ((int64_t)i * 64 + lane) * 8 < D;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { v[i][e] = ok ? to_f(xv8[i][e]) : 0.f; s += v[i][e]; }
+    }
+    const float mean = wave_sum(s) * invD;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      if (((int64_t)i * 64 + lane) * 8 < D) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { const float d = v[i][e] - mean; q += d * d; }
+      }
+    }
+    const float rstd = rsqrtf(wave_sum(q) * invD + a.eps);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int64_t c = ((int64_t)i * 64 + lane) * 8;
-      if (c < D) emit(c, v[i]);
+      if (c < D) store8(yr + c, finish(v[i], mean, rstd, wv[i], bv[i], sh[i], sc[i]));
     }
   } else {
+    // wide rows: three passes over x (the re-reads hit L2)
+    float s = 0.f;
+    for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
+      bf16x8 t = load8(xr + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s += to_f(t[e]);
+    }
+    const float mean = wave_sum(s) * invD;
+    float q = 0.f;
+    for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
+      bf16x8 t = load8(xr + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { const float d = to_f(t[e]) - mean; q += d * d; }
+    }
+    const float rstd = rsqrtf(wave_sum(q) * invD + a.eps);
     for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
       bf16x8 t = load8(xr + c);
       float xv[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) xv[e] = to_f(t[e]);
-      emit(c, xv);
+      const bf16x8 z = t;
+      store8(yr + c, finish(xv, mean, rstd, a.w ? load8(a.w + c) : z, a.b ? load8(a.b + c) : z,
+                            a.shift ? load8(a.shift + moff + c) : z, a.shift ? load8(a.scale + moff + c) : z));
     }
   }
 }
@@ -195,6 +205,86 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(RmsRopeArgs a) {
   }
 }
 
+// Row-in-registers form of rmsnorm_rope_kernel for dim <= 64 * 8 * NV with the rotation
+// tables read as 16-byte vectors (TAB 0: no rotation; 1: separate cos / sin rows, element
+// stride 1; 2: interleaved (cos, sin) pairs).  Every load of the row -- x, the weight and the
+// table entries -- is issued before the sum of squares, so a wave waits for memory once.
+// TSH: hd divides 512, so the pairs of lane's chunk (i * 64 + lane) * 8 do not depend on i and
+// the table entries are read once per lane.
+template <int NV, int TAB, bool TSH>
+__global__ __launch_bounds__(256) void rmsnorm_rope_vec_kernel(RmsRopeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.rows) return;  // wave-uniform
+  const bf16* xr = a.x + r * a.xrs;
+  const int D = (int)a.dim, hd = (int)a.hd;
+  const int pos = (int)(r % a.seq);
+  const float* crow = a.cs + (int64_t)pos * a.trs;
+  const float* srow = a.sn + (int64_t)pos * a.trs;
+  bf16x8 in[NV], wv[NV];
+  f32x4 t0[NV], t1[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * 64 + lane) * 8, cc = c < D ? c : 0;
+    in[i] = load8(xr + cc);
+    if (a.w) wv[i] = load8(a.w + cc);   // wave-uniform
+    const int j0 = ((TSH ? lane * 8 : cc) % hd) >> 1;   // first of the 4 rotation pairs of these 8 elements
+    if (TSH && i > 0) {
+      t0[i] = t0[0];
+      t1[i] = t1[0];
+    } else if constexpr (TAB == 1) {
+      t0[i] = *reinterpret_cast<const f32x4*>(crow + j0);
+      t1[i] = *reinterpret_cast<const f32x4*>(srow + j0);
+    } else if constexpr (TAB == 2) {
+      t0[i] = *reinterpret_cast<const f32x4*>(crow + 2 * j0);       // c0 s0 c1 s1
+      t1[i] = *reinterpret_cast<const f32x4*>(crow + 2 * j0 + 4);   // c2 s2 c3 s3
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const bool ok = (i * 64 + lane) * 8 < D;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { const float f = ok ? to_f(in[i][e]) : 0.f; q += f * f; }
+  }
+  const float rs = a.w ? rsqrtf(wave_sum(q) / (float)D + a.eps) : 1.0f;
+  bf16* yr = a.y + r * a.yrs;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = (i * 64 + lane) * 8;
+    if (c >= D) continue;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = to_f(in[i][e]);
+    if (a.w) {
+      // RMSNorm rounds to the storage dtype before the weight multiply (FB/wan_video_dit.py:166-167).
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = to_f(to_bf(to_f(to_bf(o[e] * rs)) * to_f(wv[i][e])));
+    }
+    if constexpr (TAB != 0) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        float cc, ss;
+        if constexpr (TAB == 1) {
+          cc = t0[i][p];
+          ss = t1[i][p];
+        } else {
+          cc = p < 2 ? t0[i][2 * p] : t1[i][2 * p - 4];
+          ss = p < 2 ? t0[i][2 * p + 1] : t1[i][2 * p - 3];
+        }
+        const float x0 = o[2 * p], x1 = o[2 * p + 1];
+        o[2 * p] = x0 * cc - x1 * ss;
+        o[2 * p + 1] = x0 * ss + x1 * cc;
+      }
+    }
+    bf16x8 out;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = to_bf(o[e]);
+    store8(yr + c, out);
+  }
+}
+
 }  // namespace fam
 
 using namespace fam;
@@ -272,6 +362,36 @@ extern "C" int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, in
                 head_dim > 0 ? head_dim : 8};
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
   hipStream_t s = (hipStream_t)stream;
+  // vector table reads: rows of 16-byte aligned fp32 with 4 consecutive pairs per 8 elements
+  const auto al16 = [](const void* p) { return fam_host::aligned16(p); };
+  int tab = 3;
+  if (!cos_tab) tab = 0;
+  else if (tab_elem_stride == 1 && tab_row_stride % 4 == 0 && al16(cos_tab) && al16(sin_tab)) tab = 1;
+  else if (tab_elem_stride == 2 && sin_tab == cos_tab + 1 && tab_row_stride % 4 == 0 && al16(cos_tab)) tab = 2;
+  if (nv != 0 && tab != 3 && dim <= (int64_t)1 << 30) {
+    const bool tsh = 512 % a.hd == 0;
+#define FAM_RR_VEC(NV)                                                                                          \
+  switch (tab) {                                                                                                \
+    case 0: FAM_LAUNCH((rmsnorm_rope_vec_kernel<NV, 0, false>), grid, block, 0, s, a); break;                   \
+    case 1:                                                                                                     \
+      if (tsh) FAM_LAUNCH((rmsnorm_rope_vec_kernel<NV, 1, true>), grid, block, 0, s, a);                        \
+      else FAM_LAUNCH((rmsnorm_rope_vec_kernel<NV, 1, false>), grid, block, 0, s, a);                           \
+      break;                                                                                                    \
+    default:                                                                                                    \
+      if (tsh) FAM_LAUNCH((rmsnorm_rope_vec_kernel<NV, 2, true>), grid, block, 0, s, a);                        \
+      else FAM_LAUNCH((rmsnorm_rope_vec_kernel<NV, 2, false>), grid, block, 0, s, a);                           \
+      break;                                                                                                    \
+  }
+    switch (nv) {
+      case 1: FAM_RR_VEC(1); break;
+      case 2: FAM_RR_VEC(2); break;
+      case 4: FAM_RR_VEC(4); break;
+      case 6: FAM_RR_VEC(6); break;
+      default: FAM_RR_VEC(8); break;
+    }
+#undef FAM_RR_VEC
+    return fam_host::check_launch("fam_rmsnorm_rope");
+  }
   switch (nv) {
     case 1: FAM_LAUNCH(rmsnorm_rope_kernel<1>, grid, block, 0, s, a); break;
     case 2: FAM_LAUNCH(rmsnorm_rope_kernel<2>, grid, block, 0, s, a); break;

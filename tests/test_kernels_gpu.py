@@ -79,7 +79,7 @@ def test_rms_norm(R, D):
     assert relerr(ops().rms_norm(dev(x), dev(w), 1e-6), ref) <= TOL
 
 
-@pytest.mark.parametrize("B,S,H,Dh", [(1, 32, 16, 64), (2, 9, 24, 128), (1, 8, 4, 8)])
+@pytest.mark.parametrize("B,S,H,Dh", [(1, 32, 16, 64), (2, 9, 24, 128), (1, 8, 4, 8), (1, 5, 4, 24)])
 @pytest.mark.parametrize("layout", ["complex", "cat", "interleaved"])
 def test_rope(B, S, H, Dh, layout):
     x = rnd(B, S, H * Dh, seed=11)
@@ -94,6 +94,24 @@ def test_rope(B, S, H, Dh, layout):
         inter = torch.view_as_real(fr).reshape(S, 1, Dh).double()
         y = ops().rope_apply_cae(dev(x), dev(inter), H)
     assert relerr(y, ref) <= TOL
+
+
+def test_rope_scalar_table_path():
+    """Tables whose rows are not 16-byte multiples take the per-element table reads."""
+    from fam import _capi
+    B, S, H, Dh = 1, 6, 4, 16
+    x = rnd(B, S, H * Dh, seed=12)
+    fr = O.action_freqs(Dh, S)
+    ref = O.rope_apply(x.float(), fr, H)
+    half = Dh // 2
+    tab = torch.zeros(S, 2 * half + 1, dtype=torch.float32)   # row stride 17 floats: (cos | sin | pad)
+    tab[:, :half], tab[:, half:2 * half] = fr.real.reshape(S, half), fr.imag.reshape(S, half)
+    t = dev(tab)
+    xd = dev(x).reshape(S, H * Dh)
+    y = torch.empty_like(xd)
+    _capi.call("fam_rmsnorm_rope", xd.data_ptr(), H * Dh, y.data_ptr(), H * Dh, S, S, H * Dh, None, 0.0,
+               t.data_ptr(), t.data_ptr() + 4 * half, 2 * half + 1, 1, Dh, 0)
+    assert relerr(y.reshape(B, S, H * Dh), ref) <= TOL
 
 
 def test_rope_3d_video_table():
@@ -278,6 +296,11 @@ def test_euler_step():
     dB = torch.tensor([-0.1, -0.2, -0.3, -0.4], dtype=torch.bfloat16)
     refB = O.scheduler_step(v, dB, x)
     assert torch.equal(ops().euler_step(dev(v), dev(dB), dev(x)).cpu(), refB)
+    # element counts off the 8-element vector path (scalar kernel) and a many-block vector case
+    for shape, nb in (((3, 5, 7), 3), ((8, 129, 64), 8)):
+        xs, vs = rnd(*shape, seed=59), rnd(*shape, seed=60)
+        dd = (torch.arange(nb, dtype=torch.float32) * -0.05 - 0.01).to(torch.bfloat16)
+        assert torch.equal(ops().euler_step(dev(vs), dev(dd), dev(xs)).cpu(), O.scheduler_step(vs, dd, xs))
     sched = ops().WanContinuousFlowMatchScheduler(shift=5.0)
     ts, ds = sched.build_inference_schedule(10, "cuda", torch.bfloat16)
     ots, ods = O.build_inference_schedule(10, 5.0, torch.bfloat16)
