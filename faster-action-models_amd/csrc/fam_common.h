@@ -91,6 +91,17 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Workgroup barrier that waits for this wave's LDS operations only (lgkmcnt(0)), not for its
+// global loads: __syncthreads() also drains vmcnt, which would stall on register prefetches
+// issued just before it.  The empty asm statements keep the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // vmcnt 63 (no wait), expcnt 7, lgkmcnt 0
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Raw buffer resource over [base, base + bytes): loads at byte offsets >= bytes return 0.
 // The descriptor lives in SGPRs, so `base` and `bytes` must be wave-uniform.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {

@@ -526,6 +526,236 @@ __global__ __launch_bounds__(256) void tiled_kernel(GemmArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// big_kernel (M >= 128, no prologue, K % 64 == 0): the throughput GEMM of the video backbone
+// and of batched action calls.
+//   * 256 threads = 2 x 2 waves; a wave owns (16 WFM) x (16 WFN) outputs (up to 128 x 128,
+//     256 fp32 accumulators per lane in the accumulation registers), the workgroup
+//     BM x BN = (32 WFM) x (32 WFN);
+//   * K in blocks of 64 through double-buffered LDS: rows of 128 bytes (8 chunks of 16 B)
+//     with chunk kc of row r stored at kc ^ (r & 7), which keeps both the 16-byte fragment
+//     reads (16 rows x 4 chunks per wave) and the staging writes free of LDS bank conflicts
+//     (measured) with no padding;
+//   * global loads of the next block (raw buffer loads: rows past M or N read as zero, 32-bit
+//     offsets) are in flight during the current block's 2 x WFM x WFN MFMAs, then land in the
+//     other LDS buffer; one barrier per block;
+//   * workgroups are spread over the 8 XCDs in contiguous task ranges, and a range walks the
+//     tile grid column by column in groups of row tiles, so consecutive tiles on one XCD share
+//     their weight panel (and row panels) in that XCD's L2;
+//   * epilogue: bias, activation, gate * value + residual on 4 consecutive columns per lane,
+//     8-byte (bf16) or 16-byte (fp32) stores.
+// MFMA operands: A = weight rows (n), B = activation rows (m), so a lane's accumulator holds
+// out[m][n .. n + 3] for one m.
+template <int WFM, int WFN>
+__global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int tiles_n) {
+  constexpr int BM = 32 * WFM, BN = 32 * WFN, BKB = 64;
+  constexpr int CA = BM * 8 / 256, CW = BN * 8 / 256;   // 16-byte chunks per thread per block
+  __shared__ __attribute__((aligned(16))) bf16 As[2][BM * BKB];
+  __shared__ __attribute__((aligned(16))) bf16 Ws[2][BN * BKB];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int wm0 = (wave >> 1) * (16 * WFM), wn0 = (wave & 1) * (16 * WFN);
+
+  // task order: XCD-contiguous ranges (the grid is padded to a multiple of 8; workgroups past
+  // the last task exit), then column-major over groups of up to 8 row tiles
+  const int nwg = tiles_m * tiles_n, tpx = (nwg + 7) >> 3;
+  const int task = (blockIdx.x & 7) * tpx + (blockIdx.x >> 3);
+  if (task >= nwg) return;   // workgroup-uniform, before any barrier
+  const int GM = tiles_m < 8 ? tiles_m : 8;
+  const int grp = task / (GM * tiles_n), rem = task - grp * (GM * tiles_n);
+  const int gm = (tiles_m - grp * GM) < GM ? (tiles_m - grp * GM) : GM;   // rows in this group
+  const int tm = grp * GM + rem % gm, tn = rem / gm;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int Mi = (int)g.M, Ni = (int)g.N;
+  const uint32_t lda2 = (uint32_t)g.lda * 2u, ldw2 = (uint32_t)g.ldw * 2u;
+  const auto arsrc = buffer_rsrc(g.a + (int64_t)m0 * g.lda, (uint32_t)(Mi - m0) * lda2);
+  const auto wrsrc = buffer_rsrc(g.w + (int64_t)n0 * g.ldw, (uint32_t)(Ni - n0 < BN ? Ni - n0 : BN) * ldw2);
+  // staging chunk q = tid + 256 p: row q / 8, chunk q % 8 (rows of one p are 32 apart)
+  const int sr = tid >> 3, skc = tid & 7;
+  auto swz = [](int r) { return r & 7; };
+  const uint32_t aoff = (uint32_t)sr * lda2 + (uint32_t)skc * 16u;
+  const uint32_t woff = (uint32_t)sr * ldw2 + (uint32_t)skc * 16u;
+  bf16x8 ra[CA], rw[CW];
+  auto gload = [&](int kb) {
+    const uint32_t k2 = (uint32_t)kb * (BKB * 2);
+#pragma unroll
+    for (int p = 0; p < CA; ++p) ra[p] = buffer_load8(arsrc, aoff + k2, (uint32_t)p * 32u * lda2);
+#pragma unroll
+    for (int p = 0; p < CW; ++p) rw[p] = buffer_load8(wrsrc, woff + k2, (uint32_t)p * 32u * ldw2);
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < CA; ++p) {
+      const int r = sr + 32 * p;
+      *reinterpret_cast<bf16x8*>(&As[buf][r * BKB + ((skc ^ swz(r)) << 3)]) = ra[p];
+    }
+#pragma unroll
+    for (int p = 0; p < CW; ++p) {
+      const int r = sr + 32 * p;
+      *reinterpret_cast<bf16x8*>(&Ws[buf][r * BKB + ((skc ^ swz(r)) << 3)]) = rw[p];
+    }
+  };
+  auto frag = [&](const bf16* tile, int r, int kc) {
+    return *reinterpret_cast<const bf16x8*>(&tile[r * BKB + ((kc ^ swz(r)) << 3)]);
+  };
+
+  f32x4 acc[WFM][WFN];
+#pragma unroll
+  for (int i = 0; i < WFM; ++i)
+#pragma unroll
+    for (int j = 0; j < WFN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Fragments of the two 32-wide k-steps of a block live in separate registers (F0, F1), and
+  // the staging registers carry a block from its global load (one iteration ahead) to its LDS
+  // store.  Iteration kb, with no branches inside:
+  //   [read F1 = kb step 1]
+  //   MFMA(F0) interleaved with, per staging chunk, [LDS store of kb+1] [global load of kb+2]
+  //   barrier   [read F0 = kb+1 step 0]   MFMA(F1)
+  // The MFMA pipe stays fed while the stores and loads issue; past the end of K the loads read
+  // zeros or unused data into buffers no MFMA reads (the barrier's wait for outstanding LDS
+  // operations keeps a buffer's last readers ahead of its next writers).
+  bf16x8 a0[WFM], w0[WFN], a1[WFM], w1[WFN];
+  auto rfrag = [&](int buf, int s, bf16x8* af, bf16x8* wf) {
+#pragma unroll
+    for (int i = 0; i < WFM; ++i) af[i] = frag(As[buf], wm0 + i * 16 + l16, s * 4 + lg);
+#pragma unroll
+    for (int j = 0; j < WFN; ++j) wf[j] = frag(Ws[buf], wn0 + j * 16 + l16, s * 4 + lg);
+  };
+  auto mfmas = [&](const bf16x8* af, const bf16x8* wf) {
+#pragma unroll
+    for (int i = 0; i < WFM; ++i)
+#pragma unroll
+      for (int j = 0; j < WFN; ++j) acc[i][j] = mfma16(wf[j], af[i], acc[i][j]);
+  };
+  // staging chunk c < CA: A rows sr + 32 c; c >= CA: W rows sr + 32 (c - CA)
+  auto store_chunk = [&](int buf, int c) {
+    if (c < CA) {
+      const int r = sr + 32 * c;
+      *reinterpret_cast<bf16x8*>(&As[buf][r * BKB + ((skc ^ swz(r)) << 3)]) = ra[c];
+    } else {
+      const int r = sr + 32 * (c - CA);
+      *reinterpret_cast<bf16x8*>(&Ws[buf][r * BKB + ((skc ^ swz(r)) << 3)]) = rw[c - CA];
+    }
+  };
+  auto load_chunk = [&](int kb, int c) {
+    const uint32_t k2 = (uint32_t)kb * (BKB * 2);
+    if (c < CA) ra[c] = buffer_load8(arsrc, aoff + k2, (uint32_t)c * 32u * lda2);
+    else rw[c - CA] = buffer_load8(wrsrc, woff + k2, (uint32_t)(c - CA) * 32u * ldw2);
+  };
+  constexpr int NC = CA + CW, NM = WFM * WFN;
+  const int nkb = (int)(g.K / BKB);
+  if constexpr (NM > 32) {
+    // 8 x 8 wave tiles: the interleaved schedule below does not fit the registers; the block's
+    // global loads go out at the top of its iteration and land in LDS between the two halves
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    rfrag(0, 0, a0, w0);
+    for (int kb = 0; kb < nkb; ++kb) {
+      const int buf = kb & 1;
+      const bool more = kb + 1 < nkb;
+      if (more) gload(kb + 1);
+      rfrag(buf, 1, a1, w1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(a0, w0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (more) lstore(buf ^ 1);
+      __syncthreads();
+      if (more) rfrag(buf ^ 1, 0, a0, w0);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(a1, w1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+  gload(0);
+  lstore(0);
+  gload(1);
+  lds_barrier();
+  rfrag(0, 0, a0, w0);
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int buf = kb & 1;
+    rfrag(buf, 1, a1, w1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      const int i = mi / WFN, j = mi % WFN;
+      acc[i][j] = mfma16(w0[j], a0[i], acc[i][j]);
+      if ((mi + 1) * NC / NM > mi * NC / NM) {
+        const int c = mi * NC / NM;
+        store_chunk(buf ^ 1, c);
+        load_chunk(kb + 2, c);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    lds_barrier();
+    rfrag(buf ^ 1, 0, a0, w0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(a1, w1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  }
+
+  // lane owns out[m0 + wm0 + i*16 + l16][n0 + wn0 + j*16 + 4*lg + e] (N % 4 == 0 and the
+  // operand alignment of 4-column vectors are host-checked)
+#pragma unroll
+  for (int i = 0; i < WFM; ++i) {
+    const int m = m0 + wm0 + i * 16 + l16;
+    if (m >= Mi) continue;
+    const int64_t bi = m / g.rpb, si = m - bi * g.rpb;
+#pragma unroll
+    for (int j = 0; j < WFN; ++j) {
+      const int nb = n0 + wn0 + j * 16 + lg * 4;
+      if (nb >= Ni) continue;
+      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      if (g.bias) {
+        const bf16x4 bv = *reinterpret_cast<const bf16x4*>(g.bias + nb);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += to_f(bv[e]);
+      }
+      if (g.act == FAM_ACT_GELU_TANH) {
+        // 0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)), u = sqrt(2/pi) (x + 0.044715 x^3)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float x = v[e], u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+          v[e] = x / (1.0f + __expf(-2.0f * u));
+        }
+      } else if (g.act == FAM_ACT_SILU) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = v[e] / (1.0f + __expf(-v[e]));
+      }
+      if (g.res) {
+        float gt[4] = {1.f, 1.f, 1.f, 1.f}, rv[4];
+        if (g.gate) {
+          const bf16x4 gv = *reinterpret_cast<const bf16x4*>(g.gate + bi * g.gbs + si * g.grs + nb);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) gt[e] = to_f(gv[e]);
+        }
+        if (g.out_f32) {
+          const f32x4 r4 = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(g.res) + (int64_t)m * g.ldr + nb);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rv[e] = r4[e];
+        } else {
+          const bf16x4 r4 = *reinterpret_cast<const bf16x4*>(g.res + (int64_t)m * g.ldr + nb);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rv[e] = to_f(r4[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = rv[e] + gt[e] * v[e];
+      }
+      if (g.out_f32) {
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(g.out) + (int64_t)m * g.ldo + nb) = f32x4{v[0], v[1], v[2], v[3]};
+      } else {
+        bf16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = to_bf(v[e]);
+        *reinterpret_cast<bf16x4*>(g.out + (int64_t)m * g.ldo + nb) = o;
+      }
+    }
+  }
+}
+
 static int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 template <int MT, int NW, int KS>
@@ -548,6 +778,47 @@ template <int MT>
 static void launch_skinny_k(const GemmArgs& a, int pro, hipStream_t s) {
   if (a.K <= 1024) launch_skinny<MT, 8, 4>(a, pro, s);
   else launch_skinny<MT, 16, 8>(a, pro, s);
+}
+
+// The big kernel's envelope: no prologue, K % 64 == 0, M >= 128, 32-bit byte offsets into a
+// and w, and a 4-column vector epilogue (N % 4 == 0, unit gate column stride, aligned vectors).
+static bool big_ok(const fam_gemm_desc* d) {
+  const int64_t ob = d->out_f32 ? 16 : 8;
+  const auto al = [](const void* p, int64_t b) { return ((uintptr_t)p % (uintptr_t)b) == 0; };
+  return d->prologue == FAM_PRO_NONE && d->K % 64 == 0 && d->M >= 128 && d->M * d->lda * 2 < ((int64_t)1 << 31) &&
+         d->N * d->ldw * 2 < ((int64_t)1 << 31) && d->N % 4 == 0 && d->ldo % 4 == 0 && al(d->out, ob) &&
+         (!d->bias || al(d->bias, 8)) && (!d->res || (d->ldr % 4 == 0 && al(d->res, ob))) &&
+         (!d->gate || (d->gate_ns == 1 && d->gate_bs % 4 == 0 && d->gate_rs % 4 == 0 && al(d->gate, 8)));
+}
+
+template <int WFM, int WFN>
+static void launch_big(const GemmArgs& a, hipStream_t s) {
+  const int tm = (int)((a.M + 32 * WFM - 1) / (32 * WFM)), tn = (int)((a.N + 32 * WFN - 1) / (32 * WFN));
+  const unsigned grid = (unsigned)(((tm * tn + 7) / 8) * 8);
+  FAM_LAUNCH((big_kernel<WFM, WFN>), dim3(grid), dim3(256), 0, s, a, tm, tn);
+}
+
+// Tile of the big kernel: 256 x 256 (8 x 8 wave tiles, one workgroup per CU) or 128 x 128
+// (4 x 4 wave tiles, two workgroups per CU), whichever has the smaller estimated time =
+// (most tiles any CU gets) x tile area / efficiency, the per-FLOP throughput of a CU relative
+// to the 256 x 256 tile (measured on gfx950: 0.97 for 128 x 128 at two workgroups per CU).
+static void big_plan(int64_t M, int64_t N, int* wfm, int* wfn) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus = n;
+  }
+  struct C { int fm, fn; double eff; } cands[] = {{8, 8, 1.0}, {4, 4, 0.97}};
+  double best = 1e300;
+  for (const C& c : cands) {
+    const int64_t bm = 32 * c.fm, bn = 32 * c.fn;
+    const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    const double per_cu = (double)((tiles + cus - 1) / cus);
+    const double t = per_cu * (double)(bm * bn) / c.eff;
+    if (t < best) { best = t; *wfm = c.fm; *wfn = c.fn; }
+  }
 }
 
 template <int BM, int BN, int WM>
@@ -613,7 +884,12 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
   if (skinny && d->M <= 16) launch_skinny_k<1>(a, d->prologue, s);
   else if (skinny && d->M <= 32) launch_skinny_k<2>(a, d->prologue, s);
   else if (skinny) launch_skinny_k<4>(a, d->prologue, s);
-  else if (round_up(d->M, 128) / 128 * (round_up(d->N, 128) / 128) >= 200) launch_tiled<128, 128, 2>(a, d->prologue, s);
+  else if (big_ok(d)) {
+    int fm = 8, fn = 8;
+    big_plan(d->M, d->N, &fm, &fn);
+    if (fm == 8) launch_big<8, 8>(a, s);
+    else launch_big<4, 4>(a, s);
+  } else if (round_up(d->M, 128) / 128 * (round_up(d->N, 128) / 128) >= 200) launch_tiled<128, 128, 2>(a, d->prologue, s);
   else launch_tiled<64, 64, 2>(a, d->prologue, s);
   return fam_host::check_launch("fam_gemm");
 }

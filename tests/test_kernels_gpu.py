@@ -231,6 +231,32 @@ def test_gemm_deterministic(M, N, K):
     assert torch.equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 128), (3900, 3900, 128), (2600, 3000, 192), (300, 520, 320)])
+def test_gemm_large_tiles_epilogue(M, N, K):
+    """Large-M products on the big-tile kernel (256 x 256 tiles for the first two shapes,
+    128 x 128 for the others; ragged M and N): bias + GELU, then gate * y + residual with a
+    per-row gate, then an fp32 residual output; and a shape off its envelope (N % 4 != 0) on
+    the tiled kernel."""
+    from fam import _capi
+    x, w, b = rnd(M, K, seed=65), rnd(N, K, seed=66, scale=0.05), rnd(N, seed=67, scale=0.05)
+    lin = O.linear(x.float(), w.float(), b.float())
+    y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ops().gemm(dev(x), dev(w), dev(b), y, act=_capi.FAM_ACT_GELU_TANH)
+    assert relerr(y, O.gelu_tanh(lin)) <= TOL
+    res, gate = rnd(M, N, seed=68), rnd(M, N, seed=69, scale=0.3)
+    out = dev(res.clone())
+    ops().gemm(dev(x), dev(w), dev(b), out, res=out, gate=dev(gate), gate_bs=0, gate_rs=N, gate_ns=1,
+               rows_per_batch=M)
+    assert relerr(out, res.float() + gate.float() * lin) <= TOL
+    resf = torch.randn(M, N, generator=torch.Generator().manual_seed(70))
+    outf = dev(resf.clone())
+    ops().gemm(dev(x), dev(w), dev(b), outf, res=outf, out_f32=True)
+    assert (outf.cpu() - (resf + lin)).abs().max().item() <= 2e-2 * lin.abs().max().item()
+    if M == 300:
+        w3, b3 = rnd(N - 1, K, seed=71, scale=0.05), rnd(N - 1, seed=72, scale=0.05)
+        assert relerr(ops().linear(dev(x), dev(w3), dev(b3)), O.linear(x.float(), w3.float(), b3.float())) <= TOL
+
+
 def test_gemm_fp32_residual_out():
     """out_f32: fp32 residual and output (the fused Euler update of fp32 latents)."""
     M, N, K = 32, 7, 1024
