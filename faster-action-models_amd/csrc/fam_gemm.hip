@@ -798,10 +798,11 @@ static void launch_big(const GemmArgs& a, hipStream_t s) {
   FAM_LAUNCH((big_kernel<WFM, WFN>), dim3(grid), dim3(256), 0, s, a, tm, tn);
 }
 
-// Tile of the big kernel: 256 x 256 (8 x 8 wave tiles, one workgroup per CU) or 128 x 128
-// (4 x 4 wave tiles, two workgroups per CU), whichever has the smaller estimated time =
-// (most tiles any CU gets) x tile area / efficiency, the per-FLOP throughput of a CU relative
-// to the 256 x 256 tile (measured on gfx950: 0.97 for 128 x 128 at two workgroups per CU).
+// Tile of the big kernel: 256 x 256 (8 x 8 wave tiles, 1 workgroup per CU), 128 x 128 (4 x 4,
+// 2 per CU) or 64 x 64 (2 x 2, 4 per CU), whichever has the smallest estimated time =
+// rounds x (concurrent tiles per CU) x tile area / efficiency, where a round fills every CU
+// with its concurrent tiles and the efficiency is the per-FLOP throughput of a full CU
+// relative to the 256 x 256 tile (measured on gfx950 at large K: 0.91 and 0.65).
 static void big_plan(int64_t M, int64_t N, int* wfm, int* wfn) {
   static int cus = 0;
   if (cus == 0) {
@@ -810,13 +811,14 @@ static void big_plan(int64_t M, int64_t N, int* wfm, int* wfn) {
       n = 256;
     cus = n;
   }
-  struct C { int fm, fn; double eff; } cands[] = {{8, 8, 1.0}, {4, 4, 0.97}};
+  struct C { int fm, fn, conc; double eff; } cands[] = {{8, 8, 1, 1.0}, {4, 4, 2, 0.91}, {2, 2, 4, 0.65}};
   double best = 1e300;
   for (const C& c : cands) {
     const int64_t bm = 32 * c.fm, bn = 32 * c.fn;
     const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    const double per_cu = (double)((tiles + cus - 1) / cus);
-    const double t = per_cu * (double)(bm * bn) / c.eff;
+    const int64_t slots = (int64_t)cus * c.conc;
+    const double rounds = (double)((tiles + slots - 1) / slots);
+    const double t = rounds * c.conc * (double)(bm * bn) / c.eff;
     if (t < best) { best = t; *wfm = c.fm; *wfn = c.fn; }
   }
 }
@@ -888,7 +890,8 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
     int fm = 8, fn = 8;
     big_plan(d->M, d->N, &fm, &fn);
     if (fm == 8) launch_big<8, 8>(a, s);
-    else launch_big<4, 4>(a, s);
+    else if (fm == 4) launch_big<4, 4>(a, s);
+    else launch_big<2, 2>(a, s);
   } else if (round_up(d->M, 128) / 128 * (round_up(d->N, 128) / 128) >= 200) launch_tiled<128, 128, 2>(a, d->prologue, s);
   else launch_tiled<64, 64, 2>(a, d->prologue, s);
   return fam_host::check_launch("fam_gemm");
