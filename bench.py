@@ -56,10 +56,11 @@ def parse():
     ap.add_argument("--no-eager", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--cpu-sample-s", type=float, default=20.0, help="CPU baseline time budget")
-    ap.add_argument("--workload", choices=["c1", "c2", "c3"], default="c1",
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "hbm"], default="c1",
                     help="c1: the action-DiT denoise loop (the metric); c2: one long-sequence video DiT block "
                          "(config 2 shape), reported as ms per 30-block forward with MFMA utilisation; c3: the "
-                         "compact expert loop + action-VAE decoder at B=1 and B=256")
+                         "compact expert loop + action-VAE decoder at B=1 and B=256; hbm: size sweep of the "
+                         "HBM-bound kernels (AdaLN, RMSNorm+RoPE, Euler) from config 2 / config 3 B=256 shapes up")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -388,6 +389,80 @@ def bench_c2(args):
     print(json.dumps(out), flush=True)
 
 
+# --------------------------------------------------------------------------- HBM-bound kernels, size sweep
+def bench_hbm(args):
+    """Achieved HBM bandwidth of the norm, RoPE and Euler kernels against rows / elements: the
+    config-2 row count (1560 tokens x 3072) and larger, and the config-3 B=256 Euler update
+    (256 x 8 x 16) and larger.  Each launch is timed by HIP events recorded at the kernel's
+    own begin and end (fam_set_launch_events); the median of `steps` launches is reported."""
+    import torch
+    from fam import ops, _capi
+    lib = _capi.lib()
+    dev = torch.device("cuda:0")
+    g = torch.Generator("cpu").manual_seed(77)
+    st = torch.cuda.current_stream()
+
+    def timed(fn, n):
+        for _ in range(3):
+            fn()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        for e0, e1 in ev:
+            e0.record(st)
+            e1.record(st)
+        torch.cuda.synchronize()
+        for e0, e1 in ev:
+            lib.fam_set_launch_events(e0.cuda_event, e1.cuda_event)
+            try:
+                fn()
+            finally:
+                lib.fam_set_launch_events(None, None)
+        torch.cuda.synchronize()
+        return statistics.median(e0.elapsed_time(e1) * 1e3 for e0, e1 in ev)
+
+    rows = []
+    D, heads = 3072, 24
+    n = max(args.steps, 5)
+    for R in (1560, 8192, 32768):
+        x = torch.randn(1, R, D, generator=g).to(dev, torch.bfloat16)
+        sh = (torch.randn(1, R, D, generator=g) * 0.1).to(dev, torch.bfloat16)
+        sc = (torch.randn(1, R, D, generator=g) * 0.1).to(dev, torch.bfloat16)
+        norm = torch.nn.LayerNorm(D, elementwise_affine=False, eps=1e-6)
+        out = [None]
+        us = timed(lambda: out.__setitem__(0, ops.adaln_forward(x, norm, sh, sc)), n)
+        rows.append(("adaln per-token modulation", f"{R}x{D}", 8 * R * D, us))
+        us = timed(lambda: out.__setitem__(0, ops.adaln_forward(x, norm, sh[:, :1], sc[:, :1])), n)
+        rows.append(("adaln broadcast modulation", f"{R}x{D}", 4 * R * D, us))
+        w = torch.ones(D, device=dev, dtype=torch.bfloat16)
+        ang = torch.rand(R, 1, D // heads // 2, generator=g, dtype=torch.float64)
+        fr = torch.polar(torch.ones_like(ang), ang)
+        us = timed(lambda: out.__setitem__(0, ops.rms_norm_rope(x, w, 1e-6, fr, heads)), n)
+        rows.append(("rmsnorm + rope (q of config 2)", f"{R}x{D}", 4 * R * D + 4 * 2 * R * (D // heads // 2), us))
+        del x, sh, sc
+    for numel in (256 * 8 * 16, 1 << 20, 16 << 20, 64 << 20):
+        s_ = torch.randn(numel, generator=g).to(dev, torch.bfloat16)
+        v_ = torch.randn(numel, generator=g).to(dev, torch.bfloat16)
+        o_ = torch.empty_like(s_)
+        dl = torch.tensor(-0.1, dtype=torch.bfloat16, device=dev)
+        us = timed(lambda: ops.euler_step(v_, dl, s_, out=o_), n)
+        rows.append(("euler update", str(numel), 6 * numel, us))
+    table = [{"kernel": k, "size": sz, "bytes": b, "us": round(u, 2), "GBs": round(b / (u * 1e-6) / 1e9, 1),
+              "frac_of_hbm": round(b / (u * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)} for k, sz, b, u in rows]
+    for r in table:
+        log(f"{r['kernel']:32s} {r['size']:>12s} {r['us']:9.2f} us {r['GBs']:8.1f} GB/s ({100 * r['frac_of_hbm']:.0f}%)")
+    best = max(table, key=lambda r: r["GBs"])
+    out = {
+        "metric": "achieved HBM GB/s of the norm, RoPE and Euler kernels (size sweep)", "value": best["GBs"],
+        "unit": "GB/s", "n_gpus": 1, "steps": n, "warmup": 3, "ms_per_step": None, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic: seeded N(0,1)",
+        "config": {"workload": "HBM-bound kernels: AdaLN and RMSNorm+RoPE over R x 3072 rows (R = 1560 is config 2), "
+                               "Euler over n elements (n = 32768 is config 3 at B=256)"},
+        "roofline": {"kernel": best["kernel"], "bound": "hbm", "achieved": best["GBs"], "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": best["frac_of_hbm"], "traffic": None},
+        "sweep": table,
+    }
+    print(json.dumps(out), flush=True)
+
+
 # --------------------------------------------------------------------------- config 3: compact expert + decoder
 def bench_c3(args):
     """Config 3: the compact action expert (hidden 32, 4 x 8 heads, 8 blocks) denoising an 8 x 16
@@ -471,6 +546,9 @@ def main():
         return
     if args.workload == "c2":
         bench_c2(args)
+        return
+    if args.workload == "hbm":
+        bench_hbm(args)
         return
     if args.workload == "c3":
         bench_c3(args)

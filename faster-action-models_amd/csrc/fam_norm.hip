@@ -210,78 +210,88 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(RmsRopeArgs a) {
 // stride 1; 2: interleaved (cos, sin) pairs).  Every load of the row -- x, the weight and the
 // table entries -- is issued before the sum of squares, so a wave waits for memory once.
 // TSH: hd divides 512, so the pairs of lane's chunk (i * 64 + lane) * 8 do not depend on i and
-// the table entries are read once per lane.
-template <int NV, int TAB, bool TSH>
+// the table entries are read once per lane and row.  RPW: rows per wave (a wave owns rows
+// RPW * w .. RPW * w + RPW - 1 and issues the loads of all of them at once, sharing the weight).
+template <int NV, int TAB, bool TSH, int RPW>
 __global__ __launch_bounds__(256) void rmsnorm_rope_vec_kernel(RmsRopeArgs a) {
+  constexpr int NT = TSH ? 1 : NV;   // table vectors per row
   const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= a.rows) return;  // wave-uniform
-  const bf16* xr = a.x + r * a.xrs;
+  const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+  if (r0 >= a.rows) return;  // wave-uniform
   const int D = (int)a.dim, hd = (int)a.hd;
-  const int pos = (int)(r % a.seq);
-  const float* crow = a.cs + (int64_t)pos * a.trs;
-  const float* srow = a.sn + (int64_t)pos * a.trs;
-  bf16x8 in[NV], wv[NV];
-  f32x4 t0[NV], t1[NV];
+  bf16x8 in[RPW][NV], wv[NV];
+  f32x4 t0[RPW][NT], t1[RPW][NT];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = (i * 64 + lane) * 8, cc = c < D ? c : 0;
-    in[i] = load8(xr + cc);
-    if (a.w) wv[i] = load8(a.w + cc);   // wave-uniform
-    const int j0 = ((TSH ? lane * 8 : cc) % hd) >> 1;   // first of the 4 rotation pairs of these 8 elements
-    if (TSH && i > 0) {
-      t0[i] = t0[0];
-      t1[i] = t1[0];
-    } else if constexpr (TAB == 1) {
-      t0[i] = *reinterpret_cast<const f32x4*>(crow + j0);
-      t1[i] = *reinterpret_cast<const f32x4*>(srow + j0);
-    } else if constexpr (TAB == 2) {
-      t0[i] = *reinterpret_cast<const f32x4*>(crow + 2 * j0);       // c0 s0 c1 s1
-      t1[i] = *reinterpret_cast<const f32x4*>(crow + 2 * j0 + 4);   // c2 s2 c3 s3
+  for (int k = 0; k < RPW; ++k) {
+    const int64_t r = r0 + k < a.rows ? r0 + k : a.rows - 1;
+    const bf16* xr = a.x + r * a.xrs;
+    const int pos = (int)(r % a.seq);
+    const float* crow = a.cs + (int64_t)pos * a.trs;
+    const float* srow = a.sn + (int64_t)pos * a.trs;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * 64 + lane) * 8, cc = c < D ? c : 0;
+      in[k][i] = load8(xr + cc);
+      if (k == 0 && a.w) wv[i] = load8(a.w + cc);   // wave-uniform
+      if (i < NT) {
+        const int j0 = ((TSH ? lane * 8 : cc) % hd) >> 1;   // first of the 4 rotation pairs of these 8 elements
+        if constexpr (TAB == 1) {
+          t0[k][i] = *reinterpret_cast<const f32x4*>(crow + j0);
+          t1[k][i] = *reinterpret_cast<const f32x4*>(srow + j0);
+        } else if constexpr (TAB == 2) {
+          t0[k][i] = *reinterpret_cast<const f32x4*>(crow + 2 * j0);       // c0 s0 c1 s1
+          t1[k][i] = *reinterpret_cast<const f32x4*>(crow + 2 * j0 + 4);   // c2 s2 c3 s3
+        }
+      }
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  float q = 0.f;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const bool ok = (i * 64 + lane) * 8 < D;
+  for (int k = 0; k < RPW; ++k) {
+    if (r0 + k >= a.rows) break;  // wave-uniform
+    float q = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) { const float f = ok ? to_f(in[i][e]) : 0.f; q += f * f; }
-  }
-  const float rs = a.w ? rsqrtf(wave_sum(q) / (float)D + a.eps) : 1.0f;
-  bf16* yr = a.y + r * a.yrs;
+    for (int i = 0; i < NV; ++i) {
+      const bool ok = (i * 64 + lane) * 8 < D;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = (i * 64 + lane) * 8;
-    if (c >= D) continue;
-    float o[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = to_f(in[i][e]);
-    if (a.w) {
-      // RMSNorm rounds to the storage dtype before the weight multiply (FB/wan_video_dit.py:166-167).
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = to_f(to_bf(to_f(to_bf(o[e] * rs)) * to_f(wv[i][e])));
+      for (int e = 0; e < 8; ++e) { const float f = ok ? to_f(in[k][i][e]) : 0.f; q += f * f; }
     }
-    if constexpr (TAB != 0) {
+    const float rs = a.w ? rsqrtf(wave_sum(q) / (float)D + a.eps) : 1.0f;
+    bf16* yr = a.y + (r0 + k) * a.yrs;
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        float cc, ss;
-        if constexpr (TAB == 1) {
-          cc = t0[i][p];
-          ss = t1[i][p];
-        } else {
-          cc = p < 2 ? t0[i][2 * p] : t1[i][2 * p - 4];
-          ss = p < 2 ? t0[i][2 * p + 1] : t1[i][2 * p - 3];
-        }
-        const float x0 = o[2 * p], x1 = o[2 * p + 1];
-        o[2 * p] = x0 * cc - x1 * ss;
-        o[2 * p + 1] = x0 * ss + x1 * cc;
+    for (int i = 0; i < NV; ++i) {
+      const int c = (i * 64 + lane) * 8;
+      if (c >= D) continue;
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = to_f(in[k][i][e]);
+      if (a.w) {
+        // RMSNorm rounds to the storage dtype before the weight multiply (FB/wan_video_dit.py:166-167).
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = to_f(to_bf(to_f(to_bf(o[e] * rs)) * to_f(wv[i][e])));
       }
-    }
-    bf16x8 out;
+      if constexpr (TAB != 0) {
+        const int ti = TSH ? 0 : i;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = to_bf(o[e]);
-    store8(yr + c, out);
+        for (int p = 0; p < 4; ++p) {
+          float cc, ss;
+          if constexpr (TAB == 1) {
+            cc = t0[k][ti][p];
+            ss = t1[k][ti][p];
+          } else {
+            cc = p < 2 ? t0[k][ti][2 * p] : t1[k][ti][2 * p - 4];
+            ss = p < 2 ? t0[k][ti][2 * p + 1] : t1[k][ti][2 * p - 3];
+          }
+          const float x0 = o[2 * p], x1 = o[2 * p + 1];
+          o[2 * p] = x0 * cc - x1 * ss;
+          o[2 * p + 1] = x0 * ss + x1 * cc;
+        }
+      }
+      bf16x8 out;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = to_bf(o[e]);
+      store8(yr + c, out);
+    }
   }
 }
 
@@ -370,17 +380,25 @@ extern "C" int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, in
   else if (tab_elem_stride == 2 && sin_tab == cos_tab + 1 && tab_row_stride % 4 == 0 && al16(cos_tab)) tab = 2;
   if (nv != 0 && tab != 3 && dim <= (int64_t)1 << 30) {
     const bool tsh = 512 % a.hd == 0;
-#define FAM_RR_VEC(NV)                                                                                          \
-  switch (tab) {                                                                                                \
-    case 0: FAM_LAUNCH((rmsnorm_rope_vec_kernel<NV, 0, false>), grid, block, 0, s, a); break;                   \
-    case 1:                                                                                                     \
-      if (tsh) FAM_LAUNCH((rmsnorm_rope_vec_kernel<NV, 1, true>), grid, block, 0, s, a);                        \
-      else FAM_LAUNCH((rmsnorm_rope_vec_kernel<NV, 1, false>), grid, block, 0, s, a);                           \
-      break;                                                                                                    \
-    default:                                                                                                    \
-      if (tsh) FAM_LAUNCH((rmsnorm_rope_vec_kernel<NV, 2, true>), grid, block, 0, s, a);                        \
-      else FAM_LAUNCH((rmsnorm_rope_vec_kernel<NV, 2, false>), grid, block, 0, s, a);                           \
-      break;                                                                                                    \
+    // two rows per wave once there are enough rows to fill the machine with half the waves
+    const bool two = rows >= 4096 && nv <= 6;
+    const dim3 grid2((unsigned)((rows + 7) / 8));
+#define FAM_RR_VEC2(NV, TAB, TSH)                                                                          \
+  do {                                                                                                     \
+    if (two) FAM_LAUNCH((rmsnorm_rope_vec_kernel<NV, TAB, TSH, 2>), grid2, block, 0, s, a);                \
+    else FAM_LAUNCH((rmsnorm_rope_vec_kernel<NV, TAB, TSH, 1>), grid, block, 0, s, a);                     \
+  } while (0)
+#define FAM_RR_VEC(NV)                                      \
+  switch (tab) {                                            \
+    case 0: FAM_RR_VEC2(NV, 0, false); break;               \
+    case 1:                                                 \
+      if (tsh) FAM_RR_VEC2(NV, 1, true);                    \
+      else FAM_RR_VEC2(NV, 1, false);                       \
+      break;                                                \
+    default:                                                \
+      if (tsh) FAM_RR_VEC2(NV, 2, true);                    \
+      else FAM_RR_VEC2(NV, 2, false);                       \
+      break;                                                \
   }
     switch (nv) {
       case 1: FAM_RR_VEC(1); break;
@@ -390,6 +408,7 @@ extern "C" int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, in
       default: FAM_RR_VEC(8); break;
     }
 #undef FAM_RR_VEC
+#undef FAM_RR_VEC2
     return fam_host::check_launch("fam_rmsnorm_rope");
   }
   switch (nv) {

@@ -96,6 +96,23 @@ def test_rope(B, S, H, Dh, layout):
     assert relerr(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("layout", ["complex", "interleaved"])
+def test_rms_norm_rope_many_rows(layout):
+    """4099 rows (two rows per wave, odd tail) of a 3-D-style per-row table, with the weight."""
+    B, S, H, Dh = 1, 4099, 8, 64
+    x = rnd(B, S, H * Dh, seed=73, scale=2.0)
+    w = rnd(H * Dh, seed=74, scale=0.2) + 1
+    ang = torch.rand(S, 1, Dh // 2, generator=torch.Generator().manual_seed(75), dtype=torch.float64) * 6.0
+    fr = torch.polar(torch.ones_like(ang), ang)
+    ref = O.rope_apply(O.rms_norm(x.float(), w.float(), 1e-6), fr, H)
+    if layout == "complex":
+        y = ops().rms_norm_rope(dev(x), dev(w), 1e-6, fr, H)
+    else:
+        inter = dev(torch.view_as_real(fr).reshape(S, 1, Dh).double())
+        y = ops().rms_norm_rope(dev(x), dev(w), 1e-6, inter, H, layout="interleaved")
+    assert relerr(y, ref) <= TOL
+
+
 def test_rope_scalar_table_path():
     """Tables whose rows are not 16-byte multiples take the per-element table reads."""
     from fam import _capi
