@@ -963,9 +963,10 @@ static void launch_final_steps(const FinalArgs& a, int steps, hipStream_t s) {
 
 template <int MT>
 static void launch_final(const FinalArgs& a, hipStream_t s) {
-  // K <= 1024: 4 waves; <= 2048: 8 waves; <= 4096: 16 waves; k-steps per wave 1, 2, 4 or 8
+  // K <= 256: 4 waves; <= 1024: 8 waves; longer: 16 waves; k-steps per wave 1, 2, 4 or 8
+  // (more waves per workgroup shorten each wave's load issue, the critical path at M <= 64)
   const int64_t ksteps = (a.K + 31) / 32;
-  const int nw = ksteps <= 32 ? 4 : (ksteps <= 64 ? 8 : 16);
+  const int nw = ksteps <= 8 ? 4 : (ksteps <= 32 ? 8 : 16);
   int steps = 1;
   while (steps * nw < ksteps) steps <<= 1;
   if (nw == 4) launch_final_steps<MT, 4>(a, steps, s);
