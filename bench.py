@@ -56,10 +56,11 @@ def parse():
     ap.add_argument("--no-eager", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--cpu-sample-s", type=float, default=20.0, help="CPU baseline time budget")
-    ap.add_argument("--workload", choices=["c1", "c2", "c3", "hbm"], default="c1",
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "hbm"], default="c1",
                     help="c1: the action-DiT denoise loop (the metric); c2: one long-sequence video DiT block "
                          "(config 2 shape), reported as ms per 30-block forward with MFMA utilisation; c3: the "
-                         "compact expert loop + action-VAE decoder at B=1 and B=256; hbm: size sweep of the "
+                         "compact expert loop + action-VAE decoder at B=1 and B=256; c4: the DiT4DiT flow-matching "
+                         "head (DiT-B, 16 blocks, 4 steps) over 2048 VLM tokens; hbm: size sweep of the "
                          "HBM-bound kernels (AdaLN, RMSNorm+RoPE, Euler) from config 2 / config 3 B=256 shapes up")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -389,6 +390,48 @@ def bench_c2(args):
     print(json.dumps(out), flush=True)
 
 
+# --------------------------------------------------------------------------- config 4: DiT4DiT head
+def bench_c4(args):
+    """The DiT4DiT flow-matching action head (FlowmatchingActionHead.predict_action, state=None):
+    DiT-B (12 x 64 heads), 16 interleaved cross/self blocks, 4 Euler steps, 16 x 32 action chunk,
+    cross-attending to 2048 VLM tokens of width 2048 (config 4's backbone length), B=1, one
+    captured graph per call."""
+    import torch
+    from fam.dit4dit import DiT4DiTHeadConfig, FusedDiT4DiTHead, synthetic_params
+    cfg = DiT4DiTHeadConfig()
+    L = 2048
+    dev = torch.device("cuda:0")
+    params = {k: v.to(torch.bfloat16) for k, v in synthetic_params(cfg, 4321).items()}
+    head = FusedDiT4DiTHead(cfg, params, batch=1, vl_len=L, device=dev)
+    g = torch.Generator("cpu").manual_seed(1234)
+    vl = torch.randn(1, L, cfg.cross_dim, generator=g).to(dev, torch.bfloat16)
+    noise = torch.randn(1, cfg.horizon, cfg.action_dim, generator=g).to(dev, torch.bfloat16)
+    head.set_inputs(noise, vl)
+    head.run()
+    torch.cuda.synchronize()
+    head.capture()
+    for _ in range(args.warmup):
+        head.run()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        head.run()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    p50 = statistics.median(times)
+    out = {
+        "metric": "p50 ms per DiT4DiT head call (4-step denoise loop, bs=1)", "value": round(p50, 4), "unit": "ms",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(p50, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) VLM features and noise, N(0,0.02) weights",
+        "config": {"workload": "config4 DiT4DiT flow-matching head: DiT-B (12x64), 16 interleaved cross/self blocks, "
+                               "4 Euler steps, 16x32 actions, 2048 VLM tokens x 2048", "batch": 1, "vl_tokens": L},
+        "min_ms": round(min(times), 4), "p90_ms": round(sorted(times)[int(0.9 * (len(times) - 1))], 4),
+    }
+    print(json.dumps(out), flush=True)
+
+
 # --------------------------------------------------------------------------- HBM-bound kernels, size sweep
 def bench_hbm(args):
     """Achieved HBM bandwidth of the norm, RoPE and Euler kernels against rows / elements: the
@@ -549,6 +592,9 @@ def main():
         return
     if args.workload == "hbm":
         bench_hbm(args)
+        return
+    if args.workload == "c4":
+        bench_c4(args)
         return
     if args.workload == "c3":
         bench_c3(args)

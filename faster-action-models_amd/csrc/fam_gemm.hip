@@ -57,6 +57,7 @@ struct GemmArgs {
 __device__ __forceinline__ float apply_act(float v, int act) {
   if (act == FAM_ACT_GELU_TANH) return gelu_tanh(v);
   if (act == FAM_ACT_SILU) return silu(v);
+  if (act == FAM_ACT_RELU) return fmaxf(v, 0.f);
   return v;
 }
 
@@ -402,6 +403,7 @@ __global__ __launch_bounds__(NW * 64) void final_kernel(FinalArgs g) {
       float x = v[e] + bias[e];
       if (g.act == FAM_ACT_GELU_TANH) x = gelu_tanh(x);
       else if (g.act == FAM_ACT_SILU) x = silu(x);
+      else if (g.act == FAM_ACT_RELU) x = fmaxf(x, 0.f);
       o[e] = to_bf(x);
       const float r = to_f(o[e]);
       ss += (nc + e < g.N) ? r * r : 0.f;
@@ -724,6 +726,9 @@ __global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int t
       } else if (g.act == FAM_ACT_SILU) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = v[e] / (1.0f + __expf(-v[e]));
+      } else if (g.act == FAM_ACT_RELU) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = fmaxf(v[e], 0.f);
       }
       if (g.res) {
         float gt[4] = {1.f, 1.f, 1.f, 1.f}, rv[4];
@@ -850,7 +855,7 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
               "fam_gemm: a and w must be 16-byte aligned");
   FAM_REQUIRE(d->prologue >= FAM_PRO_NONE && d->prologue <= FAM_PRO_ADALN, FAM_ERR_INVALID_ARG,
               "fam_gemm: unknown prologue %d", d->prologue);
-  FAM_REQUIRE(d->act >= FAM_ACT_NONE && d->act <= FAM_ACT_SILU, FAM_ERR_INVALID_ARG, "fam_gemm: unknown act %d", d->act);
+  FAM_REQUIRE(d->act >= FAM_ACT_NONE && d->act <= FAM_ACT_RELU, FAM_ERR_INVALID_ARG, "fam_gemm: unknown act %d", d->act);
   if (d->prologue == FAM_PRO_LAYERNORM) {
     FAM_REQUIRE((!d->pro_w || fam_host::aligned16(d->pro_w)) && (!d->pro_b || fam_host::aligned16(d->pro_b)),
                 FAM_ERR_INVALID_ARG, "fam_gemm: LayerNorm affine must be 16-byte aligned");
@@ -984,7 +989,7 @@ extern "C" int fam_gemm_final(const void* a, int64_t lda, const void* w, int64_t
               "fam_gemm_final: lda/ldw must be >= K and multiples of 8, ldo >= N");
   FAM_REQUIRE(fam_host::aligned16(a) && fam_host::aligned16(w) && (reinterpret_cast<uintptr_t>(out) & 7u) == 0,
               FAM_ERR_INVALID_ARG, "fam_gemm_final: a, w 16-byte and out 8-byte aligned");
-  FAM_REQUIRE(act >= FAM_ACT_NONE && act <= FAM_ACT_SILU, FAM_ERR_INVALID_ARG, "fam_gemm_final: unknown act %d", act);
+  FAM_REQUIRE(act >= FAM_ACT_NONE && act <= FAM_ACT_RELU, FAM_ERR_INVALID_ARG, "fam_gemm_final: unknown act %d", act);
   FAM_REQUIRE((N + 15) / 16 <= 2147483647LL, FAM_ERR_UNSUPPORTED, "fam_gemm_final: N too large");
   if (M == 0) return FAM_OK;
   FinalArgs fa{(const bf16*)a, lda, (const bf16*)w, ldw, (const bf16*)bias, act, (bf16*)out, ldo, sumsq, M, N, K};

@@ -177,6 +177,7 @@ int fam_attention_combine(const fam_attn_desc* d, void* stream);
 #define FAM_ACT_NONE 0
 #define FAM_ACT_GELU_TANH 1
 #define FAM_ACT_SILU 2
+#define FAM_ACT_RELU 3   /* the DiT4DiT head's MLPs: DB/modules/action_model/ActionDiT.py:52-61 */
 
 /*
  * fam_gemm -- out[m, n] = epilogue( sum_k pro(a)[m, k] * w[n, k] + bias[n] ),

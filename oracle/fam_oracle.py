@@ -592,3 +592,180 @@ def cae_decode(p: Params, cfg: CaeDecoderConfig, z: torch.Tensor, suite: Optiona
     elif T < cfg.action_horizon:
         x = F.pad(x, (0, cfg.action_horizon - T))
     return F.linear(x.transpose(1, 2), p["decoder.output_proj.weight"], p["decoder.output_proj.bias"])
+
+
+# ---------------------------------------------------------------------------
+# DiT4DiT flow-matching action head (DB = src/dit4dit-baseline/DiT4DiT/model/modules/action_model)
+# ---------------------------------------------------------------------------
+# The head's transformer (DB/flow_matching_head/cross_attention_dit.py) is built from diffusers
+# modules (Attention, FeedForward, Timesteps, TimestepEmbedding; diffusers 0.37.0.dev0 @3996788
+# per scripts/dit4dit_diffusers_overlay.sh:7,35), which are not installed here.  Their published
+# semantics are restated below; no reference test or fixture pins the composition, so this part
+# of the oracle is "parity unpinned" at the composition level (the closed forms of the two
+# embeddings are pinned in tests/test_oracle.py).
+@dataclass
+class DiT4DiTHeadConfig:
+    """DiT-B head of DB/ActionDiT.py:192-195 with the diffusion_model_cfg of
+    DiT4DiT/config/real_robot/dit4dit_g1.yaml:25-49 (state encoder not used: predict_action's
+    default state=None, DB/ActionDiT.py:321)."""
+    action_dim: int = 32
+    horizon: int = 16            # future_action_window_size + 1
+    heads: int = 12              # DiT-B
+    head_dim: int = 64
+    num_layers: int = 16
+    cross_dim: int = 2048        # VLM feature width
+    output_dim: int = 2560       # DiT proj_out_2 width
+    hidden_size: int = 2560      # action decoder hidden width
+    max_seq_len: int = 1024      # position embedding table
+    num_steps: int = 4           # num_inference_timesteps
+    buckets: int = 1000          # num_timestep_buckets
+    interleave_self_attention: bool = True
+    ff_mult: int = 4             # diffusers FeedForward default inner_dim = 4 * dim
+    norm_eps: float = 1e-5       # AdaLayerNorm / norm3 (cross_attention_dit.py:47-57, 207)
+    out_eps: float = 1e-6        # norm_out (cross_attention_dit.py:253)
+
+    @property
+    def dim(self) -> int:
+        return self.heads * self.head_dim
+
+    def is_cross(self, idx: int) -> bool:
+        """Odd blocks are self-attention when interleaved (cross_attention_dit.py:231-233, 285)."""
+        return not (self.interleave_self_attention and idx % 2 == 1)
+
+
+def d4d_param_shapes(cfg: DiT4DiTHeadConfig) -> Dict[str, Tuple[int, ...]]:
+    """State-dict keys of FlowmatchingActionHead (DB/ActionDiT.py:197-236; diffusers Attention
+    to_q/to_k/to_v/to_out.0, FeedForward net.0.proj / net.2, TimestepEmbedding linear_1/2)."""
+    D, C = cfg.dim, cfg.cross_dim
+    s = {
+        "model.timestep_encoder.timestep_embedder.linear_1.weight": (D, 256),
+        "model.timestep_encoder.timestep_embedder.linear_1.bias": (D,),
+        "model.timestep_encoder.timestep_embedder.linear_2.weight": (D, D),
+        "model.timestep_encoder.timestep_embedder.linear_2.bias": (D,),
+        "model.proj_out_1.weight": (2 * D, D), "model.proj_out_1.bias": (2 * D,),
+        "model.proj_out_2.weight": (cfg.output_dim, D), "model.proj_out_2.bias": (cfg.output_dim,),
+        "action_encoder.layer1.weight": (D, cfg.action_dim), "action_encoder.layer1.bias": (D,),
+        "action_encoder.layer2.weight": (D, 2 * D), "action_encoder.layer2.bias": (D,),
+        "action_encoder.layer3.weight": (D, D), "action_encoder.layer3.bias": (D,),
+        "action_decoder.layer1.weight": (cfg.hidden_size, cfg.output_dim), "action_decoder.layer1.bias": (cfg.hidden_size,),
+        "action_decoder.layer2.weight": (cfg.action_dim, cfg.hidden_size), "action_decoder.layer2.bias": (cfg.action_dim,),
+        "position_embedding.weight": (cfg.max_seq_len, D),
+    }
+    for i in range(cfg.num_layers):
+        b = f"model.transformer_blocks.{i}."
+        kv_in = C if cfg.is_cross(i) else D
+        s.update({
+            b + "norm1.linear.weight": (2 * D, D), b + "norm1.linear.bias": (2 * D,),
+            b + "attn1.to_q.weight": (D, D), b + "attn1.to_q.bias": (D,),
+            b + "attn1.to_k.weight": (D, kv_in), b + "attn1.to_k.bias": (D,),
+            b + "attn1.to_v.weight": (D, kv_in), b + "attn1.to_v.bias": (D,),
+            b + "attn1.to_out.0.weight": (D, D), b + "attn1.to_out.0.bias": (D,),
+            b + "ff.net.0.proj.weight": (cfg.ff_mult * D, D), b + "ff.net.0.proj.bias": (cfg.ff_mult * D,),
+            b + "ff.net.2.weight": (D, cfg.ff_mult * D), b + "ff.net.2.bias": (D,),
+        })
+    return s
+
+
+def init_d4d_params(cfg: DiT4DiTHeadConfig, seed: int, std: float = 0.02) -> Params:
+    """Synthetic weights, N(0, std) for every tensor (sorted-name draws), fp32."""
+    g = torch.Generator().manual_seed(seed)
+    return {k: torch.randn(v, generator=g) * std for k, v in sorted(d4d_param_shapes(cfg).items())}
+
+
+def d4d_tau_encoding(timesteps: torch.Tensor, dim: int) -> torch.Tensor:
+    """SinusoidalPositionalEncoding (DB/flow_matching_head/action_encoder.py:21-37):
+    cat(sin(t f), cos(t f)), f_i = exp(-i ln(10000) / (dim/2)), fp32.  timesteps [..]."""
+    half = dim // 2
+    f = torch.exp(-torch.arange(half, dtype=torch.float32) * (math.log(10000.0) / half))
+    a = timesteps.float().unsqueeze(-1) * f
+    return torch.cat([torch.sin(a), torch.cos(a)], dim=-1)
+
+
+def d4d_timestep_proj(timesteps: torch.Tensor, channels: int = 256) -> torch.Tensor:
+    """diffusers Timesteps(num_channels=256, flip_sin_to_cos=True, downscale_freq_shift=1) as used
+    at DB/flow_matching_head/cross_attention_dit.py:34 (diffusers get_timestep_embedding):
+    f_i = exp(-ln(10000) i / (half - 1)), emb = cat(cos(t f), sin(t f)), fp32.  timesteps [B]."""
+    half = channels // 2
+    f = torch.exp(-math.log(10000.0) * torch.arange(half, dtype=torch.float32) / (half - 1))
+    a = timesteps.float()[:, None] * f[None, :]
+    return torch.cat([torch.cos(a), torch.sin(a)], dim=-1)
+
+
+def d4d_temb(p: Params, timesteps: torch.Tensor, dtype) -> torch.Tensor:
+    """TimestepEncoder (cross_attention_dit.py:31-41): TimestepEmbedding(linear_1, SiLU, linear_2)
+    of the projection cast to the parameter dtype.  [B] -> [B, D]."""
+    pre = "model.timestep_encoder.timestep_embedder."
+    h = d4d_timestep_proj(timesteps).to(dtype)
+    h = F.silu(F.linear(h, p[pre + "linear_1.weight"], p[pre + "linear_1.bias"]))
+    return F.linear(h, p[pre + "linear_2.weight"], p[pre + "linear_2.bias"])
+
+
+def d4d_action_encoder(p: Params, actions: torch.Tensor, timesteps: torch.Tensor) -> torch.Tensor:
+    """ActionEncoder.forward (DB/ActionDiT.py:74-98): layer1(actions); tau = sinusoid(t) cast to
+    that dtype; swish(layer2(cat(a, tau))); layer3.  actions [B, T, A], timesteps [B]."""
+    B, T, _ = actions.shape
+    a = F.linear(actions, p["action_encoder.layer1.weight"], p["action_encoder.layer1.bias"])
+    tau = d4d_tau_encoding(timesteps[:, None].expand(B, T), a.shape[-1]).to(a.dtype)
+    x = F.linear(torch.cat([a, tau], dim=-1), p["action_encoder.layer2.weight"], p["action_encoder.layer2.bias"])
+    x = x * torch.sigmoid(x)
+    return F.linear(x, p["action_encoder.layer3.weight"], p["action_encoder.layer3.bias"])
+
+
+def d4d_block(p: Params, cfg: DiT4DiTHeadConfig, idx: int, x: torch.Tensor, ctx: torch.Tensor,
+              temb: torch.Tensor) -> torch.Tensor:
+    """BasicTransformerBlock.forward with norm_type 'ada_norm', no positional embedding
+    (cross_attention_dit.py:150-187):
+      AdaLayerNorm (:59-67): (scale, shift) = chunk(Linear(SiLU(temb)), 2); LN(x)(1 + scale) + shift
+      diffusers Attention: q = to_q(h), k = to_k(c), v = to_v(c) with c = ctx (cross) or h (self),
+        SDPA with scale 1/sqrt(head_dim), to_out.0 (dropout inactive at inference)
+      x = attn + x;  norm3 = LN(no affine);  FeedForward 'gelu-approximate': net.2(GELU_tanh(net.0.proj(h)))
+      x = ff + x."""
+    b = f"model.transformer_blocks.{idx}."
+    mod = F.linear(F.silu(temb), p[b + "norm1.linear.weight"], p[b + "norm1.linear.bias"])
+    scale, shift = mod.chunk(2, dim=1)
+    D = cfg.dim
+    h = F.layer_norm(x, (D,), eps=cfg.norm_eps) * (1 + scale[:, None]) + shift[:, None]
+    c = ctx if cfg.is_cross(idx) else h
+    q = F.linear(h, p[b + "attn1.to_q.weight"], p[b + "attn1.to_q.bias"])
+    k = F.linear(c, p[b + "attn1.to_k.weight"], p[b + "attn1.to_k.bias"])
+    v = F.linear(c, p[b + "attn1.to_v.weight"], p[b + "attn1.to_v.bias"])
+    o = flash_attention(q, k, v, cfg.heads)
+    x = F.linear(o, p[b + "attn1.to_out.0.weight"], p[b + "attn1.to_out.0.bias"]) + x
+    h = F.layer_norm(x, (D,), eps=cfg.norm_eps)
+    h = gelu_tanh(F.linear(h, p[b + "ff.net.0.proj.weight"], p[b + "ff.net.0.proj.bias"]))
+    return F.linear(h, p[b + "ff.net.2.weight"], p[b + "ff.net.2.bias"]) + x
+
+
+def d4d_dit_forward(p: Params, cfg: DiT4DiTHeadConfig, x: torch.Tensor, ctx: torch.Tensor,
+                    timesteps: torch.Tensor) -> torch.Tensor:
+    """DiT.forward (cross_attention_dit.py:264-308): blocks, then (shift, scale) =
+    chunk(proj_out_1(SiLU(temb)), 2), LN_1e-6(x)(1 + scale) + shift, proj_out_2."""
+    temb = d4d_temb(p, timesteps, x.dtype)
+    for i in range(cfg.num_layers):
+        x = d4d_block(p, cfg, i, x, ctx, temb)
+    shift, scale = F.linear(F.silu(temb), p["model.proj_out_1.weight"], p["model.proj_out_1.bias"]).chunk(2, dim=1)
+    x = F.layer_norm(x, (cfg.dim,), eps=cfg.out_eps) * (1 + scale[:, None]) + shift[:, None]
+    return F.linear(x, p["model.proj_out_2.weight"], p["model.proj_out_2.bias"])
+
+
+def d4d_timesteps(cfg: DiT4DiTHeadConfig) -> List[int]:
+    """Discrete timesteps of predict_action: int((1 - i/N) * buckets) (DB/ActionDiT.py:339-341)."""
+    return [int((1.0 - i / float(cfg.num_steps)) * cfg.buckets) for i in range(cfg.num_steps)]
+
+
+def d4d_predict_action(p: Params, cfg: DiT4DiTHeadConfig, vl_embs: torch.Tensor, noise: torch.Tensor) -> torch.Tensor:
+    """FlowmatchingActionHead.predict_action with state=None (DB/ActionDiT.py:321-369): per step,
+    encode (actions, t), add position embeddings, DiT, action decoder MLP (layer2(ReLU(layer1))),
+    actions = actions - dt * velocity[:, -horizon:] (dt = 1/N)."""
+    B, T, _ = noise.shape
+    actions = noise
+    dt = 1.0 / cfg.num_steps
+    pos = p["position_embedding.weight"][:T].unsqueeze(0)
+    for t_disc in d4d_timesteps(cfg):
+        ts = torch.full((B,), t_disc, dtype=torch.long)
+        feats = d4d_action_encoder(p, actions, ts) + pos
+        out = d4d_dit_forward(p, cfg, feats, vl_embs, ts)
+        pred = F.linear(F.relu(F.linear(out, p["action_decoder.layer1.weight"], p["action_decoder.layer1.bias"])),
+                        p["action_decoder.layer2.weight"], p["action_decoder.layer2.bias"])
+        actions = actions - dt * pred[:, -cfg.horizon:]
+    return actions

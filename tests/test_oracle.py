@@ -298,3 +298,59 @@ def test_cae_decoder_detects_planted_mistake(cae_golden):
     y = O.cae_decode(q, cfg, cae_golden["base.z"])
     assert (y - cae_golden["base.out"]).abs().max() > 1e-2
     assert O.cae_strides(4) == [4] and O.cae_strides(8) == [4, 2] and O.cae_strides(12) == [4, 3]
+
+
+# --------------------------------------------------------------------------- DiT4DiT head
+def test_d4d_embeddings_closed_forms():
+    """The two sinusoidal embeddings of the DiT4DiT head (action_encoder.py:21-37, diffusers
+    Timesteps as configured at cross_attention_dit.py:34) at closed-form points."""
+    D = 768
+    t = torch.tensor([0.0, 750.0])
+    tau = O.d4d_tau_encoding(t, D)
+    assert tau.shape == (2, D)
+    assert torch.equal(tau[0, :D // 2], torch.zeros(D // 2)) and torch.equal(tau[0, D // 2:], torch.ones(D // 2))
+    # first frequency is 1, last is 10000^(-(half-1)/half); (sin, cos) order
+    assert math.isclose(tau[1, 0].item(), math.sin(750.0), abs_tol=1e-5)
+    assert math.isclose(tau[1, D // 2].item(), math.cos(750.0), abs_tol=1e-5)
+    fl = 10000.0 ** (-(D // 2 - 1) / (D // 2))
+    assert math.isclose(tau[1, D // 2 - 1].item(), math.sin(750.0 * fl), abs_tol=1e-6)
+    assert torch.allclose(tau[1, :D // 2] ** 2 + tau[1, D // 2:] ** 2, torch.ones(D // 2), atol=1e-6)
+    pr = O.d4d_timestep_proj(torch.tensor([0, 250]), 256)
+    assert pr.shape == (2, 256)
+    assert torch.equal(pr[0, :128], torch.ones(128)) and torch.equal(pr[0, 128:], torch.zeros(128))
+    # flip_sin_to_cos: cos first; downscale_freq_shift = 1 makes the last frequency exactly 1/10000
+    assert math.isclose(pr[1, 0].item(), math.cos(250.0), abs_tol=1e-5)
+    assert math.isclose(pr[1, 128].item(), math.sin(250.0), abs_tol=1e-5)
+    assert math.isclose(pr[1, 127].item(), math.cos(0.025), abs_tol=1e-7)
+    assert math.isclose(pr[1, 255].item(), math.sin(0.025), abs_tol=1e-7)
+
+
+def test_d4d_schedule_and_block_structure():
+    """Timesteps 1000, 750, 500, 250 and dt = 0.25 (SURVEY's DiT4DiT known answer); interleaved
+    blocks (odd = self attention); a block with zero AdaLN / attention / FFN weights is the
+    identity on the residual stream, and a head whose decoder outputs zero leaves the noise."""
+    cfg = O.DiT4DiTHeadConfig(num_layers=4, heads=2, head_dim=16, cross_dim=24, output_dim=40, hidden_size=40,
+                              action_dim=5, horizon=6)
+    assert O.d4d_timesteps(O.DiT4DiTHeadConfig()) == [1000, 750, 500, 250]
+    assert [cfg.is_cross(i) for i in range(4)] == [True, False, True, False]
+    p = O.init_d4d_params(cfg, 3)
+    x, ctx = torch.randn(2, 6, cfg.dim), torch.randn(2, 9, cfg.cross_dim)
+    temb = torch.randn(2, cfg.dim)
+    z = dict(p)
+    b = "model.transformer_blocks.1."
+    for n in ("attn1.to_out.0.weight", "attn1.to_out.0.bias", "ff.net.2.weight", "ff.net.2.bias"):
+        z[b + n] = torch.zeros_like(p[b + n])
+    assert torch.equal(O.d4d_block(z, cfg, 1, x, ctx, temb), x)
+    # cross blocks read the context, self blocks do not
+    y1 = O.d4d_block(p, cfg, 0, x, ctx, temb)
+    assert not torch.equal(y1, O.d4d_block(p, cfg, 0, x, ctx * 2, temb))
+    assert torch.equal(O.d4d_block(p, cfg, 1, x, ctx, temb), O.d4d_block(p, cfg, 1, x, ctx * 2, temb))
+    zd = dict(p)
+    zd["action_decoder.layer2.weight"] = torch.zeros_like(p["action_decoder.layer2.weight"])
+    zd["action_decoder.layer2.bias"] = torch.zeros_like(p["action_decoder.layer2.bias"])
+    noise = torch.randn(2, 6, 5)
+    assert torch.equal(O.d4d_predict_action(zd, cfg, ctx, noise), noise)
+    # with a constant velocity c the N Euler steps move the noise by exactly -c
+    zc = dict(zd)
+    zc["action_decoder.layer2.bias"] = torch.full_like(p["action_decoder.layer2.bias"], 0.5)
+    assert torch.allclose(O.d4d_predict_action(zc, cfg, ctx, noise), noise - 0.5, atol=1e-6)
