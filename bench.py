@@ -392,10 +392,10 @@ def bench_c2(args):
 
 # --------------------------------------------------------------------------- config 4: DiT4DiT head
 def bench_c4(args):
-    """The DiT4DiT flow-matching action head (FlowmatchingActionHead.predict_action, state=None):
-    DiT-B (12 x 64 heads), 16 interleaved cross/self blocks, 4 Euler steps, 16 x 32 action chunk,
-    cross-attending to 2048 VLM tokens of width 2048 (config 4's backbone length), B=1, one
-    captured graph per call."""
+    """The DiT4DiT flow-matching action head (FlowmatchingActionHead.predict_action with one
+    64-wide state token, as the eval clients call it): DiT-B (12 x 64 heads), 16 interleaved
+    cross/self blocks over 17 tokens, 4 Euler steps, 16 x 32 action chunk, cross-attending to
+    2048 VLM tokens of width 2048 (config 4's backbone length), B=1, one captured graph per call."""
     import torch
     from fam.dit4dit import DiT4DiTHeadConfig, FusedDiT4DiTHead, synthetic_params
     cfg = DiT4DiTHeadConfig()
@@ -406,7 +406,8 @@ def bench_c4(args):
     g = torch.Generator("cpu").manual_seed(1234)
     vl = torch.randn(1, L, cfg.cross_dim, generator=g).to(dev, torch.bfloat16)
     noise = torch.randn(1, cfg.horizon, cfg.action_dim, generator=g).to(dev, torch.bfloat16)
-    head.set_inputs(noise, vl)
+    state = torch.randn(1, 1, cfg.state_dim, generator=g).to(dev, torch.bfloat16)
+    head.set_inputs(noise, vl, state)
     head.run()
     torch.cuda.synchronize()
     head.capture()
@@ -426,7 +427,7 @@ def bench_c4(args):
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: seeded N(0,1) VLM features and noise, N(0,0.02) weights",
         "config": {"workload": "config4 DiT4DiT flow-matching head: DiT-B (12x64), 16 interleaved cross/self blocks, "
-                               "4 Euler steps, 16x32 actions, 2048 VLM tokens x 2048", "batch": 1, "vl_tokens": L},
+                               "4 Euler steps, 16x32 actions + 1 state token, 2048 VLM tokens x 2048", "batch": 1, "vl_tokens": L},
         "min_ms": round(min(times), 4), "p90_ms": round(sorted(times)[int(0.9 * (len(times) - 1))], 4),
     }
     print(json.dumps(out), flush=True)

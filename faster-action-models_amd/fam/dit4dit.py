@@ -53,6 +53,7 @@ class DiT4DiTHeadConfig:
     ff_mult: int = 4
     norm_eps: float = 1e-5
     out_eps: float = 1e-6
+    state_dim: int = 64      # state_encoder input (dit4dit_g1.yaml:31; LIBERO 16); 0: none
 
 
 def param_shapes(cfg) -> Dict[str, Tuple[int, ...]]:
@@ -74,6 +75,10 @@ def param_shapes(cfg) -> Dict[str, Tuple[int, ...]]:
         "action_decoder.layer2.weight": (cfg.action_dim, cfg.hidden_size), "action_decoder.layer2.bias": (cfg.action_dim,),
         "position_embedding.weight": (cfg.max_seq_len, D),
     }
+    if cfg.state_dim:
+        s.update({"state_encoder.layer1.weight": (cfg.hidden_size, cfg.state_dim),
+                  "state_encoder.layer1.bias": (cfg.hidden_size,),
+                  "state_encoder.layer2.weight": (D, cfg.hidden_size), "state_encoder.layer2.bias": (D,)})
     for i in range(cfg.num_layers):
         b = f"model.transformer_blocks.{i}."
         kv_in = D if (cfg.interleave_self_attention and i % 2 == 1) else cfg.cross_dim
@@ -114,23 +119,41 @@ def _timestep_proj(t: float, channels: int = 256) -> torch.Tensor:
 
 
 class FusedDiT4DiTHead:
-    """predict_action of the DiT4DiT head for `batch` action chunks and `vl_len` VLM tokens.
+    """predict_action of the DiT4DiT head for `batch` action chunks, `vl_len` VLM tokens and
+    `state_len` state tokens per chunk (0: the state=None call).
+
+    Rows are token-major: sequence position j of chunk b is row j * batch + b, with the state
+    tokens first (DB/ActionDiT.py:355-356), so the action rows of all chunks are one contiguous
+    [horizon * batch, D] block for the encoder, the output projection and the decoder.  The
+    actions buffer is [horizon, batch, action_dim] for the same reason; `set_inputs` and
+    `predict_action` take and return the reference's [batch, horizon, action_dim].
 
     Args:
         cfg: DiT4DiTHeadConfig (or any object with its fields).
         params: state dict in the reference's key layout (FlowmatchingActionHead), any float
             dtype; converted to bf16 on `device`.
+        state_len: state tokens per chunk (the reference's state is [B, 1, state_dim]);
+            default 1 when cfg.state_dim > 0.
     """
 
     def __init__(self, cfg, params: Dict[str, torch.Tensor], *, batch: int, vl_len: int,
-                 device: torch.device, attn_splits: Optional[int] = None):
+                 device: torch.device, attn_splits: Optional[int] = None, state_len: Optional[int] = None):
         self.cfg, self.B, self.L, self.device = cfg, batch, vl_len, device
         D, T, A = cfg.heads * cfg.head_dim, cfg.horizon, cfg.action_dim
-        self.D, self.T, self.M = D, T, batch * T
+        Ls = (1 if cfg.state_dim else 0) if state_len is None else state_len
+        if Ls and not cfg.state_dim:
+            raise ValueError("DiT4DiT head: state tokens need a state encoder (cfg.state_dim > 0)")
+        self.D, self.T, self.Ls = D, T, Ls
+        self.Sq = Ls + T                       # sequence length of the head DiT
+        self.M, self.R = batch * T, batch * self.Sq   # action rows, all rows
         if D % 8 or cfg.cross_dim % 8 or cfg.output_dim % 8 or cfg.hidden_size % 8:
             raise ValueError("DiT4DiT head: feature widths must be multiples of 8")
+        if Ls and cfg.state_dim % 8:
+            raise ValueError("DiT4DiT head: state_dim must be a multiple of 8")
         if A > 64:
             raise ValueError("DiT4DiT head: action_dim must be <= 64")
+        if self.Sq > 32:
+            raise ValueError("DiT4DiT head: state_len + horizon must be <= 32")
         p = {k: v.to(device=device, dtype=_BF16).contiguous() for k, v in params.items()}
         self.p = p
         nb = cfg.num_layers
@@ -169,19 +192,24 @@ class FusedDiT4DiTHead:
         self.x2 = torch.empty(S, M, 2 * D, dtype=_BF16, device=device)
         for s, t in enumerate(self.t_disc):
             self.x2[s, :, D:] = _tau_rows(float(t), D).to(device=device, dtype=_BF16)
-        self.posx = p["position_embedding.weight"][:T].repeat(batch, 1).contiguous()   # [M, D]
-        # ---- activations
-        self.actions = torch.empty(batch, T, A, dtype=_BF16, device=device)
+        self.posx = p["position_embedding.weight"][:T].repeat_interleave(batch, dim=0).contiguous()   # [M, D]
+        # ---- activations (token-major rows)
+        R = self.R
+        self.actions = torch.empty(T, batch, A, dtype=_BF16, device=device)
         self.vl_in = torch.empty(batch, vl_len, cfg.cross_dim, dtype=_BF16, device=device)
         self.ctxkv = torch.empty(batch * vl_len, len(cross) * 2 * D, dtype=_BF16, device=device)
-        self.h = torch.empty(M, D, dtype=_BF16, device=device)
+        if Ls:
+            self.st_in = torch.empty(Ls, batch, cfg.state_dim, dtype=_BF16, device=device)
+            self.st_hid = torch.empty(Ls * batch, cfg.hidden_size, dtype=_BF16, device=device)
+            self.st_feat = torch.empty(Ls * batch, D, dtype=_BF16, device=device)
+        self.h = torch.empty(R, D, dtype=_BF16, device=device)
         self.e = torch.empty(M, D, dtype=_BF16, device=device)
-        self.qkv = torch.empty(M, 3 * D, dtype=_BF16, device=device)
-        self.attn = torch.empty(batch, T, D, dtype=_BF16, device=device)
-        self.up = torch.empty(M, cfg.ff_mult * D, dtype=_BF16, device=device)
+        self.qkv = torch.empty(R, 3 * D, dtype=_BF16, device=device)
+        self.attn = torch.empty(R, D, dtype=_BF16, device=device)
+        self.up = torch.empty(R, cfg.ff_mult * D, dtype=_BF16, device=device)
         self.y = torch.empty(M, cfg.output_dim, dtype=_BF16, device=device)
         self.z = torch.empty(M, cfg.hidden_size, dtype=_BF16, device=device)
-        self.vel = torch.empty(batch, T, A, dtype=_BF16, device=device)
+        self.vel = torch.empty(T, batch, A, dtype=_BF16, device=device)
         self.delta = torch.tensor(-self.dt, dtype=_BF16, device=device)
         self.splits = attn_splits if attn_splits is not None else max(1, min(16, (vl_len + 127) // 128))
         self.graph: Optional[torch.cuda.CUDAGraph] = None
@@ -193,11 +221,21 @@ class FusedDiT4DiTHead:
         return row[D:], row[:D]   # shift, scale
 
     def _enqueue(self) -> None:
-        cfg, p, D, T, B, M = self.cfg, self.p, self.D, self.T, self.B, self.M
+        cfg, p, D, T, B, M, R, Sq = self.cfg, self.p, self.D, self.T, self.B, self.M, self.R, self.Sq
         blk = lambda i, n: p[f"model.transformer_blocks.{i}.{n}"]
+        ns = self.Ls * B                     # state rows come first
+        h_act = self.h[ns:]
         # VLM K/V of every cross block
         ops.gemm(self.vl_in.view(B * self.L, cfg.cross_dim), self.wkv, self.bkv, self.ctxkv)
         kv_w = self.ctxkv.shape[1]
+        if ns:
+            # state_encoder MLP, once per call (DB/ActionDiT.py:333)
+            ops.gemm(self.st_in.view(ns, cfg.state_dim), p["state_encoder.layer1.weight"], p["state_encoder.layer1.bias"],
+                     self.st_hid, act=_capi.FAM_ACT_RELU)
+            ops.gemm(self.st_hid, p["state_encoder.layer2.weight"], p["state_encoder.layer2.bias"], self.st_feat)
+        # [B, Sq, .] views of the token-major row buffers
+        q3 = self.qkv.view(Sq, B, 3 * D).transpose(0, 1)
+        o3 = self.attn.view(Sq, B, D).transpose(0, 1)
         for s in range(cfg.num_steps):
             # ActionEncoder: layer1 into the a-half of [a | tau], swish(layer2), layer3 + position rows
             x2 = self.x2[s]
@@ -205,39 +243,50 @@ class FusedDiT4DiTHead:
                        p["action_encoder.layer1.weight"].data_ptr(), p["action_encoder.layer1.bias"].data_ptr(),
                        x2.data_ptr(), 2 * D, M, D, cfg.action_dim, torch.cuda.current_stream(self.device).cuda_stream)
             ops.gemm(x2, p["action_encoder.layer2.weight"], p["action_encoder.layer2.bias"], self.e, act=_capi.FAM_ACT_SILU)
-            ops.gemm(self.e, p["action_encoder.layer3.weight"], p["action_encoder.layer3.bias"], self.h, res=self.posx)
+            ops.gemm(self.e, p["action_encoder.layer3.weight"], p["action_encoder.layer3.bias"], h_act, res=self.posx)
+            if ns:
+                self.h[:ns].copy_(self.st_feat)
             for i in range(cfg.num_layers):
                 shift, scale = self._mod(s, i)
                 ada = dict(prologue=_capi.FAM_PRO_ADALN, pro_shift=shift, pro_scale=scale, pro_mod_bs=0, pro_mod_rs=0,
-                           pro_eps=cfg.norm_eps, rows_per_batch=M)
-                q3 = self.qkv.view(B, T, 3 * D)
+                           pro_eps=cfg.norm_eps, rows_per_batch=R)
                 if i in self.cross_ids:
                     c = self.cross_ids.index(i)
                     ops.gemm(self.h, blk(i, "attn1.to_q.weight"), blk(i, "attn1.to_q.bias"), self.qkv[:, :D], **ada)
                     kv = self.ctxkv.view(B, self.L, kv_w)
                     k = kv[:, :, c * 2 * D:c * 2 * D + D]
                     v = kv[:, :, c * 2 * D + D:(c + 1) * 2 * D]
-                    ops.attention_bshd(q3[:, :, :D], k, v, cfg.heads, out=self.attn, num_splits=self.splits)
+                    ops.attention_bshd(q3[:, :, :D], k, v, cfg.heads, out=o3, num_splits=self.splits)
                 else:
                     ops.gemm(self.h, self.wqkv[i], self.bqkv[i], self.qkv, **ada)
-                    ops.attention_bshd(q3[:, :, :D], q3[:, :, D:2 * D], q3[:, :, 2 * D:], cfg.heads, out=self.attn)
-                ops.gemm(self.attn.view(M, D), blk(i, "attn1.to_out.0.weight"), blk(i, "attn1.to_out.0.bias"), self.h,
+                    ops.attention_bshd(q3[:, :, :D], q3[:, :, D:2 * D], q3[:, :, 2 * D:], cfg.heads, out=o3)
+                ops.gemm(self.attn, blk(i, "attn1.to_out.0.weight"), blk(i, "attn1.to_out.0.bias"), self.h,
                          res=self.h)
                 ops.gemm(self.h, blk(i, "ff.net.0.proj.weight"), blk(i, "ff.net.0.proj.bias"), self.up,
                          prologue=_capi.FAM_PRO_LAYERNORM, pro_eps=cfg.norm_eps, act=_capi.FAM_ACT_GELU_TANH)
                 ops.gemm(self.up, blk(i, "ff.net.2.weight"), blk(i, "ff.net.2.bias"), self.h, res=self.h)
-            # output AdaLN (shift, scale order) + proj_out_2, action decoder, Euler step
+            # output AdaLN (shift, scale order) + proj_out_2, action decoder, Euler step; the state
+            # rows' outputs are dropped by the reference (pred[:, -horizon:]) and not computed here
             om = self.omods[s]
-            ops.gemm(self.h, p["model.proj_out_2.weight"], p["model.proj_out_2.bias"], self.y,
+            ops.gemm(h_act, p["model.proj_out_2.weight"], p["model.proj_out_2.bias"], self.y,
                      prologue=_capi.FAM_PRO_ADALN, pro_shift=om[:D], pro_scale=om[D:], pro_mod_bs=0, pro_mod_rs=0,
                      pro_eps=cfg.out_eps, rows_per_batch=M)
             ops.gemm(self.y, p["action_decoder.layer1.weight"], p["action_decoder.layer1.bias"], self.z, act=_capi.FAM_ACT_RELU)
             ops.gemm(self.z, p["action_decoder.layer2.weight"], p["action_decoder.layer2.bias"], self.vel.view(M, -1))
             ops.euler_step(self.vel, self.delta, self.actions, out=self.actions)
 
-    def set_inputs(self, noise: torch.Tensor, vl_embs: torch.Tensor) -> None:
-        self.actions.copy_(noise.reshape(self.actions.shape))
+    def set_inputs(self, noise: torch.Tensor, vl_embs: torch.Tensor, state: Optional[torch.Tensor] = None) -> None:
+        """noise [B, horizon, action_dim], vl_embs [B, L, cross_dim], state [B, state_len, state_dim]
+        (required exactly when state_len > 0)."""
+        B, T = self.B, self.T
+        self.actions.copy_(noise.reshape(B, T, -1).transpose(0, 1))
         self.vl_in.copy_(vl_embs.reshape(self.vl_in.shape))
+        if self.Ls:
+            if state is None:
+                raise ValueError("DiT4DiT head was built for state tokens; pass state [B, state_len, state_dim]")
+            self.st_in.copy_(state.reshape(B, self.Ls, -1).transpose(0, 1))
+        elif state is not None:
+            raise ValueError("DiT4DiT head was built with state_len=0; state must be None")
 
     def run(self) -> None:
         if self.graph is not None:
@@ -259,8 +308,13 @@ class FusedDiT4DiTHead:
             self._enqueue()
         self.graph = g
 
-    def predict_action(self, vl_embs: torch.Tensor, noise: torch.Tensor) -> torch.Tensor:
-        """One call: the denoised actions [B, horizon, action_dim] (bf16, a copy)."""
-        self.set_inputs(noise, vl_embs)
+    def result(self) -> torch.Tensor:
+        """The denoised actions [B, horizon, action_dim] (bf16, a copy)."""
+        return self.actions.transpose(0, 1).contiguous()
+
+    def predict_action(self, vl_embs: torch.Tensor, noise: torch.Tensor,
+                       state: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """One call of FlowmatchingActionHead.predict_action (noise drawn by the caller)."""
+        self.set_inputs(noise, vl_embs, state)
         self.run()
-        return self.actions.clone()
+        return self.result()

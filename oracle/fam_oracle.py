@@ -606,8 +606,8 @@ def cae_decode(p: Params, cfg: CaeDecoderConfig, z: torch.Tensor, suite: Optiona
 @dataclass
 class DiT4DiTHeadConfig:
     """DiT-B head of DB/ActionDiT.py:192-195 with the diffusion_model_cfg of
-    DiT4DiT/config/real_robot/dit4dit_g1.yaml:25-49 (state encoder not used: predict_action's
-    default state=None, DB/ActionDiT.py:321)."""
+    DiT4DiT/config/real_robot/dit4dit_g1.yaml:25-49; state_dim 64 as in that file (:31) and the
+    RoboCasa-GR1 config (LIBERO uses 16); 0 means no state encoder (DB/ActionDiT.py:235-239)."""
     action_dim: int = 32
     horizon: int = 16            # future_action_window_size + 1
     heads: int = 12              # DiT-B
@@ -623,6 +623,7 @@ class DiT4DiTHeadConfig:
     ff_mult: int = 4             # diffusers FeedForward default inner_dim = 4 * dim
     norm_eps: float = 1e-5       # AdaLayerNorm / norm3 (cross_attention_dit.py:47-57, 207)
     out_eps: float = 1e-6        # norm_out (cross_attention_dit.py:253)
+    state_dim: int = 64          # state_encoder input width (0: no state encoder)
 
     @property
     def dim(self) -> int:
@@ -651,6 +652,11 @@ def d4d_param_shapes(cfg: DiT4DiTHeadConfig) -> Dict[str, Tuple[int, ...]]:
         "action_decoder.layer2.weight": (cfg.action_dim, cfg.hidden_size), "action_decoder.layer2.bias": (cfg.action_dim,),
         "position_embedding.weight": (cfg.max_seq_len, D),
     }
+    if cfg.state_dim:
+        # MLP(state_dim, hidden_size, D) (DB/ActionDiT.py:64-71, 235-239)
+        s.update({"state_encoder.layer1.weight": (cfg.hidden_size, cfg.state_dim),
+                  "state_encoder.layer1.bias": (cfg.hidden_size,),
+                  "state_encoder.layer2.weight": (D, cfg.hidden_size), "state_encoder.layer2.bias": (D,)})
     for i in range(cfg.num_layers):
         b = f"model.transformer_blocks.{i}."
         kv_in = C if cfg.is_cross(i) else D
@@ -753,19 +759,29 @@ def d4d_timesteps(cfg: DiT4DiTHeadConfig) -> List[int]:
     return [int((1.0 - i / float(cfg.num_steps)) * cfg.buckets) for i in range(cfg.num_steps)]
 
 
-def d4d_predict_action(p: Params, cfg: DiT4DiTHeadConfig, vl_embs: torch.Tensor, noise: torch.Tensor) -> torch.Tensor:
-    """FlowmatchingActionHead.predict_action with state=None (DB/ActionDiT.py:321-369): per step,
-    encode (actions, t), add position embeddings, DiT, action decoder MLP (layer2(ReLU(layer1))),
-    actions = actions - dt * velocity[:, -horizon:] (dt = 1/N)."""
+def d4d_mlp(p: Params, prefix: str, x: torch.Tensor) -> torch.Tensor:
+    """MLP.forward (DB/ActionDiT.py:64-71): layer2(ReLU(layer1(x)))."""
+    h = F.relu(F.linear(x, p[prefix + "layer1.weight"], p[prefix + "layer1.bias"]))
+    return F.linear(h, p[prefix + "layer2.weight"], p[prefix + "layer2.bias"])
+
+
+def d4d_predict_action(p: Params, cfg: DiT4DiTHeadConfig, vl_embs: torch.Tensor, noise: torch.Tensor,
+                       state: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """FlowmatchingActionHead.predict_action (DB/ActionDiT.py:321-369): state features =
+    state_encoder(state) once per call (:333) when a state [B, Ls, state_dim] is given; per step,
+    encode (actions, t), add position embeddings (:349-352), prepend the state features (:355-356),
+    DiT, action decoder MLP, actions = actions - dt * velocity[:, -horizon:] (dt = 1/N)."""
     B, T, _ = noise.shape
     actions = noise
     dt = 1.0 / cfg.num_steps
     pos = p["position_embedding.weight"][:T].unsqueeze(0)
+    sfeat = d4d_mlp(p, "state_encoder.", state) if state is not None else None
     for t_disc in d4d_timesteps(cfg):
         ts = torch.full((B,), t_disc, dtype=torch.long)
         feats = d4d_action_encoder(p, actions, ts) + pos
+        if sfeat is not None:
+            feats = torch.cat([sfeat, feats], dim=1)
         out = d4d_dit_forward(p, cfg, feats, vl_embs, ts)
-        pred = F.linear(F.relu(F.linear(out, p["action_decoder.layer1.weight"], p["action_decoder.layer1.bias"])),
-                        p["action_decoder.layer2.weight"], p["action_decoder.layer2.bias"])
+        pred = d4d_mlp(p, "action_decoder.", out)
         actions = actions - dt * pred[:, -cfg.horizon:]
     return actions
