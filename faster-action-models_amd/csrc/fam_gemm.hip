@@ -52,6 +52,7 @@ struct GemmArgs {
   const bf16* gate; int64_t gbs, grs, gns;
   int64_t rpb;
   int out_f32;
+  const float* csum;   // FAM_PRO_LN_FOLDED: sum_k w[n, k], fp32 [N]
 };
 
 __device__ __forceinline__ float apply_act(float v, int act) {
@@ -59,6 +60,29 @@ __device__ __forceinline__ float apply_act(float v, int act) {
   if (act == FAM_ACT_SILU) return silu(v);
   if (act == FAM_ACT_RELU) return fmaxf(v, 0.f);
   return v;
+}
+
+// The epilogue operands of one output element, loaded ahead of the product so that their
+// memory round trip overlaps the weight stream.
+struct EpiIn {
+  float bias, res, gate, csum;
+};
+__device__ __forceinline__ EpiIn epilogue_load(const GemmArgs& g, int64_t m, int64_t n) {
+  EpiIn e{0.f, 0.f, 1.f, 0.f};
+  if (g.bias) e.bias = to_f(g.bias[n]);
+  if (g.csum) e.csum = g.csum[n];
+  if (g.res) {
+    const int64_t bi = m / g.rpb, si = m - bi * g.rpb;
+    if (g.gate) e.gate = to_f(g.gate[bi * g.gbs + si * g.grs + n * g.gns]);
+    e.res = g.out_f32 ? reinterpret_cast<const float*>(g.res)[m * g.ldr + n] : to_f(g.res[m * g.ldr + n]);
+  }
+  return e;
+}
+__device__ __forceinline__ void epilogue_finish(const GemmArgs& g, int64_t m, int64_t n, float v, const EpiIn& e) {
+  v = apply_act(v + e.bias, g.act);
+  if (g.res) v = e.res + e.gate * v;
+  if (g.out_f32) reinterpret_cast<float*>(g.out)[m * g.ldo + n] = v;
+  else g.out[m * g.ldo + n] = to_bf(v);
 }
 
 // bias, activation, gate * value + residual, store (bf16 or fp32) for one output element
@@ -110,6 +134,32 @@ __device__ __forceinline__ bf16x8 prologue8(const GemmArgs& g, bf16x8 v, int64_t
   }
 }
 
+// LayerNorm / AdaLN of 8 elements with the per-column vectors already in registers: p0, p1 =
+// (weight, bias) for LayerNorm (use flags uw, ub), (shift, scale) for a broadcast AdaLN.
+template <int PRO>
+__device__ __forceinline__ bf16x8 prologue8_pre(bf16x8 v, float mu, float rs, bf16x8 p0, bf16x8 p1, bool uw, bool ub) {
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = (to_f(v[e]) - mu) * rs;
+  if constexpr (PRO == FAM_PRO_LAYERNORM) {
+    if (uw) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] *= to_f(p0[e]);
+    }
+    if (ub) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += to_f(p1[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = o[e] * (1.0f + to_f(p1[e])) + to_f(p0[e]);
+  }
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = to_bf(o[e]);
+  return r;
+}
+
 // Row statistics (mean, rstd) of rows m0 .. m0+rows-1: one wave per row, two passes
 // (mean, then centred variance); rows past M get zeros.
 __device__ __forceinline__ void row_stats(const GemmArgs& g, int64_t m0, int rows, int wave, int nwaves, int lane,
@@ -142,13 +192,27 @@ __device__ __forceinline__ void row_stats(const GemmArgs& g, int64_t m0, int row
 // skinny_kernel: M <= 16*MT rows, 16 output columns per workgroup, NW waves split K into
 // contiguous runs of 32-wide k-steps; each wave holds KS k-steps of weights and activations
 // in registers at once.  Every load is branch-free (out-of-range lanes load a valid address
-// and are zeroed), so the loads of a chunk are issued back to back.
+// and are zeroed), so the loads of a chunk are issued back to back.  The per-column prologue
+// vectors (LayerNorm weight / bias, a broadcast AdaLN's shift / scale) travel with the chunk
+// and each thread's epilogue operands (bias, residual, gate) are loaded before the product,
+// so a launch waits for one memory round trip instead of three.
+//
+// FAM_PRO_LN_FOLDED: the product runs on the raw rows; every lane also sums (x - pivot) and
+// (x - pivot)^2 of the elements it loaded (pivot = the row's first element, which keeps the
+// variance of rows with a large mean well conditioned), off the path into the matrix cores.
+// The sums meet in LDS with the accumulators and the epilogue forms
+//   rstd * (acc - mean * csum[n]).
 template <int MT, int NW, int KS, int PRO>
 __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
   constexpr int MR = MT * 16;
   constexpr int TPR = NW * 64 / MR;  // threads per row in the statistics pass
+  constexpr bool NORM = PRO == FAM_PRO_LAYERNORM || PRO == FAM_PRO_ADALN;   // normalise the A operand
+  constexpr bool FOLD = PRO == FAM_PRO_LN_FOLDED;
+  static_assert(!FOLD || NW <= 8, "the folded LayerNorm uses the 8-wave variant");
   __shared__ float s_mean[MR], s_rstd[MR];
   __shared__ float s_red[NW][MR][16];
+  __shared__ float2 s_st[FOLD ? NW : 1][MR];
+  __shared__ float s_piv[MR];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
@@ -163,7 +227,14 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < MT; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  bf16x8 wf[KS], af[KS][MT];
+  // per-column prologue vectors in registers: LayerNorm always, AdaLN when its modulation is
+  // one row for all rows (otherwise prologue8 loads it per row)
+  const bool pre = PRO == FAM_PRO_LAYERNORM || (PRO == FAM_PRO_ADALN && g.mbs == 0 && g.mrs == 0);
+  const bf16* pv0p = PRO == FAM_PRO_LAYERNORM ? g.pw : g.shift;
+  const bf16* pv1p = PRO == FAM_PRO_LAYERNORM ? g.pb : g.scale;
+  const bool uw = pv0p != nullptr, ub = pv1p != nullptr;
+
+  bf16x8 wf[KS], af[KS][MT], pv0[KS], pv1[KS];
   auto chunk_load = [&](int64_t sb) {
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
@@ -175,14 +246,44 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
         const int64_t m = i * 16 + l16;
         af[j][i] = load8_if(kok && m < g.M, g.a + m * g.lda + k, g.a);
       }
+      if constexpr (NORM) {
+        if (pre) {   // wave-uniform
+          pv0[j] = load8_if(kok && uw, pv0p + k, g.a);
+          pv1[j] = load8_if(kok && ub, pv1p + k, g.a);
+        }
+      }
     }
   };
   chunk_load(s_beg);  // weights and activations of the first chunk in flight at once
+  float piv[MT], s1[MT], s2[MT];
+  if constexpr (FOLD) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      const int64_t m = i * 16 + l16;
+      piv[i] = to_f(g.a[(m < g.M ? m : g.M - 1) * g.lda]);
+      s1[i] = 0.f;
+      s2[i] = 0.f;
+    }
+  }
+  // epilogue operands of this thread's outputs (at most EPT of them); the 16-wave variants
+  // (128 registers per lane) load them in the epilogue instead, as they would spill
+  constexpr int EPT = (MR * 16 + NW * 64 - 1) / (NW * 64);
+  constexpr bool EPRE = NW <= 8;
+  EpiIn ep[EPT];
+  auto ep_load = [&]() {
+#pragma unroll
+    for (int u = 0; u < EPT; ++u) {
+      const int t = tid + u * NW * 64, mr = t >> 4;
+      const int64_t n = n0 + (t & 15);
+      ep[u] = (t < MR * 16 && mr < g.M && n < g.N) ? epilogue_load(g, mr, n) : EpiIn{0.f, 0.f, 1.f, 0.f};
+    }
+  };
+  if constexpr (EPRE) ep_load();
   // keep the scheduler from sinking those loads next to their first use (it would, to save
   // registers, and each k-step would then pay a full memory round trip)
   __builtin_amdgcn_sched_barrier(0);
 
-  if constexpr (PRO != FAM_PRO_NONE) {
+  if constexpr (NORM) {
     // one pass over each row: sums about the row's first element (a shared pivot keeps the
     // difference of large sums well conditioned), reduced over the TPR lanes of the row
     const int r = tid / TPR, t = tid % TPR;
@@ -221,14 +322,47 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < MT; ++i) {
         bf16x8 a = af[j][i];
-        if constexpr (PRO != FAM_PRO_NONE) {
+        if constexpr (NORM) {
           // rows past M normalise to finite values that only reach their own (unstored)
           // outputs; k past K meets zero weights
           const int64_t m = i * 16 + l16;
-          const int64_t k = std::min((sb + j) * 32 + lg * 8, g.K - 8);
-          a = prologue8<PRO>(g, a, std::min(m, g.M - 1), k, s_mean[m], s_rstd[m]);
+          if (pre) {
+            a = prologue8_pre<PRO>(a, s_mean[m], s_rstd[m], pv0[j], pv1[j], uw, ub);
+          } else {
+            const int64_t k = std::min((sb + j) * 32 + lg * 8, g.K - 8);
+            a = prologue8<PRO>(g, a, std::min(m, g.M - 1), k, s_mean[m], s_rstd[m]);
+          }
         }
         acc[i] = mfma16(wf[j], a, acc[i]);
+      }
+    }
+    if constexpr (FOLD) {
+      // row sums of this chunk (k past the wave's range or K was loaded as zeros: skipped)
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        const bool kok = (sb + j < s_end) && (sb + j) * 32 + lg * 8 < g.K;
+        if (!kok) continue;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float d = to_f(af[j][i][e]) - piv[i];
+            s1[i] += d;
+            s2[i] += d * d;
+          }
+      }
+    }
+  }
+  if constexpr (FOLD) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      s1[i] += __shfl_xor(s1[i], 16, kWave);
+      s2[i] += __shfl_xor(s2[i], 16, kWave);
+      s1[i] += __shfl_xor(s1[i], 32, kWave);
+      s2[i] += __shfl_xor(s2[i], 32, kWave);
+      if (lg == 0) {
+        s_st[wave][i * 16 + l16] = make_float2(s1[i], s2[i]);
+        if (wave == 0) s_piv[i * 16 + l16] = piv[i];
       }
     }
   }
@@ -237,6 +371,28 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < MT; ++i) *reinterpret_cast<f32x4*>(&s_red[wave][i * 16 + l16][lg * 4]) = acc[i];
   __syncthreads();
+  if constexpr (EPRE) {
+#pragma unroll
+    for (int u = 0; u < EPT; ++u) {
+      const int t = tid + u * NW * 64, mr = t >> 4, nc = t & 15;
+      const int64_t n = n0 + nc;
+      if (t >= MR * 16 || mr >= g.M || n >= g.N) continue;
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) v += s_red[w][mr][nc];
+      if constexpr (FOLD) {
+        float t1 = 0.f, t2 = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) { t1 += s_st[w][mr].x; t2 += s_st[w][mr].y; }
+        const float invk = 1.0f / (float)g.K;
+        const float dm = t1 * invk;
+        const float rstd = rsqrtf(fmaxf(t2 * invk - dm * dm, 0.f) + g.eps);
+        v = rstd * (v - (s_piv[mr] + dm) * ep[u].csum);
+      }
+      epilogue_finish(g, mr, n, v, ep[u]);
+    }
+    return;
+  }
   for (int t = tid; t < MR * 16; t += NW * 64) {
     const int mr = t >> 4, nc = t & 15;
     const int64_t n = n0 + nc;
@@ -768,20 +924,22 @@ static void launch_skinny(const GemmArgs& a, int pro, hipStream_t s) {
   dim3 grid((unsigned)(round_up(a.N, 16) / 16));
   if constexpr (NW > 8) {
     FAM_LAUNCH((skinny_kernel<MT, NW, KS, FAM_PRO_NONE>), grid, dim3(NW * 64), 0, s, a);
-    return;
-  }
-  switch (pro) {
-    case FAM_PRO_LAYERNORM: FAM_LAUNCH((skinny_kernel<MT, NW, KS, FAM_PRO_LAYERNORM>), grid, dim3(NW * 64), 0, s, a); break;
-    case FAM_PRO_ADALN: FAM_LAUNCH((skinny_kernel<MT, NW, KS, FAM_PRO_ADALN>), grid, dim3(NW * 64), 0, s, a); break;
-    default: FAM_LAUNCH((skinny_kernel<MT, NW, KS, FAM_PRO_NONE>), grid, dim3(NW * 64), 0, s, a); break;
+  } else {
+    switch (pro) {
+      case FAM_PRO_LAYERNORM: FAM_LAUNCH((skinny_kernel<MT, NW, KS, FAM_PRO_LAYERNORM>), grid, dim3(NW * 64), 0, s, a); break;
+      case FAM_PRO_ADALN: FAM_LAUNCH((skinny_kernel<MT, NW, KS, FAM_PRO_ADALN>), grid, dim3(NW * 64), 0, s, a); break;
+      case FAM_PRO_LN_FOLDED: FAM_LAUNCH((skinny_kernel<MT, NW, KS, FAM_PRO_LN_FOLDED>), grid, dim3(NW * 64), 0, s, a); break;
+      default: FAM_LAUNCH((skinny_kernel<MT, NW, KS, FAM_PRO_NONE>), grid, dim3(NW * 64), 0, s, a); break;
+    }
   }
 }
 
 // 8 waves with 4 k-steps each cover K <= 1024 in one chunk; longer K takes 16 waves with
 // 8 k-steps each (K <= 4096 in one chunk), more chunks beyond that.
+// The folded LayerNorm always takes 8 waves (its row sums need the registers).
 template <int MT>
 static void launch_skinny_k(const GemmArgs& a, int pro, hipStream_t s) {
-  if (a.K <= 1024) launch_skinny<MT, 8, 4>(a, pro, s);
+  if (a.K <= 1024 || pro == FAM_PRO_LN_FOLDED) launch_skinny<MT, 8, 4>(a, pro, s);
   else launch_skinny<MT, 16, 8>(a, pro, s);
 }
 
@@ -853,7 +1011,7 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
   FAM_REQUIRE(d->ldo >= d->N, FAM_ERR_INVALID_ARG, "fam_gemm: ldo must be >= N");
   FAM_REQUIRE(fam_host::aligned16(d->a) && fam_host::aligned16(d->w), FAM_ERR_INVALID_ARG,
               "fam_gemm: a and w must be 16-byte aligned");
-  FAM_REQUIRE(d->prologue >= FAM_PRO_NONE && d->prologue <= FAM_PRO_ADALN, FAM_ERR_INVALID_ARG,
+  FAM_REQUIRE(d->prologue >= FAM_PRO_NONE && d->prologue <= FAM_PRO_LN_FOLDED, FAM_ERR_INVALID_ARG,
               "fam_gemm: unknown prologue %d", d->prologue);
   FAM_REQUIRE(d->act >= FAM_ACT_NONE && d->act <= FAM_ACT_RELU, FAM_ERR_INVALID_ARG, "fam_gemm: unknown act %d", d->act);
   if (d->prologue == FAM_PRO_LAYERNORM) {
@@ -865,6 +1023,12 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
     FAM_REQUIRE(fam_host::aligned16(d->pro_shift) && fam_host::aligned16(d->pro_scale) && d->pro_mod_bs % 8 == 0 &&
                     d->pro_mod_rs % 8 == 0,
                 FAM_ERR_INVALID_ARG, "fam_gemm: AdaLN shift/scale must be 16-byte aligned, strides %% 8 == 0");
+  }
+  if (d->prologue == FAM_PRO_LN_FOLDED) {
+    FAM_REQUIRE(d->pro_w && ((uintptr_t)d->pro_w & 3u) == 0, FAM_ERR_INVALID_ARG,
+                "fam_gemm: the folded LayerNorm needs the fp32 column sums of w in pro_w");
+    FAM_REQUIRE(d->M <= 64, FAM_ERR_UNSUPPORTED, "fam_gemm: the folded LayerNorm supports M <= 64 (got %lld)",
+                (long long)d->M);
   }
   FAM_REQUIRE(d->rows_per_batch >= 1, FAM_ERR_INVALID_ARG, "fam_gemm: rows_per_batch must be >= 1");
   FAM_REQUIRE(!d->gate || d->res, FAM_ERR_INVALID_ARG, "fam_gemm: a gate needs a residual");
@@ -885,9 +1049,14 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
   a.gate = (const bf16*)d->gate; a.gbs = d->gate_bs; a.grs = d->gate_rs; a.gns = d->gate_ns;
   a.rpb = d->rows_per_batch;
   a.out_f32 = d->out_f32 != 0;
+  if (d->prologue == FAM_PRO_LN_FOLDED) {
+    a.csum = (const float*)d->pro_w;
+    a.pw = nullptr;
+  }
   hipStream_t s = (hipStream_t)stream;
-  // (a prologue over K > 1024 would not fit the 16-wave skinny variant's registers)
-  const bool skinny = d->M <= 64 && (d->prologue == FAM_PRO_NONE || d->K <= 1024);
+  // (a normalising prologue over K > 1024 would not fit the 16-wave skinny variant's
+  // registers; the folded LayerNorm runs K in chunks on 8 waves)
+  const bool skinny = d->M <= 64 && (d->prologue == FAM_PRO_NONE || d->prologue == FAM_PRO_LN_FOLDED || d->K <= 1024);
   if (skinny && d->M <= 16) launch_skinny_k<1>(a, d->prologue, s);
   else if (skinny && d->M <= 32) launch_skinny_k<2>(a, d->prologue, s);
   else if (skinny) launch_skinny_k<4>(a, d->prologue, s);

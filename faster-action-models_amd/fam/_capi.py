@@ -18,7 +18,7 @@ FAM_ERR_LAUNCH = 3
 FAM_ABI_VERSION = 2
 
 FAM_MASK_NONE, FAM_MASK_BOOL, FAM_MASK_ADD_F32, FAM_MASK_ADD_BF16 = 0, 1, 2, 3
-FAM_PRO_NONE, FAM_PRO_LAYERNORM, FAM_PRO_ADALN = 0, 1, 2
+FAM_PRO_NONE, FAM_PRO_LAYERNORM, FAM_PRO_ADALN, FAM_PRO_LN_FOLDED = 0, 1, 2, 3
 FAM_ACT_NONE, FAM_ACT_GELU_TANH, FAM_ACT_SILU, FAM_ACT_RELU = 0, 1, 2, 3
 FAM_ROWSRC_PARTIALS, FAM_ROWSRC_SMALLK = 0, 1
 FAM_ROWNORM_NONE, FAM_ROWNORM_LAYERNORM, FAM_ROWNORM_ADALN, FAM_ROWNORM_RMS = 0, 1, 2, 3

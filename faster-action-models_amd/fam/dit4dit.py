@@ -134,10 +134,15 @@ class FusedDiT4DiTHead:
             dtype; converted to bf16 on `device`.
         state_len: state tokens per chunk (the reference's state is [B, 1, state_dim]);
             default 1 when cfg.state_dim > 0.
+        fold_norms: evaluate every LayerNorm / AdaLN that feeds a projection as
+            rstd * (x W'^T - mean * colsum(W')) with the (fixed-schedule) modulation folded into
+            W' and the bias at construction (fam_gemm FAM_PRO_LN_FOLDED, <= 64 rows); otherwise
+            normalise the rows in the GEMM prologue.
     """
 
     def __init__(self, cfg, params: Dict[str, torch.Tensor], *, batch: int, vl_len: int,
-                 device: torch.device, attn_splits: Optional[int] = None, state_len: Optional[int] = None):
+                 device: torch.device, attn_splits: Optional[int] = None, state_len: Optional[int] = None,
+                 fold_norms: bool = True):
         self.cfg, self.B, self.L, self.device = cfg, batch, vl_len, device
         D, T, A = cfg.heads * cfg.head_dim, cfg.horizon, cfg.action_dim
         Ls = (1 if cfg.state_dim else 0) if state_len is None else state_len
@@ -193,6 +198,23 @@ class FusedDiT4DiTHead:
         for s, t in enumerate(self.t_disc):
             self.x2[s, :, D:] = _tau_rows(float(t), D).to(device=device, dtype=_BF16)
         self.posx = p["position_embedding.weight"][:T].repeat_interleave(batch, dim=0).contiguous()   # [M, D]
+        # folded normalisations: per (step, block) the AdaLN of that step's timestep inside the
+        # q / qkv weights; FFN up's plain LayerNorm needs only column sums; per step the output
+        # AdaLN inside proj_out_2
+        self.fold = fold_norms and self.R <= 64
+        if self.fold:
+            self.fq: List[List[tuple]] = []
+            for s in range(S):
+                row = []
+                for i in range(nb):
+                    shift, scale = self._mod(s, i)
+                    w, b = ((blk(i, "attn1.to_q.weight"), blk(i, "attn1.to_q.bias")) if i in cross
+                            else (self.wqkv[i], self.bqkv[i]))
+                    row.append(ops.fold_layernorm(w, b, scale=scale, shift=shift))
+                self.fq.append(row)
+            self.fup_cs = [ops.fold_layernorm(blk(i, "ff.net.0.proj.weight"))[2] for i in range(nb)]
+            self.fout = [ops.fold_layernorm(p["model.proj_out_2.weight"], p["model.proj_out_2.bias"],
+                                            scale=self.omods[s, D:], shift=self.omods[s, :D]) for s in range(S)]
         # ---- activations (token-major rows)
         R = self.R
         self.actions = torch.empty(T, batch, A, dtype=_BF16, device=device)
@@ -247,30 +269,47 @@ class FusedDiT4DiTHead:
             if ns:
                 self.h[:ns].copy_(self.st_feat)
             for i in range(cfg.num_layers):
-                shift, scale = self._mod(s, i)
-                ada = dict(prologue=_capi.FAM_PRO_ADALN, pro_shift=shift, pro_scale=scale, pro_mod_bs=0, pro_mod_rs=0,
-                           pro_eps=cfg.norm_eps, rows_per_batch=R)
+                if self.fold:
+                    wq, bq, cq = self.fq[s][i]
+                    qproj = lambda out: ops.gemm(self.h, wq, bq, out, prologue=_capi.FAM_PRO_LN_FOLDED, pro_w=cq,
+                                                 pro_eps=cfg.norm_eps)
+                else:
+                    shift, scale = self._mod(s, i)
+                    ada = dict(prologue=_capi.FAM_PRO_ADALN, pro_shift=shift, pro_scale=scale, pro_mod_bs=0,
+                               pro_mod_rs=0, pro_eps=cfg.norm_eps, rows_per_batch=R)
+                    wq, bq = ((blk(i, "attn1.to_q.weight"), blk(i, "attn1.to_q.bias")) if i in self.cross_ids
+                              else (self.wqkv[i], self.bqkv[i]))
+                    qproj = lambda out: ops.gemm(self.h, wq, bq, out, **ada)
                 if i in self.cross_ids:
                     c = self.cross_ids.index(i)
-                    ops.gemm(self.h, blk(i, "attn1.to_q.weight"), blk(i, "attn1.to_q.bias"), self.qkv[:, :D], **ada)
+                    qproj(self.qkv[:, :D])
                     kv = self.ctxkv.view(B, self.L, kv_w)
                     k = kv[:, :, c * 2 * D:c * 2 * D + D]
                     v = kv[:, :, c * 2 * D + D:(c + 1) * 2 * D]
                     ops.attention_bshd(q3[:, :, :D], k, v, cfg.heads, out=o3, num_splits=self.splits)
                 else:
-                    ops.gemm(self.h, self.wqkv[i], self.bqkv[i], self.qkv, **ada)
+                    qproj(self.qkv)
                     ops.attention_bshd(q3[:, :, :D], q3[:, :, D:2 * D], q3[:, :, 2 * D:], cfg.heads, out=o3)
                 ops.gemm(self.attn, blk(i, "attn1.to_out.0.weight"), blk(i, "attn1.to_out.0.bias"), self.h,
                          res=self.h)
-                ops.gemm(self.h, blk(i, "ff.net.0.proj.weight"), blk(i, "ff.net.0.proj.bias"), self.up,
-                         prologue=_capi.FAM_PRO_LAYERNORM, pro_eps=cfg.norm_eps, act=_capi.FAM_ACT_GELU_TANH)
+                if self.fold:
+                    ops.gemm(self.h, blk(i, "ff.net.0.proj.weight"), blk(i, "ff.net.0.proj.bias"), self.up,
+                             prologue=_capi.FAM_PRO_LN_FOLDED, pro_w=self.fup_cs[i], pro_eps=cfg.norm_eps,
+                             act=_capi.FAM_ACT_GELU_TANH)
+                else:
+                    ops.gemm(self.h, blk(i, "ff.net.0.proj.weight"), blk(i, "ff.net.0.proj.bias"), self.up,
+                             prologue=_capi.FAM_PRO_LAYERNORM, pro_eps=cfg.norm_eps, act=_capi.FAM_ACT_GELU_TANH)
                 ops.gemm(self.up, blk(i, "ff.net.2.weight"), blk(i, "ff.net.2.bias"), self.h, res=self.h)
             # output AdaLN (shift, scale order) + proj_out_2, action decoder, Euler step; the state
             # rows' outputs are dropped by the reference (pred[:, -horizon:]) and not computed here
-            om = self.omods[s]
-            ops.gemm(h_act, p["model.proj_out_2.weight"], p["model.proj_out_2.bias"], self.y,
-                     prologue=_capi.FAM_PRO_ADALN, pro_shift=om[:D], pro_scale=om[D:], pro_mod_bs=0, pro_mod_rs=0,
-                     pro_eps=cfg.out_eps, rows_per_batch=M)
+            if self.fold:
+                wo, bo, co = self.fout[s]
+                ops.gemm(h_act, wo, bo, self.y, prologue=_capi.FAM_PRO_LN_FOLDED, pro_w=co, pro_eps=cfg.out_eps)
+            else:
+                om = self.omods[s]
+                ops.gemm(h_act, p["model.proj_out_2.weight"], p["model.proj_out_2.bias"], self.y,
+                         prologue=_capi.FAM_PRO_ADALN, pro_shift=om[:D], pro_scale=om[D:], pro_mod_bs=0,
+                         pro_mod_rs=0, pro_eps=cfg.out_eps, rows_per_batch=M)
             ops.gemm(self.y, p["action_decoder.layer1.weight"], p["action_decoder.layer1.bias"], self.z, act=_capi.FAM_ACT_RELU)
             ops.gemm(self.z, p["action_decoder.layer2.weight"], p["action_decoder.layer2.bias"], self.vel.view(M, -1))
             ops.euler_step(self.vel, self.delta, self.actions, out=self.actions)

@@ -374,9 +374,13 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: to
          pro_mod_bs: int = 0, pro_mod_rs: int = 0, pro_eps: float = 1e-6, act: int = _capi.FAM_ACT_NONE,
          res: Optional[torch.Tensor] = None, gate: Optional[torch.Tensor] = None, gate_bs: int = 0,
          gate_rs: int = 0, gate_ns: int = 1, rows_per_batch: Optional[int] = None, out_f32: bool = False) -> None:
-    """Fused GEMM on 2-D views (see fam_gemm in include/fam_hip.h): a [M, K], w [N, K], out [M, N]."""
+    """Fused GEMM on 2-D views (see fam_gemm in include/fam_hip.h): a [M, K], w [N, K], out [M, N].
+    With prologue=FAM_PRO_LN_FOLDED, pro_w is the fp32 [N] column-sum vector of `fold_layernorm`."""
     M, K = a.shape
     N = w.shape[0]
+    if prologue == _capi.FAM_PRO_LN_FOLDED:
+        if pro_w is None or pro_w.dtype != torch.float32 or pro_w.numel() != N or not pro_w.is_contiguous():
+            raise ValueError("FAM_PRO_LN_FOLDED needs pro_w = fp32 contiguous [N] column sums of w")
     d = _capi.GemmDesc()
     d.a, d.lda = a.data_ptr(), a.stride(0)
     d.w, d.ldw = w.data_ptr(), w.stride(0)
@@ -396,6 +400,42 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: to
     d.rows_per_batch = rows_per_batch if rows_per_batch is not None else max(M, 1)
     d.out_f32 = int(out_f32)
     call("fam_gemm", C.byref(d), _stream(a))
+
+
+def fold_layernorm(w: torch.Tensor, bias: Optional[torch.Tensor] = None, *, ln_weight: Optional[torch.Tensor] = None,
+                   ln_bias: Optional[torch.Tensor] = None, scale: Optional[torch.Tensor] = None,
+                   shift: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Fold what follows a LayerNorm and precedes a linear layer -- its affine (ln_weight,
+    ln_bias) and an AdaLN modulation (1 + scale, shift), each one [K] vector for every row --
+    into the layer, for fam_gemm's FAM_PRO_LN_FOLDED:
+
+        ((LN(x) * ln_weight + ln_bias) * (1 + scale) + shift) w^T + bias
+          = rstd * (x w'^T - mean * colsum) + bias'
+
+    with w' = w diag(g), g = ln_weight (1 + scale); bias' = bias + w c, c = ln_bias (1 + scale)
+    + shift; colsum[n] = sum_k w'[n, k] of the bf16 w' (fp32).  Returns (w' bf16, bias' bf16,
+    colsum fp32), all on w's device.  A weight-preparation step (run once per weight and
+    modulation), not a hot-path op."""
+    N, K = w.shape
+    dev = w.device
+    g = torch.ones(K, dtype=torch.float64, device=dev)
+    c = torch.zeros(K, dtype=torch.float64, device=dev)
+    if ln_weight is not None:
+        g = ln_weight.to(torch.float64).reshape(K)
+    if ln_bias is not None:
+        c = ln_bias.to(torch.float64).reshape(K)
+    if scale is not None:
+        s1 = 1.0 + scale.to(torch.float64).reshape(K)
+        g, c = g * s1, c * s1
+    if shift is not None:
+        c = c + shift.to(torch.float64).reshape(K)
+    w64 = w.to(torch.float64)
+    w2 = (w64 * g[None, :]).to(_BF16).contiguous()
+    b2 = w64 @ c
+    if bias is not None:
+        b2 = b2 + bias.to(torch.float64).reshape(N)
+    colsum = w2.to(torch.float64).sum(dim=1).to(torch.float32).contiguous()
+    return w2, b2.to(_BF16).contiguous(), colsum
 
 
 def gemm_partial(a: torch.Tensor, w: torch.Tensor):

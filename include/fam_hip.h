@@ -174,6 +174,7 @@ int fam_attention_combine(const fam_attn_desc* d, void* stream);
 #define FAM_PRO_NONE 0
 #define FAM_PRO_LAYERNORM 1  /* LN(a) [* pro_w + pro_b]                        */
 #define FAM_PRO_ADALN 2      /* LN(a) * (1 + pro_scale) + pro_shift            */
+#define FAM_PRO_LN_FOLDED 3  /* LN(a) with its affine / modulation folded into w, bias (below) */
 #define FAM_ACT_NONE 0
 #define FAM_ACT_GELU_TANH 1
 #define FAM_ACT_SILU 2
@@ -188,6 +189,13 @@ int fam_attention_combine(const fam_attn_desc* d, void* stream);
  * res may equal out (in-place residual update).  out_f32 != 0 makes out and res fp32
  * (e.g. the fused Euler update of fp32 latents); otherwise both are bf16.  AdaLN shift/scale use the same
  * (rows_per_batch, pro_mod_bs, pro_mod_rs) indexing with a unit column stride.
+ * FAM_PRO_LN_FOLDED (M <= 64): sum_k LN(a)[m, k] * w[n, k] is evaluated as
+ *   rstd_m * (sum_k a[m, k] * w[n, k] - mean_m * pro_w[n]),
+ * mean_m and rstd_m = 1/sqrt(var_m + pro_eps) of row m of a over K, pro_w an fp32 [N] vector
+ * holding sum_k w[n, k] of the bf16 w; the product runs on the raw rows, so no normalisation
+ * sits between the loads and the matrix cores.  A LayerNorm affine (g, b) and an AdaLN
+ * modulation (1 + s, t) that are the same for every row fold into w' = w diag(g (1 + s)),
+ * bias' = bias + w (b (1 + s) + t) beforehand (fam.ops.fold_layernorm).
  * Work split: for M <= 64 a workgroup of 8 waves owns 16 output columns and the waves split
  * K (reduced through LDS in wave order); for larger M, 64x64 or 128x128 output tiles.
  * Replaces: nn.Linear / F.linear on the hot path (FB/wan_video_dit.py:188-191,215-218,262-263,

@@ -16,7 +16,7 @@ def _params(cfg, seed):
     return {k: v.to(torch.bfloat16) for k, v in O.init_d4d_params(cfg, seed).items()}
 
 
-def _run(cfg, B, L, seed, state_len):
+def _run(cfg, B, L, seed, state_len, fold_norms=True):
     """state_len 0 is the reference's state=None call; 1 is what the eval clients pass."""
     from fam.dit4dit import FusedDiT4DiTHead
     p = _params(cfg, seed)
@@ -24,7 +24,8 @@ def _run(cfg, B, L, seed, state_len):
     vl = torch.randn(B, L, cfg.cross_dim, generator=g).to(torch.bfloat16)
     noise = torch.randn(B, cfg.horizon, cfg.action_dim, generator=g).to(torch.bfloat16)
     state = torch.randn(B, state_len, cfg.state_dim, generator=g).to(torch.bfloat16) if state_len else None
-    head = FusedDiT4DiTHead(cfg, p, batch=B, vl_len=L, device=torch.device("cuda:0"), state_len=state_len)
+    head = FusedDiT4DiTHead(cfg, p, batch=B, vl_len=L, device=torch.device("cuda:0"), state_len=state_len,
+                            fold_norms=fold_norms)
     out = head.predict_action(vl.cuda(), noise.cuda(), None if state is None else state.cuda())
     ref = O.d4d_predict_action({k: v.float() for k, v in p.items()}, cfg, vl.float(), noise.float(),
                                None if state is None else state.float())
@@ -35,13 +36,17 @@ def _relerr(y, ref):
     return ((y - ref).abs().max() / ref.abs().max()).item()
 
 
-@pytest.mark.parametrize("B,state_len", [(2, 1), (3, 0), (2, 2)])
-def test_d4d_head_tiny_config(B, state_len):
+@pytest.mark.parametrize("B,state_len,fold", [(2, 1, True), (3, 0, True), (2, 2, True), (2, 1, False), (10, 1, True)])
+def test_d4d_head_tiny_config(B, state_len, fold):
+    """fold: LayerNorm / AdaLN folded into the projections (<= 64 rows; B=10 has 70 rows and
+    takes the normalising prologue) or applied in the GEMM prologue."""
     cfg = O.DiT4DiTHeadConfig(num_layers=4, heads=2, head_dim=16, cross_dim=24, output_dim=40, hidden_size=40,
                               action_dim=5, horizon=6, state_dim=16)
-    _, _, out, ref = _run(cfg, B, 40, 11, state_len)
+    head, _, out, ref = _run(cfg, B, 40, 11, state_len, fold)
+    assert head.fold == (fold and B * (6 + state_len) <= 64)
     err = _relerr(out, ref)
-    print(f"tiny DiT4DiT head B={B} state_len={state_len}: relerr {err:.3e}, max|d| {(out - ref).abs().max().item():.3e}")
+    print(f"tiny DiT4DiT head B={B} state_len={state_len} fold={head.fold}: relerr {err:.3e}, "
+          f"max|d| {(out - ref).abs().max().item():.3e}")
     assert err <= 3e-2
 
 

@@ -87,3 +87,46 @@ def test_video_rope_table_matches_oracle():
     from fam.video_dit import video_freqs_3d
     for dh, (f, h, w) in ((128, (2, 30, 26)), (64, (1, 4, 5))):
         assert torch.equal(video_freqs_3d(dh, f, h, w), O.video_freqs(O.precompute_freqs_cis_3d(dh), f, h, w))
+
+
+def test_fold_layernorm_identity_fp64():
+    """fold_layernorm's (w', bias', colsum) reproduce LN -> affine -> AdaLN -> linear through
+    rstd * (x w'^T - mean * colsum) + bias' (evaluated here in fp64 on the CPU); a dropped
+    (1 + scale), a shift folded without the weight, or a wrong colsum fails it."""
+    import torch.nn.functional as F
+    from fam import ops
+    g = torch.Generator().manual_seed(5)
+    M, K, N = 7, 48, 24
+    x = (torch.randn(M, K, generator=g) * 2 + torch.randn(M, 1, generator=g) * 5).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.1).to(torch.bfloat16)
+    b = (torch.randn(N, generator=g) * 0.1).to(torch.bfloat16)
+    lw, lb = torch.randn(K, generator=g) * 0.3 + 1, torch.randn(K, generator=g) * 0.3
+    sc, sh = torch.randn(K, generator=g) * 0.2, torch.randn(K, generator=g) * 0.2
+    eps = 1e-5
+    x64 = x.double()
+    z = F.layer_norm(x64, (K,), eps=eps) * lw.double() + lb.double()
+    z = z * (1 + sc.double()) + sh.double()
+    ref = z @ w.double().t() + b.double()
+    w2, b2, cs = ops.fold_layernorm(w, b, ln_weight=lw, ln_bias=lb, scale=sc, shift=sh)
+    assert w2.dtype == torch.bfloat16 and b2.dtype == torch.bfloat16 and cs.dtype == torch.float32
+    mu = x64.mean(1, keepdim=True)
+    rstd = 1.0 / torch.sqrt(x64.var(1, unbiased=False, keepdim=True) + eps)
+    y = rstd * (x64 @ w2.double().t() - mu * cs.double()[None, :]) + b2.double()
+    err = ((y - ref).abs().max() / ref.abs().max()).item()
+    assert err < 1e-2, err          # bf16 rounding of w' and bias' only
+    # plain LayerNorm: w' is w itself, bias' is bias itself
+    w3, b3, cs3 = ops.fold_layernorm(w, b)
+    assert torch.equal(w3, w) and torch.equal(b3, b)
+    assert torch.allclose(cs3.double(), w.double().sum(1), rtol=1e-6, atol=1e-6)
+
+
+def test_d4d_param_shapes_and_init_match_oracle():
+    from fam import dit4dit as D4
+    for kw in ({}, {"state_dim": 0}, {"num_layers": 3, "heads": 2, "head_dim": 16, "cross_dim": 24, "state_dim": 16}):
+        a, b = D4.DiT4DiTHeadConfig(**kw), O.DiT4DiTHeadConfig(**kw)
+        assert D4.param_shapes(a) == O.d4d_param_shapes(b)
+    small = {"num_layers": 2, "heads": 2, "head_dim": 16, "cross_dim": 24, "output_dim": 40, "hidden_size": 40,
+             "state_dim": 16}
+    pa = D4.synthetic_params(D4.DiT4DiTHeadConfig(**small), 9)
+    pb = O.init_d4d_params(O.DiT4DiTHeadConfig(**small), 9)
+    assert sorted(pa) == sorted(pb) and all(torch.equal(pa[k], pb[k]) for k in pa)

@@ -317,6 +317,57 @@ def test_gemm_adaln_prologue_gate_residual(M, rpb):
     assert relerr(out, ref2) <= TOL
 
 
+@pytest.mark.parametrize("M,K,N,kind", [(1, 768, 768, "adaln"), (17, 768, 2304, "adaln"), (17, 768, 3072, "ln_gelu"),
+                                         (33, 1000, 520, "affine_res"), (64, 3072, 768, "adaln"), (16, 4096, 256, "ln_gelu")])
+def test_gemm_folded_layernorm(M, K, N, kind):
+    """FAM_PRO_LN_FOLDED: rstd (x w'^T - mean colsum) + bias' with the affine / modulation folded by
+    fam.ops.fold_layernorm, against LN -> (affine | AdaLN) -> linear (-> GELU, + residual) in fp32.
+    Rows carry a mean offset of several standard deviations (the pivoted row sums keep the
+    variance exact enough); K = 3072 / 4096 run in several chunks per wave."""
+    from fam import _capi
+    x = rnd(M, K, seed=60, scale=1.0)
+    x = (x.float() + 4.0 * rnd(M, 1, seed=61).float()).to(torch.bfloat16)
+    w, b = rnd(N, K, seed=62, scale=0.02), rnd(N, seed=63, scale=0.02)
+    lw, lb = rnd(K, seed=64, scale=0.3).float() + 1, rnd(K, seed=65, scale=0.3).float()
+    sc, sh = rnd(K, seed=66, scale=0.1), rnd(K, seed=67, scale=0.1)
+    res = rnd(M, N, seed=68)
+    eps = 1e-5
+    if kind == "adaln":
+        h = O.adaln(x.float()[None], sh.float()[None, None], sc.float()[None, None], eps)[0]
+        fold = dict(scale=dev(sc), shift=dev(sh))
+    elif kind == "affine_res":
+        h = O.layer_norm(x.float(), lw, lb, eps)
+        fold = dict(ln_weight=dev(lw), ln_bias=dev(lb))
+    else:
+        h = O.layer_norm(x.float(), None, None, eps)
+        fold = {}
+    ref = O.linear(h, w.float(), b.float())
+    if kind == "ln_gelu":
+        ref = O.gelu_tanh(ref)
+    if kind == "affine_res":
+        ref = res.float() + ref
+    w2, b2, cs = ops().fold_layernorm(dev(w), dev(b), **fold)
+    y = dev(res.clone()) if kind == "affine_res" else torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ops().gemm(dev(x), w2, b2, y, prologue=_capi.FAM_PRO_LN_FOLDED, pro_w=cs, pro_eps=eps,
+               act=_capi.FAM_ACT_GELU_TANH if kind == "ln_gelu" else _capi.FAM_ACT_NONE,
+               res=y if kind == "affine_res" else None)
+    err = relerr(y, ref)
+    print(f"folded LN M={M} K={K} N={N} {kind}: relerr {err:.3e}")
+    assert err <= TOL
+
+
+def test_gemm_folded_layernorm_rejects():
+    from fam import _capi
+    x = torch.zeros(65, 64, dtype=torch.bfloat16, device="cuda")
+    w = torch.zeros(16, 64, dtype=torch.bfloat16, device="cuda")
+    cs = torch.zeros(16, dtype=torch.float32, device="cuda")
+    y = torch.empty(65, 16, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(_capi.FamError):
+        ops().gemm(x, w, None, y, prologue=_capi.FAM_PRO_LN_FOLDED, pro_w=cs)   # M > 64
+    with pytest.raises(ValueError):
+        ops().gemm(x[:8], w, None, y[:8], prologue=_capi.FAM_PRO_LN_FOLDED, pro_w=cs.to(torch.bfloat16))
+
+
 def test_gemm_layernorm_affine_prologue():
     from fam import _capi
     M, K, N = 64, 1024, 1024
