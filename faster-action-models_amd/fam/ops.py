@@ -252,14 +252,12 @@ def _mask_args(mask: Optional[torch.Tensor], B: int, H: int, Sq: int, Sk: int):
     return m4.data_ptr(), kind, m4.stride(0), m4.stride(1), m4.stride(2), m4
 
 
-def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
-                   mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
-                   k_prefix: Optional[torch.Tensor] = None, v_prefix: Optional[torch.Tensor] = None,
-                   out: Optional[torch.Tensor] = None, num_splits: int = 1,
-                   qk_norm: Optional[dict] = None) -> torch.Tensor:
-    """Attention on [B, S, H*Dh] tensors; keys/values are cat(k_prefix, k) when a prefix is
-    given (the MoT joint attention over a cached video K/V, FB/mot.py:446-478) without
-    materialising the concatenation."""
+def _attn_desc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
+               mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+               k_prefix: Optional[torch.Tensor] = None, v_prefix: Optional[torch.Tensor] = None,
+               out: Optional[torch.Tensor] = None, qk_norm: Optional[dict] = None):
+    """fam_attn_desc for [B, S, H*Dh] tensors (see attention_bshd); returns (desc, out, keep),
+    keep = tensors the descriptor points into (a converted mask) that must outlive the launch."""
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _check(t, n)
         if t.dim() != 3:
@@ -313,7 +311,20 @@ def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads:
         if n.get("rope") is not None:
             cs, sn, trs = n["rope"]
             d.rope_cos, d.rope_sin, d.rope_row_stride = cs.data_ptr(), sn.data_ptr(), trs
-    part_o = part_ml = None
+    return d, out, keep
+
+
+def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
+                   mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+                   k_prefix: Optional[torch.Tensor] = None, v_prefix: Optional[torch.Tensor] = None,
+                   out: Optional[torch.Tensor] = None, num_splits: int = 1,
+                   qk_norm: Optional[dict] = None) -> torch.Tensor:
+    """Attention on [B, S, H*Dh] tensors; keys/values are cat(k_prefix, k) when a prefix is
+    given (the MoT joint attention over a cached video K/V, FB/mot.py:446-478) without
+    materialising the concatenation."""
+    d, out, keep = _attn_desc(q, k, v, num_heads, mask, scale, k_prefix, v_prefix, out, qk_norm)
+    B, Sq, ND = q.shape
+    Dh = ND // num_heads
     if num_splits > 1:
         # key splits over workgroups: per-split partials, then an ordered merge
         nq = B * num_heads * Sq
@@ -334,6 +345,24 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads
         raise NotImplementedError("Only compatibility mode is implemented for flash attention. "
                                   "Please set compatibility_mode=True.")
     return attention_bshd(q, k, v, num_heads, ctx_mask)
+
+
+def attention_oproj_partial(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int, w: torch.Tensor,
+                            scale: Optional[float] = None, qk_norm: Optional[dict] = None):
+    """Self-attention of [B, S, H*Dh] q/k/v (S <= 32, B <= 2) fused into the split-K product
+    with w [N, H*Dh] (fam_attention_oproj_partial): returns (partials [P, B*S, N] fp32, P),
+    sum over planes = attention(q, k, v) w^T, in fam_gemm_partial's layout for rowop."""
+    _check(w, "w")
+    d, _, _ = _attn_desc(q, k, v, num_heads, None, scale, None, None, q, qk_norm)
+    N = w.shape[0]
+    P = _capi.lib().fam_attention_oproj_splits(C.byref(d), N)
+    if P < 1:
+        raise ValueError("attention_oproj_partial: unsupported shape (batch <= 2, head_dim 64/128, "
+                         "heads a multiple of (256 / batch) / head_dim)")
+    B, S = q.shape[0], q.shape[1]
+    part = torch.empty((P, B * S, N), dtype=torch.float32, device=q.device)
+    call("fam_attention_oproj_partial", C.byref(d), w.data_ptr(), w.stride(0), part.data_ptr(), N, _stream(q))
+    return part, P
 
 
 # --------------------------------------------------------------------------- linear
