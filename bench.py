@@ -481,7 +481,21 @@ def bench_hbm(args):
         fr = torch.polar(torch.ones_like(ang), ang)
         us = timed(lambda: out.__setitem__(0, ops.rms_norm_rope(x, w, 1e-6, fr, heads)), n)
         rows.append(("rmsnorm + rope (q of config 2)", f"{R}x{D}", 4 * R * D + 4 * 2 * R * (D // heads // 2), us))
-        del x, sh, sc
+        # calibration, not a library kernel: torch's device-to-device copy of the same x (read +
+        # write), timed over n back-to-back copies -- the streaming rate this memory system
+        # delivers at this size
+        y_ = torch.empty_like(x)
+        for _ in range(3):
+            y_.copy_(x)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            y_.copy_(x)
+        e1.record()
+        torch.cuda.synchronize()
+        rows.append(("copy (torch, calibration)", f"{R}x{D}", 4 * R * D, e0.elapsed_time(e1) * 1e3 / n))
+        del x, sh, sc, y_
     for numel in (256 * 8 * 16, 1 << 20, 16 << 20, 64 << 20):
         s_ = torch.randn(numel, generator=g).to(dev, torch.bfloat16)
         v_ = torch.randn(numel, generator=g).to(dev, torch.bfloat16)
@@ -493,7 +507,7 @@ def bench_hbm(args):
               "frac_of_hbm": round(b / (u * 1e-6) / 1e9 / HBM_PEAK_GBS, 3)} for k, sz, b, u in rows]
     for r in table:
         log(f"{r['kernel']:32s} {r['size']:>12s} {r['us']:9.2f} us {r['GBs']:8.1f} GB/s ({100 * r['frac_of_hbm']:.0f}%)")
-    best = max(table, key=lambda r: r["GBs"])
+    best = max((r for r in table if "calibration" not in r["kernel"]), key=lambda r: r["GBs"])
     out = {
         "metric": "achieved HBM GB/s of the norm, RoPE and Euler kernels (size sweep)", "value": best["GBs"],
         "unit": "GB/s", "n_gpus": 1, "steps": n, "warmup": 3, "ms_per_step": None, "higher_is_better": True,

@@ -21,32 +21,32 @@ struct AdalnArgs {
   float eps;
 };
 
-template <int NV>
+// AFF: the LayerNorm affine is present.  MOD: no AdaLN shift-scale (0), one per row (1, an
+// HBM stream: loaded with x), or one per batch (2, an L2-resident row: loaded after the
+// statistics, so its registers do not cost occupancy while x is in flight).  Compile-time,
+// because occupancy is what keeps HBM busy here.
+template <int NV, bool AFF, int MOD>
 __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
   const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= a.rows) return;  // wave-uniform
-  const bf16* xr = a.x + r * a.xrs;
+  const int64_t r0 = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r0 >= a.rows) return;  // wave-uniform
   const int64_t D = a.dim;
   const float invD = 1.0f / (float)D;
-  const int64_t bidx = r / a.rpb, sidx = r - bidx * a.rpb;
-  const int64_t moff = bidx * a.mbs + sidx * a.mrs;
-  bf16* yr = a.y + r * a.yrs;
 
   // LayerNorm of 8 elements (two-pass statistics given), then affine and modulation
   auto finish = [&](const float* xv, float mean, float rstd, bf16x8 wv, bf16x8 bv, bf16x8 sh, bf16x8 sc) {
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = (xv[e] - mean) * rstd;
-    if (a.w) {
+    if (AFF && a.w) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] *= to_f(wv[e]);
     }
-    if (a.b) {
+    if (AFF && a.b) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] += to_f(bv[e]);
     }
-    if (a.shift) {
+    if (MOD) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = o[e] * (1.0f + to_f(sc[e])) + to_f(sh[e]);
     }
@@ -57,52 +57,83 @@ __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
   };
 
   if constexpr (NV > 0) {
-    // Every load of the row (x, LayerNorm affine, shift / scale) is issued before the
-    // statistics, so a wave waits for memory once (the branches are wave-uniform).
-    bf16x8 xv8[NV], wv[NV], bv[NV], sh[NV], sc[NV];
+    // Every load of the row (x, LayerNorm affine, per-row shift / scale) is issued before the
+    // statistics, so a wave waits for memory once; x stays bf16 in registers and is widened in
+    // each pass.
+    constexpr int NA = AFF ? NV : 1, NMD = MOD == 1 ? NV : 1;
+    bf16x8 xv8[1][NV], wv[NA], bv[NA], sh[NMD], sc[NMD];
+    constexpr int RPW = 1;
     auto col = [&](int i) { const int64_t c = ((int64_t)i * 64 + lane) * 8; return c < D ? c : 0; };
 #pragma unroll
-    for (int i = 0; i < NV; ++i) xv8[i] = load8(xr + col(i));
-    if (a.w) {
+    for (int k = 0; k < RPW; ++k) {
+      const int64_t r = r0 + k < a.rows ? r0 + k : a.rows - 1;
 #pragma unroll
-      for (int i = 0; i < NV; ++i) wv[i] = load8(a.w + col(i));
+      for (int i = 0; i < NV; ++i) xv8[k][i] = load8(a.x + r * a.xrs + col(i));
     }
-    if (a.b) {
+    if constexpr (AFF) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) bv[i] = load8(a.b + col(i));
+      for (int i = 0; i < NV; ++i) {
+        wv[i] = a.w ? load8(a.w + col(i)) : xv8[0][i];
+        bv[i] = a.b ? load8(a.b + col(i)) : xv8[0][i];
+      }
     }
-    if (a.shift) {
+    if constexpr (MOD == 1) {
+      const int64_t bidx = r0 / a.rpb, sidx = r0 - bidx * a.rpb;
+      const int64_t moff = bidx * a.mbs + sidx * a.mrs;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         sh[i] = load8(a.shift + moff + col(i));
         sc[i] = load8(a.scale + moff + col(i));
       }
     }
-    float v[NV][8];
-    float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const bool ok = ((int64_t)i * 64 + lane) * 8 < D;
+    for (int k = 0; k < RPW; ++k) {
+      const int64_t r = r0 + k;
+      if (r >= a.rows) break;   // wave-uniform
+      const int64_t bidx = r / a.rpb, sidx = r - bidx * a.rpb;
+      const int64_t moff = bidx * a.mbs + sidx * a.mrs;
+      bf16* yr = a.y + r * a.yrs;
+      float s = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) { v[i][e] = ok ? to_f(xv8[i][e]) : 0.f; s += v[i][e]; }
-    }
-    const float mean = wave_sum(s) * invD;
-    float q = 0.f;
+      for (int i = 0; i < NV; ++i) {
+        if (((int64_t)i * 64 + lane) * 8 < D) {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      if (((int64_t)i * 64 + lane) * 8 < D) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) { const float d = v[i][e] - mean; q += d * d; }
+          for (int e = 0; e < 8; ++e) s += to_f(xv8[k][i][e]);
+        }
       }
-    }
-    const float rstd = rsqrtf(wave_sum(q) * invD + a.eps);
+      const float mean = wave_sum(s) * invD;
+      float q = 0.f;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int64_t c = ((int64_t)i * 64 + lane) * 8;
-      if (c < D) store8(yr + c, finish(v[i], mean, rstd, wv[i], bv[i], sh[i], sc[i]));
+      for (int i = 0; i < NV; ++i) {
+        if (((int64_t)i * 64 + lane) * 8 < D) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) { const float d = to_f(xv8[k][i][e]) - mean; q += d * d; }
+        }
+      }
+      const float rstd = rsqrtf(wave_sum(q) * invD + a.eps);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int64_t c = ((int64_t)i * 64 + lane) * 8;
+        if (c < D) {
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = to_f(xv8[k][i][e]);
+          if constexpr (MOD == 2) {
+            sh[0] = load8(a.shift + moff + c);
+            sc[0] = load8(a.scale + moff + c);
+          }
+          store8(yr + c, finish(v, mean, rstd, wv[AFF ? i : 0], bv[AFF ? i : 0], sh[MOD == 1 ? i : 0],
+                                sc[MOD == 1 ? i : 0]));
+        }
+      }
     }
   } else {
     // wide rows: three passes over x (the re-reads hit L2)
+    const int64_t r = r0;
+    const bf16* xr = a.x + r * a.xrs;
+    const int64_t bidx = r / a.rpb, sidx = r - bidx * a.rpb;
+    const int64_t moff = bidx * a.mbs + sidx * a.mrs;
+    bf16* yr = a.y + r * a.yrs;
     float s = 0.f;
     for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
       bf16x8 t = load8(xr + c);
@@ -123,8 +154,8 @@ __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) xv[e] = to_f(t[e]);
       const bf16x8 z = t;
-      store8(yr + c, finish(xv, mean, rstd, a.w ? load8(a.w + c) : z, a.b ? load8(a.b + c) : z,
-                            a.shift ? load8(a.shift + moff + c) : z, a.shift ? load8(a.scale + moff + c) : z));
+      store8(yr + c, finish(xv, mean, rstd, AFF && a.w ? load8(a.w + c) : z, AFF && a.b ? load8(a.b + c) : z,
+                            MOD ? load8(a.shift + moff + c) : z, MOD ? load8(a.scale + moff + c) : z));
     }
   }
 }
@@ -299,6 +330,20 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_vec_kernel(RmsRopeArgs a) {
 
 using namespace fam;
 
+template <int NV, int MOD>
+static void launch_adaln_m(const AdalnArgs& a, bool aff, hipStream_t s) {
+  const dim3 grid((unsigned)((a.rows + 3) / 4));
+  if (aff) FAM_LAUNCH((adaln_kernel<NV, true, MOD>), grid, dim3(256), 0, s, a);
+  else FAM_LAUNCH((adaln_kernel<NV, false, MOD>), grid, dim3(256), 0, s, a);
+}
+// mod: 0 none, 1 per row, 2 per batch (mod_row_stride 0)
+template <int NV>
+static void launch_adaln(const AdalnArgs& a, bool aff, int mod, hipStream_t s) {
+  if (mod == 1) launch_adaln_m<NV, 1>(a, aff, s);
+  else if (mod == 2) launch_adaln_m<NV, 2>(a, aff, s);
+  else launch_adaln_m<NV, 0>(a, aff, s);
+}
+
 static int nv_for(int64_t dim) {
   const int64_t nv = (dim + 511) / 512;
   if (nv <= 1) return 1;
@@ -332,15 +377,16 @@ extern "C" int fam_adaln(const void* x, int64_t x_row_stride, const void* shift,
   AdalnArgs a{(const bf16*)x, x_row_stride, (const bf16*)shift, (const bf16*)scale, mod_batch_stride,
               mod_row_stride, (const bf16*)ln_weight, (const bf16*)ln_bias, (bf16*)y, y_row_stride,
               rows, rows_per_batch, dim, eps};
-  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
   hipStream_t s = (hipStream_t)stream;
+  const bool aff = ln_weight || ln_bias;
+  const int mod = shift == nullptr ? 0 : (mod_row_stride == 0 && rows_per_batch > 1 ? 2 : 1);
   switch (nv_for(dim)) {
-    case 1: FAM_LAUNCH(adaln_kernel<1>, grid, block, 0, s, a); break;
-    case 2: FAM_LAUNCH(adaln_kernel<2>, grid, block, 0, s, a); break;
-    case 4: FAM_LAUNCH(adaln_kernel<4>, grid, block, 0, s, a); break;
-    case 6: FAM_LAUNCH(adaln_kernel<6>, grid, block, 0, s, a); break;
-    case 8: FAM_LAUNCH(adaln_kernel<8>, grid, block, 0, s, a); break;
-    default: FAM_LAUNCH(adaln_kernel<0>, grid, block, 0, s, a); break;
+    case 1: launch_adaln<1>(a, aff, mod, s); break;
+    case 2: launch_adaln<2>(a, aff, mod, s); break;
+    case 4: launch_adaln<4>(a, aff, mod, s); break;
+    case 6: launch_adaln<6>(a, aff, mod, s); break;
+    case 8: launch_adaln<8>(a, aff, mod, s); break;
+    default: launch_adaln<0>(a, aff, mod, s); break;
   }
   return fam_host::check_launch("fam_adaln");
 }
