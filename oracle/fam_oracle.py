@@ -483,6 +483,48 @@ def mot_action_forward(p: Params, cfg: ActionDiTConfig, x: torch.Tensor, freqs: 
     return x
 
 
+def mot_prefill_video_cache(p: Params, cfg: ActionDiTConfig, x: torch.Tensor, freqs: torch.Tensor,
+                            t_mod: torch.Tensor, context: Optional[torch.Tensor], video_mask: torch.Tensor,
+                            context_mask: Optional[torch.Tensor] = None,
+                            num_run: int = 0) -> List[Tuple[torch.Tensor, torch.Tensor]]:
+    """MoT.prefill_video_cache (FB/mot.py:262-376): the video tokens through the first
+    `num_run` blocks (all when 0 or >= num_layers), returning each block's attention K/V.
+
+    Per block (`_prefill_one_layer`, :360-376, with :63-80, :104-189): AdaLN ->
+    q, k (RMSNorm + RoPE), v -> attention under the [Sv, Sv] video mask -> x += g_msa * o ->
+    (context given) x += cross_attention(norm3(x), context) -> AdaLN -> x += g_mlp * FFN.
+    The cached k is the normalised, rotated key and v the raw value projection.  Blocks past
+    `num_run` reuse the last computed block's K/V (video layer drafting, :345-351)."""
+    L = cfg.num_layers
+    n_run = L if num_run <= 0 or num_run > L else num_run
+    cmask = context_mask
+    if cmask is not None and cmask.dim() == 3:
+        cmask = cmask.unsqueeze(1)
+    cache: List[Tuple[torch.Tensor, torch.Tensor]] = []
+    for i in range(n_run):
+        pre = f"blocks.{i}."
+        sh_a, sc_a, g_a, sh_m, sc_m, g_m = split_modulation(p[pre + "modulation"], t_mod)
+        h = adaln(x, sh_a, sc_a, cfg.eps)
+        sp = pre + "self_attn."
+        q = rms_norm(linear(h, p[sp + "q.weight"], p[sp + "q.bias"]), p[sp + "norm_q.weight"], cfg.eps)
+        k = rms_norm(linear(h, p[sp + "k.weight"], p[sp + "k.bias"]), p[sp + "norm_k.weight"], cfg.eps)
+        v = linear(h, p[sp + "v.weight"], p[sp + "v.bias"])
+        q = rope_apply(q, freqs, cfg.num_heads)
+        k = rope_apply(k, freqs, cfg.num_heads)
+        cache.append((k, v))
+        mixed = flash_attention(q, k, v, cfg.num_heads, video_mask)
+        x = x + g_a * linear(mixed, p[sp + "o.weight"], p[sp + "o.bias"])
+        if context is not None:
+            x = x + cross_attention(p, pre + "cross_attn.",
+                                    layer_norm(x, p[pre + "norm3.weight"], p[pre + "norm3.bias"], cfg.eps),
+                                    context, cfg.num_heads, cfg.eps, cmask)
+        h = adaln(x, sh_m, sc_m, cfg.eps)
+        x = x + g_m * ffn(p, pre, h)
+    while len(cache) < L:
+        cache.append(cache[-1])
+    return cache
+
+
 def mot_joint_mask(video_seq_len: int, action_seq_len: int, video_tokens_per_frame: int) -> torch.Tensor:
     """Joint [video+action] bool mask for first_frame_causal video (FB/fastwam.py:389-410,
     FB/wan_video_dit.py:493-498): video->video first-frame causal, action->action all,

@@ -244,6 +244,47 @@ def test_golden_mot(golden, tiny_params, name, dt):
     assert torch.allclose(y.float(), golden[f"mot.out.{name}"], rtol=rt, atol=at)
 
 
+@pytest.fixture(scope="module")
+def prefill_golden():
+    return load_file(os.path.join(os.path.dirname(__file__), "golden", "mot_prefill_tiny.safetensors"))
+
+
+def _prefill(g, p, dt, num_run):
+    fr = torch.view_as_complex(g["in.freqs_real"].double().contiguous())
+    return O.mot_prefill_video_cache(p, TINY, g["in.x"].to(dt), fr, g["in.t_mod"].to(dt), g["in.context"].to(dt),
+                                     g["in.video_mask"].bool(), g["in.context_mask"].bool(), num_run)
+
+
+@pytest.mark.parametrize("tag,num_run", [("all", 0), ("draft1", 1)])
+@pytest.mark.parametrize("name,dt", [("fp32", torch.float32), ("bf16", torch.bfloat16)])
+def test_golden_mot_prefill(prefill_golden, tiny_params, tag, num_run, name, dt):
+    """The oracle's video K/V prefill against MoT.prefill_video_cache of the reference: every
+    layer's k (normalised, rotated) and v, first-frame-causal video mask, per-token t_mod,
+    ragged text mask; drafted (one layer run, its K/V reused) and full."""
+    g = prefill_golden
+    kv = _prefill(g, O.cast_params(tiny_params, dt), dt, num_run)
+    rt, at = _tol(name)
+    assert len(kv) == TINY.num_layers
+    for i, (k, v) in enumerate(kv):
+        assert torch.allclose(k.float(), g[f"out.{tag}.{name}.k{i}"], rtol=rt, atol=at), (tag, i, "k")
+        assert torch.allclose(v.float(), g[f"out.{tag}.{name}.v{i}"], rtol=rt, atol=at), (tag, i, "v")
+
+
+def test_golden_mot_prefill_detects_planted_mistakes(prefill_golden, tiny_params):
+    """Plausible slips fail the prefill golden: the video mask ignored (bidirectional), or the
+    cached key taken before RoPE."""
+    g = prefill_golden
+    p = O.cast_params(tiny_params, torch.float32)
+    fr = torch.view_as_complex(g["in.freqs_real"].double().contiguous())
+    args = (g["in.x"], fr, g["in.t_mod"], g["in.context"])
+    kv = O.mot_prefill_video_cache(p, TINY, *args, torch.ones_like(g["in.video_mask"].bool()),
+                                   g["in.context_mask"].bool())
+    assert not torch.allclose(kv[1][0], g["out.all.fp32.k1"], rtol=2e-5, atol=2e-5)
+    no_rope = O.mot_prefill_video_cache(p, TINY, g["in.x"], torch.ones_like(fr), g["in.t_mod"], g["in.context"],
+                                        g["in.video_mask"].bool(), g["in.context_mask"].bool())
+    assert not torch.allclose(no_rope[0][0], g["out.all.fp32.k0"], rtol=2e-5, atol=2e-5)
+
+
 def test_golden_detects_planted_mistake(golden, tiny_params):
     """A dropped term in the block (no cross-attention) must fail the golden comparison."""
     p = O.cast_params(tiny_params, torch.float32)
