@@ -55,12 +55,28 @@ def video_freqs_3d(head_dim: int, f: int, h: int, w: int):
 
 
 class FusedVideoDiTBlock:
-    """One DiT block (the reference's `blocks.{idx}.` parameters) for fixed (B, S, Lc)."""
+    """One DiT block (the reference's `blocks.{idx}.` parameters) for fixed (B, S, Lc).
+
+    Optional, for the MoT video prefill (FB/mot.py:262-376):
+        self_mask: bool [S, S] on the self-attention (True = attend), shared by batch and heads.
+        ctx_mask: bool [B, S, Lc] on the cross-attention (the video context payload's mask).
+        ctx_len = 0: no cross-attention (a prefill without a context payload).
+        shared: buffers to use instead of allocating ("x", "tmod_in", "ctx" and the scratch
+            "mods", "h", "attn", "qc", "ckv", "hid"), so that blocks chain in place.
+        kv_only: build only what the block's K/V need -- modulation, AdaLN1, the q/k/v
+            projection and the key's RMSNorm + RoPE -- for a last prefill block whose output
+            nobody reads.
+    `self.qkv` holds [q | k | v] per row; after `run()` its k (normalised, rotated) and v
+    columns are the block's attention K/V (`kv()`).
+    """
 
     def __init__(self, params: Dict[str, torch.Tensor], idx: int, *, hidden: int, num_heads: int, head_dim: int,
                  ffn_dim: int, batch: int, seq_len: int, ctx_len: int, freqs: torch.Tensor, eps: float = 1e-6,
-                 per_token_mod: bool = True, device="cuda"):
+                 per_token_mod: bool = True, device="cuda", self_mask: Optional[torch.Tensor] = None,
+                 ctx_mask: Optional[torch.Tensor] = None, shared: Optional[Dict[str, torch.Tensor]] = None,
+                 kv_only: bool = False):
         dev = torch.device(device)
+        self.kv_only = kv_only
         self.lib = _capi.load()
         self.B, self.S, self.Lc = batch, seq_len, ctx_len
         self.H, self.nh, self.Dh, self.F = hidden, num_heads, head_dim, ffn_dim
@@ -93,17 +109,34 @@ class FusedVideoDiTBlock:
         cos, sin, trs, tes = rope_tables(freqs, "complex", dev)
         self.rope = (cos, sin, trs, tes)
 
-        z = lambda *s: torch.zeros(*s, dtype=_BF16, device=dev)  # noqa: E731
-        self.x = z(M, H)
-        self.tmod_in = z(M if per_token_mod else batch, 6 * H)
-        self.ctx = z(batch * ctx_len, H)
-        self.mods = z(M if per_token_mod else batch, 6 * H)
-        self.h = z(M, H)
-        self.qkv = z(M, 3 * A)
-        self.attn = z(M, A)
-        self.qc = z(M, A)
-        self.ckv = z(batch * ctx_len, 2 * A)
-        self.hid = z(M, F)
+        sh = shared or {}
+
+        def buf(name, *shape):
+            t = sh.get(name)
+            if t is None:
+                return torch.zeros(*shape, dtype=_BF16, device=dev)
+            if tuple(t.shape) != tuple(shape) or t.dtype != _BF16 or not t.is_contiguous():
+                raise ValueError(f"shared buffer {name!r} must be contiguous bf16 {tuple(shape)}")
+            return t
+        self.x = buf("x", M, H)
+        self.tmod_in = buf("tmod_in", M if per_token_mod else batch, 6 * H)
+        self.ctx = buf("ctx", batch * ctx_len, H)
+        self.mods = buf("mods", M if per_token_mod else batch, 6 * H)
+        self.h = buf("h", M, H)
+        self.qkv = torch.zeros(M, 3 * A, dtype=_BF16, device=dev)   # per block: its K/V cache
+        self.attn = buf("attn", M, A)
+        self.qc = buf("qc", M, A)
+        self.ckv = buf("ckv", batch * ctx_len, 2 * A)
+        self.hid = buf("hid", M, F)
+        if self_mask is not None:
+            self_mask = self_mask.to(device=dev, dtype=torch.bool).contiguous()
+            if tuple(self_mask.shape) != (seq_len, seq_len):
+                raise ValueError(f"self_mask must be bool [S, S] = [{seq_len}, {seq_len}]")
+        if ctx_mask is not None:
+            ctx_mask = ctx_mask.to(device=dev, dtype=torch.bool).contiguous()
+            if tuple(ctx_mask.shape) != (batch, seq_len, ctx_len):
+                raise ValueError(f"ctx_mask must be bool [B, S, Lc] = [{batch}, {seq_len}, {ctx_len}]")
+        self.self_mask, self.ctx_mask = self_mask, ctx_mask
         self._descs: List = []
         self.steps: List = []
         self.meta: List[dict] = []
@@ -155,7 +188,7 @@ class FusedVideoDiTBlock:
                 cs.data_ptr() if cs is not None else None, sn.data_ptr() if sn is not None else None, trs, tes, Dh)
         self._add(name, "fam_rmsnorm_rope", args, "rmsnorm_rope")
 
-    def _attention(self, name, q, q_rs, k, k_rs, v, v_rs, sq, sk, kv_batch_rows):
+    def _attention(self, name, q, q_rs, k, k_rs, v, v_rs, sq, sk, kv_batch_rows, mask=None, mask_strides=(0, 0, 0)):
         d = _capi.AttnDesc()
         A, Dh = self.A, self.Dh
         d.q, d.q_bs, d.q_rs, d.q_hs = q, sq * q_rs, q_rs, Dh
@@ -165,6 +198,9 @@ class FusedVideoDiTBlock:
         d.batch, d.heads, d.sq, d.sk0, d.sk1, d.head_dim = self.B, self.nh, sq, sk, 0, Dh
         d.scale = 1.0 / math.sqrt(Dh)
         d.num_splits = 1
+        if mask is not None:   # bool, [b, q, k] strides (mask_bs, mask_qs) and no head stride
+            d.mask, d.mask_kind = mask.data_ptr(), _capi.FAM_MASK_BOOL
+            d.mask_bs, d.mask_hs, d.mask_qs = mask_strides
         self._descs.append(d)
         self._add(name, "fam_attention", (C.byref(d),), "attention", 4 * self.B * self.nh * sq * sk * Dh)
 
@@ -183,19 +219,24 @@ class FusedVideoDiTBlock:
         self._adaln("adaln1", self.x, self.h, shift=mod(0), scale=mod(1))
         self._gemm("qkv", self.h, w["qkv_w"], w["qkv_b"], self.qkv)
         qp = self.qkv.data_ptr()
-        self._rms("q_norm_rope", qp, 3 * A, M, S, w["nq"], True)
         self._rms("k_norm_rope", qp + 2 * A, 3 * A, M, S, w["nk"], True)
-        self._attention("self_attn", qp, 3 * A, qp + 2 * A, 3 * A, qp + 4 * A, 3 * A, S, S, S)
+        if self.kv_only:
+            return
+        self._rms("q_norm_rope", qp, 3 * A, M, S, w["nq"], True)
+        self._attention("self_attn", qp, 3 * A, qp + 2 * A, 3 * A, qp + 4 * A, 3 * A, S, S, S,
+                        mask=self.self_mask, mask_strides=(0, 0, S))
         self._gemm("o", self.attn, w["o_w"], w["o_b"], self.x, res=self.x, gate=mod(2), gate_strides=gstr)
         # cross-attention
-        self._adaln("norm3", self.x, self.h, lw=w["n3_w"], lb=w["n3_b"])
-        self._gemm("cross_q", self.h, w["cq_w"], w["cq_b"], self.qc)
-        self._rms("cross_q_norm", self.qc.data_ptr(), A, M, S, w["cnq"], False)
-        self._gemm("cross_kv", self.ctx, w["ckv_w"], w["ckv_b"], self.ckv)
-        kp = self.ckv.data_ptr()
-        self._rms("cross_k_norm", kp, 2 * A, self.B * Lc, Lc, w["cnk"], False)
-        self._attention("cross_attn", self.qc.data_ptr(), A, kp, 2 * A, kp + 2 * A, 2 * A, S, Lc, Lc)
-        self._gemm("cross_o", self.attn, w["co_w"], w["co_b"], self.x, res=self.x)
+        if Lc > 0:
+            self._adaln("norm3", self.x, self.h, lw=w["n3_w"], lb=w["n3_b"])
+            self._gemm("cross_q", self.h, w["cq_w"], w["cq_b"], self.qc)
+            self._rms("cross_q_norm", self.qc.data_ptr(), A, M, S, w["cnq"], False)
+            self._gemm("cross_kv", self.ctx, w["ckv_w"], w["ckv_b"], self.ckv)
+            kp = self.ckv.data_ptr()
+            self._rms("cross_k_norm", kp, 2 * A, self.B * Lc, Lc, w["cnk"], False)
+            self._attention("cross_attn", self.qc.data_ptr(), A, kp, 2 * A, kp + 2 * A, 2 * A, S, Lc, Lc,
+                            mask=self.ctx_mask, mask_strides=(S * Lc, 0, Lc))
+            self._gemm("cross_o", self.attn, w["co_w"], w["co_b"], self.x, res=self.x)
         # FFN
         self._adaln("adaln2", self.x, self.h, shift=mod(3), scale=mod(4))
         self._gemm("ffn_up", self.h, w["f0_w"], w["f0_b"], self.hid, act=_capi.FAM_ACT_GELU_TANH)
@@ -236,3 +277,92 @@ class FusedVideoDiTBlock:
         self.set_inputs(x, t_mod, context)
         self.run()
         return self.x.clone().view(self.B, self.S, self.H)
+
+    def kv(self):
+        """The block's attention K (normalised, rotated) and V as [B, S, A] views of `qkv`."""
+        q3 = self.qkv.view(self.B, self.S, 3 * self.A)
+        return q3[:, :, self.A:2 * self.A], q3[:, :, 2 * self.A:]
+
+
+class FusedVideoPrefill:
+    """MoT.prefill_video_cache (FB/mot.py:262-376) of the video expert for fixed (B, Sv, Lc):
+    the video tokens through the expert's first `num_run` blocks (all when 0), keeping each
+    block's attention K/V.  The blocks share the residual stream, t_mod, context and scratch
+    buffers and run back to back (one graph with `capture()`); each keeps its own q/k/v buffer,
+    whose k and v columns are the cache (`kv_cache()`, views valid until the next run).  The
+    last block run builds only its K/V -- its output is not part of the cache -- and blocks
+    past `num_run` reuse that block's K/V (video layer drafting, FB/mot.py:345-351).
+
+    Args: as FusedVideoDiTBlock, plus num_layers (the expert's depth), video_mask bool [Sv, Sv]
+    (None: every key), ctx_mask bool [B, Sv, Lc] (None: every context token), ctx_len 0 for a
+    prefill without a context payload.
+    """
+
+    def __init__(self, params: Dict[str, torch.Tensor], *, num_layers: int, hidden: int, num_heads: int,
+                 head_dim: int, ffn_dim: int, batch: int, video_len: int, ctx_len: int, freqs: torch.Tensor,
+                 eps: float = 1e-6, per_token_mod: bool = True, video_mask: Optional[torch.Tensor] = None,
+                 ctx_mask: Optional[torch.Tensor] = None, num_run: int = 0, device="cuda"):
+        dev = torch.device(device)
+        self.L = num_layers
+        self.n_run = num_layers if num_run <= 0 or num_run > num_layers else num_run
+        self.B, self.S, self.Lc, self.H, self.A = batch, video_len, ctx_len, hidden, num_heads * head_dim
+        M = batch * video_len
+        z = lambda *s: torch.zeros(*s, dtype=_BF16, device=dev)  # noqa: E731
+        rows = M if per_token_mod else batch
+        self.shared = {"x": z(M, hidden), "tmod_in": z(rows, 6 * hidden), "ctx": z(batch * ctx_len, hidden),
+                       "mods": z(rows, 6 * hidden), "h": z(M, hidden), "attn": z(M, self.A), "qc": z(M, self.A),
+                       "ckv": z(batch * ctx_len, 2 * self.A), "hid": z(M, ffn_dim)}
+        self.blocks = [FusedVideoDiTBlock(params, i, hidden=hidden, num_heads=num_heads, head_dim=head_dim,
+                                          ffn_dim=ffn_dim, batch=batch, seq_len=video_len, ctx_len=ctx_len,
+                                          freqs=freqs, eps=eps, per_token_mod=per_token_mod, device=dev,
+                                          self_mask=video_mask, ctx_mask=ctx_mask, shared=self.shared,
+                                          kv_only=(i == self.n_run - 1))
+                       for i in range(self.n_run)]
+        self.steps = [f for b in self.blocks for f in b.steps]
+        self.meta = [m for b in self.blocks for m in b.meta]
+        self.graph: Optional[torch.cuda.CUDAGraph] = None
+
+    @property
+    def num_launches(self) -> int:
+        return len(self.steps)
+
+    def set_inputs(self, x: torch.Tensor, t_mod: torch.Tensor, context: Optional[torch.Tensor]) -> None:
+        """x [B, Sv, H]; t_mod [B, Sv, 6, H] (per token) or [B, 6, H]; context [B, Lc, H] (bf16)."""
+        sh = self.shared
+        sh["x"].copy_(x.reshape(sh["x"].shape))
+        sh["tmod_in"].copy_(t_mod.reshape(sh["tmod_in"].shape))
+        if self.Lc > 0:
+            sh["ctx"].copy_(context.reshape(sh["ctx"].shape))
+
+    def run(self) -> None:
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            s = torch.cuda.current_stream().cuda_stream
+            for f in self.steps:
+                f(s)
+
+    def capture(self) -> None:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for f in self.steps:
+                f(s.cuda_stream)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            st = torch.cuda.current_stream().cuda_stream
+            for f in self.steps:
+                f(st)
+        self.graph = g
+
+    def kv_cache(self):
+        """[(k, v)] for every one of the expert's num_layers blocks, [B, Sv, A] views."""
+        kv = [b.kv() for b in self.blocks]
+        return kv + [kv[-1]] * (self.L - self.n_run)
+
+    def prefill(self, x: torch.Tensor, t_mod: torch.Tensor, context: Optional[torch.Tensor]):
+        self.set_inputs(x, t_mod, context)
+        self.run()
+        return self.kv_cache()
