@@ -56,12 +56,13 @@ def parse():
     ap.add_argument("--no-eager", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--cpu-sample-s", type=float, default=20.0, help="CPU baseline time budget")
-    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "hbm"], default="c1",
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "hbm", "prefill"], default="c1",
                     help="c1: the action-DiT denoise loop (the metric); c2: one long-sequence video DiT block "
                          "(config 2 shape), reported as ms per 30-block forward with MFMA utilisation; c3: the "
                          "compact expert loop + action-VAE decoder at B=1 and B=256; c4: the DiT4DiT flow-matching "
                          "head (DiT-B, 16 blocks, 4 steps) over 2048 VLM tokens; hbm: size sweep of the "
-                         "HBM-bound kernels (AdaLN, RMSNorm+RoPE, Euler) from config 2 / config 3 B=256 shapes up")
+                         "HBM-bound kernels (AdaLN, RMSNorm+RoPE, Euler) from config 2 / config 3 B=256 shapes up; "
+                         "prefill: the MoT video K/V prefill of the FastWAM call (30 blocks, 98 video tokens)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
@@ -521,6 +522,84 @@ def bench_hbm(args):
     print(json.dumps(out), flush=True)
 
 
+# --------------------------------------------------------------------------- video K/V prefill
+def bench_prefill(args):
+    """The MoT video K/V prefill of the real FastWAM call (FB/mot.py:262-376, called at
+    FB/fastwam.py:1032-1041): the first frame's 98 video tokens through the 30 blocks of the
+    Wan2.2-5B-style video expert (hidden 3072, 24 x 128 heads, FFN 14336) with per-token t_mod
+    and cross-attention to 129 context tokens, keeping every block's K/V; one captured graph.
+    HBM-bound on the weights (M = 98 rows per projection): `roofline` divides the weight bytes
+    one prefill reads by its time."""
+    import torch
+    from fam.video_dit import FusedVideoPrefill
+    dev = torch.device("cuda:0")
+    L, H, nh, Dh, F, Sv, Lc = 30, 3072, 24, 128, 14336, 98, 129
+    A = nh * Dh
+    g = torch.Generator(device=dev).manual_seed(4321)
+
+    def rn(*shape, std=0.02):
+        return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * std).to(torch.bfloat16)
+    ones = lambda n: torch.ones(n, device=dev, dtype=torch.bfloat16)   # noqa: E731
+    zeros = lambda n: torch.zeros(n, device=dev, dtype=torch.bfloat16)  # noqa: E731
+    params = {}
+    for i in range(L):
+        b = f"blocks.{i}."
+        for n in "qkvo":
+            params[b + f"self_attn.{n}.weight"] = rn(A if n != "o" else H, H if n != "o" else A)
+            params[b + f"self_attn.{n}.bias"] = rn(A if n != "o" else H)
+            params[b + f"cross_attn.{n}.weight"] = rn(A if n != "o" else H, H if n != "o" else A)
+            params[b + f"cross_attn.{n}.bias"] = rn(A if n != "o" else H)
+        for n in ("self_attn.norm_q", "self_attn.norm_k", "cross_attn.norm_q", "cross_attn.norm_k"):
+            params[b + n + ".weight"] = ones(A)
+        params[b + "norm3.weight"], params[b + "norm3.bias"] = ones(H), zeros(H)
+        params[b + "ffn.0.weight"], params[b + "ffn.0.bias"] = rn(F, H), rn(F)
+        params[b + "ffn.2.weight"], params[b + "ffn.2.bias"] = rn(H, F), rn(H)
+        params[b + "modulation"] = rn(1, 6, H, std=1.0 / math.sqrt(H))
+    from fam.video_dit import video_freqs_3d
+    freqs = video_freqs_3d(Dh, 1, 7, 14)   # one latent frame, 7 x 14 patches = 98 tokens
+    pf = FusedVideoPrefill(params, num_layers=L, hidden=H, num_heads=nh, head_dim=Dh, ffn_dim=F, batch=1,
+                           video_len=Sv, ctx_len=Lc, freqs=freqs, device=dev)
+    del params
+    torch.cuda.empty_cache()
+    gi = torch.Generator("cpu").manual_seed(99)
+    x = torch.randn(1, Sv, H, generator=gi).to(dev, torch.bfloat16)
+    tm = (torch.randn(1, Sv, 6, H, generator=gi) * 0.2).to(dev, torch.bfloat16)
+    ctx = torch.randn(1, Lc, H, generator=gi).to(dev, torch.bfloat16)
+    pf.set_inputs(x, tm, ctx)
+    pf.run()
+    torch.cuda.synchronize()
+    pf.capture()
+    for _ in range(args.warmup):
+        pf.run()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        pf.run()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    p50 = statistics.median(times)
+    full = 2 * (3 * A * H + H * A + A * H + 2 * A * H + H * A + 2 * H * F)   # weight bytes of one block
+    wbytes = (L - 1) * full + 2 * 3 * A * H                                  # the last block: q/k/v only
+    gbs = wbytes / (p50 * 1e-3) / 1e9
+    out = {
+        "metric": "p50 ms per video K/V prefill (30 blocks, 98 video tokens, bs=1)", "value": round(p50, 4),
+        "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(p50, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) tokens/context, N(0,0.02) weights, modulation N(0,1/H)",
+        "config": {"workload": "MoT video K/V prefill of the FastWAM call: Wan2.2-5B-style video expert, 30 blocks, "
+                               "hidden 3072, 24x128 heads, FFN 14336, 98 tokens (1 x 7 x 14 grid, 3-D RoPE), "
+                               "per-token t_mod, 129 context tokens", "batch": 1, "video_tokens": Sv,
+                   "context_tokens": Lc, "blocks": L},
+        "min_ms": round(min(times), 4), "p90_ms": round(sorted(times)[int(0.9 * (len(times) - 1))], 4),
+        "launches_per_call": pf.num_launches,
+        "roofline": {"kernel": "whole prefill (weight stream)", "bound": "hbm", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "alg_bytes_per_call": wbytes},
+    }
+    print(json.dumps(out), flush=True)
+
+
 # --------------------------------------------------------------------------- config 3: compact expert + decoder
 def bench_c3(args):
     """Config 3: the compact action expert (hidden 32, 4 x 8 heads, 8 blocks) denoising an 8 x 16
@@ -613,6 +692,9 @@ def main():
         return
     if args.workload == "c3":
         bench_c3(args)
+        return
+    if args.workload == "prefill":
+        bench_prefill(args)
         return
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)

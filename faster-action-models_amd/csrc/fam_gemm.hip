@@ -19,7 +19,7 @@
 //     the epilogue runs one output element per thread.
 //   Bytes per launch (HBM roofline numerator): 2*(N*K + M*K + M*N) + bias/residual/modulation.
 //
-// partial_kernel (M <= 64, used by the fused action expert): split-K without any
+// partial_kernel (M <= 128, used by the fused action expert and the video prefill): split-K without any
 // cross-workgroup traffic.  A workgroup of 4 waves owns 16 output columns over one K slice
 // and its waves split the slice again (summed through LDS); every weight and activation
 // fragment of a wave is loaded before the first MFMA.  The slice length is chosen so that
@@ -1073,15 +1073,15 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
 
 // Split plan of fam_gemm_partial: STEPS (32-wide k-steps per wave; a workgroup covers
 // 4*32*STEPS of K) is the longest of 8, 4, 2, 1 that still gives >= 256 workgroups (one per
-// CU), so the partial planes are as few as the machine's width allows.
+// CU), so the partial planes are as few as the machine's width allows.  Above 64 rows the
+// eight m-tiles' activation fragments cap STEPS at 4 (registers).
 static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* splits) {
   const int64_t groups = (N + 15) / 16;
   const int64_t ksteps = (K + 31) / 32;
-  int st = 8;
+  int st = M > 64 ? 4 : 8;
   while (st > 1 && ((ksteps + 4 * st - 1) / (4 * st)) * groups < 256) st >>= 1;
   *steps = st;
   *splits = (int)((ksteps + 4 * st - 1) / (4 * st));
-  (void)M;
 }
 
 extern "C" int fam_gemm_partial_splits(int64_t M, int64_t N, int64_t K) {
@@ -1098,15 +1098,17 @@ static void launch_partial(const PartArgs& a, int steps, int splits, hipStream_t
     case 1: FAM_LAUNCH((partial_kernel<MT, 1>), grid, dim3(256), 0, s, a); break;
     case 2: FAM_LAUNCH((partial_kernel<MT, 2>), grid, dim3(256), 0, s, a); break;
     case 4: FAM_LAUNCH((partial_kernel<MT, 4>), grid, dim3(256), 0, s, a); break;
-    default: FAM_LAUNCH((partial_kernel<MT, 8>), grid, dim3(256), 0, s, a); break;
+    default:
+      if constexpr (MT <= 4) FAM_LAUNCH((partial_kernel<MT, 8>), grid, dim3(256), 0, s, a);
+      break;
   }
 }
 
 extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64_t ldw, float* partials,
                                 int64_t M, int64_t N, int64_t K, void* stream) {
   FAM_REQUIRE(a && w && partials, FAM_ERR_INVALID_ARG, "fam_gemm_partial: null pointer");
-  FAM_REQUIRE(M >= 0 && M <= 64 && N >= 1 && K >= 8 && K % 8 == 0, FAM_ERR_INVALID_ARG,
-              "fam_gemm_partial: need 0 <= M <= 64, N >= 1, K a positive multiple of 8 (M=%lld N=%lld K=%lld)",
+  FAM_REQUIRE(M >= 0 && M <= 128 && N >= 1 && K >= 8 && K % 8 == 0, FAM_ERR_INVALID_ARG,
+              "fam_gemm_partial: need 0 <= M <= 128, N >= 1, K a positive multiple of 8 (M=%lld N=%lld K=%lld)",
               (long long)M, (long long)N, (long long)K);
   FAM_REQUIRE(lda >= K && ldw >= K && lda % 8 == 0 && ldw % 8 == 0, FAM_ERR_INVALID_ARG,
               "fam_gemm_partial: lda/ldw must be >= K and multiples of 8");
@@ -1120,7 +1122,8 @@ extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64
   hipStream_t s = (hipStream_t)stream;
   if (M <= 16) launch_partial<1>(pa, steps, splits, s);
   else if (M <= 32) launch_partial<2>(pa, steps, splits, s);
-  else launch_partial<4>(pa, steps, splits, s);
+  else if (M <= 64) launch_partial<4>(pa, steps, splits, s);
+  else launch_partial<8>(pa, steps, splits, s);
   return fam_host::check_launch("fam_gemm_partial");
 }
 

@@ -128,6 +128,18 @@ class FusedVideoDiTBlock:
         self.qc = buf("qc", M, A)
         self.ckv = buf("ckv", batch * ctx_len, 2 * A)
         self.hid = buf("hid", M, F)
+        # <= 128 rows (the video prefill at 98 tokens): the N = hidden projections stream their
+        # weights through fam_gemm_partial (split-K over >= 256 workgroups, every load issued
+        # at once) and a row kernel applies bias / gate / residual (and the cross query's
+        # RMSNorm); the tiled GEMM's k-loop would wait on memory once per 64-wide k-block
+        self.splitk = M <= 128 and H <= 4096 and A <= 4096
+        if self.splitk:
+            need = max(self.lib.fam_gemm_partial_splits(M, n_, k_) * M * n_
+                       for n_, k_ in ((H, A), (A, H), (H, F)))
+            t = sh.get("part")
+            if t is not None and (t.dtype != torch.float32 or t.numel() < need):
+                raise ValueError(f"shared buffer 'part' must be fp32 with >= {need} elements")
+            self.part = t if t is not None else torch.zeros(need, dtype=torch.float32, device=dev)
         if self_mask is not None:
             self_mask = self_mask.to(device=dev, dtype=torch.bool).contiguous()
             if tuple(self_mask.shape) != (seq_len, seq_len):
@@ -171,6 +183,53 @@ class FusedVideoDiTBlock:
         d.rows_per_batch = self.S if M == self.B * self.S else M
         self._descs.append(d)
         self._add(name, "fam_gemm", (C.byref(d),), "gemm", 2 * M * N * K)
+
+    def _partial(self, name, a, w):
+        """Split-K partials of a [M, K] x w[N, K]^T into self.part; returns the plane count."""
+        M, K = a.shape
+        N = w.shape[0]
+        splits = self.lib.fam_gemm_partial_splits(M, N, K)
+        self._add(name, "fam_gemm_partial", (a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0),
+                                             self.part.data_ptr(), M, N, K), "gemm_partial", 2 * M * N * K)
+        return splits
+
+    def _rowop(self, name, *, N, splits, bias, out, res=None, gate=None, gate_strides=(0, 0, 1), rms_w=None):
+        """out = res + gate * (sum of the partial planes + bias) (or the plain sum + bias), then,
+        with rms_w, RMSNorm of the row over N with that weight, in place."""
+        M = self.B * self.S
+        d = _capi.RowopDesc()
+        d.src = _capi.FAM_ROWSRC_PARTIALS
+        d.partials, d.splits, d.split_stride = self.part.data_ptr(), splits, M * N
+        d.M, d.N = M, N
+        d.bias = bias.data_ptr()
+        d.act = _capi.FAM_ACT_NONE
+        if res is not None:
+            d.res, d.ldr = res.data_ptr(), res.stride(0)
+        d.gate = gate.data_ptr() if gate is not None else None
+        d.gate_bs, d.gate_rs, d.gate_ns = gate_strides
+        d.rows_per_batch = self.S
+        d.out, d.ldo, d.out_f32 = out.data_ptr(), out.stride(0), 0
+        d.eps = self.eps
+        if rms_w is not None:
+            d.norm = _capi.FAM_ROWNORM_RMS
+            d.nseg = 1
+            d.seg_col0[0], d.seg_weight[0] = 0, rms_w.data_ptr()
+            d.seg_width = N
+            d.nout, d.ldn = out.data_ptr(), out.stride(0)
+        self._descs.append(d)
+        self._add(name, "fam_rowop", (C.byref(d),), "rowop")
+
+    def _proj(self, name, a, w, bias, out, res=None, gate=None, gate_strides=(0, 0, 1), rms_w=None):
+        """out = [res +] [gate *] (a w^T + bias) [then RMSNorm]: split-K + row kernel at <= 128
+        rows, otherwise one fam_gemm (+ fam_rmsnorm_rope for the norm)."""
+        if self.splitk:
+            sp = self._partial(name, a, w)
+            self._rowop(name + "_row", N=w.shape[0], splits=sp, bias=bias, out=out, res=res, gate=gate,
+                        gate_strides=gate_strides, rms_w=rms_w)
+        else:
+            self._gemm(name, a, w, bias, out, res=res, gate=gate, gate_strides=gate_strides)
+            if rms_w is not None:
+                self._rms(name + "_norm", out.data_ptr(), out.stride(0), out.shape[0], self.S, rms_w, False)
 
     def _adaln(self, name, x, y, shift=None, scale=None, lw=None, lb=None):
         M, H = x.shape
@@ -225,22 +284,21 @@ class FusedVideoDiTBlock:
         self._rms("q_norm_rope", qp, 3 * A, M, S, w["nq"], True)
         self._attention("self_attn", qp, 3 * A, qp + 2 * A, 3 * A, qp + 4 * A, 3 * A, S, S, S,
                         mask=self.self_mask, mask_strides=(0, 0, S))
-        self._gemm("o", self.attn, w["o_w"], w["o_b"], self.x, res=self.x, gate=mod(2), gate_strides=gstr)
+        self._proj("o", self.attn, w["o_w"], w["o_b"], self.x, res=self.x, gate=mod(2), gate_strides=gstr)
         # cross-attention
         if Lc > 0:
             self._adaln("norm3", self.x, self.h, lw=w["n3_w"], lb=w["n3_b"])
-            self._gemm("cross_q", self.h, w["cq_w"], w["cq_b"], self.qc)
-            self._rms("cross_q_norm", self.qc.data_ptr(), A, M, S, w["cnq"], False)
+            self._proj("cross_q", self.h, w["cq_w"], w["cq_b"], self.qc, rms_w=w["cnq"])
             self._gemm("cross_kv", self.ctx, w["ckv_w"], w["ckv_b"], self.ckv)
             kp = self.ckv.data_ptr()
             self._rms("cross_k_norm", kp, 2 * A, self.B * Lc, Lc, w["cnk"], False)
             self._attention("cross_attn", self.qc.data_ptr(), A, kp, 2 * A, kp + 2 * A, 2 * A, S, Lc, Lc,
                             mask=self.ctx_mask, mask_strides=(S * Lc, 0, Lc))
-            self._gemm("cross_o", self.attn, w["co_w"], w["co_b"], self.x, res=self.x)
+            self._proj("cross_o", self.attn, w["co_w"], w["co_b"], self.x, res=self.x)
         # FFN
         self._adaln("adaln2", self.x, self.h, shift=mod(3), scale=mod(4))
         self._gemm("ffn_up", self.h, w["f0_w"], w["f0_b"], self.hid, act=_capi.FAM_ACT_GELU_TANH)
-        self._gemm("ffn_down", self.hid, w["f2_w"], w["f2_b"], self.x, res=self.x, gate=mod(5), gate_strides=gstr)
+        self._proj("ffn_down", self.hid, w["f2_w"], w["f2_b"], self.x, res=self.x, gate=mod(5), gate_strides=gstr)
 
     # ------------------------------------------------------------------ execution
     def set_inputs(self, x: torch.Tensor, t_mod: torch.Tensor, context: torch.Tensor) -> None:
@@ -312,6 +370,11 @@ class FusedVideoPrefill:
         self.shared = {"x": z(M, hidden), "tmod_in": z(rows, 6 * hidden), "ctx": z(batch * ctx_len, hidden),
                        "mods": z(rows, 6 * hidden), "h": z(M, hidden), "attn": z(M, self.A), "qc": z(M, self.A),
                        "ckv": z(batch * ctx_len, 2 * self.A), "hid": z(M, ffn_dim)}
+        if M <= 128:   # one split-K partial buffer for every block
+            lib = _capi.load()
+            need = max(lib.fam_gemm_partial_splits(M, n_, k_) * M * n_
+                       for n_, k_ in ((hidden, self.A), (self.A, hidden), (hidden, ffn_dim)))
+            self.shared["part"] = torch.zeros(need, dtype=torch.float32, device=dev)
         self.blocks = [FusedVideoDiTBlock(params, i, hidden=hidden, num_heads=num_heads, head_dim=head_dim,
                                           ffn_dim=ffn_dim, batch=batch, seq_len=video_len, ctx_len=ctx_len,
                                           freqs=freqs, eps=eps, per_token_mod=per_token_mod, device=dev,

@@ -247,7 +247,7 @@ typedef struct fam_gemm_desc {
 int fam_gemm(const fam_gemm_desc* d, void* stream);
 
 /*
- * fam_gemm_partial -- split-K product for 1 <= M <= 64 rows without any cross-workgroup
+ * fam_gemm_partial -- split-K product for 1 <= M <= 128 rows without any cross-workgroup
  * traffic: partials[z][m][n] = sum over k in split z of a[m, k] * w[n, k], fp32,
  * z < fam_gemm_partial_splits(M, N, K) (a deterministic function of the shape).  The caller
  * allocates splits*M*N floats and sums them with fam_rowop, which also applies the
@@ -255,7 +255,7 @@ int fam_gemm(const fam_gemm_desc* d, void* stream);
  * Replaces: the projections of the action tokens (q/k/v/o, cross q/o, FFN up/down, head;
  *           FB/wan_video_dit.py:188-191,215-218,262-263, FB/action_dit.py:317-318) and the
  *           reference's split-K kernel fastwam::skmm (FG/mot.py:1080-1243).
- * Limits: M <= 64; K % 8 == 0; lda, ldw multiples of 8; 16-byte aligned a, w, partials.
+ * Limits: M <= 128; K % 8 == 0; lda, ldw multiples of 8; 16-byte aligned a, w, partials.
  */
 int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64_t ldw, float* partials,
                      int64_t M, int64_t N, int64_t K, void* stream);
