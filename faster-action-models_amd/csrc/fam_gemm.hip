@@ -482,6 +482,71 @@ __global__ __launch_bounds__(256) void partial_kernel(PartArgs g) {
 }
 
 // ---------------------------------------------------------------------------------------
+// partial_wide_kernel (64 < M <= 128: the video prefill's 98-token projections): the same
+// split-K partials, but a workgroup owns 64 output columns (16 per wave) over one K slice of
+// 512, and the slice of every activation row is staged once in LDS with direct global->LDS
+// loads (one 1 KB row per wave instruction: lane j lands at the row start + 16 j) and read by
+// all four waves, which divides the activation re-reads of a 16-column workgroup by four.
+// Each wave streams its own 16 x 512 weight panel into registers; every load is issued before
+// the first MFMA.  Rows past M and k past K read finite data that only reaches unstored
+// outputs or meets zero weights.
+template <int MT>
+__global__ __launch_bounds__(256) void partial_wide_kernel(PartArgs g) {
+  constexpr int KSW = 16, KS = 32 * KSW;   // 32-wide k-steps per slice, slice length
+  constexpr int PITCH = KS + 16;           // bf16; a 32-byte pad: the 16-byte B-fragment reads of
+                                           // a half-wave (16 rows x 2 chunks) hit distinct banks
+  __shared__ __attribute__((aligned(16))) bf16 As[MT * 16 * PITCH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * 64 + wave * 16;
+  const int64_t k0 = (int64_t)blockIdx.y * KS;
+  const int M = (int)g.M;
+
+  // activation slice: wave w stages rows w, w + 4, ...; k past K re-reads the row's first 8
+  const int64_t ka = k0 + lane * 8;
+  const int64_t kc = ka + 8 <= g.K ? ka : 0;
+  for (int r = wave; r < M; r += 4)
+    __builtin_amdgcn_global_load_lds((const void*)(g.a + (int64_t)r * g.lda + kc),
+                                     (__attribute__((address_space(3))) void*)&As[r * PITCH], 16, 0, 0);
+  // this wave's weight panel
+  const int64_t wn = n0 + l16;
+  const bf16* wp = g.w + (wn < g.N ? wn : 0) * g.ldw;
+  bf16x8 wf[KSW];
+#pragma unroll
+  for (int s = 0; s < KSW; ++s) {
+    const int64_t k = k0 + s * 32 + lg * 8;
+    wf[s] = load8_if(k < g.K, wp + k, g.w);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < KSW; ++s)
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(&As[(t * 16 + l16) * PITCH + s * 32 + lg * 8]);
+      acc[t] = mfma16(wf[s], b, acc[t]);   // D[col n0 + 4 lg + e][row t*16 + l16]
+    }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int64_t m = t * 16 + l16;
+    const int64_t n = n0 + lg * 4;
+    if (m >= M) continue;
+    float* dst = g.part + ((int64_t)blockIdx.y * g.M + m) * g.N + n;
+    if ((g.N & 3) == 0) {
+      if (n < g.N) *reinterpret_cast<f32x4*>(dst) = acc[t];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < g.N) dst[e] = acc[t][e];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // final_kernel (fam_gemm_final, M <= 64): the whole K of 16 output columns in one workgroup
 // of NW waves, each wave a contiguous quarter/eighth/sixteenth of K with every fragment
 // loaded before the first MFMA; the wave accumulators are summed through LDS in wave order
@@ -1074,10 +1139,16 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
 // Split plan of fam_gemm_partial: STEPS (32-wide k-steps per wave; a workgroup covers
 // 4*32*STEPS of K) is the longest of 8, 4, 2, 1 that still gives >= 256 workgroups (one per
 // CU), so the partial planes are as few as the machine's width allows.  Above 64 rows the
-// eight m-tiles' activation fragments cap STEPS at 4 (registers).
+// eight m-tiles' activation fragments cap STEPS at 4 (registers), and the wide kernel (64
+// columns x 512 of K per workgroup, steps = 0 here) takes over when it alone fills the chip.
 static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* splits) {
   const int64_t groups = (N + 15) / 16;
   const int64_t ksteps = (K + 31) / 32;
+  if (M > 64 && ((N + 63) / 64) * ((K + 511) / 512) >= 256) {
+    *steps = 0;
+    *splits = (int)((K + 511) / 512);
+    return;
+  }
   int st = M > 64 ? 4 : 8;
   while (st > 1 && ((ksteps + 4 * st - 1) / (4 * st)) * groups < 256) st >>= 1;
   *steps = st;
@@ -1120,7 +1191,9 @@ extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64
   partial_plan(M, N, K, &steps, &splits);
   PartArgs pa{(const bf16*)a, lda, (const bf16*)w, ldw, partials, M, N, K};
   hipStream_t s = (hipStream_t)stream;
-  if (M <= 16) launch_partial<1>(pa, steps, splits, s);
+  if (steps == 0) FAM_LAUNCH((partial_wide_kernel<8>), dim3((unsigned)((N + 63) / 64), (unsigned)splits), dim3(256),
+                             0, s, pa);
+  else if (M <= 16) launch_partial<1>(pa, steps, splits, s);
   else if (M <= 32) launch_partial<2>(pa, steps, splits, s);
   else if (M <= 64) launch_partial<4>(pa, steps, splits, s);
   else launch_partial<8>(pa, steps, splits, s);

@@ -196,7 +196,7 @@ __global__ __launch_bounds__(RT) void rowop_kernel(RowArgs a) {
 // 4 consecutive columns per thread (N <= 256 * NW); all global loads of the row (up to
 // MAXS partial planes, bias, residual, gate, modulation, norm weights, RoPE tables) are
 // issued before the first use, so a row costs one memory round trip instead of one per
-// operand.
+// operand (one more per further MAXS planes of a long-K split plan).
 __device__ __forceinline__ void ld4(const bf16* p, float o[4]) {
   const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
 #pragma unroll
@@ -334,6 +334,21 @@ __global__ __launch_bounds__(NW * 64) void rowop_vec_kernel(RowArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] += pz[z][e];
     }
+  // planes past the first MAXS (long-K split plans): further batches of MAXS loads, still in
+  // split order
+  for (int64_t z0 = MAXS; z0 < ns; z0 += MAXS) {
+#pragma unroll
+    for (int z = 0; z < MAXS; ++z) {
+      const int64_t zz = z0 + z < ns ? z0 + z : ns - 1;
+      pz[z] = *reinterpret_cast<const f32x4*>(a.part + zz * a.split_stride + m * a.N + cs);
+    }
+#pragma unroll
+    for (int z = 0; z < MAXS; ++z)
+      if (z0 + z < ns) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += pz[z][e];
+      }
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     float x = act_fn(v[e] + bias[e], a.act);
@@ -410,7 +425,7 @@ using namespace fam;
 // starts on a 4-column boundary; anything else runs the generic per-element kernel.
 static bool vec_eligible(const fam_rowop_desc* d) {
   auto al = [](const void* p, unsigned b) { return (reinterpret_cast<uintptr_t>(p) & (b - 1)) == 0; };
-  if (d->src != FAM_ROWSRC_PARTIALS || d->N % 4 != 0 || d->splits > 16 || d->ldo % 4 != 0) return false;
+  if (d->src != FAM_ROWSRC_PARTIALS || d->N % 4 != 0 || d->splits > 64 || d->ldo % 4 != 0) return false;
   if (!al(d->out, d->out_f32 ? 16 : 8) || (d->bias && !al(d->bias, 8))) return false;
   if (d->res && (d->ldr % 4 != 0 || !al(d->res, d->out_f32 ? 16 : 8))) return false;
   if (d->gate && !(d->gate_ns == 0 || (d->gate_ns == 1 && d->gate_bs % 4 == 0 && d->gate_rs % 4 == 0 &&

@@ -419,9 +419,13 @@ def test_sinusoid_and_modulation():
 
 # --------------------------------------------------------------------------- split-K partials + row kernel
 @pytest.mark.parametrize("M,N,K", [(32, 3072, 1024), (32, 1024, 4096), (32, 7, 1024), (1, 64, 8), (7, 1000, 256),
-                                    (64, 4096, 1024), (17, 2048, 1000), (33, 96, 64)])
+                                    (64, 4096, 1024), (17, 2048, 1000), (33, 96, 64), (98, 3072, 3072),
+                                    (98, 3072, 14336), (128, 4090, 3000), (65, 1000, 1024), (100, 4096, 520)])
 def test_gemm_partial_rowop(M, N, K):
-    """Split-K partials summed in split order by the row kernel = linear; bit-identical reruns."""
+    """Split-K partials summed in split order by the row kernel = linear; bit-identical reruns.
+    Above 64 rows: the wide kernel (64 columns x 512 of K per workgroup, activations staged in
+    LDS; (98, 3072, 14336) gives 28 planes, past the row kernel's first batch of 16) and the
+    8-m-tile register kernel where the wide one would not fill the chip."""
     x, w, b = rnd(M, K, seed=70), rnd(N, K, seed=71, scale=0.02), rnd(N, seed=72, scale=0.02)
     ref = O.linear(x.float(), w.float(), b.float())
     xd, wd, bd = dev(x), dev(w), dev(b)
