@@ -62,7 +62,10 @@ class FusedVideoDiTBlock:
         ctx_mask: bool [B, S, Lc] on the cross-attention (the video context payload's mask).
         ctx_len = 0: no cross-attention (a prefill without a context payload).
         shared: buffers to use instead of allocating ("x", "tmod_in", "ctx" and the scratch
-            "mods", "h", "attn", "qc", "ckv", "hid"), so that blocks chain in place.
+            "mods", "h", "attn", "qc", "ckv", "hid", "part"), so that blocks chain in place.
+        ctx_kv: (buffer [B*Lc, W] bf16, column of this block's [k | v]): the context K/V of the
+            cross-attention computed outside (one GEMM for every block of a prefill) with k
+            already normalised; the block then skips its own context projection and K norm.
         kv_only: build only what the block's K/V need -- modulation, AdaLN1, the q/k/v
             projection and the key's RMSNorm + RoPE -- for a last prefill block whose output
             nobody reads.
@@ -74,9 +77,10 @@ class FusedVideoDiTBlock:
                  ffn_dim: int, batch: int, seq_len: int, ctx_len: int, freqs: torch.Tensor, eps: float = 1e-6,
                  per_token_mod: bool = True, device="cuda", self_mask: Optional[torch.Tensor] = None,
                  ctx_mask: Optional[torch.Tensor] = None, shared: Optional[Dict[str, torch.Tensor]] = None,
-                 kv_only: bool = False):
+                 kv_only: bool = False, ctx_kv: Optional[tuple] = None):
         dev = torch.device(device)
         self.kv_only = kv_only
+        self.ctx_kv = ctx_kv
         self.lib = _capi.load()
         self.B, self.S, self.Lc = batch, seq_len, ctx_len
         self.H, self.nh, self.Dh, self.F = hidden, num_heads, head_dim, ffn_dim
@@ -289,10 +293,14 @@ class FusedVideoDiTBlock:
         if Lc > 0:
             self._adaln("norm3", self.x, self.h, lw=w["n3_w"], lb=w["n3_b"])
             self._proj("cross_q", self.h, w["cq_w"], w["cq_b"], self.qc, rms_w=w["cnq"])
-            self._gemm("cross_kv", self.ctx, w["ckv_w"], w["ckv_b"], self.ckv)
-            kp = self.ckv.data_ptr()
-            self._rms("cross_k_norm", kp, 2 * A, self.B * Lc, Lc, w["cnk"], False)
-            self._attention("cross_attn", self.qc.data_ptr(), A, kp, 2 * A, kp + 2 * A, 2 * A, S, Lc, Lc,
+            if self.ctx_kv is None:
+                self._gemm("cross_kv", self.ctx, w["ckv_w"], w["ckv_b"], self.ckv)
+                kp, kld = self.ckv.data_ptr(), 2 * A
+                self._rms("cross_k_norm", kp, kld, self.B * Lc, Lc, w["cnk"], False)
+            else:
+                buf, col = self.ctx_kv
+                kp, kld = buf.data_ptr() + 2 * col, buf.stride(0)
+            self._attention("cross_attn", self.qc.data_ptr(), A, kp, kld, kp + 2 * A, kld, S, Lc, Lc,
                             mask=self.ctx_mask, mask_strides=(S * Lc, 0, Lc))
             self._proj("cross_o", self.attn, w["co_w"], w["co_b"], self.x, res=self.x)
         # FFN
@@ -370,20 +378,63 @@ class FusedVideoPrefill:
         self.shared = {"x": z(M, hidden), "tmod_in": z(rows, 6 * hidden), "ctx": z(batch * ctx_len, hidden),
                        "mods": z(rows, 6 * hidden), "h": z(M, hidden), "attn": z(M, self.A), "qc": z(M, self.A),
                        "ckv": z(batch * ctx_len, 2 * self.A), "hid": z(M, ffn_dim)}
+        self.lib = lib = _capi.load()
         if M <= 128:   # one split-K partial buffer for every block
-            lib = _capi.load()
             need = max(lib.fam_gemm_partial_splits(M, n_, k_) * M * n_
                        for n_, k_ in ((hidden, self.A), (self.A, hidden), (hidden, ffn_dim)))
             self.shared["part"] = torch.zeros(need, dtype=torch.float32, device=dev)
+        # the context K/V of every block that cross-attends, in one GEMM per call: the context
+        # does not change between blocks, only the weights do
+        ncross = self.n_run - 1 if ctx_len > 0 else 0     # the last block run builds only its K/V
+        self.steps, self.meta, self._descs = [], [], []
+        if ncross > 0:
+            def cat(names):
+                return torch.cat([params[f"blocks.{i}.cross_attn.{n}"].to(device=dev, dtype=torch.float32)
+                                  for i in range(ncross) for n in names], 0).to(_BF16).contiguous()
+            self.ckv_w = cat(["k.weight", "v.weight"])
+            self.ckv_b = cat(["k.bias", "v.bias"])
+            self.ctxkv = z(batch * ctx_len, ncross * 2 * self.A)
+            self.cnk = [params[f"blocks.{i}.cross_attn.norm_k.weight"].to(device=dev, dtype=_BF16).contiguous()
+                        for i in range(ncross)]
+            self._ctx_launches(batch * ctx_len, ctx_len, head_dim, eps)
         self.blocks = [FusedVideoDiTBlock(params, i, hidden=hidden, num_heads=num_heads, head_dim=head_dim,
                                           ffn_dim=ffn_dim, batch=batch, seq_len=video_len, ctx_len=ctx_len,
                                           freqs=freqs, eps=eps, per_token_mod=per_token_mod, device=dev,
                                           self_mask=video_mask, ctx_mask=ctx_mask, shared=self.shared,
-                                          kv_only=(i == self.n_run - 1))
+                                          kv_only=(i == self.n_run - 1),
+                                          ctx_kv=(self.ctxkv, i * 2 * self.A) if i < ncross else None)
                        for i in range(self.n_run)]
-        self.steps = [f for b in self.blocks for f in b.steps]
-        self.meta = [m for b in self.blocks for m in b.meta]
+        self.steps += [f for b in self.blocks for f in b.steps]
+        self.meta += [m for b in self.blocks for m in b.meta]
         self.graph: Optional[torch.cuda.CUDAGraph] = None
+
+    def _ctx_launches(self, rows, seq, head_dim, eps):
+        """ctxkv = ctx [k|v weights of every block]^T + bias, then each block's K RMSNorm."""
+        lib, A = self.lib, self.A
+        d = _capi.GemmDesc()
+        ctx = self.shared["ctx"]
+        d.a, d.lda, d.w, d.ldw = ctx.data_ptr(), ctx.stride(0), self.ckv_w.data_ptr(), self.ckv_w.stride(0)
+        d.bias = self.ckv_b.data_ptr()
+        d.out, d.ldo = self.ctxkv.data_ptr(), self.ctxkv.stride(0)
+        d.M, d.N, d.K = rows, self.ckv_w.shape[0], ctx.shape[1]
+        d.rows_per_batch = rows
+        self._descs.append(d)
+
+        def add(name, fname, args, kind):
+            f = getattr(lib, fname)
+
+            def run(stream):
+                rc = f(*args, stream)
+                if rc != 0:
+                    raise _capi.FamError(f"{fname}[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
+            self.steps.append(run)
+            self.meta.append({"name": name, "kernel": kind})
+        add("ctx_kv_all", "fam_gemm", (C.byref(d),), "gemm")
+        ld = self.ctxkv.stride(0)
+        for i, wk in enumerate(self.cnk):
+            p = self.ctxkv.data_ptr() + 2 * (i * 2 * A)
+            add(f"b{i}.cross_k_norm", "fam_rmsnorm_rope",
+                (p, ld, p, ld, rows, seq, A, wk.data_ptr(), float(eps), None, None, 0, 0, head_dim), "rmsnorm_rope")
 
     @property
     def num_launches(self) -> int:
