@@ -483,29 +483,30 @@ __global__ __launch_bounds__(256) void partial_kernel(PartArgs g) {
 
 // ---------------------------------------------------------------------------------------
 // partial_wide_kernel (64 < M <= 128: the video prefill's 98-token projections): the same
-// split-K partials, but a workgroup owns 64 output columns (16 per wave) over one K slice of
-// 512, and the slice of every activation row is staged once in LDS with direct global->LDS
-// loads (one 1 KB row per wave instruction: lane j lands at the row start + 16 j) and read by
-// all four waves, which divides the activation re-reads of a 16-column workgroup by four.
+// split-K partials, but a workgroup of NWV waves owns 16 NWV output columns (16 per wave)
+// over one K slice of 512, and the slice of every activation row is staged once in LDS with
+// direct global->LDS loads (one 1 KB row per wave instruction: lane j lands at the row start
+// + 16 j) and read by all the waves, which divides the activation re-reads of a 16-column
+// workgroup by NWV.
 // Each wave streams its own 16 x 512 weight panel into registers; every load is issued before
 // the first MFMA.  Rows past M and k past K read finite data that only reaches unstored
 // outputs or meets zero weights.
-template <int MT>
-__global__ __launch_bounds__(256) void partial_wide_kernel(PartArgs g) {
+template <int MT, int NWV>
+__global__ __launch_bounds__(NWV * 64) void partial_wide_kernel(PartArgs g) {
   constexpr int KSW = 16, KS = 32 * KSW;   // 32-wide k-steps per slice, slice length
   constexpr int PITCH = KS + 16;           // bf16; a 32-byte pad: the 16-byte B-fragment reads of
                                            // a half-wave (16 rows x 2 chunks) hit distinct banks
   __shared__ __attribute__((aligned(16))) bf16 As[MT * 16 * PITCH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * 64 + wave * 16;
+  const int64_t n0 = (int64_t)blockIdx.x * (16 * NWV) + wave * 16;
   const int64_t k0 = (int64_t)blockIdx.y * KS;
   const int M = (int)g.M;
 
   // activation slice: wave w stages rows w, w + 4, ...; k past K re-reads the row's first 8
   const int64_t ka = k0 + lane * 8;
   const int64_t kc = ka + 8 <= g.K ? ka : 0;
-  for (int r = wave; r < M; r += 4)
+  for (int r = wave; r < M; r += NWV)
     __builtin_amdgcn_global_load_lds((const void*)(g.a + (int64_t)r * g.lda + kc),
                                      (__attribute__((address_space(3))) void*)&As[r * PITCH], 16, 0, 0);
   // this wave's weight panel
@@ -1144,7 +1145,7 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
 static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* splits) {
   const int64_t groups = (N + 15) / 16;
   const int64_t ksteps = (K + 31) / 32;
-  if (M > 64 && ((N + 63) / 64) * ((K + 511) / 512) >= 256) {
+  if (M > 64 && ((N + 127) / 128) * ((K + 511) / 512) >= 128) {
     *steps = 0;
     *splits = (int)((K + 511) / 512);
     return;
@@ -1175,6 +1176,34 @@ static void launch_partial(const PartArgs& a, int steps, int splits, hipStream_t
   }
 }
 
+// Waves per workgroup of the wide kernel (one 16-column strip each): the workgroup holds the
+// 135 KB activation slice in LDS, so one runs per CU; the estimate is rounds over the CUs
+// times the bytes a workgroup loads (weights 16 NWV x 512, activations M x 512).
+static int wide_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus = n;
+  }
+  return cus;
+}
+static void launch_partial_wide(const PartArgs& a, int splits, hipStream_t s) {
+  const int64_t cus = wide_cus();
+  int best = 4;
+  int64_t best_cost = -1;
+  for (int nwv : {4, 6, 8}) {
+    const int64_t wgs = (a.N + 16 * nwv - 1) / (16 * nwv) * splits;
+    const int64_t cost = (wgs + cus - 1) / cus * (16 * nwv + a.M);
+    if (best_cost < 0 || cost < best_cost) { best_cost = cost; best = nwv; }
+  }
+  const unsigned gy = (unsigned)splits;
+  if (best == 8) FAM_LAUNCH((partial_wide_kernel<8, 8>), dim3((unsigned)((a.N + 127) / 128), gy), dim3(512), 0, s, a);
+  else if (best == 6) FAM_LAUNCH((partial_wide_kernel<8, 6>), dim3((unsigned)((a.N + 95) / 96), gy), dim3(384), 0, s, a);
+  else FAM_LAUNCH((partial_wide_kernel<8, 4>), dim3((unsigned)((a.N + 63) / 64), gy), dim3(256), 0, s, a);
+}
+
 extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64_t ldw, float* partials,
                                 int64_t M, int64_t N, int64_t K, void* stream) {
   FAM_REQUIRE(a && w && partials, FAM_ERR_INVALID_ARG, "fam_gemm_partial: null pointer");
@@ -1191,8 +1220,7 @@ extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64
   partial_plan(M, N, K, &steps, &splits);
   PartArgs pa{(const bf16*)a, lda, (const bf16*)w, ldw, partials, M, N, K};
   hipStream_t s = (hipStream_t)stream;
-  if (steps == 0) FAM_LAUNCH((partial_wide_kernel<8>), dim3((unsigned)((N + 63) / 64), (unsigned)splits), dim3(256),
-                             0, s, pa);
+  if (steps == 0) launch_partial_wide(pa, splits, s);
   else if (M <= 16) launch_partial<1>(pa, steps, splits, s);
   else if (M <= 32) launch_partial<2>(pa, steps, splits, s);
   else if (M <= 64) launch_partial<4>(pa, steps, splits, s);
