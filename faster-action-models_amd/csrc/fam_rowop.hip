@@ -31,6 +31,7 @@ struct RowArgs {
   int nseg; int64_t seg0[2]; int64_t segw; const bf16* segwt[2];
   const float* cs; const float* sn; int64_t trs, tes, hd, seq;
   bf16* nout; int64_t ldn;
+  int64_t ldp;   // row stride of the partial planes
 };
 
 constexpr int RT = 256;  // threads per row
@@ -70,7 +71,7 @@ __global__ __launch_bounds__(RT) void rowop_kernel(RowArgs a) {
     if (a.src == 0) {
       if ((a.N & 3) == 0) {
         if (c < a.N) {
-          const float* p = a.part + m * a.N + c;
+          const float* p = a.part + m * a.ldp + c;
 #pragma unroll 8
           for (int64_t z = 0; z < a.splits; ++z) {
             const f32x4 t = *reinterpret_cast<const f32x4*>(p + z * a.split_stride);
@@ -82,7 +83,7 @@ __global__ __launch_bounds__(RT) void rowop_kernel(RowArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (ok[j][e])
-            for (int64_t z = 0; z < a.splits; ++z) v[j][e] += a.part[z * a.split_stride + m * a.N + c + e];
+            for (int64_t z = 0; z < a.splits; ++z) v[j][e] += a.part[z * a.split_stride + m * a.ldp + c + e];
       }
     } else {
 #pragma unroll
@@ -252,7 +253,7 @@ __global__ __launch_bounds__(NW * 64) void rowop_vec_kernel(RowArgs a) {
 #pragma unroll
   for (int z = 0; z < MAXS; ++z) {
     const int64_t zz = z < ns ? z : ns - 1;
-    pz[z] = *reinterpret_cast<const f32x4*>(a.part + zz * a.split_stride + m * a.N + cs);
+    pz[z] = *reinterpret_cast<const f32x4*>(a.part + zz * a.split_stride + m * a.ldp + cs);
   }
   auto raw4 = [&](const bf16* p) { return *reinterpret_cast<const uint2*>(p ? (const void*)p : (const void*)safe); };
   const uint2 r_bias = raw4(a.bias ? a.bias + cs : nullptr);
@@ -340,7 +341,7 @@ __global__ __launch_bounds__(NW * 64) void rowop_vec_kernel(RowArgs a) {
 #pragma unroll
     for (int z = 0; z < MAXS; ++z) {
       const int64_t zz = z0 + z < ns ? z0 + z : ns - 1;
-      pz[z] = *reinterpret_cast<const f32x4*>(a.part + zz * a.split_stride + m * a.N + cs);
+      pz[z] = *reinterpret_cast<const f32x4*>(a.part + zz * a.split_stride + m * a.ldp + cs);
     }
 #pragma unroll
     for (int z = 0; z < MAXS; ++z)
@@ -426,6 +427,7 @@ using namespace fam;
 static bool vec_eligible(const fam_rowop_desc* d) {
   auto al = [](const void* p, unsigned b) { return (reinterpret_cast<uintptr_t>(p) & (b - 1)) == 0; };
   if (d->src != FAM_ROWSRC_PARTIALS || d->N % 4 != 0 || d->splits > 64 || d->ldo % 4 != 0) return false;
+  if (d->ldp % 4 != 0) return false;
   if (!al(d->out, d->out_f32 ? 16 : 8) || (d->bias && !al(d->bias, 8))) return false;
   if (d->res && (d->ldr % 4 != 0 || !al(d->res, d->out_f32 ? 16 : 8))) return false;
   if (d->gate && !(d->gate_ns == 0 || (d->gate_ns == 1 && d->gate_bs % 4 == 0 && d->gate_rs % 4 == 0 &&
@@ -450,6 +452,9 @@ extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
   FAM_REQUIRE(d->out, FAM_ERR_INVALID_ARG, "fam_rowop: out must be non-null");
   FAM_REQUIRE(d->ldo >= d->N, FAM_ERR_INVALID_ARG, "fam_rowop: ldo must be >= N");
   if (d->src == FAM_ROWSRC_PARTIALS) {
+    const int64_t ldp = d->ldp > 0 ? d->ldp : d->N;
+    FAM_REQUIRE(ldp >= d->N && (d->M == 0 || d->split_stride >= (d->M - 1) * ldp + d->N), FAM_ERR_INVALID_ARG,
+                "fam_rowop: need ldp >= N and split_stride >= (M - 1) * ldp + N");
     FAM_REQUIRE(d->partials && d->splits >= 1 && d->split_stride >= d->M * d->N, FAM_ERR_INVALID_ARG,
                 "fam_rowop: partials need splits >= 1 and split_stride >= M*N");
     FAM_REQUIRE(d->N % 4 != 0 || fam_host::aligned16(d->partials), FAM_ERR_INVALID_ARG,
@@ -496,6 +501,7 @@ extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
   RowArgs a{};
   a.src = d->src;
   a.part = d->partials; a.splits = d->splits; a.split_stride = d->split_stride;
+  a.ldp = d->ldp > 0 ? d->ldp : d->N;
   a.xin = d->x_in; a.ldx = d->ldx; a.kin = d->k_in; a.win = (const bf16*)d->w_in;
   a.M = d->M; a.N = d->N;
   a.bias = (const bf16*)d->bias; a.act = d->act;

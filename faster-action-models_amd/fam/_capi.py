@@ -93,7 +93,7 @@ class RowopDesc(C.Structure):
         ("nseg", C.c_int), ("seg_col0", _i64 * 2), ("seg_width", _i64), ("seg_weight", _vp * 2),
         ("rope_cos", _vp), ("rope_sin", _vp), ("rope_row_stride", _i64), ("rope_elem_stride", _i64),
         ("head_dim", _i64), ("seq_len", _i64),
-        ("nout", _vp), ("ldn", _i64),
+        ("nout", _vp), ("ldn", _i64), ("ldp", _i64),
     ]
 
 

@@ -501,15 +501,20 @@ def rowop(out: torch.Tensor, *, partials: Optional[torch.Tensor] = None, x_in: O
           w_in: Optional[torch.Tensor] = None, bias=None, act: int = _capi.FAM_ACT_NONE, res=None, gate=None,
           gate_strides=(0, 0, 1), rows_per_batch: Optional[int] = None, norm: int = _capi.FAM_ROWNORM_NONE,
           eps: float = 1e-6, ln_w=None, ln_b=None, shift=None, scale=None, mod_strides=(0, 0), segs=(),
-          seg_width: int = 0, rope=None, nout: Optional[torch.Tensor] = None) -> None:
+          seg_width: int = 0, rope=None, nout: Optional[torch.Tensor] = None, col0: int = 0) -> None:
     """Row kernel (fam_rowop in include/fam_hip.h) on 2-D row-major tensors.  `partials` is the
-    [S, M, N] output of gemm_partial; `rope` is (cos, sin, row_stride, elem_stride, head_dim,
-    seq_len) with fp32 tables."""
+    [S, M, P] output of gemm_partial, of which columns [col0, col0 + N) are read (P may exceed
+    N); `rope` is (cos, sin, row_stride, elem_stride, head_dim, seq_len) with fp32 tables."""
     M, N = out.shape
     d = _capi.RowopDesc()
     keep = []
     if partials is not None:
-        d.src, d.partials, d.splits, d.split_stride = _capi.FAM_ROWSRC_PARTIALS, partials.data_ptr(), partials.shape[0], M * N
+        S, Mp, P = partials.shape
+        if Mp != M or not partials.is_contiguous() or col0 < 0 or col0 + N > P:
+            raise ValueError(f"rowop: partials {tuple(partials.shape)} do not hold columns [{col0}, {col0 + N}) "
+                             f"of {M} rows")
+        d.src, d.partials, d.splits = _capi.FAM_ROWSRC_PARTIALS, partials.data_ptr() + 4 * col0, S
+        d.split_stride, d.ldp = M * P, P
     else:
         d.src = _capi.FAM_ROWSRC_SMALLK
         d.x_in, d.ldx, d.k_in, d.w_in = x_in.data_ptr(), x_in.stride(0), w_in.shape[1], w_in.data_ptr()

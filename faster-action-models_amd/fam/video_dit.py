@@ -139,7 +139,7 @@ class FusedVideoDiTBlock:
         self.splitk = M <= 128 and H <= 4096 and A <= 4096
         if self.splitk:
             need = max(self.lib.fam_gemm_partial_splits(M, n_, k_) * M * n_
-                       for n_, k_ in ((H, A), (A, H), (H, F)))
+                       for n_, k_ in ((H, A), (A, H), (H, F), (3 * A, H)))
             t = sh.get("part")
             if t is not None and (t.dtype != torch.float32 or t.numel() < need):
                 raise ValueError(f"shared buffer 'part' must be fp32 with >= {need} elements")
@@ -197,13 +197,17 @@ class FusedVideoDiTBlock:
                                              self.part.data_ptr(), M, N, K), "gemm_partial", 2 * M * N * K)
         return splits
 
-    def _rowop(self, name, *, N, splits, bias, out, res=None, gate=None, gate_strides=(0, 0, 1), rms_w=None):
+    def _rowop(self, name, *, N, splits, bias, out, res=None, gate=None, gate_strides=(0, 0, 1), rms_w=None,
+               rope=False, col0=0, ldp=0):
         """out = res + gate * (sum of the partial planes + bias) (or the plain sum + bias), then,
-        with rms_w, RMSNorm of the row over N with that weight, in place."""
+        with rms_w, RMSNorm of the row over N with that weight (and RoPE), in place.  col0 / ldp:
+        columns [col0, col0 + N) of planes whose rows are ldp wide."""
         M = self.B * self.S
+        ldp = ldp or N
         d = _capi.RowopDesc()
         d.src = _capi.FAM_ROWSRC_PARTIALS
-        d.partials, d.splits, d.split_stride = self.part.data_ptr(), splits, M * N
+        d.partials, d.splits, d.split_stride = self.part.data_ptr() + 4 * col0, splits, M * ldp
+        d.ldp = ldp
         d.M, d.N = M, N
         d.bias = bias.data_ptr()
         d.act = _capi.FAM_ACT_NONE
@@ -220,6 +224,11 @@ class FusedVideoDiTBlock:
             d.seg_col0[0], d.seg_weight[0] = 0, rms_w.data_ptr()
             d.seg_width = N
             d.nout, d.ldn = out.data_ptr(), out.stride(0)
+            if rope:
+                cos, sin, trs, tes = self.rope
+                d.rope_cos, d.rope_sin = cos.data_ptr(), sin.data_ptr()
+                d.rope_row_stride, d.rope_elem_stride = trs, tes
+                d.head_dim, d.seq_len = self.Dh, self.S
         self._descs.append(d)
         self._add(name, "fam_rowop", (C.byref(d),), "rowop")
 
@@ -280,12 +289,25 @@ class FusedVideoDiTBlock:
         gstr = (S * 6 * H, 6 * H, 1) if self.per_token else (6 * H, 0, 1)
         # self-attention
         self._adaln("adaln1", self.x, self.h, shift=mod(0), scale=mod(1))
-        self._gemm("qkv", self.h, w["qkv_w"], w["qkv_b"], self.qkv)
         qp = self.qkv.data_ptr()
-        self._rms("k_norm_rope", qp + 2 * A, 3 * A, M, S, w["nk"], True)
-        if self.kv_only:
-            return
-        self._rms("q_norm_rope", qp, 3 * A, M, S, w["nq"], True)
+        if self.splitk:
+            # one split-K product for q|k|v, finished window by window: k and q with their
+            # RMSNorm + RoPE, v with its bias
+            sp = self._partial("qkv", self.h, w["qkv_w"])
+            b = w["qkv_b"]
+            self._rowop("k_row", N=A, splits=sp, bias=b[A:2 * A], out=self.qkv[:, A:2 * A], rms_w=w["nk"], rope=True,
+                        col0=A, ldp=3 * A)
+            self._rowop("v_row", N=A, splits=sp, bias=b[2 * A:], out=self.qkv[:, 2 * A:], col0=2 * A, ldp=3 * A)
+            if self.kv_only:
+                return
+            self._rowop("q_row", N=A, splits=sp, bias=b[:A], out=self.qkv[:, :A], rms_w=w["nq"], rope=True,
+                        col0=0, ldp=3 * A)
+        else:
+            self._gemm("qkv", self.h, w["qkv_w"], w["qkv_b"], self.qkv)
+            self._rms("k_norm_rope", qp + 2 * A, 3 * A, M, S, w["nk"], True)
+            if self.kv_only:
+                return
+            self._rms("q_norm_rope", qp, 3 * A, M, S, w["nq"], True)
         self._attention("self_attn", qp, 3 * A, qp + 2 * A, 3 * A, qp + 4 * A, 3 * A, S, S, S,
                         mask=self.self_mask, mask_strides=(0, 0, S))
         self._proj("o", self.attn, w["o_w"], w["o_b"], self.x, res=self.x, gate=mod(2), gate_strides=gstr)
@@ -381,7 +403,7 @@ class FusedVideoPrefill:
         self.lib = lib = _capi.load()
         if M <= 128:   # one split-K partial buffer for every block
             need = max(lib.fam_gemm_partial_splits(M, n_, k_) * M * n_
-                       for n_, k_ in ((hidden, self.A), (self.A, hidden), (hidden, ffn_dim)))
+                       for n_, k_ in ((hidden, self.A), (self.A, hidden), (hidden, ffn_dim), (3 * self.A, hidden)))
             self.shared["part"] = torch.zeros(need, dtype=torch.float32, device=dev)
         # the context K/V of every block that cross-attends, in one GEMM per call: the context
         # does not change between blocks, only the weights do

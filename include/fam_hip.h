@@ -304,6 +304,9 @@ int fam_gemm_final(const void* a, int64_t lda, const void* w, int64_t ldw, const
  *   GELU           FB/wan_video_dit.py:262;  the reference's fused epilogue kernels fastwam::skpost,
  *   qkv_post, res_ln* (FG/mot.py:1280-1348, 786-816, 1771-1941); the Euler update of
  *   geak_head::mmx (DG/modules/action_model/ActionDiT.py:1260-1272) with out_f32.
+ * Partials source: v = sum over z < splits of partials[z * split_stride + m * ldp + n] (ldp = N when
+ * 0): with ldp above N a row kernel reads a column window of wider planes (a q/k/v split-K
+ * product finished segment by segment).
  * Limits: 1 <= N <= 4096; a normalised row must be bf16 (out_f32 == 0).
  */
 typedef struct fam_rowop_desc {
@@ -321,6 +324,7 @@ typedef struct fam_rowop_desc {
   int nseg; int64_t seg_col0[2]; int64_t seg_width; const void* seg_weight[2];
   const float* rope_cos; const float* rope_sin; int64_t rope_row_stride, rope_elem_stride, head_dim, seq_len;
   void* nout; int64_t ldn;
+  int64_t ldp;   /* row stride of the partial planes (elements); 0 means N */
 } fam_rowop_desc;
 
 int fam_rowop(const fam_rowop_desc* d, void* stream);

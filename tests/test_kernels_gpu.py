@@ -442,6 +442,39 @@ def test_gemm_partial_rowop(M, N, K):
     assert relerr(part.sum(0), O.linear(x.float(), w.float(), None)) <= 1e-3
 
 
+@pytest.mark.parametrize("M,H", [(98, 24), (40, 4)])
+def test_gemm_partial_qkv_windows(M, H):
+    """One split-K product for q|k|v finished by three row-kernel windows of its planes (rows
+    3A wide): q and k RMS-normalised over their A columns and rotated, v with its bias only
+    (FB/wan_video_dit.py:116-131 on the fused projection, rope_apply :49-55)."""
+    from fam import _capi
+    Dh = 128
+    A, K = H * Dh, 3072 if H == 24 else 512
+    x, w, b = rnd(M, K, seed=90), rnd(3 * A, K, seed=91, scale=0.02), rnd(3 * A, seed=92, scale=0.02)
+    wq, wk = rnd(A, seed=93, scale=0.2) + 1, rnd(A, seed=94, scale=0.2) + 1
+    fr = O.action_freqs(Dh, M)
+    cs, sn, trs, tes = ops().rope_tables(fr, "complex", torch.device("cuda"))
+    part, _ = ops().gemm_partial(dev(x), dev(w))
+    qkv = torch.empty(M, 3 * A, dtype=torch.bfloat16, device="cuda")
+    bd = dev(b)
+    for i, nw in ((1, dev(wk)), (2, None), (0, dev(wq))):
+        o = qkv[:, i * A:(i + 1) * A]
+        if nw is None:
+            ops().rowop(o, partials=part, bias=bd[i * A:], col0=i * A)
+        else:
+            ops().rowop(o, partials=part, bias=bd[i * A:], col0=i * A, norm=_capi.FAM_ROWNORM_RMS, eps=1e-6,
+                        segs=[(0, nw)], seg_width=A, rope=(cs, sn, trs, tes, Dh, M), nout=o)
+    lin = O.linear(x.float(), w.float(), b.float()).to(torch.bfloat16).float()
+    qr = O.rope_apply(O.rms_norm(lin[None, :, :A], wq.float(), 1e-6), fr, H)[0]
+    kr = O.rope_apply(O.rms_norm(lin[None, :, A:2 * A], wk.float(), 1e-6), fr, H)[0]
+    y = qkv.cpu()
+    assert relerr(y[:, :A], qr) <= TOL
+    assert relerr(y[:, A:2 * A], kr) <= TOL
+    assert relerr(y[:, 2 * A:], lin[:, 2 * A:]) <= TOL
+    with pytest.raises(ValueError):
+        ops().rowop(qkv[:, :A], partials=part, bias=bd, col0=2 * A + 1)
+
+
 @pytest.mark.parametrize("M,rpb", [(32, 32), (96, 32)])
 def test_rowop_gelu_gate_residual_adaln(M, rpb):
     """out = res + gate[b] * gelu(a w^T + b), then AdaLN(out) for the next block (FB/wan_video_dit.py:281-288)."""
