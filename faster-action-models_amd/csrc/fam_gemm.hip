@@ -548,6 +548,109 @@ __global__ __launch_bounds__(NWV * 64) void partial_wide_kernel(PartArgs g) {
 }
 
 // ---------------------------------------------------------------------------------------
+// partial_stream_kernel (64 < M <= 128, long K ranges): a workgroup of 8 waves owns 128
+// output columns (16 per wave) over kper = C x 256 of K and walks it in 256-wide chunks.
+// While the MFMAs of chunk c run, the next chunk is already in flight: each wave's 16 x 256
+// weight panel in registers and the activation chunk (M rows x 256) in registers on its way
+// to the single LDS buffer.  Loads go through buffer descriptors, so k past the range (and
+// the whole prefetch after the last chunk) reads zeros without a select on the loaded value,
+// which would make the compiler wait on each load right after issuing it; the prologue is
+// drained before the loop for the same reason.  Inside a chunk the activation fragments of
+// k-step s + 1 are read from LDS while the MFMAs of step s run.  Rows past M stay
+// uninitialised in LDS and only reach output rows that are never stored.
+template <int MT>
+__global__ __launch_bounds__(512) void partial_stream_kernel(PartArgs g, int kper) {
+  constexpr int NWV = 8, KS = 256, KSW = KS / 32, PITCH = KS + 16, UPR = KS / 8, NTH = NWV * 64;
+  constexpr int UPT = (MT * 16 * UPR + NTH - 1) / NTH;
+  constexpr uint32_t kOob = 0x80000000u;   // beyond every descriptor's range (checked on the host)
+  __shared__ __attribute__((aligned(16))) bf16 As[MT * 16 * PITCH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lg = lane >> 4;
+  const int M = (int)g.M, K = (int)g.K, N = (int)g.N;
+  const int nb0 = blockIdx.x * (16 * NWV), n0 = nb0 + wave * 16;
+  const int kb = blockIdx.y * kper;
+  const int ke = min(K, kb + kper);
+  // descriptors over this workgroup's <= 128 weight rows and the <= 128 activation rows:
+  // both ranges stay below 2^31 bytes for strides below 2^23 elements (checked on the host)
+  const int nrows = min(16 * NWV, N - nb0);
+  const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(g.w + (int64_t)nb0 * g.ldw, (uint32_t)(nrows * g.ldw * 2));
+  const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(g.a, (uint32_t)(g.M * g.lda * 2));
+  const int lr = wave * 16 + l16;
+  const uint32_t wrow = (uint32_t)((lr < nrows ? lr : 0) * g.ldw) * 2u;
+  const int nunits = M * UPR;
+  bf16x8 ar[UPT], wc[KSW], wx[KSW];
+  auto loadA = [&](int k0, int klim) {
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int idx = tid + u * NTH, r = idx / UPR, k = k0 + (idx % UPR) * 8;
+      ar[u] = buffer_load8(ars, idx < nunits && k < klim ? (uint32_t)(r * g.lda + k) * 2u : kOob);
+    }
+  };
+  auto storeA = [&]() {
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int idx = tid + u * NTH;
+      if (idx < nunits) *reinterpret_cast<bf16x8*>(&As[(idx / UPR) * PITCH + (idx % UPR) * 8]) = ar[u];
+    }
+  };
+  auto loadW = [&](int k0, int klim, bf16x8* wf) {
+#pragma unroll
+    for (int s = 0; s < KSW; ++s) {
+      const int k = k0 + s * 32 + lg * 8;
+      wf[s] = buffer_load8(wrs, k < klim ? wrow + (uint32_t)k * 2u : kOob);
+    }
+  };
+  loadA(kb, K);
+  loadW(kb, K, wc);
+  storeA();
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  f32x4 acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int k0 = kb; k0 < ke; k0 += KS) {
+    const int klim = k0 + KS < ke ? K : 0;   // 0: past the last chunk, every offset is out of range
+    loadW(k0 + KS, klim, wx);
+    loadA(k0 + KS, klim);
+    __builtin_amdgcn_sched_barrier(0);
+    bf16x8 bc[MT], bn[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) bc[t] = *reinterpret_cast<const bf16x8*>(&As[(t * 16 + l16) * PITCH + lg * 8]);
+#pragma unroll
+    for (int s = 0; s < KSW; ++s) {
+      if (s + 1 < KSW) {
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+          bn[t] = *reinterpret_cast<const bf16x8*>(&As[(t * 16 + l16) * PITCH + (s + 1) * 32 + lg * 8]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[t] = mfma16(wc[s], bc[t], acc[t]);   // D[col n0 + 4 lg + e][row t*16 + l16]
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) bc[t] = bn[t];
+    }
+    __syncthreads();
+    storeA();
+#pragma unroll
+    for (int s = 0; s < KSW; ++s) wc[s] = wx[s];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = 0; t < MT; ++t) {
+    const int m = t * 16 + l16, n = n0 + lg * 4;
+    if (m >= M) continue;
+    float* dst = g.part + ((int64_t)blockIdx.y * g.M + m) * g.N + n;
+    if ((N & 3) == 0) {
+      if (n < N) *reinterpret_cast<f32x4*>(dst) = acc[t];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < N) dst[e] = acc[t][e];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // final_kernel (fam_gemm_final, M <= 64): the whole K of 16 output columns in one workgroup
 // of NW waves, each wave a contiguous quarter/eighth/sixteenth of K with every fragment
 // loaded before the first MFMA; the wave accumulators are summed through LDS in wave order
@@ -1137,14 +1240,29 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
   return fam_host::check_launch("fam_gemm");
 }
 
-// Split plan of fam_gemm_partial: STEPS (32-wide k-steps per wave; a workgroup covers
-// 4*32*STEPS of K) is the longest of 8, 4, 2, 1 that still gives >= 256 workgroups (one per
-// CU), so the partial planes are as few as the machine's width allows.  Above 64 rows the
-// eight m-tiles' activation fragments cap STEPS at 4 (registers), and the wide kernel (64
-// columns x 512 of K per workgroup, steps = 0 here) takes over when it alone fills the chip.
+static int wide_cus();
+
+// Split plan of fam_gemm_partial.  Above 64 rows, first the streaming kernel: 128 columns per
+// workgroup, as many K splits as one round over the CUs allows, each split a whole number of
+// 256-wide chunks; it runs when every workgroup gets at least 3 chunks to pipeline (steps
+// returns -chunks).  Otherwise the wide kernel (one 512-wide K slice per workgroup, steps 0)
+// when it alone fills the chip.  Otherwise, and up to 64 rows always, STEPS (32-wide k-steps
+// per wave; a workgroup covers 4*32*STEPS of K) is the longest of 8, 4, 2, 1 that still gives
+// >= 256 workgroups (one per CU), so the partial planes are as few as the machine's width
+// allows; above 64 rows the eight m-tiles' activation fragments cap STEPS at 4 (registers).
 static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* splits) {
   const int64_t groups = (N + 15) / 16;
   const int64_t ksteps = (K + 31) / 32;
+  if (M > 64) {
+    const int64_t nblk = (N + 127) / 128, chunks = (K + 255) / 256;
+    const int64_t smax = std::max((int64_t)1, (int64_t)wide_cus() / nblk);
+    const int64_t c = (chunks + std::min(chunks, smax) - 1) / std::min(chunks, smax);
+    if (c >= 3) {
+      *steps = -(int)c;
+      *splits = (int)((chunks + c - 1) / c);
+      return;
+    }
+  }
   if (M > 64 && ((N + 127) / 128) * ((K + 511) / 512) >= 128) {
     *steps = 0;
     *splits = (int)((K + 511) / 512);
@@ -1215,12 +1333,18 @@ extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64
   FAM_REQUIRE(fam_host::aligned16(a) && fam_host::aligned16(w) && fam_host::aligned16(partials), FAM_ERR_INVALID_ARG,
               "fam_gemm_partial: a, w and partials must be 16-byte aligned");
   FAM_REQUIRE((N + 15) / 16 <= 2147483647LL, FAM_ERR_UNSUPPORTED, "fam_gemm_partial: N too large");
+  FAM_REQUIRE(M <= 64 || (lda < (1LL << 23) && ldw < (1LL << 23) && N < (1LL << 31)), FAM_ERR_UNSUPPORTED,
+              "fam_gemm_partial: above 64 rows lda and ldw must be < 2^23 elements");
   if (M == 0) return FAM_OK;
   int steps, splits;
   partial_plan(M, N, K, &steps, &splits);
   PartArgs pa{(const bf16*)a, lda, (const bf16*)w, ldw, partials, M, N, K};
   hipStream_t s = (hipStream_t)stream;
-  if (steps == 0) launch_partial_wide(pa, splits, s);
+  if (steps < 0) {
+    const dim3 grid((unsigned)((N + 127) / 128), (unsigned)splits);
+    if (M <= 112) FAM_LAUNCH((partial_stream_kernel<7>), grid, dim3(512), 0, s, pa, -steps * 256);
+    else FAM_LAUNCH((partial_stream_kernel<8>), grid, dim3(512), 0, s, pa, -steps * 256);
+  } else if (steps == 0) launch_partial_wide(pa, splits, s);
   else if (M <= 16) launch_partial<1>(pa, steps, splits, s);
   else if (M <= 32) launch_partial<2>(pa, steps, splits, s);
   else if (M <= 64) launch_partial<4>(pa, steps, splits, s);

@@ -241,7 +241,8 @@ __global__ __launch_bounds__(NW * 64) void rowop_vec_kernel(RowArgs a) {
   const uint32_t m32 = blockIdx.x, rpb32 = (uint32_t)a.rpb;
   const int64_t m = m32;
   const int64_t bi = m32 / rpb32, si = m32 - (uint32_t)bi * rpb32;
-  const int64_t c = (int64_t)tid * 4;
+  // rows wider than one workgroup (no normalisation only) are tiled over grid.y
+  const int64_t c = (int64_t)blockIdx.y * (NW * 256) + (int64_t)tid * 4;
   const bool act = c < a.N;
   const int64_t cs = act ? c : 0;  // a valid column for inactive threads' loads
 
@@ -447,8 +448,11 @@ static bool vec_eligible(const fam_rowop_desc* d) {
 
 extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
   FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_rowop: null descriptor");
-  FAM_REQUIRE(d->M >= 0 && d->N >= 1 && d->N <= 4 * RT * 4, FAM_ERR_INVALID_ARG,
-              "fam_rowop: need 1 <= N <= 4096 (N=%lld)", (long long)d->N);
+  FAM_REQUIRE(d->M >= 0 && d->N >= 1 && (d->N <= 4 * RT * 4 || (d->N < (1LL << 30) && d->norm == FAM_ROWNORM_NONE &&
+                                                                  vec_eligible(d))),
+              FAM_ERR_INVALID_ARG,
+              "fam_rowop: need 1 <= N <= 4096, or a wider row without normalisation on the vectorised path "
+              "(N %% 4 == 0, partials source, 16-byte aligned operands) (N=%lld)", (long long)d->N);
   FAM_REQUIRE(d->out, FAM_ERR_INVALID_ARG, "fam_rowop: out must be non-null");
   FAM_REQUIRE(d->ldo >= d->N, FAM_ERR_INVALID_ARG, "fam_rowop: ldo must be >= N");
   if (d->src == FAM_ROWSRC_PARTIALS) {
@@ -518,9 +522,9 @@ extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
   a.hd = d->head_dim > 0 ? d->head_dim : 4; a.seq = d->seq_len > 0 ? d->seq_len : 1;
   a.nout = (bf16*)d->nout; a.ldn = d->ldn;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)d->M);
   if (vec_eligible(d)) {
     const int nw = d->N <= 1024 ? 4 : (d->N <= 2048 ? 8 : 16);
+    const dim3 grid((unsigned)d->M, (unsigned)((d->N + nw * 256 - 1) / (nw * 256)));
     const int ms = d->splits <= 4 ? 4 : (d->splits <= 8 ? 8 : 16);
 #define FAM_ROWVEC(NW_, MS_) \
   if (nw == NW_ && ms == MS_) FAM_LAUNCH((rowop_vec_kernel<NW_, MS_>), grid, dim3(NW_ * 64), 0, s, a)
@@ -530,6 +534,7 @@ extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
 #undef FAM_ROWVEC
     return fam_host::check_launch("fam_rowop");
   }
+  const dim3 grid((unsigned)d->M);
   if (d->N <= 4 * RT) FAM_LAUNCH(rowop_kernel<1>, grid, dim3(RT), 0, s, a);
   else if (d->N <= 8 * RT) FAM_LAUNCH(rowop_kernel<2>, grid, dim3(RT), 0, s, a);
   else FAM_LAUNCH(rowop_kernel<4>, grid, dim3(RT), 0, s, a);

@@ -139,7 +139,7 @@ class FusedVideoDiTBlock:
         self.splitk = M <= 128 and H <= 4096 and A <= 4096
         if self.splitk:
             need = max(self.lib.fam_gemm_partial_splits(M, n_, k_) * M * n_
-                       for n_, k_ in ((H, A), (A, H), (H, F), (3 * A, H)))
+                       for n_, k_ in ((H, A), (A, H), (H, F), (3 * A, H), (F, H)))
             t = sh.get("part")
             if t is not None and (t.dtype != torch.float32 or t.numel() < need):
                 raise ValueError(f"shared buffer 'part' must be fp32 with >= {need} elements")
@@ -198,8 +198,8 @@ class FusedVideoDiTBlock:
         return splits
 
     def _rowop(self, name, *, N, splits, bias, out, res=None, gate=None, gate_strides=(0, 0, 1), rms_w=None,
-               rope=False, col0=0, ldp=0):
-        """out = res + gate * (sum of the partial planes + bias) (or the plain sum + bias), then,
+               rope=False, col0=0, ldp=0, act=_capi.FAM_ACT_NONE):
+        """out = res + gate * act(sum of the partial planes + bias) (or act(sum + bias)), then,
         with rms_w, RMSNorm of the row over N with that weight (and RoPE), in place.  col0 / ldp:
         columns [col0, col0 + N) of planes whose rows are ldp wide."""
         M = self.B * self.S
@@ -210,7 +210,7 @@ class FusedVideoDiTBlock:
         d.ldp = ldp
         d.M, d.N = M, N
         d.bias = bias.data_ptr()
-        d.act = _capi.FAM_ACT_NONE
+        d.act = act
         if res is not None:
             d.res, d.ldr = res.data_ptr(), res.stride(0)
         d.gate = gate.data_ptr() if gate is not None else None
@@ -232,15 +232,16 @@ class FusedVideoDiTBlock:
         self._descs.append(d)
         self._add(name, "fam_rowop", (C.byref(d),), "rowop")
 
-    def _proj(self, name, a, w, bias, out, res=None, gate=None, gate_strides=(0, 0, 1), rms_w=None):
-        """out = [res +] [gate *] (a w^T + bias) [then RMSNorm]: split-K + row kernel at <= 128
+    def _proj(self, name, a, w, bias, out, res=None, gate=None, gate_strides=(0, 0, 1), rms_w=None,
+              act=_capi.FAM_ACT_NONE):
+        """out = [res +] [gate *] act(a w^T + bias) [then RMSNorm]: split-K + row kernel at <= 128
         rows, otherwise one fam_gemm (+ fam_rmsnorm_rope for the norm)."""
         if self.splitk:
             sp = self._partial(name, a, w)
             self._rowop(name + "_row", N=w.shape[0], splits=sp, bias=bias, out=out, res=res, gate=gate,
-                        gate_strides=gate_strides, rms_w=rms_w)
+                        gate_strides=gate_strides, rms_w=rms_w, act=act)
         else:
-            self._gemm(name, a, w, bias, out, res=res, gate=gate, gate_strides=gate_strides)
+            self._gemm(name, a, w, bias, out, act=act, res=res, gate=gate, gate_strides=gate_strides)
             if rms_w is not None:
                 self._rms(name + "_norm", out.data_ptr(), out.stride(0), out.shape[0], self.S, rms_w, False)
 
@@ -327,7 +328,7 @@ class FusedVideoDiTBlock:
             self._proj("cross_o", self.attn, w["co_w"], w["co_b"], self.x, res=self.x)
         # FFN
         self._adaln("adaln2", self.x, self.h, shift=mod(3), scale=mod(4))
-        self._gemm("ffn_up", self.h, w["f0_w"], w["f0_b"], self.hid, act=_capi.FAM_ACT_GELU_TANH)
+        self._proj("ffn_up", self.h, w["f0_w"], w["f0_b"], self.hid, act=_capi.FAM_ACT_GELU_TANH)
         self._proj("ffn_down", self.hid, w["f2_w"], w["f2_b"], self.x, res=self.x, gate=mod(5), gate_strides=gstr)
 
     # ------------------------------------------------------------------ execution
@@ -403,7 +404,8 @@ class FusedVideoPrefill:
         self.lib = lib = _capi.load()
         if M <= 128:   # one split-K partial buffer for every block
             need = max(lib.fam_gemm_partial_splits(M, n_, k_) * M * n_
-                       for n_, k_ in ((hidden, self.A), (self.A, hidden), (hidden, ffn_dim), (3 * self.A, hidden)))
+                       for n_, k_ in ((hidden, self.A), (self.A, hidden), (hidden, ffn_dim), (3 * self.A, hidden),
+                                      (ffn_dim, hidden)))
             self.shared["part"] = torch.zeros(need, dtype=torch.float32, device=dev)
         # the context K/V of every block that cross-attends, in one GEMM per call: the context
         # does not change between blocks, only the weights do

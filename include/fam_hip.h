@@ -255,7 +255,8 @@ int fam_gemm(const fam_gemm_desc* d, void* stream);
  * Replaces: the projections of the action tokens (q/k/v/o, cross q/o, FFN up/down, head;
  *           FB/wan_video_dit.py:188-191,215-218,262-263, FB/action_dit.py:317-318) and the
  *           reference's split-K kernel fastwam::skmm (FG/mot.py:1080-1243).
- * Limits: M <= 128; K % 8 == 0; lda, ldw multiples of 8; 16-byte aligned a, w, partials.
+ * Limits: M <= 128; K % 8 == 0; lda, ldw multiples of 8; 16-byte aligned a, w, partials;
+ * above 64 rows lda, ldw < 2^23 elements.
  */
 int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64_t ldw, float* partials,
                      int64_t M, int64_t N, int64_t K, void* stream);
@@ -307,7 +308,9 @@ int fam_gemm_final(const void* a, int64_t lda, const void* w, int64_t ldw, const
  * Partials source: v = sum over z < splits of partials[z * split_stride + m * ldp + n] (ldp = N when
  * 0): with ldp above N a row kernel reads a column window of wider planes (a q/k/v split-K
  * product finished segment by segment).
- * Limits: 1 <= N <= 4096; a normalised row must be bf16 (out_f32 == 0).
+ * Limits: 1 <= N <= 4096, or any N < 2^30 without normalisation when the row is vectorisable
+ * (partials source, N % 4 == 0, <= 64 splits, ldo / ldp / ldr multiples of 4, 8-byte aligned
+ * bf16 operands, 16-byte aligned fp32 ones); a normalised row must be bf16 (out_f32 == 0).
  */
 typedef struct fam_rowop_desc {
   int src;

@@ -119,6 +119,13 @@ def test_validation_rejects_before_launch(lib):
     assert [lib.fam_gemm_partial_splits(32, n, k) for n, k in ((3072, 1024), (1024, 1024), (4096, 1024),
                                                               (1024, 4096), (7, 1024))] == [2, 4, 1, 4, 8]
     assert lib.fam_gemm_partial_splits(0, 64, 64) == 0
+    # the video prefill's 98-row projections: the streaming kernel (one round of 128-column
+    # workgroups, whole 256-wide chunks per split) for FFN down / FFN up / q|k|v, the one-slice
+    # wide kernel for the 3072 x 3072 ones
+    assert [lib.fam_gemm_partial_splits(98, n, k) for n, k in ((3072, 14336), (14336, 3072), (9216, 3072),
+                                                              (3072, 3072))] == [10, 2, 3, 6]
+    # above 64 rows the strides must stay below 2^23 elements (32-bit buffer offsets)
+    assert lib.fam_gemm_partial(16, 3072, 32, 1 << 23, 48, 98, 64, 64, None) == _capi.FAM_ERR_UNSUPPORTED
 
     r = _capi.RowopDesc()
     r.src, r.partials, r.splits, r.split_stride = _capi.FAM_ROWSRC_PARTIALS, 16, 2, 4 * 64
@@ -130,8 +137,15 @@ def test_validation_rejects_before_launch(lib):
     assert "shift" in _err(lib)
     r.norm, r.nseg, r.seg_width = _capi.FAM_ROWNORM_RMS, 1, 6  # segment width not a multiple of 4
     assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG
-    r.norm, r.nseg, r.N, r.ldo = _capi.FAM_ROWNORM_NONE, 0, 20000, 20000  # N beyond one workgroup row
-    assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG
+    # rows beyond one workgroup (4096 columns): only without normalisation on the vectorised path
+    r.norm, r.nseg, r.N, r.ldo, r.split_stride = _capi.FAM_ROWNORM_NONE, 0, 20002, 20002, 4 * 20002
+    assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG    # N % 4 != 0
+    assert "4096" in _err(lib)
+    r.N, r.ldo, r.split_stride, r.ldn = 20000, 20000, 4 * 20000, 20000
+    r.norm = _capi.FAM_ROWNORM_LAYERNORM
+    assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG    # a norm needs the whole row
+    assert "4096" in _err(lib)
+    r.norm = _capi.FAM_ROWNORM_NONE
     r.N, r.ldo, r.split_stride = 64, 64, 10  # partial planes overlap
     assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG
     r.split_stride, r.src = 256, 9
