@@ -552,7 +552,8 @@ __global__ __launch_bounds__(NWV * 64) void partial_wide_kernel(PartArgs g) {
 // output columns (16 per wave) over kper = C x 256 of K and walks it in 256-wide chunks.
 // While the MFMAs of chunk c run, the next chunk is already in flight: each wave's 16 x 256
 // weight panel in registers and the activation chunk (M rows x 256) in registers on its way
-// to the single LDS buffer.  Loads go through buffer descriptors, so k past the range (and
+// to the single LDS buffer, the activations issued first so that the LDS store between the
+// chunks does not also wait for the weights.  Loads go through buffer descriptors, so k past the range (and
 // the whole prefetch after the last chunk) reads zeros without a select on the loaded value,
 // which would make the compiler wait on each load right after issuing it; the prologue is
 // drained before the loop for the same reason.  Inside a chunk the activation fragments of
@@ -609,8 +610,8 @@ __global__ __launch_bounds__(512) void partial_stream_kernel(PartArgs g, int kpe
   for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int k0 = kb; k0 < ke; k0 += KS) {
     const int klim = k0 + KS < ke ? K : 0;   // 0: past the last chunk, every offset is out of range
+    loadA(k0 + KS, klim);   // first: loads return in order, so the LDS store waits for these only
     loadW(k0 + KS, klim, wx);
-    loadA(k0 + KS, klim);
     __builtin_amdgcn_sched_barrier(0);
     bf16x8 bc[MT], bn[MT];
 #pragma unroll

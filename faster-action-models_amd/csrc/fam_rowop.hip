@@ -446,13 +446,28 @@ static bool vec_eligible(const fam_rowop_desc* d) {
   return true;
 }
 
+// Rows wider than one workgroup are tiled over grid.y, one tile of 256 NW columns per
+// workgroup: without normalisation any tiling works; an RMS row tiles when every segment is
+// exactly one tile (the q | k | v row of a fused projection, each segment normalised inside
+// its own workgroup).  Returns the waves per workgroup, or 0 when the row does not tile.
+static int rms_tile_waves(const fam_rowop_desc* d) {
+  if (d->norm != FAM_ROWNORM_RMS || d->seg_width % 256 != 0) return 0;
+  const int64_t nw = d->seg_width / 256;
+  if (nw != 4 && nw != 8 && nw != 12 && nw != 16) return 0;
+  for (int g = 0; g < d->nseg && g < 2; ++g)
+    if (d->seg_col0[g] % d->seg_width != 0) return 0;
+  return (int)nw;
+}
+
 extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
   FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_rowop: null descriptor");
-  FAM_REQUIRE(d->M >= 0 && d->N >= 1 && (d->N <= 4 * RT * 4 || (d->N < (1LL << 30) && d->norm == FAM_ROWNORM_NONE &&
-                                                                  vec_eligible(d))),
+  FAM_REQUIRE(d->M >= 0 && d->N >= 1 &&
+                  (d->N <= 4 * RT * 4 ||
+                   (d->N < (1LL << 30) && (d->norm == FAM_ROWNORM_NONE || rms_tile_waves(d) > 0) && vec_eligible(d))),
               FAM_ERR_INVALID_ARG,
-              "fam_rowop: need 1 <= N <= 4096, or a wider row without normalisation on the vectorised path "
-              "(N %% 4 == 0, partials source, 16-byte aligned operands) (N=%lld)", (long long)d->N);
+              "fam_rowop: need 1 <= N <= 4096, or a wider row on the vectorised path (N %% 4 == 0, partials "
+              "source, aligned operands) without normalisation or with RMS segments of one tile each (N=%lld)",
+              (long long)d->N);
   FAM_REQUIRE(d->out, FAM_ERR_INVALID_ARG, "fam_rowop: out must be non-null");
   FAM_REQUIRE(d->ldo >= d->N, FAM_ERR_INVALID_ARG, "fam_rowop: ldo must be >= N");
   if (d->src == FAM_ROWSRC_PARTIALS) {
@@ -523,13 +538,15 @@ extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
   a.nout = (bf16*)d->nout; a.ldn = d->ldn;
   hipStream_t s = (hipStream_t)stream;
   if (vec_eligible(d)) {
-    const int nw = d->N <= 1024 ? 4 : (d->N <= 2048 ? 8 : 16);
+    const int tw = d->N > 4096 ? rms_tile_waves(d) : 0;
+    const int nw = tw > 0 ? tw : (d->N <= 1024 ? 4 : (d->N <= 2048 ? 8 : 16));
     const dim3 grid((unsigned)d->M, (unsigned)((d->N + nw * 256 - 1) / (nw * 256)));
     const int ms = d->splits <= 4 ? 4 : (d->splits <= 8 ? 8 : 16);
 #define FAM_ROWVEC(NW_, MS_) \
   if (nw == NW_ && ms == MS_) FAM_LAUNCH((rowop_vec_kernel<NW_, MS_>), grid, dim3(NW_ * 64), 0, s, a)
     FAM_ROWVEC(4, 4); FAM_ROWVEC(4, 8); FAM_ROWVEC(4, 16);
     FAM_ROWVEC(8, 4); FAM_ROWVEC(8, 8); FAM_ROWVEC(8, 16);
+    FAM_ROWVEC(12, 4); FAM_ROWVEC(12, 8); FAM_ROWVEC(12, 16);
     FAM_ROWVEC(16, 4); FAM_ROWVEC(16, 8); FAM_ROWVEC(16, 16);
 #undef FAM_ROWVEC
     return fam_host::check_launch("fam_rowop");

@@ -198,10 +198,14 @@ class FusedVideoDiTBlock:
         return splits
 
     def _rowop(self, name, *, N, splits, bias, out, res=None, gate=None, gate_strides=(0, 0, 1), rms_w=None,
-               rope=False, col0=0, ldp=0, act=_capi.FAM_ACT_NONE):
-        """out = res + gate * act(sum of the partial planes + bias) (or act(sum + bias)), then,
-        with rms_w, RMSNorm of the row over N with that weight (and RoPE), in place.  col0 / ldp:
-        columns [col0, col0 + N) of planes whose rows are ldp wide."""
+               rope=False, col0=0, ldp=0, act=_capi.FAM_ACT_NONE, segs=None, seg_width=0, ln=None, adaln=None,
+               nout=None):
+        """out = res + gate * act(sum of the partial planes + bias) (or act(sum + bias)), then
+        one normalisation of the stored row: rms_w, RMSNorm over the N columns in place; segs
+        [(col0, weight)] of seg_width, RMSNorm per segment in place; ln (weight, bias),
+        LayerNorm into nout; adaln (shift, scale) [rows, H] views, AdaLN into nout; RoPE on the
+        RMS segments with rope.  col0 / ldp: columns [col0, col0 + N) of planes whose rows are
+        ldp wide."""
         M = self.B * self.S
         ldp = ldp or N
         d = _capi.RowopDesc()
@@ -219,10 +223,22 @@ class FusedVideoDiTBlock:
         d.out, d.ldo, d.out_f32 = out.data_ptr(), out.stride(0), 0
         d.eps = self.eps
         if rms_w is not None:
+            segs, seg_width = [(0, rms_w)], N
+        if ln is not None:
+            d.norm = _capi.FAM_ROWNORM_LAYERNORM
+            d.ln_weight, d.ln_bias = ln[0].data_ptr(), ln[1].data_ptr()
+            d.nout, d.ldn = nout.data_ptr(), nout.stride(0)
+        elif adaln is not None:
+            d.norm = _capi.FAM_ROWNORM_ADALN
+            d.shift, d.scale = adaln[0].data_ptr(), adaln[1].data_ptr()
+            d.mod_bs, d.mod_rs = self._mod_strides()
+            d.nout, d.ldn = nout.data_ptr(), nout.stride(0)
+        elif segs:
             d.norm = _capi.FAM_ROWNORM_RMS
-            d.nseg = 1
-            d.seg_col0[0], d.seg_weight[0] = 0, rms_w.data_ptr()
-            d.seg_width = N
+            d.nseg = len(segs)
+            for i, (c0, wt) in enumerate(segs):
+                d.seg_col0[i], d.seg_weight[i] = c0, wt.data_ptr()
+            d.seg_width = seg_width
             d.nout, d.ldn = out.data_ptr(), out.stride(0)
             if rope:
                 cos, sin, trs, tes = self.rope
@@ -233,21 +249,31 @@ class FusedVideoDiTBlock:
         self._add(name, "fam_rowop", (C.byref(d),), "rowop")
 
     def _proj(self, name, a, w, bias, out, res=None, gate=None, gate_strides=(0, 0, 1), rms_w=None,
-              act=_capi.FAM_ACT_NONE):
-        """out = [res +] [gate *] act(a w^T + bias) [then RMSNorm]: split-K + row kernel at <= 128
-        rows, otherwise one fam_gemm (+ fam_rmsnorm_rope for the norm)."""
+              act=_capi.FAM_ACT_NONE, ln=None, adaln=None, nout=None):
+        """out = [res +] [gate *] act(a w^T + bias) [then RMSNorm in place, or LayerNorm / AdaLN
+        of the stored row into nout]: split-K + row kernel at <= 128 rows, otherwise one
+        fam_gemm followed by the norm's own kernel."""
         if self.splitk:
             sp = self._partial(name, a, w)
             self._rowop(name + "_row", N=w.shape[0], splits=sp, bias=bias, out=out, res=res, gate=gate,
-                        gate_strides=gate_strides, rms_w=rms_w, act=act)
+                        gate_strides=gate_strides, rms_w=rms_w, act=act, ln=ln, adaln=adaln, nout=nout)
         else:
             self._gemm(name, a, w, bias, out, act=act, res=res, gate=gate, gate_strides=gate_strides)
             if rms_w is not None:
                 self._rms(name + "_norm", out.data_ptr(), out.stride(0), out.shape[0], self.S, rms_w, False)
+            if ln is not None:
+                self._adaln(name + "_ln", out, nout, lw=ln[0], lb=ln[1])
+            if adaln is not None:
+                self._adaln(name + "_adaln", out, nout, shift=adaln[0], scale=adaln[1])
+
+    def _mod_strides(self):
+        """(batch, row) element strides of a modulation chunk view: per token or per batch."""
+        H = self.x.shape[1]
+        return (self.S * 6 * H, 6 * H) if self.per_token else (6 * H, 0)
 
     def _adaln(self, name, x, y, shift=None, scale=None, lw=None, lb=None):
         M, H = x.shape
-        mbs, mrs = (self.S * 6 * H, 6 * H) if self.per_token else (6 * H, 0)
+        mbs, mrs = self._mod_strides()
         args = (x.data_ptr(), x.stride(0), shift.data_ptr() if shift is not None else None,
                 scale.data_ptr() if scale is not None else None, mbs, mrs,
                 lw.data_ptr() if lw is not None else None, lb.data_ptr() if lb is not None else None,
@@ -292,17 +318,24 @@ class FusedVideoDiTBlock:
         self._adaln("adaln1", self.x, self.h, shift=mod(0), scale=mod(1))
         qp = self.qkv.data_ptr()
         if self.splitk:
-            # one split-K product for q|k|v, finished window by window: k and q with their
-            # RMSNorm + RoPE, v with its bias
+            # one split-K product for q|k|v; one row launch finishes it, q and k RMS-normalised
+            # and rotated in their own workgroups, v with its bias (a q|k|v row tiles when the
+            # head width A is 1024, 2048, 3072 or 4096, otherwise one launch per segment)
             sp = self._partial("qkv", self.h, w["qkv_w"])
             b = w["qkv_b"]
-            self._rowop("k_row", N=A, splits=sp, bias=b[A:2 * A], out=self.qkv[:, A:2 * A], rms_w=w["nk"], rope=True,
-                        col0=A, ldp=3 * A)
-            self._rowop("v_row", N=A, splits=sp, bias=b[2 * A:], out=self.qkv[:, 2 * A:], col0=2 * A, ldp=3 * A)
-            if self.kv_only:
-                return
-            self._rowop("q_row", N=A, splits=sp, bias=b[:A], out=self.qkv[:, :A], rms_w=w["nq"], rope=True,
-                        col0=0, ldp=3 * A)
+            if A % 1024 == 0 and A <= 4096:
+                self._rowop("qkv_row", N=3 * A, splits=sp, bias=b, out=self.qkv, segs=[(0, w["nq"]), (A, w["nk"])],
+                            seg_width=A, rope=True)
+                if self.kv_only:
+                    return
+            else:
+                self._rowop("k_row", N=A, splits=sp, bias=b[A:2 * A], out=self.qkv[:, A:2 * A], rms_w=w["nk"],
+                            rope=True, col0=A, ldp=3 * A)
+                self._rowop("v_row", N=A, splits=sp, bias=b[2 * A:], out=self.qkv[:, 2 * A:], col0=2 * A, ldp=3 * A)
+                if self.kv_only:
+                    return
+                self._rowop("q_row", N=A, splits=sp, bias=b[:A], out=self.qkv[:, :A], rms_w=w["nq"], rope=True,
+                            col0=0, ldp=3 * A)
         else:
             self._gemm("qkv", self.h, w["qkv_w"], w["qkv_b"], self.qkv)
             self._rms("k_norm_rope", qp + 2 * A, 3 * A, M, S, w["nk"], True)
@@ -311,10 +344,16 @@ class FusedVideoDiTBlock:
             self._rms("q_norm_rope", qp, 3 * A, M, S, w["nq"], True)
         self._attention("self_attn", qp, 3 * A, qp + 2 * A, 3 * A, qp + 4 * A, 3 * A, S, S, S,
                         mask=self.self_mask, mask_strides=(0, 0, S))
-        self._proj("o", self.attn, w["o_w"], w["o_b"], self.x, res=self.x, gate=mod(2), gate_strides=gstr)
+        # the o row also normalises for what follows: norm3 (LayerNorm) before the cross
+        # attention, else the FFN's AdaLN
+        if Lc > 0:
+            self._proj("o", self.attn, w["o_w"], w["o_b"], self.x, res=self.x, gate=mod(2), gate_strides=gstr,
+                       ln=(w["n3_w"], w["n3_b"]), nout=self.h)
+        else:
+            self._proj("o", self.attn, w["o_w"], w["o_b"], self.x, res=self.x, gate=mod(2), gate_strides=gstr,
+                       adaln=(mod(3), mod(4)), nout=self.h)
         # cross-attention
         if Lc > 0:
-            self._adaln("norm3", self.x, self.h, lw=w["n3_w"], lb=w["n3_b"])
             self._proj("cross_q", self.h, w["cq_w"], w["cq_b"], self.qc, rms_w=w["cnq"])
             if self.ctx_kv is None:
                 self._gemm("cross_kv", self.ctx, w["ckv_w"], w["ckv_b"], self.ckv)
@@ -325,9 +364,9 @@ class FusedVideoDiTBlock:
                 kp, kld = buf.data_ptr() + 2 * col, buf.stride(0)
             self._attention("cross_attn", self.qc.data_ptr(), A, kp, kld, kp + 2 * A, kld, S, Lc, Lc,
                             mask=self.ctx_mask, mask_strides=(S * Lc, 0, Lc))
-            self._proj("cross_o", self.attn, w["co_w"], w["co_b"], self.x, res=self.x)
-        # FFN
-        self._adaln("adaln2", self.x, self.h, shift=mod(3), scale=mod(4))
+            self._proj("cross_o", self.attn, w["co_w"], w["co_b"], self.x, res=self.x, adaln=(mod(3), mod(4)),
+                       nout=self.h)
+        # FFN (its AdaLN came with the last projection's row)
         self._proj("ffn_up", self.h, w["f0_w"], w["f0_b"], self.hid, act=_capi.FAM_ACT_GELU_TANH)
         self._proj("ffn_down", self.hid, w["f2_w"], w["f2_b"], self.x, res=self.x, gate=mod(5), gate_strides=gstr)
 

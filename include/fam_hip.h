@@ -308,9 +308,11 @@ int fam_gemm_final(const void* a, int64_t lda, const void* w, int64_t ldw, const
  * Partials source: v = sum over z < splits of partials[z * split_stride + m * ldp + n] (ldp = N when
  * 0): with ldp above N a row kernel reads a column window of wider planes (a q/k/v split-K
  * product finished segment by segment).
- * Limits: 1 <= N <= 4096, or any N < 2^30 without normalisation when the row is vectorisable
- * (partials source, N % 4 == 0, <= 64 splits, ldo / ldp / ldr multiples of 4, 8-byte aligned
- * bf16 operands, 16-byte aligned fp32 ones); a normalised row must be bf16 (out_f32 == 0).
+ * Limits: 1 <= N <= 4096, or any N < 2^30 when the row is vectorisable (partials source,
+ * N % 4 == 0, <= 64 splits, ldo / ldp / ldr multiples of 4, 8-byte aligned bf16 operands,
+ * 16-byte aligned fp32 ones) and either has no normalisation or RMS segments that each fill
+ * one tile (seg_width in {1024, 2048, 3072, 4096}, seg_col0 multiples of seg_width: a
+ * q | k | v row); a normalised row must be bf16 (out_f32 == 0).
  */
 typedef struct fam_rowop_desc {
   int src;

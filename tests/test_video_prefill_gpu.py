@@ -17,11 +17,16 @@ def _relerr(y, ref):
     return ((y.float() - ref).abs().max() / ref.abs().max()).item()
 
 
-@pytest.mark.parametrize("frames,tpf,Lc,num_run,ragged", [(2, 49, 40, 0, True), (1, 98, 40, 0, False),
-                                                          (2, 24, 24, 2, True), (1, 48, 0, 0, False)])
-def test_video_prefill_kv_matches_oracle(frames, tpf, Lc, num_run, ragged):
+@pytest.mark.parametrize("frames,tpf,Lc,num_run,ragged,nh", [(2, 49, 40, 0, True, 4), (1, 98, 40, 0, False, 4),
+                                                             (2, 24, 24, 2, True, 4), (1, 48, 0, 0, False, 4),
+                                                             (2, 49, 40, 0, True, 8), (1, 48, 0, 0, False, 8)])
+def test_video_prefill_kv_matches_oracle(frames, tpf, Lc, num_run, ragged, nh):
+    """Every layer's K/V against the oracle's prefill.  Each block's q|k|v row is finished by
+    one row launch when the head width A = nh * 128 tiles it (nh=8: A=1024), segment by
+    segment otherwise; the o row carries norm3 (or, without context, the FFN's AdaLN) and the
+    cross-o row the FFN's AdaLN."""
     from fam.video_dit import FusedVideoPrefill
-    Sv, H, nh, Dh, F, L = frames * tpf, 512, 4, 128, 1024, 3
+    Sv, H, Dh, F, L = frames * tpf, 512, 128, 1024, 3
     ocfg = O.ActionDiTConfig(hidden_dim=H, action_dim=7, ffn_dim=F, text_dim=H, freq_dim=256, num_heads=nh,
                              attn_head_dim=Dh, num_layers=L)
     p = {k: v.to(torch.bfloat16) for k, v in O.init_action_dit_params(ocfg, 41).items()}
@@ -48,7 +53,7 @@ def test_video_prefill_kv_matches_oracle(frames, tpf, Lc, num_run, ragged):
         ek, ev = _relerr(k.cpu(), rk), _relerr(v.cpu(), rv)
         worst = max(worst, ek, ev)
         assert ek <= 2e-2 and ev <= 2e-2, (i, ek, ev)
-    print(f"prefill frames={frames} tpf={tpf} Lc={Lc} num_run={num_run}: {pf.num_launches} launches, "
+    print(f"prefill frames={frames} tpf={tpf} Lc={Lc} num_run={num_run} heads={nh}: {pf.num_launches} launches, "
           f"worst relerr {worst:.3e}")
     # graph replay: the same bits
     first = [(k.clone(), v.clone()) for k, v in kv]
