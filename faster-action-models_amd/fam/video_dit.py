@@ -69,6 +69,11 @@ class FusedVideoDiTBlock:
         kv_only: build only what the block's K/V need -- modulation, AdaLN1, the q/k/v
             projection and the key's RMSNorm + RoPE -- for a last prefill block whose output
             nobody reads.
+        pre_normed: the block's modulation and AdaLN1 output (in "mods" and "h") were produced
+            by the block before it (see next_mod); the block starts at its q/k/v projection.
+        next_mod: (the next block's modulation [6H] bf16, that block's "mods" buffer): before
+            its FFN the block also builds the next block's modulation, and its FFN-down row
+            applies the next block's AdaLN1 into "h" (only with the split-K projections).
     `self.qkv` holds [q | k | v] per row; after `run()` its k (normalised, rotated) and v
     columns are the block's attention K/V (`kv()`).
     """
@@ -77,9 +82,11 @@ class FusedVideoDiTBlock:
                  ffn_dim: int, batch: int, seq_len: int, ctx_len: int, freqs: torch.Tensor, eps: float = 1e-6,
                  per_token_mod: bool = True, device="cuda", self_mask: Optional[torch.Tensor] = None,
                  ctx_mask: Optional[torch.Tensor] = None, shared: Optional[Dict[str, torch.Tensor]] = None,
-                 kv_only: bool = False, ctx_kv: Optional[tuple] = None):
+                 kv_only: bool = False, ctx_kv: Optional[tuple] = None, pre_normed: bool = False,
+                 next_mod: Optional[tuple] = None):
         dev = torch.device(device)
         self.kv_only = kv_only
+        self.pre_normed, self.next_mod = pre_normed, next_mod
         self.ctx_kv = ctx_kv
         self.lib = _capi.load()
         self.B, self.S, self.Lc = batch, seq_len, ctx_len
@@ -307,15 +314,18 @@ class FusedVideoDiTBlock:
         w, H, A, S, Lc = self.w, self.H, self.A, self.S, self.Lc
         M = self.B * S
         rows = self.mods.shape[0]
-        self._add("modulation", "fam_add_modulation",
-                  (self.tmod_in.data_ptr(), w["mod"].data_ptr(), self.mods.data_ptr(), rows, 1, 6 * H), "modulation")
+        if not self.pre_normed:
+            self._add("modulation", "fam_add_modulation",
+                      (self.tmod_in.data_ptr(), w["mod"].data_ptr(), self.mods.data_ptr(), rows, 1, 6 * H),
+                      "modulation")
 
-        def mod(i):  # chunk i of (modulation + t_mod), [rows, H] view with row stride 6H
-            return self.mods[:, i * H:(i + 1) * H]
+        def mod(i, mods=None):  # chunk i of (modulation + t_mod), [rows, H] view with row stride 6H
+            return (self.mods if mods is None else mods)[:, i * H:(i + 1) * H]
 
         gstr = (S * 6 * H, 6 * H, 1) if self.per_token else (6 * H, 0, 1)
         # self-attention
-        self._adaln("adaln1", self.x, self.h, shift=mod(0), scale=mod(1))
+        if not self.pre_normed:
+            self._adaln("adaln1", self.x, self.h, shift=mod(0), scale=mod(1))
         qp = self.qkv.data_ptr()
         if self.splitk:
             # one split-K product for q|k|v; one row launch finishes it, q and k RMS-normalised
@@ -368,7 +378,18 @@ class FusedVideoDiTBlock:
                        nout=self.h)
         # FFN (its AdaLN came with the last projection's row)
         self._proj("ffn_up", self.h, w["f0_w"], w["f0_b"], self.hid, act=_capi.FAM_ACT_GELU_TANH)
-        self._proj("ffn_down", self.hid, w["f2_w"], w["f2_b"], self.x, res=self.x, gate=mod(5), gate_strides=gstr)
+        if self.next_mod is not None:
+            if not self.splitk:
+                raise ValueError("next_mod needs the split-K projections (<= 128 rows, widths <= 4096)")
+            # the next block's modulation now, so that this row can apply its AdaLN1
+            nw, nmods = self.next_mod
+            self._add("next_modulation", "fam_add_modulation",
+                      (self.tmod_in.data_ptr(), nw.data_ptr(), nmods.data_ptr(), rows, 1, 6 * H), "modulation")
+            self._proj("ffn_down", self.hid, w["f2_w"], w["f2_b"], self.x, res=self.x, gate=mod(5), gate_strides=gstr,
+                       adaln=(mod(0, nmods), mod(1, nmods)), nout=self.h)
+        else:
+            self._proj("ffn_down", self.hid, w["f2_w"], w["f2_b"], self.x, res=self.x, gate=mod(5),
+                       gate_strides=gstr)
 
     # ------------------------------------------------------------------ execution
     def set_inputs(self, x: torch.Tensor, t_mod: torch.Tensor, context: torch.Tensor) -> None:
@@ -460,12 +481,25 @@ class FusedVideoPrefill:
             self.cnk = [params[f"blocks.{i}.cross_attn.norm_k.weight"].to(device=dev, dtype=_BF16).contiguous()
                         for i in range(ncross)]
             self._ctx_launches(batch * ctx_len, ctx_len, head_dim, eps)
+        # at <= 128 rows each block's FFN-down row also applies the next block's AdaLN1, with the
+        # next block's modulation built one block early into the other of two "mods" buffers
+        chain = M <= 128 and hidden <= 4096 and self.A <= 4096     # the blocks' split-K condition
+        mods = [self.shared["mods"], z(rows, 6 * hidden) if chain else self.shared["mods"]]
+
+        def next_mod(i):
+            if not chain or i + 1 >= self.n_run:
+                return None
+            nw = params[f"blocks.{i + 1}.modulation"].to(device=dev, dtype=_BF16).reshape(6 * hidden).contiguous()
+            return nw, mods[(i + 1) % 2]
+
         self.blocks = [FusedVideoDiTBlock(params, i, hidden=hidden, num_heads=num_heads, head_dim=head_dim,
                                           ffn_dim=ffn_dim, batch=batch, seq_len=video_len, ctx_len=ctx_len,
                                           freqs=freqs, eps=eps, per_token_mod=per_token_mod, device=dev,
-                                          self_mask=video_mask, ctx_mask=ctx_mask, shared=self.shared,
+                                          self_mask=video_mask, ctx_mask=ctx_mask,
+                                          shared={**self.shared, "mods": mods[i % 2]},
                                           kv_only=(i == self.n_run - 1),
-                                          ctx_kv=(self.ctxkv, i * 2 * self.A) if i < ncross else None)
+                                          ctx_kv=(self.ctxkv, i * 2 * self.A) if i < ncross else None,
+                                          pre_normed=chain and i > 0, next_mod=next_mod(i))
                        for i in range(self.n_run)]
         self.steps += [f for b in self.blocks for f in b.steps]
         self.meta += [m for b in self.blocks for m in b.meta]
