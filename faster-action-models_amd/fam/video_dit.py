@@ -69,11 +69,12 @@ class FusedVideoDiTBlock:
         kv_only: build only what the block's K/V need -- modulation, AdaLN1, the q/k/v
             projection and the key's RMSNorm + RoPE -- for a last prefill block whose output
             nobody reads.
-        pre_normed: the block's modulation and AdaLN1 output (in "mods" and "h") were produced
-            by the block before it (see next_mod); the block starts at its q/k/v projection.
-        next_mod: (the next block's modulation [6H] bf16, that block's "mods" buffer): before
-            its FFN the block also builds the next block's modulation, and its FFN-down row
-            applies the next block's AdaLN1 into "h" (only with the split-K projections).
+        mods_ready: "mods" (may be a row-strided view, e.g. one block of a [rows, L, 6H]
+            buffer) already holds this block's modulation + t_mod; no modulation launch.
+        pre_normed: the block's AdaLN1 output ("h") was produced by the block before it (see
+            next_mod); the block starts at its q/k/v projection.
+        next_mod: the next block's ready "mods" view: this block's FFN-down row applies the
+            next block's AdaLN1 into "h" (only with the split-K projections).
     `self.qkv` holds [q | k | v] per row; after `run()` its k (normalised, rotated) and v
     columns are the block's attention K/V (`kv()`).
     """
@@ -82,11 +83,11 @@ class FusedVideoDiTBlock:
                  ffn_dim: int, batch: int, seq_len: int, ctx_len: int, freqs: torch.Tensor, eps: float = 1e-6,
                  per_token_mod: bool = True, device="cuda", self_mask: Optional[torch.Tensor] = None,
                  ctx_mask: Optional[torch.Tensor] = None, shared: Optional[Dict[str, torch.Tensor]] = None,
-                 kv_only: bool = False, ctx_kv: Optional[tuple] = None, pre_normed: bool = False,
-                 next_mod: Optional[tuple] = None):
+                 kv_only: bool = False, ctx_kv: Optional[tuple] = None, mods_ready: bool = False,
+                 pre_normed: bool = False, next_mod: Optional[torch.Tensor] = None):
         dev = torch.device(device)
         self.kv_only = kv_only
-        self.pre_normed, self.next_mod = pre_normed, next_mod
+        self.mods_ready, self.pre_normed, self.next_mod = mods_ready, pre_normed, next_mod
         self.ctx_kv = ctx_kv
         self.lib = _capi.load()
         self.B, self.S, self.Lc = batch, seq_len, ctx_len
@@ -122,17 +123,20 @@ class FusedVideoDiTBlock:
 
         sh = shared or {}
 
-        def buf(name, *shape):
+        def buf(name, *shape, row_strided=False):
             t = sh.get(name)
             if t is None:
                 return torch.zeros(*shape, dtype=_BF16, device=dev)
-            if tuple(t.shape) != tuple(shape) or t.dtype != _BF16 or not t.is_contiguous():
-                raise ValueError(f"shared buffer {name!r} must be contiguous bf16 {tuple(shape)}")
+            dense = t.is_contiguous() or (row_strided and t.stride(1) == 1 and t.stride(0) >= shape[1]
+                                          and t.stride(0) % 8 == 0)
+            if tuple(t.shape) != tuple(shape) or t.dtype != _BF16 or not dense:
+                raise ValueError(f"shared buffer {name!r} must be {'row-strided' if row_strided else 'contiguous'} "
+                                 f"bf16 {tuple(shape)}")
             return t
         self.x = buf("x", M, H)
         self.tmod_in = buf("tmod_in", M if per_token_mod else batch, 6 * H)
         self.ctx = buf("ctx", batch * ctx_len, H)
-        self.mods = buf("mods", M if per_token_mod else batch, 6 * H)
+        self.mods = buf("mods", M if per_token_mod else batch, 6 * H, row_strided=True)
         self.h = buf("h", M, H)
         self.qkv = torch.zeros(M, 3 * A, dtype=_BF16, device=dev)   # per block: its K/V cache
         self.attn = buf("attn", M, A)
@@ -273,10 +277,10 @@ class FusedVideoDiTBlock:
             if adaln is not None:
                 self._adaln(name + "_adaln", out, nout, shift=adaln[0], scale=adaln[1])
 
-    def _mod_strides(self):
+    def _mod_strides(self, mods=None):
         """(batch, row) element strides of a modulation chunk view: per token or per batch."""
-        H = self.x.shape[1]
-        return (self.S * 6 * H, 6 * H) if self.per_token else (6 * H, 0)
+        rs = (self.mods if mods is None else mods).stride(0)
+        return (self.S * rs, rs) if self.per_token else (rs, 0)
 
     def _adaln(self, name, x, y, shift=None, scale=None, lw=None, lb=None):
         M, H = x.shape
@@ -314,7 +318,7 @@ class FusedVideoDiTBlock:
         w, H, A, S, Lc = self.w, self.H, self.A, self.S, self.Lc
         M = self.B * S
         rows = self.mods.shape[0]
-        if not self.pre_normed:
+        if not self.mods_ready:
             self._add("modulation", "fam_add_modulation",
                       (self.tmod_in.data_ptr(), w["mod"].data_ptr(), self.mods.data_ptr(), rows, 1, 6 * H),
                       "modulation")
@@ -322,7 +326,7 @@ class FusedVideoDiTBlock:
         def mod(i, mods=None):  # chunk i of (modulation + t_mod), [rows, H] view with row stride 6H
             return (self.mods if mods is None else mods)[:, i * H:(i + 1) * H]
 
-        gstr = (S * 6 * H, 6 * H, 1) if self.per_token else (6 * H, 0, 1)
+        gstr = (*self._mod_strides(), 1)
         # self-attention
         if not self.pre_normed:
             self._adaln("adaln1", self.x, self.h, shift=mod(0), scale=mod(1))
@@ -381,10 +385,9 @@ class FusedVideoDiTBlock:
         if self.next_mod is not None:
             if not self.splitk:
                 raise ValueError("next_mod needs the split-K projections (<= 128 rows, widths <= 4096)")
-            # the next block's modulation now, so that this row can apply its AdaLN1
-            nw, nmods = self.next_mod
-            self._add("next_modulation", "fam_add_modulation",
-                      (self.tmod_in.data_ptr(), nw.data_ptr(), nmods.data_ptr(), rows, 1, 6 * H), "modulation")
+            nmods = self.next_mod
+            if nmods.stride(0) != self.mods.stride(0):
+                raise ValueError("next_mod must have the row stride of this block's mods")
             self._proj("ffn_down", self.hid, w["f2_w"], w["f2_b"], self.x, res=self.x, gate=mod(5), gate_strides=gstr,
                        adaln=(mod(0, nmods), mod(1, nmods)), nout=self.h)
         else:
@@ -481,29 +484,45 @@ class FusedVideoPrefill:
             self.cnk = [params[f"blocks.{i}.cross_attn.norm_k.weight"].to(device=dev, dtype=_BF16).contiguous()
                         for i in range(ncross)]
             self._ctx_launches(batch * ctx_len, ctx_len, head_dim, eps)
-        # at <= 128 rows each block's FFN-down row also applies the next block's AdaLN1, with the
-        # next block's modulation built one block early into the other of two "mods" buffers
+        # at <= 128 rows the modulation + t_mod of every block comes from one launch into a
+        # [rows, blocks, 6H] buffer, and each block's FFN-down row also applies the next block's
+        # AdaLN1
         chain = M <= 128 and hidden <= 4096 and self.A <= 4096     # the blocks' split-K condition
-        mods = [self.shared["mods"], z(rows, 6 * hidden) if chain else self.shared["mods"]]
+        if chain:
+            self.mod_table = torch.stack([params[f"blocks.{i}.modulation"].reshape(6 * hidden)
+                                          for i in range(self.n_run)]).to(device=dev, dtype=_BF16).contiguous()
+            self.mods_all = z(rows, self.n_run, 6 * hidden)
+            self._add_step("modulation_all", "fam_add_modulation",
+                           (self.shared["tmod_in"].data_ptr(), self.mod_table.data_ptr(), self.mods_all.data_ptr(),
+                            rows, self.n_run, 6 * hidden), "modulation")
 
-        def next_mod(i):
-            if not chain or i + 1 >= self.n_run:
-                return None
-            nw = params[f"blocks.{i + 1}.modulation"].to(device=dev, dtype=_BF16).reshape(6 * hidden).contiguous()
-            return nw, mods[(i + 1) % 2]
+        def mods(i):
+            return self.mods_all[:, i, :] if chain else self.shared["mods"]
 
         self.blocks = [FusedVideoDiTBlock(params, i, hidden=hidden, num_heads=num_heads, head_dim=head_dim,
                                           ffn_dim=ffn_dim, batch=batch, seq_len=video_len, ctx_len=ctx_len,
                                           freqs=freqs, eps=eps, per_token_mod=per_token_mod, device=dev,
                                           self_mask=video_mask, ctx_mask=ctx_mask,
-                                          shared={**self.shared, "mods": mods[i % 2]},
+                                          shared={**self.shared, "mods": mods(i)},
                                           kv_only=(i == self.n_run - 1),
                                           ctx_kv=(self.ctxkv, i * 2 * self.A) if i < ncross else None,
-                                          pre_normed=chain and i > 0, next_mod=next_mod(i))
+                                          mods_ready=chain, pre_normed=chain and i > 0,
+                                          next_mod=mods(i + 1) if chain and i + 1 < self.n_run else None)
                        for i in range(self.n_run)]
         self.steps += [f for b in self.blocks for f in b.steps]
         self.meta += [m for b in self.blocks for m in b.meta]
         self.graph: Optional[torch.cuda.CUDAGraph] = None
+
+    def _add_step(self, name, fname, args, kind):
+        f = getattr(self.lib, fname)
+        lib = self.lib
+
+        def run(stream):
+            rc = f(*args, stream)
+            if rc != 0:
+                raise _capi.FamError(f"{fname}[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
+        self.steps.append(run)
+        self.meta.append({"name": name, "kernel": kind})
 
     def _ctx_launches(self, rows, seq, head_dim, eps):
         """ctxkv = ctx [k|v weights of every block]^T + bias, then each block's K RMSNorm."""
@@ -517,15 +536,7 @@ class FusedVideoPrefill:
         d.rows_per_batch = rows
         self._descs.append(d)
 
-        def add(name, fname, args, kind):
-            f = getattr(lib, fname)
-
-            def run(stream):
-                rc = f(*args, stream)
-                if rc != 0:
-                    raise _capi.FamError(f"{fname}[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
-            self.steps.append(run)
-            self.meta.append({"name": name, "kernel": kind})
+        add = self._add_step
         add("ctx_kv_all", "fam_gemm", (C.byref(d),), "gemm")
         ld = self.ctxkv.stride(0)
         for i, wk in enumerate(self.cnk):
