@@ -62,6 +62,34 @@ def test_video_prefill_kv_matches_oracle(frames, tpf, Lc, num_run, ragged, nh):
     assert all(torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) for a, b in zip(first, kv2))
 
 
+def test_video_prefill_broadcast_modulation():
+    """Per-batch t_mod ([B, 6, H], per_token_mod=False): the chained blocks read their
+    modulation from one [B, blocks, 6H] buffer with a zero row stride; against the oracle fed
+    the same t_mod for every token."""
+    from fam.video_dit import FusedVideoPrefill
+    Sv, H, nh, Dh, F, L, Lc = 98, 512, 8, 128, 1024, 3, 40
+    ocfg = O.ActionDiTConfig(hidden_dim=H, action_dim=7, ffn_dim=F, text_dim=H, freq_dim=256, num_heads=nh,
+                             attn_head_dim=Dh, num_layers=L)
+    p = {k: v.to(torch.bfloat16) for k, v in O.init_action_dit_params(ocfg, 61).items()}
+    g = torch.Generator().manual_seed(62)
+    x = torch.randn(1, Sv, H, generator=g).to(torch.bfloat16)
+    tm = (torch.randn(1, 6, H, generator=g) * 0.2).to(torch.bfloat16)
+    ctx = torch.randn(1, Lc, H, generator=g).to(torch.bfloat16)
+    freqs = O.action_freqs(Dh, Sv)
+    pf = FusedVideoPrefill(p, num_layers=L, hidden=H, num_heads=nh, head_dim=Dh, ffn_dim=F, batch=1, video_len=Sv,
+                           ctx_len=Lc, freqs=freqs, per_token_mod=False)
+    kv = pf.prefill(x.cuda(), tm.cuda(), ctx.cuda())
+    p32 = {k: v.float() for k, v in p.items()}
+    ref = O.mot_prefill_video_cache(p32, ocfg, x.float(), freqs, tm.float()[:, None].expand(1, Sv, 6, H), ctx.float(),
+                                    torch.ones(Sv, Sv, dtype=torch.bool))
+    worst = 0.0
+    for i, ((k, v), (rk, rv)) in enumerate(zip(kv, ref)):
+        ek, ev = _relerr(k.cpu(), rk), _relerr(v.cpu(), rv)
+        worst = max(worst, ek, ev)
+        assert ek <= 2e-2 and ev <= 2e-2, (i, ek, ev)
+    print(f"prefill with per-batch t_mod: {pf.num_launches} launches, worst relerr {worst:.3e}")
+
+
 def test_video_prefill_feeds_the_mot_action_loop():
     """The inference call's video half feeding its action half: GPU prefill of a single-frame
     video (98 tokens, 2 layers, hidden 768) -> FusedActionDiT in MoT mode (set_video_kv from the
