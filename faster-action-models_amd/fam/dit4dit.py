@@ -229,6 +229,13 @@ class FusedDiT4DiTHead:
         self.qkv = torch.empty(R, 3 * D, dtype=_BF16, device=device)
         self.attn = torch.empty(R, D, dtype=_BF16, device=device)
         self.up = torch.empty(R, cfg.ff_mult * D, dtype=_BF16, device=device)
+        # FFN down (D x ff_mult*D): at <= 64 rows a split-K product over >= 256 workgroups,
+        # finished by the row kernel with bias and residual; the whole-K GEMM of D = 768
+        # output columns would run on only D / 16 workgroups
+        self.ff_split = R <= 64
+        if self.ff_split:
+            S = _capi.lib().fam_gemm_partial_splits(R, D, cfg.ff_mult * D)
+            self.ff_part = torch.empty(S, R, D, dtype=torch.float32, device=device)
         self.y = torch.empty(M, cfg.output_dim, dtype=_BF16, device=device)
         self.z = torch.empty(M, cfg.hidden_size, dtype=_BF16, device=device)
         self.vel = torch.empty(T, batch, A, dtype=_BF16, device=device)
@@ -299,7 +306,14 @@ class FusedDiT4DiTHead:
                 else:
                     ops.gemm(self.h, blk(i, "ff.net.0.proj.weight"), blk(i, "ff.net.0.proj.bias"), self.up,
                              prologue=_capi.FAM_PRO_LAYERNORM, pro_eps=cfg.norm_eps, act=_capi.FAM_ACT_GELU_TANH)
-                ops.gemm(self.up, blk(i, "ff.net.2.weight"), blk(i, "ff.net.2.bias"), self.h, res=self.h)
+                if self.ff_split:
+                    w2 = blk(i, "ff.net.2.weight")
+                    _capi.call("fam_gemm_partial", self.up.data_ptr(), self.up.stride(0), w2.data_ptr(), w2.stride(0),
+                               self.ff_part.data_ptr(), self.R, self.D, w2.shape[1],
+                               torch.cuda.current_stream().cuda_stream)
+                    ops.rowop(self.h, partials=self.ff_part, bias=blk(i, "ff.net.2.bias"), res=self.h)
+                else:
+                    ops.gemm(self.up, blk(i, "ff.net.2.weight"), blk(i, "ff.net.2.bias"), self.h, res=self.h)
             # output AdaLN (shift, scale order) + proj_out_2, action decoder, Euler step; the state
             # rows' outputs are dropped by the reference (pred[:, -horizon:]) and not computed here
             if self.fold:
