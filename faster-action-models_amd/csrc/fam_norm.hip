@@ -166,6 +166,7 @@ struct RmsRopeArgs {
   int64_t rows, seq, dim;
   const bf16* w; float eps;
   const float* cs; const float* sn; int64_t trs, tes, hd;
+  int64_t wgp;   // weight groups: row r is scaled by w + (r % wgp) * dim
 };
 
 template <int NV>
@@ -198,13 +199,14 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(RmsRopeArgs a) {
   const float rs = a.w ? rsqrtf(wave_sum(q) / (float)D + a.eps) : 1.0f;
   const int64_t pos = r % a.seq;
   bf16* yr = a.y + r * a.yrs;
+  const bf16* wr = a.w ? a.w + (r % a.wgp) * D : nullptr;
   auto emit = [&](int64_t c, bf16x8 t) {
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = to_f(t[e]);
     if (a.w) {
       // RMSNorm rounds to the storage dtype before the weight multiply (FB/wan_video_dit.py:166-167).
-      bf16x8 wv = load8(a.w + c);
+      bf16x8 wv = load8(wr + c);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = to_f(to_bf(to_f(to_bf(o[e] * rs)) * to_f(wv[e])));
     }
@@ -250,6 +252,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_vec_kernel(RmsRopeArgs a) {
   const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
   if (r0 >= a.rows) return;  // wave-uniform
   const int D = (int)a.dim, hd = (int)a.hd;
+  const bf16* wr = a.w ? a.w + (r0 % a.wgp) * (int64_t)D : nullptr;   // RPW > 1 only with one group
   bf16x8 in[RPW][NV], wv[NV];
   f32x4 t0[RPW][NT], t1[RPW][NT];
 #pragma unroll
@@ -263,7 +266,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_vec_kernel(RmsRopeArgs a) {
     for (int i = 0; i < NV; ++i) {
       const int c = (i * 64 + lane) * 8, cc = c < D ? c : 0;
       in[k][i] = load8(xr + cc);
-      if (k == 0 && a.w) wv[i] = load8(a.w + cc);   // wave-uniform
+      if (k == 0 && a.w) wv[i] = load8(wr + cc);   // wave-uniform
       if (i < NT) {
         const int j0 = ((TSH ? lane * 8 : cc) % hd) >> 1;   // first of the 4 rotation pairs of these 8 elements
         if constexpr (TAB == 1) {
@@ -391,10 +394,10 @@ extern "C" int fam_adaln(const void* x, int64_t x_row_stride, const void* shift,
   return fam_host::check_launch("fam_adaln");
 }
 
-extern "C" int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride,
-                                int64_t rows, int64_t seq_len, int64_t dim, const void* weight, float eps,
-                                const float* cos_tab, const float* sin_tab, int64_t tab_row_stride,
-                                int64_t tab_elem_stride, int64_t head_dim, void* stream) {
+static int rmsnorm_rope_impl(const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride, int64_t rows,
+                             int64_t seq_len, int64_t dim, const void* weight, int64_t groups, float eps,
+                             const float* cos_tab, const float* sin_tab, int64_t tab_row_stride,
+                             int64_t tab_elem_stride, int64_t head_dim, void* stream) {
   FAM_REQUIRE(x && y, FAM_ERR_INVALID_ARG, "fam_rmsnorm_rope: x and y must be non-null");
   FAM_REQUIRE(rows >= 0 && dim >= 8 && dim <= 16384 && dim % 8 == 0, FAM_ERR_INVALID_ARG,
               "fam_rmsnorm_rope: need dim %% 8 == 0 and 8 <= dim <= 16384 (dim=%lld)", (long long)dim);
@@ -415,7 +418,7 @@ extern "C" int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, in
   if (rows == 0) return FAM_OK;
   RmsRopeArgs a{(const bf16*)x, x_row_stride, (bf16*)y, y_row_stride, rows, seq_len > 0 ? seq_len : 1, dim,
                 (const bf16*)weight, eps, cos_tab, sin_tab, tab_row_stride, tab_elem_stride,
-                head_dim > 0 ? head_dim : 8};
+                head_dim > 0 ? head_dim : 8, groups};
   dim3 grid((unsigned)((rows + 3) / 4)), block(256);
   hipStream_t s = (hipStream_t)stream;
   // vector table reads: rows of 16-byte aligned fp32 with 4 consecutive pairs per 8 elements
@@ -427,7 +430,7 @@ extern "C" int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, in
   if (nv != 0 && tab != 3 && dim <= (int64_t)1 << 30) {
     const bool tsh = 512 % a.hd == 0;
     // two rows per wave once there are enough rows to fill the machine with half the waves
-    const bool two = rows >= 4096 && nv <= 6;
+    const bool two = rows >= 4096 && nv <= 6 && groups == 1;
     const dim3 grid2((unsigned)((rows + 7) / 8));
 #define FAM_RR_VEC2(NV, TAB, TSH)                                                                          \
   do {                                                                                                     \
@@ -466,4 +469,21 @@ extern "C" int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, in
     default: FAM_LAUNCH(rmsnorm_rope_kernel<0>, grid, block, 0, s, a); break;
   }
   return fam_host::check_launch("fam_rmsnorm_rope");
+}
+
+extern "C" int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride,
+                                int64_t rows, int64_t seq_len, int64_t dim, const void* weight, float eps,
+                                const float* cos_tab, const float* sin_tab, int64_t tab_row_stride,
+                                int64_t tab_elem_stride, int64_t head_dim, void* stream) {
+  return rmsnorm_rope_impl(x, x_row_stride, y, y_row_stride, rows, seq_len, dim, weight, 1, eps, cos_tab, sin_tab,
+                           tab_row_stride, tab_elem_stride, head_dim, stream);
+}
+
+extern "C" int fam_rmsnorm_grouped(const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride,
+                                   int64_t rows, int64_t dim, const void* weights, int64_t groups, float eps,
+                                   void* stream) {
+  FAM_REQUIRE(weights && groups >= 1, FAM_ERR_INVALID_ARG, "fam_rmsnorm_grouped: need weights and groups >= 1");
+  FAM_REQUIRE(rows % groups == 0, FAM_ERR_INVALID_ARG, "fam_rmsnorm_grouped: rows must be a multiple of groups");
+  return rmsnorm_rope_impl(x, x_row_stride, y, y_row_stride, rows, 1, dim, weights, groups, eps, nullptr, nullptr,
+                           0, 0, 0, stream);
 }

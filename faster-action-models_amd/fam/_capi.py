@@ -121,6 +121,7 @@ SIGNATURES = {
     "fam_adaln": (C.c_int, [_vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, C.c_float, _vp]),
     "fam_rmsnorm_rope": (C.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, C.c_float, _vp, _vp, _i64, _i64,
                                    _i64, _vp]),
+    "fam_rmsnorm_grouped": (C.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _i64, C.c_float, _vp]),
     "fam_attention": (C.c_int, [C.POINTER(AttnDesc), _vp]),
     "fam_attention_combine": (C.c_int, [C.POINTER(AttnDesc), _vp]),
     "fam_attention_oproj_partial": (C.c_int, [C.POINTER(AttnDesc), _vp, _i64, _vp, _i64, _vp]),

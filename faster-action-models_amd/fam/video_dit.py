@@ -538,11 +538,13 @@ class FusedVideoPrefill:
 
         add = self._add_step
         add("ctx_kv_all", "fam_gemm", (C.byref(d),), "gemm")
-        ld = self.ctxkv.stride(0)
-        for i, wk in enumerate(self.cnk):
-            p = self.ctxkv.data_ptr() + 2 * (i * 2 * A)
-            add(f"b{i}.cross_k_norm", "fam_rmsnorm_rope",
-                (p, ld, p, ld, rows, seq, A, wk.data_ptr(), float(eps), None, None, 0, 0, head_dim), "rmsnorm_rope")
+        # every block's context keys in one launch: rows (context row, block) with the block's
+        # k columns 2A apart, normalised with that block's norm_k weight
+        nb = len(self.cnk)
+        self.cnk_all = torch.stack(self.cnk).contiguous()
+        p = self.ctxkv.data_ptr()
+        add("cross_k_norm_all", "fam_rmsnorm_grouped",
+            (p, 2 * A, p, 2 * A, rows * nb, A, self.cnk_all.data_ptr(), nb, float(eps)), "rmsnorm_rope")
 
     @property
     def num_launches(self) -> int:

@@ -98,6 +98,20 @@ int fam_rmsnorm_rope(const void* x, int64_t x_row_stride, void* y, int64_t y_row
                      int64_t tab_row_stride, int64_t tab_elem_stride, int64_t head_dim,
                      void* stream);
 
+/*
+ * fam_rmsnorm_grouped -- RMSNorm of every row with one of `groups` weight vectors:
+ *   y[r] = bf16(x[r] * rsqrt(mean(x[r]^2) + eps)) * weights[(r % groups) * dim ..]
+ * with the rounding of fam_rmsnorm_rope.  One launch for the context keys of every block of
+ * a prefill: rows = (context rows) x (blocks), row stride = the stride between consecutive
+ * blocks' keys, group = block.
+ * Replaces: RMSNorm.forward of each block's cross_attn.norm_k (FB/wan_video_dit.py:156-167,
+ *           applied per block at FB/wan_video_dit.py:226).
+ * Limits: as fam_rmsnorm_rope; rows % groups == 0; weights [groups, dim] 16-byte aligned.
+ */
+int fam_rmsnorm_grouped(const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride,
+                        int64_t rows, int64_t dim, const void* weights, int64_t groups, float eps,
+                        void* stream);
+
 /* Attention mask kinds for fam_attn_desc.mask_kind. */
 #define FAM_MASK_NONE 0
 #define FAM_MASK_BOOL 1      /* uint8, nonzero = attend (torch bool)      */

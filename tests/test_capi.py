@@ -151,6 +151,10 @@ def test_validation_rejects_before_launch(lib):
     r.split_stride, r.src = 256, 9
     assert lib.fam_rowop(C.byref(r), None) == _capi.FAM_ERR_INVALID_ARG
 
+    # grouped RMSNorm: groups >= 1 dividing the rows, weights present
+    assert lib.fam_rmsnorm_grouped(16, 64, 32, 64, 9, 64, 48, 2, 1e-6, None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_rmsnorm_grouped(16, 64, 32, 64, 8, 64, 48, 0, 1e-6, None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_rmsnorm_grouped(16, 64, 32, 64, 8, 64, None, 2, 1e-6, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_set_launch_events(16, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_set_launch_events(None, None) == _capi.FAM_OK
     assert lib.fam_linear_smallk(16, 7, 0, 32, None, 48, 64, 4, 64, 65, None) == _capi.FAM_ERR_INVALID_ARG

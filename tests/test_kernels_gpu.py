@@ -79,6 +79,45 @@ def test_rms_norm(R, D):
     assert relerr(ops().rms_norm(dev(x), dev(w), 1e-6), ref) <= TOL
 
 
+@pytest.mark.parametrize("Lc,nb,A", [(129, 29, 3072), (7, 3, 64), (40, 5, 5000)])
+def test_rms_norm_grouped_context_keys(Lc, nb, A):
+    """Every block's context keys in one launch (rows (context row, block), block keys 2A
+    apart, block b's weight): the oracle per block, and bit-identical to one fam_rmsnorm_rope
+    per block; the v columns between the keys are untouched (A = 5000: the out-of-place
+    wide-row kernel on a copy)."""
+    from fam import _capi
+    kv = rnd(Lc, nb * 2 * A, seed=95, scale=2.0)
+    ws = rnd(nb, A, seed=96, scale=0.2) + 1
+    lib, eps = _capi.lib(), 1e-6
+    src = dev(kv)
+    got = src.clone() if A <= 4096 else torch.zeros_like(src)
+    out_p = got.data_ptr()
+    wd = dev(ws)
+    _capi.call("fam_rmsnorm_grouped", src.data_ptr() if A > 4096 else out_p, 2 * A, out_p, 2 * A, Lc * nb, A,
+               wd.data_ptr(), nb, eps, None)
+    per = src.clone()
+    for b in range(nb):
+        p = per.data_ptr() + 2 * (b * 2 * A)
+        out = p if A <= 4096 else torch.zeros(Lc, A, dtype=torch.bfloat16, device="cuda")
+        if A <= 4096:
+            _capi.call("fam_rmsnorm_rope", p, nb * 2 * A, p, nb * 2 * A, Lc, Lc, A, wd[b].data_ptr(), eps, None, None,
+                       0, 0, 0, None)
+        else:
+            _capi.call("fam_rmsnorm_rope", p, nb * 2 * A, out.data_ptr(), A, Lc, Lc, A, wd[b].data_ptr(), eps, None,
+                       None, 0, 0, 0, None)
+            per[:, b * 2 * A:b * 2 * A + A] = out
+    torch.cuda.synchronize()
+    g3 = got.reshape(Lc, nb, 2 * A)
+    for b in range(nb):
+        ref = O.rms_norm(kv.reshape(Lc, nb, 2 * A)[:, b, :A].float(), ws[b].float(), eps)
+        assert relerr(g3[:, b, :A], ref) <= TOL
+    assert torch.equal(g3[..., :A], per.reshape(Lc, nb, 2 * A)[..., :A])
+    if A <= 4096:
+        assert torch.equal(g3[..., A:].cpu(), kv.reshape(Lc, nb, 2 * A)[..., A:])
+    with pytest.raises(_capi.FamError):
+        _capi.call("fam_rmsnorm_grouped", out_p, 2 * A, out_p, 2 * A, Lc * nb + 1, A, wd.data_ptr(), nb, eps, None)
+
+
 @pytest.mark.parametrize("B,S,H,Dh", [(1, 32, 16, 64), (2, 9, 24, 128), (1, 8, 4, 8), (1, 5, 4, 24)])
 @pytest.mark.parametrize("layout", ["complex", "cat", "interleaved"])
 def test_rope(B, S, H, Dh, layout):
