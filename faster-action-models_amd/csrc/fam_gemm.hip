@@ -548,8 +548,8 @@ __global__ __launch_bounds__(NWV * 64) void partial_wide_kernel(PartArgs g) {
 }
 
 // ---------------------------------------------------------------------------------------
-// partial_stream_kernel (64 < M <= 128, long K ranges): a workgroup of 8 waves owns 128
-// output columns (16 per wave) over kper = C x 256 of K and walks it in 256-wide chunks.
+// partial_stream_kernel (64 < M <= 128, long K ranges): a workgroup of NWV (8 or 4) waves owns
+// 16 NWV output columns (16 per wave) over kper = C x 256 of K and walks it in 256-wide chunks.
 // While the MFMAs of chunk c run, the next chunk is already in flight: each wave's 16 x 256
 // weight panel in registers and the activation chunk (M rows x 256) in registers on its way
 // to the single LDS buffer, the activations issued first so that the LDS store between the
@@ -559,9 +559,9 @@ __global__ __launch_bounds__(NWV * 64) void partial_wide_kernel(PartArgs g) {
 // drained before the loop for the same reason.  Inside a chunk the activation fragments of
 // k-step s + 1 are read from LDS while the MFMAs of step s run.  Rows past M stay
 // uninitialised in LDS and only reach output rows that are never stored.
-template <int MT>
-__global__ __launch_bounds__(512) void partial_stream_kernel(PartArgs g, int kper) {
-  constexpr int NWV = 8, KS = 256, KSW = KS / 32, PITCH = KS + 16, UPR = KS / 8, NTH = NWV * 64;
+template <int MT, int NWV>
+__global__ __launch_bounds__(NWV * 64) void partial_stream_kernel(PartArgs g, int kper) {
+  constexpr int KS = 256, KSW = KS / 32, PITCH = KS + 16, UPR = KS / 8, NTH = NWV * 64;
   constexpr int UPT = (MT * 16 * UPR + NTH - 1) / NTH;
   constexpr uint32_t kOob = 0x80000000u;   // beyond every descriptor's range (checked on the host)
   __shared__ __attribute__((aligned(16))) bf16 As[MT * 16 * PITCH];
@@ -570,7 +570,7 @@ __global__ __launch_bounds__(512) void partial_stream_kernel(PartArgs g, int kpe
   const int nb0 = blockIdx.x * (16 * NWV), n0 = nb0 + wave * 16;
   const int kb = blockIdx.y * kper;
   const int ke = min(K, kb + kper);
-  // descriptors over this workgroup's <= 128 weight rows and the <= 128 activation rows:
+  // descriptors over this workgroup's <= 16 NWV weight rows and the <= 128 activation rows:
   // both ranges stay below 2^31 bytes for strides below 2^23 elements (checked on the host)
   const int nrows = min(16 * NWV, N - nb0);
   const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(g.w + (int64_t)nb0 * g.ldw, (uint32_t)(nrows * g.ldw * 2));
@@ -1244,24 +1244,28 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
 static int wide_cus();
 
 // Split plan of fam_gemm_partial.  Above 64 rows, first the streaming kernel: 128 columns per
-// workgroup, as many K splits as one round over the CUs allows, each split a whole number of
-// 256-wide chunks; it runs when every workgroup gets at least 3 chunks to pipeline (steps
-// returns -chunks).  Otherwise the wide kernel (one 512-wide K slice per workgroup, steps 0)
+// workgroup (64 when that is what gives every split 3 chunks), as many K splits as one round
+// over the CUs allows, each split a whole number of 256-wide chunks; it runs when every
+// workgroup gets at least 3 chunks to pipeline (steps returns -chunks, *nwv the waves).  Otherwise the wide kernel (one 512-wide K slice per workgroup, steps 0)
 // when it alone fills the chip.  Otherwise, and up to 64 rows always, STEPS (32-wide k-steps
 // per wave; a workgroup covers 4*32*STEPS of K) is the longest of 8, 4, 2, 1 that still gives
 // >= 256 workgroups (one per CU), so the partial planes are as few as the machine's width
 // allows; above 64 rows the eight m-tiles' activation fragments cap STEPS at 4 (registers).
-static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* splits) {
+static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* splits, int* nwv = nullptr) {
   const int64_t groups = (N + 15) / 16;
   const int64_t ksteps = (K + 31) / 32;
   if (M > 64) {
-    const int64_t nblk = (N + 127) / 128, chunks = (K + 255) / 256;
-    const int64_t smax = std::max((int64_t)1, (int64_t)wide_cus() / nblk);
-    const int64_t c = (chunks + std::min(chunks, smax) - 1) / std::min(chunks, smax);
-    if (c >= 3) {
-      *steps = -(int)c;
-      *splits = (int)((chunks + c - 1) / c);
-      return;
+    const int64_t chunks = (K + 255) / 256;
+    for (int w : {8, 4}) {
+      const int64_t nblk = (N + 16 * w - 1) / (16 * w);
+      const int64_t smax = std::max((int64_t)1, (int64_t)wide_cus() / nblk);
+      const int64_t c = (chunks + std::min(chunks, smax) - 1) / std::min(chunks, smax);
+      if (c >= 3) {
+        *steps = -(int)c;
+        *splits = (int)((chunks + c - 1) / c);
+        if (nwv) *nwv = w;
+        return;
+      }
     }
   }
   if (M > 64 && ((N + 127) / 128) * ((K + 511) / 512) >= 128) {
@@ -1337,14 +1341,20 @@ extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64
   FAM_REQUIRE(M <= 64 || (lda < (1LL << 23) && ldw < (1LL << 23) && N < (1LL << 31)), FAM_ERR_UNSUPPORTED,
               "fam_gemm_partial: above 64 rows lda and ldw must be < 2^23 elements");
   if (M == 0) return FAM_OK;
-  int steps, splits;
-  partial_plan(M, N, K, &steps, &splits);
+  int steps, splits, nwv = 8;
+  partial_plan(M, N, K, &steps, &splits, &nwv);
   PartArgs pa{(const bf16*)a, lda, (const bf16*)w, ldw, partials, M, N, K};
   hipStream_t s = (hipStream_t)stream;
   if (steps < 0) {
-    const dim3 grid((unsigned)((N + 127) / 128), (unsigned)splits);
-    if (M <= 112) FAM_LAUNCH((partial_stream_kernel<7>), grid, dim3(512), 0, s, pa, -steps * 256);
-    else FAM_LAUNCH((partial_stream_kernel<8>), grid, dim3(512), 0, s, pa, -steps * 256);
+    const dim3 grid((unsigned)((N + 16 * nwv - 1) / (16 * nwv)), (unsigned)splits);
+    const int kper = -steps * 256;
+    if (nwv == 8) {
+      if (M <= 112) FAM_LAUNCH((partial_stream_kernel<7, 8>), grid, dim3(512), 0, s, pa, kper);
+      else FAM_LAUNCH((partial_stream_kernel<8, 8>), grid, dim3(512), 0, s, pa, kper);
+    } else {
+      if (M <= 112) FAM_LAUNCH((partial_stream_kernel<7, 4>), grid, dim3(256), 0, s, pa, kper);
+      else FAM_LAUNCH((partial_stream_kernel<8, 4>), grid, dim3(256), 0, s, pa, kper);
+    }
   } else if (steps == 0) launch_partial_wide(pa, splits, s);
   else if (M <= 16) launch_partial<1>(pa, steps, splits, s);
   else if (M <= 32) launch_partial<2>(pa, steps, splits, s);

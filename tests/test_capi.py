@@ -120,10 +120,11 @@ def test_validation_rejects_before_launch(lib):
                                                               (1024, 4096), (7, 1024))] == [2, 4, 1, 4, 8]
     assert lib.fam_gemm_partial_splits(0, 64, 64) == 0
     # the video prefill's 98-row projections: the streaming kernel (one round of 128-column
-    # workgroups, whole 256-wide chunks per split) for FFN down / FFN up / q|k|v, the one-slice
-    # wide kernel for the 3072 x 3072 ones
+    # workgroups, whole 256-wide chunks per split) for FFN down / FFN up / q|k|v, 64-column
+    # workgroups with 3 chunks per split for the 3072 x 3072 ones; the register kernel where
+    # neither gives 3 chunks and the wide one would not fill the chip (98 x 4096 x 1024)
     assert [lib.fam_gemm_partial_splits(98, n, k) for n, k in ((3072, 14336), (14336, 3072), (9216, 3072),
-                                                              (3072, 3072))] == [10, 2, 3, 6]
+                                                              (3072, 3072), (4096, 1024))] == [10, 2, 3, 4, 2]
     # above 64 rows the strides must stay below 2^23 elements (32-bit buffer offsets)
     assert lib.fam_gemm_partial(16, 3072, 32, 1 << 23, 48, 98, 64, 64, None) == _capi.FAM_ERR_UNSUPPORTED
 

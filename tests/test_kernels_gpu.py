@@ -460,13 +460,16 @@ def test_sinusoid_and_modulation():
 @pytest.mark.parametrize("M,N,K", [(32, 3072, 1024), (32, 1024, 4096), (32, 7, 1024), (1, 64, 8), (7, 1000, 256),
                                     (64, 4096, 1024), (17, 2048, 1000), (33, 96, 64), (98, 3072, 3072),
                                     (98, 3072, 14336), (128, 4090, 3000), (65, 1000, 1024), (100, 4096, 520),
-                                    (98, 14336, 3072), (128, 9216, 3072), (77, 6004, 4104), (77, 4094, 4104)])
+                                    (98, 14336, 3072), (128, 9216, 3072), (77, 6004, 4104), (77, 4094, 4104),
+                                    (98, 3000, 3072), (128, 3072, 3080)])
 def test_gemm_partial_rowop(M, N, K):
     """Split-K partials summed in split order by the row kernel = linear; bit-identical reruns.
     Above 64 rows: the streaming kernel where a one-round grid gives every workgroup >= 3
     chunks of 256 along K ((98, 3072, 14336): 10 planes; FFN up (98, 14336, 3072) with a
     14336-wide row finished over several row-kernel workgroups; 8 m-tiles at 128 rows; a
-    ragged last column block and a K tail at (77, 6004 / 4094, 4104)), the wide kernel (a
+    ragged last column block and a K tail at (77, 6004 / 4094, 4104); 64-column workgroups for
+    the 3072 x 3072 projections, with a ragged block at N=3000 and a K tail at 128 rows), the
+    wide kernel (a
     512-wide K slice per workgroup, activations staged in LDS) and the 8-m-tile register
     kernel where neither fills the chip."""
     x, w, b = rnd(M, K, seed=70), rnd(N, K, seed=71, scale=0.02), rnd(N, seed=72, scale=0.02)
