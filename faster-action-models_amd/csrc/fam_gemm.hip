@@ -1257,6 +1257,7 @@ static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* split
   if (M > 64) {
     const int64_t chunks = (K + 255) / 256;
     for (int w : {8, 4}) {
+      if (w == 4 && M > 128) break;   // 9 m-tiles only with 8 waves
       const int64_t nblk = (N + 16 * w - 1) / (16 * w);
       const int64_t smax = std::max((int64_t)1, (int64_t)wide_cus() / nblk);
       const int64_t c = (chunks + std::min(chunks, smax) - 1) / std::min(chunks, smax);
@@ -1279,11 +1280,12 @@ static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* split
   *splits = (int)((ksteps + 4 * st - 1) / (4 * st));
 }
 
+// Above 128 rows (<= 144) only the streaming plan runs; 0 when it does not apply.
 extern "C" int fam_gemm_partial_splits(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (M <= 0 || N <= 0 || K <= 0 || M > 144) return 0;
   int st, sp;
   partial_plan(M, N, K, &st, &sp);
-  return sp;
+  return M > 128 && st >= 0 ? 0 : sp;
 }
 
 template <int MT>
@@ -1330,8 +1332,8 @@ static void launch_partial_wide(const PartArgs& a, int splits, hipStream_t s) {
 extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64_t ldw, float* partials,
                                 int64_t M, int64_t N, int64_t K, void* stream) {
   FAM_REQUIRE(a && w && partials, FAM_ERR_INVALID_ARG, "fam_gemm_partial: null pointer");
-  FAM_REQUIRE(M >= 0 && M <= 128 && N >= 1 && K >= 8 && K % 8 == 0, FAM_ERR_INVALID_ARG,
-              "fam_gemm_partial: need 0 <= M <= 128, N >= 1, K a positive multiple of 8 (M=%lld N=%lld K=%lld)",
+  FAM_REQUIRE(M >= 0 && M <= 144 && N >= 1 && K >= 8 && K % 8 == 0, FAM_ERR_INVALID_ARG,
+              "fam_gemm_partial: need 0 <= M <= 144, N >= 1, K a positive multiple of 8 (M=%lld N=%lld K=%lld)",
               (long long)M, (long long)N, (long long)K);
   FAM_REQUIRE(lda >= K && ldw >= K && lda % 8 == 0 && ldw % 8 == 0, FAM_ERR_INVALID_ARG,
               "fam_gemm_partial: lda/ldw must be >= K and multiples of 8");
@@ -1343,6 +1345,9 @@ extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64
   if (M == 0) return FAM_OK;
   int steps, splits, nwv = 8;
   partial_plan(M, N, K, &steps, &splits, &nwv);
+  FAM_REQUIRE(M <= 128 || steps < 0, FAM_ERR_UNSUPPORTED,
+              "fam_gemm_partial: above 128 rows only the streaming plan runs (>= 3 chunks of 256 per split with "
+              "128-column workgroups; fam_gemm_partial_splits returns 0 otherwise)");
   PartArgs pa{(const bf16*)a, lda, (const bf16*)w, ldw, partials, M, N, K};
   hipStream_t s = (hipStream_t)stream;
   if (steps < 0) {
@@ -1350,7 +1355,8 @@ extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64
     const int kper = -steps * 256;
     if (nwv == 8) {
       if (M <= 112) FAM_LAUNCH((partial_stream_kernel<7, 8>), grid, dim3(512), 0, s, pa, kper);
-      else FAM_LAUNCH((partial_stream_kernel<8, 8>), grid, dim3(512), 0, s, pa, kper);
+      else if (M <= 128) FAM_LAUNCH((partial_stream_kernel<8, 8>), grid, dim3(512), 0, s, pa, kper);
+      else FAM_LAUNCH((partial_stream_kernel<9, 8>), grid, dim3(512), 0, s, pa, kper);
     } else {
       if (M <= 112) FAM_LAUNCH((partial_stream_kernel<7, 4>), grid, dim3(256), 0, s, pa, kper);
       else FAM_LAUNCH((partial_stream_kernel<8, 4>), grid, dim3(256), 0, s, pa, kper);

@@ -537,7 +537,23 @@ class FusedVideoPrefill:
         self._descs.append(d)
 
         add = self._add_step
-        add("ctx_kv_all", "fam_gemm", (C.byref(d),), "gemm")
+        N, K = self.ckv_w.shape[0], ctx.shape[1]
+        sp = lib.fam_gemm_partial_splits(rows, N, K) if 64 < rows <= 144 else 0
+        if sp > 0:
+            # up to 144 context rows: the streaming split-K kernel reads the 1 GB of stacked
+            # weights once; the large-M GEMM's 256-row tiles would double the products of 129 rows
+            self.ctx_part = torch.empty(sp * rows * N, dtype=torch.float32, device=ctx.device)
+            add("ctx_kv_all", "fam_gemm_partial", (ctx.data_ptr(), ctx.stride(0), self.ckv_w.data_ptr(),
+                                                    self.ckv_w.stride(0), self.ctx_part.data_ptr(), rows, N, K),
+                "gemm_partial")
+            r = _capi.RowopDesc()
+            r.src, r.partials, r.splits, r.split_stride = _capi.FAM_ROWSRC_PARTIALS, self.ctx_part.data_ptr(), sp, rows * N
+            r.M, r.N, r.bias, r.rows_per_batch = rows, N, self.ckv_b.data_ptr(), rows
+            r.out, r.ldo = self.ctxkv.data_ptr(), self.ctxkv.stride(0)
+            self._descs.append(r)
+            add("ctx_kv_all_row", "fam_rowop", (C.byref(r),), "rowop")
+        else:
+            add("ctx_kv_all", "fam_gemm", (C.byref(d),), "gemm")
         # every block's context keys in one launch: rows (context row, block) with the block's
         # k columns 2A apart, normalised with that block's norm_k weight
         nb = len(self.cnk)

@@ -261,7 +261,7 @@ typedef struct fam_gemm_desc {
 int fam_gemm(const fam_gemm_desc* d, void* stream);
 
 /*
- * fam_gemm_partial -- split-K product for 1 <= M <= 128 rows without any cross-workgroup
+ * fam_gemm_partial -- split-K product for 1 <= M <= 144 rows without any cross-workgroup
  * traffic: partials[z][m][n] = sum over k in split z of a[m, k] * w[n, k], fp32,
  * z < fam_gemm_partial_splits(M, N, K) (a deterministic function of the shape).  The caller
  * allocates splits*M*N floats and sums them with fam_rowop, which also applies the
@@ -269,8 +269,10 @@ int fam_gemm(const fam_gemm_desc* d, void* stream);
  * Replaces: the projections of the action tokens (q/k/v/o, cross q/o, FFN up/down, head;
  *           FB/wan_video_dit.py:188-191,215-218,262-263, FB/action_dit.py:317-318) and the
  *           reference's split-K kernel fastwam::skmm (FG/mot.py:1080-1243).
- * Limits: M <= 128; K % 8 == 0; lda, ldw multiples of 8; 16-byte aligned a, w, partials;
- * above 64 rows lda, ldw < 2^23 elements.
+ * Limits: M <= 128, or up to 144 where fam_gemm_partial_splits is non-zero (the streaming
+ * plan: >= 3 chunks of 256 along K per split, e.g. a prefill's 129-row context K/V of every
+ * block); K % 8 == 0; lda, ldw multiples of 8; 16-byte aligned a, w, partials; above 64 rows
+ * lda, ldw < 2^23 elements.
  */
 int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64_t ldw, float* partials,
                      int64_t M, int64_t N, int64_t K, void* stream);

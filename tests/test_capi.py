@@ -112,7 +112,11 @@ def test_validation_rejects_before_launch(lib):
     assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_INVALID_ARG
 
     # split-K partials: M above 128, unaligned K, misaligned partial buffer
-    assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 129, 64, 64, None) == _capi.FAM_ERR_INVALID_ARG
+    assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 145, 64, 64, None) == _capi.FAM_ERR_INVALID_ARG
+    # 129..144 rows only on the streaming plan: not for a short K
+    assert lib.fam_gemm_partial_splits(129, 64, 64) == 0
+    assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 129, 64, 64, None) == _capi.FAM_ERR_UNSUPPORTED
+    assert lib.fam_gemm_partial_splits(129, 178176, 3072) == 1
     assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 4, 64, 60, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_gemm_partial(16, 64, 32, 64, 52, 4, 64, 64, None) == _capi.FAM_ERR_INVALID_ARG
     # the split plan of the action projections: >= 256 workgroups of 16 columns, fewest planes

@@ -461,14 +461,15 @@ def test_sinusoid_and_modulation():
                                     (64, 4096, 1024), (17, 2048, 1000), (33, 96, 64), (98, 3072, 3072),
                                     (98, 3072, 14336), (128, 4090, 3000), (65, 1000, 1024), (100, 4096, 520),
                                     (98, 14336, 3072), (128, 9216, 3072), (77, 6004, 4104), (77, 4094, 4104),
-                                    (98, 3000, 3072), (128, 3072, 3080)])
+                                    (98, 3000, 3072), (128, 3072, 3080), (129, 12288, 3072), (140, 20000, 1600)])
 def test_gemm_partial_rowop(M, N, K):
     """Split-K partials summed in split order by the row kernel = linear; bit-identical reruns.
     Above 64 rows: the streaming kernel where a one-round grid gives every workgroup >= 3
     chunks of 256 along K ((98, 3072, 14336): 10 planes; FFN up (98, 14336, 3072) with a
     14336-wide row finished over several row-kernel workgroups; 8 m-tiles at 128 rows; a
     ragged last column block and a K tail at (77, 6004 / 4094, 4104); 64-column workgroups for
-    the 3072 x 3072 projections, with a ragged block at N=3000 and a K tail at 128 rows), the
+    the 3072 x 3072 projections, with a ragged block at N=3000 and a K tail at 128 rows; 9
+    m-tiles for 129-144 rows, ragged and with a K tail at (140, 20000, 1600)), the
     wide kernel (a
     512-wide K slice per workgroup, activations staged in LDS) and the 8-m-tile register
     kernel where neither fills the chip."""

@@ -62,6 +62,37 @@ def test_video_prefill_kv_matches_oracle(frames, tpf, Lc, num_run, ragged, nh):
     assert all(torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) for a, b in zip(first, kv2))
 
 
+def test_video_prefill_context_kv_split_k():
+    """129 context rows: the stacked context K/V of the 11 cross-attending blocks
+    (129 x 16896 x 768) on the streaming split-K kernel with 9 m-tiles + a bias row launch,
+    instead of the large-M GEMM; every layer's K/V against the oracle."""
+    from fam import _capi
+    from fam.video_dit import FusedVideoPrefill
+    Sv, H, nh, Dh, F, L, Lc = 98, 768, 6, 128, 1536, 12, 129
+    assert _capi.lib().fam_gemm_partial_splits(Lc, (L - 1) * 2 * nh * Dh, H) == 1
+    ocfg = O.ActionDiTConfig(hidden_dim=H, action_dim=7, ffn_dim=F, text_dim=H, freq_dim=256, num_heads=nh,
+                             attn_head_dim=Dh, num_layers=L)
+    p = {k: v.to(torch.bfloat16) for k, v in O.init_action_dit_params(ocfg, 71).items()}
+    g = torch.Generator().manual_seed(72)
+    x = torch.randn(1, Sv, H, generator=g).to(torch.bfloat16)
+    tm = (torch.randn(1, Sv, 6, H, generator=g) * 0.2).to(torch.bfloat16)
+    ctx = torch.randn(1, Lc, H, generator=g).to(torch.bfloat16)
+    freqs = O.action_freqs(Dh, Sv)
+    pf = FusedVideoPrefill(p, num_layers=L, hidden=H, num_heads=nh, head_dim=Dh, ffn_dim=F, batch=1, video_len=Sv,
+                           ctx_len=Lc, freqs=freqs)
+    assert [m["name"] for m in pf.meta[:2]] == ["ctx_kv_all", "ctx_kv_all_row"]
+    kv = pf.prefill(x.cuda(), tm.cuda(), ctx.cuda())
+    p32 = {k: v.float() for k, v in p.items()}
+    ref = O.mot_prefill_video_cache(p32, ocfg, x.float(), freqs, tm.float(), ctx.float(),
+                                    torch.ones(Sv, Sv, dtype=torch.bool))
+    worst = 0.0
+    for i, ((k, v), (rk, rv)) in enumerate(zip(kv, ref)):
+        ek, ev = _relerr(k.cpu(), rk), _relerr(v.cpu(), rv)
+        worst = max(worst, ek, ev)
+        assert ek <= 2e-2 and ev <= 2e-2, (i, ek, ev)
+    print(f"prefill, 129 context rows on split-K: {pf.num_launches} launches, worst relerr {worst:.3e}")
+
+
 def test_video_prefill_broadcast_modulation():
     """Per-batch t_mod ([B, 6, H], per_token_mod=False): the chained blocks read their
     modulation from one [B, blocks, 6H] buffer with a zero row stride; against the oracle fed
