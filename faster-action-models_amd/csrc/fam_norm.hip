@@ -22,8 +22,8 @@ struct AdalnArgs {
 };
 
 // AFF: the LayerNorm affine is present.  MOD: no AdaLN shift-scale (0), one per row (1, an
-// HBM stream: loaded with x), or one per batch (2, an L2-resident row: loaded after the
-// statistics, so its registers do not cost occupancy while x is in flight).  Compile-time,
+// HBM stream: loaded with x), or one per batch (2, an L2-resident row: loaded in one batch
+// after the statistics, so its registers do not cost occupancy while x is in flight).  Compile-time,
 // because occupancy is what keeps HBM busy here.
 template <int NV, bool AFF, int MOD>
 __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
     // Every load of the row (x, LayerNorm affine, per-row shift / scale) is issued before the
     // statistics, so a wave waits for memory once; x stays bf16 in registers and is widened in
     // each pass.
-    constexpr int NA = AFF ? NV : 1, NMD = MOD == 1 ? NV : 1;
+    constexpr int NA = AFF ? NV : 1, NMD = MOD != 0 ? NV : 1;
     bf16x8 xv8[1][NV], wv[NA], bv[NA], sh[NMD], sc[NMD];
     constexpr int RPW = 1;
     auto col = [&](int i) { const int64_t c = ((int64_t)i * 64 + lane) * 8; return c < D ? c : 0; };
@@ -111,6 +111,14 @@ __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
         }
       }
       const float rstd = rsqrtf(wave_sum(q) * invD + a.eps);
+      if constexpr (MOD == 2) {
+        // the batch's shift / scale row (L2-resident), all of it in one round trip
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+          sh[i] = load8(a.shift + moff + col(i));
+          sc[i] = load8(a.scale + moff + col(i));
+        }
+      }
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
         const int64_t c = ((int64_t)i * 64 + lane) * 8;
@@ -118,12 +126,8 @@ __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
           float v[8];
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[e] = to_f(xv8[k][i][e]);
-          if constexpr (MOD == 2) {
-            sh[0] = load8(a.shift + moff + c);
-            sc[0] = load8(a.scale + moff + c);
-          }
-          store8(yr + c, finish(v, mean, rstd, wv[AFF ? i : 0], bv[AFF ? i : 0], sh[MOD == 1 ? i : 0],
-                                sc[MOD == 1 ? i : 0]));
+          store8(yr + c, finish(v, mean, rstd, wv[AFF ? i : 0], bv[AFF ? i : 0], sh[MOD != 0 ? i : 0],
+                                sc[MOD != 0 ? i : 0]));
         }
       }
     }
