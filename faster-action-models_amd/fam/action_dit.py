@@ -100,17 +100,18 @@ def param_shapes(cfg: ActionDiTConfig) -> Dict[str, tuple]:
 def synthetic_params(cfg: ActionDiTConfig, seed: int, std: float = 0.02) -> Dict[str, torch.Tensor]:
     """Seeded random weights for benchmarking (no checkpoints are available offline):
     N(0, std) weights and biases, modulation randn/sqrt(H) as the reference initialises it
-    (FB/wan_video_dit.py:264), RMSNorm/LayerNorm weights 1 and LayerNorm biases 0; drawn in
-    sorted-name order from one CPU generator, fp32."""
+    (FB/wan_video_dit.py:264), RMSNorm/LayerNorm weights N(1, 0.2) and LayerNorm biases
+    N(0, 0.2) (a trained checkpoint's affines are not the identity); drawn in sorted-name
+    order from one CPU generator, fp32."""
     g = torch.Generator("cpu").manual_seed(seed)
     out = {}
     for name, shape in sorted(param_shapes(cfg).items()):
         if name.endswith("modulation"):
             out[name] = torch.randn(shape, generator=g) / math.sqrt(cfg.hidden_dim)
         elif ".norm_q." in name or ".norm_k." in name or name.endswith("norm3.weight"):
-            out[name] = torch.ones(shape)
+            out[name] = 1.0 + torch.randn(shape, generator=g) * 0.2
         elif name.endswith("norm3.bias"):
-            out[name] = torch.zeros(shape)
+            out[name] = torch.randn(shape, generator=g) * 0.2
         else:
             out[name] = torch.randn(shape, generator=g) * std
     return out
@@ -181,22 +182,16 @@ class FusedActionDiT:
             are given per call through `set_video_kv`.
         video_mask: optional bool [S, Sv + S], the action rows of the joint mask
             (FB/fastwam.py:388-410; True = attend); None = every key.
-        fuse_attn_o: run the action tokens' self-attention inside the o projection's split-K
-            kernel (fam_attention_oproj_partial) where its envelope allows (B <= 2, the
-            single-kernel q/k path).  Off by default: on gfx950 the fused kernel (11.1 us at
-            config 1) is slower than the attention + split-K pair it replaces (4.7 + 3.9 us),
-            because each workgroup re-derives four heads' normalised q/k/v before its product.
     """
 
     def __init__(self, cfg: ActionDiTConfig, params: Dict[str, torch.Tensor], *, batch: int, seq_len: int,
                  ctx_len: int, num_steps: int, shift: float = 5.0, device="cuda", mode: str = "denoise",
-                 video_len: int = 0, video_mask: Optional[torch.Tensor] = None, fuse_attn_o: bool = False):
+                 video_len: int = 0, video_mask: Optional[torch.Tensor] = None):
         if mode not in ("denoise", "forward"):
             raise ValueError(f"mode must be 'denoise' or 'forward', got {mode!r}")
         if mode == "forward" and num_steps != 1:
             raise ValueError("forward mode runs one ActionDiT.forward: num_steps must be 1")
         self.mode = mode
-        self.fuse_attn_o = fuse_attn_o
         self.cfg = cfg
         self.B, self.S, self.Lc, self.T = batch, seq_len, ctx_len, num_steps
         self.shift = shift
@@ -290,8 +285,6 @@ class FusedActionDiT:
         part_need = 0
         for (n_, k_) in ((3 * A, H), (H, A), (A, H), (Fd, H), (H, Fd), (cfg.action_dim, H)):
             part_need = max(part_need, self._part_splits(M, n_, k_) * M * n_)
-        if batch <= 2 and cfg.attn_head_dim in (64, 128):   # fused attention + o projection planes
-            part_need = max(part_need, cfg.num_heads * M * H)
         self.part = torch.zeros(part_need, dtype=torch.float32, device=dev)
         # key-split partials of the cross-attention: ~4 blocks of 32 keys per workgroup
         self.kv_splits = max(1, min(64, -(-ctx_len // 128)))
@@ -466,22 +459,6 @@ class FusedActionDiT:
             self._launch(name + "_combine", "fam_attention_combine", C.byref(d), "attn_combine",
                          splits * nq * (4 * Dh + 8) + 2 * nq * Dh)
 
-    def _attn_oproj(self, name, qkvp, S, qk_norm, w):
-        """Self-attention of the action rows fused into the split-K o projection (partials into
-        self.part, summed by the next row kernel); returns the partial plane count."""
-        cfg = self.cfg
-        A, Dh = cfg.attn_dim, cfg.attn_head_dim
-        d = self._attn_desc(qkvp, S * 3 * A, 3 * A, qkvp + 2 * A, S * 3 * A, 3 * A, qkvp + 4 * A, S * 3 * A, 3 * A,
-                            self.attn, S, S, qk_norm=qk_norm)
-        N = w.shape[0]
-        splits = self.lib.fam_attention_oproj_splits(C.byref(d), N)
-        M = self.B * S
-        nbytes = 2 * 3 * M * A + 2 * N * A + 4 * splits * M * N
-        flops = 4 * self.B * cfg.num_heads * S * S * Dh + 2 * M * N * A
-        self.plan.add(name, _checked(self.lib, "fam_attention_oproj_partial", C.byref(d), w.data_ptr(), w.stride(0),
-                                     self.part.data_ptr(), N), "attn_oproj", nbytes, flops)
-        return splits
-
     def _attn_joint(self, name, l, out):
         """MoT self-attention of the action rows over [video K/V cache of layer l ; action K/V]
         with the action rows of the joint mask (FB/mot.py:446-478): two key segments read in
@@ -555,8 +532,6 @@ class FusedActionDiT:
         # M <= 64 rows, Sq <= 32 and an RMS width the on-load normaliser supports: q/k projections
         # are single kernels and their norms run inside the attention kernels
         fused_qk = M <= 64 and S <= 32 and A % 1024 == 0 and Dh in (64, 128) and self.Sv == 0
-        # ... and the self-attention runs inside the o projection's split-K kernel
-        fused_ao = fused_qk and self.fuse_attn_o and self.B <= 2 and cfg.num_heads % ((256 // self.B) // Dh) == 0
 
         def mod(t, l, i):   # chunk i of (modulation + t_mod) of block l at step t: [H]
             return self.mods[t, l, i * H:(i + 1) * H]
@@ -573,9 +548,8 @@ class FusedActionDiT:
                     self._gemm_final(tag + ".qkv", h, w[f"qkv_w{l}"], w[f"qkv_b{l}"], qkv, sumsq=self.ss_qkv)
                     qkn = dict(ss=self.ss_qkv, q_w=w[f"sa_norm_q_w{l}"], k_w=w[f"sa_norm_k_w{l}"], k_group0=A // 16,
                                rope=True)
-                    if not fused_ao:
-                        self._attn(tag + ".self_attn", qkvp, S * 3 * A, 3 * A, qkvp + 2 * A, S * 3 * A, 3 * A,
-                                   qkvp + 4 * A, S * 3 * A, 3 * A, attn, S, S, qk_norm=qkn)
+                    self._attn(tag + ".self_attn", qkvp, S * 3 * A, 3 * A, qkvp + 2 * A, S * 3 * A, 3 * A,
+                               qkvp + 4 * A, S * 3 * A, 3 * A, attn, S, S, qk_norm=qkn)
                 else:
                     # q, k, v projection; RMSNorm + RoPE of q and k in the row kernel
                     sp = self._gemm_partial(tag + ".qkv", h, w[f"qkv_w{l}"])
@@ -587,10 +561,7 @@ class FusedActionDiT:
                         self._attn(tag + ".self_attn", qkvp, S * 3 * A, 3 * A, qkvp + 2 * A, S * 3 * A, 3 * A,
                                    qkvp + 4 * A, S * 3 * A, 3 * A, attn, S, S)
                 # o projection; x += gate_msa * o; LayerNorm3 (affine) for the cross-attention query
-                if fused_qk and fused_ao:
-                    sp = self._attn_oproj(tag + ".self_attn_o", qkvp, S, qkn, w[f"sa_o_w{l}"])
-                else:
-                    sp = self._gemm_partial(tag + ".o", attn, w[f"sa_o_w{l}"])
+                sp = self._gemm_partial(tag + ".o", attn, w[f"sa_o_w{l}"])
                 self._rowop(tag + ".o_row", N=H, splits=sp, bias=w[f"sa_o_b{l}"], res=x, gate=mod(t, l, 2), out=x,
                             norm=LN, ln_w=w[f"n3_w{l}"], ln_b=w[f"n3_b{l}"], nout=h)
                 kb = kvp + 2 * (l * 2 * A)

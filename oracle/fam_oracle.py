@@ -300,19 +300,24 @@ def action_dit_param_shapes(cfg: ActionDiTConfig) -> Dict[str, Tuple[int, ...]]:
     return shapes
 
 
+NORM_AFFINE_STD = 0.2
+
+
 def init_action_dit_params(cfg: ActionDiTConfig, seed: int, std: float = 0.02) -> Params:
     """Seeded synthetic weights: N(0,std) weights and biases, modulation randn/sqrt(H)
-    (FB/wan_video_dit.py:264), norm weights 1 and norm biases 0.  Drawn in sorted-name order
-    from one CPU generator, fp32."""
+    (FB/wan_video_dit.py:264).  The norm affines are drawn away from the identity the reference
+    initialises them to (a trained checkpoint carries its own): RMSNorm / LayerNorm weights
+    N(1, 0.2), LayerNorm biases N(0, 0.2), so that a swapped, dropped or mis-indexed norm
+    weight changes every output.  Drawn in sorted-name order from one CPU generator, fp32."""
     g = torch.Generator("cpu").manual_seed(seed)
     out: Params = {}
     for name, shape in sorted(action_dit_param_shapes(cfg).items()):
         if name.endswith("modulation"):
             out[name] = torch.randn(shape, generator=g) / math.sqrt(cfg.hidden_dim)
         elif ".norm_q." in name or ".norm_k." in name or name.endswith("norm3.weight"):
-            out[name] = torch.ones(shape)
+            out[name] = 1.0 + torch.randn(shape, generator=g) * NORM_AFFINE_STD
         elif name.endswith("norm3.bias"):
-            out[name] = torch.zeros(shape)
+            out[name] = torch.randn(shape, generator=g) * NORM_AFFINE_STD
         else:
             out[name] = torch.randn(shape, generator=g) * std
     return out

@@ -187,7 +187,7 @@ def golden():
 
 @pytest.fixture(scope="module")
 def tiny_params(golden):
-    p = O.init_action_dit_params(TINY, int(golden["meta.seed"][0]))
+    p = O.init_action_dit_params(TINY, int(golden["meta.seed"][0]), std=float(golden["meta.std"][0]))
     acc = torch.zeros((), dtype=torch.float64)
     for i, k in enumerate(sorted(p)):
         acc = acc + (i + 1) * p[k].double().sum()
@@ -296,6 +296,54 @@ def test_golden_detects_planted_mistake(golden, tiny_params):
     y = O.dit_block(p, 0, golden["block.in.x"], golden["block.in.context"], golden["block.in.t_mod"],
                     O.action_freqs(TINY.attn_head_dim, S), TINY.num_heads, TINY.eps, cm)
     assert not torch.allclose(y, golden["block.out.fp32"], rtol=2e-5, atol=2e-5)
+
+
+def _swap_norm_qk(p, att):
+    q = p
+    for k in list(q):
+        if f".{att}.norm_q." in k:
+            kk = k.replace(".norm_q.", ".norm_k.")
+            q[k], q[kk] = q[kk], q[k]
+    return q
+
+
+@pytest.mark.parametrize("slip", ["swap_self_qk", "drop_cross_norm_q", "drop_norm3_bias", "norm3_weight_of_next_layer"])
+def test_golden_detects_planted_norm_affine_mistakes(golden, tiny_params, slip):
+    """With non-identity norm affines in the golden run, a swapped self-attention q/k RMSNorm
+    weight, a dropped cross-attention query norm weight, a dropped norm3 bias or a norm weight
+    taken from the wrong layer must each fail the reference goldens.  (Swapping the
+    cross-attention q/k norm weights is an exact symmetry: without RoPE the score is
+    sum_d q_d w_q[d] k_d w_k[d], so no output can detect it.)"""
+    p = O.cast_params(tiny_params, torch.float32)
+    if slip == "swap_self_qk":
+        _swap_norm_qk(p, "self_attn")
+    elif slip == "drop_cross_norm_q":
+        for k in list(p):
+            if ".cross_attn.norm_q." in k:
+                p[k] = torch.ones_like(p[k])
+    elif slip == "drop_norm3_bias":
+        for k in list(p):
+            if k.endswith("norm3.bias"):
+                p[k] = torch.zeros_like(p[k])
+    else:
+        p["blocks.0.norm3.weight"] = p["blocks.1.norm3.weight"].clone()
+    S = golden["block.in.x"].shape[1]
+    cm = golden["in.context_mask"].bool().unsqueeze(1).expand(-1, S, -1)
+    y = O.dit_block(p, 0, golden["block.in.x"], golden["block.in.context"], golden["block.in.t_mod"],
+                    O.action_freqs(TINY.attn_head_dim, S), TINY.num_heads, TINY.eps, cm)
+    assert not torch.allclose(y, golden["block.out.fp32"], rtol=2e-5, atol=2e-5)
+    y = O.action_dit_forward(p, TINY, golden["in.actions"], golden["in.timestep"], golden["in.context"],
+                             golden["in.context_mask"].bool())
+    assert not torch.allclose(y, golden["action_dit.out.fp32"], rtol=2e-5, atol=2e-5)
+
+
+def test_golden_norm_affines_are_not_identity(tiny_params):
+    """The golden weights carry non-trivial norm affines (otherwise the tests above pin nothing)."""
+    for k, v in tiny_params.items():
+        if ".norm_q." in k or ".norm_k." in k or k.endswith("norm3.weight"):
+            assert (v - 1).abs().max() > 0.1, k
+        if k.endswith("norm3.bias"):
+            assert v.abs().max() > 0.1, k
 
 
 # --------------------------------------------------------------------------- CAE action decoder
