@@ -570,8 +570,9 @@ __global__ __launch_bounds__(NWV * 64) void partial_stream_kernel(PartArgs g, in
   const int nb0 = blockIdx.x * (16 * NWV), n0 = nb0 + wave * 16;
   const int kb = blockIdx.y * kper;
   const int ke = min(K, kb + kper);
-  // descriptors over this workgroup's <= 16 NWV weight rows and the <= 128 activation rows:
-  // both ranges stay below 2^31 bytes for strides below 2^23 elements (checked on the host)
+  // descriptors over this workgroup's <= 16 NWV weight rows and the <= 144 activation rows:
+  // the host requires M * lda * 2 < 2^31 and 128 * ldw * 2 < 2^31, so both ranges stay below
+  // kOob and every out-of-range offset reads zero
   const int nrows = min(16 * NWV, N - nb0);
   const __amdgpu_buffer_rsrc_t wrs = buffer_rsrc(g.w + (int64_t)nb0 * g.ldw, (uint32_t)(nrows * g.ldw * 2));
   const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(g.a, (uint32_t)(g.M * g.lda * 2));
@@ -1340,8 +1341,12 @@ extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64
   FAM_REQUIRE(fam_host::aligned16(a) && fam_host::aligned16(w) && fam_host::aligned16(partials), FAM_ERR_INVALID_ARG,
               "fam_gemm_partial: a, w and partials must be 16-byte aligned");
   FAM_REQUIRE((N + 15) / 16 <= 2147483647LL, FAM_ERR_UNSUPPORTED, "fam_gemm_partial: N too large");
-  FAM_REQUIRE(M <= 64 || (lda < (1LL << 23) && ldw < (1LL << 23) && N < (1LL << 31)), FAM_ERR_UNSUPPORTED,
-              "fam_gemm_partial: above 64 rows lda and ldw must be < 2^23 elements");
+  // above 64 rows the streaming kernel addresses the activations and a workgroup's <= 128 weight
+  // rows through 32-bit buffer descriptors whose out-of-range offset is 2^31: both spans must
+  // stay below it
+  FAM_REQUIRE(M <= 64 || (M * lda * 2 < (1LL << 31) && ldw < (1LL << 23) && N < (1LL << 31)), FAM_ERR_UNSUPPORTED,
+              "fam_gemm_partial: above 64 rows M * lda * 2 must be < 2^31 bytes and ldw < 2^23 elements "
+              "(M=%lld lda=%lld ldw=%lld)", (long long)M, (long long)lda, (long long)ldw);
   if (M == 0) return FAM_OK;
   int steps, splits, nwv = 8;
   partial_plan(M, N, K, &steps, &splits, &nwv);

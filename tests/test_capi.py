@@ -131,6 +131,10 @@ def test_validation_rejects_before_launch(lib):
                                                               (3072, 3072), (4096, 1024))] == [10, 2, 3, 4, 2]
     # above 64 rows the strides must stay below 2^23 elements (32-bit buffer offsets)
     assert lib.fam_gemm_partial(16, 3072, 32, 1 << 23, 48, 98, 64, 64, None) == _capi.FAM_ERR_UNSUPPORTED
+    # ... and the activation span M * lda * 2 below 2^31 bytes: 144 rows at lda = 2^23 - 8 span
+    # 2.4 GB although lda alone is below 2^23 (the out-of-range offsets would then read memory)
+    assert lib.fam_gemm_partial(16, (1 << 23) - 8, 32, 3072, 48, 144, 178176, 3072, None) == _capi.FAM_ERR_UNSUPPORTED
+    assert lib.fam_gemm_partial(16, (1 << 23) - 8, 32, 3072, 48, 129, 178176, 3072, None) == _capi.FAM_ERR_UNSUPPORTED
 
     r = _capi.RowopDesc()
     r.src, r.partials, r.splits, r.split_stride = _capi.FAM_ROWSRC_PARTIALS, 16, 2, 4 * 64
