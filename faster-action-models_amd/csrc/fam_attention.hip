@@ -642,219 +642,6 @@ __global__ __launch_bounds__(256) void attn_self_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// attn_oproj_kernel: the action tokens' self-attention fused into the split-K output
-// projection that consumes it.  Grid (N/16 column groups, H/G head groups); workgroup
-// (x, z) owns output columns n0 = 16x .. +15 and the G heads of group z, i.e. the k-slice
-// [z*G*DH, (z+1)*G*DH) of the projection:
-//   1. issue the loads of its 16 x G*DH weight panel (MFMA A-operand, registers), then of q,
-//      k, v of its G heads for every batch (RMSNorm + RoPE applied on the way when QKN);
-//   2. stage q, k and the transposed v in LDS; each 16-query tile of each (batch, head) gets
-//      an exact softmax over its <= 32 keys (the attn_self_kernel formulation);
-//   3. write O [B*S, G*DH] (bf16, as fam_attention stores it) to LDS and multiply:
-//      partial[z][m][n] = sum over the slice of O[m][k] * w[n][k], the four waves splitting k,
-//      reduced through LDS in wave order, fam_gemm_partial's layout.
-// Each of the N/16 workgroups of a head group recomputes that group's attention (G * 0.26
-// MFLOP at S = 32, DH = 64); in exchange the attention launch and its output round trip go.
-// MT = 2: one batch (row slots 0..31); MT = 4: two batches (slots 32b .. 32b + 31).
-template <int DH, bool QKN, int MT>
-__global__ __launch_bounds__(256) void attn_oproj_kernel(AttnArgs a, const bf16* __restrict__ w, int64_t ldw,
-                                                         float* __restrict__ part, int64_t N, int B, int S) {
-  constexpr int MR = 16 * MT;            // row slots (32 per batch)
-  constexpr int GD = 512 / MT;           // dims of the head group
-  constexpr int G = GD / DH;             // heads per group
-  constexpr int NC = DH / 32;            // 32-wide k-chunks of the head dim (scores)
-  constexpr int NDT = DH / 16;           // 16-row output tiles of the head dim
-  constexpr int CPRW = GD / 8;           // 16-byte chunks per row slot
-  constexpr int CH = MR * CPRW / 256;    // chunks per thread per tensor
-  constexpr int KSW = GD / 128;          // 32-wide k-steps per wave in the projection
-  constexpr int NTASK = (MR / 32) * G * 2;
-  constexpr int TPW = NTASK / 4;         // attention tasks per wave
-  static_assert(CH * 256 == MR * CPRW && TPW * 4 == NTASK && KSW >= 1, "tile shape");
-  __shared__ bf16 Qs[MR][GD + 8];        // q, later O
-  __shared__ bf16 Ks[MR][GD + 8];
-  __shared__ bf16 Vt[GD][MR + 8];
-  __shared__ f32x4 red[4][MT][64];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l16 = lane & 15, lg = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const int z = blockIdx.y, h0 = z * G;
-  const int M = B * S;
-
-  // ---- phase 1: weight panel, then q / k / v chunks (and the normaliser's operands)
-  const int64_t wn = n0 + l16;
-  const bf16* wp = w + (wn < N ? wn : 0) * ldw + (int64_t)h0 * DH + wave * (GD / 4) + lg * 8;
-  bf16x8 wf[KSW];
-#pragma unroll
-  for (int s = 0; s < KSW; ++s) wf[s] = load8(wp + s * 32);
-
-  bf16x8 qr[CH], kr[CH], vr[CH];
-  bf16x8 qw, kw;                         // a thread's chunks share their column (256 % CPRW == 0)
-  f32x4 qcs[CH], qsn[CH];
-  float2 qss[CH], kss[CH];
-  const bool rope = QKN && a.rcs != nullptr;
-  const int64_t per = QKN ? a.nwidth / 16 / CPRW : 0;   // sum-of-squares groups per thread
-  if constexpr (QKN) {
-    const int col = (tid % CPRW) * 8;
-    qw = load8(a.qnw + (h0 + col / DH) * DH + col % DH);
-    kw = load8(a.knw + (h0 + col / DH) * DH + col % DH);
-  }
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int idx = tid + 256 * c, r = idx / CPRW, col = (idx % CPRW) * 8;
-    const int b = r >> 5, i = r & 31;
-    const bool ok = b < B && i < S;
-    const int bb = ok ? b : 0, ii = ok ? i : 0;
-    const int g = col / DH, d0 = col % DH, h = h0 + g;
-    qr[c] = load8(a.q + bb * a.q_bs + ii * a.q_rs + h * a.q_hs + d0);
-    kr[c] = load8(a.k0 + bb * a.k0_bs + ii * a.k0_rs + h * a.k0_hs + d0);
-    vr[c] = load8(a.v0 + bb * a.v0_bs + ii * a.v0_rs + h * a.v0_hs + d0);
-    if constexpr (QKN) {
-      const int64_t srow = (bb * a.ssbr + ii) * a.ssrs + (idx % CPRW) * per;
-      qss[c] = *reinterpret_cast<const float2*>(a.qss + srow + a.qg0);
-      kss[c] = *reinterpret_cast<const float2*>(a.kss + srow + a.kg0);
-      const float* cb = rope ? a.rcs + ii * a.rrs + d0 / 2 : a.qss;
-      const float* sb = rope ? a.rsn + ii * a.rrs + d0 / 2 : a.qss;
-      qcs[c] = *reinterpret_cast<const f32x4*>(cb);
-      qsn[c] = *reinterpret_cast<const f32x4*>(sb);
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // ---- phase 2: normalise, stage in LDS (row slots past the batches / sequence get zeros)
-#pragma unroll
-  for (int c = 0; c < CH; ++c) {
-    const int idx = tid + 256 * c, r = idx / CPRW, col = (idx % CPRW) * 8;
-    const int b = r >> 5, i = r & 31;
-    const bool ok = b < B && i < S;
-    bf16x8 qn = qr[c], kn = kr[c], vn = vr[c];
-    if constexpr (QKN) {
-      const int bb = ok ? b : 0, ii = ok ? i : 0;
-      const int64_t srow = (bb * a.ssbr + ii) * a.ssrs + (idx % CPRW) * per;
-      float sq = qss[c].x + qss[c].y, sk = kss[c].x + kss[c].y;
-      for (int64_t gi = 2; gi < per; gi += 2) {   // wider rows: the rest of this thread's share
-        const float2 x = *reinterpret_cast<const float2*>(a.qss + srow + a.qg0 + gi);
-        const float2 y = *reinterpret_cast<const float2*>(a.kss + srow + a.kg0 + gi);
-        sq += x.x + x.y;
-        sk += y.x + y.y;
-      }
-      // the CPRW threads of a row are consecutive lanes: fixed butterfly order
-#pragma unroll
-      for (int o = 1; o < CPRW; o <<= 1) {
-        sq += __shfl_xor(sq, o, kWave);
-        sk += __shfl_xor(sk, o, kWave);
-      }
-      const float rq = rsqrtf(sq / (float)a.nwidth + a.neps), rk = rsqrtf(sk / (float)a.nwidth + a.neps);
-      qn = norm_rope8(qr[c], rq, qw, qcs[c], qsn[c], rope);
-      kn = norm_rope8(kr[c], rk, kw, qcs[c], qsn[c], rope);   // same token position
-    }
-    if (!ok) {
-      qn = zero8();
-      kn = zero8();
-      vn = zero8();
-    }
-    *reinterpret_cast<bf16x8*>(&Qs[r][col]) = qn;
-    *reinterpret_cast<bf16x8*>(&Ks[r][col]) = kn;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) Vt[col + e][r] = vn[e];
-  }
-  __syncthreads();
-
-  // ---- phase 3: attention of this wave's (batch, head, 16-query tile) tasks, O^T in registers
-  f32x4 ot[TPW][NDT];
-#pragma unroll
-  for (int u = 0; u < TPW; ++u) {
-    const int t = wave + 4 * u, b = t / (2 * G), g = (t / 2) % G, qt = t & 1;
-#pragma unroll
-    for (int d = 0; d < NDT; ++d) ot[u][d] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (b >= B || qt * 16 >= S) continue;   // wave-uniform
-    bf16x8 qf[NC], kf[2][NC];
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      qf[c] = *reinterpret_cast<const bf16x8*>(&Qs[b * 32 + qt * 16 + l16][g * DH + c * 32 + lg * 8]);
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-        kf[kt][c] = *reinterpret_cast<const bf16x8*>(&Ks[b * 32 + kt * 16 + l16][g * DH + c * 32 + lg * 8]);
-    }
-    float sc[2][4];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) acc = mfma16(kf[kt][c], qf[c], acc);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int kk = kt * 16 + lg * 4 + e;   // keys {4g..4g+3} and {16+4g..16+4g+3} of lane group g
-        const float v = kk < S ? acc[e] * a.scale_log2 : -INFINITY;
-        sc[kt][e] = v;
-        mx = fmaxf(mx, v);
-      }
-    }
-    mx = group4_max(mx);
-    float psum = 0.f;
-    bf16x8 pf;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float pv = exp2f(sc[kt][e] - mx);
-        psum += pv;
-        pf[kt * 4 + e] = to_bf(pv);
-      }
-    const float inv = 1.0f / group4_sum(psum);
-#pragma unroll
-    for (int d = 0; d < NDT; ++d) {
-      const int dd = g * DH + d * 16 + l16;
-      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&Vt[dd][b * 32 + lg * 4]);
-      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(&Vt[dd][b * 32 + 16 + lg * 4]);
-      bf16x8 vf;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) { vf[e] = lo[e]; vf[4 + e] = hi[e]; }
-      ot[u][d] = mfma16(vf, pf, f32x4{0.f, 0.f, 0.f, 0.f}) * inv;   // O^T[d*16 + 4lg + i][query l16]
-    }
-  }
-  __syncthreads();   // every wave is done with Qs
-
-  // ---- phase 4: O (bf16, packed rows b*S + i) over Qs
-#pragma unroll
-  for (int u = 0; u < TPW; ++u) {
-    const int t = wave + 4 * u, b = t / (2 * G), g = (t / 2) % G, qt = t & 1;
-    const int q = qt * 16 + l16;
-    if (b >= B || q >= S) continue;
-    const int m = b * S + q;
-#pragma unroll
-    for (int d = 0; d < NDT; ++d) {
-      bf16x4 ov;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ov[e] = to_bf(ot[u][d][e]);
-      *reinterpret_cast<bf16x4*>(&Qs[m][g * DH + d * 16 + lg * 4]) = ov;
-    }
-  }
-  __syncthreads();
-
-  // ---- phase 5: partial[z][m][n0 + 4lg + e] = sum over this wave's k of w[n][k] O[m][k]
-  f32x4 acc[MT];
-#pragma unroll
-  for (int t = 0; t < MT; ++t) {
-    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KSW; ++s) {
-      const bf16x8 of = *reinterpret_cast<const bf16x8*>(&Qs[t * 16 + l16][wave * (GD / 4) + s * 32 + lg * 8]);
-      acc[t] = mfma16(wf[s], of, acc[t]);
-    }
-    red[wave][t][lane] = acc[t];
-  }
-  __syncthreads();
-  for (int t = wave; t < MT; t += 4) {
-    const f32x4 v = ((red[0][t][lane] + red[1][t][lane]) + red[2][t][lane]) + red[3][t][lane];
-    const int m = t * 16 + l16;
-    const int64_t n = n0 + lg * 4;
-    if (m < M && n < N) *reinterpret_cast<f32x4*>(part + ((int64_t)z * M + m) * N + n) = v;
-  }
-}
-
-// ---------------------------------------------------------------------------------------
 // attn_cross_kernel: 32 or fewer queries over a long key sequence in one segment, no mask (the
 // action tokens over the context).  Grid (batch*head, key split), 4 waves.  The workgroup's
 // threads normalise the head's queries once into LDS (QN: RMSNorm from the producer's sums of
@@ -1594,94 +1381,4 @@ extern "C" int fam_attention_combine(const fam_attn_desc* d, void* stream) {
   else if (a.splits <= 16) FAM_LAUNCH((attn_combine_kernel<16>), grid, dim3(64), 0, s, a, d->head_dim, bh);
   else FAM_LAUNCH((attn_combine_kernel<0>), grid, dim3(64), 0, s, a, d->head_dim, bh);
   return fam_host::check_launch("fam_attention_combine");
-}
-
-// Head-group plan of fam_attention_oproj_partial: MT = 2 for one batch, 4 for two; the group
-// spans 512 / MT dims of the head dim axis.
-static int oproj_mt(int64_t B) { return B == 1 ? 2 : 4; }
-static int64_t oproj_heads_per_group(int64_t B, int64_t Dh) { return (512 / oproj_mt(B)) / Dh; }
-
-static int oproj_validate(const fam_attn_desc* d, const void* w, int64_t ldw, const float* partials, int64_t N) {
-  FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_attention_oproj_partial: null descriptor");
-  const int64_t Dh = d->head_dim;
-  FAM_REQUIRE(Dh == 64 || Dh == 128, FAM_ERR_UNSUPPORTED, "fam_attention_oproj_partial: head_dim must be 64 or 128");
-  FAM_REQUIRE(d->batch >= 1 && d->batch <= 2 && d->heads >= 1 && d->sq >= 1 && d->sq <= 32 && d->sk0 == d->sq &&
-                  d->sk1 == 0,
-              FAM_ERR_UNSUPPORTED, "fam_attention_oproj_partial: self-attention with batch <= 2 and Sq == Sk <= 32");
-  FAM_REQUIRE(d->mask_kind == FAM_MASK_NONE && d->num_splits <= 1, FAM_ERR_UNSUPPORTED,
-              "fam_attention_oproj_partial: no mask and no key splits");
-  FAM_REQUIRE(d->heads % oproj_heads_per_group(d->batch, Dh) == 0, FAM_ERR_UNSUPPORTED,
-              "fam_attention_oproj_partial: heads must be a multiple of %lld", (long long)oproj_heads_per_group(d->batch, Dh));
-  FAM_REQUIRE(d->q && d->k0 && d->v0 && w && partials, FAM_ERR_INVALID_ARG, "fam_attention_oproj_partial: missing pointer");
-  const int64_t strides[] = {d->q_bs, d->q_rs, d->q_hs, d->k0_bs, d->k0_rs, d->k0_hs, d->v0_bs, d->v0_rs, d->v0_hs};
-  for (int64_t st : strides)
-    FAM_REQUIRE(st % 8 == 0, FAM_ERR_INVALID_ARG, "fam_attention_oproj_partial: strides must be multiples of 8 elements");
-  FAM_REQUIRE(fam_host::aligned16(d->q) && fam_host::aligned16(d->k0) && fam_host::aligned16(d->v0) &&
-                  fam_host::aligned16(w) && fam_host::aligned16(partials),
-              FAM_ERR_INVALID_ARG, "fam_attention_oproj_partial: q, k, v, w and partials must be 16-byte aligned");
-  FAM_REQUIRE(N >= 4 && N % 4 == 0 && N <= (int64_t)65535 * 16 && ldw >= d->heads * Dh && ldw % 8 == 0,
-              FAM_ERR_INVALID_ARG, "fam_attention_oproj_partial: need N %% 4 == 0, ldw >= heads*head_dim, ldw %% 8 == 0");
-  if (d->qk_norm) {
-    FAM_REQUIRE(d->q_sumsq && d->k_sumsq && d->q_norm_w && d->k_norm_w, FAM_ERR_INVALID_ARG,
-                "fam_attention_oproj_partial: q/k normalisation needs both sums of squares and both weights");
-    FAM_REQUIRE(d->norm_width >= 1024 && d->norm_width % 1024 == 0 && d->ss_row_stride % 4 == 0 &&
-                    d->q_group0 % 4 == 0 && d->k_group0 % 4 == 0 && d->ss_batch_rows >= 0 &&
-                    d->q_group0 >= 0 && d->k_group0 >= 0 && d->q_group0 + d->norm_width / 16 <= d->ss_row_stride &&
-                    d->k_group0 + d->norm_width / 16 <= d->ss_row_stride && d->heads * Dh <= d->norm_width,
-                FAM_ERR_INVALID_ARG, "fam_attention_oproj_partial: bad sums-of-squares layout");
-    FAM_REQUIRE(fam_host::aligned16(d->q_norm_w) && fam_host::aligned16(d->k_norm_w) &&
-                    fam_host::aligned16(d->q_sumsq) && fam_host::aligned16(d->k_sumsq),
-                FAM_ERR_INVALID_ARG, "fam_attention_oproj_partial: norm weights and sums must be 16-byte aligned");
-    FAM_REQUIRE((d->rope_cos == nullptr) == (d->rope_sin == nullptr) &&
-                    (!d->rope_cos || (fam_host::aligned16(d->rope_cos) && fam_host::aligned16(d->rope_sin) &&
-                                      d->rope_row_stride % 4 == 0 && d->rope_row_stride >= Dh / 2)),
-                FAM_ERR_INVALID_ARG, "fam_attention_oproj_partial: bad RoPE tables");
-  }
-  return FAM_OK;
-}
-
-extern "C" int fam_attention_oproj_splits(const fam_attn_desc* d, int64_t N) {
-  if (d == nullptr || (d->head_dim != 64 && d->head_dim != 128) || d->batch < 1 || d->batch > 2) return -1;
-  const int64_t g = oproj_heads_per_group(d->batch, d->head_dim);
-  if (d->heads % g != 0) return -1;
-  (void)N;
-  return (int)(d->heads / g);
-}
-
-template <int DH, bool QKN>
-static void launch_oproj(const AttnArgs& a, const bf16* w, int64_t ldw, float* part, int64_t N, int B, int S,
-                         dim3 grid, hipStream_t s) {
-  if (B == 1) FAM_LAUNCH((attn_oproj_kernel<DH, QKN, 2>), grid, dim3(256), 0, s, a, w, ldw, part, N, B, S);
-  else FAM_LAUNCH((attn_oproj_kernel<DH, QKN, 4>), grid, dim3(256), 0, s, a, w, ldw, part, N, B, S);
-}
-
-extern "C" int fam_attention_oproj_partial(const fam_attn_desc* d, const void* w, int64_t ldw, float* partials,
-                                           int64_t N, void* stream) {
-  const int rc = oproj_validate(d, w, ldw, partials, N);
-  if (rc != FAM_OK) return rc;
-  AttnArgs a{};
-  a.q = (const bf16*)d->q; a.q_bs = d->q_bs; a.q_rs = d->q_rs; a.q_hs = d->q_hs;
-  a.k0 = (const bf16*)d->k0; a.k0_bs = d->k0_bs; a.k0_rs = d->k0_rs; a.k0_hs = d->k0_hs;
-  a.v0 = (const bf16*)d->v0; a.v0_bs = d->v0_bs; a.v0_rs = d->v0_rs; a.v0_hs = d->v0_hs;
-  a.H = d->heads; a.Sq = d->sq; a.sk0 = d->sk0; a.Sk = d->sk0;
-  a.scale_log2 = d->scale * kLog2e;
-  if (d->qk_norm) {
-    a.qss = d->q_sumsq; a.kss = d->k_sumsq; a.ssrs = d->ss_row_stride; a.ssbr = d->ss_batch_rows;
-    a.qg0 = d->q_group0; a.kg0 = d->k_group0; a.nwidth = d->norm_width;
-    a.qnw = (const bf16*)d->q_norm_w; a.knw = (const bf16*)d->k_norm_w; a.neps = d->norm_eps;
-    a.rcs = d->rope_cos; a.rsn = d->rope_sin; a.rrs = d->rope_row_stride;
-  }
-  const int64_t splits = fam_attention_oproj_splits(d, N);
-  const dim3 grid((unsigned)((N + 15) / 16), (unsigned)splits);
-  const int B = (int)d->batch, S = (int)d->sq;
-  hipStream_t s = (hipStream_t)stream;
-  const bf16* wb = (const bf16*)w;
-  if (d->head_dim == 64) {
-    if (d->qk_norm) launch_oproj<64, true>(a, wb, ldw, partials, N, B, S, grid, s);
-    else launch_oproj<64, false>(a, wb, ldw, partials, N, B, S, grid, s);
-  } else {
-    if (d->qk_norm) launch_oproj<128, true>(a, wb, ldw, partials, N, B, S, grid, s);
-    else launch_oproj<128, false>(a, wb, ldw, partials, N, B, S, grid, s);
-  }
-  return fam_host::check_launch("fam_attention_oproj_partial");
 }

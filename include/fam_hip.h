@@ -184,28 +184,6 @@ int fam_attention(const fam_attn_desc* d, void* stream);
  */
 int fam_attention_combine(const fam_attn_desc* d, void* stream);
 
-/*
- * fam_attention_oproj_partial -- the action tokens' self-attention fused into the split-K
- * output projection that consumes it.  With O = the attention fam_attention computes for the
- * same descriptor (o and the key-split fields unused), it writes
- *   partials[z][b*Sq + i][n] = sum over the dims of head group z of O[b, i, :] * w[n, :],
- * z < S = fam_attention_oproj_splits(d, N); group z holds heads [z*H/S, (z+1)*H/S).  The
- * partials have fam_gemm_partial's layout: fam_rowop sums them in z order and applies bias,
- * gate, residual and the next normalisation.  w [N, H*head_dim] bf16 (nn.Linear layout).
- * Every workgroup recomputes its head group's attention (a few hundred kFLOP), which removes
- * the attention launch and the round trip of its output.
- * Replaces: the self-attention of the action tokens and its to_o projection
- *           (FB/wan_video_dit.py:180-204 with :201-202), the pair fam_attention + fam_gemm_partial.
- * Limits: self-attention (sk0 == sq, sk1 == 0) with 1 <= sq <= 32, batch 1 or 2, head_dim 64
- *         or 128, heads a multiple of (256 / batch) / head_dim, no mask, no key splits; the
- *         q/k normalisation of fam_attention (both sides) is supported; N % 4 == 0,
- *         ldw >= heads*head_dim, ldw % 8 == 0; q, k, v, w, partials 16-byte aligned.
- */
-int fam_attention_oproj_partial(const fam_attn_desc* d, const void* w, int64_t ldw, float* partials, int64_t N,
-                                void* stream);
-/* The number of head groups (partial planes) of fam_attention_oproj_partial, -1 if unsupported. */
-int fam_attention_oproj_splits(const fam_attn_desc* d, int64_t N);
-
 /* GEMM prologues (applied to each row of A before the product) and activations. */
 #define FAM_PRO_NONE 0
 #define FAM_PRO_LAYERNORM 1  /* LN(a) [* pro_w + pro_b]                        */

@@ -732,60 +732,6 @@ def test_attention_qk_norm_on_load(B):
     assert relerr(y, ref) <= TOL
 
 
-@pytest.mark.parametrize("B,S,H,Dh,qkn", [(1, 32, 16, 64, True), (2, 32, 16, 64, True), (1, 32, 24, 128, True),
-                                           (2, 17, 8, 128, True), (1, 17, 4, 64, False), (2, 5, 2, 64, False),
-                                           (1, 1, 8, 128, False)])
-def test_attention_oproj_partial(B, S, H, Dh, qkn):
-    """Self-attention fused into the split-K o projection: the partial planes sum to
-    attention(q, k, v) w^T against the oracle (q/k RMSNorm + RoPE on load when qkn), and when
-    the head-group split equals fam_gemm_partial's split of the same product the planes are
-    bit-identical to fam_attention followed by fam_gemm_partial."""
-    A, N = H * Dh, 1024
-    M = B * S
-    x = rnd(M, 1024, seed=140)
-    wqkv, bqkv = rnd(3 * A, 1024, seed=141, scale=0.02), rnd(3 * A, seed=142, scale=0.02)
-    wo = rnd(N, A, seed=143, scale=0.03)
-    qkv, ss = ops().gemm_final(dev(x), dev(wqkv), dev(bqkv), want_sumsq=True)
-    q3 = qkv.view(B, S, 3 * A)
-    q, k, v = q3[:, :, :A], q3[:, :, A:2 * A], q3[:, :, 2 * A:]
-    raw = qkv.float().cpu().view(B, S, 3 * A)
-    qk_norm = None
-    if qkn:
-        wq, wk = rnd(A, seed=144, scale=0.2) + 1, rnd(A, seed=145, scale=0.2) + 1
-        fr = O.action_freqs(Dh, S)
-        cs, sn, trs, _ = ops().rope_tables(fr, "complex", torch.device("cuda"))
-        qk_norm = dict(q_sumsq=ss, k_sumsq=ss, ss_batch_rows=S, q_group0=0, k_group0=A // 16, norm_width=A,
-                       q_norm_w=dev(wq), k_norm_w=dev(wk), eps=1e-6, rope=(cs, sn, trs))
-        qr = O.rope_apply(O.rms_norm(raw[..., :A].to(torch.bfloat16), wq, 1e-6).float(), fr, H)
-        kr = O.rope_apply(O.rms_norm(raw[..., A:2 * A].to(torch.bfloat16), wk, 1e-6).float(), fr, H)
-    else:
-        qr, kr = raw[..., :A], raw[..., A:2 * A]
-    ref = O.linear(O.flash_attention(qr, kr, raw[..., 2 * A:], H).reshape(M, A), wo.float(), None)
-    wod = dev(wo)
-    part, P = ops().attention_oproj_partial(q, k, v, H, wod, qk_norm=qk_norm)
-    err = relerr(part.sum(0), ref)
-    # the two-launch path over the same inputs
-    o2 = ops().attention_bshd(q, k, v, H, qk_norm=qk_norm)
-    part2, P2 = ops().gemm_partial(o2.view(M, A), wod)
-    same = P2 == P and torch.equal(part, part2)
-    print(f"attn+oproj B={B} S={S} H={H} Dh={Dh} qkn={qkn}: planes {P} (gemm_partial {P2}), relerr {err:.3e}, "
-          f"bit-identical to the two-launch path: {same}")
-    assert err <= TOL
-    if P2 == P and (B, S, H, Dh) == (1, 32, 16, 64):
-        assert same    # the config-1 shape: one head group per fam_gemm_partial split, same k order
-
-
-def test_attention_oproj_partial_rejects():
-    from fam import _capi
-    q = torch.zeros(3, 8, 1024, dtype=torch.bfloat16, device="cuda")
-    w = torch.zeros(64, 1024, dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(ValueError):          # batch 3
-        ops().attention_oproj_partial(q, q, q, 16, w)
-    q2 = torch.zeros(1, 33, 1024, dtype=torch.bfloat16, device="cuda")
-    with pytest.raises(_capi.FamError):      # Sq > 32
-        ops().attention_oproj_partial(q2, q2, q2, 16, w)
-
-
 def test_attention_q_norm_cross_with_splits():
     """Cross attention with the query normalised on load (no RoPE) and 13 key splits."""
     S, H, Dh, Lc, Kd = 32, 16, 64, 1560, 1024
