@@ -20,11 +20,19 @@ src/cae-fastwam/..., SCH = FB/schedulers/scheduler_continuous.py.)
 Tensors must be bf16 CUDA (HIP) tensors with a contiguous last dimension; anything else
 raises -- there is no fallback implementation.  Outputs are new tensors allocated on the
 input's device, launches go to torch's current stream.
+
+Each of these functions is a thin wrapper over a ``torch.library`` custom operator in the
+``fam`` namespace (``torch.ops.fam.adaln``, ``rope``, ``attention``, ``linear``,
+``euler_step``) with a fake implementation, so ``torch.compile(fullgraph=True)`` and
+``torch.export`` trace through them as single graph nodes, the way the reference's own
+``fastwam::*`` operators are traced (FG/wan_video_dit.py:1680-1721).  The reference's
+``fastwam::*`` operator forms themselves are in ``fam.fastwam_ops``.
 """
 from __future__ import annotations
 
 import ctypes as C
 import math
+from collections import OrderedDict
 from typing import Dict, Optional, Tuple
 
 import torch
@@ -39,10 +47,13 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-def _check(t: torch.Tensor, name: str, dtype=_BF16) -> None:
+def _check(t: torch.Tensor, name: str, dtype=_BF16, device: bool = True) -> None:
+    """dtype / last-dim checks, and (device=True) that t lives on a HIP device.  The fake
+    implementations run the same checks with device=False, so a traced graph rejects what the
+    real operator would."""
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a tensor")
-    if t.device.type != "cuda":
+    if device and t.device.type != "cuda":
         raise ValueError(f"{name} must be on a HIP device (got {t.device})")
     if dtype is not None and t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
@@ -110,6 +121,25 @@ def _adaln_launch(x: torch.Tensor, shift, scale, weight, bias, eps: float) -> to
     return y.reshape(x.shape)
 
 
+@torch.library.custom_op("fam::adaln", mutates_args=())
+def _adaln_op(x: torch.Tensor, shift: Optional[torch.Tensor], scale: Optional[torch.Tensor],
+              weight: Optional[torch.Tensor], bias: Optional[torch.Tensor], eps: float) -> torch.Tensor:
+    """LayerNorm over the last dim (optional affine), then optional modulation (1 + scale), + shift."""
+    if (shift is None) != (scale is None):
+        raise ValueError("adaln: shift and scale go together")
+    return _adaln_launch(x, shift, scale, weight, bias, eps)
+
+
+@_adaln_op.register_fake
+def _adaln_fake(x, shift, scale, weight, bias, eps):
+    _check(x, "x", device=False)
+    if x.dim() not in (2, 3):
+        raise ValueError(f"expected a 2-D or 3-D tensor, got shape {tuple(x.shape)}")
+    if (shift is None) != (scale is None):
+        raise ValueError("adaln: shift and scale go together")
+    return x.new_empty(x.shape)
+
+
 def adaln_forward(x: torch.Tensor, norm: torch.nn.LayerNorm, shift: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """norm(x) * (1 + scale) + shift in one kernel (FB/fused_adaln.py:513-523).
 
@@ -117,29 +147,22 @@ def adaln_forward(x: torch.Tensor, norm: torch.nn.LayerNorm, shift: torch.Tensor
     used); shift/scale broadcast as [B,1,D] (per sample) or [B,S,D] (per token)."""
     w = norm.weight if getattr(norm, "elementwise_affine", False) else None
     b = norm.bias if getattr(norm, "elementwise_affine", False) else None
-    return _adaln_launch(x, shift, scale, w, b, norm.eps)
+    return torch.ops.fam.adaln(x, shift, scale, w, b, float(norm.eps))
 
 
 def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor], eps: float) -> torch.Tensor:
     """nn.LayerNorm forward over the last dim (FB/wan_video_dit.py:258-261)."""
-    return _adaln_launch(x, None, None, weight, bias, eps)
+    return torch.ops.fam.adaln(x, None, None, weight, bias, float(eps))
 
 
 def modulate_layer_norm(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """modulate(LayerNorm(x, affine=False), shift, scale) -- the CAE form (CA/wan_video_dit.py:590-591)."""
-    return _adaln_launch(x, shift, scale, None, None, eps)
+    return torch.ops.fam.adaln(x, shift, scale, None, None, float(eps))
 
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     """RMSNorm.forward: bf16(x*rsqrt(mean(x^2)+eps)) * weight (FB/wan_video_dit.py:156-167)."""
-    _check(x, "x")
-    _check(weight, "weight")
-    x2, rows, _, D = _rows(x)
-    y = torch.empty((rows, D), dtype=_BF16, device=x.device)
-    wc = weight.contiguous()
-    call("fam_rmsnorm_rope", x2.data_ptr(), x2.stride(0), y.data_ptr(), D, rows, 1, D,
-         wc.data_ptr(), float(eps), None, None, 0, 0, 0, _stream(x))
-    return y.reshape(x.shape)
+    return torch.ops.fam.rope(x, None, 1, "none", weight, float(eps))
 
 
 class RMSNorm(torch.nn.Module):
@@ -155,7 +178,26 @@ class RMSNorm(torch.nn.Module):
 
 
 # --------------------------------------------------------------------------- rope
-_TABLES: Dict[tuple, Tuple[torch.Tensor, torch.Tensor, int, int]] = {}
+# (source tensor, cos, sin, row stride, element stride) per source; the entry holds the source
+# itself, so its address cannot be handed to another tensor while the entry exists and the key
+# (address, shape, strides, dtype, version) names one content
+_TABLES: "OrderedDict[tuple, tuple]" = OrderedDict()
+_TABLES_MAX = 64
+
+
+def _check_pair_layout(f: torch.Tensor, layout: str) -> None:
+    """Reject a real table whose (cos, sin) pairs are not where `layout` says: FG packs
+    cat(cos, sin) per row, CA interleaves (cos, sin) pairs, and both are [S, 1, Dh] -- read
+    with the other convention, every position rotates the wrong pairs.  The pairs of the right
+    layout have unit modulus; position 0 of the other layout pairs (1, 1) or (0, 0)."""
+    half = f.shape[1] // 2
+    c, s_ = (f[:, :half], f[:, half:]) if layout == "cat" else (f[:, 0::2], f[:, 1::2])
+    dev = (c.double() ** 2 + s_.double() ** 2 - 1.0).abs().max().item() if f.numel() else 0.0
+    if dev > 1e-3:
+        other = "rope_apply_cae (CA's interleaved (cos, sin) table)" if layout == "cat" else \
+            "rope_apply (FG's packed cat(cos, sin) table)"
+        raise ValueError(f"freqs is not a {layout!r} RoPE table (|cos|^2 + |sin|^2 deviates from 1 by {dev:.3g}); "
+                         f"a table in the other packing belongs to {other}")
 
 
 def rope_tables(freqs: torch.Tensor, layout: str, device: torch.device):
@@ -164,11 +206,23 @@ def rope_tables(freqs: torch.Tensor, layout: str, device: torch.device):
     layout 'complex'     complex [S, 1, Dh/2] (FB/wan_video_dit.py:49-55)
            'cat'         real [S, 1, Dh] = cat(cos, sin) (FG/wan_video_dit.py:173-177)
            'interleaved' real [S, 1, Dh] = (cos0, sin0, cos1, sin1, ...) (CA/wan_video_dit.py:736-766)
-    Conversions (complex -> fp32, fp64 -> fp32, host -> device) are cached per source tensor."""
-    key = (freqs.data_ptr(), tuple(freqs.shape), freqs.dtype, str(freqs.device), freqs._version, layout, str(device))
+
+    A real fp32 table already on `device` with unit-stride rows is used in place (views of the
+    source, no copy).  Anything else (complex, fp64, host) is converted once per source tensor
+    and cached; the first use of a real table checks its packing (a host sync), so a caller that
+    captures a graph makes one eager call per table first."""
+    if layout not in ("complex", "cat", "interleaved"):
+        raise ValueError(f"unknown RoPE layout {layout!r}")
+    if layout == "complex" and not freqs.is_complex():
+        raise ValueError("layout 'complex' needs a complex freqs tensor")
+    if layout != "complex" and freqs.is_complex():
+        raise ValueError(f"layout {layout!r} needs a real freqs tensor")
+    key = (freqs.data_ptr(), tuple(freqs.shape), tuple(freqs.stride()), freqs.dtype, str(freqs.device),
+           freqs._version, layout, str(device))
     hit = _TABLES.get(key)
     if hit is not None:
-        return hit
+        _TABLES.move_to_end(key)
+        return hit[1:]
     S = freqs.shape[0]
     if layout == "complex":
         f = freqs.reshape(S, -1)
@@ -176,59 +230,97 @@ def rope_tables(freqs: torch.Tensor, layout: str, device: torch.device):
         sin = f.imag.to(device=device, dtype=torch.float32).contiguous()
         res = (cos, sin, cos.shape[1], 1)
     else:
-        f = freqs.reshape(S, -1).to(device=device, dtype=torch.float32).contiguous()
+        f = freqs.reshape(S, -1)
+        if not (f.dtype == torch.float32 and f.device == torch.device(device) and f.stride(-1) == 1
+                and f.data_ptr() % 16 == 0):
+            f = f.to(device=device, dtype=torch.float32).contiguous()
+        _check_pair_layout(f, layout)
         half = f.shape[1] // 2
         if layout == "cat":
-            res = (f, f[:, half:], f.shape[1], 1)
-        elif layout == "interleaved":
-            res = (f, f[:, 1:], f.shape[1], 2)
+            res = (f, f[:, half:], f.stride(0), 1)
         else:
-            raise ValueError(f"unknown RoPE layout {layout!r}")
-    if len(_TABLES) > 64:
-        _TABLES.clear()
-    _TABLES[key] = res
+            res = (f, f[:, 1:], f.stride(0), 2)
+    _TABLES[key] = (freqs,) + res
+    while len(_TABLES) > _TABLES_MAX:
+        _TABLES.popitem(last=False)
     return res
 
 
-def _rope_launch(x: torch.Tensor, freqs: torch.Tensor, num_heads: int, layout: str,
+def _rope_launch(x: torch.Tensor, freqs: Optional[torch.Tensor], num_heads: int, layout: str,
                  weight: Optional[torch.Tensor] = None, eps: float = 0.0) -> torch.Tensor:
     _check(x, "x")
-    if x.dim() != 3:
-        raise ValueError(f"x must be [B, S, H*Dh], got {tuple(x.shape)}")
-    B, S, ND = x.shape
-    if ND % num_heads:
-        raise ValueError(f"last dim {ND} not divisible by num_heads {num_heads}")
-    Dh = ND // num_heads
-    if freqs.shape[0] < S:
-        raise ValueError(f"freqs has {freqs.shape[0]} positions, need {S}")
-    cos, sin, trs, tes = rope_tables(freqs, layout, x.device)
-    x2, rows, _, D = _rows(x)
+    if weight is not None:
+        _check(weight, "weight")
+    x2, rows, S, D = _rows(x)
     y = torch.empty((rows, D), dtype=_BF16, device=x.device)
     wc = weight.contiguous() if weight is not None else None
     w_p = wc.data_ptr() if wc is not None else None
+    if layout == "none":
+        call("fam_rmsnorm_rope", x2.data_ptr(), x2.stride(0), y.data_ptr(), D, rows, 1, D, w_p, float(eps),
+             None, None, 0, 0, 0, _stream(x))
+        return y.reshape(x.shape)
+    _rope_shape(x, freqs, num_heads)
+    cos, sin, trs, tes = rope_tables(freqs, layout, x.device)
     call("fam_rmsnorm_rope", x2.data_ptr(), x2.stride(0), y.data_ptr(), D, rows, S, D, w_p, float(eps),
-         cos.data_ptr(), sin.data_ptr(), trs, tes, Dh, _stream(x))
+         cos.data_ptr(), sin.data_ptr(), trs, tes, D // num_heads, _stream(x))
     return y.reshape(x.shape)
+
+
+def _rope_shape(x: torch.Tensor, freqs: Optional[torch.Tensor], num_heads: int) -> None:
+    if x.dim() != 3:
+        raise ValueError(f"x must be [B, S, H*Dh], got {tuple(x.shape)}")
+    if freqs is None:
+        raise ValueError("a RoPE layout needs freqs")
+    B, S, ND = x.shape
+    if num_heads <= 0 or ND % num_heads:
+        raise ValueError(f"last dim {ND} not divisible by num_heads {num_heads}")
+    if freqs.shape[0] < S:
+        raise ValueError(f"freqs has {freqs.shape[0]} positions, need {S}")
+
+
+@torch.library.custom_op("fam::rope", mutates_args=())
+def _rope_op(x: torch.Tensor, freqs: Optional[torch.Tensor], num_heads: int, layout: str,
+             weight: Optional[torch.Tensor], eps: float) -> torch.Tensor:
+    """Optional RMSNorm (weight given; bf16 rounding before the weight) then the rotation of
+    `layout` ('complex', 'cat', 'interleaved', or 'none' for the norm alone)."""
+    if layout not in ("none", "complex", "cat", "interleaved"):
+        raise ValueError(f"unknown RoPE layout {layout!r}")
+    return _rope_launch(x, freqs, num_heads, layout, weight, eps)
+
+
+@_rope_op.register_fake
+def _rope_fake(x, freqs, num_heads, layout, weight, eps):
+    _check(x, "x", device=False)
+    if layout not in ("none", "complex", "cat", "interleaved"):
+        raise ValueError(f"unknown RoPE layout {layout!r}")
+    if layout != "none":
+        _rope_shape(x, freqs, num_heads)
+    elif x.dim() not in (2, 3):
+        raise ValueError(f"expected a 2-D or 3-D tensor, got shape {tuple(x.shape)}")
+    return x.new_empty(x.shape)
 
 
 def rope_apply(x: torch.Tensor, freqs: torch.Tensor, num_heads: int) -> torch.Tensor:
     """Rotary embedding with the FB/FG call signature: freqs complex [S,1,Dh/2] or packed
-    real cat(cos, sin) [S,1,Dh] (FB/wan_video_dit.py:58-70, FG/wan_video_dit.py:193-215)."""
-    return _rope_launch(x, freqs, num_heads, "complex" if freqs.is_complex() else "cat")
+    real cat(cos, sin) [S,1,Dh] (FB/wan_video_dit.py:58-70, FG/wan_video_dit.py:193-215).
+    A real table in CA's interleaved packing is rejected (it belongs to rope_apply_cae)."""
+    return torch.ops.fam.rope(x, freqs, int(num_heads), "complex" if freqs.is_complex() else "cat", None, 0.0)
 
 
 def rope_apply_cae(x: torch.Tensor, freqs: torch.Tensor, num_heads: int, force_complex: bool = False) -> torch.Tensor:
     """Rotary embedding with the CAE call signature: freqs complex or interleaved real
     (cos, sin) pairs [S,1,Dh] (CA/wan_video_dit.py:769-799).  force_complex only selects the
-    reference's arithmetic route; the rotation is the same."""
+    reference's arithmetic route; the rotation is the same.  A real table in FG's
+    cat(cos, sin) packing is rejected (it belongs to rope_apply)."""
     del force_complex
-    return _rope_launch(x, freqs, num_heads, "complex" if freqs.is_complex() else "interleaved")
+    return torch.ops.fam.rope(x, freqs, int(num_heads), "complex" if freqs.is_complex() else "interleaved", None,
+                              0.0)
 
 
 def rms_norm_rope(x: torch.Tensor, weight: torch.Tensor, eps: float, freqs: torch.Tensor, num_heads: int,
                   layout: str = "complex") -> torch.Tensor:
     """rope_apply(RMSNorm(x), freqs) in one kernel (the q/k post-processing, FG/mot.py:786-816)."""
-    return _rope_launch(x, freqs, num_heads, layout, weight, eps)
+    return torch.ops.fam.rope(x, freqs, int(num_heads), layout, weight, float(eps))
 
 
 # --------------------------------------------------------------------------- attention
@@ -314,14 +406,7 @@ def _attn_desc(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int
     return d, out, keep
 
 
-def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
-                   mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
-                   k_prefix: Optional[torch.Tensor] = None, v_prefix: Optional[torch.Tensor] = None,
-                   out: Optional[torch.Tensor] = None, num_splits: int = 1,
-                   qk_norm: Optional[dict] = None) -> torch.Tensor:
-    """Attention on [B, S, H*Dh] tensors; keys/values are cat(k_prefix, k) when a prefix is
-    given (the MoT joint attention over a cached video K/V, FB/mot.py:446-478) without
-    materialising the concatenation."""
+def _attention_launch(q, k, v, num_heads, mask, scale, k_prefix, v_prefix, out, num_splits, qk_norm):
     d, out, keep = _attn_desc(q, k, v, num_heads, mask, scale, k_prefix, v_prefix, out, qk_norm)
     B, Sq, ND = q.shape
     Dh = ND // num_heads
@@ -334,7 +419,41 @@ def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads:
     call("fam_attention", C.byref(d), _stream(q))
     if num_splits > 1:
         call("fam_attention_combine", C.byref(d), _stream(q))
+    del keep
     return out
+
+
+@torch.library.custom_op("fam::attention", mutates_args=())
+def _attention_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor], num_heads: int,
+                  scale: Optional[float], k_prefix: Optional[torch.Tensor], v_prefix: Optional[torch.Tensor],
+                  num_splits: int) -> torch.Tensor:
+    """softmax(q k^T * scale + mask) v over [B, S, H*Dh] tensors, keys cat(k_prefix, k)."""
+    return _attention_launch(q, k, v, num_heads, mask, scale, k_prefix, v_prefix, None, num_splits, None)
+
+
+@_attention_op.register_fake
+def _attention_fake(q, k, v, mask, num_heads, scale, k_prefix, v_prefix, num_splits):
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _check(t, n, device=False)
+        if t.dim() != 3:
+            raise ValueError(f"{n} must be [B, S, H*Dh], got {tuple(t.shape)}")
+    if num_heads <= 0 or q.shape[-1] % num_heads or k.shape[-1] != q.shape[-1] or v.shape[-1] != q.shape[-1]:
+        raise ValueError("q/k/v last dims must equal num_heads * head_dim")
+    return q.new_empty(q.shape)
+
+
+def attention_bshd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
+                   mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+                   k_prefix: Optional[torch.Tensor] = None, v_prefix: Optional[torch.Tensor] = None,
+                   out: Optional[torch.Tensor] = None, num_splits: int = 1,
+                   qk_norm: Optional[dict] = None) -> torch.Tensor:
+    """Attention on [B, S, H*Dh] tensors; keys/values are cat(k_prefix, k) when a prefix is
+    given (the MoT joint attention over a cached video K/V, FB/mot.py:446-478) without
+    materialising the concatenation.  With `out` or `qk_norm` (the fused models' on-load
+    normalisation from fam_gemm_final sums of squares) the launch is direct, not an operator."""
+    if out is not None or qk_norm is not None:
+        return _attention_launch(q, k, v, num_heads, mask, scale, k_prefix, v_prefix, out, num_splits, qk_norm)
+    return torch.ops.fam.attention(q, k, v, mask, int(num_heads), scale, k_prefix, v_prefix, int(num_splits))
 
 
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int,
@@ -344,35 +463,18 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads
     if not compatibility_mode:
         raise NotImplementedError("Only compatibility mode is implemented for flash attention. "
                                   "Please set compatibility_mode=True.")
-    return attention_bshd(q, k, v, num_heads, ctx_mask)
-
-
-def attention_oproj_partial(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int, w: torch.Tensor,
-                            scale: Optional[float] = None, qk_norm: Optional[dict] = None):
-    """Self-attention of [B, S, H*Dh] q/k/v (S <= 32, B <= 2) fused into the split-K product
-    with w [N, H*Dh] (fam_attention_oproj_partial): returns (partials [P, B*S, N] fp32, P),
-    sum over planes = attention(q, k, v) w^T, in fam_gemm_partial's layout for rowop."""
-    _check(w, "w")
-    d, _, _ = _attn_desc(q, k, v, num_heads, None, scale, None, None, q, qk_norm)
-    N = w.shape[0]
-    P = _capi.lib().fam_attention_oproj_splits(C.byref(d), N)
-    if P < 1:
-        raise ValueError("attention_oproj_partial: unsupported shape (batch <= 2, head_dim 64/128, "
-                         "heads a multiple of (256 / batch) / head_dim)")
-    B, S = q.shape[0], q.shape[1]
-    part = torch.empty((P, B * S, N), dtype=torch.float32, device=q.device)
-    call("fam_attention_oproj_partial", C.byref(d), w.data_ptr(), w.stride(0), part.data_ptr(), N, _stream(q))
-    return part, P
+    return torch.ops.fam.attention(q, k, v, ctx_mask, int(num_heads), None, None, None, 1)
 
 
 # --------------------------------------------------------------------------- linear
-def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """y = x W^T + b for bf16 x [..., K], W [N, K] (nn.Linear)."""
+@torch.library.custom_op("fam::linear", mutates_args=())
+def _linear_op(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]) -> torch.Tensor:
+    """y = x W^T + b, bf16 in and out, fp32 accumulation."""
     _check(x, "x")
     _check(weight, "weight")
     K = x.shape[-1]
     N = weight.shape[0]
-    if weight.shape[1] != K:
+    if weight.dim() != 2 or weight.shape[1] != K:
         raise ValueError(f"weight {tuple(weight.shape)} does not match input features {K}")
     x2 = x.reshape(-1, K)
     if x2.stride(-1) != 1:
@@ -396,6 +498,20 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
             return y.reshape(*x.shape[:-1], N)
     gemm(x2, w, b, y)
     return y.reshape(*x.shape[:-1], N)
+
+
+@_linear_op.register_fake
+def _linear_fake(x, weight, bias):
+    _check(x, "x", device=False)
+    _check(weight, "weight", device=False)
+    if weight.dim() != 2 or weight.shape[1] != x.shape[-1]:
+        raise ValueError(f"weight {tuple(weight.shape)} does not match input features {x.shape[-1]}")
+    return x.new_empty((*x.shape[:-1], weight.shape[0]))
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = x W^T + b for bf16 x [..., K], W [N, K] (nn.Linear)."""
+    return torch.ops.fam.linear(x, weight, bias)
 
 
 def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: torch.Tensor, *,
@@ -548,15 +664,11 @@ def rowop(out: torch.Tensor, *, partials: Optional[torch.Tensor] = None, x_in: O
 
 
 # --------------------------------------------------------------------------- sampler
-def euler_step(model_output: torch.Tensor, delta: torch.Tensor, sample: torch.Tensor,
-               out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """sample + model_output * delta in bf16 (SCH:82-88); delta a scalar or per-batch [B]."""
+def _euler_launch(model_output, delta, sample, out=None):
     _check(sample, "sample")
     _check(model_output, "model_output")
     if model_output.shape != sample.shape:
         raise ValueError("model_output and sample must have the same shape")
-    if not isinstance(delta, torch.Tensor):
-        delta = torch.tensor(float(delta))
     delta = delta.to(device=sample.device, dtype=_BF16).contiguous()
     n = sample.numel()
     if delta.numel() == 1:
@@ -571,6 +683,33 @@ def euler_step(model_output: torch.Tensor, delta: torch.Tensor, sample: torch.Te
         out = torch.empty_like(s)
     call("fam_euler_step", s.data_ptr(), v.data_ptr(), delta.data_ptr(), out.data_ptr(), n, inner, _stream(s))
     return out
+
+
+@torch.library.custom_op("fam::euler_step", mutates_args=())
+def _euler_op(model_output: torch.Tensor, delta: torch.Tensor, sample: torch.Tensor) -> torch.Tensor:
+    """sample + model_output * delta in bf16 with the reference's two roundings."""
+    return _euler_launch(model_output, delta, sample)
+
+
+@_euler_op.register_fake
+def _euler_fake(model_output, delta, sample):
+    _check(sample, "sample", device=False)
+    _check(model_output, "model_output", device=False)
+    if model_output.shape != sample.shape:
+        raise ValueError("model_output and sample must have the same shape")
+    return torch.empty_like(sample, memory_format=torch.contiguous_format)
+
+
+def euler_step(model_output: torch.Tensor, delta: torch.Tensor, sample: torch.Tensor,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """sample + model_output * delta in bf16 (SCH:82-88); delta a scalar or per-batch [B].
+    With `out` the launch is direct (writes into it), otherwise it is the fam::euler_step
+    operator."""
+    if not isinstance(delta, torch.Tensor):
+        delta = torch.tensor(float(delta))
+    if out is not None:
+        return _euler_launch(model_output, delta, sample, out)
+    return torch.ops.fam.euler_step(model_output, delta, sample)
 
 
 class WanContinuousFlowMatchScheduler:

@@ -1,0 +1,152 @@
+"""CPU checks of the torch.library operator layer: the drop-ins trace as single graph nodes under
+torch.compile(fullgraph=True) (their fake implementations run; nothing launches), and the RoPE
+table cache / layout checks of fam.ops.rope_tables."""
+import pytest
+import torch
+
+from fam import ops
+
+
+def _compile_graph(module, *args):
+    graphs = []
+
+    def backend(gm, example_inputs):
+        graphs.append(gm)
+        return gm.forward
+
+    with torch.no_grad():
+        y = torch.compile(module, fullgraph=True, backend=backend)(*args)
+        y2 = torch.compile(module, fullgraph=True, backend="aot_eager")(*args)
+    targets = [str(n.target) for n in graphs[0].graph.nodes if n.op == "call_function"]
+    return y, y2, targets
+
+
+def _meta(*shape, dtype=torch.bfloat16):
+    return torch.empty(*shape, dtype=dtype, device="meta")
+
+
+class _Block(torch.nn.Module):
+    """The reference block's call pattern: adaln_forward -> linear -> RMSNorm+RoPE / rope_apply ->
+    flash_attention -> layer_norm -> scheduler step."""
+
+    def __init__(self, D=64, H=4):
+        super().__init__()
+        self.H = H
+        self.norm = torch.nn.LayerNorm(D, elementwise_affine=False, eps=1e-6)
+        self.wq = torch.nn.Parameter(_meta(D, D), requires_grad=False)
+        self.bq = torch.nn.Parameter(_meta(D), requires_grad=False)
+        self.nq = torch.nn.Parameter(_meta(D), requires_grad=False)
+
+    def forward(self, x, shift, scale, freqs, delta, mask):
+        h = ops.adaln_forward(x, self.norm, shift, scale)
+        q = ops.rms_norm_rope(ops.linear(h, self.wq, self.bq), self.nq, 1e-6, freqs, self.H, "cat")
+        k = ops.rope_apply(ops.linear(h, self.wq), freqs, self.H)
+        o = ops.flash_attention(q, k, h, self.H, ctx_mask=mask)
+        o = ops.layer_norm(o, None, None, 1e-6) + ops.rms_norm(o, self.nq, 1e-6)
+        return ops.WanContinuousFlowMatchScheduler.step(o, delta, x)
+
+
+def test_fam_ops_trace_as_single_nodes():
+    m = _Block()
+    x = _meta(2, 8, 64)
+    y, y2, targets = _compile_graph(m, x, _meta(2, 1, 64), _meta(2, 1, 64), _meta(8, 1, 16, dtype=torch.float32),
+                                    _meta((), dtype=torch.bfloat16), _meta(8, 8, dtype=torch.bool))
+    assert y.shape == x.shape and y.dtype == torch.bfloat16 and y2.shape == x.shape
+    for op in ("fam.adaln", "fam.linear", "fam.rope", "fam.attention", "fam.euler_step"):
+        assert any(t.startswith(op) for t in targets), (op, targets)
+    # one node per drop-in call, nothing decomposed into aten kernels around them
+    assert sum(t.startswith("fam.rope") for t in targets) == 3
+    assert sum(t.startswith("fam.adaln") for t in targets) == 2
+
+
+def test_fam_ops_fake_shapes_and_checks():
+    q = _meta(1, 32, 1024)
+    assert torch.ops.fam.attention(q, _meta(1, 1560, 1024), _meta(1, 1560, 1024), None, 16, None, None, None,
+                                   1).shape == (1, 32, 1024)
+    assert torch.ops.fam.linear(q, _meta(3072, 1024), None).shape == (1, 32, 3072)
+    with pytest.raises(ValueError):
+        torch.ops.fam.linear(q, _meta(3072, 512), None)
+    with pytest.raises(TypeError):
+        torch.ops.fam.adaln(_meta(1, 4, 64, dtype=torch.float16), None, None, None, None, 1e-6)
+    with pytest.raises(ValueError):
+        torch.ops.fam.rope(q, _meta(16, 1, 32, dtype=torch.float32), 16, "cat", None, 0.0)   # 16 < 32 positions
+
+
+def test_fastwam_ops_trace_with_mutation():
+    from fam import fastwam_ops  # noqa: F401  (defines torch.ops.fastwam.*)
+
+    class M(torch.nn.Module):
+        def forward(self, qkv, wqk, freqs, sgn, kbuf, vbuf, vk, vv, x, w, bias, res, mod, tmod, lnw, lnb):
+            q = torch.ops.fastwam.qkv_post.default(qkv, wqk, freqs, sgn, kbuf, vbuf, 6, 16, 1e-6)
+            qh = q.view(1, 8, 4, 16).transpose(1, 2)
+            kh = kbuf.view(1, 14, 4, 16).transpose(1, 2)
+            vh = vbuf.view(1, 14, 4, 16).transpose(1, 2)
+            o4 = torch.ops.fastwam.short_attn.default(qh, kh, vh, None, 4)
+            o3 = torch.ops.fastwam.short_attn_bsd.default(qh, kh, vh, None, 4)
+            oq = torch.ops.fastwam.qrms_attn.default(q, wqk[0], vk, vv, None, 4, 1e-6)
+            qq, kk = torch.ops.fastwam.qk_post.default(qkv, wqk, freqs, sgn, 16, 1e-6)
+            y = torch.ops.fastwam.skmm.default(o3 + oq + qq + kk, w)
+            xo, yo = torch.ops.fastwam.skpost.default(y, w, bias, res, mod, mod, tmod, lnw, lnb, 2, -1, -1, 1e-6, 0)
+            return o4, xo, yo
+
+    args = (_meta(8, 192), _meta(2, 64), _meta(8, 16, dtype=torch.float32), _meta(2, dtype=torch.float32),
+            _meta(1, 14, 64), _meta(1, 14, 64), _meta(1, 20, 64), _meta(1, 20, 64), None, _meta(64, 64), _meta(64),
+            _meta(1, 8, 64), _meta(1, 6, 64), _meta(1, 6, 64), _meta(64), _meta(64))
+    (o4, xo, yo), _, targets = _compile_graph(M(), *args)
+    assert o4.shape == (1, 4, 8, 16) and xo.shape == (1, 8, 64) and yo.shape == (1, 8, 64)
+    for op in ("fastwam.qkv_post", "fastwam.short_attn", "fastwam.short_attn_bsd", "fastwam.qrms_attn",
+               "fastwam.qk_post", "fastwam.skmm", "fastwam.skpost"):
+        assert any(t.startswith(op) for t in targets), (op, targets)
+
+
+# --------------------------------------------------------------------------- RoPE tables
+def _cat_table(S, Dh, offset=0.0):
+    ang = (torch.arange(S, dtype=torch.float64)[:, None] + offset) * \
+        (1.0 / 10000 ** (torch.arange(0, Dh, 2, dtype=torch.float64) / Dh))[None, :]
+    return torch.cat([ang.cos(), ang.sin()], -1).float().reshape(S, 1, Dh)
+
+
+def _interleaved(cat):
+    S, _, Dh = cat.shape
+    c, s = cat[..., : Dh // 2], cat[..., Dh // 2:]
+    return torch.stack([c, s], -1).reshape(S, 1, Dh)
+
+
+def test_rope_tables_cache_never_returns_a_freed_tables_values():
+    """A cached conversion keeps its source alive, so a new same-shape table with other values
+    (the reference builds a fresh freqs every pre_dit call) is never served the old entry."""
+    dev = torch.device("cpu")
+    seen = []
+    for i in range(6):
+        t = _cat_table(16, 32, offset=float(i)).double()       # fp64 -> converted and cached
+        cos, sin, trs, tes = ops.rope_tables(t, "cat", dev)
+        assert torch.equal(cos[:, :16], t.reshape(16, 32)[:, :16].float())
+        seen.append(cos.data_ptr())
+        del t
+    assert len(ops._TABLES) >= 6
+    t = _cat_table(16, 32, offset=3.0).double()
+    t.mul_(1.0)                                               # in-place change bumps the version
+    cos, _, _, _ = ops.rope_tables(t, "cat", dev)
+    assert torch.equal(cos[:, :16], t.reshape(16, 32)[:, :16].float())
+
+
+def test_rope_tables_fp32_device_table_used_in_place():
+    t = _cat_table(8, 16)
+    cos, sin, trs, tes = ops.rope_tables(t, "cat", torch.device("cpu"))
+    assert cos.data_ptr() == t.data_ptr() and sin.data_ptr() == t.data_ptr() + 4 * 8 and (trs, tes) == (16, 1)
+    ti = _interleaved(t).contiguous()
+    cos, sin, trs, tes = ops.rope_tables(ti, "interleaved", torch.device("cpu"))
+    assert cos.data_ptr() == ti.data_ptr() and sin.data_ptr() == ti.data_ptr() + 4 and (trs, tes) == (16, 2)
+
+
+def test_rope_tables_reject_the_other_packing():
+    """FG's cat(cos, sin) and CA's interleaved tables have the same shape; each entry point
+    rejects the other's table instead of rotating the wrong pairs."""
+    cat = _cat_table(8, 16, offset=2.0)
+    inter = _interleaved(cat).contiguous()
+    with pytest.raises(ValueError, match="rope_apply_cae"):
+        ops.rope_tables(inter, "cat", torch.device("cpu"))
+    with pytest.raises(ValueError, match="rope_apply "):
+        ops.rope_tables(cat, "interleaved", torch.device("cpu"))
+    with pytest.raises(ValueError):
+        ops.rope_tables(cat, "complex", torch.device("cpu"))
