@@ -21,6 +21,7 @@
 //
 // Algorithmic bytes per launch: 2*B*H*Dh*(2*Sq + 2*Sk) (+ mask); flops 4*B*H*Sq*Sk*Dh.
 #include <algorithm>
+#include <mutex>
 
 #include "fam_common.h"
 
@@ -1381,4 +1382,66 @@ extern "C" int fam_attention_combine(const fam_attn_desc* d, void* stream) {
   else if (a.splits <= 16) FAM_LAUNCH((attn_combine_kernel<16>), grid, dim3(64), 0, s, a, d->head_dim, bh);
   else FAM_LAUNCH((attn_combine_kernel<0>), grid, dim3(64), 0, s, a, d->head_dim, bh);
   return fam_host::check_launch("fam_attention_combine");
+}
+
+// ---------------------------------------------------------------------------------------
+// fam_attention_noalloc: key-split attention (fam_attention + fam_attention_combine) whose split
+// partials live in `scratch`, a library-owned device array, instead of caller buffers.  Every
+// split writes its partial (o, m, l) for every query it covers, an empty split included (o = 0,
+// m = -inf), before the combine reads it, so nothing needs clearing between calls.
+#define FAM_ATTN_SCRATCH_BYTES (8u << 20)
+static __device__ __align__(256) unsigned char scratch[FAM_ATTN_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per device.  In host
+// code the array's own name is not a device address; only this pointer may reach a kernel.
+void* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fam_host::set_error("fam_attention_noalloc: no current HIP device (or device index >= %d)", kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      fam_host::set_error("fam_attention_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                          hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int64_t fam_attention_noalloc_max_bytes(void) { return (int64_t)FAM_ATTN_SCRATCH_BYTES; }
+
+extern "C" int fam_attention_noalloc(const fam_attn_desc* d, void* stream) {
+  FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_attention_noalloc: null descriptor");
+  FAM_REQUIRE(d->num_splits >= 2 && d->num_splits <= 64, FAM_ERR_INVALID_ARG,
+              "fam_attention_noalloc: num_splits must be in [2, 64] (got %d)", d->num_splits);
+  FAM_REQUIRE(d->batch >= 0 && d->heads >= 1 && d->sq >= 0 && d->head_dim >= 1, FAM_ERR_INVALID_ARG,
+              "fam_attention_noalloc: bad sizes");
+  const int64_t rows = (int64_t)d->num_splits * d->batch * d->heads * d->sq;
+  const int64_t o_bytes = (rows * d->head_dim * 4 + 255) / 256 * 256;
+  const int64_t need = o_bytes + rows * 2 * 4;
+  FAM_REQUIRE(need <= (int64_t)FAM_ATTN_SCRATCH_BYTES, FAM_ERR_UNSUPPORTED,
+              "fam_attention_noalloc: the split partials need %lld bytes, above the %lld-byte scratch "
+              "(num_splits * batch * heads * Sq * (head_dim + 2) * 4 <= %lld)",
+              (long long)need, (long long)FAM_ATTN_SCRATCH_BYTES, (long long)FAM_ATTN_SCRATCH_BYTES);
+  unsigned char* base = static_cast<unsigned char*>(scratch_on_current_device());
+  if (base == nullptr) return FAM_ERR_LAUNCH;
+  fam_attn_desc dd = *d;
+  dd.part_o = reinterpret_cast<float*>(base);
+  dd.part_ml = reinterpret_cast<float*>(base + o_bytes);
+  const int rc = fam_attention(&dd, stream);
+  if (rc != FAM_OK) return rc;
+  if (dd.batch == 0 || dd.sq == 0) return FAM_OK;
+  return fam_attention_combine(&dd, stream);
 }

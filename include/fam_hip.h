@@ -184,6 +184,21 @@ int fam_attention(const fam_attn_desc* d, void* stream);
  */
 int fam_attention_combine(const fam_attn_desc* d, void* stream);
 
+/*
+ * fam_attention_noalloc -- fam_attention with key splits followed by fam_attention_combine,
+ * with the split partials in a library-owned device array (8 MiB per GPU, held until the
+ * process ends) instead of the caller's part_o / part_ml, which are ignored.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc); it calls no allocating
+ * routine.  The caller passes q, k, v and o as for fam_attention; num_splits in [2, 64] and
+ *   num_splits * batch * heads * sq * (head_dim + 2) * 4 bytes <= fam_attention_noalloc_max_bytes()
+ * (larger calls return FAM_ERR_UNSUPPORTED).  Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams, or host threads) race and must be
+ * serialised by the caller.  Results equal fam_attention + fam_attention_combine bit for bit.
+ */
+int fam_attention_noalloc(const fam_attn_desc* d, void* stream);
+int64_t fam_attention_noalloc_max_bytes(void);
+
 /* GEMM prologues (applied to each row of A before the product) and activations. */
 #define FAM_PRO_NONE 0
 #define FAM_PRO_LAYERNORM 1  /* LN(a) [* pro_w + pro_b]                        */
