@@ -643,6 +643,230 @@ __global__ __launch_bounds__(256) void attn_self_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
+// attn_small_kernel: up to 32 queries over up to 32 NW keys (two segments, optional mask): the
+// MoT joint attention of the action tokens over [cached video K/V ; action K/V] and their
+// cross-attention to a short context.  Grid (batch * head, NV): workgroup (bh, y) produces
+// output dims [y DH/NV, (y+1) DH/NV) of its head, one wave per 32-key block.  Every workgroup of
+// a head computes the same full scores, so the dim split needs no combine; it divides the V
+// reads and spreads a head over NV CUs.  Every global load is issued before the first use:
+//   - the queries, once per workgroup, staged in LDS (NSS > 0: q arrives raw from
+//     fam_gemm_final and is RMS-normalised on the way from the producer's per-16-column sums of
+//     squares, the DH/8 threads of a query each summing a share of the row);
+//   - the wave's K block as MFMA A-fragments straight from global memory;
+//   - the wave's V block (its dims only), row-major into the wave's own LDS rows, read back
+//     as the V^T operand through transposing LDS reads;
+//   - the mask entries of the lane's scores.
+// Keys past Sk are not loaded.  Each wave takes an exact softmax over its block (S^T = K Q^T, a
+// lane holds one query); the waves' (m, l, o) are merged through LDS in wave order.
+template <int DH, int NW, int NV, int NSS>
+__global__ __launch_bounds__(NW * 64) void attn_small_kernel(AttnArgs a) {
+  constexpr int NC = DH / 32, CPR = DH / 8, NT = NW * 64;
+  constexpr int DVW = DH / NV, NDT = DVW / 16, VCPR = DVW / 8;   // this workgroup's output dims
+  constexpr int NVC = KB * VCPR / 64;                              // 16-byte V chunks per lane
+  constexpr int VLD = DVW + 16;      // V row pitch: 8 rows x 32 bytes of a transposing read
+                                     // land in distinct banks
+  constexpr int QLD = DH + 8;
+  constexpr int QCH = (32 * CPR + NT - 1) / NT;                    // q chunks per thread
+  constexpr int VS_BYTES = NW * KB * VLD * 2, SO_BYTES = NW * 32 * DVW * 4;
+  constexpr int LDS_BYTES = VS_BYTES > SO_BYTES ? VS_BYTES : SO_BYTES;
+  constexpr bool QN = NSS > 0;
+  static_assert(NVC >= 1 && NDT >= 1, "unsupported dim split");
+  // the V blocks, then (after a barrier) the waves' fp32 partial outputs, in one buffer
+  __shared__ __attribute__((aligned(16))) unsigned char smem[LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) bf16 Qs[32][QLD];
+  __shared__ float s_m[NW][32], s_l[NW][32];
+  bf16 (*Vs)[KB][VLD] = reinterpret_cast<bf16 (*)[KB][VLD]>(smem);
+  float (*So)[32][DVW] = reinterpret_cast<float (*)[32][DVW]>(smem);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const uint32_t bh32 = blockIdx.x, H32 = (uint32_t)a.H;
+  const int64_t b = bh32 / H32, h = bh32 - (uint32_t)b * H32;
+  const int dv0 = (int)blockIdx.y * DVW;
+  const int Sq = (int)a.Sq, Sk = (int)a.Sk;
+  const int k0 = wave * KB;
+  const SegRows krows = key_rows(a, b, h), vrows = val_rows(a, b, h);
+
+  // ---- phase 1: every load
+  const bf16* qbase = a.q + b * a.q_bs + h * a.q_hs;
+  bf16x8 qr[QCH], qw[QCH];
+  f32x4 ssv[QCH][QN ? NSS : 1];
+  const int nss = QN ? (int)(a.nwidth / 16 / CPR / 4) : 0;   // 16-byte chunks of a thread's share
+#pragma unroll
+  for (int j = 0; j < QCH; ++j) {
+    const int idx = tid + NT * j, q = idx / CPR, d0 = (idx % CPR) * 8;
+    const int qc = q < Sq ? q : 0;
+    qr[j] = load8(qbase + qc * a.q_rs + d0);
+    if constexpr (QN) {
+      qw[j] = load8(a.qnw + h * DH + d0);
+      const float* p = a.qss + (b * a.ssbr + qc) * a.ssrs + a.qg0 + (idx % CPR) * (a.nwidth / 16 / CPR);
+#pragma unroll
+      for (int u = 0; u < NSS; ++u) ssv[j][u] = *reinterpret_cast<const f32x4*>(p + 4 * (u < nss ? u : 0));
+    }
+  }
+  bf16x8 kf[2][NC];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+    const int kk = k0 + kt * 16 + l16;
+    const bf16* kr = krows.row(kk < Sk ? kk : 0);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      kf[kt][c] = zero8();
+      if (kk < Sk) kf[kt][c] = load8(kr + c * 32 + lg * 8);
+    }
+  }
+  bf16x8 vc[NVC];
+#pragma unroll
+  for (int p = 0; p < NVC; ++p) {
+    const int cidx = lane + 64 * p, key = cidx / VCPR, d0 = dv0 + (cidx % VCPR) * 8;
+    const int kk = k0 + key;
+    vc[p] = zero8();
+    if (kk < Sk) vc[p] = load8(vrows.row(kk) + d0);
+  }
+  float madd[2][2][4];
+  if (a.mask_kind != FAM_MASK_NONE) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int q = t * 16 + l16, kk = k0 + kt * 16 + lg * 4 + e;
+          const int64_t mi = b * a.mbs + h * a.mhs + (int64_t)(q < Sq ? q : 0) * a.mqs + (kk < Sk ? kk : 0);
+          if (a.mask_kind == FAM_MASK_BOOL)
+            madd[t][kt][e] = reinterpret_cast<const uint8_t*>(a.mask)[mi] ? 0.f : -INFINITY;
+          else if (a.mask_kind == FAM_MASK_ADD_F32)
+            madd[t][kt][e] = reinterpret_cast<const float*>(a.mask)[mi] * kLog2e;
+          else
+            madd[t][kt][e] = to_f(reinterpret_cast<const bf16*>(a.mask)[mi]) * kLog2e;
+        }
+  } else {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) madd[t][kt][e] = 0.f;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- phase 2: queries (normalised) and the V block into LDS
+#pragma unroll
+  for (int j = 0; j < QCH; ++j) {
+    const int idx = tid + NT * j, q = idx / CPR, d0 = (idx % CPR) * 8;
+    bf16x8 qn = qr[j];
+    if constexpr (QN) {
+      float sq = 0.f;
+#pragma unroll
+      for (int u = 0; u < NSS; ++u)
+        if (u < nss) sq += (ssv[j][u][0] + ssv[j][u][1]) + (ssv[j][u][2] + ssv[j][u][3]);
+      // the CPR threads of a query are consecutive lanes: fixed butterfly order
+#pragma unroll
+      for (int o = 1; o < CPR; o <<= 1) sq += __shfl_xor(sq, o, kWave);
+      const float rstd = rsqrtf(sq / (float)a.nwidth + a.neps);
+      const f32x4 zero4 = f32x4{0.f, 0.f, 0.f, 0.f};
+      qn = norm_rope8(qr[j], rstd, qw[j], zero4, zero4, false);
+    }
+    if (q < 32 && idx < 32 * CPR) *reinterpret_cast<bf16x8*>(&Qs[q][d0]) = qn;
+  }
+#pragma unroll
+  for (int p = 0; p < NVC; ++p) {
+    const int cidx = lane + 64 * p, key = cidx / VCPR, d0 = (cidx % VCPR) * 8;
+    *reinterpret_cast<bf16x8*>(&Vs[wave][key][d0]) = vc[p];
+  }
+  __syncthreads();
+
+  // ---- the block's scores and exact softmax, per query tile (a lane holds query t*16 + l16)
+  float mw[2], lw[2];
+  bf16x8 pf[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    bf16x8 qf[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qf[c] = *reinterpret_cast<const bf16x8*>(&Qs[t * 16 + l16][c * 32 + lg * 8]);
+    float sc[2][4];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) acc = mfma16(kf[kt][c], qf[c], acc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int kk = k0 + kt * 16 + lg * 4 + e;
+        const float v = kk < Sk ? acc[e] * a.scale_log2 + madd[t][kt][e] : -INFINITY;
+        sc[kt][e] = v;
+        mloc = fmaxf(mloc, v);
+      }
+    }
+    const float m = group4_max(mloc);
+    float psum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float pv = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sc[kt][e] - m);
+        psum += pv;
+        pf[t][kt * 4 + e] = to_bf(pv);
+      }
+    mw[t] = m;
+    lw[t] = group4_sum(psum);
+  }
+  // O^T of the block over this workgroup's dims: V^T (row = dim, k = key in the score order
+  // above) from the row-major V rows with transposing reads -- lane s of a 16-lane group loads
+  // key 4lg + s/4 (+16 for the upper half), dims 16dt + 4(s%4) .. +3, and lane i receives keys
+  // 4lg .. 4lg+3 of dim 16dt + i
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  f32x4 oacc[2][NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+    const int key = lg * 4 + (l16 >> 2), dim = dt * 16 + 4 * (l16 & 3);
+    lds_s16x4* p0 = (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&Vs[wave][key][dim];
+    lds_s16x4* p1 = (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&Vs[wave][key + 16][dim];
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p0);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p1);
+    const s16x8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    const bf16x8 vf = __builtin_bit_cast(bf16x8, v8);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) oacc[t][dt] = mfma16(vf, pf[t], f32x4{0.f, 0.f, 0.f, 0.f});
+  }
+
+  // ---- phase 3: merge the waves' blocks in wave order
+  __syncthreads();   // every V read is done: the partial outputs reuse the buffer
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int q = t * 16 + l16;
+    if (lg == 0) { s_m[wave][q] = mw[t]; s_l[wave][q] = lw[t]; }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<f32x4*>(&So[wave][q][dt * 16 + lg * 4]) = oacc[t][dt];
+  }
+  __syncthreads();
+  for (int idx = tid; idx < Sq * (DVW / 4); idx += NT) {
+    const int q = idx / (DVW / 4), d0 = (idx % (DVW / 4)) * 4;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_m[w][q]);
+    float L = 0.f;
+    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float sw = __builtin_amdgcn_exp2f(s_m[w][q] - mx);   // an empty block: -inf -> 0
+        L += s_l[w][q] * sw;
+        o += *reinterpret_cast<const f32x4*>(&So[w][q][d0]) * sw;
+      }
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    bf16x4 ov;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ov[e] = to_bf(o[e] * inv);
+    *reinterpret_cast<bf16x4*>(a.o + b * a.o_bs + q * a.o_rs + h * a.o_hs + dv0 + d0) = ov;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // attn_cross_kernel: 32 or fewer queries over a long key sequence in one segment, no mask (the
 // action tokens over the context).  Grid (batch*head, key split), 4 waves.  The workgroup's
 // threads normalise the head's queries once into LDS (QN: RMSNorm from the producer's sums of
@@ -1233,6 +1457,25 @@ static void launch_short_q(const AttnArgs& a, int64_t nkb, dim3 grid, hipStream_
   else FAM_LAUNCH((attn_short_kernel<DH, QT, (wide ? 4 : 8)>), grid, dim3((wide ? 4 : 8) * 64), 0, s, a);
 }
 
+template <int DH, int NW, int NV>
+static void launch_small_nv(const AttnArgs& a, bool qn, dim3 grid, hipStream_t s) {
+  if (qn) FAM_LAUNCH((attn_small_kernel<DH, NW, NV, 8>), grid, dim3(NW * 64), 0, s, a);
+  else FAM_LAUNCH((attn_small_kernel<DH, NW, NV, 0>), grid, dim3(NW * 64), 0, s, a);
+}
+template <int DH, int NW>
+static void launch_small_nw(const AttnArgs& a, bool qn, int64_t bh, hipStream_t s) {
+  // a head over 4 CUs (four output-dim quarters) while that keeps the grid within one round
+  if (bh <= 64) launch_small_nv<DH, NW, 4>(a, qn, dim3((unsigned)bh, 4), s);
+  else launch_small_nv<DH, NW, 1>(a, qn, dim3((unsigned)bh, 1), s);
+}
+template <int DH>
+static void launch_small(const AttnArgs& a, int nw, bool qn, int64_t bh, hipStream_t s) {
+  if (nw <= 2) launch_small_nw<DH, 2>(a, qn, bh, s);
+  else if (nw <= 4) launch_small_nw<DH, 4>(a, qn, bh, s);
+  else if (nw <= 6) launch_small_nw<DH, 6>(a, qn, bh, s);
+  else launch_small_nw<DH, 8>(a, qn, bh, s);
+}
+
 template <int DH>
 static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
   if constexpr (DH == 64 || DH == 128) {
@@ -1245,6 +1488,14 @@ static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
     }
   }
   if constexpr (DH == 64 || DH == 128) {
+    // up to 32 queries over up to 256 keys in one workgroup per head (no key splits): the MoT
+    // joint attention over [video K/V ; action K/V], a short context
+    if (a.Sq <= 32 && a.Sk >= 1 && a.Sk <= 256 && a.splits == 1 && a.kss == nullptr &&
+        (a.qss == nullptr || a.nwidth <= 4096)) {
+      const int nw = (int)((a.Sk + KB - 1) / KB);
+      launch_small<DH>(a, nw, a.qss != nullptr, bh, s);
+      return;
+    }
     // up to 32 queries over one long unmasked key segment (the context)
     if (a.Sq <= 32 && a.sk0 == a.Sk && a.mask_kind == FAM_MASK_NONE && a.kss == nullptr) {
       const dim3 grid((unsigned)bh, (unsigned)a.splits);

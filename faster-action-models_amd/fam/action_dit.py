@@ -182,11 +182,15 @@ class FusedActionDiT:
             are given per call through `set_video_kv`.
         video_mask: optional bool [S, Sv + S], the action rows of the joint mask
             (FB/fastwam.py:388-410; True = attend); None = every key.
+        video_kv: optional per-layer [(k, v)] device views [B, Sv, A] (bf16, unit last-dim
+            stride, any row / batch stride) that the joint attention reads in place, e.g. the
+            video prefill's cache (FusedVideoPrefill.kv_cache()); then no static copy exists and
+            set_video_kv is not needed.  The views must stay valid while this model runs.
     """
 
     def __init__(self, cfg: ActionDiTConfig, params: Dict[str, torch.Tensor], *, batch: int, seq_len: int,
                  ctx_len: int, num_steps: int, shift: float = 5.0, device="cuda", mode: str = "denoise",
-                 video_len: int = 0, video_mask: Optional[torch.Tensor] = None):
+                 video_len: int = 0, video_mask: Optional[torch.Tensor] = None, video_kv=None):
         if mode not in ("denoise", "forward"):
             raise ValueError(f"mode must be 'denoise' or 'forward', got {mode!r}")
         if mode == "forward" and num_steps != 1:
@@ -268,9 +272,21 @@ class FusedActionDiT:
         self.h = z(M, H)   # normalised input of the next projection
         # MoT: per-layer cached video K/V [L, B, Sv, A] and the action rows of the joint mask
         self.Sv = int(video_len)
+        self.video_kv = None
         if self.Sv > 0:
-            self.video_k = z(L, batch, self.Sv, A)
-            self.video_v = z(L, batch, self.Sv, A)
+            if video_kv is not None:
+                if len(video_kv) != L:
+                    raise ValueError(f"video_kv needs one (k, v) per layer ({L}), got {len(video_kv)}")
+                for k_, v_ in video_kv:
+                    for t_ in (k_, v_):
+                        if (t_.dtype != _BF16 or t_.device != dev or tuple(t_.shape) != (batch, self.Sv, A)
+                                or t_.stride(-1) != 1 or t_.stride(1) % 8 or t_.stride(0) % 8 or t_.data_ptr() % 16):
+                            raise ValueError(f"video_kv entries must be bf16 [{batch}, {self.Sv}, {A}] views on "
+                                             f"{dev} with unit last-dim stride and 16-byte aligned rows")
+                self.video_kv = [(k_, v_) for k_, v_ in video_kv]
+            else:
+                self.video_k = z(L, batch, self.Sv, A)
+                self.video_v = z(L, batch, self.Sv, A)
             self.video_mask = None
             if video_mask is not None:
                 vm = video_mask.to(device=dev, dtype=torch.bool).contiguous()
@@ -287,7 +303,8 @@ class FusedActionDiT:
             part_need = max(part_need, self._part_splits(M, n_, k_) * M * n_)
         self.part = torch.zeros(part_need, dtype=torch.float32, device=dev)
         # key-split partials of the cross-attention: ~4 blocks of 32 keys per workgroup
-        self.kv_splits = max(1, min(64, -(-ctx_len // 128)))
+        # (up to 256 context tokens one workgroup per head takes every key: no splits, no combine)
+        self.kv_splits = 1 if ctx_len <= 256 else max(1, min(64, -(-ctx_len // 128)))
         nq = batch * cfg.num_heads * seq_len
         self.apart_o = torch.zeros(self.kv_splits * nq * cfg.attn_head_dim, dtype=torch.float32, device=dev)
         self.apart_ml = torch.zeros(self.kv_splits * nq * 2, dtype=torch.float32, device=dev)
@@ -468,9 +485,9 @@ class FusedActionDiT:
         qkvp = self.qkv.data_ptr()
         d = _capi.AttnDesc()
         d.q, d.q_bs, d.q_rs, d.q_hs = qkvp, S * 3 * A, 3 * A, Dh
-        vk, vv = self.video_k[l], self.video_v[l]
-        d.k0, d.k0_bs, d.k0_rs, d.k0_hs = vk.data_ptr(), Sv * A, A, Dh
-        d.v0, d.v0_bs, d.v0_rs, d.v0_hs = vv.data_ptr(), Sv * A, A, Dh
+        vk, vv = self.video_kv[l] if self.video_kv is not None else (self.video_k[l], self.video_v[l])
+        d.k0, d.k0_bs, d.k0_rs, d.k0_hs = vk.data_ptr(), vk.stride(0), vk.stride(1), Dh
+        d.v0, d.v0_bs, d.v0_rs, d.v0_hs = vv.data_ptr(), vv.stride(0), vv.stride(1), Dh
         d.k1, d.k1_bs, d.k1_rs, d.k1_hs = qkvp + 2 * A, S * 3 * A, 3 * A, Dh
         d.v1, d.v1_bs, d.v1_rs, d.v1_hs = qkvp + 4 * A, S * 3 * A, 3 * A, Dh
         d.o, d.o_bs, d.o_rs, d.o_hs = out.data_ptr(), S * A, A, Dh
@@ -490,6 +507,8 @@ class FusedActionDiT:
         and rotated as the video expert's prefill leaves them) into the static buffers."""
         if self.Sv == 0:
             raise ValueError("this model was built without a video prefix (video_len=0)")
+        if self.video_kv is not None:
+            raise ValueError("this model reads its video K/V in place (video_kv); there is no static copy")
         for l, (k, v) in enumerate(zip(keys, values)):
             self.video_k[l].copy_(k.reshape(self.video_k[l].shape) if k.dim() == 3 else k.expand_as(self.video_k[l]))
             self.video_v[l].copy_(v.reshape(self.video_v[l].shape) if v.dim() == 3 else v.expand_as(self.video_v[l]))
@@ -532,6 +551,9 @@ class FusedActionDiT:
         # M <= 64 rows, Sq <= 32 and an RMS width the on-load normaliser supports: q/k projections
         # are single kernels and their norms run inside the attention kernels
         fused_qk = M <= 64 and S <= 32 and A % 1024 == 0 and Dh in (64, 128) and self.Sv == 0
+        # the cross-attention query alone (also in MoT mode): raw projection + sums of squares,
+        # normalised as the attention loads it (the short-context kernel takes widths <= 4096)
+        fused_q = M <= 64 and S <= 32 and A % 1024 == 0 and Dh in (64, 128) and (Lc > 256 or A <= 4096)
 
         def mod(t, l, i):   # chunk i of (modulation + t_mod) of block l at step t: [H]
             return self.mods[t, l, i * H:(i + 1) * H]
@@ -565,7 +587,7 @@ class FusedActionDiT:
                 self._rowop(tag + ".o_row", N=H, splits=sp, bias=w[f"sa_o_b{l}"], res=x, gate=mod(t, l, 2), out=x,
                             norm=LN, ln_w=w[f"n3_w{l}"], ln_b=w[f"n3_b{l}"], nout=h)
                 kb = kvp + 2 * (l * 2 * A)
-                if fused_qk:
+                if fused_q:
                     # raw cross-attention query; its RMSNorm happens as the attention loads it
                     self._gemm_final(tag + ".cross_q", h, w[f"ca_q_w{l}"], w[f"ca_q_b{l}"], qc, sumsq=self.ss_q)
                     self._attn(tag + ".cross_attn", qc.data_ptr(), S * A, A, kb, 0, L * 2 * A, kb + 2 * A, 0,
