@@ -482,7 +482,8 @@ __global__ __launch_bounds__(256) void partial_kernel(PartArgs g) {
 }
 
 // ---------------------------------------------------------------------------------------
-// partial_wide_kernel (64 < M <= 128: the video prefill's 98-token projections): the same
+// partial_wide_kernel (64 < M <= 128: the video prefill's 98-token projections; M <= 64 with
+// two strips for the large action projections, see partial_plan): the same
 // split-K partials, but a workgroup of NWV waves owns 16 NWV output columns (16 per wave)
 // over one K slice of 512, and the slice of every activation row is staged once in LDS with
 // direct global->LDS loads (one 1 KB row per wave instruction: lane j lands at the row start
@@ -1279,6 +1280,18 @@ static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* split
   while (st > 1 && ((ksteps + 4 * st - 1) / (4 * st)) * groups < 256) st >>= 1;
   *steps = st;
   *splits = (int)((ksteps + 4 * st - 1) / (4 * st));
+  if (M <= 64) {
+    // two 16-column strips per workgroup sharing one LDS-staged 512-wide activation slice
+    // halve the activation re-reads of the register kernel's one-strip workgroups; measured
+    // faster at M = 32 once that still fills >= 192 workgroups (9216 x 1024: 10.5 -> 6.8 us;
+    // 1024 x 3072: 5.1 -> 4.3 us), taken unless it multiplies the partial planes the row
+    // kernel sums by more than 1.5
+    const int64_t wsp = (K + 511) / 512, wblk = (N + 31) / 32;
+    if (wblk * wsp >= 192 && wsp <= std::max((int64_t)2, (int64_t)(*splits) * 3 / 2)) {
+      *steps = 0;
+      *splits = (int)wsp;
+    }
+  }
 }
 
 // Above 128 rows (<= 144) only the streaming plan runs; 0 when it does not apply.
@@ -1316,6 +1329,13 @@ static int wide_cus() {
   return cus;
 }
 static void launch_partial_wide(const PartArgs& a, int splits, hipStream_t s) {
+  if (a.M <= 64) {   // two strips per workgroup (partial_plan)
+    const dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)splits);
+    if (a.M <= 16) FAM_LAUNCH((partial_wide_kernel<1, 2>), grid, dim3(128), 0, s, a);
+    else if (a.M <= 32) FAM_LAUNCH((partial_wide_kernel<2, 2>), grid, dim3(128), 0, s, a);
+    else FAM_LAUNCH((partial_wide_kernel<4, 2>), grid, dim3(128), 0, s, a);
+    return;
+  }
   const int64_t cus = wide_cus();
   int best = 4;
   int64_t best_cost = -1;

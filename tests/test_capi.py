@@ -119,9 +119,12 @@ def test_validation_rejects_before_launch(lib):
     assert lib.fam_gemm_partial_splits(129, 178176, 3072) == 1
     assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 4, 64, 60, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_gemm_partial(16, 64, 32, 64, 52, 4, 64, 64, None) == _capi.FAM_ERR_INVALID_ARG
-    # the split plan of the action projections: >= 256 workgroups of 16 columns, fewest planes
+    # the split plan of the action projections: >= 256 workgroups of 16 columns, fewest planes;
+    # two-strip workgroups over 512-wide slices where they fill >= 192 workgroups without 1.5x
+    # the planes (4096 x 1024, the real model's 9216 x 1024 q|k|v and 1024 x 3072 o)
     assert [lib.fam_gemm_partial_splits(32, n, k) for n, k in ((3072, 1024), (1024, 1024), (4096, 1024),
-                                                              (1024, 4096), (7, 1024))] == [2, 4, 1, 4, 8]
+                                                              (1024, 4096), (7, 1024), (9216, 1024),
+                                                              (1024, 3072))] == [2, 4, 2, 4, 8, 2, 6]
     assert lib.fam_gemm_partial_splits(0, 64, 64) == 0
     # the video prefill's 98-row projections: the streaming kernel (one round of 128-column
     # workgroups, whole 256-wide chunks per split) for FFN down / FFN up / q|k|v, 64-column

@@ -461,7 +461,9 @@ def test_sinusoid_and_modulation():
                                     (64, 4096, 1024), (17, 2048, 1000), (33, 96, 64), (98, 3072, 3072),
                                     (98, 3072, 14336), (128, 4090, 3000), (65, 1000, 1024), (100, 4096, 520),
                                     (98, 14336, 3072), (128, 9216, 3072), (77, 6004, 4104), (77, 4094, 4104),
-                                    (98, 3000, 3072), (128, 3072, 3080), (129, 12288, 3072), (140, 20000, 1600)])
+                                    (98, 3000, 3072), (128, 3072, 3080), (129, 12288, 3072), (140, 20000, 1600),
+                                    (32, 9216, 1024), (32, 1024, 3072), (16, 6000, 1000), (64, 4100, 1048),
+                                    (40, 2048, 2056), (16, 4002, 1000)])
 def test_gemm_partial_rowop(M, N, K):
     """Split-K partials summed in split order by the row kernel = linear; bit-identical reruns.
     Above 64 rows: the streaming kernel where a one-round grid gives every workgroup >= 3
@@ -472,7 +474,10 @@ def test_gemm_partial_rowop(M, N, K):
     m-tiles for 129-144 rows, ragged and with a K tail at (140, 20000, 1600)), the
     wide kernel (a
     512-wide K slice per workgroup, activations staged in LDS) and the 8-m-tile register
-    kernel where neither fills the chip."""
+    kernel where neither fills the chip.  At <= 64 rows the wide kernel with two strips per
+    workgroup for the large action projections (the real model's 9216 x 1024 q|k|v and
+    1024 x 3072 o), with 1, 2 and 4 m-tiles, rows past M in a tile, ragged N (also N % 4 != 0)
+    and K tails."""
     x, w, b = rnd(M, K, seed=70), rnd(N, K, seed=71, scale=0.02), rnd(N, seed=72, scale=0.02)
     ref = O.linear(x.float(), w.float(), b.float())
     xd, wd, bd = dev(x), dev(w), dev(b)
