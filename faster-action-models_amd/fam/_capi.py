@@ -136,6 +136,9 @@ SIGNATURES = {
     "fam_euler_step": (C.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "fam_sinusoid": (C.c_int, [_vp, _vp, _i64, _i64, _vp]),
     "fam_add_modulation": (C.c_int, [_vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "fam_patchify": (C.c_int, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "fam_unpatchify": (C.c_int, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
+    "fam_gather_rows": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp]),
 }
 
 _lib = None

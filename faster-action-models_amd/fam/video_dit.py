@@ -160,9 +160,12 @@ class FusedVideoDiTBlock:
             if tuple(self_mask.shape) != (seq_len, seq_len):
                 raise ValueError(f"self_mask must be bool [S, S] = [{seq_len}, {seq_len}]")
         if ctx_mask is not None:
+            # [B, S, Lc], or [B, Lc] shared by every query of a sample (read in place: a caller
+            # may update it between calls)
             ctx_mask = ctx_mask.to(device=dev, dtype=torch.bool).contiguous()
-            if tuple(ctx_mask.shape) != (batch, seq_len, ctx_len):
-                raise ValueError(f"ctx_mask must be bool [B, S, Lc] = [{batch}, {seq_len}, {ctx_len}]")
+            if tuple(ctx_mask.shape) not in ((batch, seq_len, ctx_len), (batch, ctx_len)):
+                raise ValueError(f"ctx_mask must be bool [B, S, Lc] = [{batch}, {seq_len}, {ctx_len}] or "
+                                 f"[B, Lc] = [{batch}, {ctx_len}]")
         self.self_mask, self.ctx_mask = self_mask, ctx_mask
         self._descs: List = []
         self.steps: List = []
@@ -376,8 +379,9 @@ class FusedVideoDiTBlock:
             else:
                 buf, col = self.ctx_kv
                 kp, kld = buf.data_ptr() + 2 * col, buf.stride(0)
+            cms = (S * Lc, 0, Lc) if self.ctx_mask is None or self.ctx_mask.dim() == 3 else (Lc, 0, 0)
             self._attention("cross_attn", self.qc.data_ptr(), A, kp, kld, kp + 2 * A, kld, S, Lc, Lc,
-                            mask=self.ctx_mask, mask_strides=(S * Lc, 0, Lc))
+                            mask=self.ctx_mask, mask_strides=cms)
             self._proj("cross_o", self.attn, w["co_w"], w["co_b"], self.x, res=self.x, adaln=(mod(3), mod(4)),
                        nout=self.h)
         # FFN (its AdaLN came with the last projection's row)
@@ -446,15 +450,19 @@ class FusedVideoPrefill:
     past `num_run` reuse that block's K/V (video layer drafting, FB/mot.py:345-351).
 
     Args: as FusedVideoDiTBlock, plus num_layers (the expert's depth), video_mask bool [Sv, Sv]
-    (None: every key), ctx_mask bool [B, Sv, Lc] (None: every context token), ctx_len 0 for a
-    prefill without a context payload.
+    (None: every key), ctx_mask bool [B, Sv, Lc] or [B, Lc] (None: every context token), ctx_len
+    0 for a prefill without a context payload.  keep_output: every block runs in full, so that
+    after `run()` the shared "x" holds the last block's output (the block stack of
+    WanVideoDiT.forward, FB/wan_video_dit.py:667-682) besides the K/V cache.
     """
 
     def __init__(self, params: Dict[str, torch.Tensor], *, num_layers: int, hidden: int, num_heads: int,
                  head_dim: int, ffn_dim: int, batch: int, video_len: int, ctx_len: int, freqs: torch.Tensor,
                  eps: float = 1e-6, per_token_mod: bool = True, video_mask: Optional[torch.Tensor] = None,
-                 ctx_mask: Optional[torch.Tensor] = None, num_run: int = 0, device="cuda"):
+                 ctx_mask: Optional[torch.Tensor] = None, num_run: int = 0, device="cuda",
+                 keep_output: bool = False):
         dev = torch.device(device)
+        self.keep_output = keep_output
         self.L = num_layers
         self.n_run = num_layers if num_run <= 0 or num_run > num_layers else num_run
         self.B, self.S, self.Lc, self.H, self.A = batch, video_len, ctx_len, hidden, num_heads * head_dim
@@ -472,7 +480,8 @@ class FusedVideoPrefill:
             self.shared["part"] = torch.zeros(need, dtype=torch.float32, device=dev)
         # the context K/V of every block that cross-attends, in one GEMM per call: the context
         # does not change between blocks, only the weights do
-        ncross = self.n_run - 1 if ctx_len > 0 else 0     # the last block run builds only its K/V
+        # (without keep_output the last block run builds only its K/V)
+        ncross = (self.n_run if keep_output else self.n_run - 1) if ctx_len > 0 else 0
         self.steps, self.meta, self._descs = [], [], []
         if ncross > 0:
             def cat(names):
@@ -504,7 +513,7 @@ class FusedVideoPrefill:
                                           freqs=freqs, eps=eps, per_token_mod=per_token_mod, device=dev,
                                           self_mask=video_mask, ctx_mask=ctx_mask,
                                           shared={**self.shared, "mods": mods(i)},
-                                          kv_only=(i == self.n_run - 1),
+                                          kv_only=(i == self.n_run - 1 and not keep_output),
                                           ctx_kv=(self.ctxkv, i * 2 * self.A) if i < ncross else None,
                                           mods_ready=chain, pre_normed=chain and i > 0,
                                           next_mod=mods(i + 1) if chain and i + 1 < self.n_run else None)
@@ -606,3 +615,220 @@ class FusedVideoPrefill:
         self.set_inputs(x, t_mod, context)
         self.run()
         return self.kv_cache()
+
+
+class FusedWanVideoDiT:
+    """WanVideoDiT (FB/wan_video_dit.py:328-684) of the video expert on the library for a fixed
+    call shape: latents [B, in_dim, F, Hl, Wl], one timestep per sample, Lc context tokens.
+
+    pre_dit (:527-648, seperated_timestep with the VAE embedding fused in the latents):
+        patches = patch gather of the latents                      fam_patchify
+        tokens  = patches conv_w^T + conv_b                        fam_gemm
+        t, t_mod of the two distinct token timesteps per sample (the first latent frame at 0,
+            the others at the sample's timestep): sinusoid -> Linear, SiLU, Linear -> SiLU,
+            Linear, each row computed once      fam_sinusoid, fam_gemm (SiLU epilogues)
+        per-token t_mod (and t for the head) by row gather       fam_gather_rows
+        context = Linear(GELU(Linear(text)))                      fam_gemm (GELU epilogue)
+    blocks: the chain of FusedVideoPrefill (keep_output with mode "forward"), reading the
+        tokens, the per-token t_mod and the embedded context in place; the context mask [B, Lc]
+        is broadcast over the tokens inside the attention.
+    post_dit (mode "forward", :650-654, Head :309-325):
+        shift, scale = head.modulation + t (per token)           fam_add_modulation
+        y = Linear(LN(x) (1 + scale) + shift)                     fam_adaln, fam_gemm
+        out = unpatchify(y)                                       fam_unpatchify
+
+    mode "prefill" stops after the blocks and exposes their K/V (`kv_cache()`): the video half of
+    FastWAM.infer_action (FB/fastwam.py:1018-1041), whose first latent frame runs at t = 0.
+    video_mask: bool [S, S] on the self-attention (None: every key).
+    """
+
+    def __init__(self, cfg, params: Dict[str, torch.Tensor], *, batch: int, frames: int, height: int, width: int,
+                 ctx_len: int, video_mask: Optional[torch.Tensor] = None, mode: str = "forward", device="cuda"):
+        if mode not in ("forward", "prefill"):
+            raise ValueError(f"mode must be 'forward' or 'prefill', got {mode!r}")
+        dev = torch.device(device)
+        self.mode, self.cfg, self.device = mode, cfg, dev
+        pt, ph, pw = cfg.patch_size
+        if frames % pt or height % ph or width % pw:
+            raise ValueError(f"latent shape ({frames}, {height}, {width}) not divisible by the patch {cfg.patch_size}")
+        f, h, w = frames // pt, height // ph, width // pw
+        self.grid, self.tpf = (f, h, w), h * w
+        B, H, C, Lc = batch, cfg.hidden_dim, cfg.in_dim, ctx_len
+        S = f * h * w
+        P = pt * ph * pw
+        self.B, self.S, self.Lc = B, S, Lc
+        self.lib = lib = _capi.load()
+        z = lambda *s: torch.zeros(*s, dtype=_BF16, device=dev)  # noqa: E731
+
+        def Pm(n):
+            if n not in params:
+                raise KeyError(f"missing parameter {n}")
+            return params[n].to(device=dev, dtype=_BF16).contiguous()
+        self.w = w_ = {
+            "patch_w": Pm("patch_embedding.weight").reshape(H, C * P).contiguous(), "patch_b": Pm("patch_embedding.bias"),
+            "te0_w": Pm("time_embedding.0.weight"), "te0_b": Pm("time_embedding.0.bias"),
+            "te2_w": Pm("time_embedding.2.weight"), "te2_b": Pm("time_embedding.2.bias"),
+            "tp_w": Pm("time_projection.1.weight"), "tp_b": Pm("time_projection.1.bias"),
+            "txt0_w": Pm("text_embedding.0.weight"), "txt0_b": Pm("text_embedding.0.bias"),
+            "txt2_w": Pm("text_embedding.2.weight"), "txt2_b": Pm("text_embedding.2.bias"),
+        }
+        if mode == "forward":
+            w_["head_w"], w_["head_b"] = Pm("head.head.weight"), Pm("head.head.bias")
+            w_["head_mod"] = Pm("head.modulation").reshape(2, H).contiguous()
+
+        # inputs (static, for graph replay)
+        self.x_in = z(B, C, frames, height, width)
+        self.ts_in = z(B)
+        self.ts2 = z(2 * B)                       # (0, t_b) per sample: the distinct token timesteps
+        self.ctx_in = z(B * Lc, cfg.text_dim)
+        self.cmask = torch.ones(B, Lc, dtype=torch.bool, device=dev)
+        # token -> distinct-row index: sample b, frame 0 -> 2b, later frames -> 2b + 1
+        tok = torch.arange(S)
+        idx = (2 * torch.arange(B)[:, None] + (tok[None, :] >= self.tpf).long()).reshape(-1)
+        self.row_idx = idx.to(device=dev, dtype=torch.int32).contiguous()
+
+        freqs = video_freqs_3d(cfg.attn_head_dim, f, h, w)
+        self.freqs = freqs
+        self.blocks = FusedVideoPrefill(params, num_layers=cfg.num_layers, hidden=H, num_heads=cfg.num_heads,
+                                        head_dim=cfg.attn_head_dim, ffn_dim=cfg.ffn_dim, batch=B, video_len=S,
+                                        ctx_len=Lc, freqs=freqs, eps=cfg.eps, video_mask=video_mask,
+                                        ctx_mask=self.cmask if Lc > 0 else None, device=dev,
+                                        keep_output=(mode == "forward"))
+        sh = self.blocks.shared
+        self.patches = z(B * S, C * P)
+        self.emb = z(2 * B, cfg.freq_dim)
+        self.t1 = z(2 * B, H)
+        self.t2s = z(2 * B, H)                    # SiLU(t) of the distinct rows
+        self.tmod2 = z(2 * B, 6 * H)
+        self.ctx_h = z(B * Lc, H)
+        self.steps: List = []
+        self.meta: List[dict] = []
+        self._descs: List = []
+        add = self._add
+        add("patchify", "fam_patchify", (self.x_in.data_ptr(), B, C, frames, height, width, pt, ph, pw,
+                                         self.patches.data_ptr()), "patchify", 4 * self.x_in.numel())
+        self._gemm("patch_embed", self.patches, w_["patch_w"], w_["patch_b"], sh["x"])
+        add("sinusoid", "fam_sinusoid", (self.ts2.data_ptr(), self.emb.data_ptr(), 2 * B, cfg.freq_dim), "sinusoid")
+        self._gemm("time_emb0", self.emb, w_["te0_w"], w_["te0_b"], self.t1, act=_capi.FAM_ACT_SILU)
+        self._gemm("time_emb2_silu", self.t1, w_["te2_w"], w_["te2_b"], self.t2s, act=_capi.FAM_ACT_SILU)
+        self._gemm("time_proj", self.t2s, w_["tp_w"], w_["tp_b"], self.tmod2)
+        add("tmod_tokens", "fam_gather_rows", (self.tmod2.data_ptr(), 6 * H, 2 * B, self.row_idx.data_ptr(),
+                                               sh["tmod_in"].data_ptr(), 6 * H, B * S, 6 * H), "gather")
+        if mode == "forward":
+            self.t2 = z(2 * B, H)
+            self.t_tok = z(B * S, H)
+            self._gemm("time_emb2", self.t1, w_["te2_w"], w_["te2_b"], self.t2)
+            add("t_tokens", "fam_gather_rows", (self.t2.data_ptr(), H, 2 * B, self.row_idx.data_ptr(),
+                                                self.t_tok.data_ptr(), H, B * S, H), "gather")
+        if Lc > 0:
+            self._gemm("text_emb0", self.ctx_in, w_["txt0_w"], w_["txt0_b"], self.ctx_h, act=_capi.FAM_ACT_GELU_TANH)
+            self._gemm("text_emb2", self.ctx_h, w_["txt2_w"], w_["txt2_b"], sh["ctx"])
+        self.steps += self.blocks.steps
+        self.meta += self.blocks.meta
+        if mode == "forward":
+            self.head_mod = z(B * S, 2, H)
+            self.hn = z(B * S, H)
+            self.head_out = z(B * S, cfg.out_dim * P)
+            self.out = z(B, cfg.out_dim, frames, height, width)
+            add("head_modulation", "fam_add_modulation", (self.t_tok.data_ptr(), w_["head_mod"].data_ptr(),
+                                                          self.head_mod.data_ptr(), B * S, 2, H), "modulation")
+            hm = self.head_mod.data_ptr()
+            add("head_adaln", "fam_adaln", (sh["x"].data_ptr(), H, hm, hm + 2 * H, 0, 2 * H, None, None,
+                                            self.hn.data_ptr(), H, B * S, B * S, H, float(cfg.eps)), "adaln")
+            self._gemm("head", self.hn, w_["head_w"], w_["head_b"], self.head_out)
+            add("unpatchify", "fam_unpatchify", (self.head_out.data_ptr(), B, cfg.out_dim, f, h, w, pt, ph, pw,
+                                                 self.out.data_ptr()), "patchify", 4 * self.out.numel())
+        self.graph: Optional[torch.cuda.CUDAGraph] = None
+
+    # ------------------------------------------------------------------ plan building
+    def _add(self, name, fname, args, kind, nbytes=0):
+        f, lib = getattr(self.lib, fname), self.lib
+
+        def run(stream):
+            rc = f(*args, stream)
+            if rc != 0:
+                raise _capi.FamError(f"{fname}[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
+        self.steps.append(run)
+        self.meta.append({"name": name, "kernel": kind, "bytes": int(nbytes)})
+
+    def _gemm(self, name, a, w, bias, out, act=_capi.FAM_ACT_NONE):
+        d = _capi.GemmDesc()
+        d.a, d.lda, d.w, d.ldw = a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0)
+        d.bias = bias.data_ptr() if bias is not None else None
+        d.out, d.ldo = out.data_ptr(), out.stride(0)
+        d.M, d.N, d.K = a.shape[0], w.shape[0], w.shape[1]
+        d.act = act
+        d.rows_per_batch = max(a.shape[0], 1)
+        self._descs.append(d)
+        self._add(name, "fam_gemm", (C.byref(d),), "gemm", 2 * (a.numel() + w.numel() + out.numel()))
+
+    # ------------------------------------------------------------------ execution
+    def set_inputs(self, latents: torch.Tensor, timestep: torch.Tensor, context: Optional[torch.Tensor] = None,
+                   context_mask: Optional[torch.Tensor] = None) -> None:
+        """latents [B, in_dim, F, Hl, Wl]; timestep [B] or [1]; context [B, Lc, text_dim];
+        context_mask bool [B, Lc] (None: every token), all copied into the static buffers."""
+        self.x_in.copy_(latents.reshape(self.x_in.shape))
+        t = timestep.reshape(-1).to(device=self.device, dtype=_BF16)
+        self.ts_in.copy_(t.expand(self.B) if t.numel() == 1 else t)
+        ts2 = self.ts2.view(self.B, 2)
+        ts2[:, 0].zero_()
+        ts2[:, 1].copy_(self.ts_in if self.grid[0] > 1 else torch.zeros_like(self.ts_in))
+        if self.Lc > 0:
+            self.ctx_in.copy_(context.reshape(self.ctx_in.shape))
+            if context_mask is None:
+                self.cmask.fill_(True)
+            else:
+                self.cmask.copy_(context_mask.reshape(self.cmask.shape))
+
+    def run(self) -> None:
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            s = torch.cuda.current_stream(self.device).cuda_stream
+            for f in self.steps:
+                f(s)
+
+    def capture(self) -> None:
+        s = torch.cuda.Stream(self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            for f in self.steps:
+                f(s.cuda_stream)
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            st = torch.cuda.current_stream(self.device).cuda_stream
+            for f in self.steps:
+                f(st)
+        self.graph = g
+
+    def forward(self, latents, timestep, context=None, context_mask=None) -> torch.Tensor:
+        """WanVideoDiT.forward: the predicted latents [B, out_dim, F, Hl, Wl] (a copy)."""
+        if self.mode != "forward":
+            raise RuntimeError("forward() needs mode='forward'")
+        self.set_inputs(latents, timestep, context, context_mask)
+        self.run()
+        return self.out.clone()
+
+    def prefill(self, latents, timestep, context=None, context_mask=None):
+        """pre_dit + every block's K/V: [(k, v)] per layer, [B, S, A] views valid until the next run."""
+        self.set_inputs(latents, timestep, context, context_mask)
+        self.run()
+        return self.kv_cache()
+
+    def kv_cache(self):
+        return self.blocks.kv_cache()
+
+    def pre_state(self):
+        """The pre_dit outputs in the reference's layout (FB/wan_video_dit.py:642-648): tokens
+        [B, S, H] (before the blocks ran), t_mod [B, S, 6, H], context [B, Lc, H], freqs."""
+        sh = self.blocks.shared
+        H = self.cfg.hidden_dim
+        return {"tokens": sh["x"].view(self.B, self.S, H), "t_mod": sh["tmod_in"].view(self.B, self.S, 6, H),
+                "context": sh["ctx"].view(self.B, self.Lc, H), "freqs": self.freqs,
+                "t": self.t_tok.view(self.B, self.S, H) if self.mode == "forward" else None}
+
+    @property
+    def num_launches(self) -> int:
+        return len(self.steps)

@@ -370,6 +370,38 @@ int fam_euler_step(const void* sample, const void* model_output, const void* del
 int fam_sinusoid(const void* positions, void* out, int64_t T, int64_t dim, void* stream);
 
 /*
+ * fam_patchify -- the patch gather in front of the patch-embedding GEMM: x [B, C, F, H, W]
+ * (contiguous bf16) into rows out[b*S + (fi*h + hi)*w + wi, ((c*pt + kt)*ph + kh)*pw + kw] =
+ * x[b, c, fi*pt + kt, hi*ph + kh, wi*pw + kw], S = f*h*w tokens (f = F/pt, h = H/ph, w = W/pw),
+ * so that rows x conv_weight.reshape(hidden, -1)^T + bias is the strided Conv3d.
+ * Replaces: WanVideoDiT.patchify (nn.Conv3d(in_dim, dim, kernel = stride = patch_size))
+ *           FB/wan_video_dit.py:385-386, 420-426.
+ * Limits: F, H, W divisible by the patch; B*C*F*H*W < 2^38.
+ */
+int fam_patchify(const void* x, int64_t B, int64_t C, int64_t F, int64_t H, int64_t W, int64_t pt, int64_t ph,
+                 int64_t pw, void* out, void* stream);
+
+/*
+ * fam_unpatchify -- the inverse layout after the head GEMM: y [B*S, pt*ph*pw*C] with the
+ * features ordered (kt, kh, kw, c) into out [B, C, f*pt, h*ph, w*pw] (contiguous bf16),
+ * rearrange 'b (f h w) (x y z c) -> b c (f x) (h y) (w z)'.
+ * Replaces: WanVideoDiT.unpatchify FB/wan_video_dit.py:428-433.
+ */
+int fam_unpatchify(const void* y, int64_t B, int64_t C, int64_t f, int64_t h, int64_t w, int64_t pt, int64_t ph,
+                   int64_t pw, void* out, void* stream);
+
+/*
+ * fam_gather_rows -- dst[r, :] = src[idx[r], :] for r < rows, cols bf16 elements per row;
+ * idx int32 in device memory, clamped into [0, src_rows).  Broadcasts the time embedding and
+ * t_mod of the few distinct per-frame timesteps to every token.
+ * Replaces: the per-token time_embedding / time_projection rows of WanVideoDiT.pre_dit
+ *           (FB/wan_video_dit.py:555-568), computed once per distinct timestep.
+ * Limits: cols % 8 == 0; strides multiples of 8; 16-byte aligned.
+ */
+int fam_gather_rows(const void* src, int64_t ld_src, int64_t src_rows, const int32_t* idx, void* dst,
+                    int64_t ld_dst, int64_t rows, int64_t cols, void* stream);
+
+/*
  * fam_add_modulation -- out[t, l, :] = bf16(modulation[l, :] + t_mod[t, :]) for every
  * denoise step t < T and block l < L, vectors of length n (= 6 * hidden): the
  * `modulation + t_mod` of every block (FB/wan_video_dit.py:273-274, FB/mot.py:63-80).

@@ -546,6 +546,139 @@ def mot_joint_mask(video_seq_len: int, action_seq_len: int, video_tokens_per_fra
 
 
 # ---------------------------------------------------------------------------
+# WanVideoDiT: the video expert's pre_dit / post_dit around the blocks
+# ---------------------------------------------------------------------------
+@dataclass(frozen=True)
+class WanVideoConfig:
+    """Hyper-parameters of WanVideoDiT (FB/wan_video_dit.py:329-411) in the inference setting
+    the reference supports (seperated_timestep, VAE embedding fused in the latents)."""
+    hidden_dim: int = 3072
+    in_dim: int = 48
+    ffn_dim: int = 14336
+    out_dim: int = 48
+    text_dim: int = 4096
+    freq_dim: int = 256
+    eps: float = 1e-6
+    patch_size: Tuple[int, int, int] = (1, 2, 2)
+    num_heads: int = 24
+    attn_head_dim: int = 128
+    num_layers: int = 30
+
+    @property
+    def attn_dim(self) -> int:
+        return self.num_heads * self.attn_head_dim
+
+    def block_config(self) -> ActionDiTConfig:
+        """The per-block hyper-parameters in the form dit_block's callers use."""
+        return ActionDiTConfig(hidden_dim=self.hidden_dim, action_dim=1, ffn_dim=self.ffn_dim, text_dim=self.text_dim,
+                               freq_dim=self.freq_dim, eps=self.eps, num_heads=self.num_heads,
+                               attn_head_dim=self.attn_head_dim, num_layers=self.num_layers)
+
+
+def wan_param_shapes(cfg: WanVideoConfig) -> Dict[str, Tuple[int, ...]]:
+    """State-dict keys of WanVideoDiT (FB/wan_video_dit.py:385-401, Head :309-316)."""
+    H = cfg.hidden_dim
+    P = cfg.patch_size[0] * cfg.patch_size[1] * cfg.patch_size[2]
+    shapes = {k: v for k, v in action_dit_param_shapes(cfg.block_config()).items() if k.startswith("blocks.")}
+    shapes.update({
+        "patch_embedding.weight": (H, cfg.in_dim) + tuple(cfg.patch_size), "patch_embedding.bias": (H,),
+        "text_embedding.0.weight": (H, cfg.text_dim), "text_embedding.0.bias": (H,),
+        "text_embedding.2.weight": (H, H), "text_embedding.2.bias": (H,),
+        "time_embedding.0.weight": (H, cfg.freq_dim), "time_embedding.0.bias": (H,),
+        "time_embedding.2.weight": (H, H), "time_embedding.2.bias": (H,),
+        "time_projection.1.weight": (6 * H, H), "time_projection.1.bias": (6 * H,),
+        "head.head.weight": (cfg.out_dim * P, H), "head.head.bias": (cfg.out_dim * P,),
+        "head.modulation": (1, 2, H),
+    })
+    return shapes
+
+
+def init_wan_params(cfg: WanVideoConfig, seed: int, std: float = 0.02) -> Params:
+    """Seeded synthetic weights with init_action_dit_params' rules (the two modulations
+    randn/sqrt(H), norm affines N(1, 0.2) / N(0, 0.2)), sorted-name draws, fp32."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    out: Params = {}
+    for name, shape in sorted(wan_param_shapes(cfg).items()):
+        if name.endswith("modulation"):
+            out[name] = torch.randn(shape, generator=g) / math.sqrt(cfg.hidden_dim)
+        elif ".norm_q." in name or ".norm_k." in name or name.endswith("norm3.weight"):
+            out[name] = 1.0 + torch.randn(shape, generator=g) * NORM_AFFINE_STD
+        elif name.endswith("norm3.bias"):
+            out[name] = torch.randn(shape, generator=g) * NORM_AFFINE_STD
+        else:
+            out[name] = torch.randn(shape, generator=g) * std
+    return out
+
+
+def wan_patchify(p: Params, x: torch.Tensor, patch) -> torch.Tensor:
+    """nn.Conv3d(in_dim, H, kernel = stride = patch) of the latents [B, C, F, Hl, Wl] ->
+    [B, H, f, h, w] (FB/wan_video_dit.py:385-386, 420-426)."""
+    return F.conv3d(x, p["patch_embedding.weight"], p["patch_embedding.bias"], stride=tuple(patch))
+
+
+def wan_pre_dit(p: Params, cfg: WanVideoConfig, x: torch.Tensor, timestep: torch.Tensor, context: torch.Tensor,
+                context_mask: Optional[torch.Tensor] = None) -> dict:
+    """WanVideoDiT.pre_dit with seperated_timestep and the VAE embedding fused in the latents
+    (FB/wan_video_dit.py:527-648, no action conditioning): every token carries the timestep of
+    its latent frame, the first frame's being 0 (:555-568); t = time_embedding(sinusoid) per
+    token, t_mod = time_projection(t) [B, S, 6, H]; tokens = patchify(x) in (f, h, w) order;
+    context = text_embedding(context); the context mask broadcast over the tokens; the 3-D RoPE
+    table of the (f, h, w) grid (:642-646)."""
+    B = x.shape[0]
+    pt, ph, pw = cfg.patch_size
+    tpf = (x.shape[3] // ph) * (x.shape[4] // pw)
+    if timestep.shape[0] == 1 and B > 1:
+        timestep = timestep.expand(B)
+    tt = torch.ones((B, x.shape[2], tpf), dtype=timestep.dtype) * timestep.view(B, 1, 1)
+    tt[:, 0, :] = 0
+    tt = tt.reshape(B, -1)
+    emb = sinusoidal_embedding_1d(cfg.freq_dim, tt.reshape(-1))
+    t = linear(silu(linear(emb, p["time_embedding.0.weight"], p["time_embedding.0.bias"])),
+               p["time_embedding.2.weight"], p["time_embedding.2.bias"]).reshape(B, -1, cfg.hidden_dim)
+    t_mod = linear(silu(t), p["time_projection.1.weight"], p["time_projection.1.bias"]).unflatten(2, (6, cfg.hidden_dim))
+    xp = wan_patchify(p, x, cfg.patch_size)
+    f, h, w = xp.shape[2:]
+    ctx = text_embedding(p, context)
+    if context_mask is None:
+        context_mask = torch.ones((context.shape[0], context.shape[1]), dtype=torch.bool)
+    cmask = context_mask.unsqueeze(1).expand(-1, f * h * w, -1)
+    tokens = xp.flatten(2).transpose(1, 2).contiguous()
+    freqs = video_freqs(precompute_freqs_cis_3d(cfg.attn_head_dim), f, h, w)
+    return {"tokens": tokens, "freqs": freqs, "t": t, "t_mod": t_mod, "context": ctx, "context_mask": cmask,
+            "grid": (f, h, w), "tokens_per_frame": tpf}
+
+
+def wan_head(p: Params, x: torch.Tensor, t: torch.Tensor, eps: float) -> torch.Tensor:
+    """Head.forward with per-token t [B, S, H] (FB/wan_video_dit.py:318-322): shift, scale =
+    modulation + t; Linear(LN(x) (1 + scale) + shift)."""
+    m = p["head.modulation"].unsqueeze(0).to(t.dtype) + t.unsqueeze(2)
+    shift, scale = m.chunk(2, dim=2)
+    return linear(adaln(x, shift.squeeze(2), scale.squeeze(2), eps), p["head.head.weight"], p["head.head.bias"])
+
+
+def wan_unpatchify(x: torch.Tensor, grid, patch, out_dim: int) -> torch.Tensor:
+    """rearrange 'b (f h w) (x y z c) -> b c (f x) (h y) (w z)' (FB/wan_video_dit.py:428-433)."""
+    f, h, w = grid
+    pt, ph, pw = patch
+    B = x.shape[0]
+    y = x.reshape(B, f, h, w, pt, ph, pw, out_dim).permute(0, 7, 1, 4, 2, 5, 3, 6)
+    return y.reshape(B, out_dim, f * pt, h * ph, w * pw)
+
+
+def wan_forward(p: Params, cfg: WanVideoConfig, x: torch.Tensor, timestep: torch.Tensor, context: torch.Tensor,
+                context_mask: Optional[torch.Tensor] = None, video_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """WanVideoDiT.forward = pre_dit -> blocks -> post_dit (FB/wan_video_dit.py:651-684);
+    video_mask: the [S, S] self-attention mask (None for bidirectional)."""
+    pre = wan_pre_dit(p, cfg, x, timestep, context, context_mask)
+    xt = pre["tokens"]
+    for i in range(cfg.num_layers):
+        xt = dit_block(p, i, xt, pre["context"], pre["t_mod"], pre["freqs"], cfg.num_heads, cfg.eps,
+                       pre["context_mask"], video_mask)
+    y = wan_head(p, xt, pre["t"], cfg.eps)
+    return wan_unpatchify(y, pre["grid"], cfg.patch_size, cfg.out_dim)
+
+
+# ---------------------------------------------------------------------------
 # CAE-FastWAM action-VAE decoder (fp32)
 # ---------------------------------------------------------------------------
 @dataclass

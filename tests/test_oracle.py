@@ -443,3 +443,81 @@ def test_d4d_schedule_and_block_structure():
     zc = dict(zd)
     zc["action_decoder.layer2.bias"] = torch.full_like(p["action_decoder.layer2.bias"], 0.5)
     assert torch.allclose(O.d4d_predict_action(zc, cfg, ctx, noise), noise - 0.5, atol=1e-6)
+
+
+# --------------------------------------------------------------------------- WanVideoDiT pre_dit / forward
+WAN_TINY = O.WanVideoConfig(hidden_dim=32, in_dim=4, ffn_dim=64, out_dim=4, text_dim=24, freq_dim=16, eps=1e-6,
+                            patch_size=(1, 2, 2), num_heads=2, attn_head_dim=24, num_layers=2)
+
+
+@pytest.fixture(scope="module")
+def wan_golden():
+    return load_file(os.path.join(os.path.dirname(__file__), "golden", "wan_video_tiny.safetensors"))
+
+
+@pytest.fixture(scope="module")
+def wan_params(wan_golden):
+    p = O.init_wan_params(WAN_TINY, int(wan_golden["meta.seed"][0]), std=float(wan_golden["meta.std"][0]))
+    assert math.isclose(_checksum(p), float(wan_golden["meta.param_checksum"][0]), rel_tol=0, abs_tol=1e-9)
+    return p
+
+
+def _wan_in(g, dt):
+    return g["in.x"].to(dt), g["in.timestep"].to(dt), g["in.context"].to(dt), g["in.context_mask"].bool()
+
+
+@pytest.mark.parametrize("name,dt", [("fp32", torch.float32), ("bf16", torch.bfloat16)])
+def test_golden_wan_pre_dit(wan_golden, wan_params, name, dt):
+    """The oracle's pre_dit against WanVideoDiT.pre_dit: tokens of the patch embedding, per-token
+    t and t_mod (first latent frame at timestep 0), the text embedding, the broadcast context mask
+    and the 3-D RoPE table of the (f, h, w) grid."""
+    g = wan_golden
+    pre = O.wan_pre_dit(O.cast_params(wan_params, dt), WAN_TINY, *_wan_in(g, dt))
+    rt, at = _tol(name)
+    for k in ("tokens", "t", "t_mod", "context"):
+        assert torch.allclose(pre[k].float(), g[f"pre.{k}.{name}"], rtol=rt, atol=at), k
+    assert torch.equal(pre["context_mask"].to(torch.uint8), g["pre.context_mask"])
+    assert torch.equal(torch.view_as_real(pre["freqs"].to(torch.complex128)).float(), g["pre.freqs_real"])
+    assert pre["grid"] == (2, 2, 3) and pre["tokens_per_frame"] == 6
+
+
+@pytest.mark.parametrize("name,dt", [("fp32", torch.float32), ("bf16", torch.bfloat16)])
+def test_golden_wan_forward(wan_golden, wan_params, name, dt):
+    """pre_dit -> 2 blocks under the first-frame-causal video mask -> head -> unpatchify, against
+    WanVideoDiT.forward."""
+    g = wan_golden
+    x, t, c, cm = _wan_in(g, dt)
+    S = 12
+    vmask = O.mot_joint_mask(S, 0, 6)
+    y = O.wan_forward(O.cast_params(wan_params, dt), WAN_TINY, x, t, c, cm, vmask)
+    rt, at = _tol(name)
+    assert y.shape == (2, 4, 2, 4, 6)
+    assert torch.allclose(y.float(), g[f"forward.{name}"], rtol=rt, atol=at)
+
+
+def test_golden_wan_detects_planted_mistakes(wan_golden, wan_params):
+    """Plausible slips fail the goldens: every token at the shared timestep (the first frame's
+    zero dropped), the un-patchify's channel taken slowest instead of fastest, and the head's
+    shift and scale swapped."""
+    g = wan_golden
+    p = O.cast_params(wan_params, torch.float32)
+    x, t, c, cm = _wan_in(g, torch.float32)
+    pre = O.wan_pre_dit(p, WAN_TINY, x, t, c, cm)
+    # (1) no first-frame zero: recompute t as if every token carried the sample's timestep
+    emb = O.sinusoidal_embedding_1d(16, t.repeat_interleave(12))
+    t_all = O.linear(O.silu(O.linear(emb, p["time_embedding.0.weight"], p["time_embedding.0.bias"])),
+                     p["time_embedding.2.weight"], p["time_embedding.2.bias"]).reshape(2, 12, 32)
+    assert not torch.allclose(t_all, g["pre.t.fp32"], rtol=2e-5, atol=2e-5)
+    assert torch.allclose(pre["t"], g["pre.t.fp32"], rtol=2e-5, atol=2e-5)
+    # (2) un-patchify with (c x y z) feature order
+    y_tok = torch.randn(2, 12, 16, generator=torch.Generator().manual_seed(1))
+    good = O.wan_unpatchify(y_tok, (2, 2, 3), (1, 2, 2), 4)
+    bad = y_tok.reshape(2, 2, 2, 3, 4, 1, 2, 2).permute(0, 4, 1, 5, 2, 6, 3, 7).reshape(2, 4, 2, 4, 6)
+    assert not torch.equal(good, bad)
+    # (3) head shift / scale swapped
+    m = p["head.modulation"]
+    p2 = dict(p)
+    p2["head.modulation"] = m.flip(1).contiguous()
+    vmask = O.mot_joint_mask(12, 0, 6)
+    y = O.wan_forward(p2, WAN_TINY, x, t, c, cm, vmask)
+    assert not torch.allclose(y, g["forward.fp32"], rtol=2e-5, atol=2e-5)

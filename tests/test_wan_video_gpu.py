@@ -1,0 +1,100 @@
+"""WanVideoDiT on the library (fam.video_dit.FusedWanVideoDiT) against the oracle's restatement
+of pre_dit / forward, which the reference's own WanVideoDiT pins (tests/golden/
+wan_video_tiny.safetensors): fp32 oracle on bf16-valued weights and inputs, normwise relative
+error <= 2e-2 on the outputs.  Cases: the block chain at <= 128 tokens (split-K projections)
+and above (large-M GEMM), a first-frame-causal video mask and a ragged text mask, the prefill
+mode of FastWAM.infer_action (one latent frame at t = 0), and two blocks at config 2's full
+shape (2 x 30 x 26 latent patches, hidden 3072, 24 x 128 heads, FFN 14336, 512 text tokens)."""
+import pytest
+import torch
+
+from oracle import fam_oracle as O
+
+pytestmark = pytest.mark.gpu
+BF = torch.bfloat16
+
+
+def _rel(y, ref):
+    y, ref = y.float().cpu(), ref.float().cpu()
+    return ((y - ref).abs().max() / ref.abs().max()).item()
+
+
+def _setup(cfg, B, F, Hl, Wl, Lc, seed, ragged=True):
+    p = {k: v.to(BF) for k, v in O.init_wan_params(cfg, seed).items()}
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(B, cfg.in_dim, F, Hl, Wl, generator=g).to(BF)
+    ctx = torch.randn(B, Lc, cfg.text_dim, generator=g).to(BF)
+    cm = torch.ones(B, Lc, dtype=torch.bool)
+    if ragged:
+        cm[-1, Lc - 5:] = False
+    t = torch.tensor([437.0 + 100 * i for i in range(B)], dtype=BF)
+    return p, x, ctx, cm, t
+
+
+@pytest.mark.parametrize("B,F,Hl,Wl,causal", [(1, 2, 8, 12, True), (2, 2, 8, 12, False), (1, 2, 16, 24, True)])
+def test_wan_forward_matches_oracle(B, F, Hl, Wl, causal):
+    from fam.video_dit import FusedWanVideoDiT
+    cfg = O.WanVideoConfig(hidden_dim=1024, in_dim=16, ffn_dim=2048, out_dim=16, text_dim=512, freq_dim=256,
+                           num_heads=8, attn_head_dim=128, num_layers=2)
+    Lc = 24
+    p, x, ctx, cm, t = _setup(cfg, B, F, Hl, Wl, Lc, 61)
+    S = F * (Hl // 2) * (Wl // 2)
+    vmask = O.mot_joint_mask(S, 0, S // F) if causal else None
+    m = FusedWanVideoDiT(cfg, p, batch=B, frames=F, height=Hl, width=Wl, ctx_len=Lc, video_mask=vmask)
+    y = m.forward(x.cuda(), t.cuda(), ctx.cuda(), cm.cuda())
+    p32 = {k: v.float() for k, v in p.items()}
+    ref = O.wan_forward(p32, cfg, x.float(), t.float(), ctx.float(), cm, vmask)
+    err = _rel(y, ref)
+    print(f"wan forward B={B} S={S} causal={causal}: {m.num_launches} launches, relerr {err:.3e}")
+    assert y.shape == ref.shape
+    assert err <= 2e-2
+    # pre_dit's per-token t and the embedded context stay in the buffers
+    pre = O.wan_pre_dit(p32, cfg, x.float(), t.float(), ctx.float(), cm)
+    st = m.pre_state()
+    assert _rel(st["t"], pre["t"]) <= 2e-2
+    assert _rel(st["t_mod"], pre["t_mod"]) <= 2e-2
+    assert _rel(st["context"], pre["context"]) <= 2e-2
+    # graph replay gives the same bits
+    m.capture()
+    assert torch.equal(m.forward(x.cuda(), t.cuda(), ctx.cuda(), cm.cuda()), y)
+
+
+def test_wan_prefill_mode_first_frame():
+    """FastWAM.infer_action's video half: pre_dit of one latent frame at t = 0 (7 x 14 patches,
+    98 tokens) feeding the K/V prefill; every layer's K/V against the oracle's prefill on the
+    oracle's pre_dit outputs."""
+    from fam.video_dit import FusedWanVideoDiT
+    cfg = O.WanVideoConfig(hidden_dim=768, in_dim=48, ffn_dim=1536, out_dim=48, text_dim=1024, freq_dim=256,
+                           num_heads=6, attn_head_dim=128, num_layers=3)
+    Lc = 29
+    p, x, ctx, cm, _ = _setup(cfg, 1, 1, 14, 28, Lc, 71)
+    t0 = torch.zeros(1, dtype=BF)
+    m = FusedWanVideoDiT(cfg, p, batch=1, frames=1, height=14, width=28, ctx_len=Lc, mode="prefill")
+    kv = m.prefill(x.cuda(), t0.cuda(), ctx.cuda(), cm.cuda())
+    p32 = {k: v.float() for k, v in p.items()}
+    pre = O.wan_pre_dit(p32, cfg, x.float(), t0.float(), ctx.float(), cm)
+    ref = O.mot_prefill_video_cache(p32, cfg.block_config(), pre["tokens"], pre["freqs"], pre["t_mod"], pre["context"],
+                                    torch.ones(98, 98, dtype=torch.bool), pre["context_mask"])
+    worst = 0.0
+    for i, ((k, v), (rk, rv)) in enumerate(zip(kv, ref)):
+        ek, ev = _rel(k, rk), _rel(v, rv)
+        worst = max(worst, ek, ev)
+        assert ek <= 2e-2 and ev <= 2e-2, (i, ek, ev)
+    print(f"wan pre_dit + prefill (98 tokens): {m.num_launches} launches, worst relerr {worst:.3e}")
+
+
+def test_wan_forward_config2_shape_two_blocks():
+    """Two blocks at config 2's shape through pre_dit and the head: latents [1, 48, 2, 60, 52]
+    (1560 tokens), 512 text tokens of width 4096."""
+    from fam.video_dit import FusedWanVideoDiT
+    cfg = O.WanVideoConfig(hidden_dim=3072, in_dim=48, ffn_dim=14336, out_dim=48, text_dim=4096, freq_dim=256,
+                           num_heads=24, attn_head_dim=128, num_layers=2)
+    Lc = 512
+    p, x, ctx, cm, t = _setup(cfg, 1, 2, 60, 52, Lc, 81, ragged=False)
+    m = FusedWanVideoDiT(cfg, p, batch=1, frames=2, height=60, width=52, ctx_len=Lc)
+    y = m.forward(x.cuda(), t.cuda(), ctx.cuda(), cm.cuda())
+    p32 = {k: v.float() for k, v in p.items()}
+    ref = O.wan_forward(p32, cfg, x.float(), t.float(), ctx.float(), cm, None)
+    err = _rel(y, ref)
+    print(f"wan forward config-2 shape, 2 blocks: relerr {err:.3e}")
+    assert err <= 2e-2
