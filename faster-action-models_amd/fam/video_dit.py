@@ -639,13 +639,16 @@ class FusedWanVideoDiT:
 
     mode "prefill" stops after the blocks and exposes their K/V (`kv_cache()`): the video half of
     FastWAM.infer_action (FB/fastwam.py:1018-1041), whose first latent frame runs at t = 0.
+    mode "features" runs every block in full and stops before the head: `features()` is the last
+    block's output, the backbone.hidden_states[-1] a DiT4DiT head consumes
+    (DB/framework/DiT4DiT.py:205-222).
     video_mask: bool [S, S] on the self-attention (None: every key).
     """
 
     def __init__(self, cfg, params: Dict[str, torch.Tensor], *, batch: int, frames: int, height: int, width: int,
                  ctx_len: int, video_mask: Optional[torch.Tensor] = None, mode: str = "forward", device="cuda"):
-        if mode not in ("forward", "prefill"):
-            raise ValueError(f"mode must be 'forward' or 'prefill', got {mode!r}")
+        if mode not in ("forward", "prefill", "features"):
+            raise ValueError(f"mode must be 'forward', 'prefill' or 'features', got {mode!r}")
         dev = torch.device(device)
         self.mode, self.cfg, self.device = mode, cfg, dev
         pt, ph, pw = cfg.patch_size
@@ -693,7 +696,7 @@ class FusedWanVideoDiT:
                                         head_dim=cfg.attn_head_dim, ffn_dim=cfg.ffn_dim, batch=B, video_len=S,
                                         ctx_len=Lc, freqs=freqs, eps=cfg.eps, video_mask=video_mask,
                                         ctx_mask=self.cmask if Lc > 0 else None, device=dev,
-                                        keep_output=(mode == "forward"))
+                                        keep_output=(mode != "prefill"))
         sh = self.blocks.shared
         self.patches = z(B * S, C * P)
         self.emb = z(2 * B, cfg.freq_dim)
@@ -819,6 +822,13 @@ class FusedWanVideoDiT:
 
     def kv_cache(self):
         return self.blocks.kv_cache()
+
+    def features(self) -> torch.Tensor:
+        """The last block's output [B, S, H] (a view of the residual stream, valid until the next
+        run); modes "forward" and "features"."""
+        if self.mode == "prefill":
+            raise RuntimeError("the prefill mode does not run its last block in full")
+        return self.blocks.shared["x"].view(self.B, self.S, self.cfg.hidden_dim)
 
     def pre_state(self):
         """The pre_dit outputs in the reference's layout (FB/wan_video_dit.py:642-648): tokens

@@ -98,3 +98,30 @@ def test_wan_forward_config2_shape_two_blocks():
     err = _rel(y, ref)
     print(f"wan forward config-2 shape, 2 blocks: relerr {err:.3e}")
     assert err <= 2e-2
+
+
+def test_config4_backbone_shape_two_blocks_features():
+    """Two backbone blocks at config 4's shape (Cosmos-Predict2.5-2B-style: hidden 2048, 16 x 128
+    heads, FFN 8192, 2048 video tokens = 2 x 32 x 32 latent patches with 3-D RoPE, 512 text tokens
+    of width 1024), the last block's output (what the DiT4DiT head reads) against the oracle.
+    The block arithmetic is the Wan block's: Cosmos' own modules live in diffusers, which no
+    reference file or fixture here pins (parity unpinned as to Cosmos specifics)."""
+    from fam.video_dit import FusedWanVideoDiT
+    cfg = O.WanVideoConfig(hidden_dim=2048, in_dim=16, ffn_dim=8192, out_dim=16, text_dim=1024, freq_dim=256,
+                           num_heads=16, attn_head_dim=128, num_layers=2)
+    Lc = 512
+    p, x, ctx, cm, t = _setup(cfg, 1, 2, 64, 64, Lc, 91, ragged=False)
+    m = FusedWanVideoDiT(cfg, p, batch=1, frames=2, height=64, width=64, ctx_len=Lc, mode="features")
+    m.set_inputs(x.cuda(), t.cuda(), ctx.cuda(), cm.cuda())
+    m.run()
+    y = m.features()
+    p32 = {k: v.float() for k, v in p.items()}
+    pre = O.wan_pre_dit(p32, cfg, x.float(), t.float(), ctx.float(), cm)
+    xt = pre["tokens"]
+    for i in range(cfg.num_layers):
+        xt = O.dit_block(p32, i, xt, pre["context"], pre["t_mod"], pre["freqs"], cfg.num_heads, cfg.eps,
+                         pre["context_mask"])
+    err = _rel(y, xt)
+    print(f"config-4 backbone shape (2048 tokens, hidden 2048), 2 blocks: relerr {err:.3e}")
+    assert y.shape == (1, 2048, 2048)
+    assert err <= 2e-2
