@@ -2,7 +2,7 @@
 //     out[m, n] = epi( sum_k pro(a)[m, k] * w[n, k] + bias[n] )
 // w is in nn.Linear layout [N, K] (K contiguous), a is [M, K] (K contiguous).
 //
-// Two kernels, chosen by M; neither communicates between workgroups (on gfx950 a release /
+// Kernels chosen by M and shape; none communicates between workgroups (on gfx950 a release /
 // acquire fence between workgroups writes back and invalidates the XCD's L2, which costs far
 // more than these small products), so every workgroup owns its outputs outright.
 //
@@ -28,11 +28,16 @@
 // fp32 partials partial[z][m][n] are summed, in split order, by the row kernel that follows
 // (fam_rowop), which also runs the epilogue and the next normalisation on whole rows.
 //
-// tiled_kernel (M > 64: the per-call context projections, batched throughput points):
+// big_kernel (M >= 128, no prologue, K % 64 == 0: the video backbone's projections, the
+// per-call context K/V, batched throughput points): 256 x 256 down to 64 x 64 tiles fed by
+// direct-to-LDS loads; described at its definition.
+//
+// tiled_kernel (M > 64 outside the big kernel's envelope, e.g. with a normalising prologue):
 //   * 256-thread workgroup, BM x BN output tile (64x64 or 128x128), 2x2 waves of 16x16 MFMA
 //     tiles, K in steps of 64 through double-buffered LDS, next step's global loads issued
 //     before the current step's MFMAs; prologue statistics per tile row at kernel start.
 #include <algorithm>
+#include <type_traits>
 
 #include "fam_common.h"
 
@@ -860,15 +865,27 @@ __global__ __launch_bounds__(256) void tiled_kernel(GemmArgs g) {
 // big_kernel (M >= 128, no prologue, K % 64 == 0): the throughput GEMM of the video backbone
 // and of batched action calls.
 //   * 256 threads = 2 x 2 waves; a wave owns (16 WFM) x (16 WFN) outputs (up to 128 x 128,
-//     256 fp32 accumulators per lane in the accumulation registers), the workgroup
-//     BM x BN = (32 WFM) x (32 WFN);
-//   * K in blocks of 64 through double-buffered LDS: rows of 128 bytes (8 chunks of 16 B)
-//     with chunk kc of row r stored at kc ^ (r & 7), which keeps both the 16-byte fragment
-//     reads (16 rows x 4 chunks per wave) and the staging writes free of LDS bank conflicts
-//     (measured) with no padding;
-//   * global loads of the next block (raw buffer loads: rows past M or N read as zero, 32-bit
-//     offsets) are in flight during the current block's 2 x WFM x WFN MFMAs, then land in the
-//     other LDS buffer; one barrier per block;
+//     256 fp32 accumulators per lane), the workgroup BM x BN = (32 WFM) x (32 WFN):
+//     256 x 256, 224 x 256 (M = 1560 splits into 7 such row tiles with 8 padding rows),
+//     128 x 128 (two workgroups per CU) or 64 x 64;
+//   * K in blocks of 64 through two LDS slots.  Rows of a slot are 128 bytes (8 chunks of
+//     16 B) with chunk c of row r stored at c ^ (r & 7): the 16-byte fragment reads of 8
+//     consecutive lanes (8 rows, one chunk) hit 8 distinct bank groups;
+//   * the slots are filled by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds): one
+//     load writes 1 KB = 8 rows x 128 B, lane l fetching chunk (l % 8) ^ (l / 8) of row l / 8,
+//     so the swizzle costs nothing; the descriptors make rows past M or N read zeros; the
+//     soffset (k position) and M0 (LDS slot) are scalar, so issuing a load costs no VALU work;
+//   * block b: k-step 0 computes from fragments read during block b - 1 while k-step 1's
+//     fragments are read; then one barrier (after which block b + 1 has landed and every wave
+//     is done with block b's slot), block b + 2 is sent into that slot and k-step 1 computes
+//     while k-step 0 of block b + 1 is read.  Loads, fragment reads and MFMAs interleave per
+//     MFMA row;
+//   * the MFMAs are written as inline assembly with the accumulator tied to an accumulation
+//     register ("+a"): with all 256 of them holding accumulators, the compiler's own MFMA
+//     form wants a free destination quad and shuffles accumulators through VGPRs every
+//     iteration.  Being opaque to the hazard recognizer, the chain is fenced by s_nop before
+//     its first and after its last MFMA (the VALU writes of the zero accumulators, the
+//     accumulator reads of the epilogue);
 //   * workgroups are spread over the 8 XCDs in contiguous task ranges, and a range walks the
 //     tile grid column by column in groups of row tiles, so consecutive tiles on one XCD share
 //     their weight panel (and row panels) in that XCD's L2;
@@ -876,14 +893,26 @@ __global__ __launch_bounds__(256) void tiled_kernel(GemmArgs g) {
 //     8-byte (bf16) or 16-byte (fp32) stores.
 // MFMA operands: A = weight rows (n), B = activation rows (m), so a lane's accumulator holds
 // out[m][n .. n + 3] for one m.
-template <int WFM, int WFN>
-__global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int tiles_n) {
-  constexpr int BM = 32 * WFM, BN = 32 * WFN, BKB = 64;
-  constexpr int CA = BM * 8 / 256, CW = BN * 8 / 256;   // 16-byte chunks per thread per block
-  __shared__ __attribute__((aligned(16))) bf16 As[2][BM * BKB];
-  __shared__ __attribute__((aligned(16))) bf16 Ws[2][BN * BKB];
+#define FAM_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ void mfma_acc(f32x4& acc, const bf16x8& w, const bf16x8& a) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(w), "v"(a));
+}
+
+template <int WFM, int WFN>
+__global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int tiles_n, int vec8) {
+  // the A part of a slot holds BMA >= BM rows, a multiple of 64 (a 224-row tile also loads the
+  // next 32 rows, unused: measured 2-4 % faster than 7 loads per wave per block)
+  constexpr int BM = 32 * WFM, BN = 32 * WFN, BK = 64, BMA = (BM + 63) / 64 * 64;
+  constexpr int SA = BMA * BK, SS = (BMA + BN) * BK;           // elements of a slot's A part, slot
+  constexpr int NIA = BMA / 32, NIW = BN / 32, IPW = NIA + NIW;   // 1 KB loads per wave per block
+  static_assert(IPW < 64, "vmcnt");
+  // two K slots, later the bf16 output tile with its padded rows
+  constexpr int LDS_ELEMS = 2 * SS > BM * (BN + 8) ? 2 * SS : BM * (BN + 8);
+  __shared__ __attribute__((aligned(1024))) bf16 sm[LDS_ELEMS];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
   const int wm0 = (wave >> 1) * (16 * WFM), wn0 = (wave & 1) * (16 * WFN);
 
@@ -900,193 +929,174 @@ __global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int t
 
   const int Mi = (int)g.M, Ni = (int)g.N;
   const uint32_t lda2 = (uint32_t)g.lda * 2u, ldw2 = (uint32_t)g.ldw * 2u;
-  const auto arsrc = buffer_rsrc(g.a + (int64_t)m0 * g.lda, (uint32_t)(Mi - m0) * lda2);
-  const auto wrsrc = buffer_rsrc(g.w + (int64_t)n0 * g.ldw, (uint32_t)(Ni - n0 < BN ? Ni - n0 : BN) * ldw2);
-  // staging chunk q = tid + 256 p: row q / 8, chunk q % 8 (rows of one p are 32 apart)
-  const int sr = tid >> 3, skc = tid & 7;
-  auto swz = [](int r) { return r & 7; };
-  const uint32_t aoff = (uint32_t)sr * lda2 + (uint32_t)skc * 16u;
-  const uint32_t woff = (uint32_t)sr * ldw2 + (uint32_t)skc * 16u;
-  bf16x8 ra[CA], rw[CW];
-  auto gload = [&](int kb) {
-    const uint32_t k2 = (uint32_t)kb * (BKB * 2);
-#pragma unroll
-    for (int p = 0; p < CA; ++p) ra[p] = buffer_load8(arsrc, aoff + k2, (uint32_t)p * 32u * lda2);
-#pragma unroll
-    for (int p = 0; p < CW; ++p) rw[p] = buffer_load8(wrsrc, woff + k2, (uint32_t)p * 32u * ldw2);
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int p = 0; p < CA; ++p) {
-      const int r = sr + 32 * p;
-      *reinterpret_cast<bf16x8*>(&As[buf][r * BKB + ((skc ^ swz(r)) << 3)]) = ra[p];
-    }
-#pragma unroll
-    for (int p = 0; p < CW; ++p) {
-      const int r = sr + 32 * p;
-      *reinterpret_cast<bf16x8*>(&Ws[buf][r * BKB + ((skc ^ swz(r)) << 3)]) = rw[p];
+  const auto ra = buffer_rsrc(g.a + (int64_t)m0 * g.lda, (uint32_t)(Mi - m0) * lda2);
+  const auto rw = buffer_rsrc(g.w + (int64_t)n0 * g.ldw, (uint32_t)(Ni - n0 < BN ? Ni - n0 : BN) * ldw2);
+  const int lr = lane >> 3;
+  const uint32_t lc16 = (uint32_t)(((lane & 7) ^ lr) * 16);
+  const uint32_t voa = (uint32_t)lr * lda2 + lc16, vow = (uint32_t)lr * ldw2 + lc16;
+  const int nb = (int)(g.K / BK);
+  // load p of this wave for block blk into slot: A rows 8 (wave + 4p) .. + 7 for p < NIA, else
+  // W rows 8 (wave + 4 (p - NIA)) .. + 7; blocks past the end re-read the last one (unused)
+  auto dma = [&](int p, int blk, int slot) {
+    const uint32_t kb = (uint32_t)(blk < nb ? blk : nb - 1) * (BK * 2);
+    if (p < NIA) {
+      const int r = wave + 4 * p;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, FAM_LDS(sm + slot * SS + r * 512), 16, voa,
+                                               (uint32_t)(8 * r) * lda2 + kb, 0, 0);
+    } else {
+      const int r = wave + 4 * (p - NIA);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, FAM_LDS(sm + slot * SS + SA + r * 512), 16, vow,
+                                               (uint32_t)(8 * r) * ldw2 + kb, 0, 0);
     }
   };
-  auto frag = [&](const bf16* tile, int r, int kc) {
-    return *reinterpret_cast<const bf16x8*>(&tile[r * BKB + ((kc ^ swz(r)) << 3)]);
-  };
+  // the fragment of k-step h: row base + l16, chunk 4 h + lg, stored at (4 h + lg) ^ (l16 & 7)
+  const int fp0 = (lg ^ (l16 & 7)) << 3, fp1 = ((4 + lg) ^ (l16 & 7)) << 3;
+  const bf16* fa = sm + (wm0 + l16) * BK;
+  const bf16* fw = sm + SA + (wn0 + l16) * BK;
 
   f32x4 acc[WFM][WFN];
 #pragma unroll
   for (int i = 0; i < WFM; ++i)
 #pragma unroll
-    for (int j = 0; j < WFN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Fragments of the two 32-wide k-steps of a block live in separate registers (F0, F1), and
-  // the staging registers carry a block from its global load (one iteration ahead) to its LDS
-  // store.  Iteration kb, with no branches inside:
-  //   [read F1 = kb step 1]
-  //   MFMA(F0) interleaved with, per staging chunk, [LDS store of kb+1] [global load of kb+2]
-  //   barrier   [read F0 = kb+1 step 0]   MFMA(F1)
-  // The MFMA pipe stays fed while the stores and loads issue; past the end of K the loads read
-  // zeros or unused data into buffers no MFMA reads (the barrier's wait for outstanding LDS
-  // operations keeps a buffer's last readers ahead of its next writers).
-  bf16x8 a0[WFM], w0[WFN], a1[WFM], w1[WFN];
-  auto rfrag = [&](int buf, int s, bf16x8* af, bf16x8* wf) {
-#pragma unroll
-    for (int i = 0; i < WFM; ++i) af[i] = frag(As[buf], wm0 + i * 16 + l16, s * 4 + lg);
-#pragma unroll
-    for (int j = 0; j < WFN; ++j) wf[j] = frag(Ws[buf], wn0 + j * 16 + l16, s * 4 + lg);
-  };
-  auto mfmas = [&](const bf16x8* af, const bf16x8* wf) {
-#pragma unroll
-    for (int i = 0; i < WFM; ++i)
-#pragma unroll
-      for (int j = 0; j < WFN; ++j) acc[i][j] = mfma16(wf[j], af[i], acc[i][j]);
-  };
-  // staging chunk c < CA: A rows sr + 32 c; c >= CA: W rows sr + 32 (c - CA)
-  auto store_chunk = [&](int buf, int c) {
-    if (c < CA) {
-      const int r = sr + 32 * c;
-      *reinterpret_cast<bf16x8*>(&As[buf][r * BKB + ((skc ^ swz(r)) << 3)]) = ra[c];
-    } else {
-      const int r = sr + 32 * (c - CA);
-      *reinterpret_cast<bf16x8*>(&Ws[buf][r * BKB + ((skc ^ swz(r)) << 3)]) = rw[c - CA];
-    }
-  };
-  auto load_chunk = [&](int kb, int c) {
-    const uint32_t k2 = (uint32_t)kb * (BKB * 2);
-    if (c < CA) ra[c] = buffer_load8(arsrc, aoff + k2, (uint32_t)c * 32u * lda2);
-    else rw[c - CA] = buffer_load8(wrsrc, woff + k2, (uint32_t)(c - CA) * 32u * ldw2);
-  };
-  constexpr int NC = CA + CW, NM = WFM * WFN;
-  const int nkb = (int)(g.K / BKB);
-  if constexpr (NM > 32) {
-    // 8 x 8 wave tiles: the interleaved schedule below does not fit the registers; the block's
-    // global loads go out at the top of its iteration and land in LDS between the two halves
-    gload(0);
-    lstore(0);
-    __syncthreads();
-    rfrag(0, 0, a0, w0);
-    for (int kb = 0; kb < nkb; ++kb) {
-      const int buf = kb & 1;
-      const bool more = kb + 1 < nkb;
-      if (more) gload(kb + 1);
-      rfrag(buf, 1, a1, w1);
-      __builtin_amdgcn_sched_barrier(0);
-      mfmas(a0, w0);
-      __builtin_amdgcn_sched_barrier(0);
-      if (more) lstore(buf ^ 1);
-      __syncthreads();
-      if (more) rfrag(buf ^ 1, 0, a0, w0);
-      __builtin_amdgcn_sched_barrier(0);
-      mfmas(a1, w1);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  } else {
-  gload(0);
-  lstore(0);
-  gload(1);
-  lds_barrier();
-  rfrag(0, 0, a0, w0);
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
-    rfrag(buf, 1, a1, w1);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int mi = 0; mi < NM; ++mi) {
-      const int i = mi / WFN, j = mi % WFN;
-      acc[i][j] = mfma16(w0[j], a0[i], acc[i][j]);
-      if ((mi + 1) * NC / NM > mi * NC / NM) {
-        const int c = mi * NC / NM;
-        store_chunk(buf ^ 1, c);
-        load_chunk(kb + 2, c);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    lds_barrier();
-    rfrag(buf ^ 1, 0, a0, w0);
-    __builtin_amdgcn_sched_barrier(0);
-    mfmas(a1, w1);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  }
-
-  // lane owns out[m0 + wm0 + i*16 + l16][n0 + wn0 + j*16 + 4*lg + e] (N % 4 == 0 and the
-  // operand alignment of 4-column vectors are host-checked)
-#pragma unroll
-  for (int i = 0; i < WFM; ++i) {
-    const int m = m0 + wm0 + i * 16 + l16;
-    if (m >= Mi) continue;
-    const int64_t bi = m / g.rpb, si = m - bi * g.rpb;
-#pragma unroll
     for (int j = 0; j < WFN; ++j) {
-      const int nb = n0 + wn0 + j * 16 + lg * 4;
-      if (nb >= Ni) continue;
-      float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-      if (g.bias) {
-        const bf16x4 bv = *reinterpret_cast<const bf16x4*>(g.bias + nb);
+      acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      asm volatile("" : "+a"(acc[i][j]));
+    }
+  asm volatile("s_nop 7");
+
+  bf16x8 a0[WFM], w0[WFN], a1[WFM], w1[WFN];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] += to_f(bv[e]);
-      }
-      if (g.act == FAM_ACT_GELU_TANH) {
-        // 0.5 x (1 + tanh(u)) = x / (1 + exp(-2u)), u = sqrt(2/pi) (x + 0.044715 x^3)
+  for (int p = 0; p < IPW; ++p) dma(p, 0, 0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float x = v[e], u = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-          v[e] = x / (1.0f + __expf(-2.0f * u));
-        }
-      } else if (g.act == FAM_ACT_SILU) {
+  for (int p = 0; p < IPW; ++p) dma(p, 1, 1);
+  __builtin_amdgcn_s_waitcnt(0x0070 | (IPW & 15) | ((IPW >> 4) << 14));   // vmcnt(IPW): block 0
+  __builtin_amdgcn_s_barrier();
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = v[e] / (1.0f + __expf(-v[e]));
-      } else if (g.act == FAM_ACT_RELU) {
+  for (int i = 0; i < WFM; ++i) a0[i] = *reinterpret_cast<const bf16x8*>(fa + i * 16 * BK + fp0);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = fmaxf(v[e], 0.f);
+  for (int j = 0; j < WFN; ++j) w0[j] = *reinterpret_cast<const bf16x8*>(fw + j * 16 * BK + fp0);
+
+  for (int b = 0; b < nb; ++b) {
+    const int cur = (b & 1) * SS, nxt = ((b + 1) & 1) * SS;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < WFM; ++i) {
+      a1[i] = *reinterpret_cast<const bf16x8*>(fa + cur + i * 16 * BK + fp1);
+#pragma unroll
+      for (int j = i * WFN / WFM; j < (i + 1) * WFN / WFM; ++j)
+        w1[j] = *reinterpret_cast<const bf16x8*>(fw + cur + j * 16 * BK + fp1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < WFN; ++j) mfma_acc(acc[i][j], w0[j], a0[i]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): block b + 1 landed, slot b read
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < WFM; ++i) {
+#pragma unroll
+      for (int p = i * IPW / WFM; p < (i + 1) * IPW / WFM; ++p) dma(p, b + 2, b & 1);
+      a0[i] = *reinterpret_cast<const bf16x8*>(fa + nxt + i * 16 * BK + fp0);
+#pragma unroll
+      for (int j = i * WFN / WFM; j < (i + 1) * WFN / WFM; ++j)
+        w0[j] = *reinterpret_cast<const bf16x8*>(fw + nxt + j * 16 * BK + fp0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < WFN; ++j) mfma_acc(acc[i][j], w1[j], a1[i]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);   // the (unused) loads of blocks nb, nb + 1 drain before exit
+  asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15");
+#pragma unroll
+  for (int i = 0; i < WFM; ++i)
+#pragma unroll
+    for (int j = 0; j < WFN; ++j) asm volatile("" : "+a"(acc[i][j]));
+
+  // Epilogue in two passes through LDS (the slots are free now).  Pass 1: every lane adds the
+  // bias to its accumulators (lane: out[m][n .. n + 3], one m per lane), rounds to bf16 -- the
+  // reference's nn.Linear output -- and parks them in a row-major bf16 tile.  Pass 2: a thread
+  // takes VEC consecutive columns of a row (a wave covers 64 VEC contiguous columns) and applies
+  // the activation and gate * y + residual on the rounded values, as the reference's separate
+  // bf16 ops do, with coalesced residual / gate reads and output stores.  Both passes are
+  // compact loops: a per-accumulator copy of a branchy epilogue costs the kernel's instruction
+  // cache more than the epilogue's own work, and the stores of a single-round grid are all tail.
+  constexpr int EP = BN + 8;   // bf16 row pitch of the parked tile: 16 B of padding per row
+  bf16* ot = sm;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < WFN; ++j) {
+    const int nl = wn0 + j * 16 + lg * 4, n = n0 + nl;
+    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (g.bias && n < Ni) {
+      const bf16x4 b4 = *reinterpret_cast<const bf16x4*>(g.bias + n);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bv[e] = to_f(b4[e]);
+    }
+#pragma unroll
+    for (int i = 0; i < WFM; ++i) {
+      bf16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = to_bf(acc[i][j][e] + bv[e]);
+      *reinterpret_cast<bf16x4*>(ot + (wm0 + i * 16 + l16) * EP + nl) = o;
+    }
+  }
+  __syncthreads();
+  auto pass2 = [&](auto vec_tag) {
+    constexpr int VEC = decltype(vec_tag)::value;
+    typedef __bf16 bfv __attribute__((ext_vector_type(VEC)));
+    for (int q = tid; q < BM * (BN / VEC); q += 256) {
+      const int r = q / (BN / VEC), c = (q - r * (BN / VEC)) * VEC;
+      const int m = m0 + r, n = n0 + c;
+      if (m >= Mi || n >= Ni) continue;
+      const bfv y = *reinterpret_cast<const bfv*>(ot + r * EP + c);
+      float v[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[e] = to_f(y[e]);
+      if (g.act != FAM_ACT_NONE) {
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) v[e] = apply_act(v[e], g.act);
       }
       if (g.res) {
-        float gt[4] = {1.f, 1.f, 1.f, 1.f}, rv[4];
-        if (g.gate) {
-          const bf16x4 gv = *reinterpret_cast<const bf16x4*>(g.gate + bi * g.gbs + si * g.grs + nb);
+        float gt[VEC];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) gt[e] = to_f(gv[e]);
+        for (int e = 0; e < VEC; ++e) gt[e] = 1.f;
+        if (g.gate) {
+          const int rpb = (int)g.rpb, bi = m / rpb, si = m - bi * rpb;
+          const bfv gv = *reinterpret_cast<const bfv*>(g.gate + bi * g.gbs + si * g.grs + n);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) gt[e] = to_f(gv[e]);
         }
         if (g.out_f32) {
-          const f32x4 r4 = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(g.res) + (int64_t)m * g.ldr + nb);
+          const float* rp = reinterpret_cast<const float*>(g.res) + (int64_t)m * g.ldr + n;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) rv[e] = r4[e];
+          for (int e4 = 0; e4 < VEC; e4 += 4) {
+            const f32x4 r4 = *reinterpret_cast<const f32x4*>(rp + e4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e4 + e] = r4[e] + gt[e4 + e] * v[e4 + e];
+          }
         } else {
-          const bf16x4 r4 = *reinterpret_cast<const bf16x4*>(g.res + (int64_t)m * g.ldr + nb);
+          const bfv r8 = *reinterpret_cast<const bfv*>(g.res + (int64_t)m * g.ldr + n);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) rv[e] = to_f(r4[e]);
+          for (int e = 0; e < VEC; ++e) v[e] = to_f(r8[e]) + gt[e] * v[e];
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = rv[e] + gt[e] * v[e];
       }
       if (g.out_f32) {
-        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(g.out) + (int64_t)m * g.ldo + nb) = f32x4{v[0], v[1], v[2], v[3]};
-      } else {
-        bf16x4 o;
+        float* op = reinterpret_cast<float*>(g.out) + (int64_t)m * g.ldo + n;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = to_bf(v[e]);
-        *reinterpret_cast<bf16x4*>(g.out + (int64_t)m * g.ldo + nb) = o;
+        for (int e4 = 0; e4 < VEC; e4 += 4)
+          *reinterpret_cast<f32x4*>(op + e4) = f32x4{v[e4], v[e4 + 1], v[e4 + 2], v[e4 + 3]};
+      } else {
+        bfv o;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) o[e] = to_bf(v[e]);
+        *reinterpret_cast<bfv*>(g.out + (int64_t)m * g.ldo + n) = o;
       }
     }
-  }
+  };
+  if (vec8) pass2(std::integral_constant<int, 8>{});
+  else pass2(std::integral_constant<int, 4>{});
 }
 
 static int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
@@ -1116,12 +1126,13 @@ static void launch_skinny_k(const GemmArgs& a, int pro, hipStream_t s) {
 }
 
 // The big kernel's envelope: no prologue, K % 64 == 0, M >= 128, 32-bit byte offsets into a
-// and w, and a 4-column vector epilogue (N % 4 == 0, unit gate column stride, aligned vectors).
+// and w (a tile's loads reach up to 256 rows past its first), and a 4-column vector epilogue
+// (N % 4 == 0, unit gate column stride, aligned vectors).
 static bool big_ok(const fam_gemm_desc* d) {
   const int64_t ob = d->out_f32 ? 16 : 8;
   const auto al = [](const void* p, int64_t b) { return ((uintptr_t)p % (uintptr_t)b) == 0; };
-  return d->prologue == FAM_PRO_NONE && d->K % 64 == 0 && d->M >= 128 && d->M * d->lda * 2 < ((int64_t)1 << 31) &&
-         d->N * d->ldw * 2 < ((int64_t)1 << 31) && d->N % 4 == 0 && d->ldo % 4 == 0 && al(d->out, ob) &&
+  return d->prologue == FAM_PRO_NONE && d->K % 64 == 0 && d->M >= 128 &&
+         (d->M + 256) * d->lda * 2 < ((int64_t)1 << 31) && (d->N + 256) * d->ldw * 2 < ((int64_t)1 << 31) && d->N % 4 == 0 && d->ldo % 4 == 0 && al(d->out, ob) &&
          (!d->bias || al(d->bias, 8)) && (!d->res || (d->ldr % 4 == 0 && al(d->res, ob))) &&
          (!d->gate || (d->gate_ns == 1 && d->gate_bs % 4 == 0 && d->gate_rs % 4 == 0 && al(d->gate, 8)));
 }
@@ -1130,14 +1141,18 @@ template <int WFM, int WFN>
 static void launch_big(const GemmArgs& a, hipStream_t s) {
   const int tm = (int)((a.M + 32 * WFM - 1) / (32 * WFM)), tn = (int)((a.N + 32 * WFN - 1) / (32 * WFN));
   const unsigned grid = (unsigned)(((tm * tn + 7) / 8) * 8);
-  FAM_LAUNCH((big_kernel<WFM, WFN>), dim3(grid), dim3(256), 0, s, a, tm, tn);
+  // 8-column epilogue vectors when every 8-column group of the operands is 16-byte aligned
+  const auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  const int vec8 = a.N % 8 == 0 && a.ldo % 8 == 0 && al16(a.out) && (!a.res || (a.ldr % 8 == 0 && al16(a.res))) &&
+                   (!a.gate || (a.gbs % 8 == 0 && a.grs % 8 == 0 && al16(a.gate)));
+  FAM_LAUNCH((big_kernel<WFM, WFN>), dim3(grid), dim3(256), 0, s, a, tm, tn, vec8);
 }
 
-// Tile of the big kernel: 256 x 256 (8 x 8 wave tiles, 1 workgroup per CU), 128 x 128 (4 x 4,
-// 2 per CU) or 64 x 64 (2 x 2, 4 per CU), whichever has the smallest estimated time =
-// rounds x (concurrent tiles per CU) x tile area / efficiency, where a round fills every CU
-// with its concurrent tiles and the efficiency is the per-FLOP throughput of a full CU
-// relative to the 256 x 256 tile (measured on gfx950 at large K: 0.91 and 0.65).
+// Tile of the big kernel: the candidate with the least estimated time on the busiest CU,
+// tiles per CU (ceil(tiles / CUs)) x tile area / efficiency, where the 128 x 128 and 64 x 64
+// tiles run 2 and 3 workgroups per CU and the efficiency is the per-CU throughput relative to
+// the 256-wide tiles (measured on gfx950: 0.85 for 128 x 128; 64 x 64 is bound by LDS reads,
+// four fragments per four MFMAs, about 0.4); ties go to the larger tile.
 static void big_plan(int64_t M, int64_t N, int* wfm, int* wfn) {
   static int cus = 0;
   if (cus == 0) {
@@ -1146,14 +1161,12 @@ static void big_plan(int64_t M, int64_t N, int* wfm, int* wfn) {
       n = 256;
     cus = n;
   }
-  struct C { int fm, fn, conc; double eff; } cands[] = {{8, 8, 1, 1.0}, {4, 4, 2, 0.91}, {2, 2, 4, 0.65}};
+  struct C { int fm, fn; double eff; } cands[] = {{8, 8, 1.0}, {7, 8, 1.0}, {4, 4, 0.85}, {2, 2, 0.4}};
   double best = 1e300;
   for (const C& c : cands) {
     const int64_t bm = 32 * c.fm, bn = 32 * c.fn;
     const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    const int64_t slots = (int64_t)cus * c.conc;
-    const double rounds = (double)((tiles + slots - 1) / slots);
-    const double t = rounds * c.conc * (double)(bm * bn) / c.eff;
+    const double t = (double)((tiles + cus - 1) / cus) * (double)(bm * bn) / c.eff;
     if (t < best) { best = t; *wfm = c.fm; *wfn = c.fn; }
   }
 }
@@ -1236,6 +1249,7 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
     int fm = 8, fn = 8;
     big_plan(d->M, d->N, &fm, &fn);
     if (fm == 8) launch_big<8, 8>(a, s);
+    else if (fm == 7) launch_big<7, 8>(a, s);
     else if (fm == 4) launch_big<4, 4>(a, s);
     else launch_big<2, 2>(a, s);
   } else if (round_up(d->M, 128) / 128 * (round_up(d->N, 128) / 128) >= 200) launch_tiled<128, 128, 2>(a, d->prologue, s);
