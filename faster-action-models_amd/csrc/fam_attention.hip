@@ -1085,7 +1085,7 @@ __global__ __launch_bounds__(256) void attn_cross_kernel(AttnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// attn_long_kernel: long query sequences (video tokens), no mask, one key segment.
+// attn_long_kernel: long query sequences (video tokens), one key segment, no mask or a key mask.
 // A workgroup of 4 waves owns 128 queries of one (batch, head), 32 per wave; keys stream in
 // 64-key tiles through double-buffered LDS (K and V row-major), one barrier per tile, the
 // next tile's buffer loads in flight during the current tile's math.  Per wave and tile:
@@ -1099,7 +1099,10 @@ __global__ __launch_bounds__(256) void attn_cross_kernel(AttnArgs a) {
 // At most 256 registers per lane, so two workgroups share a CU and one's vector work fills
 // the other's matrix-core gaps.  Work-groups are mapped so that all query blocks of one head
 // run on the same XCD (its 4 MB L2 then holds that head's K/V once).
-template <int DH>
+// KMASK: a boolean key mask shared by every query (mask query stride 0: the text padding mask
+// of the cross-attention, [B, Lc] or [B, H, Lc]); each tile's 64 entries travel with the K/V
+// tile as additive 0 / -inf terms in LDS (keys past Sk included).
+template <int DH, bool KMASK>
 __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) {
   constexpr int BN = 64;                 // keys per tile
   constexpr int KS = DH / 16;            // 16-wide k-steps of S^T = K Q^T
@@ -1112,6 +1115,7 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   constexpr int KLD = DH + 8, VLD = DH == 128 ? 160 : 96;
   __shared__ bf16 Ks[2][BN][KLD];
   __shared__ bf16 Vs[2][BN][VLD];
+  __shared__ __attribute__((aligned(16))) float Mb[KMASK ? 2 : 1][BN];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5;
@@ -1163,6 +1167,21 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
       *reinterpret_cast<bf16x8*>(&Ks[buf][key][d0]) = kr[j];
     }
   };
+  // key mask of tile t (thread tid < BN: key t * BN + tid), as an additive term
+  const uint8_t* mrow = KMASK ? reinterpret_cast<const uint8_t*>(a.mask) + b * a.mbs + h * a.mhs : nullptr;
+  // (the raw byte is kept until the LDS store, so that the load's wait lands there)
+  int mr = 0;
+  auto gload_m = [&](int t) {
+    if constexpr (KMASK) {
+      const int key = t * BN + (tid & (BN - 1));
+      mr = key < Sk ? (int)mrow[key] : 0;
+    }
+  };
+  auto lstore_m = [&](int buf) {
+    if constexpr (KMASK) {
+      if (tid < BN) Mb[buf][tid] = mr ? 0.f : -INFINITY;
+    }
+  };
   auto lstore_v = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -1203,21 +1222,34 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   const int ntiles = (Sk + BN - 1) / BN;
   gload_k(0);
   gload_v(0);
+  gload_m(0);
   __builtin_amdgcn_sched_barrier(0);
   lstore_k(0);
   lstore_v(0);
+  lstore_m(0);
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const int buf = t & 1;
     gload_k(t + 1);   // zeros past Sk
     gload_v(t + 1);
+    gload_m(t + 1);
     __builtin_amdgcn_sched_barrier(0);
     f32x16 st[2] = {f32x16{}, f32x16{}};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) st[kt] = mfma32(kfrag(buf, kt, ks), qf[ks], st[kt]);
-    if ((t + 1) * BN > Sk) {
+    if constexpr (KMASK) {
+      // registers 4g..4g+3 of half kt: keys kt*32 + 8g + 4hh .. + 3
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const f32x4 m4 = *reinterpret_cast<const f32x4*>(&Mb[buf][kt * 32 + 8 * g4 + 4 * hh]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) st[kt][4 * g4 + e] += m4[e];
+        }
+    } else if ((t + 1) * BN > Sk) {
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -1244,13 +1276,15 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
       for (int d = 0; d < DT; ++d) acc[d] *= alpha;
       m_run = m_new;
     }
+    // (a query whose keys so far are all masked keeps m_run = -inf: its p are exp2(-inf) = 0)
+    const float m_use = KMASK && m_run == -INFINITY ? 0.f : m_run;
     float psum = 0.f;
     bf16x8 pf[2][2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kt][r], sl2, -m_run));
+        const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(st[kt][r], sl2, -m_use));
         psum += pv;
         pf[kt][r / 8][r % 8] = to_bf(pv);
       }
@@ -1265,6 +1299,7 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
         for (int d = 0; d < DT; ++d) acc[d] = mfma32(vfrag(buf, kt * 32 + 16 * c, d), pf[kt][c], acc[d]);
     lstore_k(buf ^ 1);
     lstore_v(buf ^ 1);
+    lstore_m(buf ^ 1);
     __syncthreads();
   }
 
@@ -1515,10 +1550,12 @@ static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
     if constexpr (DH == 64 || DH == 128) {
       // (buffer loads address a head's K and V rows with 32-bit byte offsets)
       const bool fits32 = a.Sk * a.k0_rs * 2 < ((int64_t)1 << 31) && a.Sk * a.v0_rs * 2 < ((int64_t)1 << 31);
-      if (a.sk0 == a.Sk && a.mask_kind == FAM_MASK_NONE && a.Sk >= 1 && fits32 && a.k0_rs >= DH &&
+      const bool kmask = a.mask_kind == FAM_MASK_BOOL && a.mqs == 0;
+      if (a.sk0 == a.Sk && (a.mask_kind == FAM_MASK_NONE || kmask) && a.Sk >= 1 && fits32 && a.k0_rs >= DH &&
           a.v0_rs >= DH) {
         const int nqb = (int)((a.Sq + 127) / 128);
-        FAM_LAUNCH((attn_long_kernel<DH>), dim3((unsigned)(nqb * bh)), dim3(256), 0, s, a, nqb);
+        if (kmask) FAM_LAUNCH((attn_long_kernel<DH, true>), dim3((unsigned)(nqb * bh)), dim3(256), 0, s, a, nqb);
+        else FAM_LAUNCH((attn_long_kernel<DH, false>), dim3((unsigned)(nqb * bh)), dim3(256), 0, s, a, nqb);
         return;
       }
     }

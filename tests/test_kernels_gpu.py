@@ -783,6 +783,26 @@ def test_attention_qk_norm_on_load_wide_heads():
     assert relerr(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("B,H,Sq,Sk,Dh,kind", [(2, 4, 200, 333, 64, "random"), (1, 24, 1560, 512, 128, "tail"),
+                                                (2, 3, 129, 300, 128, "head")])
+def test_attention_long_key_mask(B, H, Sq, Sk, Dh, kind):
+    """Video tokens over a padded context: a bool key mask shared by the queries ([B, 1, 1, Sk],
+    the cross-attention's text mask) on the long kernel.  "head" masks the first 70 keys of the
+    second sample, so its first 64-key tile is all masked (running max still -inf)."""
+    q, k, v = rnd(B, Sq, H * Dh, seed=138), rnd(B, Sk, H * Dh, seed=139), rnd(B, Sk, H * Dh, seed=140)
+    g = torch.Generator().manual_seed(141)
+    mask = torch.ones(B, 1, 1, Sk, dtype=torch.bool)
+    if kind == "random":
+        mask = torch.rand(B, 1, 1, Sk, generator=g) > 0.3
+    elif kind == "tail":
+        mask[..., Sk - 37:] = False
+    else:
+        mask[1, ..., :70] = False
+    ref = O.flash_attention(q.float(), k.float(), v.float(), H, mask)
+    y = ops().flash_attention(dev(q), dev(k), dev(v), H, ctx_mask=dev(mask))
+    assert relerr(y, ref) <= TOL
+
+
 @pytest.mark.parametrize("B,H,Sq,Sk,Dh", [(1, 8, 1560, 1560, 128), (2, 4, 200, 333, 64), (1, 2, 129, 512, 128),
                                            (1, 3, 65, 1, 128)])
 def test_attention_long_sequences(B, H, Sq, Sk, Dh):
