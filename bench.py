@@ -67,6 +67,9 @@ def parse():
                          "loop, one graph)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--traffic-from", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
+                    help="only write profiles/traffic_per_launch.txt from four rocprofv3 --pmc output directories "
+                         "(FETCH_SIZE and WRITE_SIZE over this bench, then over --copy-probe); no GPU needed")
     return ap.parse_args()
 
 
@@ -94,20 +97,103 @@ def pct(xs, q):
 # --------------------------------------------------------------------------- roofline
 # HBM traffic per launch of a kernel class, from two rocprofv3 --pmc runs of this script
 # (FETCH_SIZE, then WRITE_SIZE), each scaled by what the counter reads for the --copy-probe
-# copy of known size.  Written by hand from those runs into this text file (one line per
-# class: "<class> <bytes per launch>"); absent file or class -> traffic null.
+# copy of known size.  `bench.py --traffic-from F W CF CW` turns the four runs' counter CSVs
+# into this file: one line per class, "<class> <bytes per launch>", plus the hash of the
+# kernel sources the counters were taken on.  A file whose hash differs from the current
+# sources (or no file) gives traffic null rather than a stale figure.
 TRAFFIC_FILE = os.path.join(REPO, "profiles", "traffic_per_launch.txt")
+
+
+def sources_hash() -> str:
+    import hashlib
+    h = hashlib.sha256()
+    csrc = os.path.join(REPO, "faster-action-models_amd", "csrc")
+    for name in sorted(os.listdir(csrc)) + ["../../include/fam_hip.h"]:
+        path = os.path.join(csrc, name)
+        if name.endswith((".hip", ".h")) and os.path.isfile(path):
+            h.update(open(path, "rb").read())
+    return h.hexdigest()[:16]
 
 
 def measured_traffic(cls: str):
     try:
-        for line in open(TRAFFIC_FILE):
-            f = line.split()
-            if len(f) >= 2 and not line.startswith("#") and f[0] == cls:
-                return int(float(f[1]))
+        lines = open(TRAFFIC_FILE).read().splitlines()
     except OSError:
-        pass
+        return None
+    if not any(l.startswith("# sources ") and l.split()[2] == sources_hash() for l in lines):
+        return None
+    for line in lines:
+        f = line.split()
+        if len(f) >= 2 and not line.startswith("#") and f[0] == cls:
+            return int(float(f[1]))
     return None
+
+
+# library kernel name (rocprofv3's Kernel_Name, "fam::<name>...") -> bench.py's kernel class
+_KERNEL_CLASSES = [("final_kernel", "gemm_final"), ("partial", "gemm_partial"), ("rowop", "rowop"),
+                   ("attn_combine", "attn_combine"), ("attn_", "attention"), ("rmsnorm_rope", "rmsnorm_rope"),
+                   ("add_mod", "modulation"), ("sinusoid", "sinusoid"), ("big_kernel", "gemm"),
+                   ("skinny_kernel", "gemm"), ("tiled_kernel", "gemm"), ("euler", "euler"), ("adaln", "adaln")]
+
+
+def _kernel_class(name: str):
+    if not name.startswith(("fam::", "void fam::")):
+        return None
+    base = name.split("fam::", 1)[1]
+    for key, cls in _KERNEL_CLASSES:
+        if base.startswith(key):
+            return cls
+    return None
+
+
+def traffic_from(fetch_dir: str, write_dir: str, cfetch_dir: str, cwrite_dir: str):
+    """Writes TRAFFIC_FILE from the counter CSVs of the four rocprofv3 runs (each directory holds
+    one *counter_collection.csv): FETCH_SIZE / WRITE_SIZE over this bench, and over --copy-probe.
+    Per class: the dispatch-weighted mean of fetch * sf + write * sw, where sf, sw turn the KiB
+    counters into bytes so that the 256 MiB probe copy reads and writes 256 MiB."""
+    import csv
+    import glob
+    from collections import defaultdict
+
+    def load(d, counter):
+        path = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if not path:
+            raise SystemExit(f"no counter_collection.csv under {d}")
+        per = defaultdict(list)
+        for r in csv.DictReader(open(path[0])):
+            if r["Counter_Name"] == counter:
+                per[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+        return per
+
+    probe = 256 << 20
+    cf, cw = load(cfetch_dir, "FETCH_SIZE"), load(cwrite_dir, "WRITE_SIZE")
+    copy_f = [max(v) for k, v in cf.items() if "copy" in k.lower()]
+    copy_w = [max(v) for k, v in cw.items() if "copy" in k.lower()]
+    if not copy_f or not copy_w:
+        raise SystemExit("no copy kernel in the probe runs")
+    sf, sw = probe / (max(copy_f) * 1024), probe / (max(copy_w) * 1024)
+    fetch, write = load(fetch_dir, "FETCH_SIZE"), load(write_dir, "WRITE_SIZE")
+    tot, cnt, rows = defaultdict(float), defaultdict(int), []
+    for name in sorted(fetch, key=lambda n: -len(fetch[n])):
+        cls = _kernel_class(name)
+        if cls is None or name not in write:
+            continue
+        n = min(len(fetch[name]), len(write[name]))
+        fk, wk = sum(fetch[name][:n]) / n, sum(write[name][:n]) / n
+        b = fk * 1024 * sf + wk * 1024 * sw
+        tot[cls] += b * n
+        cnt[cls] += n
+        rows.append((name.split("(")[0], cls, n, fk, wk, b))
+    with open(TRAFFIC_FILE, "w") as f:
+        f.write("# HBM bytes per launch per kernel class, config 1 B=1: FETCH_SIZE x%.4f + WRITE_SIZE x%.4f "
+                "(KiB -> bytes, calibrated on the 256 MiB copy), written by bench.py --traffic-from\n" % (sf, sw))
+        f.write(f"# sources {sources_hash()}\n")
+        for cls in sorted(tot, key=lambda c: -tot[c]):
+            f.write(f"{cls} {int(round(tot[cls] / cnt[cls]))}\n")
+    print(f"| kernel | class | dispatches | FETCH KiB | WRITE KiB | bytes / dispatch |\n|---|---|---|---|---|---|")
+    for name, cls, n, fk, wk, b in rows:
+        print(f"| `{name}` | {cls} | {n} | {fk:.1f} | {wk:.1f} | {int(b)} |")
+    print(f"scale factors: FETCH x{sf:.4f}, WRITE x{sw:.4f}; wrote {TRAFFIC_FILE}")
 
 
 def copy_probe():
@@ -172,6 +258,23 @@ def kernel_breakdown(model, calls: int = 3):
 
 
 # --------------------------------------------------------------------------- CPU baseline (oracle)
+def cpu_description() -> str:
+    """The host CPU as /proc/cpuinfo names it: model name, family / model / stepping, cache,
+    clock of the first logical CPU, and the logical CPUs this process may use."""
+    info = {}
+    try:
+        for line in open("/proc/cpuinfo"):
+            if not line.strip():
+                break
+            k, _, v = line.partition(":")
+            info.setdefault(k.strip(), v.strip())
+    except OSError:
+        return "unknown"
+    return (f"{info.get('model name', 'unknown')} (family {info.get('cpu family', '?')}, model {info.get('model', '?')}, "
+            f"stepping {info.get('stepping', '?')}, {info.get('cache size', '?')} cache, {info.get('cpu MHz', '?')} MHz; "
+            f"{len(os.sched_getaffinity(0))} of {os.cpu_count()} logical CPUs usable)")
+
+
 def cpu_baseline(batch: int, budget_s: float):
     import torch
     from oracle import fam_oracle as O
@@ -192,7 +295,8 @@ def cpu_baseline(batch: int, budget_s: float):
             x = x + O.action_dit_forward(p, cfg, x, t.reshape(1), ctx.expand(batch, -1, -1), context_emb=emb) * d
         return x
 
-    call(1)  # warmup: one step
+    for _ in range(3):   # warmup: three full policy calls
+        call()
     times = []
     t_begin = time.perf_counter()
     while True:
@@ -201,18 +305,11 @@ def cpu_baseline(batch: int, budget_s: float):
         times.append((time.perf_counter() - t0) * 1e3)
         if time.perf_counter() - t_begin + times[-1] / 1e3 > budget_s or len(times) >= 20:
             break
-    model = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    model = cpu_description()
     return {"value": round(statistics.median(times), 1), "unit": "ms per policy call", "cores": cores,
             "kind": "port", "cpu_model": model, "min_ms": round(min(times), 1),
             "sample": f"{len(times)} full policy calls (config 1, B={batch}, fp32 oracle, 12 blocks x 10 steps, "
-                      f"context K/V recomputed per block and step as the reference does) after a 1-step warmup"}
+                      f"context K/V recomputed per block and step as the reference does) after 3 warmup calls"}
 
 
 # --------------------------------------------------------------------------- eager GPU reference
@@ -291,7 +388,7 @@ class EagerReference:
         return x
 
 
-def eager_gpu_baseline(cfg, params, noise, ctx, warmup=3, iters=10):
+def eager_gpu_baseline(cfg, params, noise, ctx, warmup=25, iters=40):
     import torch
     dev = torch.device("cuda")
     ref = EagerReference(cfg, params, dev)
@@ -858,6 +955,9 @@ def main():
               "launches and this build ships no multi-GPU path (see the sharding notes in DESIGN.md). "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+    if args.traffic_from:
+        traffic_from(*args.traffic_from)
+        return
     import torch
     from fam.action_dit import FusedActionDiT, synthetic_params
 

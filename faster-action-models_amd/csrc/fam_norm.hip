@@ -22,9 +22,10 @@ struct AdalnArgs {
 };
 
 // AFF: the LayerNorm affine is present.  MOD: no AdaLN shift-scale (0), one per row (1, an
-// HBM stream: loaded with x), or one per batch (2, an L2-resident row: loaded in one batch
-// after the statistics, so its registers do not cost occupancy while x is in flight).  Compile-time,
-// because occupancy is what keeps HBM busy here.
+// HBM stream: loaded with x), or one per batch (2, an L2-resident row, loaded after the
+// statistics).  Both modulated forms hold NV shift and NV scale vectors next to x (about 96
+// registers at NV = 8), so they run at the same occupancy; compile-time, because occupancy is
+// what keeps HBM busy here.
 template <int NV, bool AFF, int MOD>
 __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
   const int lane = threadIdx.x & 63;

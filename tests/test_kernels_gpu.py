@@ -41,7 +41,8 @@ def relerr(y, ref):
 
 # --------------------------------------------------------------------------- AdaLN / LayerNorm
 @pytest.mark.parametrize("B,S,D,per_token", [(1, 32, 1024, False), (2, 7, 3072, True), (1, 5, 32, False),
-                                              (3, 17, 2048, False), (1, 3, 8192, False), (2, 4, 6144, True)])
+                                              (3, 17, 2048, False), (1, 3, 8192, False), (2, 4, 6144, True),
+                                              (2, 64, 3072, False), (2, 33, 4096, False)])
 def test_adaln(B, S, D, per_token):
     x = rnd(B, S, D, seed=1, scale=2.0) + 0.3
     Sm = S if per_token else 1
