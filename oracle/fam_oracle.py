@@ -34,6 +34,8 @@ Pinning (what checks each function, see ``tests/test_oracle.py``):
                             golden vectors written by tests/golden/make_golden.py from
                             the reference modules themselves (tiny seeded configs)
   mot_action_forward        golden vectors from the reference MoT (tiny seeded config)
+  wan_vae_encode_first_frame golden vectors from the reference VideoVAE38_.encode (tiny seeded
+                            config, two image sizes) + planted slips; vae_avg_down closed forms
 """
 from __future__ import annotations
 
@@ -965,3 +967,176 @@ def d4d_predict_action(p: Params, cfg: DiT4DiTHeadConfig, vl_embs: torch.Tensor,
         pred = d4d_mlp(p, "action_decoder.", out)
         actions = actions - dt * pred[:, -cfg.horizon:]
     return actions
+
+
+# ---------------------------------------------------------------------------
+# Wan2.2 VAE (VAE38) encoder, first frame only (fp32)
+# ---------------------------------------------------------------------------
+@dataclass
+class WanVaeConfig:
+    """VideoVAE38_'s encoder shape (FB/wan_video_vae.py:1272-1295, Encoder3d_38 :619-676):
+    dims = dim * [1] + dim_mult, two residual blocks per level, spatial /2 after every level
+    but the last, temporal /2 after levels 1 and 2 (inert on the first frame)."""
+    dim: int = 160
+    z_dim: int = 48
+    dim_mult: Tuple[int, ...] = (1, 2, 4, 4)
+    num_res_blocks: int = 2
+    temporal_downsample: Tuple[bool, ...] = (False, True, True)
+
+    def dims(self) -> List[int]:
+        return [self.dim * u for u in (1,) + tuple(self.dim_mult)]
+
+
+def wan_vae_param_shapes(cfg: WanVaeConfig) -> Dict[str, Tuple[int, ...]]:
+    """The encoder's state-dict entries that the first frame reads, under the reference's names
+    (VideoVAE38_ state dict: "encoder.*", "conv1.*").  The downsample3d time_conv weights exist
+    in the checkpoint but never run on the first chunk (Resample.forward, FB/wan_video_vae.py:162-167)."""
+    d = cfg.dims()
+    s = {"encoder.conv1.weight": (d[0], 12, 3, 3, 3), "encoder.conv1.bias": (d[0],)}
+
+    def res(pre, ci, co):
+        s[pre + "residual.0.gamma"] = (ci, 1, 1, 1)
+        s[pre + "residual.2.weight"] = (co, ci, 3, 3, 3)
+        s[pre + "residual.2.bias"] = (co,)
+        s[pre + "residual.3.gamma"] = (co, 1, 1, 1)
+        s[pre + "residual.6.weight"] = (co, co, 3, 3, 3)
+        s[pre + "residual.6.bias"] = (co,)
+        if ci != co:
+            s[pre + "shortcut.weight"] = (co, ci, 1, 1, 1)
+            s[pre + "shortcut.bias"] = (co,)
+
+    for i, (ci, co) in enumerate(zip(d[:-1], d[1:])):
+        pre = f"encoder.downsamples.{i}.downsamples."
+        for j in range(cfg.num_res_blocks):
+            res(f"{pre}{j}.", ci if j == 0 else co, co)
+        if i != len(cfg.dim_mult) - 1:
+            s[f"{pre}{cfg.num_res_blocks}.resample.1.weight"] = (co, co, 3, 3)
+            s[f"{pre}{cfg.num_res_blocks}.resample.1.bias"] = (co,)
+    c = d[-1]
+    res("encoder.middle.0.", c, c)
+    s["encoder.middle.1.norm.gamma"] = (c, 1, 1)
+    s["encoder.middle.1.to_qkv.weight"] = (3 * c, c, 1, 1)
+    s["encoder.middle.1.to_qkv.bias"] = (3 * c,)
+    s["encoder.middle.1.proj.weight"] = (c, c, 1, 1)
+    s["encoder.middle.1.proj.bias"] = (c,)
+    res("encoder.middle.2.", c, c)
+    s["encoder.head.0.gamma"] = (c, 1, 1, 1)
+    s["encoder.head.2.weight"] = (2 * cfg.z_dim, c, 3, 3, 3)
+    s["encoder.head.2.bias"] = (2 * cfg.z_dim,)
+    s["conv1.weight"] = (2 * cfg.z_dim, 2 * cfg.z_dim, 1, 1, 1)
+    s["conv1.bias"] = (2 * cfg.z_dim,)
+    return s
+
+
+def init_wan_vae_params(cfg: WanVaeConfig, seed: int, std: float = 0.125) -> Params:
+    """Seeded weights: convolutions N(0, std) scaled by 1/sqrt(fan_in / 64) (unit-scale outputs at
+    the default std), biases N(0, std), RMS_norm gammas N(1, 0.2) (away from the identity, so that
+    a misplaced gamma shows)."""
+    g = torch.Generator().manual_seed(seed)
+    out = {}
+    for k, shape in wan_vae_param_shapes(cfg).items():
+        if k.endswith("gamma"):
+            out[k] = 1.0 + 0.2 * torch.randn(shape, generator=g)
+        elif k.endswith("weight"):
+            fan_in = math.prod(shape[1:])
+            out[k] = torch.randn(shape, generator=g) * std / math.sqrt(max(fan_in, 64) / 64)
+        else:
+            out[k] = torch.randn(shape, generator=g) * std
+    return out
+
+
+def vae_patchify(x: torch.Tensor, patch: int = 2) -> torch.Tensor:
+    """FB/wan_video_vae.py:196-208 on an image: 'b c (h q) (w r) -> b (c r q) h w'."""
+    b, c, h, w = x.shape
+    x = x.reshape(b, c, h // patch, patch, w // patch, patch)          # b c h q w r
+    return x.permute(0, 1, 5, 3, 2, 4).reshape(b, c * patch * patch, h // patch, w // patch)
+
+
+def vae_rms_norm(x: torch.Tensor, gamma: torch.Tensor) -> torch.Tensor:
+    """RMS_norm (FB/wan_video_vae.py:55-70), channel-first: F.normalize over the channels
+    (x / max(||x||_2, 1e-12)) * sqrt(C) * gamma."""
+    return F.normalize(x, dim=1) * (x.shape[1] ** 0.5) * gamma.reshape(1, -1, 1, 1)
+
+
+def vae_causal_conv_first(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """CausalConv3d (FB/wan_video_vae.py:33-52) on a single frame with no cache: the temporal
+    padding is 2*pad zero frames in front, so only the last temporal tap sees the frame and the
+    layer is a 2-D convolution with weight[:, :, -1] and 'same' spatial padding."""
+    k = w.shape[-1]
+    return F.conv2d(x, w[:, :, -1], b, padding=k // 2)
+
+
+def vae_residual_block(p: Params, pre: str, x: torch.Tensor) -> torch.Tensor:
+    """ResidualBlock (FB/wan_video_vae.py:267-301): shortcut (1x1x1 conv when the width changes)
+    + [RMS_norm, SiLU, conv 3x3x3, RMS_norm, SiLU, (dropout), conv 3x3x3]."""
+    h = x
+    if pre + "shortcut.weight" in p:
+        h = vae_causal_conv_first(x, p[pre + "shortcut.weight"], p[pre + "shortcut.bias"])
+    y = F.silu(vae_rms_norm(x, p[pre + "residual.0.gamma"]))
+    y = vae_causal_conv_first(y, p[pre + "residual.2.weight"], p[pre + "residual.2.bias"])
+    y = F.silu(vae_rms_norm(y, p[pre + "residual.3.gamma"]))
+    y = vae_causal_conv_first(y, p[pre + "residual.6.weight"], p[pre + "residual.6.bias"])
+    return y + h
+
+
+def vae_avg_down(x: torch.Tensor, out_channels: int, factor_t: int, factor_s: int) -> torch.Tensor:
+    """AvgDown3D (FB/wan_video_vae.py:345-395) on one frame: the frame axis is front-padded with
+    factor_t - 1 zero frames, space-time blocks of factor_t x factor_s^2 become channels
+    (index c * F + t * fs^2 + i * fs + j), and each output channel is the mean of a group of
+    C * F / out_channels consecutive ones."""
+    b, c, h, w = x.shape
+    f = factor_t * factor_s * factor_s
+    xt = x.unsqueeze(2)
+    if factor_t > 1:
+        xt = torch.cat([torch.zeros(b, c, factor_t - 1, h, w, dtype=x.dtype), xt], 2)
+    xt = xt.reshape(b, c, 1, factor_t, h // factor_s, factor_s, w // factor_s, factor_s)
+    xt = xt.permute(0, 1, 3, 5, 7, 2, 4, 6).reshape(b, c * f, h // factor_s, w // factor_s)
+    return xt.reshape(b, out_channels, c * f // out_channels, h // factor_s, w // factor_s).mean(dim=2)
+
+
+def vae_attention_block(p: Params, pre: str, x: torch.Tensor) -> torch.Tensor:
+    """AttentionBlock (FB/wan_video_vae.py:304-342): one head over the frame's h*w tokens with
+    the full channel width, q | k | v = consecutive channel blocks of to_qkv."""
+    b, c, h, w = x.shape
+    y = vae_rms_norm(x, p[pre + "norm.gamma"])
+    qkv = F.conv2d(y, p[pre + "to_qkv.weight"], p[pre + "to_qkv.bias"])           # b 3c h w
+    qkv = qkv.reshape(b, 3 * c, h * w).transpose(1, 2)                             # b hw 3c
+    q, k, v = qkv[..., :c], qkv[..., c:2 * c], qkv[..., 2 * c:]
+    o = attention(q.unsqueeze(1), k.unsqueeze(1), v.unsqueeze(1)).squeeze(1)       # b hw c
+    o = o.transpose(1, 2).reshape(b, c, h, w)
+    return F.conv2d(o, p[pre + "proj.weight"], p[pre + "proj.bias"]) + x
+
+
+def wan_vae_encode_first_frame(p: Params, cfg: WanVaeConfig, image: torch.Tensor, mean: torch.Tensor,
+                               std: torch.Tensor) -> torch.Tensor:
+    """VideoVAE38_.encode (FB/wan_video_vae.py:1299-1323) of a single frame image [B, 3, H, W]
+    (FB/fastwam.py:256-268 encodes the first frame this way): patchify 2x2, Encoder3d_38.forward
+    (:678-732) on the first chunk, conv1, mu = first z_dim channels, (mu - mean) / std.
+    Returns [B, z_dim, 1, H / 16, W / 16]."""
+    d = cfg.dims()
+    x = vae_patchify(image, 2)
+    x = vae_causal_conv_first(x, p["encoder.conv1.weight"], p["encoder.conv1.bias"])
+    nlev = len(cfg.dim_mult)
+    for i, (ci, co) in enumerate(zip(d[:-1], d[1:])):
+        pre = f"encoder.downsamples.{i}.downsamples."
+        x_copy = x
+        for j in range(cfg.num_res_blocks):
+            x = vae_residual_block(p, f"{pre}{j}.", x)
+        down = i != nlev - 1
+        t_down = cfg.temporal_downsample[i] if i < len(cfg.temporal_downsample) else False
+        if down:
+            # Resample38 downsample2d / downsample3d (FB/wan_video_vae.py:245-262, :158-175):
+            # ZeroPad2d((0, 1, 0, 1)) + 3x3 stride-2 conv; the time_conv waits for a second chunk
+            x = F.conv2d(F.pad(x, (0, 1, 0, 1)), p[f"{pre}{cfg.num_res_blocks}.resample.1.weight"],
+                         p[f"{pre}{cfg.num_res_blocks}.resample.1.bias"], stride=2)
+        # Down_ResidualBlock (FB/wan_video_vae.py:442-474): + AvgDown3D of the level's input
+        x = x + vae_avg_down(x_copy, co, 2 if t_down else 1, 2 if down else 1)
+    x = vae_residual_block(p, "encoder.middle.0.", x)
+    x = vae_attention_block(p, "encoder.middle.1.", x)
+    x = vae_residual_block(p, "encoder.middle.2.", x)
+    x = F.silu(vae_rms_norm(x, p["encoder.head.0.gamma"]))
+    x = vae_causal_conv_first(x, p["encoder.head.2.weight"], p["encoder.head.2.bias"])
+    x = F.conv2d(x, p["conv1.weight"][:, :, 0], p["conv1.bias"])
+    mu = x[:, :cfg.z_dim]
+    mu = (mu - mean.reshape(1, -1, 1, 1)) * (1.0 / std).reshape(1, -1, 1, 1)
+    return mu.unsqueeze(2)

@@ -521,3 +521,85 @@ def test_golden_wan_detects_planted_mistakes(wan_golden, wan_params):
     vmask = O.mot_joint_mask(12, 0, 6)
     y = O.wan_forward(p2, WAN_TINY, x, t, c, cm, vmask)
     assert not torch.allclose(y, g["forward.fp32"], rtol=2e-5, atol=2e-5)
+
+
+# --------------------------------------------------------------------------- Wan2.2 VAE encoder
+VAE_TINY = O.WanVaeConfig(dim=16, z_dim=8)
+
+
+@pytest.fixture(scope="module")
+def vae_golden():
+    return load_file(os.path.join(os.path.dirname(__file__), "golden", "wan_vae_tiny.safetensors"))
+
+
+@pytest.fixture(scope="module")
+def vae_params(vae_golden):
+    p = O.init_wan_vae_params(VAE_TINY, int(vae_golden["meta.seed"][0]))
+    assert math.isclose(_checksum(p), float(vae_golden["meta.param_checksum"][0]), rel_tol=0, abs_tol=1e-9)
+    return p
+
+
+def _vae(g, p, name, **kw):
+    return O.wan_vae_encode_first_frame(p, VAE_TINY, g[f"in.image.{name}"], g["in.mean"], g["in.std"], **kw)
+
+
+@pytest.mark.parametrize("name", ["a", "b"])
+def test_golden_wan_vae_encode_first_frame(vae_golden, vae_params, name):
+    """The oracle's first-frame encode against VideoVAE38_.encode (64 x 128 and 48 x 80 images)."""
+    y = _vae(vae_golden, vae_params, name)
+    ref = vae_golden[f"out.mu.{name}"]
+    assert y.shape == ref.shape
+    assert torch.allclose(y, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_golden_wan_vae_detects_planted_mistakes(vae_golden, vae_params, monkeypatch):
+    """Plausible slips fail the goldens: the patchify's sub-pixel order transposed (c q r instead
+    of c r q), the AvgDown3D shortcut without its zero frame, the two RMS_norm gammas of a
+    residual block swapped, and the attention's k and q swapped."""
+    g, p = vae_golden, vae_params
+    ref = g["out.mu.a"]
+    close = lambda y: torch.allclose(y, ref, rtol=1e-4, atol=1e-4)   # noqa: E731
+    assert close(_vae(g, p, "a"))
+
+    def patch_cqr(x, patch=2):
+        b, c, h, w = x.shape
+        x = x.reshape(b, c, h // patch, patch, w // patch, patch)
+        return x.permute(0, 1, 3, 5, 2, 4).reshape(b, c * patch * patch, h // patch, w // patch)
+    with monkeypatch.context() as m:
+        m.setattr(O, "vae_patchify", patch_cqr)
+        assert not close(_vae(g, p, "a"))
+
+    real_avg = O.vae_avg_down
+
+    def avg_no_zero_frame(x, out_channels, factor_t, factor_s):
+        return real_avg(x, out_channels, 1, factor_s) if factor_t == 1 else \
+            real_avg(torch.cat([x, x], 1), out_channels, 1, factor_s)
+    with monkeypatch.context() as m:
+        m.setattr(O, "vae_avg_down", avg_no_zero_frame)
+        assert not close(_vae(g, p, "a"))
+
+    p2 = dict(p)
+    pre = "encoder.downsamples.0.downsamples.1."
+    p2[pre + "residual.0.gamma"], p2[pre + "residual.3.gamma"] = p[pre + "residual.3.gamma"], p[pre + "residual.0.gamma"]
+    assert not close(_vae(g, p2, "a"))
+
+    real_att = O.attention
+
+    def att_kq(q, k, v, mask=None, scale=None):
+        return real_att(k, q, v, mask, scale)
+    with monkeypatch.context() as m:
+        m.setattr(O, "attention", att_kq)
+        assert not close(_vae(g, p, "a"))
+
+
+def test_wan_vae_avg_down_closed_forms():
+    """AvgDown3D on one frame: factor_t 1 / factor_s 2 with out = in channels is a 2x2 average
+    pool; factor_t 2 doubles the channels, even outputs averaging the zero frame (0), odd
+    outputs the 2x2 pool of channel o // 2; factor 1 is the identity."""
+    x = torch.randn(1, 6, 4, 8, generator=torch.Generator().manual_seed(3))
+    pool = F.avg_pool2d(x, 2)
+    assert torch.allclose(O.vae_avg_down(x, 6, 1, 2), pool, atol=1e-6)
+    y = O.vae_avg_down(x, 12, 2, 2)
+    assert torch.equal(y[:, 0::2], torch.zeros_like(y[:, 0::2]))
+    assert torch.allclose(y[:, 1::2], pool, atol=1e-6)
+    assert torch.equal(O.vae_avg_down(x, 6, 1, 1), x)
