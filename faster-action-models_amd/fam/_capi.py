@@ -139,6 +139,12 @@ SIGNATURES = {
     "fam_patchify": (C.c_int, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     "fam_unpatchify": (C.c_int, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     "fam_gather_rows": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "fam_vae_patch_im2col": (C.c_int, [_vp, _i64, _i64, _vp, _i64, _vp]),
+    "fam_im2col3x3": (C.c_int, [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp]),
+    "fam_chan_rmsnorm": (C.c_int, [_vp, _i64, _i64, _i64, _vp, C.c_int, _vp, _i64, _vp]),
+    "fam_vae_avgdown": (C.c_int, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
+    "fam_softmax_rows": (C.c_int, [_vp, _i64, _i64, _i64, C.c_float, _vp, _i64, _vp]),
+    "fam_chan_affine_nchw": (C.c_int, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
 }
 
 _lib = None

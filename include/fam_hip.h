@@ -401,6 +401,72 @@ int fam_unpatchify(const void* y, int64_t B, int64_t C, int64_t f, int64_t h, in
 int fam_gather_rows(const void* src, int64_t ld_src, int64_t src_rows, const int32_t* idx, void* dst,
                     int64_t ld_dst, int64_t rows, int64_t cols, void* stream);
 
+/* ------------------------------------------------------------------ Wan2.2 VAE encoder (first frame)
+ * Activations are channels-last rows (one row per pixel, [h*w, C] bf16); the convolutions are
+ * fam_gemm calls over these rows (1x1) or over an im2col operand (3x3) whose row is the pixel's
+ * neighbourhood with the taps outermost, (kh*3 + kw)*C + c, zero-padded to kpad columns.  The
+ * reference's causal 3-D convolutions see only their last temporal tap on the first frame
+ * (two zero frames in front, no cache): CausalConv3d FB/wan_video_vae.py:33-52.
+ */
+
+/*
+ * fam_vae_patch_im2col -- conv1's operand straight from the image: img [3, H, W] bf16
+ * (channel-first), patchified 2x2 to 12 channels c*4 + r*2 + q ('b c (h q) (w r) -> b (c r q) h w')
+ * and gathered as the 3x3 neighbourhoods of the (H/2) x (W/2) grid: out [(H/2)*(W/2), 128],
+ * columns (kh*3 + kw)*12 + channel, columns 108..127 zero.
+ * Replaces: patchify FB/wan_video_vae.py:196-208 + Encoder3d_38.conv1's input :650, :680-695.
+ */
+int fam_vae_patch_im2col(const void* img, int64_t H, int64_t W, void* out, int64_t ldo, void* stream);
+
+/*
+ * fam_im2col3x3 -- out[p, (kh*3 + kw)*C + c] = x[y, x', c] around output pixel p of the H x W
+ * channels-last grid x (row stride ldx); stride 1: 'same' zero padding (CausalConv3d's spatial
+ * padding); stride 2: zero padding at the bottom / right only and (H/2) x (W/2) outputs
+ * (ZeroPad2d((0, 1, 0, 1)) + Conv2d(3, stride 2) of Resample38 FB/wan_video_vae.py:245-262).
+ * Columns 9*C..kpad-1 are zero.
+ * Limits: C, ldx, kpad, ldo multiples of 8, kpad >= 9*C; 16-byte aligned; stride 2 needs even H, W.
+ */
+int fam_im2col3x3(const void* x, int64_t ldx, int64_t H, int64_t W, int64_t C, int64_t stride, void* out,
+                  int64_t ldo, int64_t kpad, void* stream);
+
+/*
+ * fam_chan_rmsnorm -- y = act(x / max(||x||_2, 1e-12) * sqrt(C) * gamma) per row of C channels
+ * (act FAM_ACT_NONE or FAM_ACT_SILU).
+ * Replaces: RMS_norm FB/wan_video_vae.py:55-70 (channel_first, bias-free) and the nn.SiLU that
+ *           follows it in ResidualBlock :274-278 and the encoder head :670-674.
+ * Limits: C and strides multiples of 8; 16-byte aligned.
+ */
+int fam_chan_rmsnorm(const void* x, int64_t ldx, int64_t rows, int64_t C, const void* gamma, int act, void* y,
+                     int64_t ldy, void* stream);
+
+/*
+ * fam_vae_avgdown -- AvgDown3D of one frame: x [H*W, Cin] channels-last; the frame axis is
+ * front-padded with ft - 1 zero frames, ft x fs x fs blocks fold into channels c*F + t*fs*fs +
+ * i*fs + j (F = ft*fs*fs) and output channel o is the mean of group [o*G, (o+1)*G), G =
+ * Cin*F/Cout: out [(H/fs)*(W/fs), Cout], plus add [same layout, row stride ld_add] when non-null
+ * (the sum with the last residual block's shortcut on a level without downsampling).
+ * Replaces: AvgDown3D.forward FB/wan_video_vae.py:345-395 (the Down_ResidualBlock shortcut :442-474).
+ * Limits: ft, fs in {1, 2}; fs divides H and W; Cout divides Cin*F.
+ */
+int fam_vae_avgdown(const void* x, int64_t ldx, int64_t H, int64_t W, int64_t Cin, int64_t Cout, int64_t ft,
+                    int64_t fs, const void* add, int64_t ld_add, void* out, int64_t ldo, void* stream);
+
+/*
+ * fam_softmax_rows -- p = softmax(scale * s) per row, fp32 scores in, bf16 out.
+ * Replaces: the softmax of the single-head F.scaled_dot_product_attention in AttentionBlock
+ *           FB/wan_video_vae.py:321-342 (scores and P V are fam_gemm products around it).
+ */
+int fam_softmax_rows(const float* s, int64_t lds, int64_t rows, int64_t cols, float scale, void* p, int64_t ldp,
+                     void* stream);
+
+/*
+ * fam_chan_affine_nchw -- out[c, p] = (x[p, c] - mean[c]) * inv_std[c]: the latent normalisation
+ * of VideoVAE38_.encode with the channels-last rows written channel-first; mean and inv_std fp32.
+ * Replaces: mu = (mu - scale[0]) * scale[1], FB/wan_video_vae.py:1313-1319.
+ */
+int fam_chan_affine_nchw(const void* x, int64_t ldx, int64_t P, int64_t C, const float* mean, const float* inv_std,
+                         void* out, void* stream);
+
 /*
  * fam_add_modulation -- out[t, l, :] = bf16(modulation[l, :] + t_mod[t, :]) for every
  * denoise step t < T and block l < L, vectors of length n (= 6 * hidden): the
