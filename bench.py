@@ -758,37 +758,75 @@ def _time_calls(run, steps, warmup):
     return statistics.median(times), min(times), sorted(times)[int(0.9 * (len(times) - 1))]
 
 
+def _vae_params(dev, g, cfg):
+    """Synthetic Wan2.2 VAE38 encoder weights (unit-scale convolutions, gammas N(1, 0.2))."""
+    import torch
+    from fam.vae import encoder_param_shapes
+    out = {}
+    for k, shape in encoder_param_shapes(cfg).items():
+        t = torch.randn(*shape, generator=g, device=dev, dtype=torch.float32)
+        if k.endswith("gamma"):
+            t = 1.0 + 0.2 * t
+        elif k.endswith("weight"):
+            t = t / math.sqrt(math.prod(shape[1:]))
+        else:
+            t = 0.02 * t
+        out[k] = t.to(torch.bfloat16)
+    return out
+
+
 def bench_fastwam(args):
-    """One FastWAM policy call at the reference model's real shape (FB/fastwam.py:924-1073),
-    without the first-frame VAE encode: the MoT video K/V prefill (30 video blocks, hidden 3072,
-    24 x 128 heads, FFN 14336, 98 video tokens, 129 context tokens) followed by the 10-step
-    flow-matching loop of the action expert (30 blocks, hidden 1024, attention 24 x 128 = 3072
-    wide, FFN 4096, 32 x 7 chunk) whose self-attention runs over [that layer's cached video
-    K/V ; action K/V] (Sk = 130, every key attended, as infer_action's mask), cross-attending to
-    the 129 context tokens (128 text tokens of width 4096 + the proprio token).  The prefill's
-    K/V buffers are read in place by the loop, and the whole call is one captured graph."""
+    """One FastWAM policy call, FastWAM.infer_action (FB/fastwam.py:924-1073), at the reference
+    model's real shape, B=1, one captured graph:
+      1. the Wan2.2 VAE38 encode of the first frame (224 x 448 image -> 48 x 14 x 28 latent,
+         FB/fastwam.py:980 -> :256-268);
+      2. the video expert's pre_dit of that latent frame at t = 0 (7 x 14 patches = 98 tokens,
+         129 context tokens of width 4096) and the MoT K/V prefill through its 30 blocks (hidden
+         3072, 24 x 128 heads, FFN 14336; FB/fastwam.py:1018-1041);
+      3. the 10-step flow-matching loop of the action expert (30 blocks, hidden 1024, attention
+         24 x 128 = 3072 wide, FFN 4096, 32 x 7 chunk) whose self-attention runs over [that
+         layer's cached video K/V ; action K/V] (Sk = 130, every key attended, as infer_action's
+         mask), cross-attending to the same 129 context tokens.
+    The latent is read by pre_dit through one device copy; the prefill's K/V buffers are read in
+    place by the loop.  (The text encoder and the proprio encoder run before the call and are
+    outside the reference's timed loop too.)"""
     import torch
     from fam.action_dit import ActionDiTConfig, FusedActionDiT
+    from fam.vae import FusedWanVAEEncoder, WanVaeConfig
+    from fam.video_dit import FusedWanVideoDiT
     dev = torch.device("cuda:0")
-    L, H, nh, Dh, F, Sv, Lc = 30, 3072, 24, 128, 14336, 98, 129
-    pf = _real_video_prefill(dev, L, H, nh, Dh, F, Sv, Lc)
-    acfg = ActionDiTConfig(hidden_dim=1024, action_dim=7, ffn_dim=4096, text_dim=4096, freq_dim=256, num_heads=nh,
-                           attn_head_dim=Dh, num_layers=L)
+    L, H, nh, Dh, F, Lc, T = 30, 3072, 24, 128, 14336, 129, 4096
+    IH, IW = 224, 448
     g = torch.Generator(device=dev).manual_seed(8765)
-    ap = _block_params(dev, g, L, 1024, nh * Dh, 4096, text_dim=4096, action_dim=7)
+    vcfg = WanVaeConfig()
+    vae = FusedWanVAEEncoder(vcfg, _vae_params(dev, g, vcfg), height=IH, width=IW, device=dev)
+    wcfg = _WanCfg(hidden_dim=H, in_dim=48, ffn_dim=F, out_dim=48, text_dim=T, freq_dim=256, eps=1e-6,
+                   patch_size=(1, 2, 2), num_heads=nh, attn_head_dim=Dh, num_layers=L)
+    lh, lw = vae.latent_hw
+    video = FusedWanVideoDiT(wcfg, _wan_params(dev, g, wcfg), batch=1, frames=1, height=lh, width=lw, ctx_len=Lc,
+                             mode="prefill", device=dev)
+    torch.cuda.empty_cache()
+    Sv = video.S
+    acfg = ActionDiTConfig(hidden_dim=1024, action_dim=7, ffn_dim=4096, text_dim=T, freq_dim=256, num_heads=nh,
+                           attn_head_dim=Dh, num_layers=L)
+    ap = _block_params(dev, g, L, 1024, nh * Dh, 4096, text_dim=T, action_dim=7)
     am = FusedActionDiT(acfg, ap, batch=1, seq_len=32, ctx_len=Lc, num_steps=10, shift=5.0, device=dev,
-                        video_len=Sv, video_kv=pf.kv_cache())
+                        video_len=Sv, video_kv=video.kv_cache())
     del ap
     torch.cuda.empty_cache()
     gi = torch.Generator("cpu").manual_seed(99)
-    pf.set_inputs(torch.randn(1, Sv, H, generator=gi).to(dev, torch.bfloat16),
-                  (torch.randn(1, Sv, 6, H, generator=gi) * 0.2).to(dev, torch.bfloat16),
-                  torch.randn(1, Lc, H, generator=gi).to(dev, torch.bfloat16))
-    am.set_inputs(torch.randn(1, 32, 7, generator=gi).to(dev, torch.bfloat16),
-                  torch.randn(Lc, 4096, generator=gi).to(dev, torch.bfloat16))
+    image = torch.rand(1, 3, IH, IW, generator=gi) * 2 - 1
+    ctx = torch.randn(1, Lc, T, generator=gi).to(dev, torch.bfloat16)
+    vae.set_input(image.to(dev))
+    video.set_inputs(torch.zeros(1, 48, 1, lh, lw, dtype=torch.bfloat16, device=dev), torch.zeros(1), ctx)
+    am.set_inputs(torch.randn(1, 32, 7, generator=gi).to(dev, torch.bfloat16), ctx[0])
+    latent_in = video.x_in
 
     def eager(stream):
-        for f in pf.steps:
+        for f in vae.steps:
+            f(stream)
+        latent_in.copy_(vae.out)
+        for f in video.steps:
             f(stream)
         am.plan.run(stream)
     s = torch.cuda.Stream(dev)
@@ -801,27 +839,31 @@ def bench_fastwam(args):
     with torch.cuda.graph(graph):
         eager(torch.cuda.current_stream(dev).cuda_stream)
     p50, mn, p90 = _time_calls(graph.replay, args.steps, args.warmup)
-    # the two halves alone, for the per-part anchors
-    pf.capture()
-    pf_p50, _, _ = _time_calls(pf.run, args.steps, args.warmup)
+    # the three parts alone, for the per-part anchors
+    vae.capture()
+    vae_p50, _, _ = _time_calls(vae.run, args.steps, args.warmup)
+    video.capture()
+    pf_p50, _, _ = _time_calls(video.run, args.steps, args.warmup)
     am.capture()
     loop_p50, _, _ = _time_calls(am.run, args.steps, args.warmup)
-    launches = pf.num_launches + am.num_launches
+    launches = vae.num_launches + 1 + video.num_launches + am.num_launches
     out = {
-        "metric": "p50 ms per FastWAM policy call at the real model shape (video K/V prefill + 10-step action loop, "
-                  "bs=1)", "value": round(p50, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(p50, 4), "higher_is_better": False, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic: seeded N(0,1) tokens/context/noise, N(0,0.02) weights, norm affines N(1,0.2)",
-        "config": {"workload": "FastWAM infer_action without the VAE encode: MoT video K/V prefill (30 blocks, hidden "
-                               "3072, 24x128 heads, FFN 14336, 98 video tokens, 3-D RoPE, 129 context tokens) + 10 "
-                               "Euler steps of the action expert (30 blocks, hidden 1024, 24x128 heads, FFN 4096, "
-                               "32 action tokens, joint attention over 98 cached video + 32 action keys, 129 context "
-                               "tokens of width 4096)", "batch": 1, "video_tokens": Sv, "action_tokens": 32,
-                   "context_tokens": Lc, "denoise_steps": 10, "blocks": L},
+        "metric": "p50 ms per FastWAM policy call at the real model shape (first-frame VAE encode + video pre_dit "
+                  "and K/V prefill + 10-step action loop, bs=1)", "value": round(p50, 4), "unit": "ms", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(p50, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded uniform image, N(0,1) context/noise, N(0,0.02) DiT weights, unit-scale VAE "
+                "convolutions, norm affines N(1,0.2)",
+        "config": {"workload": "FastWAM infer_action: Wan2.2 VAE38 encode of a 224x448 first frame (-> 48x14x28), "
+                               "video pre_dit at t=0 + MoT K/V prefill (30 blocks, hidden 3072, 24x128 heads, FFN "
+                               "14336, 98 video tokens, 3-D RoPE, 129 context tokens of width 4096) + 10 Euler steps "
+                               "of the action expert (30 blocks, hidden 1024, 24x128 heads, FFN 4096, 32 action "
+                               "tokens, joint attention over 98 cached video + 32 action keys)", "batch": 1,
+                   "image": [IH, IW], "video_tokens": Sv, "action_tokens": 32, "context_tokens": Lc,
+                   "denoise_steps": 10, "blocks": L},
         "min_ms": round(mn, 4), "p90_ms": round(p90, 4), "launches_per_call": launches,
-        "prefill_p50_ms": round(pf_p50, 4), "action_loop_p50_ms": round(loop_p50, 4),
-        "action_step_ms": round(loop_p50 / 10, 4),
+        "vae_encode_p50_ms": round(vae_p50, 4), "prefill_p50_ms": round(pf_p50, 4),
+        "action_loop_p50_ms": round(loop_p50, 4), "action_step_ms": round(loop_p50 / 10, 4),
         "reference_anchors_unpublished": {
             "note": "GEAK campaign figures quoted in the reference's source comments, not published results",
             "prefill_ms": 6.02, "prefill_source": "FG/wan_video_dit.py:973-974",

@@ -900,7 +900,7 @@ __device__ __forceinline__ void mfma_acc(f32x4& acc, const bf16x8& w, const bf16
 }
 
 template <int WFM, int WFN>
-__global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int tiles_n, int vec8) {
+__global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int tiles_n, int vec8, int ksplit) {
   // the A part of a slot holds BMA >= BM rows, a multiple of 64 (a 224-row tile also loads the
   // next 32 rows, unused: measured 2-4 % faster than 7 loads per wave per block)
   constexpr int BM = 32 * WFM, BN = 32 * WFN, BK = 64, BMA = (BM + 63) / 64 * 64;
@@ -917,10 +917,12 @@ __global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int t
   const int wm0 = (wave >> 1) * (16 * WFM), wn0 = (wave & 1) * (16 * WFN);
 
   // task order: XCD-contiguous ranges (the grid is padded to a multiple of 8; workgroups past
-  // the last task exit), then column-major over groups of up to 8 row tiles
-  const int nwg = tiles_m * tiles_n, tpx = (nwg + 7) >> 3;
-  const int task = (blockIdx.x & 7) * tpx + (blockIdx.x >> 3);
-  if (task >= nwg) return;   // workgroup-uniform, before any barrier
+  // the last task exit), split-major (split z covers K blocks [z nb / ksplit, (z+1) nb / ksplit)),
+  // then column-major over groups of up to 8 row tiles
+  const int ntile = tiles_m * tiles_n, nwg = ntile * ksplit, tpx = (nwg + 7) >> 3;
+  const int task_all = (blockIdx.x & 7) * tpx + (blockIdx.x >> 3);
+  if (task_all >= nwg) return;   // workgroup-uniform, before any barrier
+  const int split = task_all / ntile, task = task_all - split * ntile;
   const int GM = tiles_m < 8 ? tiles_m : 8;
   const int grp = task / (GM * tiles_n), rem = task - grp * (GM * tiles_n);
   const int gm = (tiles_m - grp * GM) < GM ? (tiles_m - grp * GM) : GM;   // rows in this group
@@ -934,11 +936,13 @@ __global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int t
   const int lr = lane >> 3;
   const uint32_t lc16 = (uint32_t)(((lane & 7) ^ lr) * 16);
   const uint32_t voa = (uint32_t)lr * lda2 + lc16, vow = (uint32_t)lr * ldw2 + lc16;
-  const int nb = (int)(g.K / BK);
-  // load p of this wave for block blk into slot: A rows 8 (wave + 4p) .. + 7 for p < NIA, else
-  // W rows 8 (wave + 4 (p - NIA)) .. + 7; blocks past the end re-read the last one (unused)
+  const int nball = (int)(g.K / BK);
+  const int kb0 = (int)((int64_t)split * nball / ksplit), nb = (int)((int64_t)(split + 1) * nball / ksplit) - kb0;
+  // load p of this wave for block blk (of this split) into slot: A rows 8 (wave + 4p) .. + 7 for
+  // p < NIA, else W rows 8 (wave + 4 (p - NIA)) .. + 7; blocks past the end re-read the last one
+  // (unused)
   auto dma = [&](int p, int blk, int slot) {
-    const uint32_t kb = (uint32_t)(blk < nb ? blk : nb - 1) * (BK * 2);
+    const uint32_t kb = (uint32_t)(kb0 + (blk < nb ? blk : nb - 1)) * (BK * 2);
     if (p < NIA) {
       const int r = wave + 4 * p;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, FAM_LDS(sm + slot * SS + r * 512), 16, voa,
@@ -1013,6 +1017,23 @@ __global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int t
   for (int i = 0; i < WFM; ++i)
 #pragma unroll
     for (int j = 0; j < WFN; ++j) asm volatile("" : "+a"(acc[i][j]));
+
+  if (ksplit > 1) {
+    // split-K: the raw fp32 sums of this split into plane `split` of out ([ksplit][M][ldo] fp32;
+    // bias, activation and residual are the reduction's)
+    float* part = reinterpret_cast<float*>(g.out) + (int64_t)split * Mi * g.ldo;
+#pragma unroll
+    for (int i = 0; i < WFM; ++i) {
+      const int m = m0 + wm0 + i * 16 + l16;
+      if (m >= Mi) continue;
+#pragma unroll
+      for (int j = 0; j < WFN; ++j) {
+        const int nb4 = n0 + wn0 + j * 16 + lg * 4;
+        if (nb4 < Ni) *reinterpret_cast<f32x4*>(part + (int64_t)m * g.ldo + nb4) = acc[i][j];
+      }
+    }
+    return;
+  }
 
   // Epilogue in two passes through LDS (the slots are free now).  Pass 1: every lane adds the
   // bias to its accumulators (lane: out[m][n .. n + 3], one m per lane), rounds to bf16 -- the
@@ -1138,21 +1159,21 @@ static bool big_ok(const fam_gemm_desc* d) {
 }
 
 template <int WFM, int WFN>
-static void launch_big(const GemmArgs& a, hipStream_t s) {
+static void launch_big(const GemmArgs& a, hipStream_t s, int ksplit = 1) {
   const int tm = (int)((a.M + 32 * WFM - 1) / (32 * WFM)), tn = (int)((a.N + 32 * WFN - 1) / (32 * WFN));
-  const unsigned grid = (unsigned)(((tm * tn + 7) / 8) * 8);
+  const unsigned grid = (unsigned)(((tm * tn * ksplit + 7) / 8) * 8);
   // 8-column epilogue vectors when every 8-column group of the operands is 16-byte aligned
   const auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
   const int vec8 = a.N % 8 == 0 && a.ldo % 8 == 0 && al16(a.out) && (!a.res || (a.ldr % 8 == 0 && al16(a.res))) &&
                    (!a.gate || (a.gbs % 8 == 0 && a.grs % 8 == 0 && al16(a.gate)));
-  FAM_LAUNCH((big_kernel<WFM, WFN>), dim3(grid), dim3(256), 0, s, a, tm, tn, vec8);
+  FAM_LAUNCH((big_kernel<WFM, WFN>), dim3(grid), dim3(256), 0, s, a, tm, tn, vec8, ksplit);
 }
 
 // Tile of the big kernel: the candidate with the least estimated time on the busiest CU,
 // tiles per CU (ceil(tiles / CUs)) x tile area / efficiency, where the 128 x 128 and 64 x 64
 // tiles run 2 and 3 workgroups per CU and the efficiency is the per-CU throughput relative to
 // the 256-wide tiles (measured on gfx950: 0.85 for 128 x 128; 64 x 64 is bound by LDS reads,
-// four fragments per four MFMAs, about 0.4); ties go to the larger tile.
+// four fragments per four MFMAs, about 0.25); ties go to the larger tile.
 static void big_plan(int64_t M, int64_t N, int* wfm, int* wfn) {
   static int cus = 0;
   if (cus == 0) {
@@ -1161,13 +1182,43 @@ static void big_plan(int64_t M, int64_t N, int* wfm, int* wfn) {
       n = 256;
     cus = n;
   }
-  struct C { int fm, fn; double eff; } cands[] = {{8, 8, 1.0}, {7, 8, 1.0}, {4, 4, 0.85}, {2, 2, 0.4}};
+  struct C { int fm, fn; double eff; } cands[] = {{8, 8, 1.0}, {7, 8, 1.0}, {4, 4, 0.85}, {2, 2, 0.25}};
   double best = 1e300;
   for (const C& c : cands) {
     const int64_t bm = 32 * c.fm, bn = 32 * c.fn;
     const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const double t = (double)((tiles + cus - 1) / cus) * (double)(bm * bn) / c.eff;
     if (t < best) { best = t; *wfm = c.fm; *wfn = c.fn; }
+  }
+}
+
+// Split-K choice for fam_gemm_ws: among the big kernel's tiles and K splits (each split at
+// least 2 blocks of 64, at most 16 splits, partial planes within the workspace), the least
+// estimated time = tiles x splits rounded up to whole rounds over the CUs x the tile's work on
+// one CU (about 4.7 TFLOP/s per CU for the 256-wide tiles, times the tile's efficiency as in
+// big_plan), plus, with splits, the reduction: the fp32 planes written and read once at about
+// 4 TB/s and one more launch (about 4 us).
+static void big_plan_split(int64_t M, int64_t N, int64_t K, int64_t ws_floats, int* wfm, int* wfn, int* ks) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus = n;
+  }
+  struct C { int fm, fn; double eff; } cands[] = {{8, 8, 1.0}, {7, 8, 1.0}, {4, 4, 0.85}, {2, 2, 0.25}};
+  const int64_t nb = K / 64;
+  double best = 1e300;
+  for (const C& c : cands) {
+    const int64_t bm = 32 * c.fm, bn = 32 * c.fn;
+    const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    for (int z = 1; z <= 16; ++z) {
+      if (z > 1 && (nb < 2 * z || z * M * N > ws_floats)) break;
+      const double rounds = (double)((tiles * z + cus - 1) / cus);
+      double t = rounds * 2.0 * (double)(bm * bn) * (double)(K / z) / (4.7e12 * c.eff);
+      if (z > 1) t += (double)z * (double)(M * N) * 8.0 / 4e12 + 4e-6;
+      if (t < best * 0.999) { best = t; *wfm = c.fm; *wfn = c.fn; *ks = z; }
+    }
   }
 }
 
@@ -1255,6 +1306,49 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
   } else if (round_up(d->M, 128) / 128 * (round_up(d->N, 128) / 128) >= 200) launch_tiled<128, 128, 2>(a, d->prologue, s);
   else launch_tiled<64, 64, 2>(a, d->prologue, s);
   return fam_host::check_launch("fam_gemm");
+}
+
+
+// fam_gemm with a workspace: products inside the big kernel's envelope may split K over
+// workgroups (big_plan_split), the fp32 planes summed in split order by fam_rowop, which also
+// applies the bias / activation / gate / residual epilogue; everything else is fam_gemm.
+extern "C" int64_t fam_gemm_ws_floats(int64_t M, int64_t N, int64_t K) {
+  if (M < 128 || N < 1 || K < 128 || K % 64) return 0;
+  return 16 * M * N;
+}
+
+extern "C" int fam_gemm_ws(const fam_gemm_desc* d, float* ws, int64_t ws_floats, void* stream) {
+  FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_gemm_ws: null descriptor");
+  FAM_REQUIRE(ws_floats >= 0 && (ws_floats == 0 || (ws && ((uintptr_t)ws & 15u) == 0)), FAM_ERR_INVALID_ARG,
+              "fam_gemm_ws: workspace must be 16-byte aligned");
+  if (!big_ok(d) || d->M < 128 || ws_floats < 2 * d->M * d->N || d->N % 4 != 0 || d->act > FAM_ACT_RELU)
+    return fam_gemm(d, stream);
+  int fm = 8, fn = 8, ks = 1;
+  big_plan_split(d->M, d->N, d->K, ws_floats, &fm, &fn, &ks);
+  if (ks == 1) return fam_gemm(d, stream);
+  GemmArgs a{};
+  a.a = (const bf16*)d->a; a.lda = d->lda;
+  a.w = (const bf16*)d->w; a.ldw = d->ldw;
+  a.out = (bf16*)ws; a.ldo = d->N; a.out_f32 = 1;
+  a.M = d->M; a.N = d->N; a.K = d->K; a.rpb = d->M;
+  hipStream_t s = (hipStream_t)stream;
+  if (fm == 8) launch_big<8, 8>(a, s, ks);
+  else if (fm == 7) launch_big<7, 8>(a, s, ks);
+  else if (fm == 4) launch_big<4, 4>(a, s, ks);
+  else launch_big<2, 2>(a, s, ks);
+  const int rc = fam_host::check_launch("fam_gemm_ws");
+  if (rc != FAM_OK) return rc;
+  fam_rowop_desc r{};
+  r.src = FAM_ROWSRC_PARTIALS;
+  r.partials = ws; r.splits = ks; r.split_stride = d->M * d->N; r.ldp = d->N;
+  r.M = d->M; r.N = d->N;
+  r.bias = d->bias; r.act = d->act;
+  r.res = d->res; r.ldr = d->ldr;
+  r.gate = d->gate; r.gate_bs = d->gate_bs; r.gate_rs = d->gate_rs; r.gate_ns = d->gate_ns;
+  r.rows_per_batch = d->rows_per_batch;
+  r.out = d->out; r.ldo = d->ldo; r.out_f32 = d->out_f32;
+  r.norm = FAM_ROWNORM_NONE;
+  return fam_rowop(&r, stream);
 }
 
 static int wide_cus();

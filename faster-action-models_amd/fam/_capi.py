@@ -139,6 +139,8 @@ SIGNATURES = {
     "fam_patchify": (C.c_int, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     "fam_unpatchify": (C.c_int, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp]),
     "fam_gather_rows": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "fam_gemm_ws": (C.c_int, [_vp, _vp, _i64, _vp]),
+    "fam_gemm_ws_floats": (_i64, [_i64, _i64, _i64]),
     "fam_vae_patch_im2col": (C.c_int, [_vp, _i64, _i64, _vp, _i64, _vp]),
     "fam_im2col3x3": (C.c_int, [_vp, _i64, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp]),
     "fam_chan_rmsnorm": (C.c_int, [_vp, _i64, _i64, _i64, _vp, C.c_int, _vp, _i64, _vp]),

@@ -518,9 +518,12 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: to
          prologue: int = _capi.FAM_PRO_NONE, pro_w=None, pro_b=None, pro_shift=None, pro_scale=None,
          pro_mod_bs: int = 0, pro_mod_rs: int = 0, pro_eps: float = 1e-6, act: int = _capi.FAM_ACT_NONE,
          res: Optional[torch.Tensor] = None, gate: Optional[torch.Tensor] = None, gate_bs: int = 0,
-         gate_rs: int = 0, gate_ns: int = 1, rows_per_batch: Optional[int] = None, out_f32: bool = False) -> None:
+         gate_rs: int = 0, gate_ns: int = 1, rows_per_batch: Optional[int] = None, out_f32: bool = False,
+         ws: Optional[torch.Tensor] = None) -> None:
     """Fused GEMM on 2-D views (see fam_gemm in include/fam_hip.h): a [M, K], w [N, K], out [M, N].
-    With prologue=FAM_PRO_LN_FOLDED, pro_w is the fp32 [N] column-sum vector of `fold_layernorm`."""
+    With prologue=FAM_PRO_LN_FOLDED, pro_w is the fp32 [N] column-sum vector of `fold_layernorm`.
+    ws: an fp32 workspace (fam_gemm_ws): the library may then split K over workgroups (sized by
+    `gemm_ws_floats(M, N, K)`; a smaller one limits the splits)."""
     M, K = a.shape
     N = w.shape[0]
     if prologue == _capi.FAM_PRO_LN_FOLDED:
@@ -544,7 +547,17 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], out: to
     d.gate_bs, d.gate_rs, d.gate_ns = gate_bs, gate_rs, gate_ns
     d.rows_per_batch = rows_per_batch if rows_per_batch is not None else max(M, 1)
     d.out_f32 = int(out_f32)
-    call("fam_gemm", C.byref(d), _stream(a))
+    if ws is not None:
+        if ws.dtype != torch.float32 or not ws.is_contiguous() or ws.device != a.device:
+            raise ValueError("ws must be a contiguous fp32 tensor on the device of a")
+        call("fam_gemm_ws", C.byref(d), ws.data_ptr(), ws.numel(), _stream(a))
+    else:
+        call("fam_gemm", C.byref(d), _stream(a))
+
+
+def gemm_ws_floats(M: int, N: int, K: int) -> int:
+    """Workspace (fp32 elements) with which fam_gemm_ws may choose any K split for this shape."""
+    return int(_capi.load().fam_gemm_ws_floats(M, N, K))
 
 
 def fold_layernorm(w: torch.Tensor, bias: Optional[torch.Tensor] = None, *, ln_weight: Optional[torch.Tensor] = None,

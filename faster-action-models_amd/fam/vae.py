@@ -8,10 +8,11 @@ it is a 2-D convolution with its last temporal tap, and the downsample3d time_co
 for a second chunk, :162-167) does not run.
 
 Layout: activations are channels-last rows, one per pixel ([h*w, C] bf16).  A 1x1 convolution
-is one fam_gemm over the rows; a 3x3 convolution is fam_im2col3x3 (the pixel's neighbourhood,
-taps outermost, zero-padded to a multiple of 64 columns) followed by fam_gemm with the weight
-laid out the same way; biases, the residual adds and the Down_ResidualBlock shortcut are GEMM
-epilogues.  The middle AttentionBlock (one head, C = 640 wide, h*w tokens) is two fam_gemm
+is one GEMM over the rows; a 3x3 convolution is fam_im2col3x3 (the pixel's neighbourhood, taps
+outermost, zero-padded to a multiple of 64 columns) followed by a GEMM with the weight laid out
+the same way; biases, the residual adds and the Down_ResidualBlock shortcut are GEMM epilogues.
+The GEMMs go through fam_gemm_ws with one shared fp32 workspace, so the deep levels (392 to
+1568 pixels, K up to 5760) split K over workgroups instead of leaving most CUs idle.  The middle AttentionBlock (one head, C = 640 wide, h*w tokens) is two fam_gemm
 products around fam_softmax_rows: S = q k^T, P = softmax(S / sqrt(C)), O = P v0 + b_v, where
 v0^T = W_v y^T is computed directly in the transposed layout the second product reads (the rows
 of P sum to one, so the value bias moves after the product).
@@ -61,6 +62,37 @@ WAN22_LATENT_STD = (
 
 def _kpad(n: int) -> int:
     return (n + 63) // 64 * 64
+
+
+def encoder_param_shapes(cfg: WanVaeConfig) -> Dict[str, Tuple[int, ...]]:
+    """The state-dict entries the first-frame encode reads (reference names, VideoVAE38_ :1272-1295)."""
+    d = cfg.dims()
+    s = {"encoder.conv1.weight": (d[0], 12, 3, 3, 3), "encoder.conv1.bias": (d[0],)}
+
+    def res(pre, ci, co):
+        s.update({pre + "residual.0.gamma": (ci, 1, 1, 1), pre + "residual.2.weight": (co, ci, 3, 3, 3),
+                  pre + "residual.2.bias": (co,), pre + "residual.3.gamma": (co, 1, 1, 1),
+                  pre + "residual.6.weight": (co, co, 3, 3, 3), pre + "residual.6.bias": (co,)})
+        if ci != co:
+            s.update({pre + "shortcut.weight": (co, ci, 1, 1, 1), pre + "shortcut.bias": (co,)})
+
+    for i, (ci, co) in enumerate(zip(d[:-1], d[1:])):
+        pre = f"encoder.downsamples.{i}.downsamples."
+        for j in range(cfg.num_res_blocks):
+            res(f"{pre}{j}.", ci if j == 0 else co, co)
+        if i != len(cfg.dim_mult) - 1:
+            s.update({f"{pre}{cfg.num_res_blocks}.resample.1.weight": (co, co, 3, 3),
+                      f"{pre}{cfg.num_res_blocks}.resample.1.bias": (co,)})
+    c = d[-1]
+    res("encoder.middle.0.", c, c)
+    s.update({"encoder.middle.1.norm.gamma": (c, 1, 1), "encoder.middle.1.to_qkv.weight": (3 * c, c, 1, 1),
+              "encoder.middle.1.to_qkv.bias": (3 * c,), "encoder.middle.1.proj.weight": (c, c, 1, 1),
+              "encoder.middle.1.proj.bias": (c,)})
+    res("encoder.middle.2.", c, c)
+    s.update({"encoder.head.0.gamma": (c, 1, 1, 1), "encoder.head.2.weight": (2 * cfg.z_dim, c, 3, 3, 3),
+              "encoder.head.2.bias": (2 * cfg.z_dim,), "conv1.weight": (2 * cfg.z_dim, 2 * cfg.z_dim, 1, 1, 1),
+              "conv1.bias": (2 * cfg.z_dim,)})
+    return s
 
 
 class FusedWanVAEEncoder:
@@ -176,6 +208,10 @@ class FusedWanVAEEncoder:
                                                         self.inv_std.data_ptr(), self.out.data_ptr()),
                   "affine", 4 * mu.numel())
         self.latent_hw = (h, w)
+        # one fp32 workspace for the split-K products (the deep levels: few pixels, long K)
+        wsf = max([lib.fam_gemm_ws_floats(d.M, d.N, d.K) for d in self._descs] + [0])
+        self.ws = torch.empty(max(wsf, 4), dtype=torch.float32, device=dev)
+        self._ws_args = (self.ws.data_ptr(), wsf)
         self.graph: Optional[torch.cuda.CUDAGraph] = None
 
     # ------------------------------------------------------------------ plan building
@@ -216,7 +252,14 @@ class FusedWanVAEEncoder:
         d.rows_per_batch = max(d.M, 1)
         d.out_f32 = int(out_f32)
         self._descs.append(d)
-        self._add(name, "fam_gemm", (C.byref(d),), "gemm", 2 * (d.M * d.K + d.N * d.K + d.M * d.N))
+        f, lib = self.lib.fam_gemm_ws, self.lib
+
+        def run(stream):
+            rc = f(C.byref(d), *self._ws_args, stream)
+            if rc != 0:
+                raise _capi.FamError(f"fam_gemm_ws[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
+        self.steps.append(run)
+        self.meta.append({"name": name, "kernel": "gemm", "bytes": 2 * (d.M * d.K + d.N * d.K + d.M * d.N)})
 
     def _im2col(self, name, x, h, w, c, stride):
         ho, wo = (h, w) if stride == 1 else (h // 2, w // 2)

@@ -254,6 +254,21 @@ typedef struct fam_gemm_desc {
 int fam_gemm(const fam_gemm_desc* d, void* stream);
 
 /*
+ * fam_gemm_ws -- fam_gemm with a caller-owned fp32 workspace: a product inside the large-M
+ * kernel's envelope (no prologue, M >= 128, K % 64 == 0, N % 4 == 0) whose tiles cannot fill the
+ * GPU (few rows and columns, long K: the deep levels of the VAE encoder) is split along K over
+ * workgroups into fp32 planes ws[z][M][N] and finished by fam_rowop (planes summed in split order,
+ * then the same bias / activation / gate / residual epilogue); otherwise, or when the workspace
+ * is too small for two planes, it is exactly fam_gemm.  fam_gemm_ws_floats(M, N, K) is the
+ * workspace size (floats) that lets the plan choose any split (0: never splits).
+ * Replaces: as fam_gemm; the reference's convolutions run here as such GEMMs
+ *           (CausalConv3d FB/wan_video_vae.py:33-52 on the first frame).
+ * Limits: as fam_gemm; ws 16-byte aligned.
+ */
+int fam_gemm_ws(const fam_gemm_desc* d, float* ws, int64_t ws_floats, void* stream);
+int64_t fam_gemm_ws_floats(int64_t M, int64_t N, int64_t K);
+
+/*
  * fam_gemm_partial -- split-K product for 1 <= M <= 144 rows without any cross-workgroup
  * traffic: partials[z][m][n] = sum over k in split z of a[m, k] * w[n, k], fp32,
  * z < fam_gemm_partial_splits(M, N, K) (a deterministic function of the shape).  The caller

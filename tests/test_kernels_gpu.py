@@ -314,6 +314,41 @@ def test_gemm_large_tiles_epilogue(M, N, K):
         assert relerr(ops().linear(dev(x), dev(w3), dev(b3)), O.linear(x.float(), w3.float(), b3.float())) <= TOL
 
 
+@pytest.mark.parametrize("M,N,K,epi", [(392, 640, 5760, "bias_res"), (1568, 640, 2880, "gelu"), (392, 392, 640, "f32"),
+                                       (200, 96, 1024, "gate_res"), (4096, 4096, 128, "bias_res")])
+def test_gemm_ws_split_k(M, N, K, epi):
+    """fam_gemm_ws: few output tiles over a long K split over workgroups (the VAE encoder's deep
+    levels), the fp32 planes summed in split order with the epilogue; deterministic; the same
+    product as fam_gemm within bf16 rounding; a workspace too small for two planes is fam_gemm."""
+    from fam import _capi
+    x, w, b = rnd(M, K, seed=91), rnd(N, K, seed=92, scale=0.05), rnd(N, seed=93, scale=0.05)
+    res, gate = rnd(M, N, seed=94), rnd(M, N, seed=95, scale=0.3)
+    lin = O.linear(x.float(), w.float(), b.float())
+    kw, ref = {}, lin
+    if epi == "bias_res":
+        kw, ref = dict(res=dev(res)), res.float() + lin
+    elif epi == "gelu":
+        kw, ref = dict(act=_capi.FAM_ACT_GELU_TANH), O.gelu_tanh(lin)
+    elif epi == "gate_res":
+        kw = dict(res=dev(res), gate=dev(gate), gate_bs=0, gate_rs=N, gate_ns=1, rows_per_batch=M)
+        ref = res.float() + gate.float() * lin
+    dt = torch.float32 if epi == "f32" else torch.bfloat16
+    ws = torch.empty(ops().gemm_ws_floats(M, N, K) or 4, dtype=torch.float32, device="cuda")
+    outs = []
+    for _ in range(2):
+        y = torch.empty(M, N, dtype=dt, device="cuda")
+        ops().gemm(dev(x), dev(w), dev(b), y, out_f32=(epi == "f32"), ws=ws, **kw)
+        outs.append(y)
+    assert relerr(outs[0], ref) <= TOL
+    assert torch.equal(outs[0], outs[1])
+    y1 = torch.empty(M, N, dtype=dt, device="cuda")
+    ops().gemm(dev(x), dev(w), dev(b), y1, out_f32=(epi == "f32"), **kw)
+    y2 = torch.empty(M, N, dtype=dt, device="cuda")
+    ops().gemm(dev(x), dev(w), dev(b), y2, out_f32=(epi == "f32"), ws=ws[:M * N - 1], **kw)
+    assert torch.equal(y1, y2)
+    assert relerr(outs[0], y1.float().cpu()) <= TOL
+
+
 def test_gemm_fp32_residual_out():
     """out_f32: fp32 residual and output (the fused Euler update of fp32 latents)."""
     M, N, K = 32, 7, 1024
