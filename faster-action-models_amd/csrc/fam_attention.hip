@@ -704,51 +704,90 @@ __global__ __launch_bounds__(NW * 64) void attn_small_kernel(AttnArgs a) {
       for (int u = 0; u < NSS; ++u) ssv[j][u] = *reinterpret_cast<const f32x4*>(p + 4 * (u < nss ? u : 0));
     }
   }
+  // K, V and mask loads are unconditional (keys past Sk read key 0 and are zeroed or masked
+  // after the wait) and keep raw bits until then: a load under a branch, consumed on the spot,
+  // made the compiler wait for every load issued before it, one round trip per load
   bf16x8 kf[2][NC];
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
     const int kk = k0 + kt * 16 + l16;
     const bf16* kr = krows.row(kk < Sk ? kk : 0);
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      kf[kt][c] = zero8();
-      if (kk < Sk) kf[kt][c] = load8(kr + c * 32 + lg * 8);
-    }
+    for (int c = 0; c < NC; ++c) kf[kt][c] = load8(kr + c * 32 + lg * 8);
   }
   bf16x8 vc[NVC];
 #pragma unroll
   for (int p = 0; p < NVC; ++p) {
     const int cidx = lane + 64 * p, key = cidx / VCPR, d0 = dv0 + (cidx % VCPR) * 8;
     const int kk = k0 + key;
-    vc[p] = zero8();
-    if (kk < Sk) vc[p] = load8(vrows.row(kk) + d0);
+    vc[p] = load8(vrows.row(kk < Sk ? kk : 0) + d0);
   }
-  float madd[2][2][4];
-  if (a.mask_kind != FAM_MASK_NONE) {
+  // the lane's mask entries, raw: buffer loads off the (batch, head) base with 32-bit offsets
+  // (64-bit addresses for 16 entries cost enough registers to force a wait mid-issue)
+  uint32_t mraw[2][2][4];
+  const int mk = a.mask_kind;
+  const int msz = mk == FAM_MASK_BOOL ? 1 : (mk == FAM_MASK_ADD_F32 ? 4 : 2);
+  const auto mrs = buffer_rsrc(mk == FAM_MASK_NONE ? (const void*)a.q
+                                                   : (const void*)((const char*)a.mask + (b * a.mbs + h * a.mhs) * msz),
+                               mk == FAM_MASK_NONE ? 0u : (uint32_t)(((int64_t)(Sq - 1) * a.mqs + Sk) * msz));
+  auto moff = [&](int t, int kt, int e) {
+    const int q = t * 16 + l16, kk = k0 + kt * 16 + lg * 4 + e;
+    return ((uint32_t)(q < Sq ? q : 0) * (uint32_t)a.mqs + (uint32_t)(kk < Sk ? kk : 0)) * (uint32_t)msz;
+  };
+  // one kind-uniform branch around all of a lane's loads (a branch per entry waits per entry)
+  if (mk == FAM_MASK_BOOL) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int q = t * 16 + l16, kk = k0 + kt * 16 + lg * 4 + e;
-          const int64_t mi = b * a.mbs + h * a.mhs + (int64_t)(q < Sq ? q : 0) * a.mqs + (kk < Sk ? kk : 0);
-          if (a.mask_kind == FAM_MASK_BOOL)
-            madd[t][kt][e] = reinterpret_cast<const uint8_t*>(a.mask)[mi] ? 0.f : -INFINITY;
-          else if (a.mask_kind == FAM_MASK_ADD_F32)
-            madd[t][kt][e] = reinterpret_cast<const float*>(a.mask)[mi] * kLog2e;
-          else
-            madd[t][kt][e] = to_f(reinterpret_cast<const bf16*>(a.mask)[mi]) * kLog2e;
-        }
+        for (int e = 0; e < 4; ++e) mraw[t][kt][e] = __builtin_amdgcn_raw_buffer_load_b8(mrs, moff(t, kt, e), 0, 0);
+  } else if (mk == FAM_MASK_ADD_F32) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mraw[t][kt][e] = __builtin_amdgcn_raw_buffer_load_b32(mrs, moff(t, kt, e), 0, 0);
+  } else if (mk == FAM_MASK_ADD_BF16) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mraw[t][kt][e] = __builtin_amdgcn_raw_buffer_load_b16(mrs, moff(t, kt, e), 0, 0);
   } else {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) madd[t][kt][e] = 0.f;
+        for (int e = 0; e < 4; ++e) mraw[t][kt][e] = 0u;
   }
   __builtin_amdgcn_sched_barrier(0);
+  // keys past Sk: zero K and V fragments; the mask entries as additive log2-domain terms
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      if (k0 + kt * 16 + l16 >= Sk) kf[kt][c] = zero8();
+#pragma unroll
+  for (int p = 0; p < NVC; ++p)
+    if (k0 + (lane + 64 * p) / VCPR >= Sk) vc[p] = zero8();
+  float madd[2][2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t r = mraw[t][kt][e];
+        float m = 0.f;
+        if (a.mask_kind == FAM_MASK_BOOL) m = r ? 0.f : -INFINITY;
+        else if (a.mask_kind == FAM_MASK_ADD_F32) m = __uint_as_float(r) * kLog2e;
+        else if (a.mask_kind == FAM_MASK_ADD_BF16) m = __uint_as_float(r << 16) * kLog2e;
+        madd[t][kt][e] = m;
+      }
 
   // ---- phase 2: queries (normalised) and the V block into LDS
 #pragma unroll
@@ -1525,7 +1564,11 @@ static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
   if constexpr (DH == 64 || DH == 128) {
     // up to 32 queries over up to 256 keys in one workgroup per head (no key splits): the MoT
     // joint attention over [video K/V ; action K/V], a short context
-    if (a.Sq <= 32 && a.Sk >= 1 && a.Sk <= 256 && a.splits == 1 && a.kss == nullptr &&
+    // (its mask entries are buffer loads with 32-bit offsets over one (batch, head) span)
+    const int64_t msz = a.mask_kind == FAM_MASK_BOOL ? 1 : (a.mask_kind == FAM_MASK_ADD_F32 ? 4 : 2);
+    const bool mask_fits = a.mask_kind == FAM_MASK_NONE ||
+                           (a.mqs >= 0 && ((a.Sq - 1) * a.mqs + a.Sk) * msz < ((int64_t)1 << 31));
+    if (a.Sq <= 32 && a.Sk >= 1 && a.Sk <= 256 && a.splits == 1 && a.kss == nullptr && mask_fits &&
         (a.qss == nullptr || a.nwidth <= 4096)) {
       const int nw = (int)((a.Sk + KB - 1) / KB);
       launch_small<DH>(a, nw, a.qss != nullptr, bh, s);
@@ -1646,6 +1689,12 @@ extern "C" int fam_attention(const fam_attn_desc* d, void* stream) {
     default: launch_dh<128>(a, bh, s); break;
   }
   return fam_host::check_launch("fam_attention");
+}
+
+extern "C" int fam_attention_key_splits(int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t head_dim) {
+  if (batch < 1 || heads < 1 || sq < 1 || sk < 1 || head_dim < 1) return 0;
+  if (sk <= 256) return 1;
+  return (int)std::min<int64_t>(64, (sk + 4 * KB - 1) / (4 * KB));
 }
 
 extern "C" int fam_attention_combine(const fam_attn_desc* d, void* stream) {

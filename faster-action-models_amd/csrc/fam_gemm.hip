@@ -67,25 +67,31 @@ __device__ __forceinline__ float apply_act(float v, int act) {
   return v;
 }
 
-// The epilogue operands of one output element, loaded ahead of the product so that their
-// memory round trip overlaps the weight stream.
+// The epilogue operands of one output element (row m < M, column n < N: callers clamp), loaded
+// ahead of the product so that their memory round trip overlaps the weight stream.  The loads
+// are branch-free and keep the raw bits: an absent operand reads element 0 of the weight matrix
+// (a valid address) and epilogue_finish ignores it.  A load under a branch, converted on the
+// spot, made the compiler wait for every load issued before it (the weight stream included),
+// one memory round trip per operand.
 struct EpiIn {
-  float bias, res, gate, csum;
+  bf16 bias, gate, resb;
+  float resf, csum;
 };
 __device__ __forceinline__ EpiIn epilogue_load(const GemmArgs& g, int64_t m, int64_t n) {
-  EpiIn e{0.f, 0.f, 1.f, 0.f};
-  if (g.bias) e.bias = to_f(g.bias[n]);
-  if (g.csum) e.csum = g.csum[n];
-  if (g.res) {
-    const int64_t bi = m / g.rpb, si = m - bi * g.rpb;
-    if (g.gate) e.gate = to_f(g.gate[bi * g.gbs + si * g.grs + n * g.gns]);
-    e.res = g.out_f32 ? reinterpret_cast<const float*>(g.res)[m * g.ldr + n] : to_f(g.res[m * g.ldr + n]);
-  }
+  const int64_t bi = m / g.rpb, si = m - bi * g.rpb;
+  const bool rb = g.res && !g.out_f32, rf = g.res && g.out_f32;
+  const float* wf = reinterpret_cast<const float*>(g.w);
+  EpiIn e;
+  e.bias = (g.bias ? g.bias : g.w)[g.bias ? n : 0];
+  e.gate = (g.gate ? g.gate : g.w)[g.gate ? bi * g.gbs + si * g.grs + n * g.gns : 0];
+  e.resb = (rb ? g.res : g.w)[rb ? m * g.ldr + n : 0];
+  e.resf = (rf ? reinterpret_cast<const float*>(g.res) : wf)[rf ? m * g.ldr + n : 0];
+  e.csum = (g.csum ? g.csum : wf)[g.csum ? n : 0];
   return e;
 }
 __device__ __forceinline__ void epilogue_finish(const GemmArgs& g, int64_t m, int64_t n, float v, const EpiIn& e) {
-  v = apply_act(v + e.bias, g.act);
-  if (g.res) v = e.res + e.gate * v;
+  v = apply_act(v + (g.bias ? to_f(e.bias) : 0.f), g.act);
+  if (g.res) v = (g.out_f32 ? e.resf : to_f(e.resb)) + (g.gate ? to_f(e.gate) : 1.f) * v;
   if (g.out_f32) reinterpret_cast<float*>(g.out)[m * g.ldo + n] = v;
   else g.out[m * g.ldo + n] = to_bf(v);
 }
@@ -280,7 +286,8 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
     for (int u = 0; u < EPT; ++u) {
       const int t = tid + u * NW * 64, mr = t >> 4;
       const int64_t n = n0 + (t & 15);
-      ep[u] = (t < MR * 16 && mr < g.M && n < g.N) ? epilogue_load(g, mr, n) : EpiIn{0.f, 0.f, 1.f, 0.f};
+      // (outputs past M or N are never stored: their operands are those of a valid element)
+      ep[u] = epilogue_load(g, std::min((int64_t)mr, g.M - 1), std::min(n, g.N - 1));
     }
   };
   if constexpr (EPRE) ep_load();
@@ -392,7 +399,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
         const float invk = 1.0f / (float)g.K;
         const float dm = t1 * invk;
         const float rstd = rsqrtf(fmaxf(t2 * invk - dm * dm, 0.f) + g.eps);
-        v = rstd * (v - (s_piv[mr] + dm) * ep[u].csum);
+        v = rstd * (v - (s_piv[mr] + dm) * (g.csum ? ep[u].csum : 0.f));
       }
       epilogue_finish(g, mr, n, v, ep[u]);
     }
@@ -699,15 +706,17 @@ __global__ __launch_bounds__(NW * 64) void final_kernel(FinalArgs g) {
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) af[t][s] = load8(kok[s] ? ap + kw + s * 32 : g.a);
   }
-  // the epilogue's bias (4 consecutive columns per lane), loaded with the operands
+  // the epilogue's bias (4 consecutive columns per lane), loaded with the operands: branch-free
+  // (a branch per element made the compiler wait for every load before the next bias load)
   const int64_t nc = n0 + lg * 4;
-  float bias[4] = {0.f, 0.f, 0.f, 0.f};
+  const bf16* bsrc = g.bias ? g.bias : g.w;   // a readable address when there is no bias
+  float bias[4];
   bf16 braw[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) braw[e] = g.bias ? g.bias[nc + e < g.N ? nc + e : 0] : (bf16)0.0f;
+  for (int e = 0; e < 4; ++e) braw[e] = bsrc[min(nc + e, g.N - 1)];
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) bias[e] = to_f(braw[e]);
+  for (int e = 0; e < 4; ++e) bias[e] = g.bias ? to_f(braw[e]) : 0.f;
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll

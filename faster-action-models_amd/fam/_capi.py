@@ -124,6 +124,7 @@ SIGNATURES = {
     "fam_rmsnorm_grouped": (C.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _i64, C.c_float, _vp]),
     "fam_attention": (C.c_int, [C.POINTER(AttnDesc), _vp]),
     "fam_attention_combine": (C.c_int, [C.POINTER(AttnDesc), _vp]),
+    "fam_attention_key_splits": (C.c_int, [_i64, _i64, _i64, _i64, _i64]),
     "fam_attention_noalloc": (C.c_int, [C.POINTER(AttnDesc), _vp]),
     "fam_attention_noalloc_max_bytes": (_i64, []),
     "fam_gemm_partial": (C.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),

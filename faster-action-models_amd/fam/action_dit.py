@@ -302,9 +302,9 @@ class FusedActionDiT:
         for (n_, k_) in ((3 * A, H), (H, A), (A, H), (Fd, H), (H, Fd), (cfg.action_dim, H)):
             part_need = max(part_need, self._part_splits(M, n_, k_) * M * n_)
         self.part = torch.zeros(part_need, dtype=torch.float32, device=dev)
-        # key-split partials of the cross-attention: ~4 blocks of 32 keys per workgroup
-        # (up to 256 context tokens one workgroup per head takes every key: no splits, no combine)
-        self.kv_splits = 1 if ctx_len <= 256 else max(1, min(64, -(-ctx_len // 128)))
+        # cross-attention key splits (1: a single launch, no combine) as the library advises
+        self.kv_splits = int(self.lib.fam_attention_key_splits(batch, cfg.num_heads, seq_len, ctx_len,
+                                                               cfg.attn_head_dim))
         nq = batch * cfg.num_heads * seq_len
         self.apart_o = torch.zeros(self.kv_splits * nq * cfg.attn_head_dim, dtype=torch.float32, device=dev)
         self.apart_ml = torch.zeros(self.kv_splits * nq * 2, dtype=torch.float32, device=dev)

@@ -240,7 +240,8 @@ class FusedDiT4DiTHead:
         self.z = torch.empty(M, cfg.hidden_size, dtype=_BF16, device=device)
         self.vel = torch.empty(T, batch, A, dtype=_BF16, device=device)
         self.delta = torch.tensor(-self.dt, dtype=_BF16, device=device)
-        self.splits = attn_splits if attn_splits is not None else max(1, min(16, (vl_len + 127) // 128))
+        self.splits = (attn_splits if attn_splits is not None else
+                       int(_capi.lib().fam_attention_key_splits(batch, cfg.heads, self.Sq, vl_len, cfg.head_dim)))
         self.graph: Optional[torch.cuda.CUDAGraph] = None
 
     # ------------------------------------------------------------------ one policy call

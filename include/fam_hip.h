@@ -185,6 +185,18 @@ int fam_attention(const fam_attn_desc* d, void* stream);
 int fam_attention_combine(const fam_attn_desc* d, void* stream);
 
 /*
+ * fam_attention_key_splits -- the num_splits to use for an unmasked, single-segment attention
+ * of sq queries over sk keys: the cross-attention over the context (replaces the split choice
+ * around flash_attention in CrossAttention.forward, FB/wan_video_dit.py:224-229).  Returns 1
+ * up to 256 keys (one workgroup per head takes every key), otherwise about four 32-key blocks
+ * per split (one per wave of the split's workgroup), at most 64.  Each split's workgroup runs
+ * its own softmax, so the splits spread that vector work over the CUs; splitting a head's
+ * output dims instead (every workgroup scoring every key) multiplied it and measured slower.
+ * A deterministic function of the shape; 0 for invalid arguments.
+ */
+int fam_attention_key_splits(int64_t batch, int64_t heads, int64_t sq, int64_t sk, int64_t head_dim);
+
+/*
  * fam_attention_noalloc -- fam_attention with key splits followed by fam_attention_combine,
  * with the split partials in a library-owned device array (8 MiB per GPU, held until the
  * process ends) instead of the caller's part_o / part_ml, which are ignored.  No counterpart in

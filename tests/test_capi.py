@@ -126,6 +126,13 @@ def test_validation_rejects_before_launch(lib):
                                                               (1024, 4096), (7, 1024), (9216, 1024),
                                                               (1024, 3072))] == [2, 4, 2, 4, 8, 2, 6]
     assert lib.fam_gemm_partial_splits(0, 64, 64) == 0
+    # cross-attention key splits: one launch up to 256 keys, about four 32-key blocks per split
+    # beyond, at most 64 (config 1 at B=1 and 32, DiT4DiT over 2048 VLM tokens, a long context)
+    assert [lib.fam_attention_key_splits(*a) for a in ((1, 16, 32, 1560, 64), (32, 16, 32, 1560, 64),
+                                                      (1, 16, 16, 2048, 64), (1, 24, 32, 129, 128),
+                                                      (1, 16, 32, 256, 64), (1, 16, 32, 257, 128),
+                                                      (1, 16, 32, 100000, 64))] == [13, 13, 16, 1, 1, 3, 64]
+    assert lib.fam_attention_key_splits(0, 16, 32, 1560, 64) == 0
     # the video prefill's 98-row projections: the streaming kernel (one round of 128-column
     # workgroups, whole 256-wide chunks per split) for FFN down / FFN up / q|k|v, 64-column
     # workgroups with 3 chunks per split for the 3072 x 3072 ones; the register kernel where

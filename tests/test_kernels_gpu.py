@@ -191,6 +191,8 @@ def test_rms_norm_rope_fused():
 
 # --------------------------------------------------------------------------- attention
 @pytest.mark.parametrize("B,H,Sq,Sk,Dh", [(1, 16, 32, 32, 64), (1, 16, 32, 1560, 64), (2, 24, 32, 130, 128),
+                                           (2, 3, 17, 1001, 128), (1, 2, 5, 300, 64), (2, 2, 9, 700, 64),
+                                           (1, 4, 32, 2048, 64), (1, 2, 32, 2049, 64), (1, 2, 16, 1024, 128),
                                            (1, 4, 8, 1560, 8), (1, 2, 100, 77, 32), (3, 3, 1, 5, 16),
                                            (1, 4, 300, 300, 128)])
 def test_attention(B, H, Sq, Sk, Dh):
@@ -773,16 +775,18 @@ def test_attention_qk_norm_on_load(B):
     assert relerr(y, ref) <= TOL
 
 
-def test_attention_q_norm_cross_with_splits():
-    """Cross attention with the query normalised on load (no RoPE) and 13 key splits."""
-    S, H, Dh, Lc, Kd = 32, 16, 64, 1560, 1024
+@pytest.mark.parametrize("S,H,Dh,Lc,splits", [(32, 16, 64, 1560, 13), (32, 16, 64, 1560, 1), (20, 8, 128, 777, 1)])
+def test_attention_q_norm_cross_with_splits(S, H, Dh, Lc, splits):
+    """Cross attention with the query normalised on load (no RoPE): 13 key splits + combine, or
+    none (a head's output dims split over workgroups that each score every key)."""
+    Kd = 1024
     A = H * Dh
     x, w, bb = rnd(S, Kd, seed=121), rnd(A, Kd, seed=122, scale=0.02), rnd(A, seed=123, scale=0.02)
     wq = rnd(A, seed=124, scale=0.2) + 1
     k, v = rnd(1, Lc, A, seed=125), rnd(1, Lc, A, seed=126)
     q_raw, ss = ops().gemm_final(dev(x), dev(w), dev(bb), want_sumsq=True)
     wqd, kd, vd = dev(wq), dev(k), dev(v)
-    y = ops().attention_bshd(q_raw.view(1, S, A), kd, vd, H, num_splits=13,
+    y = ops().attention_bshd(q_raw.view(1, S, A), kd, vd, H, num_splits=splits,
                              qk_norm=dict(q_sumsq=ss, ss_batch_rows=S, norm_width=A, q_norm_w=wqd, eps=1e-6))
     q = O.rms_norm(q_raw.cpu().view(1, S, A), wq, 1e-6).float()
     ref = O.flash_attention(q, k.float(), v.float(), H)
