@@ -1322,8 +1322,11 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
 // workgroups (big_plan_split), the fp32 planes summed in split order by fam_rowop, which also
 // applies the bias / activation / gate / residual epilogue; everything else is fam_gemm.
 extern "C" int64_t fam_gemm_ws_floats(int64_t M, int64_t N, int64_t K) {
-  if (M < 128 || N < 1 || K < 128 || K % 64) return 0;
-  return 16 * M * N;
+  if (M < 128 || N < 1 || N % 4 != 0 || K < 128 || K % 64) return 0;
+  // the planes of the split the unconstrained plan picks (deterministic for the device)
+  int fm = 8, fn = 8, ks = 1;
+  big_plan_split(M, N, K, INT64_MAX, &fm, &fn, &ks);
+  return ks > 1 ? (int64_t)ks * M * N : 0;
 }
 
 extern "C" int fam_gemm_ws(const fam_gemm_desc* d, float* ws, int64_t ws_floats, void* stream) {

@@ -155,6 +155,19 @@ class FusedVideoDiTBlock:
             if t is not None and (t.dtype != torch.float32 or t.numel() < need):
                 raise ValueError(f"shared buffer 'part' must be fp32 with >= {need} elements")
             self.part = t if t is not None else torch.zeros(need, dtype=torch.float32, device=dev)
+        # above 128 rows: the fp32 planes of the large-M products the GEMM plan splits along K
+        # (fam_gemm_ws; at config 2 only FFN down, whose 3072 output columns leave the big tiles
+        # too few), one workspace shared by the blocks of a stack
+        self.ws = None
+        if not self.splitk:
+            need = max([self.lib.fam_gemm_ws_floats(M, n_, k_)
+                        for n_, k_ in ((3 * A, H), (H, A), (A, H), (F, H), (H, F))] +
+                       [self.lib.fam_gemm_ws_floats(batch * ctx_len, 2 * A, H)] + [0])
+            if need > 0:
+                t = sh.get("ws")
+                if t is not None and (t.dtype != torch.float32 or t.numel() < need or t.data_ptr() % 16):
+                    raise ValueError(f"shared buffer 'ws' must be 16-byte aligned fp32 with >= {need} elements")
+                self.ws = t if t is not None else torch.zeros(need, dtype=torch.float32, device=dev)
         if self_mask is not None:
             self_mask = self_mask.to(device=dev, dtype=torch.bool).contiguous()
             if tuple(self_mask.shape) != (seq_len, seq_len):
@@ -200,7 +213,10 @@ class FusedVideoDiTBlock:
             d.gate_bs, d.gate_rs, d.gate_ns = gate_strides
         d.rows_per_batch = self.S if M == self.B * self.S else M
         self._descs.append(d)
-        self._add(name, "fam_gemm", (C.byref(d),), "gemm", 2 * M * N * K)
+        if self.ws is not None and self.lib.fam_gemm_ws_floats(M, N, K) > 0:
+            self._add(name, "fam_gemm_ws", (C.byref(d), self.ws.data_ptr(), self.ws.numel()), "gemm", 2 * M * N * K)
+        else:
+            self._add(name, "fam_gemm", (C.byref(d),), "gemm", 2 * M * N * K)
 
     def _partial(self, name, a, w):
         """Split-K partials of a [M, K] x w[N, K]^T into self.part; returns the plane count."""
@@ -478,6 +494,13 @@ class FusedVideoPrefill:
                        for n_, k_ in ((hidden, self.A), (self.A, hidden), (hidden, ffn_dim), (3 * self.A, hidden),
                                       (ffn_dim, hidden)))
             self.shared["part"] = torch.zeros(need, dtype=torch.float32, device=dev)
+        else:          # one split-K workspace of the large-M products for every block
+            need = max([lib.fam_gemm_ws_floats(M, n_, k_)
+                        for n_, k_ in ((3 * self.A, hidden), (hidden, self.A), (self.A, hidden), (ffn_dim, hidden),
+                                       (hidden, ffn_dim))] +
+                       [lib.fam_gemm_ws_floats(batch * ctx_len, 2 * self.A, hidden), 0])
+            if need > 0:
+                self.shared["ws"] = torch.zeros(need, dtype=torch.float32, device=dev)
         # the context K/V of every block that cross-attends, in one GEMM per call: the context
         # does not change between blocks, only the weights do
         # (without keep_output the last block run builds only its K/V)

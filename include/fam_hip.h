@@ -272,7 +272,8 @@ int fam_gemm(const fam_gemm_desc* d, void* stream);
  * workgroups into fp32 planes ws[z][M][N] and finished by fam_rowop (planes summed in split order,
  * then the same bias / activation / gate / residual epilogue); otherwise, or when the workspace
  * is too small for two planes, it is exactly fam_gemm.  fam_gemm_ws_floats(M, N, K) is the
- * workspace size (floats) that lets the plan choose any split (0: never splits).
+ * workspace (floats) of the split the plan picks for the shape when the workspace does not
+ * limit it, splits * M * N (0: the plan does not split); a smaller workspace limits the split.
  * Replaces: as fam_gemm; the reference's convolutions run here as such GEMMs
  *           (CausalConv3d FB/wan_video_vae.py:33-52 on the first frame).
  * Limits: as fam_gemm; ws 16-byte aligned.
