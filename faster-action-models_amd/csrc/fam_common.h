@@ -71,13 +71,21 @@ __device__ __forceinline__ bf16x8 load8_if(bool ok, const bf16* p, const bf16* s
 }
 
 __device__ __forceinline__ float gelu_tanh(float x) {
-  // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+  // 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), evaluated as x / (1 + e^(-2u)) (the
+  // same function: 0.5 (1 + tanh(u)) = 1 / (1 + e^(-2u))) with the hardware exp2 and reciprocal,
+  // branch-free (the library tanhf runs two divergent paths) and without the cancellation of
+  // 1 + tanh(u) for negative u; e^(-2u) overflowing to +inf gives x * 0
   const float k0 = 0.7978845608028654f;
   const float u = k0 * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(u));
+  const float e = __builtin_amdgcn_exp2f(u * -2.8853900817779268f);   // e^(-2u) = 2^(-2u log2 e)
+  return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+// x sigmoid(x) with the hardware exp2 and reciprocal (no IEEE division); e^(-x) overflowing to
+// +inf gives x * 0
+__device__ __forceinline__ float silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
 
 // MFMA 16x16x32 bf16 -> fp32 (gfx950).  Lane l holds A[row=l%16][k=8*(l/16)..+7],
 // B[k=8*(l/16)..+7][col=l%16]; D[row=4*(l/16)+i][col=l%16], i = 0..3.
@@ -126,14 +134,17 @@ extern thread_local hipEvent_t t_evt_start, t_evt_stop;
 }  // namespace fam_host
 
 // Every kernel launch of the library goes through this macro: when the calling thread has
-// armed a start/stop event pair, the launch records them at the kernel's own begin and end
-// (hipExtLaunchKernelGGL), which is how bench.py measures per-kernel durations.
+// armed a start/stop event pair, the first launch records the start at its begin and every
+// launch the stop at its end (hipExtLaunchKernelGGL), so the pair spans the kernels of one
+// library call; this is how bench.py measures per-call kernel durations.
 #define FAM_LAUNCH(kernel, grid, block, shmem, stream, ...)                                              \
   do {                                                                                                   \
-    if (fam_host::t_evt_start != nullptr)                                                                \
+    if (fam_host::t_evt_stop != nullptr) {                                                               \
+      /* a call of several launches: the first records the start, every one the stop */                 \
       hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, fam_host::t_evt_start, fam_host::t_evt_stop, \
                             0, __VA_ARGS__);                                                             \
-    else                                                                                                 \
+      fam_host::t_evt_start = nullptr;                                                                   \
+    } else                                                                                               \
       hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                               \
   } while (0)
 

@@ -47,11 +47,12 @@ int fam_version(void);
 const char* fam_last_error(void);
 
 /*
- * fam_set_launch_events -- profiling aid with no counterpart in the reference: while a pair
- * of hipEvent_t (created with timing enabled) is armed on the calling thread, every kernel
- * the library launches records start_event at its begin and stop_event at its end
- * (hipExtLaunchKernelGGL), so hipEventElapsedTime gives that kernel's own duration.  Pass
- * two nulls to disarm.  Not for use under stream capture.
+ * fam_set_launch_events -- profiling aid with no counterpart in the reference: after a pair
+ * of hipEvent_t (created with timing enabled) is armed on the calling thread, the first kernel
+ * the library launches records start_event at its begin and every kernel records stop_event at
+ * its end (hipExtLaunchKernelGGL), so hipEventElapsedTime spans the kernels of one call (a
+ * call such as fam_gemm_ws launches two); arm a fresh pair per call.  Pass two nulls to
+ * disarm.  Not for use under stream capture.
  */
 int fam_set_launch_events(void* start_event, void* stop_event);
 
