@@ -37,6 +37,7 @@
 //     tiles, K in steps of 64 through double-buffered LDS, next step's global loads issued
 //     before the current step's MFMAs; prologue statistics per tile row at kernel start.
 #include <algorithm>
+#include <cmath>
 #include <type_traits>
 
 #include "fam_common.h"
@@ -909,7 +910,7 @@ __device__ __forceinline__ void mfma_acc(f32x4& acc, const bf16x8& w, const bf16
 }
 
 template <int WFM, int WFN>
-__global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int tiles_n, int vec8, int ksplit) {
+__global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int tiles_n, int vec8, int ksplit, int raw) {
   // the A part of a slot holds BMA >= BM rows, a multiple of 64 (a 224-row tile also loads the
   // next 32 rows, unused: measured 2-4 % faster than 7 loads per wave per block)
   constexpr int BM = 32 * WFM, BN = 32 * WFN, BK = 64, BMA = (BM + 63) / 64 * 64;
@@ -1027,9 +1028,9 @@ __global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int t
 #pragma unroll
     for (int j = 0; j < WFN; ++j) asm volatile("" : "+a"(acc[i][j]));
 
-  if (ksplit > 1) {
-    // split-K: the raw fp32 sums of this split into plane `split` of out ([ksplit][M][ldo] fp32;
-    // bias, activation and residual are the reduction's)
+  if (raw) {
+    // split-K (or fam_gemm_partial's single plane): the raw fp32 sums of this split into plane
+    // `split` of out ([ksplit][M][ldo] fp32; bias, activation and residual are the reduction's)
     float* part = reinterpret_cast<float*>(g.out) + (int64_t)split * Mi * g.ldo;
 #pragma unroll
     for (int i = 0; i < WFM; ++i) {
@@ -1167,15 +1168,17 @@ static bool big_ok(const fam_gemm_desc* d) {
          (!d->gate || (d->gate_ns == 1 && d->gate_bs % 4 == 0 && d->gate_rs % 4 == 0 && al(d->gate, 8)));
 }
 
+// raw: fp32 planes without epilogue (always with ksplit > 1)
 template <int WFM, int WFN>
-static void launch_big(const GemmArgs& a, hipStream_t s, int ksplit = 1) {
+static void launch_big(const GemmArgs& a, hipStream_t s, int ksplit = 1, bool raw = false) {
   const int tm = (int)((a.M + 32 * WFM - 1) / (32 * WFM)), tn = (int)((a.N + 32 * WFN - 1) / (32 * WFN));
   const unsigned grid = (unsigned)(((tm * tn * ksplit + 7) / 8) * 8);
   // 8-column epilogue vectors when every 8-column group of the operands is 16-byte aligned
   const auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
   const int vec8 = a.N % 8 == 0 && a.ldo % 8 == 0 && al16(a.out) && (!a.res || (a.ldr % 8 == 0 && al16(a.res))) &&
                    (!a.gate || (a.gbs % 8 == 0 && a.grs % 8 == 0 && al16(a.gate)));
-  FAM_LAUNCH((big_kernel<WFM, WFN>), dim3(grid), dim3(256), 0, s, a, tm, tn, vec8, ksplit);
+  FAM_LAUNCH((big_kernel<WFM, WFN>), dim3(grid), dim3(256), 0, s, a, tm, tn, vec8, ksplit,
+             (int)(raw || ksplit > 1));
 }
 
 // Tile of the big kernel: the candidate with the least estimated time on the busiest CU,
@@ -1201,13 +1204,19 @@ static void big_plan(int64_t M, int64_t N, int* wfm, int* wfn) {
   }
 }
 
-// Split-K choice for fam_gemm_ws: among the big kernel's tiles and K splits (each split at
-// least 2 blocks of 64, at most 16 splits, partial planes within the workspace), the least
-// estimated time = tiles x splits rounded up to whole rounds over the CUs x the tile's work on
-// one CU (about 4.7 TFLOP/s per CU for the 256-wide tiles, times the tile's efficiency as in
-// big_plan), plus, with splits, the reduction: the fp32 planes written and read once at about
-// 4 TB/s and one more launch (about 4 us).
-static void big_plan_split(int64_t M, int64_t N, int64_t K, int64_t ws_floats, int* wfm, int* wfn, int* ks) {
+// K split of the big kernel (fam_gemm_ws, and fam_gemm_partial above 144 rows).  Estimated time
+// of a tile shape with z splits, a least-squares fit to gfx950 measurements (15 shapes from
+// 512 x 6144 x 4096 to 8192^3, every tile, 1-8 splits):
+//   t = ceil(tiles z / (CUs occ)) (c0 + 2 bm bn K_z / rate * occ) + [z > 1] z M N 4 B / 12 TB/s
+// (K_z = the split's K range; per tile: c0 = 10, 8, 4, 1 us, rate = 6.5, 6.5, 5.5, 3.0 TFLOP/s
+// per CU, occ = 1, 1, 2, 2 workgroups per CU for 256x256, 224x256, 128x128, 64x64).  The cost of
+// consuming the planes is added: a row launch that sums them (fam_gemm_ws: about 5 us + the
+// bf16 output written at 4 TB/s + z planes read at 8.8 TB/s), or, when a row kernel follows
+// anyway (fam_gemm_partial), the reads of the extra planes.  A split (2, 3, 4, 6 or 8 planes, each
+// at least 2 blocks of 64 along K, within the workspace) is taken only where this estimate is
+// at least 15% below the unsplit one; otherwise *ks = 1 and the tile is big_plan's.
+static void big_plan_split(int64_t M, int64_t N, int64_t K, int64_t ws_floats, bool planes_consumed, int* wfm,
+                           int* wfn, int* ks) {
   static int cus = 0;
   if (cus == 0) {
     int dev = 0, n = 0;
@@ -1215,20 +1224,32 @@ static void big_plan_split(int64_t M, int64_t N, int64_t K, int64_t ws_floats, i
       n = 256;
     cus = n;
   }
-  struct C { int fm, fn; double eff; } cands[] = {{8, 8, 1.0}, {7, 8, 1.0}, {4, 4, 0.85}, {2, 2, 0.25}};
+  struct Fit { int fm, fn; double c0, rate, occ; };
+  static const Fit fits[] = {{8, 8, 10.0, 6.5, 1.0}, {7, 8, 8.0, 6.5, 1.0}, {4, 4, 4.0, 5.5, 2.0}, {2, 2, 1.0, 3.0, 2.0}};
   const int64_t nb = K / 64;
-  double best = 1e300;
-  for (const C& c : cands) {
-    const int64_t bm = 32 * c.fm, bn = 32 * c.fn;
+  const double mn = (double)M * (double)N;
+  auto est = [&](const Fit& f, int z) {
+    const int64_t bm = 32 * f.fm, bn = 32 * f.fn;
     const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    for (int z = 1; z <= 16; ++z) {
-      if (z > 1 && (nb < 2 * z || z * M * N > ws_floats)) break;
-      const double rounds = (double)((tiles * z + cus - 1) / cus);
-      double t = rounds * 2.0 * (double)(bm * bn) * (double)(K / z) / (4.7e12 * c.eff);
-      if (z > 1) t += (double)z * (double)(M * N) * 8.0 / 4e12 + 4e-6;
-      if (t < best * 0.999) { best = t; *wfm = c.fm; *wfn = c.fn; *ks = z; }
+    const double rounds = std::ceil((double)(tiles * z) / ((double)cus * f.occ));
+    const double kz = (double)((nb + z - 1) / z) * 64.0;
+    double t = rounds * (f.c0 + 2.0 * (double)(bm * bn) * kz / (f.rate * 1e6) * f.occ);
+    if (z > 1) t += (double)z * mn * 4.0 / 12e6;
+    return t;
+  };
+  double unsplit = 1e300;
+  for (const Fit& f : fits) unsplit = std::min(unsplit, est(f, 1));
+  double best = 0.85 * unsplit;
+  big_plan(M, N, wfm, wfn);
+  *ks = 1;
+  for (const Fit& f : fits)
+    for (int z : {2, 3, 4, 6, 8}) {
+      if (nb < 2 * z || (double)z * mn > (double)ws_floats) continue;
+      const double consume = planes_consumed ? (double)(z - 1) * mn * 4.0 / 8.8e6
+                                             : 5.0 + mn * 2.0 / 4e6 + (double)z * mn * 4.0 / 8.8e6;
+      const double t = est(f, z) + consume;
+      if (t < best) { best = t; *wfm = f.fm; *wfn = f.fn; *ks = z; }
     }
-  }
 }
 
 template <int BM, int BN, int WM>
@@ -1325,7 +1346,7 @@ extern "C" int64_t fam_gemm_ws_floats(int64_t M, int64_t N, int64_t K) {
   if (M < 128 || N < 1 || N % 4 != 0 || K < 128 || K % 64) return 0;
   // the planes of the split the unconstrained plan picks (deterministic for the device)
   int fm = 8, fn = 8, ks = 1;
-  big_plan_split(M, N, K, INT64_MAX, &fm, &fn, &ks);
+  big_plan_split(M, N, K, INT64_MAX, false, &fm, &fn, &ks);
   return ks > 1 ? (int64_t)ks * M * N : 0;
 }
 
@@ -1336,7 +1357,7 @@ extern "C" int fam_gemm_ws(const fam_gemm_desc* d, float* ws, int64_t ws_floats,
   if (!big_ok(d) || d->M < 128 || ws_floats < 2 * d->M * d->N || d->N % 4 != 0 || d->act > FAM_ACT_RELU)
     return fam_gemm(d, stream);
   int fm = 8, fn = 8, ks = 1;
-  big_plan_split(d->M, d->N, d->K, ws_floats, &fm, &fn, &ks);
+  big_plan_split(d->M, d->N, d->K, ws_floats, false, &fm, &fn, &ks);
   if (ks == 1) return fam_gemm(d, stream);
   GemmArgs a{};
   a.a = (const bf16*)d->a; a.lda = d->lda;
@@ -1415,8 +1436,19 @@ static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* split
 }
 
 // Above 128 rows (<= 144) only the streaming plan runs; 0 when it does not apply.
+// above 144 rows: the big kernel writes the planes (K a multiple of 64, at least 128; N % 4 == 0)
+static bool partial_big_shape(int64_t M, int64_t N, int64_t K) {
+  return M > 144 && N >= 4 && N % 4 == 0 && K >= 128 && K % 64 == 0;
+}
+
 extern "C" int fam_gemm_partial_splits(int64_t M, int64_t N, int64_t K) {
-  if (M <= 0 || N <= 0 || K <= 0 || M > 144) return 0;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  if (M > 144) {
+    if (!partial_big_shape(M, N, K)) return 0;
+    int fm = 8, fn = 8, ks = 1;
+    big_plan_split(M, N, K, INT64_MAX, true, &fm, &fn, &ks);
+    return ks;
+  }
   int st, sp;
   partial_plan(M, N, K, &st, &sp);
   return M > 128 && st >= 0 ? 0 : sp;
@@ -1473,9 +1505,34 @@ static void launch_partial_wide(const PartArgs& a, int splits, hipStream_t s) {
 extern "C" int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64_t ldw, float* partials,
                                 int64_t M, int64_t N, int64_t K, void* stream) {
   FAM_REQUIRE(a && w && partials, FAM_ERR_INVALID_ARG, "fam_gemm_partial: null pointer");
-  FAM_REQUIRE(M >= 0 && M <= 144 && N >= 1 && K >= 8 && K % 8 == 0, FAM_ERR_INVALID_ARG,
-              "fam_gemm_partial: need 0 <= M <= 144, N >= 1, K a positive multiple of 8 (M=%lld N=%lld K=%lld)",
+  FAM_REQUIRE(M >= 0 && N >= 1 && K >= 8 && K % 8 == 0, FAM_ERR_INVALID_ARG,
+              "fam_gemm_partial: need M >= 0, N >= 1, K a positive multiple of 8 (M=%lld N=%lld K=%lld)",
               (long long)M, (long long)N, (long long)K);
+  if (M > 144) {
+    // the big kernel's split-K planes (raw fp32; one plane is its fp32 output without epilogue)
+    FAM_REQUIRE(partial_big_shape(M, N, K), FAM_ERR_UNSUPPORTED,
+                "fam_gemm_partial: above 144 rows N must be a multiple of 4 and K a multiple of 64, >= 128 "
+                "(fam_gemm_partial_splits returns 0 otherwise; M=%lld N=%lld K=%lld)",
+                (long long)M, (long long)N, (long long)K);
+    FAM_REQUIRE(lda >= K && ldw >= K && lda % 8 == 0 && ldw % 8 == 0 && fam_host::aligned16(a) &&
+                    fam_host::aligned16(w) && fam_host::aligned16(partials),
+                FAM_ERR_INVALID_ARG, "fam_gemm_partial: lda/ldw >= K and multiples of 8, 16-byte aligned pointers");
+    FAM_REQUIRE((M + 256) * lda * 2 < (1LL << 31) && (N + 256) * ldw * 2 < (1LL << 31), FAM_ERR_UNSUPPORTED,
+                "fam_gemm_partial: above 144 rows (M + 256) * lda * 2 and (N + 256) * ldw * 2 must be < 2^31 bytes");
+    int fm = 8, fn = 8, ks = 1;
+    big_plan_split(M, N, K, INT64_MAX, true, &fm, &fn, &ks);
+    GemmArgs g{};
+    g.a = (const bf16*)a; g.lda = lda;
+    g.w = (const bf16*)w; g.ldw = ldw;
+    g.out = (bf16*)partials; g.ldo = N; g.out_f32 = 1;
+    g.M = M; g.N = N; g.K = K; g.rpb = M;
+    hipStream_t s = (hipStream_t)stream;
+    if (fm == 8) launch_big<8, 8>(g, s, ks, true);
+    else if (fm == 7) launch_big<7, 8>(g, s, ks, true);
+    else if (fm == 4) launch_big<4, 4>(g, s, ks, true);
+    else launch_big<2, 2>(g, s, ks, true);
+    return fam_host::check_launch("fam_gemm_partial");
+  }
   FAM_REQUIRE(lda >= K && ldw >= K && lda % 8 == 0 && ldw % 8 == 0, FAM_ERR_INVALID_ARG,
               "fam_gemm_partial: lda/ldw must be >= K and multiples of 8");
   FAM_REQUIRE(fam_host::aligned16(a) && fam_host::aligned16(w) && fam_host::aligned16(partials), FAM_ERR_INVALID_ARG,

@@ -365,14 +365,18 @@ class FusedActionDiT:
         self.plan.add(name, run, kernel, nbytes, flops)
 
     def _part_splits(self, M, N, K):
-        # above 64 rows the tiled GEMM writes a single fp32 plane
-        return 1 if M > 64 else self.lib.fam_gemm_partial_splits(M, N, K)
+        # up to 64 rows the weight-streaming split; above 144 the large-M kernel's planes (split
+        # along K where the planes cost less than idle CUs); else (or off the large-M kernel's
+        # shapes) the GEMM writes a single fp32 plane
+        if M <= 64:
+            return self.lib.fam_gemm_partial_splits(M, N, K)
+        return (self.lib.fam_gemm_partial_splits(M, N, K) or 1) if M > 144 else 1
 
     def _gemm_partial(self, name, a, w):
         """Split-K partials of a [M, K] x w[N, K]^T into self.part; returns the split count."""
         M, K = a.shape[0], w.shape[1]
         N = w.shape[0]
-        if M > 64:
+        if M > 64 and not (M > 144 and self.lib.fam_gemm_partial_splits(M, N, K) > 0):
             self._gemm(name, a, w, None, self.part, ldo=N, out_f32=True)
             return 1
         splits = self._part_splits(M, N, K)

@@ -597,12 +597,15 @@ def fold_layernorm(w: torch.Tensor, bias: Optional[torch.Tensor] = None, *, ln_w
 
 
 def gemm_partial(a: torch.Tensor, w: torch.Tensor):
-    """Split-K partials of a [M, K] x w [N, K]^T (M <= 64): returns ([S, M, N] fp32, S)."""
+    """Split-K partials of a [M, K] x w [N, K]^T: returns ([S, M, N] fp32, S) (the shapes
+    fam_gemm_partial takes; S = 0 for one it does not)."""
     _check(a, "a")
     _check(w, "w")
     M, K = a.shape
     N = w.shape[0]
     S = _capi.lib().fam_gemm_partial_splits(M, N, K)
+    if S <= 0:
+        raise ValueError(f"fam_gemm_partial does not take M={M} N={N} K={K} (fam_gemm_partial_splits is 0)")
     part = torch.empty((S, M, N), dtype=torch.float32, device=a.device)
     call("fam_gemm_partial", a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0), part.data_ptr(), M, N, K,
          _stream(a))

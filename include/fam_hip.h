@@ -283,17 +283,22 @@ int fam_gemm_ws(const fam_gemm_desc* d, float* ws, int64_t ws_floats, void* stre
 int64_t fam_gemm_ws_floats(int64_t M, int64_t N, int64_t K);
 
 /*
- * fam_gemm_partial -- split-K product for 1 <= M <= 144 rows without any cross-workgroup
- * traffic: partials[z][m][n] = sum over k in split z of a[m, k] * w[n, k], fp32,
+ * fam_gemm_partial -- split-K product without any cross-workgroup traffic:
+ * partials[z][m][n] = sum over k in split z of a[m, k] * w[n, k], fp32,
  * z < fam_gemm_partial_splits(M, N, K) (a deterministic function of the shape).  The caller
  * allocates splits*M*N floats and sums them with fam_rowop, which also applies the
- * epilogue.  a [M, K] and w [N, K] bf16 (nn.Linear layout).
+ * epilogue.  a [M, K] and w [N, K] bf16 (nn.Linear layout).  Up to 144 rows the weights stream
+ * through the small-M kernels; above, the large-M tile kernel writes the planes, split along K
+ * only where the extra planes (read by the row kernel that follows anyway) cost less than the
+ * idle CUs of an unsplit grid (one plane: the plain fp32 product).
  * Replaces: the projections of the action tokens (q/k/v/o, cross q/o, FFN up/down, head;
  *           FB/wan_video_dit.py:188-191,215-218,262-263, FB/action_dit.py:317-318) and the
  *           reference's split-K kernel fastwam::skmm (FG/mot.py:1080-1243).
  * Limits: M <= 128, or up to 144 where fam_gemm_partial_splits is non-zero (the streaming
  * plan: >= 3 chunks of 256 along K per split, e.g. a prefill's 129-row context K/V of every
- * block); K % 8 == 0; lda, ldw multiples of 8; 16-byte aligned a, w, partials; above 64 rows
+ * block), or above 144 with N % 4 == 0, K % 64 == 0, K >= 128 and (M + 256) * lda * 2,
+ * (N + 256) * ldw * 2 < 2^31 bytes (fam_gemm_partial_splits returns 0 for an unsupported shape);
+ * K % 8 == 0; lda, ldw multiples of 8; 16-byte aligned a, w, partials; from 65 to 144 rows
  * lda, ldw < 2^23 elements.
  */
 int fam_gemm_partial(const void* a, int64_t lda, const void* w, int64_t ldw, float* partials,

@@ -111,8 +111,9 @@ def test_validation_rejects_before_launch(lib):
     a.num_splits = 65
     assert lib.fam_attention(C.byref(a), None) == _capi.FAM_ERR_INVALID_ARG
 
-    # split-K partials: M above 128, unaligned K, misaligned partial buffer
-    assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 145, 64, 64, None) == _capi.FAM_ERR_INVALID_ARG
+    # split-K partials: above 144 rows a K below 128 (off the large-M kernel), unaligned K,
+    # misaligned partial buffer
+    assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 145, 64, 64, None) == _capi.FAM_ERR_UNSUPPORTED
     # 129..144 rows only on the streaming plan: not for a short K
     assert lib.fam_gemm_partial_splits(129, 64, 64) == 0
     assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 129, 64, 64, None) == _capi.FAM_ERR_UNSUPPORTED
@@ -126,6 +127,11 @@ def test_validation_rejects_before_launch(lib):
                                                               (1024, 4096), (7, 1024), (9216, 1024),
                                                               (1024, 3072))] == [2, 4, 2, 4, 8, 2, 6]
     assert lib.fam_gemm_partial_splits(0, 64, 64) == 0
+    # above 144 rows the large-M kernel's planes: any shape with N % 4 == 0 and K % 64 == 0 (>= 128)
+    # gets >= 1 plane; the head's N = 7 or a K tail does not
+    assert lib.fam_gemm_partial_splits(1024, 3072, 1024) >= 1 and lib.fam_gemm_partial_splits(1024, 1024, 4096) >= 2
+    assert lib.fam_gemm_partial_splits(1024, 7, 1024) == 0 and lib.fam_gemm_partial_splits(1024, 1024, 1000) == 0
+    assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 1024, 7, 64, None) == _capi.FAM_ERR_UNSUPPORTED
     # cross-attention key splits: one launch up to 256 keys, about four 32-key blocks per split
     # beyond, at most 64 (config 1 at B=1 and 32, DiT4DiT over 2048 VLM tokens, a long context)
     assert [lib.fam_attention_key_splits(*a) for a in ((1, 16, 32, 1560, 64), (32, 16, 32, 1560, 64),

@@ -501,7 +501,8 @@ def test_sinusoid_and_modulation():
                                     (98, 14336, 3072), (128, 9216, 3072), (77, 6004, 4104), (77, 4094, 4104),
                                     (98, 3000, 3072), (128, 3072, 3080), (129, 12288, 3072), (140, 20000, 1600),
                                     (32, 9216, 1024), (32, 1024, 3072), (16, 6000, 1000), (64, 4100, 1048),
-                                    (40, 2048, 2056), (16, 4002, 1000)])
+                                    (40, 2048, 2056), (16, 4002, 1000),
+                                    (1024, 1024, 4096), (1024, 3072, 1024), (200, 68, 192), (1560, 3072, 14336)])
 def test_gemm_partial_rowop(M, N, K):
     """Split-K partials summed in split order by the row kernel = linear; bit-identical reruns.
     Above 64 rows: the streaming kernel where a one-round grid gives every workgroup >= 3
@@ -515,7 +516,9 @@ def test_gemm_partial_rowop(M, N, K):
     kernel where neither fills the chip.  At <= 64 rows the wide kernel with two strips per
     workgroup for the large action projections (the real model's 9216 x 1024 q|k|v and
     1024 x 3072 o), with 1, 2 and 4 m-tiles, rows past M in a tile, ragged N (also N % 4 != 0)
-    and K tails."""
+    and K tails.  Above 144 rows the large-M tile kernel writes the planes: 2 K splits at config
+    1's B=32 FFN down (1024 x 1024 x 4096), one plain fp32 plane at its q|k|v (1024 x 3072 x 1024),
+    a ragged 200 x 68 product, 3 splits at config 2's FFN down."""
     x, w, b = rnd(M, K, seed=70), rnd(N, K, seed=71, scale=0.02), rnd(N, seed=72, scale=0.02)
     ref = O.linear(x.float(), w.float(), b.float())
     xd, wd, bd = dev(x), dev(w), dev(b)
