@@ -475,9 +475,9 @@ def bench_c2(args):
     del blk
     torch.cuda.empty_cache()
     # the whole forward: WanVideoDiT.pre_dit -> 30 blocks -> head, one captured graph
-    from fam.video_dit import FusedWanVideoDiT
-    wcfg = _WanCfg(hidden_dim=H, in_dim=48, ffn_dim=F, out_dim=48, text_dim=4096, freq_dim=256, eps=1e-6,
-                   patch_size=(1, 2, 2), num_heads=nh, attn_head_dim=Dh, num_layers=L)
+    from fam.video_dit import FusedWanVideoDiT, WanVideoConfig
+    wcfg = WanVideoConfig(hidden_dim=H, in_dim=48, ffn_dim=F, out_dim=48, text_dim=4096, freq_dim=256, eps=1e-6,
+                          patch_size=(1, 2, 2), num_heads=nh, attn_head_dim=Dh, num_layers=L)
     gw = torch.Generator(device=dev).manual_seed(2468)
     wm = FusedWanVideoDiT(wcfg, _wan_params(dev, gw, wcfg), batch=1, frames=f, height=2 * hh, width=2 * ww, ctx_len=Lc,
                           device=dev)
@@ -523,11 +523,11 @@ def bench_c4(args):
     diffusers, absent here)."""
     import torch
     from fam.dit4dit import DiT4DiTHeadConfig, FusedDiT4DiTHead, synthetic_params
-    from fam.video_dit import FusedWanVideoDiT
+    from fam.video_dit import FusedWanVideoDiT, WanVideoConfig
     dev = torch.device("cuda:0")
     L, Lc = 2048, 512
-    bcfg = _WanCfg(hidden_dim=2048, in_dim=16, ffn_dim=8192, out_dim=16, text_dim=1024, freq_dim=256, eps=1e-6,
-                   patch_size=(1, 2, 2), num_heads=16, attn_head_dim=128, num_layers=28)
+    bcfg = WanVideoConfig(hidden_dim=2048, in_dim=16, ffn_dim=8192, out_dim=16, text_dim=1024, freq_dim=256, eps=1e-6,
+                          patch_size=(1, 2, 2), num_heads=16, attn_head_dim=128, num_layers=28)
     gb = torch.Generator(device=dev).manual_seed(1357)
     bb = FusedWanVideoDiT(bcfg, _wan_params(dev, gb, bcfg), batch=1, frames=2, height=64, width=64, ctx_len=Lc,
                           mode="features", device=dev)
@@ -701,13 +701,6 @@ def _block_params(dev, g, L, H, A, F, text_dim=None, freq_dim=256, action_dim=No
     return params
 
 
-class _WanCfg:
-    """WanVideoDiT hyper-parameters (the fields fam.video_dit.FusedWanVideoDiT reads)."""
-
-    def __init__(self, **kw):
-        self.__dict__.update(kw)
-
-
 def _wan_params(dev, g, cfg):
     """Synthetic WanVideoDiT weights on the device (the blocks as _block_params, plus the patch
     embedding, text / time embeddings and the head)."""
@@ -793,14 +786,14 @@ def bench_fastwam(args):
     import torch
     from fam.action_dit import ActionDiTConfig, FusedActionDiT
     from fam.vae import FusedWanVAEEncoder, WanVaeConfig
-    from fam.video_dit import FusedWanVideoDiT
+    from fam.video_dit import FusedWanVideoDiT, WanVideoConfig
     dev = torch.device("cuda:0")
     L, H, nh, Dh, F, Lc, T = 30, 3072, 24, 128, 14336, 129, 4096
     IH, IW = 224, 448
     g = torch.Generator(device=dev).manual_seed(8765)
     vcfg = WanVaeConfig()
     vae = FusedWanVAEEncoder(vcfg, _vae_params(dev, g, vcfg), height=IH, width=IW, device=dev)
-    wcfg = _WanCfg(hidden_dim=H, in_dim=48, ffn_dim=F, out_dim=48, text_dim=T, freq_dim=256, eps=1e-6,
+    wcfg = WanVideoConfig(hidden_dim=H, in_dim=48, ffn_dim=F, out_dim=48, text_dim=T, freq_dim=256, eps=1e-6,
                    patch_size=(1, 2, 2), num_heads=nh, attn_head_dim=Dh, num_layers=L)
     lh, lw = vae.latent_hw
     video = FusedWanVideoDiT(wcfg, _wan_params(dev, g, wcfg), batch=1, frames=1, height=lh, width=lw, ctx_len=Lc,

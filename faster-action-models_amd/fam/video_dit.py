@@ -25,7 +25,8 @@ from __future__ import annotations
 
 import ctypes as C
 import math
-from typing import Dict, List, Optional
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Tuple
 
 import torch
 
@@ -640,6 +641,25 @@ class FusedVideoPrefill:
         return self.kv_cache()
 
 
+@dataclass
+class WanVideoConfig:
+    """WanVideoDiT's hyper-parameters (FB/wan_video_dit.py:329-411) as FusedWanVideoDiT reads
+    them; the defaults are the Wan2.2-TI2V-5B video expert of FastWAM (configs 2 and the
+    prefill).  The config-4 backbone is WanVideoConfig(hidden_dim=2048, in_dim=16, ffn_dim=8192,
+    out_dim=16, text_dim=1024, num_heads=16, num_layers=28)."""
+    hidden_dim: int = 3072
+    in_dim: int = 48
+    ffn_dim: int = 14336
+    out_dim: int = 48
+    text_dim: int = 4096
+    freq_dim: int = 256
+    eps: float = 1e-6
+    patch_size: Tuple[int, int, int] = (1, 2, 2)
+    num_heads: int = 24
+    attn_head_dim: int = 128
+    num_layers: int = 30
+
+
 class FusedWanVideoDiT:
     """WanVideoDiT (FB/wan_video_dit.py:328-684) of the video expert on the library for a fixed
     call shape: latents [B, in_dim, F, Hl, Wl], one timestep per sample, Lc context tokens.
@@ -668,8 +688,9 @@ class FusedWanVideoDiT:
     video_mask: bool [S, S] on the self-attention (None: every key).
     """
 
-    def __init__(self, cfg, params: Dict[str, torch.Tensor], *, batch: int, frames: int, height: int, width: int,
-                 ctx_len: int, video_mask: Optional[torch.Tensor] = None, mode: str = "forward", device="cuda"):
+    def __init__(self, cfg: WanVideoConfig, params: Dict[str, torch.Tensor], *, batch: int, frames: int, height: int,
+                 width: int, ctx_len: int, video_mask: Optional[torch.Tensor] = None, mode: str = "forward",
+                 device="cuda"):
         if mode not in ("forward", "prefill", "features"):
             raise ValueError(f"mode must be 'forward', 'prefill' or 'features', got {mode!r}")
         dev = torch.device(device)
