@@ -162,13 +162,13 @@ __device__ __forceinline__ bf16x8 softmax_update(const float (&s)[2][4], float& 
     for (int j = 0; j < 8; ++j) pf[j] = (bf16)0.0f;
     return pf;
   }
-  const float alpha = exp2f(m_run - m_new);  // m_run = -inf -> 0
+  const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // m_run = -inf -> 0
   float psum = 0.f;
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float p = exp2f(s[kt][e] - m_new);
+      const float p = __builtin_amdgcn_exp2f(s[kt][e] - m_new);
       psum += p;
       pf[kt * 4 + e] = to_bf(p);
     }
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
     float mx = -INFINITY;
 #pragma unroll
     for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_m[w][q]);
-    wscale[qt] = (mx == -INFINITY) ? 0.f : exp2f(m_run[qt] - mx);
+    wscale[qt] = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[qt] - mx);
   }
   for (int w = 0; w < NW; ++w) {
     if (wave == w) {
@@ -469,7 +469,7 @@ __global__ __launch_bounds__(NW * 64) void attn_short_kernel(AttnArgs a) {
     float L = 0.f;
     if (mx != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < NW; ++w) L += s_l[w][q] * exp2f(s_m[w][q] - mx);
+      for (int w = 0; w < NW; ++w) L += s_l[w][q] * __builtin_amdgcn_exp2f(s_m[w][q] - mx);
     }
     const f32x4 v = *reinterpret_cast<const f32x4*>(&s_o[q][d0]);
     if (a.splits > 1) {
@@ -502,7 +502,8 @@ __global__ __launch_bounds__(256) void attn_self_kernel(AttnArgs a) {
   constexpr int LD = DH + 8;              // padded LDS rows (bf16)
   __shared__ bf16 Qs[32][LD];
   __shared__ bf16 Ks[32][LD];
-  __shared__ bf16 Vt[DH][32 + 8];
+  // V row-major ([key][dim], pitch DH + 16), read back as V^T by transposing LDS reads
+  __shared__ __attribute__((aligned(16))) bf16 Vs[32][DH + 16];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l16 = lane & 15, lg = lane >> 4;
@@ -581,8 +582,7 @@ __global__ __launch_bounds__(256) void attn_self_kernel(AttnArgs a) {
     }
     *reinterpret_cast<bf16x8*>(&Qs[r][d0]) = qn;
     *reinterpret_cast<bf16x8*>(&Ks[r][d0]) = kn;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) Vt[d0 + e][r] = vr[c][e];
+    *reinterpret_cast<bf16x8*>(&Vs[r][d0]) = vr[c];
   }
   __syncthreads();
   if (wave >= 2 || wave * 16 >= Sq) return;
@@ -618,20 +618,26 @@ __global__ __launch_bounds__(256) void attn_self_kernel(AttnArgs a) {
   for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float pv = exp2f(sc[kt][e] - mx);
+      const float pv = __builtin_amdgcn_exp2f(sc[kt][e] - mx);
       psum += pv;
       pf[kt * 4 + e] = to_bf(pv);
     }
   const float inv = 1.0f / group4_sum(psum);
   const int q = qt * 16 + l16;
+  // V^T fragment of dim tile t: lane s of a 16-lane group loads key 4 lg + s / 4 (+ 16), dims
+  // 16 t + 4 (s % 4) .. + 3; lane i receives keys 4 lg .. 4 lg + 3 of dim 16 t + i (P's order)
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 #pragma unroll
   for (int t = 0; t < NDT; ++t) {
-    const int d = t * 16 + l16;
-    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&Vt[d][lg * 4]);
-    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(&Vt[d][16 + lg * 4]);
-    bf16x8 vf;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) { vf[e] = lo[e]; vf[4 + e] = hi[e]; }
+    const int key = lg * 4 + (l16 >> 2), dim = t * 16 + 4 * (l16 & 3);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&Vs[key][dim]);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&Vs[key + 16][dim]);
+    const s16x8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    const bf16x8 vf = __builtin_bit_cast(bf16x8, v8);
     const f32x4 o = mfma16(vf, pf, f32x4{0.f, 0.f, 0.f, 0.f});   // O^T[d = 16t + 4lg + i][q]
     if (q < Sq) {
       bf16x4 ov;
@@ -919,7 +925,10 @@ __global__ __launch_bounds__(256) void attn_cross_kernel(AttnArgs a) {
   constexpr int NVC = KB * DH / 8 / 64;    // 16-byte V chunks per lane per block
   constexpr int LD = DH + 8;
   __shared__ bf16 Qs[32][LD];
-  __shared__ bf16 Vt[NW][DH][KB + 8];
+  // each wave's V block row-major ([key][dim], pitch DH + 16: 8 rows x 32 bytes of a
+  // transposing read land in distinct banks), read back as V^T by ds_read_b64_tr_b16
+  constexpr int VLD = DH + 16;
+  __shared__ __attribute__((aligned(16))) bf16 Vs[NW][KB][VLD];
   __shared__ float s_m[NW][32], s_l[NW][32];
   __shared__ float s_o[NW][32][DH + 4];
 
@@ -1016,18 +1025,25 @@ __global__ __launch_bounds__(256) void attn_cross_kernel(AttnArgs a) {
 #pragma unroll
     for (int p = 0; p < NVC; ++p) {
       const int cidx = lane + 64 * p, key = cidx / CPR, d0 = (cidx % CPR) * 8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[wave][d0 + e][key] = vc[p][e];
+      *reinterpret_cast<bf16x8*>(&Vs[wave][key][d0]) = vc[p];
     }
     __builtin_amdgcn_wave_barrier();
+    // V^T fragment of dim tile t (row = dim, k = key): lane s of a 16-lane group loads key
+    // 4 lg + s / 4 (+ 16 for the upper half), dims 16 t + 4 (s % 4) .. + 3, and lane i receives
+    // keys 4 lg .. 4 lg + 3 of dim 16 t + i -- the key order of the P fragment below
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
     bf16x8 vfr[NDT];
 #pragma unroll
     for (int t = 0; t < NDT; ++t) {
-      const int d = t * 16 + l16;
-      const bf16x4 lo = *reinterpret_cast<const bf16x4*>(&Vt[wave][d][lg * 4]);
-      const bf16x4 hi = *reinterpret_cast<const bf16x4*>(&Vt[wave][d][16 + lg * 4]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) { vfr[t][e] = lo[e]; vfr[t][4 + e] = hi[e]; }
+      const int key = lg * 4 + (l16 >> 2), dim = t * 16 + 4 * (l16 & 3);
+      lds_s16x4* p0 = (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&Vs[wave][key][dim];
+      lds_s16x4* p1 = (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&Vs[wave][key + 16][dim];
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p0);
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p1);
+      const s16x8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      vfr[t] = __builtin_bit_cast(bf16x8, v8);
     }
     const bool full = (blk + 1) * KB <= Sk;
 #pragma unroll
@@ -1048,14 +1064,14 @@ __global__ __launch_bounds__(256) void attn_cross_kernel(AttnArgs a) {
         }
       }
       const float m_new = fmaxf(m_run[qt], group4_max(mloc));   // finite: the block has a valid key
-      const float alpha = exp2f(m_run[qt] - m_new);
+      const float alpha = __builtin_amdgcn_exp2f(m_run[qt] - m_new);
       float psum = 0.f;
       bf16x8 pf;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float pv = exp2f(sc[kt][e] - m_new);
+          const float pv = __builtin_amdgcn_exp2f(sc[kt][e] - m_new);
           psum += pv;
           pf[kt * 4 + e] = to_bf(pv);
         }
@@ -1088,7 +1104,7 @@ __global__ __launch_bounds__(256) void attn_cross_kernel(AttnArgs a) {
     float mx = -INFINITY;
 #pragma unroll
     for (int w = 0; w < NW; ++w) mx = fmaxf(mx, s_m[w][q]);
-    const float sc = (mx == -INFINITY) ? 0.f : exp2f(m_run[qt] - mx);  // a wave without keys has m = -inf
+    const float sc = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[qt] - mx);  // a wave without keys has m = -inf
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
       *reinterpret_cast<f32x4*>(&s_o[wave][q][t * 16 + lg * 4]) = oacc[qt][t] * sc;
@@ -1105,7 +1121,7 @@ __global__ __launch_bounds__(256) void attn_cross_kernel(AttnArgs a) {
     if (mx != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        L += s_l[w][q] * exp2f(s_m[w][q] - mx);
+        L += s_l[w][q] * __builtin_amdgcn_exp2f(s_m[w][q] - mx);
         v += *reinterpret_cast<const f32x4*>(&s_o[w][q][d0]);
       }
     }
@@ -1357,16 +1373,20 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
 }
 
 // Merge of the key-split partials: one thread per (b*h, q, 4 channels), splits in order.
-// Up to MAXS splits are loaded before the first use (one memory round trip); more splits
-// (MAXS = 0) take the looped form.
-template <int MAXS>
-__global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, int64_t DH, int64_t BH) {
-  const int64_t idx = (int64_t)blockIdx.x * 64 + threadIdx.x;
-  const int64_t nd4 = DH / 4;
-  if (idx >= BH * a.Sq * nd4) return;
-  const int64_t d0 = (idx % nd4) * 4, rq = idx / nd4;   // rq = bh * Sq + q
-  const int64_t q = rq % a.Sq, bh = rq / a.Sq, b = bh / a.H, h = bh - b * a.H;
-  const int64_t plane = BH * a.Sq;
+// Index math in 32 bits (the host checks that the thread count fits) with the head dim a
+// template constant where it is 64 or 128 (DHC = 0: at run time): 64-bit divisions cost
+// dozens of instructions each on the kernel's one wave per CU.  Up to MAXS splits are loaded
+// before the first use (one memory round trip); more splits (MAXS = 0) take the looped form.
+template <int MAXS, int DHC>
+__global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, int dh_rt, uint32_t total) {
+  const uint32_t idx = blockIdx.x * 64u + threadIdx.x;
+  if (idx >= total) return;
+  const uint32_t DH = DHC ? (uint32_t)DHC : (uint32_t)dh_rt, nd4 = DH / 4;
+  const uint32_t d0 = (idx % nd4) * 4u, rq = idx / nd4;   // rq = bh * Sq + q
+  const uint32_t Sq = (uint32_t)a.Sq, H = (uint32_t)a.H;
+  const uint32_t q = rq % Sq, bh = rq / Sq, b = bh / H, h = bh - b * H;
+  const uint32_t plane = total / nd4;                      // BH * Sq rows per split
+  const int S = a.splits;
   f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
   float L = 0.f;
   if constexpr (MAXS > 0) {
@@ -1374,7 +1394,7 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, int64_t DH
     f32x4 po[MAXS];
 #pragma unroll
     for (int z = 0; z < MAXS; ++z) {
-      const int64_t row = (int64_t)(z < a.splits ? z : a.splits - 1) * plane + rq;
+      const int64_t row = (int64_t)(z < S ? z : S - 1) * plane + rq;
       ml[z] = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
       po[z] = *reinterpret_cast<const f32x4*>(a.part_o + row * DH + d0);
     }
@@ -1382,23 +1402,23 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, int64_t DH
     float mx = -INFINITY;
 #pragma unroll
     for (int z = 0; z < MAXS; ++z)
-      if (z < a.splits) mx = fmaxf(mx, ml[z].x);
+      if (z < S) mx = fmaxf(mx, ml[z].x);
     if (mx != -INFINITY) {
 #pragma unroll
       for (int z = 0; z < MAXS; ++z)
-        if (z < a.splits) {
-          const float w = exp2f(ml[z].x - mx);  // an empty split has m = -inf -> 0
+        if (z < S) {
+          const float w = __builtin_amdgcn_exp2f(ml[z].x - mx);   // an empty split has m = -inf -> 0
           L += ml[z].y * w;
           o += po[z] * w;
         }
     }
   } else {
     float mx = -INFINITY;
-    for (int z = 0; z < a.splits; ++z) mx = fmaxf(mx, a.part_ml[((int64_t)z * plane + rq) * 2]);
+    for (int z = 0; z < S; ++z) mx = fmaxf(mx, a.part_ml[((int64_t)z * plane + rq) * 2]);
     if (mx != -INFINITY) {
-      for (int z = 0; z < a.splits; ++z) {
+      for (int z = 0; z < S; ++z) {
         const int64_t row = (int64_t)z * plane + rq;
-        const float w = exp2f(a.part_ml[row * 2] - mx);
+        const float w = __builtin_amdgcn_exp2f(a.part_ml[row * 2] - mx);
         L += a.part_ml[row * 2 + 1] * w;
         o += *reinterpret_cast<const f32x4*>(a.part_o + row * DH + d0) * w;
       }
@@ -1409,6 +1429,14 @@ __global__ __launch_bounds__(64) void attn_combine_kernel(AttnArgs a, int64_t DH
 #pragma unroll
   for (int e = 0; e < 4; ++e) ov[e] = to_bf(o[e] * inv);
   *reinterpret_cast<bf16x4*>(a.o + b * a.o_bs + q * a.o_rs + h * a.o_hs + d0) = ov;
+}
+
+template <int MAXS>
+static void launch_combine_s(const AttnArgs& a, int dh, uint32_t total, hipStream_t s) {
+  const dim3 grid((total + 63) / 64);
+  if (dh == 64) FAM_LAUNCH((attn_combine_kernel<MAXS, 64>), grid, dim3(64), 0, s, a, dh, total);
+  else if (dh == 128) FAM_LAUNCH((attn_combine_kernel<MAXS, 128>), grid, dim3(64), 0, s, a, dh, total);
+  else FAM_LAUNCH((attn_combine_kernel<MAXS, 0>), grid, dim3(64), 0, s, a, dh, total);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1712,12 +1740,15 @@ extern "C" int fam_attention_combine(const fam_attn_desc* d, void* stream) {
   a.H = d->heads; a.Sq = d->sq;
   a.splits = d->num_splits; a.part_o = d->part_o; a.part_ml = d->part_ml;
   const int64_t n = bh * d->sq * (d->head_dim / 4);
-  const dim3 grid((unsigned)((n + 63) / 64));
+  FAM_REQUIRE(n < ((int64_t)1 << 32) - 64 && d->head_dim <= (1 << 20), FAM_ERR_UNSUPPORTED,
+              "fam_attention_combine: batch*heads*sq*head_dim/4 must be < 2^32");
+  const uint32_t total = (uint32_t)n;
+  const int dh = (int)d->head_dim;
   hipStream_t s = (hipStream_t)stream;
-  if (a.splits <= 4) FAM_LAUNCH((attn_combine_kernel<4>), grid, dim3(64), 0, s, a, d->head_dim, bh);
-  else if (a.splits <= 8) FAM_LAUNCH((attn_combine_kernel<8>), grid, dim3(64), 0, s, a, d->head_dim, bh);
-  else if (a.splits <= 16) FAM_LAUNCH((attn_combine_kernel<16>), grid, dim3(64), 0, s, a, d->head_dim, bh);
-  else FAM_LAUNCH((attn_combine_kernel<0>), grid, dim3(64), 0, s, a, d->head_dim, bh);
+  if (a.splits <= 4) launch_combine_s<4>(a, dh, total, s);
+  else if (a.splits <= 8) launch_combine_s<8>(a, dh, total, s);
+  else if (a.splits <= 16) launch_combine_s<16>(a, dh, total, s);
+  else launch_combine_s<0>(a, dh, total, s);
   return fam_host::check_launch("fam_attention_combine");
 }
 
