@@ -664,7 +664,10 @@ __global__ __launch_bounds__(256) void attn_self_kernel(AttnArgs a) {
 //   - the mask entries of the lane's scores.
 // Keys past Sk are not loaded.  Each wave takes an exact softmax over its block (S^T = K Q^T, a
 // lane holds one query); the waves' (m, l, o) are merged through LDS in wave order.
-template <int DH, int NW, int NV, int NSS>
+// MK: the mask's kind as a template constant (0 none, 1 bool, 2 additive fp32 / bf16), so that
+// each instantiation has one load path (a runtime switch merges the paths' pending loads and
+// the compiler then waits for all of them in every path)
+template <int DH, int NW, int NV, int NSS, int MK>
 __global__ __launch_bounds__(NW * 64) void attn_small_kernel(AttnArgs a) {
   constexpr int NC = DH / 32, CPR = DH / 8, NT = NW * 64;
   constexpr int DVW = DH / NV, NDT = DVW / 16, VCPR = DVW / 8;   // this workgroup's output dims
@@ -732,43 +735,43 @@ __global__ __launch_bounds__(NW * 64) void attn_small_kernel(AttnArgs a) {
   // (64-bit addresses for 16 entries cost enough registers to force a wait mid-issue)
   uint32_t mraw[2][2][4];
   const int mk = a.mask_kind;
-  const int msz = mk == FAM_MASK_BOOL ? 1 : (mk == FAM_MASK_ADD_F32 ? 4 : 2);
-  const auto mrs = buffer_rsrc(mk == FAM_MASK_NONE ? (const void*)a.q
-                                                   : (const void*)((const char*)a.mask + (b * a.mbs + h * a.mhs) * msz),
-                               mk == FAM_MASK_NONE ? 0u : (uint32_t)(((int64_t)(Sq - 1) * a.mqs + Sk) * msz));
-  auto moff = [&](int t, int kt, int e) {
-    const int q = t * 16 + l16, kk = k0 + kt * 16 + lg * 4 + e;
-    return ((uint32_t)(q < Sq ? q : 0) * (uint32_t)a.mqs + (uint32_t)(kk < Sk ? kk : 0)) * (uint32_t)msz;
-  };
-  // one kind-uniform branch around all of a lane's loads (a branch per entry waits per entry)
-  if (mk == FAM_MASK_BOOL) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) mraw[t][kt][e] = __builtin_amdgcn_raw_buffer_load_b8(mrs, moff(t, kt, e), 0, 0);
-  } else if (mk == FAM_MASK_ADD_F32) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) mraw[t][kt][e] = __builtin_amdgcn_raw_buffer_load_b32(mrs, moff(t, kt, e), 0, 0);
-  } else if (mk == FAM_MASK_ADD_BF16) {
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) mraw[t][kt][e] = __builtin_amdgcn_raw_buffer_load_b16(mrs, moff(t, kt, e), 0, 0);
-  } else {
+  if constexpr (MK == 0) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int e = 0; e < 4; ++e) mraw[t][kt][e] = 0u;
+  } else {
+    const int msz = MK == 1 ? 1 : (mk == FAM_MASK_ADD_F32 ? 4 : 2);
+    const auto mrs = buffer_rsrc((const void*)((const char*)a.mask + (b * a.mbs + h * a.mhs) * msz),
+                                 (uint32_t)(((int64_t)(Sq - 1) * a.mqs + Sk) * msz));
+    auto moff = [&](int t, int kt, int e) {
+      const int q = t * 16 + l16, kk = k0 + kt * 16 + lg * 4 + e;
+      return ((uint32_t)(q < Sq ? q : 0) * (uint32_t)a.mqs + (uint32_t)(kk < Sk ? kk : 0)) * (uint32_t)msz;
+    };
+    if constexpr (MK == 1) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mraw[t][kt][e] = __builtin_amdgcn_raw_buffer_load_b8(mrs, moff(t, kt, e), 0, 0);
+    } else if (mk == FAM_MASK_ADD_F32) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mraw[t][kt][e] = __builtin_amdgcn_raw_buffer_load_b32(mrs, moff(t, kt, e), 0, 0);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) mraw[t][kt][e] = __builtin_amdgcn_raw_buffer_load_b16(mrs, moff(t, kt, e), 0, 0);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   // keys past Sk: zero K and V fragments; the mask entries as additive log2-domain terms
@@ -789,9 +792,8 @@ __global__ __launch_bounds__(NW * 64) void attn_small_kernel(AttnArgs a) {
       for (int e = 0; e < 4; ++e) {
         const uint32_t r = mraw[t][kt][e];
         float m = 0.f;
-        if (a.mask_kind == FAM_MASK_BOOL) m = r ? 0.f : -INFINITY;
-        else if (a.mask_kind == FAM_MASK_ADD_F32) m = __uint_as_float(r) * kLog2e;
-        else if (a.mask_kind == FAM_MASK_ADD_BF16) m = __uint_as_float(r << 16) * kLog2e;
+        if constexpr (MK == 1) m = r ? 0.f : -INFINITY;
+        else if constexpr (MK == 2) m = (mk == FAM_MASK_ADD_F32 ? __uint_as_float(r) : __uint_as_float(r << 16)) * kLog2e;
         madd[t][kt][e] = m;
       }
 
@@ -1559,14 +1561,28 @@ static void launch_short_q(const AttnArgs& a, int64_t nkb, dim3 grid, hipStream_
   else FAM_LAUNCH((attn_short_kernel<DH, QT, (wide ? 4 : 8)>), grid, dim3((wide ? 4 : 8) * 64), 0, s, a);
 }
 
+template <int DH, int NW, int NV, int NSS>
+static void launch_small_mk(const AttnArgs& a, dim3 grid, hipStream_t s) {
+  if (a.mask_kind == FAM_MASK_NONE) FAM_LAUNCH((attn_small_kernel<DH, NW, NV, NSS, 0>), grid, dim3(NW * 64), 0, s, a);
+  else if (a.mask_kind == FAM_MASK_BOOL) FAM_LAUNCH((attn_small_kernel<DH, NW, NV, NSS, 1>), grid, dim3(NW * 64), 0, s, a);
+  else FAM_LAUNCH((attn_small_kernel<DH, NW, NV, NSS, 2>), grid, dim3(NW * 64), 0, s, a);
+}
 template <int DH, int NW, int NV>
 static void launch_small_nv(const AttnArgs& a, bool qn, dim3 grid, hipStream_t s) {
-  if (qn) FAM_LAUNCH((attn_small_kernel<DH, NW, NV, 8>), grid, dim3(NW * 64), 0, s, a);
-  else FAM_LAUNCH((attn_small_kernel<DH, NW, NV, 0>), grid, dim3(NW * 64), 0, s, a);
+  if (qn) launch_small_mk<DH, NW, NV, 8>(a, grid, s);
+  else launch_small_mk<DH, NW, NV, 0>(a, grid, s);
 }
 template <int DH, int NW>
 static void launch_small_nw(const AttnArgs& a, bool qn, int64_t bh, hipStream_t s) {
-  // a head over 4 CUs (four output-dim quarters) while that keeps the grid within one round
+  // a head over 8 or 4 CUs (output-dim eighths / quarters) while that keeps the grid within one
+  // round: each slice's workgroup repeats the scores but runs 1/NV of P V and of the merge
+  // (eighths only at DH = 128: a slice keeps at least one 16-dim MFMA tile)
+  if constexpr (DH == 128) {
+    if (bh <= 32) {
+      launch_small_nv<DH, NW, 8>(a, qn, dim3((unsigned)bh, 8), s);
+      return;
+    }
+  }
   if (bh <= 64) launch_small_nv<DH, NW, 4>(a, qn, dim3((unsigned)bh, 4), s);
   else launch_small_nv<DH, NW, 1>(a, qn, dim3((unsigned)bh, 1), s);
 }
