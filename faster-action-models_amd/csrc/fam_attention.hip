@@ -22,6 +22,7 @@
 // Algorithmic bytes per launch: 2*B*H*Dh*(2*Sq + 2*Sk) (+ mask); flops 4*B*H*Sq*Sk*Dh.
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "fam_common.h"
 
@@ -1161,11 +1162,12 @@ __global__ __launch_bounds__(256) void attn_cross_kernel(AttnArgs a) {
 // tile as additive 0 / -inf terms in LDS (keys past Sk included).
 template <int DH, bool KMASK>
 __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) {
+  constexpr int NTH = 256;               // threads; 32 queries per wave
   constexpr int BN = 64;                 // keys per tile
   constexpr int KS = DH / 16;            // 16-wide k-steps of S^T = K Q^T
   constexpr int DT = DH / 32;            // 32-row dim tiles of O^T
   constexpr int CPR = DH / 8;            // 16-byte chunks per K/V row
-  constexpr int NCH = BN * CPR / 256;    // chunks of K (and of V) per thread per tile
+  constexpr int NCH = BN * CPR / NTH;    // chunks of K (and of V) per thread per tile
   // K and V tiles row-major ([key][dim]).  Row pitches: K 272 bytes (16-byte reads of 32 rows
   // hit distinct LDS banks); V a multiple of 64 bytes that is 64 mod 256 (DH 128) or 192 mod
   // 256 (DH 64), so the transposing reads of 8 rows x 64 bytes fill the banks twice exactly
@@ -1200,7 +1202,7 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   // per tile over the rows from the tile's first key to Sk, so rows past the end (and whole
   // tiles past the end) read as zero and each thread keeps only 32-bit row offsets
   const uint32_t krs = (uint32_t)a.k0_rs * 2u, vrs = (uint32_t)a.v0_rs * 2u;   // bytes per row
-  // chunk j of a thread is key tid / CPR + j * (256 / CPR), dims (tid % CPR) * 8 .. + 7: one
+  // chunk j of a thread is key tid / CPR + j * (NTH / CPR), dims (tid % CPR) * 8 .. + 7: one
   // per-lane offset, the j steps go to the scalar offset
   const uint32_t koff = (uint32_t)(tid / CPR) * krs + (uint32_t)(tid % CPR) * 16u;
   const uint32_t voff = (uint32_t)(tid / CPR) * vrs + (uint32_t)(tid % CPR) * 16u;
@@ -1209,18 +1211,18 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
     const int k0 = t * BN, left = Sk - k0 > 0 ? Sk - k0 : 0;
     const auto rsrc = buffer_rsrc(kbase + (int64_t)k0 * a.k0_rs, (uint32_t)left * krs);
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) kr[j] = buffer_load8(rsrc, koff, (uint32_t)j * (256 / CPR) * krs);
+    for (int j = 0; j < NCH; ++j) kr[j] = buffer_load8(rsrc, koff, (uint32_t)j * (NTH / CPR) * krs);
   };
   auto gload_v = [&](int t) {
     const int k0 = t * BN, left = Sk - k0 > 0 ? Sk - k0 : 0;
     const auto rsrc = buffer_rsrc(vbase + (int64_t)k0 * a.v0_rs, (uint32_t)left * vrs);
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) vr[j] = buffer_load8(rsrc, voff, (uint32_t)j * (256 / CPR) * vrs);
+    for (int j = 0; j < NCH; ++j) vr[j] = buffer_load8(rsrc, voff, (uint32_t)j * (NTH / CPR) * vrs);
   };
   auto lstore_k = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
-      const int c = tid + 256 * j, key = c / CPR, d0 = (c % CPR) * 8;
+      const int c = tid + NTH * j, key = c / CPR, d0 = (c % CPR) * 8;
       *reinterpret_cast<bf16x8*>(&Ks[buf][key][d0]) = kr[j];
     }
   };
@@ -1242,7 +1244,7 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   auto lstore_v = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
-      const int c = tid + 256 * j, key = c / CPR, d0 = (c % CPR) * 8;
+      const int c = tid + NTH * j, key = c / CPR, d0 = (c % CPR) * 8;
       *reinterpret_cast<bf16x8*>(&Vs[buf][key][d0]) = vr[j];
     }
   };
@@ -1252,23 +1254,25 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   // group loads key k0 + s / 4, dims dbase + 4 (s % 4) .. + 3, and lane i ends up with keys
   // k0 .. k0 + 3 of dim dbase + i.  Lanes 0-15 / 16-31 take dims 0-15 / 16-31 of the 32-dim
   // tile, lanes 32-63 the same dims for keys 4 further (their k-half of the MFMA).
-  auto vfrag = [&](int buf, int k0, int d) {
-    typedef short s16x4 __attribute__((ext_vector_type(4)));
-    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-    const int s = lane & 15, key = k0 + 4 * hh + (s >> 2);
-    const int dim = d * 32 + 16 * ((lane >> 4) & 1) + 4 * (s & 3);
-    lds_s16x4* p0 = (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&Vs[buf][key][dim];
-    lds_s16x4* p1 = (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&Vs[buf][key + 8][dim];
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p0);
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(p1);
+  // The lane-dependent parts of both fragments' LDS addresses are computed once; inside a tile
+  // every read is the tile buffer's base plus a compile-time offset.
+  typedef __attribute__((address_space(3))) bf16 lds_bf16;
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const int s16 = lane & 15;
+  const int koff_l = l32 * KLD + hh * 8;
+  const int voff_l = (4 * hh + (s16 >> 2)) * VLD + 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
+  auto vfrag = [&](const lds_bf16* vb, int k0, int d) {
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + k0 * VLD + d * 32));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + (k0 + 8) * VLD + d * 32));
     typedef short s16x8 __attribute__((ext_vector_type(8)));
     const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     return __builtin_bit_cast(bf16x8, v);
   };
   // S^T of a tile: register r of half kt holds key kt*32 + 8*(r/4) + 4*hh + r%4 of the lane's
   // query; the two halves are independent MFMA chains, interleaved
-  auto kfrag = [&](int buf, int kt, int ks) {
-    return *reinterpret_cast<const bf16x8*>(&Ks[buf][kt * 32 + l32][ks * 16 + hh * 8]);
+  auto kfrag = [&](const lds_bf16* kb, int kt, int ks) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(kb + kt * 32 * KLD + ks * 16);
   };
   f32x16 acc[DT];
 #pragma unroll
@@ -1276,17 +1280,13 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = a.scale_log2;
 
-  const int ntiles = (Sk + BN - 1) / BN;
-  gload_k(0);
-  gload_v(0);
-  gload_m(0);
-  __builtin_amdgcn_sched_barrier(0);
-  lstore_k(0);
-  lstore_v(0);
-  lstore_m(0);
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
+  // one 64-key tile; TAIL (the partial last tile without a key mask) sets the scores of keys
+  // past Sk to -inf, so full tiles carry no per-score masking
+  auto tile = [&](int t, auto tail_tag) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
     const int buf = t & 1;
+    const lds_bf16* kb = (const lds_bf16*)&Ks[buf][0][0] + koff_l;
+    const lds_bf16* vb = (const lds_bf16*)&Vs[buf][0][0] + voff_l;
     gload_k(t + 1);   // zeros past Sk
     gload_v(t + 1);
     gload_m(t + 1);
@@ -1295,7 +1295,7 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) st[kt] = mfma32(kfrag(buf, kt, ks), qf[ks], st[kt]);
+      for (int kt = 0; kt < 2; ++kt) st[kt] = mfma32(kfrag(kb, kt, ks), qf[ks], st[kt]);
     if constexpr (KMASK) {
       // registers 4g..4g+3 of half kt: keys kt*32 + 8g + 4hh .. + 3
 #pragma unroll
@@ -1306,14 +1306,13 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
 #pragma unroll
           for (int e = 0; e < 4; ++e) st[kt][4 * g4 + e] += m4[e];
         }
-    } else if ((t + 1) * BN > Sk) {
+    } else if constexpr (TAIL) {
+      const int kleft = Sk - t * BN - 4 * hh;   // keys of this tile below Sk, relative to the lane's first
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = t * BN + kt * 32 + 8 * (r / 4) + 4 * hh + (r % 4);
-          st[kt][r] = key < Sk ? st[kt][r] : -INFINITY;
-        }
+        for (int r = 0; r < 16; ++r)
+          st[kt][r] = kt * 32 + 8 * (r / 4) + (r % 4) < kleft ? st[kt][r] : -INFINITY;
     }
     // online softmax (log2 domain).  The running max only moves when a score exceeds it by
     // more than 2^8 (or on the first tile), so the accumulator rescale is skipped on most
@@ -1353,12 +1352,25 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int d = 0; d < DT; ++d) acc[d] = mfma32(vfrag(buf, kt * 32 + 16 * c, d), pf[kt][c], acc[d]);
+        for (int d = 0; d < DT; ++d) acc[d] = mfma32(vfrag(vb, kt * 32 + 16 * c, d), pf[kt][c], acc[d]);
     lstore_k(buf ^ 1);
     lstore_v(buf ^ 1);
     lstore_m(buf ^ 1);
     __syncthreads();
-  }
+  };
+
+  const int ntiles = (Sk + BN - 1) / BN;
+  const int nfull = KMASK ? ntiles : Sk / BN;   // tiles whose keys are all below Sk (or masked)
+  gload_k(0);
+  gload_v(0);
+  gload_m(0);
+  __builtin_amdgcn_sched_barrier(0);
+  lstore_k(0);
+  lstore_v(0);
+  lstore_m(0);
+  __syncthreads();
+  for (int t = 0; t < nfull; ++t) tile(t, std::false_type{});
+  if (nfull < ntiles) tile(nfull, std::true_type{});
 
   if (q >= Sq) return;
   const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;

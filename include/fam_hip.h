@@ -171,7 +171,7 @@ int fam_attention(const fam_attn_desc* d, void* stream);
  *   with rope_cos/sin (complex layout [pos][head_dim/2], row stride rope_row_stride, pos = s):
  *   (y[2j], y[2j+1]) rotated by (cos, sin)[s][ (d of y[2j]) / 2 ].
  * A null q_sumsq / k_sumsq leaves that side as loaded.
- * Limits: head_dim 64 or 128; norm_width a multiple of 256; ss_row_stride, q_group0, k_group0
+ * Limits: head_dim 64 or 128; norm_width a multiple of 1024; ss_row_stride, q_group0, k_group0
  * and rope_row_stride multiples of 4; one key segment when k is normalised; 16-byte aligned
  * weights and tables.
  */

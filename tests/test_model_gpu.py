@@ -126,14 +126,14 @@ def test_tiny_golden_config_through_fused_model():
     assert (y - ref).abs().max().item() <= 3e-2
 
 
-@pytest.mark.parametrize("tokens_per_frame", [98, 49])
-def test_mot_loop_over_video_prefix(tokens_per_frame):
+@pytest.mark.parametrize("tokens_per_frame,heads,head_dim", [(98, 12, 64), (49, 12, 64), (98, 16, 64), (49, 8, 128)])
+def test_mot_loop_over_video_prefix(tokens_per_frame, heads, head_dim):
     """MoT action step (FB/mot.py:378-478) in the fused loop: the action tokens' self-attention
     runs over [cached video K/V ; action K/V] with the action rows of the joint mask; attention
-    width (12 x 64) differs from the hidden size (512); 3 Euler steps."""
+    width (768 or 1024, head dims 64 and 128) differs from the hidden size (512); 3 Euler steps."""
     Cfg, Model = _model_cls()
-    cfg = Cfg(hidden_dim=512, action_dim=7, ffn_dim=1024, text_dim=256, freq_dim=256, num_heads=12,
-              attn_head_dim=64, num_layers=2)
+    cfg = Cfg(hidden_dim=512, action_dim=7, ffn_dim=1024, text_dim=256, freq_dim=256, num_heads=heads,
+              attn_head_dim=head_dim, num_layers=2)
     S, Sv, Lc, steps = 32, 98, 129, 3
     A = cfg.num_heads * cfg.attn_head_dim
     p = _params(cfg, 21)
