@@ -1168,15 +1168,23 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   constexpr int DT = DH / 32;            // 32-row dim tiles of O^T
   constexpr int CPR = DH / 8;            // 16-byte chunks per K/V row
   constexpr int NCH = BN * CPR / NTH;    // chunks of K (and of V) per thread per tile
-  // K and V tiles row-major ([key][dim]).  Row pitches: K 272 bytes (16-byte reads of 32 rows
-  // hit distinct LDS banks); V a multiple of 64 bytes that is 64 mod 256 (DH 128) or 192 mod
-  // 256 (DH 64), so the transposing reads of 8 rows x 64 bytes fill the banks twice exactly
+  // Head dim 128: K and V tiles arrive by direct-to-LDS buffer loads (no register staging, no
+  // LDS stores by the waves) into unpadded 256-byte rows whose 16-byte chunks are XOR-swizzled:
+  // chunk c of K row r at c ^ (r & 15) (the 16-byte fragment reads of 16 rows then hit 16
+  // distinct bank groups), of V row r at c ^ 4 (r & 3) (the transposing reads of 4 rows x 4
+  // chunks then cover the 64 banks once).  Head dim 64: the tiles go through registers into
+  // padded rows -- K 144 bytes, V 192 mod 256, so the transposing reads of 8 rows x 64 bytes
+  // fill the banks twice exactly.
+  constexpr bool DMA = DH == 128;
   constexpr int KLD = DH + 8, VLD = DH == 128 ? 160 : 96;
-  __shared__ bf16 Ks[2][BN][KLD];
-  __shared__ bf16 Vs[2][BN][VLD];
+  __shared__ bf16 Ks[2][DMA ? 1 : BN][DMA ? 8 : KLD];
+  __shared__ bf16 Vs[2][DMA ? 1 : BN][DMA ? 8 : VLD];
+  __shared__ __attribute__((aligned(1024))) bf16 Kd[DMA ? 2 : 1][DMA ? BN * DH : 8];
+  __shared__ __attribute__((aligned(1024))) bf16 Vd[DMA ? 2 : 1][DMA ? BN * DH : 8];
   __shared__ __attribute__((aligned(16))) float Mb[KMASK ? 2 : 1][BN];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
   const int l32 = lane & 31, hh = lane >> 5;
   // XCD-aware task order: workgroup i runs on XCD i % 8; give each XCD a contiguous range of
   // (head, query block) tasks so that a head's query blocks share that XCD's L2
@@ -1202,28 +1210,50 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   // per tile over the rows from the tile's first key to Sk, so rows past the end (and whole
   // tiles past the end) read as zero and each thread keeps only 32-bit row offsets
   const uint32_t krs = (uint32_t)a.k0_rs * 2u, vrs = (uint32_t)a.v0_rs * 2u;   // bytes per row
-  // chunk j of a thread is key tid / CPR + j * (NTH / CPR), dims (tid % CPR) * 8 .. + 7: one
-  // per-lane offset, the j steps go to the scalar offset
+  // direct loads: instruction n of wave w writes rows 4 (w + 4n) .. + 3 of the slot (1 KB;
+  // lane j -> row + j / 16, chunk slot j % 16) and lane j fetches the chunk that belongs there
+  const int dr = lane >> 4;
+  const uint32_t dk = (uint32_t)dr * krs + (uint32_t)(((lane & 15) ^ ((4 * wave + dr) & 15)) * 16);
+  const uint32_t dv = (uint32_t)dr * vrs + (uint32_t)(((lane & 15) ^ (4 * dr)) * 16);
+  auto dma_kv = [&](int t, int buf) {
+    if constexpr (DMA) {
+      const int k0 = t * BN, left = Sk - k0 > 0 ? Sk - k0 : 0;
+      const auto rk = buffer_rsrc(kbase + (int64_t)k0 * a.k0_rs, (uint32_t)left * krs);
+      const auto rv = buffer_rsrc(vbase + (int64_t)k0 * a.v0_rs, (uint32_t)left * vrs);
+#pragma unroll
+      for (int n = 0; n < BN / 16; ++n) {
+        const int r0 = 4 * (wv + 4 * n);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)&Kd[buf][r0 * DH], 16, dk,
+                                                 (uint32_t)r0 * krs, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&Vd[buf][r0 * DH], 16, dv,
+                                                 (uint32_t)r0 * vrs, 0, 0);
+      }
+    }
+  };
+  // register path: chunk j of a thread is key tid / CPR + j * (NTH / CPR), dims (tid % CPR) * 8
+  // .. + 7: one per-lane offset, the j steps go to the scalar offset
   const uint32_t koff = (uint32_t)(tid / CPR) * krs + (uint32_t)(tid % CPR) * 16u;
   const uint32_t voff = (uint32_t)(tid / CPR) * vrs + (uint32_t)(tid % CPR) * 16u;
-  bf16x8 kr[NCH], vr[NCH];
-  auto gload_k = [&](int t) {
-    const int k0 = t * BN, left = Sk - k0 > 0 ? Sk - k0 : 0;
-    const auto rsrc = buffer_rsrc(kbase + (int64_t)k0 * a.k0_rs, (uint32_t)left * krs);
+  bf16x8 kr[DMA ? 1 : NCH], vr[DMA ? 1 : NCH];
+  auto gload_kv = [&](int t) {
+    if constexpr (!DMA) {
+      const int k0 = t * BN, left = Sk - k0 > 0 ? Sk - k0 : 0;
+      const auto rk = buffer_rsrc(kbase + (int64_t)k0 * a.k0_rs, (uint32_t)left * krs);
+      const auto rv = buffer_rsrc(vbase + (int64_t)k0 * a.v0_rs, (uint32_t)left * vrs);
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) kr[j] = buffer_load8(rsrc, koff, (uint32_t)j * (NTH / CPR) * krs);
+      for (int j = 0; j < NCH; ++j) kr[j] = buffer_load8(rk, koff, (uint32_t)j * (NTH / CPR) * krs);
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) vr[j] = buffer_load8(rv, voff, (uint32_t)j * (NTH / CPR) * vrs);
+    }
   };
-  auto gload_v = [&](int t) {
-    const int k0 = t * BN, left = Sk - k0 > 0 ? Sk - k0 : 0;
-    const auto rsrc = buffer_rsrc(vbase + (int64_t)k0 * a.v0_rs, (uint32_t)left * vrs);
+  auto lstore_kv = [&](int buf) {
+    if constexpr (!DMA) {
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) vr[j] = buffer_load8(rsrc, voff, (uint32_t)j * (NTH / CPR) * vrs);
-  };
-  auto lstore_k = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = tid + NTH * j, key = c / CPR, d0 = (c % CPR) * 8;
-      *reinterpret_cast<bf16x8*>(&Ks[buf][key][d0]) = kr[j];
+      for (int j = 0; j < NCH; ++j) {
+        const int c = tid + NTH * j, key = c / CPR, d0 = (c % CPR) * 8;
+        *reinterpret_cast<bf16x8*>(&Ks[buf][key][d0]) = kr[j];
+        *reinterpret_cast<bf16x8*>(&Vs[buf][key][d0]) = vr[j];
+      }
     }
   };
   // key mask of tile t (thread tid < BN: key t * BN + tid), as an additive term
@@ -1241,38 +1271,51 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
       if (tid < BN) Mb[buf][tid] = mr ? 0.f : -INFINITY;
     }
   };
-  auto lstore_v = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int c = tid + NTH * j, key = c / CPR, d0 = (c % CPR) * 8;
-      *reinterpret_cast<bf16x8*>(&Vs[buf][key][d0]) = vr[j];
-    }
-  };
   // A operand of the PV product (V^T: row = dim, k = key) straight from the row-major tile
   // with two transposing LDS reads (ds_read_b64_tr_b16).  Within each 16-lane group, lane i
   // receives element i % 4 of the 8-byte loads of lanes i / 4 + 4e (e = 0..3); so lane s of a
   // group loads key k0 + s / 4, dims dbase + 4 (s % 4) .. + 3, and lane i ends up with keys
   // k0 .. k0 + 3 of dim dbase + i.  Lanes 0-15 / 16-31 take dims 0-15 / 16-31 of the 32-dim
   // tile, lanes 32-63 the same dims for keys 4 further (their k-half of the MFMA).
-  // The lane-dependent parts of both fragments' LDS addresses are computed once; inside a tile
-  // every read is the tile buffer's base plus a compile-time offset.
+  // The lane-dependent parts of both fragments' LDS addresses are computed once (per k-step /
+  // dim tile where the swizzle makes them differ); with the tile's buffer a compile-time
+  // constant every read is a lane register plus an immediate offset.
   typedef __attribute__((address_space(3))) bf16 lds_bf16;
   typedef short s16x4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
   const int s16 = lane & 15;
   const int koff_l = l32 * KLD + hh * 8;
   const int voff_l = (4 * hh + (s16 >> 2)) * VLD + 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
-  auto vfrag = [&](const lds_bf16* vb, int k0, int d) {
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + k0 * VLD + d * 32));
-    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(vb + (k0 + 8) * VLD + d * 32));
+  int kofs[DMA ? KS : 1], vofs[DMA ? DT : 1];
+  if constexpr (DMA) {
+    // K: row l32 (+ 32 kt), chunk 2 ks + hh at (2 ks + hh) ^ (l32 & 15)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kofs[ks] = l32 * DH + (((2 * ks + hh) ^ (l32 & 15)) * 8);
+    // V: row 4 hh + s/4 (+ k0), dims 32 d + 16 ((lane >> 4) & 1) + 4 (s & 3): chunk 4 d + e with
+    // e = 2 ((lane >> 4) & 1) + (s & 3) / 2 at 4 (d ^ (s / 4)) + e (the row's r & 3 is s / 4),
+    // 8 bytes into it for odd s
+    const int e = 2 * ((lane >> 4) & 1) + ((s16 & 3) >> 1);
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+      vofs[d] = (4 * hh + (s16 >> 2)) * DH + (4 * (d ^ (s16 >> 2)) + e) * 8 + (s16 & 1) * 4;
+  }
+  auto vfrag = [&](int buf, int k0, int d) {
+    const lds_bf16* p0;
+    if constexpr (DMA) p0 = (const lds_bf16*)&Vd[buf][0] + vofs[d] + k0 * DH;
+    else p0 = (const lds_bf16*)&Vs[buf][0][0] + voff_l + k0 * VLD + d * 32;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + 8 * (DMA ? DH : VLD)));
     typedef short s16x8 __attribute__((ext_vector_type(8)));
     const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     return __builtin_bit_cast(bf16x8, v);
   };
   // S^T of a tile: register r of half kt holds key kt*32 + 8*(r/4) + 4*hh + r%4 of the lane's
   // query; the two halves are independent MFMA chains, interleaved
-  auto kfrag = [&](const lds_bf16* kb, int kt, int ks) {
-    return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(kb + kt * 32 * KLD + ks * 16);
+  auto kfrag = [&](int buf, int kt, int ks) {
+    const lds_bf16* p;
+    if constexpr (DMA) p = (const lds_bf16*)&Kd[buf][0] + kofs[ks] + kt * 32 * DH;
+    else p = (const lds_bf16*)&Ks[buf][0][0] + koff_l + kt * 32 * KLD + ks * 16;
+    return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(p);
   };
   f32x16 acc[DT];
 #pragma unroll
@@ -1280,22 +1323,20 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = a.scale_log2;
 
-  // one 64-key tile; TAIL (the partial last tile without a key mask) sets the scores of keys
-  // past Sk to -inf, so full tiles carry no per-score masking
-  auto tile = [&](int t, auto tail_tag) {
+  // one 64-key tile from LDS buffer BUF (= t & 1); TAIL (the partial last tile without a key
+  // mask) sets the scores of keys past Sk to -inf, so full tiles carry no per-score masking
+  auto tile = [&](int t, auto tail_tag, auto buf_tag) {
     constexpr bool TAIL = decltype(tail_tag)::value;
-    const int buf = t & 1;
-    const lds_bf16* kb = (const lds_bf16*)&Ks[buf][0][0] + koff_l;
-    const lds_bf16* vb = (const lds_bf16*)&Vs[buf][0][0] + voff_l;
-    gload_k(t + 1);   // zeros past Sk
-    gload_v(t + 1);
+    constexpr int buf = decltype(buf_tag)::value;
+    dma_kv(t + 1, buf ^ 1);   // zeros past Sk; that buffer was released by the last barrier
+    gload_kv(t + 1);
     gload_m(t + 1);
     __builtin_amdgcn_sched_barrier(0);
     f32x16 st[2] = {f32x16{}, f32x16{}};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) st[kt] = mfma32(kfrag(kb, kt, ks), qf[ks], st[kt]);
+      for (int kt = 0; kt < 2; ++kt) st[kt] = mfma32(kfrag(buf, kt, ks), qf[ks], st[kt]);
     if constexpr (KMASK) {
       // registers 4g..4g+3 of half kt: keys kt*32 + 8g + 4hh .. + 3
 #pragma unroll
@@ -1352,25 +1393,38 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
 #pragma unroll
       for (int c = 0; c < 2; ++c)
 #pragma unroll
-        for (int d = 0; d < DT; ++d) acc[d] = mfma32(vfrag(vb, kt * 32 + 16 * c, d), pf[kt][c], acc[d]);
-    lstore_k(buf ^ 1);
-    lstore_v(buf ^ 1);
+        for (int d = 0; d < DT; ++d) acc[d] = mfma32(vfrag(buf, kt * 32 + 16 * c, d), pf[kt][c], acc[d]);
+    lstore_kv(buf ^ 1);
     lstore_m(buf ^ 1);
+    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): tile t + 1 landed
     __syncthreads();
   };
 
   const int ntiles = (Sk + BN - 1) / BN;
   const int nfull = KMASK ? ntiles : Sk / BN;   // tiles whose keys are all below Sk (or masked)
-  gload_k(0);
-  gload_v(0);
+  dma_kv(0, 0);
+  gload_kv(0);
   gload_m(0);
   __builtin_amdgcn_sched_barrier(0);
-  lstore_k(0);
-  lstore_v(0);
+  lstore_kv(0);
   lstore_m(0);
+  if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0070);
   __syncthreads();
-  for (int t = 0; t < nfull; ++t) tile(t, std::false_type{});
-  if (nfull < ntiles) tile(nfull, std::true_type{});
+  using F = std::false_type;
+  using T = std::true_type;
+  using B0 = std::integral_constant<int, 0>;
+  using B1 = std::integral_constant<int, 1>;
+  int t = 0;
+  for (; t + 1 < nfull; t += 2) {
+    tile(t, F{}, B0{});
+    tile(t + 1, F{}, B1{});
+  }
+  if (t < nfull) {
+    tile(t, F{}, B0{});
+    if (t + 1 < ntiles) tile(t + 1, T{}, B1{});
+  } else if (t < ntiles) {
+    tile(t, T{}, B0{});
+  }
 
   if (q >= Sq) return;
   const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
