@@ -562,24 +562,28 @@ __global__ __launch_bounds__(NWV * 64) void partial_wide_kernel(PartArgs g) {
 }
 
 // ---------------------------------------------------------------------------------------
-// partial_stream_kernel (64 < M <= 128, long K ranges): a workgroup of NWV (8 or 4) waves owns
+// partial_stream_kernel (64 < M <= 144, long K ranges): a workgroup of NWV (8 or 4) waves owns
 // 16 NWV output columns (16 per wave) over kper = C x 256 of K and walks it in 256-wide chunks.
 // While the MFMAs of chunk c run, the next chunk is already in flight: each wave's 16 x 256
-// weight panel in registers and the activation chunk (M rows x 256) in registers on its way
-// to the single LDS buffer, the activations issued first so that the LDS store between the
-// chunks does not also wait for the weights.  Loads go through buffer descriptors, so k past the range (and
-// the whole prefetch after the last chunk) reads zeros without a select on the loaded value,
-// which would make the compiler wait on each load right after issuing it; the prologue is
-// drained before the loop for the same reason.  Inside a chunk the activation fragments of
-// k-step s + 1 are read from LDS while the MFMAs of step s run.  Rows past M stay
-// uninitialised in LDS and only reach output rows that are never stored.
+// weight panel in registers, and the activation chunk (M rows x 512 B) by direct-to-LDS buffer
+// loads into the other of two LDS slots -- no register staging and no LDS stores by the waves.
+// A staged row's 16-byte units are XOR-swizzled (unit u of row r at u ^ (r & 15)), so the
+// B-fragment reads of 16 rows hit 16 distinct bank groups without padding, and a load
+// instruction (2 rows x 512 B, lane j -> row + j / 32, slot j % 32) just fetches the unit that
+// belongs in its slot.  Loads go through buffer descriptors: k past the range (and the whole
+// weight prefetch after the last chunk) reads zeros without a select on the loaded value, and
+// activation rows past M read zeros; activation units past K hold the row's next values, which
+// only meet zero weights.  Inside a chunk the fragments of k-step s + 1 are read from LDS while
+// the MFMAs of step s run.  Rows past M (M odd: up to one) only reach output rows that are
+// never stored.  The partial planes are written with non-temporal stores: the row kernel that
+// follows reads them from beyond this XCD's L2 either way, and the L2 is not left holding them.
 template <int MT, int NWV>
 __global__ __launch_bounds__(NWV * 64) void partial_stream_kernel(PartArgs g, int kper) {
-  constexpr int KS = 256, KSW = KS / 32, PITCH = KS + 16, UPR = KS / 8, NTH = NWV * 64;
-  constexpr int UPT = (MT * 16 * UPR + NTH - 1) / NTH;
+  constexpr int KS = 256, KSW = KS / 32;
   constexpr uint32_t kOob = 0x80000000u;   // beyond every descriptor's range (checked on the host)
-  __shared__ __attribute__((aligned(16))) bf16 As[MT * 16 * PITCH];
+  __shared__ __attribute__((aligned(1024))) bf16 As[2][MT * 16 * KS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lg = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
   const int M = (int)g.M, K = (int)g.K, N = (int)g.N;
   const int nb0 = blockIdx.x * (16 * NWV), n0 = nb0 + wave * 16;
   const int kb = blockIdx.y * kper;
@@ -592,22 +596,18 @@ __global__ __launch_bounds__(NWV * 64) void partial_stream_kernel(PartArgs g, in
   const __amdgpu_buffer_rsrc_t ars = buffer_rsrc(g.a, (uint32_t)(g.M * g.lda * 2));
   const int lr = wave * 16 + l16;
   const uint32_t wrow = (uint32_t)((lr < nrows ? lr : 0) * g.ldw) * 2u;
-  const int nunits = M * UPR;
-  bf16x8 ar[UPT], wc[KSW], wx[KSW];
-  auto loadA = [&](int k0, int klim) {
-#pragma unroll
-    for (int u = 0; u < UPT; ++u) {
-      const int idx = tid + u * NTH, r = idx / UPR, k = k0 + (idx % UPR) * 8;
-      ar[u] = buffer_load8(ars, idx < nunits && k < klim ? (uint32_t)(r * g.lda + k) * 2u : kOob);
+  // activation staging: wave w loads row pairs w, w + NWV, ...; lane j's row and unit
+  const int npairs = (M + 1) / 2, sr = lane >> 5;
+  const uint32_t lda2 = (uint32_t)g.lda * 2u;
+  auto issueA = [&](int k0, int buf) {
+    for (int p = wv; p < npairs; p += NWV) {
+      // (row & 15) of row 2p + sr is (2p & 15) + sr: the pair's part of the swizzle goes with p
+      const uint32_t sw = (uint32_t)((lane & 31) ^ (((2 * p) & 15) + sr)) * 16u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)&As[buf][2 * p * KS], 16,
+                                               (uint32_t)sr * lda2 + sw, (uint32_t)(2 * p) * lda2 + (uint32_t)k0 * 2u, 0, 0);
     }
   };
-  auto storeA = [&]() {
-#pragma unroll
-    for (int u = 0; u < UPT; ++u) {
-      const int idx = tid + u * NTH;
-      if (idx < nunits) *reinterpret_cast<bf16x8*>(&As[(idx / UPR) * PITCH + (idx % UPR) * 8]) = ar[u];
-    }
-  };
+  bf16x8 wc[KSW], wx[KSW];
   auto loadW = [&](int k0, int klim, bf16x8* wf) {
 #pragma unroll
     for (int s = 0; s < KSW; ++s) {
@@ -615,28 +615,30 @@ __global__ __launch_bounds__(NWV * 64) void partial_stream_kernel(PartArgs g, in
       wf[s] = buffer_load8(wrs, k < klim ? wrow + (uint32_t)k * 2u : kOob);
     }
   };
-  loadA(kb, K);
+  issueA(kb, 0);
   loadW(kb, K, wc);
-  storeA();
-  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
   __syncthreads();
   f32x4 acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int k0 = kb; k0 < ke; k0 += KS) {
+  for (int k0 = kb, c = 0; k0 < ke; k0 += KS, ++c) {
+    const int buf = c & 1;
     const int klim = k0 + KS < ke ? K : 0;   // 0: past the last chunk, every offset is out of range
-    loadA(k0 + KS, klim);   // first: loads return in order, so the LDS store waits for these only
+    if (k0 + KS < ke) issueA(k0 + KS, buf ^ 1);   // that slot was released by the last barrier
     loadW(k0 + KS, klim, wx);
     __builtin_amdgcn_sched_barrier(0);
+    const bf16* Ab = As[buf];
     bf16x8 bc[MT], bn[MT];
 #pragma unroll
-    for (int t = 0; t < MT; ++t) bc[t] = *reinterpret_cast<const bf16x8*>(&As[(t * 16 + l16) * PITCH + lg * 8]);
+    for (int t = 0; t < MT; ++t)
+      bc[t] = *reinterpret_cast<const bf16x8*>(&Ab[(t * 16 + l16) * KS + ((lg ^ l16) * 8)]);
 #pragma unroll
     for (int s = 0; s < KSW; ++s) {
       if (s + 1 < KSW) {
 #pragma unroll
         for (int t = 0; t < MT; ++t)
-          bn[t] = *reinterpret_cast<const bf16x8*>(&As[(t * 16 + l16) * PITCH + (s + 1) * 32 + lg * 8]);
+          bn[t] = *reinterpret_cast<const bf16x8*>(&Ab[(t * 16 + l16) * KS + ((((s + 1) * 4 + lg) ^ l16) * 8)]);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -645,11 +647,10 @@ __global__ __launch_bounds__(NWV * 64) void partial_stream_kernel(PartArgs g, in
 #pragma unroll
       for (int t = 0; t < MT; ++t) bc[t] = bn[t];
     }
+    __builtin_amdgcn_s_waitcnt(0x0070);   // chunk c + 1's activations and weights landed, slot read
     __syncthreads();
-    storeA();
 #pragma unroll
     for (int s = 0; s < KSW; ++s) wc[s] = wx[s];
-    __syncthreads();
   }
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
@@ -657,11 +658,11 @@ __global__ __launch_bounds__(NWV * 64) void partial_stream_kernel(PartArgs g, in
     if (m >= M) continue;
     float* dst = g.part + ((int64_t)blockIdx.y * g.M + m) * g.N + n;
     if ((N & 3) == 0) {
-      if (n < N) *reinterpret_cast<f32x4*>(dst) = acc[t];
+      if (n < N) __builtin_nontemporal_store(acc[t], reinterpret_cast<f32x4*>(dst));
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (n + e < N) dst[e] = acc[t][e];
+        if (n + e < N) __builtin_nontemporal_store(acc[t][e], dst + e);
     }
   }
 }
