@@ -302,9 +302,13 @@ class FusedActionDiT:
         for (n_, k_) in ((3 * A, H), (H, A), (A, H), (Fd, H), (H, Fd), (cfg.action_dim, H)):
             part_need = max(part_need, self._part_splits(M, n_, k_) * M * n_)
         self.part = torch.zeros(part_need, dtype=torch.float32, device=dev)
-        # cross-attention key splits (1: a single launch, no combine) as the library advises
-        self.kv_splits = int(self.lib.fam_attention_key_splits(batch, cfg.num_heads, seq_len, ctx_len,
-                                                               cfg.attn_head_dim))
+        # Above 64 rows the cross-attention query arrives normalised from its row kernel and every
+        # batch row attends to the same (batch-shared) context K/V: the batch rows' queries are one
+        # sequence of B*S queries per head, the long-sequence kernel's shape (no key splits, no
+        # combine).  Otherwise key splits (1: a single launch, no combine) as the library advises.
+        self.cross_flat = batch * seq_len > 64 and cfg.attn_head_dim in (64, 128) and batch > 1
+        self.kv_splits = 1 if self.cross_flat else int(self.lib.fam_attention_key_splits(
+            batch, cfg.num_heads, seq_len, ctx_len, cfg.attn_head_dim))
         nq = batch * cfg.num_heads * seq_len
         self.apart_o = torch.zeros(self.kv_splits * nq * cfg.attn_head_dim, dtype=torch.float32, device=dev)
         self.apart_ml = torch.zeros(self.kv_splits * nq * 2, dtype=torch.float32, device=dev)
@@ -436,7 +440,8 @@ class FusedActionDiT:
         nbytes += (2 * M * N if res is not None else 0) + (2 * M * N if nout is not None else 0)
         self._launch(name, "fam_rowop", C.byref(d), "rowop", nbytes)
 
-    def _attn_desc(self, q, q_bs, q_rs, k, k_bs, k_rs, v, v_bs, v_rs, out, sq, sk, splits=1, qk_norm=None):
+    def _attn_desc(self, q, q_bs, q_rs, k, k_bs, k_rs, v, v_bs, v_rs, out, sq, sk, splits=1, qk_norm=None,
+                   batch=None):
         cfg = self.cfg
         Dh = cfg.attn_head_dim
         d = _capi.AttnDesc()
@@ -444,7 +449,7 @@ class FusedActionDiT:
         d.k0, d.k0_bs, d.k0_rs, d.k0_hs = k, k_bs, k_rs, Dh
         d.v0, d.v0_bs, d.v0_rs, d.v0_hs = v, v_bs, v_rs, Dh
         d.o, d.o_bs, d.o_rs, d.o_hs = out.data_ptr(), sq * cfg.attn_dim, cfg.attn_dim, Dh
-        d.batch, d.heads, d.sq, d.sk0, d.sk1, d.head_dim = self.B, cfg.num_heads, sq, sk, 0, Dh
+        d.batch, d.heads, d.sq, d.sk0, d.sk1, d.head_dim = self.B if batch is None else batch, cfg.num_heads, sq, sk, 0, Dh
         d.scale = 1.0 / math.sqrt(Dh)
         d.mask_kind = _capi.FAM_MASK_NONE
         d.num_splits = splits
@@ -466,17 +471,19 @@ class FusedActionDiT:
         self._descs.append(d)
         return d
 
-    def _attn(self, name, q, q_bs, q_rs, k, k_bs, k_rs, v, v_bs, v_rs, out, sq, sk, splits=1, qk_norm=None):
+    def _attn(self, name, q, q_bs, q_rs, k, k_bs, k_rs, v, v_bs, v_rs, out, sq, sk, splits=1, qk_norm=None,
+              batch=None):
         cfg = self.cfg
         Dh = cfg.attn_head_dim
-        d = self._attn_desc(q, q_bs, q_rs, k, k_bs, k_rs, v, v_bs, v_rs, out, sq, sk, splits, qk_norm)
+        B = self.B if batch is None else batch
+        d = self._attn_desc(q, q_bs, q_rs, k, k_bs, k_rs, v, v_bs, v_rs, out, sq, sk, splits, qk_norm, batch=B)
         A = cfg.attn_dim
-        kv_batches = self.B if k_bs else 1   # a batch-broadcast context is read once
-        nbytes = 2 * (2 * self.B * sq * A + 2 * kv_batches * sk * A)
+        kv_batches = B if k_bs else 1   # a batch-broadcast context is read once
+        nbytes = 2 * (2 * B * sq * A + 2 * kv_batches * sk * A)
         self._launch(name, "fam_attention", C.byref(d), "attention", nbytes,
-                     4 * self.B * cfg.num_heads * sq * sk * Dh)
+                     4 * B * cfg.num_heads * sq * sk * Dh)
         if splits > 1:
-            nq = self.B * cfg.num_heads * sq
+            nq = B * cfg.num_heads * sq
             self._launch(name + "_combine", "fam_attention_combine", C.byref(d), "attn_combine",
                          splits * nq * (4 * Dh + 8) + 2 * nq * Dh)
 
@@ -602,8 +609,13 @@ class FusedActionDiT:
                     sp = self._gemm_partial(tag + ".cross_q", h, w[f"ca_q_w{l}"])
                     self._rowop(tag + ".cross_q_row", N=A, splits=sp, bias=w[f"ca_q_b{l}"], out=qc, norm=RMS,
                                 segs=((0, w[f"ca_nq_w{l}"]),), nout=qc)
-                    self._attn(tag + ".cross_attn", qc.data_ptr(), S * A, A, kb, 0, L * 2 * A, kb + 2 * A, 0,
-                               L * 2 * A, attn, S, Lc, splits=self.kv_splits)
+                    if self.cross_flat:
+                        # the B*S normalised queries as one sequence over the shared context
+                        self._attn(tag + ".cross_attn", qc.data_ptr(), 0, A, kb, 0, L * 2 * A, kb + 2 * A, 0,
+                                   L * 2 * A, attn, B * S, Lc, batch=1)
+                    else:
+                        self._attn(tag + ".cross_attn", qc.data_ptr(), S * A, A, kb, 0, L * 2 * A, kb + 2 * A, 0,
+                                   L * 2 * A, attn, S, Lc, splits=self.kv_splits)
                 # cross o projection; x += o; AdaLN2 for the FFN
                 sp = self._gemm_partial(tag + ".cross_o", attn, w[f"ca_o_w{l}"])
                 self._rowop(tag + ".cross_o_row", N=H, splits=sp, bias=w[f"ca_o_b{l}"], res=x, out=x, norm=ADALN,
