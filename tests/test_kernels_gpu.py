@@ -847,9 +847,13 @@ def test_attention_long_key_mask(B, H, Sq, Sk, Dh, kind):
 
 
 @pytest.mark.parametrize("B,H,Sq,Sk,Dh", [(1, 8, 1560, 1560, 128), (2, 4, 200, 333, 64), (1, 2, 129, 512, 128),
-                                           (1, 3, 65, 1, 128)])
+                                           (1, 3, 65, 1, 128), (1, 2, 129, 192, 128), (2, 3, 130, 330, 128),
+                                           (1, 1, 300, 64, 128)])
 def test_attention_long_sequences(B, H, Sq, Sk, Dh):
-    """Video-token attention (Sq > 64, no mask): 128-query workgroups, 64-key LDS tiles, 32x32 MFMA."""
+    """Video-token attention (Sq > 64, no mask): 128-query workgroups, 64-key LDS tiles, 32x32 MFMA.
+    The loop takes two tiles per iteration with the partial last tile separate, so the cases cover
+    an even and an odd number of full tiles, each with and without a partial tile, a partial tile
+    alone (Sk = 1) and a single full tile."""
     q, k, v = rnd(B, Sq, H * Dh, seed=135), rnd(B, Sk, H * Dh, seed=136), rnd(B, Sk, H * Dh, seed=137)
     ref = O.flash_attention(q.float(), k.float(), v.float(), H)
     y = ops().flash_attention(dev(q), dev(k), dev(v), H)
