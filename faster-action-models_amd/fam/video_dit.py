@@ -76,6 +76,9 @@ class FusedVideoDiTBlock:
             next_mod); the block starts at its q/k/v projection.
         next_mod: the next block's ready "mods" view: this block's FFN-down row applies the
             next block's AdaLN1 into "h" (only with the split-K projections).
+        mod_group: tokens that share one modulation row (t_mod and "mods" hold B*S / mod_group
+            rows; consecutive groups of mod_group tokens read one row): 0 follows per_token_mod
+            (1 or S); WanVideoDiT passes the tokens of one latent frame, whose timestep is one.
     `self.qkv` holds [q | k | v] per row; after `run()` its k (normalised, rotated) and v
     columns are the block's attention K/V (`kv()`).
     """
@@ -85,7 +88,7 @@ class FusedVideoDiTBlock:
                  per_token_mod: bool = True, device="cuda", self_mask: Optional[torch.Tensor] = None,
                  ctx_mask: Optional[torch.Tensor] = None, shared: Optional[Dict[str, torch.Tensor]] = None,
                  kv_only: bool = False, ctx_kv: Optional[tuple] = None, mods_ready: bool = False,
-                 pre_normed: bool = False, next_mod: Optional[torch.Tensor] = None):
+                 pre_normed: bool = False, next_mod: Optional[torch.Tensor] = None, mod_group: int = 0):
         dev = torch.device(device)
         self.kv_only = kv_only
         self.mods_ready, self.pre_normed, self.next_mod = mods_ready, pre_normed, next_mod
@@ -95,7 +98,9 @@ class FusedVideoDiTBlock:
         self.H, self.nh, self.Dh, self.F = hidden, num_heads, head_dim, ffn_dim
         self.A = A = num_heads * head_dim
         self.eps = float(eps)
-        self.per_token = per_token_mod
+        self.mod_group = g = mod_group if mod_group > 0 else (1 if per_token_mod else seq_len)
+        if seq_len % g:
+            raise ValueError(f"mod_group {g} must divide seq_len {seq_len}")
         H, F = hidden, ffn_dim
         M = batch * seq_len
         pre = f"blocks.{idx}."
@@ -135,9 +140,9 @@ class FusedVideoDiTBlock:
                                  f"bf16 {tuple(shape)}")
             return t
         self.x = buf("x", M, H)
-        self.tmod_in = buf("tmod_in", M if per_token_mod else batch, 6 * H)
+        self.tmod_in = buf("tmod_in", M // g, 6 * H)
         self.ctx = buf("ctx", batch * ctx_len, H)
-        self.mods = buf("mods", M if per_token_mod else batch, 6 * H, row_strided=True)
+        self.mods = buf("mods", M // g, 6 * H, row_strided=True)
         self.h = buf("h", M, H)
         self.qkv = torch.zeros(M, 3 * A, dtype=_BF16, device=dev)   # per block: its K/V cache
         self.attn = buf("attn", M, A)
@@ -212,7 +217,7 @@ class FusedVideoDiTBlock:
         if gate is not None:
             d.gate = gate.data_ptr()
             d.gate_bs, d.gate_rs, d.gate_ns = gate_strides
-        d.rows_per_batch = self.S if M == self.B * self.S else M
+        d.rows_per_batch = self.mod_group if M == self.B * self.S else M   # the gate's modulation rows
         self._descs.append(d)
         if self.ws is not None and self.lib.fam_gemm_ws_floats(M, N, K) > 0:
             self._add(name, "fam_gemm_ws", (C.byref(d), self.ws.data_ptr(), self.ws.numel()), "gemm", 2 * M * N * K)
@@ -250,7 +255,7 @@ class FusedVideoDiTBlock:
             d.res, d.ldr = res.data_ptr(), res.stride(0)
         d.gate = gate.data_ptr() if gate is not None else None
         d.gate_bs, d.gate_rs, d.gate_ns = gate_strides
-        d.rows_per_batch = self.S
+        d.rows_per_batch = self.mod_group   # rows per gate / modulation row (RoPE positions use seq_len)
         d.out, d.ldo, d.out_f32 = out.data_ptr(), out.stride(0), 0
         d.eps = self.eps
         if rms_w is not None:
@@ -298,9 +303,10 @@ class FusedVideoDiTBlock:
                 self._adaln(name + "_adaln", out, nout, shift=adaln[0], scale=adaln[1])
 
     def _mod_strides(self, mods=None):
-        """(batch, row) element strides of a modulation chunk view: per token or per batch."""
+        """(group, row) element strides of a modulation chunk view: row r of the activations reads
+        modulation row r / mod_group (consumers take rows_per_batch = mod_group)."""
         rs = (self.mods if mods is None else mods).stride(0)
-        return (self.S * rs, rs) if self.per_token else (rs, 0)
+        return (rs, 0)
 
     def _adaln(self, name, x, y, shift=None, scale=None, lw=None, lb=None):
         M, H = x.shape
@@ -308,7 +314,7 @@ class FusedVideoDiTBlock:
         args = (x.data_ptr(), x.stride(0), shift.data_ptr() if shift is not None else None,
                 scale.data_ptr() if scale is not None else None, mbs, mrs,
                 lw.data_ptr() if lw is not None else None, lb.data_ptr() if lb is not None else None,
-                y.data_ptr(), y.stride(0), M, self.S, H, self.eps)
+                y.data_ptr(), y.stride(0), M, self.mod_group, H, self.eps)
         self._add(name, "fam_adaln", args, "adaln")
 
     def _rms(self, name, x_ptr, ld, rows, seq, weight, rope):
@@ -477,7 +483,7 @@ class FusedVideoPrefill:
                  head_dim: int, ffn_dim: int, batch: int, video_len: int, ctx_len: int, freqs: torch.Tensor,
                  eps: float = 1e-6, per_token_mod: bool = True, video_mask: Optional[torch.Tensor] = None,
                  ctx_mask: Optional[torch.Tensor] = None, num_run: int = 0, device="cuda",
-                 keep_output: bool = False):
+                 keep_output: bool = False, mod_group: int = 0):
         dev = torch.device(device)
         self.keep_output = keep_output
         self.L = num_layers
@@ -485,7 +491,8 @@ class FusedVideoPrefill:
         self.B, self.S, self.Lc, self.H, self.A = batch, video_len, ctx_len, hidden, num_heads * head_dim
         M = batch * video_len
         z = lambda *s: torch.zeros(*s, dtype=_BF16, device=dev)  # noqa: E731
-        rows = M if per_token_mod else batch
+        g = mod_group if mod_group > 0 else (1 if per_token_mod else video_len)
+        rows = M // g   # modulation rows: one per group of g tokens
         self.shared = {"x": z(M, hidden), "tmod_in": z(rows, 6 * hidden), "ctx": z(batch * ctx_len, hidden),
                        "mods": z(rows, 6 * hidden), "h": z(M, hidden), "attn": z(M, self.A), "qc": z(M, self.A),
                        "ckv": z(batch * ctx_len, 2 * self.A), "hid": z(M, ffn_dim)}
@@ -534,7 +541,8 @@ class FusedVideoPrefill:
 
         self.blocks = [FusedVideoDiTBlock(params, i, hidden=hidden, num_heads=num_heads, head_dim=head_dim,
                                           ffn_dim=ffn_dim, batch=batch, seq_len=video_len, ctx_len=ctx_len,
-                                          freqs=freqs, eps=eps, per_token_mod=per_token_mod, device=dev,
+                                          freqs=freqs, eps=eps, per_token_mod=per_token_mod, mod_group=g,
+                                          device=dev,
                                           self_mask=video_mask, ctx_mask=ctx_mask,
                                           shared={**self.shared, "mods": mods(i)},
                                           kv_only=(i == self.n_run - 1 and not keep_output),
@@ -729,9 +737,12 @@ class FusedWanVideoDiT:
         self.ts2 = z(2 * B)                       # (0, t_b) per sample: the distinct token timesteps
         self.ctx_in = z(B * Lc, cfg.text_dim)
         self.cmask = torch.ones(B, Lc, dtype=torch.bool, device=dev)
-        # token -> distinct-row index: sample b, frame 0 -> 2b, later frames -> 2b + 1
-        tok = torch.arange(S)
-        idx = (2 * torch.arange(B)[:, None] + (tok[None, :] >= self.tpf).long()).reshape(-1)
+        # the timestep, hence t and t_mod, is one per latent frame: the modulation tables hold a
+        # row per (sample, frame) -- gathered from the two distinct rows, frame 0 -> 2b, later
+        # frames -> 2b + 1 -- and every consumer reads row (token / tokens per frame)
+        self.nf = f
+        fr = torch.arange(f)
+        idx = (2 * torch.arange(B)[:, None] + (fr[None, :] > 0).long()).reshape(-1)
         self.row_idx = idx.to(device=dev, dtype=torch.int32).contiguous()
 
         freqs = video_freqs_3d(cfg.attn_head_dim, f, h, w)
@@ -740,7 +751,7 @@ class FusedWanVideoDiT:
                                         head_dim=cfg.attn_head_dim, ffn_dim=cfg.ffn_dim, batch=B, video_len=S,
                                         ctx_len=Lc, freqs=freqs, eps=cfg.eps, video_mask=video_mask,
                                         ctx_mask=self.cmask if Lc > 0 else None, device=dev,
-                                        keep_output=(mode != "prefill"))
+                                        keep_output=(mode != "prefill"), mod_group=self.tpf)
         sh = self.blocks.shared
         self.patches = z(B * S, C * P)
         self.emb = z(2 * B, cfg.freq_dim)
@@ -759,29 +770,29 @@ class FusedWanVideoDiT:
         self._gemm("time_emb0", self.emb, w_["te0_w"], w_["te0_b"], self.t1, act=_capi.FAM_ACT_SILU)
         self._gemm("time_emb2_silu", self.t1, w_["te2_w"], w_["te2_b"], self.t2s, act=_capi.FAM_ACT_SILU)
         self._gemm("time_proj", self.t2s, w_["tp_w"], w_["tp_b"], self.tmod2)
-        add("tmod_tokens", "fam_gather_rows", (self.tmod2.data_ptr(), 6 * H, 2 * B, self.row_idx.data_ptr(),
-                                               sh["tmod_in"].data_ptr(), 6 * H, B * S, 6 * H), "gather")
+        add("tmod_frames", "fam_gather_rows", (self.tmod2.data_ptr(), 6 * H, 2 * B, self.row_idx.data_ptr(),
+                                               sh["tmod_in"].data_ptr(), 6 * H, B * f, 6 * H), "gather")
         if mode == "forward":
             self.t2 = z(2 * B, H)
-            self.t_tok = z(B * S, H)
+            self.t_frm = z(B * f, H)
             self._gemm("time_emb2", self.t1, w_["te2_w"], w_["te2_b"], self.t2)
-            add("t_tokens", "fam_gather_rows", (self.t2.data_ptr(), H, 2 * B, self.row_idx.data_ptr(),
-                                                self.t_tok.data_ptr(), H, B * S, H), "gather")
+            add("t_frames", "fam_gather_rows", (self.t2.data_ptr(), H, 2 * B, self.row_idx.data_ptr(),
+                                                self.t_frm.data_ptr(), H, B * f, H), "gather")
         if Lc > 0:
             self._gemm("text_emb0", self.ctx_in, w_["txt0_w"], w_["txt0_b"], self.ctx_h, act=_capi.FAM_ACT_GELU_TANH)
             self._gemm("text_emb2", self.ctx_h, w_["txt2_w"], w_["txt2_b"], sh["ctx"])
         self.steps += self.blocks.steps
         self.meta += self.blocks.meta
         if mode == "forward":
-            self.head_mod = z(B * S, 2, H)
+            self.head_mod = z(B * f, 2, H)
             self.hn = z(B * S, H)
             self.head_out = z(B * S, cfg.out_dim * P)
             self.out = z(B, cfg.out_dim, frames, height, width)
-            add("head_modulation", "fam_add_modulation", (self.t_tok.data_ptr(), w_["head_mod"].data_ptr(),
-                                                          self.head_mod.data_ptr(), B * S, 2, H), "modulation")
+            add("head_modulation", "fam_add_modulation", (self.t_frm.data_ptr(), w_["head_mod"].data_ptr(),
+                                                          self.head_mod.data_ptr(), B * f, 2, H), "modulation")
             hm = self.head_mod.data_ptr()
-            add("head_adaln", "fam_adaln", (sh["x"].data_ptr(), H, hm, hm + 2 * H, 0, 2 * H, None, None,
-                                            self.hn.data_ptr(), H, B * S, B * S, H, float(cfg.eps)), "adaln")
+            add("head_adaln", "fam_adaln", (sh["x"].data_ptr(), H, hm, hm + 2 * H, 2 * H, 0, None, None,
+                                            self.hn.data_ptr(), H, B * S, self.tpf, H, float(cfg.eps)), "adaln")
             self._gemm("head", self.hn, w_["head_w"], w_["head_b"], self.head_out)
             add("unpatchify", "fam_unpatchify", (self.head_out.data_ptr(), B, cfg.out_dim, f, h, w, pt, ph, pw,
                                                  self.out.data_ptr()), "patchify", 4 * self.out.numel())
@@ -879,9 +890,11 @@ class FusedWanVideoDiT:
         [B, S, H] (before the blocks ran), t_mod [B, S, 6, H], context [B, Lc, H], freqs."""
         sh = self.blocks.shared
         H = self.cfg.hidden_dim
-        return {"tokens": sh["x"].view(self.B, self.S, H), "t_mod": sh["tmod_in"].view(self.B, self.S, 6, H),
-                "context": sh["ctx"].view(self.B, self.Lc, H), "freqs": self.freqs,
-                "t": self.t_tok.view(self.B, self.S, H) if self.mode == "forward" else None}
+        # per-token views of the per-frame tables (host-side expansion, for inspection)
+        tm = sh["tmod_in"].view(self.B, self.nf, 6, H).repeat_interleave(self.tpf, dim=1)
+        t = self.t_frm.view(self.B, self.nf, H).repeat_interleave(self.tpf, dim=1) if self.mode == "forward" else None
+        return {"tokens": sh["x"].view(self.B, self.S, H), "t_mod": tm,
+                "context": sh["ctx"].view(self.B, self.Lc, H), "freqs": self.freqs, "t": t}
 
     @property
     def num_launches(self) -> int:
