@@ -693,12 +693,15 @@ __global__ __launch_bounds__(NW * 64) void attn_small_kernel(AttnArgs a) {
   const uint32_t bh32 = blockIdx.x, H32 = (uint32_t)a.H;
   const int64_t b = bh32 / H32, h = bh32 - (uint32_t)b * H32;
   const int dv0 = (int)blockIdx.y * DVW;
-  const int Sq = (int)a.Sq, Sk = (int)a.Sk;
+  // grid.z: chunks of 32 queries (more than 32 queries without on-load normalisation); Sq is
+  // this chunk's query count, qz its first query
+  const int qz = (int)blockIdx.z * 32;
+  const int Sq = min(32, (int)a.Sq - qz), Sk = (int)a.Sk;
   const int k0 = wave * KB;
   const SegRows krows = key_rows(a, b, h), vrows = val_rows(a, b, h);
 
   // ---- phase 1: every load
-  const bf16* qbase = a.q + b * a.q_bs + h * a.q_hs;
+  const bf16* qbase = a.q + b * a.q_bs + h * a.q_hs + (int64_t)qz * a.q_rs;
   bf16x8 qr[QCH], qw[QCH];
   f32x4 ssv[QCH][QN ? NSS : 1];
   const int nss = QN ? (int)(a.nwidth / 16 / CPR / 4) : 0;   // 16-byte chunks of a thread's share
@@ -709,7 +712,7 @@ __global__ __launch_bounds__(NW * 64) void attn_small_kernel(AttnArgs a) {
     qr[j] = load8(qbase + qc * a.q_rs + d0);
     if constexpr (QN) {
       qw[j] = load8(a.qnw + h * DH + d0);
-      const float* p = a.qss + (b * a.ssbr + qc) * a.ssrs + a.qg0 + (idx % CPR) * (a.nwidth / 16 / CPR);
+      const float* p = a.qss + (b * a.ssbr + qz + qc) * a.ssrs + a.qg0 + (idx % CPR) * (a.nwidth / 16 / CPR);
 #pragma unroll
       for (int u = 0; u < NSS; ++u) ssv[j][u] = *reinterpret_cast<const f32x4*>(p + 4 * (u < nss ? u : 0));
     }
@@ -745,7 +748,7 @@ __global__ __launch_bounds__(NW * 64) void attn_small_kernel(AttnArgs a) {
         for (int e = 0; e < 4; ++e) mraw[t][kt][e] = 0u;
   } else {
     const int msz = MK == 1 ? 1 : (mk == FAM_MASK_ADD_F32 ? 4 : 2);
-    const auto mrs = buffer_rsrc((const void*)((const char*)a.mask + (b * a.mbs + h * a.mhs) * msz),
+    const auto mrs = buffer_rsrc((const void*)((const char*)a.mask + (b * a.mbs + h * a.mhs + (int64_t)qz * a.mqs) * msz),
                                  (uint32_t)(((int64_t)(Sq - 1) * a.mqs + Sk) * msz));
     auto moff = [&](int t, int kt, int e) {
       const int q = t * 16 + l16, kk = k0 + kt * 16 + lg * 4 + e;
@@ -910,7 +913,7 @@ __global__ __launch_bounds__(NW * 64) void attn_small_kernel(AttnArgs a) {
     bf16x4 ov;
 #pragma unroll
     for (int e = 0; e < 4; ++e) ov[e] = to_bf(o[e] * inv);
-    *reinterpret_cast<bf16x4*>(a.o + b * a.o_bs + q * a.o_rs + h * a.o_hs + dv0 + d0) = ov;
+    *reinterpret_cast<bf16x4*>(a.o + b * a.o_bs + (int64_t)(qz + q) * a.o_rs + h * a.o_hs + dv0 + d0) = ov;
   }
 }
 
@@ -1639,25 +1642,27 @@ static void launch_small_nv(const AttnArgs& a, bool qn, dim3 grid, hipStream_t s
   else launch_small_mk<DH, NW, NV, 0>(a, grid, s);
 }
 template <int DH, int NW>
-static void launch_small_nw(const AttnArgs& a, bool qn, int64_t bh, hipStream_t s) {
-  // a head over 8 or 4 CUs (output-dim eighths / quarters) while that keeps the grid within one
-  // round: each slice's workgroup repeats the scores but runs 1/NV of P V and of the merge
-  // (eighths only at DH = 128: a slice keeps at least one 16-dim MFMA tile)
+static void launch_small_nw(const AttnArgs& a, bool qn, int64_t bh, int nqc, hipStream_t s) {
+  // a (head, query chunk) over 8 or 4 CUs (output-dim eighths / quarters) while that keeps the
+  // grid within one round: each slice's workgroup repeats the scores but runs 1/NV of P V and of
+  // the merge (eighths only at DH = 128: a slice keeps at least one 16-dim MFMA tile)
+  const int64_t units = bh * nqc;
   if constexpr (DH == 128) {
-    if (bh <= 32) {
-      launch_small_nv<DH, NW, 8>(a, qn, dim3((unsigned)bh, 8), s);
+    if (units <= 32) {
+      launch_small_nv<DH, NW, 8>(a, qn, dim3((unsigned)bh, 8, (unsigned)nqc), s);
       return;
     }
   }
-  if (bh <= 64) launch_small_nv<DH, NW, 4>(a, qn, dim3((unsigned)bh, 4), s);
-  else launch_small_nv<DH, NW, 1>(a, qn, dim3((unsigned)bh, 1), s);
+  if (units <= 64) launch_small_nv<DH, NW, 4>(a, qn, dim3((unsigned)bh, 4, (unsigned)nqc), s);
+  else launch_small_nv<DH, NW, 1>(a, qn, dim3((unsigned)bh, 1, (unsigned)nqc), s);
 }
 template <int DH>
 static void launch_small(const AttnArgs& a, int nw, bool qn, int64_t bh, hipStream_t s) {
-  if (nw <= 2) launch_small_nw<DH, 2>(a, qn, bh, s);
-  else if (nw <= 4) launch_small_nw<DH, 4>(a, qn, bh, s);
-  else if (nw <= 6) launch_small_nw<DH, 6>(a, qn, bh, s);
-  else launch_small_nw<DH, 8>(a, qn, bh, s);
+  const int nqc = (int)((a.Sq + 31) / 32);   // query chunks (one unless more than 32 queries)
+  if (nw <= 2) launch_small_nw<DH, 2>(a, qn, bh, nqc, s);
+  else if (nw <= 4) launch_small_nw<DH, 4>(a, qn, bh, nqc, s);
+  else if (nw <= 6) launch_small_nw<DH, 6>(a, qn, bh, nqc, s);
+  else launch_small_nw<DH, 8>(a, qn, bh, nqc, s);
 }
 
 template <int DH>
@@ -1673,13 +1678,14 @@ static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
   }
   if constexpr (DH == 64 || DH == 128) {
     // up to 32 queries over up to 256 keys in one workgroup per head (no key splits): the MoT
-    // joint attention over [video K/V ; action K/V], a short context
-    // (its mask entries are buffer loads with 32-bit offsets over one (batch, head) span)
+    // joint attention over [video K/V ; action K/V], a short context; up to 128 queries without
+    // on-load normalisation as chunks of 32 (grid.z; the video prefill's 98 tokens over 98 / 129
+    // keys) (its mask entries are buffer loads with 32-bit offsets over one (batch, head) span)
     const int64_t msz = a.mask_kind == FAM_MASK_BOOL ? 1 : (a.mask_kind == FAM_MASK_ADD_F32 ? 4 : 2);
     const bool mask_fits = a.mask_kind == FAM_MASK_NONE ||
                            (a.mqs >= 0 && ((a.Sq - 1) * a.mqs + a.Sk) * msz < ((int64_t)1 << 31));
-    if (a.Sq <= 32 && a.Sk >= 1 && a.Sk <= 256 && a.splits == 1 && a.kss == nullptr && mask_fits &&
-        (a.qss == nullptr || a.nwidth <= 4096)) {
+    if ((a.Sq <= 32 || (a.Sq <= 128 && a.qss == nullptr)) && a.Sk >= 1 && a.Sk <= 256 && a.splits == 1 &&
+        a.kss == nullptr && mask_fits && (a.qss == nullptr || a.nwidth <= 4096)) {
       const int nw = (int)((a.Sk + KB - 1) / KB);
       launch_small<DH>(a, nw, a.qss != nullptr, bh, s);
       return;

@@ -234,6 +234,34 @@ def test_attention_masks(kind):
     assert torch.all(y[:, 3] == 0)
 
 
+@pytest.mark.parametrize("B,H,Sq,Sk,Dh,mask", [(1, 24, 98, 98, 128, None), (1, 24, 98, 129, 128, "keys"),
+                                                (2, 4, 98, 98, 64, None), (2, 3, 70, 200, 128, "rows"),
+                                                (1, 2, 128, 256, 64, "rows"), (1, 2, 33, 31, 128, "rows")])
+def test_attention_small_query_chunks(B, H, Sq, Sk, Dh, mask):
+    """33-128 queries over <= 256 keys run the small kernel in chunks of 32 queries (grid.z): the
+    video prefill's 98 tokens over their own 98 keys and over 129 context keys with the text mask
+    ("keys": [B, Sk], shared by the queries), and a per-query bool mask ("rows": [B, 1, Sq, Sk],
+    whose rows each chunk must take from its own offset, with a fully masked row), ragged last
+    chunks (98 = 3 x 32 + 2, 70, 33) and a full 128."""
+    q, k, v = rnd(B, Sq, H * Dh, seed=31), rnd(B, Sk, H * Dh, seed=32), rnd(B, Sk, H * Dh, seed=33)
+    g = torch.Generator().manual_seed(34)
+    m = None
+    if mask == "keys":
+        m = torch.ones(B, 1, 1, Sk, dtype=torch.bool)
+        m[..., Sk - 29:] = False
+    elif mask == "rows":
+        m = torch.rand(B, 1, Sq, Sk, generator=g) > 0.4
+        m[:, :, Sq - 1] = False    # a fully masked row in the last chunk -> zeros
+    ref = O.flash_attention(q.float(), k.float(), v.float(), H, m)
+    if mask == "keys":
+        y = ops().flash_attention(dev(q), dev(k), dev(v), H, ctx_mask=dev(m))
+    else:
+        y = ops().flash_attention(dev(q), dev(k), dev(v), H, None if m is None else dev(m))
+    assert relerr(y, ref) <= TOL
+    if mask == "rows":
+        assert torch.all(y[:, Sq - 1] == 0)
+
+
 def test_attention_two_segments_joint_mask():
     """Joint attention over a cached video prefix + action tokens with the MoT mask (FB/mot.py:446-478)."""
     Sv, Sa, H, Dh, tpf = 98, 32, 24, 128, 98
