@@ -1,6 +1,6 @@
 // Flash-style attention on bf16 MFMA (gfx950):  o = softmax(q k^T * scale + mask) v.
 //
-// Formulation (both kernels).  Scores are computed transposed, S^T = K Q^T, with the key
+// Formulation (every kernel).  Scores are computed transposed, S^T = K Q^T, with the key
 // tile as the MFMA A-operand and the query tile as the B-operand (v_mfma_f32_16x16x32_bf16).
 // A lane then owns ONE query (column l%16) and four keys per 16-key sub-tile, so the running
 // max / sum of the online softmax are per-lane scalars reduced over the 4 lane groups with
@@ -18,6 +18,12 @@
 //
 // attn_tiled_kernel (Sq > 64: video tokens): a workgroup of 4 waves owns 64 queries of one
 // (batch, head); 32-key K/V blocks are staged through LDS and shared by the waves.
+//
+// Head dims 64 and 128 take specialised kernels first (launch_dh): attn_self_kernel (the action
+// tokens over their own keys), attn_small_kernel (up to 128 queries over up to 256 keys),
+// attn_cross_kernel (up to 32 queries over a long context, key splits + attn_combine_kernel)
+// and attn_long_kernel (128 queries per workgroup over one long key segment); the two kernels
+// above take what none of them covers.
 //
 // Algorithmic bytes per launch: 2*B*H*Dh*(2*Sq + 2*Sk) (+ mask); flops 4*B*H*Sq*Sk*Dh.
 #include <algorithm>
@@ -652,8 +658,10 @@ __global__ __launch_bounds__(256) void attn_self_kernel(AttnArgs a) {
 // ---------------------------------------------------------------------------------------
 // attn_small_kernel: up to 32 queries over up to 32 NW keys (two segments, optional mask): the
 // MoT joint attention of the action tokens over [cached video K/V ; action K/V] and their
-// cross-attention to a short context.  Grid (batch * head, NV): workgroup (bh, y) produces
-// output dims [y DH/NV, (y+1) DH/NV) of its head, one wave per 32-key block.  Every workgroup of
+// cross-attention to a short context; without on-load q normalisation also up to 128 queries
+// as chunks of 32 (grid.z: the video prefill's 98 tokens over their own 98 keys or 129 text
+// keys).  Grid (batch * head, NV, chunks): workgroup (bh, y, z) produces output dims
+// [y DH/NV, (y+1) DH/NV) of queries [32 z, 32 z + 32) of its head, one wave per 32-key block.  Every workgroup of
 // a head computes the same full scores, so the dim split needs no combine; it divides the V
 // reads and spreads a head over NV CUs.  Every global load is issued before the first use:
 //   - the queries, once per workgroup, staged in LDS (NSS > 0: q arrives raw from

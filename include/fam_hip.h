@@ -127,9 +127,16 @@ int fam_rmsnorm_grouped(const void* x, int64_t x_row_stride, void* y, int64_t y_
  * sk0..sk0+sk1-1 from (k1, v1) (sk1 = 0: one segment), e.g. a cached video prefix followed
  * by the action tokens.  The mask element for (b, h, q, key) is
  * mask[b*mask_bs + h*mask_hs + q*mask_qs + key].  A query row with every key masked gives 0.
- * Work split: for Sq <= 64 one workgroup per (b, h) holds all queries and its waves split
- * the keys (partial softmax states merged in LDS in a fixed order); for longer Sq each
- * workgroup owns 64 queries of one (b, h).
+ * Work split (head_dim 64 / 128): up to 32 queries over their own <= 32 unmasked keys, one
+ * workgroup per (b, h) with q, k and v staged in LDS; up to 32 queries over <= 256 keys (up to
+ * 128 queries when q is not normalised on load, as chunks of 32), one workgroup per (b, h) and
+ * chunk whose waves split the keys (partial softmax states merged in LDS in a fixed order); up
+ * to 32 queries over one long unmasked key segment, one workgroup per (b, h) and key split;
+ * longer query sequences over one key segment with no mask or a key-only boolean mask, 128
+ * queries per workgroup with the K/V tiles streamed through LDS; otherwise (and for the other
+ * head dims) one workgroup per (b, h) holding all queries up to 32 (64 for head_dim < 128),
+ * 64 queries per workgroup beyond.  Every path gives the same result up to fp32 summation
+ * order; for a given shape and arguments the path, and so the bits, are fixed.
  * Replaces: flash_attention(q, k, v, num_heads, ctx_mask)  FB/wan_video_dit.py:17-26,
  *           FG/wan_video_dit.py:18-39, CA/wan_video_dit.py:569-587;
  *           fastwam::short_attn / short_attn_bsd          FG/wan_video_dit.py:1680-1721, FG/mot.py:682-722;
