@@ -72,10 +72,14 @@ __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
       for (int i = 0; i < NV; ++i) xv8[k][i] = load8(a.x + r * a.xrs + col(i));
     }
     if constexpr (AFF) {
+      // an absent weight or bias reads x instead (a valid address; finish ignores the value):
+      // a load under a branch, or a select on its value, would wait for the x loads before it
+      const bf16* wsrc = a.w ? a.w : a.x;
+      const bf16* bsrc = a.b ? a.b : a.x;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
-        wv[i] = a.w ? load8(a.w + col(i)) : xv8[0][i];
-        bv[i] = a.b ? load8(a.b + col(i)) : xv8[0][i];
+        wv[i] = load8(wsrc + col(i));
+        bv[i] = load8(bsrc + col(i));
       }
     }
     if constexpr (MOD == 1) {
@@ -257,7 +261,9 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_vec_kernel(RmsRopeArgs a) {
   const int64_t r0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
   if (r0 >= a.rows) return;  // wave-uniform
   const int D = (int)a.dim, hd = (int)a.hd;
-  const bf16* wr = a.w ? a.w + (r0 % a.wgp) * (int64_t)D : nullptr;   // RPW > 1 only with one group
+  // without a weight the weight loads read x (a valid address, value unused): an unconditional
+  // load joins the others in one wait, where a load under a branch waits for those before it
+  const bf16* wr = a.w ? a.w + (r0 % a.wgp) * (int64_t)D : a.x;   // RPW > 1 only with one group
   bf16x8 in[RPW][NV], wv[NV];
   f32x4 t0[RPW][NT], t1[RPW][NT];
 #pragma unroll
@@ -271,7 +277,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_vec_kernel(RmsRopeArgs a) {
     for (int i = 0; i < NV; ++i) {
       const int c = (i * 64 + lane) * 8, cc = c < D ? c : 0;
       in[k][i] = load8(xr + cc);
-      if (k == 0 && a.w) wv[i] = load8(wr + cc);   // wave-uniform
+      if (k == 0) wv[i] = load8(wr + cc);
       if (i < NT) {
         const int j0 = ((TSH ? lane * 8 : cc) % hd) >> 1;   // first of the 4 rotation pairs of these 8 elements
         if constexpr (TAB == 1) {
