@@ -524,11 +524,12 @@ class FusedVideoPrefill:
             self.cnk = [params[f"blocks.{i}.cross_attn.norm_k.weight"].to(device=dev, dtype=_BF16).contiguous()
                         for i in range(ncross)]
             self._ctx_launches(batch * ctx_len, ctx_len, head_dim, eps)
-        # at <= 128 rows the modulation + t_mod of every block comes from one launch into a
-        # [rows, blocks, 6H] buffer, and each block's FFN-down row also applies the next block's
-        # AdaLN1
+        # the modulation + t_mod of every block comes from one launch into a [rows, blocks, 6H]
+        # buffer (up to 256 MB of it; per block otherwise), and at <= 128 rows each block's
+        # FFN-down row also applies the next block's AdaLN1
         chain = M <= 128 and hidden <= 4096 and self.A <= 4096     # the blocks' split-K condition
-        if chain:
+        one_mod = chain or rows * self.n_run * 6 * hidden * 2 <= (256 << 20)
+        if one_mod:
             self.mod_table = torch.stack([params[f"blocks.{i}.modulation"].reshape(6 * hidden)
                                           for i in range(self.n_run)]).to(device=dev, dtype=_BF16).contiguous()
             self.mods_all = z(rows, self.n_run, 6 * hidden)
@@ -537,7 +538,7 @@ class FusedVideoPrefill:
                             rows, self.n_run, 6 * hidden), "modulation")
 
         def mods(i):
-            return self.mods_all[:, i, :] if chain else self.shared["mods"]
+            return self.mods_all[:, i, :] if one_mod else self.shared["mods"]
 
         self.blocks = [FusedVideoDiTBlock(params, i, hidden=hidden, num_heads=num_heads, head_dim=head_dim,
                                           ffn_dim=ffn_dim, batch=batch, seq_len=video_len, ctx_len=ctx_len,
@@ -547,7 +548,7 @@ class FusedVideoPrefill:
                                           shared={**self.shared, "mods": mods(i)},
                                           kv_only=(i == self.n_run - 1 and not keep_output),
                                           ctx_kv=(self.ctxkv, i * 2 * self.A) if i < ncross else None,
-                                          mods_ready=chain, pre_normed=chain and i > 0,
+                                          mods_ready=one_mod, pre_normed=chain and i > 0,
                                           next_mod=mods(i + 1) if chain and i + 1 < self.n_run else None)
                        for i in range(self.n_run)]
         self.steps += [f for b in self.blocks for f in b.steps]
