@@ -1171,9 +1171,13 @@ __global__ __launch_bounds__(256) void attn_cross_kernel(AttnArgs a) {
 // KMASK: a boolean key mask shared by every query (mask query stride 0: the text padding mask
 // of the cross-attention, [B, Lc] or [B, H, Lc]); each tile's 64 entries travel with the K/V
 // tile as additive 0 / -inf terms in LDS (keys past Sk included).
-template <int DH, bool KMASK>
-__global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) {
-  constexpr int NTH = 256;               // threads; 32 queries per wave
+// KW = 2 (head dim 128, a grid of at most one workgroup per CU): 8 waves in two key groups of
+// 4; group g takes the tiles g, g + 2, g + 4, ... of the same 128 queries with its own LDS slots,
+// so each SIMD runs two waves (one's softmax under the other's MFMAs) although the grid leaves
+// one workgroup per CU, and group 1 hands its softmax state to group 0 through LDS at the end.
+template <int DH, bool KMASK, int KW>
+__global__ __launch_bounds__(256 * KW, 2 / KW) void attn_long_kernel(AttnArgs a, int nqb) {
+  constexpr int NTH = 256 * KW;          // threads; 32 queries per wave, KW waves per query group
   constexpr int BN = 64;                 // keys per tile
   constexpr int KS = DH / 16;            // 16-wide k-steps of S^T = K Q^T
   constexpr int DT = DH / 32;            // 32-row dim tiles of O^T
@@ -1187,15 +1191,18 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   // padded rows -- K 144 bytes, V 192 mod 256, so the transposing reads of 8 rows x 64 bytes
   // fill the banks twice exactly.
   constexpr bool DMA = DH == 128;
+  static_assert(KW == 1 || (KW == 2 && DMA), "key groups need the direct-to-LDS path");
   constexpr int KLD = DH + 8, VLD = DH == 128 ? 160 : 96;
   __shared__ bf16 Ks[2][DMA ? 1 : BN][DMA ? 8 : KLD];
   __shared__ bf16 Vs[2][DMA ? 1 : BN][DMA ? 8 : VLD];
-  __shared__ __attribute__((aligned(1024))) bf16 Kd[DMA ? 2 : 1][DMA ? BN * DH : 8];
-  __shared__ __attribute__((aligned(1024))) bf16 Vd[DMA ? 2 : 1][DMA ? BN * DH : 8];
-  __shared__ __attribute__((aligned(16))) float Mb[KMASK ? 2 : 1][BN];
+  __shared__ __attribute__((aligned(1024))) bf16 Kd[DMA ? 2 : 1][KW][DMA ? BN * DH : 8];
+  __shared__ __attribute__((aligned(1024))) bf16 Vd[DMA ? 2 : 1][KW][DMA ? BN * DH : 8];
+  __shared__ __attribute__((aligned(16))) float Mb[KMASK ? 2 : 1][KW][BN];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & 3;   // wave: query group
   const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int kg = KW == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid >> 8);   // key group
+  const int gtid = KW == 1 ? tid : tid & 255;                               // thread within it
   const int l32 = lane & 31, hh = lane >> 5;
   // XCD-aware task order: workgroup i runs on XCD i % 8; give each XCD a contiguous range of
   // (head, query block) tasks so that a head's query blocks share that XCD's L2
@@ -1234,9 +1241,9 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
 #pragma unroll
       for (int n = 0; n < BN / 16; ++n) {
         const int r0 = 4 * (wv + 4 * n);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)&Kd[buf][r0 * DH], 16, dk,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)&Kd[buf][kg][r0 * DH], 16, dk,
                                                  (uint32_t)r0 * krs, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&Vd[buf][r0 * DH], 16, dv,
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&Vd[buf][kg][r0 * DH], 16, dv,
                                                  (uint32_t)r0 * vrs, 0, 0);
       }
     }
@@ -1273,13 +1280,13 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   int mr = 0;
   auto gload_m = [&](int t) {
     if constexpr (KMASK) {
-      const int key = t * BN + (tid & (BN - 1));
+      const int key = t * BN + (gtid & (BN - 1));
       mr = key < Sk ? (int)mrow[key] : 0;
     }
   };
   auto lstore_m = [&](int buf) {
     if constexpr (KMASK) {
-      if (tid < BN) Mb[buf][tid] = mr ? 0.f : -INFINITY;
+      if (gtid < BN) Mb[buf][kg][gtid] = mr ? 0.f : -INFINITY;
     }
   };
   // A operand of the PV product (V^T: row = dim, k = key) straight from the row-major tile
@@ -1312,7 +1319,7 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   }
   auto vfrag = [&](int buf, int k0, int d) {
     const lds_bf16* p0;
-    if constexpr (DMA) p0 = (const lds_bf16*)&Vd[buf][0] + vofs[d] + k0 * DH;
+    if constexpr (DMA) p0 = (const lds_bf16*)&Vd[buf][kg][0] + vofs[d] + k0 * DH;
     else p0 = (const lds_bf16*)&Vs[buf][0][0] + voff_l + k0 * VLD + d * 32;
     const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p0);
     const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0 + 8 * (DMA ? DH : VLD)));
@@ -1324,7 +1331,7 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   // query; the two halves are independent MFMA chains, interleaved
   auto kfrag = [&](int buf, int kt, int ks) {
     const lds_bf16* p;
-    if constexpr (DMA) p = (const lds_bf16*)&Kd[buf][0] + kofs[ks] + kt * 32 * DH;
+    if constexpr (DMA) p = (const lds_bf16*)&Kd[buf][kg][0] + kofs[ks] + kt * 32 * DH;
     else p = (const lds_bf16*)&Ks[buf][0][0] + koff_l + kt * 32 * KLD + ks * 16;
     return *reinterpret_cast<const __attribute__((address_space(3))) bf16x8*>(p);
   };
@@ -1333,16 +1340,16 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
   for (int d = 0; d < DT; ++d) acc[d] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
   const float sl2 = a.scale_log2;
+  const int ntiles_kw = (Sk + BN - 1) / BN;
+  const int nfull_kw = KMASK ? ntiles_kw : Sk / BN;
 
-  // one 64-key tile from LDS buffer BUF (= t & 1); TAIL (the partial last tile without a key
-  // mask) sets the scores of keys past Sk to -inf, so full tiles carry no per-score masking
-  auto tile = [&](int t, auto tail_tag, auto buf_tag) {
+  // one 64-key tile t of this key group from LDS buffer BUF; TAIL (the partial last tile
+  // without a key mask) sets the scores of keys past Sk to -inf, so full tiles carry no
+  // per-score masking.  The group's next tile (t + KW) goes to the other buffer first, which the
+  // last barrier released (zeros past Sk).
+  auto compute = [&](int t, auto tail_tag, auto buf_tag) {
     constexpr bool TAIL = decltype(tail_tag)::value;
     constexpr int buf = decltype(buf_tag)::value;
-    dma_kv(t + 1, buf ^ 1);   // zeros past Sk; that buffer was released by the last barrier
-    gload_kv(t + 1);
-    gload_m(t + 1);
-    __builtin_amdgcn_sched_barrier(0);
     f32x16 st[2] = {f32x16{}, f32x16{}};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
@@ -1354,7 +1361,7 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
-          const f32x4 m4 = *reinterpret_cast<const f32x4*>(&Mb[buf][kt * 32 + 8 * g4 + 4 * hh]);
+          const f32x4 m4 = *reinterpret_cast<const f32x4*>(&Mb[buf][kg][kt * 32 + 8 * g4 + 4 * hh]);
 #pragma unroll
           for (int e = 0; e < 4; ++e) st[kt][4 * g4 + e] += m4[e];
         }
@@ -1405,36 +1412,87 @@ __global__ __launch_bounds__(256, 2) void attn_long_kernel(AttnArgs a, int nqb) 
       for (int c = 0; c < 2; ++c)
 #pragma unroll
         for (int d = 0; d < DT; ++d) acc[d] = mfma32(vfrag(buf, kt * 32 + 16 * c, d), pf[kt][c], acc[d]);
-    lstore_kv(buf ^ 1);
-    lstore_m(buf ^ 1);
-    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): tile t + 1 landed
+  };
+  auto prefetch = [&](int t, int buf) {
+    dma_kv(t, buf);
+    gload_kv(t);
+    gload_m(t);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto finish = [&](int buf) {
+    lstore_kv(buf);
+    lstore_m(buf);
+    if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): the next tile landed
     __syncthreads();
   };
+  auto tile = [&](int t, auto tail_tag, auto buf_tag) {
+    constexpr int buf = decltype(buf_tag)::value;
+    prefetch(t + 1, buf ^ 1);
+    compute(t, tail_tag, buf_tag);
+    finish(buf ^ 1);
+  };
+  // KW = 2: stage s holds tile 2 s + kg of each key group; a group whose tile is past the end
+  // (odd tile count) only loads zeros and meets the barriers
+  auto stage = [&](int s, auto buf_tag) {
+    constexpr int buf = decltype(buf_tag)::value;
+    const int tg = KW * s + kg;
+    prefetch(tg + KW, buf ^ 1);
+    if (tg < nfull_kw) compute(tg, std::false_type{}, buf_tag);
+    else if (tg < ntiles_kw) compute(tg, std::true_type{}, buf_tag);
+    finish(buf ^ 1);
+  };
 
-  const int ntiles = (Sk + BN - 1) / BN;
-  const int nfull = KMASK ? ntiles : Sk / BN;   // tiles whose keys are all below Sk (or masked)
-  dma_kv(0, 0);
-  gload_kv(0);
-  gload_m(0);
-  __builtin_amdgcn_sched_barrier(0);
-  lstore_kv(0);
-  lstore_m(0);
-  if constexpr (DMA) __builtin_amdgcn_s_waitcnt(0x0070);
-  __syncthreads();
+  const int ntiles = ntiles_kw;
+  const int nfull = nfull_kw;   // tiles whose keys are all below Sk (or masked)
+  prefetch(kg, 0);
+  finish(0);
   using F = std::false_type;
   using T = std::true_type;
   using B0 = std::integral_constant<int, 0>;
   using B1 = std::integral_constant<int, 1>;
-  int t = 0;
-  for (; t + 1 < nfull; t += 2) {
-    tile(t, F{}, B0{});
-    tile(t + 1, F{}, B1{});
-  }
-  if (t < nfull) {
-    tile(t, F{}, B0{});
-    if (t + 1 < ntiles) tile(t + 1, T{}, B1{});
-  } else if (t < ntiles) {
-    tile(t, T{}, B0{});
+  if constexpr (KW == 1) {
+    int t = 0;
+    for (; t + 1 < nfull; t += 2) {
+      tile(t, F{}, B0{});
+      tile(t + 1, F{}, B1{});
+    }
+    if (t < nfull) {
+      tile(t, F{}, B0{});
+      if (t + 1 < ntiles) tile(t + 1, T{}, B1{});
+    } else if (t < ntiles) {
+      tile(t, T{}, B0{});
+    }
+  } else {
+    const int nst = (ntiles + KW - 1) / KW;
+    int s = 0;
+    for (; s + 1 < nst; s += 2) {
+      stage(s, B0{});
+      stage(s + 1, B1{});
+    }
+    if (s < nst) stage(s, B0{});
+    // group 1 parks its (m, l, O^T) in the K/V slots (free after the last barrier: the loads of
+    // tiles past the end have landed), group 0 merges them into its own
+    float* park = reinterpret_cast<float*>(&Kd[0][0][0]);   // DT * 16 floats per lane, per wave
+    float* pml = reinterpret_cast<float*>(&Vd[0][0][0]);    // (m, l) per lane, per wave
+    if (kg == 1) {
+#pragma unroll
+      for (int d = 0; d < DT; ++d)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) park[((wave * DT + d) * 16 + r) * 64 + lane] = acc[d][r];
+      pml[(wave * 2) * 64 + lane] = m_run;
+      pml[(wave * 2 + 1) * 64 + lane] = l_run;
+    }
+    __syncthreads();
+    if (kg == 1) return;   // no barrier follows
+    const float m1 = pml[(wave * 2) * 64 + lane], l1 = pml[(wave * 2 + 1) * 64 + lane];
+    const float mm = fmaxf(m_run, m1);
+    const float a0 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - mm);
+    const float a1 = mm == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
+#pragma unroll
+    for (int d = 0; d < DT; ++d)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[d][r] = acc[d][r] * a0 + park[((wave * DT + d) * 16 + r) * 64 + lane] * a1;
+    l_run = l_run * a0 + l1 * a1;
   }
 
   if (q >= Sq) return;
@@ -1673,6 +1731,18 @@ static void launch_small(const AttnArgs& a, int nw, bool qn, int64_t bh, hipStre
   else launch_small_nw<DH, 8>(a, qn, bh, nqc, s);
 }
 
+// Compute units of the current device (cached; 256 on MI355X when the query fails).
+static int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus = n;
+  }
+  return cus;
+}
+
 template <int DH>
 static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
   if constexpr (DH == 64 || DH == 128) {
@@ -1721,8 +1791,18 @@ static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
       if (a.sk0 == a.Sk && (a.mask_kind == FAM_MASK_NONE || kmask) && a.Sk >= 1 && fits32 && a.k0_rs >= DH &&
           a.v0_rs >= DH) {
         const int nqb = (int)((a.Sq + 127) / 128);
-        if (kmask) FAM_LAUNCH((attn_long_kernel<DH, true>), dim3((unsigned)(nqb * bh)), dim3(256), 0, s, a, nqb);
-        else FAM_LAUNCH((attn_long_kernel<DH, false>), dim3((unsigned)(nqb * bh)), dim3(256), 0, s, a, nqb);
+        const dim3 grid((unsigned)(nqb * bh));
+        // a grid of at most one workgroup per CU runs each workgroup as two key groups of 4 waves
+        // (two waves per SIMD); more workgroups share the CUs two by two instead
+        if constexpr (DH == 128) {
+          if (nqb * bh <= device_cus()) {
+            if (kmask) FAM_LAUNCH((attn_long_kernel<DH, true, 2>), grid, dim3(512), 0, s, a, nqb);
+            else FAM_LAUNCH((attn_long_kernel<DH, false, 2>), grid, dim3(512), 0, s, a, nqb);
+            return;
+          }
+        }
+        if (kmask) FAM_LAUNCH((attn_long_kernel<DH, true, 1>), grid, dim3(256), 0, s, a, nqb);
+        else FAM_LAUNCH((attn_long_kernel<DH, false, 1>), grid, dim3(256), 0, s, a, nqb);
         return;
       }
     }

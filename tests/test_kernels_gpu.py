@@ -855,11 +855,13 @@ def test_attention_qk_norm_on_load_wide_heads():
 
 
 @pytest.mark.parametrize("B,H,Sq,Sk,Dh,kind", [(2, 4, 200, 333, 64, "random"), (1, 24, 1560, 512, 128, "tail"),
-                                                (2, 3, 129, 300, 128, "head")])
+                                                (2, 3, 129, 300, 128, "head"), (2, 4, 200, 333, 128, "random")])
 def test_attention_long_key_mask(B, H, Sq, Sk, Dh, kind):
     """Video tokens over a padded context: a bool key mask shared by the queries ([B, 1, 1, Sk],
     the cross-attention's text mask) on the long kernel.  "head" masks the first 70 keys of the
-    second sample, so its first 64-key tile is all masked (running max still -inf)."""
+    second sample, so its first 64-key tile is all masked (running max still -inf).  At head dim
+    128 a grid of at most one workgroup per CU (every case here but the 1560-query one) runs two
+    key groups per workgroup whose softmax states merge at the end."""
     q, k, v = rnd(B, Sq, H * Dh, seed=138), rnd(B, Sk, H * Dh, seed=139), rnd(B, Sk, H * Dh, seed=140)
     g = torch.Generator().manual_seed(141)
     mask = torch.ones(B, 1, 1, Sk, dtype=torch.bool)
@@ -876,12 +878,15 @@ def test_attention_long_key_mask(B, H, Sq, Sk, Dh, kind):
 
 @pytest.mark.parametrize("B,H,Sq,Sk,Dh", [(1, 8, 1560, 1560, 128), (2, 4, 200, 333, 64), (1, 2, 129, 512, 128),
                                            (1, 3, 65, 1, 128), (1, 2, 129, 192, 128), (2, 3, 130, 330, 128),
-                                           (1, 1, 300, 64, 128)])
+                                           (1, 1, 300, 64, 128), (1, 24, 1560, 200, 128)])
 def test_attention_long_sequences(B, H, Sq, Sk, Dh):
     """Video-token attention (Sq > 64, no mask): 128-query workgroups, 64-key LDS tiles, 32x32 MFMA.
     The loop takes two tiles per iteration with the partial last tile separate, so the cases cover
     an even and an odd number of full tiles, each with and without a partial tile, a partial tile
-    alone (Sk = 1) and a single full tile."""
+    alone (Sk = 1) and a single full tile.  At head dim 128 grids of at most one workgroup per CU
+    split each workgroup's tiles between two key groups (odd tile counts leave the second group a
+    stage without a tile; Sk <= 64 leaves it none); 24 heads x 1560 queries (312 workgroups)
+    takes the one-group kernel."""
     q, k, v = rnd(B, Sq, H * Dh, seed=135), rnd(B, Sk, H * Dh, seed=136), rnd(B, Sk, H * Dh, seed=137)
     ref = O.flash_attention(q.float(), k.float(), v.float(), H)
     y = ops().flash_attention(dev(q), dev(k), dev(v), H)
