@@ -910,20 +910,29 @@ __device__ __forceinline__ void mfma_acc(f32x4& acc, const bf16x8& w, const bf16
   asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(w), "v"(a));
 }
 
-template <int WFM, int WFN>
-__global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int tiles_n, int vec8, int ksplit, int raw) {
+// KG = 2 (128 x 128 tiles on a grid of at most one workgroup per CU, an even number of K
+// blocks): 8 waves in two K groups of 4; group g takes the K blocks g, g + 2, ... into its own
+// two slots, so each SIMD runs two waves although the grid leaves one workgroup per CU; group 1
+// then parks its accumulators in LDS for group 0 to add (in a fixed order) before the epilogue.
+template <int WFM, int WFN, int KG = 1>
+__global__ __launch_bounds__(256 * KG) void big_kernel(GemmArgs g, int tiles_m, int tiles_n, int vec8, int ksplit, int raw) {
   // the A part of a slot holds BMA >= BM rows, a multiple of 64 (a 224-row tile also loads the
   // next 32 rows, unused: measured 2-4 % faster than 7 loads per wave per block)
   constexpr int BM = 32 * WFM, BN = 32 * WFN, BK = 64, BMA = (BM + 63) / 64 * 64;
   constexpr int SA = BMA * BK, SS = (BMA + BN) * BK;           // elements of a slot's A part, slot
   constexpr int NIA = BMA / 32, NIW = BN / 32, IPW = NIA + NIW;   // 1 KB loads per wave per block
   static_assert(IPW < 64, "vmcnt");
-  // two K slots, later the bf16 output tile with its padded rows
-  constexpr int LDS_ELEMS = 2 * SS > BM * (BN + 8) ? 2 * SS : BM * (BN + 8);
+  static_assert(KG == 1 || (KG == 2 && WFM == 4 && WFN == 4), "K groups only on 128 x 128 tiles");
+  // two K slots per group, later the bf16 output tile with its padded rows (and with KG = 2
+  // first group 1's accumulators: 4 WFM WFN floats per lane)
+  constexpr int LDS_SLOTS = KG * 2 * SS, LDS_OUT = BM * (BN + 8);
+  constexpr int LDS_ELEMS = LDS_SLOTS > LDS_OUT ? LDS_SLOTS : LDS_OUT;
+  static_assert(KG == 1 || LDS_ELEMS * 2 >= 4 * (4 * WFM * WFN) * 256, "park area");
   __shared__ __attribute__((aligned(1024))) bf16 sm[LDS_ELEMS];
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 3);   // wave within the K group
+  const int kgi = KG == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid >> 8);
   const int l16 = lane & 15, lg = lane >> 4;
   const int wm0 = (wave >> 1) * (16 * WFM), wn0 = (wave & 1) * (16 * WFN);
 
@@ -948,26 +957,28 @@ __global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int t
   const uint32_t lc16 = (uint32_t)(((lane & 7) ^ lr) * 16);
   const uint32_t voa = (uint32_t)lr * lda2 + lc16, vow = (uint32_t)lr * ldw2 + lc16;
   const int nball = (int)(g.K / BK);
-  const int kb0 = (int)((int64_t)split * nball / ksplit), nb = (int)((int64_t)(split + 1) * nball / ksplit) - kb0;
-  // load p of this wave for block blk (of this split) into slot: A rows 8 (wave + 4p) .. + 7 for
-  // p < NIA, else W rows 8 (wave + 4 (p - NIA)) .. + 7; blocks past the end re-read the last one
-  // (unused)
+  const int kb0 = (int)((int64_t)split * nball / ksplit), nbs = (int)((int64_t)(split + 1) * nball / ksplit) - kb0;
+  const int nb = nbs / KG;   // blocks of this K group (KG = 2 runs with an even count only)
+  // load p of this wave for the group's block blk (of this split) into slot: A rows 8 (wave + 4p)
+  // .. + 7 for p < NIA, else W rows 8 (wave + 4 (p - NIA)) .. + 7; blocks past the end re-read
+  // the last one (unused).  The group's block j is block KG j + kgi of the split.
+  bf16* const smg = sm + kgi * 2 * SS;   // this group's two slots
   auto dma = [&](int p, int blk, int slot) {
-    const uint32_t kb = (uint32_t)(kb0 + (blk < nb ? blk : nb - 1)) * (BK * 2);
+    const uint32_t kb = (uint32_t)(kb0 + KG * (blk < nb ? blk : nb - 1) + kgi) * (BK * 2);
     if (p < NIA) {
       const int r = wave + 4 * p;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, FAM_LDS(sm + slot * SS + r * 512), 16, voa,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, FAM_LDS(smg + slot * SS + r * 512), 16, voa,
                                                (uint32_t)(8 * r) * lda2 + kb, 0, 0);
     } else {
       const int r = wave + 4 * (p - NIA);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, FAM_LDS(sm + slot * SS + SA + r * 512), 16, vow,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, FAM_LDS(smg + slot * SS + SA + r * 512), 16, vow,
                                                (uint32_t)(8 * r) * ldw2 + kb, 0, 0);
     }
   };
   // the fragment of k-step h: row base + l16, chunk 4 h + lg, stored at (4 h + lg) ^ (l16 & 7)
   const int fp0 = (lg ^ (l16 & 7)) << 3, fp1 = ((4 + lg) ^ (l16 & 7)) << 3;
-  const bf16* fa = sm + (wm0 + l16) * BK;
-  const bf16* fw = sm + SA + (wn0 + l16) * BK;
+  const bf16* fa = smg + (wm0 + l16) * BK;
+  const bf16* fw = smg + SA + (wn0 + l16) * BK;
 
   f32x4 acc[WFM][WFN];
 #pragma unroll
@@ -1028,6 +1039,36 @@ __global__ __launch_bounds__(256) void big_kernel(GemmArgs g, int tiles_m, int t
   for (int i = 0; i < WFM; ++i)
 #pragma unroll
     for (int j = 0; j < WFN; ++j) asm volatile("" : "+a"(acc[i][j]));
+  if constexpr (KG == 2) {
+    // group 1's accumulators through LDS into group 0's (every wave is past its last fragment
+    // read after the first barrier)
+    float* park = reinterpret_cast<float*>(sm);
+    __syncthreads();
+    if (kgi == 1) {
+#pragma unroll
+      for (int i = 0; i < WFM; ++i)
+#pragma unroll
+        for (int j = 0; j < WFN; ++j)
+          *reinterpret_cast<f32x4*>(park + (((wave * WFM + i) * WFN + j) * 64 + lane) * 4) = acc[i][j];
+    }
+    __syncthreads();
+    if (kgi == 1) {
+      // the epilogue's two barriers (pass 1 parks the output tile over the same LDS), without
+      // its work; the raw form has none
+      if (!raw) {
+        __syncthreads();
+        __syncthreads();
+      }
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < WFM; ++i)
+#pragma unroll
+      for (int j = 0; j < WFN; ++j) {
+        const f32x4 o = *reinterpret_cast<const f32x4*>(park + (((wave * WFM + i) * WFN + j) * 64 + lane) * 4);
+        acc[i][j] += o;
+      }
+  }
 
   if (raw) {
     // split-K (or fam_gemm_partial's single plane): the raw fp32 sums of this split into plane
@@ -1170,7 +1211,7 @@ static bool big_ok(const fam_gemm_desc* d) {
 }
 
 // raw: fp32 planes without epilogue (always with ksplit > 1)
-template <int WFM, int WFN>
+template <int WFM, int WFN, int KG = 1>
 static void launch_big(const GemmArgs& a, hipStream_t s, int ksplit = 1, bool raw = false) {
   const int tm = (int)((a.M + 32 * WFM - 1) / (32 * WFM)), tn = (int)((a.N + 32 * WFN - 1) / (32 * WFN));
   const unsigned grid = (unsigned)(((tm * tn * ksplit + 7) / 8) * 8);
@@ -1178,7 +1219,7 @@ static void launch_big(const GemmArgs& a, hipStream_t s, int ksplit = 1, bool ra
   const auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
   const int vec8 = a.N % 8 == 0 && a.ldo % 8 == 0 && al16(a.out) && (!a.res || (a.ldr % 8 == 0 && al16(a.res))) &&
                    (!a.gate || (a.gbs % 8 == 0 && a.grs % 8 == 0 && al16(a.gate)));
-  FAM_LAUNCH((big_kernel<WFM, WFN>), dim3(grid), dim3(256), 0, s, a, tm, tn, vec8, ksplit,
+  FAM_LAUNCH((big_kernel<WFM, WFN, KG>), dim3(grid), dim3(256 * KG), 0, s, a, tm, tn, vec8, ksplit,
              (int)(raw || ksplit > 1));
 }
 
@@ -1191,6 +1232,17 @@ static void launch_big(const GemmArgs& a, hipStream_t s, int ksplit = 1, bool ra
 // the matrix cores idle, where one of two 128 x 128 workgroups runs its epilogue while the other
 // multiplies (measured with GELU: 1560 x 14336 x 3072 164 -> 144 us, 2048 x 8192 x 2048 81 -> 74
 // us on 128 x 128 tiles; without an activation the 256-wide tiles stay ahead on both shapes).
+static int big_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus = n;
+  }
+  return cus;
+}
+
 static void big_plan(int64_t M, int64_t N, int act, int* wfm, int* wfn) {
   static int cus = 0;
   if (cus == 0) {
@@ -1337,8 +1389,12 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
     big_plan(d->M, d->N, d->act, &fm, &fn);
     if (fm == 8) launch_big<8, 8>(a, s);
     else if (fm == 7) launch_big<7, 8>(a, s);
-    else if (fm == 4) launch_big<4, 4>(a, s);
-    else launch_big<2, 2>(a, s);
+    else if (fm == 4) {
+      // at most one 128 x 128 workgroup per CU: two K groups per workgroup (an even block count)
+      const int64_t tiles = ((d->M + 127) / 128) * ((d->N + 127) / 128);
+      if (tiles <= big_cus() && (d->K / 64) % 2 == 0) launch_big<4, 4, 2>(a, s);
+      else launch_big<4, 4>(a, s);
+    } else launch_big<2, 2>(a, s);
   } else if (round_up(d->M, 128) / 128 * (round_up(d->N, 128) / 128) >= 200) launch_tiled<128, 128, 2>(a, d->prologue, s);
   else launch_tiled<64, 64, 2>(a, d->prologue, s);
   return fam_host::check_launch("fam_gemm");
