@@ -1731,18 +1731,6 @@ static void launch_small(const AttnArgs& a, int nw, bool qn, int64_t bh, hipStre
   else launch_small_nw<DH, 8>(a, qn, bh, nqc, s);
 }
 
-// Compute units of the current device (cached; 256 on MI355X when the query fails).
-static int device_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cus = n;
-  }
-  return cus;
-}
-
 template <int DH>
 static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
   if constexpr (DH == 64 || DH == 128) {
@@ -1795,7 +1783,7 @@ static void launch_dh(const AttnArgs& a, int64_t bh, hipStream_t s) {
         // a grid of at most one workgroup per CU runs each workgroup as two key groups of 4 waves
         // (two waves per SIMD); more workgroups share the CUs two by two instead
         if constexpr (DH == 128) {
-          if (nqb * bh <= device_cus()) {
+          if (nqb * bh <= fam_host::device_cus()) {
             if (kmask) FAM_LAUNCH((attn_long_kernel<DH, true, 2>), grid, dim3(512), 0, s, a, nqb);
             else FAM_LAUNCH((attn_long_kernel<DH, false, 2>), grid, dim3(512), 0, s, a, nqb);
             return;

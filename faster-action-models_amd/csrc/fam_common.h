@@ -129,6 +129,18 @@ namespace fam_host {
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// Compute units of the device current at the first call (cached; 256, MI355X's count, when the
+// query fails); the launch plans size their grids with it.
+inline int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus = n;
+  }
+  return cus;
+}
 // Launch-timing events armed by fam_set_launch_events (null: plain launches).
 extern thread_local hipEvent_t t_evt_start, t_evt_stop;
 }  // namespace fam_host

@@ -1232,25 +1232,8 @@ static void launch_big(const GemmArgs& a, hipStream_t s, int ksplit = 1, bool ra
 // the matrix cores idle, where one of two 128 x 128 workgroups runs its epilogue while the other
 // multiplies (measured with GELU: 1560 x 14336 x 3072 164 -> 144 us, 2048 x 8192 x 2048 81 -> 74
 // us on 128 x 128 tiles; without an activation the 256-wide tiles stay ahead on both shapes).
-static int big_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cus = n;
-  }
-  return cus;
-}
-
 static void big_plan(int64_t M, int64_t N, int act, int* wfm, int* wfn) {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cus = n;
-  }
+  const int cus = fam_host::device_cus();
   const double big_eff = act == FAM_ACT_NONE ? 1.0 : 0.8;
   struct C { int fm, fn; double eff; } cands[] = {{8, 8, big_eff}, {7, 8, big_eff}, {4, 4, 0.85}, {2, 2, 0.25}};
   double best = 1e300;
@@ -1275,13 +1258,7 @@ static void big_plan(int64_t M, int64_t N, int act, int* wfm, int* wfn) {
 // at least 15% below the unsplit one; otherwise *ks = 1 and the tile is big_plan's.
 static void big_plan_split(int64_t M, int64_t N, int64_t K, int64_t ws_floats, bool planes_consumed, int* wfm,
                            int* wfn, int* ks) {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cus = n;
-  }
+  const int cus = fam_host::device_cus();
   struct Fit { int fm, fn; double c0, rate, occ; };
   static const Fit fits[] = {{8, 8, 10.0, 6.5, 1.0}, {7, 8, 8.0, 6.5, 1.0}, {4, 4, 4.0, 5.5, 2.0}, {2, 2, 1.0, 3.0, 2.0}};
   const int64_t nb = K / 64;
@@ -1392,7 +1369,7 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
     else if (fm == 4) {
       // at most one 128 x 128 workgroup per CU: two K groups per workgroup (an even block count)
       const int64_t tiles = ((d->M + 127) / 128) * ((d->N + 127) / 128);
-      if (tiles <= big_cus() && (d->K / 64) % 2 == 0) launch_big<4, 4, 2>(a, s);
+      if (tiles <= fam_host::device_cus() && (d->K / 64) % 2 == 0) launch_big<4, 4, 2>(a, s);
       else launch_big<4, 4>(a, s);
     } else launch_big<2, 2>(a, s);
   } else if (round_up(d->M, 128) / 128 * (round_up(d->N, 128) / 128) >= 200) launch_tiled<128, 128, 2>(a, d->prologue, s);
@@ -1446,7 +1423,6 @@ extern "C" int fam_gemm_ws(const fam_gemm_desc* d, float* ws, int64_t ws_floats,
   return fam_rowop(&r, stream);
 }
 
-static int wide_cus();
 
 // Split plan of fam_gemm_partial.  Above 64 rows, first the streaming kernel: 128 columns per
 // workgroup (64 when that is what gives every split 3 chunks), as many K splits as one round
@@ -1464,7 +1440,7 @@ static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* split
     for (int w : {8, 4}) {
       if (w == 4 && M > 128) break;   // 9 m-tiles only with 8 waves
       const int64_t nblk = (N + 16 * w - 1) / (16 * w);
-      const int64_t smax = std::max((int64_t)1, (int64_t)wide_cus() / nblk);
+      const int64_t smax = std::max((int64_t)1, (int64_t)fam_host::device_cus() / nblk);
       const int64_t c = (chunks + std::min(chunks, smax) - 1) / std::min(chunks, smax);
       if (c >= 3) {
         *steps = -(int)c;
@@ -1532,16 +1508,6 @@ static void launch_partial(const PartArgs& a, int steps, int splits, hipStream_t
 // Waves per workgroup of the wide kernel (one 16-column strip each): the workgroup holds the
 // 135 KB activation slice in LDS, so one runs per CU; the estimate is rounds over the CUs
 // times the bytes a workgroup loads (weights 16 NWV x 512, activations M x 512).
-static int wide_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cus = n;
-  }
-  return cus;
-}
 static void launch_partial_wide(const PartArgs& a, int splits, hipStream_t s) {
   if (a.M <= 64) {   // two strips per workgroup (partial_plan)
     const dim3 grid((unsigned)((a.N + 31) / 32), (unsigned)splits);
@@ -1550,7 +1516,7 @@ static void launch_partial_wide(const PartArgs& a, int splits, hipStream_t s) {
     else FAM_LAUNCH((partial_wide_kernel<4, 2>), grid, dim3(128), 0, s, a);
     return;
   }
-  const int64_t cus = wide_cus();
+  const int64_t cus = fam_host::device_cus();
   int best = 4;
   int64_t best_cost = -1;
   for (int nwv : {4, 6, 8}) {
