@@ -987,7 +987,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures the denoise loop on ONE GPU: the B=1 loop is a sequential chain of "
-              "launches and this build ships no multi-GPU path (see the sharding notes in DESIGN.md). "
+              "launches and this build ships no multi-GPU path (its sharding is a design note only). "
               "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     if args.traffic_from:

@@ -1,4 +1,4 @@
-"""DiT4DiT flow-matching action head on the gfx950 kernels (SURVEY row a19).
+"""DiT4DiT flow-matching action head on the gfx950 kernels.
 
 `FusedDiT4DiTHead` runs `FlowmatchingActionHead.predict_action` (state=None) of
 src/dit4dit-baseline/DiT4DiT/model/modules/action_model/ActionDiT.py:321-369 for a fixed call

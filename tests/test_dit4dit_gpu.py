@@ -1,4 +1,4 @@
-"""DiT4DiT flow-matching head (SURVEY row a19) on the library vs the oracle's restatement of
+"""DiT4DiT flow-matching head on the library vs the oracle's restatement of
 FlowmatchingActionHead.predict_action (fp32 oracle on bf16-rounded weights and inputs).
 
 The oracle's head composition follows diffusers semantics that no reference fixture pins here

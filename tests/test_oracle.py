@@ -415,7 +415,7 @@ def test_d4d_embeddings_closed_forms():
 
 
 def test_d4d_schedule_and_block_structure():
-    """Timesteps 1000, 750, 500, 250 and dt = 0.25 (SURVEY's DiT4DiT known answer); interleaved
+    """Timesteps 1000, 750, 500, 250 and dt = 0.25 (the DiT4DiT 4-step schedule's known answer); interleaved
     blocks (odd = self attention); a block with zero AdaLN / attention / FFN weights is the
     identity on the residual stream, and a head whose decoder outputs zero leaves the noise."""
     cfg = O.DiT4DiTHeadConfig(num_layers=4, heads=2, head_dim=16, cross_dim=24, output_dim=40, hidden_size=40,
