@@ -1232,12 +1232,18 @@ static void launch_big(const GemmArgs& a, hipStream_t s, int ksplit = 1, bool ra
 // the matrix cores idle, where one of two 128 x 128 workgroups runs its epilogue while the other
 // multiplies (measured with GELU: 1560 x 14336 x 3072 164 -> 144 us, 2048 x 8192 x 2048 81 -> 74
 // us on 128 x 128 tiles; without an activation the 256-wide tiles stay ahead on both shapes).
-static void big_plan(int64_t M, int64_t N, int act, int* wfm, int* wfn) {
+// narrow (fam_gemm only): 128 x 96 tiles (0.8) are a candidate too where the 128 x 128 tiles
+// outnumber the CUs -- config 2's 1560 x 3072 products: 312 tiles put two workgroups on 56 CUs,
+// 416 narrow ones spread two on 160 CUs with three quarters of the work each.
+static void big_plan(int64_t M, int64_t N, int act, int* wfm, int* wfn, bool narrow = false) {
   const int cus = fam_host::device_cus();
   const double big_eff = act == FAM_ACT_NONE ? 1.0 : 0.8;
-  struct C { int fm, fn; double eff; } cands[] = {{8, 8, big_eff}, {7, 8, big_eff}, {4, 4, 0.85}, {2, 2, 0.25}};
+  const bool n43 = narrow && ((M + 127) / 128) * ((N + 127) / 128) > cus;
+  struct C { int fm, fn; double eff; } cands[] = {{8, 8, big_eff}, {7, 8, big_eff}, {4, 4, 0.85}, {4, 3, n43 ? 0.8 : 0.0},
+                                                  {2, 2, 0.25}};
   double best = 1e300;
   for (const C& c : cands) {
+    if (c.eff <= 0.0) continue;
     const int64_t bm = 32 * c.fm, bn = 32 * c.fn;
     const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const double t = (double)((tiles + cus - 1) / cus) * (double)(bm * bn) / c.eff;
@@ -1363,9 +1369,10 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
   else if (skinny) launch_skinny_k<4>(a, d->prologue, s);
   else if (big_ok(d)) {
     int fm = 8, fn = 8;
-    big_plan(d->M, d->N, d->act, &fm, &fn);
+    big_plan(d->M, d->N, d->act, &fm, &fn, true);
     if (fm == 8) launch_big<8, 8>(a, s);
     else if (fm == 7) launch_big<7, 8>(a, s);
+    else if (fm == 4 && fn == 3) launch_big<4, 3>(a, s);
     else if (fm == 4) {
       // at most one 128 x 128 workgroup per CU: two K groups per workgroup (an even block count)
       const int64_t tiles = ((d->M + 127) / 128) * ((d->N + 127) / 128);
