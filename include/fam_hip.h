@@ -133,9 +133,10 @@ int fam_rmsnorm_grouped(const void* x, int64_t x_row_stride, void* y, int64_t y_
  * chunk whose waves split the keys (partial softmax states merged in LDS in a fixed order); up
  * to 32 queries over one long unmasked key segment, one workgroup per (b, h) and key split;
  * longer query sequences over one key segment with no mask or a key-only boolean mask, 128
- * queries per workgroup with the K/V tiles streamed through LDS; otherwise (and for the other
- * head dims) one workgroup per (b, h) holding all queries up to 32 (64 for head_dim < 128),
- * 64 queries per workgroup beyond.  Every path gives the same result up to fp32 summation
+ * queries per workgroup with the K/V tiles streamed through LDS (at head_dim 128 on a grid of
+ * at most one workgroup per CU, two groups of waves take alternate tiles and merge in LDS);
+ * otherwise (and for the other head dims) one workgroup per (b, h) holding all queries up to
+ * 32 (64 for head_dim < 128), 64 queries per workgroup beyond.  Every path gives the same result up to fp32 summation
  * order; for a given shape and arguments the path, and so the bits, are fixed.
  * Replaces: flash_attention(q, k, v, num_heads, ctx_mask)  FB/wan_video_dit.py:17-26,
  *           FG/wan_video_dit.py:18-39, CA/wan_video_dit.py:569-587;
@@ -246,7 +247,11 @@ int64_t fam_attention_noalloc_max_bytes(void);
  * modulation (1 + s, t) that are the same for every row fold into w' = w diag(g (1 + s)),
  * bias' = bias + w (b (1 + s) + t) beforehand (fam.ops.fold_layernorm).
  * Work split: for M <= 64 a workgroup of 8 waves owns 16 output columns and the waves split
- * K (reduced through LDS in wave order); for larger M, 64x64 or 128x128 output tiles.
+ * K (reduced through LDS in wave order); for M >= 128 without a prologue and with K % 64 == 0,
+ * output tiles of 256x256, 224x256, 128x128, 128x96 or 64x64 chosen for the shape and the
+ * device's CU count (128x128 tiles on a grid of at most one workgroup per CU split K between
+ * two groups of waves whose sums meet in LDS in a fixed order); otherwise 64x64 or 128x128
+ * tiles.  The choice, and so the bits, are a fixed function of the shape on a given device.
  * Replaces: nn.Linear / F.linear on the hot path (FB/wan_video_dit.py:188-191,215-218,262-263,
  *           FB/action_dit.py:76-97,317-318), fastwam::skmm + skpost (split-K GEMM with
  *           bias/gate/residual/norm epilogue, FG/mot.py:1080-1348), geak_head::mmx with the
