@@ -1226,7 +1226,9 @@ __global__ __launch_bounds__(256 * KW, 2 / KW) void attn_long_kernel(AttnArgs a,
 
   // K/V tiles come in through raw buffer loads: the descriptor (scalar registers) is rebuilt
   // per tile over the rows from the tile's first key to Sk, so rows past the end (and whole
-  // tiles past the end) read as zero and each thread keeps only 32-bit row offsets
+  // tiles past the end) read as zero and each thread keeps only 32-bit row offsets.  Every row
+  // offset goes into the per-lane (vector) offset: the range check covers the vector and
+  // instruction offsets only, not the scalar one, so a row placed there would be read past Sk.
   const uint32_t krs = (uint32_t)a.k0_rs * 2u, vrs = (uint32_t)a.v0_rs * 2u;   // bytes per row
   // direct loads: instruction n of wave w writes rows 4 (w + 4n) .. + 3 of the slot (1 KB;
   // lane j -> row + j / 16, chunk slot j % 16) and lane j fetches the chunk that belongs there
@@ -1241,15 +1243,15 @@ __global__ __launch_bounds__(256 * KW, 2 / KW) void attn_long_kernel(AttnArgs a,
 #pragma unroll
       for (int n = 0; n < BN / 16; ++n) {
         const int r0 = 4 * (wv + 4 * n);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)&Kd[buf][kg][r0 * DH], 16, dk,
-                                                 (uint32_t)r0 * krs, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&Vd[buf][kg][r0 * DH], 16, dv,
-                                                 (uint32_t)r0 * vrs, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)&Kd[buf][kg][r0 * DH], 16,
+                                                 dk + (uint32_t)r0 * krs, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)&Vd[buf][kg][r0 * DH], 16,
+                                                 dv + (uint32_t)r0 * vrs, 0, 0, 0);
       }
     }
   };
   // register path: chunk j of a thread is key tid / CPR + j * (NTH / CPR), dims (tid % CPR) * 8
-  // .. + 7: one per-lane offset, the j steps go to the scalar offset
+  // .. + 7: one per-lane offset plus the j step
   const uint32_t koff = (uint32_t)(tid / CPR) * krs + (uint32_t)(tid % CPR) * 16u;
   const uint32_t voff = (uint32_t)(tid / CPR) * vrs + (uint32_t)(tid % CPR) * 16u;
   bf16x8 kr[DMA ? 1 : NCH], vr[DMA ? 1 : NCH];
@@ -1259,9 +1261,9 @@ __global__ __launch_bounds__(256 * KW, 2 / KW) void attn_long_kernel(AttnArgs a,
       const auto rk = buffer_rsrc(kbase + (int64_t)k0 * a.k0_rs, (uint32_t)left * krs);
       const auto rv = buffer_rsrc(vbase + (int64_t)k0 * a.v0_rs, (uint32_t)left * vrs);
 #pragma unroll
-      for (int j = 0; j < NCH; ++j) kr[j] = buffer_load8(rk, koff, (uint32_t)j * (NTH / CPR) * krs);
+      for (int j = 0; j < NCH; ++j) kr[j] = buffer_load8(rk, koff + (uint32_t)j * (NTH / CPR) * krs);
 #pragma unroll
-      for (int j = 0; j < NCH; ++j) vr[j] = buffer_load8(rv, voff, (uint32_t)j * (NTH / CPR) * vrs);
+      for (int j = 0; j < NCH; ++j) vr[j] = buffer_load8(rv, voff + (uint32_t)j * (NTH / CPR) * vrs);
     }
   };
   auto lstore_kv = [&](int buf) {
@@ -1952,7 +1954,12 @@ void* scratch_on_current_device() {
 }
 }  // namespace
 
-extern "C" int64_t fam_attention_noalloc_max_bytes(void) { return (int64_t)FAM_ATTN_SCRATCH_BYTES; }
+// Set-up call: resolves the scratch address on the current device (once per device), so that a
+// later fam_attention_noalloc, e.g. one under graph capture, makes no runtime lookup.
+extern "C" int64_t fam_attention_noalloc_max_bytes(void) {
+  if (scratch_on_current_device() == nullptr) return -(int64_t)FAM_ERR_LAUNCH;
+  return (int64_t)FAM_ATTN_SCRATCH_BYTES;
+}
 
 extern "C" int fam_attention_noalloc(const fam_attn_desc* d, void* stream) {
   FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_attention_noalloc: null descriptor");

@@ -115,7 +115,8 @@ __device__ __forceinline__ void lds_barrier() {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
-// 16 bytes at byte offset voff (per lane) + soff (wave-uniform)
+// 16 bytes at byte offset voff (per lane) + soff (wave-uniform).  Only voff is range-checked
+// against the descriptor: an offset that must read zero past the end goes into voff.
 __device__ __forceinline__ bf16x8 buffer_load8(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0) {
   typedef int i32x4 __attribute__((ext_vector_type(4)));
   const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);

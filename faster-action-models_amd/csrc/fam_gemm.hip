@@ -604,7 +604,7 @@ __global__ __launch_bounds__(NWV * 64) void partial_stream_kernel(PartArgs g, in
       // (row & 15) of row 2p + sr is (2p & 15) + sr: the pair's part of the swizzle goes with p
       const uint32_t sw = (uint32_t)((lane & 31) ^ (((2 * p) & 15) + sr)) * 16u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (__attribute__((address_space(3))) void*)&As[buf][2 * p * KS], 16,
-                                               (uint32_t)sr * lda2 + sw, (uint32_t)(2 * p) * lda2 + (uint32_t)k0 * 2u, 0, 0);
+                                               (uint32_t)(2 * p + sr) * lda2 + (uint32_t)k0 * 2u + sw, 0, 0, 0);
     }
   };
   bf16x8 wc[KSW], wx[KSW];
@@ -884,8 +884,9 @@ __global__ __launch_bounds__(256) void tiled_kernel(GemmArgs g) {
 //     consecutive lanes (8 rows, one chunk) hit 8 distinct bank groups;
 //   * the slots are filled by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds): one
 //     load writes 1 KB = 8 rows x 128 B, lane l fetching chunk (l % 8) ^ (l / 8) of row l / 8,
-//     so the swizzle costs nothing; the descriptors make rows past M or N read zeros; the
-//     soffset (k position) and M0 (LDS slot) are scalar, so issuing a load costs no VALU work;
+//     so the swizzle costs nothing; the descriptors make rows past M or N read zeros (row and
+//     k position both go into the vector offset, which the range check covers; the scalar
+//     offset is not checked); M0 (LDS slot) is scalar, so a load costs one VALU add;
 //   * block b: k-step 0 computes from fragments read during block b - 1 while k-step 1's
 //     fragments are read; then one barrier (after which block b + 1 has landed and every wave
 //     is done with block b's slot), block b + 2 is sent into that slot and k-step 1 computes
@@ -967,12 +968,12 @@ __global__ __launch_bounds__(256 * KG) void big_kernel(GemmArgs g, int tiles_m, 
     const uint32_t kb = (uint32_t)(kb0 + KG * (blk < nb ? blk : nb - 1) + kgi) * (BK * 2);
     if (p < NIA) {
       const int r = wave + 4 * p;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, FAM_LDS(smg + slot * SS + r * 512), 16, voa,
-                                               (uint32_t)(8 * r) * lda2 + kb, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, FAM_LDS(smg + slot * SS + r * 512), 16,
+                                               voa + (uint32_t)(8 * r) * lda2 + kb, 0, 0, 0);
     } else {
       const int r = wave + 4 * (p - NIA);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, FAM_LDS(smg + slot * SS + SA + r * 512), 16, vow,
-                                               (uint32_t)(8 * r) * ldw2 + kb, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, FAM_LDS(smg + slot * SS + SA + r * 512), 16,
+                                               vow + (uint32_t)(8 * r) * ldw2 + kb, 0, 0, 0);
     }
   };
   // the fragment of k-step h: row base + l16, chunk 4 h + lg, stored at (4 h + lg) ^ (l16 & 7)

@@ -216,6 +216,10 @@ int fam_attention_key_splits(int64_t batch, int64_t heads, int64_t sq, int64_t s
  * (larger calls return FAM_ERR_UNSUPPORTED).  Every call on one GPU shares that GPU's array:
  * calls that overlap on one GPU (different streams, or host threads) race and must be
  * serialised by the caller.  Results equal fam_attention + fam_attention_combine bit for bit.
+ * fam_attention_noalloc_max_bytes is the set-up call: made once per device with that device
+ * current (before any graph capture), it looks up the array's device address and returns the
+ * scratch size, or -FAM_ERR_LAUNCH when the lookup fails; a device whose set-up call was never
+ * made is set up by its first fam_attention_noalloc.
  */
 int fam_attention_noalloc(const fam_attn_desc* d, void* stream);
 int64_t fam_attention_noalloc_max_bytes(void);

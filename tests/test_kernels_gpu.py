@@ -895,3 +895,51 @@ def test_attention_long_sequences(B, H, Sq, Sk, Dh):
     ref = O.flash_attention(q.float(), k.float(), v.float(), H)
     y = ops().flash_attention(dev(q), dev(k), dev(v), H)
     assert relerr(y, ref) <= TOL
+
+
+# --------------------------------------------------------------------------- rows past the end
+def _nan_tailed(rows, cols, pad, seed, scale=1.0):
+    """[rows + pad, cols] bf16 whose first `rows` rows are N(0, scale) and the rest NaN: a view of
+    the first rows has NaN right after its last row, inside the same allocation."""
+    buf = torch.full((rows + pad, cols), float("nan"), dtype=torch.bfloat16)
+    buf[:rows] = rnd(rows, cols, seed=seed, scale=scale)
+    return buf
+
+
+@pytest.mark.parametrize("B,H,Sq,Sk,Dh,masked", [(1, 4, 200, 333, 128, False), (1, 4, 200, 333, 64, False),
+                                                  (1, 24, 1560, 200, 128, False), (1, 4, 200, 333, 128, True)])
+def test_attention_long_keys_past_the_end_read_as_zero(B, H, Sq, Sk, Dh, masked):
+    """K and V are column windows of one [Sk + 64, 3A] q|k|v buffer whose rows past Sk are NaN (as
+    config 2's self attention reads them from its projection output).  The partial last 64-key
+    tile must not read those rows: 0 x NaN from a masked key's V would reach the stored output,
+    and a NaN score stays NaN under the key mask."""
+    A = H * Dh
+    qkv = _nan_tailed(Sk, 3 * A, 64, seed=150).reshape(1, Sk + 64, 3 * A)
+    q = rnd(B, Sq, A, seed=151)
+    k, v = qkv[:, :Sk, A:2 * A], qkv[:, :Sk, 2 * A:]
+    mask = None
+    if masked:
+        mask = torch.ones(1, 1, 1, Sk, dtype=torch.bool)
+        mask[..., Sk - 29:] = False
+    ref = O.flash_attention(q.float(), k.float(), v.float(), H, mask)
+    qkv_d = dev(qkv)
+    y = ops().flash_attention(dev(q), qkv_d[:, :Sk, A:2 * A], qkv_d[:, :Sk, 2 * A:], H,
+                              ctx_mask=None if mask is None else dev(mask))
+    assert relerr(y, ref) <= TOL   # relerr asserts the output is finite
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 520, 320), (1560, 3072, 1024), (98, 3072, 3072), (99, 4096, 1024)])
+def test_gemm_rows_past_the_end_read_as_zero(M, N, K):
+    """The activation and weight operands are views of the first M / N rows of buffers with NaN rows
+    after them: the large-M tile kernel (tiles past M and N) and the 98-row streaming split-K kernel
+    (row pairs, an odd M) must read zeros there, so every output is finite and equals the product."""
+    a = _nan_tailed(M, K, 256, seed=152)
+    w = _nan_tailed(N, K, 256, seed=153, scale=0.02)
+    b = rnd(N, seed=154, scale=0.02)
+    ref = O.linear(a[:M].float(), w[:N].float(), b.float())
+    ad, wd, bd = dev(a), dev(w), dev(b)
+    assert relerr(ops().linear(ad[:M], wd[:N], bd), ref) <= TOL
+    part, _ = ops().gemm_partial(ad[:M], wd[:N])
+    y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ops().rowop(y, partials=part, bias=bd)
+    assert relerr(y, ref) <= TOL

@@ -62,6 +62,37 @@ def _inputs(seed, B, Sq, Sk, H, Dh, ctx_batch):
     return q, k, v
 
 
+def test_noalloc_first_call_under_graph_capture():
+    """The set-up call resolves the scratch address; the first fam_attention_noalloc of the process
+    (when this file runs alone) is then made under torch.cuda.graph capture.  Each replay, with new
+    inputs copied into the captured buffers and eager library work and synchronisations between
+    replays, is bit-identical to fam_attention + fam_attention_combine on caller buffers."""
+    from fam import _capi
+    lib = _capi.load()
+    assert lib.fam_attention_noalloc_max_bytes() == 8 << 20   # set-up, before any capture
+    B, Sq, Sk, H, Dh, splits = 1, 32, 1560, 16, 64, 13
+    q, k, v = _inputs(200, B, Sq, Sk, H, Dh, 1)
+    o = torch.full_like(q, float("nan"))
+    d = _desc(q, k, v, o, H, splits)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = lib.fam_attention_noalloc(C.byref(d), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.fam_last_error().decode()
+    for rep in range(3):
+        q2, k2, v2 = _inputs(300 + rep, B, Sq, Sk, H, Dh, 1)
+        q.copy_(q2), k.copy_(k2), v.copy_(v2)
+        o.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        # eager library work between replays, on other inputs, through the same scratch
+        _noalloc(lib, *_inputs(400 + rep, 1, 17, 600, 8, 128, 1), 8, 5)
+        ref = _reference(lib, q, k, v, H, splits)
+        torch.cuda.synchronize()
+        print(f"graph replay {rep}: bit-identical {torch.equal(o, ref)}", flush=True)
+        assert torch.equal(o, ref)
+
+
 def test_noalloc_matches_caller_buffers_on_two_calls():
     from fam import _capi
     lib = _capi.load()
@@ -80,9 +111,15 @@ def test_noalloc_matches_caller_buffers_on_two_calls():
               flush=True)
         assert torch.equal(got, ref)
         outs.append(got)
-    # the first call's result is unaffected by the second (outputs are the caller's)
-    q, k, v = _inputs(100 + 32, *cases[0][:1], 32, 1560, 16, 64, 1)
-    assert torch.equal(outs[0], _reference(lib, q, k, v, 16, 13))
+    # the scratch now holds the second call's partials over a stale tail of the first's: a third
+    # call with mostly empty key splits (40 keys over 8 splits) and the first call again must read
+    # only partials they wrote themselves
+    for (B, Sq, Sk, H, Dh, splits, cb) in [(1, 32, 40, 16, 64, 8, 1), cases[0]]:
+        q, k, v = _inputs(500 + Sk, B, Sq, Sk, H, Dh, cb)
+        ref = _reference(lib, q, k, v, H, splits)
+        got = _noalloc(lib, q, k, v, H, splits)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), (Sk, splits)
 
 
 def test_noalloc_masked_batched_rows():
