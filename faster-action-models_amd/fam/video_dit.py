@@ -451,6 +451,18 @@ class FusedVideoDiTBlock:
                 f(st)
         self.graph = g
 
+    def run_until(self, name: str) -> None:
+        """Eager launches of this block up to and including its step `name`, to inspect the
+        buffers in between: after "self_attn" / "cross_attn", `attn` [B*S, A] holds that
+        attention's output before its o projection; after "o", `x` holds the residual stream
+        after the self-attention branch."""
+        names = [m["name"] for m in self.meta]
+        if name not in names:
+            raise ValueError(f"no step {name!r} in this block (steps: {names})")
+        s = torch.cuda.current_stream().cuda_stream
+        for f in self.steps[:names.index(name) + 1]:
+            f(s)
+
     def forward(self, x: torch.Tensor, t_mod: torch.Tensor, context: torch.Tensor) -> torch.Tensor:
         """One block forward; returns a copy of the new x, [B, S, H]."""
         self.set_inputs(x, t_mod, context)
@@ -869,6 +881,21 @@ class FusedWanVideoDiT:
         self.set_inputs(latents, timestep, context, context_mask)
         self.run()
         return self.out.clone()
+
+    def run_until(self, name: str, block: int) -> None:
+        """Eager launches from pre_dit up to and including step `name` of block `block` (inputs
+        from `set_inputs`), to inspect the shared buffers there: after "self_attn" /
+        "cross_attn" the stack's "attn" holds that block's attention output before its o
+        projection (see FusedVideoDiTBlock.run_until)."""
+        blk = self.blocks.blocks[block]
+        names = [m["name"] for m in blk.meta]
+        if name not in names:
+            raise ValueError(f"no step {name!r} in block {block} (steps: {names})")
+        target = blk.steps[names.index(name)]
+        end = next(i for i, f in enumerate(self.steps) if f is target)
+        s = torch.cuda.current_stream(self.device).cuda_stream
+        for f in self.steps[:end + 1]:
+            f(s)
 
     def prefill(self, latents, timestep, context=None, context_mask=None):
         """pre_dit + every block's K/V: [(k, v)] per layer, [B, S, A] views valid until the next run."""

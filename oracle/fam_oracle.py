@@ -347,14 +347,17 @@ def split_modulation(modulation: torch.Tensor, t_mod: torch.Tensor):
 
 
 def self_attention(p: Params, pre: str, x: torch.Tensor, freqs: torch.Tensor, num_heads: int, eps: float,
-                   mask: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """SelfAttention.forward (FB/wan_video_dit.py:197-204)."""
+                   mask: Optional[torch.Tensor] = None, trace: Optional[dict] = None) -> torch.Tensor:
+    """SelfAttention.forward (FB/wan_video_dit.py:197-204).  `trace`, when given, records the
+    rotated q, k, the v and the attention output before the o projection."""
     q = rms_norm(linear(x, p[pre + "q.weight"], p[pre + "q.bias"]), p[pre + "norm_q.weight"], eps)
     k = rms_norm(linear(x, p[pre + "k.weight"], p[pre + "k.bias"]), p[pre + "norm_k.weight"], eps)
     v = linear(x, p[pre + "v.weight"], p[pre + "v.bias"])
     q = rope_apply(q, freqs, num_heads)
     k = rope_apply(k, freqs, num_heads)
     o = flash_attention(q, k, v, num_heads, mask)
+    if trace is not None:
+        trace.update(q=q, k=k, v=v, self_attn=o)
     return linear(o, p[pre + "o.weight"], p[pre + "o.bias"])
 
 
@@ -366,11 +369,14 @@ def cross_kv(p: Params, pre: str, context: torch.Tensor, eps: float) -> Tuple[to
 
 
 def cross_attention(p: Params, pre: str, x: torch.Tensor, context: torch.Tensor, num_heads: int, eps: float,
-                    mask: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """CrossAttention.forward (FB/wan_video_dit.py:224-229)."""
+                    mask: Optional[torch.Tensor] = None, trace: Optional[dict] = None) -> torch.Tensor:
+    """CrossAttention.forward (FB/wan_video_dit.py:224-229).  `trace` records the attention
+    output before the o projection."""
     q = rms_norm(linear(x, p[pre + "q.weight"], p[pre + "q.bias"]), p[pre + "norm_q.weight"], eps)
     k, v = cross_kv(p, pre, context, eps)
     o = flash_attention(q, k, v, num_heads, mask)
+    if trace is not None:
+        trace.update(cross_attn=o)
     return linear(o, p[pre + "o.weight"], p[pre + "o.bias"])
 
 
@@ -383,20 +389,28 @@ def ffn(p: Params, pre: str, x: torch.Tensor) -> torch.Tensor:
 def dit_block(p: Params, idx: int, x: torch.Tensor, context: torch.Tensor, t_mod: torch.Tensor,
               freqs: torch.Tensor, num_heads: int, eps: float,
               context_mask: Optional[torch.Tensor] = None,
-              self_attn_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+              self_attn_mask: Optional[torch.Tensor] = None, trace: Optional[dict] = None) -> torch.Tensor:
     """DiTBlock.forward (FB/wan_video_dit.py:267-286).
 
     context_mask: None, bool [B,Sq,L] (unsqueezed to [B,1,Sq,L] as at :268-269) or [B,1,Sq,L].
+    trace: when given, records the branch values (q, k, v, self_attn, cross_attn: see
+    self_attention / cross_attention) and the residual stream after each branch (x_self,
+    x_cross), so a test can compare a block's inner values and not only its residual-dominated
+    output.
     """
     pre = f"blocks.{idx}."
     if context_mask is not None and context_mask.dim() == 3:
         context_mask = context_mask.unsqueeze(1)
     sh_a, sc_a, g_a, sh_m, sc_m, g_m = split_modulation(p[pre + "modulation"], t_mod)
     h = adaln(x, sh_a, sc_a, eps)
-    x = x + g_a * self_attention(p, pre + "self_attn.", h, freqs, num_heads, eps, self_attn_mask)
+    x = x + g_a * self_attention(p, pre + "self_attn.", h, freqs, num_heads, eps, self_attn_mask, trace)
+    if trace is not None:
+        trace.update(x_self=x)
     x = x + cross_attention(p, pre + "cross_attn.",
                             layer_norm(x, p[pre + "norm3.weight"], p[pre + "norm3.bias"], eps),
-                            context, num_heads, eps, context_mask)
+                            context, num_heads, eps, context_mask, trace)
+    if trace is not None:
+        trace.update(x_cross=x)
     h = adaln(x, sh_m, sc_m, eps)
     x = x + g_m * ffn(p, pre, h)
     return x

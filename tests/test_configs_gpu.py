@@ -16,6 +16,7 @@ import os
 import pytest
 import torch
 
+from block_checks import BAR, gpu_block_errors
 from oracle import fam_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -74,10 +75,17 @@ def test_config2_video_block_full_shape():
                              freqs=freqs, per_token_mod=True)
     y = blk.forward(x.cuda(), tm.cuda(), ctx.cuda()).float().cpu()
     p32 = {k: v.float() for k, v in p.items()}
-    ref = O.dit_block(p32, 0, x.float(), ctx.float(), tm.float(), freqs, nh, 1e-6)
+    tr = {}
+    ref = O.dit_block(p32, 0, x.float(), ctx.float(), tm.float(), freqs, nh, 1e-6, trace=tr)
     err = ((y - ref).abs().max() / ref.abs().max()).item()
-    print(f"config2 block (1560 x 3072, 24 x 128, FFN 14336, 512 text): normwise rel err {err:.3e}")
-    assert err <= 2e-2
+    # the output is dominated by the residual stream: the branch metrics are the ones a dropped
+    # or transposed RoPE or a zeroed self-attention moves past the bar
+    # (tests/test_oracle.py::test_block_branch_metrics_catch_planted_slips, same seeds and shape)
+    errs = gpu_block_errors(blk, x, tm, ctx, tr, y, ref)
+    print(f"config2 block (1560 x 3072, 24 x 128, FFN 14336, 512 text): normwise rel err {err:.3e}; branches "
+          + ", ".join(f"{k} {v:.3e}" for k, v in errs.items()))
+    assert err <= BAR
+    assert all(v <= BAR for v in errs.values()), errs
 
 
 def test_config3_b256_loop_and_decoder():

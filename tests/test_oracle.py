@@ -445,6 +445,124 @@ def test_d4d_schedule_and_block_structure():
     assert torch.allclose(O.d4d_predict_action(zc, cfg, ctx, noise), noise - 0.5, atol=1e-6)
 
 
+def _d4d_tiny():
+    cfg = O.DiT4DiTHeadConfig(num_layers=2, heads=2, head_dim=8, cross_dim=12, output_dim=16, hidden_size=16,
+                              action_dim=5, horizon=6, state_dim=0)
+    g = torch.Generator().manual_seed(41)
+    x = torch.randn(2, 6, cfg.dim, generator=g, dtype=torch.float64)
+    x[1, 2] = 0.3 + 1e-3 * x[1, 2]          # a row of variance ~1e-6: its LayerNorm output depends on eps
+    ctx = torch.randn(2, 7, cfg.cross_dim, generator=g, dtype=torch.float64)
+    temb = torch.randn(2, cfg.dim, generator=g, dtype=torch.float64)
+    p = {k: v.double() for k, v in O.init_d4d_params(cfg, 42).items()}
+    return cfg, g, x, ctx, temb, p
+
+
+def _ln(x, eps):
+    """LayerNorm without affine, written out: (x - mean) / sqrt(biased var + eps)."""
+    mu = x.mean(-1, keepdim=True)
+    return (x - mu) / torch.sqrt(((x - mu) ** 2).mean(-1, keepdim=True) + eps)
+
+
+def test_d4d_block_adaln_closed_form():
+    """AdaLayerNorm of a DiT4DiT head block (DB/.../flow_matching_head/cross_attention_dit.py:59-67:
+    (scale, shift) = chunk(linear(SiLU(temb)), 2), LN without affine at eps 1e-5) through a self
+    block whose attention is a plain token mean: zero to_q / to_k (a uniform softmax), identity
+    to_v / to_out and a zero FFN give x + mean_tokens(LN(x)(1 + scale) + shift).  With the linear's
+    weight zero its bias is the (scale, shift) pair: a swapped pair or another eps fails."""
+    cfg, g, x, ctx, temb, p = _d4d_tiny()
+    D, b = cfg.dim, "model.transformer_blocks.1."       # block 1: self attention (interleaved)
+    assert not cfg.is_cross(1)
+    I = torch.eye(D, dtype=torch.float64)
+    scale, shift = torch.randn(D, generator=g, dtype=torch.float64), torch.randn(D, generator=g, dtype=torch.float64)
+    q = dict(p)
+    q[b + "norm1.linear.weight"] = torch.zeros(2 * D, D, dtype=torch.float64)
+    q[b + "norm1.linear.bias"] = torch.cat([scale, shift])
+    for n in ("to_q", "to_k"):
+        q[b + f"attn1.{n}.weight"], q[b + f"attn1.{n}.bias"] = torch.zeros(D, D, dtype=torch.float64), torch.zeros(D, dtype=torch.float64)
+    for n in ("to_v", "to_out.0"):
+        q[b + f"attn1.{n}.weight"], q[b + f"attn1.{n}.bias"] = I.clone(), torch.zeros(D, dtype=torch.float64)
+    q[b + "ff.net.2.weight"], q[b + "ff.net.2.bias"] = torch.zeros(D, 4 * D, dtype=torch.float64), torch.zeros(D, dtype=torch.float64)
+    y = O.d4d_block(q, cfg, 1, x, ctx, temb)
+
+    def expect(sc, sh, eps):
+        return x + (_ln(x, eps) * (1 + sc) + sh).mean(1, keepdim=True)
+    assert torch.allclose(y, expect(scale, shift, 1e-5), atol=1e-9)
+    assert (y - expect(shift, scale, 1e-5)).abs().max() > 0.1          # (shift, scale) order: fails
+    assert (y - expect(scale, shift, 1e-6)).abs().max() > 1e-2         # eps 1e-6: fails
+
+
+def test_d4d_block_norm3_and_ffn_closed_form():
+    """norm3 is a LayerNorm without affine at eps 1e-5 (cross_attention_dit.py:136, 207-208 with
+    DiT's norm_elementwise_affine False) and the FeedForward is net.2(GELU_tanh(net.0.proj(h)))
+    added to x: with the attention branch zero and identity-embedding FFN weights ([I; 0] up,
+    [I, 0] down) a cross block gives x + GELU_tanh(LN(x)) -- independent of the AdaLN
+    modulation (norm3 does not take it) and of the context."""
+    cfg, g, x, ctx, temb, p = _d4d_tiny()
+    D, b = cfg.dim, "model.transformer_blocks.0."
+    assert cfg.is_cross(0)
+    q = dict(p)
+    q[b + "attn1.to_out.0.weight"], q[b + "attn1.to_out.0.bias"] = torch.zeros(D, D, dtype=torch.float64), torch.zeros(D, dtype=torch.float64)
+    q[b + "ff.net.0.proj.weight"] = torch.cat([torch.eye(D, dtype=torch.float64), torch.zeros(3 * D, D, dtype=torch.float64)])
+    q[b + "ff.net.0.proj.bias"] = torch.zeros(4 * D, dtype=torch.float64)
+    q[b + "ff.net.2.weight"] = torch.cat([torch.eye(D, dtype=torch.float64), torch.zeros(D, 3 * D, dtype=torch.float64)], 1)
+    q[b + "ff.net.2.bias"] = torch.zeros(D, dtype=torch.float64)
+    y = O.d4d_block(q, cfg, 0, x, ctx, temb)
+
+    def gelu(u):
+        return 0.5 * u * (1 + torch.tanh(math.sqrt(2 / math.pi) * (u + 0.044715 * u ** 3)))
+    assert torch.allclose(y, x + gelu(_ln(x, 1e-5)), atol=1e-9)
+    assert (y - (x + gelu(_ln(x, 1e-6)))).abs().max() > 1e-2
+    assert (y - (x + torch.nn.functional.gelu(_ln(x, 1e-5)))).abs().max() > 1e-5   # erf GELU differs
+    assert torch.equal(y, O.d4d_block(q, cfg, 0, x, ctx * 3, temb * 2))
+
+
+def test_d4d_output_stage_closed_form():
+    """DiT.forward's output stage (cross_attention_dit.py:302-304): (shift, scale) =
+    chunk(proj_out_1(SiLU(temb)), 2) -- the opposite order of the blocks' AdaLayerNorm --
+    LN without affine at eps 1e-6 (norm_out, :253), then proj_out_2.  Blocks that are the
+    identity (zero attention output and FFN) and an identity proj_out_2 leave
+    LN_1e-6(x)(1 + scale) + shift; a swapped pair or eps 1e-5 fails."""
+    cfg, g, x, ctx, temb, p = _d4d_tiny()
+    D = cfg.dim
+    q = dict(p)
+    for i in range(cfg.num_layers):
+        b = f"model.transformer_blocks.{i}."
+        for n in ("attn1.to_out.0", "ff.net.2"):
+            q[b + n + ".weight"] = torch.zeros_like(p[b + n + ".weight"])
+            q[b + n + ".bias"] = torch.zeros_like(p[b + n + ".bias"])
+    shift, scale = torch.randn(D, generator=g, dtype=torch.float64), torch.randn(D, generator=g, dtype=torch.float64)
+    q["model.proj_out_1.weight"] = torch.zeros(2 * D, D, dtype=torch.float64)
+    q["model.proj_out_1.bias"] = torch.cat([shift, scale])
+    q["model.proj_out_2.weight"] = torch.eye(cfg.output_dim, D, dtype=torch.float64)
+    q["model.proj_out_2.bias"] = torch.zeros(cfg.output_dim, dtype=torch.float64)
+    y = O.d4d_dit_forward(q, cfg, x, ctx, torch.tensor([1000, 250]))
+    assert torch.allclose(y, _ln(x, 1e-6) * (1 + scale) + shift, atol=1e-9)
+    assert (y - (_ln(x, 1e-6) * (1 + shift) + scale)).abs().max() > 0.1
+    assert (y - (_ln(x, 1e-5) * (1 + scale) + shift)).abs().max() > 1e-2
+
+
+def test_d4d_action_encoder_closed_form():
+    """ActionEncoder (DB/modules/action_model/ActionDiT.py:74-98): layer2 reads cat(layer1(a), tau)
+    in that order, swish, layer3.  With layer2 = [0 | I] (it keeps only the tau half), layer3 = I
+    and zero biases the output is swish(tau(t)) for every token, whatever the actions; with
+    layer2 = [I | 0] it is swish(layer1(a)).  Reading (tau, a) instead fails both."""
+    cfg, g, _, _, _, p = _d4d_tiny()
+    D = cfg.dim
+    acts = torch.randn(2, 6, cfg.action_dim, generator=g, dtype=torch.float64)
+    t = torch.tensor([1000, 250])
+    q = dict(p)
+    I, Z = torch.eye(D, dtype=torch.float64), torch.zeros(D, D, dtype=torch.float64)
+    q["action_encoder.layer2.bias"] = torch.zeros(D, dtype=torch.float64)
+    q["action_encoder.layer3.weight"], q["action_encoder.layer3.bias"] = I.clone(), torch.zeros(D, dtype=torch.float64)
+    swish = lambda u: u * torch.sigmoid(u)  # noqa: E731
+    q["action_encoder.layer2.weight"] = torch.cat([Z, I], 1)
+    tau = O.d4d_tau_encoding(t[:, None].expand(2, 6), D).double()
+    assert torch.allclose(O.d4d_action_encoder(q, acts, t), swish(tau), atol=1e-9)
+    q["action_encoder.layer2.weight"] = torch.cat([I, Z], 1)
+    a = acts @ p["action_encoder.layer1.weight"].t() + p["action_encoder.layer1.bias"]
+    assert torch.allclose(O.d4d_action_encoder(q, acts, t), swish(a), atol=1e-9)
+
+
 # --------------------------------------------------------------------------- WanVideoDiT pre_dit / forward
 WAN_TINY = O.WanVideoConfig(hidden_dim=32, in_dim=4, ffn_dim=64, out_dim=4, text_dim=24, freq_dim=16, eps=1e-6,
                             patch_size=(1, 2, 2), num_heads=2, attn_head_dim=24, num_layers=2)
@@ -603,3 +721,50 @@ def test_wan_vae_avg_down_closed_forms():
     assert torch.equal(y[:, 0::2], torch.zeros_like(y[:, 0::2]))
     assert torch.allclose(y[:, 1::2], pool, atol=1e-6)
     assert torch.equal(O.vae_avg_down(x, 6, 1, 1), x)
+
+
+# --------------------------------------------------------------------------- branch metrics' power
+def test_block_branch_metrics_catch_planted_slips(monkeypatch):
+    """The config-2 block test (tests/test_configs_gpu.py::test_config2_video_block_full_shape, same
+    seeds and shape: 1560 tokens on a 2 x 30 x 26 grid, hidden 3072, 24 x 128 heads, FFN 14336,
+    512 text tokens) asserts its branch metrics at 2e-2.  Each slip planted here in the oracle moves
+    at least one of them past that bar, while the block's output alone moves less than the bar for
+    the first two (measured 1.8e-2 and 2.0e-2): RoPE dropped, the (h, w) grid of the 3-D table
+    transposed, the self-attention zeroed, and V read one head off (a mis-strided head)."""
+    from block_checks import BAR, rel, trace_errors
+    f, hh, ww = 2, 30, 26
+    S, H, nh, Dh, F_, Lc = f * hh * ww, 3072, 24, 128, 14336, 512
+    ocfg = O.ActionDiTConfig(hidden_dim=H, action_dim=7, ffn_dim=F_, text_dim=H, freq_dim=256, num_heads=nh,
+                             attn_head_dim=Dh, num_layers=1)
+    p = {k: v.to(torch.bfloat16).float() for k, v in O.init_action_dit_params(ocfg, 103).items()}
+    g = torch.Generator().manual_seed(104)
+    x = torch.randn(1, S, H, generator=g).to(torch.bfloat16).float()
+    ctx = torch.randn(1, Lc, H, generator=g).to(torch.bfloat16).float()
+    tm = (torch.randn(1, S, 6, H, generator=g) * 0.2).to(torch.bfloat16).float()
+    tab = O.precompute_freqs_cis_3d(Dh)
+    freqs = O.video_freqs(tab, f, hh, ww)
+    tr = {}
+    ref = O.dit_block(p, 0, x, ctx, tm, freqs, nh, 1e-6, trace=tr)
+
+    def planted(params=p, fr=freqs):
+        t = {}
+        y = O.dit_block(params, 0, x, ctx, tm, fr, nh, 1e-6, trace=t)
+        return trace_errors(t, tr, x, y, ref), rel(y, ref)
+
+    zeroed = dict(p)
+    for n in ("o.weight", "o.bias"):
+        zeroed["blocks.0.self_attn." + n] = torch.zeros_like(p["blocks.0.self_attn." + n])
+    cases = {"rope dropped": planted(fr=torch.ones_like(freqs)),
+             "(h, w) transposed": planted(fr=O.video_freqs(tab, f, ww, hh)),
+             "self-attention zeroed": planted(params=zeroed)}
+    attn = O.flash_attention
+    monkeypatch.setattr(O, "flash_attention",
+                        lambda q, k, v, n, mask=None: attn(q, k, v.roll(v.shape[-1] // n, dims=-1), n, mask))
+    cases["V one head off"] = planted()
+    monkeypatch.undo()
+    for name, (errs, out_err) in cases.items():
+        print(f"{name}: output {out_err:.3e}, " + ", ".join(f"{k} {v:.3e}" for k, v in errs.items()))
+        assert max(errs.values()) > BAR, (name, errs)
+    assert cases["rope dropped"][1] < BAR and cases["(h, w) transposed"][1] < BAR
+    assert cases["rope dropped"][0]["self_attn"] > 10 * BAR and cases["(h, w) transposed"][0]["self_attn"] > 10 * BAR
+    assert cases["self-attention zeroed"][0]["delta"] > BAR
