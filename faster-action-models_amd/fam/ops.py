@@ -185,15 +185,18 @@ _TABLES: "OrderedDict[tuple, tuple]" = OrderedDict()
 _TABLES_MAX = 64
 
 
-def _check_pair_layout(f: torch.Tensor, layout: str) -> None:
+def _check_pair_layout(f: torch.Tensor, layout: str, src_dtype: torch.dtype = torch.float32) -> None:
     """Reject a real table whose (cos, sin) pairs are not where `layout` says: FG packs
     cat(cos, sin) per row, CA interleaves (cos, sin) pairs, and both are [S, 1, Dh] -- read
     with the other convention, every position rotates the wrong pairs.  The pairs of the right
-    layout have unit modulus; position 0 of the other layout pairs (1, 1) or (0, 0)."""
+    layout have unit modulus up to the rounding of the table's own dtype (FG's pack_rope_real
+    takes a dtype: a bf16 table is off by up to ~8e-3); position 0 of the other layout pairs
+    (1, 1) or (0, 0), a deviation of 1."""
+    tol = max(1e-3, 8.0 * torch.finfo(src_dtype).eps) if src_dtype.is_floating_point else 1e-3
     half = f.shape[1] // 2
     c, s_ = (f[:, :half], f[:, half:]) if layout == "cat" else (f[:, 0::2], f[:, 1::2])
     dev = (c.double() ** 2 + s_.double() ** 2 - 1.0).abs().max().item() if f.numel() else 0.0
-    if dev > 1e-3:
+    if dev > tol:
         other = "rope_apply_cae (CA's interleaved (cos, sin) table)" if layout == "cat" else \
             "rope_apply (FG's packed cat(cos, sin) table)"
         raise ValueError(f"freqs is not a {layout!r} RoPE table (|cos|^2 + |sin|^2 deviates from 1 by {dev:.3g}); "
@@ -234,7 +237,7 @@ def rope_tables(freqs: torch.Tensor, layout: str, device: torch.device):
         if not (f.dtype == torch.float32 and f.device == torch.device(device) and f.stride(-1) == 1
                 and f.data_ptr() % 16 == 0):
             f = f.to(device=device, dtype=torch.float32).contiguous()
-        _check_pair_layout(f, layout)
+        _check_pair_layout(f, layout, freqs.dtype)
         half = f.shape[1] // 2
         if layout == "cat":
             res = (f, f[:, half:], f.stride(0), 1)

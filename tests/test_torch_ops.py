@@ -150,3 +150,19 @@ def test_rope_tables_reject_the_other_packing():
         ops.rope_tables(cat, "interleaved", torch.device("cpu"))
     with pytest.raises(ValueError):
         ops.rope_tables(cat, "complex", torch.device("cpu"))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rope_tables_accept_a_half_precision_table_in_the_right_packing(dtype):
+    """A table packed right but stored in bf16 / fp16 (FG's pack_rope_real takes a dtype) has
+    pairs off unit modulus by its own rounding: it is accepted (and converted to fp32), while the
+    same table in the other packing is still refused."""
+    cat = _cat_table(64, 128, offset=0.0).to(dtype)
+    inter = _interleaved(cat).contiguous()
+    cos, sin, trs, tes = ops.rope_tables(cat, "cat", torch.device("cpu"))
+    assert cos.dtype == torch.float32 and torch.equal(cos[:, :64], cat.reshape(64, 128)[:, :64].float())
+    ops.rope_tables(inter, "interleaved", torch.device("cpu"))
+    with pytest.raises(ValueError, match="rope_apply_cae"):
+        ops.rope_tables(inter, "cat", torch.device("cpu"))
+    with pytest.raises(ValueError, match="rope_apply "):
+        ops.rope_tables(cat, "interleaved", torch.device("cpu"))

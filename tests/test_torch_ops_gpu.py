@@ -137,6 +137,52 @@ def test_skpost(fw, mode):
     assert _rel(yo, o) <= 2e-2
 
 
+@pytest.mark.parametrize("xdt,affine", [(0, True), (0, False), (1, True), (1, False)])
+def test_skpost_follows_the_eager_rounding(fw, xdt, affine):
+    """fastwam::skpost pinned to the eager block it stands in for (FB/wan_video_dit.py:271-285), far
+    inside the 2e-2 bar: the gate is the bf16 sum modulation + t_mod (the eager chunk), the
+    residual add rounds once to bf16 and the norm reads that bf16 row.  (The GEAK Triton op,
+    FG/mot.py:1283-1313, sums the gate in fp32 and normalises the unrounded fp32 x instead: a
+    different rounding order, about one bf16 ulp apart.)  With xdt = 1 the stored x is the fp32
+    res + gate * (a w^T + bias)."""
+    g = torch.Generator().manual_seed(17)
+    M, N, K = 32, 1024, 3072
+    a, w = _rand(g, 1, M, K), _rand(g, N, K, scale=0.02)
+    bias, res = _rand(g, N, scale=0.02), _rand(g, 1, M, N)
+    modg, moda, tmod = _rand(g, 1, 6, N, scale=0.1), _rand(g, 1, 6, N, scale=0.1), _rand(g, 1, 6, N, scale=0.1)
+    lnw, lnb = (1 + 0.2 * torch.randn(N, generator=g)).to(BF), (0.2 * torch.randn(N, generator=g)).to(BF)
+    gi, si, hi = 2, 4, 3
+    d = lambda t: t.cuda() if t is not None else None  # noqa: E731
+    xo, yo = torch.ops.fastwam.skpost.default(d(a), d(w), d(bias), d(res), d(modg), d(moda), d(tmod),
+                                              d(lnw) if affine else None, d(lnb) if affine else None,
+                                              gi, si, hi, 1e-6, xdt)
+    # eager bf16 composition: chunks of (modulation + t_mod) in bf16, nn.Linear output in bf16,
+    # x = x + gate * y in bf16, then the norm of the bf16 x
+    chunks, chunks_a = (modg + tmod)[0], (moda + tmod)[0]         # bf16 sums
+    y32 = a[0].double() @ w.double().t() + bias.double()
+    gate = chunks[gi].double()
+    x_e = (res[0].double() + gate * y32.to(BF).double()).to(BF)
+    xf = x_e.double()
+    ln = (xf - xf.mean(-1, keepdim=True)) / torch.sqrt(xf.var(-1, unbiased=False, keepdim=True) + 1e-6)
+    if affine:
+        o_e = ln * lnw.double() + lnb.double()
+    else:
+        o_e = ln * (1 + chunks_a[si].double()) + chunks_a[hi].double()
+    xo, yo = xo[0].cpu().double(), yo[0].cpu().double()
+    if xdt:
+        x32 = res[0].double() + gate * y32
+        assert ((xo - x32).abs().max() / x32.abs().max()).item() <= 1e-5
+    else:
+        # one bf16 rounding of x apart at most (the eager form rounds y and gate * y as well)
+        ulp = torch.finfo(BF).eps
+        assert ((xo - xf).abs() <= ulp * (xf.abs() + (gate * y32).abs()) + 1e-6).all()
+    assert ((yo - o_e).abs().max() / o_e.abs().max()).item() <= 8e-3
+    # a swapped scale / shift or a dropped gate moves the result far past these bounds
+    if not affine:
+        swapped = ln * (1 + chunks_a[hi].double()) + chunks_a[si].double()
+        assert ((yo - swapped).abs().max() / o_e.abs().max()).item() > 5e-2
+
+
 def test_fam_ops_under_torch_compile_match_eager():
     """A block-shaped module calling the fam:: drop-ins, compiled with fullgraph=True
     (aot_eager: no generated kernels around them), gives the eager result bit for bit."""
