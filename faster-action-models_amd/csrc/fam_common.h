@@ -81,6 +81,10 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
+// 0.5 x (1 + erf(x / sqrt(2))): nn.GELU() without approximation (the Cosmos backbone's
+// FeedForward, activation_fn "gelu"), with the device library's erff
+__device__ __forceinline__ float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f)); }
+
 // x sigmoid(x) with the hardware exp2 and reciprocal (no IEEE division); e^(-x) overflowing to
 // +inf gives x * 0
 __device__ __forceinline__ float silu(float x) {

@@ -65,6 +65,7 @@ __device__ __forceinline__ float apply_act(float v, int act) {
   if (act == FAM_ACT_GELU_TANH) return gelu_tanh(v);
   if (act == FAM_ACT_SILU) return silu(v);
   if (act == FAM_ACT_RELU) return fmaxf(v, 0.f);
+  if (act == FAM_ACT_GELU_ERF) return gelu_erf(v);
   return v;
 }
 
@@ -748,6 +749,7 @@ __global__ __launch_bounds__(NW * 64) void final_kernel(FinalArgs g) {
       if (g.act == FAM_ACT_GELU_TANH) x = gelu_tanh(x);
       else if (g.act == FAM_ACT_SILU) x = silu(x);
       else if (g.act == FAM_ACT_RELU) x = fmaxf(x, 0.f);
+      else if (g.act == FAM_ACT_GELU_ERF) x = gelu_erf(x);
       o[e] = to_bf(x);
       const float r = to_f(o[e]);
       ss += (nc + e < g.N) ? r * r : 0.f;
@@ -1321,7 +1323,7 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
               "fam_gemm: a and w must be 16-byte aligned");
   FAM_REQUIRE(d->prologue >= FAM_PRO_NONE && d->prologue <= FAM_PRO_LN_FOLDED, FAM_ERR_INVALID_ARG,
               "fam_gemm: unknown prologue %d", d->prologue);
-  FAM_REQUIRE(d->act >= FAM_ACT_NONE && d->act <= FAM_ACT_RELU, FAM_ERR_INVALID_ARG, "fam_gemm: unknown act %d", d->act);
+  FAM_REQUIRE(d->act >= FAM_ACT_NONE && d->act <= FAM_ACT_GELU_ERF, FAM_ERR_INVALID_ARG, "fam_gemm: unknown act %d", d->act);
   if (d->prologue == FAM_PRO_LAYERNORM) {
     FAM_REQUIRE((!d->pro_w || fam_host::aligned16(d->pro_w)) && (!d->pro_b || fam_host::aligned16(d->pro_b)),
                 FAM_ERR_INVALID_ARG, "fam_gemm: LayerNorm affine must be 16-byte aligned");
@@ -1401,7 +1403,7 @@ extern "C" int fam_gemm_ws(const fam_gemm_desc* d, float* ws, int64_t ws_floats,
   FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_gemm_ws: null descriptor");
   FAM_REQUIRE(ws_floats >= 0 && (ws_floats == 0 || (ws && ((uintptr_t)ws & 15u) == 0)), FAM_ERR_INVALID_ARG,
               "fam_gemm_ws: workspace must be 16-byte aligned");
-  if (!big_ok(d) || d->M < 128 || ws_floats < 2 * d->M * d->N || d->N % 4 != 0 || d->act > FAM_ACT_RELU)
+  if (!big_ok(d) || d->M < 128 || ws_floats < 2 * d->M * d->N || d->N % 4 != 0 || d->act > FAM_ACT_GELU_ERF)
     return fam_gemm(d, stream);
   int fm = 8, fn = 8, ks = 1;
   big_plan_split(d->M, d->N, d->K, ws_floats, false, &fm, &fn, &ks);
@@ -1641,7 +1643,7 @@ extern "C" int fam_gemm_final(const void* a, int64_t lda, const void* w, int64_t
               "fam_gemm_final: lda/ldw must be >= K and multiples of 8, ldo >= N");
   FAM_REQUIRE(fam_host::aligned16(a) && fam_host::aligned16(w) && (reinterpret_cast<uintptr_t>(out) & 7u) == 0,
               FAM_ERR_INVALID_ARG, "fam_gemm_final: a, w 16-byte and out 8-byte aligned");
-  FAM_REQUIRE(act >= FAM_ACT_NONE && act <= FAM_ACT_RELU, FAM_ERR_INVALID_ARG, "fam_gemm_final: unknown act %d", act);
+  FAM_REQUIRE(act >= FAM_ACT_NONE && act <= FAM_ACT_GELU_ERF, FAM_ERR_INVALID_ARG, "fam_gemm_final: unknown act %d", act);
   FAM_REQUIRE((N + 15) / 16 <= 2147483647LL, FAM_ERR_UNSUPPORTED, "fam_gemm_final: N too large");
   if (M == 0) return FAM_OK;
   FinalArgs fa{(const bf16*)a, lda, (const bf16*)w, ldw, (const bf16*)bias, act, (bf16*)out, ldo, sumsq, M, N, K};

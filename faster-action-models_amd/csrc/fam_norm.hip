@@ -498,3 +498,124 @@ extern "C" int fam_rmsnorm_grouped(const void* x, int64_t x_row_stride, void* y,
   return rmsnorm_rope_impl(x, x_row_stride, y, y_row_stride, rows, 1, dim, weights, groups, eps, nullptr, nullptr,
                            0, 0, 0, stream);
 }
+
+// ---------------------------------------------------------------------------------------
+// Per-head RMSNorm + rotate-half RoPE (the Cosmos backbone's q / k: RMSNorm(head_dim) with a
+// head_dim-wide weight shared by the heads, then apply_rotary_emb(use_real=True,
+// use_real_unbind_dim=-2), whose pairs are (d, d + head_dim / 2)).
+//
+// One thread owns 8 consecutive elements (16 bytes) of one head; the LPH = head_dim / 8 lanes of
+// a head are consecutive lanes of one wave (a segment's width is a whole number of heads, so a
+// head never straddles a wave), its sum of squares is an xor-shuffle reduction over them, and
+// the rotation partner of element d -- d + head_dim / 2 or d - head_dim / 2 -- sits in lane
+// l ^ (LPH / 2) at the same position.  Loads (x, weight, the table rows) are issued first.
+// Bytes per row segment: 2 * width (x) + 2 * width (y); the weight and the tables are L2-resident.
+namespace fam {
+struct HeadNormArgs {
+  const bf16* x; int64_t xrs;
+  bf16* y; int64_t yrs;
+  int64_t rows, seq, nseg, seg_stride, width;
+  const bf16* w; int64_t wss;
+  float eps;
+  const float* cs; const float* sn; int64_t trs;
+  uint32_t total;   // rows * nseg * width / 8 threads
+};
+
+template <int LPH, bool ROPE>
+__global__ __launch_bounds__(256) void headnorm_rope_kernel(HeadNormArgs a) {
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  if (t >= a.total) return;   // a head's lanes share the test: total is a multiple of LPH
+  const uint32_t cpr = (uint32_t)(a.width >> 3), cps = cpr * (uint32_t)a.nseg;
+  const uint32_t r = t / cps, rem = t - r * cps;
+  const uint32_t seg = rem / cpr, c = rem - seg * cpr;
+  const uint32_t cl = c & (LPH - 1);                      // chunk within the head
+  const int64_t col = (int64_t)seg * a.seg_stride + (int64_t)c * 8;
+  const bf16x8 v = load8(a.x + (int64_t)r * a.xrs + col);
+  const bf16x8 w = load8(a.w + (int64_t)seg * a.wss + cl * 8);
+  f32x4 c0, c1, s0, s1;
+  if constexpr (ROPE) {
+    const int64_t pos = (int64_t)(r % (uint32_t)a.seq);
+    const float* cp = a.cs + pos * a.trs + cl * 8;
+    const float* sp = a.sn + pos * a.trs + cl * 8;
+    c0 = *reinterpret_cast<const f32x4*>(cp);
+    c1 = *reinterpret_cast<const f32x4*>(cp + 4);
+    s0 = *reinterpret_cast<const f32x4*>(sp);
+    s1 = *reinterpret_cast<const f32x4*>(sp + 4);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += to_f(v[e]) * to_f(v[e]);
+#pragma unroll
+  for (int o = LPH / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, kWave);
+  const float rstd = rsqrtf(ss * (1.0f / (float)(LPH * 8)) + a.eps);
+  float n[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) n[e] = to_f(to_bf(to_f(to_bf(to_f(v[e]) * rstd)) * to_f(w[e])));
+  bf16x8 o;
+  if constexpr (ROPE) {
+    // rotated = cat(-x[D/2:], x[:D/2]): the first half takes minus its partner, the second plus
+    const float sg = cl < (uint32_t)(LPH / 2) ? -1.f : 1.f;
+    const float cv[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+    const float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = __shfl_xor(n[e], LPH / 2, kWave);
+      o[e] = to_bf(n[e] * cv[e] + sg * p * sv[e]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = to_bf(n[e]);
+  }
+  store8(a.y + (int64_t)r * a.yrs + col, o);
+}
+}  // namespace fam
+
+extern "C" int fam_headnorm_rope(const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride, int64_t rows,
+                                 int64_t seq_len, int64_t nseg, int64_t seg_stride, int64_t width, int64_t head_dim,
+                                 const void* weight, int64_t weight_seg_stride, float eps, const float* cos_tab,
+                                 const float* sin_tab, int64_t tab_row_stride, void* stream) {
+  using namespace fam;
+  FAM_REQUIRE(x && y && weight, FAM_ERR_INVALID_ARG, "fam_headnorm_rope: x, y and weight must be non-null");
+  FAM_REQUIRE(head_dim >= 16 && head_dim <= 512 && (head_dim & (head_dim - 1)) == 0, FAM_ERR_INVALID_ARG,
+              "fam_headnorm_rope: head_dim must be a power of two in [16, 512] (got %lld)", (long long)head_dim);
+  FAM_REQUIRE(rows >= 0 && nseg >= 1 && width >= head_dim && width % head_dim == 0, FAM_ERR_INVALID_ARG,
+              "fam_headnorm_rope: need rows >= 0, nseg >= 1 and width a multiple of head_dim");
+  FAM_REQUIRE(seg_stride % 8 == 0 && x_row_stride % 8 == 0 && y_row_stride % 8 == 0 && weight_seg_stride % 8 == 0 &&
+                  (nseg == 1 || seg_stride >= width) &&
+                  x_row_stride >= (nseg - 1) * seg_stride + width && y_row_stride >= (nseg - 1) * seg_stride + width,
+              FAM_ERR_INVALID_ARG,
+              "fam_headnorm_rope: strides must be multiples of 8 elements and the segments must fit the rows");
+  FAM_REQUIRE(fam_host::aligned16(x) && fam_host::aligned16(y) && fam_host::aligned16(weight), FAM_ERR_INVALID_ARG,
+              "fam_headnorm_rope: x, y and weight must be 16-byte aligned");
+  FAM_REQUIRE((cos_tab == nullptr) == (sin_tab == nullptr), FAM_ERR_INVALID_ARG,
+              "fam_headnorm_rope: cos_tab and sin_tab must both be given or both be null");
+  if (cos_tab)
+    FAM_REQUIRE(seq_len >= 1 && tab_row_stride >= head_dim && tab_row_stride % 4 == 0 &&
+                    fam_host::aligned16(cos_tab) && fam_host::aligned16(sin_tab),
+                FAM_ERR_INVALID_ARG,
+                "fam_headnorm_rope: tables need seq_len >= 1, a row stride >= head_dim (multiple of 4) and "
+                "16-byte alignment");
+  const int64_t total = rows * nseg * (width / 8);
+  FAM_REQUIRE(total < ((int64_t)1 << 32) - 256, FAM_ERR_UNSUPPORTED, "fam_headnorm_rope: too many elements");
+  if (total == 0) return FAM_OK;
+  HeadNormArgs a{(const bf16*)x, x_row_stride, (bf16*)y, y_row_stride, rows, seq_len > 0 ? seq_len : 1, nseg,
+                 seg_stride, width, (const bf16*)weight, weight_seg_stride, eps, cos_tab, sin_tab, tab_row_stride,
+                 (uint32_t)total};
+  const dim3 grid((unsigned)((total + 255) / 256)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+#define FAM_HN(L)                                                                         \
+  do {                                                                                    \
+    if (cos_tab) FAM_LAUNCH((headnorm_rope_kernel<L, true>), grid, block, 0, s, a);       \
+    else FAM_LAUNCH((headnorm_rope_kernel<L, false>), grid, block, 0, s, a);              \
+  } while (0)
+  switch (head_dim) {
+    case 16: FAM_HN(2); break;
+    case 32: FAM_HN(4); break;
+    case 64: FAM_HN(8); break;
+    case 128: FAM_HN(16); break;
+    case 256: FAM_HN(32); break;
+    default: FAM_HN(64); break;
+  }
+#undef FAM_HN
+  return fam_host::check_launch("fam_headnorm_rope");
+}

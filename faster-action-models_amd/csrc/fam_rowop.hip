@@ -40,6 +40,7 @@ __device__ __forceinline__ float act_fn(float v, int act) {
   if (act == FAM_ACT_GELU_TANH) return gelu_tanh(v);
   if (act == FAM_ACT_SILU) return silu(v);
   if (act == FAM_ACT_RELU) return fmaxf(v, 0.f);
+  if (act == FAM_ACT_GELU_ERF) return gelu_erf(v);
   return v;
 }
 
@@ -486,7 +487,7 @@ extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
   } else {
     FAM_REQUIRE(false, FAM_ERR_INVALID_ARG, "fam_rowop: unknown source %d", d->src);
   }
-  FAM_REQUIRE(d->act >= FAM_ACT_NONE && d->act <= FAM_ACT_RELU, FAM_ERR_INVALID_ARG, "fam_rowop: unknown act");
+  FAM_REQUIRE(d->act >= FAM_ACT_NONE && d->act <= FAM_ACT_GELU_ERF, FAM_ERR_INVALID_ARG, "fam_rowop: unknown act");
   FAM_REQUIRE(!d->gate || d->res, FAM_ERR_INVALID_ARG, "fam_rowop: a gate needs a residual");
   FAM_REQUIRE(d->rows_per_batch >= 1, FAM_ERR_INVALID_ARG, "fam_rowop: rows_per_batch must be >= 1");
   FAM_REQUIRE(d->norm >= FAM_ROWNORM_NONE && d->norm <= FAM_ROWNORM_RMS, FAM_ERR_INVALID_ARG, "fam_rowop: unknown norm");

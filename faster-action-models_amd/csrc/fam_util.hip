@@ -124,11 +124,45 @@ __global__ __launch_bounds__(256) void linear_smallk_kernel(const XT* __restrict
   y[m * ldy + n] = to_bf(acc);
 }
 
+// y = bf16(act(x)) elementwise over rows of 8-element chunks; one thread per chunk.
+__global__ __launch_bounds__(256) void act_rows_kernel(const bf16* x, int64_t ldx, bf16* y, int64_t ldy,
+                                                       uint32_t rows, uint32_t c8, int act) {
+  const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
+  if (idx >= rows * c8) return;
+  const uint32_t r = idx / c8, c = (idx - r * c8) * 8;
+  const bf16x8 v = load8(x + (int64_t)r * ldx + c);
+  bf16x8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float f = to_f(v[e]);
+    o[e] = to_bf(act == FAM_ACT_SILU ? silu(f) : act == FAM_ACT_GELU_TANH ? gelu_tanh(f)
+                 : act == FAM_ACT_GELU_ERF ? gelu_erf(f) : act == FAM_ACT_RELU ? fmaxf(f, 0.f) : f);
+  }
+  store8(y + (int64_t)r * ldy + c, o);
+}
+
 }  // namespace fam
 
 using namespace fam;
 
 extern "C" int fam_version(void) { return FAM_ABI_VERSION; }
+
+extern "C" int fam_act_rows(const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride, int64_t rows,
+                            int64_t cols, int act, void* stream) {
+  FAM_REQUIRE(x && y, FAM_ERR_INVALID_ARG, "fam_act_rows: x and y must be non-null");
+  FAM_REQUIRE(act >= FAM_ACT_NONE && act <= FAM_ACT_GELU_ERF, FAM_ERR_INVALID_ARG, "fam_act_rows: unknown act %d", act);
+  FAM_REQUIRE(rows >= 0 && cols >= 0 && cols % 8 == 0 && x_row_stride % 8 == 0 && y_row_stride % 8 == 0 &&
+                  x_row_stride >= cols && y_row_stride >= cols,
+              FAM_ERR_INVALID_ARG, "fam_act_rows: cols and row strides must be multiples of 8, strides >= cols");
+  FAM_REQUIRE(fam_host::aligned16(x) && fam_host::aligned16(y), FAM_ERR_INVALID_ARG,
+              "fam_act_rows: x and y must be 16-byte aligned");
+  const int64_t n = rows * (cols / 8);
+  FAM_REQUIRE(n < ((int64_t)1 << 32) - 256, FAM_ERR_UNSUPPORTED, "fam_act_rows: too many elements");
+  if (n == 0) return FAM_OK;
+  FAM_LAUNCH(act_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream, (const bf16*)x,
+             x_row_stride, (bf16*)y, y_row_stride, (uint32_t)rows, (uint32_t)(cols / 8), act);
+  return fam_host::check_launch("fam_act_rows");
+}
 
 extern "C" const char* fam_last_error(void) { return fam_host::g_err; }
 

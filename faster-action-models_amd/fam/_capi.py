@@ -19,7 +19,7 @@ FAM_ABI_VERSION = 2
 
 FAM_MASK_NONE, FAM_MASK_BOOL, FAM_MASK_ADD_F32, FAM_MASK_ADD_BF16 = 0, 1, 2, 3
 FAM_PRO_NONE, FAM_PRO_LAYERNORM, FAM_PRO_ADALN, FAM_PRO_LN_FOLDED = 0, 1, 2, 3
-FAM_ACT_NONE, FAM_ACT_GELU_TANH, FAM_ACT_SILU, FAM_ACT_RELU = 0, 1, 2, 3
+FAM_ACT_NONE, FAM_ACT_GELU_TANH, FAM_ACT_SILU, FAM_ACT_RELU, FAM_ACT_GELU_ERF = 0, 1, 2, 3, 4
 FAM_ROWSRC_PARTIALS, FAM_ROWSRC_SMALLK = 0, 1
 FAM_ROWNORM_NONE, FAM_ROWNORM_LAYERNORM, FAM_ROWNORM_ADALN, FAM_ROWNORM_RMS = 0, 1, 2, 3
 
@@ -122,6 +122,9 @@ SIGNATURES = {
     "fam_rmsnorm_rope": (C.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _vp, C.c_float, _vp, _vp, _i64, _i64,
                                    _i64, _vp]),
     "fam_rmsnorm_grouped": (C.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp, _i64, C.c_float, _vp]),
+    "fam_headnorm_rope": (C.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _i64, C.c_float,
+                                    _vp, _vp, _i64, _vp]),
+    "fam_act_rows": (C.c_int, [_vp, _i64, _vp, _i64, _i64, _i64, C.c_int, _vp]),
     "fam_attention": (C.c_int, [C.POINTER(AttnDesc), _vp]),
     "fam_attention_combine": (C.c_int, [C.POINTER(AttnDesc), _vp]),
     "fam_attention_key_splits": (C.c_int, [_i64, _i64, _i64, _i64, _i64]),

@@ -113,6 +113,38 @@ int fam_rmsnorm_grouped(const void* x, int64_t x_row_stride, void* y, int64_t y_
                         int64_t rows, int64_t dim, const void* weights, int64_t groups, float eps,
                         void* stream);
 
+/*
+ * fam_headnorm_rope -- per-head RMSNorm, then rotate-half RoPE, over nseg column segments of
+ * each row (the Cosmos backbone's q / k).  Segment s covers columns [s * seg_stride,
+ * s * seg_stride + width) in heads of head_dim; for each head h of row r:
+ *   n = bf16(bf16(x_h * rsqrt(mean(x_h^2) + eps)) * weight[s * weight_seg_stride + d])
+ *   rope (cos_tab != NULL): y_h[d] = bf16(n[d] c[d] + r[d] s[d]),  r = cat(-n[D/2:], n[:D/2]),
+ *     (c, s) = (cos_tab, sin_tab)[(r % seq_len) * tab_row_stride + d], fp32 tables [S, head_dim]
+ *     whose halves repeat the same angles (pairs (d, d + head_dim / 2))
+ * y may equal x.  One launch normalises q and k of a block (nseg = 2, seg_stride = A, weights
+ * [norm_q; norm_k]) or the context keys of every block (nseg = blocks).
+ * Replaces: CosmosAttnProcessor2_0's norm_q / norm_k (RMSNorm(attention_head_dim), diffusers'
+ *           RMSNorm: bf16 rounding before the weight) and apply_rotary_emb(use_real=True,
+ *           use_real_unbind_dim=-2) (src/dit4dit-geak/patches/diffusers-3996788-transformer_cosmos-
+ *           geak.patch:1289-1316, 1525-1710; the fused form _geak_qkrope :846-907).
+ * Limits: head_dim a power of two in [16, 512]; width a multiple of head_dim; strides and
+ * seg_stride multiples of 8 elements; 16-byte aligned x, y, weight and tables.
+ */
+int fam_headnorm_rope(const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride, int64_t rows,
+                      int64_t seq_len, int64_t nseg, int64_t seg_stride, int64_t width, int64_t head_dim,
+                      const void* weight, int64_t weight_seg_stride, float eps, const float* cos_tab,
+                      const float* sin_tab, int64_t tab_row_stride, void* stream);
+
+/*
+ * fam_act_rows -- y[r, c] = bf16(act(x[r, c])) for rows x cols (act FAM_ACT_*).
+ * Replaces: the SiLU of CosmosAdaLayerNormZero.forward (`self.activation(embedded_timestep)`,
+ *           shared by every AdaLN unit of the Cosmos blocks; the patch applies it once,
+ *           diffusers-3996788-transformer_cosmos-geak.patch:2171-2175).
+ * Limits: cols and row strides multiples of 8; 16-byte aligned rows.
+ */
+int fam_act_rows(const void* x, int64_t x_row_stride, void* y, int64_t y_row_stride, int64_t rows, int64_t cols,
+                 int act, void* stream);
+
 /* Attention mask kinds for fam_attn_desc.mask_kind. */
 #define FAM_MASK_NONE 0
 #define FAM_MASK_BOOL 1      /* uint8, nonzero = attend (torch bool)      */
@@ -233,6 +265,7 @@ int64_t fam_attention_noalloc_max_bytes(void);
 #define FAM_ACT_GELU_TANH 1
 #define FAM_ACT_SILU 2
 #define FAM_ACT_RELU 3   /* the DiT4DiT head's MLPs: DB/modules/action_model/ActionDiT.py:52-61 */
+#define FAM_ACT_GELU_ERF 4  /* exact GELU, the Cosmos backbone's FeedForward ("gelu"); erff */
 
 /*
  * fam_gemm -- out[m, n] = epilogue( sum_k pro(a)[m, k] * w[n, k] + bias[n] ),

@@ -1154,3 +1154,238 @@ def wan_vae_encode_first_frame(p: Params, cfg: WanVaeConfig, image: torch.Tensor
     mu = x[:, :cfg.z_dim]
     mu = (mu - mean.reshape(1, -1, 1, 1)) * (1.0 / std).reshape(1, -1, 1, 1)
     return mu.unsqueeze(2)
+
+
+# ---------------------------------------------------------------------------
+# Cosmos-Predict2.5 backbone of DiT4DiT (config 4): diffusers' CosmosTransformer3DModel at
+# 3996788 (scripts/dit4dit_diffusers_overlay.sh:7,35) as the reference patches it,
+#   CP = src/dit4dit-geak/patches/diffusers-3996788-transformer_cosmos-geak.patch
+# and as DB/modules/vlm/Cosmos25.py:60-160 drives it (the output of block extract_layer is the
+# feature the head reads).  diffusers is not installed here and the reference holds no fixture
+# of this model: the composition is restated from the patch (its stock and fast paths, which
+# must agree, CP:2074-2130) and pinned by closed forms in tests/test_oracle.py (AdaLN-LoRA chunk
+# order, the three gated sub-blocks, per-head RMSNorm, rotate-half RoPE, the 3-D table split);
+# parity unpinned as to diffusers itself.
+# ---------------------------------------------------------------------------
+@dataclass
+class CosmosConfig:
+    """Cosmos-Predict2.5-2B-style transformer: hidden 2048 = 16 x 128 heads,
+    28 blocks, MLP ratio 4, AdaLN-LoRA rank 256, patch (1, 2, 2), text features of width 1024
+    (after the pipeline's crossattn_proj), eps 1e-6.  in_channels counts the latent channels plus
+    the condition and padding masks the model concatenates (CP:2289-2360)."""
+    hidden: int = 2048
+    num_heads: int = 16
+    head_dim: int = 128
+    num_layers: int = 28
+    mlp_ratio: int = 4
+    in_channels: int = 18
+    patch_size: Tuple[int, int, int] = (1, 2, 2)
+    text_dim: int = 1024
+    adaln_lora_dim: int = 256
+    rope_scale: Tuple[float, float, float] = (1.0, 3.0, 3.0)
+    base_fps: int = 24
+    eps: float = 1e-6
+
+    @property
+    def attn_dim(self) -> int:
+        return self.num_heads * self.head_dim
+
+
+def cosmos_param_shapes(cfg: CosmosConfig) -> Dict[str, Tuple[int, ...]]:
+    """diffusers state-dict keys of the modules the features path uses: patch_embed.proj
+    (Linear, no bias), time_embed (t_embedder.linear_1 / linear_2 without bias, norm = RMSNorm),
+    and per block norm{1,2,3}.linear_{1,2} (AdaLN-LoRA, no bias), attn1 / attn2 to_q / to_k /
+    to_v / to_out.0 (no bias) with norm_q / norm_k (RMSNorm(head_dim)), ff.net.0.proj / ff.net.2
+    (no bias)."""
+    C, A, D, L = cfg.hidden, cfg.attn_dim, cfg.head_dim, cfg.adaln_lora_dim
+    pt, ph, pw = cfg.patch_size
+    s = {"patch_embed.proj.weight": (C, cfg.in_channels * pt * ph * pw),
+         "time_embed.t_embedder.linear_1.weight": (C, C),
+         "time_embed.t_embedder.linear_2.weight": (3 * C, C),
+         "time_embed.norm.weight": (C,)}
+    for i in range(cfg.num_layers):
+        b = f"transformer_blocks.{i}."
+        for n in ("norm1", "norm2", "norm3"):
+            s[b + n + ".linear_1.weight"] = (L, C)
+            s[b + n + ".linear_2.weight"] = (3 * C, L)
+        for a, kv_in in (("attn1", C), ("attn2", cfg.text_dim)):
+            s[b + a + ".to_q.weight"] = (A, C)
+            s[b + a + ".to_k.weight"] = (A, kv_in)
+            s[b + a + ".to_v.weight"] = (A, kv_in)
+            s[b + a + ".to_out.0.weight"] = (C, A)
+            s[b + a + ".norm_q.weight"] = (D,)
+            s[b + a + ".norm_k.weight"] = (D,)
+        s[b + "ff.net.0.proj.weight"] = (cfg.mlp_ratio * C, C)
+        s[b + "ff.net.2.weight"] = (C, cfg.mlp_ratio * C)
+    return s
+
+
+def init_cosmos_params(cfg: CosmosConfig, seed: int, std: float = 0.02) -> Params:
+    """Seeded synthetic weights, sorted-name draws, fp32: N(0, std), the RMSNorm weights N(1, 0.2)
+    (away from the identity, so that a swapped or mis-indexed norm weight shows)."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    out: Params = {}
+    for name, shape in sorted(cosmos_param_shapes(cfg).items()):
+        if name.endswith("norm_q.weight") or name.endswith("norm_k.weight") or name == "time_embed.norm.weight":
+            out[name] = 1.0 + torch.randn(shape, generator=g) * NORM_AFFINE_STD
+        else:
+            out[name] = torch.randn(shape, generator=g) * std
+    return out
+
+
+def cosmos_rope_tables(cfg: CosmosConfig, t: int, h: int, w: int, fps: Optional[float] = None):
+    """CosmosRotaryPosEmbed.forward (CP:1953-1976): per head dim D the (t, h, w) split is
+    D - 2 (D // 6 * 2), D // 6 * 2, D // 6 * 2 (128 -> 44 / 42 / 42); axis a has angles
+    pos * theta_a^(-2j / dim_a), theta_a = 10000 * rope_scale[a]^(dim_a / (dim_a - 2)) (NTK);
+    the temporal positions are scaled by base_fps / fps when an fps is given; freqs =
+    cat([t, h, w] * 2) per token in (t, h, w) order -- the halves repeat, so pairs are
+    (d, d + D / 2) -- and the tables are cos / sin in fp32, [t h w, D]."""
+    D = cfg.head_dim
+    dh = D // 6 * 2
+    dw = dh
+    dt = D - dh - dw
+    rs_t, rs_h, rs_w = cfg.rope_scale
+
+    def freqs(dim, scale):
+        theta = 10000.0 * scale ** (dim / (dim - 2))
+        rng = torch.arange(0, dim, 2, dtype=torch.float32)[: dim // 2] / dim
+        return 1.0 / theta ** rng
+
+    seq = torch.arange(max(t, h, w), dtype=torch.float32)
+    tpos = seq[:t] if fps is None else seq[:t] / fps * cfg.base_fps
+    et = torch.outer(tpos, freqs(dt, rs_t))[:, None, None, :].expand(t, h, w, dt // 2)
+    eh = torch.outer(seq[:h], freqs(dh, rs_h))[None, :, None, :].expand(t, h, w, dh // 2)
+    ew = torch.outer(seq[:w], freqs(dw, rs_w))[None, None, :, :].expand(t, h, w, dw // 2)
+    f = torch.cat([et, eh, ew] * 2, dim=-1).reshape(t * h * w, D).float()
+    return torch.cos(f), torch.sin(f)
+
+
+def cosmos_apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, num_heads: int) -> torch.Tensor:
+    """apply_rotary_emb(use_real=True, use_real_unbind_dim=-2) as CP:1311-1316: per head,
+    rotated = cat(-x[D/2:], x[:D/2]); out = x cos + rotated sin in fp32, cast back.
+    x [B, S, H*D], cos / sin [S, D]."""
+    b, s, nd = x.shape
+    xh = x.reshape(b, s, num_heads, nd // num_heads).float()
+    half = xh.shape[-1] // 2
+    rot = torch.cat([-xh[..., half:], xh[..., :half]], dim=-1)
+    out = xh * cos[None, :, None, :] + rot * sin[None, :, None, :]
+    return out.reshape(b, s, nd).to(x.dtype)
+
+
+def cosmos_head_rms_norm(x: torch.Tensor, weight: torch.Tensor, num_heads: int, eps: float) -> torch.Tensor:
+    """RMSNorm(head_dim) over each head of x [B, S, H*D] (norm_q / norm_k of the Cosmos attention,
+    CP:1289-1308: diffusers' RMSNorm, x rsqrt(mean(x^2) + eps) cast to the weight's dtype, then
+    times the weight)."""
+    b, s, nd = x.shape
+    return rms_norm(x.reshape(b, s, num_heads, nd // num_heads), weight, eps).reshape(b, s, nd)
+
+
+def cosmos_timestep_proj(timesteps: torch.Tensor, dim: int) -> torch.Tensor:
+    """diffusers Timesteps(dim, flip_sin_to_cos=True, downscale_freq_shift=0) of CosmosEmbedding:
+    f_i = exp(-ln(10000) i / (dim / 2)), cat(cos(t f), sin(t f)), fp32.  [N] -> [N, dim]."""
+    half = dim // 2
+    f = torch.exp(-math.log(10000.0) * torch.arange(half, dtype=torch.float32) / half)
+    a = timesteps.float()[:, None] * f[None, :]
+    return torch.cat([torch.cos(a), torch.sin(a)], dim=-1)
+
+
+def cosmos_time_embed(p: Params, cfg: CosmosConfig, timesteps: torch.Tensor, dtype=torch.float32):
+    """CosmosEmbedding (time_embed; CP:2015-2030 memoises it): the projection cast to the model
+    dtype; temb = linear_2(SiLU(linear_1(proj))) [N, 3C] (the AdaLN-LoRA residual);
+    embedded_timestep = RMSNorm(proj) [N, C]."""
+    pr = cosmos_timestep_proj(timesteps, cfg.hidden).to(dtype)
+    h = silu(F.linear(pr, p["time_embed.t_embedder.linear_1.weight"]))
+    temb = F.linear(h, p["time_embed.t_embedder.linear_2.weight"])
+    et = rms_norm(pr, p["time_embed.norm.weight"], cfg.eps)
+    return temb, et
+
+
+def cosmos_modulation(p: Params, pre: str, et: torch.Tensor, temb: torch.Tensor):
+    """CosmosAdaLayerNormZero's modulation (CP:2091 restates it; fused over all units at
+    CP:2148-2182): linear_2(linear_1(SiLU(e))) + temb, chunked into (shift, scale, gate)."""
+    m = F.linear(F.linear(silu(et), p[pre + "linear_1.weight"]), p[pre + "linear_2.weight"]) + temb
+    return m.chunk(3, dim=-1)
+
+
+def cosmos_attention(p: Params, pre: str, x: torch.Tensor, ctx: Optional[torch.Tensor], cos, sin,
+                     cfg: CosmosConfig, mask: Optional[torch.Tensor] = None,
+                     trace: Optional[dict] = None, tag: str = "") -> torch.Tensor:
+    """CosmosAttnProcessor2_0 (CP:1525-1710 stock path): q = to_q(x), k = to_k(c), v = to_v(c)
+    with c = x (self) or the text (cross); per-head RMSNorm of q and k; rotate-half RoPE on both
+    for self attention; SDPA; to_out.0.  No biases."""
+    c = x if ctx is None else ctx
+    nh = cfg.num_heads
+    q = cosmos_head_rms_norm(F.linear(x, p[pre + "to_q.weight"]), p[pre + "norm_q.weight"], nh, cfg.eps)
+    k = cosmos_head_rms_norm(F.linear(c, p[pre + "to_k.weight"]), p[pre + "norm_k.weight"], nh, cfg.eps)
+    v = F.linear(c, p[pre + "to_v.weight"])
+    if cos is not None:
+        q = cosmos_apply_rope(q, cos, sin, nh)
+        k = cosmos_apply_rope(k, cos, sin, nh)
+    o = flash_attention(q, k, v, nh, mask)
+    if trace is not None:
+        trace.update({f"q{tag}": q, f"k{tag}": k, f"v{tag}": v, f"attn{tag}": o})
+    return F.linear(o, p[pre + "to_out.0.weight"])
+
+
+def cosmos_block(p: Params, cfg: CosmosConfig, idx: int, x: torch.Tensor, ctx: torch.Tensor,
+                 et: torch.Tensor, temb: torch.Tensor, cos, sin, ctx_mask: Optional[torch.Tensor] = None,
+                 trace: Optional[dict] = None) -> torch.Tensor:
+    """CosmosTransformerBlock.forward (CP:1851-1879 restates the stock order): three AdaLN-Zero
+    sub-blocks, each x = x + gate * f(LN(x) (1 + scale) + shift) with its own LoRA modulation,
+    LN without affine at eps 1e-6: self attention (RoPE), cross attention to the text, and the
+    FeedForward net.2(GELU(net.0.proj(h))) with the exact (erf) GELU.  et [B, S, C] and temb
+    [B, S, 3C] per token (the frame's rows expanded, CP:2378-2400).  trace records q / k / v /
+    attn of the self attention (suffix "") and the cross attention ("_x"), and x after each
+    sub-block (x_self, x_cross)."""
+    b = f"transformer_blocks.{idx}."
+
+    def sub(n, x, f):
+        shift, scale, gate = cosmos_modulation(p, b + n + ".", et, temb)
+        h = layer_norm(x, None, None, cfg.eps) * (1 + scale) + shift
+        return x + gate * f(h)
+
+    x = sub("norm1", x, lambda h: cosmos_attention(p, b + "attn1.", h, None, cos, sin, cfg, None, trace, ""))
+    if trace is not None:
+        trace.update(x_self=x)
+    x = sub("norm2", x, lambda h: cosmos_attention(p, b + "attn2.", h, ctx, None, None, cfg, ctx_mask, trace, "_x"))
+    if trace is not None:
+        trace.update(x_cross=x)
+    return sub("norm3", x, lambda h: F.linear(F.gelu(F.linear(h, p[b + "ff.net.0.proj.weight"])),
+                                             p[b + "ff.net.2.weight"]))
+
+
+def cosmos_patch_embed(p: Params, cfg: CosmosConfig, latents: torch.Tensor) -> torch.Tensor:
+    """CosmosPatchEmbed: [B, C, T, H, W] -> (t, h, w)-major tokens of (C, pt, ph, pw) features ->
+    Linear without bias (diffusers; CP:1282).  Returns [B, S, hidden]."""
+    B, C, T, H, W = latents.shape
+    pt, ph, pw = cfg.patch_size
+    x = latents.reshape(B, C, T // pt, pt, H // ph, ph, W // pw, pw).permute(0, 2, 4, 6, 1, 3, 5, 7)
+    x = x.reshape(B, (T // pt) * (H // ph) * (W // pw), C * pt * ph * pw)
+    return F.linear(x, p["patch_embed.proj.weight"])
+
+
+def cosmos_features(p: Params, cfg: CosmosConfig, latents: torch.Tensor, timestep: torch.Tensor,
+                    ctx: torch.Tensor, stop_layer: Optional[int] = None, ctx_mask: Optional[torch.Tensor] = None,
+                    fps: Optional[float] = None, traces: Optional[list] = None) -> torch.Tensor:
+    """CosmosTransformer3DModel.forward up to the output of block stop_layer (CP:2289-2490, the
+    stop_at_layer the reference adds; DB/modules/vlm/Cosmos25.py:150-160 hooks that block):
+    patch embedding, the time embedding of one timestep per latent frame ([B, T], the 5-D
+    timestep of CP:2378-2400, expanded over each frame's tokens), the 3-D RoPE tables, blocks
+    0 .. stop_layer.  latents [B, in_channels, T, H, W]; ctx [B, Lc, text_dim]."""
+    B, _, T, H, W = latents.shape
+    pt, ph, pw = cfg.patch_size
+    t, h, w = T // pt, H // ph, W // pw
+    x = cosmos_patch_embed(p, cfg, latents)
+    ts = timestep.reshape(B, -1).expand(B, t).reshape(-1)
+    temb, et = cosmos_time_embed(p, cfg, ts, x.dtype)
+    temb = temb.reshape(B, t, 1, -1).expand(B, t, h * w, temb.shape[-1]).reshape(B, t * h * w, -1)
+    et = et.reshape(B, t, 1, -1).expand(B, t, h * w, et.shape[-1]).reshape(B, t * h * w, -1)
+    cos, sin = cosmos_rope_tables(cfg, t, h, w, fps)
+    last = cfg.num_layers - 1 if stop_layer is None else stop_layer
+    mask = None if ctx_mask is None else ctx_mask.reshape(B, 1, 1, -1)
+    for i in range(last + 1):
+        tr = {} if traces is not None else None
+        x = cosmos_block(p, cfg, i, x, ctx, et, temb, cos, sin, mask, tr)
+        if traces is not None:
+            traces.append(tr)
+    return x

@@ -131,3 +131,15 @@ def test_d4d_param_shapes_and_init_match_oracle():
     pa = D4.synthetic_params(D4.DiT4DiTHeadConfig(**small), 9)
     pb = O.init_d4d_params(O.DiT4DiTHeadConfig(**small), 9)
     assert sorted(pa) == sorted(pb) and all(torch.equal(pa[k], pb[k]) for k in pa)
+
+
+def test_cosmos_shapes_and_rope_tables_match_oracle():
+    """fam.cosmos's parameter layout and host fp32 RoPE tables equal the oracle's restatement."""
+    from fam import cosmos
+    cfg = cosmos.CosmosConfig(num_layers=3)
+    ocfg = O.CosmosConfig(num_layers=3)
+    assert cosmos.param_shapes(cfg) == O.cosmos_param_shapes(ocfg)
+    for fps in (None, 16.0):
+        c1, s1 = cosmos.cosmos_rope_tables(cfg, 2, 32, 32, fps, "cpu")
+        c2, s2 = O.cosmos_rope_tables(ocfg, 2, 32, 32, fps)
+        assert torch.equal(c1, c2) and torch.equal(s1, s2)

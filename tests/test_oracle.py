@@ -768,3 +768,152 @@ def test_block_branch_metrics_catch_planted_slips(monkeypatch):
     assert cases["rope dropped"][1] < BAR and cases["(h, w) transposed"][1] < BAR
     assert cases["rope dropped"][0]["self_attn"] > 10 * BAR and cases["(h, w) transposed"][0]["self_attn"] > 10 * BAR
     assert cases["self-attention zeroed"][0]["delta"] > BAR
+
+
+# --------------------------------------------------------------------------- Cosmos backbone (config 4)
+def test_cosmos_rope_table_closed_form():
+    """CosmosRotaryPosEmbed (CP = src/dit4dit-geak/patches/diffusers-3996788-transformer_cosmos-geak.patch
+    :1953-1976): head dims 128 split 44 / 42 / 42 over (t, h, w); angle of dim j of the t part =
+    t_pos * theta_t^(-2j/44) with theta_t = 1e4 * s_t^(44/42) (NTK), likewise h and w; the second
+    half repeats the first; temporal positions scale by base_fps / fps."""
+    cfg = O.CosmosConfig()
+    T, H, W = 3, 5, 7
+    cos, sin = O.cosmos_rope_tables(cfg, T, H, W)
+    assert cos.shape == (T * H * W, 128) and cos.dtype == torch.float32
+    assert torch.equal(cos[:, :64], cos[:, 64:]) and torch.equal(sin[:, :64], sin[:, 64:])
+
+    def angle(pos, j, dim, s):
+        theta = 1e4 * s ** (dim / (dim - 2))
+        return pos * theta ** (-2.0 * j / dim)
+    st, sh, sw = cfg.rope_scale
+    for (ti, hi, wi) in [(0, 0, 0), (2, 4, 6), (1, 3, 0)]:
+        r = (ti * H + hi) * W + wi
+        want = [angle(ti, j, 44, st) for j in range(22)] + [angle(hi, j, 42, sh) for j in range(21)] + \
+               [angle(wi, j, 42, sw) for j in range(21)]
+        got = torch.atan2(sin[r, :64].double(), cos[r, :64].double())
+        want = torch.tensor(want, dtype=torch.float64)
+        assert torch.allclose(torch.cos(got - want), torch.ones(64, dtype=torch.float64), atol=1e-6), (ti, hi, wi)
+    c2, s2 = O.cosmos_rope_tables(cfg, T, H, W, fps=12.0)       # t positions doubled (24 / 12)
+    r = (2 * H + 0) * W + 0
+    assert math.isclose(math.atan2(s2[r, 1].item(), c2[r, 1].item()), angle(4, 1, 44, st), abs_tol=1e-5)
+
+
+def test_cosmos_rope_and_head_norm_closed_forms():
+    """apply_rotary_emb(use_real=True, use_real_unbind_dim=-2) rotates the pairs (d, d + D/2) of each
+    head: a 2x2 rotation brute force, pair norms kept; the per-head RMSNorm gives every head unit
+    RMS (weight ones) and one head's scale does not reach the others."""
+    g = torch.Generator().manual_seed(5)
+    B, S, nh, D = 1, 6, 3, 16
+    x = torch.randn(B, S, nh * D, generator=g, dtype=torch.float64)
+    ang = torch.rand(S, D // 2, generator=g, dtype=torch.float64) * 6
+    cos, sin = torch.cat([ang.cos()] * 2, -1), torch.cat([ang.sin()] * 2, -1)
+    y = O.cosmos_apply_rope(x, cos, sin, nh)
+    xh, yh = x.reshape(S, nh, D), y.reshape(S, nh, D)
+    for s_ in range(S):
+        for hh in range(nh):
+            for d in range(D // 2):
+                c, s = ang[s_, d].cos(), ang[s_, d].sin()
+                a, b = xh[s_, hh, d], xh[s_, hh, d + D // 2]
+                assert torch.allclose(yh[s_, hh, d], a * c - b * s) and torch.allclose(yh[s_, hh, d + D // 2], b * c + a * s)
+    assert torch.allclose(xh[..., :D // 2] ** 2 + xh[..., D // 2:] ** 2, yh[..., :D // 2] ** 2 + yh[..., D // 2:] ** 2)
+    n = O.cosmos_head_rms_norm(x, torch.ones(D, dtype=torch.float64), nh, 1e-12).reshape(S, nh, D)
+    assert torch.allclose(n.pow(2).mean(-1), torch.ones(S, nh, dtype=torch.float64))
+    x2 = x.clone().reshape(S, nh, D)
+    x2[:, 1] *= 7.0
+    n2 = O.cosmos_head_rms_norm(x2.reshape(B, S, nh * D), torch.ones(D, dtype=torch.float64), nh, 1e-12).reshape(S, nh, D)
+    assert torch.allclose(n2, n)
+
+
+def _cosmos_tiny():
+    cfg = O.CosmosConfig(hidden=32, num_heads=2, head_dim=16, num_layers=1, in_channels=4, text_dim=12,
+                         adaln_lora_dim=8)
+    p = {k: v.double() for k, v in O.init_cosmos_params(cfg, 61).items()}
+    g = torch.Generator().manual_seed(62)
+    S, C = 6, cfg.hidden
+    x = torch.randn(1, S, C, generator=g, dtype=torch.float64)
+    ctx = torch.randn(1, 5, cfg.text_dim, generator=g, dtype=torch.float64)
+    et = torch.randn(1, S, C, generator=g, dtype=torch.float64)
+    temb = torch.randn(1, S, 3 * C, generator=g, dtype=torch.float64)
+    cos, sin = O.cosmos_rope_tables(cfg, 1, 2, 3)
+    return cfg, p, g, x, ctx, et, temb, cos.double(), sin.double()
+
+
+def _zero(p, *names):
+    q = dict(p)
+    for n in names:
+        q[n] = torch.zeros_like(p[n])
+    return q
+
+
+def test_cosmos_block_self_attention_subblock_closed_form():
+    """The first sub-block of a Cosmos block (CP:1851-1879): with the LoRA up-projection of norm1 zero
+    its modulation is temb, chunked (shift, scale, gate); zero to_q / to_k make the softmax uniform
+    (the per-head RMSNorm of zero is zero), identity to_v / to_out leave the token mean, and zero
+    output projections of the other two sub-blocks make them the identity:
+    y = x + gate * mean_tokens(LN_1e-6(x) (1 + scale) + shift).  Another chunk order fails."""
+    cfg, p, g, x, ctx, et, temb, cos, sin = _cosmos_tiny()
+    C, b = cfg.hidden, "transformer_blocks.0."
+    q = _zero(p, b + "norm1.linear_2.weight", b + "attn1.to_q.weight", b + "attn1.to_k.weight",
+              b + "attn2.to_out.0.weight", b + "ff.net.2.weight")
+    q[b + "attn1.to_v.weight"] = torch.eye(C, dtype=torch.float64)
+    q[b + "attn1.to_out.0.weight"] = torch.eye(C, dtype=torch.float64)
+    y = O.cosmos_block(q, cfg, 0, x, ctx, et, temb, cos, sin)
+    c0, c1, c2 = temb[..., :C], temb[..., C:2 * C], temb[..., 2 * C:]
+
+    def expect(shift, scale, gate):
+        h = _ln(x, 1e-6) * (1 + scale) + shift
+        return x + gate * h.mean(1, keepdim=True)
+    assert torch.allclose(y, expect(c0, c1, c2), atol=1e-9)
+    for order in [(c1, c0, c2), (c0, c2, c1), (c2, c1, c0)]:
+        assert (y - expect(*order)).abs().max() > 0.1
+
+
+def test_cosmos_block_ffn_subblock_and_lora_closed_form():
+    """The FFN sub-block: x + gate3 * net.2(GELU_erf(net.0.proj(LN(x) (1 + scale3) + shift3))) with
+    identity-embedding FFN weights and both attention outputs zero; the modulation is the LoRA
+    linear_2(linear_1(SiLU(e))) + temb (CP:2091): with linear_1 = [I 0] and linear_2 = [I; 0]-like
+    embeddings, the shift picks up SiLU(e)."""
+    cfg, p, g, x, ctx, et, temb, cos, sin = _cosmos_tiny()
+    C, L, b = cfg.hidden, cfg.adaln_lora_dim, "transformer_blocks.0."
+    q = _zero(p, b + "attn1.to_out.0.weight", b + "attn2.to_out.0.weight")
+    q[b + "ff.net.0.proj.weight"] = torch.cat([torch.eye(C, dtype=torch.float64),
+                                               torch.zeros(3 * C, C, dtype=torch.float64)])
+    q[b + "ff.net.2.weight"] = torch.cat([torch.eye(C, dtype=torch.float64),
+                                          torch.zeros(C, 3 * C, dtype=torch.float64)], 1)
+    l1 = torch.zeros(L, C, dtype=torch.float64)
+    l1[:, :L] = torch.eye(L, dtype=torch.float64)            # the first L channels of SiLU(e)
+    l2 = torch.zeros(3 * C, L, dtype=torch.float64)
+    l2[:L, :] = torch.eye(L, dtype=torch.float64)            # into the first L channels of the shift
+    q[b + "norm3.linear_1.weight"], q[b + "norm3.linear_2.weight"] = l1, l2
+    y = O.cosmos_block(q, cfg, 0, x, ctx, et, temb, cos, sin)
+    silu_e = et * torch.sigmoid(et)
+    shift = temb[..., :C].clone()
+    shift[..., :L] += silu_e[..., :L]
+    scale, gate = temb[..., C:2 * C], temb[..., 2 * C:]
+    h = _ln(x, 1e-6) * (1 + scale) + shift
+    gelu = 0.5 * h * (1 + torch.erf(h / math.sqrt(2)))
+    assert torch.allclose(y, x + gate * gelu, atol=1e-9)
+    tanh_gelu = 0.5 * h * (1 + torch.tanh(math.sqrt(2 / math.pi) * (h + 0.044715 * h ** 3)))
+    assert (y - (x + gate * tanh_gelu)).abs().max() > 1e-5
+    shift_nosilu = temb[..., :C].clone()
+    shift_nosilu[..., :L] += et[..., :L]
+    h2 = _ln(x, 1e-6) * (1 + scale) + shift_nosilu
+    assert (y - (x + gate * 0.5 * h2 * (1 + torch.erf(h2 / math.sqrt(2))))).abs().max() > 1e-3
+
+
+def test_cosmos_time_embedding_closed_form():
+    """CosmosEmbedding's Timesteps(C, flip_sin_to_cos=True, downscale_freq_shift=0): cat(cos, sin) with
+    f_i = 10000^(-i / (C/2)) (shift 0: the last frequency is 10000^(-(C/2 - 1)/(C/2)), unlike the DiT4DiT
+    head's shift 1); t = 0 gives (1, 0); embedded_timestep = RMSNorm(proj) has unit RMS with weight 1."""
+    C = 64
+    pr = O.cosmos_timestep_proj(torch.tensor([0.0, 500.0]), C)
+    assert torch.equal(pr[0, :32], torch.ones(32)) and torch.equal(pr[0, 32:], torch.zeros(32))
+    f_last = 10000.0 ** (-(31 / 32))
+    assert math.isclose(pr[1, 31].item(), math.cos(500.0 * f_last), abs_tol=1e-5)
+    assert math.isclose(pr[1, 63].item(), math.sin(500.0 * f_last), abs_tol=1e-5)
+    assert math.isclose(pr[1, 1].item(), math.cos(500.0 * 10000.0 ** (-1 / 32)), abs_tol=1e-4)
+    cfg = O.CosmosConfig(hidden=C, num_heads=2, head_dim=32, num_layers=1)
+    p = {"time_embed.t_embedder.linear_1.weight": torch.randn(C, C), "time_embed.t_embedder.linear_2.weight":
+         torch.randn(3 * C, C), "time_embed.norm.weight": torch.ones(C)}
+    temb, et = O.cosmos_time_embed(p, cfg, torch.tensor([0.0, 500.0]))
+    assert temb.shape == (2, 3 * C) and torch.allclose(et.pow(2).mean(-1), torch.ones(2), atol=1e-5)
