@@ -55,16 +55,19 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-eager", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--no-policy-calls", action="store_true",
+                    help="skip the FastWAM / CAE-FastWAM policy-call figures added to the default line")
     ap.add_argument("--cpu-sample-s", type=float, default=20.0, help="CPU baseline time budget")
-    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "hbm", "prefill", "fastwam"], default="c1",
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "hbm", "prefill", "fastwam", "cae"], default="c1",
                     help="c1: the action-DiT denoise loop (the metric); c2: one long-sequence video DiT block "
                          "(config 2 shape), reported as ms per 30-block forward with MFMA utilisation; c3: the "
-                         "compact expert loop + action-VAE decoder at B=1 and B=256; c4: the DiT4DiT flow-matching "
-                         "head (DiT-B, 16 blocks, 4 steps) over 2048 VLM tokens; hbm: size sweep of the "
+                         "compact expert loop + action-VAE decoder at B=1 and B=256; c4: the DiT4DiT policy call "
+                         "(Cosmos backbone, 28 blocks, + the flow-matching head, 16 blocks, 4 steps); hbm: size sweep of the "
                          "HBM-bound kernels (AdaLN, RMSNorm+RoPE, Euler) from config 2 / config 3 B=256 shapes up; "
                          "prefill: the MoT video K/V prefill of the FastWAM call (30 blocks, 98 video tokens); "
-                         "fastwam: one FastWAM policy call at the real model shape (prefill + 10-step MoT action "
-                         "loop, one graph)")
+                         "fastwam: one FastWAM policy call at the real model shape (VAE encode + prefill + 10-step "
+                         "MoT action loop, one graph); cae: the same call with the CAE-FastWAM action expert "
+                         "(hidden 32) and its action-VAE decoder")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--traffic-from", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
@@ -771,23 +774,42 @@ def _vae_params(dev, g, cfg):
     return out
 
 
-def bench_fastwam(args):
-    """One FastWAM policy call, FastWAM.infer_action (FB/fastwam.py:924-1073), at the reference
-    model's real shape, B=1, one captured graph:
+def _cae_decoder_params(g):
+    """Synthetic CAE action-VAE decoder weights (CAm/action_ae.py:123-166 layout), host fp32."""
+    import torch
+    out = {}
+    for name, shape in sorted({"decoder.input_proj.weight": (128, 16), "decoder.input_proj.bias": (128,),
+                               "decoder.output_proj.weight": (7, 128), "decoder.output_proj.bias": (7,),
+                               "decoder.up.0.weight": (128, 128, 8), "decoder.up.0.bias": (128,),
+                               "decoder.up.1.weight": (128,), "decoder.up.1.bias": (128,),
+                               "decoder.up.3.net.0.weight": (128, 128, 3), "decoder.up.3.net.0.bias": (128,),
+                               "decoder.up.3.net.1.weight": (128,), "decoder.up.3.net.1.bias": (128,),
+                               "decoder.up.3.net.3.weight": (128, 128, 3), "decoder.up.3.net.3.bias": (128,),
+                               "decoder.up.3.net.4.weight": (128,), "decoder.up.3.net.4.bias": (128,)}.items()):
+        out[name] = torch.randn(shape, generator=g) * (0.05 if len(shape) > 1 else 0.02)
+    return out
+
+
+def _mot_policy_call(args, cae: bool):
+    """One FastWAM.infer_action policy call at the real model shape, B=1, one captured graph:
       1. the Wan2.2 VAE38 encode of the first frame (224 x 448 image -> 48 x 14 x 28 latent,
          FB/fastwam.py:980 -> :256-268);
       2. the video expert's pre_dit of that latent frame at t = 0 (7 x 14 patches = 98 tokens,
          129 context tokens of width 4096) and the MoT K/V prefill through its 30 blocks (hidden
          3072, 24 x 128 heads, FFN 14336; FB/fastwam.py:1018-1041);
-      3. the 10-step flow-matching loop of the action expert (30 blocks, hidden 1024, attention
-         24 x 128 = 3072 wide, FFN 4096, 32 x 7 chunk) whose self-attention runs over [that
-         layer's cached video K/V ; action K/V] (Sk = 130, every key attended, as infer_action's
-         mask), cross-attending to the same 129 context tokens.
+      3. the 10-step flow-matching loop of the action expert (30 blocks, attention 24 x 128 = 3072
+         wide) whose self-attention runs over [that layer's cached video K/V ; action K/V] (every
+         key attended, as infer_action's mask), cross-attending to the same 129 context tokens:
+         FastWAM's expert has hidden 1024, FFN 4096 and a 32 x 7 chunk; the CAE-FastWAM expert
+         (cae=True, FastWAM/configs/model/fastwam_32hdim_latent_b4_joint.yaml:36-46, the loop
+         CA/fastwam.py:1081-1274) hidden 32, FFN 256 and an 8 x 16 latent chunk,
+      4. (CAE only) the action-VAE decode of the latent chunk to 32 x 7 (CAm/action_ae.py:123-166).
     The latent is read by pre_dit through one device copy; the prefill's K/V buffers are read in
     place by the loop.  (The text encoder and the proprio encoder run before the call and are
-    outside the reference's timed loop too.)"""
+    outside the reference's timed loop too.)  Returns the result dict (not printed)."""
     import torch
     from fam.action_dit import ActionDiTConfig, FusedActionDiT
+    from fam.cae import CaeDecoder
     from fam.vae import FusedWanVAEEncoder, WanVaeConfig
     from fam.video_dit import FusedWanVideoDiT, WanVideoConfig
     dev = torch.device("cuda:0")
@@ -797,25 +819,31 @@ def bench_fastwam(args):
     vcfg = WanVaeConfig()
     vae = FusedWanVAEEncoder(vcfg, _vae_params(dev, g, vcfg), height=IH, width=IW, device=dev)
     wcfg = WanVideoConfig(hidden_dim=H, in_dim=48, ffn_dim=F, out_dim=48, text_dim=T, freq_dim=256, eps=1e-6,
-                   patch_size=(1, 2, 2), num_heads=nh, attn_head_dim=Dh, num_layers=L)
+                          patch_size=(1, 2, 2), num_heads=nh, attn_head_dim=Dh, num_layers=L)
     lh, lw = vae.latent_hw
     video = FusedWanVideoDiT(wcfg, _wan_params(dev, g, wcfg), batch=1, frames=1, height=lh, width=lw, ctx_len=Lc,
                              mode="prefill", device=dev)
     torch.cuda.empty_cache()
     Sv = video.S
-    acfg = ActionDiTConfig(hidden_dim=1024, action_dim=7, ffn_dim=4096, text_dim=T, freq_dim=256, num_heads=nh,
+    ah, ad, af, S = (32, 16, 256, 8) if cae else (1024, 7, 4096, 32)
+    acfg = ActionDiTConfig(hidden_dim=ah, action_dim=ad, ffn_dim=af, text_dim=T, freq_dim=256, num_heads=nh,
                            attn_head_dim=Dh, num_layers=L)
-    ap = _block_params(dev, g, L, 1024, nh * Dh, 4096, text_dim=T, action_dim=7)
-    am = FusedActionDiT(acfg, ap, batch=1, seq_len=32, ctx_len=Lc, num_steps=10, shift=5.0, device=dev,
+    ap = _block_params(dev, g, L, ah, nh * Dh, af, text_dim=T, action_dim=ad)
+    am = FusedActionDiT(acfg, ap, batch=1, seq_len=S, ctx_len=Lc, num_steps=10, shift=5.0, device=dev,
                         video_len=Sv, video_kv=video.kv_cache())
     del ap
     torch.cuda.empty_cache()
     gi = torch.Generator("cpu").manual_seed(99)
+    dec = None
+    if cae:
+        dec = CaeDecoder(_cae_decoder_params(gi), latent_dim=16, num_tokens=8, action_horizon=32, action_dim=7,
+                         decoder_hidden=128, batch=1, device=dev)
+        dec.d.z = am.latents.data_ptr()   # the decoder reads the loop's fp32 latents in place
     image = torch.rand(1, 3, IH, IW, generator=gi) * 2 - 1
     ctx = torch.randn(1, Lc, T, generator=gi).to(dev, torch.bfloat16)
     vae.set_input(image.to(dev))
     video.set_inputs(torch.zeros(1, 48, 1, lh, lw, dtype=torch.bfloat16, device=dev), torch.zeros(1), ctx)
-    am.set_inputs(torch.randn(1, 32, 7, generator=gi).to(dev, torch.bfloat16), ctx[0])
+    am.set_inputs(torch.randn(1, S, ad, generator=gi).to(dev, torch.bfloat16), ctx[0])
     latent_in = video.x_in
 
     def eager(stream):
@@ -825,6 +853,8 @@ def bench_fastwam(args):
         for f in video.steps:
             f(stream)
         am.plan.run(stream)
+        if dec is not None:
+            dec.launch(stream)
     s = torch.cuda.Stream(dev)
     s.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(s):
@@ -842,30 +872,49 @@ def bench_fastwam(args):
     pf_p50, _, _ = _time_calls(video.run, args.steps, args.warmup)
     am.capture()
     loop_p50, _, _ = _time_calls(am.run, args.steps, args.warmup)
-    launches = vae.num_launches + 1 + video.num_launches + am.num_launches
-    out = {
-        "metric": "p50 ms per FastWAM policy call at the real model shape (first-frame VAE encode + video pre_dit "
-                  "and K/V prefill + 10-step action loop, bs=1)", "value": round(p50, 4), "unit": "ms", "n_gpus": 1,
+    launches = vae.num_launches + 1 + video.num_launches + am.num_launches + (4 if cae else 0)
+    name = "CAE-FastWAM" if cae else "FastWAM"
+    expert = ("CAE action expert (30 blocks, hidden 32, 24x128 heads, FFN 256, 8x16 latent, joint attention over "
+              "98 cached video + 8 action keys) + action-VAE decode to 32x7") if cae else \
+        ("action expert (30 blocks, hidden 1024, 24x128 heads, FFN 4096, 32 action tokens, joint attention over 98 "
+         "cached video + 32 action keys)")
+    published = {"ms": 12.82, "source": "docs/cae-fastwam-libero.md:34 (CAE-FastWAM + GEAK, 10 steps, one MI355X)"} \
+        if cae else {"ms": 24.17, "source": "docs/fastwam-geak-inference-optimization.md:25 (FastWAM + GEAK, 10 steps, "
+                                           "one MI355X)"}
+    return {
+        "metric": f"p50 ms per {name} policy call at the real model shape (first-frame VAE encode + video pre_dit "
+                  "and K/V prefill + 10-step action loop" + (" + action-VAE decode" if cae else "") + ", bs=1)",
+        "value": round(p50, 4), "unit": "ms", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(p50, 4), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: seeded uniform image, N(0,1) context/noise, N(0,0.02) DiT weights, unit-scale VAE "
                 "convolutions, norm affines N(1,0.2)",
-        "config": {"workload": "FastWAM infer_action: Wan2.2 VAE38 encode of a 224x448 first frame (-> 48x14x28), "
+        "config": {"workload": f"{name} infer_action: Wan2.2 VAE38 encode of a 224x448 first frame (-> 48x14x28), "
                                "video pre_dit at t=0 + MoT K/V prefill (30 blocks, hidden 3072, 24x128 heads, FFN "
                                "14336, 98 video tokens, 3-D RoPE, 129 context tokens of width 4096) + 10 Euler steps "
-                               "of the action expert (30 blocks, hidden 1024, 24x128 heads, FFN 4096, 32 action "
-                               "tokens, joint attention over 98 cached video + 32 action keys)", "batch": 1,
-                   "image": [IH, IW], "video_tokens": Sv, "action_tokens": 32, "context_tokens": Lc,
+                               f"of the {expert}", "batch": 1,
+                   "image": [IH, IW], "video_tokens": Sv, "action_tokens": S, "context_tokens": Lc,
                    "denoise_steps": 10, "blocks": L},
         "min_ms": round(mn, 4), "p90_ms": round(p90, 4), "launches_per_call": launches,
         "vae_encode_p50_ms": round(vae_p50, 4), "prefill_p50_ms": round(pf_p50, 4),
         "action_loop_p50_ms": round(loop_p50, 4), "action_step_ms": round(loop_p50 / 10, 4),
-        "reference_anchors_unpublished": {
-            "note": "GEAK campaign figures quoted in the reference's source comments, not published results",
-            "prefill_ms": 6.02, "prefill_source": "FG/wan_video_dit.py:973-974",
-            "denoise_step_ms": 2.14, "denoise_step_source": "FG/wan_video_dit.py:51-52"},
+        "published_reference_ms": published,
     }
+
+
+def bench_fastwam(args):
+    """FastWAM.infer_action at the real model shape (see _mot_policy_call)."""
+    out = _mot_policy_call(args, cae=False)
+    out["reference_anchors_unpublished"] = {
+        "note": "GEAK campaign figures quoted in the reference's source comments, not published results",
+        "prefill_ms": 6.02, "prefill_source": "FG/wan_video_dit.py:973-974",
+        "denoise_step_ms": 2.14, "denoise_step_source": "FG/wan_video_dit.py:51-52"}
     print(json.dumps(out), flush=True)
+
+
+def bench_cae(args):
+    """CAE-FastWAM's infer_action at the real model shape (see _mot_policy_call)."""
+    print(json.dumps(_mot_policy_call(args, cae=True)), flush=True)
 
 
 def bench_prefill(args):
@@ -931,16 +980,7 @@ def bench_c3(args):
                           attn_head_dim=8, num_layers=8)
     params = synthetic_params(cfg, 4321)
     g = torch.Generator("cpu").manual_seed(99)
-    dec_params = {}
-    for name, shape in sorted({"decoder.input_proj.weight": (128, 16), "decoder.input_proj.bias": (128,),
-                               "decoder.output_proj.weight": (7, 128), "decoder.output_proj.bias": (7,),
-                               "decoder.up.0.weight": (128, 128, 8), "decoder.up.0.bias": (128,),
-                               "decoder.up.1.weight": (128,), "decoder.up.1.bias": (128,),
-                               "decoder.up.3.net.0.weight": (128, 128, 3), "decoder.up.3.net.0.bias": (128,),
-                               "decoder.up.3.net.1.weight": (128,), "decoder.up.3.net.1.bias": (128,),
-                               "decoder.up.3.net.3.weight": (128, 128, 3), "decoder.up.3.net.3.bias": (128,),
-                               "decoder.up.3.net.4.weight": (128,), "decoder.up.3.net.4.bias": (128,)}.items()):
-        dec_params[name] = torch.randn(shape, generator=g) * (0.05 if len(shape) > 1 else 0.02)
+    dec_params = _cae_decoder_params(g)
     dev = torch.device("cuda:0")
     ctx = torch.randn(1, 1560, 1024, generator=g).to(dev, torch.bfloat16)
     res = {}
@@ -1021,6 +1061,9 @@ def main():
     if args.workload == "fastwam":
         bench_fastwam(args)
         return
+    if args.workload == "cae":
+        bench_cae(args)
+        return
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     cfg, shape = workload(args.batch)
@@ -1079,6 +1122,22 @@ def main():
         log("eager GPU reference sequence")
         out["eager_gpu_baseline"] = eager_gpu_baseline(cfg, params, noise, ctx)
         out["speedup_vs_eager_gpu"] = round(out["eager_gpu_baseline"]["p50_ms"] / p50, 2)
+
+    if not args.no_policy_calls:
+        # the reference's two published whole-policy latencies on one MI355X, measured on the same
+        # box after the config-1 figure: FastWAM and CAE-FastWAM infer_action at their real shapes
+        del model
+        torch.cuda.empty_cache()
+        for key, cae in (("fastwam_policy_call", False), ("cae_fastwam_policy_call", True)):
+            log(f"{key}: building and timing")
+            r = _mot_policy_call(args, cae=cae)
+            pub = r["published_reference_ms"]
+            out[key] = {"metric": r["metric"], "p50_ms": r["value"], "min_ms": r["min_ms"], "p90_ms": r["p90_ms"],
+                        "vae_encode_p50_ms": r["vae_encode_p50_ms"], "prefill_p50_ms": r["prefill_p50_ms"],
+                        "action_loop_p50_ms": r["action_loop_p50_ms"], "launches_per_call": r["launches_per_call"],
+                        "published_reference_ms": pub["ms"], "published_source": pub["source"],
+                        "ratio_published_over_ours": round(pub["ms"] / r["value"], 4)}
+            torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle) on host cores")

@@ -122,8 +122,15 @@ def test_tiny_golden_config_through_fused_model():
     y = m.infer(gold["loop.in.noise"].to(torch.bfloat16).cuda(),
                 gold["in.context"][:1].to(torch.bfloat16).cuda()).float().cpu()
     ref = gold["loop.out.fp32"]
-    print(f"tiny golden loop max|d| {(y - ref).abs().max().item():.3e}")
-    assert (y - ref).abs().max().item() <= 3e-2
+    ref_bf16 = gold["loop.out.bf16"]
+    d32, d16 = (y - ref).abs().max().item(), (y - ref_bf16).abs().max().item()
+    # the fused loop carries the chunk in fp32 between steps; the reference's bf16 loop rounds
+    # it twice per step (SCH:82-88): its own bf16 and fp32 outputs differ by about 1.2e-2
+    own = (ref_bf16 - ref).abs().max().item()
+    print(f"tiny golden loop max|d| vs the reference's fp32 loop {d32:.3e}, vs its bf16 loop {d16:.3e} "
+          f"(reference bf16 vs fp32: {own:.3e})")
+    assert d32 <= 3e-2
+    assert d16 <= own + 3e-2
 
 
 @pytest.mark.parametrize("tokens_per_frame,heads,head_dim", [(98, 12, 64), (49, 12, 64), (98, 16, 64), (49, 8, 128)])
@@ -163,6 +170,45 @@ def test_mot_loop_over_video_prefix(tokens_per_frame, heads, head_dim):
         x_lat = x_lat + O.linear(x, p32["head.weight"], p32["head.bias"]) * d
     dd = (y - x_lat).abs()
     print(f"MoT loop: max|d| {dd.max().item():.3e} mean|d| {dd.mean().item():.3e}")
+    assert dd.max().item() <= 1e-2
+
+
+def test_cae_fastwam_action_expert_real_shape():
+    """The CAE-FastWAM action expert at its real shape (FastWAM/configs/model/
+    fastwam_32hdim_latent_b4_joint.yaml:36-46): hidden 32, FFN 256, 24 x 128 attention (3072 wide),
+    30 blocks, an 8 x 16 latent chunk, text context 129 x 4096; the MoT joint self-attention over
+    each layer's cached 98 video tokens + the 8 action tokens (every key attended, as
+    infer_action's mask), 10 Euler steps with shift 5 (CA/fastwam.py:1081-1274)."""
+    Cfg, Model = _model_cls()
+    cfg = Cfg(hidden_dim=32, action_dim=16, ffn_dim=256, text_dim=4096, freq_dim=256, num_heads=24,
+              attn_head_dim=128, num_layers=30)
+    S, Sv, Lc, steps = 8, 98, 129, 10
+    A = cfg.num_heads * cfg.attn_head_dim
+    p = _params(cfg, 61)
+    g = torch.Generator().manual_seed(62)
+    noise = torch.randn(1, S, 16, generator=g).to(torch.bfloat16)
+    ctx = torch.randn(1, Lc, 4096, generator=g).to(torch.bfloat16)
+    vks = [torch.randn(1, Sv, A, generator=g).to(torch.bfloat16) for _ in range(cfg.num_layers)]
+    vvs = [torch.randn(1, Sv, A, generator=g).to(torch.bfloat16) for _ in range(cfg.num_layers)]
+    m = Model(cfg, p, batch=1, seq_len=S, ctx_len=Lc, num_steps=steps, shift=5.0, video_len=Sv)
+    m.set_video_kv([k.cuda() for k in vks], [v.cuda() for v in vvs])
+    y = m.infer(noise.cuda(), ctx.cuda()).float().cpu()
+    p32 = {k: v.float() for k, v in p.items()}
+    ocfg = O.ActionDiTConfig(**cfg.to_dict())
+    ts, ds = O.build_inference_schedule(steps, 5.0, torch.bfloat16)
+    ctx_emb = O.text_embedding(p32, ctx.float())
+    freqs = O.action_freqs(cfg.attn_head_dim, S)
+    vkv = [(k.float(), v.float()) for k, v in zip(vks, vvs)]
+    joint = torch.ones(Sv + S, Sv + S, dtype=torch.bool)
+    x_lat = noise.float()
+    for t, d in zip(ts.float(), ds.float()):
+        _, t_mod = O.time_mlp(p32, ocfg, t.reshape(1))
+        x = O.linear(x_lat, p32["action_encoder.weight"], p32["action_encoder.bias"])
+        x = O.mot_action_forward(p32, ocfg, x, freqs, t_mod, ctx_emb, vkv, joint, Sv)
+        x_lat = x_lat + O.linear(x, p32["head.weight"], p32["head.bias"]) * d
+    dd = (y - x_lat).abs()
+    print(f"CAE-FastWAM expert (30 blocks, hidden 32, 24x128 heads, 10 steps): max|d| {dd.max().item():.3e} "
+          f"mean|d| {dd.mean().item():.3e}, {m.num_launches} launches")
     assert dd.max().item() <= 1e-2
 
 
