@@ -114,6 +114,27 @@ class CaeDesc(C.Structure):
     ]
 
 
+class TinyDesc(C.Structure):
+    """fam_tiny_desc (include/fam_hip.h)."""
+    _fields_ = [
+        ("batch", C.c_int32), ("seq", C.c_int32), ("hidden", C.c_int32), ("heads", C.c_int32),
+        ("head_dim", C.c_int32), ("ffn", C.c_int32), ("action_dim", C.c_int32), ("layers", C.c_int32),
+        ("steps", C.c_int32), ("video_len", C.c_int32), ("ctx_len", C.c_int32), ("slice", C.c_int32),
+        ("eps", C.c_float), ("scale", C.c_float),
+        ("noise", _vp), ("mods", _vp), ("deltas", _vp),
+        ("rope_cos", _vp), ("rope_sin", _vp),
+        ("ctxkv", _vp), ("ctx_ld", _i64),
+        ("video_k", _vp), ("video_v", _vp), ("video_bs", _i64), ("video_rs", _i64),
+        ("video_mask", _vp), ("mask_rs", _i64),
+        ("enc_w", _vp), ("enc_b", _vp), ("head_w", _vp), ("head_b", _vp),
+        ("qkv_w", _vp), ("qkv_b", _vp), ("nq_w", _vp), ("nk_w", _vp), ("o_w", _vp), ("o_b", _vp),
+        ("n3_w", _vp), ("n3_b", _vp), ("cq_w", _vp), ("cq_b", _vp), ("cnq_w", _vp),
+        ("co_w", _vp), ("co_b", _vp), ("ff0_w", _vp), ("ff0_b", _vp), ("ff2_w", _vp), ("ff2_b", _vp),
+        ("gram", _vp), ("gram_c", _vp), ("gram_b", _vp),
+        ("lat", _vp), ("xa", _vp), ("xb", _vp), ("part_s", _vp), ("part_c", _vp), ("out", _vp),
+    ]
+
+
 SIGNATURES = {
     "fam_version": (C.c_int, []),
     "fam_last_error": (C.c_char_p, []),
@@ -132,6 +153,7 @@ SIGNATURES = {
     "fam_attention_noalloc_max_bytes": (_i64, []),
     "fam_gemm_partial": (C.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "fam_cae_decode": (C.c_int, [C.POINTER(CaeDesc), _vp]),
+    "fam_tiny_expert": (C.c_int, [C.POINTER(TinyDesc), _i64, _i64, _vp]),
     "fam_gemm_final": (C.c_int, [_vp, _i64, _vp, _i64, _vp, C.c_int, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "fam_gemm_partial_splits": (C.c_int, [_i64, _i64, _i64]),
     "fam_rowop": (C.c_int, [C.POINTER(RowopDesc), _vp]),

@@ -186,11 +186,16 @@ class FusedActionDiT:
             stride, any row / batch stride) that the joint attention reads in place, e.g. the
             video prefill's cache (FusedVideoPrefill.kv_cache()); then no static copy exists and
             set_video_kv is not needed.  The views must stay valid while this model runs.
+        tiny: run the blocks through fam_tiny_expert (two launches per block step; hidden 32
+            only).  None (default) picks it whenever the library covers the shape.
+        tiny_slice: the attention columns per workgroup of fam_tiny_expert (0: the library's
+            choice, 128 or all A columns when A <= 128).
     """
 
     def __init__(self, cfg: ActionDiTConfig, params: Dict[str, torch.Tensor], *, batch: int, seq_len: int,
                  ctx_len: int, num_steps: int, shift: float = 5.0, device="cuda", mode: str = "denoise",
-                 video_len: int = 0, video_mask: Optional[torch.Tensor] = None, video_kv=None):
+                 video_len: int = 0, video_mask: Optional[torch.Tensor] = None, video_kv=None,
+                 tiny: Optional[bool] = None, tiny_slice: int = 0):
         if mode not in ("denoise", "forward"):
             raise ValueError(f"mode must be 'denoise' or 'forward', got {mode!r}")
         if mode == "forward" and num_steps != 1:
@@ -200,6 +205,8 @@ class FusedActionDiT:
         self.B, self.S, self.Lc, self.T = batch, seq_len, ctx_len, num_steps
         self.shift = shift
         self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
         self.lib = _capi.load()
         H, A, Fd, L = cfg.hidden_dim, cfg.attn_dim, cfg.ffn_dim, cfg.num_layers
         dev = self.device
@@ -314,6 +321,12 @@ class FusedActionDiT:
         self.apart_ml = torch.zeros(self.kv_splits * nq * 2, dtype=torch.float32, device=dev)
 
         self._descs: list = []   # keeps ctypes descriptors alive
+        self.tiny = None
+        if mode == "denoise" and tiny is not False:
+            self.tiny = self._tiny_setup(params, tiny_slice)
+            if self.tiny is None and tiny:
+                raise ValueError("tiny=True but fam_tiny_expert does not cover this shape: "
+                                 + self.lib.fam_last_error().decode(errors="replace"))
         self.plan = self._build_plan()
         self.graph: Optional[torch.cuda.CUDAGraph] = None
 
@@ -513,6 +526,125 @@ class FusedActionDiT:
         self._launch(name, "fam_attention", C.byref(d), "attention", nbytes,
                      4 * self.B * cfg.num_heads * S * (Sv + S) * Dh)
 
+    # ------------------------------------------------------------------ tiny-hidden path
+    def _tiny_setup(self, params: Dict[str, torch.Tensor], slice_: int):
+        """Layer-major weight stacks, the Gram matrices of the q / k / cross-q projections and
+        the state buffers of fam_tiny_expert; None when the library does not cover the shape
+        (checked with an empty phase range, which validates without launching)."""
+        cfg, dev = self.cfg, self.device
+        H, A, Fd, L, Dh = cfg.hidden_dim, cfg.attn_dim, cfg.ffn_dim, cfg.num_layers, cfg.attn_head_dim
+        B, S, T = self.B, self.S, self.T
+        if H != 32:
+            return None
+        W = slice_ if slice_ > 0 else (A if A <= 128 else 128)
+        if W <= 0 or A % W:
+            return None
+        G = A // W
+
+        def stack(fmt):
+            return torch.stack([params[fmt.format(i)].to(torch.float32) for i in range(L)]).to(
+                device=dev, dtype=_BF16).contiguous()
+
+        tw = {}
+        tw["qkv_w"] = torch.stack([torch.cat([params[f"blocks.{i}.self_attn.{n}.weight"].to(torch.float32)
+                                              for n in "qkv"]) for i in range(L)]).to(device=dev, dtype=_BF16).contiguous()
+        tw["qkv_b"] = torch.stack([torch.cat([params[f"blocks.{i}.self_attn.{n}.bias"].to(torch.float32)
+                                              for n in "qkv"]) for i in range(L)]).to(device=dev, dtype=_BF16).contiguous()
+        for key, fmt in (("nq_w", "blocks.{}.self_attn.norm_q.weight"), ("nk_w", "blocks.{}.self_attn.norm_k.weight"),
+                         ("o_w", "blocks.{}.self_attn.o.weight"), ("o_b", "blocks.{}.self_attn.o.bias"),
+                         ("n3_w", "blocks.{}.norm3.weight"), ("n3_b", "blocks.{}.norm3.bias"),
+                         ("cq_w", "blocks.{}.cross_attn.q.weight"), ("cq_b", "blocks.{}.cross_attn.q.bias"),
+                         ("cnq_w", "blocks.{}.cross_attn.norm_q.weight"), ("co_w", "blocks.{}.cross_attn.o.weight"),
+                         ("co_b", "blocks.{}.cross_attn.o.bias"), ("ff0_w", "blocks.{}.ffn.0.weight"),
+                         ("ff0_b", "blocks.{}.ffn.0.bias"), ("ff2_w", "blocks.{}.ffn.2.weight"),
+                         ("ff2_b", "blocks.{}.ffn.2.bias")):
+            tw[key] = stack(fmt)
+        # sum_j q_j^2 = h G h + 2 h.c + beta for q = h Wq^T + bq, from the bf16 weights in fp64:
+        # G = Wq^T Wq as hi + lo bf16 parts, c = Wq^T bq, beta = |bq|^2 (self q, self k, cross q)
+        gram = torch.zeros(L, 3, 2, H, H, dtype=_BF16)
+        gc = torch.zeros(L, 3, H, dtype=torch.float32)
+        gb = torch.zeros(L, 3, dtype=torch.float32)
+        qkw, qkb = tw["qkv_w"].cpu().double(), tw["qkv_b"].cpu().double()
+        cqw, cqb = tw["cq_w"].cpu().double(), tw["cq_b"].cpu().double()
+        for l in range(L):
+            for j, (wm, bv) in enumerate(((qkw[l, :A], qkb[l, :A]), (qkw[l, A:2 * A], qkb[l, A:2 * A]),
+                                          (cqw[l], cqb[l]))):
+                g = wm.t() @ wm
+                hi = g.to(_BF16)
+                gram[l, j, 0], gram[l, j, 1] = hi, (g - hi.double()).to(_BF16)
+                gc[l, j] = (wm.t() @ bv).float()
+                gb[l, j] = float(bv @ bv)
+        tw["gram"], tw["gram_c"], tw["gram_b"] = gram.to(dev), gc.to(dev), gb.to(dev)
+        tw["nk_stack"] = stack("blocks.{}.cross_attn.norm_k.weight")
+        # state
+        f32 = dict(dtype=torch.float32, device=dev)
+        tw["lat"] = torch.zeros(2, B, S, cfg.action_dim, **f32)
+        tw["xa"] = torch.zeros(B, S, H, **f32)
+        tw["xb"] = torch.zeros(B, S, H, **f32)
+        tw["part_s"] = torch.zeros(B, G, S, H, **f32)
+        tw["part_c"] = torch.zeros(B, G, S, H, **f32)
+        d = _capi.TinyDesc()
+        d.batch, d.seq, d.hidden, d.heads, d.head_dim = B, S, H, cfg.num_heads, Dh
+        d.ffn, d.action_dim, d.layers, d.steps = Fd, cfg.action_dim, L, T
+        d.video_len, d.ctx_len, d.slice = self.Sv, self.Lc, W
+        d.eps, d.scale = float(cfg.eps), 1.0 / math.sqrt(Dh)
+        d.noise, d.mods, d.deltas = self.noise_in.data_ptr(), self.mods.data_ptr(), self.deltas.data_ptr()
+        d.rope_cos, d.rope_sin = self.rope_cos.data_ptr(), self.rope_sin.data_ptr()
+        d.ctxkv, d.ctx_ld = self.ctxkv.data_ptr(), L * 2 * A
+        if self.Sv > 0:
+            kvs = (self.video_kv if self.video_kv is not None else
+                   [(self.video_k[l], self.video_v[l]) for l in range(L)])
+            bs, rs = kvs[0][0].stride(0), kvs[0][0].stride(1)
+            if any(t_.stride(0) != bs or t_.stride(1) != rs for kv in kvs for t_ in kv):
+                return None
+            tw["vk_tab"] = torch.tensor([kv[0].data_ptr() for kv in kvs], dtype=torch.int64, device=dev)
+            tw["vv_tab"] = torch.tensor([kv[1].data_ptr() for kv in kvs], dtype=torch.int64, device=dev)
+            d.video_k, d.video_v = tw["vk_tab"].data_ptr(), tw["vv_tab"].data_ptr()
+            d.video_bs, d.video_rs = bs, rs
+            if self.video_mask is not None:
+                d.video_mask, d.mask_rs = self.video_mask.data_ptr(), self.Sv + S
+        w = self.w
+        d.enc_w, d.enc_b, d.head_w, d.head_b = (w["enc_w"].data_ptr(), w["enc_b"].data_ptr(), w["head_w"].data_ptr(),
+                                                w["head_b"].data_ptr())
+        for key in ("qkv_w", "qkv_b", "nq_w", "nk_w", "o_w", "o_b", "n3_w", "n3_b", "cq_w", "cq_b", "cnq_w", "co_w",
+                    "co_b", "ff0_w", "ff0_b", "ff2_w", "ff2_b", "gram", "gram_c", "gram_b", "lat", "xa", "xb",
+                    "part_s", "part_c"):
+            setattr(d, key, tw[key].data_ptr())
+        d.out = self.latents.data_ptr()
+        if self.lib.fam_tiny_expert(C.byref(d), 0, 0, None) != 0:
+            return None
+        tw["desc"] = d
+        tw["G"] = G
+        return tw
+
+    def _tiny_plan(self, plan: _Plan) -> None:
+        """The blocks, head and Euler updates of every step as fam_tiny_expert phases: per block
+        step a self phase and a cross phase, then the final phase (last FFN, head, last update)."""
+        cfg, tw = self.cfg, self.tiny
+        H, A, L, T, S, B = cfg.hidden_dim, cfg.attn_dim, cfg.num_layers, self.T, self.S, self.B
+        G, Sv, Lc, Fd = tw["G"], self.Sv, self.Lc, cfg.ffn_dim
+        ref = C.byref(tw["desc"])
+        f, lib = self.lib.fam_tiny_expert, self.lib
+        rows = B * S
+
+        def phase(p):
+            def run(stream):
+                rc = f(ref, p, p + 1, stream)
+                if rc != 0:
+                    raise FamError(f"fam_tiny_expert[{p}]", rc, lib.fam_last_error().decode(errors="replace"))
+            return run
+        # algorithmic bytes: the weights a phase streams once (bf16), the K/V it reads, the partials
+        w_self = 2 * (3 * A * H + 2 * A + H * A) + 2 * (2 * Fd * H)
+        w_cross = 2 * (A * H + A + H * A)
+        for t in range(T):
+            for l in range(L):
+                p = 2 * (t * L + l)
+                plan.add(f"s{t}.b{l}.tiny_self", phase(p), "tiny_self",
+                         w_self + 2 * 2 * B * Sv * A + 4 * 2 * G * rows * H, 4 * B * cfg.num_heads * S * (Sv + S) * cfg.attn_head_dim)
+                plan.add(f"s{t}.b{l}.tiny_cross", phase(p + 1), "tiny_cross",
+                         w_cross + 2 * 2 * Lc * A + 4 * 2 * G * rows * H, 4 * B * cfg.num_heads * S * Lc * cfg.attn_head_dim)
+        plan.add("tiny_final", phase(2 * L * T), "tiny_final", 2 * (2 * Fd * H) + 4 * G * rows * H)
+
     def set_video_kv(self, keys, values) -> None:
         """Copy the per-layer cached video K/V (each [B, Sv, A] or [Sv, A], already normalised
         and rotated as the video expert's prefill leaves them) into the static buffers."""
@@ -534,7 +666,8 @@ class FusedActionDiT:
         eps = float(cfg.eps)
 
         # -- input copy and per-call prologue
-        plan.add("latents<-noise", lambda s: self.latents.copy_(self.noise_in), "copy", 4 * self.latents.numel())
+        if self.tiny is None:
+            plan.add("latents<-noise", lambda s: self.latents.copy_(self.noise_in), "copy", 4 * self.latents.numel())
         plan.add("sinusoid", _checked(lib, "fam_sinusoid", self.timesteps.data_ptr(), self.t_emb.data_ptr(), T,
                                       cfg.freq_dim), "sinusoid", 2 * T * (1 + cfg.freq_dim))
         self._gemm("time_emb0", self.t_emb, w["te0_w"], w["te0_b"], self.t1, act=_capi.FAM_ACT_SILU)
@@ -547,11 +680,13 @@ class FusedActionDiT:
         self._gemm("ctx_emb2", self.ctx_h, w["txt2_w"], w["txt2_b"], self.ctx_emb)
         self._gemm("ctx_kv", self.ctx_emb, w["ctxkv_w"], w["ctxkv_b"], self.ctxkv)
         kvp = self.ctxkv.data_ptr()
-        for l in range(L):
-            plan.add(f"ctx_knorm{l}", _checked(lib, "fam_rmsnorm_rope", kvp + 2 * (l * 2 * A), L * 2 * A,
-                                               kvp + 2 * (l * 2 * A), L * 2 * A, Lc, 1, A,
-                                               w[f"ca_nk_w{l}"].data_ptr(), eps, None, None, 0, 0, 0),
-                     "rmsnorm_rope", 2 * (2 * Lc * A + A))
+        # RMSNorm of every block's context keys in one launch: row (i, l) = ctxkv[i, 2 A l ..]
+        w["nk_stack"] = torch.stack([w[f"ca_nk_w{l}"] for l in range(L)]).contiguous()
+        plan.add("ctx_knorm", _checked(lib, "fam_rmsnorm_grouped", kvp, 2 * A, kvp, 2 * A, Lc * L, A,
+                                       w["nk_stack"].data_ptr(), L, eps), "rmsnorm_rope", 2 * (2 * Lc * L * A + L * A))
+        if self.tiny is not None:
+            self._tiny_plan(plan)
+            return plan
 
         lat = self.latents.view(M, cfg.action_dim)
         x, qkv, attn, qc, hid, h = self.x, self.qkv, self.attn, self.qc, self.hid, self.h

@@ -585,6 +585,71 @@ typedef struct fam_cae_desc {
 
 int fam_cae_decode(const fam_cae_desc* d, void* stream);
 
+/*
+ * fam_tiny_expert -- the denoise loop of an action expert whose hidden width is 32 (the
+ * CAE-FastWAM expert: hidden 32, 24 x 128 attention, 30 blocks; the compact expert of config 3:
+ * hidden 32, 4 x 8 heads), in 2 launches per block step.  Phase p of the call (0 <= p <= 2 L T):
+ *   p = 2 (t L + l)     self (MoT joint) attention sub-block of block l at step t,
+ *   p = 2 (t L + l) + 1 cross-attention sub-block,
+ *   p = 2 L T           the last block's FFN, the head and the last Euler update -> out.
+ * The attention width A = heads * head_dim is cut into G = A / slice column slices of whole
+ * heads; workgroup (g, b) of a phase owns slice g of batch row b:
+ *   self:  completes the previous block (x += o_c + co_b, then x += gate_mlp FFN(AdaLN(x)))
+ *          -- at l = 0 also the head, the Euler update of the chunk and the action encoder --
+ *          then q, k, v of its heads from AdaLN(x), RMSNorm over all A columns (the sums of
+ *          squares of the other slices from the layer's Gram matrix, gram below), 1-D RoPE,
+ *          attention over [the layer's video K/V ; the action K/V] and its share of the o
+ *          projection -> part_s[b, g];
+ *   cross: x += gate_msa (sum_g part_s + o_b), then the slice's cross-attention query from the
+ *          affine LayerNorm3 (RMSNorm as above), attention over the context K/V (already
+ *          RMS-normalised) and its share of the cross o projection -> part_c[b, g].
+ * Every workgroup recomputes the [S, hidden] rows it needs from the previous phase's fp32
+ * partials in a fixed order (no atomics, no communication within a launch); slice 0 stores
+ * them for the next phase.  With G = 1 (A <= 128) the whole call is one launch per batch row.
+ * Rounding: the residual stream and the chunk stay fp32; every product takes bf16 operands
+ * with fp32 accumulation (as fam_gemm); q and k are rounded to bf16 after the norm and after
+ * the rotation.
+ *   gram (G > 1): bf16 [L, 3, 2, 32, 32] -- hi and lo bf16 parts of W^T W for the self q, self k
+ *   and cross q weights (W [A, 32] of the layer, as bf16 values); gram_c fp32 [L, 3, 32] = W^T b;
+ *   gram_b fp32 [L, 3] = |b|^2.  Then sum_j q_j^2 = h G h + 2 c.h + |b|^2 for the row h.
+ *   video_k / video_v: device arrays of L pointers to [B, Sv, A] views with common strides.
+ * Weights are layer-major stacks of the reference's nn.Linear layouts:
+ *   qkv_w [L, 3A, 32] (q; k; v), qkv_b [L, 3A], nq_w / nk_w / cnq_w [L, A], o_w / co_w [L, 32, A],
+ *   o_b / co_b / n3_w / n3_b / ff2_b [L, 32], cq_w [L, A, 32], cq_b [L, A], ff0_w [L, F, 32],
+ *   ff0_b [L, F], ff2_w [L, 32, F]; enc_w [32, Da], enc_b [32], head_w [Da, 32], head_b [Da].
+ *   mods bf16 [T, L, 6 * 32] = modulation + t_mod (shift, scale, gate of the attention; of the FFN).
+ *   ctxkv bf16 [Lc, ctx_ld]: block l's normalised keys at columns 2 A l, values at 2 A l + A.
+ *   rope_cos / rope_sin fp32 [S, head_dim / 2] (pair j of position s).
+ * State (fp32, caller-owned): lat [2, B, S, Da], xa / xb [B, S, 32], part_s / part_c
+ * [B, G, S, 32]; out [B, S, Da].  noise bf16 [B, S, Da] is read at phase 0.
+ * fam_tiny_expert launches phases [phase_begin, phase_end) in order (one launch when G = 1).
+ * Replaces: the action branch of MoT.forward per block step  FB/mot.py:378-478 (DiTBlock
+ *           FB/wan_video_dit.py:267-286), its loop FB/fastwam.py:1051-1069, and the CAE tree's
+ *           single-program ops for this expert: fastwam::mot_qkv_post, mot_attn_oproj,
+ *           mot_ffn, mod_n3q, xattn_qn (CA/mot.py:2793-3010, 3227-3340, 3673-3760) with the
+ *           time-independent parts of CA/action_dit.py:127-231.
+ * Limits: hidden 32; S <= 16; slice in {32, 64, 128}, a multiple of head_dim, A % slice == 0,
+ * (slice / head_dim) * S <= 32; head_dim a multiple of 8; F % 32 == 0, F <= 256; A / slice <= 64;
+ * Da <= 32 and S * Da <= 256; 16-byte aligned weights, rows and strides (multiples of 8).
+ */
+typedef struct fam_tiny_desc {
+  int32_t batch, seq, hidden, heads, head_dim, ffn, action_dim, layers, steps, video_len, ctx_len, slice;
+  float eps, scale;
+  const void* noise; const void* mods; const void* deltas;
+  const float* rope_cos; const float* rope_sin;
+  const void* ctxkv; int64_t ctx_ld;
+  const void* const* video_k; const void* const* video_v; int64_t video_bs, video_rs;
+  const uint8_t* video_mask; int64_t mask_rs;
+  const void* enc_w; const void* enc_b; const void* head_w; const void* head_b;
+  const void* qkv_w; const void* qkv_b; const void* nq_w; const void* nk_w; const void* o_w; const void* o_b;
+  const void* n3_w; const void* n3_b; const void* cq_w; const void* cq_b; const void* cnq_w;
+  const void* co_w; const void* co_b; const void* ff0_w; const void* ff0_b; const void* ff2_w; const void* ff2_b;
+  const void* gram; const float* gram_c; const float* gram_b;
+  float* lat; float* xa; float* xb; float* part_s; float* part_c; float* out;
+} fam_tiny_desc;
+
+int fam_tiny_expert(const fam_tiny_desc* d, int64_t phase_begin, int64_t phase_end, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -59,7 +59,8 @@ def _c_offsets(struct: str, fields):
 
 
 @pytest.mark.parametrize("cls,cname", [(_capi.AttnDesc, "fam_attn_desc"), (_capi.GemmDesc, "fam_gemm_desc"),
-                                       (_capi.RowopDesc, "fam_rowop_desc")])
+                                       (_capi.RowopDesc, "fam_rowop_desc"), (_capi.CaeDesc, "fam_cae_desc"),
+                                       (_capi.TinyDesc, "fam_tiny_desc")])
 def test_struct_layout_matches_header(cls, cname):
     fields = [f for f, _ in cls._fields_]
     size, offs = _c_offsets(cname, fields)
@@ -70,6 +71,50 @@ def test_struct_layout_matches_header(cls, cname):
 
 def _err(lib):
     return lib.fam_last_error().decode()
+
+
+def _tiny_desc(**kw):
+    """A fam_tiny_desc at the CAE expert's shape with every pointer set to an aligned fake
+    address (validation only; nothing is launched when a check fails)."""
+    d = _capi.TinyDesc()
+    dims = dict(batch=1, seq=8, hidden=32, heads=24, head_dim=128, ffn=256, action_dim=16, layers=30, steps=10,
+                video_len=98, ctx_len=129, slice=0)
+    dims.update({k: v for k, v in kw.items() if k in dims})
+    for k, v in dims.items():
+        setattr(d, k, v)
+    d.eps, d.scale = 1e-6, 128 ** -0.5
+    for i, (name, typ) in enumerate(_capi.TinyDesc._fields_):
+        if typ is C.c_void_p:
+            setattr(d, name, 4096 * (i + 1))
+    A = d.heads * d.head_dim
+    d.ctx_ld, d.video_rs, d.video_bs, d.mask_rs = 2 * A * d.layers, 3 * A, 0, 0
+    d.video_mask = None
+    for k, v in kw.items():
+        if k not in dims:
+            setattr(d, k, v)
+    return d
+
+
+def test_tiny_expert_validation(lib):
+    """fam_tiny_expert refuses what its kernel does not cover before any launch (no GPU here:
+    an accepted descriptor with an empty phase range returns FAM_OK without launching)."""
+    f = lib.fam_tiny_expert
+    assert f(C.byref(_tiny_desc()), 0, 0, None) == _capi.FAM_OK
+    assert f(C.byref(_tiny_desc()), 0, 602, None) == _capi.FAM_ERR_INVALID_ARG      # past the final phase (2 L T)
+    assert "phases" in _err(lib)
+    assert f(C.byref(_tiny_desc(hidden=64)), 0, 0, None) == _capi.FAM_ERR_UNSUPPORTED
+    assert f(C.byref(_tiny_desc(seq=17)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
+    assert f(C.byref(_tiny_desc(ffn=512)), 0, 0, None) == _capi.FAM_ERR_UNSUPPORTED
+    assert f(C.byref(_tiny_desc(head_dim=12, heads=8)), 0, 0, None) == _capi.FAM_ERR_UNSUPPORTED
+    # 16 heads of 8 in one 128-wide slice: 16 x 8 tokens = 128 attention columns > 32
+    assert f(C.byref(_tiny_desc(heads=16, head_dim=8)), 0, 0, None) == _capi.FAM_ERR_UNSUPPORTED
+    assert f(C.byref(_tiny_desc(gram=None)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG     # 24 slices need it
+    assert f(C.byref(_tiny_desc(heads=4, head_dim=8, gram=None)), 0, 0, None) == _capi.FAM_OK   # one slice
+    assert f(C.byref(_tiny_desc(qkv_w=4096 + 8)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
+    assert "aligned" in _err(lib)
+    assert f(C.byref(_tiny_desc(ctx_ld=100)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
+    assert f(C.byref(_tiny_desc(video_rs=3072 * 3 + 4)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
+    assert f(C.byref(_tiny_desc(action_dim=40)), 0, 0, None) == _capi.FAM_ERR_UNSUPPORTED
 
 
 def test_validation_rejects_before_launch(lib):

@@ -42,8 +42,8 @@ def test_fused_plan_builds_on_host():
     for batch in (1, 4):
         m = AD.FusedActionDiT(cfg, params, batch=batch, seq_len=32, ctx_len=200, num_steps=3, device="cpu")
         kinds = [d["kernel"] for d in m.plan.meta]
-        # prologue: copy, sinusoid, 3 time GEMMs, modulation, 3 context GEMMs, one K-norm per layer
-        pro = 9 + cfg.num_layers
+        # prologue: copy, sinusoid, 3 time GEMMs, modulation, 3 context GEMMs, the K-norm of every layer
+        pro = 10
         # per step: encoder row + per block (6 projections x 2 + self-attn + cross-attn + combine) + head x 2;
         # at M <= 64 the FFN-up projection is one whole-K kernel with its epilogue (and, when the
         # attention width allows the on-load q/k norm, so are the q/k/v and cross-q projections)
@@ -82,6 +82,39 @@ def test_fused_plan_mot_mode_on_host():
     k = [torch.full((98, cfg.attn_dim), float(i + 1)) for i in range(cfg.num_layers)]
     m.set_video_kv(k, k)
     assert float(m.video_k[1].float().mean()) == 2.0
+
+
+def test_tiny_expert_plan_and_gram_on_host():
+    """Hidden 32 selects fam_tiny_expert: two launches per block step plus the final phase after
+    the prologue (no noise copy: phase 0 reads it).  The packed Gram parts reproduce the whole-row
+    sums of squares the RMSNorm needs, sum_j q_j^2 = h G h + 2 h.c + |b|^2 (fp64 here): with the
+    lo part dropped, or c not doubled, the identity fails."""
+    cfg = AD.ActionDiTConfig(num_layers=3, hidden_dim=32, action_dim=16, ffn_dim=256, text_dim=64, freq_dim=32,
+                             num_heads=24, attn_head_dim=128)
+    params = AD.synthetic_params(cfg, 9)
+    m = AD.FusedActionDiT(cfg, params, batch=1, seq_len=8, ctx_len=129, num_steps=4, device="cpu", video_len=98)
+    assert m.tiny is not None and m.tiny["G"] == 24
+    kinds = [d["kernel"] for d in m.plan.meta]
+    assert kinds.count("tiny_self") == kinds.count("tiny_cross") == 3 * 4 and kinds[-1] == "tiny_final"
+    assert "copy" not in kinds and m.num_launches == 9 + 2 * 3 * 4 + 1
+    g = torch.Generator().manual_seed(1)
+    h = torch.randn(5, 32, generator=g, dtype=torch.float64)
+    A = cfg.attn_dim
+    gram, gc, gb = m.tiny["gram"].double(), m.tiny["gram_c"].double(), m.tiny["gram_b"].double()
+    for l in range(3):
+        for j, (w, b) in enumerate(((m.tiny["qkv_w"][l, :A], m.tiny["qkv_b"][l, :A]),
+                                    (m.tiny["qkv_w"][l, A:2 * A], m.tiny["qkv_b"][l, A:2 * A]),
+                                    (m.tiny["cq_w"][l], m.tiny["cq_b"][l]))):
+            q = h @ w.double().t() + b.double()
+            direct = (q * q).sum(1)
+            G = gram[l, j, 0] + gram[l, j, 1]
+            form = ((h @ G) * h).sum(1) + 2 * h @ gc[l, j] + gb[l, j]
+            assert torch.allclose(form, direct, rtol=2e-5), (l, j)
+            assert not torch.allclose(((h @ gram[l, j, 0]) * h).sum(1) + 2 * h @ gc[l, j] + gb[l, j], direct, rtol=2e-5)
+            assert not torch.allclose(form - h @ gc[l, j], direct, rtol=2e-5)
+    # the generic plan stays available, and hidden 64 never takes the tiny path
+    assert AD.FusedActionDiT(cfg, params, batch=1, seq_len=8, ctx_len=129, num_steps=4, device="cpu", video_len=98,
+                             tiny=False).tiny is None
 
 
 def test_video_rope_table_matches_oracle():
