@@ -29,7 +29,9 @@
 // uses the transposed scores S^T = K Q^T with a block-diagonal Q^T so that several small heads
 // of a slice share one MFMA (column (head, token)), and O^T = V^T P^T from a wave-private V tile
 // read back by transposing LDS reads.  Every global load a phase needs that does not depend on
-// the rows (weights, the first video / context block) is issued before the first barrier.
+// the rows (weights, the first video / context block) is issued before the first barrier, and
+// the barriers wait for LDS traffic only (lds_barrier): a global store is read by the next
+// launch, never by this one, so no barrier has to drain the loads still in flight.
 #include "fam_common.h"
 
 namespace fam {
@@ -201,7 +203,7 @@ __device__ __forceinline__ void ffn_apply(const TinyArgs& a, TinySmem<W, NCB>& s
       *reinterpret_cast<bf16x4*>(&sm.u.f.hid[l16][tau * 16 + lg * 4]) = hv;
     }
   }
-  __syncthreads();
+  lds_barrier();
   f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
   for (int j = 0; j < TF / 128; ++j) {
@@ -216,7 +218,7 @@ __device__ __forceinline__ void ffn_apply(const TinyArgs& a, TinySmem<W, NCB>& s
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int e = 0; e < 4; ++e) sm.u.f.red[wave][l16][t * 16 + lg * 4 + e] = acc[t][e];
-  __syncthreads();
+  lds_barrier();
   const int s = threadIdx.x >> 4, j = threadIdx.x & 15;
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
@@ -225,7 +227,7 @@ __device__ __forceinline__ void ffn_apply(const TinyArgs& a, TinySmem<W, NCB>& s
                     to_f(b2[c]);
     sm.x[s][n] += to_f(gate[c]) * y;
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // ---------------------------------------------------------------------------------------
@@ -280,6 +282,10 @@ __device__ __forceinline__ void gram_sumsq(TinySmem<W, NCB>& sm, const GramFrags
 // Attention of the slice's heads: S queries (columns (head, token) of a block-diagonal Q^T)
 // over keys [segment 0 (global rows) ; segment 1 (the action rows in LDS)], 32-key blocks
 // round-robin over the 4 waves, online softmax per column, waves merged in order -> sm.o.
+// Keys past the end load a valid row of the same operand (row 0), never zero-selected right
+// after the load: a select on a loaded value makes the compiler wait for that load before
+// issuing the next one.  Such keys cost nothing downstream: their scores are masked to -inf
+// (p = 0) and their finite values times p = 0 add 0.
 template <int W>
 struct KvBlock {
   bf16x8 k[2][W / 32];
@@ -304,8 +310,7 @@ __device__ __forceinline__ void kv_load(TinySmem<W, NCB>& sm, const KvSrc& src, 
     for (int kb = 0; kb < W / 32; ++kb) {
       const int col = kb * 32 + lg * 8;
       const bf16* p = kk < src.n0 ? src.k0 + kk * src.rs0 + col : &sm.k[kk < n ? kk - src.n0 : 0][col];
-      const bf16x8 x = load8(p);
-      kv.k[sub][kb] = kk < n ? x : zero8();
+      kv.k[sub][kb] = load8(p);
     }
   }
   constexpr int CPR = W / 8;   // 16-byte chunks per row
@@ -314,8 +319,7 @@ __device__ __forceinline__ void kv_load(TinySmem<W, NCB>& sm, const KvSrc& src, 
     const int ci = lane + 64 * i, row = ci / CPR, c8 = ci - row * CPR;
     const int kk = blk * 32 + row;
     const bf16* p = kk < src.n0 ? src.v0 + kk * src.rs0 + c8 * 8 : &sm.v[kk < n ? kk - src.n0 : 0][c8 * 8];
-    const bf16x8 x = load8(p);
-    kv.v[i] = kk < n ? x : zero8();
+    kv.v[i] = load8(p);
   }
 }
 
@@ -326,23 +330,44 @@ __device__ __forceinline__ void kv_load_global(const KvSrc& src, int blk, KvBloc
 #pragma unroll
   for (int sub = 0; sub < 2; ++sub) {
     int kk = blk * 32 + sub * 16 + l16;
-    const bool ok = kk < src.n0;
-    kk = ok ? kk : 0;
+    kk = kk < src.n0 ? kk : 0;
 #pragma unroll
-    for (int kb = 0; kb < W / 32; ++kb) {
-      const bf16x8 x = load8(src.k0 + kk * src.rs0 + kb * 32 + lg * 8);
-      kv.k[sub][kb] = ok ? x : zero8();
-    }
+    for (int kb = 0; kb < W / 32; ++kb) kv.k[sub][kb] = load8(src.k0 + kk * src.rs0 + kb * 32 + lg * 8);
   }
   constexpr int CPR = W / 8;
 #pragma unroll
   for (int i = 0; i < W / 16; ++i) {
     const int ci = lane + 64 * i, row = ci / CPR, c8 = ci - row * CPR;
     int kk = blk * 32 + row;
-    const bool ok = kk < src.n0;
-    kk = ok ? kk : 0;
-    const bf16x8 x = load8(src.v0 + kk * src.rs0 + c8 * 8);
-    kv.v[i] = ok ? x : zero8();
+    kk = kk < src.n0 ? kk : 0;
+    kv.v[i] = load8(src.v0 + kk * src.rs0 + c8 * 8);
+  }
+}
+
+// Keys [n0, n) of a block prefetched by kv_load_global (which read row 0 for them) come from the
+// action rows in LDS once they exist.
+template <int W, int NCB>
+__device__ __forceinline__ void kv_patch(TinySmem<W, NCB>& sm, const KvSrc& src, int blk, KvBlock<W>& kv) {
+  const int lane = threadIdx.x & 63, l16 = lane & 15, lg = lane >> 4;
+  const int n = src.n0 + src.n1;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    const int kk = blk * 32 + sub * 16 + l16;
+    const bool act = kk >= src.n0 && kk < n;
+#pragma unroll
+    for (int kb = 0; kb < W / 32; ++kb) {
+      const bf16x8 x = *reinterpret_cast<const bf16x8*>(&sm.k[act ? kk - src.n0 : 0][kb * 32 + lg * 8]);
+      kv.k[sub][kb] = act ? x : kv.k[sub][kb];
+    }
+  }
+  constexpr int CPR = W / 8;
+#pragma unroll
+  for (int i = 0; i < W / 16; ++i) {
+    const int ci = lane + 64 * i, row = ci / CPR, c8 = ci - row * CPR;
+    const int kk = blk * 32 + row;
+    const bool act = kk >= src.n0 && kk < n;
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(&sm.v[act ? kk - src.n0 : 0][c8 * 8]);
+    kv.v[i] = act ? x : kv.v[i];
   }
 }
 
@@ -377,6 +402,7 @@ __device__ __forceinline__ void attend(const TinyArgs& a, TinySmem<W, NCB>& sm, 
     for (int dt = 0; dt < WT; ++dt) acc[dt][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   bf16(*vt)[W + 16] = sm.vt[wave];
+  if (prefetched && src.n1 > 0 && wave * 32 + 32 > src.n0) kv_patch(sm, src, wave, kv);
   if (!prefetched && wave < nblk) {
     if (src.n1 == 0)
       kv_load_global<W>(src, wave, kv);
@@ -467,7 +493,7 @@ __device__ __forceinline__ void attend(const TinyArgs& a, TinySmem<W, NCB>& sm, 
     for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
       for (int e = 0; e < 4; ++e) sm.u.mg.acc[wave][dt * 16 + lg * 4 + e][cb * 16 + l16] = acc[dt][cb][e];
-  __syncthreads();
+  lds_barrier();
   for (int idx = threadIdx.x; idx < S * W; idx += 256) {
     const int s = idx / W, d = idx - s * W, c = (d / DH) * S + s;
     float mx = -INFINITY;
@@ -484,7 +510,7 @@ __device__ __forceinline__ void attend(const TinyArgs& a, TinySmem<W, NCB>& sm, 
     }
     sm.o[s][d] = to_bf(den > 0.f ? num / den : 0.f);
   }
-  __syncthreads();
+  lds_barrier();
 }
 
 // The slice's share of an o projection: part[s][n] = sum_d o[s][d] Wo[n][g W + d] (waves 0, 1:
@@ -571,8 +597,8 @@ __device__ __forceinline__ void part_issue(const float* part, int b, int G, int 
   for (int u = 0; u < 8; ++u) {
     const int g = gi + NGI * (8 * round + u);
     const bool ok = gi < NGI && g < G;
-    const f32x4 x = *reinterpret_cast<const f32x4*>(part + (((size_t)b * G + (ok ? g : 0)) * S + (ok ? s : 0)) * TH + 4 * (ok ? n4 : 0));
-    pl.v[u] = ok ? x : f32x4{0.f, 0.f, 0.f, 0.f};
+    // out-of-range slots read slice 0's (finite) row; part_reduce weighs them by 0
+    pl.v[u] = *reinterpret_cast<const f32x4*>(part + (((size_t)b * G + (ok ? g : 0)) * S + (ok ? s : 0)) * TH + 4 * (ok ? n4 : 0));
   }
 }
 
@@ -581,13 +607,14 @@ __device__ __forceinline__ void part_reduce(TinySmem<W, NCB>& sm, const float* p
                                             PartLoads& pl) {
   const int NV = S * 8, NGI = min(4, 256 / NV), tid = threadIdx.x;
   const int gi = tid / NV, slot = tid - gi * NV, s = slot >> 3, n4 = slot & 7;
-  f32x4 acc = pl.v[0];
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int round = 0; round * 8 * NGI < G; ++round) {
+    if (round > 0) part_issue(part, b, G, S, round, pl);
 #pragma unroll
-  for (int u = 1; u < 8; ++u) acc += pl.v[u];
-  for (int round = 1; round * 8 * NGI < G; ++round) {
-    part_issue(part, b, G, S, round, pl);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) acc += pl.v[u];
+    for (int u = 0; u < 8; ++u) {
+      const int g = gi + NGI * (8 * round + u);
+      acc += pl.v[u] * ((gi < NGI && g < G) ? 1.0f : 0.0f);
+    }
   }
   if (gi < NGI) *reinterpret_cast<f32x4*>(&sm.u.f.red[gi][s][4 * n4]) = acc;
 }
@@ -698,7 +725,7 @@ __device__ __forceinline__ void phase_self(const TinyArgs& a, TinySmem<W, NCB>& 
   src.rs0 = a.v_rs;
   src.k0 = a.Sv > 0 ? a.vk[l] + b * a.v_bs + g * W : nullptr;
   src.v0 = a.Sv > 0 ? a.vv[l] + b * a.v_bs + g * W : nullptr;
-  const bool pre = a.Sv >= (wave + 1) * 32;   // the wave's first block lies in the video keys
+  const bool pre = a.Sv > wave * 32;   // the wave's first block holds video keys (action rows patched in later)
   // row-op operands
   const bf16* modt = a.mods + ((size_t)t * L + l) * 6 * TH;
   const RowMod m1 = row_mod_load(modt, modt + TH);   // shift_msa, scale_msa
@@ -721,15 +748,13 @@ __device__ __forceinline__ void phase_self(const TinyArgs& a, TinySmem<W, NCB>& 
   }
   if (step0) {
     eb = *reinterpret_cast<const bf16x2*>(a.enc_b + 2 * j_r);
-    const int Da = a.Da;
-    if (tid < S * Da) {
-      if (first)
-        lat_old = to_f(a.noise[(size_t)b * S * Da + tid]);
-      else {
-        lat_old = a.lat[(size_t)((t - 1) & 1) * rows * Da + (size_t)b * S * Da + tid];
-        hbj = to_f(a.head_b[tid % Da]);
-        delta = to_f(a.deltas[t - 1]);
-      }
+    const int Da = a.Da, e = tid < S * Da ? tid : 0;
+    if (first) {
+      lat_old = to_f(a.noise[(size_t)b * S * Da + e]);
+    } else {
+      lat_old = a.lat[(size_t)((t - 1) & 1) * rows * Da + (size_t)b * S * Da + e];
+      hbj = to_f(a.head_b[e % Da]);
+      delta = to_f(a.deltas[t - 1]);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -738,15 +763,15 @@ __device__ __forceinline__ void phase_self(const TinyArgs& a, TinySmem<W, NCB>& 
   if (step0) small_store(a, sm, sw);
   if (!first) {
     part_reduce(sm, a.part_c, b, G, S, pl);
-    __syncthreads();
+    lds_barrier();
     const float x0 = yv[0] + (to_f(cob[0]) + part_sum(sm, S, s_r, 2 * j_r));
     const float x1 = yv[1] + (to_f(cob[1]) + part_sum(sm, S, s_r, 2 * j_r + 1));
-    __syncthreads();
+    lds_barrier();
     sm.x[s_r][2 * j_r] = s_r < S ? x0 : 0.f;
     sm.x[s_r][2 * j_r + 1] = s_r < S ? x1 : 0.f;
-    __syncthreads();
+    lds_barrier();
     row_norm(sm, S, a.eps, m2, true);
-    __syncthreads();
+    lds_barrier();
     ffn_apply(a, sm, ff, b2, gmlp);
   }
   // second stage of the early loads (after the FFN fragments are consumed)
@@ -767,14 +792,14 @@ __device__ __forceinline__ void phase_self(const TinyArgs& a, TinySmem<W, NCB>& 
     } else {
       head_euler(a, sm, lat_old, hbj, delta, dst);
     }
-    __syncthreads();
+    lds_barrier();
     encoder(a, sm, eb);
-    __syncthreads();
+    lds_barrier();
   }
   if (g == 0 && s_r < S)
     *reinterpret_cast<f32x2*>(a.xa + ((size_t)b * S + s_r) * TH + 2 * j_r) = f32x2{sm.x[s_r][2 * j_r], sm.x[s_r][2 * j_r + 1]};
   row_norm(sm, S, a.eps, m1, true);
-  __syncthreads();
+  lds_barrier();
 
   // ---- q, k, v of the slice (+ the rows' sums of squares over all A columns)
   {
@@ -793,11 +818,11 @@ __device__ __forceinline__ void phase_self(const TinyArgs& a, TinySmem<W, NCB>& 
     }
     if (G > 1 && wave < 2) gram_sumsq(sm, gf, wave, S);
   }
-  __syncthreads();
+  lds_barrier();
   if (G == 1) {
     direct_sumsq(sm, 0, 0, S);
     direct_sumsq(sm, 1, W, S);
-    __syncthreads();
+    lds_barrier();
   }
   norm_slice(a, sm, 0, 0, sm.q, a.nq_w + (size_t)l * A + g * W, true);
   norm_slice(a, sm, 1, W, sm.k, a.nk_w + (size_t)l * A + g * W, true);
@@ -808,7 +833,7 @@ __device__ __forceinline__ void phase_self(const TinyArgs& a, TinySmem<W, NCB>& 
     for (int e = 0; e < 8; ++e) o[e] = to_bf(sm.u.raw[s][2 * W + d0 + e]);
     *reinterpret_cast<bf16x8*>(&sm.v[s][d0]) = o;
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- attention over [video K/V ; action K/V], then the slice's o-projection partial
   attend(a, sm, src, a.mask, a.mask_rs, kv, pre);
@@ -861,7 +886,7 @@ __device__ __forceinline__ void phase_cross(const TinyArgs& a, TinySmem<W, NCB>&
   __builtin_amdgcn_sched_barrier(0);
 
   part_reduce(sm, a.part_s, b, G, S, pl);
-  __syncthreads();
+  lds_barrier();
   {
     const float o0 = to_f(ob[0]) + part_sum(sm, S, s_r, 2 * j_r);
     const float o1 = to_f(ob[1]) + part_sum(sm, S, s_r, 2 * j_r + 1);
@@ -870,9 +895,9 @@ __device__ __forceinline__ void phase_cross(const TinyArgs& a, TinySmem<W, NCB>&
     sm.x[s_r][2 * j_r + 1] = s_r < S ? x1 : 0.f;
     if (g == 0 && s_r < S) *reinterpret_cast<f32x2*>(a.xb + ((size_t)b * S + s_r) * TH + 2 * j_r) = f32x2{x0, x1};
   }
-  __syncthreads();
+  lds_barrier();
   row_norm(sm, S, a.eps, n3, false);
-  __syncthreads();
+  lds_barrier();
   {
     const bf16x8 hf = hb_frag(sm);
 #pragma unroll
@@ -888,13 +913,13 @@ __device__ __forceinline__ void phase_cross(const TinyArgs& a, TinySmem<W, NCB>&
     }
     if (G > 1 && wave == 0) gram_sumsq(sm, gf, 2, S);
   }
-  __syncthreads();
+  lds_barrier();
   if (G == 1) {
     direct_sumsq(sm, 2, 0, S);
-    __syncthreads();
+    lds_barrier();
   }
   norm_slice(a, sm, 2, 0, sm.q, a.cnq_w + (size_t)l * A + g * W, false);
-  __syncthreads();
+  lds_barrier();
   attend(a, sm, src, nullptr, 0, kv, pre);
   oproj_store(sm, of, a.part_c + ((size_t)b * G + g) * S * TH, S);
 }
@@ -918,25 +943,22 @@ __device__ __forceinline__ void phase_final(const TinyArgs& a, TinySmem<W, NCB>&
   const f32x2 y = *reinterpret_cast<const f32x2*>(a.xb + ((size_t)b * S + sr) * TH + 2 * j_r);
   PartLoads pl;
   part_issue(a.part_c, b, G, S, 0, pl);
-  float lat_old = 0.f, hbj = 0.f;
-  const int Da = a.Da;
-  if (tid < S * Da) {
-    lat_old = a.lat[(size_t)(tp & 1) * rows * Da + (size_t)b * S * Da + tid];
-    hbj = to_f(a.head_b[tid % Da]);
-  }
+  const int Da = a.Da, e = tid < S * Da ? tid : 0;
+  const float lat_old = a.lat[(size_t)(tp & 1) * rows * Da + (size_t)b * S * Da + e];
+  const float hbj = to_f(a.head_b[e % Da]);
   const float delta = to_f(a.deltas[tp]);
   __builtin_amdgcn_sched_barrier(0);
   small_store(a, sm, sw);
   part_reduce(sm, a.part_c, b, G, S, pl);
-  __syncthreads();
+  lds_barrier();
   const float x0 = y[0] + (to_f(cob[0]) + part_sum(sm, S, s_r, 2 * j_r));
   const float x1 = y[1] + (to_f(cob[1]) + part_sum(sm, S, s_r, 2 * j_r + 1));
-  __syncthreads();
+  lds_barrier();
   sm.x[s_r][2 * j_r] = s_r < S ? x0 : 0.f;
   sm.x[s_r][2 * j_r + 1] = s_r < S ? x1 : 0.f;
-  __syncthreads();
+  lds_barrier();
   row_norm(sm, S, a.eps, m2, true);
-  __syncthreads();
+  lds_barrier();
   ffn_apply(a, sm, ff, b2, gmlp);
   head_euler(a, sm, lat_old, hbj, delta, a.out + (size_t)b * S * Da);
 }
