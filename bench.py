@@ -58,11 +58,13 @@ def parse():
     ap.add_argument("--no-policy-calls", action="store_true",
                     help="skip the FastWAM / CAE-FastWAM policy-call figures added to the default line")
     ap.add_argument("--cpu-sample-s", type=float, default=20.0, help="CPU baseline time budget")
-    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "hbm", "prefill", "fastwam", "cae"], default="c1",
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "d4d", "hbm", "prefill", "fastwam", "cae"], default="c1",
                     help="c1: the action-DiT denoise loop (the metric); c2: one long-sequence video DiT block "
                          "(config 2 shape), reported as ms per 30-block forward with MFMA utilisation; c3: the "
                          "compact expert loop + action-VAE decoder at B=1 and B=256; c4: the DiT4DiT policy call "
-                         "(Cosmos backbone, 28 blocks, + the flow-matching head, 16 blocks, 4 steps); hbm: size sweep of the "
+                         "(Cosmos backbone, 28 blocks, + the flow-matching head, 16 blocks, 4 steps); d4d: the DiT4DiT "
+                         "RoboCasa-GR1 policy call at its real shape (Cosmos backbone to extract_layer 17 over 588 "
+                         "video tokens + the DiT-B head); hbm: size sweep of the "
                          "HBM-bound kernels (AdaLN, RMSNorm+RoPE, Euler) from config 2 / config 3 B=256 shapes up; "
                          "prefill: the MoT video K/V prefill of the FastWAM call (30 blocks, 98 video tokens); "
                          "fastwam: one FastWAM policy call at the real model shape (VAE encode + prefill + 10-step "
@@ -515,30 +517,43 @@ def bench_c2(args):
 
 
 # --------------------------------------------------------------------------- config 4: DiT4DiT head
-def bench_c4(args):
-    """Config 4, one DiT4DiT policy call (DB/framework/DiT4DiT.py:176-222): the Cosmos-Predict2.5-2B
-    backbone (diffusers' CosmosTransformer3DModel as the reference patches it: 28 blocks, hidden
-    2048, 16 x 128 heads, MLP 8192, AdaLN-LoRA 256; 2048 video tokens = 2 x 32 x 32 latent patches
-    with 3-D rotate-half RoPE, 512 text tokens of width 1024) to its last block's output, then the
-    flow-matching action head (hidden 1024 = 16 x 64 heads, 16 interleaved cross / self blocks, a
-    16 x 29 action chunk -- 16 rows per product, state=None -- 4 Euler steps) cross-attending to
-    those 2048 x 2048 features; B=1, one captured graph."""
+def _d4d_policy_call(args, real: bool):
+    """One DiT4DiT policy call (DB/framework/DiT4DiT.py:176-222), B=1, one captured graph: the
+    Cosmos-Predict2.5-2B backbone (diffusers' CosmosTransformer3DModel as the reference patches it:
+    hidden 2048, 16 x 128 heads, MLP 8192, AdaLN-LoRA 256, 3-D rotate-half RoPE, 512 text tokens of
+    width 1024) to the output of block `extract_layer`, then the flow-matching action head over
+    those features (4 Euler steps).
+      real=False (config 4): 28 blocks over 2048 video tokens (2 x 32 x 32 latent patches) -> a
+        hidden-1024 head (16 x 64 heads, 16 interleaved blocks) on a 16 x 29 chunk, no state;
+      real=True (the RoboCasa-GR1 policy, DiT4DiT/config/robocasa/dit4dit_robocasa_gr1.yaml):
+        224 x 224 frames, 9 frames after the 2x temporal downsampling -> 3 latent frames of 28 x 28
+        (Wan2.1 VAE, 8x spatial, 4x temporal) = 588 video tokens, blocks 0..17 (extract_layer 17),
+        then the DiT-B head (12 x 64 heads, 16 blocks, decoder 2560) on a 16 x 32 chunk with one
+        64-wide state token.
+    The VAE encode of the frames and the text encoder run before the backbone and are not timed
+    here.  Returns the result dict."""
     import torch
     from fam.cosmos import CosmosConfig, FusedCosmosBackbone, synthetic_params as cosmos_params
     from fam.dit4dit import DiT4DiTHeadConfig, FusedDiT4DiTHead, synthetic_params
     dev = torch.device("cuda:0")
-    L, Lc = 2048, 512
-    bcfg = CosmosConfig()
-    bb = FusedCosmosBackbone(bcfg, cosmos_params(bcfg, 1357, dev), batch=1, frames=2, height=64, width=64,
-                             ctx_len=Lc, device=dev)
+    Lc = 512
+    bcfg = CosmosConfig() if not real else CosmosConfig(num_layers=18)
+    frames, hw = (3, 28) if real else (2, 64)
+    bb = FusedCosmosBackbone(bcfg, cosmos_params(bcfg, 1357, dev), batch=1, frames=frames, height=hw, width=hw,
+                             ctx_len=Lc, device=dev, stop_layer=17 if real else None)
     torch.cuda.empty_cache()
-    hcfg = DiT4DiTHeadConfig(heads=16, head_dim=64, action_dim=29, horizon=16, num_steps=4, cross_dim=2048)
+    L = bb.S
+    hcfg = DiT4DiTHeadConfig() if real else DiT4DiTHeadConfig(heads=16, head_dim=64, action_dim=29, horizon=16,
+                                                               num_steps=4, cross_dim=2048)
     params = {k: v.to(torch.bfloat16) for k, v in synthetic_params(hcfg, 4321).items()}
-    head = FusedDiT4DiTHead(hcfg, params, batch=1, vl_len=L, device=dev, state_len=0)
+    state_len = 1 if real else 0
+    head = FusedDiT4DiTHead(hcfg, params, batch=1, vl_len=L, device=dev, state_len=state_len)
     g = torch.Generator("cpu").manual_seed(1234)
-    bb.set_inputs(torch.randn(1, bcfg.in_channels, 2, 64, 64, generator=g).to(dev, torch.bfloat16),
-                  torch.tensor([[1.0, 600.0]]), torch.randn(1, Lc, bcfg.text_dim, generator=g).to(dev, torch.bfloat16))
+    ts = torch.tensor([[1.0] + [600.0] * (frames - 1)])   # the conditioning frame near t = 0
+    bb.set_inputs(torch.randn(1, bcfg.in_channels, frames, hw, hw, generator=g).to(dev, torch.bfloat16), ts,
+                  torch.randn(1, Lc, bcfg.text_dim, generator=g).to(dev, torch.bfloat16))
     noise = torch.randn(1, hcfg.horizon, hcfg.action_dim, generator=g).to(dev, torch.bfloat16)
+    state = torch.randn(1, 1, hcfg.state_dim, generator=g).to(dev, torch.bfloat16) if state_len else None
     feats = bb.features()
 
     def call(stream):
@@ -546,7 +561,7 @@ def bench_c4(args):
             f(stream)
         head.vl_in.copy_(feats)
         head._enqueue()
-    head.set_inputs(noise, torch.zeros(1, L, 2048, dtype=torch.bfloat16, device=dev))
+    head.set_inputs(noise, torch.zeros(1, L, 2048, dtype=torch.bfloat16, device=dev), state)
     s = torch.cuda.Stream(dev)
     s.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(s):
@@ -562,27 +577,47 @@ def bench_c4(args):
     head.capture()
     head_p50, _, _ = _time_calls(head.run, args.steps, args.warmup)
     flops = sum(m.get("flops", 0) for m in bb.meta)
+    if real:
+        what = ("DiT4DiT RoboCasa-GR1 policy call: Cosmos-Predict2.5-2B backbone blocks 0..17 (extract_layer 17; "
+                "AdaLN-LoRA modulated self / cross / FFN sub-blocks, per-head q/k RMSNorm, rotate-half 3-D RoPE; "
+                "hidden 2048, 16x128 heads, MLP 8192) over 588 video tokens (3 latent frames x 14 x 14 patches of "
+                "224x224 frames) + 512 text tokens x 1024 -> DiT-B action head (12x64 heads, 16 interleaved blocks, "
+                "decoder 2560, 16x32 chunk, one 64-wide state token, 4 Euler steps) over the 588 x 2048 features")
+        metric = ("p50 ms per DiT4DiT RoboCasa-GR1 policy call at the real model shape (Cosmos backbone to "
+                  "extract_layer 17 + 4-step DiT-B action head, bs=1; VAE encode and text encoder not included)")
+    else:
+        what = ("config4 DiT4DiT: Cosmos-Predict2.5-2B backbone (28 Cosmos blocks: AdaLN-LoRA modulated self / "
+                "cross / FFN sub-blocks, per-head q/k RMSNorm, rotate-half 3-D RoPE; hidden 2048, 16x128 heads, MLP "
+                "8192, 2048 video tokens 2x32x32, 512 text tokens x 1024) -> last block's output -> action head "
+                "(hidden 1024 = 16x64, 16 interleaved blocks, 16x29 chunk, 4 Euler steps) over the 2048 x 2048 "
+                "features")
+        metric = "p50 ms per DiT4DiT policy call (Cosmos backbone forward + 4-step action head, bs=1)"
     out = {
-        "metric": "p50 ms per DiT4DiT policy call (Cosmos backbone forward + 4-step action head, bs=1)",
-        "value": round(p50, 4),
+        "metric": metric, "value": round(p50, 4),
         "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(p50, 4),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic: seeded N(0,1) latents, text and noise, N(0,0.02) weights",
-        "config": {"workload": "config4 DiT4DiT: Cosmos-Predict2.5-2B backbone (28 Cosmos blocks: AdaLN-LoRA "
-                               "modulated self / cross / FFN sub-blocks, per-head q/k RMSNorm, rotate-half 3-D RoPE; "
-                               "hidden 2048, 16x128 heads, MLP 8192, 2048 video tokens 2x32x32, 512 text tokens x "
-                               "1024) -> last block's output -> action head (hidden 1024 = 16x64, 16 interleaved "
-                               "blocks, 16x29 chunk, 4 Euler steps) over the 2048 x 2048 features",
-                   "batch": 1, "video_tokens": L},
+        "data": "synthetic: seeded N(0,1) latents, text, state and noise, N(0,0.02) weights",
+        "config": {"workload": what, "batch": 1, "video_tokens": L, "backbone_blocks": bb.n},
         "min_ms": round(mn, 4), "p90_ms": round(p90, 4), "backbone_ms": round(bb_p50, 4), "head_ms": round(head_p50, 4),
         "backbone_tflops": round(flops / (bb_p50 * 1e-3) / 1e12, 1),
-        "launches_per_call": bb.num_launches,
-        "reference_anchor_unpublished": {"note": "whole-policy GEAK figure quoted in the reference's source, not a "
-                                                 "published result; the reference runs the backbone to block 19 "
-                                                 "(extract_layer) on its own shapes",
-                                         "policy_call_ms": 6.49, "source": "DG/modules/action_model/ActionDiT.py"},
+        "backbone_launches": bb.num_launches,
     }
-    print(json.dumps(out), flush=True)
+    if real:
+        out["published_reference_ms"] = 6.69
+        out["published_source"] = ("docs/fastwam-geak-inference-optimization.md:24-25 (DiT4DiT RoboCasa-GR1 + GEAK, "
+                                   "4 steps, one MI355X; latency per policy decision, which also covers the VAE "
+                                   "encode and the text encoder)")
+    return out
+
+
+def bench_c4(args):
+    """Config 4, one DiT4DiT policy call (see _d4d_policy_call, real=False)."""
+    print(json.dumps(_d4d_policy_call(args, real=False)), flush=True)
+
+
+def bench_d4d(args):
+    """The DiT4DiT RoboCasa-GR1 policy call at its real shape (see _d4d_policy_call, real=True)."""
+    print(json.dumps(_d4d_policy_call(args, real=True)), flush=True)
 
 
 # --------------------------------------------------------------------------- HBM-bound kernels, size sweep
@@ -1052,6 +1087,9 @@ def main():
     if args.workload == "c4":
         bench_c4(args)
         return
+    if args.workload == "d4d":
+        bench_d4d(args)
+        return
     if args.workload == "c3":
         bench_c3(args)
         return
@@ -1124,8 +1162,9 @@ def main():
         out["speedup_vs_eager_gpu"] = round(out["eager_gpu_baseline"]["p50_ms"] / p50, 2)
 
     if not args.no_policy_calls:
-        # the reference's two published whole-policy latencies on one MI355X, measured on the same
-        # box after the config-1 figure: FastWAM and CAE-FastWAM infer_action at their real shapes
+        # the reference's published whole-policy latencies on one MI355X, measured on the same box
+        # after the config-1 figure: FastWAM and CAE-FastWAM infer_action and the DiT4DiT RoboCasa-GR1
+        # call at their real shapes
         del model
         torch.cuda.empty_cache()
         for key, cae in (("fastwam_policy_call", False), ("cae_fastwam_policy_call", True)):
@@ -1138,6 +1177,15 @@ def main():
                         "published_reference_ms": pub["ms"], "published_source": pub["source"],
                         "ratio_published_over_ours": round(pub["ms"] / r["value"], 4)}
             torch.cuda.empty_cache()
+        log("dit4dit_policy_call: building and timing")
+        r = _d4d_policy_call(args, real=True)
+        out["dit4dit_policy_call"] = {"metric": r["metric"], "p50_ms": r["value"], "min_ms": r["min_ms"],
+                                      "p90_ms": r["p90_ms"], "backbone_p50_ms": r["backbone_ms"],
+                                      "head_p50_ms": r["head_ms"], "backbone_launches": r["backbone_launches"],
+                                      "published_reference_ms": r["published_reference_ms"],
+                                      "published_source": r["published_source"],
+                                      "ratio_published_over_ours": round(r["published_reference_ms"] / r["value"], 4)}
+        torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle) on host cores")

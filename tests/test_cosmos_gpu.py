@@ -169,3 +169,28 @@ def test_cosmos_backbone_config4_shape_two_blocks():
     assert y.shape == (1, 2048, 2048)
     assert err <= BAR
     assert all(v <= BAR for v in errs.values()), errs
+
+
+def test_cosmos_backbone_robocasa_shape_stops_at_extract_layer():
+    """The DiT4DiT RoboCasa-GR1 call's backbone shape: 3 latent frames of 28 x 28 (224 x 224 frames,
+    588 tokens on a 3 x 14 x 14 grid), 512 text tokens; a 3-block stack stopped after block 1
+    (stop_layer, the reference's extract_layer hook) returns exactly the oracle's 2-block features."""
+    from fam.cosmos import CosmosConfig, FusedCosmosBackbone
+    cfg = O.CosmosConfig(num_layers=2)
+    Lc = 512
+    p, lat, ctx, cm, ts = _cosmos_case(O.CosmosConfig(num_layers=3), 1, 3, 28, 28, Lc, 350, True)
+    ts = torch.tensor([[1.0, 500.0, 500.0]], dtype=BF)
+    m = FusedCosmosBackbone(CosmosConfig(num_layers=3), p, batch=1, frames=3, height=28, width=28, ctx_len=Lc,
+                            stop_layer=1)
+    assert m.S == 588 and m.n == 2
+    y = m.forward(lat.cuda(), ts.cuda(), ctx.cuda(), cm.cuda()).clone()
+    p32 = {k: v.float() for k, v in p.items()}
+    traces = []
+    ref = O.cosmos_features(p32, cfg, lat.float(), ts.float(), ctx.float(), ctx_mask=cm, traces=traces)
+    err = rel(y, ref)
+    errs = _branch_errors(m, cfg, p32, lat, ts, ctx, cm, traces, ref)
+    print(f"cosmos RoboCasa shape, stop after block 1 of 3: relerr {err:.3e}; branches "
+          + ", ".join(f"{k} {v:.3e}" for k, v in errs.items()))
+    assert y.shape == (1, 588, 2048)
+    assert err <= BAR
+    assert all(v <= BAR for v in errs.values()), errs

@@ -65,6 +65,16 @@ def test_d4d_head_dit_b_config_and_graph_replay():
         assert torch.equal(again, out)
 
 
+def test_d4d_head_robocasa_shape():
+    """The DiT-B head at the RoboCasa-GR1 policy's shape: 588 VLM tokens (the backbone's 3 x 14 x 14
+    video tokens at extract_layer), one 64-wide state token, a 16 x 32 chunk, 4 steps."""
+    cfg = O.DiT4DiTHeadConfig()
+    head, (vl, noise, state), out, ref = _run(cfg, 1, 588, 23, 1)
+    err = _relerr(out, ref)
+    print(f"DiT-B head over 588 tokens: relerr {err:.3e}, max|d| {(out - ref).abs().max().item():.3e}")
+    assert err <= 3e-2
+
+
 def test_d4d_head_rejects_state_mismatch():
     from fam.dit4dit import FusedDiT4DiTHead
     cfg = O.DiT4DiTHeadConfig(num_layers=2, heads=2, head_dim=16, cross_dim=24, output_dim=40, hidden_size=40,
