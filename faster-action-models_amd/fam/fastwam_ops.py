@@ -19,7 +19,36 @@ own the name.
     fastwam::skpost(a, w, bias, res, modg, moda, tmod, lnw, lnb, gi, si, hi, eps, xdt)
                                                             FG/mot.py:1315-1348
 
-(FG = src/fastwam-geak/fastwam/models/wan22.)
+The GEAK tree's prefill (FG/mot.py:1693-1905) and the CAE-FastWAM tree's action expert
+(CA = src/cae-fastwam/fastwam/models/wan22; CA/mot.py:2793-3010, :3585-3712,
+CA/action_dit.py:127-231) add:
+
+    fastwam::pf_mm(x, w, b), pf_mm_gelu(x, w, b)            FG/mot.py:1693-1710
+    fastwam::res_ln1(x, o, mb, tm, wn, bn, go, eps)         FG/mot.py:1829-1844
+    fastwam::res_ln2(x, o1, o2, mb, mb2, tm, go, sho, sco, eps)   FG/mot.py:1846-1862
+    fastwam::res_ln_tail(x, o, mb, mb2, tm, go, sho, sco, eps)    FG/mot.py:1883-1899
+    fastwam::mot_attn(q, k, v, msk, nh, hd, head_major)     CA/mot.py:2948-2976
+    fastwam::mot_qkv_post(qkv, qw, kw, freqs, kbuf, vbuf, sv, eps)  CA/mot.py:2793-2822
+    fastwam::xattn_qn(qr, qw, k, v, msk, nh, hd, eps)       CA/mot.py:3673-3700
+    fastwam::ctx_kv_norm(g, nkw, nl, ahd, eps)              CA/mot.py:3585-3608
+    fastwam::mot_oproj(a, w, b), mot_ffn(x, w1, b1, w2, b2) CA/mot.py:2904-2946
+    fastwam::adit_tmod(te, inv, w0, b0, w1, b1, w2, b2, atok, aw, ab, fuse_sin)
+                                                            CA/action_dit.py:191-225
+
+Per-operator rounding differences from the Triton kernels they stand in for (all within one
+bf16 rounding of an intermediate; the GPU tests hold each against an eager restatement of the
+reference kernel at 2e-2):
+  res_ln*   the norm reads the bf16-rounded residual (the reference takes its statistics from
+            the fp32 sum); the gate / shift / scale sums modulation + t_mod in fp32 as it does;
+  mot_qkv_post, xattn_qn, ctx_kv_norm
+            RMSNorm rounds to bf16 before the weight (the eager module's order); the CAE
+            kernels of xattn_qn and ctx_kv_norm multiply the weight before their one rounding;
+  mot_ffn, pf_mm_gelu, adit_tmod
+            the activation runs on the fp32 accumulator (+ bias) and rounds once; the
+            reference kernels round the pre-activation to bf16 first.
+ctx_kv_norm returns the K half only ([1, nl, 1, S, ahd]), the reference's default
+(FASTWAM_R2_NORM_V unset, CA/mot.py:578).  adit_tmod computes the sinusoid with the library's
+own fp64 frequencies; `inv` must be 10000^(-j / (FD/2)), which is what the call site passes.
 
 Numerics follow the reference's eager modules (src/fastwam-baseline), which the GEAK kernels
 approximate: RMSNorm rounds to bf16 before its weight (FB/wan_video_dit.py:156-167), and
@@ -318,3 +347,313 @@ def _(a, w, bias, res, modg, moda, tmod, lnw, lnb, gi, si, hi, eps, xdt=0):
     n = w.shape[0]
     xd = torch.float32 if xdt else a.dtype
     return a.new_empty((1, a.shape[-2], n), dtype=xd), a.new_empty((1, a.shape[-2], n))
+
+
+# --------------------------------------------------------------------------- prefill projections (FG)
+@torch.library.custom_op("fastwam::pf_mm", mutates_args=())
+def pf_mm(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """F.linear(x, w, b) for the prefill's 98-row projections (FG/mot.py:1693-1700)."""
+    for t, n in ((x, "x"), (w, "w"), (b, "b")):
+        _check(t, n)
+    x2 = _rows2d(x)
+    out = torch.empty(tuple(x.shape[:-1]) + (w.shape[0],), dtype=x.dtype, device=x.device)
+    gemm(x2, w.contiguous(), b.contiguous(), out.view(x2.shape[0], w.shape[0]))
+    return out
+
+
+@pf_mm.register_fake
+def _(x, w, b):
+    return x.new_empty(tuple(x.shape[:-1]) + (int(w.shape[0]),))
+
+
+@torch.library.custom_op("fastwam::pf_mm_gelu", mutates_args=())
+def pf_mm_gelu(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """GELU(tanh)(x w^T + b) (aten _addmm_activation(use_gelu=True), FG/mot.py:1703-1707)."""
+    for t, n in ((x, "x"), (w, "w"), (b, "b")):
+        _check(t, n)
+    x2 = _rows2d(x)
+    out = torch.empty(tuple(x.shape[:-1]) + (w.shape[0],), dtype=x.dtype, device=x.device)
+    gemm(x2, w.contiguous(), b.contiguous(), out.view(x2.shape[0], w.shape[0]), act=_capi.FAM_ACT_GELU_TANH)
+    return out
+
+
+@pf_mm_gelu.register_fake
+def _(x, w, b):
+    return x.new_empty(tuple(x.shape[:-1]) + (int(w.shape[0]),))
+
+
+def _mod_rows(mb: torch.Tensor, tm: torch.Tensor, off: int, S: int, N: int) -> torch.Tensor:
+    """(modulation + per-token t_mod) chunk at column `off`: [S, N], summed in fp32 and rounded
+    once (the reference kernel adds the two bf16 loads in fp32, FG/mot.py:1783-1795)."""
+    if tm.dim() != 2 or tm.shape[0] < S or tm.shape[1] < off + N:
+        raise ValueError(f"t_mod must be [S, >= {off + N}] rows, got {tuple(tm.shape)}")
+    return (mb.reshape(-1)[off:off + N].float()[None, :] + tm[:S, off:off + N].float()).to(_BF16).contiguous()
+
+
+def _res_norm(x, parts, gate, eps, ln=None, ada=None):
+    """x + gate * parts[0] (+ parts[1]) in fp32, stored bf16, then LayerNorm (affine, ln = (w, b))
+    or AdaLN (ada = (shift rows, scale rows)) of that row into a second bf16 tensor."""
+    S, N = x.shape[1], x.shape[2]
+    p = parts[0].reshape(S, N).float() * gate.float()
+    for extra in parts[1:]:
+        p = p + extra.reshape(S, N).float()
+    p = p.reshape(1, S, N).contiguous()
+    xo = torch.empty((1, S, N), dtype=x.dtype, device=x.device)
+    no = torch.empty((1, S, N), dtype=x.dtype, device=x.device)
+    kw = dict(partials=p, res=_rows2d(x), eps=eps, nout=no.view(S, N))
+    if ln is not None:
+        rowop(xo.view(S, N), norm=_capi.FAM_ROWNORM_LAYERNORM, ln_w=ln[0].contiguous(), ln_b=ln[1].contiguous(), **kw)
+    else:
+        rowop(xo.view(S, N), norm=_capi.FAM_ROWNORM_ADALN, shift=ada[0], scale=ada[1], mod_strides=(0, N), **kw)
+    return xo, no
+
+
+@torch.library.custom_op("fastwam::res_ln1", mutates_args=())
+def res_ln1(x: torch.Tensor, o: torch.Tensor, mb: torch.Tensor, tm: torch.Tensor, wn: torch.Tensor,
+            bn: torch.Tensor, go: int, eps: float) -> torch.Tensor:
+    """LayerNorm(x + g o) * wn + bn per token, g = chunk `go` of modulation mb + t_mod row tm[s]
+    (the prefill's norm3 after the self-attention residual, FG/mot.py:1829-1844); [1, S, N]."""
+    for t, n in ((x, "x"), (o, "o"), (mb, "mb"), (tm, "tm"), (wn, "wn"), (bn, "bn")):
+        _check(t, n)
+    S, N = x.shape[1], x.shape[2]
+    _, no = _res_norm(x, [o], _mod_rows(mb, tm, go, S, N), eps, ln=(wn, bn))
+    return no
+
+
+@res_ln1.register_fake
+def _(x, o, mb, tm, wn, bn, go, eps):
+    return x.new_empty((1, int(x.shape[1]), int(x.shape[2])))
+
+
+@torch.library.custom_op("fastwam::res_ln2", mutates_args=())
+def res_ln2(x: torch.Tensor, o1: torch.Tensor, o2: torch.Tensor, mb: torch.Tensor, mb2: torch.Tensor,
+            tm: torch.Tensor, go: int, sho: int, sco: int, eps: float) -> List[torch.Tensor]:
+    """[xo, no]: xo = x + g o1 + o2, no = LN(xo) (1 + scale) + shift, g / shift / scale the chunks
+    `go` of mb and `sho` / `sco` of mb2, each plus t_mod row tm[s] (FG/mot.py:1846-1862)."""
+    for t, n in ((x, "x"), (o1, "o1"), (o2, "o2"), (mb, "mb"), (mb2, "mb2"), (tm, "tm")):
+        _check(t, n)
+    S, N = x.shape[1], x.shape[2]
+    xo, no = _res_norm(x, [o1, o2], _mod_rows(mb, tm, go, S, N), eps,
+                       ada=(_mod_rows(mb2, tm, sho, S, N), _mod_rows(mb2, tm, sco, S, N)))
+    return [xo, no]
+
+
+@res_ln2.register_fake
+def _(x, o1, o2, mb, mb2, tm, go, sho, sco, eps):
+    S, N = int(x.shape[1]), int(x.shape[2])
+    return [x.new_empty((1, S, N)), x.new_empty((1, S, N))]
+
+
+@torch.library.custom_op("fastwam::res_ln_tail", mutates_args=())
+def res_ln_tail(x: torch.Tensor, o: torch.Tensor, mb: torch.Tensor, mb2: torch.Tensor, tm: torch.Tensor,
+                go: int, sho: int, sco: int, eps: float) -> List[torch.Tensor]:
+    """res_ln2 without the second output term: the layer boundary x + gate_mlp ffn, then the next
+    block's AdaLN1 (FG/mot.py:1883-1899)."""
+    for t, n in ((x, "x"), (o, "o"), (mb, "mb"), (mb2, "mb2"), (tm, "tm")):
+        _check(t, n)
+    S, N = x.shape[1], x.shape[2]
+    xo, no = _res_norm(x, [o], _mod_rows(mb, tm, go, S, N), eps,
+                       ada=(_mod_rows(mb2, tm, sho, S, N), _mod_rows(mb2, tm, sco, S, N)))
+    return [xo, no]
+
+
+@res_ln_tail.register_fake
+def _(x, o, mb, mb2, tm, go, sho, sco, eps):
+    S, N = int(x.shape[1]), int(x.shape[2])
+    return [x.new_empty((1, S, N)), x.new_empty((1, S, N))]
+
+
+# --------------------------------------------------------------------------- CAE action expert (CA)
+def _keep_plane(msk: torch.Tensor, M: int, SK: int) -> torch.Tensor:
+    """The [M, SK] keep plane (nonzero = attend) of a CAE mask operand, as bool."""
+    m = msk
+    while m.dim() > 2:
+        m = m[0]
+    if m.dim() == 1:
+        m = m[None, :]
+    return torch.broadcast_to(m != 0, (M, SK))
+
+
+@torch.library.custom_op("fastwam::mot_attn", mutates_args=())
+def mot_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, msk: torch.Tensor, nh: int, hd: int,
+             head_major: bool) -> torch.Tensor:
+    """softmax(q k^T / sqrt(hd), keys where msk != 0) v per head (CA/mot.py:2948-2976): q [1, H, M,
+    hd] and k / v [1, H, SK, hd] when head_major, else [1, M, H*hd] / [1, SK, H*hd] rows;
+    output [1, M, H*hd]."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _check(t, n)
+    H, D = int(nh), int(hd)
+    if head_major:
+        M, SK = q.shape[2], k.shape[2]
+        qs, ks, vs = _bhsd_strides(q), _bhsd_strides(k), _bhsd_strides(v)
+    else:
+        M, SK = q.shape[1], k.shape[1]
+        qs, ks, vs = (0, q.stride(1), D), (0, k.stride(1), D), (0, v.stride(1), D)
+    o = torch.empty((1, M, H * D), dtype=q.dtype, device=q.device)
+    _launch_attention(q, qs, k, ks, v, vs, o, _bshd_strides(o, D), 1, H, M, SK, D, _keep_plane(msk, M, SK))
+    return o
+
+
+@mot_attn.register_fake
+def _(q, k, v, msk, nh, hd, head_major):
+    m = q.shape[2] if head_major else q.shape[1]
+    return q.new_empty((1, m, nh * hd))
+
+
+@torch.library.custom_op("fastwam::mot_qkv_post", mutates_args={"kbuf", "vbuf"})
+def mot_qkv_post(qkv: torch.Tensor, qw: torch.Tensor, kw: torch.Tensor, freqs: torch.Tensor, kbuf: torch.Tensor,
+                 vbuf: torch.Tensor, sv: int, eps: float) -> torch.Tensor:
+    """The CAE expert's q / k post-processing (CA/mot.py:2793-2822, kernel :1369-1456): from the
+    fused projection qkv [1, M, 3D] (D = H hd), RMSNorm over D of q and k with their weights,
+    then the interleaved rotation by freqs [M, hd] (cos at 2p, sin at 2p + 1 of each token's row);
+    q returned head-major [1, H, M, hd], k and v written to rows sv .. sv + M of the head-major
+    cache buffers kbuf / vbuf [1, H, SKV, hd]."""
+    for t, n in ((qkv, "qkv"), (qw, "qw"), (kw, "kw"), (kbuf, "kbuf"), (vbuf, "vbuf")):
+        _check(t, n)
+    M, D3 = qkv.shape[1], qkv.shape[2]
+    D = D3 // 3
+    H, hd, SKV = kbuf.shape[1], kbuf.shape[3], kbuf.shape[2]
+    if H * hd != D or sv < 0 or sv + M > SKV:
+        raise ValueError(f"kbuf {tuple(kbuf.shape)} does not take {M} rows of {D} at row {sv}")
+    f = freqs.reshape(-1, hd).float().contiguous()
+    if f.shape[0] < M:
+        raise ValueError(f"freqs must hold {M} rows of {hd}, got {tuple(freqs.shape)}")
+    x2 = qkv.reshape(M, D3)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8:
+        x2 = x2.contiguous()
+    tab = (f, f[:, 1:], hd, 2, hd)
+    qn = torch.empty((M, D), dtype=qkv.dtype, device=qkv.device)
+    kn = torch.empty((M, D), dtype=qkv.dtype, device=qkv.device)
+    for src, dst, w in ((x2[:, :D], qn, qw), (x2[:, D:2 * D], kn, kw)):
+        cos, sin, trs, tes, head = tab
+        call("fam_rmsnorm_rope", src.data_ptr(), src.stride(0), dst.data_ptr(), dst.stride(0), M, M, D,
+             w.contiguous().data_ptr(), float(eps), cos.data_ptr(), sin.data_ptr(), trs, tes, head, _stream(qkv))
+    kbuf[0, :, sv:sv + M, :].copy_(kn.view(M, H, hd).transpose(0, 1))
+    vbuf[0, :, sv:sv + M, :].copy_(x2[:, 2 * D:].reshape(M, H, hd).transpose(0, 1))
+    return qn.view(M, H, hd).transpose(0, 1).contiguous().unsqueeze(0)
+
+
+@mot_qkv_post.register_fake
+def _(qkv, qw, kw, freqs, kbuf, vbuf, sv, eps):
+    return qkv.new_empty((1, kbuf.shape[1], qkv.shape[1], kbuf.shape[3]))
+
+
+@torch.library.custom_op("fastwam::xattn_qn", mutates_args=())
+def xattn_qn(qr: torch.Tensor, qw: torch.Tensor, k: torch.Tensor, v: torch.Tensor, msk: torch.Tensor, nh: int,
+             hd: int, eps: float) -> torch.Tensor:
+    """Cross attention with the query's RMSNorm over its whole C-wide row (CA/mot.py:3673-3700,
+    kernel :2240-2305): q = RMSNorm(qr) qw; o = softmax(q k^T / sqrt(hd), keys where msk != 0) v
+    per head over [1, N, C] rows of k / v; output [1, M, C]."""
+    for t, n in ((qr, "qr"), (qw, "qw"), (k, "k"), (v, "v")):
+        _check(t, n)
+    M, Cw = qr.shape[1], qr.shape[2]
+    N, H, D = k.shape[1], int(nh), int(hd)
+    q = torch.empty((M, Cw), dtype=qr.dtype, device=qr.device)
+    _rms(_rows2d(qr), q, qw.contiguous(), eps)
+    o = torch.empty((1, M, Cw), dtype=qr.dtype, device=qr.device)
+    q3 = q.view(1, M, Cw)
+    _launch_attention(q3, _bshd_strides(q3, D), k, (0, k.stride(1), D), v, (0, v.stride(1), D), o,
+                      _bshd_strides(o, D), 1, H, M, N, D, _keep_plane(msk, M, N))
+    return o
+
+
+@xattn_qn.register_fake
+def _(qr, qw, k, v, msk, nh, hd, eps):
+    return torch.empty_like(qr)
+
+
+@torch.library.custom_op("fastwam::ctx_kv_norm", mutates_args=())
+def ctx_kv_norm(g: torch.Tensor, nkw: torch.Tensor, nl: int, ahd: int, eps: float) -> torch.Tensor:
+    """RMSNorm of every layer's context keys (CA/mot.py:3585-3608, kernel :2119-2142): g [S, 2 nl ahd]
+    holds the keys of layer l at columns l ahd and the values after all keys; returns the keys
+    normalised with nkw [nl, ahd], [1, nl, 1, S, ahd]."""
+    _check(g, "g")
+    _check(nkw, "nkw")
+    S, nl, ahd = g.shape[0], int(nl), int(ahd)
+    if g.dim() != 2 or g.shape[1] != 2 * nl * ahd or nkw.numel() != nl * ahd:
+        raise ValueError(f"g must be [S, {2 * nl * ahd}] and nkw [{nl}, {ahd}]")
+    keys = g[:, :nl * ahd].reshape(S * nl, ahd).contiguous()    # row (s, l): layer l's key of token s
+    y = torch.empty_like(keys)
+    call("fam_rmsnorm_grouped", keys.data_ptr(), ahd, y.data_ptr(), ahd, S * nl, ahd,
+         nkw.reshape(nl, ahd).contiguous().data_ptr(), nl, float(eps), _stream(g))
+    return y.view(S, nl, ahd).transpose(0, 1).contiguous().view(1, nl, 1, S, ahd)
+
+
+@ctx_kv_norm.register_fake
+def _(g, nkw, nl, ahd, eps):
+    return g.new_empty((1, nl, 1, g.shape[0], ahd))
+
+
+@torch.library.custom_op("fastwam::mot_oproj", mutates_args=())
+def mot_oproj(a: torch.Tensor, w: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """a w^T + b on the M action rows, [1, M, K] -> [1, M, N] (CA/mot.py:2929-2946)."""
+    for t, n in ((a, "a"), (w, "w"), (b, "b")):
+        _check(t, n)
+    a2 = _rows2d(a)
+    out = torch.empty((1, a2.shape[0], w.shape[0]), dtype=a.dtype, device=a.device)
+    gemm(a2, w.contiguous(), b.contiguous(), out.view(a2.shape[0], w.shape[0]))
+    return out
+
+
+@mot_oproj.register_fake
+def _(a, w, b):
+    return a.new_empty((1, a.shape[1], w.shape[0]))
+
+
+@torch.library.custom_op("fastwam::mot_ffn", mutates_args=())
+def mot_ffn(x: torch.Tensor, w1: torch.Tensor, b1: torch.Tensor, w2: torch.Tensor, b2: torch.Tensor) -> torch.Tensor:
+    """W2 GELU(tanh)(W1 x + b1) + b2 on the action rows (CA/mot.py:2904-2927, kernel :2308-2343)."""
+    for t, n in ((x, "x"), (w1, "w1"), (b1, "b1"), (w2, "w2"), (b2, "b2")):
+        _check(t, n)
+    x2 = _rows2d(x)
+    M = x2.shape[0]
+    hid = torch.empty((M, w1.shape[0]), dtype=x.dtype, device=x.device)
+    gemm(x2, w1.contiguous(), b1.contiguous(), hid, act=_capi.FAM_ACT_GELU_TANH)
+    out = torch.empty_like(x)
+    gemm(hid, w2.contiguous(), b2.contiguous(), out.view(M, w2.shape[0]))
+    return out
+
+
+@mot_ffn.register_fake
+def _(x, w1, b1, w2, b2):
+    return torch.empty_like(x)
+
+
+@torch.library.custom_op("fastwam::adit_tmod", mutates_args=())
+def adit_tmod(te: torch.Tensor, inv: torch.Tensor, w0: torch.Tensor, b0: torch.Tensor, w1: torch.Tensor,
+              b1: torch.Tensor, w2: torch.Tensor, b2: torch.Tensor, atok: torch.Tensor, aw: torch.Tensor,
+              ab: torch.Tensor, fuse_sin: int) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The action expert's time MLP and action encoder (CA/action_dit.py:127-225): te the timestep
+    (fuse_sin: its sinusoidal embedding is formed here) or that embedding [FD]; returns
+    t = W1 SiLU(W0 te + b0) + b1 [1, H], t_mod = W2 SiLU(t) + b2 [1, 6H] and the encoded action
+    tokens atok [1, S, A] W_aw^T + ab [1, S, H]."""
+    for t, n in ((w0, "w0"), (w1, "w1"), (w2, "w2"), (atok, "atok"), (aw, "aw")):
+        _check(t, n)
+    dev, odt = atok.device, atok.dtype
+    FD, H, H6 = w0.shape[1], w0.shape[0], w2.shape[0]
+    if fuse_sin:
+        emb = torch.empty((1, FD), dtype=odt, device=dev)
+        pos = te.reshape(1).to(odt).contiguous()
+        call("fam_sinusoid", pos.data_ptr(), emb.data_ptr(), 1, FD, _stream(atok))
+    else:
+        emb = te.reshape(1, FD).to(odt).contiguous()
+    h0 = torch.empty((1, H), dtype=odt, device=dev)
+    gemm(emb, w0.contiguous(), b0.contiguous(), h0, act=_capi.FAM_ACT_SILU)
+    t = torch.empty((1, H), dtype=odt, device=dev)
+    gemm(h0, w1.contiguous(), b1.contiguous(), t)
+    st = torch.empty((1, H), dtype=odt, device=dev)
+    call("fam_act_rows", t.data_ptr(), H, st.data_ptr(), H, 1, H, _capi.FAM_ACT_SILU, _stream(atok))
+    tm = torch.empty((1, H6), dtype=odt, device=dev)
+    gemm(st, w2.contiguous(), b2.contiguous(), tm)
+    S, A = atok.shape[1], atok.shape[2]
+    tk = torch.empty((1, S, H), dtype=odt, device=dev)
+    a2 = atok.reshape(S, A).contiguous()
+    call("fam_linear_smallk", a2.data_ptr(), A, 0, aw.contiguous().data_ptr(), ab.contiguous().data_ptr(),
+         tk.data_ptr(), H, S, H, A, _stream(atok))
+    return t, tm, tk
+
+
+@adit_tmod.register_fake
+def _(te, inv, w0, b0, w1, b1, w2, b2, atok, aw, ab, fuse_sin):
+    return (atok.new_empty((1, w0.shape[0])), atok.new_empty((1, w2.shape[0])),
+            atok.new_empty((1, atok.shape[1], w0.shape[0])))

@@ -36,6 +36,8 @@ Pinning (what checks each function, see ``tests/test_oracle.py``):
   mot_action_forward        golden vectors from the reference MoT (tiny seeded config)
   wan_vae_encode_first_frame golden vectors from the reference VideoVAE38_.encode (tiny seeded
                             config, two image sizes) + planted slips; vae_avg_down closed forms
+  geak_res_ln / cae_*       against the pinned primitives they compose (layer_norm, attention,
+                            rope_apply, time_mlp, ffn) with planted slips
 """
 from __future__ import annotations
 
@@ -1154,6 +1156,75 @@ def wan_vae_encode_first_frame(p: Params, cfg: WanVaeConfig, image: torch.Tensor
     mu = x[:, :cfg.z_dim]
     mu = (mu - mean.reshape(1, -1, 1, 1)) * (1.0 / std).reshape(1, -1, 1, 1)
     return mu.unsqueeze(2)
+
+
+# ---------------------------------------------------------------------------
+# The GEAK trees' fused operators (FG = src/fastwam-geak/fastwam/models/wan22, CA =
+# src/cae-fastwam/fastwam/models/wan22): each restates the arithmetic of one Triton kernel in
+# fp32 from the oracle's pinned primitives (layer_norm, rms_norm's RMS, attention, the
+# sinusoid, gelu_tanh, silu); tests/test_oracle.py pins each against those primitives.
+# ---------------------------------------------------------------------------
+def geak_res_ln(x: torch.Tensor, parts: Sequence[torch.Tensor], gate: torch.Tensor, eps: float,
+                ln: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
+                ada: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """_fw_resln_kernel (FG/mot.py:1769-1827): t = x + gate * parts[0] (+ parts[1]); returns
+    (t, LN(t) * w + b) with ln = (w, b), or (t, LN(t) * (1 + scale) + shift) with
+    ada = (shift, scale); gate / shift / scale broadcast over rows or given per row."""
+    t = x + gate * parts[0]
+    for extra in parts[1:]:
+        t = t + extra
+    n = layer_norm(t, None, None, eps)
+    if ln is not None:
+        return t, n * ln[0] + ln[1]
+    return t, n * (1 + ada[1]) + ada[0]
+
+
+def cae_qkv_post(qkv: torch.Tensor, qw: torch.Tensor, kw: torch.Tensor, freqs: torch.Tensor, num_heads: int,
+                 eps: float):
+    """_fwam_qkvpost_kernel (CA/mot.py:1369-1456): from qkv [M, 3D]: RMSNorm over D of q and k
+    with their weights, then each (2p, 2p + 1) pair rotated by (cos, sin) = freqs[t, 2p],
+    freqs[t, 2p + 1] of token t; returns q, k, v as [H, M, hd] (head-major)."""
+    M, D3 = qkv.shape
+    D = D3 // 3
+    hd = D // num_heads
+
+    def nr(x, w):
+        y = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) * w
+        y = y.reshape(M, num_heads, hd // 2, 2)
+        c, s_ = freqs[:M, 0::2][:, None, :], freqs[:M, 1::2][:, None, :]
+        r = torch.stack([y[..., 0] * c - y[..., 1] * s_, y[..., 0] * s_ + y[..., 1] * c], -1)
+        return r.reshape(M, num_heads, hd).transpose(0, 1)
+    q, k = nr(qkv[:, :D], qw), nr(qkv[:, D:2 * D], kw)
+    return q, k, qkv[:, 2 * D:].reshape(M, num_heads, hd).transpose(0, 1)
+
+
+def cae_xattn_qn(qr: torch.Tensor, qw: torch.Tensor, k: torch.Tensor, v: torch.Tensor, keep: torch.Tensor,
+                 num_heads: int, eps: float) -> torch.Tensor:
+    """_fwam_xattn_qn_kernel (CA/mot.py:2240-2305): q = qr rsqrt(mean(qr^2) + eps) qw over the whole
+    row, then attention per head over [N, C] keys / values with keep [M, N]; [M, C]."""
+    q = qr * torch.rsqrt((qr * qr).mean(-1, keepdim=True) + eps) * qw
+    return flash_attention(q[None], k[None], v[None], num_heads, keep[None, None])[0]
+
+
+def cae_ctx_kv_norm(g: torch.Tensor, nkw: torch.Tensor, nl: int, ahd: int, eps: float) -> torch.Tensor:
+    """_fwam_ctxkv_norm_kernel (CA/mot.py:2119-2142): layer l's keys g[:, l ahd:(l + 1) ahd]
+    RMS-normalised with nkw[l]; [nl, S, ahd]."""
+    k = g[:, :nl * ahd].reshape(-1, nl, ahd)
+    y = k * torch.rsqrt((k * k).mean(-1, keepdim=True) + eps) * nkw.reshape(nl, ahd)
+    return y.transpose(0, 1)
+
+
+def cae_ffn(x: torch.Tensor, w1, b1, w2, b2) -> torch.Tensor:
+    """_fwam_ffn_kernel (CA/mot.py:2308-2343): W2 GELU(tanh)(W1 x + b1) + b2."""
+    return linear(gelu_tanh(linear(x, w1, b1)), w2, b2)
+
+
+def cae_adit_tmod(t: torch.Tensor, w0, b0, w1, b1, w2, b2, atok: torch.Tensor, aw, ab):
+    """_fwam_adit_tmod_kernel (CA/action_dit.py:127-187): te = sinusoid(t) [FD], x = SiLU(W0 te + b0),
+    tt = W1 x + b1, t_mod = W2 SiLU(tt) + b2, tokens = atok W_aw^T + ab; returns (tt, t_mod, tokens)."""
+    te = sinusoidal_embedding_1d(w0.shape[1], t.reshape(1))
+    tt = linear(silu(linear(te, w0, b0)), w1, b1)
+    return tt, linear(silu(tt), w2, b2), linear(atok, aw, ab)
 
 
 # ---------------------------------------------------------------------------

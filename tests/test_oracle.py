@@ -917,3 +917,72 @@ def test_cosmos_time_embedding_closed_form():
          torch.randn(3 * C, C), "time_embed.norm.weight": torch.ones(C)}
     temb, et = O.cosmos_time_embed(p, cfg, torch.tensor([0.0, 500.0]))
     assert temb.shape == (2, 3 * C) and torch.allclose(et.pow(2).mean(-1), torch.ones(2), atol=1e-5)
+
+
+def test_geak_operator_restatements_pinned():
+    """The GEAK trees' fused operators in the oracle reduce to the pinned primitives: the prefill's
+    residual + LayerNorm / AdaLN (F.layer_norm, adaln), the CAE q/k post-processing (RMSNorm then
+    rope_apply with the interleaved table as a complex one), the CAE cross attention with its
+    whole-row query norm (attention), the context-key norm, the FFN and the time MLP (the
+    golden-pinned ffn / time_mlp); a planted slip in each fails."""
+    g = torch.Generator().manual_seed(77)
+    r = lambda *s: torch.randn(*s, generator=g, dtype=torch.float64)  # noqa: E731
+    S, N, eps = 5, 48, 1e-6
+    x, o1, o2, gate, w, b, sh, sc = r(S, N), r(S, N), r(S, N), r(S, N), r(N), r(N), r(S, N), r(S, N)
+    t, y = O.geak_res_ln(x, [o1], gate, eps, ln=(w, b))
+    assert torch.allclose(y, F.layer_norm(x + gate * o1, (N,), w, b, eps))
+    t2, y2 = O.geak_res_ln(x, [o1, o2], gate, eps, ada=(sh, sc))
+    assert torch.allclose(t2, x + gate * o1 + o2) and torch.allclose(y2, O.adaln(t2, sh, sc, eps))
+    assert (O.geak_res_ln(x, [o1, o2 * gate], gate, eps, ada=(sh, sc))[1] - y2).abs().max() > 1e-2  # gate on o2
+    # CAE q/k post-processing
+    H, hd, M = 3, 16, 6
+    D = H * hd
+    qkv, qw, kw = r(M, 3 * D), r(D), r(D)
+    ang = torch.arange(M, dtype=torch.float64)[:, None] * (10000.0 ** (-torch.arange(0, hd, 2, dtype=torch.float64) / hd))
+    inter = torch.stack([ang.cos(), ang.sin()], -1).reshape(M, hd)            # cos at 2p, sin at 2p + 1
+    q, k, v = O.cae_qkv_post(qkv, qw, kw, inter, H, eps)
+    fc = torch.polar(torch.ones_like(ang), ang).reshape(M, 1, hd // 2)
+
+    def rms(u, wt):
+        return u * torch.rsqrt((u * u).mean(-1, keepdim=True) + eps) * wt
+    qref = O.rope_apply(rms(qkv[:, :D], qw)[None], fc, H)[0].reshape(M, H, hd).transpose(0, 1)
+    kref = O.rope_apply(rms(qkv[:, D:2 * D], kw)[None], fc, H)[0].reshape(M, H, hd).transpose(0, 1)
+    assert torch.allclose(q, qref) and torch.allclose(k, kref)
+    assert torch.equal(v, qkv[:, 2 * D:].reshape(M, H, hd).transpose(0, 1))
+    swapped = torch.stack([ang.sin(), ang.cos()], -1).reshape(M, hd)
+    assert (O.cae_qkv_post(qkv, qw, kw, swapped, H, eps)[0] - qref).abs().max() > 1e-2
+    # CAE cross attention, whole-row query RMSNorm
+    Nk = 7
+    qr, kc, vc = r(M, D), r(Nk, D), r(Nk, D)
+    keep = torch.rand(M, Nk, generator=g) > 0.3
+    keep[:, 0] = True
+    ox = O.cae_xattn_qn(qr, qw, kc, vc, keep, H, eps)
+    assert torch.allclose(ox, O.attention(rms(qr, qw).reshape(M, H, hd).transpose(0, 1)[None],
+                                          kc.reshape(Nk, H, hd).transpose(0, 1)[None],
+                                          vc.reshape(Nk, H, hd).transpose(0, 1)[None], keep[None, None])[0]
+                          .transpose(0, 1).reshape(M, D))
+    per_head = torch.cat([rms(qr[:, i * hd:(i + 1) * hd], qw[i * hd:(i + 1) * hd]) for i in range(H)], 1)
+    assert (O.flash_attention(per_head[None], kc[None], vc[None], H, keep[None, None])[0] - ox).abs().max() > 1e-2
+    # context keys of every layer
+    nl, ahd = 3, 16
+    gk, nkw = r(S, 2 * nl * ahd), r(nl, ahd)
+    kn = O.cae_ctx_kv_norm(gk, nkw, nl, ahd, eps)
+    for l in range(nl):
+        assert torch.allclose(kn[l], rms(gk[:, l * ahd:(l + 1) * ahd], nkw[l]))
+    assert (rms(gk[:, (nl + 1) * ahd:(nl + 2) * ahd], nkw[1]) - kn[1]).abs().max() > 1e-2   # a V slice
+    # FFN and time MLP (golden-pinned ffn / time_mlp)
+    cfg = O.ActionDiTConfig(hidden_dim=32, action_dim=16, ffn_dim=64, text_dim=24, freq_dim=32, num_heads=2,
+                            attn_head_dim=16, num_layers=1)
+    p = {k_: v_.double() for k_, v_ in O.init_action_dit_params(cfg, 5, std=0.2).items()}
+    xa = r(1, 8, 32)
+    assert torch.allclose(O.cae_ffn(xa, p["blocks.0.ffn.0.weight"], p["blocks.0.ffn.0.bias"], p["blocks.0.ffn.2.weight"],
+                                    p["blocks.0.ffn.2.bias"]), O.ffn(p, "blocks.0.", xa))
+    ts = torch.tensor([640.0], dtype=torch.float64)
+    atok = r(1, 8, 16)
+    tt, tm, tk = O.cae_adit_tmod(ts, p["time_embedding.0.weight"], p["time_embedding.0.bias"],
+                                 p["time_embedding.2.weight"], p["time_embedding.2.bias"],
+                                 p["time_projection.1.weight"], p["time_projection.1.bias"], atok,
+                                 p["action_encoder.weight"], p["action_encoder.bias"])
+    t_ref, tm_ref = O.time_mlp(p, cfg, ts)
+    assert torch.allclose(tt, t_ref) and torch.allclose(tm, tm_ref.reshape(1, -1))
+    assert torch.allclose(tk, O.linear(atok, p["action_encoder.weight"], p["action_encoder.bias"]))

@@ -99,6 +99,44 @@ def test_fastwam_ops_trace_with_mutation():
         assert any(t.startswith(op) for t in targets), (op, targets)
 
 
+def test_geak_prefill_and_cae_ops_trace():
+    """The GEAK prefill's and the CAE tree's fastwam:: operators trace as single nodes (fake
+    kernels give the reference's output shapes)."""
+    from fam import fastwam_ops  # noqa: F401
+
+    class M(torch.nn.Module):
+        def forward(self, x, w, b, mb, tm, wn, qkv, qw, kw, freqs, kbuf, vbuf, msk, k, v, g, nkw, a, w1, b1, w2, b2,
+                    te, inv, w0, b0, w1t, b1t, w2t, b2t, atok, aw, ab):
+            y = torch.ops.fastwam.pf_mm.default(x, w, b)
+            yg = torch.ops.fastwam.pf_mm_gelu.default(x, w, b)
+            h3 = torch.ops.fastwam.res_ln1.default(x, y, mb, tm, wn, b, 128, 1e-6)
+            x1, n1 = torch.ops.fastwam.res_ln2.default(x, y, yg, mb, mb, tm, 128, 192, 256, 1e-6)
+            x2, n2 = torch.ops.fastwam.res_ln_tail.default(x1, y, mb, mb, tm, 320, 0, 64, 1e-6)
+            q = torch.ops.fastwam.mot_qkv_post.default(qkv, qw, kw, freqs, kbuf, vbuf, 5, 1e-6)
+            oa = torch.ops.fastwam.mot_attn.default(q, kbuf, vbuf, msk, 2, 16, True)
+            ox = torch.ops.fastwam.xattn_qn.default(oa, qw, k, v, msk, 2, 16, 1e-6)
+            kv = torch.ops.fastwam.ctx_kv_norm.default(g, nkw, 3, 32, 1e-6)
+            op = torch.ops.fastwam.mot_oproj.default(ox, w1, b1)
+            f = torch.ops.fastwam.mot_ffn.default(a, w1t, b1t, w2t, b2t)
+            t, tmod, tk = torch.ops.fastwam.adit_tmod.default(te, inv, w0, b0, w2, b2, w1, b1, atok, aw, ab, 1)
+            return h3, n1, x2, n2, oa, kv, op, f, t, tmod, tk
+
+    args = (_meta(1, 6, 64), _meta(64, 64), _meta(64), _meta(384), _meta(6, 384), _meta(64),
+            _meta(1, 4, 96), _meta(32), _meta(32), _meta(4, 16, dtype=torch.float32), _meta(1, 2, 9, 16),
+            _meta(1, 2, 9, 16), _meta(4, 9, dtype=torch.bool), _meta(1, 9, 32), _meta(1, 9, 32),
+            _meta(9, 192), _meta(3, 32), _meta(1, 4, 32), _meta(32, 32), _meta(32), _meta(32, 32), _meta(32),
+            _meta(1, dtype=torch.float32), _meta(16, dtype=torch.float64), _meta(32, 32), _meta(32), _meta(64, 32),
+            _meta(64), _meta(32, 64), _meta(32), _meta(1, 4, 16), _meta(32, 16), _meta(32))
+    outs, _, targets = _compile_graph(M(), *args)
+    h3, n1, x2, n2, oa, kv, op, f, t, tmod, tk = outs
+    assert h3.shape == n1.shape == x2.shape == n2.shape == (1, 6, 64)
+    assert oa.shape == (1, 4, 32) and kv.shape == (1, 3, 1, 9, 32) and op.shape == (1, 4, 32)
+    assert f.shape == (1, 4, 32) and t.shape == (1, 32) and tmod.shape == (1, 32) and tk.shape == (1, 4, 32)
+    for op_ in ("pf_mm", "pf_mm_gelu", "res_ln1", "res_ln2", "res_ln_tail", "mot_qkv_post", "mot_attn",
+                "xattn_qn", "ctx_kv_norm", "mot_oproj", "mot_ffn", "adit_tmod"):
+        assert any(t_.startswith("fastwam." + op_ + ".") for t_ in targets), (op_, targets)
+
+
 # --------------------------------------------------------------------------- RoPE tables
 def _cat_table(S, Dh, offset=0.0):
     ang = (torch.arange(S, dtype=torch.float64)[:, None] + offset) * \

@@ -246,3 +246,95 @@ def test_rope_real_device_tables_match_complex(layout):
             ops.rope_apply(x, inter.cuda(), 16)
     assert _rel(y, ref) <= 2e-2
     assert torch.equal(y, ops.rope_apply(x, fr.cuda(), 16))
+
+
+# --------------------------------------------------------------------------- GEAK prefill / CAE operators
+def test_geak_prefill_ops(fw):
+    """pf_mm, pf_mm_gelu and the residual + LayerNorm / AdaLN operators of the GEAK prefill at its
+    shape (98 tokens, hidden 3072, per-token t_mod [S, 6N]) against the oracle's restatement of the
+    reference kernel (FG/mot.py:1693-1899)."""
+    g = torch.Generator().manual_seed(91)
+    S, N, K, eps = 98, 3072, 512, 1e-6
+    x, w, b = _rand(g, 1, S, K), _rand(g, N, K, scale=0.05), _rand(g, N, scale=0.1)
+    assert _rel(fw.pf_mm(x.cuda(), w.cuda(), b.cuda()), O.linear(x.float(), w.float(), b.float())) <= 2e-2
+    assert _rel(fw.pf_mm_gelu(x.cuda(), w.cuda(), b.cuda()),
+                O.gelu_tanh(O.linear(x.float(), w.float(), b.float()))) <= 2e-2
+    xr, o1, o2 = _rand(g, 1, S, N), _rand(g, 1, S, N), _rand(g, 1, S, N)
+    mb, mb2, tm = _rand(g, 6 * N, scale=0.3), _rand(g, 6 * N, scale=0.3), _rand(g, S, 6 * N, scale=0.3)
+    wn, bn = (1 + 0.2 * torch.randn(N, generator=g)).to(BF), _rand(g, N, scale=0.2)
+    f = lambda t: t.float()  # noqa: E731
+
+    def ch(m, off):
+        return f(m).reshape(-1)[off:off + N][None, :] + f(tm)[:, off:off + N]
+    dev = [t.cuda() for t in (xr, o1, o2, mb, mb2, tm, wn, bn)]
+    xd, o1d, o2d, mbd, mb2d, tmd, wnd, bnd = dev
+    y1 = fw.res_ln1(xd, o1d, mbd, tmd, wnd, bnd, 2 * N, eps)
+    _, r1 = O.geak_res_ln(f(xr)[0], [f(o1)[0]], ch(mb, 2 * N), eps, ln=(f(wn), f(bn)))
+    x2, y2 = fw.res_ln2(xd, o1d, o2d, mbd, mb2d, tmd, 2 * N, 3 * N, 4 * N, eps)
+    t2, r2 = O.geak_res_ln(f(xr)[0], [f(o1)[0], f(o2)[0]], ch(mb, 2 * N), eps, ada=(ch(mb2, 3 * N), ch(mb2, 4 * N)))
+    x3, y3 = fw.res_ln_tail(xd, o1d, mbd, mb2d, tmd, 5 * N, 0, N, eps)
+    t3, r3 = O.geak_res_ln(f(xr)[0], [f(o1)[0]], ch(mb, 5 * N), eps, ada=(ch(mb2, 0), ch(mb2, N)))
+    errs = [_rel(y1[0], r1), _rel(x2[0], t2), _rel(y2[0], r2), _rel(x3[0], t3), _rel(y3[0], r3)]
+    print("res_ln1 / res_ln2 (x, norm) / res_ln_tail (x, norm):", " ".join(f"{e:.2e}" for e in errs))
+    assert max(errs) <= 2e-2
+
+
+def test_cae_ops(fw):
+    """The CAE action expert's operators at its shape (8 tokens, hidden 32, 24 x 128 heads, 98 + 8
+    joint keys, 129 context keys, 30 layers' context K) against the oracle's restatements of the
+    reference kernels (CA/mot.py:1369-1456, 2119-2142, 2240-2343, 2485-2521; CA/action_dit.py:127-187)."""
+    g = torch.Generator().manual_seed(92)
+    M, H, hd, Sv, Lc, eps = 8, 24, 128, 98, 129, 1e-6
+    D = H * hd
+    f = lambda t: t.float()  # noqa: E731
+    # q/k post-processing into the head-major joint K/V cache
+    qkv = _rand(g, 1, M, 3 * D)
+    qw, kw = (1 + 0.2 * torch.randn(D, generator=g)).to(BF), (1 + 0.2 * torch.randn(D, generator=g)).to(BF)
+    ang = torch.arange(M, dtype=torch.float64)[:, None] * (10000.0 ** (-torch.arange(0, hd, 2, dtype=torch.float64) / hd))
+    freqs = torch.stack([ang.cos(), ang.sin()], -1).reshape(M, hd).float()
+    kbuf, vbuf = _rand(g, 1, H, Sv + M, hd), _rand(g, 1, H, Sv + M, hd)
+    kb, vb = kbuf.cuda(), vbuf.cuda()
+    q = fw.mot_qkv_post(qkv.cuda(), qw.cuda(), kw.cuda(), freqs.cuda(), kb, vb, Sv, eps)
+    rq, rk, rv = O.cae_qkv_post(f(qkv[0]), f(qw), f(kw), freqs.double().float(), H, eps)
+    errs = {"qkv_post q": _rel(q[0], rq), "k rows": _rel(kb[0, :, Sv:], rk), "v rows": _rel(vb[0, :, Sv:], rv)}
+    assert torch.equal(kb[0, :, :Sv].cpu(), kbuf[0, :, :Sv]) and torch.equal(vb[0, :, :Sv].cpu(), vbuf[0, :, :Sv])
+    # joint attention, head-major and row layouts, with a keep mask
+    keep = torch.rand(M, Sv + M, generator=g) > 0.25
+    keep[:, Sv:] = True
+    oa = fw.mot_attn(q, kb, vb, keep.to(torch.uint8).cuda(), H, hd, True)
+    ra = O.attention(f(q.cpu()), f(kb.cpu()), f(vb.cpu()), keep[None, None])[0].transpose(0, 1).reshape(M, D)
+    errs["mot_attn"] = _rel(oa[0], ra)
+    qb = q[0].transpose(0, 1).reshape(1, M, D).contiguous()
+    kr = kb[0].transpose(0, 1).reshape(1, Sv + M, D).contiguous()
+    vr = vb[0].transpose(0, 1).reshape(1, Sv + M, D).contiguous()
+    errs["mot_attn rows"] = _rel(fw.mot_attn(qb, kr, vr, keep.cuda(), H, hd, False)[0], ra)
+    # cross attention with the whole-row query norm
+    qr, kc, vc = _rand(g, 1, M, D), _rand(g, 1, Lc, D), _rand(g, 1, Lc, D)
+    ck = torch.ones(M, Lc, dtype=torch.bool)
+    ck[:, Lc - 20:] = False
+    ox = fw.xattn_qn(qr.cuda(), qw.cuda(), kc.cuda(), vc.cuda(), ck.cuda(), H, hd, eps)
+    errs["xattn_qn"] = _rel(ox[0], O.cae_xattn_qn(f(qr[0]), f(qw), f(kc[0]), f(vc[0]), ck, H, eps))
+    # every layer's context keys
+    nl = 30
+    gk, nkw = _rand(g, Lc, 2 * nl * D), (1 + 0.2 * torch.randn(nl, D, generator=g)).to(BF)
+    kn = fw.ctx_kv_norm(gk.cuda(), nkw.cuda(), nl, D, eps)
+    assert kn.shape == (1, nl, 1, Lc, D)
+    errs["ctx_kv_norm"] = _rel(kn[0, :, 0], O.cae_ctx_kv_norm(f(gk), f(nkw), nl, D, eps))
+    # o projection, FFN, time MLP + action encoder
+    wo, bo = _rand(g, 32, D, scale=0.02), _rand(g, 32, scale=0.1)
+    errs["mot_oproj"] = _rel(fw.mot_oproj(ox, wo.cuda(), bo.cuda())[0], O.linear(f(ox[0].cpu()), f(wo), f(bo)))
+    xa = _rand(g, 1, M, 32)
+    w1, b1, w2, b2 = _rand(g, 256, 32, scale=0.2), _rand(g, 256, scale=0.1), _rand(g, 32, 256, scale=0.06), _rand(g, 32, scale=0.1)
+    errs["mot_ffn"] = _rel(fw.mot_ffn(xa.cuda(), w1.cuda(), b1.cuda(), w2.cuda(), b2.cuda())[0],
+                           O.cae_ffn(f(xa[0]), f(w1), f(b1), f(w2), f(b2)))
+    w0, b0 = _rand(g, 32, 256, scale=0.06), _rand(g, 32, scale=0.1)
+    wt1, bt1, wt2, bt2 = _rand(g, 32, 32, scale=0.2), _rand(g, 32, scale=0.1), _rand(g, 192, 32, scale=0.2), _rand(g, 192, scale=0.1)
+    atok, aw, ab = _rand(g, 1, M, 16), _rand(g, 32, 16, scale=0.25), _rand(g, 32, scale=0.1)
+    inv = (10000.0 ** (-torch.arange(128, dtype=torch.float64) / 128)).cuda()
+    ts = torch.tensor([640.0])
+    t, tmod, tk = fw.adit_tmod(ts.cuda(), inv, w0.cuda(), b0.cuda(), wt1.cuda(), bt1.cuda(), wt2.cuda(), bt2.cuda(),
+                               atok.cuda(), aw.cuda(), ab.cuda(), 1)
+    rt, rtm, rtk = O.cae_adit_tmod(ts, f(w0), f(b0), f(wt1), f(bt1), f(wt2), f(bt2), f(atok), f(aw), f(ab))
+    errs["adit_tmod t"], errs["t_mod"], errs["tokens"] = _rel(t, rt), _rel(tmod, rtm), _rel(tk, rtk)
+    print("CAE operators:", ", ".join(f"{k} {v:.2e}" for k, v in errs.items()))
+    assert max(errs.values()) <= 2e-2, errs
