@@ -1254,6 +1254,19 @@ static void big_plan(int64_t M, int64_t N, int act, int* wfm, int* wfn, bool nar
   }
 }
 
+// 64 x 64 instead of 128 x 128 tiles where the fitted estimate of big_plan_split (below; unsplit:
+// ceil(tiles / (CUs occ)) (c0 + 2 bm bn K / rate occ)) is at least 15% lower: a few hundred rows
+// (the DiT4DiT backbone's 588 video tokens) give 128 x 128 tiles too few workgroups to fill the
+// chip (588 x 2048 x 2048: 80 of 256 CUs), which big_plan's tile-area count does not see.
+static bool big_prefers_64(int64_t M, int64_t N, int64_t K) {
+  const int cus = fam_host::device_cus();
+  auto est = [&](int64_t bm, double c0, double rate) {
+    const int64_t tiles = ((M + bm - 1) / bm) * ((N + bm - 1) / bm);
+    return std::ceil((double)tiles / (2.0 * cus)) * (c0 + 2.0 * (double)(bm * bm) * (double)K / (rate * 1e6) * 2.0);
+  };
+  return est(64, 1.0, 3.0) < 0.85 * est(128, 4.0, 5.5);
+}
+
 // K split of the big kernel (fam_gemm_ws, and fam_gemm_partial above 144 rows).  Estimated time
 // of a tile shape with z splits, a least-squares fit to gfx950 measurements (15 shapes from
 // 512 x 6144 x 4096 to 8192^3, every tile, 1-8 splits):
@@ -1376,7 +1389,7 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
     if (fm == 8) launch_big<8, 8>(a, s);
     else if (fm == 7) launch_big<7, 8>(a, s);
     else if (fm == 4 && fn == 3) launch_big<4, 3>(a, s);
-    else if (fm == 4) {
+    else if (fm == 4 && !big_prefers_64(d->M, d->N, d->K)) {
       // at most one 128 x 128 workgroup per CU: two K groups per workgroup (an even block count)
       const int64_t tiles = ((d->M + 127) / 128) * ((d->N + 127) / 128);
       if (tiles <= fam_host::device_cus() && (d->K / 64) % 2 == 0) launch_big<4, 4, 2>(a, s);
