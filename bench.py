@@ -58,7 +58,7 @@ def parse():
     ap.add_argument("--no-policy-calls", action="store_true",
                     help="skip the FastWAM / CAE-FastWAM policy-call figures added to the default line")
     ap.add_argument("--cpu-sample-s", type=float, default=20.0, help="CPU baseline time budget")
-    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "d4d", "hbm", "prefill", "fastwam", "cae"], default="c1",
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "d4d", "hbm", "prefill", "fastwam", "cae", "gemm"], default="c1",
                     help="c1: the action-DiT denoise loop (the metric); c2: one long-sequence video DiT block "
                          "(config 2 shape), reported as ms per 30-block forward with MFMA utilisation; c3: the "
                          "compact expert loop + action-VAE decoder at B=1 and B=256; c4: the DiT4DiT policy call "
@@ -69,7 +69,8 @@ def parse():
                          "prefill: the MoT video K/V prefill of the FastWAM call (30 blocks, 98 video tokens); "
                          "fastwam: one FastWAM policy call at the real model shape (VAE encode + prefill + 10-step "
                          "MoT action loop, one graph); cae: the same call with the CAE-FastWAM action expert "
-                         "(hidden 32) and its action-VAE decoder")
+                         "(hidden 32) and its action-VAE decoder; gemm: fam_gemm against hipBLASLt "
+                         "(torch.nn.functional.linear) at the backbones' large-M shapes")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     ap.add_argument("--traffic-from", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "COPY_FETCH_DIR", "COPY_WRITE_DIR"),
@@ -1060,6 +1061,93 @@ def bench_c3(args):
     print(json.dumps(out), flush=True)
 
 
+# (M, N, K, role) of the large-M products the backbones issue, plus the square reference point
+GEMM_SHAPES = (
+    (1560, 9216, 3072, "config 2 q|k|v"),
+    (1560, 3072, 3072, "config 2 o / cross q / cross o"),
+    (1560, 14336, 3072, "config 2 FFN up"),
+    (1560, 3072, 14336, "config 2 FFN down"),
+    (1560, 9216, 14336, "1560 x 9216 x 14336 (grid point)"),
+    (1560, 14336, 14336, "1560 x 14336 x 14336 (grid point)"),
+    (512, 6144, 3072, "config 2 context k|v of one block"),
+    (1560, 24576, 1024, "config 1 context k|v of 12 blocks"),
+    (2048, 6144, 2048, "config 4 q|k|v"),
+    (2048, 2048, 2048, "config 4 o / cross q / cross o"),
+    (2048, 8192, 2048, "config 4 FFN up"),
+    (2048, 2048, 8192, "config 4 FFN down"),
+    (588, 6144, 2048, "DiT4DiT RoboCasa q|k|v (588 tokens)"),
+    (588, 8192, 2048, "DiT4DiT RoboCasa FFN up"),
+    (588, 2048, 8192, "DiT4DiT RoboCasa FFN down"),
+    (8192, 8192, 8192, "8192^3"),
+)
+
+
+def bench_gemm(args):
+    """Large-M GEMM against the library the reference calls: for each (M, N, K), y = x w^T + b in
+    bf16 through fam_gemm (the large-M kernel and its planner), fam_gemm_ws (the same with a
+    K-split workspace) and torch.nn.functional.linear (hipBLASLt on this image), each timed as
+    the mean of back-to-back launches between two HIP events on one stream, after warmups.
+    Outputs of the two paths are compared (max |d| relative to max |y|) so the table times
+    the same product."""
+    import torch
+    import torch.nn.functional as F
+    from fam import ops
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    g = torch.Generator("cpu").manual_seed(55)
+    st = torch.cuda.current_stream()
+    reps = max(args.steps, 5)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        for _ in range(reps):
+            fn()
+        e1.record(st)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    rows = []
+    for M, N, K, role in GEMM_SHAPES:
+        x = torch.randn(M, K, generator=g).to(dev, torch.bfloat16)
+        w = (torch.randn(N, K, generator=g) * K ** -0.5).to(dev, torch.bfloat16)
+        b = (torch.randn(N, generator=g) * 0.1).to(dev, torch.bfloat16)
+        y = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+        nws = ops.gemm_ws_floats(M, N, K)
+        ws = torch.empty(max(nws, 1), device=dev, dtype=torch.float32)
+        us_fam = timed(lambda: ops.gemm(x, w, b, y))
+        y_fam = y.clone()
+        us_ws = timed(lambda: ops.gemm(x, w, b, y, ws=ws)) if nws > 0 else None
+        ref = [None]
+        us_lt = timed(lambda: ref.__setitem__(0, F.linear(x, w, b)))
+        d = ((y_fam.float() - ref[0].float()).abs().max() / ref[0].float().abs().max()).item()
+        fl = 2.0 * M * N * K
+        best = min(u for u in (us_fam, us_ws) if u is not None)
+        rows.append({"shape": f"{M}x{N}x{K}", "role": role, "fam_gemm_us": round(us_fam, 2),
+                     "fam_gemm_ws_us": round(us_ws, 2) if us_ws is not None else None,
+                     "hipblaslt_us": round(us_lt, 2), "fam_best_tflops": round(fl / best * 1e-6, 1),
+                     "hipblaslt_tflops": round(fl / us_lt * 1e-6, 1), "ratio_fam_over_hipblaslt": round(us_lt / best, 3),
+                     "max_rel_diff": float(f"{d:.2e}")})
+        r = rows[-1]
+        log(f"{r['shape']:>20s} {role:38s} fam {r['fam_gemm_us']:9.1f} ws {r['fam_gemm_ws_us'] or 0:9.1f} "
+            f"hipBLASLt {r['hipblaslt_us']:9.1f} us -> {r['fam_best_tflops']:7.1f} vs {r['hipblaslt_tflops']:7.1f} "
+            f"TFLOP/s (rel diff {d:.1e})")
+        del x, w, b, y, ws, y_fam, ref
+        torch.cuda.empty_cache()
+    lib_name = str(torch.backends.cuda.preferred_blas_library())
+    out = {"metric": "large-M GEMM TFLOP/s, fam_gemm against hipBLASLt (torch.nn.functional.linear)",
+           "value": round(min(r["ratio_fam_over_hipblaslt"] for r in rows), 3), "unit": "min ratio (hipBLASLt us / fam us)",
+           "n_gpus": 1, "steps": reps, "warmup": 3, "ms_per_step": None, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic: seeded N(0,1) x, N(0,1/K) w",
+           "config": {"workload": "y = x w^T + b at the backbones' large-M shapes and 8192^3",
+                      "torch_blas_library": lib_name},
+           "table": rows}
+    print(json.dumps(out), flush=True)
+
+
 # --------------------------------------------------------------------------- main
 def main():
     args = parse()
@@ -1101,6 +1189,9 @@ def main():
         return
     if args.workload == "cae":
         bench_cae(args)
+        return
+    if args.workload == "gemm":
+        bench_gemm(args)
         return
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
