@@ -1383,7 +1383,7 @@ __global__ __launch_bounds__(256 * KW, 2 / KW) void attn_long_kernel(AttnArgs a,
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mraw = fmaxf(mraw, st[kt][r]);
-    mraw = fmaxf(mraw, __shfl_xor(mraw, 32, kWave));
+    mraw = max_xor32(mraw);
     const float mloc = mraw * sl2;   // sl2 > 0
     if (__any(mloc > m_run + 8.0f)) {
       const float m_new = fmaxf(m_run, mloc);
@@ -1405,7 +1405,7 @@ __global__ __launch_bounds__(256 * KW, 2 / KW) void attn_long_kernel(AttnArgs a,
         psum += pv;
         pf[kt][r / 8][r % 8] = to_bf(pv);
       }
-    psum += __shfl_xor(psum, 32, kWave);
+    psum = sum_xor32(psum);
     l_run += psum;
     // O^T += V^T P^T: k-step c of half kt covers keys kt*32 + 16c + {4hh..4hh+3, 8+4hh..8+4hh+3}
 #pragma unroll

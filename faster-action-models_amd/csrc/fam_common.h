@@ -39,15 +39,55 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Sum over the four lane groups {l, l^16, l^32, l^48} (MFMA 16x16 column reductions).
+// Lane l's value and lane (l ^ 16)'s / (l ^ 32)'s, lower lane first, through the gfx950 lane
+// swaps (VALU, no LDS round trip as __shfl_xor's ds_bpermute): for a commutative op, r[0] op r[1]
+// is the same in both lanes of a pair and equals v op __shfl_xor(v, 16 / 32).
+__device__ __forceinline__ void pair_xor16(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void pair_xor32(float v, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  float a, b;
+  pair_xor32(v, a, b);
+  return a + b;
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  float a, b;
+  pair_xor32(v, a, b);
+  return fmaxf(a, b);
+}
+
+// Sum over the four lane groups {l, l^16, l^32, l^48} (MFMA 16x16 column reductions); the same
+// pairing and order as v += shfl_xor(v, 16); v += shfl_xor(v, 32).
 __device__ __forceinline__ float group4_sum(float v) {
-  v += __shfl_xor(v, 16, kWave);
-  v += __shfl_xor(v, 32, kWave);
-  return v;
+  float a, b;
+  pair_xor16(v, a, b);
+  return sum_xor32(a + b);
 }
 __device__ __forceinline__ float group4_max(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16, kWave));
-  v = fmaxf(v, __shfl_xor(v, 32, kWave));
+  float a, b;
+  pair_xor16(v, a, b);
+  return max_xor32(fmaxf(a, b));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+// Sum over the 16 lanes of a row, the same in every lane: the pairs of the xor butterfly 1, 2,
+// 4, 8 through DPP (quad_perm [1,0,3,2], [2,3,0,1]; row_half_mirror pairs the two equal quads of
+// each half-row, row_mirror the two equal half-rows), so the result equals the __shfl_xor loop.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  v += dpp_mov<0x140>(v);
   return v;
 }
 

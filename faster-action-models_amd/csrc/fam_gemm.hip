@@ -370,10 +370,8 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(GemmArgs g) {
   if constexpr (FOLD) {
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
-      s1[i] += __shfl_xor(s1[i], 16, kWave);
-      s2[i] += __shfl_xor(s2[i], 16, kWave);
-      s1[i] += __shfl_xor(s1[i], 32, kWave);
-      s2[i] += __shfl_xor(s2[i], 32, kWave);
+      s1[i] = group4_sum(s1[i]);
+      s2[i] = group4_sum(s2[i]);
       if (lg == 0) {
         s_st[wave][i * 16 + l16] = make_float2(s1[i], s2[i]);
         if (wave == 0) s_piv[i * 16 + l16] = piv[i];

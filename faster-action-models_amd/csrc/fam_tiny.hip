@@ -90,8 +90,8 @@ struct TinySmem {
     } f;
     struct {
       float m[4][NCB * 16], l[4][NCB * 16];
-      float acc[4][W][NCB * 16 + 1];
-    } mg;                                                // per-wave softmax states
+      float acc[4][NCB * 16][W + 8];                     // [wave][column][dim]: W + 8 keeps 16-byte
+    } mg;                                                // accesses of 32 lanes in distinct banks
   } u;
 };
 
@@ -123,13 +123,11 @@ __device__ __forceinline__ void row_norm(TinySmem<W, NCB>& sm, int S, float eps,
   const int s = threadIdx.x >> 4, j = threadIdx.x & 15;
   const float x0 = sm.x[s][2 * j], x1 = sm.x[s][2 * j + 1];
   float sum = x0 + x1;
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o, kWave);
+  sum = row16_sum(sum);
   const float mean = sum * (1.0f / TH);
   const float d0 = x0 - mean, d1 = x1 - mean;
   float var = d0 * d0 + d1 * d1;
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) var += __shfl_xor(var, o, kWave);
+  var = row16_sum(var);
   const float rstd = rsqrtf(var * (1.0f / TH) + eps);
   float y0 = d0 * rstd, y1 = d1 * rstd;
   if (adaln) {
@@ -371,12 +369,96 @@ __device__ __forceinline__ void kv_patch(TinySmem<W, NCB>& sm, const KvSrc& src,
   }
 }
 
+// One 32-key block of a wave: V rows into the wave's tile, scores, online softmax, O^T += V^T P^T.
 template <int W, int NCB>
+__device__ __forceinline__ void attend_block(const TinyArgs& a, const KvBlock<W>& kv, int blk, int n,
+                                             const uint8_t* mask, int64_t mask_rs, const bf16x8 (&qf)[NCB][W / 32],
+                                             const int (&qs)[NCB], float (&m)[NCB], float (&lsum)[NCB],
+                                             f32x4 (&acc)[W / 16][NCB], bf16 (*vt)[W + 16]) {
+  constexpr int WK = W / 32, WT = W / 16, CPR = W / 8;
+  const int lane = threadIdx.x & 63, l16 = lane & 15, lg = lane >> 4;
+  // the block's V rows into the wave's tile
+#pragma unroll
+  for (int i = 0; i < WT; ++i) {
+    const int ci = lane + 64 * i, row = ci / CPR, c8 = ci - row * CPR;
+    *reinterpret_cast<bf16x8*>(&vt[row][c8 * 8]) = kv.v[i];
+  }
+  // scores of the block: keys 32 blk + 16 sub + 4 lg + e, column cb * 16 + l16
+  bf16x8 pf[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    float sc[2][4];
+    float mb = -INFINITY;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < WK; ++kb) d = mfma16(kv.k[sub][kb], qf[cb][kb], d);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int kk = blk * 32 + sub * 16 + lg * 4 + e;
+        bool ok = kk < n;
+        if (mask != nullptr) ok = ok && (qs[cb] < 0 || mask[(int64_t)qs[cb] * mask_rs + kk] != 0);
+        const float x = ok ? d[e] * a.scale_log2 : -INFINITY;
+        sc[sub][e] = x;
+        mb = fmaxf(mb, x);
+      }
+    }
+    mb = group4_max(mb);
+    // the running max moves only when a score passes it by more than 2^8 (exp2 units), so p <= 2^8
+    // in between (exact in fp32, bf16 keeps its relative precision) and the accumulators are
+    // rescaled only on the blocks where some column of the wave moved (the first, mostly)
+    const bool up = mb > m[cb] + 8.0f;
+    const float mn = up ? mb : m[cb];
+    const float ms = mn == -INFINITY ? 0.f : mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p = __builtin_amdgcn_exp2f(sc[sub][e] - ms);
+        ps += p;
+        pf[cb][sub * 4 + e] = to_bf(p);
+      }
+    ps = group4_sum(ps);
+    if (__any(up)) {
+      const float alpha = __builtin_amdgcn_exp2f(m[cb] - ms);   // unchanged max: 1; -inf: 0
+      lsum[cb] = lsum[cb] * alpha + ps;
+#pragma unroll
+      for (int dt = 0; dt < WT; ++dt) acc[dt][cb] *= alpha;
+    } else {
+      lsum[cb] += ps;
+    }
+    m[cb] = mn;
+  }
+  // O^T += V^T P^T: V^T fragment rows = dims 16 dt + l16, k = keys {4 lg..+3, 16 + 4 lg..+3}
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+#pragma unroll
+  for (int dt = 0; dt < WT; ++dt) {
+    const int key = lg * 4 + (l16 >> 2), dim = dt * 16 + 4 * (l16 & 3);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&vt[key][dim]);
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&vt[key + 16][dim]);
+    const s16x8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    const bf16x8 vf = __builtin_bit_cast(bf16x8, v8);
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) acc[dt][cb] = mfma16(vf, pf[cb], acc[dt][cb]);
+  }
+}
+
+// PD blocks of a wave in flight: PD = 1 for any key source; PD = 2 or 3 only for keys wholly in
+// segment 0 (src.n1 == 0), as a ring of PD + 1 named register blocks (the loop unrolled by
+// PD + 1, so no slot is indexed at run time) whose loads are all issued, past the end too
+// (kv_load_global reads row 0 there), so the wait before each block counts exactly the loads
+// issued after it.
+template <int PD, int W, int NCB>
 __device__ __forceinline__ void attend(const TinyArgs& a, TinySmem<W, NCB>& sm, const KvSrc& src, const uint8_t* mask,
                                        int64_t mask_rs, KvBlock<W>& kv, bool prefetched) {
-  constexpr int WK = W / 32, WT = W / 16, CPR = W / 8;
+  constexpr int WK = W / 32, WT = W / 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lg = lane >> 4;
-  const int S = a.S, DH = a.DH, HPW = W / DH, nc = HPW * S;
+  const int S = a.S, DH = a.DH;
+  const int dsh = __builtin_ctz(DH), nc = (W >> dsh) * S;
   const int n = src.n0 + src.n1, nblk = (n + 31) / 32;
   // Q^T fragments: column c = (head hh, token s); dims of other heads read as zero
   bf16x8 qf[NCB][WK];
@@ -389,7 +471,7 @@ __device__ __forceinline__ void attend(const TinyArgs& a, TinySmem<W, NCB>& sm, 
     for (int kb = 0; kb < WK; ++kb) {
       const int d0 = kb * 32 + lg * 8;
       const bf16x8 x = *reinterpret_cast<const bf16x8*>(&sm.q[c < nc ? s : 0][d0]);
-      qf[cb][kb] = (c < nc && d0 / DH == hh) ? x : zero8();
+      qf[cb][kb] = (c < nc && (d0 >> dsh) == hh) ? x : zero8();
     }
   }
   float m[NCB], lsum[NCB];
@@ -402,82 +484,55 @@ __device__ __forceinline__ void attend(const TinyArgs& a, TinySmem<W, NCB>& sm, 
     for (int dt = 0; dt < WT; ++dt) acc[dt][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   bf16(*vt)[W + 16] = sm.vt[wave];
-  if (prefetched && src.n1 > 0 && wave * 32 + 32 > src.n0) kv_patch(sm, src, wave, kv);
-  if (!prefetched && wave < nblk) {
-    if (src.n1 == 0)
-      kv_load_global<W>(src, wave, kv);
-    else
-      kv_load(sm, src, wave, kv);
-  }
-  for (int blk = wave; blk < nblk; blk += 4) {
-    // the wave's next block in flight while this one is computed
-    KvBlock<W> nx;
-    if (blk + 4 < nblk) {
+  if constexpr (PD == 1) {
+    if (prefetched && src.n1 > 0 && wave * 32 + 32 > src.n0) kv_patch(sm, src, wave, kv);
+    if (!prefetched && wave < nblk) {
       if (src.n1 == 0)
-        kv_load_global<W>(src, blk + 4, nx);
+        kv_load_global<W>(src, wave, kv);
       else
-        kv_load(sm, src, blk + 4, nx);
+        kv_load(sm, src, wave, kv);
     }
-    // the block's V rows into the wave's tile
-#pragma unroll
-    for (int i = 0; i < WT; ++i) {
-      const int ci = lane + 64 * i, row = ci / CPR, c8 = ci - row * CPR;
-      *reinterpret_cast<bf16x8*>(&vt[row][c8 * 8]) = kv.v[i];
-    }
-    // scores of the block: keys 32 blk + 16 sub + 4 lg + e, column cb * 16 + l16
-    bf16x8 pf[NCB];
-#pragma unroll
-    for (int cb = 0; cb < NCB; ++cb) {
-      float sc[2][4];
-      float mb = -INFINITY;
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < WK; ++kb) d = mfma16(kv.k[sub][kb], qf[cb][kb], d);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int kk = blk * 32 + sub * 16 + lg * 4 + e;
-          bool ok = kk < n;
-          if (mask != nullptr) ok = ok && (qs[cb] < 0 || mask[(int64_t)qs[cb] * mask_rs + kk] != 0);
-          const float x = ok ? d[e] * a.scale_log2 : -INFINITY;
-          sc[sub][e] = x;
-          mb = fmaxf(mb, x);
-        }
+    for (int blk = wave; blk < nblk; blk += 4) {
+      // the wave's next block in flight while this one is computed
+      KvBlock<W> nx;
+      if (blk + 4 < nblk) {
+        if (src.n1 == 0)
+          kv_load_global<W>(src, blk + 4, nx);
+        else
+          kv_load(sm, src, blk + 4, nx);
       }
-      mb = group4_max(mb);
-      const float mn = fmaxf(m[cb], mb);
-      const float ms = mn == -INFINITY ? 0.f : mn;
-      const float alpha = __builtin_amdgcn_exp2f(m[cb] - ms);
-      float ps = 0.f;
-#pragma unroll
-      for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p = __builtin_amdgcn_exp2f(sc[sub][e] - ms);
-          ps += p;
-          pf[cb][sub * 4 + e] = to_bf(p);
-        }
-      lsum[cb] = lsum[cb] * alpha + group4_sum(ps);
-      m[cb] = mn;
-#pragma unroll
-      for (int dt = 0; dt < WT; ++dt) acc[dt][cb] *= alpha;
+      attend_block<W, NCB>(a, kv, blk, n, mask, mask_rs, qf, qs, m, lsum, acc, vt);
+      if (blk + 4 < nblk) kv = nx;
     }
-    // O^T += V^T P^T: V^T fragment rows = dims 16 dt + l16, k = keys {4 lg..+3, 16 + 4 lg..+3}
-    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-#pragma unroll
-    for (int dt = 0; dt < WT; ++dt) {
-      const int key = lg * 4 + (l16 >> 2), dim = dt * 16 + 4 * (l16 & 3);
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&vt[key][dim]);
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&vt[key + 16][dim]);
-      const s16x8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      const bf16x8 vf = __builtin_bit_cast(bf16x8, v8);
-#pragma unroll
-      for (int cb = 0; cb < NCB; ++cb) acc[dt][cb] = mfma16(vf, pf[cb], acc[dt][cb]);
+  } else {
+    static_assert(PD == 2 || PD == 3, "ring depth");
+    // slot j of step j is consumed; the block PD steps ahead goes into the slot of step j - 1
+    KvBlock<W> r0, r1, r2, r3;
+    if (prefetched)
+      r0 = kv;
+    else
+      kv_load_global<W>(src, wave, r0);
+    kv_load_global<W>(src, wave + 4, r1);
+    if constexpr (PD == 3) kv_load_global<W>(src, wave + 8, r2);
+#define FAM_TINY_STEP(J, CUR, NXT)                                                                        \
+  {                                                                                                       \
+    const int blk = base + 4 * (J);                                                                       \
+    kv_load_global<W>(src, blk + 4 * PD, NXT);                                                            \
+    if (blk < nblk) attend_block<W, NCB>(a, CUR, blk, n, mask, mask_rs, qf, qs, m, lsum, acc, vt);       \
+  }
+    for (int base = wave; base < nblk; base += 4 * (PD + 1)) {
+      if constexpr (PD == 3) {
+        FAM_TINY_STEP(0, r0, r3)
+        FAM_TINY_STEP(1, r1, r0)
+        FAM_TINY_STEP(2, r2, r1)
+        FAM_TINY_STEP(3, r3, r2)
+      } else {
+        FAM_TINY_STEP(0, r0, r2)
+        FAM_TINY_STEP(1, r1, r0)
+        FAM_TINY_STEP(2, r2, r1)
+      }
     }
-    if (blk + 4 < nblk) kv = nx;
+#undef FAM_TINY_STEP
   }
   // merge the waves' states through LDS, in wave order
   if (lg == 0) {
@@ -491,24 +546,39 @@ __device__ __forceinline__ void attend(const TinyArgs& a, TinySmem<W, NCB>& sm, 
   for (int dt = 0; dt < WT; ++dt)
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sm.u.mg.acc[wave][dt * 16 + lg * 4 + e][cb * 16 + l16] = acc[dt][cb][e];
+      *reinterpret_cast<f32x4*>(&sm.u.mg.acc[wave][cb * 16 + l16][dt * 16 + lg * 4]) = acc[dt][cb];
   lds_barrier();
-  for (int idx = threadIdx.x; idx < S * W; idx += 256) {
-    const int s = idx / W, d = idx - s * W, c = (d / DH) * S + s;
-    float mx = -INFINITY;
+  // one thread per (token, 8 dims of one head): the waves' weights once, then two 16-byte reads
+  // per wave (head_dim is a power of two: W and a multiple of it are)
+  if (threadIdx.x < S * (W / 8)) {
+    const int idx = threadIdx.x, s = idx / (W / 8), d0 = (idx - s * (W / 8)) * 8, c = (d0 >> dsh) * S + s;
+    float mw[4], mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sm.u.mg.m[w][c]);
-    float num = 0.f, den = 0.f;
-    if (mx != -INFINITY) {
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float f = __builtin_amdgcn_exp2f(sm.u.mg.m[w][c] - mx);
-        num += f * sm.u.mg.acc[w][d][c];
-        den += f * sm.u.mg.l[w][c];
-      }
+    for (int w = 0; w < 4; ++w) {
+      mw[w] = sm.u.mg.m[w][c];
+      mx = fmaxf(mx, mw[w]);
     }
-    sm.o[s][d] = to_bf(den > 0.f ? num / den : 0.f);
+    const float ms = mx == -INFINITY ? 0.f : mx;
+    float f[4], den = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      f[w] = __builtin_amdgcn_exp2f(mw[w] - ms);
+      den += f[w] * sm.u.mg.l[w][c];
+    }
+    f32x4 n0 = f32x4{0.f, 0.f, 0.f, 0.f}, n1 = n0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      n0 += f[w] * *reinterpret_cast<const f32x4*>(&sm.u.mg.acc[w][c][d0]);
+      n1 += f[w] * *reinterpret_cast<const f32x4*>(&sm.u.mg.acc[w][c][d0 + 4]);
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = to_bf(n0[e] * inv);
+      o[4 + e] = to_bf(n1[e] * inv);
+    }
+    *reinterpret_cast<bf16x8*>(&sm.o[s][d0]) = o;
   }
   lds_barrier();
 }
@@ -576,8 +646,7 @@ __device__ __forceinline__ void direct_sumsq(TinySmem<W, NCB>& sm, int which, in
     const float x = sm.u.raw[s][rawcol + j * (W / 16) + e];
     acc += x * x;
   }
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) acc += __shfl_xor(acc, o, kWave);
+  acc = row16_sum(acc);
   if (j == 0 && s < S) sm.ss[which][s] = acc;
 }
 
@@ -590,15 +659,23 @@ struct PartLoads {
   f32x4 v[8];
 };
 
+// loads of round `round` that any thread needs (the same count for the whole workgroup)
+__device__ __forceinline__ int part_loads(int G, int NGI, int round) {
+  return min(8, (G + NGI - 1) / NGI - 8 * round);
+}
+
 __device__ __forceinline__ void part_issue(const float* part, int b, int G, int S, int round, PartLoads& pl) {
-  const int NV = S * 8, NGI = min(4, 256 / NV), tid = threadIdx.x;
+  const int NV = S * 8, NGI = min(4, 256 / NV), tid = threadIdx.x, nu = part_loads(G, NGI, round);
   const int gi = tid / NV, slot = tid - gi * NV, s = slot >> 3, n4 = slot & 7;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    const int g = gi + NGI * (8 * round + u);
-    const bool ok = gi < NGI && g < G;
-    // out-of-range slots read slice 0's (finite) row; part_reduce weighs them by 0
-    pl.v[u] = *reinterpret_cast<const f32x4*>(part + (((size_t)b * G + (ok ? g : 0)) * S + (ok ? s : 0)) * TH + 4 * (ok ? n4 : 0));
+    if (u < nu) {
+      const int g = gi + NGI * (8 * round + u);
+      const bool ok = gi < NGI && g < G;
+      // out-of-range slots read slice 0's (finite) row; part_reduce weighs them by 0
+      pl.v[u] = *reinterpret_cast<const f32x4*>(part + (((size_t)b * G + (ok ? g : 0)) * S + (ok ? s : 0)) * TH +
+                                                4 * (ok ? n4 : 0));
+    }
   }
 }
 
@@ -610,10 +687,11 @@ __device__ __forceinline__ void part_reduce(TinySmem<W, NCB>& sm, const float* p
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int round = 0; round * 8 * NGI < G; ++round) {
     if (round > 0) part_issue(part, b, G, S, round, pl);
+    const int nu = part_loads(G, NGI, round);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int g = gi + NGI * (8 * round + u);
-      acc += pl.v[u] * ((gi < NGI && g < G) ? 1.0f : 0.0f);
+      if (u < nu) acc += pl.v[u] * ((gi < NGI && g < G) ? 1.0f : 0.0f);
     }
   }
   if (gi < NGI) *reinterpret_cast<f32x4*>(&sm.u.f.red[gi][s][4 * n4]) = acc;
@@ -836,7 +914,7 @@ __device__ __forceinline__ void phase_self(const TinyArgs& a, TinySmem<W, NCB>& 
   lds_barrier();
 
   // ---- attention over [video K/V ; action K/V], then the slice's o-projection partial
-  attend(a, sm, src, a.mask, a.mask_rs, kv, pre);
+  attend<1>(a, sm, src, a.mask, a.mask_rs, kv, pre);
   oproj_store(sm, of, a.part_s + ((size_t)b * G + g) * S * TH, S);
 }
 
@@ -873,8 +951,9 @@ __device__ __forceinline__ void phase_cross(const TinyArgs& a, TinySmem<W, NCB>&
   src.rs0 = a.ctx_ld;
   src.k0 = a.ctxkv + (size_t)l * 2 * A + g * W;
   src.v0 = a.ctxkv + (size_t)l * 2 * A + A + g * W;
-  const bool pre = a.Lc > wave * 32;
-  if (pre) kv_load_global<W>(src, wave, kv);
+  // every wave's first block is loaded, also by a wave without one (rows past Lc read row 0): an
+  // unconditional load keeps the block in registers where the attention picks it up
+  kv_load_global<W>(src, wave, kv);
   const bf16* modt = a.mods + ((size_t)t * L + l) * 6 * TH;
   const bf16x2 gmsa = *reinterpret_cast<const bf16x2*>(modt + 2 * TH + 2 * j_r);
   const bf16x2 ob = *reinterpret_cast<const bf16x2*>(a.o_b + (size_t)l * TH + 2 * j_r);
@@ -920,7 +999,7 @@ __device__ __forceinline__ void phase_cross(const TinyArgs& a, TinySmem<W, NCB>&
   }
   norm_slice(a, sm, 2, 0, sm.q, a.cnq_w + (size_t)l * A + g * W, false);
   lds_barrier();
-  attend(a, sm, src, nullptr, 0, kv, pre);
+  attend<(W == 32 ? 3 : W == 64 ? 2 : 1)>(a, sm, src, nullptr, 0, kv, true);
   oproj_store(sm, of, a.part_c + ((size_t)b * G + g) * S * TH, S);
 }
 
@@ -963,33 +1042,46 @@ __device__ __forceinline__ void phase_final(const TinyArgs& a, TinySmem<W, NCB>&
   head_euler(a, sm, lat_old, hbj, delta, a.out + (size_t)b * S * Da);
 }
 
-// One phase per launch: a loop over phases inside one kernel lets the compiler hoist every
-// lane's addresses of every phase out of the loop and keep them live (spilling to scratch).
+// One phase per launch, one kernel per phase kind.  A loop over phases inside one kernel lets the
+// compiler hoist every lane's addresses of every phase out of the loop and keep them live
+// (spilling to scratch); one kernel for all three kinds loads every kind's pointers from the
+// kernel arguments at entry and spills scalar registers.
 template <int W, int NCB>
-__global__ __launch_bounds__(256, 1) void tiny_expert_kernel(TinyArgs a) {
+__global__ __launch_bounds__(256, 1) void tiny_self_kernel(TinyArgs a) {
   __shared__ TinySmem<W, NCB> sm;
-  const int g = blockIdx.x, b = blockIdx.y;
-  const int per = 2 * a.L, p = a.p0;
-  if (p == per * a.T) {
-    phase_final(a, sm, b);
-  } else {
-    const int t = p / per, r = p - t * per, l = r >> 1;
-    if (r & 1)
-      phase_cross(a, sm, g, b, t, l);
-    else
-      phase_self(a, sm, g, b, t, l);
-  }
+  const int per = 2 * a.L, t = a.p0 / per, l = (a.p0 - t * per) >> 1;
+  phase_self(a, sm, blockIdx.x, blockIdx.y, t, l);
+}
+
+template <int W, int NCB>
+__global__ __launch_bounds__(256, 1) void tiny_cross_kernel(TinyArgs a) {
+  __shared__ TinySmem<W, NCB> sm;
+  const int per = 2 * a.L, t = a.p0 / per, l = (a.p0 - t * per) >> 1;
+  phase_cross(a, sm, blockIdx.x, blockIdx.y, t, l);
+}
+
+template <int W, int NCB>
+__global__ __launch_bounds__(256, 1) void tiny_final_kernel(TinyArgs a) {
+  __shared__ TinySmem<W, NCB> sm;
+  phase_final(a, sm, blockIdx.y);
 }
 
 template <int W, int NCB>
 int launch_tiny(const TinyArgs& a0, int64_t p0, int64_t p1, hipStream_t st) {
   TinyArgs a = a0;
   const int64_t last = 2LL * a.L * a.T;
-  void (*kern)(TinyArgs) = tiny_expert_kernel<W, NCB>;
+  void (*self_k)(TinyArgs) = tiny_self_kernel<W, NCB>;
+  void (*cross_k)(TinyArgs) = tiny_cross_kernel<W, NCB>;
+  void (*final_k)(TinyArgs) = tiny_final_kernel<W, NCB>;
   for (int64_t p = p0; p < p1; ++p) {
     a.p0 = (int)p;
     a.p1 = (int)p + 1;
-    FAM_LAUNCH(kern, dim3(p == last ? 1 : a.G, a.B), dim3(256), 0, st, a);
+    if (p == last)
+      FAM_LAUNCH(final_k, dim3(1, a.B), dim3(256), 0, st, a);
+    else if (p & 1)
+      FAM_LAUNCH(cross_k, dim3(a.G, a.B), dim3(256), 0, st, a);
+    else
+      FAM_LAUNCH(self_k, dim3(a.G, a.B), dim3(256), 0, st, a);
     const int rc = fam_host::check_launch("fam_tiny_expert");
     if (rc != FAM_OK) return rc;
   }
