@@ -1076,6 +1076,7 @@ GEMM_SHAPES = (
     (2048, 8192, 2048, "config 4 FFN up"),
     (2048, 2048, 8192, "config 4 FFN down"),
     (588, 6144, 2048, "DiT4DiT RoboCasa q|k|v (588 tokens)"),
+    (588, 2048, 2048, "DiT4DiT RoboCasa o / cross q / cross o"),
     (588, 8192, 2048, "DiT4DiT RoboCasa FFN up"),
     (588, 2048, 8192, "DiT4DiT RoboCasa FFN down"),
     (8192, 8192, 8192, "8192^3"),

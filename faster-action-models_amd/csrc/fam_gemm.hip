@@ -879,7 +879,8 @@ __global__ __launch_bounds__(256) void tiled_kernel(GemmArgs g) {
 //     256 fp32 accumulators per lane), the workgroup BM x BN = (32 WFM) x (32 WFN):
 //     256 x 256, 224 x 256 (M = 1560 splits into 7 such row tiles with 8 padding rows),
 //     128 x 128 (two workgroups per CU) or 64 x 64;
-//   * K in blocks of 64 through two LDS slots.  Rows of a slot are 128 bytes (8 chunks of
+//   * K in blocks of 64 through NS LDS slots (two; four for the 64 x 64 tile, whose handful of
+//     MFMAs per block cannot cover a block's load latency).  Rows of a slot are 128 bytes (8 chunks of
 //     16 B) with chunk c of row r stored at c ^ (r & 7): the 16-byte fragment reads of 8
 //     consecutive lanes (8 rows, one chunk) hit 8 distinct bank groups;
 //   * the slots are filled by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds): one
@@ -889,7 +890,7 @@ __global__ __launch_bounds__(256) void tiled_kernel(GemmArgs g) {
 //     offset is not checked); M0 (LDS slot) is scalar, so a load costs one VALU add;
 //   * block b: k-step 0 computes from fragments read during block b - 1 while k-step 1's
 //     fragments are read; then one barrier (after which block b + 1 has landed and every wave
-//     is done with block b's slot), block b + 2 is sent into that slot and k-step 1 computes
+//     is done with block b's slot), block b + NS is sent into that slot and k-step 1 computes
 //     while k-step 0 of block b + 1 is read.  Loads, fragment reads and MFMAs interleave per
 //     MFMA row;
 //   * the MFMAs are written as inline assembly with the accumulator tied to an accumulation
@@ -915,7 +916,7 @@ __device__ __forceinline__ void mfma_acc(f32x4& acc, const bf16x8& w, const bf16
 // blocks): 8 waves in two K groups of 4; group g takes the K blocks g, g + 2, ... into its own
 // two slots, so each SIMD runs two waves although the grid leaves one workgroup per CU; group 1
 // then parks its accumulators in LDS for group 0 to add (in a fixed order) before the epilogue.
-template <int WFM, int WFN, int KG = 1>
+template <int WFM, int WFN, int KG = 1, int NS = 2>
 __global__ __launch_bounds__(256 * KG) void big_kernel(GemmArgs g, int tiles_m, int tiles_n, int vec8, int ksplit, int raw) {
   // the A part of a slot holds BMA >= BM rows, a multiple of 64 (a 224-row tile also loads the
   // next 32 rows, unused: measured 2-4 % faster than 7 loads per wave per block)
@@ -924,9 +925,15 @@ __global__ __launch_bounds__(256 * KG) void big_kernel(GemmArgs g, int tiles_m, 
   constexpr int NIA = BMA / 32, NIW = BN / 32, IPW = NIA + NIW;   // 1 KB loads per wave per block
   static_assert(IPW < 64, "vmcnt");
   static_assert(KG == 1 || (KG == 2 && WFM == 4 && WFN == 4), "K groups only on 128 x 128 tiles");
-  // two K slots per group, later the bf16 output tile with its padded rows (and with KG = 2
-  // first group 1's accumulators: 4 WFM WFN floats per lane)
-  constexpr int LDS_SLOTS = KG * 2 * SS, LDS_OUT = BM * (BN + 8);
+  // NS K slots per group (NS - 1 blocks in flight while one is computed): 2, or 4 for a 64 x 64
+  // tile whose grid fits one round at two workgroups per CU (its few MFMAs per block cannot
+  // cover a block's load latency; four 16 KB slots still leave room for two workgroups per CU,
+  // but not for the three to five a longer grid keeps resident with two).  Later the slots hold
+  // the bf16 output tile with its padded rows (and with KG = 2 first group 1's accumulators: 4
+  // WFM WFN floats per lane)
+  static_assert(NS == 2 || (NS == 4 && WFM == 2 && WFN == 2 && KG == 1), "four slots only on 64 x 64 tiles");
+  static_assert((NS - 1) * IPW < 64, "vmcnt");
+  constexpr int LDS_SLOTS = KG * NS * SS, LDS_OUT = BM * (BN + 8);
   constexpr int LDS_ELEMS = LDS_SLOTS > LDS_OUT ? LDS_SLOTS : LDS_OUT;
   static_assert(KG == 1 || LDS_ELEMS * 2 >= 4 * (4 * WFM * WFN) * 256, "park area");
   __shared__ __attribute__((aligned(1024))) bf16 sm[LDS_ELEMS];
@@ -963,7 +970,7 @@ __global__ __launch_bounds__(256 * KG) void big_kernel(GemmArgs g, int tiles_m, 
   // load p of this wave for the group's block blk (of this split) into slot: A rows 8 (wave + 4p)
   // .. + 7 for p < NIA, else W rows 8 (wave + 4 (p - NIA)) .. + 7; blocks past the end re-read
   // the last one (unused).  The group's block j is block KG j + kgi of the split.
-  bf16* const smg = sm + kgi * 2 * SS;   // this group's two slots
+  bf16* const smg = sm + kgi * NS * SS;   // this group's slots
   auto dma = [&](int p, int blk, int slot) {
     const uint32_t kb = (uint32_t)(kb0 + KG * (blk < nb ? blk : nb - 1) + kgi) * (BK * 2);
     if (p < NIA) {
@@ -993,10 +1000,11 @@ __global__ __launch_bounds__(256 * KG) void big_kernel(GemmArgs g, int tiles_m, 
 
   bf16x8 a0[WFM], w0[WFN], a1[WFM], w1[WFN];
 #pragma unroll
-  for (int p = 0; p < IPW; ++p) dma(p, 0, 0);
+  for (int sl = 0; sl < NS; ++sl)
 #pragma unroll
-  for (int p = 0; p < IPW; ++p) dma(p, 1, 1);
-  __builtin_amdgcn_s_waitcnt(0x0070 | (IPW & 15) | ((IPW >> 4) << 14));   // vmcnt(IPW): block 0
+    for (int p = 0; p < IPW; ++p) dma(p, sl, sl);
+  constexpr int VW0 = (NS - 1) * IPW, VW = (NS - 2) * IPW;
+  __builtin_amdgcn_s_waitcnt(0x0070 | (VW0 & 15) | ((VW0 >> 4) << 14));   // vmcnt((NS-1) IPW): block 0
   __builtin_amdgcn_s_barrier();
 #pragma unroll
   for (int i = 0; i < WFM; ++i) a0[i] = *reinterpret_cast<const bf16x8*>(fa + i * 16 * BK + fp0);
@@ -1004,7 +1012,7 @@ __global__ __launch_bounds__(256 * KG) void big_kernel(GemmArgs g, int tiles_m, 
   for (int j = 0; j < WFN; ++j) w0[j] = *reinterpret_cast<const bf16x8*>(fw + j * 16 * BK + fp0);
 
   for (int b = 0; b < nb; ++b) {
-    const int cur = (b & 1) * SS, nxt = ((b + 1) & 1) * SS;
+    const int cur = (b % NS) * SS, nxt = ((b + 1) % NS) * SS;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < WFM; ++i) {
@@ -1017,13 +1025,14 @@ __global__ __launch_bounds__(256 * KG) void big_kernel(GemmArgs g, int tiles_m, 
       for (int j = 0; j < WFN; ++j) mfma_acc(acc[i][j], w0[j], a0[i]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0): block b + 1 landed, slot b read
+    // vmcnt((NS-2) IPW) lgkmcnt(0): block b + 1 landed (loads complete in order), slot b read
+    __builtin_amdgcn_s_waitcnt(0x0070 | (VW & 15) | ((VW >> 4) << 14));
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < WFM; ++i) {
 #pragma unroll
-      for (int p = i * IPW / WFM; p < (i + 1) * IPW / WFM; ++p) dma(p, b + 2, b & 1);
+      for (int p = i * IPW / WFM; p < (i + 1) * IPW / WFM; ++p) dma(p, b + NS, b % NS);
       a0[i] = *reinterpret_cast<const bf16x8*>(fa + nxt + i * 16 * BK + fp0);
 #pragma unroll
       for (int j = i * WFN / WFM; j < (i + 1) * WFN / WFM; ++j)
@@ -1034,7 +1043,7 @@ __global__ __launch_bounds__(256 * KG) void big_kernel(GemmArgs g, int tiles_m, 
       __builtin_amdgcn_sched_barrier(0);
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);   // the (unused) loads of blocks nb, nb + 1 drain before exit
+  __builtin_amdgcn_s_waitcnt(0);   // the (unused) loads of blocks nb .. nb + NS - 1 drain before exit
   asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15");
 #pragma unroll
   for (int i = 0; i < WFM; ++i)
@@ -1220,6 +1229,12 @@ static void launch_big(const GemmArgs& a, hipStream_t s, int ksplit = 1, bool ra
   const auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
   const int vec8 = a.N % 8 == 0 && a.ldo % 8 == 0 && al16(a.out) && (!a.res || (a.ldr % 8 == 0 && al16(a.res))) &&
                    (!a.gate || (a.gbs % 8 == 0 && a.grs % 8 == 0 && al16(a.gate)));
+  if constexpr (WFM == 2 && WFN == 2 && KG == 1) {
+    if ((int64_t)tm * tn * ksplit <= 2 * (int64_t)fam_host::device_cus()) {
+      FAM_LAUNCH((big_kernel<2, 2, 1, 4>), dim3(grid), dim3(256), 0, s, a, tm, tn, vec8, ksplit, (int)(raw || ksplit > 1));
+      return;
+    }
+  }
   FAM_LAUNCH((big_kernel<WFM, WFN, KG>), dim3(grid), dim3(256 * KG), 0, s, a, tm, tn, vec8, ksplit,
              (int)(raw || ksplit > 1));
 }
@@ -1256,13 +1271,27 @@ static void big_plan(int64_t M, int64_t N, int act, int* wfm, int* wfn, bool nar
 // ceil(tiles / (CUs occ)) (c0 + 2 bm bn K / rate occ)) is at least 15% lower: a few hundred rows
 // (the DiT4DiT backbone's 588 video tokens) give 128 x 128 tiles too few workgroups to fill the
 // chip (588 x 2048 x 2048: 80 of 256 CUs), which big_plan's tile-area count does not see.
+// 64 x 64 tiles with four K slots (a grid of at most two workgroups per CU, launch_big):
+// t = 3.8 us + n W / r_n, W = 2 64 64 K flops per tile, n = ceil(tasks / CUs) <= 2 tiles on the
+// busiest CU, r_1 = 2.68 and r_2 = 3.2 TFLOP/s per CU (gfx950: 1024 x 1024 x 1024 6.9 us,
+// 1024 x 1024 x 4096 16.3 us at one per CU; 588 x 2048 x 2048 13.8 us, 588 x 2048 x 8192 46.7 us
+// with two on 64 CUs).  Returns a negative value for a longer grid (two slots: the fits below).
+static double est64_four(int64_t tasks, double kz) {
+  const int64_t cus = fam_host::device_cus();
+  if (tasks > 2 * cus) return -1.0;
+  const int n = tasks > cus ? 2 : 1;
+  return 3.8 + (double)n * 2.0 * 64.0 * 64.0 * kz / ((n == 1 ? 2.68 : 3.2) * 1e6);
+}
+
 static bool big_prefers_64(int64_t M, int64_t N, int64_t K) {
   const int cus = fam_host::device_cus();
   auto est = [&](int64_t bm, double c0, double rate) {
     const int64_t tiles = ((M + bm - 1) / bm) * ((N + bm - 1) / bm);
     return std::ceil((double)tiles / (2.0 * cus)) * (c0 + 2.0 * (double)(bm * bm) * (double)K / (rate * 1e6) * 2.0);
   };
-  return est(64, 1.0, 3.0) < 0.85 * est(128, 4.0, 5.5);
+  double e64 = est64_four(((M + 63) / 64) * ((N + 63) / 64), (double)K);
+  if (e64 < 0.0) e64 = est(64, 1.0, 3.0);
+  return e64 < 0.85 * est(128, 4.0, 5.5);
 }
 
 // K split of the big kernel (fam_gemm_ws, and fam_gemm_partial above 144 rows).  Estimated time
@@ -1270,7 +1299,8 @@ static bool big_prefers_64(int64_t M, int64_t N, int64_t K) {
 // 512 x 6144 x 4096 to 8192^3, every tile, 1-8 splits):
 //   t = ceil(tiles z / (CUs occ)) (c0 + 2 bm bn K_z / rate * occ) + [z > 1] z M N 4 B / 12 TB/s
 // (K_z = the split's K range; per tile: c0 = 10, 8, 4, 1 us, rate = 6.5, 6.5, 5.5, 3.0 TFLOP/s
-// per CU, occ = 1, 1, 2, 2 workgroups per CU for 256x256, 224x256, 128x128, 64x64).  The cost of
+// per CU, occ = 1, 1, 2, 2 workgroups per CU for 256x256, 224x256, 128x128, 64x64; the 64 x 64
+// tile with four K slots as est64_four).  The cost of
 // consuming the planes is added: a row launch that sums them (fam_gemm_ws: about 5 us + the
 // bf16 output written at 4 TB/s + z planes read at 8.8 TB/s), or, when a row kernel follows
 // anyway (fam_gemm_partial), the reads of the extra planes.  A split (2, 3, 4, 6 or 8 planes, each
@@ -1288,7 +1318,8 @@ static void big_plan_split(int64_t M, int64_t N, int64_t K, int64_t ws_floats, b
     const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
     const double rounds = std::ceil((double)(tiles * z) / ((double)cus * f.occ));
     const double kz = (double)((nb + z - 1) / z) * 64.0;
-    double t = rounds * (f.c0 + 2.0 * (double)(bm * bn) * kz / (f.rate * 1e6) * f.occ);
+    double t = f.fm == 2 ? est64_four(tiles * z, kz) : -1.0;
+    if (t < 0.0) t = rounds * (f.c0 + 2.0 * (double)(bm * bn) * kz / (f.rate * 1e6) * f.occ);
     if (z > 1) t += (double)z * mn * 4.0 / 12e6;
     return t;
   };
@@ -1300,6 +1331,10 @@ static void big_plan_split(int64_t M, int64_t N, int64_t K, int64_t ws_floats, b
   for (const Fit& f : fits)
     for (int z : {2, 3, 4, 6, 8}) {
       if (nb < 2 * z || (double)z * mn > (double)ws_floats) continue;
+      // 64 x 64 splits only where the four-slot estimate holds (the two-slot fit comes from
+      // unsplit grids and is optimistic for split ones: 588 x 2048 x 2048 in 3 splits measured
+      // 13.8 us of planes against 10.9 estimated)
+      if (f.fm == 2 && ((M + 63) / 64) * ((N + 63) / 64) * z > 2 * (int64_t)cus) continue;
       const double consume = planes_consumed ? (double)(z - 1) * mn * 4.0 / 8.8e6
                                              : 5.0 + mn * 2.0 / 4e6 + (double)z * mn * 4.0 / 8.8e6;
       const double t = est(f, z) + consume;

@@ -319,15 +319,19 @@ def test_gemm_deterministic(M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 128), (3900, 3900, 128), (2600, 3000, 192), (300, 520, 320),
-                                   (1000, 1500, 640), (1000, 1500, 576), (1560, 3072, 1024)])
+                                   (1000, 1500, 640), (1000, 1500, 576), (1560, 3072, 1024), (588, 2048, 2048),
+                                   (588, 2048, 128), (130, 200, 192)])
 def test_gemm_large_tiles_epilogue(M, N, K):
     """Large-M products on the big-tile kernel (256 x 256 tiles for the first two shapes,
     128 x 128 for the third, 64 x 64 for the fourth; ragged M and N): bias + GELU, then
     gate * y + residual with a per-row gate, then an fp32 residual output; and a shape off its
-    envelope (N % 4 != 0) on the tiled kernel.  The last two run 96 tiles of 128 x 128 (at most
+    envelope (N % 4 != 0) on the tiled kernel.  1000 x 1500 runs 96 tiles of 128 x 128 (at most
     one workgroup per CU): with 10 K blocks as two K groups per workgroup whose sums meet in
     LDS, with 9 (odd) as one group.  1560 x 3072 (config 2's o-projection rows and columns) runs
-    416 tiles of 128 x 96."""
+    416 tiles of 128 x 96.  The 64 x 64 grids of at most two workgroups per CU keep three K
+    blocks in flight through four LDS slots: 300 x 520 (5 blocks), the DiT4DiT call's
+    588 x 2048 x 2048 (320 tiles, 32 blocks), fewer blocks than slots (588 x 2048 x 128: 2) and a
+    ragged 130 x 200 grid (3 blocks)."""
     from fam import _capi
     x, w, b = rnd(M, K, seed=65), rnd(N, K, seed=66, scale=0.05), rnd(N, seed=67, scale=0.05)
     lin = O.linear(x.float(), w.float(), b.float())
