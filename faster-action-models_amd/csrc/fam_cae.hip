@@ -114,17 +114,29 @@ __global__ __launch_bounds__(CT) void cae_up_kernel(CaeArgs a) {
 }
 
 // Conv1d (k = 3, padding 1) of this group's channels over every input channel, GroupNorm,
-// then SiLU or the residual add.
-template <int NJ>
+// then SiLU or the residual add.  The input rows sit in LDS with a zero column at each end (the
+// padding), so the three taps need no branch; with WL the group's CG x C x 3 weights are staged
+// in LDS too (one contiguous block of the [C][C][3] weight, read once with coalesced loads)
+// instead of each output's 3 C scalar global reads.  Every output sums its taps in the order
+// (input channel, tap) from the bias.
+template <int NJ, bool WL>
 __global__ __launch_bounds__(CT) void cae_conv_kernel(CaeArgs a) {
-  extern __shared__ float xs[];  // [C][T]
+  extern __shared__ float xs[];  // [C][T + 2], then (WL) [CG][C][3]
   __shared__ float red[4];
   const int tid = threadIdx.x;
   const int64_t bi = blockIdx.x, g = blockIdx.y;
-  const int64_t C = a.C, T = a.T_out;
-  for (int64_t e = tid; e < C * T; e += CT) xs[e] = a.x[bi * C * T + e];
+  const int64_t C = a.C, T = a.T_out, TP = T + 2, CG = C / a.G, c0 = g * CG;
+  for (int64_t e = tid; e < C * TP; e += CT) {
+    const int64_t c = e / TP, t = e - c * TP;
+    const bool in = t >= 1 && t <= T;
+    const float v = a.x[(bi * C + c) * T + (in ? t - 1 : 0)];
+    xs[e] = in ? v : 0.f;
+  }
+  float* wsm = xs + C * TP;
+  if constexpr (WL) {
+    for (int64_t e = tid; e < CG * C * 3; e += CT) wsm[e] = a.w[c0 * C * 3 + e];
+  }
   __syncthreads();
-  const int64_t CG = C / a.G, c0 = g * CG;
   const int n = (int)(CG * T);
   float vals[NJ];
 #pragma unroll
@@ -132,14 +144,15 @@ __global__ __launch_bounds__(CT) void cae_conv_kernel(CaeArgs a) {
     const int e = tid + CT * j;
     vals[j] = 0.f;
     if (e >= n) continue;
-    const int64_t co = c0 + e / T, t = e % T;
+    const int64_t col = e / T, co = c0 + col, t = e % T;
+    const float* wr = WL ? wsm + col * C * 3 : a.w + co * C * 3;
+    const float* xr = xs + t;   // x[ci][t - 1 + k] at xr[ci (T + 2) + k]
     float acc = a.b[co];
+#pragma unroll 4
     for (int64_t ci = 0; ci < C; ++ci) {
-      const float* wr = a.w + (co * C + ci) * 3;
-      const float* xr = xs + ci * T;
-      if (t >= 1) acc += wr[0] * xr[t - 1];
-      acc += wr[1] * xr[t];
-      if (t + 1 < T) acc += wr[2] * xr[t + 1];
+      acc += wr[3 * ci] * xr[ci * TP];
+      acc += wr[3 * ci + 1] * xr[ci * TP + 1];
+      acc += wr[3 * ci + 2] * xr[ci * TP + 2];
     }
     vals[j] = acc;
   }
@@ -162,14 +175,20 @@ __global__ __launch_bounds__(CT) void cae_out_kernel(CaeArgs a) {
 
 using namespace fam;
 
-static int launch_nj(int n, bool up, const CaeArgs& a, size_t lds, hipStream_t s) {
+// up: the stage head (LDS: C T_in floats); else the k = 3 convolution (LDS: C (T + 2) floats,
+// plus the group's weights where both fit in 64 KB)
+static int launch_nj(int n, bool up, const CaeArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)a.B, (unsigned)a.G);
   const int nj = (n + CT - 1) / CT;
   if (nj > 16) return FAM_ERR_UNSUPPORTED;
+  const size_t xs = up ? (size_t)(a.C * a.T_in * 4) : (size_t)(a.C * (a.T_out + 2) * 4);
+  const size_t wl = (size_t)((a.C / a.G) * a.C * 3 * 4);
+  const bool wlds = !up && xs + wl <= 64 * 1024;
 #define FAM_CAE(NJ)                                                                   \
   if (nj <= NJ) {                                                                     \
-    if (up) FAM_LAUNCH((cae_up_kernel<NJ>), grid, dim3(CT), lds, s, a);               \
-    else FAM_LAUNCH((cae_conv_kernel<NJ>), grid, dim3(CT), lds, s, a);                \
+    if (up) FAM_LAUNCH((cae_up_kernel<NJ>), grid, dim3(CT), xs, s, a);                \
+    else if (wlds) FAM_LAUNCH((cae_conv_kernel<NJ, true>), grid, dim3(CT), xs + wl, s, a); \
+    else FAM_LAUNCH((cae_conv_kernel<NJ, false>), grid, dim3(CT), xs, s, a);          \
     return FAM_OK;                                                                    \
   }
   FAM_CAE(2) FAM_CAE(4) FAM_CAE(8) FAM_CAE(16)
@@ -194,7 +213,7 @@ extern "C" int fam_cae_decode(const fam_cae_desc* d, void* stream) {
     // ConvTranspose1d(k = 2s, stride s, padding s/2): T -> (T-1)s - 2(s/2) + 2s
     T = (T - 1) * d->strides[i] - 2 * (d->strides[i] / 2) + 2 * d->strides[i];
   }
-  FAM_REQUIRE(T <= 1024 && (C / G) * T <= (int64_t)CT * 16 && C * T * 4 <= 64 * 1024, FAM_ERR_UNSUPPORTED,
+  FAM_REQUIRE(T <= 1024 && (C / G) * T <= (int64_t)CT * 16 && C * (T + 2) * 4 <= 64 * 1024, FAM_ERR_UNSUPPORTED,
               "fam_cae_decode: decoded length %lld too long for one workgroup per group", (long long)T);
   if (d->batch == 0) return FAM_OK;
   hipStream_t s = (hipStream_t)stream;
@@ -213,14 +232,14 @@ extern "C" int fam_cae_decode(const fam_cae_desc* d, void* stream) {
     a.z = i == 0 ? d->z : nullptr; a.suite = i == 0 ? d->suite : nullptr; a.in_w = d->in_w; a.in_b = d->in_b;
     a.x = wr; a.T_in = Tin; a.T_out = Tout; a.stride = st;
     a.w = d->up_w[i]; a.b = d->up_b[i]; a.gw = d->gn_w[i]; a.gb = d->gn_b[i]; a.res = nullptr; a.silu = 1; a.y = wa;
-    int rc = launch_nj((int)((C / G) * Tout), true, a, (size_t)(C * Tin * 4), s);
+    int rc = launch_nj((int)((C / G) * Tout), true, a, s);
     if (rc) { fam_host::set_error("fam_cae_decode: unsupported stage shape"); return rc; }
     // residual block: conv, GN, SiLU -> wb; conv, GN, + wa -> wr
     a.z = nullptr; a.x = wa; a.T_in = Tout; a.T_out = Tout;
     a.w = d->r1_w[i]; a.b = d->r1_b[i]; a.gw = d->rg1_w[i]; a.gb = d->rg1_b[i]; a.res = nullptr; a.silu = 1; a.y = wb;
-    launch_nj((int)((C / G) * Tout), false, a, (size_t)(C * Tout * 4), s);
+    launch_nj((int)((C / G) * Tout), false, a, s);
     a.x = wb; a.w = d->r2_w[i]; a.b = d->r2_b[i]; a.gw = d->rg2_w[i]; a.gb = d->rg2_b[i]; a.res = wa; a.silu = 0; a.y = wr;
-    launch_nj((int)((C / G) * Tout), false, a, (size_t)(C * Tout * 4), s);
+    launch_nj((int)((C / G) * Tout), false, a, s);
     Tin = Tout;
   }
   a.x = wr; a.T_in = Tin; a.ow = d->out_w; a.ob = d->out_b; a.out = d->out;

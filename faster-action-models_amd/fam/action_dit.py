@@ -274,7 +274,17 @@ class FusedActionDiT:
         self.tmod = z(num_steps, 6 * H)
         self.mods = z(num_steps, L, 6 * H)
         self.ctx_h = z(ctx_len, H)
-        self.ctx_emb = z(ctx_len, H)
+        # the context K/V of every layer is one GEMM over K = H; a hidden width that is not a
+        # multiple of 64 (the tiny experts' 32) is zero-padded to the next one, so that product
+        # runs on the large-M kernel (which takes K in blocks of 64) instead of the generic tiled
+        # one: the embedding lands in the first H columns, the rest stay zero
+        Hp = H if H % 64 == 0 or ctx_len < 128 else (H + 63) // 64 * 64
+        if Hp != H:
+            kvw = w["ctxkv_w"]
+            w["ctxkv_w"] = torch.cat([kvw, torch.zeros(kvw.shape[0], Hp - H, dtype=kvw.dtype, device=kvw.device)],
+                                     dim=1).contiguous()
+        self.ctx_emb_pad = z(ctx_len, Hp)
+        self.ctx_emb = self.ctx_emb_pad[:, :H]
         self.ctxkv = z(ctx_len, L * 2 * A)
         self.h = z(M, H)   # normalised input of the next projection
         # MoT: per-layer cached video K/V [L, B, Sv, A] and the action rows of the joint mask
@@ -678,7 +688,7 @@ class FusedActionDiT:
                  2 * 6 * H * (T + L + T * L))
         self._gemm("ctx_emb0", self.context_in, w["txt0_w"], w["txt0_b"], self.ctx_h, act=_capi.FAM_ACT_GELU_TANH)
         self._gemm("ctx_emb2", self.ctx_h, w["txt2_w"], w["txt2_b"], self.ctx_emb)
-        self._gemm("ctx_kv", self.ctx_emb, w["ctxkv_w"], w["ctxkv_b"], self.ctxkv)
+        self._gemm("ctx_kv", self.ctx_emb_pad, w["ctxkv_w"], w["ctxkv_b"], self.ctxkv)
         kvp = self.ctxkv.data_ptr()
         # RMSNorm of every block's context keys in one launch: row (i, l) = ctxkv[i, 2 A l ..]
         w["nk_stack"] = torch.stack([w[f"ca_nk_w{l}"] for l in range(L)]).contiguous()

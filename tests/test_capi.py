@@ -173,8 +173,11 @@ def test_validation_rejects_before_launch(lib):
                                                               (1024, 3072))] == [2, 4, 2, 4, 8, 2, 6]
     assert lib.fam_gemm_partial_splits(0, 64, 64) == 0
     # above 144 rows the large-M kernel's planes: any shape with N % 4 == 0 and K % 64 == 0 (>= 128)
-    # gets >= 1 plane; the head's N = 7 or a K tail does not
-    assert lib.fam_gemm_partial_splits(1024, 3072, 1024) >= 1 and lib.fam_gemm_partial_splits(1024, 1024, 4096) >= 2
+    # gets >= 1 plane; the head's N = 7 or a K tail does not.  1024 x 1024 x 4096 (config 1 at
+    # B = 32, FFN down) is one round of 64 x 64 tiles with four K slots, unsplit (16.3 us measured
+    # against 23.5 us for two planes); 2048 x 2048 x 8192 is split
+    assert lib.fam_gemm_partial_splits(1024, 3072, 1024) >= 1 and lib.fam_gemm_partial_splits(1024, 1024, 4096) == 1
+    assert lib.fam_gemm_partial_splits(2048, 2048, 8192) >= 2
     assert lib.fam_gemm_partial_splits(1024, 7, 1024) == 0 and lib.fam_gemm_partial_splits(1024, 1024, 1000) == 0
     assert lib.fam_gemm_partial(16, 64, 32, 64, 48, 1024, 7, 64, None) == _capi.FAM_ERR_UNSUPPORTED
     # cross-attention key splits: one launch up to 256 keys, about four 32-key blocks per split
