@@ -17,6 +17,7 @@ constexpr int CT = 256;  // threads per workgroup
 
 struct CaeArgs {
   int64_t B, T0, L, C, G, T_in, T_out, stride, horizon, A;
+  int64_t wchunk;   // input channels per LDS weight chunk of the stage head
   const float* z; const float* suite; const float* in_w; const float* in_b;
   const float* x;   // stage input [B, C, T_in] (stages after the first)
   const float* w; const float* b; const float* gw; const float* gb;
@@ -69,16 +70,19 @@ __device__ __forceinline__ void cae_gn_store(const CaeArgs& a, float (&vals)[NJ]
 }
 
 // Stage head: input projection (first stage) or the previous stage's output, then the
-// transposed convolution of this group's channels, GroupNorm, SiLU.
+// transposed convolution of this group's channels, GroupNorm, SiLU.  The group's weights
+// (w[ci][c0 .. c0 + CG)[0 .. 2s), contiguous per input channel) pass through LDS in chunks of
+// `wchunk` input channels after the input rows; every output sums its two taps per input
+// channel in input-channel order from the bias.
 template <int NJ>
 __global__ __launch_bounds__(CT) void cae_up_kernel(CaeArgs a) {
-  extern __shared__ float xs[];  // [C][T_in]
+  extern __shared__ float xs[];  // [C][T_in], then [wchunk][CG][2s]
   __shared__ float red[4];
   const int tid = threadIdx.x;
   const int64_t bi = blockIdx.x, g = blockIdx.y;
-  const int64_t C = a.C, Ti = a.T_in, To = a.T_out, s = a.stride, K = 2 * s, P = s / 2;
-  for (int64_t e = tid; e < C * Ti; e += CT) {
-    const int64_t c = e / Ti, i = e % Ti;
+  const int C = (int)a.C, Ti = (int)a.T_in, To = (int)a.T_out, s = (int)a.stride, K = 2 * s, P = s / 2;
+  for (int e = tid; e < C * Ti; e += CT) {
+    const int c = e / Ti, i = e - c * Ti;
     float v;
     if (a.z) {  // x[c][i] = in_b[c] + sum_l in_w[c][l] z[i][l] (+ suite[c])
       v = a.in_b[c];
@@ -90,26 +94,44 @@ __global__ __launch_bounds__(CT) void cae_up_kernel(CaeArgs a) {
     }
     xs[e] = v;
   }
-  __syncthreads();
-  const int64_t CG = C / a.G, c0 = g * CG;
-  const int n = (int)(CG * To);
-  float vals[NJ];
+  const int CG = C / (int)a.G, c0 = (int)g * CG, CK = CG * K, wc = (int)a.wchunk;
+  float* wsm = xs + C * Ti;
+  const int n = CG * To;
+  float acc[NJ];
+  int col[NJ], ihi[NJ], khi[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int e = tid + CT * j;
-    vals[j] = 0.f;
-    if (e >= n) continue;
-    const int64_t co = c0 + e / To, t = e % To;
-    float acc = a.b[co];
-    // taps: input step i contributes at t = i*s - P + kk, kk in [0, 2s)
-    const int64_t ihi = (t + P) / s, ilo = ihi - 1;
-    for (int64_t ci = 0; ci < C; ++ci) {
-      const float* wr = a.w + (ci * C + co) * K;
-      if (ihi < Ti) acc += xs[ci * Ti + ihi] * wr[t + P - ihi * s];
-      if (ilo >= 0 && ilo < Ti) acc += xs[ci * Ti + ilo] * wr[t + P - ilo * s];
-    }
-    vals[j] = acc;
+    const int e = tid + CT * j, ee = e < n ? e : 0;
+    col[j] = ee / To;
+    const int t = ee - col[j] * To;
+    // taps: input step i contributes at t = i s - P + kk, kk in [0, 2s): i = ihi (kk = khi) and
+    // i = ihi - 1 (kk = khi + s)
+    ihi[j] = (t + P) / s;
+    khi[j] = t + P - ihi[j] * s;
+    acc[j] = a.b[c0 + col[j]];
   }
+  for (int ci0 = 0; ci0 < C; ci0 += wc) {
+    const int nc = C - ci0 < wc ? C - ci0 : wc;
+    __syncthreads();   // the input rows are staged; the previous chunk is consumed
+    for (int e = tid; e < nc * CK; e += CT) {
+      const int ci = e / CK, r = e - ci * CK;
+      wsm[e] = a.w[((int64_t)(ci0 + ci) * C + c0) * K + r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int hi = ihi[j], lo = hi - 1;
+      const float* wr = wsm + col[j] * K;
+      for (int ci = 0; ci < nc; ++ci) {
+        const float* xr = xs + (ci0 + ci) * Ti;
+        if (hi < Ti) acc[j] += xr[hi] * wr[ci * CK + khi[j]];
+        if (lo >= 0 && lo < Ti) acc[j] += xr[lo] * wr[ci * CK + khi[j] + s];
+      }
+    }
+  }
+  float vals[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) vals[j] = tid + CT * j < n ? acc[j] : 0.f;
   cae_gn_store<NJ>(a, vals, n, c0, To, red);
 }
 
@@ -126,15 +148,15 @@ __global__ __launch_bounds__(CT) void cae_conv_kernel(CaeArgs a) {
   const int tid = threadIdx.x;
   const int64_t bi = blockIdx.x, g = blockIdx.y;
   const int64_t C = a.C, T = a.T_out, TP = T + 2, CG = C / a.G, c0 = g * CG;
-  for (int64_t e = tid; e < C * TP; e += CT) {
-    const int64_t c = e / TP, t = e - c * TP;
-    const bool in = t >= 1 && t <= T;
+  for (int e = tid; e < (int)(C * TP); e += CT) {
+    const int c = e / (int)TP, t = e - c * (int)TP;
+    const bool in = t >= 1 && t <= (int)T;
     const float v = a.x[(bi * C + c) * T + (in ? t - 1 : 0)];
     xs[e] = in ? v : 0.f;
   }
   float* wsm = xs + C * TP;
   if constexpr (WL) {
-    for (int64_t e = tid; e < CG * C * 3; e += CT) wsm[e] = a.w[c0 * C * 3 + e];
+    for (int e = tid; e < (int)(CG * C * 3); e += CT) wsm[e] = a.w[c0 * C * 3 + e];
   }
   __syncthreads();
   const int n = (int)(CG * T);
@@ -159,15 +181,22 @@ __global__ __launch_bounds__(CT) void cae_conv_kernel(CaeArgs a) {
   cae_gn_store<NJ>(a, vals, n, c0, T, red);
 }
 
-// output_proj over the horizon (time steps past the decoded length read zeros).
+// output_proj over the horizon (time steps past the decoded length read zeros); the sample's
+// decoded rows [C][T_in] and the projection [A][C] are staged in LDS first.
 __global__ __launch_bounds__(CT) void cae_out_kernel(CaeArgs a) {
+  extern __shared__ float xs[];  // [C][T_in], then ow [A][C]
   const int64_t bi = blockIdx.x;
-  for (int64_t e = threadIdx.x; e < a.horizon * a.A; e += CT) {
-    const int64_t t = e / a.A, k = e % a.A;
+  const int C = (int)a.C, Ti = (int)a.T_in, A = (int)a.A;
+  for (int e = threadIdx.x; e < C * Ti; e += CT) xs[e] = a.x[bi * C * Ti + e];
+  float* ow = xs + C * Ti;
+  for (int e = threadIdx.x; e < A * C; e += CT) ow[e] = a.ow[e];
+  __syncthreads();
+  for (int e = threadIdx.x; e < (int)a.horizon * A; e += CT) {
+    const int t = e / A, k = e - t * A;
     float acc = a.ob[k];
-    if (t < a.T_in)
-      for (int64_t c = 0; c < a.C; ++c) acc += a.ow[k * a.C + c] * a.x[(bi * a.C + c) * a.T_in + t];
-    a.out[(bi * a.horizon + t) * a.A + k] = acc;
+    if (t < Ti)
+      for (int c = 0; c < C; ++c) acc += ow[k * C + c] * xs[c * Ti + t];
+    a.out[(bi * a.horizon + t) * A + k] = acc;
   }
 }
 
@@ -184,9 +213,10 @@ static int launch_nj(int n, bool up, const CaeArgs& a, hipStream_t s) {
   const size_t xs = up ? (size_t)(a.C * a.T_in * 4) : (size_t)(a.C * (a.T_out + 2) * 4);
   const size_t wl = (size_t)((a.C / a.G) * a.C * 3 * 4);
   const bool wlds = !up && xs + wl <= 64 * 1024;
+  const size_t upl = xs + (size_t)(a.wchunk * (a.C / a.G) * 2 * a.stride * 4);
 #define FAM_CAE(NJ)                                                                   \
   if (nj <= NJ) {                                                                     \
-    if (up) FAM_LAUNCH((cae_up_kernel<NJ>), grid, dim3(CT), xs, s, a);                \
+    if (up) FAM_LAUNCH((cae_up_kernel<NJ>), grid, dim3(CT), upl, s, a);               \
     else if (wlds) FAM_LAUNCH((cae_conv_kernel<NJ, true>), grid, dim3(CT), xs + wl, s, a); \
     else FAM_LAUNCH((cae_conv_kernel<NJ, false>), grid, dim3(CT), xs, s, a);          \
     return FAM_OK;                                                                    \
@@ -210,9 +240,15 @@ extern "C" int fam_cae_decode(const fam_cae_desc* d, void* stream) {
     FAM_REQUIRE(d->strides[i] >= 1 && d->up_w[i] && d->up_b[i] && d->gn_w[i] && d->gn_b[i] && d->r1_w[i] &&
                     d->r1_b[i] && d->rg1_w[i] && d->rg1_b[i] && d->r2_w[i] && d->r2_b[i] && d->rg2_w[i] && d->rg2_b[i],
                 FAM_ERR_INVALID_ARG, "fam_cae_decode: stage %d incomplete", i);
+    FAM_REQUIRE(d->strides[i] <= 64 && (C * T + (C / G) * 2 * d->strides[i]) * 4 <= 64 * 1024, FAM_ERR_UNSUPPORTED,
+                "fam_cae_decode: stage %d (stride %lld over %lld steps) does not fit one workgroup's LDS", i,
+                (long long)d->strides[i], (long long)T);
     // ConvTranspose1d(k = 2s, stride s, padding s/2): T -> (T-1)s - 2(s/2) + 2s
     T = (T - 1) * d->strides[i] - 2 * (d->strides[i] / 2) + 2 * d->strides[i];
   }
+  FAM_REQUIRE((C * T + d->action_dim * C) * 4 <= 64 * 1024, FAM_ERR_UNSUPPORTED,
+              "fam_cae_decode: the output projection's rows (%lld x %lld) and weights (%lld x %lld) exceed 64 KiB",
+              (long long)C, (long long)T, (long long)d->action_dim, (long long)C);
   FAM_REQUIRE(T <= 1024 && (C / G) * T <= (int64_t)CT * 16 && C * (T + 2) * 4 <= 64 * 1024, FAM_ERR_UNSUPPORTED,
               "fam_cae_decode: decoded length %lld too long for one workgroup per group", (long long)T);
   if (d->batch == 0) return FAM_OK;
@@ -232,6 +268,8 @@ extern "C" int fam_cae_decode(const fam_cae_desc* d, void* stream) {
     a.z = i == 0 ? d->z : nullptr; a.suite = i == 0 ? d->suite : nullptr; a.in_w = d->in_w; a.in_b = d->in_b;
     a.x = wr; a.T_in = Tin; a.T_out = Tout; a.stride = st;
     a.w = d->up_w[i]; a.b = d->up_b[i]; a.gw = d->gn_w[i]; a.gb = d->gn_b[i]; a.res = nullptr; a.silu = 1; a.y = wa;
+    // input channels per weight chunk: what fits in 64 KB beside the input rows (>= 1)
+    a.wchunk = std::max<int64_t>(1, std::min<int64_t>(C, (64 * 1024 - C * Tin * 4) / ((C / G) * 2 * st * 4)));
     int rc = launch_nj((int)((C / G) * Tout), true, a, s);
     if (rc) { fam_host::set_error("fam_cae_decode: unsupported stage shape"); return rc; }
     // residual block: conv, GN, SiLU -> wb; conv, GN, + wa -> wr
@@ -243,6 +281,6 @@ extern "C" int fam_cae_decode(const fam_cae_desc* d, void* stream) {
     Tin = Tout;
   }
   a.x = wr; a.T_in = Tin; a.ow = d->out_w; a.ob = d->out_b; a.out = d->out;
-  FAM_LAUNCH(cae_out_kernel, dim3((unsigned)a.B), dim3(CT), 0, s, a);
+  FAM_LAUNCH(cae_out_kernel, dim3((unsigned)a.B), dim3(CT), (size_t)((C * Tin + d->action_dim * C) * 4), s, a);
   return fam_host::check_launch("fam_cae_decode");
 }

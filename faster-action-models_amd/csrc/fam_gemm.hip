@@ -428,6 +428,9 @@ struct PartArgs {
   const bf16* w; int64_t ldw;
   float* part;               // [splits][M][N]
   int64_t M, N, K;
+  // partial_stream_kernel with one split: bf16(sum + bias) into out [M][ldo] instead of a plane
+  const bf16* bias;
+  bf16* out; int64_t ldo;
 };
 
 template <int MT, int STEPS>
@@ -650,6 +653,23 @@ __global__ __launch_bounds__(NWV * 64) void partial_stream_kernel(PartArgs g, in
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < KSW; ++s) wc[s] = wx[s];
+  }
+  if (g.out != nullptr) {
+    // one split (fam_gemm): the finished bf16 row segment with its bias, as nn.Linear rounds it
+    // (N % 4 == 0 here)
+    const int n = n0 + lg * 4;
+    const int nc = n < N ? n : 0;
+    bf16x4 bv = *reinterpret_cast<const bf16x4*>(g.bias + nc);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      const int m = t * 16 + l16;
+      if (m >= M || n >= N) continue;
+      bf16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = to_bf(acc[t][e] + to_f(bv[e]));
+      *reinterpret_cast<bf16x4*>(g.out + (int64_t)m * g.ldo + n) = o;
+    }
+    return;
   }
 #pragma unroll
   for (int t = 0; t < MT; ++t) {
@@ -1356,6 +1376,20 @@ static void launch_tiled(const GemmArgs& a, int pro, hipStream_t s) {
 
 using namespace fam;
 
+static void partial_plan(int64_t M, int64_t N, int64_t K, int* steps, int* splits, int* nwv);
+
+// fam_gemm's streaming path: a plain product with a bias (or none) into bf16, 64 < M <= 144, and a
+// partial plan of one split of 8-wave workgroups (N >= 32768)
+static bool stream_single(const fam_gemm_desc* d) {
+  if (d->M <= 64 || d->M > 144 || d->prologue != FAM_PRO_NONE || d->act != FAM_ACT_NONE || d->res || d->gate ||
+      d->out_f32 || d->N % 4 || d->ldo % 4 || ((uintptr_t)d->out & 7u) || (d->bias && ((uintptr_t)d->bias & 7u)) ||
+      !d->bias || d->M * d->lda * 2 >= (1LL << 31) || d->ldw >= (1LL << 23) || d->N >= (1LL << 31))
+    return false;
+  int steps, splits, nwv = 8;
+  partial_plan(d->M, d->N, d->K, &steps, &splits, &nwv);
+  return steps < 0 && splits == 1 && nwv == 8;
+}
+
 extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
   FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_gemm: null descriptor");
   FAM_REQUIRE(d->a && d->w && d->out, FAM_ERR_INVALID_ARG, "fam_gemm: a, w and out must be non-null");
@@ -1410,6 +1444,21 @@ extern "C" int fam_gemm(const fam_gemm_desc* d, void* stream) {
     a.pw = nullptr;
   }
   hipStream_t s = (hipStream_t)stream;
+  // 64 < M <= 144 rows against N >= 32768 columns (the stacked context K/V of every block): the
+  // streaming split-K plan needs no K split there (one round of 128-column workgroups), so it
+  // reads the weights once and stores the finished bf16 rows itself
+  if (stream_single(d)) {
+    int steps, splits, nwv = 8;
+    partial_plan(d->M, d->N, d->K, &steps, &splits, &nwv);
+    PartArgs pa{(const bf16*)d->a, d->lda, (const bf16*)d->w, d->ldw, nullptr, d->M, d->N, d->K,
+                (const bf16*)d->bias, (bf16*)d->out, d->ldo};
+    const dim3 grid((unsigned)((d->N + 127) / 128), 1u);
+    const int kper = -steps * 256;
+    if (d->M <= 112) FAM_LAUNCH((partial_stream_kernel<7, 8>), grid, dim3(512), 0, s, pa, kper);
+    else if (d->M <= 128) FAM_LAUNCH((partial_stream_kernel<8, 8>), grid, dim3(512), 0, s, pa, kper);
+    else FAM_LAUNCH((partial_stream_kernel<9, 8>), grid, dim3(512), 0, s, pa, kper);
+    return fam_host::check_launch("fam_gemm");
+  }
   // (a normalising prologue over K > 1024 would not fit the 16-wave skinny variant's
   // registers; the folded LayerNorm runs K in chunks on 8 waves)
   const bool skinny = d->M <= 64 && (d->prologue == FAM_PRO_NONE || d->prologue == FAM_PRO_LN_FOLDED || d->K <= 1024);

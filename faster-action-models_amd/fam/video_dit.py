@@ -593,7 +593,7 @@ class FusedVideoPrefill:
         add = self._add_step
         N, K = self.ckv_w.shape[0], ctx.shape[1]
         sp = lib.fam_gemm_partial_splits(rows, N, K) if 64 < rows <= 144 else 0
-        if sp > 0:
+        if sp > 1:
             # up to 144 context rows: the streaming split-K kernel reads the 1 GB of stacked
             # weights once; the large-M GEMM's 256-row tiles would double the products of 129 rows
             self.ctx_part = torch.empty(sp * rows * N, dtype=torch.float32, device=ctx.device)
@@ -607,6 +607,8 @@ class FusedVideoPrefill:
             self._descs.append(r)
             add("ctx_kv_all_row", "fam_rowop", (C.byref(r),), "rowop")
         else:
+            # (one split: fam_gemm runs the same streaming kernel and stores the bf16 rows with
+            # their bias itself, no fp32 plane and no row launch)
             add("ctx_kv_all", "fam_gemm", (C.byref(d),), "gemm")
         # every block's context keys in one launch: rows (context row, block) with the block's
         # k columns 2A apart, normalised with that block's norm_k weight

@@ -568,7 +568,8 @@ int fam_add_modulation(const void* t_mod, const void* modulation, void* out,
  *   time axis cropped / zero-padded to horizon, then out_w x + out_b per position.
  * Weights in PyTorch layouts: ConvTranspose1d [in, out, k], Conv1d [out, in, 3], Linear [out, in].
  * work: 3 * B * C * T floats of scratch (T = decoded length).  Limits: C <= 512 and divisible by
- * min(8, C); C * (T + 2) * 4 bytes <= 64 KiB; (C / G) * T <= 4096; nstages <= 3.
+ * min(8, C); C * (T + 2) * 4 and (C T + action_dim C) * 4 bytes <= 64 KiB (T = decoded length), and per
+ * stage (C T_in + 2 s C / G) * 4 <= 64 KiB; (C / G) * T <= 4096; nstages <= 3.
  */
 typedef struct fam_cae_desc {
   const float* z; int64_t batch, tokens, latent_dim;

@@ -352,6 +352,24 @@ def test_gemm_large_tiles_epilogue(M, N, K):
         assert relerr(ops().linear(dev(x), dev(w3), dev(b3)), O.linear(x.float(), w3.float(), b3.float())) <= TOL
 
 
+@pytest.mark.parametrize("M,N,K", [(129, 36864, 768), (98, 32768, 1024), (120, 33000, 768)])
+def test_gemm_streaming_single_split(M, N, K):
+    """fam_gemm at 64 < M <= 144 rows against N >= 32768 columns (the stacked context K/V of every
+    block) runs the streaming split-K kernel in one split, which adds the bias and stores bf16
+    rows itself: against the oracle, and bit-identical to that kernel's fp32 plane + the row
+    kernel's bias (both round sum + bias once).  7, 8 and 9 m-tiles; a ragged last column block."""
+    from fam import _capi
+    assert _capi.lib().fam_gemm_partial_splits(M, N, K) == 1
+    x, w, b = rnd(M, K, seed=81), rnd(N, K, seed=82, scale=0.05), rnd(N, seed=83, scale=0.05)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ops().gemm(dev(x), dev(w), dev(b), y)
+    assert relerr(y, O.linear(x.float(), w.float(), b.float())) <= TOL
+    part, S = ops().gemm_partial(dev(x), dev(w))
+    y2 = torch.empty_like(y)
+    ops().rowop(y2, partials=part, bias=dev(b))
+    assert S == 1 and torch.equal(y, y2)
+
+
 @pytest.mark.parametrize("M,N,K,epi", [(392, 640, 5760, "bias_res"), (1568, 640, 2880, "gelu"), (392, 392, 640, "f32"),
                                        (200, 96, 1024, "gate_res"), (4096, 4096, 128, "bias_res")])
 def test_gemm_ws_split_k(M, N, K, epi):

@@ -64,8 +64,9 @@ def test_video_prefill_kv_matches_oracle(frames, tpf, Lc, num_run, ragged, nh):
 
 def test_video_prefill_context_kv_split_k():
     """129 context rows: the stacked context K/V of the 11 cross-attending blocks
-    (129 x 16896 x 768) on the streaming split-K kernel with 9 m-tiles + a bias row launch,
-    instead of the large-M GEMM; every layer's K/V against the oracle."""
+    (129 x 16896 x 768) on the streaming split-K kernel with 9 m-tiles in one split, which
+    stores the bf16 rows with their bias itself (fam_gemm; no plane, no row launch), instead of
+    the large-M GEMM; every layer's K/V against the oracle."""
     from fam import _capi
     from fam.video_dit import FusedVideoPrefill
     Sv, H, nh, Dh, F, L, Lc = 98, 768, 6, 128, 1536, 12, 129
@@ -80,7 +81,7 @@ def test_video_prefill_context_kv_split_k():
     freqs = O.action_freqs(Dh, Sv)
     pf = FusedVideoPrefill(p, num_layers=L, hidden=H, num_heads=nh, head_dim=Dh, ffn_dim=F, batch=1, video_len=Sv,
                            ctx_len=Lc, freqs=freqs)
-    assert [m["name"] for m in pf.meta[:2]] == ["ctx_kv_all", "ctx_kv_all_row"]
+    assert [m["name"] for m in pf.meta[:2]] == ["ctx_kv_all", "cross_k_norm_all"]
     kv = pf.prefill(x.cuda(), tm.cuda(), ctx.cuda())
     p32 = {k: v.float() for k, v in p.items()}
     ref = O.mot_prefill_video_cache(p32, ocfg, x.float(), freqs, tm.float(), ctx.float(),
