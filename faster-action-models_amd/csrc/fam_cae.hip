@@ -135,6 +135,83 @@ __global__ __launch_bounds__(CT) void cae_up_kernel(CaeArgs a) {
   cae_gn_store<NJ>(a, vals, n, c0, To, red);
 }
 
+// The stage head on v_mfma_f32_16x16x4f32.  Output step t reads input steps m = (t + P) / s
+// (tap r = (t + P) % s) and m - 1 (tap r + s), so the outputs of one residue class r form a GEMM
+// D_r[co][m] = sum_q w[ci][co][r + tap s] x[ci][m - tap], q = 2 ci + tap over [0, 2C): the class's
+// weights pass through LDS one class at a time ([tap][ci][CG]), the input rows sit there with a
+// zero column at each end (steps -1 and T_in), the four waves take quarters of the 2C / 4
+// k-steps, and their partial tiles are summed in wave order.  Requires CG <= 16, s <= 4, and at
+// most 16 output steps per class (one column tile).
+template <int NJ, int S>
+__global__ __launch_bounds__(CT) void cae_up_mfma_kernel(CaeArgs a) {
+  extern __shared__ float xs[];  // [C][T_in + 2], then [2][C][CG] class weights, then [4][S][64][4]
+  __shared__ float red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lg = lane >> 4;
+  const int64_t bi = blockIdx.x, g = blockIdx.y;
+  const int C = (int)a.C, Ti = (int)a.T_in, To = (int)a.T_out, TP = Ti + 2, P = S / 2;
+  for (int e = tid; e < C * TP; e += CT) {
+    const int c = e / TP, u = e - c * TP, i = u - 1;
+    float v = 0.f;
+    if (i >= 0 && i < Ti) {
+      if (a.z) {  // x[c][i] = in_b[c] + sum_l in_w[c][l] z[i][l] (+ suite[c])
+        v = a.in_b[c];
+        const float* zr = a.z + (bi * a.T0 + i) * a.L;
+        for (int64_t l = 0; l < a.L; ++l) v += a.in_w[c * a.L + l] * zr[l];
+        if (a.suite) v += a.suite[bi * C + c];
+      } else {
+        v = a.x[(bi * C + c) * Ti + i];
+      }
+    }
+    xs[e] = v;
+  }
+  const int CG = C / (int)a.G, c0 = (int)g * CG;
+  float* wc = xs + C * TP;
+  float* part = wc + 2 * C * CG;
+  const int nks = (2 * C) / 4, ks0 = wave * nks / 4, ks1 = (wave + 1) * nks / 4;
+  const int row = l16 < CG ? l16 : 0;
+  const float rmask = l16 < CG ? 1.f : 0.f;
+  f32x4 acc[S];
+#pragma unroll
+  for (int r = 0; r < S; ++r) {
+    acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // class r: output steps t = r - P + S m for m in [m0, m1)
+    const int m0 = r < P ? 1 : 0, m1 = (To + P - r + S - 1) / S;
+    const int m = m0 + l16;
+    const float cmask = m < m1 ? 1.f : 0.f;
+    const int mc = m < m1 ? m : m0;
+    __syncthreads();   // the input rows are staged; the previous class's weights are consumed
+    for (int e = tid; e < 2 * C * CG; e += CT) {
+      const int tap = e / (C * CG), rem = e - tap * (C * CG), ci = rem / CG, col = rem - ci * CG;
+      wc[e] = a.w[((int64_t)ci * C + c0 + col) * (2 * S) + r + tap * S];
+    }
+    __syncthreads();
+    for (int ks = ks0; ks < ks1; ++ks) {
+      const int q = ks * 4 + lg, ci = q >> 1, tap = q & 1;
+      const float av = wc[(tap * C + ci) * CG + row] * rmask;
+      const float bv = xs[ci * TP + mc - tap + 1] * cmask;
+      acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[r], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < S; ++r) *reinterpret_cast<f32x4*>(part + ((wave * S + r) * 64 + lane) * 4) = acc[r];
+  __syncthreads();
+  const int n = CG * To;
+  float vals[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int e = tid + CT * j;
+    vals[j] = 0.f;
+    if (e >= n) continue;
+    const int col = e / To, t = e - col * To, r = (t + P) % S, m = (t + P) / S, m0 = r < P ? 1 : 0;
+    const int ln = (col >> 2) * 16 + (m - m0), el = col & 3;
+    float v = a.b[c0 + col];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v += part[((w * S + r) * 64 + ln) * 4 + el];
+    vals[j] = v;
+  }
+  cae_gn_store<NJ>(a, vals, n, c0, To, red);
+}
+
 // Conv1d (k = 3, padding 1) of this group's channels over every input channel, GroupNorm,
 // then SiLU or the residual add.  The input rows sit in LDS with a zero column at each end (the
 // padding), so the three taps need no branch; with WL the group's CG x C x 3 weights are staged
@@ -181,6 +258,70 @@ __global__ __launch_bounds__(CT) void cae_conv_kernel(CaeArgs a) {
   cae_gn_store<NJ>(a, vals, n, c0, T, red);
 }
 
+// The same convolution on v_mfma_f32_16x16x4f32 (fp32 in and out): D[co][t] = b[co] +
+// sum_q W[co][q] X[q / 3][t + q % 3] over q = (input channel, tap) in [0, 3C), W the group's
+// CG <= 16 rows of the [C][C][3] weight (contiguous in q; rows past CG read as zero), X the
+// zero-padded input rows.  Operand lanes: A[l % 16][q0 + l / 16], B[q0 + l / 16][16 nt + l % 16];
+// lane l holds D[4 (l / 16) + r][16 nt + l % 16].  The four waves take consecutive quarters of
+// the 3C / 4 k-steps; their partial tiles meet in LDS and are summed in wave order.
+template <int NJ, int NT>
+__global__ __launch_bounds__(CT) void cae_conv_mfma_kernel(CaeArgs a) {
+  extern __shared__ float xs[];  // [C][T + 2], then [CG][3C] weights, then [4][NT][64][4] partials
+  __shared__ float red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lg = lane >> 4;
+  const int64_t bi = blockIdx.x, g = blockIdx.y;
+  const int C = (int)a.C, T = (int)a.T_out, TP = T + 2, CG = C / (int)a.G, c0 = (int)g * CG, K3 = 3 * C;
+  for (int e = tid; e < C * TP; e += CT) {
+    const int c = e / TP, t = e - c * TP;
+    const bool in = t >= 1 && t <= T;
+    const float v = a.x[(bi * C + c) * T + (in ? t - 1 : 0)];
+    xs[e] = in ? v : 0.f;
+  }
+  float* wsm = xs + C * TP;
+  for (int e = tid; e < CG * K3; e += CT) wsm[e] = a.w[(int64_t)c0 * K3 + e];
+  float* part = wsm + CG * K3;
+  __syncthreads();
+  const int nks = K3 / 4, ks0 = wave * nks / 4, ks1 = (wave + 1) * nks / 4;
+  const int row = l16 < CG ? l16 : 0;
+  const float rmask = l16 < CG ? 1.f : 0.f;
+  f32x4 acc[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int tcol[NT];
+  float cmask[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int t = nt * 16 + l16;
+    tcol[nt] = t < T ? t : 0;
+    cmask[nt] = t < T ? 1.f : 0.f;
+  }
+  for (int ks = ks0; ks < ks1; ++ks) {
+    const int q = ks * 4 + lg, ci = q / 3, k = q - ci * 3;
+    const float av = wsm[row * K3 + q] * rmask;
+    const float* xr = xs + ci * TP + k;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, xr[tcol[nt]] * cmask[nt], acc[nt], 0, 0, 0);
+  }
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt)
+    *reinterpret_cast<f32x4*>(part + ((wave * NT + nt) * 64 + lane) * 4) = acc[nt];
+  __syncthreads();
+  const int n = CG * T;
+  float vals[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int e = tid + CT * j;
+    vals[j] = 0.f;
+    if (e >= n) continue;
+    const int col = e / T, t = e - col * T, nt = t >> 4, ln = (col >> 2) * 16 + (t & 15), r = col & 3;
+    float v = a.b[c0 + col];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) v += part[((w * NT + nt) * 64 + ln) * 4 + r];
+    vals[j] = v;
+  }
+  cae_gn_store<NJ>(a, vals, n, c0, T, red);
+}
+
 // output_proj over the horizon (time steps past the decoded length read zeros); the sample's
 // decoded rows [C][T_in] and the projection [A][C] are staged in LDS first.
 __global__ __launch_bounds__(CT) void cae_out_kernel(CaeArgs a) {
@@ -214,6 +355,47 @@ static int launch_nj(int n, bool up, const CaeArgs& a, hipStream_t s) {
   const size_t wl = (size_t)((a.C / a.G) * a.C * 3 * 4);
   const bool wlds = !up && xs + wl <= 64 * 1024;
   const size_t upl = xs + (size_t)(a.wchunk * (a.C / a.G) * 2 * a.stride * 4);
+  // the k = 3 convolution on the matrix cores: a group of <= 16 channels, <= 64 steps, 3C a
+  // multiple of 16 (4 waves x k-steps of 4), input rows + weights + partial tiles in 64 KB
+  const int64_t CG = a.C / a.G, NT = (a.T_out + 15) / 16;
+  const size_t mfl = xs + wl + (size_t)(4 * NT * 64 * 4 * 4);
+  // the stage head on the matrix cores: s <= 4, a group of <= 16 channels, <= 16 output steps per
+  // residue class, 2C a multiple of 16
+  const int64_t st = a.stride, P = st / 2;
+  bool up_m = up && st >= 1 && st <= 4 && CG <= 16 && (2 * a.C) % 16 == 0;
+  for (int64_t r = 0; up_m && r < st; ++r) {
+    const int64_t m0 = r < P ? 1 : 0, m1 = (a.T_out + P - r + st - 1) / st;
+    up_m = m1 - m0 <= 16;
+  }
+  const size_t upm = (size_t)((a.C * (a.T_in + 2) + 2 * a.C * CG + 4 * st * 64 * 4) * 4);
+  if (up_m && upm <= 64 * 1024) {
+#define FAM_CAE_U(NJ)                                                                       \
+    if (nj <= NJ) {                                                                         \
+      switch (st) {                                                                         \
+        case 1: FAM_LAUNCH((cae_up_mfma_kernel<NJ, 1>), grid, dim3(CT), upm, s, a); break;  \
+        case 2: FAM_LAUNCH((cae_up_mfma_kernel<NJ, 2>), grid, dim3(CT), upm, s, a); break;  \
+        case 3: FAM_LAUNCH((cae_up_mfma_kernel<NJ, 3>), grid, dim3(CT), upm, s, a); break;  \
+        default: FAM_LAUNCH((cae_up_mfma_kernel<NJ, 4>), grid, dim3(CT), upm, s, a); break; \
+      }                                                                                     \
+      return FAM_OK;                                                                        \
+    }
+    FAM_CAE_U(2) FAM_CAE_U(4)
+#undef FAM_CAE_U
+  }
+  if (!up && CG <= 16 && NT <= 4 && (3 * a.C) % 16 == 0 && mfl <= 64 * 1024) {
+#define FAM_CAE_M(NJ)                                                                         \
+    if (nj <= NJ) {                                                                           \
+      switch (NT) {                                                                           \
+        case 1: FAM_LAUNCH((cae_conv_mfma_kernel<NJ, 1>), grid, dim3(CT), mfl, s, a); break;  \
+        case 2: FAM_LAUNCH((cae_conv_mfma_kernel<NJ, 2>), grid, dim3(CT), mfl, s, a); break;  \
+        case 3: FAM_LAUNCH((cae_conv_mfma_kernel<NJ, 3>), grid, dim3(CT), mfl, s, a); break;  \
+        default: FAM_LAUNCH((cae_conv_mfma_kernel<NJ, 4>), grid, dim3(CT), mfl, s, a); break; \
+      }                                                                                       \
+      return FAM_OK;                                                                          \
+    }
+    FAM_CAE_M(2) FAM_CAE_M(4)
+#undef FAM_CAE_M
+  }
 #define FAM_CAE(NJ)                                                                   \
   if (nj <= NJ) {                                                                     \
     if (up) FAM_LAUNCH((cae_up_kernel<NJ>), grid, dim3(CT), upl, s, a);               \

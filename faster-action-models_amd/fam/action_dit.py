@@ -273,16 +273,19 @@ class FusedActionDiT:
         self.t2 = z(num_steps, H)
         self.tmod = z(num_steps, 6 * H)
         self.mods = z(num_steps, L, 6 * H)
-        self.ctx_h = z(ctx_len, H)
-        # the context K/V of every layer is one GEMM over K = H; a hidden width that is not a
-        # multiple of 64 (the tiny experts' 32) is zero-padded to the next one, so that product
-        # runs on the large-M kernel (which takes K in blocks of 64) instead of the generic tiled
-        # one: the embedding lands in the first H columns, the rest stay zero
+        # the text embedding's second layer and the context K/V of every layer are GEMMs over
+        # K = H; a hidden width that is not a multiple of 64 (the tiny experts' 32) is
+        # zero-padded to the next one, so those products run on the large-M kernel (which takes
+        # K in blocks of 64) instead of the generic tiled one: each activation lands in the first
+        # H columns of its buffer, the rest stay zero, and the weights get zero columns
         Hp = H if H % 64 == 0 or ctx_len < 128 else (H + 63) // 64 * 64
         if Hp != H:
-            kvw = w["ctxkv_w"]
-            w["ctxkv_w"] = torch.cat([kvw, torch.zeros(kvw.shape[0], Hp - H, dtype=kvw.dtype, device=kvw.device)],
-                                     dim=1).contiguous()
+            for key in ("txt2_w", "ctxkv_w"):
+                wt = w[key]
+                w[key] = torch.cat([wt, torch.zeros(wt.shape[0], Hp - H, dtype=wt.dtype, device=wt.device)],
+                                   dim=1).contiguous()
+        self.ctx_h_pad = z(ctx_len, Hp)
+        self.ctx_h = self.ctx_h_pad[:, :H]
         self.ctx_emb_pad = z(ctx_len, Hp)
         self.ctx_emb = self.ctx_emb_pad[:, :H]
         self.ctxkv = z(ctx_len, L * 2 * A)
@@ -343,7 +346,7 @@ class FusedActionDiT:
     # ------------------------------------------------------------------ plan building
     def _gemm(self, name, a, w, bias, out, *, prologue=_capi.FAM_PRO_NONE, pro_w=None, pro_b=None,
               shift=None, scale=None, act=_capi.FAM_ACT_NONE, res=None, gate=None, gate_strides=(0, 0, 1),
-              rows_per_batch=None, M=None, K=None, lda=None, ldo=None, ldr=None, out_f32=False):
+              rows_per_batch=None, M=None, K=None, lda=None, ldo=None, ldr=None, out_f32=False, ws=None):
         d = _capi.GemmDesc()
         Mv = a.shape[0] if M is None else M
         Kv = w.shape[1] if K is None else K
@@ -367,14 +370,24 @@ class FusedActionDiT:
         d.rows_per_batch = rows_per_batch or max(Mv, 1)
         d.out_f32 = int(out_f32)
         self._descs.append(d)
-        f = self.lib.fam_gemm
         lib = self.lib
         ref = C.byref(d)
+        if ws is not None:
+            # fam_gemm_ws: the planner may split K over the workspace (its planes summed by a row
+            # launch that also applies the epilogue)
+            f, wsp, wsn = self.lib.fam_gemm_ws, ws.data_ptr(), ws.numel()
 
-        def run(stream):
-            rc = f(ref, stream)
-            if rc != 0:
-                raise FamError(f"fam_gemm[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
+            def run(stream):
+                rc = f(ref, wsp, wsn, stream)
+                if rc != 0:
+                    raise FamError(f"fam_gemm_ws[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
+        else:
+            f = self.lib.fam_gemm
+
+            def run(stream):
+                rc = f(ref, stream)
+                if rc != 0:
+                    raise FamError(f"fam_gemm[{name}]", rc, lib.fam_last_error().decode(errors="replace"))
         N = d.N
         nbytes = 2 * (Mv * Kv + N * Kv + Mv * N) + (2 * N if bias is not None else 0)
         nbytes += 2 * Mv * N if res is not None else 0
@@ -686,8 +699,13 @@ class FusedActionDiT:
         plan.add("modulation", _checked(lib, "fam_add_modulation", self.tmod.data_ptr(), w["mod"].data_ptr(),
                                         self.mods.data_ptr(), T, L, 6 * H), "modulation",
                  2 * 6 * H * (T + L + T * L))
-        self._gemm("ctx_emb0", self.context_in, w["txt0_w"], w["txt0_b"], self.ctx_h, act=_capi.FAM_ACT_GELU_TANH)
-        self._gemm("ctx_emb2", self.ctx_h, w["txt2_w"], w["txt2_b"], self.ctx_emb)
+        # the text embedding's first layer (ctx_len x H x text_dim: few output tiles, a long K) may
+        # split K over a workspace
+        nws = int(lib.fam_gemm_ws_floats(Lc, H, cfg.text_dim))
+        self.ctx_ws = torch.empty(max(nws, 1), dtype=torch.float32, device=self.device) if nws > 0 else None
+        self._gemm("ctx_emb0", self.context_in, w["txt0_w"], w["txt0_b"], self.ctx_h, act=_capi.FAM_ACT_GELU_TANH,
+                   ws=self.ctx_ws)
+        self._gemm("ctx_emb2", self.ctx_h_pad, w["txt2_w"], w["txt2_b"], self.ctx_emb)
         self._gemm("ctx_kv", self.ctx_emb_pad, w["ctxkv_w"], w["ctxkv_b"], self.ctxkv)
         kvp = self.ctxkv.data_ptr()
         # RMSNorm of every block's context keys in one launch: row (i, l) = ctxkv[i, 2 A l ..]
