@@ -137,18 +137,21 @@ __global__ __launch_bounds__(CT) void cae_up_kernel(CaeArgs a) {
 
 // The stage head on v_mfma_f32_16x16x4f32.  Output step t reads input steps m = (t + P) / s
 // (tap r = (t + P) % s) and m - 1 (tap r + s), so the outputs of one residue class r form a GEMM
-// D_r[co][m] = sum_q w[ci][co][r + tap s] x[ci][m - tap], q = 2 ci + tap over [0, 2C): the class's
-// weights pass through LDS one class at a time ([tap][ci][CG]), the input rows sit there with a
-// zero column at each end (steps -1 and T_in), the four waves take quarters of the 2C / 4
-// k-steps, and their partial tiles are summed in wave order.  Requires CG <= 16, s <= 4, and at
-// most 16 output steps per class (one column tile).
+// D_r[co][m] = sum_q w[ci][co][r + tap s] x[ci][m - tap], q = 2 ci + tap over [0, 2C).  The
+// group's weights (w[ci][c0 .. c0 + CG)[0 .. 2s): 2 s CG contiguous floats per input channel)
+// pass through LDS in two halves of the input channels by 16-byte loads; the input rows sit
+// there with a zero column at each end (steps -1 and T_in); in each half the four waves take
+// quarters of the k-steps of every class, and their partial tiles are summed in wave order.
+// Requires CG <= 16, s <= 4, at most 16 output steps per class, 2 s CG and C / 2 multiples of 4.
 template <int NJ, int S>
 __global__ __launch_bounds__(CT) void cae_up_mfma_kernel(CaeArgs a) {
-  extern __shared__ float xs[];  // [C][T_in + 2], then [2][C][CG] class weights, then [4][S][64][4]
+  extern __shared__ float xs[];  // [C][T_in + 2], then [C / 2][CG][2s] weights, then [4][S][64][4]
   __shared__ float red[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lg = lane >> 4;
   const int64_t bi = blockIdx.x, g = blockIdx.y;
-  const int C = (int)a.C, Ti = (int)a.T_in, To = (int)a.T_out, TP = Ti + 2, P = S / 2;
+  const int C = (int)a.C, Ti = (int)a.T_in, To = (int)a.T_out, TP = Ti + 2, P = S / 2, K2 = 2 * S;
+  const int CG = C / (int)a.G, c0 = (int)g * CG, RW = CG * K2, CH = C / 2;
+  const bool v4 = a.L % 4 == 0;
   for (int e = tid; e < C * TP; e += CT) {
     const int c = e / TP, u = e - c * TP, i = u - 1;
     float v = 0.f;
@@ -156,7 +159,18 @@ __global__ __launch_bounds__(CT) void cae_up_mfma_kernel(CaeArgs a) {
       if (a.z) {  // x[c][i] = in_b[c] + sum_l in_w[c][l] z[i][l] (+ suite[c])
         v = a.in_b[c];
         const float* zr = a.z + (bi * a.T0 + i) * a.L;
-        for (int64_t l = 0; l < a.L; ++l) v += a.in_w[c * a.L + l] * zr[l];
+        const float* wr = a.in_w + c * a.L;
+        if (v4) {
+          for (int64_t l = 0; l < a.L; l += 4) {
+            const f32x4 wv = *reinterpret_cast<const f32x4*>(wr + l), zv = *reinterpret_cast<const f32x4*>(zr + l);
+            v += wv[0] * zv[0];
+            v += wv[1] * zv[1];
+            v += wv[2] * zv[2];
+            v += wv[3] * zv[3];
+          }
+        } else {
+          for (int64_t l = 0; l < a.L; ++l) v += wr[l] * zr[l];
+        }
         if (a.suite) v += a.suite[bi * C + c];
       } else {
         v = a.x[(bi * C + c) * Ti + i];
@@ -164,32 +178,39 @@ __global__ __launch_bounds__(CT) void cae_up_mfma_kernel(CaeArgs a) {
     }
     xs[e] = v;
   }
-  const int CG = C / (int)a.G, c0 = (int)g * CG;
   float* wc = xs + C * TP;
-  float* part = wc + 2 * C * CG;
-  const int nks = (2 * C) / 4, ks0 = wave * nks / 4, ks1 = (wave + 1) * nks / 4;
+  float* part = wc + CH * RW;
+  const int nks = CH / 2, ks0 = wave * nks / 4, ks1 = (wave + 1) * nks / 4;   // k-steps of 4 per half
   const int row = l16 < CG ? l16 : 0;
   const float rmask = l16 < CG ? 1.f : 0.f;
   f32x4 acc[S];
+  int mcol[S];
+  float cmask[S];
 #pragma unroll
   for (int r = 0; r < S; ++r) {
     acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
     // class r: output steps t = r - P + S m for m in [m0, m1)
-    const int m0 = r < P ? 1 : 0, m1 = (To + P - r + S - 1) / S;
-    const int m = m0 + l16;
-    const float cmask = m < m1 ? 1.f : 0.f;
-    const int mc = m < m1 ? m : m0;
-    __syncthreads();   // the input rows are staged; the previous class's weights are consumed
-    for (int e = tid; e < 2 * C * CG; e += CT) {
-      const int tap = e / (C * CG), rem = e - tap * (C * CG), ci = rem / CG, col = rem - ci * CG;
-      wc[e] = a.w[((int64_t)ci * C + c0 + col) * (2 * S) + r + tap * S];
+    const int m0 = r < P ? 1 : 0, m1 = (To + P - r + S - 1) / S, m = m0 + l16;
+    cmask[r] = m < m1 ? 1.f : 0.f;
+    mcol[r] = m < m1 ? m : m0;
+  }
+  for (int h = 0; h < 2; ++h) {
+    const int ci0 = h * CH;
+    __syncthreads();   // the input rows are staged; the previous half's weights are consumed
+    for (int e = tid; e < CH * RW / 4; e += CT) {
+      const int ci = e / (RW / 4), q4 = e - ci * (RW / 4);
+      *reinterpret_cast<f32x4*>(wc + 4 * e) =
+          *reinterpret_cast<const f32x4*>(a.w + ((int64_t)(ci0 + ci) * C + c0) * K2 + 4 * q4);
     }
     __syncthreads();
-    for (int ks = ks0; ks < ks1; ++ks) {
-      const int q = ks * 4 + lg, ci = q >> 1, tap = q & 1;
-      const float av = wc[(tap * C + ci) * CG + row] * rmask;
-      const float bv = xs[ci * TP + mc - tap + 1] * cmask;
-      acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[r], 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < S; ++r) {
+      for (int ks = ks0; ks < ks1; ++ks) {
+        const int q = ks * 4 + lg, ci = q >> 1, tap = q & 1;
+        const float av = wc[ci * RW + row * K2 + r + tap * S] * rmask;
+        const float bv = xs[(ci0 + ci) * TP + mcol[r] - tap + 1] * cmask[r];
+        acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc[r], 0, 0, 0);
+      }
     }
   }
 #pragma unroll
@@ -362,12 +383,14 @@ static int launch_nj(int n, bool up, const CaeArgs& a, hipStream_t s) {
   // the stage head on the matrix cores: s <= 4, a group of <= 16 channels, <= 16 output steps per
   // residue class, 2C a multiple of 16
   const int64_t st = a.stride, P = st / 2;
-  bool up_m = up && st >= 1 && st <= 4 && CG <= 16 && (2 * a.C) % 16 == 0;
+  bool up_m = up && st >= 1 && st <= 4 && CG <= 16 && (a.C / 2) % 8 == 0 && (2 * st * CG) % 4 == 0 &&
+              ((uintptr_t)a.w & 15u) == 0 &&
+              (!a.z || (((uintptr_t)a.in_w & 15u) == 0 && ((uintptr_t)a.z & 15u) == 0));
   for (int64_t r = 0; up_m && r < st; ++r) {
     const int64_t m0 = r < P ? 1 : 0, m1 = (a.T_out + P - r + st - 1) / st;
     up_m = m1 - m0 <= 16;
   }
-  const size_t upm = (size_t)((a.C * (a.T_in + 2) + 2 * a.C * CG + 4 * st * 64 * 4) * 4);
+  const size_t upm = (size_t)((a.C * (a.T_in + 2) + (a.C / 2) * CG * 2 * st + 4 * st * 64 * 4) * 4);
   if (up_m && upm <= 64 * 1024) {
 #define FAM_CAE_U(NJ)                                                                       \
     if (nj <= NJ) {                                                                         \
