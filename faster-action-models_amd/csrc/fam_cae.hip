@@ -28,10 +28,11 @@ struct CaeArgs {
   const float* ow; const float* ob; float* out;
 };
 
-// Sum of v over the workgroup (fixed order: wave sums, then waves in order).
+// Sum of v over the workgroup (fixed order: 16-lane rows by DPP, the four rows by lane swaps,
+// then the waves in order).
 __device__ __forceinline__ float cae_block_sum(float v, float* red) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  v = wave_sum(v);
+  v = group4_sum(row16_sum(v));
   __syncthreads();
   if (lane == 0) red[wave] = v;
   __syncthreads();
@@ -299,7 +300,9 @@ __global__ __launch_bounds__(CT) void cae_conv_mfma_kernel(CaeArgs a) {
     xs[e] = in ? v : 0.f;
   }
   float* wsm = xs + C * TP;
-  for (int e = tid; e < CG * K3; e += CT) wsm[e] = a.w[(int64_t)c0 * K3 + e];
+  // the group's CG x 3C weights: one contiguous block (16-byte aligned: 3C % 16 == 0 here)
+  for (int e = tid; e < CG * K3 / 4; e += CT)
+    *reinterpret_cast<f32x4*>(wsm + 4 * e) = *reinterpret_cast<const f32x4*>(a.w + (int64_t)c0 * K3 + 4 * e);
   float* part = wsm + CG * K3;
   __syncthreads();
   const int nks = K3 / 4, ks0 = wave * nks / 4, ks1 = (wave + 1) * nks / 4;
@@ -405,7 +408,7 @@ static int launch_nj(int n, bool up, const CaeArgs& a, hipStream_t s) {
     FAM_CAE_U(2) FAM_CAE_U(4)
 #undef FAM_CAE_U
   }
-  if (!up && CG <= 16 && NT <= 4 && (3 * a.C) % 16 == 0 && mfl <= 64 * 1024) {
+  if (!up && CG <= 16 && NT <= 4 && (3 * a.C) % 16 == 0 && mfl <= 64 * 1024 && ((uintptr_t)a.w & 15u) == 0) {
 #define FAM_CAE_M(NJ)                                                                         \
     if (nj <= NJ) {                                                                           \
       switch (NT) {                                                                           \
