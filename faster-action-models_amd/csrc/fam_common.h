@@ -91,6 +91,10 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// Sum over the 64 lanes, the same in every lane, without LDS: the 16-lane rows (DPP), then the
+// four rows (lane swaps).  (wave_sum's order is the reverse: 32, 16, ..., 1.)
+__device__ __forceinline__ float wave_sum_valu(float v) { return group4_sum(row16_sum(v)); }
+
 __device__ __forceinline__ bf16x8 load8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 __device__ __forceinline__ void store8(bf16* p, bf16x8 v) { *reinterpret_cast<bf16x8*>(p) = v; }
 

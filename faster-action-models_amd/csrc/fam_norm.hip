@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
           for (int e = 0; e < 8; ++e) s += to_f(xv8[k][i][e]);
         }
       }
-      const float mean = wave_sum(s) * invD;
+      const float mean = wave_sum_valu(s) * invD;
       float q = 0.f;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
@@ -115,7 +115,7 @@ __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
           for (int e = 0; e < 8; ++e) { const float d = to_f(xv8[k][i][e]) - mean; q += d * d; }
         }
       }
-      const float rstd = rsqrtf(wave_sum(q) * invD + a.eps);
+      const float rstd = rsqrtf(wave_sum_valu(q) * invD + a.eps);
       if constexpr (MOD == 2) {
         // the batch's shift / scale row (L2-resident), all of it in one round trip
 #pragma unroll
@@ -149,14 +149,14 @@ __global__ __launch_bounds__(256) void adaln_kernel(AdalnArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) s += to_f(t[e]);
     }
-    const float mean = wave_sum(s) * invD;
+    const float mean = wave_sum_valu(s) * invD;
     float q = 0.f;
     for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
       bf16x8 t = load8(xr + c);
 #pragma unroll
       for (int e = 0; e < 8; ++e) { const float d = to_f(t[e]) - mean; q += d * d; }
     }
-    const float rstd = rsqrtf(wave_sum(q) * invD + a.eps);
+    const float rstd = rsqrtf(wave_sum_valu(q) * invD + a.eps);
     for (int64_t c = (int64_t)lane * 8; c < D; c += 512) {
       bf16x8 t = load8(xr + c);
       float xv[8];
@@ -205,7 +205,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_kernel(RmsRopeArgs a) {
       for (int e = 0; e < 8; ++e) { const float f = to_f(t[e]); q += f * f; }
     }
   }
-  const float rs = a.w ? rsqrtf(wave_sum(q) / (float)D + a.eps) : 1.0f;
+  const float rs = a.w ? rsqrtf(wave_sum_valu(q) / (float)D + a.eps) : 1.0f;
   const int64_t pos = r % a.seq;
   bf16* yr = a.y + r * a.yrs;
   const bf16* wr = a.w ? a.w + (r % a.wgp) * D : nullptr;
@@ -301,7 +301,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rope_vec_kernel(RmsRopeArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) { const float f = ok ? to_f(in[k][i][e]) : 0.f; q += f * f; }
     }
-    const float rs = a.w ? rsqrtf(wave_sum(q) / (float)D + a.eps) : 1.0f;
+    const float rs = a.w ? rsqrtf(wave_sum_valu(q) / (float)D + a.eps) : 1.0f;
     bf16* yr = a.y + (r0 + k) * a.yrs;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
