@@ -13,8 +13,9 @@
 //                 in column slice g, RMSNorm + 1-D RoPE, attention over [video K/V ; action
 //                 K/V], and the slice's share of the o projection (fp32 partial);
 //   cross (g, b): x += gate_msa (sum of the o partials + bias), affine LayerNorm3, the slice's
-//                 cross-attention query + RMSNorm, attention over the context K/V, and the
-//                 slice's share of the cross o projection.
+//                 cross-attention query + RMSNorm, attention over the context, and the slice's
+//                 share of the cross o projection.  A slice wider than the 32-wide rows attends
+//                 in the space of the context rows (attend_ctx) instead of reading its K / V.
 //
 // The phase boundaries are exactly the two cross-head reductions of a block (the o projections
 // sum over all heads); everything else a workgroup needs it recomputes from the previous
@@ -66,6 +67,11 @@ struct TinyArgs {
   const float* gram_c;
   const float* gram_b;
   float *lat, *xa, *xb, *part_s, *part_c, *out;
+  const bf16* ctx_emb;
+  int64_t ctx_emb_ld;
+  const bf16 *ck_wt, *ck_b, *cnk_w, *cv_w, *cv_b;
+  float* ctx_rs;
+  int Lcp;   // keys of ctx_rs per layer (Lc rounded up to 32)
   int p0, p1;
 };
 
@@ -252,10 +258,10 @@ __device__ __forceinline__ void gram_load(const TinyArgs& a, int l, int which, G
   for (int t = 0; t < 2; ++t) {
 #pragma unroll
     for (int hl = 0; hl < 2; ++hl)
-      gf.g[t][hl] = load8(a.gram + ((size_t)((l * 3 + which) * 2 + hl) * TH + t * 16 + l16) * TH + lg * 8);
-    gf.c[t] = *reinterpret_cast<const f32x4*>(a.gram_c + (size_t)(l * 3 + which) * TH + t * 16 + lg * 4);
+      gf.g[t][hl] = load8(a.gram + ((size_t)((l * 4 + which) * 2 + hl) * TH + t * 16 + l16) * TH + lg * 8);
+    gf.c[t] = *reinterpret_cast<const f32x4*>(a.gram_c + (size_t)(l * 4 + which) * TH + t * 16 + lg * 4);
   }
-  gf.beta = a.gram_b[l * 3 + which];
+  gf.beta = a.gram_b[l * 4 + which];
 }
 
 // sum_j q_j^2 of row l16 from the Gram form; lanes of group 0 store it (rows < S)
@@ -369,6 +375,43 @@ __device__ __forceinline__ void kv_patch(TinySmem<W, NCB>& sm, const KvSrc& src,
   }
 }
 
+// Online softmax of one 32-key block for one column block: sc[sub][e] is the score (exp2 units,
+// -inf when masked) of key 16 sub + 4 lg + e of column l16.  The running max moves only when a
+// score passes it by more than 2^8 (exp2 units), so p <= 2^8 in between (exact in fp32, bf16 keeps
+// its relative precision) and the accumulators are rescaled only on the blocks where some column
+// of the wave moved (the first, mostly): returns true with alpha then.  pf: the P^T fragment.
+__device__ __forceinline__ bool softmax_block(const float (&sc)[2][4], float& m, float& lsum, bf16x8& pf,
+                                              float& alpha) {
+  float mb = -INFINITY;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mb = fmaxf(mb, sc[sub][e]);
+  mb = group4_max(mb);
+  const bool up = mb > m + 8.0f;
+  const float mn = up ? mb : m;
+  const float ms = mn == -INFINITY ? 0.f : mn;
+  float ps = 0.f;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p = __builtin_amdgcn_exp2f(sc[sub][e] - ms);
+      ps += p;
+      pf[sub * 4 + e] = to_bf(p);
+    }
+  ps = group4_sum(ps);
+  if (__any(up)) {
+    alpha = __builtin_amdgcn_exp2f(m - ms);   // unchanged max: 1; -inf: 0
+    lsum = lsum * alpha + ps;
+    m = mn;
+    return true;
+  }
+  lsum += ps;
+  m = mn;
+  return false;
+}
+
 // One 32-key block of a wave: V rows into the wave's tile, scores, online softmax, O^T += V^T P^T.
 template <int W, int NCB>
 __device__ __forceinline__ void attend_block(const TinyArgs& a, const KvBlock<W>& kv, int blk, int n,
@@ -388,7 +431,6 @@ __device__ __forceinline__ void attend_block(const TinyArgs& a, const KvBlock<W>
 #pragma unroll
   for (int cb = 0; cb < NCB; ++cb) {
     float sc[2][4];
-    float mb = -INFINITY;
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
       f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -399,37 +441,14 @@ __device__ __forceinline__ void attend_block(const TinyArgs& a, const KvBlock<W>
         const int kk = blk * 32 + sub * 16 + lg * 4 + e;
         bool ok = kk < n;
         if (mask != nullptr) ok = ok && (qs[cb] < 0 || mask[(int64_t)qs[cb] * mask_rs + kk] != 0);
-        const float x = ok ? d[e] * a.scale_log2 : -INFINITY;
-        sc[sub][e] = x;
-        mb = fmaxf(mb, x);
+        sc[sub][e] = ok ? d[e] * a.scale_log2 : -INFINITY;
       }
     }
-    mb = group4_max(mb);
-    // the running max moves only when a score passes it by more than 2^8 (exp2 units), so p <= 2^8
-    // in between (exact in fp32, bf16 keeps its relative precision) and the accumulators are
-    // rescaled only on the blocks where some column of the wave moved (the first, mostly)
-    const bool up = mb > m[cb] + 8.0f;
-    const float mn = up ? mb : m[cb];
-    const float ms = mn == -INFINITY ? 0.f : mn;
-    float ps = 0.f;
-#pragma unroll
-    for (int sub = 0; sub < 2; ++sub)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float p = __builtin_amdgcn_exp2f(sc[sub][e] - ms);
-        ps += p;
-        pf[cb][sub * 4 + e] = to_bf(p);
-      }
-    ps = group4_sum(ps);
-    if (__any(up)) {
-      const float alpha = __builtin_amdgcn_exp2f(m[cb] - ms);   // unchanged max: 1; -inf: 0
-      lsum[cb] = lsum[cb] * alpha + ps;
+    float alpha;
+    if (softmax_block(sc, m[cb], lsum[cb], pf[cb], alpha)) {
 #pragma unroll
       for (int dt = 0; dt < WT; ++dt) acc[dt][cb] *= alpha;
-    } else {
-      lsum[cb] += ps;
     }
-    m[cb] = mn;
   }
   // O^T += V^T P^T: V^T fragment rows = dims 16 dt + l16, k = keys {4 lg..+3, 16 + 4 lg..+3}
   typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -583,6 +602,234 @@ __device__ __forceinline__ void attend(const TinyArgs& a, TinySmem<W, NCB>& sm, 
   lds_barrier();
 }
 
+// ---------------------------------------------------------------------------------------
+// Context attention in the 32-wide space of the context rows (slices wider than the rows).  For
+// the key k = r (W_k h + b_k) * w_k of a context row h (r: its RMS factor over all A columns, w_k:
+// the key norm weight) and the query q_c of column c = (head, token), zero outside its head,
+//   q_c . k = r (h . Q_c + beta_c),   Q_c = W_k^T (q_c * w_k),   beta_c = b_k . (q_c * w_k),
+// and the output is  sum_key p (W_v h + b_v) / l = W_v Z_c + b_v  with  Z_c = sum_key p h / l.
+// A 32-key block then reads 2 KB of rows and 128 B of factors (the slice's K and V would be
+// 4 W bytes per key), and its products are 32 deep.  Q_c and Z_c enter their products as hi + lo
+// bf16 parts; q_c * w_k is rounded to bf16 once (sm.q holds it).  The block's 32-wide columns
+// run in the order {4 lg .. 4 lg + 3, 16 + 4 lg .. + 3} in every operand (the order in which an
+// MFMA result leaves Q_c in the lanes), which leaves each product's sum unchanged.
+template <int W>
+struct CtxFrags {
+  static constexpr int PV = (W / 16 + 3) / 4;   // W_v tiles per wave
+  bf16x8 kt[2][W / 32];   // W_k^T rows 16 t + l16, slice columns 32 kb + 8 lg .. + 7
+  bf16x8 bk[W / 32];      // b_k at the same columns
+  bf16x8 vw[PV];          // W_v rows g W + 16 tau + l16 (tau = wave + 4 i), columns 8 lg .. + 7
+  bf16x4 vb[PV];          // b_v[g W + 16 tau + 4 lg .. + 3]
+};
+
+template <int W>
+__device__ __forceinline__ void ctx_frags_load(const TinyArgs& a, int l, int g, CtxFrags<W>& f) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lg = lane >> 4;
+  const int A = a.A;
+  const bf16* kt = a.ck_wt + (size_t)l * TH * A + g * W;
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int kb = 0; kb < W / 32; ++kb) f.kt[t][kb] = load8(kt + (size_t)(t * 16 + l16) * A + kb * 32 + lg * 8);
+#pragma unroll
+  for (int kb = 0; kb < W / 32; ++kb) f.bk[kb] = load8(a.ck_b + (size_t)l * A + g * W + kb * 32 + lg * 8);
+#pragma unroll
+  for (int i = 0; i < CtxFrags<W>::PV; ++i) {
+    int tau = wave + 4 * i;
+    tau = tau < W / 16 ? tau : W / 16 - 1;
+    const int row = g * W + tau * 16;
+    f.vw[i] = load8(a.cv_w + ((size_t)l * A + row + l16) * TH + lg * 8);
+    f.vb[i] = *reinterpret_cast<const bf16x4*>(a.cv_b + (size_t)l * A + row + lg * 4);
+  }
+}
+
+struct CtxBlock {
+  bf16x8 h[2];   // row 32 blk + 16 sub + l16, columns {4 lg .. + 3, 16 + 4 lg .. + 3}
+  f32x4 r[2];    // factors (r * scale * log2 e) of keys 32 blk + 16 sub + 4 lg .. + 3
+};
+
+// rows past Lc read row 0, blocks past the last read block 0 (scores masked, values weighed by 0)
+__device__ __forceinline__ void ctx_block_load(const TinyArgs& a, int l, int blk, CtxBlock& cb) {
+  const int lane = threadIdx.x & 63, l16 = lane & 15, lg = lane >> 4;
+  const int bb = blk * 32 < a.Lcp ? blk : 0;
+#pragma unroll
+  for (int sub = 0; sub < 2; ++sub) {
+    int kk = bb * 32 + sub * 16 + l16;
+    kk = kk < a.Lc ? kk : 0;
+    const bf16* row = a.ctx_emb + (size_t)kk * a.ctx_emb_ld;
+    const bf16x4 lo = *reinterpret_cast<const bf16x4*>(row + 4 * lg);
+    const bf16x4 hi = *reinterpret_cast<const bf16x4*>(row + 16 + 4 * lg);
+    cb.h[sub] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    cb.r[sub] = *reinterpret_cast<const f32x4*>(a.ctx_rs + (size_t)l * a.Lcp + bb * 32 + sub * 16 + 4 * lg);
+  }
+}
+
+// Folded queries, online softmax over the context blocks (round-robin over the waves, the wave's
+// rows staged in its tile for the transposed reads of Z^T += H^T P^T), the waves merged in order
+// into Z (hi + lo bf16 in LDS), then O^T = W_v Z^T + b_v of the slice's dims -> sm.o.
+template <int W, int NCB>
+__device__ __forceinline__ void attend_ctx(const TinyArgs& a, TinySmem<W, NCB>& sm, int l, const CtxFrags<W>& f,
+                                           CtxBlock& cur) {
+  constexpr int WK = W / 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lg = lane >> 4;
+  const int S = a.S, n = a.Lc, nblk = (n + 31) / 32;
+  const int dsh = __builtin_ctz(a.DH), nc = (W >> dsh) * S;
+  // Q_c^T (hi, lo) and beta_c of column c = cb * 16 + l16 = (head hh, token s)
+  bf16x8 qh[NCB], ql[NCB];
+  float beta[NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    const int c = cb * 16 + l16, hh = c / S, s = c - hh * S;
+    f32x4 d0 = f32x4{0.f, 0.f, 0.f, 0.f}, d1 = d0;
+    float bs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < WK; ++kb) {
+      const int c0 = kb * 32 + lg * 8;
+      const bf16x8 x = *reinterpret_cast<const bf16x8*>(&sm.q[c < nc ? s : 0][c0]);
+      const bf16x8 qf = (c < nc && (c0 >> dsh) == hh) ? x : zero8();
+#pragma unroll
+      for (int e = 0; e < 8; ++e) bs += to_f(qf[e]) * to_f(f.bk[kb][e]);
+      d0 = mfma16(f.kt[0][kb], qf, d0);   // Q_c[4 lg + e]
+      d1 = mfma16(f.kt[1][kb], qf, d1);   // Q_c[16 + 4 lg + e]
+    }
+    beta[cb] = group4_sum(bs);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      qh[cb][e] = to_bf(d0[e]);
+      ql[cb][e] = to_bf(d0[e] - to_f(qh[cb][e]));
+      qh[cb][4 + e] = to_bf(d1[e]);
+      ql[cb][4 + e] = to_bf(d1[e] - to_f(qh[cb][4 + e]));
+    }
+  }
+  float m[NCB], lsum[NCB];
+  f32x4 acc[2][NCB];
+#pragma unroll
+  for (int cb = 0; cb < NCB; ++cb) {
+    m[cb] = -INFINITY;
+    lsum[cb] = 0.f;
+    acc[0][cb] = acc[1][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  bf16(*ht)[48] = reinterpret_cast<bf16(*)[48]>(&sm.vt[wave][0][0]);   // 32 rows x 32 (+ 16 pad)
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  for (int blk = wave; blk < nblk; blk += 4) {
+    CtxBlock nx;
+    if (blk + 4 < nblk) ctx_block_load(a, l, blk + 4, nx);
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      *reinterpret_cast<bf16x4*>(&ht[sub * 16 + l16][4 * lg]) = __builtin_shufflevector(cur.h[sub], cur.h[sub], 0, 1, 2, 3);
+      *reinterpret_cast<bf16x4*>(&ht[sub * 16 + l16][16 + 4 * lg]) =
+          __builtin_shufflevector(cur.h[sub], cur.h[sub], 4, 5, 6, 7);
+    }
+    bf16x8 pf[NCB];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      float sc[2][4];
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        f32x4 d = mfma16(cur.h[sub], qh[cb], f32x4{0.f, 0.f, 0.f, 0.f});
+        d = mfma16(cur.h[sub], ql[cb], d);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int kk = blk * 32 + sub * 16 + lg * 4 + e;
+          sc[sub][e] = kk < n ? (d[e] + beta[cb]) * cur.r[sub][e] : -INFINITY;
+        }
+      }
+      float alpha;
+      if (softmax_block(sc, m[cb], lsum[cb], pf[cb], alpha)) {
+        acc[0][cb] *= alpha;
+        acc[1][cb] *= alpha;
+      }
+    }
+    // H^T fragments: rows = columns 16 t + l16, k = keys {4 lg .. + 3, 16 + 4 lg .. + 3}
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int key = lg * 4 + (l16 >> 2), col = t * 16 + 4 * (l16 & 3);
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&ht[key][col]);
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s16x4*)(__attribute__((address_space(3))) bf16*)&ht[key + 16][col]);
+      const s16x8 h8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      const bf16x8 hf = __builtin_bit_cast(bf16x8, h8);
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) acc[t][cb] = mfma16(hf, pf[cb], acc[t][cb]);
+    }
+    if (blk + 4 < nblk) cur = nx;
+  }
+  // merge the waves' states through LDS, in wave order
+  if (lg == 0) {
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+      sm.u.mg.m[wave][cb * 16 + l16] = m[cb];
+      sm.u.mg.l[wave][cb * 16 + l16] = lsum[cb];
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb)
+      *reinterpret_cast<f32x4*>(&sm.u.mg.acc[wave][cb * 16 + l16][t * 16 + lg * 4]) = acc[t][cb];
+  lds_barrier();
+  // Z of every column (8 of its 32 entries per thread) as hi + lo bf16; the wave tiles are free
+  bf16(*zh)[40] = reinterpret_cast<bf16(*)[40]>(&sm.vt[0][0][0]);
+  bf16(*zl)[40] = zh + NCB * 16;
+  if (threadIdx.x < NCB * 64) {
+    const int c = threadIdx.x >> 2, j0 = (threadIdx.x & 3) * 8;
+    float mw[4], mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      mw[w] = sm.u.mg.m[w][c];
+      mx = fmaxf(mx, mw[w]);
+    }
+    const float ms = mx == -INFINITY ? 0.f : mx;
+    float fw[4], den = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      fw[w] = __builtin_amdgcn_exp2f(mw[w] - ms);
+      den += fw[w] * sm.u.mg.l[w][c];
+    }
+    f32x4 z0 = f32x4{0.f, 0.f, 0.f, 0.f}, z1 = z0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      z0 += fw[w] * *reinterpret_cast<const f32x4*>(&sm.u.mg.acc[w][c][j0]);
+      z1 += fw[w] * *reinterpret_cast<const f32x4*>(&sm.u.mg.acc[w][c][j0 + 4]);
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    bf16x8 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float u = z0[e] * inv, v = z1[e] * inv;
+      hi[e] = to_bf(u);
+      lo[e] = to_bf(u - to_f(hi[e]));
+      hi[4 + e] = to_bf(v);
+      lo[4 + e] = to_bf(v - to_f(hi[4 + e]));
+    }
+    *reinterpret_cast<bf16x8*>(&zh[c][j0]) = hi;
+    *reinterpret_cast<bf16x8*>(&zl[c][j0]) = lo;
+  }
+  lds_barrier();
+  // O^T = W_v Z^T + b_v: dims 16 tau + 4 lg + e of column cb * 16 + l16, kept where the dims
+  // belong to the column's head (4 consecutive dims never straddle a head: head_dim % 8 == 0)
+#pragma unroll
+  for (int i = 0; i < CtxFrags<W>::PV; ++i) {
+    const int tau = wave + 4 * i;
+    if (tau < W / 16) {
+#pragma unroll
+      for (int cb = 0; cb < NCB; ++cb) {
+        const int c = cb * 16 + l16, hh = c / S, s = c - hh * S, d0 = tau * 16 + lg * 4;
+        f32x4 d = mfma16(f.vw[i], *reinterpret_cast<const bf16x8*>(&zh[c][lg * 8]), f32x4{0.f, 0.f, 0.f, 0.f});
+        d = mfma16(f.vw[i], *reinterpret_cast<const bf16x8*>(&zl[c][lg * 8]), d);
+        if (c < nc && (d0 >> dsh) == hh) {
+          bf16x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = to_bf(d[e] + to_f(f.vb[i][e]));
+          *reinterpret_cast<bf16x4*>(&sm.o[s][d0]) = o;
+        }
+      }
+    }
+  }
+  lds_barrier();
+}
+
 // The slice's share of an o projection: part[s][n] = sum_d o[s][d] Wo[n][g W + d] (waves 0, 1:
 // one 16-row tile of the 32 outputs each, all W / 32 k-blocks).
 template <int W, int NCB>
@@ -605,19 +852,25 @@ __device__ __forceinline__ void oproj_load(const bf16* w, int A, int g, bf16x8 (
 }
 
 // Normalise (RMS over A columns from ss[which]) a slice of raw rows into dst (bf16), with the
-// reference's rounding (bf16 before the weight), optionally rotating pairs by the 1-D table.
+// reference's rounding (bf16 before the weight), optionally rotating pairs by the 1-D table, or
+// weighting the rounded result by a second vector nw2 (the key norm weight a folded query carries).
 template <int W, int NCB>
 __device__ __forceinline__ void norm_slice(const TinyArgs& a, TinySmem<W, NCB>& sm, int which, int rawcol,
-                                           bf16 (*dst)[W + 8], const bf16* nw, bool rope) {
+                                           bf16 (*dst)[W + 8], const bf16* nw, bool rope, const bf16* nw2 = nullptr) {
   constexpr int CPR = W / 8;
   const int S = a.S;
   for (int idx = threadIdx.x; idx < S * CPR; idx += 256) {
     const int s = idx / CPR, d0 = (idx - s * CPR) * 8;
     const float r = rsqrtf(sm.ss[which][s] / (float)a.A + a.eps);
     const bf16x8 w8 = load8(nw + d0);
+    const bf16x8 w2 = nw2 != nullptr ? load8(nw2 + d0) : zero8();
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) y[e] = to_f(to_bf(sm.u.raw[s][rawcol + d0 + e] * r)) * to_f(w8[e]);
+    if (nw2 != nullptr) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = to_f(to_bf(y[e])) * to_f(w2[e]);
+    }
     if (rope) {
       const int j0 = (d0 % a.DH) / 2, hd2 = a.DH / 2;
       const f32x4 cs = *reinterpret_cast<const f32x4*>(a.rcos + s * hd2 + j0);
@@ -944,16 +1197,24 @@ __device__ __forceinline__ void phase_cross(const TinyArgs& a, TinySmem<W, NCB>&
   if (G > 1) gram_load(a, l, 2, gf);
   bf16x8 of[W / 32];
   oproj_load<W>(a.co_w + (size_t)l * TH * A, A, g, of);
+  // every wave's first context block is loaded, also by a wave without one (rows past Lc read
+  // row 0): an unconditional load keeps the block in registers where the attention picks it up
+  constexpr bool folded = W > TH;   // attention in the space of the 32-wide context rows
   KvBlock<W> kv;
   KvSrc src;
-  src.n0 = a.Lc;
-  src.n1 = 0;
-  src.rs0 = a.ctx_ld;
-  src.k0 = a.ctxkv + (size_t)l * 2 * A + g * W;
-  src.v0 = a.ctxkv + (size_t)l * 2 * A + A + g * W;
-  // every wave's first block is loaded, also by a wave without one (rows past Lc read row 0): an
-  // unconditional load keeps the block in registers where the attention picks it up
-  kv_load_global<W>(src, wave, kv);
+  CtxFrags<W> cf;
+  CtxBlock cblk;
+  if constexpr (folded) {
+    ctx_frags_load<W>(a, l, g, cf);
+    ctx_block_load(a, l, wave, cblk);
+  } else {
+    src.n0 = a.Lc;
+    src.n1 = 0;
+    src.rs0 = a.ctx_ld;
+    src.k0 = a.ctxkv + (size_t)l * 2 * A + g * W;
+    src.v0 = a.ctxkv + (size_t)l * 2 * A + A + g * W;
+    kv_load_global<W>(src, wave, kv);
+  }
   const bf16* modt = a.mods + ((size_t)t * L + l) * 6 * TH;
   const bf16x2 gmsa = *reinterpret_cast<const bf16x2*>(modt + 2 * TH + 2 * j_r);
   const bf16x2 ob = *reinterpret_cast<const bf16x2*>(a.o_b + (size_t)l * TH + 2 * j_r);
@@ -997,9 +1258,13 @@ __device__ __forceinline__ void phase_cross(const TinyArgs& a, TinySmem<W, NCB>&
     direct_sumsq(sm, 2, 0, S);
     lds_barrier();
   }
-  norm_slice(a, sm, 2, 0, sm.q, a.cnq_w + (size_t)l * A + g * W, false);
+  norm_slice(a, sm, 2, 0, sm.q, a.cnq_w + (size_t)l * A + g * W, false,
+             folded ? a.cnk_w + (size_t)l * A + g * W : nullptr);
   lds_barrier();
-  attend<(W == 32 ? 3 : W == 64 ? 2 : 1)>(a, sm, src, nullptr, 0, kv, true);
+  if constexpr (folded)
+    attend_ctx<W, NCB>(a, sm, l, cf, cblk);
+  else
+    attend<3>(a, sm, src, nullptr, 0, kv, true);
   oproj_store(sm, of, a.part_c + ((size_t)b * G + g) * S * TH, S);
 }
 
@@ -1066,6 +1331,38 @@ __global__ __launch_bounds__(256, 1) void tiny_final_kernel(TinyArgs a) {
   phase_final(a, sm, blockIdx.y);
 }
 
+// The context keys' factors r * scale * log2 e, r = rsqrt(mean_j k_j^2 + eps) over all A columns
+// of k = W_k h + b_k, from the cross key weight's Gram form h G h + 2 h.c + |b|^2 (G = hi + lo):
+// one thread per (key, layer); keys past Lc (to the 32-key block) read row 0.
+__global__ __launch_bounds__(256) void tiny_ctx_rs_kernel(TinyArgs a) {
+  __shared__ float gs[TH][TH + 1];
+  __shared__ float cs[TH];
+  const int l = blockIdx.y, tid = threadIdx.x;
+  const bf16* gh = a.gram + (size_t)(l * 4 + 3) * 2 * TH * TH;
+  for (int i = tid; i < TH * TH; i += 256) gs[i / TH][i % TH] = to_f(gh[i]) + to_f(gh[TH * TH + i]);
+  if (tid < TH) cs[tid] = 2.0f * a.gram_c[(size_t)(l * 4 + 3) * TH + tid];
+  __syncthreads();
+  const int key = blockIdx.x * 256 + tid;
+  if (key >= a.Lcp) return;
+  const bf16* row = a.ctx_emb + (size_t)(key < a.Lc ? key : 0) * a.ctx_emb_ld;
+  float h[TH];
+#pragma unroll
+  for (int i = 0; i < TH / 4; ++i) {
+    const bf16x4 v = *reinterpret_cast<const bf16x4*>(row + 4 * i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[4 * i + e] = to_f(v[e]);
+  }
+  float q = a.gram_b[l * 4 + 3];
+#pragma unroll 4
+  for (int i = 0; i < TH; ++i) {
+    float gi = cs[i];
+#pragma unroll
+    for (int j = 0; j < TH; ++j) gi += gs[i][j] * h[j];
+    q += h[i] * gi;
+  }
+  a.ctx_rs[(size_t)l * a.Lcp + key] = rsqrtf(fmaxf(q, 0.f) / (float)a.A + a.eps) * a.scale_log2;
+}
+
 template <int W, int NCB>
 int launch_tiny(const TinyArgs& a0, int64_t p0, int64_t p1, hipStream_t st) {
   TinyArgs a = a0;
@@ -1093,12 +1390,14 @@ int launch_tiny(const TinyArgs& a0, int64_t p0, int64_t p1, hipStream_t st) {
 
 using fam::bf16;
 
-extern "C" int fam_tiny_expert(const fam_tiny_desc* d, int64_t phase_begin, int64_t phase_end, void* stream) {
+// Checks a descriptor against what the kernels cover and fills the kernel arguments; W (the
+// slice) and nc (attention columns per workgroup) for the dispatch.
+static int tiny_prepare(const fam_tiny_desc* d, fam::TinyArgs& a, int64_t& W, int64_t& nc) {
   FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_tiny_expert: null descriptor");
   const int64_t B = d->batch, S = d->seq, Hd = d->hidden, NH = d->heads, DH = d->head_dim, F = d->ffn, Da = d->action_dim;
   const int64_t L = d->layers, T = d->steps, Sv = d->video_len, Lc = d->ctx_len;
   const int64_t A = NH * DH;
-  const int64_t W = d->slice > 0 ? d->slice : (A <= 128 ? A : 128);
+  W = d->slice > 0 ? d->slice : (A <= 128 ? A : 128);
   FAM_REQUIRE(Hd == 32, FAM_ERR_UNSUPPORTED, "fam_tiny_expert: hidden must be 32 (got %lld)", (long long)Hd);
   FAM_REQUIRE(B >= 1 && B <= 65535 && S >= 1 && S <= 16 && NH >= 1 && L >= 1 && T >= 1 && Lc >= 1 && Sv >= 0,
               FAM_ERR_INVALID_ARG, "fam_tiny_expert: bad shape (B %lld, S %lld, heads %lld, L %lld, T %lld, Lc %lld, Sv %lld)",
@@ -1106,7 +1405,8 @@ extern "C" int fam_tiny_expert(const fam_tiny_desc* d, int64_t phase_begin, int6
   FAM_REQUIRE(DH >= 8 && DH % 8 == 0 && (W == 32 || W == 64 || W == 128) && W % DH == 0 && A % W == 0,
               FAM_ERR_UNSUPPORTED, "fam_tiny_expert: head_dim %lld / slice %lld / width %lld not supported",
               (long long)DH, (long long)W, (long long)A);
-  const int64_t G = A / W, nc = (W / DH) * S;
+  const int64_t G = A / W;
+  nc = (W / DH) * S;
   FAM_REQUIRE(nc <= 32 && G <= 64, FAM_ERR_UNSUPPORTED, "fam_tiny_expert: (slice / head_dim) * S = %lld > 32 or %lld slices > 64",
               (long long)nc, (long long)G);
   FAM_REQUIRE(F >= 32 && F % 32 == 0 && F <= fam::TF, FAM_ERR_UNSUPPORTED,
@@ -1115,30 +1415,41 @@ extern "C" int fam_tiny_expert(const fam_tiny_desc* d, int64_t phase_begin, int6
               (long long)Da, (long long)S);
   FAM_REQUIRE(Sv + S <= (int64_t)1 << 30 && Lc <= (int64_t)1 << 30 && 2 * L * T < (int64_t)1 << 30, FAM_ERR_INVALID_ARG,
               "fam_tiny_expert: sizes too large");
-  const int64_t last = 2 * L * T;
-  FAM_REQUIRE(phase_begin >= 0 && phase_begin <= phase_end && phase_end <= last + 1, FAM_ERR_INVALID_ARG,
-              "fam_tiny_expert: phases [%lld, %lld) outside [0, %lld]", (long long)phase_begin, (long long)phase_end,
-              (long long)(last + 1));
-  const void* need[] = {d->noise, d->mods, d->deltas, d->rope_cos, d->rope_sin, d->ctxkv, d->enc_w, d->enc_b,
+  const bool folded = W > 32;
+  const void* need[] = {d->noise, d->mods, d->deltas, d->rope_cos, d->rope_sin, d->enc_w, d->enc_b,
                         d->head_w, d->head_b, d->qkv_w, d->qkv_b, d->nq_w, d->nk_w, d->o_w, d->o_b, d->n3_w, d->n3_b,
                         d->cq_w, d->cq_b, d->cnq_w, d->co_w, d->co_b, d->ff0_w, d->ff0_b, d->ff2_w, d->ff2_b, d->lat,
                         d->xa, d->xb, d->part_s, d->part_c, d->out};
   for (const void* p : need) FAM_REQUIRE(p != nullptr, FAM_ERR_INVALID_ARG, "fam_tiny_expert: a required pointer is null");
-  const void* al16[] = {d->mods, d->rope_cos, d->rope_sin, d->ctxkv, d->qkv_w, d->nq_w, d->nk_w, d->o_w, d->cq_w,
+  const void* al16[] = {d->mods, d->rope_cos, d->rope_sin, d->qkv_w, d->nq_w, d->nk_w, d->o_w, d->cq_w,
                         d->cnq_w, d->co_w, d->ff0_w, d->ff2_w, d->xa, d->xb, d->part_s, d->part_c};
   for (const void* p : al16) FAM_REQUIRE(fam_host::aligned16(p), FAM_ERR_INVALID_ARG, "fam_tiny_expert: operands must be 16-byte aligned");
   const void* al8[] = {d->qkv_b, d->cq_b, d->ff0_b};
   for (const void* p : al8) FAM_REQUIRE(((uintptr_t)p & 7) == 0, FAM_ERR_INVALID_ARG, "fam_tiny_expert: biases must be 8-byte aligned");
   const void* al4[] = {d->o_b, d->co_b, d->n3_w, d->n3_b, d->ff2_b, d->enc_b};
   for (const void* p : al4) FAM_REQUIRE(((uintptr_t)p & 3) == 0, FAM_ERR_INVALID_ARG, "fam_tiny_expert: row vectors must be 4-byte aligned");
-  FAM_REQUIRE(d->ctx_ld >= 2 * A * L && d->ctx_ld % 8 == 0, FAM_ERR_INVALID_ARG,
-              "fam_tiny_expert: ctx_ld %lld (need >= 2 A L = %lld, a multiple of 8)", (long long)d->ctx_ld, (long long)(2 * A * L));
+  if (folded) {
+    const void* ctx16[] = {d->ck_wt, d->ck_b, d->cnk_w, d->cv_w, d->ctx_rs};
+    for (const void* p : ctx16)
+      FAM_REQUIRE(p != nullptr && fam_host::aligned16(p), FAM_ERR_INVALID_ARG,
+                  "fam_tiny_expert: slice %lld needs ck_wt, ck_b, cnk_w, cv_w and ctx_rs (16-byte aligned)", (long long)W);
+    FAM_REQUIRE(d->ctx_emb != nullptr && ((uintptr_t)d->ctx_emb & 7) == 0 && d->ctx_emb_ld >= 32 && d->ctx_emb_ld % 4 == 0 &&
+                    d->cv_b != nullptr && ((uintptr_t)d->cv_b & 7) == 0,
+                FAM_ERR_INVALID_ARG, "fam_tiny_expert: ctx_emb (8-byte aligned, row stride %lld >= 32, a multiple of 4) and cv_b",
+                (long long)d->ctx_emb_ld);
+  } else {
+    FAM_REQUIRE(d->ctxkv != nullptr && fam_host::aligned16(d->ctxkv), FAM_ERR_INVALID_ARG,
+                "fam_tiny_expert: a 32-wide slice reads ctxkv (16-byte aligned)");
+    FAM_REQUIRE(d->ctx_ld >= 2 * A * L && d->ctx_ld % 8 == 0, FAM_ERR_INVALID_ARG,
+                "fam_tiny_expert: ctx_ld %lld (need >= 2 A L = %lld, a multiple of 8)", (long long)d->ctx_ld, (long long)(2 * A * L));
+  }
   FAM_REQUIRE((DH / 2) % 4 == 0, FAM_ERR_UNSUPPORTED, "fam_tiny_expert: head_dim %lld (the rope tables are read 4 pairs at a time)",
               (long long)DH);
-  if (G > 1)
+  if (G > 1 || folded)
     FAM_REQUIRE(d->gram != nullptr && d->gram_c != nullptr && d->gram_b != nullptr && fam_host::aligned16(d->gram) &&
                     fam_host::aligned16(d->gram_c),
-                FAM_ERR_INVALID_ARG, "fam_tiny_expert: %lld slices need the Gram matrices (16-byte aligned)", (long long)G);
+                FAM_ERR_INVALID_ARG, "fam_tiny_expert: %lld slices of %lld need the Gram matrices (16-byte aligned)",
+                (long long)G, (long long)W);
   if (Sv > 0) {
     FAM_REQUIRE(d->video_k != nullptr && d->video_v != nullptr && d->video_rs >= A && d->video_rs % 8 == 0 &&
                     d->video_bs % 8 == 0 && (B == 1 || d->video_bs >= Sv * d->video_rs),
@@ -1147,9 +1458,6 @@ extern "C" int fam_tiny_expert(const fam_tiny_desc* d, int64_t phase_begin, int6
     FAM_REQUIRE(d->video_mask == nullptr || d->mask_rs >= Sv + S, FAM_ERR_INVALID_ARG,
                 "fam_tiny_expert: mask row stride %lld < Sv + S", (long long)d->mask_rs);
   }
-  if (phase_begin == phase_end) return FAM_OK;
-
-  fam::TinyArgs a;
   a.B = (int)B; a.S = (int)S; a.A = (int)A; a.DH = (int)DH; a.F = (int)F; a.Da = (int)Da; a.L = (int)L; a.T = (int)T;
   a.Sv = (int)Sv; a.Lc = (int)Lc; a.G = (int)G;
   a.eps = d->eps;
@@ -1170,7 +1478,24 @@ extern "C" int fam_tiny_expert(const fam_tiny_desc* d, int64_t phase_begin, int6
   a.ff2_w = (const bf16*)d->ff2_w; a.ff2_b = (const bf16*)d->ff2_b;
   a.gram = (const bf16*)d->gram; a.gram_c = d->gram_c; a.gram_b = d->gram_b;
   a.lat = d->lat; a.xa = d->xa; a.xb = d->xb; a.part_s = d->part_s; a.part_c = d->part_c; a.out = d->out;
+  a.ctx_emb = (const bf16*)d->ctx_emb; a.ctx_emb_ld = d->ctx_emb_ld;
+  a.ck_wt = (const bf16*)d->ck_wt; a.ck_b = (const bf16*)d->ck_b; a.cnk_w = (const bf16*)d->cnk_w;
+  a.cv_w = (const bf16*)d->cv_w; a.cv_b = (const bf16*)d->cv_b; a.ctx_rs = d->ctx_rs;
+  a.Lcp = (int)((Lc + 31) / 32 * 32);
   a.p0 = a.p1 = 0;
+  return FAM_OK;
+}
+
+extern "C" int fam_tiny_expert(const fam_tiny_desc* d, int64_t phase_begin, int64_t phase_end, void* stream) {
+  fam::TinyArgs a;
+  int64_t W = 0, nc = 0;
+  const int rc = tiny_prepare(d, a, W, nc);
+  if (rc != FAM_OK) return rc;
+  const int64_t last = 2LL * a.L * a.T;
+  FAM_REQUIRE(phase_begin >= 0 && phase_begin <= phase_end && phase_end <= last + 1, FAM_ERR_INVALID_ARG,
+              "fam_tiny_expert: phases [%lld, %lld) outside [0, %lld]", (long long)phase_begin, (long long)phase_end,
+              (long long)(last + 1));
+  if (phase_begin == phase_end) return FAM_OK;
   hipStream_t st = (hipStream_t)stream;
   const bool two = nc > 16;
   switch (W) {
@@ -1178,4 +1503,14 @@ extern "C" int fam_tiny_expert(const fam_tiny_desc* d, int64_t phase_begin, int6
     case 64: return two ? fam::launch_tiny<64, 2>(a, phase_begin, phase_end, st) : fam::launch_tiny<64, 1>(a, phase_begin, phase_end, st);
     default: return two ? fam::launch_tiny<128, 2>(a, phase_begin, phase_end, st) : fam::launch_tiny<128, 1>(a, phase_begin, phase_end, st);
   }
+}
+
+extern "C" int fam_tiny_context(const fam_tiny_desc* d, void* stream) {
+  fam::TinyArgs a;
+  int64_t W = 0, nc = 0;
+  const int rc = tiny_prepare(d, a, W, nc);
+  if (rc != FAM_OK) return rc;
+  if (W <= 32) return FAM_OK;
+  FAM_LAUNCH(fam::tiny_ctx_rs_kernel, dim3((a.Lcp + 255) / 256, a.L), dim3(256), 0, (hipStream_t)stream, a);
+  return fam_host::check_launch("fam_tiny_context");
 }

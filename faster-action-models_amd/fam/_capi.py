@@ -15,7 +15,7 @@ FAM_OK = 0
 FAM_ERR_INVALID_ARG = 1
 FAM_ERR_UNSUPPORTED = 2
 FAM_ERR_LAUNCH = 3
-FAM_ABI_VERSION = 2
+FAM_ABI_VERSION = 3
 
 FAM_MASK_NONE, FAM_MASK_BOOL, FAM_MASK_ADD_F32, FAM_MASK_ADD_BF16 = 0, 1, 2, 3
 FAM_PRO_NONE, FAM_PRO_LAYERNORM, FAM_PRO_ADALN, FAM_PRO_LN_FOLDED = 0, 1, 2, 3
@@ -132,6 +132,9 @@ class TinyDesc(C.Structure):
         ("co_w", _vp), ("co_b", _vp), ("ff0_w", _vp), ("ff0_b", _vp), ("ff2_w", _vp), ("ff2_b", _vp),
         ("gram", _vp), ("gram_c", _vp), ("gram_b", _vp),
         ("lat", _vp), ("xa", _vp), ("xb", _vp), ("part_s", _vp), ("part_c", _vp), ("out", _vp),
+        ("ctx_emb", _vp), ("ctx_emb_ld", _i64),
+        ("ck_wt", _vp), ("ck_b", _vp), ("cnk_w", _vp), ("cv_w", _vp), ("cv_b", _vp),
+        ("ctx_rs", _vp),
     ]
 
 
@@ -154,6 +157,7 @@ SIGNATURES = {
     "fam_gemm_partial": (C.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "fam_cae_decode": (C.c_int, [C.POINTER(CaeDesc), _vp]),
     "fam_tiny_expert": (C.c_int, [C.POINTER(TinyDesc), _i64, _i64, _vp]),
+    "fam_tiny_context": (C.c_int, [C.POINTER(TinyDesc), _vp]),
     "fam_gemm_final": (C.c_int, [_vp, _i64, _vp, _i64, _vp, C.c_int, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "fam_gemm_partial_splits": (C.c_int, [_i64, _i64, _i64]),
     "fam_rowop": (C.c_int, [C.POINTER(RowopDesc), _vp]),

@@ -582,16 +582,30 @@ class FusedActionDiT:
                          ("ff0_b", "blocks.{}.ffn.0.bias"), ("ff2_w", "blocks.{}.ffn.2.weight"),
                          ("ff2_b", "blocks.{}.ffn.2.bias")):
             tw[key] = stack(fmt)
+        # a slice wider than the 32-wide rows attends in the space of the context rows: the cross
+        # key weight transposed, the value weight and both biases per layer
+        folded = W > H
+        if folded:
+            tw["ck_wt"] = torch.stack([params[f"blocks.{i}.cross_attn.k.weight"].to(torch.float32).t()
+                                       for i in range(L)]).to(device=dev, dtype=_BF16).contiguous()
+            for key, fmt in (("ck_b", "blocks.{}.cross_attn.k.bias"), ("cv_w", "blocks.{}.cross_attn.v.weight"),
+                             ("cv_b", "blocks.{}.cross_attn.v.bias")):
+                tw[key] = stack(fmt)
         # sum_j q_j^2 = h G h + 2 h.c + beta for q = h Wq^T + bq, from the bf16 weights in fp64:
-        # G = Wq^T Wq as hi + lo bf16 parts, c = Wq^T bq, beta = |bq|^2 (self q, self k, cross q)
-        gram = torch.zeros(L, 3, 2, H, H, dtype=_BF16)
-        gc = torch.zeros(L, 3, H, dtype=torch.float32)
-        gb = torch.zeros(L, 3, dtype=torch.float32)
+        # G = Wq^T Wq as hi + lo bf16 parts, c = Wq^T bq, beta = |bq|^2 (self q, self k, cross q,
+        # cross k)
+        gram = torch.zeros(L, 4, 2, H, H, dtype=_BF16)
+        gc = torch.zeros(L, 4, H, dtype=torch.float32)
+        gb = torch.zeros(L, 4, dtype=torch.float32)
         qkw, qkb = tw["qkv_w"].cpu().double(), tw["qkv_b"].cpu().double()
         cqw, cqb = tw["cq_w"].cpu().double(), tw["cq_b"].cpu().double()
+        ckw = torch.stack([params[f"blocks.{i}.cross_attn.k.weight"].to(torch.float32) for i in range(L)]).to(
+            _BF16).double()
+        ckb = torch.stack([params[f"blocks.{i}.cross_attn.k.bias"].to(torch.float32) for i in range(L)]).to(
+            _BF16).double()
         for l in range(L):
             for j, (wm, bv) in enumerate(((qkw[l, :A], qkb[l, :A]), (qkw[l, A:2 * A], qkb[l, A:2 * A]),
-                                          (cqw[l], cqb[l]))):
+                                          (cqw[l], cqb[l]), (ckw[l], ckb[l]))):
                 g = wm.t() @ wm
                 hi = g.to(_BF16)
                 gram[l, j, 0], gram[l, j, 1] = hi, (g - hi.double()).to(_BF16)
@@ -613,7 +627,14 @@ class FusedActionDiT:
         d.eps, d.scale = float(cfg.eps), 1.0 / math.sqrt(Dh)
         d.noise, d.mods, d.deltas = self.noise_in.data_ptr(), self.mods.data_ptr(), self.deltas.data_ptr()
         d.rope_cos, d.rope_sin = self.rope_cos.data_ptr(), self.rope_sin.data_ptr()
-        d.ctxkv, d.ctx_ld = self.ctxkv.data_ptr(), L * 2 * A
+        if folded:
+            tw["ctx_rs"] = torch.zeros(L, (self.Lc + 31) // 32 * 32, **f32)
+            d.ctx_emb, d.ctx_emb_ld = self.ctx_emb_pad.data_ptr(), self.ctx_emb_pad.stride(0)
+            for key in ("ck_wt", "ck_b", "cv_w", "cv_b", "ctx_rs"):
+                setattr(d, key, tw[key].data_ptr())
+            d.cnk_w = tw["nk_stack"].data_ptr()
+        else:
+            d.ctxkv, d.ctx_ld = self.ctxkv.data_ptr(), L * 2 * A
         if self.Sv > 0:
             kvs = (self.video_kv if self.video_kv is not None else
                    [(self.video_k[l], self.video_v[l]) for l in range(L)])
@@ -637,7 +658,7 @@ class FusedActionDiT:
         if self.lib.fam_tiny_expert(C.byref(d), 0, 0, None) != 0:
             return None
         tw["desc"] = d
-        tw["G"] = G
+        tw["G"], tw["folded"] = G, folded
         return tw
 
     def _tiny_plan(self, plan: _Plan) -> None:
@@ -656,16 +677,21 @@ class FusedActionDiT:
                 if rc != 0:
                     raise FamError(f"fam_tiny_expert[{p}]", rc, lib.fam_last_error().decode(errors="replace"))
             return run
-        # algorithmic bytes: the weights a phase streams once (bf16), the K/V it reads, the partials
+        # algorithmic bytes: the weights a phase streams once (bf16), the K/V (or the context rows
+        # and the keys' factors) it reads, the partials
         w_self = 2 * (3 * A * H + 2 * A + H * A) + 2 * (2 * Fd * H)
         w_cross = 2 * (A * H + A + H * A)
+        if tw["folded"]:
+            w_cross += 2 * (2 * A * H + 3 * A) + 2 * Lc * H + 4 * Lc
+        else:
+            w_cross += 2 * 2 * Lc * A
         for t in range(T):
             for l in range(L):
                 p = 2 * (t * L + l)
                 plan.add(f"s{t}.b{l}.tiny_self", phase(p), "tiny_self",
                          w_self + 2 * 2 * B * Sv * A + 4 * 2 * G * rows * H, 4 * B * cfg.num_heads * S * (Sv + S) * cfg.attn_head_dim)
                 plan.add(f"s{t}.b{l}.tiny_cross", phase(p + 1), "tiny_cross",
-                         w_cross + 2 * 2 * Lc * A + 4 * 2 * G * rows * H, 4 * B * cfg.num_heads * S * Lc * cfg.attn_head_dim)
+                         w_cross + 4 * 2 * G * rows * H, 4 * B * cfg.num_heads * S * Lc * cfg.attn_head_dim)
         plan.add("tiny_final", phase(2 * L * T), "tiny_final", 2 * (2 * Fd * H) + 4 * G * rows * H)
 
     def set_video_kv(self, keys, values) -> None:
@@ -706,6 +732,14 @@ class FusedActionDiT:
         self._gemm("ctx_emb0", self.context_in, w["txt0_w"], w["txt0_b"], self.ctx_h, act=_capi.FAM_ACT_GELU_TANH,
                    ws=self.ctx_ws)
         self._gemm("ctx_emb2", self.ctx_h_pad, w["txt2_w"], w["txt2_b"], self.ctx_emb)
+        if self.tiny is not None and self.tiny["folded"]:
+            # the tiny expert's wide slices attend in the space of the context rows: only the
+            # keys' RMS factors are computed here (no context K/V)
+            ref = C.byref(self.tiny["desc"])
+            plan.add("tiny_context", _checked(lib, "fam_tiny_context", ref), "tiny_context",
+                     2 * Lc * H + 4 * L * self.tiny["ctx_rs"].shape[1] + 2 * L * (2 * H * H + 4 * H + 4))
+            self._tiny_plan(plan)
+            return plan
         self._gemm("ctx_kv", self.ctx_emb_pad, w["ctxkv_w"], w["ctxkv_b"], self.ctxkv)
         kvp = self.ctxkv.data_ptr()
         # RMSNorm of every block's context keys in one launch: row (i, l) = ctxkv[i, 2 A l ..]

@@ -32,7 +32,7 @@ extern "C" {
 #define FAM_ERR_UNSUPPORTED 2
 #define FAM_ERR_LAUNCH 3
 
-#define FAM_ABI_VERSION 2
+#define FAM_ABI_VERSION 3
 
 /*
  * No entry point allocates, keeps state between calls or communicates between
@@ -602,24 +602,34 @@ int fam_cae_decode(const fam_cae_desc* d, void* stream);
  *          attention over [the layer's video K/V ; the action K/V] and its share of the o
  *          projection -> part_s[b, g];
  *   cross: x += gate_msa (sum_g part_s + o_b), then the slice's cross-attention query from the
- *          affine LayerNorm3 (RMSNorm as above), attention over the context K/V (already
- *          RMS-normalised) and its share of the cross o projection -> part_c[b, g].
+ *          affine LayerNorm3 (RMSNorm as above), attention over the context and its share of
+ *          the cross o projection -> part_c[b, g].  A 32-wide slice reads the context K/V
+ *          (ctxkv, already RMS-normalised).  A wider slice attends in the 32-wide space of the
+ *          context rows h (ctx_emb): with k = r (W_k h + b_k) * w_k (r the key's RMS factor over
+ *          all A columns, w_k the key norm weight) the score of query q is
+ *          r (h . W_k^T (q * w_k) + b_k . (q * w_k)), and the output
+ *          sum p (W_v h + b_v) / l = W_v (sum p h / l) + b_v -- the same values with bf16
+ *          rounding at other places; r comes from fam_tiny_context.
  * Every workgroup recomputes the [S, hidden] rows it needs from the previous phase's fp32
  * partials in a fixed order (no atomics, no communication within a launch); slice 0 stores
  * them for the next phase.  With G = 1 (A <= 128) the whole call is one launch per batch row.
  * Rounding: the residual stream and the chunk stay fp32; every product takes bf16 operands
  * with fp32 accumulation (as fam_gemm); q and k are rounded to bf16 after the norm and after
  * the rotation.
- *   gram (G > 1): bf16 [L, 3, 2, 32, 32] -- hi and lo bf16 parts of W^T W for the self q, self k
- *   and cross q weights (W [A, 32] of the layer, as bf16 values); gram_c fp32 [L, 3, 32] = W^T b;
- *   gram_b fp32 [L, 3] = |b|^2.  Then sum_j q_j^2 = h G h + 2 c.h + |b|^2 for the row h.
+ *   gram (G > 1 or slice > 32): bf16 [L, 4, 2, 32, 32] -- hi and lo bf16 parts of W^T W for the
+ *   self q, self k, cross q and cross k weights (W [A, 32] of the layer, as bf16 values); gram_c
+ *   fp32 [L, 4, 32] = W^T b; gram_b fp32 [L, 4] = |b|^2.  Then sum_j q_j^2 = h G h + 2 c.h + |b|^2
+ *   for the row h.
  *   video_k / video_v: device arrays of L pointers to [B, Sv, A] views with common strides.
  * Weights are layer-major stacks of the reference's nn.Linear layouts:
  *   qkv_w [L, 3A, 32] (q; k; v), qkv_b [L, 3A], nq_w / nk_w / cnq_w [L, A], o_w / co_w [L, 32, A],
  *   o_b / co_b / n3_w / n3_b / ff2_b [L, 32], cq_w [L, A, 32], cq_b [L, A], ff0_w [L, F, 32],
  *   ff0_b [L, F], ff2_w [L, 32, F]; enc_w [32, Da], enc_b [32], head_w [Da, 32], head_b [Da].
  *   mods bf16 [T, L, 6 * 32] = modulation + t_mod (shift, scale, gate of the attention; of the FFN).
- *   ctxkv bf16 [Lc, ctx_ld]: block l's normalised keys at columns 2 A l, values at 2 A l + A.
+ *   ctxkv bf16 [Lc, ctx_ld] (slice 32): block l's normalised keys at columns 2 A l, values at
+ *   2 A l + A.  slice > 32 instead: ctx_emb bf16 [Lc, ctx_emb_ld] (the text embedding's rows),
+ *   ck_wt [L, 32, A] (the cross key weight transposed), ck_b / cnk_w / cv_b [L, A], cv_w
+ *   [L, A, 32], and ctx_rs fp32 [L, ceil(Lc / 32) * 32], which fam_tiny_context fills.
  *   rope_cos / rope_sin fp32 [S, head_dim / 2] (pair j of position s).
  * State (fp32, caller-owned): lat [2, B, S, Da], xa / xb [B, S, 32], part_s / part_c
  * [B, G, S, 32]; out [B, S, Da].  noise bf16 [B, S, Da] is read at phase 0.
@@ -631,7 +641,8 @@ int fam_cae_decode(const fam_cae_desc* d, void* stream);
  *           time-independent parts of CA/action_dit.py:127-231.
  * Limits: hidden 32; S <= 16; slice in {32, 64, 128}, a multiple of head_dim, A % slice == 0,
  * (slice / head_dim) * S <= 32; head_dim a multiple of 8; F % 32 == 0, F <= 256; A / slice <= 64;
- * Da <= 32 and S * Da <= 256; 16-byte aligned weights, rows and strides (multiples of 8).
+ * Da <= 32 and S * Da <= 256; 16-byte aligned weights, rows and strides (multiples of 8);
+ * ctx_emb 8-byte aligned with ctx_emb_ld a multiple of 4.
  */
 typedef struct fam_tiny_desc {
   int32_t batch, seq, hidden, heads, head_dim, ffn, action_dim, layers, steps, video_len, ctx_len, slice;
@@ -647,9 +658,23 @@ typedef struct fam_tiny_desc {
   const void* co_w; const void* co_b; const void* ff0_w; const void* ff0_b; const void* ff2_w; const void* ff2_b;
   const void* gram; const float* gram_c; const float* gram_b;
   float* lat; float* xa; float* xb; float* part_s; float* part_c; float* out;
+  const void* ctx_emb; int64_t ctx_emb_ld;
+  const void* ck_wt; const void* ck_b; const void* cnk_w; const void* cv_w; const void* cv_b;
+  float* ctx_rs;
 } fam_tiny_desc;
 
 int fam_tiny_expert(const fam_tiny_desc* d, int64_t phase_begin, int64_t phase_end, void* stream);
+
+/*
+ * fam_tiny_context -- for slices wider than 32: every context key's factor
+ * ctx_rs[l, i] = rsqrt(mean_j k_j^2 + eps) * scale * log2(e) of k = W_k h_i + b_k (block l's cross
+ * key, all A columns, from the Gram form with gram[l, 3]); keys past Lc read row 0.  One launch;
+ * run it whenever ctx_emb changes, before the first cross phase.  A 32-wide slice needs nothing
+ * here (the call validates and returns FAM_OK).
+ * Replaces: the per-call context keys' projection and RMSNorm k = norm_k(k(ctx))
+ *           FB/wan_video_dit.py:216 (CrossAttention.forward) for every block.
+ */
+int fam_tiny_context(const fam_tiny_desc* d, void* stream);
 
 #ifdef __cplusplus
 }

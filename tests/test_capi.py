@@ -88,6 +88,7 @@ def _tiny_desc(**kw):
             setattr(d, name, 4096 * (i + 1))
     A = d.heads * d.head_dim
     d.ctx_ld, d.video_rs, d.video_bs, d.mask_rs = 2 * A * d.layers, 3 * A, 0, 0
+    d.ctx_emb_ld = 64
     d.video_mask = None
     for k, v in kw.items():
         if k not in dims:
@@ -112,7 +113,17 @@ def test_tiny_expert_validation(lib):
     assert f(C.byref(_tiny_desc(heads=4, head_dim=8, gram=None)), 0, 0, None) == _capi.FAM_OK   # one slice
     assert f(C.byref(_tiny_desc(qkv_w=4096 + 8)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
     assert "aligned" in _err(lib)
-    assert f(C.byref(_tiny_desc(ctx_ld=100)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
+    # a 32-wide slice reads the context K/V (ctx_ld), a wider one the context rows and factors
+    assert f(C.byref(_tiny_desc(heads=4, head_dim=8, ctx_ld=100)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
+    assert f(C.byref(_tiny_desc(ctx_ld=100, ctxkv=None)), 0, 0, None) == _capi.FAM_OK
+    assert f(C.byref(_tiny_desc(heads=4, head_dim=8, ctxkv=None)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
+    assert f(C.byref(_tiny_desc(ctx_emb_ld=30)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
+    assert f(C.byref(_tiny_desc(ck_wt=None)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
+    assert f(C.byref(_tiny_desc(ctx_rs=4096 + 8)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
+    assert f(C.byref(_tiny_desc(ctx_emb=4096 + 4)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
+    # fam_tiny_context validates the same descriptor; a 32-wide slice has nothing to compute
+    assert lib.fam_tiny_context(C.byref(_tiny_desc(heads=4, head_dim=8)), None) == _capi.FAM_OK
+    assert lib.fam_tiny_context(C.byref(_tiny_desc(ck_b=None)), None) == _capi.FAM_ERR_INVALID_ARG
     assert f(C.byref(_tiny_desc(video_rs=3072 * 3 + 4)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
     assert f(C.byref(_tiny_desc(action_dim=40)), 0, 0, None) == _capi.FAM_ERR_UNSUPPORTED
 

@@ -96,7 +96,9 @@ def test_tiny_expert_plan_and_gram_on_host():
     assert m.tiny is not None and m.tiny["G"] == 24
     kinds = [d["kernel"] for d in m.plan.meta]
     assert kinds.count("tiny_self") == kinds.count("tiny_cross") == 3 * 4 and kinds[-1] == "tiny_final"
-    assert "copy" not in kinds and m.num_launches == 9 + 2 * 3 * 4 + 1
+    # 128-wide slices: the keys' factors in one launch replace the context K/V GEMM and key norm
+    assert m.tiny["folded"] and kinds.count("tiny_context") == 1 and "rmsnorm_rope" not in kinds
+    assert "copy" not in kinds and m.num_launches == 8 + 2 * 3 * 4 + 1
     g = torch.Generator().manual_seed(1)
     h = torch.randn(5, 32, generator=g, dtype=torch.float64)
     A = cfg.attn_dim
@@ -104,7 +106,8 @@ def test_tiny_expert_plan_and_gram_on_host():
     for l in range(3):
         for j, (w, b) in enumerate(((m.tiny["qkv_w"][l, :A], m.tiny["qkv_b"][l, :A]),
                                     (m.tiny["qkv_w"][l, A:2 * A], m.tiny["qkv_b"][l, A:2 * A]),
-                                    (m.tiny["cq_w"][l], m.tiny["cq_b"][l]))):
+                                    (m.tiny["cq_w"][l], m.tiny["cq_b"][l]),
+                                    (m.tiny["ck_wt"][l].t(), m.tiny["ck_b"][l]))):
             q = h @ w.double().t() + b.double()
             direct = (q * q).sum(1)
             G = gram[l, j, 0] + gram[l, j, 1]
@@ -115,6 +118,64 @@ def test_tiny_expert_plan_and_gram_on_host():
     # the generic plan stays available, and hidden 64 never takes the tiny path
     assert AD.FusedActionDiT(cfg, params, batch=1, seq_len=8, ctx_len=129, num_steps=4, device="cpu", video_len=98,
                              tiny=False).tiny is None
+    # 32-wide slices keep the context K/V
+    c32 = AD.ActionDiTConfig(num_layers=3, hidden_dim=32, action_dim=16, ffn_dim=256, text_dim=64, freq_dim=32,
+                             num_heads=4, attn_head_dim=32)
+    m32 = AD.FusedActionDiT(c32, AD.synthetic_params(c32, 9), batch=1, seq_len=8, ctx_len=129, num_steps=4,
+                            device="cpu", video_len=98, tiny_slice=32)
+    k32 = [d["kernel"] for d in m32.plan.meta]
+    assert not m32.tiny["folded"] and "tiny_context" not in k32 and m32.num_launches == 9 + 2 * 3 * 4 + 1
+
+
+def test_tiny_folded_context_attention_identity():
+    """The wide-slice cross attention of fam_tiny_expert works in the 32-wide space of the context
+    rows h with the packed host weights: for a head's query q (already RMS-normalised) the
+    reference's score q . norm_k(W_k h + b_k) equals r (h . W_k^T (q * w_k) + b_k . (q * w_k)), r the
+    key's RMS factor from the Gram form, and its output sum p v / l equals W_v (sum p h / l) + b_v
+    (fp64 here).  A folded query without the bias term, without w_k, or with the Gram's lo part
+    dropped misses the explicit scores."""
+    cfg = AD.ActionDiTConfig(num_layers=2, hidden_dim=32, action_dim=16, ffn_dim=256, text_dim=64, freq_dim=32,
+                             num_heads=4, attn_head_dim=32)
+    params = AD.synthetic_params(cfg, 11)
+    # unit-scale key weights and biases so that every term matters
+    g = torch.Generator().manual_seed(12)
+    for l in range(2):
+        params[f"blocks.{l}.cross_attn.k.weight"] = (torch.randn(128, 32, generator=g) / 32 ** 0.5).to(torch.bfloat16)
+        params[f"blocks.{l}.cross_attn.k.bias"] = (0.5 * torch.randn(128, generator=g)).to(torch.bfloat16)
+        params[f"blocks.{l}.cross_attn.norm_k.weight"] = (1 + 0.3 * torch.randn(128, generator=g)).to(torch.bfloat16)
+        params[f"blocks.{l}.cross_attn.v.bias"] = (0.5 * torch.randn(128, generator=g)).to(torch.bfloat16)
+    m = AD.FusedActionDiT(cfg, params, batch=1, seq_len=8, ctx_len=40, num_steps=2, device="cpu")
+    tw, A, eps = m.tiny, cfg.attn_dim, float(cfg.eps)
+    assert tw["folded"] and tw["G"] == 1
+    h = torch.randn(40, 32, generator=g, dtype=torch.float64)
+    q = torch.randn(3, 32, generator=g, dtype=torch.float64)      # 3 queries of head 1 (dims 32..63)
+    p = torch.rand(3, 40, generator=g, dtype=torch.float64)
+    for l in range(2):
+        wk, bk = tw["ck_wt"][l].double().t(), tw["ck_b"][l].double()
+        wn = tw["nk_stack"][l].double()
+        wv, bv = tw["cv_w"][l].double(), tw["cv_b"][l].double()
+        k = h @ wk.t() + bk
+        kn = k * torch.rsqrt((k * k).mean(1, keepdim=True) + eps) * wn
+        qf = torch.zeros(3, A, dtype=torch.float64)
+        qf[:, 32:64] = q
+        explicit = qf @ kn.t()
+        G = tw["gram"][l, 3].double()
+        ss = ((h @ (G[0] + G[1])) * h).sum(1) + 2 * h @ tw["gram_c"][l, 3].double() + tw["gram_b"][l, 3].double()
+        r = torch.rsqrt(ss / A + eps)
+        qw = qf * wn
+        folded = r * (h @ (wk.t() @ qw.t())).t() + r * (qw @ bk)[:, None]
+        assert torch.allclose(folded, explicit, rtol=1e-4, atol=1e-4 * explicit.abs().max().item())
+        bad = {"no bias term": r * (h @ (wk.t() @ qw.t())).t(),
+               "no w_k": r * (h @ (wk.t() @ qf.t())).t() + r * (qf @ bk)[:, None]}
+        ss_hi = ((h @ G[0]) * h).sum(1) + 2 * h @ tw["gram_c"][l, 3].double() + tw["gram_b"][l, 3].double()
+        bad["Gram lo dropped"] = torch.rsqrt(ss_hi / A + eps) * (h @ (wk.t() @ qw.t())).t() + \
+            torch.rsqrt(ss_hi / A + eps) * (qw @ bk)[:, None]
+        for name, v in bad.items():
+            assert not torch.allclose(v, explicit, rtol=1e-4, atol=1e-4 * explicit.abs().max().item()), name
+        v = h @ wv.t() + bv
+        out_explicit = (p @ v) / p.sum(1, keepdim=True)
+        z = (p @ h) / p.sum(1, keepdim=True)
+        assert torch.allclose(z @ wv.t() + bv, out_explicit, rtol=1e-10, atol=1e-10)
 
 
 def test_video_rope_table_matches_oracle():
