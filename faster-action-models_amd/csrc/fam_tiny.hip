@@ -20,7 +20,11 @@
 // The phase boundaries are exactly the two cross-head reductions of a block (the o projections
 // sum over all heads); everything else a workgroup needs it recomputes from the previous
 // phase's partials, in a fixed order, so every workgroup of a batch row holds bit-identical
-// rows and slice 0 alone stores them.  The RMSNorm of q / k / cross q runs over all A columns:
+// rows and slice 0 alone stores them.  With a single 32-wide slice and few batch rows (config
+// 3's compact expert over 1560 context keys) the cross phase also splits the context over KS
+// workgroups: each stores its split's unnormalised output with the running max and sum, and
+// the next phase merges the splits in split order and applies the (32 x 32) cross o projection
+// itself, where the other layouts read the o partials.  The RMSNorm of q / k / cross q runs over all A columns:
 // a workgroup that sees only its slice gets the row's sum of squares from the layer's Gram
 // matrix G = W^T W (hi + lo bf16 parts, two MFMAs), sum_j q_j^2 = h G h + 2 h.(W^T b) + |b|^2,
 // since the input row h is only 32 wide.
@@ -33,6 +37,8 @@
 // the rows (weights, the first video / context block) is issued before the first barrier, and
 // the barriers wait for LDS traffic only (lds_barrier): a global store is read by the next
 // launch, never by this one, so no barrier has to drain the loads still in flight.
+#include <algorithm>
+
 #include "fam_common.h"
 
 namespace fam {
@@ -72,6 +78,8 @@ struct TinyArgs {
   const bf16 *ck_wt, *ck_b, *cnk_w, *cv_w, *cv_b;
   float* ctx_rs;
   int Lcp;   // keys of ctx_rs per layer (Lc rounded up to 32)
+  int KS;    // context splits of the cross phase (1: none)
+  float* part_x;   // KS > 1: [B][KS][32 columns][W + 4]: o (unnormalised), max, sum
   int p0, p1;
 };
 
@@ -471,9 +479,12 @@ __device__ __forceinline__ void attend_block(const TinyArgs& a, const KvBlock<W>
 // PD + 1, so no slot is indexed at run time) whose loads are all issued, past the end too
 // (kv_load_global reads row 0 there), so the wait before each block counts exactly the loads
 // issued after it.
+// xout != nullptr: the merged state of this workgroup's keys goes there unnormalised, per column
+// c = (head, token): [c][d] = the waves' sum of exp2(m_w - m) o_w over the head's dims d,
+// [c][W] = m, [c][W + 1] = the matching sum of p; nothing is written to sm.o.
 template <int PD, int W, int NCB>
 __device__ __forceinline__ void attend(const TinyArgs& a, TinySmem<W, NCB>& sm, const KvSrc& src, const uint8_t* mask,
-                                       int64_t mask_rs, KvBlock<W>& kv, bool prefetched) {
+                                       int64_t mask_rs, KvBlock<W>& kv, bool prefetched, float* xout = nullptr) {
   constexpr int WK = W / 32, WT = W / 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l16 = lane & 15, lg = lane >> 4;
   const int S = a.S, DH = a.DH;
@@ -590,6 +601,75 @@ __device__ __forceinline__ void attend(const TinyArgs& a, TinySmem<W, NCB>& sm, 
       n0 += f[w] * *reinterpret_cast<const f32x4*>(&sm.u.mg.acc[w][c][d0]);
       n1 += f[w] * *reinterpret_cast<const f32x4*>(&sm.u.mg.acc[w][c][d0 + 4]);
     }
+    if (xout != nullptr) {
+      float* p = xout + (size_t)c * (W + 4);
+      *reinterpret_cast<f32x4*>(p + d0) = n0;
+      *reinterpret_cast<f32x4*>(p + d0 + 4) = n1;
+      if ((d0 & (DH - 1)) == 0) *reinterpret_cast<f32x2*>(p + W) = f32x2{mx, den};
+    } else {
+      const float inv = den > 0.f ? 1.f / den : 0.f;
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] = to_bf(n0[e] * inv);
+        o[4 + e] = to_bf(n1[e] * inv);
+      }
+      *reinterpret_cast<bf16x8*>(&sm.o[s][d0]) = o;
+    }
+  }
+  lds_barrier();
+}
+
+// ---------------------------------------------------------------------------------------
+// The context splits of the previous cross phase (KS > 1; one 32-wide slice): thread (token s,
+// 8 dims d0) loads the KS splits' outputs of its column c = (head of d0, s) early; the merge
+// (splits in order, weights exp2(m_k - max m)) writes o = bf16(sum / den) to sm.o, and the cross
+// o projection of the slice fills sm.u.f.red[0] (the other red planes zero) where the other
+// layouts sum their o partials.
+constexpr int TKS = 8;   // at most 8 context splits
+
+struct XSplit {
+  f32x4 o[TKS][2];
+  f32x2 ml[TKS];
+};
+
+template <int W>
+__device__ __forceinline__ void xsplit_issue(const TinyArgs& a, int b, XSplit& x) {
+  const int tid = threadIdx.x, S = a.S;
+  const int dsh = __builtin_ctz(a.DH);
+  const int t = tid < S * (W / 8) ? tid : 0, s = t / (W / 8), d0 = (t - s * (W / 8)) * 8, c = (d0 >> dsh) * S + s;
+#pragma unroll
+  for (int k = 0; k < TKS; ++k) {
+    const int kk = k < a.KS ? k : 0;
+    const float* p = a.part_x + ((size_t)(b * a.KS + kk) * 32 + c) * (W + 4);
+    x.o[k][0] = *reinterpret_cast<const f32x4*>(p + d0);
+    x.o[k][1] = *reinterpret_cast<const f32x4*>(p + d0 + 4);
+    x.ml[k] = *reinterpret_cast<const f32x2*>(p + W);
+  }
+}
+
+template <int W, int NCB>
+__device__ __forceinline__ void xsplit_merge(const TinyArgs& a, TinySmem<W, NCB>& sm, const XSplit& x,
+                                             const bf16x8 (&of)[W / 32]) {
+  const int tid = threadIdx.x, S = a.S, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lg = lane >> 4;
+  if (tid < S * (W / 8)) {
+    const int s = tid / (W / 8), d0 = (tid - s * (W / 8)) * 8;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < TKS; ++k)
+      if (k < a.KS) mx = fmaxf(mx, x.ml[k][0]);
+    const float ms = mx == -INFINITY ? 0.f : mx;
+    float den = 0.f;
+    f32x4 n0 = f32x4{0.f, 0.f, 0.f, 0.f}, n1 = n0;
+#pragma unroll
+    for (int k = 0; k < TKS; ++k) {
+      if (k < a.KS) {
+        const float f = __builtin_amdgcn_exp2f(x.ml[k][0] - ms);
+        den += f * x.ml[k][1];
+        n0 += f * x.o[k][0];
+        n1 += f * x.o[k][1];
+      }
+    }
     const float inv = den > 0.f ? 1.f / den : 0.f;
     bf16x8 o;
 #pragma unroll
@@ -600,6 +680,20 @@ __device__ __forceinline__ void attend(const TinyArgs& a, TinySmem<W, NCB>& sm, 
     *reinterpret_cast<bf16x8*>(&sm.o[s][d0]) = o;
   }
   lds_barrier();
+  // part[s][n] = sum_d o[s][d] Wo[n][d]: waves 0, 1 one 16-row tile of the 32 outputs each
+  const int NGI = min(4, 256 / (S * 8));
+  if (wave < 2) {
+    f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < W / 32; ++kb)
+      d = mfma16(of[kb], *reinterpret_cast<const bf16x8*>(&sm.o[l16][kb * 32 + lg * 8]), d);
+    if (l16 < S) *reinterpret_cast<f32x4*>(&sm.u.f.red[0][l16][wave * 16 + lg * 4]) = d;
+  } else {
+    for (int i = tid - 128; i < (NGI - 1) * TS * TH; i += 128) {
+      const int gi = 1 + i / (TS * TH), r = i % (TS * TH);
+      sm.u.f.red[gi][r / TH][r % TH] = 0.f;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1064,6 +1158,10 @@ __device__ __forceinline__ void phase_self(const TinyArgs& a, TinySmem<W, NCB>& 
   bf16x2 cob, b2, gmlp, eb;
   float yv[2] = {0.f, 0.f};
   PartLoads pl;
+  // the previous cross phase split the context (one 32-wide slice): its splits, merged here
+  const bool xsplit = W == 32 && a.KS > 1;
+  XSplit xs;
+  bf16x8 ofc[W / 32];
   float lat_old = 0.f, hbj = 0.f, delta = 0.f;
   if (!first) {
     const bf16* modp = a.mods + ((size_t)tp * L + lp) * 6 * TH;
@@ -1075,7 +1173,12 @@ __device__ __forceinline__ void phase_self(const TinyArgs& a, TinySmem<W, NCB>& 
     const f32x2 y = *reinterpret_cast<const f32x2*>(a.xb + ((size_t)b * S + sr) * TH + 2 * j_r);
     yv[0] = y[0];
     yv[1] = y[1];
-    part_issue(a.part_c, b, G, S, 0, pl);
+    if (xsplit) {
+      xsplit_issue<W>(a, b, xs);
+      oproj_load<W>(a.co_w + (size_t)lp * TH * A, A, 0, ofc);
+    } else {
+      part_issue(a.part_c, b, G, S, 0, pl);
+    }
   }
   if (step0) {
     eb = *reinterpret_cast<const bf16x2*>(a.enc_b + 2 * j_r);
@@ -1093,7 +1196,10 @@ __device__ __forceinline__ void phase_self(const TinyArgs& a, TinySmem<W, NCB>& 
   // ---- the rows entering block l
   if (step0) small_store(a, sm, sw);
   if (!first) {
-    part_reduce(sm, a.part_c, b, G, S, pl);
+    if (xsplit)
+      xsplit_merge(a, sm, xs, ofc);
+    else
+      part_reduce(sm, a.part_c, b, G, S, pl);
     lds_barrier();
     const float x0 = yv[0] + (to_f(cob[0]) + part_sum(sm, S, s_r, 2 * j_r));
     const float x1 = yv[1] + (to_f(cob[1]) + part_sum(sm, S, s_r, 2 * j_r + 1));
@@ -1173,7 +1279,8 @@ __device__ __forceinline__ void phase_self(const TinyArgs& a, TinySmem<W, NCB>& 
 
 // Phase: cross-attention sub-block of block l at step t.
 template <int W, int NCB>
-__device__ __forceinline__ void phase_cross(const TinyArgs& a, TinySmem<W, NCB>& sm, int g, int b, int t, int l) {
+__device__ __forceinline__ void phase_cross(const TinyArgs& a, TinySmem<W, NCB>& sm, int g, int ks, int b, int t,
+                                            int l) {
   constexpr int WT = W / 16, PW = (WT + 3) / 4;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, lg = lane >> 4;
   const int S = a.S, A = a.A, L = a.L, G = a.G;
@@ -1208,11 +1315,13 @@ __device__ __forceinline__ void phase_cross(const TinyArgs& a, TinySmem<W, NCB>&
     ctx_frags_load<W>(a, l, g, cf);
     ctx_block_load(a, l, wave, cblk);
   } else {
-    src.n0 = a.Lc;
+    // split ks of KS: whole 32-key blocks [ks per, (ks + 1) per) (every split holds keys)
+    const int nblk = (a.Lc + 31) / 32, per = (nblk + a.KS - 1) / a.KS, key0 = ks * per * 32;
+    src.n0 = min(a.Lc, key0 + per * 32) - key0;
     src.n1 = 0;
     src.rs0 = a.ctx_ld;
-    src.k0 = a.ctxkv + (size_t)l * 2 * A + g * W;
-    src.v0 = a.ctxkv + (size_t)l * 2 * A + A + g * W;
+    src.k0 = a.ctxkv + (size_t)key0 * a.ctx_ld + (size_t)l * 2 * A + g * W;
+    src.v0 = a.ctxkv + (size_t)key0 * a.ctx_ld + (size_t)l * 2 * A + A + g * W;
     kv_load_global<W>(src, wave, kv);
   }
   const bf16* modt = a.mods + ((size_t)t * L + l) * 6 * TH;
@@ -1233,7 +1342,8 @@ __device__ __forceinline__ void phase_cross(const TinyArgs& a, TinySmem<W, NCB>&
     const float x0 = xv[0] + to_f(gmsa[0]) * o0, x1 = xv[1] + to_f(gmsa[1]) * o1;
     sm.x[s_r][2 * j_r] = s_r < S ? x0 : 0.f;
     sm.x[s_r][2 * j_r + 1] = s_r < S ? x1 : 0.f;
-    if (g == 0 && s_r < S) *reinterpret_cast<f32x2*>(a.xb + ((size_t)b * S + s_r) * TH + 2 * j_r) = f32x2{x0, x1};
+    if (g == 0 && ks == 0 && s_r < S)
+      *reinterpret_cast<f32x2*>(a.xb + ((size_t)b * S + s_r) * TH + 2 * j_r) = f32x2{x0, x1};
   }
   lds_barrier();
   row_norm(sm, S, a.eps, n3, false);
@@ -1261,10 +1371,15 @@ __device__ __forceinline__ void phase_cross(const TinyArgs& a, TinySmem<W, NCB>&
   norm_slice(a, sm, 2, 0, sm.q, a.cnq_w + (size_t)l * A + g * W, false,
              folded ? a.cnk_w + (size_t)l * A + g * W : nullptr);
   lds_barrier();
-  if constexpr (folded)
+  if constexpr (folded) {
     attend_ctx<W, NCB>(a, sm, l, cf, cblk);
-  else
+  } else if (a.KS > 1) {
+    // the split's state; the next phase merges the splits and projects
+    attend<3>(a, sm, src, nullptr, 0, kv, true, a.part_x + (size_t)(b * a.KS + ks) * 32 * (W + 4));
+    return;
+  } else {
     attend<3>(a, sm, src, nullptr, 0, kv, true);
+  }
   oproj_store(sm, of, a.part_c + ((size_t)b * G + g) * S * TH, S);
 }
 
@@ -1286,14 +1401,25 @@ __device__ __forceinline__ void phase_final(const TinyArgs& a, TinySmem<W, NCB>&
   const int sr = s_r < S ? s_r : 0;
   const f32x2 y = *reinterpret_cast<const f32x2*>(a.xb + ((size_t)b * S + sr) * TH + 2 * j_r);
   PartLoads pl;
-  part_issue(a.part_c, b, G, S, 0, pl);
+  const bool xsplit = W == 32 && a.KS > 1;
+  XSplit xs;
+  bf16x8 ofc[W / 32];
+  if (xsplit) {
+    xsplit_issue<W>(a, b, xs);
+    oproj_load<W>(a.co_w + (size_t)lp * TH * a.A, a.A, 0, ofc);
+  } else {
+    part_issue(a.part_c, b, G, S, 0, pl);
+  }
   const int Da = a.Da, e = tid < S * Da ? tid : 0;
   const float lat_old = a.lat[(size_t)(tp & 1) * rows * Da + (size_t)b * S * Da + e];
   const float hbj = to_f(a.head_b[e % Da]);
   const float delta = to_f(a.deltas[tp]);
   __builtin_amdgcn_sched_barrier(0);
   small_store(a, sm, sw);
-  part_reduce(sm, a.part_c, b, G, S, pl);
+  if (xsplit)
+    xsplit_merge(a, sm, xs, ofc);
+  else
+    part_reduce(sm, a.part_c, b, G, S, pl);
   lds_barrier();
   const float x0 = y[0] + (to_f(cob[0]) + part_sum(sm, S, s_r, 2 * j_r));
   const float x1 = y[1] + (to_f(cob[1]) + part_sum(sm, S, s_r, 2 * j_r + 1));
@@ -1322,7 +1448,8 @@ template <int W, int NCB>
 __global__ __launch_bounds__(256, 1) void tiny_cross_kernel(TinyArgs a) {
   __shared__ TinySmem<W, NCB> sm;
   const int per = 2 * a.L, t = a.p0 / per, l = (a.p0 - t * per) >> 1;
-  phase_cross(a, sm, blockIdx.x, blockIdx.y, t, l);
+  // (with context splits the slice is the only one: blockIdx.x numbers the splits)
+  phase_cross(a, sm, a.KS > 1 ? 0 : (int)blockIdx.x, a.KS > 1 ? (int)blockIdx.x : 0, blockIdx.y, t, l);
 }
 
 template <int W, int NCB>
@@ -1376,7 +1503,7 @@ int launch_tiny(const TinyArgs& a0, int64_t p0, int64_t p1, hipStream_t st) {
     if (p == last)
       FAM_LAUNCH(final_k, dim3(1, a.B), dim3(256), 0, st, a);
     else if (p & 1)
-      FAM_LAUNCH(cross_k, dim3(a.G, a.B), dim3(256), 0, st, a);
+      FAM_LAUNCH(cross_k, dim3(a.G * a.KS, a.B), dim3(256), 0, st, a);
     else
       FAM_LAUNCH(self_k, dim3(a.G, a.B), dim3(256), 0, st, a);
     const int rc = fam_host::check_launch("fam_tiny_expert");
@@ -1392,7 +1519,7 @@ using fam::bf16;
 
 // Checks a descriptor against what the kernels cover and fills the kernel arguments; W (the
 // slice) and nc (attention columns per workgroup) for the dispatch.
-static int tiny_prepare(const fam_tiny_desc* d, fam::TinyArgs& a, int64_t& W, int64_t& nc) {
+static int tiny_prepare(const fam_tiny_desc* d, fam::TinyArgs& a, int64_t& W, int64_t& nc, bool need_part_x = true) {
   FAM_REQUIRE(d != nullptr, FAM_ERR_INVALID_ARG, "fam_tiny_expert: null descriptor");
   const int64_t B = d->batch, S = d->seq, Hd = d->hidden, NH = d->heads, DH = d->head_dim, F = d->ffn, Da = d->action_dim;
   const int64_t L = d->layers, T = d->steps, Sv = d->video_len, Lc = d->ctx_len;
@@ -1482,8 +1609,36 @@ static int tiny_prepare(const fam_tiny_desc* d, fam::TinyArgs& a, int64_t& W, in
   a.ck_wt = (const bf16*)d->ck_wt; a.ck_b = (const bf16*)d->ck_b; a.cnk_w = (const bf16*)d->cnk_w;
   a.cv_w = (const bf16*)d->cv_w; a.cv_b = (const bf16*)d->cv_b; a.ctx_rs = d->ctx_rs;
   a.Lcp = (int)((Lc + 31) / 32 * 32);
+  // context splits of the cross phase: one 32-wide slice and rows few enough that more
+  // workgroups find idle CUs (<= 8 splits of >= 4 blocks of 32 keys; every split holds keys)
+  int64_t KS = 1;
+  if (G == 1 && W == 32) {
+    const int64_t nblk = (Lc + 31) / 32;
+    int64_t want = d->key_splits > 0 ? d->key_splits
+                                     : std::min<int64_t>(fam::TKS, std::max<int64_t>(1, fam_host::device_cus() / B));
+    want = std::max<int64_t>(1, std::min<int64_t>({want, (int64_t)fam::TKS, d->key_splits > 0 ? nblk : nblk / 4}));
+    const int64_t per = (nblk + want - 1) / want;
+    KS = (nblk + per - 1) / per;
+  } else {
+    FAM_REQUIRE(d->key_splits <= 1, FAM_ERR_UNSUPPORTED,
+                "fam_tiny_expert: context splits need one 32-wide slice (slice %lld, %lld slices)", (long long)W,
+                (long long)G);
+  }
+  if (KS > 1 && need_part_x)
+    FAM_REQUIRE(d->part_x != nullptr && fam_host::aligned16(d->part_x), FAM_ERR_INVALID_ARG,
+                "fam_tiny_expert: %lld context splits need part_x (B * %lld * 32 * (slice + 4) floats, 16-byte aligned)",
+                (long long)KS, (long long)KS);
+  a.KS = (int)KS;
+  a.part_x = d->part_x;
   a.p0 = a.p1 = 0;
   return FAM_OK;
+}
+
+extern "C" int fam_tiny_key_splits(const fam_tiny_desc* d) {
+  fam::TinyArgs a;
+  int64_t W = 0, nc = 0;
+  const int rc = tiny_prepare(d, a, W, nc, false);
+  return rc != FAM_OK ? -rc : a.KS;
 }
 
 extern "C" int fam_tiny_expert(const fam_tiny_desc* d, int64_t phase_begin, int64_t phase_end, void* stream) {

@@ -135,6 +135,7 @@ class TinyDesc(C.Structure):
         ("ctx_emb", _vp), ("ctx_emb_ld", _i64),
         ("ck_wt", _vp), ("ck_b", _vp), ("cnk_w", _vp), ("cv_w", _vp), ("cv_b", _vp),
         ("ctx_rs", _vp),
+        ("key_splits", C.c_int32), ("part_x", _vp),
     ]
 
 
@@ -158,6 +159,7 @@ SIGNATURES = {
     "fam_cae_decode": (C.c_int, [C.POINTER(CaeDesc), _vp]),
     "fam_tiny_expert": (C.c_int, [C.POINTER(TinyDesc), _i64, _i64, _vp]),
     "fam_tiny_context": (C.c_int, [C.POINTER(TinyDesc), _vp]),
+    "fam_tiny_key_splits": (C.c_int, [C.POINTER(TinyDesc)]),
     "fam_gemm_final": (C.c_int, [_vp, _i64, _vp, _i64, _vp, C.c_int, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "fam_gemm_partial_splits": (C.c_int, [_i64, _i64, _i64]),
     "fam_rowop": (C.c_int, [C.POINTER(RowopDesc), _vp]),

@@ -655,6 +655,14 @@ class FusedActionDiT:
                     "part_s", "part_c"):
             setattr(d, key, tw[key].data_ptr())
         d.out = self.latents.data_ptr()
+        # context splits of the cross phases (one 32-wide slice, few batch rows): the library's choice
+        ks = self.lib.fam_tiny_key_splits(C.byref(d))
+        if ks < 0:
+            return None
+        if ks > 1:
+            tw["part_x"] = torch.zeros(B * ks * 32 * (W + 4), **f32)
+            d.part_x = tw["part_x"].data_ptr()
+        tw["KS"] = ks
         if self.lib.fam_tiny_expert(C.byref(d), 0, 0, None) != 0:
             return None
         tw["desc"] = d

@@ -661,9 +661,25 @@ typedef struct fam_tiny_desc {
   const void* ctx_emb; int64_t ctx_emb_ld;
   const void* ck_wt; const void* ck_b; const void* cnk_w; const void* cv_w; const void* cv_b;
   float* ctx_rs;
+  int32_t key_splits; float* part_x;
 } fam_tiny_desc;
 
 int fam_tiny_expert(const fam_tiny_desc* d, int64_t phase_begin, int64_t phase_end, void* stream);
+
+/*
+ * fam_tiny_key_splits -- the context splits KS that fam_tiny_expert's cross phases use for this
+ * descriptor (a negative FAM_ERR_* when the descriptor is refused; part_x is not checked).
+ * With one 32-wide slice (A = 32) and few batch rows a cross phase runs KS workgroups per batch
+ * row, each over whole 32-key blocks of the context (key_splits = 0: the library's choice, at
+ * most 8 splits of at least 4 blocks while B * KS fits the CUs; key_splits >= 1 asks for that
+ * count, capped at 8 and at the context's blocks; either count then drops to the splits of
+ * ceil(blocks / count) blocks that hold keys); each split stores its unnormalised output
+ * with its running max and sum to part_x [B][KS][32][slice + 4] (fp32, caller-owned), and the
+ * next phase merges the splits in split order before the cross o projection.
+ * Replaces: no reference operation (the context attention of CrossAttention.forward,
+ *           FB/wan_video_dit.py:214-219, split over workgroups).
+ */
+int fam_tiny_key_splits(const fam_tiny_desc* d);
 
 /*
  * fam_tiny_context -- for slices wider than 32: every context key's factor

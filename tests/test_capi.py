@@ -126,6 +126,19 @@ def test_tiny_expert_validation(lib):
     assert lib.fam_tiny_context(C.byref(_tiny_desc(ck_b=None)), None) == _capi.FAM_ERR_INVALID_ARG
     assert f(C.byref(_tiny_desc(video_rs=3072 * 3 + 4)), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
     assert f(C.byref(_tiny_desc(action_dim=40)), 0, 0, None) == _capi.FAM_ERR_UNSUPPORTED
+    # context splits of the cross phases: one 32-wide slice (4 x 8 heads) over 1560 keys, one
+    # batch row -> 7 splits of 7 blocks (each holds keys); none at 256 rows or over 100 keys;
+    # forced counts capped; refused for several slices; part_x required once they are in use
+    ks = lib.fam_tiny_key_splits
+    c3 = dict(heads=4, head_dim=8, ctx_len=1560, video_len=0)
+    assert ks(C.byref(_tiny_desc(**c3))) == 7
+    assert ks(C.byref(_tiny_desc(**dict(c3, batch=256)))) == 1
+    assert ks(C.byref(_tiny_desc(**dict(c3, ctx_len=100)))) == 1
+    assert ks(C.byref(_tiny_desc(**dict(c3, key_splits=3)))) == 3
+    assert ks(C.byref(_tiny_desc(**dict(c3, key_splits=50)))) == 7   # 8 splits of ceil(49 / 8) blocks: 7 hold keys
+    assert ks(C.byref(_tiny_desc(ctx_len=1560, key_splits=3))) == -_capi.FAM_ERR_UNSUPPORTED
+    assert f(C.byref(_tiny_desc(**dict(c3, part_x=None))), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
+    assert f(C.byref(_tiny_desc(**dict(c3, part_x=4096 + 8))), 0, 0, None) == _capi.FAM_ERR_INVALID_ARG
 
 
 def test_validation_rejects_before_launch(lib):

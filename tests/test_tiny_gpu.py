@@ -69,6 +69,8 @@ def _oracle_mot_loop(p, cfg, noise, ctx, vks, vvs, joint, steps, shift=5.0):
         (3, 8, 2, 64, 128, 98, 129, 2, 2, 64, False, 16),   # batch of 3, 2 slices of one 64-dim head
         (2, 6, 24, 128, 256, 98, 60, 2, 2, 0, False, 7),    # the CAE heads, 6 tokens, action dim 7
         (1, 16, 2, 16, 64, 0, 20, 2, 3, 0, False, 7),       # no video prefix, 16 tokens, 2 x 16 heads
+        (1, 8, 4, 8, 64, 0, 300, 2, 3, 0, False, 16),       # config 3's heads: the context over 3 splits
+        (2, 8, 4, 8, 64, 40, 1560, 2, 2, 0, True, 16),      # 7 splits of 1560 keys, joint mask, 2 rows
     ])
 def test_tiny_expert_matches_oracle_and_generic_plan(B, S, heads, dh, ffn, Sv, Lc, layers, steps, slice_, masked,
                                                      da):
@@ -90,6 +92,8 @@ def test_tiny_expert_matches_oracle_and_generic_plan(B, S, heads, dh, ffn, Sv, L
               video_mask=joint[Sv:, :] if (Sv and masked) else None)
     m = Model(cfg, p, tiny=True, tiny_slice=slice_, **kw)
     assert m.tiny is not None and m.num_launches < 2 * layers * steps + 16
+    if heads * dh == 32 and Lc >= 128:
+        assert m.tiny["KS"] > 1   # the cross phases split the context over workgroups
     if Sv:
         m.set_video_kv([k.cuda() for k in vks], [v.cuda() for v in vvs])
     y = m.infer(noise.cuda(), ctx.cuda()).float().cpu()
