@@ -1717,14 +1717,15 @@ static void launch_final_steps(const FinalArgs& a, int steps, hipStream_t s) {
 
 template <int MT>
 static void launch_final(const FinalArgs& a, hipStream_t s) {
-  // K <= 256: 4 waves; <= 1024: 8 waves; longer: 16 waves; k-steps per wave 1, 2, 4 or 8
-  // (more waves per workgroup shorten each wave's load issue, the critical path at M <= 64)
+  // K <= 1024: 4 waves; longer: 16 waves; k-steps per wave 1, 2, 4 or 8.  Graph-timed at
+  // M = 32, K = 1024 (N = 1024 / 3072 / 4096), 4 waves of 8 k-steps beat 8 waves of 4 by
+  // 0.1-0.3 us a launch (the 4-way merge of the wave sums is shorter); above K = 1024 the 16
+  // waves keep each wave's loads at 8 k-steps
   const int64_t ksteps = (a.K + 31) / 32;
-  const int nw = ksteps <= 8 ? 4 : (ksteps <= 32 ? 8 : 16);
+  const int nw = ksteps <= 32 ? 4 : 16;
   int steps = 1;
   while (steps * nw < ksteps) steps <<= 1;
   if (nw == 4) launch_final_steps<MT, 4>(a, steps, s);
-  else if (nw == 8) launch_final_steps<MT, 8>(a, steps, s);
   else launch_final_steps<MT, 16>(a, steps, s);
 }
 
