@@ -27,6 +27,13 @@ CA/action_dit.py:127-231) add:
     fastwam::res_ln1(x, o, mb, tm, wn, bn, go, eps)         FG/mot.py:1829-1844
     fastwam::res_ln2(x, o1, o2, mb, mb2, tm, go, sho, sco, eps)   FG/mot.py:1846-1862
     fastwam::res_ln_tail(x, o, mb, mb2, tm, go, sho, sco, eps)    FG/mot.py:1883-1899
+    fastwam::pf_skmm(x, w), pf_skmm_big(x, w)               FG/mot.py:2031-2074
+    fastwam::res_ln1_sk(x, p, bi, mb, tm, wn, bn, go, eps, sk)    FG/mot.py:2155-2173
+    fastwam::res_ln2_sk(x, o1, p, bi, mb, mb2, tm, go, sho, sco, eps, sk)
+                                                            FG/mot.py:2175-2194
+    fastwam::res_ln_tail_sk(x, p, bi, mb, mb2, tm, go, sho, sco, eps, sk)
+                                                            FG/mot.py:2227-2244
+    fastwam::pf_qcomb(p, bi, wq, eps, sk)                   FG/mot.py:2320-2333
     fastwam::mot_attn(q, k, v, msk, nh, hd, head_major)     CA/mot.py:2948-2976
     fastwam::mot_qkv_post(qkv, qw, kw, freqs, kbuf, vbuf, sv, eps)  CA/mot.py:2793-2822
     fastwam::xattn_qn(qr, qw, k, v, msk, nh, hd, eps)       CA/mot.py:3673-3700
@@ -40,6 +47,10 @@ bf16 rounding of an intermediate; the GPU tests hold each against an eager resta
 reference kernel at 2e-2):
   res_ln*   the norm reads the bf16-rounded residual (the reference takes its statistics from
             the fp32 sum); the gate / shift / scale sums modulation + t_mod in fp32 as it does;
+            the *_sk forms round the split-K combine + bias to bf16 once, as the reference does;
+  pf_skmm*  the product sits whole in plane 0 and the other planes are zero (the reference
+            spreads K over its configured count of planes): any sk sums to the same product;
+  pf_qcomb  RMSNorm rounds to bf16 before the weight (the reference kernel does not);
   mot_qkv_post, xattn_qn, ctx_kv_norm
             RMSNorm rounds to bf16 before the weight (the eager module's order); the CAE
             kernels of xattn_qn and ctx_kv_norm multiply the weight before their one rounding;
@@ -461,6 +472,157 @@ def res_ln_tail(x: torch.Tensor, o: torch.Tensor, mb: torch.Tensor, mb2: torch.T
 def _(x, o, mb, mb2, tm, go, sho, sco, eps):
     S, N = int(x.shape[1]), int(x.shape[2])
     return [x.new_empty((1, S, N)), x.new_empty((1, S, N))]
+
+
+# --------------------------------------------------------------------------- prefill split-K planes (FG)
+# The prefill's o-projections and ffn.2 return fp32 planes [SKMAX, M, N] (SKMAX 8, and 16 for
+# ffn.2: fixed so the fake shape does not follow the split count) of which the consumer sums the
+# first `sk`, sk being the count its caller configured (FG/mot.py:1944-1961, :2017-2074).  Here
+# the product lands whole in plane 0 and every other plane holds zeros, so the first sk planes
+# sum to it for every sk in [1, SKMAX].  As the reference's default (FASTWAM_PFSKSHARE), one
+# buffer per (device, SKMAX, M, N) serves every call: its zero planes are written once, when it
+# is allocated, a call rewrites plane 0 only, and a result is valid until the next call of the
+# same shape.
+_PF_PARTS: dict = {}
+
+
+def _pf_planes(x: torch.Tensor, w: torch.Tensor, skmax: int) -> torch.Tensor:
+    _check(x, "x")
+    _check(w, "w")
+    x2 = _rows2d(x)
+    M, K, N = x2.shape[0], x2.shape[1], w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"pf_skmm: x has K={K} columns, w is {tuple(w.shape)}")
+    key = (x.device.type, x.device.index, skmax, M, N)
+    part = _PF_PARTS.get(key)
+    if part is None:
+        part = torch.zeros((skmax, M, N), dtype=torch.float32, device=x.device)
+        if not torch.cuda.is_current_stream_capturing():
+            _PF_PARTS[key] = part
+    gemm(x2, w.contiguous(), None, part[0], out_f32=True)
+    return part
+
+
+@torch.library.custom_op("fastwam::pf_skmm", mutates_args=())
+def pf_skmm(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x w^T as [8, M, N] fp32 split planes (FG/mot.py:2031-2043)."""
+    return _pf_planes(x, w, 8)
+
+
+@pf_skmm.register_fake
+def _(x, w):
+    return x.new_empty((8, int(x.shape[-2]), int(w.shape[0])), dtype=torch.float32)
+
+
+@torch.library.custom_op("fastwam::pf_skmm_big", mutates_args=())
+def pf_skmm_big(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x w^T as [16, M, N] fp32 split planes, the ffn.2 site's (FG/mot.py:2057-2069)."""
+    return _pf_planes(x, w, 16)
+
+
+@pf_skmm_big.register_fake
+def _(x, w):
+    return x.new_empty((16, int(x.shape[-2]), int(w.shape[0])), dtype=torch.float32)
+
+
+def _pf_combine_planes(p: torch.Tensor, sk: int, S: int, N: int) -> torch.Tensor:
+    """The first sk planes of a split-plane operand, checked."""
+    if not p.is_cuda or p.dim() != 3 or p.dtype != torch.float32 or not p.is_contiguous() or p.shape[1] != S or \
+            p.shape[2] != N:
+        raise ValueError(f"split planes must be contiguous fp32 CUDA [SKMAX, {S}, {N}], got {tuple(p.shape)} "
+                         f"{p.dtype} on {p.device}")
+    if not 1 <= sk <= p.shape[0]:
+        raise ValueError(f"sk={sk} outside [1, {p.shape[0]}]")
+    return p[:sk]
+
+
+def _pf_combine(p: torch.Tensor, bi: torch.Tensor, sk: int, S: int, N: int) -> torch.Tensor:
+    """bf16(sum of the first sk planes + bias), [S, N]: the reference kernels round the
+    combined product once, where a bf16 GEMM output would have been (FG/mot.py:2112-2120)."""
+    _check(bi, "bi")
+    planes = _pf_combine_planes(p, sk, S, N)
+    pb = torch.empty((S, N), dtype=_BF16, device=p.device)
+    rowop(pb, partials=planes, bias=bi.contiguous())
+    return pb
+
+
+@torch.library.custom_op("fastwam::res_ln1_sk", mutates_args=())
+def res_ln1_sk(x: torch.Tensor, p: torch.Tensor, bi: torch.Tensor, mb: torch.Tensor, tm: torch.Tensor,
+               wn: torch.Tensor, bn: torch.Tensor, go: int, eps: float, sk: int) -> List[torch.Tensor]:
+    """[LN(x + g o) wn + bn, o] with o = bf16(sum of sk planes of p + bi): the self-attention
+    o-projection's split-K combine, its residual and norm3 (FG/mot.py:2155-2168)."""
+    S, N = x.shape[1], x.shape[2]
+    o = _pf_combine(p, bi, sk, S, N)
+    _check(x, "x")
+    _, no = _res_norm(x, [o], _mod_rows(mb, tm, go, S, N), eps, ln=(wn, bn))
+    return [no, o.view(1, S, N)]
+
+
+@res_ln1_sk.register_fake
+def _(x, p, bi, mb, tm, wn, bn, go, eps, sk):
+    S, N = int(x.shape[1]), int(x.shape[2])
+    return [x.new_empty((1, S, N)), x.new_empty((1, S, N))]
+
+
+@torch.library.custom_op("fastwam::res_ln2_sk", mutates_args=())
+def res_ln2_sk(x: torch.Tensor, o1: torch.Tensor, p: torch.Tensor, bi: torch.Tensor, mb: torch.Tensor,
+               mb2: torch.Tensor, tm: torch.Tensor, go: int, sho: int, sco: int, eps: float,
+               sk: int) -> List[torch.Tensor]:
+    """res_ln2 with its second term the split-K combine of the cross-attention o-projection:
+    [xo, no], xo = x + g o1 + bf16(sum of sk planes of p + bi) (FG/mot.py:2175-2189)."""
+    S, N = x.shape[1], x.shape[2]
+    o2 = _pf_combine(p, bi, sk, S, N)
+    for t, n in ((x, "x"), (o1, "o1"), (mb, "mb"), (mb2, "mb2"), (tm, "tm")):
+        _check(t, n)
+    xo, no = _res_norm(x, [o1, o2], _mod_rows(mb, tm, go, S, N), eps,
+                       ada=(_mod_rows(mb2, tm, sho, S, N), _mod_rows(mb2, tm, sco, S, N)))
+    return [xo, no]
+
+
+@res_ln2_sk.register_fake
+def _(x, o1, p, bi, mb, mb2, tm, go, sho, sco, eps, sk):
+    S, N = int(x.shape[1]), int(x.shape[2])
+    return [x.new_empty((1, S, N)), x.new_empty((1, S, N))]
+
+
+@torch.library.custom_op("fastwam::res_ln_tail_sk", mutates_args=())
+def res_ln_tail_sk(x: torch.Tensor, p: torch.Tensor, bi: torch.Tensor, mb: torch.Tensor, mb2: torch.Tensor,
+                   tm: torch.Tensor, go: int, sho: int, sco: int, eps: float, sk: int) -> List[torch.Tensor]:
+    """res_ln_tail on the split-K combine of ffn.2: [xo, no], xo = x + g bf16(sum of sk planes
+    of p + bi), no = the next block's AdaLN1 of xo (FG/mot.py:2227-2239)."""
+    S, N = x.shape[1], x.shape[2]
+    o = _pf_combine(p, bi, sk, S, N)
+    for t, n in ((x, "x"), (mb, "mb"), (mb2, "mb2"), (tm, "tm")):
+        _check(t, n)
+    xo, no = _res_norm(x, [o], _mod_rows(mb, tm, go, S, N), eps,
+                       ada=(_mod_rows(mb2, tm, sho, S, N), _mod_rows(mb2, tm, sco, S, N)))
+    return [xo, no]
+
+
+@res_ln_tail_sk.register_fake
+def _(x, p, bi, mb, mb2, tm, go, sho, sco, eps, sk):
+    S, N = int(x.shape[1]), int(x.shape[2])
+    return [x.new_empty((1, S, N)), x.new_empty((1, S, N))]
+
+
+@torch.library.custom_op("fastwam::pf_qcomb", mutates_args=())
+def pf_qcomb(p: torch.Tensor, bi: torch.Tensor, wq: torch.Tensor, eps: float, sk: int) -> torch.Tensor:
+    """RMSNorm(bf16(sum of sk planes of p + bi)) * wq, [1, S, N]: the prefill cross-attention
+    query's split-K combine and norm_q (FG/mot.py:2290-2329)."""
+    S, N = p.shape[1], p.shape[2]
+    _check(wq, "wq")
+    if wq.numel() != N:
+        raise ValueError(f"pf_qcomb: wq has {wq.numel()} entries for rows of {N}")
+    q = torch.empty((S, N), dtype=_BF16, device=p.device)
+    qn = torch.empty((1, S, N), dtype=_BF16, device=p.device)
+    rowop(q, partials=_pf_combine_planes(p, sk, S, N), bias=bi.contiguous(), norm=_capi.FAM_ROWNORM_RMS, eps=eps,
+          segs=((0, wq.contiguous()),), seg_width=N, nout=qn.view(S, N))
+    return qn
+
+
+@pf_qcomb.register_fake
+def _(p, bi, wq, eps, sk):
+    return bi.new_empty((1, int(p.shape[1]), int(p.shape[2])))
 
 
 # --------------------------------------------------------------------------- CAE action expert (CA)

@@ -38,6 +38,10 @@ Pinning (what checks each function, see ``tests/test_oracle.py``):
                             config, two image sizes) + planted slips; vae_avg_down closed forms
   geak_res_ln / cae_*       against the pinned primitives they compose (layer_norm, attention,
                             rope_apply, time_mlp, ffn) with planted slips
+  geak_split_combine / geak_qcomb
+                            K-chunk planes of a product sum to the whole product (a matmul
+                            closed form), sk-plane truncation, one bf16 rounding; qcomb against
+                            unit RMS before the weight, with planted slips
 """
 from __future__ import annotations
 
@@ -1177,6 +1181,25 @@ def geak_res_ln(x: torch.Tensor, parts: Sequence[torch.Tensor], gate: torch.Tens
     if ln is not None:
         return t, n * ln[0] + ln[1]
     return t, n * (1 + ada[1]) + ada[0]
+
+
+def geak_split_combine(planes: torch.Tensor, bias: torch.Tensor, sk: int) -> torch.Tensor:
+    """The split-K combine of _fw_reslnsk_kernel / _fw_qcomb_kernel (FG/mot.py:2112-2120,
+    :2304-2311): the first sk fp32 planes summed in plane order, plus the bias, rounded to bf16
+    once (returned in fp32)."""
+    if not 1 <= sk <= planes.shape[0]:
+        raise ValueError(f"sk={sk} outside [1, {planes.shape[0]}]")
+    p = planes[0].float()
+    for i in range(1, sk):
+        p = p + planes[i].float()
+    return (p + bias.float()).to(torch.bfloat16).float()
+
+
+def geak_qcomb(planes: torch.Tensor, bias: torch.Tensor, wq: torch.Tensor, eps: float, sk: int) -> torch.Tensor:
+    """_fw_qcomb_kernel (FG/mot.py:2290-2318): x = the split-K combine, then
+    x * rsqrt(mean(x^2) + eps) * wq with no rounding between the norm and the weight."""
+    x = geak_split_combine(planes, bias, sk)
+    return x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) * wq.float()
 
 
 def cae_qkv_post(qkv: torch.Tensor, qw: torch.Tensor, kw: torch.Tensor, freqs: torch.Tensor, num_heads: int,

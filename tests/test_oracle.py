@@ -986,3 +986,32 @@ def test_geak_operator_restatements_pinned():
     t_ref, tm_ref = O.time_mlp(p, cfg, ts)
     assert torch.allclose(tt, t_ref) and torch.allclose(tm, tm_ref.reshape(1, -1))
     assert torch.allclose(tk, O.linear(atok, p["action_encoder.weight"], p["action_encoder.bias"]))
+
+
+def test_geak_split_combine_and_qcomb_pinned():
+    """The prefill's split-K combine: planes holding the K-chunks of a product sum (first sk in
+    plane order) to the whole matmul plus bias, rounded to bf16 once; planes past sk are not read.
+    qcomb's output has unit RMS before the weight.  Dropping a plane, the bias, or rounding before
+    the weight each fails."""
+    g = torch.Generator().manual_seed(78)
+    M, K, N, sk, eps = 6, 64, 40, 4, 1e-6
+    x, w = torch.randn(M, K, generator=g), torch.randn(N, K, generator=g)
+    bias = torch.randn(N, generator=g)
+    planes = torch.full((8, M, N), 1e3)            # planes past sk carry garbage
+    for i in range(sk):
+        c = slice(i * K // sk, (i + 1) * K // sk)
+        planes[i] = x[:, c] @ w[:, c].T
+    y = O.geak_split_combine(planes, bias, sk)
+    want = (x.double() @ w.double().T + bias.double()).float()
+    assert ((y - want).abs() <= 2 ** -7 * want.abs() + 1e-4).all()              # one bf16 rounding
+    assert torch.equal(y, y.to(torch.bfloat16).float())
+    assert (O.geak_split_combine(planes, bias, sk - 1) - want).abs().max() > 1.0   # a plane dropped
+    assert (O.geak_split_combine(planes, bias * 0, sk) - want).abs().max() > 0.5   # the bias dropped
+    with pytest.raises(ValueError):
+        O.geak_split_combine(planes, bias, 9)
+    wq = 1 + 0.3 * torch.randn(N, generator=g)
+    q = O.geak_qcomb(planes, bias, wq, eps, sk)
+    unit = q / wq
+    assert torch.allclose(unit.pow(2).mean(-1), torch.ones(M), atol=1e-4)
+    assert torch.allclose(unit * y.pow(2).mean(-1, keepdim=True).add(eps).sqrt(), y, rtol=1e-4, atol=1e-4)
+    assert (O.rms_norm(y.to(torch.bfloat16), wq, eps).float() - q).abs().max() > 0  # eager order rounds first

@@ -137,6 +137,33 @@ def test_geak_prefill_and_cae_ops_trace():
         assert any(t_.startswith("fastwam." + op_ + ".") for t_ in targets), (op_, targets)
 
 
+
+def test_geak_split_plane_ops_trace():
+    """pf_skmm / pf_skmm_big give fp32 planes [8 | 16, M, N] whatever the split count, and the
+    consumers res_ln1_sk, res_ln2_sk, res_ln_tail_sk and pf_qcomb trace as single nodes of the
+    reference's output shapes (FG/mot.py:2045-2074, :2170-2244, :2331-2333)."""
+    from fam import fastwam_ops  # noqa: F401
+
+    class M(torch.nn.Module):
+        def forward(self, x, a, w, bi, mb, tm, wn, bn, o1, h, w2):
+            p1 = torch.ops.fastwam.pf_skmm.default(a, w)
+            h3, o = torch.ops.fastwam.res_ln1_sk.default(x, p1, bi, mb, tm, wn, bn, 128, 1e-6, 4)
+            q = torch.ops.fastwam.pf_qcomb.default(torch.ops.fastwam.pf_skmm.default(h3, w), bi, wn, 1e-6, 4)
+            x1, n1 = torch.ops.fastwam.res_ln2_sk.default(x, o, p1, bi, mb, mb, tm, 128, 192, 256, 1e-6, 4)
+            p3 = torch.ops.fastwam.pf_skmm_big.default(h, w2)
+            x2, n2 = torch.ops.fastwam.res_ln_tail_sk.default(x1, p3, bi, mb, mb, tm, 320, 0, 64, 1e-6, 8)
+            return p1, p3, h3, o, q, x1, n1, x2, n2
+
+    args = (_meta(1, 6, 64), _meta(1, 6, 64), _meta(64, 64), _meta(64), _meta(384), _meta(6, 384), _meta(64),
+            _meta(64), _meta(1, 6, 64), _meta(1, 6, 256), _meta(64, 256))
+    outs, _, targets = _compile_graph(M(), *args)
+    p1, p3, *rest = outs
+    assert p1.shape == (8, 6, 64) and p3.shape == (16, 6, 64) and p1.dtype == p3.dtype == torch.float32
+    assert all(t_.shape == (1, 6, 64) and t_.dtype == torch.bfloat16 for t_ in rest)
+    for op_ in ("pf_skmm", "pf_skmm_big", "res_ln1_sk", "res_ln2_sk", "res_ln_tail_sk", "pf_qcomb"):
+        assert any(t_.startswith("fastwam." + op_ + ".") for t_ in targets), (op_, targets)
+
+
 # --------------------------------------------------------------------------- RoPE tables
 def _cat_table(S, Dh, offset=0.0):
     ang = (torch.arange(S, dtype=torch.float64)[:, None] + offset) * \

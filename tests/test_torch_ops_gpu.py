@@ -279,6 +279,57 @@ def test_geak_prefill_ops(fw):
     assert max(errs) <= 2e-2
 
 
+
+def test_geak_prefill_split_planes(fw):
+    """pf_skmm / pf_skmm_big and their consumers res_ln1_sk, res_ln2_sk, res_ln_tail_sk and
+    pf_qcomb at the prefill's shape (FG/mot.py:2017-2329).  The consumers get planes made the way
+    the reference's producer makes them (the K-chunks of a product in the first sk planes, other
+    values past sk) and are held to the oracle's restatement of the reference kernels; the
+    producers' planes summed over any leading count give the product."""
+    g = torch.Generator().manual_seed(93)
+    S, N, K, sk, eps = 98, 3072, 512, 4, 1e-6
+    f = lambda t: t.float()  # noqa: E731
+    a, w, bi = _rand(g, 1, S, K), _rand(g, N, K, scale=0.05), _rand(g, N, scale=0.1)
+    prod = O.linear(f(a)[0], f(w), None)
+    for op, skmax in ((fw.pf_skmm, 8), (fw.pf_skmm_big, 16)):
+        pl = op(a.cuda(), w.cuda())
+        assert pl.shape == (skmax, S, N) and pl.dtype == torch.float32
+        for n in (1, sk, skmax):
+            assert _rel(pl[:n].sum(0), prod) <= 2e-2
+    planes = torch.randn(8, S, N, generator=g) * 5.0   # past sk: values the consumer must not read
+    for i in range(sk):
+        c = slice(i * K // sk, (i + 1) * K // sk)
+        planes[i] = f(a)[0, :, c] @ f(w)[:, c].T
+    o_ref = O.geak_split_combine(planes, f(bi), sk)
+    xr, o1 = _rand(g, 1, S, N), _rand(g, 1, S, N)
+    mb, mb2, tm = _rand(g, 6 * N, scale=0.3), _rand(g, 6 * N, scale=0.3), _rand(g, S, 6 * N, scale=0.3)
+    wn, bn = (1 + 0.2 * torch.randn(N, generator=g)).to(BF), _rand(g, N, scale=0.2)
+    wq = (1 + 0.2 * torch.randn(N, generator=g)).to(BF)
+
+    def ch(m, off):
+        return f(m).reshape(-1)[off:off + N][None, :] + f(tm)[:, off:off + N]
+    pd, bid, xd, o1d, mbd, mb2d, tmd = (t.cuda() for t in (planes, bi, xr, o1, mb, mb2, tm))
+    y1, o = fw.res_ln1_sk(xd, pd, bid, mbd, tmd, wn.cuda(), bn.cuda(), 2 * N, eps, sk)
+    _, r1 = O.geak_res_ln(f(xr)[0], [o_ref], ch(mb, 2 * N), eps, ln=(f(wn), f(bn)))
+    x2, y2 = fw.res_ln2_sk(xd, o1d, pd, bid, mbd, mb2d, tmd, 2 * N, 3 * N, 4 * N, eps, sk)
+    t2, r2 = O.geak_res_ln(f(xr)[0], [f(o1)[0], o_ref], ch(mb, 2 * N), eps, ada=(ch(mb2, 3 * N), ch(mb2, 4 * N)))
+    x3, y3 = fw.res_ln_tail_sk(xd, pd, bid, mbd, mb2d, tmd, 5 * N, 0, N, eps, sk)
+    t3, r3 = O.geak_res_ln(f(xr)[0], [o_ref], ch(mb, 5 * N), eps, ada=(ch(mb2, 0), ch(mb2, N)))
+    qn = fw.pf_qcomb(pd, bid, wq.cuda(), eps, sk)
+    rq = O.geak_qcomb(planes, f(bi), f(wq), eps, sk)
+    errs = [_rel(o[0], o_ref), _rel(y1[0], r1), _rel(x2[0], t2), _rel(y2[0], r2), _rel(x3[0], t3),
+            _rel(y3[0], r3), _rel(qn[0], rq)]
+    print("combine / res_ln1_sk / res_ln2_sk (x, norm) / res_ln_tail_sk (x, norm) / pf_qcomb:",
+          " ".join(f"{e:.2e}" for e in errs))
+    assert max(errs) <= 2e-2
+    assert _rel(O.geak_split_combine(planes, f(bi), sk + 1), o_ref) > 0.5   # a plane past sk would show
+    # the producer feeding the consumer: the o-projection through pf_skmm into res_ln1_sk
+    y1c, oc = fw.res_ln1_sk(xd, fw.pf_skmm(a.cuda(), w.cuda()), bid, mbd, tmd, wn.cuda(), bn.cuda(), 2 * N, eps, sk)
+    assert _rel(oc[0], O.linear(f(a)[0], f(w), f(bi))) <= 2e-2 and _rel(y1c[0], r1) <= 2e-2
+    with pytest.raises(ValueError):
+        fw.pf_qcomb(pd, bid, wq.cuda(), eps, 9)
+
+
 def test_cae_ops(fw):
     """The CAE action expert's operators at its shape (8 tokens, hidden 32, 24 x 128 heads, 98 + 8
     joint keys, 129 context keys, 30 layers' context K) against the oracle's restatements of the
