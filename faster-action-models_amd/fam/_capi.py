@@ -22,6 +22,7 @@ FAM_PRO_NONE, FAM_PRO_LAYERNORM, FAM_PRO_ADALN, FAM_PRO_LN_FOLDED = 0, 1, 2, 3
 FAM_ACT_NONE, FAM_ACT_GELU_TANH, FAM_ACT_SILU, FAM_ACT_RELU, FAM_ACT_GELU_ERF = 0, 1, 2, 3, 4
 FAM_ROWSRC_PARTIALS, FAM_ROWSRC_SMALLK = 0, 1
 FAM_ROWNORM_NONE, FAM_ROWNORM_LAYERNORM, FAM_ROWNORM_ADALN, FAM_ROWNORM_RMS = 0, 1, 2, 3
+FAM_Q8_ROW, FAM_Q8_GELU, FAM_Q8_LN_MOD, FAM_Q8_ADD_LN_MOD = 0, 1, 2, 3
 
 _i64 = C.c_int64
 _vp = C.c_void_p
@@ -139,6 +140,16 @@ class TinyDesc(C.Structure):
     ]
 
 
+class RowQ8Desc(C.Structure):
+    """fam_rowq8_desc (include/fam_hip.h)."""
+    _fields_ = [
+        ("mode", C.c_int), ("x", _vp), ("ldx", _i64), ("x2", _vp), ("ldx2", _i64),
+        ("shift", _vp), ("scale", _vp), ("eps", C.c_float),
+        ("y", _vp), ("ldy", _i64), ("s", _vp), ("xo", _vp), ("ldxo", _i64),
+        ("M", _i64), ("D", _i64),
+    ]
+
+
 SIGNATURES = {
     "fam_version": (C.c_int, []),
     "fam_last_error": (C.c_char_p, []),
@@ -160,6 +171,8 @@ SIGNATURES = {
     "fam_tiny_expert": (C.c_int, [C.POINTER(TinyDesc), _i64, _i64, _vp]),
     "fam_tiny_context": (C.c_int, [C.POINTER(TinyDesc), _vp]),
     "fam_tiny_key_splits": (C.c_int, [C.POINTER(TinyDesc)]),
+    "fam_row_q8": (C.c_int, [C.POINTER(RowQ8Desc), _vp]),
+    "fam_mask_bias": (C.c_int, [_vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
     "fam_gemm_final": (C.c_int, [_vp, _i64, _vp, _i64, _vp, C.c_int, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "fam_gemm_partial_splits": (C.c_int, [_i64, _i64, _i64]),
     "fam_rowop": (C.c_int, [C.POINTER(RowopDesc), _vp]),

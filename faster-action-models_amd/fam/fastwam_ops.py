@@ -42,6 +42,29 @@ CA/action_dit.py:127-231) add:
     fastwam::adit_tmod(te, inv, w0, b0, w1, b1, w2, b2, atok, aw, ab, fuse_sin)
                                                             CA/action_dit.py:191-225
 
+and the CAE tree's fused levers and fp8 rows (CA/mot.py:2830-3980):
+
+    fastwam::mask_bias(am, cm, mp, skp, ncp)                CA/mot.py:3342-3369
+    fastwam::mot_attn_oproj(q, k, v, msk, wo, bo, acc, nh, hd)       (mutates acc)  :2864-2900
+    fastwam::mod_n3q(res, so, mod, tmod, lnw, lnb, qw, qb, eps)                     :2978-3008
+    fastwam::mod_n3q_qn(... qw, qb, qnw, gram, eps, eps_q)                          :3227-3262
+    fastwam::n3q_xoproj(... qnw, gram, ck, cv, msk, wo, bo, acc, nh, eps, eps_q)    :3414-3470
+    fastwam::mot_ffn_fold(x, oacc, modc, modn, tmod, w1, b1, w2, b2, eps2, eps1, hasnext)
+                                                                                    :3086-3122
+    fastwam::mot_sa_qkv(xin, w, b, qgr, kgr, qw, kw, freqs, kbuf, vbuf, za, zb, sv, eps)
+                                                                                    :3285-3322
+    fastwam::mot_ffn_sa_qkv(xp, oacc, ..., za, zb, sv, eps, eps2, eps1)             :3498-3565
+    fastwam::mot_qkv_post_z(qkv, qw, kw, freqs, kbuf, vbuf, za, zb, sv, eps)        :2830-2860
+    fastwam::mot_qkv_gemm_post_z(xin, wt, bqkv, qw, kw, freqs, kbuf, vbuf, za, zb, sv, eps)
+                                                                                    :3032-3070
+    fastwam::mot_l0_qkv_rope(q, k, v, qw, kw, freqs, kbuf, vbuf, sv, eps)           :3142-3172
+    fastwam::mot_l0_qkv_rope_z(... kbuf, vbuf, oaccx, sv, eps)                      :3180-3210
+    fastwam::ctx_kv_norm_into(g, nkw, out, nl, ahd, eps)                            :3621-3638
+    fastwam::ctx_kv_gemm_norm_into(e, w, b, nkw, out, nl, ahd, eps, has_b)          :3641-3662
+    fastwam::vqkv_post(qkv, qw, kw, freqs, kbuf, vbuf, eps)                         :3713-3750
+    fastwam::row_q8(x), gelu_q8(x), ln_mod_q8(x, shift, scale, eps),
+             add_ln_mod_q8(a, b, shift, scale, eps)                                 :3859-3960
+
 Per-operator rounding differences from the Triton kernels they stand in for (all within one
 bf16 rounding of an intermediate; the GPU tests hold each against an eager restatement of the
 reference kernel at 2e-2):
@@ -54,9 +77,20 @@ reference kernel at 2e-2):
   mot_qkv_post, xattn_qn, ctx_kv_norm
             RMSNorm rounds to bf16 before the weight (the eager module's order); the CAE
             kernels of xattn_qn and ctx_kv_norm multiply the weight before their one rounding;
-  mot_ffn, pf_mm_gelu, adit_tmod
+  mot_ffn, pf_mm_gelu, adit_tmod, mot_ffn_fold
             the activation runs on the fp32 accumulator (+ bias) and rounds once; the
-            reference kernels round the pre-activation to bf16 first.
+            reference kernels round the pre-activation to bf16 first;
+  mod_n3q*, n3q_xoproj, mot_ffn_fold
+            the gated residual is formed in fp32 and rounded once (the reference rounds the
+            gate, so and gate * so first), the norms read the bf16 residual; the FFN's output
+            enters xout unrounded;
+  mod_n3q_qn, n3q_xoproj, mot_sa_qkv, mot_ffn_sa_qkv
+            the whole-row q / k norm sums the squares of the (bf16) row itself instead of the
+            Gram form of the unrounded product (gram / qgr / kgr are checked for shape only);
+  mot_l0_qkv_rope, vqkv_post and the *_z forms
+            as mot_qkv_post (bf16 before the norm weight);
+  gelu_q8   exp through the hardware exp2 (a handful of fp8 codes one step apart);
+            row_q8, ln_mod_q8 and add_ln_mod_q8 give the reference's codes.
 ctx_kv_norm returns the K half only ([1, nl, 1, S, ahd]), the reference's default
 (FASTWAM_R2_NORM_V unset, CA/mot.py:578).  adit_tmod computes the sinusoid with the library's
 own fp64 frequencies; `inv` must be 10000^(-j / (FD/2)), which is what the call site passes.
@@ -670,29 +704,45 @@ def mot_qkv_post(qkv: torch.Tensor, qw: torch.Tensor, kw: torch.Tensor, freqs: t
     then the interleaved rotation by freqs [M, hd] (cos at 2p, sin at 2p + 1 of each token's row);
     q returned head-major [1, H, M, hd], k and v written to rows sv .. sv + M of the head-major
     cache buffers kbuf / vbuf [1, H, SKV, hd]."""
-    for t, n in ((qkv, "qkv"), (qw, "qw"), (kw, "kw"), (kbuf, "kbuf"), (vbuf, "vbuf")):
-        _check(t, n)
+    _check(qkv, "qkv")
     M, D3 = qkv.shape[1], qkv.shape[2]
     D = D3 // 3
+    x2 = qkv.reshape(M, D3)
+    qn = _cae_qkv_rows(x2[:, :D], x2[:, D:2 * D], x2[:, 2 * D:], qw, kw, freqs, kbuf, vbuf, sv, eps)
+    return _head_major(qn, kbuf.shape[1])
+
+
+def _head_major(rows: torch.Tensor, H: int) -> torch.Tensor:
+    """[M, H hd] token rows -> [1, H, M, hd] contiguous."""
+    M, D = rows.shape
+    return rows.view(M, H, D // H).transpose(0, 1).contiguous().unsqueeze(0)
+
+
+def _cae_qkv_rows(q2: torch.Tensor, k2: torch.Tensor, v2: torch.Tensor, qw: torch.Tensor, kw: torch.Tensor,
+                  freqs: torch.Tensor, kbuf: torch.Tensor, vbuf: torch.Tensor, sv: int, eps: float,
+                  q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The CAE q / k / v post-processing on [M, D] row views: RMSNorm over D of q and k with their
+    weights and the interleaved rotation by freqs [M, hd] (cos at 2p, sin at 2p + 1), k and v
+    written head-major to rows sv .. sv + M of kbuf / vbuf [1, H, SKV, hd]; returns the rotated q
+    rows [M, D] (into q_out when given)."""
+    for t, n in ((q2, "q"), (k2, "k"), (v2, "v"), (qw, "qw"), (kw, "kw"), (kbuf, "kbuf"), (vbuf, "vbuf")):
+        _check(t, n)
+    M, D = q2.shape
     H, hd, SKV = kbuf.shape[1], kbuf.shape[3], kbuf.shape[2]
-    if H * hd != D or sv < 0 or sv + M > SKV:
+    if H * hd != D or k2.shape != (M, D) or v2.shape != (M, D) or sv < 0 or sv + M > SKV or vbuf.shape != kbuf.shape:
         raise ValueError(f"kbuf {tuple(kbuf.shape)} does not take {M} rows of {D} at row {sv}")
     f = freqs.reshape(-1, hd).float().contiguous()
     if f.shape[0] < M:
         raise ValueError(f"freqs must hold {M} rows of {hd}, got {tuple(freqs.shape)}")
-    x2 = qkv.reshape(M, D3)
-    if x2.stride(-1) != 1 or x2.stride(0) % 8:
-        x2 = x2.contiguous()
-    tab = (f, f[:, 1:], hd, 2, hd)
-    qn = torch.empty((M, D), dtype=qkv.dtype, device=qkv.device)
-    kn = torch.empty((M, D), dtype=qkv.dtype, device=qkv.device)
-    for src, dst, w in ((x2[:, :D], qn, qw), (x2[:, D:2 * D], kn, kw)):
-        cos, sin, trs, tes, head = tab
+    q2, k2 = (t if t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0 else t.contiguous() for t in (q2, k2))
+    qn = q_out if q_out is not None else torch.empty((M, D), dtype=q2.dtype, device=q2.device)
+    kn = torch.empty((M, D), dtype=q2.dtype, device=q2.device)
+    for src, dst, w in ((q2, qn, qw), (k2, kn, kw)):
         call("fam_rmsnorm_rope", src.data_ptr(), src.stride(0), dst.data_ptr(), dst.stride(0), M, M, D,
-             w.contiguous().data_ptr(), float(eps), cos.data_ptr(), sin.data_ptr(), trs, tes, head, _stream(qkv))
+             w.contiguous().data_ptr(), float(eps), f.data_ptr(), f[:, 1:].data_ptr(), hd, 2, hd, _stream(src))
     kbuf[0, :, sv:sv + M, :].copy_(kn.view(M, H, hd).transpose(0, 1))
-    vbuf[0, :, sv:sv + M, :].copy_(x2[:, 2 * D:].reshape(M, H, hd).transpose(0, 1))
-    return qn.view(M, H, hd).transpose(0, 1).contiguous().unsqueeze(0)
+    vbuf[0, :, sv:sv + M, :].copy_(v2.reshape(M, H, hd).transpose(0, 1))
+    return qn
 
 
 @mot_qkv_post.register_fake
@@ -819,3 +869,559 @@ def adit_tmod(te: torch.Tensor, inv: torch.Tensor, w0: torch.Tensor, b0: torch.T
 def _(te, inv, w0, b0, w1, b1, w2, b2, atok, aw, ab, fuse_sin):
     return (atok.new_empty((1, w0.shape[0])), atok.new_empty((1, w2.shape[0])),
             atok.new_empty((1, atok.shape[1], w0.shape[0])))
+
+
+# --------------------------------------------------------------------------- CAE fused levers (CA)
+def _mod_vec(mod: torch.Tensor, tmod: torch.Tensor, i: int, n: int) -> torch.Tensor:
+    """Chunk i (width n) of modulation + t_mod, one row for every token: the fp32 sum the CAE
+    kernels form, rounded once to bf16 for the row kernel."""
+    m, t = mod.reshape(-1), tmod.reshape(-1)
+    if m.numel() < (i + 1) * n or t.numel() < (i + 1) * n:
+        raise ValueError(f"modulation / t_mod hold fewer than {i + 1} chunks of {n}")
+    return (m[i * n:(i + 1) * n].float() + t[i * n:(i + 1) * n].float()).to(_BF16).contiguous()
+
+
+def _plane(t: torch.Tensor, M: int, N: int, name: str) -> torch.Tensor:
+    """An fp32 [1, M, N] partial plane of t (the fp32 accumulators are used in place)."""
+    if t.numel() != M * N:
+        raise ValueError(f"{name} must hold {M} x {N} values, got {tuple(t.shape)}")
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        t = t.float().contiguous()
+    return t.view(1, M, N)
+
+
+def _zero_rows(z: torch.Tensor, rows: int, name: str) -> None:
+    """Rows [0, rows) of an fp32 [.., ZN] accumulator set to zero (the reference kernels clear
+    the next layer's o-projection accumulators in passing)."""
+    if z.dtype != torch.float32 or not z.is_contiguous() or z.numel() < rows * z.shape[-1]:
+        raise ValueError(f"{name} must be a contiguous fp32 [>= {rows}, ZN] accumulator")
+    z.view(-1, z.shape[-1])[:rows].zero_()
+
+
+def _acc_add(acc: torch.Tensor, a2: torch.Tensor, w: torch.Tensor, b: torch.Tensor) -> None:
+    """acc[:M] += a2 w^T + b in fp32 (the reference's o-projections accumulate into acc)."""
+    _check(w, "wo")
+    _check(b, "bo")
+    M, K = a2.shape
+    N = w.shape[0]
+    if acc.dtype != torch.float32 or not acc.is_contiguous() or acc.numel() < M * N or acc.shape[-1] != N:
+        raise ValueError(f"acc must be a contiguous fp32 [.., >= {M}, {N}] accumulator, got {tuple(acc.shape)}")
+    acc2 = acc.view(-1, N)[:M]
+    if M <= 64 and K % 8 == 0 and _capi.lib().fam_gemm_partial_splits(M, N, K) > 0:
+        part, _ = gemm_partial(a2, w.contiguous())
+    else:
+        part = torch.empty((1, M, N), dtype=torch.float32, device=a2.device)
+        gemm(a2, w.contiguous(), None, part.view(M, N), out_f32=True)
+    rowop(acc2, partials=part, bias=b.contiguous(), res=acc2)
+
+
+def _cae_mask(msk: torch.Tensor, M: int, SK: int, bias_form: bool):
+    """The attention mask operand: the additive 0 / -inf fp32 plane of fastwam::mask_bias when
+    bias_form (read in place, row stride kept), else a keep plane (nonzero = attend)."""
+    if bias_form:
+        return msk[:M, :SK]
+    return _keep_plane(msk, M, SK)
+
+
+def _pow2(n: int) -> int:
+    return 1 << (int(n) - 1).bit_length()
+
+
+@torch.library.custom_op("fastwam::mask_bias", mutates_args=())
+def mask_bias(am: torch.Tensor, cm: torch.Tensor, mp: int, skp: int, ncp: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The CAE expert's two additive attention-bias planes in one launch (CA/mot.py:3342-3369):
+    sb [mp, skp] fp32, 0 where row m < M keeps action key c of am [M, SK] (padding rows keep key 0
+    only), and xb [mp, ncp], 0 where row m < M keeps context key c of cm ([M, NS], or [1, NS] for
+    every row); -inf elsewhere."""
+    if am.dim() != 2 or cm.dim() != 2:
+        raise ValueError("am must be [M, SK] and cm [M or 1, NS]")
+    M, SK = am.shape
+    NS = cm.shape[1]
+    if cm.shape[0] not in (1, M):
+        raise ValueError(f"cm must have 1 or {M} rows, got {tuple(cm.shape)}")
+
+    def u8(t):
+        t = t.contiguous() if t.dtype in (torch.bool, torch.uint8) else (t != 0).contiguous()
+        return t.view(torch.uint8) if t.dtype == torch.bool else t
+    a8, c8 = u8(am), u8(cm)
+    cms = 0 if cm.shape[0] == 1 and M != 1 else NS
+    sb = torch.empty((mp, skp), dtype=torch.float32, device=am.device)
+    xb = torch.empty((mp, ncp), dtype=torch.float32, device=am.device)
+    call("fam_mask_bias", a8.data_ptr(), c8.data_ptr(), cms, M, SK, NS, mp, skp, ncp, sb.data_ptr(), xb.data_ptr(),
+         _stream(sb))
+    return sb, xb
+
+
+@mask_bias.register_fake
+def _(am, cm, mp, skp, ncp):
+    return am.new_empty((mp, skp), dtype=torch.float32), am.new_empty((mp, ncp), dtype=torch.float32)
+
+
+@torch.library.custom_op("fastwam::mot_attn_oproj", mutates_args={"acc"})
+def mot_attn_oproj(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, msk: torch.Tensor, wo: torch.Tensor,
+                   bo: torch.Tensor, acc: torch.Tensor, nh: int, hd: int) -> None:
+    """The self attention of head-major q [1, H, M, hd] over k / v [1, H, SK, hd] with its o
+    projection added into the fp32 accumulator: acc[:M] += attn wo^T + bo (CA/mot.py:2864-2900,
+    kernel :2563-2680).  msk is a keep plane (nonzero = attend) or, as [mp, skp] fp32 with mp =
+    max(16, pow2(M)) and skp = pow2(SK), fastwam::mask_bias's additive plane."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _check(t, n)
+    H, D = int(nh), int(hd)
+    M, SK = q.shape[2], k.shape[2]
+    bias_form = msk.dim() == 2 and msk.dtype == torch.float32 and tuple(msk.shape) == (max(16, _pow2(M)), _pow2(SK))
+    o = torch.empty((1, M, H * D), dtype=q.dtype, device=q.device)
+    _launch_attention(q, _bhsd_strides(q), k, _bhsd_strides(k), v, _bhsd_strides(v), o, _bshd_strides(o, D), 1, H,
+                      M, SK, D, _cae_mask(msk, M, SK, bias_form))
+    _acc_add(acc, o.view(M, H * D), wo, bo)
+
+
+@mot_attn_oproj.register_fake
+def _(q, k, v, msk, wo, bo, acc, nh, hd):
+    return None
+
+
+def _n3q(res, so, mod, tmod, lnw, lnb, qw, qb, eps):
+    """x = res + gate_msa so (chunk 2), n = norm3(x) with its affine, cq = n qw^T + qb; bf16."""
+    for t, n in ((res, "res"), (mod, "mod"), (tmod, "tmod"), (lnw, "lnw"), (lnb, "lnb"), (qw, "qw"), (qb, "qb")):
+        _check(t, n)
+    D = res.shape[-1]
+    M = res.numel() // D
+    r2 = _rows2d(res)
+    x = torch.empty((1, M, D), dtype=_BF16, device=res.device)
+    n = torch.empty((M, D), dtype=_BF16, device=res.device)
+    rowop(x.view(M, D), partials=_plane(so, M, D, "so"), res=r2, gate=_mod_vec(mod, tmod, 2, D),
+          norm=_capi.FAM_ROWNORM_LAYERNORM, eps=eps, ln_w=lnw.contiguous(), ln_b=lnb.contiguous(), nout=n)
+    cq = torch.empty((1, M, qw.shape[0]), dtype=_BF16, device=res.device)
+    gemm(n, qw.contiguous(), qb.contiguous(), cq.view(M, qw.shape[0]))
+    return x, cq
+
+
+def _check_gram(gram: torch.Tensor, D: int) -> None:
+    if gram.numel() != D * D + D + 1:
+        raise ValueError(f"gram must hold [[Wq^T Wq], [Wq^T bq], [|bq|^2]] = {D * D + D + 1} values, "
+                         f"got {gram.numel()}")
+
+
+@torch.library.custom_op("fastwam::mod_n3q", mutates_args=())
+def mod_n3q(res: torch.Tensor, so: torch.Tensor, mod: torch.Tensor, tmod: torch.Tensor, lnw: torch.Tensor,
+            lnb: torch.Tensor, qw: torch.Tensor, qb: torch.Tensor, eps: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(x, cq): x = res + gate_msa so (so the self-attention o-projection, bf16 or its fp32
+    accumulator), cq = LN3(x) lnw + lnb projected by the cross-attention q (CA/mot.py:2978-3008,
+    kernel :2707-2780)."""
+    return _n3q(res, so, mod, tmod, lnw, lnb, qw, qb, eps)
+
+
+@mod_n3q.register_fake
+def _(res, so, mod, tmod, lnw, lnb, qw, qb, eps):
+    d = int(res.shape[-1])
+    m = int(res.shape[-2])
+    return res.new_empty((1, m, d)), res.new_empty((1, m, int(qw.shape[0])))
+
+
+def _n3q_qn(res, so, mod, tmod, lnw, lnb, qw, qb, qnw, gram, eps, eps_q):
+    _check(qnw, "qnw")
+    _check_gram(gram, res.shape[-1])
+    x, cq = _n3q(res, so, mod, tmod, lnw, lnb, qw, qb, eps)
+    M, N = cq.shape[1], cq.shape[2]
+    cqn = torch.empty_like(cq)
+    _rms(cq.view(M, N), cqn.view(M, N), qnw.contiguous(), eps_q)
+    return x, cqn
+
+
+@torch.library.custom_op("fastwam::mod_n3q_qn", mutates_args=())
+def mod_n3q_qn(res: torch.Tensor, so: torch.Tensor, mod: torch.Tensor, tmod: torch.Tensor, lnw: torch.Tensor,
+               lnb: torch.Tensor, qw: torch.Tensor, qb: torch.Tensor, qnw: torch.Tensor, gram: torch.Tensor,
+               eps: float, eps_q: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """mod_n3q with the cross-attention norm_q (RMSNorm over the whole q row, weight qnw) applied
+    to cq (CA/mot.py:3227-3262).  The reference takes the row's sum of squares from the Gram
+    block gram; here the row kernel sums the squares of the row itself (the same quantity; gram
+    is checked for its shape only)."""
+    return _n3q_qn(res, so, mod, tmod, lnw, lnb, qw, qb, qnw, gram, eps, eps_q)
+
+
+@mod_n3q_qn.register_fake
+def _(res, so, mod, tmod, lnw, lnb, qw, qb, qnw, gram, eps, eps_q):
+    d = int(res.shape[-1])
+    m = int(res.shape[-2])
+    return res.new_empty((1, m, d)), res.new_empty((1, m, int(qw.shape[0])))
+
+
+@torch.library.custom_op("fastwam::n3q_xoproj", mutates_args={"acc"})
+def n3q_xoproj(res: torch.Tensor, so: torch.Tensor, mod: torch.Tensor, tmod: torch.Tensor, lnw: torch.Tensor,
+               lnb: torch.Tensor, qw: torch.Tensor, qb: torch.Tensor, qnw: torch.Tensor, gram: torch.Tensor,
+               ck: torch.Tensor, cv: torch.Tensor, msk: torch.Tensor, wo: torch.Tensor, bo: torch.Tensor,
+               acc: torch.Tensor, nh: int, eps: float, eps_q: float) -> torch.Tensor:
+    """mod_n3q_qn, then the cross attention of that query per head over the context keys / values
+    ck / cv [1, NSEQ, NQ] (row stride ck.stride(1), so a layer's slice of a stacked buffer reads
+    in place) and the cross o-projection added into acc: acc[:M] += attn wo^T + bo; returns x
+    (CA/mot.py:3414-3470, kernel :1556-1680).  msk: a [1, M, NSEQ] keep plane, or fastwam::
+    mask_bias's fp32 plane (2-D, at least max(16, pow2(M)) rows and NSEQ columns)."""
+    _check(ck, "ck")
+    _check(cv, "cv")
+    x, cqn = _n3q_qn(res, so, mod, tmod, lnw, lnb, qw, qb, qnw, gram, eps, eps_q)
+    M, NQ = cqn.shape[1], cqn.shape[2]
+    H = int(nh)
+    hd, NSEQ = NQ // H, ck.shape[1]
+    if H * hd != NQ or ck.shape[-1] != NQ or cv.shape[1] != NSEQ or cv.shape[-1] != NQ:
+        raise ValueError(f"ck / cv must be [1, {NSEQ}, {NQ}] for {H} heads")
+    bias_form = msk.dim() == 2 and msk.dtype == torch.float32 and msk.shape[0] >= max(16, _pow2(M)) and \
+        msk.shape[1] >= NSEQ
+    o = torch.empty((1, M, NQ), dtype=_BF16, device=res.device)
+    _launch_attention(cqn, _bshd_strides(cqn, hd), ck, (0, ck.stride(1), hd), cv, (0, cv.stride(1), hd), o,
+                      _bshd_strides(o, hd), 1, H, M, NSEQ, hd, _cae_mask(msk, M, NSEQ, bias_form))
+    _acc_add(acc, o.view(M, NQ), wo, bo)
+    return x
+
+
+@n3q_xoproj.register_fake
+def _(res, so, mod, tmod, lnw, lnb, qw, qb, qnw, gram, ck, cv, msk, wo, bo, acc, nh, eps, eps_q):
+    d = int(res.shape[-1])
+    return res.new_empty((1, int(res.shape[-2]), d))
+
+
+def _ffn_fold(x, oacc, modc, modn, tmod, w1, b1, w2, b2, eps2, eps1, hasnext):
+    for t, n in ((x, "x"), (modc, "modc"), (modn, "modn"), (tmod, "tmod"), (w1, "w1"), (b1, "b1"), (w2, "w2"),
+                 (b2, "b2")):
+        _check(t, n)
+    H = x.shape[-1]
+    M = x.numel() // H
+    x2 = _rows2d(x)
+    v = torch.empty((M, H), dtype=_BF16, device=x.device)
+    a = torch.empty((M, H), dtype=_BF16, device=x.device)
+    rowop(v, partials=_plane(oacc, M, H, "oacc"), res=x2, norm=_capi.FAM_ROWNORM_ADALN, eps=eps2,
+          shift=_mod_vec(modc, tmod, 3, H), scale=_mod_vec(modc, tmod, 4, H), mod_strides=(0, 0), nout=a)
+    hid = torch.empty((M, w1.shape[0]), dtype=_BF16, device=x.device)
+    gemm(a, w1.contiguous(), b1.contiguous(), hid, act=_capi.FAM_ACT_GELU_TANH)
+    f = torch.empty((1, M, H), dtype=torch.float32, device=x.device)
+    gemm(hid, w2.contiguous(), b2.contiguous(), f.view(M, H), out_f32=True)
+    xout = torch.empty((1, M, H), dtype=_BF16, device=x.device)
+    ai = torch.empty((1, M, H), dtype=_BF16, device=x.device)
+    kw = dict(partials=f, res=v, gate=_mod_vec(modc, tmod, 5, H))
+    if hasnext:
+        rowop(xout.view(M, H), norm=_capi.FAM_ROWNORM_ADALN, eps=eps1, shift=_mod_vec(modn, tmod, 0, H),
+              scale=_mod_vec(modn, tmod, 1, H), mod_strides=(0, 0), nout=ai.view(M, H), **kw)
+    else:
+        rowop(xout.view(M, H), **kw)
+    return xout, ai
+
+
+@torch.library.custom_op("fastwam::mot_ffn_fold", mutates_args=())
+def mot_ffn_fold(x: torch.Tensor, oacc: torch.Tensor, modc: torch.Tensor, modn: torch.Tensor, tmod: torch.Tensor,
+                 w1: torch.Tensor, b1: torch.Tensor, w2: torch.Tensor, b2: torch.Tensor, eps2: float, eps1: float,
+                 hasnext: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(xout, aiout): v = x + oacc (the cross o-projection's fp32 accumulator), the FFN on
+    norm2's AdaLN of v (shift / scale chunks 3 / 4 of modc + t_mod), xout = v + gate_mlp (chunk
+    5) ffn; with hasnext, aiout = the next block's AdaLN1 of xout (chunks 0 / 1 of modn + t_mod),
+    else aiout is not written, as in the reference (CA/mot.py:3086-3122, kernel :2346-2430)."""
+    return _ffn_fold(x, oacc, modc, modn, tmod, w1, b1, w2, b2, eps2, eps1, hasnext)
+
+
+@mot_ffn_fold.register_fake
+def _(x, oacc, modc, modn, tmod, w1, b1, w2, b2, eps2, eps1, hasnext):
+    d = int(x.shape[-1])
+    m = int(x.numel()) // d if x.numel() > 0 else int(x.shape[-2])
+    return x.new_empty((1, m, d)), x.new_empty((1, m, d))
+
+
+def _sa_qkv(xin, w, b, qgr, kgr, qw, kw, freqs, kbuf, vbuf, za, zb, sv, eps):
+    for t, n in ((xin, "xin"), (w, "w"), (b, "b")):
+        _check(t, n)
+    K = xin.shape[-1]
+    _check_gram(qgr, K)
+    _check_gram(kgr, K)
+    x2 = _rows2d(xin)
+    M, D3 = x2.shape[0], w.shape[0]
+    D = D3 // 3
+    qkv = torch.empty((M, D3), dtype=_BF16, device=xin.device)
+    gemm(x2, w.contiguous(), b.contiguous(), qkv)
+    _zero_rows(za, M, "za")
+    _zero_rows(zb, M, "zb")
+    return _head_major(_cae_qkv_rows(qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:], qw, kw, freqs, kbuf, vbuf, sv,
+                                     eps), kbuf.shape[1])
+
+
+@torch.library.custom_op("fastwam::mot_sa_qkv", mutates_args={"kbuf", "vbuf", "za", "zb"})
+def mot_sa_qkv(xin: torch.Tensor, w: torch.Tensor, b: torch.Tensor, qgr: torch.Tensor, kgr: torch.Tensor,
+               qw: torch.Tensor, kw: torch.Tensor, freqs: torch.Tensor, kbuf: torch.Tensor, vbuf: torch.Tensor,
+               za: torch.Tensor, zb: torch.Tensor, sv: int, eps: float) -> torch.Tensor:
+    """The fused q / k / v projection of the hidden-K action rows (w [3D, K], b [3D]) and
+    mot_qkv_post's normalisation, rotation and K / V cache writes; rows [0, M) of the fp32
+    accumulators za / zb cleared; q returned head-major (CA/mot.py:3285-3322, kernel
+    :1458-1553).  qgr / kgr are the reference's Gram blocks of the q / k norms (checked for
+    shape; the row kernel sums the row's own squares)."""
+    return _sa_qkv(xin, w, b, qgr, kgr, qw, kw, freqs, kbuf, vbuf, za, zb, sv, eps)
+
+
+@mot_sa_qkv.register_fake
+def _(xin, w, b, qgr, kgr, qw, kw, freqs, kbuf, vbuf, za, zb, sv, eps):
+    return xin.new_empty((1, kbuf.shape[1], xin.numel() // xin.shape[-1], kbuf.shape[3]))
+
+
+@torch.library.custom_op("fastwam::mot_ffn_sa_qkv", mutates_args={"kbuf", "vbuf", "za", "zb"})
+def mot_ffn_sa_qkv(xp: torch.Tensor, oacc: torch.Tensor, modc: torch.Tensor, modn: torch.Tensor, tmod: torch.Tensor,
+                   f1w: torch.Tensor, f1b: torch.Tensor, f2w: torch.Tensor, f2b: torch.Tensor, w: torch.Tensor,
+                   b: torch.Tensor, qgr: torch.Tensor, kgr: torch.Tensor, qw: torch.Tensor, kw: torch.Tensor,
+                   freqs: torch.Tensor, kbuf: torch.Tensor, vbuf: torch.Tensor, za: torch.Tensor, zb: torch.Tensor,
+                   sv: int, eps: float, eps2: float, eps1: float) -> Tuple[torch.Tensor, torch.Tensor]:
+    """mot_ffn_fold of layer L (with the next block's AdaLN1) followed by mot_sa_qkv of layer L + 1
+    on that input: returns (xout, q head-major) (CA/mot.py:3498-3565)."""
+    xout, ai = _ffn_fold(xp, oacc, modc, modn, tmod, f1w, f1b, f2w, f2b, eps2, eps1, 1)
+    return xout, _sa_qkv(ai, w, b, qgr, kgr, qw, kw, freqs, kbuf, vbuf, za, zb, sv, eps)
+
+
+@mot_ffn_sa_qkv.register_fake
+def _(xp, oacc, modc, modn, tmod, f1w, f1b, f2w, f2b, w, b, qgr, kgr, qw, kw, freqs, kbuf, vbuf, za, zb, sv, eps,
+      eps2, eps1):
+    k = int(xp.shape[-1])
+    m = int(xp.numel()) // k
+    return xp.new_empty((1, m, k)), xp.new_empty((1, kbuf.shape[1], m, kbuf.shape[3]))
+
+
+@torch.library.custom_op("fastwam::mot_qkv_post_z", mutates_args={"kbuf", "vbuf", "za", "zb"})
+def mot_qkv_post_z(qkv: torch.Tensor, qw: torch.Tensor, kw: torch.Tensor, freqs: torch.Tensor, kbuf: torch.Tensor,
+                   vbuf: torch.Tensor, za: torch.Tensor, zb: torch.Tensor, sv: int, eps: float) -> torch.Tensor:
+    """mot_qkv_post, and rows [0, M) of the fp32 accumulators za / zb cleared (CA/mot.py:2830-2860)."""
+    _check(qkv, "qkv")
+    M, D3 = qkv.shape[1], qkv.shape[2]
+    D = D3 // 3
+    x2 = qkv.reshape(M, D3)
+    _zero_rows(za, M, "za")
+    _zero_rows(zb, M, "zb")
+    return _head_major(_cae_qkv_rows(x2[:, :D], x2[:, D:2 * D], x2[:, 2 * D:], qw, kw, freqs, kbuf, vbuf, sv, eps),
+                       kbuf.shape[1])
+
+
+@mot_qkv_post_z.register_fake
+def _(qkv, qw, kw, freqs, kbuf, vbuf, za, zb, sv, eps):
+    return qkv.new_empty((1, kbuf.shape[1], qkv.shape[1], kbuf.shape[3]))
+
+
+@torch.library.custom_op("fastwam::mot_qkv_gemm_post_z", mutates_args={"kbuf", "vbuf", "za", "zb"})
+def mot_qkv_gemm_post_z(xin: torch.Tensor, wt: torch.Tensor, bqkv: torch.Tensor, qw: torch.Tensor, kw: torch.Tensor,
+                        freqs: torch.Tensor, kbuf: torch.Tensor, vbuf: torch.Tensor, za: torch.Tensor,
+                        zb: torch.Tensor, sv: int, eps: float) -> torch.Tensor:
+    """mot_qkv_post_z on qkv = xin wt + bqkv, wt the transposed [K, 3D] projection weight
+    (CA/mot.py:3032-3070, kernel :1369-1456 with GK = K)."""
+    _check(xin, "xin")
+    _check(wt, "wt")
+    _check(bqkv, "bqkv")
+    x2 = _rows2d(xin)
+    M, D3 = x2.shape[0], wt.shape[1]
+    D = D3 // 3
+    qkv = torch.empty((M, D3), dtype=_BF16, device=xin.device)
+    gemm(x2, wt.t().contiguous(), bqkv.contiguous(), qkv)
+    _zero_rows(za, M, "za")
+    _zero_rows(zb, M, "zb")
+    return _head_major(_cae_qkv_rows(qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:], qw, kw, freqs, kbuf, vbuf, sv,
+                                     eps), kbuf.shape[1])
+
+
+@mot_qkv_gemm_post_z.register_fake
+def _(xin, wt, bqkv, qw, kw, freqs, kbuf, vbuf, za, zb, sv, eps):
+    return xin.new_empty((1, kbuf.shape[1], xin.shape[-2], kbuf.shape[3]))
+
+
+def _l0_qkv(q, k, v, qw, kw, freqs, kbuf, vbuf, sv, eps):
+    _check(q, "q")
+    M, D = q.shape[1], q.shape[2]
+    qout = torch.empty_like(q, memory_format=torch.contiguous_format)
+    _cae_qkv_rows(q.reshape(M, D), k.reshape(M, D), v.reshape(M, D), qw, kw, freqs, kbuf, vbuf, sv, eps,
+                  q_out=qout.view(M, D))
+    return qout
+
+
+@torch.library.custom_op("fastwam::mot_l0_qkv_rope", mutates_args={"kbuf", "vbuf"})
+def mot_l0_qkv_rope(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qw: torch.Tensor, kw: torch.Tensor,
+                    freqs: torch.Tensor, kbuf: torch.Tensor, vbuf: torch.Tensor, sv: int, eps: float) -> torch.Tensor:
+    """Layer 0's q / k / v post-processing from separate [1, M, D] projections: the q rows
+    normalised and rotated, token-major like q; k / v to rows sv .. sv + M of the head-major
+    caches (CA/mot.py:3142-3172, kernel :2430-2480)."""
+    return _l0_qkv(q, k, v, qw, kw, freqs, kbuf, vbuf, sv, eps)
+
+
+@mot_l0_qkv_rope.register_fake
+def _(q, k, v, qw, kw, freqs, kbuf, vbuf, sv, eps):
+    return torch.empty_like(q)
+
+
+@torch.library.custom_op("fastwam::mot_l0_qkv_rope_z", mutates_args={"kbuf", "vbuf", "oaccx"})
+def mot_l0_qkv_rope_z(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, qw: torch.Tensor, kw: torch.Tensor,
+                      freqs: torch.Tensor, kbuf: torch.Tensor, vbuf: torch.Tensor, oaccx: torch.Tensor, sv: int,
+                      eps: float) -> torch.Tensor:
+    """mot_l0_qkv_rope, and rows [0, M) of layer 0's cross o-projection accumulator oaccx [M, NO]
+    cleared (CA/mot.py:3180-3210)."""
+    qout = _l0_qkv(q, k, v, qw, kw, freqs, kbuf, vbuf, sv, eps)
+    _zero_rows(oaccx, q.shape[1], "oaccx")
+    return qout
+
+
+@mot_l0_qkv_rope_z.register_fake
+def _(q, k, v, qw, kw, freqs, kbuf, vbuf, oaccx, sv, eps):
+    return torch.empty_like(q)
+
+
+def _ctx_kv_into(g: torch.Tensor, nkw: torch.Tensor, out: torch.Tensor, nl: int, ahd: int, eps: float) -> None:
+    """out [2, nl, 1, S, ahd]: [0] the normalised keys of every layer, [1] the values."""
+    S = g.shape[0]
+    if out.shape != (2, nl, 1, S, ahd) or out.dtype != _BF16 or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous bf16 [2, {nl}, 1, {S}, {ahd}] tensor, got {tuple(out.shape)}")
+    out[0].copy_(ctx_kv_norm(g, nkw, nl, ahd, eps)[0])
+    out[1].copy_(g[:, nl * ahd:].reshape(S, nl, ahd).transpose(0, 1).unsqueeze(1))
+
+
+@torch.library.custom_op("fastwam::ctx_kv_norm_into", mutates_args=("out",))
+def ctx_kv_norm_into(g: torch.Tensor, nkw: torch.Tensor, out: torch.Tensor, nl: int, ahd: int, eps: float) -> None:
+    """ctx_kv_norm with the values too, into out [2, nl, 1, S, ahd]: [0] the RMS-normalised keys,
+    [1] the values, layer-major (CA/mot.py:3621-3638)."""
+    _ctx_kv_into(g, nkw, out, int(nl), int(ahd), eps)
+
+
+@ctx_kv_norm_into.register_fake
+def _(g, nkw, out, nl, ahd, eps):
+    return None
+
+
+@torch.library.custom_op("fastwam::ctx_kv_gemm_norm_into", mutates_args=("out",))
+def ctx_kv_gemm_norm_into(e: torch.Tensor, w: torch.Tensor, b: torch.Tensor, nkw: torch.Tensor, out: torch.Tensor,
+                          nl: int, ahd: int, eps: float, has_b: bool) -> None:
+    """ctx_kv_norm_into on g = e w^T (+ b with has_b): the whole stack's context K / V projection
+    (w [2 nl ahd, C], keys of every layer before the values) and its key norm
+    (CA/mot.py:3641-3662, kernel :2166-2210)."""
+    _check(e, "e")
+    _check(w, "w")
+    S, nl, ahd = e.shape[0], int(nl), int(ahd)
+    if w.shape[0] != 2 * nl * ahd:
+        raise ValueError(f"w must have {2 * nl * ahd} rows, got {tuple(w.shape)}")
+    g = torch.empty((S, w.shape[0]), dtype=_BF16, device=e.device)
+    gemm(_rows2d(e), w.contiguous(), b.contiguous() if has_b else None, g)
+    _ctx_kv_into(g, nkw, out, nl, ahd, eps)
+
+
+@ctx_kv_gemm_norm_into.register_fake
+def _(e, w, b, nkw, out, nl, ahd, eps, has_b):
+    return None
+
+
+@torch.library.custom_op("fastwam::vqkv_post", mutates_args={"kbuf", "vbuf"})
+def vqkv_post(qkv: torch.Tensor, qw: torch.Tensor, kw: torch.Tensor, freqs: torch.Tensor, kbuf: torch.Tensor,
+              vbuf: torch.Tensor, eps: float) -> torch.Tensor:
+    """The video prefill's q / k / v post-processing: returns [3, 1, M, D] (q, k normalised and
+    rotated, v as is, token-major) and writes k / v head-major to rows [0, M) of kbuf / vbuf
+    [1, H, SKV, hd], clearing rows [M, SKV) (CA/mot.py:3713-3750, kernel :2015-2077)."""
+    _check(qkv, "qkv")
+    M, D3 = qkv.shape[1], qkv.shape[2]
+    D = D3 // 3
+    x2 = qkv.reshape(M, D3)
+    out = torch.empty((3, 1, M, D), dtype=qkv.dtype, device=qkv.device)
+    _cae_qkv_rows(x2[:, :D], x2[:, D:2 * D], x2[:, 2 * D:], qw, kw, freqs, kbuf, vbuf, 0, eps,
+                  q_out=out[0, 0])
+    H, hd = kbuf.shape[1], kbuf.shape[3]
+    out[1, 0].view(M, H, hd).copy_(kbuf[0, :, :M].transpose(0, 1))
+    out[2, 0].copy_(x2[:, 2 * D:])
+    kbuf[0, :, M:].zero_()
+    vbuf[0, :, M:].zero_()
+    return out
+
+
+@vqkv_post.register_fake
+def _(qkv, qw, kw, freqs, kbuf, vbuf, eps):
+    d = int(kbuf.shape[1]) * int(kbuf.shape[3])
+    return qkv.new_empty((3, 1, int(qkv.shape[1]), d))
+
+
+# --------------------------------------------------------------------------- fp8 rows (CA video prefill)
+_FP8 = torch.float8_e4m3fn
+
+
+def _row_q8(mode: int, x: torch.Tensor, x2: Optional[torch.Tensor] = None, shift=None, scale=None, eps: float = 0.0):
+    _check(x, "x")
+    D = x.shape[-1]
+    xc = x.contiguous()
+    M = xc.numel() // D
+    y = torch.empty((M, D), dtype=_FP8, device=x.device)
+    s = torch.empty((M, 1), dtype=torch.float32, device=x.device)
+    d = _capi.RowQ8Desc()
+    d.mode, d.x, d.ldx, d.M, d.D = mode, xc.data_ptr(), D, M, D
+    d.y, d.ldy, d.s = y.data_ptr(), D, s.data_ptr()
+    keep = [xc]
+    if shift is not None:
+        sh, sc = shift.reshape(-1).contiguous(), scale.reshape(-1).contiguous()
+        for t, n in ((sh, "shift"), (sc, "scale")):
+            _check(t, n)
+            if t.numel() != D:
+                raise ValueError(f"{n} must hold {D} values, got {t.numel()}")
+        d.shift, d.scale, d.eps = sh.data_ptr(), sc.data_ptr(), float(eps)
+        keep += [sh, sc]
+    xo = None
+    if x2 is not None:
+        _check(x2, "b")
+        if x2.shape != x.shape:
+            raise ValueError(f"a and b must have one shape, got {tuple(x.shape)} and {tuple(x2.shape)}")
+        b2 = x2.contiguous()
+        xo = torch.empty_like(xc)
+        d.x2, d.ldx2, d.xo, d.ldxo = b2.data_ptr(), D, xo.data_ptr(), D
+        keep += [b2]
+    call("fam_row_q8", C.byref(d), _stream(x))
+    del keep
+    return xo, y, s
+
+
+@torch.library.custom_op("fastwam::row_q8", mutates_args=())
+def row_q8(x: torch.Tensor) -> List[torch.Tensor]:
+    """[q, s]: the rows of x [.., D] quantised to fp8 e4m3 with a per-row scale s [M, 1]
+    (q s = x to e4m3's precision; CA/mot.py:3936-3960, kernel :3836-3849)."""
+    _, y, s = _row_q8(_capi.FAM_Q8_ROW, x)
+    return [y, s]
+
+
+@row_q8.register_fake
+def _(x):
+    d = int(x.shape[-1])
+    m = x.numel() // d
+    return [x.new_empty((m, d), dtype=_FP8), x.new_empty((m, 1), dtype=torch.float32)]
+
+
+@torch.library.custom_op("fastwam::gelu_q8", mutates_args=())
+def gelu_q8(x: torch.Tensor) -> List[torch.Tensor]:
+    """[q, s] of bf16(GELU_tanh(x)), the activation between the video FFN's two fp8 GEMMs
+    (CA/mot.py:3914-3934, kernel :3817-3833)."""
+    _, y, s = _row_q8(_capi.FAM_Q8_GELU, x)
+    return [y, s]
+
+
+@gelu_q8.register_fake
+def _(x):
+    d = int(x.shape[-1])
+    m = x.numel() // d
+    return [x.new_empty((m, d), dtype=_FP8), x.new_empty((m, 1), dtype=torch.float32)]
+
+
+@torch.library.custom_op("fastwam::ln_mod_q8", mutates_args=())
+def ln_mod_q8(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, eps: float) -> List[torch.Tensor]:
+    """[q, s] of bf16(bf16(LN(x)) (1 + scale) + shift), shift / scale [D] for every row
+    (CA/mot.py:3859-3883, kernel :3763-3787)."""
+    _, y, s = _row_q8(_capi.FAM_Q8_LN_MOD, x, shift=shift, scale=scale, eps=eps)
+    return [y, s]
+
+
+@ln_mod_q8.register_fake
+def _(x, shift, scale, eps):
+    d = int(x.shape[-1])
+    m = x.numel() // d
+    return [x.new_empty((m, d), dtype=_FP8), x.new_empty((m, 1), dtype=torch.float32)]
+
+
+@torch.library.custom_op("fastwam::add_ln_mod_q8", mutates_args=())
+def add_ln_mod_q8(a: torch.Tensor, b: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
+                  eps: float) -> List[torch.Tensor]:
+    """[xo, q, s]: xo = bf16(a + b) (the cross-attention residual), then ln_mod_q8 of xo
+    (CA/mot.py:3885-3912, kernel :3789-3814)."""
+    xo, y, s = _row_q8(_capi.FAM_Q8_ADD_LN_MOD, a, x2=b, shift=shift, scale=scale, eps=eps)
+    return [xo.view(a.shape), y, s]
+
+
+@add_ln_mod_q8.register_fake
+def _(a, b, shift, scale, eps):
+    d = int(a.shape[-1])
+    m = a.numel() // d
+    return [torch.empty_like(a), a.new_empty((m, d), dtype=_FP8), a.new_empty((m, 1), dtype=torch.float32)]

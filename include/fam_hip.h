@@ -692,6 +692,49 @@ int fam_tiny_key_splits(const fam_tiny_desc* d);
  */
 int fam_tiny_context(const fam_tiny_desc* d, void* stream);
 
+/* Modes of fam_row_q8. */
+#define FAM_Q8_ROW 0         /* y = x                                              */
+#define FAM_Q8_GELU 1        /* y = bf16(GELU_tanh(x)), in the sigmoid form         */
+#define FAM_Q8_LN_MOD 2      /* y = bf16(bf16(LN(x)) * (1 + scale) + shift)         */
+#define FAM_Q8_ADD_LN_MOD 3  /* xo = bf16(x + x2); y = LN_MOD of xo                 */
+
+/*
+ * fam_row_q8 -- per-row fp8 quantisation of a row operation, one workgroup per row m < M:
+ *   y as the mode says (LN: biased variance, fp32 statistics, (x - mean) / sqrt(var + eps));
+ *   a = max |y| over the row;  s[m] = max(a, 1e-12) / 448;
+ *   q[m, :] = fp8_e4m3(y * (448 / max(a, 1e-12)))   (OCP e4m3, round to nearest even).
+ * x / x2 / xo bf16 [M, D] rows (16-byte aligned, strides multiples of 8), shift / scale bf16 [D]
+ * broadcast over the rows, q 1-byte codes [M, D] (8-byte aligned rows), s fp32 [M].
+ * Limits: 8 <= D <= 16384, D a multiple of 8.
+ * Replaces: fastwam::row_q8, gelu_q8, ln_mod_q8, add_ln_mod_q8 (CA/mot.py:3763-3980), the
+ *           activation side of the video prefill's fp8 GEMMs.
+ */
+typedef struct fam_rowq8_desc {
+  int mode;
+  const void* x; int64_t ldx;
+  const void* x2; int64_t ldx2;
+  const void* shift; const void* scale;
+  float eps;
+  void* y; int64_t ldy;
+  float* s;
+  void* xo; int64_t ldxo;
+  int64_t M, D;
+} fam_rowq8_desc;
+
+int fam_row_q8(const fam_rowq8_desc* d, void* stream);
+
+/*
+ * fam_mask_bias -- additive attention-bias planes of the CAE action expert's masks:
+ *   sb [MP, SKP] fp32: 0 where row m < M keeps key c (c < SK and am[m * SK + c] != 0), and for
+ *      rows m >= M at key 0 only; -inf elsewhere;
+ *   xb [MP, NCP] fp32 (skipped when NULL): 0 where m < M, c < NS and cm[m * cm_row_stride + c]
+ *      != 0 (stride 0: one row for every m); -inf elsewhere.
+ * am / cm are 1-byte masks (bool).  One launch for both planes.
+ * Replaces: fastwam::mask_bias (CA/mot.py:3342-3369, kernel :2525-2560).
+ */
+int fam_mask_bias(const uint8_t* am, const uint8_t* cm, int64_t cm_row_stride, int64_t M, int64_t SK, int64_t NS,
+                  int64_t MP, int64_t SKP, int64_t NCP, float* sb, float* xb, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

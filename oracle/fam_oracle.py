@@ -42,6 +42,11 @@ Pinning (what checks each function, see ``tests/test_oracle.py``):
                             K-chunk planes of a product sum to the whole product (a matmul
                             closed form), sk-plane truncation, one bf16 rounding; qcomb against
                             unit RMS before the weight, with planted slips
+  cae_mod_n3q / cae_attn_oproj / cae_n3q_xoproj / cae_ffn_fold / cae_mask_bias / vfp8_*
+                            zero / unit gates (closed forms), F.layer_norm, the Gram identity of
+                            the whole-row query norm, F.scaled_dot_product_attention + F.linear,
+                            adaln / cae_ffn, softmax of the bias planes against the keep mask,
+                            fp8 dequantisation within e4m3's step (tests/test_oracle.py)
 """
 from __future__ import annotations
 
@@ -1248,6 +1253,122 @@ def cae_adit_tmod(t: torch.Tensor, w0, b0, w1, b1, w2, b2, atok: torch.Tensor, a
     te = sinusoidal_embedding_1d(w0.shape[1], t.reshape(1))
     tt = linear(silu(linear(te, w0, b0)), w1, b1)
     return tt, linear(silu(tt), w2, b2), linear(atok, aw, ab)
+
+
+def _rbf(x: torch.Tensor) -> torch.Tensor:
+    return x.float().to(torch.bfloat16).float()
+
+
+def _mod_chunk(mod: torch.Tensor, tmod: torch.Tensor, i: int, n: int) -> torch.Tensor:
+    """Chunk i (width n) of modulation + t_mod, one row shared by every token, fp32 sum."""
+    return mod.reshape(-1)[i * n:(i + 1) * n].float() + tmod.reshape(-1)[i * n:(i + 1) * n].float()
+
+
+def cae_mod_n3q(res: torch.Tensor, so: torch.Tensor, mod: torch.Tensor, tmod: torch.Tensor, lnw, lnb, qw, qb,
+                eps: float, qn: Optional[Tuple[torch.Tensor, float]] = None):
+    """_fwam_mod_n3q_kernel (CA/mot.py:2707-2780): the self-attention residual with gate_msa
+    (chunk 2, rounded to bf16), norm3 (affine LayerNorm) and the cross-attention q projection:
+        x = bf16(res + bf16(g bf16(so))),  n = bf16(LN(x) lnw + lnb),  cq = n qw^T + qb;
+    with qn = (qnw, eps_q) the query's RMSNorm over the whole row of cq, its sum of squares taken
+    on the unrounded product: cq = bf16(cq) rsqrt(mean(cq^2) + eps_q) qnw.  Returns (x, cq) fp32."""
+    D = res.shape[-1]
+    g = _rbf(_mod_chunk(mod, tmod, 2, D))
+    x = _rbf(res.float() + _rbf(g * _rbf(so)))
+    n = _rbf(layer_norm(x, None, None, eps) * lnw.float() + lnb.float())
+    cq = linear(n, qw.float(), qb.float())
+    if qn is not None:
+        cq = _rbf(cq) * torch.rsqrt((cq * cq).mean(-1, keepdim=True) + qn[1]) * qn[0].float()
+    return x, cq
+
+
+def cae_attn_oproj(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, keep: torch.Tensor, wo, bo) -> torch.Tensor:
+    """_fwam_attn_oproj_kernel (CA/mot.py:2563-2680): per head h, o_h = softmax(q_h k_h^T / sqrt(hd),
+    keep) v_h rounded to bf16, contracted with head h's columns of wo; the sum over heads plus bo
+    is what the kernel adds into its fp32 accumulator.  q [H, M, hd], k / v [H, SK, hd] (head-major),
+    keep [M, SK]; returns [M, NO] fp32."""
+    H, M, hd = q.shape
+
+    def rows(t):
+        return t.transpose(0, 1).reshape(1, t.shape[1], H * hd).float()
+    o = flash_attention(rows(q), rows(k), rows(v), H, keep[None, None])[0]
+    return linear(_rbf(o), wo.float(), bo.float())
+
+
+def cae_n3q_xoproj(res, so, mod, tmod, lnw, lnb, qw, qb, qnw, ck, cv, keep, wo, bo, nh: int, eps: float,
+                   eps_q: float):
+    """_fwam_n3q_xoproj_kernel (CA/mot.py:1556-1680): cae_mod_n3q with the whole-row query norm, the
+    cross attention of that query (rounded to bf16) per head over ck / cv [NSEQ, NQ] rows with keep
+    [M, NSEQ], and the cross o-projection.  Returns (x, the [M, NO] fp32 accumulator term)."""
+    x, cq = cae_mod_n3q(res, so, mod, tmod, lnw, lnb, qw, qb, eps, qn=(qnw, eps_q))
+    o = flash_attention(_rbf(cq)[None], ck[None].float(), cv[None].float(), nh, keep[None, None])[0]
+    return x, linear(_rbf(o), wo.float(), bo.float())
+
+
+def cae_ffn_fold(x: torch.Tensor, oacc: torch.Tensor, modc, modn, tmod, w1, b1, w2, b2, eps2: float, eps1: float):
+    """_fwam_ffn_fold_kernel (CA/mot.py:2346-2430): v = x + oacc (the cross o-projection's fp32
+    accumulator), norm2 AdaLN with (shift, scale) = chunks (3, 4) of modc + t_mod, the FFN on that
+    (GELU(tanh) of the bf16 pre-activation), xn = v + gate_mlp (chunk 5) bf16(ffn); then the next
+    block's AdaLN1 of xn with (shift, scale) = chunks (0, 1) of modn + t_mod.  Returns (xn, next
+    AdaLN1 input) fp32."""
+    H = x.shape[-1]
+    v = x.float() + oacc.float()
+    a = _rbf(adaln(v, _mod_chunk(modc, tmod, 3, H), _mod_chunk(modc, tmod, 4, H), eps2))
+    h = _rbf(gelu_tanh(_rbf(linear(a, w1.float(), b1.float()))))
+    xn = v + _mod_chunk(modc, tmod, 5, H) * _rbf(linear(h, w2.float(), b2.float()))
+    return xn, adaln(xn, _mod_chunk(modn, tmod, 0, H), _mod_chunk(modn, tmod, 1, H), eps1)
+
+
+def cae_mask_bias(am: torch.Tensor, cm: torch.Tensor, mp: int, skp: int, ncp: int):
+    """_fwam_mbias_kernel (CA/mot.py:2525-2560): additive planes sb [mp, skp] (0 where row m < M
+    keeps key c of am [M, SK]; padding rows keep key 0 only) and xb [mp, ncp] (0 where row m < M
+    keeps context key c of cm [M or 1, NS]; padding rows none); -inf elsewhere."""
+    M, SK = am.shape
+    NS = cm.shape[-1]
+    keep = torch.zeros(mp, skp, dtype=torch.bool)
+    keep[:M, :SK] = am != 0
+    keep[M:, 0] = True
+    keep2 = torch.zeros(mp, ncp, dtype=torch.bool)
+    keep2[:M, :NS] = torch.broadcast_to(cm != 0, (M, NS))
+    ninf = torch.tensor(float("-inf"))
+    return torch.where(keep, 0.0, ninf), torch.where(keep2, 0.0, ninf)
+
+
+def vfp8_quantize_rows(y: torch.Tensor):
+    """The per-row fp8 quantisation of CA/mot.py:3763-3850: a = max |y| per row, s = max(a, 1e-12)
+    (1 / 448), q = e4m3(y (448 / max(a, 1e-12))); returns (q as float8_e4m3fn [M, D], s [M, 1])."""
+    y = y.float()
+    a = y.abs().amax(-1, keepdim=True).clamp_min(1e-12)
+    s = a * (1.0 / 448.0)
+    # a correctly rounded fp32 quotient, as the kernel's `AMAX / max(a, 1e-12)` (torch's
+    # `448.0 / a` would take reciprocal(a) * 448, which rounds twice)
+    mul = torch.div(torch.full_like(a, 448.0), a)
+    q = (y * mul).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q, s
+
+
+def vfp8_row_q8(x: torch.Tensor):
+    """_fwam_rowq8_kernel (CA/mot.py:3836-3849): the row as it is."""
+    return vfp8_quantize_rows(x.reshape(-1, x.shape[-1]))
+
+
+def vfp8_gelu_q8(x: torch.Tensor):
+    """_fwam_geluq8_kernel (CA/mot.py:3817-3833): bf16(GELU_tanh(x)), quantised."""
+    return vfp8_quantize_rows(_rbf(gelu_tanh(x.reshape(-1, x.shape[-1]).float())))
+
+
+def vfp8_ln_mod_q8(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, eps: float):
+    """_fwam_lnmodq8_kernel (CA/mot.py:3763-3787): bf16(bf16(LN(x)) (1 + scale) + shift), quantised."""
+    x2 = x.reshape(-1, x.shape[-1]).float()
+    n = _rbf(layer_norm(x2, None, None, eps))
+    return vfp8_quantize_rows(_rbf(n * (1 + scale.reshape(-1).float()) + shift.reshape(-1).float()))
+
+
+def vfp8_add_ln_mod_q8(a: torch.Tensor, b: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, eps: float):
+    """_fwam_addlnmodq8_kernel (CA/mot.py:3789-3814): xo = bf16(a + b), then vfp8_ln_mod_q8 of xo;
+    returns (xo, q, s)."""
+    xo = _rbf(a.float() + b.float())
+    q, s = vfp8_ln_mod_q8(xo, shift, scale, eps)
+    return xo, q, s
 
 
 # ---------------------------------------------------------------------------

@@ -60,7 +60,7 @@ def _c_offsets(struct: str, fields):
 
 @pytest.mark.parametrize("cls,cname", [(_capi.AttnDesc, "fam_attn_desc"), (_capi.GemmDesc, "fam_gemm_desc"),
                                        (_capi.RowopDesc, "fam_rowop_desc"), (_capi.CaeDesc, "fam_cae_desc"),
-                                       (_capi.TinyDesc, "fam_tiny_desc")])
+                                       (_capi.TinyDesc, "fam_tiny_desc"), (_capi.RowQ8Desc, "fam_rowq8_desc")])
 def test_struct_layout_matches_header(cls, cname):
     fields = [f for f, _ in cls._fields_]
     size, offs = _c_offsets(cname, fields)
@@ -258,6 +258,33 @@ def test_validation_rejects_before_launch(lib):
     assert lib.fam_euler_step(16, 32, None, 48, 10, 10, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_sinusoid(16, 32, 4, 7, None) == _capi.FAM_ERR_INVALID_ARG
     assert lib.fam_add_modulation(16, 32, 48, 2, 3, 12, None) == _capi.FAM_ERR_INVALID_ARG
+
+
+def test_row_q8_and_mask_bias_validation(lib):
+    """fam_row_q8 / fam_mask_bias refuse what their kernels do not take, before any launch."""
+    q = _capi.RowQ8Desc()
+    q.mode, q.x, q.ldx, q.y, q.ldy, q.s, q.M, q.D = _capi.FAM_Q8_ROW, 16, 64, 32, 64, 48, 4, 60
+    assert lib.fam_row_q8(C.byref(q), None) == _capi.FAM_ERR_UNSUPPORTED          # D % 8 != 0
+    q.D, q.ldx, q.ldy = 16392, 16392, 16392
+    assert lib.fam_row_q8(C.byref(q), None) == _capi.FAM_ERR_UNSUPPORTED          # D past 16384
+    assert "16384" in _err(lib)
+    q.D, q.ldx, q.ldy = 64, 64, 64
+    q.mode = 7
+    assert lib.fam_row_q8(C.byref(q), None) == _capi.FAM_ERR_INVALID_ARG
+    q.mode = _capi.FAM_Q8_LN_MOD                                                  # no shift / scale
+    assert lib.fam_row_q8(C.byref(q), None) == _capi.FAM_ERR_INVALID_ARG
+    q.shift, q.scale, q.eps = 64, 80, 1e-6
+    q.x = 24                                                                      # x not 16-byte aligned
+    assert lib.fam_row_q8(C.byref(q), None) == _capi.FAM_ERR_INVALID_ARG
+    q.x, q.mode = 16, _capi.FAM_Q8_ADD_LN_MOD                                      # no x2 / xo
+    assert lib.fam_row_q8(C.byref(q), None) == _capi.FAM_ERR_INVALID_ARG
+    q.M = 0
+    q.x2, q.ldx2, q.xo, q.ldxo = 96, 64, 112, 64
+    assert lib.fam_row_q8(C.byref(q), None) == _capi.FAM_OK                       # no rows: nothing to do
+    assert lib.fam_mask_bias(16, None, 0, 8, 106, 0, 16, 128, 0, None, None, None) == _capi.FAM_ERR_INVALID_ARG  # sb
+    assert lib.fam_mask_bias(16, None, 0, 8, 106, 0, 4, 128, 0, 32, None, None) == _capi.FAM_ERR_INVALID_ARG   # MP < M
+    assert lib.fam_mask_bias(16, 48, 30, 8, 106, 129, 16, 128, 256, 32, 64, None) == _capi.FAM_ERR_INVALID_ARG  # row stride < NS
+    assert lib.fam_mask_bias(16, 48, 0, 8, 106, 129, 16, 128, 100, 32, 64, None) == _capi.FAM_ERR_INVALID_ARG  # NCP < NS
 
 
 def test_missing_library_fails_loudly(tmp_path):

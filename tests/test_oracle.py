@@ -1015,3 +1015,87 @@ def test_geak_split_combine_and_qcomb_pinned():
     assert torch.allclose(unit.pow(2).mean(-1), torch.ones(M), atol=1e-4)
     assert torch.allclose(unit * y.pow(2).mean(-1, keepdim=True).add(eps).sqrt(), y, rtol=1e-4, atol=1e-4)
     assert (O.rms_norm(y.to(torch.bfloat16), wq, eps).float() - q).abs().max() > 0  # eager order rounds first
+
+
+def test_cae_fused_operator_restatements_pinned():
+    """The CAE tree's fused operators in the oracle against library routines and closed forms:
+    mod_n3q's gate is chunk 2 (a zero gate leaves the residual, a unit gate adds so), its norm is
+    F.layer_norm with the affine, the whole-row query norm leaves unit RMS and its sum of squares
+    equals the Gram form the reference reads; attn_oproj per head through
+    F.scaled_dot_product_attention and F.linear; ffn_fold's gate is chunk 5 (zero gate: xn = x +
+    oacc) and its next-block input is adaln of xn; mask_bias's planes reproduce the keep mask under
+    a softmax; the fp8 rows dequantise to within e4m3's step and put the row's largest entry at 448."""
+    g = torch.Generator().manual_seed(79)
+    r = lambda *s: torch.randn(*s, generator=g)  # noqa: E731
+    bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+    M, D, N, eps = 5, 32, 48, 1e-6
+    res, so, lnw, lnb, qw, qb, qnw = bf(r(M, D)), bf(r(M, D)), bf(1 + 0.2 * r(D)), bf(0.2 * r(D)), bf(r(N, D) / 6), \
+        bf(0.1 * r(N)), bf(1 + 0.2 * r(N))
+    mod, tmod = bf(r(6 * D)), bf(r(6 * D))
+    z = mod.clone()
+    z[2 * D:3 * D] = 0
+    x0, _ = O.cae_mod_n3q(res, so, z, torch.zeros(6 * D), lnw, lnb, qw, qb, eps)
+    assert torch.equal(x0, res)
+    z[2 * D:3 * D] = 1
+    x1, cq1 = O.cae_mod_n3q(res, so, z, torch.zeros(6 * D), lnw, lnb, qw, qb, eps)
+    assert torch.equal(x1, bf(res + so))
+    assert torch.allclose(cq1, F.linear(F.layer_norm(x1, (D,), lnw, lnb, eps), qw, qb), atol=0.05, rtol=0.02)
+    assert (O.cae_mod_n3q(res, so, mod, tmod, lnw, lnb, qw, qb, eps)[0] - x1).abs().max() > 0.1
+    n = bf(F.layer_norm(x1, (D,), lnw, lnb, eps))
+    raw = F.linear(n, qw, qb)
+    gram_ss = ((n @ (qw.T @ qw)) * n).sum(-1) + 2 * (n * (qw.T @ qb)).sum(-1) + (qb * qb).sum()
+    assert torch.allclose(gram_ss, (raw * raw).sum(-1), rtol=1e-4)
+    _, cqn = O.cae_mod_n3q(res, so, z, torch.zeros(6 * D), lnw, lnb, qw, qb, eps, qn=(qnw, eps))
+    assert torch.allclose((cqn / qnw).pow(2).mean(-1), torch.ones(M), atol=2e-2)
+    # attention + o-projection, head-major operands
+    H, hd, SK = 3, 16, 7
+    q, k, v = r(H, M, hd), r(H, SK, hd), r(H, SK, hd)
+    keep = torch.rand(M, SK, generator=g) > 0.3
+    keep[:, 0] = True
+    wo, bo = r(20, H * hd) / 7, r(20)
+    ref = F.scaled_dot_product_attention(q, k, v, attn_mask=keep[None]).transpose(0, 1).reshape(M, H * hd)
+    assert torch.allclose(O.cae_attn_oproj(q, k, v, keep, wo, bo), F.linear(bf(ref), wo, bo), atol=1e-4)
+    assert (O.cae_attn_oproj(q, k.transpose(1, 2).reshape(H, SK, hd), v, keep, wo, bo)
+            - F.linear(bf(ref), wo, bo)).abs().max() > 1e-2
+    # FFN fold
+    x, oacc = bf(r(M, D)), r(M, D)
+    w1, b1, w2, b2 = bf(r(64, D) / 6), bf(0.1 * r(64)), bf(r(D, 64) / 8), bf(0.1 * r(D))
+    modc, modn = mod.clone(), bf(r(6 * D))
+    modc[5 * D:] = 0
+    t0 = tmod.clone()
+    t0[5 * D:] = 0
+    xn, nxt = O.cae_ffn_fold(x, oacc, modc, modn, t0, w1, b1, w2, b2, eps, eps)
+    assert torch.equal(xn, x + oacc)
+    assert torch.allclose(nxt, O.adaln(xn, modn[:D] + t0[:D], modn[D:2 * D] + t0[D:2 * D], eps), atol=1e-6)
+    xf, _ = O.cae_ffn_fold(x, oacc, mod, modn, tmod, w1, b1, w2, b2, eps, eps)
+    a = O.adaln(x + oacc, mod[3 * D:4 * D] + tmod[3 * D:4 * D], mod[4 * D:5 * D] + tmod[4 * D:5 * D], eps)
+    assert torch.allclose(xf, x + oacc + (mod[5 * D:] + tmod[5 * D:]) * O.cae_ffn(a, w1, b1, w2, b2),
+                          atol=0.05, rtol=0.02)
+    # mask bias planes
+    am = torch.rand(M, SK, generator=g) > 0.4
+    am[:, 1] = True
+    cm = torch.rand(1, 9, generator=g) > 0.5
+    cm[0, 0] = True
+    sb, xb = O.cae_mask_bias(am, cm, 8, 16, 12)
+    assert sb.shape == (8, 16) and xb.shape == (8, 12)
+    p = torch.softmax(r(8, 16) + sb, -1)
+    assert torch.equal(p[:M, :SK] > 0, am) and (p[:M, SK:] == 0).all() and torch.equal(p[M:, 0], torch.ones(3))
+    assert torch.equal(xb[:M, :9] == 0, cm.expand(M, 9)) and torch.isinf(xb[M:]).all() and torch.isinf(xb[:, 9:]).all()
+    # fp8 rows
+    y = r(6, 64) * torch.logspace(-3, 2, 6)[:, None]
+    qy, s = O.vfp8_row_q8(y)
+    deq = qy.float() * s
+    assert torch.equal(qy.float().abs().amax(-1), torch.full((6,), 448.0))
+    mul = (448.0 / y.abs().amax(-1, keepdim=True).double()).float()   # the correctly rounded fp32 quotient
+    assert torch.equal(qy.float(), (y * mul).to(torch.float8_e4m3fn).float())
+    assert ((deq - y).abs() <= (y.abs() * 2 ** -4 + s * 2 ** -9) * 1.0001).all()
+    assert torch.equal(O.vfp8_gelu_q8(y)[0].float(), O.vfp8_quantize_rows(bf(O.gelu_tanh(y)))[0].float())
+    sh, sc = bf(0.3 * r(64)), bf(0.3 * r(64))
+    ql, sl = O.vfp8_ln_mod_q8(y, sh, sc, eps)
+    want = O.adaln(y, sh, sc, eps)
+    assert ((ql.float() * sl - want).abs() <= want.abs() * 0.07 + 0.05).all()
+    y2 = bf(r(6, 64))
+    xo, qa, sa = O.vfp8_add_ln_mod_q8(bf(y), y2, sh, sc, eps)
+    assert torch.equal(xo, bf(bf(y) + y2))
+    want = O.adaln(xo, sh, sc, eps)
+    assert ((qa.float() * sa - want).abs() <= want.abs() * 0.07 + 0.05).all()

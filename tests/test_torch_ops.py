@@ -164,6 +164,87 @@ def test_geak_split_plane_ops_trace():
         assert any(t_.startswith("fastwam." + op_ + ".") for t_ in targets), (op_, targets)
 
 
+
+def test_cae_fused_and_fp8_ops_trace():
+    """The CAE tree's fused operators (mutating acc / kbuf / vbuf / za / zb / out as the reference
+    declares) and the fp8 row operators trace under torch.compile(fullgraph=True) with the
+    reference's output shapes (CA/mot.py:2830-3980)."""
+    from fam import fastwam_ops  # noqa: F401
+    M, D, H, hd, SK, NS, F_ = 4, 32, 2, 16, 9, 7, 64
+    NQ = H * hd
+    f32 = torch.float32
+
+    class Mod(torch.nn.Module):
+        def forward(self, res, so, mod, tmod, lnw, lnb, qw, qb, qnw, gram, ck, cv, cmsk, wo, bo, acc, q, k, v, am, cm,
+                    w1, b1, w2, b2, wqkv, bqkv, gr, freqs, kbuf, vbuf, za, zb, qkv, g, nkw, kvo, e, wc, bc, vx, vsh):
+            x, cq = torch.ops.fastwam.mod_n3q.default(res, so, mod, tmod, lnw, lnb, qw, qb, 1e-6)
+            x2, cqn = torch.ops.fastwam.mod_n3q_qn.default(res, so, mod, tmod, lnw, lnb, qw, qb, qnw, gram, 1e-6, 1e-6)
+            x3 = torch.ops.fastwam.n3q_xoproj.default(res, so, mod, tmod, lnw, lnb, qw, qb, qnw, gram, ck, cv, cmsk, wo,
+                                                      bo, acc, H, 1e-6, 1e-6)
+            sb, xb = torch.ops.fastwam.mask_bias.default(am, cm, 16, 16, 8)
+            torch.ops.fastwam.mot_attn_oproj.default(q, k, v, sb, wo, bo, acc, H, hd)
+            xo, ai = torch.ops.fastwam.mot_ffn_fold.default(x, so, mod, mod, tmod, w1, b1, w2, b2, 1e-6, 1e-6, 1)
+            qa = torch.ops.fastwam.mot_sa_qkv.default(ai, wqkv, bqkv, gr, gr, qnw, qnw, freqs, kbuf, vbuf, za, zb, 5, 1e-6)
+            xs, qs = torch.ops.fastwam.mot_ffn_sa_qkv.default(x, so, mod, mod, tmod, w1, b1, w2, b2, wqkv, bqkv, gr, gr,
+                                                              qnw, qnw, freqs, kbuf, vbuf, za, zb, 5, 1e-6, 1e-6, 1e-6)
+            qz = torch.ops.fastwam.mot_qkv_post_z.default(qkv, qnw, qnw, freqs, kbuf, vbuf, za, zb, 5, 1e-6)
+            qg = torch.ops.fastwam.mot_qkv_gemm_post_z.default(ai, wqkv.t(), bqkv, qnw, qnw, freqs, kbuf, vbuf, za, zb,
+                                                               5, 1e-6)
+            q0 = torch.ops.fastwam.mot_l0_qkv_rope.default(cq, cq, cq, qnw, qnw, freqs, kbuf, vbuf, 5, 1e-6)
+            q1 = torch.ops.fastwam.mot_l0_qkv_rope_z.default(cq, cq, cq, qnw, qnw, freqs, kbuf, vbuf, acc, 5, 1e-6)
+            torch.ops.fastwam.ctx_kv_norm_into.default(g, nkw, kvo, 3, D, 1e-6)
+            torch.ops.fastwam.ctx_kv_gemm_norm_into.default(e, wc, bc, nkw, kvo, 3, D, 1e-6, True)
+            vq = torch.ops.fastwam.vqkv_post.default(qkv, qnw, qnw, freqs, kbuf, vbuf, 1e-6)
+            r8, rs = torch.ops.fastwam.row_q8.default(vx)
+            g8, gs = torch.ops.fastwam.gelu_q8.default(vx)
+            l8, ls = torch.ops.fastwam.ln_mod_q8.default(vx, vsh, vsh, 1e-6)
+            ao, a8, as_ = torch.ops.fastwam.add_ln_mod_q8.default(vx, vx, vsh, vsh, 1e-6)
+            return x, cq, cqn, x3, sb, xb, xo, ai, qa, xs, qs, qz, qg, q0, q1, vq, r8, rs, g8, l8, ao, a8, as_
+
+    args = (_meta(1, M, D), _meta(M, D, dtype=f32), _meta(6 * D), _meta(1, 6 * D), _meta(D), _meta(D), _meta(NQ, D),
+            _meta(NQ), _meta(NQ), _meta(D * D + D + 1, dtype=f32), _meta(1, NS, NQ), _meta(1, NS, NQ),
+            _meta(1, M, NS, dtype=torch.bool), _meta(D, NQ), _meta(D), _meta(M, D, dtype=f32), _meta(1, H, M, hd),
+            _meta(1, H, SK, hd), _meta(1, H, SK, hd), _meta(M, SK, dtype=torch.bool), _meta(1, NS, dtype=torch.bool),
+            _meta(F_, D), _meta(F_), _meta(D, F_), _meta(D), _meta(3 * NQ, D), _meta(3 * NQ), _meta(D * D + D + 1),
+            _meta(M, hd, dtype=f32), _meta(1, H, SK, hd), _meta(1, H, SK, hd), _meta(M, 16, dtype=f32),
+            _meta(M, 16, dtype=f32), _meta(1, M, 3 * NQ), _meta(NS, 6 * D), _meta(3, D), _meta(2, 3, 1, NS, D),
+            _meta(NS, 24), _meta(6 * D, 24), _meta(6 * D), _meta(1, 6, 64), _meta(64))
+    outs, _, targets = _compile_graph(Mod(), *args)
+    x, cq, cqn, x3, sb, xb, xo, ai, qa, xs, qs, qz, qg, q0, q1, vq, r8, rs, g8, l8, ao, a8, as_ = outs
+    assert x.shape == x3.shape == xo.shape == ai.shape == xs.shape == (1, M, D)
+    assert cq.shape == cqn.shape == q0.shape == q1.shape == (1, M, NQ)
+    assert sb.shape == (16, 16) and xb.shape == (16, 8) and sb.dtype == f32
+    assert qa.shape == qs.shape == qz.shape == qg.shape == (1, H, M, hd) and vq.shape == (3, 1, M, NQ)
+    assert r8.shape == g8.shape == l8.shape == a8.shape == (6, 64) and r8.dtype == torch.float8_e4m3fn
+    assert rs.shape == as_.shape == (6, 1) and ao.shape == (1, 6, 64)
+    for op_ in ("mod_n3q", "mod_n3q_qn", "n3q_xoproj", "mask_bias", "mot_attn_oproj", "mot_ffn_fold", "mot_sa_qkv",
+                "mot_ffn_sa_qkv", "mot_qkv_post_z", "mot_qkv_gemm_post_z", "mot_l0_qkv_rope", "mot_l0_qkv_rope_z",
+                "ctx_kv_norm_into", "ctx_kv_gemm_norm_into", "vqkv_post", "row_q8", "gelu_q8", "ln_mod_q8",
+                "add_ln_mod_q8"):
+        assert any(t_.startswith("fastwam." + op_ + ".") for t_ in targets), (op_, targets)
+
+
+
+# every operator name the reference's GEAK trees register in the fastwam namespace
+# (src/fastwam-geak/fastwam/models/wan22/{mot,wan_video_dit}.py, src/cae-fastwam/fastwam/models/wan22/
+# {mot,action_dit}.py: the torch.library.custom_op("fastwam::...") definitions)
+_REFERENCE_FASTWAM_OPS = (
+    "add_ln_mod_q8", "adit_tmod", "ctx_kv_gemm_norm_into", "ctx_kv_norm", "ctx_kv_norm_into", "gelu_q8", "ln_mod_q8",
+    "mask_bias", "mod_n3q", "mod_n3q_qn", "mot_attn", "mot_attn_oproj", "mot_ffn", "mot_ffn_fold", "mot_ffn_sa_qkv",
+    "mot_l0_qkv_rope", "mot_l0_qkv_rope_z", "mot_oproj", "mot_qkv_gemm_post_z", "mot_qkv_post", "mot_qkv_post_z",
+    "mot_sa_qkv", "n3q_xoproj", "pf_mm", "pf_mm_gelu", "pf_qcomb", "pf_skmm", "pf_skmm_big", "qk_post", "qkv_post",
+    "qrms_attn", "res_ln1", "res_ln1_sk", "res_ln2", "res_ln2_sk", "res_ln_tail", "res_ln_tail_sk", "row_q8",
+    "short_attn", "short_attn_bsd", "skmm", "skpost", "vqkv_post", "xattn_qn")
+
+
+def test_every_reference_fastwam_op_is_defined():
+    """Importing fam.fastwam_ops defines each of the reference trees' 44 fastwam:: operators."""
+    from fam import fastwam_ops  # noqa: F401
+    assert len(_REFERENCE_FASTWAM_OPS) == 44
+    missing = [n for n in _REFERENCE_FASTWAM_OPS if not hasattr(torch.ops.fastwam, n)]
+    assert not missing, missing
+
+
 # --------------------------------------------------------------------------- RoPE tables
 def _cat_table(S, Dh, offset=0.0):
     ang = (torch.arange(S, dtype=torch.float64)[:, None] + offset) * \

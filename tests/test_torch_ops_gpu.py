@@ -389,3 +389,193 @@ def test_cae_ops(fw):
     errs["adit_tmod t"], errs["t_mod"], errs["tokens"] = _rel(t, rt), _rel(tmod, rtm), _rel(tk, rtk)
     print("CAE operators:", ", ".join(f"{k} {v:.2e}" for k, v in errs.items()))
     assert max(errs.values()) <= 2e-2, errs
+
+
+def test_cae_fused_lever_ops(fw):
+    """The CAE tree's fused operators at the action expert's shape (8 tokens, hidden 32, 24 x 128
+    attention, 98 + 8 joint keys, 129 context keys, FFN 256) against the oracle's restatements of
+    the reference kernels (CA/mot.py:1369-1680, 2015-2077, 2119-2210, 2346-2780, 2830-3565,
+    3621-3750): the accumulating o-projections add their term to what acc held, the *_z forms
+    clear rows [0, M) of their accumulators, and the bias planes of mask_bias drive the same
+    attention as the keep masks they encode."""
+    g = torch.Generator().manual_seed(94)
+    M, D, H, hd, Sv, Lc, Fd, eps = 8, 32, 24, 128, 98, 129, 256, 1e-6
+    NQ, SK = H * hd, Sv + M
+    f = lambda t: t.float().cpu()  # noqa: E731
+    cu = lambda *ts: [t.cuda() for t in ts]  # noqa: E731
+    errs = {}
+    # norm3 + cross q (+ its whole-row norm), and the cross attention with its o-projection
+    res, so = _rand(g, 1, M, D), torch.randn(M, D, generator=g) * 0.5
+    mod, tmod = _rand(g, 6 * D, scale=0.3), _rand(g, 1, 6 * D, scale=0.3)
+    lnw, lnb = (1 + 0.2 * torch.randn(D, generator=g)).to(BF), _rand(g, D, scale=0.2)
+    qw, qb = _rand(g, NQ, D, scale=D ** -0.5), _rand(g, NQ, scale=0.1)
+    qnw, gram = (1 + 0.2 * torch.randn(NQ, generator=g)).to(BF), torch.zeros(D * D + D + 1)
+    dres, dso, dmod, dtmod, dlnw, dlnb, dqw, dqb, dqnw, dgram = cu(res, so, mod, tmod, lnw, lnb, qw, qb, qnw, gram)
+    x, cq = fw.mod_n3q(dres, dso, dmod, dtmod, dlnw, dlnb, dqw, dqb, eps)
+    rx, rcq = O.cae_mod_n3q(f(res)[0], so, f(mod), f(tmod), f(lnw), f(lnb), f(qw), f(qb), eps)
+    errs["mod_n3q x"], errs["mod_n3q cq"] = _rel(x[0], rx), _rel(cq[0], rcq)
+    _, cqn = fw.mod_n3q_qn(dres, dso, dmod, dtmod, dlnw, dlnb, dqw, dqb, dqnw, dgram, eps, eps)
+    errs["mod_n3q_qn"] = _rel(cqn[0], O.cae_mod_n3q(f(res)[0], so, f(mod), f(tmod), f(lnw), f(lnb), f(qw), f(qb), eps,
+                                                    qn=(f(qnw), eps))[1])
+    ckv = _rand(g, 1, Lc, 2 * NQ)                          # keys and values interleaved per row: strided
+    dckv = ckv.cuda()
+    ck, cv = dckv[..., :NQ], dckv[..., NQ:]
+    cm = torch.ones(1, Lc, dtype=torch.bool)
+    cm[0, Lc - 20:] = False
+    wo, bo = _rand(g, D, NQ, scale=NQ ** -0.5), _rand(g, D, scale=0.1)
+    dwo, dbo = cu(wo, bo)
+    acc0 = torch.randn(M, D, generator=g)
+    acc = acc0.cuda()
+    xr = fw.n3q_xoproj(dres, dso, dmod, dtmod, dlnw, dlnb, dqw, dqb, dqnw, dgram, ck, cv,
+                       cm.expand(M, Lc)[None].cuda(), dwo, dbo, acc, H, eps, eps)
+    rxx, term = O.cae_n3q_xoproj(f(res)[0], so, f(mod), f(tmod), f(lnw), f(lnb), f(qw), f(qb), f(qnw), f(ckv)[0, :, :NQ],
+                                 f(ckv)[0, :, NQ:], cm.expand(M, Lc), f(wo), f(bo), H, eps, eps)
+    errs["n3q_xoproj x"], errs["n3q_xoproj acc"] = _rel(xr[0], rxx), _rel(acc.cpu() - acc0, term)
+    # the additive planes, and the same cross attention through them
+    am = torch.rand(M, SK, generator=g) > 0.25
+    am[:, Sv:] = True
+    mp, skp, ncp = 16, 128, 256
+    sb, xb = fw.mask_bias(am.cuda(), cm.cuda(), mp, skp, ncp)
+    rsb, rxb = O.cae_mask_bias(am, cm, mp, skp, ncp)
+    assert torch.equal(sb.cpu(), rsb) and torch.equal(xb.cpu(), rxb)
+    acc_b = acc0.cuda()
+    fw.n3q_xoproj(dres, dso, dmod, dtmod, dlnw, dlnb, dqw, dqb, dqnw, dgram, ck, cv, xb, dwo, dbo, acc_b, H, eps, eps)
+    errs["n3q_xoproj via mask_bias"] = _rel(acc_b.cpu() - acc0, term)
+    # self attention + o-projection into the accumulator, keep plane and bias plane
+    q, kb, vb = _rand(g, 1, H, M, hd), _rand(g, 1, H, SK, hd), _rand(g, 1, H, SK, hd)
+    rterm = O.cae_attn_oproj(f(q)[0], f(kb)[0], f(vb)[0], am, f(wo), f(bo))
+    for name, mk in (("keep", am.to(torch.uint8).cuda()), ("bias", sb)):
+        acc_s = acc0.cuda()
+        fw.mot_attn_oproj(*cu(q, kb, vb), mk, dwo, dbo, acc_s, H, hd)
+        errs["mot_attn_oproj " + name] = _rel(acc_s.cpu() - acc0, rterm)
+    # FFN fold (+ the next block's AdaLN1), and the fused FFN + next layer's q / k / v
+    xa, oacc = _rand(g, 1, M, D), torch.randn(M, D, generator=g) * 0.5
+    modn = _rand(g, 6 * D, scale=0.3)
+    w1, b1, w2, b2 = _rand(g, Fd, D, scale=D ** -0.5), _rand(g, Fd, scale=0.1), _rand(g, D, Fd, scale=Fd ** -0.5), \
+        _rand(g, D, scale=0.1)
+    dxa, doacc, dmodn, dw1, db1, dw2, db2 = cu(xa, oacc, modn, w1, b1, w2, b2)
+    xo, ai = fw.mot_ffn_fold(dxa, doacc, dmod, dmodn, dtmod, dw1, db1, dw2, db2, eps, eps, 1)
+    rxo, rai = O.cae_ffn_fold(f(xa)[0], oacc, f(mod), f(modn), f(tmod), f(w1), f(b1), f(w2), f(b2), eps, eps)
+    errs["ffn_fold x"], errs["ffn_fold next"] = _rel(xo[0], rxo), _rel(ai[0], rai)
+    xo0, _ = fw.mot_ffn_fold(dxa, doacc, dmod, dmodn, dtmod, dw1, db1, dw2, db2, eps, eps, 0)
+    assert torch.equal(xo0, xo)
+    # q / k / v post-processing variants, each against cae_qkv_post of the same projection
+    ang = torch.arange(M, dtype=torch.float64)[:, None] * (10000.0 ** (-torch.arange(0, hd, 2, dtype=torch.float64) / hd))
+    freqs = torch.stack([ang.cos(), ang.sin()], -1).reshape(M, hd).float()
+    nqw, nkw = (1 + 0.2 * torch.randn(NQ, generator=g)).to(BF), (1 + 0.2 * torch.randn(NQ, generator=g)).to(BF)
+    wqkv, bqkv = _rand(g, 3 * NQ, D, scale=D ** -0.5), _rand(g, 3 * NQ, scale=0.1)
+    kv0 = _rand(g, 1, H, SK, hd)
+    dfreqs, dnqw, dnkw, dwqkv, dbqkv = cu(freqs, nqw, nkw, wqkv, bqkv)
+    qgr = torch.zeros(D * D + D + 1).cuda()
+
+    def post_ref(rows):
+        return O.cae_qkv_post(rows, f(nqw), f(nkw), freqs, H, eps)
+
+    def chk(name, qo, kbuf, vbuf, rows, head_major=True, sv=Sv):
+        rq, rk, rv = post_ref(rows)
+        qh = qo[0] if head_major else qo[0].view(M, H, hd).transpose(0, 1)
+        errs[name + " q"] = _rel(qh, rq)
+        errs[name + " k"] = _rel(kbuf[0, :, sv:sv + M], rk)
+        errs[name + " v"] = _rel(vbuf[0, :, sv:sv + M], rv)
+        if sv:
+            assert torch.equal(kbuf[0, :, :sv].cpu(), kv0[0, :, :sv])
+    zn = 64
+    za, zb = torch.ones(M + 2, zn).cuda(), torch.ones(M + 2, zn).cuda()
+
+    def zeroed(z):
+        return bool((z[:M] == 0).all()) and bool((z[M:] == 1).all())
+    xin = _rand(g, 1, M, D)
+    rows = O.linear(f(xin)[0], f(wqkv), f(bqkv))
+    kbuf, vbuf = kv0.cuda(), kv0.cuda()
+    qo = fw.mot_sa_qkv(xin.cuda(), dwqkv, dbqkv, qgr, qgr, dnqw, dnkw, dfreqs, kbuf, vbuf, za, zb, Sv, eps)
+    chk("sa_qkv", qo, kbuf, vbuf, rows)
+    assert zeroed(za) and zeroed(zb)
+    za.fill_(1), zb.fill_(1)
+    kbuf, vbuf = kv0.cuda(), kv0.cuda()
+    qo = fw.mot_qkv_gemm_post_z(xin.cuda(), wqkv.t().contiguous().cuda(), dbqkv, dnqw, dnkw, dfreqs, kbuf, vbuf, za,
+                                zb, Sv, eps)
+    chk("qkv_gemm_post_z", qo, kbuf, vbuf, rows)
+    assert zeroed(za) and zeroed(zb)
+    za.fill_(1), zb.fill_(1)
+    qkv = _rand(g, 1, M, 3 * NQ)
+    kbuf, vbuf = kv0.cuda(), kv0.cuda()
+    qo = fw.mot_qkv_post_z(qkv.cuda(), dnqw, dnkw, dfreqs, kbuf, vbuf, za, zb, Sv, eps)
+    chk("qkv_post_z", qo, kbuf, vbuf, f(qkv)[0])
+    assert zeroed(za) and zeroed(zb)
+    kbuf, vbuf = kv0.cuda(), kv0.cuda()
+    qs, ks, vs = (qkv[..., i * NQ:(i + 1) * NQ].contiguous().cuda() for i in range(3))
+    qo = fw.mot_l0_qkv_rope(qs, ks, vs, dnqw, dnkw, dfreqs, kbuf, vbuf, Sv, eps)
+    assert qo.shape == (1, M, NQ)
+    chk("l0_qkv_rope", qo, kbuf, vbuf, f(qkv)[0], head_major=False)
+    oz = torch.ones(M + 1, D).cuda()
+    kbuf, vbuf = kv0.cuda(), kv0.cuda()
+    qz = fw.mot_l0_qkv_rope_z(qs, ks, vs, dnqw, dnkw, dfreqs, kbuf, vbuf, oz, Sv, eps)
+    assert torch.equal(qz, qo) and bool((oz[:M] == 0).all()) and bool((oz[M:] == 1).all())
+    za.fill_(1), zb.fill_(1)
+    kbuf, vbuf = kv0.cuda(), kv0.cuda()
+    xs, qf = fw.mot_ffn_sa_qkv(dxa, doacc, dmod, dmodn, dtmod, dw1, db1, dw2, db2, dwqkv, dbqkv, qgr, qgr, dnqw, dnkw,
+                               dfreqs, kbuf, vbuf, za, zb, Sv, eps, eps, eps)
+    errs["ffn_sa_qkv x"] = _rel(xs[0], rxo)
+    chk("ffn_sa_qkv", qf, kbuf, vbuf, O.linear(rai.to(BF).float(), f(wqkv), f(bqkv)))
+    assert zeroed(za) and zeroed(zb)
+    # the video prefill's post: token-major q / k / v, head-major caches from row 0, rows past M cleared
+    kbuf, vbuf = kv0.cuda(), kv0.cuda()
+    out = fw.vqkv_post(qkv.cuda(), dnqw, dnkw, dfreqs, kbuf, vbuf, eps)
+    assert out.shape == (3, 1, M, NQ)
+    rq, rk, rv = post_ref(f(qkv)[0])
+    errs["vqkv_post q"] = _rel(out[0, 0].view(M, H, hd).transpose(0, 1), rq)
+    errs["vqkv_post k"] = _rel(out[1, 0].view(M, H, hd).transpose(0, 1), rk)
+    assert torch.equal(out[2, 0].cpu(), qkv[0, :, 2 * NQ:])
+    errs["vqkv_post kbuf"] = _rel(kbuf[0, :, :M], rk)
+    assert bool((kbuf[0, :, M:] == 0).all()) and bool((vbuf[0, :, M:] == 0).all())
+    # every layer's context K / V into one buffer, from g and from the embedding
+    nl, C = 30, 64
+    e, wc, bc = _rand(g, Lc, C), _rand(g, 2 * nl * D, C, scale=C ** -0.5), _rand(g, 2 * nl * D, scale=0.1)
+    nkwc = (1 + 0.2 * torch.randn(nl, D, generator=g)).to(BF)
+    gg = O.linear(f(e), f(wc), f(bc))
+    kv_out = torch.empty(2, nl, 1, Lc, D, dtype=BF).cuda()
+    fw.ctx_kv_gemm_norm_into(*cu(e, wc, bc, nkwc), kv_out, nl, D, eps, True)
+    errs["ctx_kv_gemm_norm_into k"] = _rel(kv_out[0, :, 0], O.cae_ctx_kv_norm(gg, f(nkwc), nl, D, eps))
+    errs["ctx_kv_gemm_norm_into v"] = _rel(kv_out[1, :, 0], gg[:, nl * D:].reshape(Lc, nl, D).transpose(0, 1))
+    gb = gg.to(BF)
+    kv2 = torch.empty(2, nl, 1, Lc, D, dtype=BF).cuda()
+    fw.ctx_kv_norm_into(gb.cuda(), nkwc.cuda(), kv2, nl, D, eps)
+    assert torch.equal(kv2[1].cpu(), gb[:, nl * D:].reshape(Lc, nl, D).transpose(0, 1)[:, None])
+    errs["ctx_kv_norm_into k"] = _rel(kv2[0, :, 0], O.cae_ctx_kv_norm(gb.float(), f(nkwc), nl, D, eps))
+    print("CAE fused operators:", ", ".join(f"{k} {v:.2e}" for k, v in errs.items()))
+    assert max(errs.values()) <= 2e-2, errs
+
+
+@pytest.mark.parametrize("D", [3072, 14336, 4096])
+def test_vfp8_row_ops(fw, D):
+    """row_q8, gelu_q8, ln_mod_q8 and add_ln_mod_q8 at the video prefill's row widths (hidden 3072,
+    FFN 14336, text 4096) against the oracle (CA/mot.py:3763-3980): the scales agree to fp32
+    rounding, the fp8 codes are identical for the plain rows and, where the row operation's fp32
+    arithmetic may move a value across a rounding boundary, at most one e4m3 step apart in a
+    handful of entries; the dequantised rows match the oracle's rows at e4m3's precision."""
+    g = torch.Generator().manual_seed(95 + D)
+    M, eps = 98, 1e-6
+    x = (torch.randn(M, D, generator=g) * torch.logspace(-2, 1, M)[:, None]).to(BF)
+    sh, sc = _rand(g, D, scale=0.3), _rand(g, D, scale=0.3)
+    x2 = _rand(g, M, D)
+
+    def cmp(name, got, ref, exact=False):
+        (q, s), (rq, rs) = got, ref
+        assert q.dtype == torch.float8_e4m3fn and q.shape == (M, D) and s.shape == (M, 1)
+        q, s = q.cpu().float(), s.cpu()
+        rqf = rq.float()
+        assert torch.allclose(s, rs, rtol=2e-6 if exact else 1e-2), name
+        diff = (q != rqf).float().mean().item()
+        step = (q - rqf).abs() <= rqf.abs() * 2 ** -3 + 2 ** -9 * 1.0001
+        print(f"{name} D={D}: codes differing {diff:.2e}")
+        if exact:
+            assert diff == 0, name
+        else:
+            assert step.all() and diff <= 1e-3, name
+    cmp("row_q8", fw.row_q8(x.cuda()), O.vfp8_row_q8(x.float()), exact=True)
+    cmp("gelu_q8", fw.gelu_q8(x.cuda()), O.vfp8_gelu_q8(x.float()))
+    cmp("ln_mod_q8", fw.ln_mod_q8(x.cuda(), sh.cuda(), sc.cuda(), eps), O.vfp8_ln_mod_q8(x.float(), sh, sc, eps))
+    xo, q, s = fw.add_ln_mod_q8(x.cuda(), x2.cuda(), sh.cuda(), sc.cuda(), eps)
+    rxo, rq, rs = O.vfp8_add_ln_mod_q8(x.float(), x2.float(), sh, sc, eps)
+    assert xo.dtype == BF and torch.equal(xo.cpu().float(), rxo)
+    cmp("add_ln_mod_q8", (q, s), (rq, rs))
