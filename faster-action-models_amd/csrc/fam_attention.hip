@@ -1711,9 +1711,10 @@ static void launch_small_nv(const AttnArgs& a, bool qn, dim3 grid, hipStream_t s
 }
 template <int DH, int NW>
 static void launch_small_nw(const AttnArgs& a, bool qn, int64_t bh, int nqc, hipStream_t s) {
-  // a (head, query chunk) over 8 or 4 CUs (output-dim eighths / quarters) while that keeps the
-  // grid within one round: each slice's workgroup repeats the scores but runs 1/NV of P V and of
-  // the merge (eighths only at DH = 128: a slice keeps at least one 16-dim MFMA tile)
+  // a (head, query chunk) over 8, 4 or 2 CUs (output-dim eighths / quarters / halves) while that
+  // keeps the grid within one round: each slice's workgroup repeats the scores but runs 1/NV of
+  // P V and of the merge (eighths only at DH = 128: a slice keeps at least one 16-dim MFMA tile;
+  // halves for the video prefill's 24 heads x 4 query chunks)
   const int64_t units = bh * nqc;
   if constexpr (DH == 128) {
     if (units <= 32) {
@@ -1722,6 +1723,7 @@ static void launch_small_nw(const AttnArgs& a, bool qn, int64_t bh, int nqc, hip
     }
   }
   if (units <= 64) launch_small_nv<DH, NW, 4>(a, qn, dim3((unsigned)bh, 4, (unsigned)nqc), s);
+  else if (units <= 128) launch_small_nv<DH, NW, 2>(a, qn, dim3((unsigned)bh, 2, (unsigned)nqc), s);
   else launch_small_nv<DH, NW, 1>(a, qn, dim3((unsigned)bh, 1, (unsigned)nqc), s);
 }
 template <int DH>

@@ -236,6 +236,7 @@ def test_attention_masks(kind):
 
 @pytest.mark.parametrize("B,H,Sq,Sk,Dh,mask", [(1, 24, 98, 98, 128, None), (1, 24, 98, 129, 128, "keys"),
                                                 (2, 4, 98, 98, 64, None), (2, 3, 70, 200, 128, "rows"),
+                                                (1, 24, 98, 129, 64, "keys"), (1, 40, 70, 98, 128, "rows"),
                                                 (1, 2, 128, 256, 64, "rows"), (1, 2, 33, 31, 128, "rows")])
 def test_attention_small_query_chunks(B, H, Sq, Sk, Dh, mask):
     """33-128 queries over <= 256 keys run the small kernel in chunks of 32 queries (grid.z): the
