@@ -22,6 +22,9 @@ Extra legs (one JSON line in total):
                 the host cores on a bounded sample of full policy calls.
   eager_gpu     the reference's eager module sequence (ops as FB/action_dit.py,
                 FB/wan_video_dit.py issue them, bf16) on the same GPU, for comparison.
+  policy calls  the FastWAM, CAE-FastWAM and DiT4DiT RoboCasa-GR1 calls at their real shapes
+                (the reference's published latencies), then configs 2, 3 and 4 (the other
+                BASELINE configurations), each as its own key (--no-policy-calls skips them).
 """
 from __future__ import annotations
 
@@ -56,7 +59,7 @@ def parse():
     ap.add_argument("--no-eager", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
     ap.add_argument("--no-policy-calls", action="store_true",
-                    help="skip the FastWAM / CAE-FastWAM policy-call figures added to the default line")
+                    help="skip the policy-call and config 2-4 figures added to the default line")
     ap.add_argument("--cpu-sample-s", type=float, default=20.0, help="CPU baseline time budget")
     ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "d4d", "hbm", "prefill", "fastwam", "cae", "gemm"], default="c1",
                     help="c1: the action-DiT denoise loop (the metric); c2: one long-sequence video DiT block "
@@ -419,6 +422,10 @@ def eager_gpu_baseline(cfg, params, noise, ctx, warmup=25, iters=40):
 
 # --------------------------------------------------------------------------- config 2: video DiT block
 def bench_c2(args):
+    print(json.dumps(_c2_result(args)), flush=True)
+
+
+def _c2_result(args):
     """Config 2 (Wan2.2-5B-style video DiT, bf16): WanVideoDiT.forward -- pre_dit, 30 blocks at
     1560 tokens (2 x 30 x 26 with 3-D RoPE, hidden 3072, 24 x 128 heads, FFN 14336, 512 text
     tokens, per-token AdaLN), head -- replayed from one captured graph (`value`); one block alone
@@ -514,7 +521,7 @@ def bench_c2(args):
         "gemm_TFLOPs": round(gem_fl / (gem_us * 1e-6) / 1e12, 1),
         "kernels": kernels,
     }
-    print(json.dumps(out), flush=True)
+    return out
 
 
 # --------------------------------------------------------------------------- config 4: DiT4DiT head
@@ -1006,6 +1013,10 @@ def bench_prefill(args):
 
 # --------------------------------------------------------------------------- config 3: compact expert + decoder
 def bench_c3(args):
+    print(json.dumps(_c3_result(args)), flush=True)
+
+
+def _c3_result(args):
     """Config 3: the compact action expert (hidden 32, 4 x 8 heads, 8 blocks) denoising an 8 x 16
     latent over 4 Euler steps against a 1560 x 1024 context, then the action-VAE decoder to a
     32 x 7 chunk, as one captured graph per policy call; B = 1 (launch-bound) and B = 256."""
@@ -1058,7 +1069,7 @@ def bench_c3(args):
            "config": {"workload": "config3 compact expert: hidden 32, 4x8 heads, 8 blocks, 8x16 latent, 4 Euler "
                                   "steps, ctx 1560x1024, conv action-VAE decoder to 32x7", "batch": [1, 256]},
            "by_batch": res}
-    print(json.dumps(out), flush=True)
+    return out
 
 
 # (M, N, K, role) of the large-M products the backbones issue, plus the square reference point
@@ -1277,6 +1288,24 @@ def main():
                                       "published_reference_ms": r["published_reference_ms"],
                                       "published_source": r["published_source"],
                                       "ratio_published_over_ours": round(r["published_reference_ms"] / r["value"], 4)}
+        torch.cuda.empty_cache()
+        # the other BASELINE configurations, so that every one of them is timed with this line
+        log("config 2 forward: building and timing")
+        r = _c2_result(args)
+        out["config2_forward"] = {"metric": r["metric"], "p50_ms": r["value"], "min_ms": r["min_ms"],
+                                  "p90_ms": r["p90_ms"], "forward_TFLOPs": r["forward_TFLOPs"],
+                                  "launches_per_call": r["launches_per_call"],
+                                  "attention_roofline_frac": r["roofline"]["frac"]}
+        torch.cuda.empty_cache()
+        log("config 3 call: building and timing")
+        r = _c3_result(args)
+        out["config3_call"] = {"metric": r["metric"], "by_batch": r["by_batch"]}
+        torch.cuda.empty_cache()
+        log("config 4 call: building and timing")
+        r = _d4d_policy_call(args, real=False)
+        out["config4_call"] = {"metric": r["metric"], "p50_ms": r["value"], "min_ms": r["min_ms"],
+                               "p90_ms": r["p90_ms"], "backbone_p50_ms": r["backbone_ms"],
+                               "head_p50_ms": r["head_ms"]}
         torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
