@@ -807,9 +807,11 @@ def cae_decode(p: Params, cfg: CaeDecoderConfig, z: torch.Tensor, suite: Optiona
 # The head's transformer (DB/flow_matching_head/cross_attention_dit.py) is built from diffusers
 # modules (Attention, FeedForward, Timesteps, TimestepEmbedding; diffusers 0.37.0.dev0 @3996788
 # per scripts/dit4dit_diffusers_overlay.sh:7,35), which are not installed here.  Their published
-# semantics are restated below; no reference test or fixture pins the composition, so this part
-# of the oracle is "parity unpinned" at the composition level (the closed forms of the two
-# embeddings are pinned in tests/test_oracle.py).
+# semantics are restated below.  No reference test or fixture holds this model; the composition
+# is pinned by closed forms in tests/test_oracle.py (the AdaLayerNorm's (scale, shift) order, norm3
+# without affine + the FFN, the output stage's (shift, scale) and eps, the action encoder's concat
+# order, the two embeddings, the schedule and block wiring), each with its slipped alternative
+# shown to fail; "parity unpinned" only as to diffusers' own code, which cannot run here.
 @dataclass
 class DiT4DiTHeadConfig:
     """DiT-B head of DB/ActionDiT.py:192-195 with the diffusion_model_cfg of
