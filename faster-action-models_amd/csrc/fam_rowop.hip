@@ -540,7 +540,7 @@ extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (vec_eligible(d)) {
     const int tw = d->N > 4096 ? rms_tile_waves(d) : 0;
-    const int nw = tw > 0 ? tw : (d->N <= 1024 ? 4 : (d->N <= 2048 ? 8 : 16));
+    const int nw = tw > 0 ? tw : (d->N <= 1024 ? 4 : (d->N <= 2048 ? 8 : (d->N <= 3072 ? 12 : 16)));
     const dim3 grid((unsigned)d->M, (unsigned)((d->N + nw * 256 - 1) / (nw * 256)));
     const int ms = d->splits <= 4 ? 4 : (d->splits <= 8 ? 8 : 16);
 #define FAM_ROWVEC(NW_, MS_) \
