@@ -540,7 +540,15 @@ extern "C" int fam_rowop(const fam_rowop_desc* d, void* stream) {
   hipStream_t s = (hipStream_t)stream;
   if (vec_eligible(d)) {
     const int tw = d->N > 4096 ? rms_tile_waves(d) : 0;
-    const int nw = tw > 0 ? tw : (d->N <= 1024 ? 4 : (d->N <= 2048 ? 8 : (d->N <= 3072 ? 12 : 16)));
+    int nw = tw > 0 ? tw : (d->N <= 1024 ? 4 : (d->N <= 2048 ? 8 : (d->N <= 3072 ? 12 : 16)));
+    // a wider row without normalisation tiles over grid.y: take the widest tile that divides it
+    // (14336 = 7 x 2048), so that no workgroup of the last tile idles on missing columns
+    if (tw == 0 && d->N > 4096 && d->N % (16 * 256) != 0)
+      for (int w : {12, 8})
+        if (d->N % (w * 256) == 0) {
+          nw = w;
+          break;
+        }
     const dim3 grid((unsigned)d->M, (unsigned)((d->N + nw * 256 - 1) / (nw * 256)));
     const int ms = d->splits <= 4 ? 4 : (d->splits <= 8 ? 8 : 16);
 #define FAM_ROWVEC(NW_, MS_) \
